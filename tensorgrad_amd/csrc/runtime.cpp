@@ -1,0 +1,1640 @@
+// Host runtime of the gfx950 backend: reads the traced IR, plans device memory, lowers
+// IR ops to HIP kernel launches, captures the whole step as one hipGraph and serves the
+// C ABI in include/tg.h.
+//
+// It takes the place of the reference's buffer planner (src/buffers.ts), WGSL codegen
+// (src/codegen.ts), WebGPU runtime (src/runtime.ts) and worker request handlers
+// (src/worker.ts). Design, MI355X-first rather than one dispatch per IR op:
+//  * views: reshape / stop_gradient / identity sum_to_shape and broadcast_to alias their
+//    input; permute is a strided view that GEMMs and element-wise kernels read in place
+//    and is materialised only for consumers that need contiguous rows;
+//  * patterns: one_hot -> matmul becomes a row gather (embedding forward) and
+//    transpose(one_hot) -> matmul a segmented scatter-add (embedding gradient), so the
+//    one-hot matrix is never built for them; all adam_update_{m,v,p} ops become one fused
+//    multi-tensor kernel updating p, m and v in place (no writeback copies);
+//  * memory: one arena per runtime, persistent regions for params / optimizer state /
+//    inputs, and liveness-pooled intermediates (best fit, as buffers.ts:151-209);
+//  * execution: one HIP stream; the launch sequence is captured once into a hipGraph
+//    and replayed per step; per-step host work is one H2D copy of the input region
+//    (user inputs + lrt / decayShrink / lr / PRNG seed scalars) and a 4-byte loss read.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <functional>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <set>
+#include <sstream>
+#include <stdexcept>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/tg.h"
+#include "json.hpp"
+#include "kernels.h"
+
+namespace tg {
+
+static thread_local std::string g_error;
+
+struct Error : std::runtime_error {
+  tg_status code;
+  Error(tg_status c, const std::string& m) : std::runtime_error(m), code(c) {}
+};
+
+static void hip_check(hipError_t e, const char* what) {
+  if (e != hipSuccess) throw Error(TG_DEVICE_ERROR, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+enum Dt { F32 = 0, I32 = 1, BOOL = 2 };
+static Dt parse_dt(const std::string& s) {
+  if (s == "f32") return F32;
+  if (s == "i32") return I32;
+  if (s == "bool") return BOOL;
+  throw Error(TG_INVALID_ARGUMENT, "IR: unknown dtype '" + s + "'");
+}
+static int kdt(Dt d) { return d == F32 ? tgk::DT_F32 : tgk::DT_I32; }
+
+using Dims = std::vector<int64_t>;
+static int64_t prod(const Dims& d) { int64_t n = 1; for (auto x : d) n *= x; return n; }
+static Dims contiguous_strides(const Dims& d) {
+  Dims s(d.size(), 1);
+  for (int i = (int)d.size() - 2; i >= 0; --i) s[i] = s[i + 1] * d[i + 1];
+  return s;
+}
+
+// Host-side bounds proof for every launch: the largest element offset an operand
+// descriptor can produce must lie inside its root allocation.
+static void check_span(const char* what, int64_t root_numel, int64_t base, const int64_t* dims, const int64_t* strides,
+                       int rank) {
+  int64_t hi = base, lo = base;
+  for (int d = 0; d < rank; ++d) {
+    if (dims[d] <= 0) return;   // empty iteration space touches nothing
+    int64_t ext = (dims[d] - 1) * strides[d];
+    if (ext >= 0) hi += ext; else lo += ext;
+  }
+  if (lo < 0 || hi >= std::max<int64_t>(root_numel, 1))
+    throw Error(TG_INTERNAL, std::string("bounds check failed for ") + what + ": offsets [" + std::to_string(lo) + ", " +
+                                 std::to_string(hi) + "] outside [0, " + std::to_string(root_numel) + ")");
+}
+
+// ---- learning-rate schedules (src/lr.ts:69-112) ---------------------------------------
+static double resolve_lr(const tgj::Value& s, double step) {
+  if (s.kind == tgj::Value::Number) return s.number;
+  const std::string& k = s.at("kind").str();
+  const tgj::Value* ss = s.get("startStep");
+  double start = (ss && !ss->null()) ? ss->num() : 0;
+  double st = std::max(1.0, step - start);
+  if (k == "linear") {
+    double f = std::min(st / s.at("steps").num(), 1.0);
+    return s.at("peak").num() + (s.at("final").num() - s.at("peak").num()) * f;
+  }
+  if (k == "cosineAnnealing") {
+    double f = std::min(st / s.at("steps").num(), 1.0);
+    return s.at("final").num() + 0.5 * (s.at("peak").num() - s.at("final").num()) * (1 + std::cos(M_PI * f));
+  }
+  if (k == "warmup") {
+    if (st <= s.at("steps").num()) return s.at("peak").num() * (st / s.at("steps").num());
+    return resolve_lr(s.at("after"), st - s.at("steps").num());
+  }
+  if (k == "staircase") {
+    double kk = std::floor((st - 1) / s.at("every").num());
+    return s.at("peak").num() * std::pow(s.at("gamma").num(), kk);
+  }
+  if (k == "multiStep") {
+    double kk = 0;
+    for (const auto& m : s.at("milestones").items) if (st >= m.num()) kk += 1;
+    return s.at("peak").num() * std::pow(s.at("gamma").num(), kk);
+  }
+  throw Error(TG_INVALID_ARGUMENT, "lr: unknown schedule kind '" + k + "'");
+}
+
+// Rebase a schedule so its intrinsic step 1 is `base` (src/lr.ts:108-112).
+static tgj::Value rebase_lr(tgj::Value s, long long base) {
+  if (s.kind == tgj::Value::Number) return s;
+  const tgj::Value* ss = s.get("startStep");
+  if (ss && !ss->null()) return s;
+  tgj::Value v;
+  v.kind = tgj::Value::Number;
+  v.number = (double)(base - 1);
+  bool set = false;
+  for (auto& m : s.members) if (m.first == "startStep") { m.second = v; set = true; }
+  if (!set) s.members.emplace_back("startStep", v);
+  return s;
+}
+
+// ---- IR ----------------------------------------------------------------------------------
+struct TInfo {
+  Dims shape;
+  Dt dt;
+  int64_t numel;
+  int src;  // producing op index
+};
+
+// A tensor as a strided view of a root tensor's storage (element strides, 4-byte elems).
+struct View {
+  int root;
+  Dims dims, strides;
+  bool contiguous() const {
+    Dims c = contiguous_strides(dims);
+    for (size_t i = 0; i < dims.size(); ++i) if (dims[i] != 1 && strides[i] != c[i]) return false;
+    return true;
+  }
+};
+
+struct Node {
+  std::string kind;   // kernel family, for profiling / description
+  int op = -1;        // IR op index it came from (the last one for fused nodes)
+  std::vector<int> reads, writes;   // storage roots
+  double flops = 0, bytes = 0;      // algorithmic work per launch
+  std::string shape;
+  std::function<void(hipStream_t)> launch;   // bound after allocation
+  std::function<std::function<void(hipStream_t)>()> bind;
+};
+
+class Runtime;
+
+class Runtime {
+ public:
+  Runtime(const char* json, Runtime* parent, bool plan_only = false);
+  ~Runtime();
+
+  // parameters
+  std::vector<std::string> param_names;
+  std::map<std::string, int> param_root;      // name -> tensor id of the param_input
+  int64_t param_numel(int i) const { return T_[param_root.at(param_names[i])].numel; }
+
+  void upload_params(int n, const char* const* names, const float* const* data, const int64_t* numel);
+  void download_params(int n, const char* const* names, float* const* data, const int64_t* numel);
+  float step(int n, const char* const* names, const void* const* data, const int64_t* nbytes, bool device);
+  void run(int n, const char* const* names, const void* const* data, const int64_t* nbytes, void* out, int64_t out_bytes);
+  void get_capture(const std::string& name, void* out, int64_t nbytes);
+  void reset_optimizer();
+  void set_lr(const char* json);
+  std::string describe();
+  void profile_nodes(int iters, double* ms, int64_t n);
+  double time_replays(int steps);
+
+  std::vector<std::string> capture_names;
+  std::vector<Runtime*> children;
+  Runtime* parent = nullptr;
+  bool destroyed = false;
+
+ private:
+  tgj::Value doc_;
+  std::vector<TInfo> T_;
+  std::vector<const tgj::Value*> ops_;
+  std::vector<std::string> kinds_;
+  std::vector<std::vector<int>> consumers_;
+  std::vector<View> view_;           // per tensor
+  std::vector<bool> virtual_;        // op not executed (view / folded pattern)
+  std::vector<bool> materialize_;    // permute output that needs its own storage
+  std::map<std::string, int> input_tid_, state_tid_;
+  std::vector<int> outputs_;
+  std::map<std::string, int> captures_;
+  std::vector<std::pair<int, std::string>> copy_writebacks_;  // (source tid, dest name) applied by copy
+  std::vector<Node> nodes_;
+
+  // optimizer
+  std::string opt_kind_;
+  const tgj::Value* opt_cfg_ = nullptr;
+  tgj::Value lr_;
+  long long t_ = 0;
+  bool uses_prng_ = false;
+  long long prng_counter_ = 0;
+
+  // device memory
+  hipStream_t stream_ = nullptr;
+  char* arena_ = nullptr;
+  size_t arena_bytes_ = 0;
+  std::vector<void*> ptr_;          // per root tensor
+  char* input_region_ = nullptr;    // device, contiguous tensor inputs
+  size_t input_region_bytes_ = 0;
+  std::map<int, size_t> input_offset_;   // input tid -> byte offset in region
+  char* staging_ = nullptr;         // pinned host mirror of the input region
+  float* loss_host_ = nullptr;      // pinned
+  float* workspace_ = nullptr;
+  size_t workspace_bytes_ = 0;
+  // fused Adam tables (device)
+  tgk::AdamTensor* adam_tensors_ = nullptr;
+  int64_t* adam_chunk_tensor_ = nullptr;
+  int64_t* adam_chunk_start_ = nullptr;
+  std::vector<int> state_roots_;
+
+  hipGraph_t graph_ = nullptr;
+  hipGraphExec_t graph_exec_ = nullptr;
+  bool plan_only_ = false;
+
+  bool is_leaf(int op) const {
+    const std::string& k = kinds_[op];
+    return k == "param_input" || k == "tensor_input" || k == "state_input";
+  }
+  int root(int t) const { return view_[t].root; }
+  void* dptr(int t) const { return ptr_[root(t)]; }
+  const tgj::Value& O(int op) const { return *ops_[op]; }
+  int fld(int op, const char* f) const { return O(op).at(f).i32(); }
+
+  void analyse();
+  void compute_views();
+  void lower();
+  void allocate();
+  void bind_all();
+  void launch_all(hipStream_t st);
+  void upload_inputs(int n, const char* const* names, const void* const* data, const int64_t* nbytes, bool device);
+  void ensure_graph();
+  void apply_copy_writebacks(hipStream_t st);
+
+  // GEMM lowering helpers
+  bool gemm_operand(int t, int which, const Dims& op_shape, bool batched, int64_t& M, int64_t& K, int64_t& batch,
+                    int64_t& bdiv, int64_t& s0, int64_t& s1, int64_t& sr, int64_t& sc, bool transposeOk);
+  void add_node(Node n) { nodes_.push_back(std::move(n)); }
+  void lower_op(int i);
+};
+
+// ---------------------------------------------------------------------------------------
+
+Runtime::Runtime(const char* json, Runtime* par, bool plan_only) : parent(par) {
+  try {
+    doc_ = tgj::parse(json);
+  } catch (std::exception& e) {
+    throw Error(TG_INVALID_ARGUMENT, e.what());
+  }
+  const tgj::Value& g = doc_.at("graph");
+  for (const auto& t : g.at("tensors").items) {
+    TInfo ti;
+    for (const auto& d : t.at("shape").items) ti.shape.push_back(d.i64());
+    ti.dt = parse_dt(t.at("dtype").str());
+    ti.numel = prod(ti.shape);
+    ti.src = -1;
+    T_.push_back(ti);
+  }
+  for (const auto& op : g.at("ops").items) {
+    ops_.push_back(&op);
+    kinds_.push_back(op.at("kind").str());
+  }
+  for (size_t i = 0; i < ops_.size(); ++i) {
+    int out = ops_[i]->at("out").i32();
+    if (out < 0 || out >= (int)T_.size()) throw Error(TG_INVALID_ARGUMENT, "IR: op output id out of range");
+    T_[out].src = (int)i;
+  }
+  for (const auto& o : g.at("outputs").items) outputs_.push_back(o.i32());
+  if (const tgj::Value* c = g.get("captures"))
+    for (const auto& m : c->members) { captures_[m.first] = m.second.i32(); capture_names.push_back(m.first); }
+  if (const tgj::Value* opt = doc_.get("optimizer"))
+    if (!opt->null()) {
+      opt_kind_ = opt->at("kind").str();
+      opt_cfg_ = &opt->at("config");
+      lr_ = opt_cfg_->at("lr");
+    }
+  if (parent && opt_cfg_) throw Error(TG_INVALID_ARGUMENT, "compileForward: a sibling graph cannot carry an optimizer");
+
+  plan_only_ = plan_only;
+  analyse();
+  compute_views();
+  lower();
+  if (!plan_only) hip_check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate");
+  allocate();
+  bind_all();   // in plan-only mode this still runs every launch's host-side bounds proof
+}
+
+Runtime::~Runtime() {
+  if (graph_exec_) hipGraphExecDestroy(graph_exec_);
+  if (graph_) hipGraphDestroy(graph_);
+  if (stream_) { hipStreamSynchronize(stream_); hipStreamDestroy(stream_); }
+  if (arena_) hipFree(arena_);
+  if (input_region_) hipFree(input_region_);
+  if (workspace_ && !plan_only_) hipFree(workspace_);
+  if (adam_tensors_) hipFree(adam_tensors_);
+  if (adam_chunk_tensor_) hipFree(adam_chunk_tensor_);
+  if (adam_chunk_start_) hipFree(adam_chunk_start_);
+  if (staging_) hipHostFree(staging_);
+  if (loss_host_) hipHostFree(loss_host_);
+}
+
+// Op -> input tensor ids, canonical order (src/ir.ts:356-395).
+static std::vector<int> op_inputs(const tgj::Value& op) {
+  static const std::map<std::string, std::vector<const char*>> F = {
+      {"randn", {"seed"}}, {"dropout", {"a", "seed"}}, {"categorical_last", {"a", "seed"}},
+      {"one_hot", {"indices"}}, {"where", {"cond", "a", "b"}}, {"relu_grad", {"x", "dy"}},
+      {"adam_update_m", {"m", "g"}}, {"adam_update_v", {"v", "g"}},
+      {"adam_update_p", {"p", "mNew", "vNew", "lrt", "decayShrinkTensor"}},
+      {"conv2d", {"input", "weight"}}, {"conv2d_input_grad", {"weight", "dy"}},
+      {"conv2d_weight_grad", {"input", "dy"}}, {"max_pool_2d", {"input"}},
+      {"max_pool_2d_grad", {"input", "dy"}},
+      {"param_input", {}}, {"tensor_input", {}}, {"state_input", {}}, {"arange", {}},
+      {"const_scalar", {}}, {"const_fill", {}},
+  };
+  const std::string& k = op.at("kind").str();
+  std::vector<int> ids;
+  if (k == "concat") {
+    for (const auto& x : op.at("inputs").items) ids.push_back(x.i32());
+    return ids;
+  }
+  auto it = F.find(k);
+  if (it != F.end()) {
+    for (const char* f : it->second) {
+      const tgj::Value& v = op.at(f);
+      if (!v.null()) ids.push_back(v.i32());
+    }
+    return ids;
+  }
+  if (op.get("b")) { ids.push_back(op.at("a").i32()); ids.push_back(op.at("b").i32()); return ids; }
+  ids.push_back(op.at("a").i32());
+  return ids;
+}
+
+void Runtime::analyse() {
+  consumers_.assign(T_.size(), {});
+  for (size_t i = 0; i < ops_.size(); ++i) {
+    for (int id : op_inputs(*ops_[i])) {
+      if (id < 0 || id >= (int)T_.size()) throw Error(TG_INVALID_ARGUMENT, "IR: op input id out of range");
+      consumers_[id].push_back((int)i);
+    }
+    const std::string& k = kinds_[i];
+    int out = ops_[i]->at("out").i32();
+    if (k == "param_input") {
+      const std::string& nm = ops_[i]->at("name").str();
+      param_names.push_back(nm);
+      param_root[nm] = out;
+    } else if (k == "tensor_input") {
+      input_tid_[ops_[i]->at("name").str()] = out;
+      if (ops_[i]->at("name").str() == "__prngSeed") uses_prng_ = true;
+    } else if (k == "state_input") {
+      state_tid_[ops_[i]->at("name").str()] = out;
+    }
+  }
+}
+
+// Views: every tensor is (root storage, dims, strides). Aliasing ops inherit their
+// input's root; permutes are strided views until a consumer needs contiguous data.
+void Runtime::compute_views() {
+  const size_t n = T_.size();
+  view_.resize(n);
+  virtual_.assign(ops_.size(), false);
+  materialize_.assign(n, false);
+  for (size_t t = 0; t < n; ++t) view_[t] = View{(int)t, T_[t].shape, contiguous_strides(T_[t].shape)};
+
+  // Leading (batch) dims of a GEMM operand view must merge into at most two strided
+  // dims for the kernel's two-level batch index.
+  auto gemm_view_ok = [&](const View& v) {
+    if (v.dims.size() < 2) return false;
+    Dims d3, s3;
+    for (size_t i = 0; i + 2 < v.dims.size(); ++i) {
+      if (v.dims[i] == 1) continue;
+      if (!d3.empty() && s3.back() == v.strides[i] * v.dims[i]) { d3.back() *= v.dims[i]; s3.back() = v.strides[i]; }
+      else { d3.push_back(v.dims[i]); s3.push_back(v.strides[i]); }
+    }
+    return d3.size() <= 2;
+  };
+  auto consumer_needs_contiguous = [&](int t, const View& v) {
+    for (int c : consumers_[t]) {
+      const std::string& k = kinds_[c];
+      if (k == "permute") continue;   // composes strides
+      if (k == "matmul" || k == "matmul_batched") {
+        if (!gemm_view_ok(v)) return true;
+        continue;
+      }
+      if (k == "add" || k == "sub" || k == "mul" || k == "div" || k == "min" || k == "max" || k == "less" ||
+          k == "greater" || k == "broadcast_to")
+        continue;   // strided element-wise kernels
+      return true;
+    }
+    for (int o : outputs_) if (o == t) return true;
+    for (auto& c : captures_) if (c.second == t) return true;
+    return false;
+  };
+
+  for (size_t i = 0; i < ops_.size(); ++i) {
+    const std::string& k = kinds_[i];
+    int out = ops_[i]->at("out").i32();
+    if (k == "reshape" || k == "stop_gradient") {
+      int a = ops_[i]->at("a").i32();
+      const View& va = view_[a];
+      if (va.contiguous()) {
+        view_[out] = View{va.root, T_[out].shape, contiguous_strides(T_[out].shape)};
+        virtual_[i] = true;
+      }
+    } else if ((k == "sum_to_shape" || k == "broadcast_to") &&
+               T_[ops_[i]->at("a").i32()].shape == T_[out].shape) {
+      int a = ops_[i]->at("a").i32();
+      if (view_[a].contiguous()) {
+        view_[out] = View{view_[a].root, T_[out].shape, contiguous_strides(T_[out].shape)};
+        virtual_[i] = true;
+      }
+    } else if (k == "permute") {
+      int a = ops_[i]->at("a").i32();
+      const View& va = view_[a];
+      std::vector<int64_t> perm;
+      for (const auto& p : ops_[i]->at("perm").items) perm.push_back(p.i64());
+      View v{va.root, {}, {}};
+      for (size_t d = 0; d < perm.size(); ++d) {
+        v.dims.push_back(va.dims[perm[d]]);
+        v.strides.push_back(va.strides[perm[d]]);
+      }
+      if (!consumer_needs_contiguous(out, v) && !v.contiguous()) {
+        view_[out] = v;
+        virtual_[i] = true;
+      } else if (v.contiguous()) {
+        view_[out] = View{va.root, T_[out].shape, contiguous_strides(T_[out].shape)};
+        virtual_[i] = true;
+      } else {
+        materialize_[out] = true;
+      }
+    }
+  }
+}
+
+// Express operand `t` of a GEMM as [batch, rows, cols] with rows/cols strides and a
+// two-level batch decomposition. `op_shape` is the IR shape of the operand.
+bool Runtime::gemm_operand(int t, int which, const Dims& op_shape, bool batched, int64_t& R, int64_t& C,
+                           int64_t& batch, int64_t& bdiv, int64_t& s0, int64_t& s1, int64_t& sr, int64_t& sc,
+                           bool) {
+  (void)which;
+  const View& v = view_[t];
+  const int r = (int)v.dims.size();
+  R = v.dims[r - 2];
+  C = v.dims[r - 1];
+  sr = v.strides[r - 2];
+  sc = v.strides[r - 1];
+  // leading dims
+  Dims ld(v.dims.begin(), v.dims.end() - 2), ls(v.strides.begin(), v.strides.end() - 2);
+  // drop size-1 dims
+  Dims d2, s2;
+  for (size_t i = 0; i < ld.size(); ++i) if (ld[i] != 1) { d2.push_back(ld[i]); s2.push_back(ls[i]); }
+  // merge adjacent dims with compatible strides
+  Dims d3, s3;
+  for (size_t i = 0; i < d2.size(); ++i) {
+    if (!d3.empty() && s3.back() == s2[i] * d2[i]) { d3.back() *= d2[i]; s3.back() = s2[i]; }
+    else { d3.push_back(d2[i]); s3.push_back(s2[i]); }
+  }
+  (void)op_shape;
+  (void)batched;
+  batch = prod(d3);
+  if (d3.size() == 0) { bdiv = 1; s0 = 0; s1 = 0; return true; }
+  if (d3.size() == 1) { bdiv = 1; s0 = s3[0]; s1 = 0; return true; }
+  if (d3.size() == 2) { bdiv = d3[1]; s0 = s3[0]; s1 = s3[1]; return true; }
+  return false;
+}
+
+void Runtime::lower() {
+  // Fused Adam: collect adam_update_p ops and their m / v producers.
+  std::vector<int> adam_p_ops;
+  for (size_t i = 0; i < ops_.size(); ++i) if (kinds_[i] == "adam_update_p") adam_p_ops.push_back((int)i);
+  std::set<int> adam_ops;
+  std::set<int> fused_wb_sources;
+  for (int pi : adam_p_ops) {
+    int mNew = fld(pi, "mNew"), vNew = fld(pi, "vNew"), p = fld(pi, "p");
+    int mo = T_[mNew].src, vo = T_[vNew].src;
+    if (kinds_[mo] != "adam_update_m" || kinds_[vo] != "adam_update_v" || kinds_[T_[p].src] != "param_input" ||
+        kinds_[T_[fld(mo, "m")].src] != "state_input" || kinds_[T_[fld(vo, "v")].src] != "state_input")
+      throw Error(TG_INVALID_ARGUMENT, "IR: adam_update_p is not fed by adam_update_m/v of state inputs");
+    adam_ops.insert(pi); adam_ops.insert(mo); adam_ops.insert(vo);
+    fused_wb_sources.insert(ops_[pi]->at("out").i32());
+    fused_wb_sources.insert(mNew);
+    fused_wb_sources.insert(vNew);
+  }
+  if (const tgj::Value* wb = doc_.get("writebacks")) {
+    for (const auto& w : wb->items) {
+      int src = w.at("source").i32();
+      if (fused_wb_sources.count(src)) continue;
+      copy_writebacks_.emplace_back(src, w.at("destName").str());
+    }
+  }
+
+  for (size_t i = 0; i < ops_.size(); ++i) {
+    if (is_leaf((int)i) || virtual_[i]) continue;
+    if (adam_ops.count((int)i)) continue;
+    lower_op((int)i);
+  }
+
+  // Drop nodes whose results nobody reads (e.g. a one_hot consumed only by the
+  // gather / scatter patterns, which read its indices instead).
+  std::set<int> keep;
+  for (int o : outputs_) keep.insert(root(o));
+  for (auto& c : captures_) keep.insert(root(c.second));
+  for (auto& w : copy_writebacks_) keep.insert(root(w.first));
+  for (bool changed = true; changed;) {
+    changed = false;
+    std::set<int> read;
+    for (auto& n : nodes_) read.insert(n.reads.begin(), n.reads.end());
+    for (int ai : adam_p_ops) {
+      int mo = T_[fld(ai, "mNew")].src;
+      read.insert(root(fld(mo, "g")));
+      read.insert(root(fld(ai, "lrt")));
+      const tgj::Value& ds = O(ai).at("decayShrinkTensor");
+      if (!ds.null()) read.insert(root(ds.i32()));
+    }
+    for (size_t q = 0; q < nodes_.size(); ++q) {
+      bool needed = false;
+      for (int w : nodes_[q].writes) if (read.count(w) || keep.count(w)) needed = true;
+      if (!needed) { nodes_.erase(nodes_.begin() + q); changed = true; break; }
+    }
+  }
+
+  if (!adam_p_ops.empty()) {
+    Node n;
+    n.kind = "adam_multi";
+    n.op = adam_p_ops.back();
+    double elems = 0;
+    for (int pi : adam_p_ops) {
+      int mo = T_[fld(pi, "mNew")].src, vo = T_[fld(pi, "vNew")].src;
+      n.reads.push_back(root(fld(mo, "g")));
+      n.reads.push_back(root(fld(pi, "p")));
+      n.reads.push_back(root(fld(mo, "m")));
+      n.reads.push_back(root(fld(vo, "v")));
+      n.reads.push_back(root(fld(pi, "lrt")));
+      const tgj::Value& ds = O(pi).at("decayShrinkTensor");
+      if (!ds.null()) n.reads.push_back(root(ds.i32()));
+      elems += (double)T_[fld(pi, "p")].numel;
+    }
+    n.bytes = 28.0 * elems;
+    n.shape = std::to_string(adam_p_ops.size()) + " tensors, " + std::to_string((long long)elems) + " params";
+    std::vector<int> pops = adam_p_ops;
+    n.bind = [this, pops]() -> std::function<void(hipStream_t)> {
+      std::vector<tgk::AdamTensor> host;
+      std::vector<int64_t> ct, cs;
+      double b1 = 0.9, b2 = 0.999, eps = 1e-8;
+      const float* lrt = nullptr;
+      for (size_t q = 0; q < pops.size(); ++q) {
+        int pi = pops[q];
+        int mo = T_[fld(pi, "mNew")].src, vo = T_[fld(pi, "vNew")].src;
+        b1 = O(mo).at("beta1").num();
+        b2 = O(vo).at("beta2").num();
+        eps = O(pi).at("eps").num();
+        lrt = (const float*)dptr(fld(pi, "lrt"));
+        const tgj::Value& ds = O(pi).at("decayShrinkTensor");
+        tgk::AdamTensor at{};
+        at.p = (float*)dptr(fld(pi, "p"));
+        at.m = (float*)dptr(fld(mo, "m"));
+        at.v = (float*)dptr(fld(vo, "v"));
+        int g = fld(mo, "g");
+        if (!view_[g].contiguous()) throw Error(TG_INTERNAL, "adam: gradient is not contiguous");
+        at.g = (const float*)dptr(g);
+        at.n = T_[fld(pi, "p")].numel;
+        if (T_[fld(mo, "m")].numel != at.n || T_[fld(vo, "v")].numel != at.n || T_[g].numel != at.n ||
+            T_[root(g)].numel < at.n)
+          throw Error(TG_INVALID_ARGUMENT, "adam: p / m / v / g size mismatch");
+        at.shrink = ds.null() ? O(pi).at("decayShrink").num() : 1.0;
+        at.shrink_ptr = ds.null() ? nullptr : (const float*)dptr(ds.i32());
+        host.push_back(at);
+        for (int64_t s = 0; s < at.n; s += 1024) { ct.push_back((int64_t)q); cs.push_back(s); }
+      }
+      if (plan_only_) return [](hipStream_t) {};
+      hip_check(hipMalloc(&adam_tensors_, host.size() * sizeof(tgk::AdamTensor)), "hipMalloc");
+      hip_check(hipMalloc(&adam_chunk_tensor_, ct.size() * sizeof(int64_t)), "hipMalloc");
+      hip_check(hipMalloc(&adam_chunk_start_, cs.size() * sizeof(int64_t)), "hipMalloc");
+      hip_check(hipMemcpy(adam_tensors_, host.data(), host.size() * sizeof(tgk::AdamTensor), hipMemcpyHostToDevice), "hipMemcpy");
+      hip_check(hipMemcpy(adam_chunk_tensor_, ct.data(), ct.size() * sizeof(int64_t), hipMemcpyHostToDevice), "hipMemcpy");
+      hip_check(hipMemcpy(adam_chunk_start_, cs.data(), cs.size() * sizeof(int64_t), hipMemcpyHostToDevice), "hipMemcpy");
+      tgk::AdamHyper h{b1, 1 - b1, b2, 1 - b2, eps};
+      int count = (int)host.size();
+      int64_t nch = (int64_t)ct.size();
+      auto* tens = adam_tensors_;
+      auto* cT = adam_chunk_tensor_;
+      auto* cS = adam_chunk_start_;
+      return [=](hipStream_t st) { tgk::adam_multi(tens, count, cT, cS, nch, lrt, h, st); };
+    };
+    add_node(std::move(n));
+  }
+}
+
+static std::string shape_str(const Dims& d) {
+  std::string s = "[";
+  for (size_t i = 0; i < d.size(); ++i) s += (i ? "," : "") + std::to_string(d[i]);
+  return s + "]";
+}
+
+void Runtime::lower_op(int i) {
+  const std::string& k = kinds_[i];
+  const tgj::Value& op = O(i);
+  const int out = op.at("out").i32();
+  const TInfo& to = T_[out];
+  Node n;
+  n.kind = k;
+  n.op = i;
+  n.writes.push_back(root(out));
+  n.shape = shape_str(to.shape);
+  auto rd = [&](int t) { n.reads.push_back(root(t)); };
+
+  // Broadcast strides of operand view `t` against output dims (right-aligned; size-1 axes
+  // of the operand get stride 0).
+  auto bstrides = [&](int t, const Dims& od) {
+    const View& v = view_[t];
+    Dims s(od.size(), 0);
+    int off = (int)od.size() - (int)v.dims.size();
+    for (size_t d = 0; d < v.dims.size(); ++d) s[off + d] = v.dims[d] == 1 ? 0 : v.strides[d];
+    return s;
+  };
+  auto make_strided = [&](const Dims& od, const Dims& a, const Dims& b, const Dims& c) {
+    tgk::Strided sp{};
+    // Drop size-1 output dims and merge dims that are contiguous in every operand.
+    Dims dd, s0, s1, s2;
+    for (size_t d = 0; d < od.size(); ++d) {
+      if (od[d] == 1) continue;
+      int64_t x = a.empty() ? 0 : a[d], y = b.empty() ? 0 : b[d], z = c.empty() ? 0 : c[d];
+      if (!dd.empty() && s0.back() == x * od[d] && s1.back() == y * od[d] && s2.back() == z * od[d]) {
+        dd.back() *= od[d]; s0.back() = x; s1.back() = y; s2.back() = z;
+      } else {
+        dd.push_back(od[d]); s0.push_back(x); s1.push_back(y); s2.push_back(z);
+      }
+    }
+    if (dd.size() > (size_t)tgk::kMaxRank) throw Error(TG_INTERNAL, "rank too large for strided kernel");
+    sp.rank = (int)dd.size();
+    for (size_t d = 0; d < dd.size(); ++d) { sp.dims[d] = dd[d]; sp.s0[d] = s0[d]; sp.s1[d] = s1[d]; sp.s2[d] = s2[d]; }
+    return sp;
+  };
+  auto need_contig = [&](int t) {
+    if (!view_[t].contiguous()) throw Error(TG_INTERNAL, "op '" + k + "' needs a contiguous operand #" + std::to_string(t));
+  };
+
+  static const std::map<std::string, int> binops = {{"add", tgk::B_ADD}, {"sub", tgk::B_SUB}, {"mul", tgk::B_MUL},
+                                                    {"div", tgk::B_DIV}, {"min", tgk::B_MIN}, {"max", tgk::B_MAX},
+                                                    {"less", tgk::B_LESS}, {"greater", tgk::B_GREATER}};
+  static const std::map<std::string, int> unops = {
+      {"sqrt", tgk::U_SQRT}, {"rsqrt", tgk::U_RSQRT}, {"log", tgk::U_LOG}, {"exp", tgk::U_EXP},
+      {"relu", tgk::U_RELU}, {"neg", tgk::U_NEG}, {"abs", tgk::U_ABS}, {"tanh", tgk::U_TANH},
+      {"sigmoid", tgk::U_SIGMOID}, {"erf", tgk::U_ERF}, {"sin", tgk::U_SIN}, {"cos", tgk::U_COS}};
+
+  if (binops.count(k)) {
+    int a = op.at("a").i32(), b = op.at("b").i32();
+    rd(a); rd(b);
+    int bop = binops.at(k);
+    n.bytes = 4.0 * (T_[a].numel + T_[b].numel + to.numel);
+    n.kind = "elementwise";
+    n.bind = [=]() -> std::function<void(hipStream_t)> {
+      tgk::Strided sp = make_strided(to.shape, bstrides(a, to.shape), bstrides(b, to.shape), {});
+      check_span("binary a", T_[root(a)].numel, 0, sp.dims, sp.s0, sp.rank);
+      check_span("binary b", T_[root(b)].numel, 0, sp.dims, sp.s1, sp.rank);
+      const void* pa = dptr(a); const void* pb = dptr(b); void* po = dptr(out);
+      int adt = kdt(T_[a].dt), bdt = kdt(T_[b].dt), odt = kdt(to.dt);
+      int64_t cnt = to.numel;
+      return [=](hipStream_t st) { tgk::binary(bop, pa, adt, pb, bdt, po, odt, sp, cnt, st); };
+    };
+  } else if (k == "mul_scalar" || k == "add_scalar") {
+    int a = op.at("a").i32();
+    need_contig(a); rd(a);
+    bool mul = k == "mul_scalar";
+    double s = op.at("scalar").num();
+    n.bytes = 8.0 * to.numel;
+    n.kind = "elementwise";
+    n.bind = [=]() -> std::function<void(hipStream_t)> {
+      const void* pa = dptr(a); float* po = (float*)dptr(out); int adt = kdt(T_[a].dt); int64_t cnt = to.numel;
+      return [=](hipStream_t st) { tgk::scalar_op(mul, pa, adt, s, po, cnt, st); };
+    };
+  } else if (unops.count(k)) {
+    int a = op.at("a").i32();
+    need_contig(a); rd(a);
+    int uop = unops.at(k);
+    n.bytes = 8.0 * to.numel;
+    n.kind = "elementwise";
+    n.bind = [=]() -> std::function<void(hipStream_t)> {
+      const float* pa = (const float*)dptr(a); float* po = (float*)dptr(out); int64_t cnt = to.numel;
+      return [=](hipStream_t st) { tgk::unary(uop, pa, po, cnt, st); };
+    };
+  } else if (k == "relu_grad") {
+    int x = op.at("x").i32(), dy = op.at("dy").i32();
+    need_contig(x); need_contig(dy); rd(x); rd(dy);
+    n.bytes = 12.0 * to.numel;
+    n.kind = "elementwise";
+    n.bind = [=]() -> std::function<void(hipStream_t)> {
+      const float* px = (const float*)dptr(x); const float* pd = (const float*)dptr(dy); float* po = (float*)dptr(out);
+      int64_t cnt = to.numel;
+      return [=](hipStream_t st) { tgk::relu_grad(px, pd, po, cnt, st); };
+    };
+  } else if (k == "where") {
+    int c = op.at("cond").i32(), a = op.at("a").i32(), b = op.at("b").i32();
+    rd(c); rd(a); rd(b);
+    n.bytes = 4.0 * (T_[c].numel + T_[a].numel + T_[b].numel + to.numel);
+    n.kind = "elementwise";
+    n.bind = [=]() -> std::function<void(hipStream_t)> {
+      tgk::Strided sp = make_strided(to.shape, bstrides(c, to.shape), bstrides(a, to.shape), bstrides(b, to.shape));
+      check_span("where cond", T_[root(c)].numel, 0, sp.dims, sp.s0, sp.rank);
+      check_span("where a", T_[root(a)].numel, 0, sp.dims, sp.s1, sp.rank);
+      check_span("where b", T_[root(b)].numel, 0, sp.dims, sp.s2, sp.rank);
+      const int32_t* pc = (const int32_t*)dptr(c); const void* pa = dptr(a); const void* pb = dptr(b);
+      void* po = dptr(out); int dt = kdt(to.dt); int64_t cnt = to.numel;
+      return [=](hipStream_t st) { tgk::where(pc, pa, pb, dt, po, sp, cnt, st); };
+    };
+  } else if (k == "where_causal") {
+    int a = op.at("a").i32();
+    need_contig(a); rd(a);
+    double fill = op.at("fillValue").num();
+    int64_t D = to.shape.back(), outer = to.numel / (D * D);
+    n.bytes = 8.0 * to.numel;
+    n.kind = "elementwise";
+    n.bind = [=]() -> std::function<void(hipStream_t)> {
+      const float* pa = (const float*)dptr(a); float* po = (float*)dptr(out);
+      return [=](hipStream_t st) { tgk::where_causal(pa, po, outer, D, fill, st); };
+    };
+  } else if (k == "const_scalar" || k == "const_fill") {
+    double v = op.at("value").num();
+    n.bytes = 4.0 * to.numel;
+    n.kind = "fill";
+    n.bind = [=]() -> std::function<void(hipStream_t)> {
+      void* po = dptr(out); int dt = kdt(to.dt); int64_t cnt = to.numel;
+      return [=](hipStream_t st) { tgk::fill(po, dt, v, cnt, st); };
+    };
+  } else if (k == "arange") {
+    n.bytes = 4.0 * to.numel;
+    n.kind = "fill";
+    n.bind = [=]() -> std::function<void(hipStream_t)> {
+      void* po = dptr(out); int dt = kdt(to.dt); int64_t cnt = to.numel;
+      return [=](hipStream_t st) { tgk::arange(po, dt, cnt, st); };
+    };
+  } else if (k == "one_hot") {
+    int idx = op.at("indices").i32();
+    need_contig(idx); rd(idx);
+    int64_t depth = op.at("depth").i64();
+    n.bytes = 4.0 * (T_[idx].numel + to.numel);
+    n.bind = [=]() -> std::function<void(hipStream_t)> {
+      const int32_t* pi = (const int32_t*)dptr(idx); void* po = dptr(out); int dt = kdt(to.dt);
+      int64_t rows = T_[idx].numel;
+      return [=](hipStream_t st) { tgk::one_hot(pi, rows, depth, po, dt, st); };
+    };
+  } else if (k == "dropout" || k == "randn" || k == "categorical_last") {
+    int seed = op.at("seed").i32();
+    rd(seed);
+    int64_t salt = op.at("salt").i64();
+    uint32_t sc = (uint32_t)(uint64_t)std::fmod((double)salt * 2654435761.0, 4294967296.0);
+    if (k == "dropout") {
+      int a = op.at("a").i32();
+      need_contig(a); rd(a);
+      double p = op.at("p").num();
+      n.bytes = 8.0 * to.numel;
+      n.kind = "elementwise";
+      n.bind = [=]() -> std::function<void(hipStream_t)> {
+        const float* pa = (const float*)dptr(a); float* po = (float*)dptr(out); const int32_t* ps = (const int32_t*)dptr(seed);
+        int64_t cnt = to.numel;
+        return [=](hipStream_t st) { tgk::dropout(pa, po, cnt, ps, sc, p, st); };
+      };
+    } else if (k == "randn") {
+      n.bytes = 4.0 * to.numel;
+      n.bind = [=]() -> std::function<void(hipStream_t)> {
+        float* po = (float*)dptr(out); const int32_t* ps = (const int32_t*)dptr(seed); int64_t cnt = to.numel;
+        return [=](hipStream_t st) { tgk::randn(po, cnt, ps, sc, st); };
+      };
+    } else {
+      int a = op.at("a").i32();
+      need_contig(a); rd(a);
+      int64_t D = T_[a].shape.back(), outer = T_[a].numel / D;
+      n.bytes = 4.0 * (T_[a].numel + to.numel);
+      n.bind = [=]() -> std::function<void(hipStream_t)> {
+        const float* pa = (const float*)dptr(a); int32_t* po = (int32_t*)dptr(out); const int32_t* ps = (const int32_t*)dptr(seed);
+        return [=](hipStream_t st) { tgk::categorical(pa, po, outer, D, ps, sc, st); };
+      };
+    }
+  } else if (k == "mean_last" || k == "sum_last" || k == "argmax_last" || k == "log_softmax_last" ||
+             k == "softmax_causal_last") {
+    int a = op.at("a").i32();
+    need_contig(a); rd(a);
+    if (T_[a].shape.empty()) throw Error(TG_INVALID_ARGUMENT, k + ": rank-0 input");
+    int64_t D = T_[a].shape.back(), outer = D > 0 ? T_[a].numel / D : 0;
+    if (k == "softmax_causal_last" && (T_[a].shape.size() < 2 || T_[a].shape[T_[a].shape.size() - 2] != D))
+      throw Error(TG_INVALID_ARGUMENT, "softmax_causal_last: last two axes must be square");
+    int64_t expect_out = (k == "log_softmax_last" || k == "softmax_causal_last") ? T_[a].numel : outer;
+    if (to.numel != expect_out) throw Error(TG_INVALID_ARGUMENT, k + ": output size mismatch");
+    n.bytes = 4.0 * (T_[a].numel + to.numel);
+    n.kind = (k == "log_softmax_last" || k == "softmax_causal_last") ? "softmax" : "reduce";
+    n.bind = [=]() -> std::function<void(hipStream_t)> {
+      const float* pa = (const float*)dptr(a); void* po = dptr(out);
+      if (k == "mean_last" || k == "sum_last") {
+        double div = k == "mean_last" ? (double)D : 1.0;
+        return [=](hipStream_t st) { tgk::row_sum(pa, (float*)po, outer, D, div, st); };
+      }
+      if (k == "argmax_last") return [=](hipStream_t st) { tgk::row_argmax(pa, (int32_t*)po, outer, D, st); };
+      if (k == "log_softmax_last") return [=](hipStream_t st) { tgk::log_softmax(pa, (float*)po, outer, D, st); };
+      int64_t mats = outer / D;
+      return [=](hipStream_t st) { tgk::softmax_causal(pa, (float*)po, mats, D, st); };
+    };
+  } else if (k == "permute" || k == "reshape" || k == "stop_gradient") {
+    // Materialise a strided view (a permute a consumer needs contiguous, or a reshape of
+    // a non-contiguous view).
+    int a = op.at("a").i32();
+    rd(a);
+    n.bytes = 8.0 * to.numel;
+    n.kind = "copy";
+    View src = view_[a];
+    if (k == "permute") {
+      std::vector<int64_t> perm;
+      for (const auto& p : op.at("perm").items) perm.push_back(p.i64());
+      View v{src.root, {}, {}};
+      for (size_t d = 0; d < perm.size(); ++d) { v.dims.push_back(src.dims[perm[d]]); v.strides.push_back(src.strides[perm[d]]); }
+      src = v;
+    }
+    // reshape of a non-contiguous view: iterate the source view in its own order.
+    n.bind = [=]() -> std::function<void(hipStream_t)> {
+      tgk::Strided sp = make_strided(src.dims, contiguous_strides(src.dims), src.strides, {});
+      check_span("copy dst", T_[root(out)].numel, 0, sp.dims, sp.s0, sp.rank);
+      check_span("copy src", T_[src.root].numel, 0, sp.dims, sp.s1, sp.rank);
+      void* po = dptr(out); const void* pa = ptr_[src.root]; int64_t cnt = to.numel;
+      return [=](hipStream_t st) { tgk::strided_copy(po, pa, sp, cnt, st); };
+    };
+  } else if (k == "broadcast_to") {
+    int a = op.at("a").i32();
+    rd(a);
+    n.bytes = 4.0 * (T_[a].numel + to.numel);
+    n.kind = "copy";
+    n.bind = [=]() -> std::function<void(hipStream_t)> {
+      tgk::Strided sp = make_strided(to.shape, contiguous_strides(to.shape), bstrides(a, to.shape), {});
+      check_span("broadcast src", T_[root(a)].numel, 0, sp.dims, sp.s1, sp.rank);
+      void* po = dptr(out); const void* pa = dptr(a); int64_t cnt = to.numel;
+      return [=](hipStream_t st) { tgk::strided_copy(po, pa, sp, cnt, st); };
+    };
+  } else if (k == "slice_range" || k == "scatter_axis" || k == "concat") {
+    n.kind = "copy";
+    int64_t ax = op.at("axis").i64();
+    std::vector<int> ins;
+    if (k == "concat") for (const auto& x : op.at("inputs").items) ins.push_back(x.i32());
+    else ins.push_back(op.at("a").i32());
+    for (int t : ins) { need_contig(t); rd(t); }
+    int64_t total_in = 0;
+    for (int t : ins) total_in += T_[t].numel;
+    n.bytes = 4.0 * (total_in + to.numel);
+    int64_t start = k == "concat" ? 0 : op.at("start").i64();
+    n.bind = [=]() -> std::function<void(hipStream_t)> {
+      std::vector<std::function<void(hipStream_t)>> parts;
+      Dims os = contiguous_strides(to.shape);
+      if (k == "scatter_axis") {
+        void* po = dptr(out); int64_t cnt = to.numel;
+        parts.push_back([=](hipStream_t st) { tgk::fill(po, tgk::DT_F32, 0.0, cnt, st); });
+      }
+      int64_t off = 0;
+      for (int t : ins) {
+        const Dims& is = T_[t].shape;
+        Dims src_str = contiguous_strides(is);
+        if (k == "slice_range") {
+          // out[..., j, ...] = a[..., j + start, ...]
+          Dims s1 = src_str;
+          int64_t base = start * src_str[ax];
+          tgk::Strided sp = make_strided(to.shape, os, s1, {});
+          check_span("slice dst", T_[root(out)].numel, 0, sp.dims, sp.s0, sp.rank);
+          check_span("slice src", T_[root(t)].numel, base, sp.dims, sp.s1, sp.rank);
+          void* po = dptr(out); const float* pa = (const float*)dptr(t) + base; int64_t cnt = to.numel;
+          parts.push_back([=](hipStream_t st) { tgk::strided_copy(po, pa, sp, cnt, st); });
+        } else {
+          // out[..., j + offset, ...] = a[..., j, ...]
+          int64_t base = (k == "concat" ? off : start) * os[ax];
+          tgk::Strided sp = make_strided(is, os, src_str, {});
+          check_span("concat dst", T_[root(out)].numel, base, sp.dims, sp.s0, sp.rank);
+          check_span("concat src", T_[root(t)].numel, 0, sp.dims, sp.s1, sp.rank);
+          float* po = (float*)dptr(out) + base; const void* pa = dptr(t); int64_t cnt = T_[t].numel;
+          parts.push_back([=](hipStream_t st) { tgk::strided_copy(po, pa, sp, cnt, st); });
+          off += is[ax];
+        }
+      }
+      return [=](hipStream_t st) { for (auto& f : parts) f(st); };
+    };
+  } else if (k == "sum_to_shape") {
+    int a = op.at("a").i32();
+    need_contig(a); rd(a);
+    const Dims& as = T_[a].shape;
+    n.bytes = 4.0 * (T_[a].numel + to.numel);
+    n.kind = "reduce";
+    n.bind = [=]() -> std::function<void(hipStream_t)> {
+      Dims ast = contiguous_strides(as);
+      int rdiff = (int)as.size() - (int)to.shape.size();
+      Dims cd, cs, rdd, rs;
+      for (int d = 0; d < (int)as.size(); ++d) {
+        bool reduced = d < rdiff || (to.shape[d - rdiff] == 1 && as[d] != 1);
+        if (as[d] == 1) continue;
+        if (reduced) { rdd.push_back(as[d]); rs.push_back(ast[d]); }
+        else { cd.push_back(as[d]); cs.push_back(ast[d]); }
+      }
+      tgk::Strided cells = make_strided(cd, cs, {}, {});
+      tgk::Strided red = make_strided(rdd, rs, {}, {});
+      int64_t ncells = prod(cd), nred = prod(rdd);
+      if (ncells != to.numel) throw Error(TG_INTERNAL, "sum_to_shape: cell count mismatch");
+      {
+        int64_t dd[2 * tgk::kMaxRank], ss[2 * tgk::kMaxRank];
+        int r = 0;
+        for (int q = 0; q < cells.rank; ++q) { dd[r] = cells.dims[q]; ss[r++] = cells.s0[q]; }
+        for (int q = 0; q < red.rank; ++q) { dd[r] = red.dims[q]; ss[r++] = red.s0[q]; }
+        check_span("sum_to_shape src", T_[root(a)].numel, 0, dd, ss, r);
+      }
+      const float* pa = (const float*)dptr(a); float* po = (float*)dptr(out);
+      return [=](hipStream_t st) { tgk::sum_to_shape(pa, po, cells, red, ncells, nred, st); };
+    };
+  } else if (k == "matmul" || k == "matmul_batched") {
+    int a = op.at("a").i32(), b = op.at("b").i32();
+    bool batched = k == "matmul_batched";
+    const Dims& ash = T_[a].shape;
+    const Dims& bsh = T_[b].shape;
+    int64_t M = ash[ash.size() - 2], K = ash.back(), N = bsh.back();
+    int64_t batch = T_[a].numel / (M * K);
+    n.flops = 2.0 * (double)batch * M * N * K;
+    n.kind = "gemm";
+    n.shape = shape_str(ash) + "x" + shape_str(bsh);
+    // Pattern: embedding forward, one_hot(idx) @ table.
+    int asrc = T_[view_[a].root].src;
+    if (!batched && asrc >= 0 && kinds_[asrc] == "one_hot" && view_[a].contiguous() && view_[b].contiguous() &&
+        T_[view_[a].root].dt == F32) {
+      int idx = fld(asrc, "indices");
+      rd(idx); rd(b);
+      n.kind = "gather";
+      n.flops = 0;
+      int64_t rows = batch * M;
+      n.bytes = 4.0 * (rows + rows * N + rows * N);
+      n.bind = [=]() -> std::function<void(hipStream_t)> {
+        const int32_t* pi = (const int32_t*)dptr(idx); const float* pt = (const float*)dptr(b); float* po = (float*)dptr(out);
+        return [=](hipStream_t st) { tgk::gather_rows(pi, rows, pt, K, N, po, st); };
+      };
+      add_node(std::move(n));
+      return;
+    }
+    // Pattern: embedding gradient, transpose(one_hot(idx)) @ dy.
+    if (!batched && asrc >= 0 && kinds_[asrc] == "one_hot" && ash.size() == 2 && T_[view_[a].root].dt == F32) {
+      const View& va = view_[a];
+      int64_t rows = T_[fld(asrc, "indices")].numel, V = O(asrc).at("depth").i64();
+      if (va.dims.size() == 2 && va.dims[0] == V && va.dims[1] == rows && va.strides[0] == 1 && va.strides[1] == V &&
+          view_[b].contiguous()) {
+        int idx = fld(asrc, "indices");
+        rd(idx); rd(b);
+        n.kind = "scatter";
+        n.flops = 0;
+        n.bytes = 4.0 * (rows + rows * N + V * N);
+        workspace_bytes_ = std::max(workspace_bytes_, (size_t)(rows + V + 1) * 4 + 256);
+        n.bind = [=]() -> std::function<void(hipStream_t)> {
+          const int32_t* pi = (const int32_t*)dptr(idx); const float* pd = (const float*)dptr(b);
+          float* po = (float*)dptr(out);
+          int32_t* perm = (int32_t*)workspace_;
+          int32_t* offs = perm + rows;
+          return [=](hipStream_t st) { tgk::scatter_rows(pi, rows, pd, V, N, po, perm, offs, st); };
+        };
+        add_node(std::move(n));
+        return;
+      }
+    }
+    rd(a); rd(b);
+    int64_t Ra, Ca, ba, bda, sa0, sa1, sar, sac;
+    int64_t Rb, Cb, bb, bdb, sb0, sb1, sbr, sbc;
+    bool okA = gemm_operand(a, 0, ash, batched, Ra, Ca, ba, bda, sa0, sa1, sar, sac, true);
+    bool okB = gemm_operand(b, 1, bsh, batched, Rb, Cb, bb, bdb, sb0, sb1, sbr, sbc, true);
+    tgk::GemmDesc d{};
+    d.N = N; d.K = K;
+    if (!okA || !okB) throw Error(TG_INTERNAL, "gemm: operand view not expressible (" + n.shape + ")");
+    if (!batched) {
+      // A [..., M, K] @ B [K, N]: fold A's leading dims into M when they are uniformly
+      // strided with the rows; otherwise batch over them with B broadcast.
+      if (ba == 1 || (bda == 1 && sa0 == M * sar)) {
+        d.M = M * ba; d.batch = 1; d.bdiv = 1;
+        d.sAz0 = d.sAz1 = 0;
+        d.sCz0 = d.sCz1 = 0;
+      } else {
+        d.M = M; d.batch = ba; d.bdiv = bda;
+        d.sAz0 = sa0; d.sAz1 = sa1;
+        d.sCz0 = M * N * bda; d.sCz1 = M * N;
+      }
+      d.sAm = sar; d.sAk = sac;
+      d.sBz0 = d.sBz1 = 0; d.sBk = sbr; d.sBn = sbc;
+    } else {
+      // Batch dims of A and B must decompose identically.
+      if (ba != bb) throw Error(TG_INTERNAL, "gemm: batch mismatch");
+      d.M = M; d.batch = ba;
+      if (bda == bdb || ba == 1) {
+        d.bdiv = bda;
+        d.sAz0 = sa0; d.sAz1 = sa1; d.sBz0 = sb0; d.sBz1 = sb1;
+      } else if (bda == 1 && bdb != 1) {
+        // A collapsed to one batch dim; split it like B.
+        d.bdiv = bdb;
+        d.sAz0 = sa0 * bdb; d.sAz1 = sa0; d.sBz0 = sb0; d.sBz1 = sb1;
+      } else if (bdb == 1 && bda != 1) {
+        d.bdiv = bda;
+        d.sAz0 = sa0; d.sAz1 = sa1; d.sBz0 = sb0 * bda; d.sBz1 = sb0;
+      } else {
+        throw Error(TG_INTERNAL, "gemm: incompatible batch decompositions");
+      }
+      d.sAm = sar; d.sAk = sac; d.sBk = sbr; d.sBn = sbc;
+      d.sCz0 = M * N * d.bdiv; d.sCz1 = M * N;
+    }
+    d.sCm = N; d.sCn = 1;
+    int64_t ws = tgk::gemm_workspace_floats(d);
+    workspace_bytes_ = std::max(workspace_bytes_, (size_t)ws * 4);
+    n.bytes = 4.0 * (T_[a].numel + T_[b].numel + to.numel);
+    n.bind = [=]() -> std::function<void(hipStream_t)> {
+      {
+        int64_t nb0 = d.batch / d.bdiv;
+        int64_t da[4] = {nb0, d.bdiv, d.M, d.K}, sa[4] = {d.sAz0, d.sAz1, d.sAm, d.sAk};
+        int64_t db[4] = {nb0, d.bdiv, d.K, d.N}, sb[4] = {d.sBz0, d.sBz1, d.sBk, d.sBn};
+        int64_t dc[4] = {nb0, d.bdiv, d.M, d.N}, sc[4] = {d.sCz0, d.sCz1, d.sCm, d.sCn};
+        if (d.batch % d.bdiv != 0) throw Error(TG_INTERNAL, "gemm: batch not divisible by bdiv");
+        check_span("gemm A", T_[root(a)].numel, 0, da, sa, 4);
+        check_span("gemm B", T_[root(b)].numel, 0, db, sb, 4);
+        check_span("gemm C", T_[root(out)].numel, 0, dc, sc, 4);
+        if (d.batch * d.M * d.N != to.numel) throw Error(TG_INTERNAL, "gemm: output size mismatch");
+      }
+      tgk::GemmDesc g = d;
+      g.A = (const float*)dptr(a);
+      g.B = (const float*)dptr(b);
+      g.C = (float*)dptr(out);
+      float* w = workspace_;
+      return [=](hipStream_t st) { tgk::gemm(g, w, st); };
+    };
+  } else if (k == "conv2d" || k == "conv2d_input_grad" || k == "conv2d_weight_grad") {
+    tgk::ConvDesc c{};
+    c.sH = op.at("strideH").i64(); c.sW = op.at("strideW").i64();
+    c.pH = op.at("padH").i64(); c.pW = op.at("padW").i64(); c.G = op.at("groups").i64();
+    int x = -1, w = -1, dy = -1;
+    if (k == "conv2d") { x = op.at("input").i32(); w = op.at("weight").i32(); }
+    else if (k == "conv2d_input_grad") { w = op.at("weight").i32(); dy = op.at("dy").i32(); }
+    else { x = op.at("input").i32(); dy = op.at("dy").i32(); }
+    Dims xs = k == "conv2d_input_grad" ? to.shape : T_[x].shape;
+    Dims ws = k == "conv2d_weight_grad" ? to.shape : T_[w].shape;
+    Dims ys = k == "conv2d" ? to.shape : T_[dy].shape;
+    c.B = xs[0]; c.Cin = xs[1]; c.H = xs[2]; c.W = xs[3];
+    c.Cout = ws[0]; c.CinPG = ws[1]; c.kH = ws[2]; c.kW = ws[3];
+    c.Ho = ys[2]; c.Wo = ys[3];
+    for (int t : {x, w, dy}) if (t >= 0) { need_contig(t); rd(t); }
+    if (x >= 0 && T_[x].numel != c.B * c.Cin * c.H * c.W) throw Error(TG_INVALID_ARGUMENT, "conv: input size mismatch");
+    if (w >= 0 && T_[w].numel != c.Cout * c.CinPG * c.kH * c.kW) throw Error(TG_INVALID_ARGUMENT, "conv: weight size mismatch");
+    if (dy >= 0 && T_[dy].numel != c.B * c.Cout * c.Ho * c.Wo) throw Error(TG_INVALID_ARGUMENT, "conv: dy size mismatch");
+    if (to.numel != (k == "conv2d" ? c.B * c.Cout * c.Ho * c.Wo : k == "conv2d_input_grad" ? c.B * c.Cin * c.H * c.W
+                                                                  : c.Cout * c.CinPG * c.kH * c.kW))
+      throw Error(TG_INVALID_ARGUMENT, "conv: output size mismatch");
+    if (c.G <= 0 || c.Cout % c.G != 0 || c.CinPG * c.G != c.Cin) throw Error(TG_INVALID_ARGUMENT, "conv: bad groups");
+    n.flops = 2.0 * c.B * c.Cout * c.Ho * c.Wo * c.CinPG * c.kH * c.kW;
+    n.bytes = 4.0 * (prod(xs) + prod(ws) + prod(ys));
+    n.kind = "conv";
+    n.shape = shape_str(xs) + "*" + shape_str(ws);
+    n.bind = [=]() -> std::function<void(hipStream_t)> {
+      float* po = (float*)dptr(out);
+      if (k == "conv2d") {
+        const float* px = (const float*)dptr(x); const float* pw = (const float*)dptr(w);
+        return [=](hipStream_t st) { tgk::conv2d(px, pw, po, c, st); };
+      }
+      if (k == "conv2d_input_grad") {
+        const float* pw = (const float*)dptr(w); const float* pd = (const float*)dptr(dy);
+        return [=](hipStream_t st) { tgk::conv2d_input_grad(pw, pd, po, c, st); };
+      }
+      const float* px = (const float*)dptr(x); const float* pd = (const float*)dptr(dy);
+      return [=](hipStream_t st) { tgk::conv2d_weight_grad(px, pd, po, c, nullptr, st); };
+    };
+  } else if (k == "max_pool_2d" || k == "max_pool_2d_grad") {
+    int x = op.at("input").i32();
+    need_contig(x); rd(x);
+    int dy = k == "max_pool_2d_grad" ? op.at("dy").i32() : -1;
+    if (dy >= 0) { need_contig(dy); rd(dy); }
+    tgk::PoolDesc p{};
+    const Dims& xs = T_[x].shape;
+    Dims ys = dy >= 0 ? T_[dy].shape : to.shape;
+    p.B = xs[0]; p.C = xs[1]; p.H = xs[2]; p.W = xs[3]; p.Ho = ys[2]; p.Wo = ys[3];
+    p.kH = op.at("kH").i64(); p.kW = op.at("kW").i64(); p.sH = op.at("strideH").i64(); p.sW = op.at("strideW").i64();
+    p.pH = op.at("padH").i64(); p.pW = op.at("padW").i64();
+    if (dy < 0 && to.numel != p.B * p.C * p.Ho * p.Wo) throw Error(TG_INVALID_ARGUMENT, "pool: output size mismatch");
+    if (dy >= 0 && (to.numel != prod(xs) || ys[0] != p.B || ys[1] != p.C)) throw Error(TG_INVALID_ARGUMENT, "pool grad: size mismatch");
+    n.bytes = 4.0 * (prod(xs) + prod(ys) + (dy >= 0 ? prod(xs) : 0));
+    n.kind = "pool";
+    n.bind = [=]() -> std::function<void(hipStream_t)> {
+      const float* px = (const float*)dptr(x); float* po = (float*)dptr(out);
+      if (dy < 0) return [=](hipStream_t st) { tgk::max_pool(px, po, p, st); };
+      const float* pd = (const float*)dptr(dy);
+      return [=](hipStream_t st) { tgk::max_pool_grad(px, pd, po, p, st); };
+    };
+  } else if (k == "adam_update_m" || k == "adam_update_v" || k == "adam_update_p") {
+    throw Error(TG_INTERNAL, "adam op outside the fused update");
+  } else {
+    throw Error(TG_INVALID_ARGUMENT, "IR: unsupported op kind '" + k + "'");
+  }
+  add_node(std::move(n));
+}
+
+// Device memory: persistent roots get dedicated regions; intermediates are pooled by
+// liveness over the node order (best fit). Tensor inputs live in one contiguous region
+// so a step uploads them with a single copy.
+void Runtime::allocate() {
+  const size_t nT = T_.size();
+  ptr_.assign(nT, nullptr);
+  std::vector<bool> persistent(nT, false), used(nT, false);
+  std::set<int> input_roots;
+  for (size_t i = 0; i < ops_.size(); ++i) {
+    int out = ops_[i]->at("out").i32();
+    const std::string& k = kinds_[i];
+    if (k == "param_input" || k == "state_input") persistent[out] = true;
+    if (k == "tensor_input") input_roots.insert(out);
+  }
+  for (int o : outputs_) persistent[root(o)] = true;
+  for (auto& c : captures_) persistent[root(c.second)] = true;
+  for (auto& w : copy_writebacks_) persistent[root(w.first)] = true;
+
+  std::vector<int> def(nT, -1), last(nT, -1);
+  for (size_t ni = 0; ni < nodes_.size(); ++ni) {
+    for (int r : nodes_[ni].writes) { if (def[r] < 0) def[r] = (int)ni; used[r] = true; }
+    for (int r : nodes_[ni].reads) { last[r] = std::max(last[r], (int)ni); used[r] = true; }
+  }
+  for (int o : outputs_) used[root(o)] = true;
+
+  // Layout: [persistent params/state/outputs][pooled intermediates]; inputs separately.
+  auto align = [](size_t x) { return (x + 255) & ~(size_t)255; };
+  size_t off = 0;
+  std::vector<size_t> offset(nT, 0);
+  std::vector<bool> placed(nT, false);
+  for (size_t t = 0; t < nT; ++t) {
+    if (root((int)t) != (int)t || input_roots.count((int)t)) continue;
+    if (persistent[t] && (used[t] || kinds_[T_[t].src] == "param_input" || kinds_[T_[t].src] == "state_input")) {
+      if (parent && kinds_[T_[t].src] == "param_input") continue;  // shared with parent
+      offset[t] = off; placed[t] = true;
+      off = align(off + std::max<int64_t>(4, T_[t].numel * 4));
+    }
+  }
+  // Pool: walk nodes in order; allocate each written intermediate root, free after last read.
+  struct Block { size_t off, size; };
+  std::vector<Block> free_list;
+  size_t pool_base = off, pool_end = off;
+  std::vector<std::vector<int>> frees_at(nodes_.size());
+  for (size_t t = 0; t < nT; ++t)
+    if (!persistent[t] && !input_roots.count((int)t) && root((int)t) == (int)t && used[t] && last[t] >= 0)
+      frees_at[last[t]].push_back((int)t);
+  std::vector<size_t> block_size(nT, 0);   // size of the pooled block a root occupies
+  for (size_t ni = 0; ni < nodes_.size(); ++ni) {
+    for (int r : nodes_[ni].writes) {
+      if (persistent[r] || input_roots.count(r) || placed[r]) continue;
+      size_t need = align(std::max<int64_t>(4, T_[r].numel * 4));
+      int best = -1;
+      for (size_t q = 0; q < free_list.size(); ++q)
+        if (free_list[q].size >= need && (best < 0 || free_list[q].size < free_list[best].size)) best = (int)q;
+      if (best >= 0) {
+        offset[r] = free_list[best].off;
+        block_size[r] = free_list[best].size;   // best fit never splits a block
+        free_list.erase(free_list.begin() + best);
+      } else {
+        offset[r] = pool_end;
+        block_size[r] = need;
+        pool_end += need;
+      }
+      placed[r] = true;
+      if (last[r] < 0) free_list.push_back({offset[r], block_size[r]});   // dead on write
+    }
+    for (int r : frees_at[ni]) free_list.push_back({offset[r], block_size[r]});
+  }
+  (void)pool_base;
+  arena_bytes_ = std::max<size_t>(pool_end, 256);
+  // Plan-only mode lays out a fake address space so every bind can run its checks.
+  char* fake = reinterpret_cast<char*>((uintptr_t)1 << 40);
+  if (plan_only_) arena_ = fake;
+  else hip_check(hipMalloc(&arena_, arena_bytes_), "hipMalloc(arena)");
+  for (size_t t = 0; t < nT; ++t) if (placed[t]) ptr_[t] = arena_ + offset[t];
+  if (parent) {
+    for (auto& kv : param_root) {
+      auto it = parent->param_root.find(kv.first);
+      if (it == parent->param_root.end()) throw Error(TG_INVALID_ARGUMENT, "compileForward: parent has no param '" + kv.first + "'");
+      if (parent->T_[it->second].numel != T_[kv.second].numel)
+        throw Error(TG_INVALID_ARGUMENT, "compileForward: param '" + kv.first + "' size differs from parent");
+      ptr_[kv.second] = parent->ptr_[it->second];
+    }
+  }
+  // Inputs.
+  size_t ioff = 0;
+  for (int t : input_roots) { input_offset_[t] = ioff; ioff = align(ioff + std::max<int64_t>(4, T_[t].numel * 4)); }
+  input_region_bytes_ = std::max<size_t>(ioff, 256);
+  if (plan_only_) {
+    input_region_ = fake + arena_bytes_ + 4096;
+    for (int t : input_roots) ptr_[t] = input_region_ + input_offset_[t];
+    workspace_ = reinterpret_cast<float*>(input_region_ + input_region_bytes_ + 4096);
+    arena_ = nullptr;
+    input_region_ = nullptr;
+    return;
+  }
+  hip_check(hipMalloc(&input_region_, input_region_bytes_), "hipMalloc(inputs)");
+  hip_check(hipHostMalloc(&staging_, input_region_bytes_, hipHostMallocDefault), "hipHostMalloc");
+  memset(staging_, 0, input_region_bytes_);
+  for (int t : input_roots) ptr_[t] = input_region_ + input_offset_[t];
+  hip_check(hipHostMalloc(&loss_host_, 256, hipHostMallocDefault), "hipHostMalloc");
+  if (workspace_bytes_) hip_check(hipMalloc(&workspace_, workspace_bytes_), "hipMalloc(workspace)");
+  // Zero everything once: params are uploaded by the caller, state starts at initValue.
+  hip_check(hipMemset(arena_, 0, arena_bytes_), "hipMemset");
+  for (auto& kv : state_tid_) {
+    int t = kv.second;
+    const tgj::Value& op = O(T_[t].src);
+    double iv = op.at("initValue").num();
+    if (iv != 0 && T_[t].dt == F32) tgk::fill(ptr_[t], tgk::DT_F32, iv, T_[t].numel, stream_);
+    state_roots_.push_back(t);
+  }
+  hip_check(hipStreamSynchronize(stream_), "hipStreamSynchronize");
+}
+
+void Runtime::bind_all() {
+  for (auto& n : nodes_) {
+    for (int r : n.reads) if (!ptr_[r]) throw Error(TG_INTERNAL, "unallocated operand in node " + n.kind);
+    for (int r : n.writes) if (!ptr_[r]) throw Error(TG_INTERNAL, "unallocated output in node " + n.kind);
+    n.launch = n.bind();
+  }
+}
+
+void Runtime::launch_all(hipStream_t st) {
+  for (auto& n : nodes_) n.launch(st);
+}
+
+void Runtime::apply_copy_writebacks(hipStream_t st) {
+  // Sources are computed from pre-step values, so all copies go after every kernel.
+  for (auto& w : copy_writebacks_) {
+    int dst = -1;
+    auto ip = param_root.find(w.second);
+    if (ip != param_root.end()) dst = ip->second;
+    auto is = state_tid_.find(w.second);
+    if (is != state_tid_.end()) dst = is->second;
+    if (dst < 0) throw Error(TG_INVALID_ARGUMENT, "writeback destination '" + w.second + "' not found");
+    int src = w.first;
+    if (T_[src].numel != T_[dst].numel) throw Error(TG_INVALID_ARGUMENT, "writeback size mismatch for " + w.second);
+    tgk::Strided sp{};
+    const View& v = view_[src];
+    Dims ds = contiguous_strides(v.dims);
+    sp.rank = (int)v.dims.size();
+    for (int d = 0; d < sp.rank; ++d) { sp.dims[d] = v.dims[d]; sp.s0[d] = ds[d]; sp.s1[d] = v.strides[d]; }
+    if (sp.rank == 0) { sp.rank = 1; sp.dims[0] = 1; sp.s0[0] = 1; sp.s1[0] = 1; }
+    tgk::strided_copy(ptr_[dst], ptr_[v.root], sp, T_[src].numel, st);
+  }
+}
+
+void Runtime::ensure_graph() {
+  if (graph_exec_) return;
+  hip_check(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+  try {
+    launch_all(stream_);
+    apply_copy_writebacks(stream_);
+  } catch (...) {
+    hipGraph_t g;
+    hipStreamEndCapture(stream_, &g);
+    if (g) hipGraphDestroy(g);
+    throw;
+  }
+  hip_check(hipStreamEndCapture(stream_, &graph_), "hipStreamEndCapture");
+  hip_check(hipGraphInstantiate(&graph_exec_, graph_, nullptr, nullptr, 0), "hipGraphInstantiate");
+}
+
+void Runtime::upload_inputs(int n, const char* const* names, const void* const* data, const int64_t* nbytes,
+                            bool device) {
+  std::set<std::string> seen;
+  std::vector<std::pair<int, int>> dev_copies;
+  for (int i = 0; i < n; ++i) {
+    std::string nm = names[i];
+    auto it = input_tid_.find(nm);
+    if (it == input_tid_.end()) continue;   // extra inputs are ignored, as a JS record would be
+    int t = it->second;
+    if (nbytes[i] != T_[t].numel * 4)
+      throw Error(TG_INVALID_ARGUMENT, "input '" + nm + "': expected " + std::to_string(T_[t].numel * 4) +
+                                           " bytes, got " + std::to_string(nbytes[i]));
+    if (!device) memcpy(staging_ + input_offset_[t], data[i], (size_t)nbytes[i]);
+    else dev_copies.emplace_back(i, t);
+    seen.insert(nm);
+  }
+  // Per-step scalars (src/worker.ts:187-214).
+  if (opt_cfg_) {
+    ++t_;
+    double lr_now = resolve_lr(lr_, (double)t_);
+    if (opt_kind_ == "adam") {
+      double b1 = opt_cfg_->at("beta1").num(), b2 = opt_cfg_->at("beta2").num();
+      float lrt = (float)(lr_now * std::sqrt(1 - std::pow(b2, (double)t_)) / (1 - std::pow(b1, (double)t_)));
+      int tid = input_tid_.at(opt_cfg_->at("lrtInputName").str());
+      memcpy(staging_ + input_offset_[tid], &lrt, 4);
+      seen.insert(opt_cfg_->at("lrtInputName").str());
+      const tgj::Value& dn = opt_cfg_->at("decayShrinkInputName");
+      if (!dn.null()) {
+        float ds = (float)(1 - lr_now * opt_cfg_->at("weightDecay").num());
+        memcpy(staging_ + input_offset_[input_tid_.at(dn.str())], &ds, 4);
+        seen.insert(dn.str());
+      }
+    } else {
+      float lr = (float)lr_now;
+      int tid = input_tid_.at(opt_cfg_->at("lrInputName").str());
+      memcpy(staging_ + input_offset_[tid], &lr, 4);
+      seen.insert(opt_cfg_->at("lrInputName").str());
+    }
+  }
+  if (uses_prng_) {
+    ++prng_counter_;
+    int32_t s = (int32_t)(uint32_t)prng_counter_;
+    memcpy(staging_ + input_offset_[input_tid_.at("__prngSeed")], &s, 4);
+    seen.insert("__prngSeed");
+  }
+  for (auto& kv : input_tid_)
+    if (!seen.count(kv.first)) throw Error(TG_INVALID_ARGUMENT, "missing input '" + kv.first + "'");
+  hip_check(hipMemcpyAsync(input_region_, staging_, input_region_bytes_, hipMemcpyHostToDevice, stream_), "hipMemcpyAsync(H2D)");
+  for (auto& c : dev_copies)
+    hip_check(hipMemcpyAsync(input_region_ + input_offset_[c.second], data[c.first], (size_t)nbytes[c.first],
+                             hipMemcpyDeviceToDevice, stream_), "hipMemcpyAsync(D2D)");
+}
+
+float Runtime::step(int n, const char* const* names, const void* const* data, const int64_t* nbytes, bool device) {
+  if (!opt_cfg_) throw Error(TG_INVALID_ARGUMENT, "step: graph has no optimizer (use run)");
+  upload_inputs(n, names, data, nbytes, device);
+  ensure_graph();
+  hip_check(hipGraphLaunch(graph_exec_, stream_), "hipGraphLaunch");
+  int lt = outputs_.at(0);
+  hip_check(hipMemcpyAsync(loss_host_, dptr(lt), 4, hipMemcpyDeviceToHost, stream_), "hipMemcpyAsync(D2H)");
+  hip_check(hipStreamSynchronize(stream_), "hipStreamSynchronize");
+  return loss_host_[0];
+}
+
+void Runtime::run(int n, const char* const* names, const void* const* data, const int64_t* nbytes, void* out,
+                  int64_t out_bytes) {
+  upload_inputs(n, names, data, nbytes, false);
+  ensure_graph();
+  hip_check(hipGraphLaunch(graph_exec_, stream_), "hipGraphLaunch");
+  int o = outputs_.at(0);
+  if (out_bytes != T_[o].numel * 4) throw Error(TG_INVALID_ARGUMENT, "run: output buffer has the wrong size");
+  if (!view_[o].contiguous()) throw Error(TG_INTERNAL, "run: output is not contiguous");
+  hip_check(hipMemcpyAsync(out, dptr(o), (size_t)out_bytes, hipMemcpyDeviceToHost, stream_), "hipMemcpyAsync(D2H)");
+  hip_check(hipStreamSynchronize(stream_), "hipStreamSynchronize");
+}
+
+void Runtime::get_capture(const std::string& name, void* out, int64_t nbytes) {
+  auto it = captures_.find(name);
+  if (it == captures_.end()) throw Error(TG_INVALID_ARGUMENT, "capture '" + name + "' not registered");
+  int t = it->second;
+  if (nbytes != T_[t].numel * 4) throw Error(TG_INVALID_ARGUMENT, "capture '" + name + "': wrong byte size");
+  hip_check(hipMemcpy(out, dptr(t), (size_t)nbytes, hipMemcpyDeviceToHost), "hipMemcpy(D2H)");
+}
+
+void Runtime::upload_params(int n, const char* const* names, const float* const* data, const int64_t* numel) {
+  std::set<std::string> seen;
+  for (int i = 0; i < n; ++i) {
+    auto it = param_root.find(names[i]);
+    if (it == param_root.end()) throw Error(TG_INVALID_ARGUMENT, std::string("uploadParams: unknown param '") + names[i] + "'");
+    if (numel[i] != T_[it->second].numel)
+      throw Error(TG_INVALID_ARGUMENT, std::string("uploadParams: '") + names[i] + "' expected " +
+                                           std::to_string(T_[it->second].numel) + " floats, got " + std::to_string(numel[i]));
+    seen.insert(names[i]);
+  }
+  for (auto& nm : param_names)
+    if (!seen.count(nm)) throw Error(TG_INVALID_ARGUMENT, "uploadParams: missing param '" + nm + "'");
+  for (int i = 0; i < n; ++i)
+    hip_check(hipMemcpy(ptr_[param_root.at(names[i])], data[i], (size_t)numel[i] * 4, hipMemcpyHostToDevice), "hipMemcpy(H2D)");
+}
+
+void Runtime::download_params(int n, const char* const* names, float* const* data, const int64_t* numel) {
+  hip_check(hipStreamSynchronize(stream_), "hipStreamSynchronize");
+  for (int i = 0; i < n; ++i) {
+    auto it = param_root.find(names[i]);
+    if (it == param_root.end()) throw Error(TG_INVALID_ARGUMENT, std::string("downloadParams: unknown param '") + names[i] + "'");
+    if (numel[i] != T_[it->second].numel) throw Error(TG_INVALID_ARGUMENT, "downloadParams: wrong size");
+    hip_check(hipMemcpy(data[i], ptr_[it->second], (size_t)numel[i] * 4, hipMemcpyDeviceToHost), "hipMemcpy(D2H)");
+  }
+}
+
+void Runtime::reset_optimizer() {
+  for (int t : state_roots_) {
+    double iv = O(T_[t].src).at("initValue").num();
+    tgk::fill(ptr_[t], kdt(T_[t].dt), T_[t].dt == F32 ? iv : 0.0, T_[t].numel, stream_);
+  }
+  hip_check(hipStreamSynchronize(stream_), "hipStreamSynchronize");
+  t_ = 0;
+}
+
+void Runtime::set_lr(const char* json) {
+  if (!opt_cfg_) throw Error(TG_INVALID_ARGUMENT, "setLR: graph has no optimizer (compileForward graphs don't take optimizer state)");
+  tgj::Value v;
+  try { v = tgj::parse(json); } catch (std::exception& e) { throw Error(TG_INVALID_ARGUMENT, e.what()); }
+  lr_ = rebase_lr(v, t_ + 1);
+}
+
+std::string Runtime::describe() {
+  std::ostringstream o;
+  o.precision(17);
+  o << "{\"nodes\":[";
+  for (size_t i = 0; i < nodes_.size(); ++i) {
+    const Node& n = nodes_[i];
+    o << (i ? "," : "") << "{\"kind\":\"" << n.kind << "\",\"op\":" << n.op << ",\"ir_kind\":\""
+      << (n.op >= 0 ? kinds_[n.op] : "") << "\",\"shape\":\"" << n.shape << "\",\"flops\":" << n.flops
+      << ",\"bytes\":" << n.bytes << "}";
+  }
+  o << "],\"arena_bytes\":" << arena_bytes_ << ",\"workspace_bytes\":" << workspace_bytes_
+    << ",\"ir_ops\":" << ops_.size() << "}";
+  return o.str();
+}
+
+void Runtime::profile_nodes(int iters, double* ms, int64_t nout) {
+  if (nout != (int64_t)nodes_.size()) throw Error(TG_INVALID_ARGUMENT, "profile: output length must equal node count");
+  std::vector<hipEvent_t> ev(nodes_.size() + 1);
+  for (auto& e : ev) hip_check(hipEventCreate(&e), "hipEventCreate");
+  std::vector<double> acc(nodes_.size(), 0.0);
+  for (int it = 0; it < iters; ++it) {
+    hip_check(hipEventRecord(ev[0], stream_), "hipEventRecord");
+    for (size_t i = 0; i < nodes_.size(); ++i) {
+      nodes_[i].launch(stream_);
+      hip_check(hipEventRecord(ev[i + 1], stream_), "hipEventRecord");
+    }
+    hip_check(hipStreamSynchronize(stream_), "hipStreamSynchronize");
+    for (size_t i = 0; i < nodes_.size(); ++i) {
+      float m = 0;
+      hip_check(hipEventElapsedTime(&m, ev[i], ev[i + 1]), "hipEventElapsedTime");
+      acc[i] += m;
+    }
+  }
+  for (auto& e : ev) hipEventDestroy(e);
+  for (size_t i = 0; i < nodes_.size(); ++i) ms[i] = acc[i] / std::max(1, iters);
+}
+
+double Runtime::time_replays(int steps) {
+  ensure_graph();
+  hipEvent_t a, b;
+  hip_check(hipEventCreate(&a), "hipEventCreate");
+  hip_check(hipEventCreate(&b), "hipEventCreate");
+  hip_check(hipEventRecord(a, stream_), "hipEventRecord");
+  for (int i = 0; i < steps; ++i) hip_check(hipGraphLaunch(graph_exec_, stream_), "hipGraphLaunch");
+  hip_check(hipEventRecord(b, stream_), "hipEventRecord");
+  hip_check(hipEventSynchronize(b), "hipEventSynchronize");
+  float ms = 0;
+  hip_check(hipEventElapsedTime(&ms, a, b), "hipEventElapsedTime");
+  hipEventDestroy(a);
+  hipEventDestroy(b);
+  return ms;
+}
+
+}  // namespace tg
+
+// ---- C ABI -------------------------------------------------------------------------------
+
+struct tg_runtime {
+  std::unique_ptr<tg::Runtime> rt;
+  std::mutex mu;
+  tg_runtime* parent = nullptr;
+  std::vector<tg_runtime*> children;
+};
+
+namespace {
+std::mutex g_registry_mu;
+std::set<tg_runtime*> g_live;
+
+template <class F>
+tg_status guarded(F&& f) {
+  try {
+    f();
+    tg::g_error.clear();
+    return TG_OK;
+  } catch (tg::Error& e) {
+    tg::g_error = e.what();
+    return e.code;
+  } catch (std::exception& e) {
+    tg::g_error = e.what();
+    return TG_INTERNAL;
+  }
+}
+
+bool live(tg_runtime* h) {
+  std::lock_guard<std::mutex> g(g_registry_mu);
+  return h && g_live.count(h);
+}
+}  // namespace
+
+extern "C" {
+
+const char* tg_last_error(void) { return tg::g_error.c_str(); }
+
+int tg_device_count(void) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+  return n;
+}
+
+tg_status tg_runtime_create(const char* ir_json, tg_runtime** out) {
+  if (!ir_json || !out) { tg::g_error = "null argument"; return TG_INVALID_ARGUMENT; }
+  return guarded([&] {
+    auto* h = new tg_runtime();
+    try {
+      h->rt.reset(new tg::Runtime(ir_json, nullptr));
+    } catch (...) {
+      delete h;
+      throw;
+    }
+    std::lock_guard<std::mutex> g(g_registry_mu);
+    g_live.insert(h);
+    *out = h;
+  });
+}
+
+tg_status tg_runtime_create_sibling(tg_runtime* parent, const char* ir_json, tg_runtime** out) {
+  if (!live(parent)) { tg::g_error = "compileForward: parent graph not found"; return TG_INVALID_ARGUMENT; }
+  return guarded([&] {
+    auto* h = new tg_runtime();
+    try {
+      h->rt.reset(new tg::Runtime(ir_json, parent->rt.get()));
+    } catch (...) {
+      delete h;
+      throw;
+    }
+    h->parent = parent;
+    std::lock_guard<std::mutex> g(g_registry_mu);
+    parent->children.push_back(h);
+    g_live.insert(h);
+    *out = h;
+  });
+}
+
+static void destroy_rec(tg_runtime* h) {
+  for (auto* c : h->children) destroy_rec(c);
+  {
+    std::lock_guard<std::mutex> lk(h->mu);
+    h->rt.reset();
+  }
+  g_live.erase(h);
+  delete h;
+}
+
+void tg_destroy(tg_runtime* h) {
+  std::lock_guard<std::mutex> g(g_registry_mu);
+  if (!h || !g_live.count(h)) return;
+  if (h->parent && g_live.count(h->parent)) {
+    auto& v = h->parent->children;
+    v.erase(std::remove(v.begin(), v.end(), h), v.end());
+  }
+  destroy_rec(h);
+}
+
+#define TG_ENTER(h)                                                       \
+  if (!live(h)) { tg::g_error = "graph destroyed"; return TG_ABORTED; } \
+  std::lock_guard<std::mutex> lk_((h)->mu);                               \
+  if (!(h)->rt) { tg::g_error = "graph destroyed"; return TG_ABORTED; }
+
+int tg_param_count(const tg_runtime* h) { return h && h->rt ? (int)h->rt->param_names.size() : 0; }
+const char* tg_param_name(const tg_runtime* h, int i) {
+  if (!h || !h->rt || i < 0 || i >= (int)h->rt->param_names.size()) return nullptr;
+  return h->rt->param_names[i].c_str();
+}
+int64_t tg_param_numel(const tg_runtime* h, int i) {
+  if (!h || !h->rt || i < 0 || i >= (int)h->rt->param_names.size()) return -1;
+  return h->rt->param_numel(i);
+}
+
+tg_status tg_upload_params(tg_runtime* h, int n, const char* const* names, const float* const* data, const int64_t* numel) {
+  TG_ENTER(h);
+  return guarded([&] { h->rt->upload_params(n, names, data, numel); });
+}
+
+tg_status tg_download_params(tg_runtime* h, int n, const char* const* names, float* const* data, const int64_t* numel) {
+  TG_ENTER(h);
+  return guarded([&] { h->rt->download_params(n, names, data, numel); });
+}
+
+tg_status tg_step(tg_runtime* h, int n, const char* const* names, const void* const* data, const int64_t* nbytes,
+                  float* loss) {
+  TG_ENTER(h);
+  return guarded([&] { float l = h->rt->step(n, names, data, nbytes, false); if (loss) *loss = l; });
+}
+
+tg_status tg_step_device(tg_runtime* h, int n, const char* const* names, const void* const* data, const int64_t* nbytes,
+                         float* loss) {
+  TG_ENTER(h);
+  return guarded([&] { float l = h->rt->step(n, names, data, nbytes, true); if (loss) *loss = l; });
+}
+
+tg_status tg_run(tg_runtime* h, int n, const char* const* names, const void* const* data, const int64_t* nbytes,
+                 void* out, int64_t out_bytes) {
+  TG_ENTER(h);
+  return guarded([&] { h->rt->run(n, names, data, nbytes, out, out_bytes); });
+}
+
+int tg_capture_count(const tg_runtime* h) { return h && h->rt ? (int)h->rt->capture_names.size() : 0; }
+const char* tg_capture_name(const tg_runtime* h, int i) {
+  if (!h || !h->rt || i < 0 || i >= (int)h->rt->capture_names.size()) return nullptr;
+  return h->rt->capture_names[i].c_str();
+}
+
+tg_status tg_get_capture(tg_runtime* h, const char* name, void* out, int64_t nbytes) {
+  TG_ENTER(h);
+  return guarded([&] { h->rt->get_capture(name, out, nbytes); });
+}
+
+tg_status tg_reset_optimizer(tg_runtime* h) {
+  TG_ENTER(h);
+  return guarded([&] { h->rt->reset_optimizer(); });
+}
+
+tg_status tg_set_lr(tg_runtime* h, const char* lr_json) {
+  TG_ENTER(h);
+  return guarded([&] { h->rt->set_lr(lr_json); });
+}
+
+tg_status tg_plan(const char* ir_json, char* buf, int64_t buflen) {
+  if (!ir_json || !buf) { tg::g_error = "null argument"; return TG_INVALID_ARGUMENT; }
+  return guarded([&] {
+    tg::Runtime rt(ir_json, nullptr, true);
+    std::string s = rt.describe();
+    if ((int64_t)s.size() + 1 > buflen) throw tg::Error(TG_INVALID_ARGUMENT, "plan: buffer too small (" + std::to_string(s.size() + 1) + ")");
+    memcpy(buf, s.c_str(), s.size() + 1);
+  });
+}
+
+tg_status tg_describe(tg_runtime* h, char* buf, int64_t buflen) {
+  TG_ENTER(h);
+  return guarded([&] {
+    std::string s = h->rt->describe();
+    if ((int64_t)s.size() + 1 > buflen) throw tg::Error(TG_INVALID_ARGUMENT, "describe: buffer too small (" + std::to_string(s.size() + 1) + ")");
+    memcpy(buf, s.c_str(), s.size() + 1);
+  });
+}
+
+tg_status tg_profile_nodes(tg_runtime* h, int iters, double* ms_out, int64_t n_out) {
+  TG_ENTER(h);
+  return guarded([&] { h->rt->profile_nodes(iters, ms_out, n_out); });
+}
+
+tg_status tg_time_replays(tg_runtime* h, int steps, double* total_ms) {
+  TG_ENTER(h);
+  return guarded([&] { *total_ms = h->rt->time_replays(steps); });
+}
+
+}  // extern "C"
