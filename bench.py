@@ -1,0 +1,168 @@
+"""Benchmark: train steps/sec (fwd + bwd + Adam) per config on one MI355X.
+
+Prints ONE JSON line. `value` is the headline config's steps/s (default: the transformer,
+C5, the config the north star's roofline targets are stated on) with every batch already
+resident in HBM when the timed region starts (batches are staged into device slots
+beforehand); each timed step still uploads the per-step optimizer scalars and PRNG seed,
+replays the captured step graph and reads the 4-byte loss back (the API's semantics).
+`per_config` carries the same measurement for all five configs, plus device-only replay
+time, GEMM TFLOP/s and non-GEMM GB/s from HIP events around every launch node.
+`roofline` is for the dominant kernel family of the headline config (its f32 MFMA GEMMs);
+`cpu_baseline` is the CPU oracle (a C++ restatement of the reference's CPU evaluator, the
+reference itself being TypeScript that cannot run here) on this host's cores, on a bounded
+number of steps of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_F32_MFMA_TFLOPS = 157.3
+PEAK_HBM_GBS = 8000.0
+RING = 8
+CPU_STEPS = {'mlp_sin': 50, 'char_mlp': 3, 'cnn': 2, 'nerf': 1, 'transformer': 2}
+
+
+def measure(key, steps, warmup, profile_iters=3):
+    from tensorgrad_amd import backend, configs
+    from tensorgrad_amd.build_ir import build_training_ir
+    cfg = configs.CONFIGS[key]
+    ir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer)
+    rt = backend.NativeRuntime(ir.wire_json())
+    rt.upload_params(ir.initial_params(configs.INIT_SEED))
+    for i, b in enumerate(configs.batches(cfg, RING)):
+        rt.stage_batch(i, b)
+    for i in range(warmup):
+        rt.step_staged(i % RING)
+    t0 = time.perf_counter()
+    loss = None
+    for i in range(steps):
+        loss = rt.step_staged(i % RING)
+    dt = time.perf_counter() - t0
+    replay_ms = rt.time_replays(steps) / steps
+    nodes = rt.describe()['nodes']
+    ms = rt.profile_nodes(profile_iters)
+    rt.destroy()
+    gemm_t = sum(t for n, t in zip(nodes, ms) if n['kind'] == 'gemm')
+    gemm_f = sum(n['flops'] for n in nodes if n['kind'] == 'gemm')
+    other_t = sum(t for n, t in zip(nodes, ms) if n['kind'] not in ('gemm', 'conv'))
+    other_b = sum(n['bytes'] for n in nodes if n['kind'] not in ('gemm', 'conv'))
+    conv_t = sum(t for n, t in zip(nodes, ms) if n['kind'] == 'conv')
+    conv_f = sum(n['flops'] for n in nodes if n['kind'] == 'conv')
+    by_kind = {}
+    for n, t in zip(nodes, ms):
+        k = by_kind.setdefault(n['kind'], {'launch_nodes': 0, 'ms': 0.0})
+        k['launch_nodes'] += 1
+        k['ms'] = round(k['ms'] + t, 4)
+    top_gemm = sorted(((t, n) for n, t in zip(nodes, ms) if n['kind'] == 'gemm'), key=lambda x: -x[0])[:3]
+    return {
+        'config': key,
+        'title': cfg.title,
+        'steps_per_s': steps / dt,
+        'ms_per_step': 1e3 * dt / steps,
+        'samples_per_s': cfg.samples_per_step * steps / dt,
+        'sample_unit': cfg.sample_unit,
+        'device_replay_ms': replay_ms,
+        'launch_nodes': len(nodes),
+        'final_loss': loss,
+        'gemm': {'flop_per_step': gemm_f, 'ms': gemm_t, 'tflops': gemm_f / max(gemm_t, 1e-12) / 1e9,
+                 'frac_f32_peak': gemm_f / max(gemm_t, 1e-12) / 1e9 / PEAK_F32_MFMA_TFLOPS,
+                 'top': [{'shape': n['shape'], 'ms': round(t, 4), 'tflops': round(n['flops'] / max(t, 1e-12) / 1e9, 2)}
+                         for t, n in top_gemm]},
+        'conv': {'flop_per_step': conv_f, 'ms': conv_t, 'tflops': conv_f / max(conv_t, 1e-12) / 1e9},
+        'non_gemm': {'bytes_per_step': other_b, 'ms': other_t, 'gbs': other_b / max(other_t, 1e-12) / 1e6,
+                     'frac_hbm_peak': other_b / max(other_t, 1e-12) / 1e6 / PEAK_HBM_GBS},
+        'kinds': by_kind,
+    }
+
+
+def cpu_baseline(key):
+    sys.path.insert(0, os.path.join(ROOT, 'oracle'))
+    import pyoracle
+    from tensorgrad_amd import configs
+    from tensorgrad_amd.build_ir import build_training_ir
+    threads = max(1, min(16, os.cpu_count() or 1))
+    pyoracle.set_threads(threads)
+    cfg = configs.CONFIGS[key]
+    ir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer)
+    o = pyoracle.OracleRuntime(ir.wire())
+    o.upload_params(ir.initial_params(configs.INIT_SEED))
+    n = CPU_STEPS[key]
+    bs = configs.batches(cfg, n)
+    t0 = time.perf_counter()
+    for b in bs:
+        o.step(b)
+    dt = time.perf_counter() - t0
+    return {'value': n / dt, 'unit': 'steps/s', 'cores': threads, 'kind': 'port',
+            'sample': f'{n} full {key} training steps (fwd+bwd+Adam) of the CPU oracle, OpenMP over output elements'}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument('--gpus', type=int, default=1)
+    ap.add_argument('--steps', type=int, default=200)
+    ap.add_argument('--warmup', type=int, default=20)
+    ap.add_argument('--config', default='transformer')
+    ap.add_argument('--only', action='store_true', help='measure the headline config only')
+    ap.add_argument('--no-cpu', action='store_true')
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({'error': 'this build runs on one GPU per process; multi-GPU data parallelism is '
+                                   'designed (DESIGN.md) but not built, so --gpus must be 1'}))
+        sys.exit(2)
+    from tensorgrad_amd import backend, configs
+    if backend.device_count() < 1:
+        print(json.dumps({'error': 'no HIP device visible'}))
+        sys.exit(1)
+    keys = [args.config] + ([] if args.only else [k for k in configs.CONFIGS if k != args.config])
+    results = {}
+    for k in keys:
+        results[k] = measure(k, args.steps, args.warmup)
+        print(f'# {k}: {results[k]["steps_per_s"]:.1f} steps/s, replay {results[k]["device_replay_ms"]:.3f} ms',
+              file=sys.stderr, flush=True)
+    head = results[args.config]
+    cpu = None if args.no_cpu else cpu_baseline(args.config)
+    cfg = configs.CONFIGS[args.config]
+    g = head['gemm']
+    line = {
+        'metric': 'train steps/sec (fwd+bwd+Adam) per config; % of f32 MFMA / HBM roofline',
+        'value': round(head['steps_per_s'], 3),
+        'unit': 'steps/s',
+        'n_gpus': 1,
+        'steps': args.steps,
+        'warmup': args.warmup,
+        'ms_per_step': round(head['ms_per_step'], 4),
+        'higher_is_better': True,
+        'scaling': 'weak',
+        'vs_baseline': None,
+        'dtype': 'f32',
+        'data': 'synthetic (mulberry32(1000+c) batches, seed-42 init); batches staged in HBM before timing',
+        'config': {'workload': cfg.title, 'samples_per_step': cfg.samples_per_step, 'sample_unit': cfg.sample_unit,
+                   'samples_per_s': round(head['samples_per_s'], 1),
+                   'device_replay_ms_per_step': round(head['device_replay_ms'], 4)},
+        'roofline': {'bound': 'mfma', 'kernel': 'f32 MFMA GEMMs (all matmul / matmul_batched launches of one step)',
+                     'achieved': round(g['tflops'], 3), 'peak': PEAK_F32_MFMA_TFLOPS, 'unit': 'TFLOP/s',
+                     'frac': round(g['frac_f32_peak'], 4), 'traffic': None},
+        'roofline_non_gemm': {'bound': 'hbm', 'achieved': round(head['non_gemm']['gbs'], 1), 'peak': PEAK_HBM_GBS,
+                              'unit': 'GB/s', 'frac': round(head['non_gemm']['frac_hbm_peak'], 4)},
+        'cpu_baseline': None if cpu is None else {k: (round(v, 5) if isinstance(v, float) else v) for k, v in cpu.items()},
+        'per_config': [{'config': r['config'], 'steps_per_s': round(r['steps_per_s'], 2),
+                        'samples_per_s': round(r['samples_per_s'], 1), 'device_replay_ms': round(r['device_replay_ms'], 4),
+                        'gemm_tflops': round(r['gemm']['tflops'], 2), 'gemm_frac_f32_peak': round(r['gemm']['frac_f32_peak'], 4),
+                        'conv_tflops': round(r['conv']['tflops'], 2),
+                        'non_gemm_gbs': round(r['non_gemm']['gbs'], 1),
+                        'non_gemm_frac_hbm': round(r['non_gemm']['frac_hbm_peak'], 4),
+                        'launch_nodes': r['launch_nodes'], 'kinds': r['kinds'], 'top_gemms': r['gemm']['top']}
+                       for r in results.values()],
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == '__main__':
+    main()

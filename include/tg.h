@@ -85,6 +85,13 @@ tg_status tg_step(tg_runtime* rt, int n, const char* const* names, const void* c
 tg_status tg_step_device(tg_runtime* rt, int n, const char* const* names, const void* const* dev_data,
                          const int64_t* nbytes, float* loss);
 
+/* Device-resident batches (no reference counterpart): copy one batch of user inputs
+ * (host pointers) into device slot `slot`, then run steps from a slot without any host
+ * to device copy of user data. Used by callers that prefetch, and by the benchmark. */
+tg_status tg_stage_batch(tg_runtime* rt, int slot, int n, const char* const* names, const void* const* data,
+                         const int64_t* nbytes);
+tg_status tg_step_staged(tg_runtime* rt, int slot, float* loss);
+
 /* Forward-only dispatch; copies the graph output into `out` (`run`,
  * src/worker.ts:242-260). */
 tg_status tg_run(tg_runtime* rt, int n, const char* const* names, const void* const* data,

@@ -245,7 +245,22 @@ class Oracle {
   }
   int64_t home_numel(const std::string& name) { return (int64_t)home(name).n(); }
 
-  void set_lr(const char* json) { lr_store_ = parse_json(json); lr_ = lr_store_; lr_overridden_ = true; }
+  // setLR (worker.ts:304-319): the new schedule is rebased so its step 1 is t + 1
+  // (lr.ts:108-112) unless it carries an explicit startStep.
+  void set_lr(const char* json) {
+    lr_store_ = parse_json(json);
+    if (lr_store_.t == JV::OBJ) {
+      const JV* ss = lr_store_.find("startStep");
+      if (!ss || ss->is_null()) {
+        JV v; v.t = JV::NUM; v.n = (double)t_;
+        bool set = false;
+        for (auto& kv : lr_store_.o) if (kv.first == "startStep") { kv.second = v; set = true; }
+        if (!set) lr_store_.o.emplace_back("startStep", v);
+      }
+    }
+    lr_ = lr_store_;
+    lr_overridden_ = true;
+  }
   void reset_optimizer() {
     for (auto& kv : state_tid_) std::fill(home_[kv.first].raw.begin(), home_[kv.first].raw.end(), 0u);
     t_ = 0;
@@ -324,8 +339,11 @@ class Oracle {
   bool retain_all_ = false;
   std::unordered_map<int, Val> vals_;
 
+  // The worker always injects the per-graph counter (worker.ts:208-214). A test may
+  // instead bind `__prngSeed` explicitly, as the reference's FD harness does
+  // (test/grad.ts:78-81); an explicit seed is then used and the counter left alone.
   void inject_seed(std::map<std::string, Val>& inputs) {
-    if (!uses_prng_) return;
+    if (!uses_prng_ || inputs.count("__prngSeed")) return;
     ++prng_counter_;
     Val v = make(I32, 1); v.i()[0] = (int32_t)(uint32_t)prng_counter_;
     inputs["__prngSeed"] = v;

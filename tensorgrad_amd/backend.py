@@ -23,7 +23,7 @@ TG_OK, TG_ABORTED, TG_INVALID_ARGUMENT, TG_DEVICE_ERROR, TG_INTERNAL = range(5)
 EXPORTED = (
     'tg_last_error', 'tg_device_count', 'tg_runtime_create', 'tg_runtime_create_sibling', 'tg_destroy',
     'tg_param_count', 'tg_param_name', 'tg_param_numel', 'tg_upload_params', 'tg_download_params', 'tg_step',
-    'tg_step_device', 'tg_run', 'tg_capture_count', 'tg_capture_name', 'tg_get_capture', 'tg_reset_optimizer',
+    'tg_step_device', 'tg_stage_batch', 'tg_step_staged', 'tg_run', 'tg_capture_count', 'tg_capture_name', 'tg_get_capture', 'tg_reset_optimizer',
     'tg_set_lr', 'tg_describe', 'tg_plan', 'tg_profile_nodes', 'tg_time_replays',
 )
 
@@ -73,6 +73,8 @@ def lib():
     L.tg_step.argtypes = [vp, ctypes.c_int, c_char_pp, ctypes.POINTER(vp), i64p, ctypes.POINTER(ctypes.c_float)]
     L.tg_step_device.argtypes = L.tg_step.argtypes
     L.tg_run.argtypes = [vp, ctypes.c_int, c_char_pp, ctypes.POINTER(vp), i64p, vp, ctypes.c_int64]
+    L.tg_stage_batch.argtypes = [vp, ctypes.c_int, ctypes.c_int, c_char_pp, ctypes.POINTER(vp), i64p]
+    L.tg_step_staged.argtypes = [vp, ctypes.c_int, ctypes.POINTER(ctypes.c_float)]
     L.tg_capture_count.argtypes = [vp]
     L.tg_capture_name.argtypes = [vp, ctypes.c_int]
     L.tg_capture_name.restype = ctypes.c_char_p
@@ -177,6 +179,15 @@ class NativeRuntime:
         ptrs = (ctypes.c_void_p * len(names))(*dev_ptrs)
         sizes = (ctypes.c_int64 * len(names))(*nbytes)
         _check(lib().tg_step_device(self._h, len(names), _names(names), ptrs, sizes, ctypes.byref(loss)))
+        return float(loss.value)
+
+    def stage_batch(self, slot: int, inputs: Dict[str, np.ndarray]) -> None:
+        n, names, ptrs, sizes, keep = _inputs(inputs)
+        _check(lib().tg_stage_batch(self._h, slot, n, names, ptrs, sizes))
+
+    def step_staged(self, slot: int) -> float:
+        loss = ctypes.c_float()
+        _check(lib().tg_step_staged(self._h, slot, ctypes.byref(loss)))
         return float(loss.value)
 
     def run(self, inputs: Dict[str, np.ndarray], out_shape, out_dtype) -> np.ndarray:

@@ -231,20 +231,42 @@ __global__ void k_gather_rows(const int32_t* __restrict__ idx, int64_t rows, con
   }
 }
 
-// Stable counting sort of row ids by token: offs[v]..offs[v+1] lists rows with idx == v
-// in increasing row order. Single block; rows are at most a few hundred thousand.
-__global__ void k_bucket_rows(const int32_t* __restrict__ idx, int64_t rows, int64_t V, int32_t* __restrict__ perm,
-                              int32_t* __restrict__ offs) {
-  // offs[v] = number of rows with token < v (tokens outside [0, V) are dropped).
-  for (int64_t v = threadIdx.x; v <= V; v += blockDim.x) {
-    int32_t c = 0;
-    for (int64_t r = 0; r < rows; ++r) { int32_t t = idx[r]; c += (t >= 0 && t < (int32_t)v) ? 1 : 0; }
-    offs[v] = c;
-  }
+// Stable counting sort of row ids by token: rows with idx == v land in
+// perm[offs[v] .. offs[v+1]) in increasing row order; tokens outside [0, V) are dropped.
+// One 256-thread block: integer-atomic histogram, exclusive scan, then one wavefront
+// places rows 64 at a time — a lane's rank among equal tokens is counted with shuffles,
+// so the order within a bucket is the row order. `cur` is V ints of scratch.
+__global__ __launch_bounds__(256) void k_bucket_rows(const int32_t* __restrict__ idx, int64_t rows, int64_t V,
+                                                     int32_t* __restrict__ perm, int32_t* __restrict__ offs,
+                                                     int32_t* __restrict__ cur) {
+  for (int64_t v = threadIdx.x; v <= V; v += blockDim.x) offs[v] = 0;
   __syncthreads();
-  for (int64_t v = threadIdx.x; v < V; v += blockDim.x) {
-    int32_t w = offs[v];
-    for (int64_t r = 0; r < rows; ++r) if (idx[r] == (int32_t)v) perm[w++] = (int32_t)r;
+  for (int64_t r = threadIdx.x; r < rows; r += blockDim.x) {
+    int32_t t = idx[r];
+    if (t >= 0 && t < V) atomicAdd(&offs[t + 1], 1);
+  }
+  __threadfence_block();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int64_t v = 0; v < V; ++v) { offs[v + 1] += offs[v]; cur[v] = offs[v]; }
+  }
+  __threadfence_block();
+  __syncthreads();
+  if (threadIdx.x >= 64) return;
+  const int lane = threadIdx.x;
+  for (int64_t r0 = 0; r0 < rows; r0 += 64) {
+    const int64_t r = r0 + lane;
+    int32_t t = r < rows ? idx[r] : -1;
+    if (t < 0 || t >= V) t = -1;
+    int rank = 0, later = 0;
+    for (int j = 0; j < 64; ++j) {
+      int32_t tj = __shfl(t, j, 64);
+      if (tj == t) { if (j < lane) ++rank; else if (j > lane) ++later; }
+    }
+    int32_t base = t >= 0 ? cur[t] : 0;
+    if (t >= 0) perm[base + rank] = (int32_t)r;
+    if (t >= 0 && later == 0) cur[t] = base + rank + 1;   // last lane of its token group
+    __threadfence_block();
   }
 }
 
@@ -275,7 +297,7 @@ void gather_rows(const int32_t* idx, int64_t rows, const float* table, int64_t V
 void scatter_rows(const int32_t* idx, int64_t rows, const float* dy, int64_t V, int64_t N, float* out, int32_t* perm,
                   int32_t* offs, hipStream_t st) {
   if (V * N <= 0) return;
-  k_bucket_rows<<<1, 1024, 0, st>>>(idx, rows, V, perm, offs);
+  k_bucket_rows<<<1, 256, 0, st>>>(idx, rows, V, perm, offs, offs + V + 1);
   k_scatter_rows<<<grid_for(V * N), 256, 0, st>>>(dy, V, N, perm, offs, out);
 }
 

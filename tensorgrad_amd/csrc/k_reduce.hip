@@ -28,18 +28,6 @@ inline int blocks_for_rows(int64_t rows) {
   return (int)(b < 1 ? 1 : b);
 }
 
-__global__ void k_row_sum(const float* __restrict__ a, float* __restrict__ out, int64_t outer, int64_t D, double div) {
-  const int lane = threadIdx.x % kWave;
-  for (int64_t r = blockIdx.x * (int64_t)kRowsPerBlock + threadIdx.x / kWave; r < outer;
-       r += (int64_t)gridDim.x * kRowsPerBlock) {
-    const float* row = a + r * D;
-    double s = 0.0;
-    for (int64_t j = lane; j < D; j += kWave) s += (double)row[j];
-    s = wave_sum(s);
-    if (lane == 0) out[r] = (float)(s / div);
-  }
-}
-
 struct ArgBest { float v; int32_t i; bool ok; };
 
 __device__ __forceinline__ ArgBest arg_combine(ArgBest a, ArgBest b) {
@@ -116,29 +104,100 @@ __device__ __forceinline__ int64_t strided_offset(const Strided& sp, int64_t i) 
   return o;
 }
 
-// One thread per output cell; its sources are visited in increasing flat order and
-// summed in f32, as the reference evaluator does (_eval.ts:492-523).
-__global__ void k_sum_to_shape(const float* __restrict__ a, float* __restrict__ out, Strided cells, Strided red,
-                               int64_t ncells, int64_t nred) {
-  for (int64_t c = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; c < ncells; c += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t base = strided_offset(cells, c);
-    float s = 0.0f;
-    if (red.rank == 1) {
-      const int64_t st = red.s0[0];
-      for (int64_t r = 0; r < nred; ++r) s += a[base + r * st];
-    } else {
-      for (int64_t r = 0; r < nred; ++r) s += a[base + strided_offset(red, r)];
+// Deterministic parallel sum over a reduced index space, f64 accumulation.
+// Work is split into (cell, chunk) items; each item sums a contiguous range of the
+// reduced index in order, partials are combined per cell in chunk order. Two layouts:
+//  * column form: the cells' last axis is unit-stride, so consecutive threads take
+//    consecutive cells and every load instruction is coalesced;
+//  * row form: the reduced index is innermost, so a wavefront's lanes stride over it and
+//    combine through a fixed shuffle tree.
+__device__ __forceinline__ int64_t red_offset(const Strided& sp, int64_t i) {
+  if (sp.rank == 0) return 0;
+  if (sp.rank == 1) return i * sp.s0[0];
+  if (sp.rank == 2) return (i / sp.dims[1]) * sp.s0[0] + (i % sp.dims[1]) * sp.s0[1];
+  return strided_offset(sp, i);
+}
+
+__global__ void k_sum_cols(const float* __restrict__ a, double* __restrict__ part, float* __restrict__ out,
+                           Strided cells, Strided red, int64_t ncells, int64_t nred, int64_t chunk, int nchunks,
+                           double div) {
+  const int64_t c = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  const int q = blockIdx.y;
+  if (c >= ncells) return;
+  const int64_t base = red_offset(cells, c);
+  const int64_t r0 = q * chunk, r1 = min(nred, r0 + chunk);
+  double s = 0.0;
+  if (red.rank == 1) {
+    const int64_t st = red.s0[0];
+    const float* p = a + base + r0 * st;
+    int64_t r = r0;
+    for (; r + 4 <= r1; r += 4, p += 4 * st) {
+      float v0 = p[0], v1 = p[st], v2 = p[2 * st], v3 = p[3 * st];
+      s += (double)v0; s += (double)v1; s += (double)v2; s += (double)v3;
     }
-    out[c] = s;
+    for (; r < r1; ++r, p += st) s += (double)*p;
+  } else {
+    for (int64_t r = r0; r < r1; ++r) s += (double)a[base + red_offset(red, r)];
+  }
+  if (nchunks == 1) out[c] = (float)(s / div);
+  else part[c * nchunks + q] = s;
+}
+
+__global__ void k_sum_rows(const float* __restrict__ a, double* __restrict__ part, float* __restrict__ out,
+                           Strided cells, Strided red, int64_t ncells, int64_t nred, int64_t chunk, int nchunks,
+                           double div) {
+  const int lane = threadIdx.x % kWave;
+  const int64_t items = ncells * nchunks;
+  for (int64_t it = blockIdx.x * (int64_t)kRowsPerBlock + threadIdx.x / kWave; it < items;
+       it += (int64_t)gridDim.x * kRowsPerBlock) {
+    const int64_t c = it / nchunks;
+    const int q = (int)(it % nchunks);
+    const int64_t base = red_offset(cells, c);
+    const int64_t r0 = q * chunk, r1 = min(nred, r0 + chunk);
+    double s = 0.0;
+    if (red.rank == 1 && red.s0[0] == 1) {
+      const float* p = a + base;
+      for (int64_t r = r0 + lane; r < r1; r += kWave) s += (double)p[r];
+    } else {
+      for (int64_t r = r0 + lane; r < r1; r += kWave) s += (double)a[base + red_offset(red, r)];
+    }
+    s = wave_sum(s);
+    if (lane == 0) {
+      if (nchunks == 1) out[c] = (float)(s / div);
+      else part[c * nchunks + q] = s;
+    }
   }
 }
 
-}  // namespace
-
-void row_sum(const float* a, float* out, int64_t outer, int64_t D, double div, hipStream_t st) {
-  if (outer <= 0) return;
-  k_row_sum<<<blocks_for_rows(outer), kWave * kRowsPerBlock, 0, st>>>(a, out, outer, D, div);
+__global__ void k_sum_finish(const double* __restrict__ part, float* __restrict__ out, int64_t ncells, int nchunks,
+                             double div) {
+  for (int64_t c = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; c < ncells; c += (int64_t)gridDim.x * blockDim.x) {
+    double s = 0.0;
+    for (int q = 0; q < nchunks; ++q) s += part[c * nchunks + q];
+    out[c] = (float)(s / div);
+  }
 }
+
+struct SumPlan { bool cols; int64_t chunk; int nchunks; };
+
+SumPlan sum_plan(const Strided& cells, int64_t ncells, int64_t nred) {
+  SumPlan p;
+  p.cols = cells.rank >= 1 && cells.s0[cells.rank - 1] == 1 && ncells >= 64;
+  // Aim for ~16k work items (columns) or ~4k wavefronts (rows), chunks of >= 256 terms.
+  int64_t target = p.cols ? 16384 : 4096;
+  int64_t want = (target + ncells - 1) / ncells;
+  int64_t maxc = nred / 256;
+  if (maxc < 1) maxc = 1;
+  int64_t n = want < maxc ? want : maxc;
+  if (n > 4096) n = 4096;
+  if (n < 1) n = 1;
+  p.chunk = (nred + n - 1) / n;
+  p.nchunks = (int)((nred + p.chunk - 1) / p.chunk);
+  if (p.nchunks < 1) p.nchunks = 1;
+  return p;
+}
+
+}  // namespace
 
 void row_argmax(const float* a, int32_t* out, int64_t outer, int64_t D, hipStream_t st) {
   if (outer <= 0) return;
@@ -156,12 +215,29 @@ void softmax_causal(const float* a, float* out, int64_t mats, int64_t D, hipStre
   k_softmax_causal<<<blocks_for_rows(rows), kWave * kRowsPerBlock, 0, st>>>(a, out, rows, D);
 }
 
-void sum_to_shape(const float* a, float* out, const Strided& cells, const Strided& red, int64_t ncells, int64_t nred,
-                  hipStream_t st) {
+int64_t sum_workspace_doubles(const Strided& cells, int64_t ncells, int64_t nred) {
+  SumPlan p = sum_plan(cells, ncells, nred);
+  return p.nchunks > 1 ? ncells * p.nchunks : 0;
+}
+
+void reduce_sum(const float* a, float* out, const Strided& cells, const Strided& red, int64_t ncells, int64_t nred,
+                double div, double* work, hipStream_t st) {
   if (ncells <= 0) return;
-  int64_t b = (ncells + 255) / 256;
-  if (b > 4096) b = 4096;
-  k_sum_to_shape<<<(int)b, 256, 0, st>>>(a, out, cells, red, ncells, nred);
+  SumPlan p = sum_plan(cells, ncells, nred);
+  if (p.cols) {
+    dim3 grid((unsigned)((ncells + 255) / 256), (unsigned)p.nchunks);
+    k_sum_cols<<<grid, 256, 0, st>>>(a, work, out, cells, red, ncells, nred, p.chunk, p.nchunks, div);
+  } else {
+    int64_t items = ncells * p.nchunks;
+    int64_t b = (items + kRowsPerBlock - 1) / kRowsPerBlock;
+    if (b > 16384) b = 16384;
+    k_sum_rows<<<(int)b, kWave * kRowsPerBlock, 0, st>>>(a, work, out, cells, red, ncells, nred, p.chunk, p.nchunks, div);
+  }
+  if (p.nchunks > 1) {
+    int64_t b = (ncells + 255) / 256;
+    if (b > 4096) b = 4096;
+    k_sum_finish<<<(int)b, 256, 0, st>>>(work, out, ncells, p.nchunks, div);
+  }
 }
 
 }  // namespace tgk

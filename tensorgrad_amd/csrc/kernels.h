@@ -50,16 +50,17 @@ void categorical(const float* a, int32_t* out, int64_t outer, int64_t D, const i
                  hipStream_t st);
 
 // ---- reductions / softmax (k_reduce.hip) --------------------------------------------
-// Row reductions over a contiguous last axis, f64 accumulation.
-void row_sum(const float* a, float* out, int64_t outer, int64_t D, double div, hipStream_t st);
+// Deterministic parallel sums with f64 accumulation: out[c] = f32(sum_r a[cell(c) +
+// red(r)] / div) for c < ncells, r < nred. `cells` / `red` carry dims and element
+// strides in s0. Used for sum_last / mean_last (red = last axis) and for the
+// un-broadcast sums of autograd (sum_to_shape). `work` must hold
+// sum_workspace_doubles(...) doubles of partials.
+int64_t sum_workspace_doubles(const Strided& cells, int64_t ncells, int64_t nred);
+void reduce_sum(const float* a, float* out, const Strided& cells, const Strided& red, int64_t ncells, int64_t nred,
+                double div, double* work, hipStream_t st);
 void row_argmax(const float* a, int32_t* out, int64_t outer, int64_t D, hipStream_t st);
 void log_softmax(const float* a, float* out, int64_t outer, int64_t D, hipStream_t st);
 void softmax_causal(const float* a, float* out, int64_t mats, int64_t D, hipStream_t st);
-// Un-broadcast sum: out cell c = sum over the `red` index space (f32 running sum in
-// source-flat order). `sp` dims/s0 describe the output cells' source base offsets,
-// `rsp` dims/s0 the reduced axes.
-void sum_to_shape(const float* a, float* out, const Strided& cells, const Strided& red, int64_t ncells,
-                  int64_t nred, hipStream_t st);
 
 // ---- GEMM (k_gemm.hip) --------------------------------------------------------------
 // C[z][m][n] = sum_k A[z][m][k] * B[z][k][n], f32 MFMA, f32 accumulate.
@@ -79,7 +80,7 @@ void gemm(const GemmDesc& d, float* work, hipStream_t st);
 void gather_rows(const int32_t* idx, int64_t rows, const float* table, int64_t V, int64_t N, float* out,
                  hipStream_t st);
 // Embedding gradient: out[v, :] = sum over rows r with idx[r] == v of dy[r, :], in row
-// order, f64 accumulation; needs `perm` (rows ints) and `offs` (V + 1 ints) scratch.
+// order, f64 accumulation; needs `perm` (rows ints) and `offs` (2V + 1 ints) scratch.
 void scatter_rows(const int32_t* idx, int64_t rows, const float* dy, int64_t V, int64_t N, float* out,
                   int32_t* perm, int32_t* offs, hipStream_t st);
 

@@ -213,8 +213,10 @@ class Runtime {
   char* arena_ = nullptr;
   size_t arena_bytes_ = 0;
   std::vector<void*> ptr_;          // per root tensor
-  char* input_region_ = nullptr;    // device, contiguous tensor inputs
+  char* input_region_ = nullptr;    // device: user inputs, then per-step scalars
   size_t input_region_bytes_ = 0;
+  size_t user_bytes_ = 0;           // user inputs occupy [0, user_bytes_)
+  std::vector<char*> slots_;        // device-resident staged batches (user part only)
   std::map<int, size_t> input_offset_;   // input tid -> byte offset in region
   char* staging_ = nullptr;         // pinned host mirror of the input region
   float* loss_host_ = nullptr;      // pinned
@@ -246,6 +248,11 @@ class Runtime {
   void bind_all();
   void launch_all(hipStream_t st);
   void upload_inputs(int n, const char* const* names, const void* const* data, const int64_t* nbytes, bool device);
+  void stage_scalars();
+ public:
+  void stage_batch(int slot, int n, const char* const* names, const void* const* data, const int64_t* nbytes);
+  float step_staged(int slot);
+ private:
   void ensure_graph();
   void apply_copy_writebacks(hipStream_t st);
 
@@ -312,6 +319,7 @@ Runtime::~Runtime() {
   if (adam_tensors_) hipFree(adam_tensors_);
   if (adam_chunk_tensor_) hipFree(adam_chunk_tensor_);
   if (adam_chunk_start_) hipFree(adam_chunk_start_);
+  for (char* p : slots_) if (p) hipFree(p);
   if (staging_) hipHostFree(staging_);
   if (loss_host_) hipHostFree(loss_host_);
 }
@@ -800,11 +808,17 @@ void Runtime::lower_op(int i) {
     if (to.numel != expect_out) throw Error(TG_INVALID_ARGUMENT, k + ": output size mismatch");
     n.bytes = 4.0 * (T_[a].numel + to.numel);
     n.kind = (k == "log_softmax_last" || k == "softmax_causal_last") ? "softmax" : "reduce";
+    tgk::Strided cells{}, red{};
+    cells.rank = 1; cells.dims[0] = outer; cells.s0[0] = D;
+    red.rank = 1; red.dims[0] = D; red.s0[0] = 1;
+    if (k == "mean_last" || k == "sum_last")
+      workspace_bytes_ = std::max(workspace_bytes_, (size_t)tgk::sum_workspace_doubles(cells, outer, D) * 8);
     n.bind = [=]() -> std::function<void(hipStream_t)> {
       const float* pa = (const float*)dptr(a); void* po = dptr(out);
       if (k == "mean_last" || k == "sum_last") {
         double div = k == "mean_last" ? (double)D : 1.0;
-        return [=](hipStream_t st) { tgk::row_sum(pa, (float*)po, outer, D, div, st); };
+        double* w = (double*)workspace_;
+        return [=](hipStream_t st) { tgk::reduce_sum(pa, (float*)po, cells, red, outer, D, div, w, st); };
       }
       if (k == "argmax_last") return [=](hipStream_t st) { tgk::row_argmax(pa, (int32_t*)po, outer, D, st); };
       if (k == "log_softmax_last") return [=](hipStream_t st) { tgk::log_softmax(pa, (float*)po, outer, D, st); };
@@ -895,20 +909,21 @@ void Runtime::lower_op(int i) {
     const Dims& as = T_[a].shape;
     n.bytes = 4.0 * (T_[a].numel + to.numel);
     n.kind = "reduce";
+    Dims ast = contiguous_strides(as);
+    int rdiff = (int)as.size() - (int)to.shape.size();
+    Dims cd, cs, rdd, rs;
+    for (int d = 0; d < (int)as.size(); ++d) {
+      bool reduced = d < rdiff || (to.shape[d - rdiff] == 1 && as[d] != 1);
+      if (as[d] == 1) continue;
+      if (reduced) { rdd.push_back(as[d]); rs.push_back(ast[d]); }
+      else { cd.push_back(as[d]); cs.push_back(ast[d]); }
+    }
+    tgk::Strided cells = make_strided(cd, cs, {}, {});
+    tgk::Strided red = make_strided(rdd, rs, {}, {});
+    int64_t ncells = prod(cd), nred = prod(rdd);
+    if (ncells != to.numel) throw Error(TG_INTERNAL, "sum_to_shape: cell count mismatch");
+    workspace_bytes_ = std::max(workspace_bytes_, (size_t)tgk::sum_workspace_doubles(cells, ncells, nred) * 8);
     n.bind = [=]() -> std::function<void(hipStream_t)> {
-      Dims ast = contiguous_strides(as);
-      int rdiff = (int)as.size() - (int)to.shape.size();
-      Dims cd, cs, rdd, rs;
-      for (int d = 0; d < (int)as.size(); ++d) {
-        bool reduced = d < rdiff || (to.shape[d - rdiff] == 1 && as[d] != 1);
-        if (as[d] == 1) continue;
-        if (reduced) { rdd.push_back(as[d]); rs.push_back(ast[d]); }
-        else { cd.push_back(as[d]); cs.push_back(ast[d]); }
-      }
-      tgk::Strided cells = make_strided(cd, cs, {}, {});
-      tgk::Strided red = make_strided(rdd, rs, {}, {});
-      int64_t ncells = prod(cd), nred = prod(rdd);
-      if (ncells != to.numel) throw Error(TG_INTERNAL, "sum_to_shape: cell count mismatch");
       {
         int64_t dd[2 * tgk::kMaxRank], ss[2 * tgk::kMaxRank];
         int r = 0;
@@ -917,7 +932,8 @@ void Runtime::lower_op(int i) {
         check_span("sum_to_shape src", T_[root(a)].numel, 0, dd, ss, r);
       }
       const float* pa = (const float*)dptr(a); float* po = (float*)dptr(out);
-      return [=](hipStream_t st) { tgk::sum_to_shape(pa, po, cells, red, ncells, nred, st); };
+      double* w = (double*)workspace_;
+      return [=](hipStream_t st) { tgk::reduce_sum(pa, po, cells, red, ncells, nred, 1.0, w, st); };
     };
   } else if (k == "matmul" || k == "matmul_batched") {
     int a = op.at("a").i32(), b = op.at("b").i32();
@@ -957,7 +973,7 @@ void Runtime::lower_op(int i) {
         n.kind = "scatter";
         n.flops = 0;
         n.bytes = 4.0 * (rows + rows * N + V * N);
-        workspace_bytes_ = std::max(workspace_bytes_, (size_t)(rows + V + 1) * 4 + 256);
+        workspace_bytes_ = std::max(workspace_bytes_, (size_t)(rows + 2 * V + 1) * 4 + 256);
         n.bind = [=]() -> std::function<void(hipStream_t)> {
           const int32_t* pi = (const int32_t*)dptr(idx); const float* pd = (const float*)dptr(b);
           float* po = (float*)dptr(out);
@@ -1186,9 +1202,22 @@ void Runtime::allocate() {
       ptr_[kv.second] = parent->ptr_[it->second];
     }
   }
-  // Inputs.
+  // Inputs: the caller's tensors first, then the runtime's per-step scalars (optimizer
+  // scalars, PRNG seed), so a step with device-resident data uploads only the tail.
+  auto internal = [&](int t) {
+    const std::string& nm = O(T_[t].src).at("name").str();
+    if (nm == "__prngSeed") return true;
+    if (!opt_cfg_) return false;
+    for (const char* f : {"lrtInputName", "decayShrinkInputName", "lrInputName"}) {
+      const tgj::Value* v = opt_cfg_->get(f);
+      if (v && v->kind == tgj::Value::String && v->str() == nm) return true;
+    }
+    return false;
+  };
   size_t ioff = 0;
-  for (int t : input_roots) { input_offset_[t] = ioff; ioff = align(ioff + std::max<int64_t>(4, T_[t].numel * 4)); }
+  for (int t : input_roots) if (!internal(t)) { input_offset_[t] = ioff; ioff = align(ioff + std::max<int64_t>(4, T_[t].numel * 4)); }
+  user_bytes_ = ioff;
+  for (int t : input_roots) if (internal(t)) { input_offset_[t] = ioff; ioff = align(ioff + std::max<int64_t>(4, T_[t].numel * 4)); }
   input_region_bytes_ = std::max<size_t>(ioff, 256);
   if (plan_only_) {
     input_region_ = fake + arena_bytes_ + 4096;
@@ -1265,57 +1294,99 @@ void Runtime::ensure_graph() {
   hip_check(hipGraphInstantiate(&graph_exec_, graph_, nullptr, nullptr, 0), "hipGraphInstantiate");
 }
 
-void Runtime::upload_inputs(int n, const char* const* names, const void* const* data, const int64_t* nbytes,
-                            bool device) {
-  std::set<std::string> seen;
-  std::vector<std::pair<int, int>> dev_copies;
-  for (int i = 0; i < n; ++i) {
-    std::string nm = names[i];
-    auto it = input_tid_.find(nm);
-    if (it == input_tid_.end()) continue;   // extra inputs are ignored, as a JS record would be
-    int t = it->second;
-    if (nbytes[i] != T_[t].numel * 4)
-      throw Error(TG_INVALID_ARGUMENT, "input '" + nm + "': expected " + std::to_string(T_[t].numel * 4) +
-                                           " bytes, got " + std::to_string(nbytes[i]));
-    if (!device) memcpy(staging_ + input_offset_[t], data[i], (size_t)nbytes[i]);
-    else dev_copies.emplace_back(i, t);
-    seen.insert(nm);
-  }
-  // Per-step scalars (src/worker.ts:187-214).
+void Runtime::stage_scalars() {
+  // Per-step scalars (src/worker.ts:187-214), written into the tail of the input region.
   if (opt_cfg_) {
     ++t_;
     double lr_now = resolve_lr(lr_, (double)t_);
     if (opt_kind_ == "adam") {
       double b1 = opt_cfg_->at("beta1").num(), b2 = opt_cfg_->at("beta2").num();
       float lrt = (float)(lr_now * std::sqrt(1 - std::pow(b2, (double)t_)) / (1 - std::pow(b1, (double)t_)));
-      int tid = input_tid_.at(opt_cfg_->at("lrtInputName").str());
-      memcpy(staging_ + input_offset_[tid], &lrt, 4);
-      seen.insert(opt_cfg_->at("lrtInputName").str());
+      memcpy(staging_ + input_offset_[input_tid_.at(opt_cfg_->at("lrtInputName").str())], &lrt, 4);
       const tgj::Value& dn = opt_cfg_->at("decayShrinkInputName");
       if (!dn.null()) {
         float ds = (float)(1 - lr_now * opt_cfg_->at("weightDecay").num());
         memcpy(staging_ + input_offset_[input_tid_.at(dn.str())], &ds, 4);
-        seen.insert(dn.str());
       }
     } else {
       float lr = (float)lr_now;
-      int tid = input_tid_.at(opt_cfg_->at("lrInputName").str());
-      memcpy(staging_ + input_offset_[tid], &lr, 4);
-      seen.insert(opt_cfg_->at("lrInputName").str());
+      memcpy(staging_ + input_offset_[input_tid_.at(opt_cfg_->at("lrInputName").str())], &lr, 4);
     }
   }
   if (uses_prng_) {
     ++prng_counter_;
     int32_t s = (int32_t)(uint32_t)prng_counter_;
     memcpy(staging_ + input_offset_[input_tid_.at("__prngSeed")], &s, 4);
-    seen.insert("__prngSeed");
+  }
+  if (input_region_bytes_ > user_bytes_)
+    hip_check(hipMemcpyAsync(input_region_ + user_bytes_, staging_ + user_bytes_, input_region_bytes_ - user_bytes_,
+                             hipMemcpyHostToDevice, stream_), "hipMemcpyAsync(H2D scalars)");
+}
+
+void Runtime::upload_inputs(int n, const char* const* names, const void* const* data, const int64_t* nbytes,
+                            bool device) {
+  // Validate the whole record before touching any state.
+  std::map<int, int> given;   // input tid -> argument index
+  for (int i = 0; i < n; ++i) {
+    auto it = input_tid_.find(names[i]);
+    if (it == input_tid_.end()) continue;   // extra inputs are ignored, as a JS record's would be
+    int t = it->second;
+    if (input_offset_[t] >= user_bytes_) continue;   // runtime-owned scalar: the worker overrides it
+    if (nbytes[i] != T_[t].numel * 4)
+      throw Error(TG_INVALID_ARGUMENT, std::string("input '") + names[i] + "': expected " +
+                                           std::to_string(T_[t].numel * 4) + " bytes, got " + std::to_string(nbytes[i]));
+    given[t] = i;
   }
   for (auto& kv : input_tid_)
-    if (!seen.count(kv.first)) throw Error(TG_INVALID_ARGUMENT, "missing input '" + kv.first + "'");
-  hip_check(hipMemcpyAsync(input_region_, staging_, input_region_bytes_, hipMemcpyHostToDevice, stream_), "hipMemcpyAsync(H2D)");
-  for (auto& c : dev_copies)
-    hip_check(hipMemcpyAsync(input_region_ + input_offset_[c.second], data[c.first], (size_t)nbytes[c.first],
-                             hipMemcpyDeviceToDevice, stream_), "hipMemcpyAsync(D2D)");
+    if (input_offset_[kv.second] < user_bytes_ && !given.count(kv.second))
+      throw Error(TG_INVALID_ARGUMENT, "missing input '" + kv.first + "'");
+  for (auto& g : given) {
+    int t = g.first, i = g.second;
+    if (device)
+      hip_check(hipMemcpyAsync(input_region_ + input_offset_[t], data[i], (size_t)nbytes[i], hipMemcpyDeviceToDevice,
+                               stream_), "hipMemcpyAsync(D2D)");
+    else
+      memcpy(staging_ + input_offset_[t], data[i], (size_t)nbytes[i]);
+  }
+  if (!device && user_bytes_)
+    hip_check(hipMemcpyAsync(input_region_, staging_, user_bytes_, hipMemcpyHostToDevice, stream_), "hipMemcpyAsync(H2D)");
+  stage_scalars();
+}
+
+// Device-resident batches for measurement and for callers that prefetch: slot k holds a
+// copy of the user-input part of the input region.
+void Runtime::stage_batch(int slot, int n, const char* const* names, const void* const* data, const int64_t* nbytes) {
+  if (slot < 0 || slot > 4096) throw Error(TG_INVALID_ARGUMENT, "stage: slot out of range");
+  if ((int)slots_.size() <= slot) slots_.resize(slot + 1, nullptr);
+  if (!slots_[slot]) hip_check(hipMalloc(&slots_[slot], std::max<size_t>(user_bytes_, 256)), "hipMalloc(slot)");
+  std::map<int, int> given;
+  for (int i = 0; i < n; ++i) {
+    auto it = input_tid_.find(names[i]);
+    if (it == input_tid_.end() || input_offset_[it->second] >= user_bytes_) continue;
+    if (nbytes[i] != T_[it->second].numel * 4) throw Error(TG_INVALID_ARGUMENT, std::string("stage: input '") + names[i] + "' has the wrong size");
+    given[it->second] = i;
+  }
+  std::vector<char> host(std::max<size_t>(user_bytes_, 1), 0);
+  for (auto& kv : input_tid_) {
+    if (input_offset_[kv.second] >= user_bytes_) continue;
+    auto g = given.find(kv.second);
+    if (g == given.end()) throw Error(TG_INVALID_ARGUMENT, "stage: missing input '" + kv.first + "'");
+    memcpy(host.data() + input_offset_[kv.second], data[g->second], (size_t)nbytes[g->second]);
+  }
+  if (user_bytes_) hip_check(hipMemcpy(slots_[slot], host.data(), user_bytes_, hipMemcpyHostToDevice), "hipMemcpy(slot)");
+}
+
+float Runtime::step_staged(int slot) {
+  if (!opt_cfg_) throw Error(TG_INVALID_ARGUMENT, "step: graph has no optimizer (use run)");
+  if (slot < 0 || slot >= (int)slots_.size() || !slots_[slot]) throw Error(TG_INVALID_ARGUMENT, "step: slot not staged");
+  if (user_bytes_)
+    hip_check(hipMemcpyAsync(input_region_, slots_[slot], user_bytes_, hipMemcpyDeviceToDevice, stream_), "hipMemcpyAsync(D2D)");
+  stage_scalars();
+  ensure_graph();
+  hip_check(hipGraphLaunch(graph_exec_, stream_), "hipGraphLaunch");
+  hip_check(hipMemcpyAsync(loss_host_, dptr(outputs_.at(0)), 4, hipMemcpyDeviceToHost, stream_), "hipMemcpyAsync(D2H)");
+  hip_check(hipStreamSynchronize(stream_), "hipStreamSynchronize");
+  return loss_host_[0];
 }
 
 float Runtime::step(int n, const char* const* names, const void* const* data, const int64_t* nbytes, bool device) {
@@ -1579,6 +1650,17 @@ tg_status tg_step_device(tg_runtime* h, int n, const char* const* names, const v
                          float* loss) {
   TG_ENTER(h);
   return guarded([&] { float l = h->rt->step(n, names, data, nbytes, true); if (loss) *loss = l; });
+}
+
+tg_status tg_stage_batch(tg_runtime* h, int slot, int n, const char* const* names, const void* const* data,
+                         const int64_t* nbytes) {
+  TG_ENTER(h);
+  return guarded([&] { h->rt->stage_batch(slot, n, names, data, nbytes); });
+}
+
+tg_status tg_step_staged(tg_runtime* h, int slot, float* loss) {
+  TG_ENTER(h);
+  return guarded([&] { float l = h->rt->step_staged(slot); if (loss) *loss = l; });
 }
 
 tg_status tg_run(tg_runtime* h, int n, const char* const* names, const void* const* data, const int64_t* nbytes,

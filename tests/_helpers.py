@@ -1,0 +1,74 @@
+"""Shared test helpers: trace small graphs, evaluate them on the CPU oracle, run the
+reference's finite-difference harness (test/_fdgrad.ts) against the oracle."""
+from __future__ import annotations
+
+import numpy as np
+
+import pyoracle
+from tensorgrad_amd import ir as IR
+from tensorgrad_amd.grad import append_grad
+from tensorgrad_amd.module import Mulberry32
+from tensorgrad_amd.trace import param_input, trace_fn
+
+
+def make_range(shape) -> np.ndarray:
+    """The reference tests' fixture: sin(0.1 i) * 0.5 (test/grad.ts:254-259)."""
+    n = int(np.prod(shape)) if len(shape) else 1
+    return (np.sin(np.arange(n, dtype=np.float64) * 0.1) * 0.5).astype(np.float32)
+
+
+def random_buf(n: int, seed: int = 12345) -> np.ndarray:
+    """mulberry32 uniform in [-0.5, 0.5) (test/_fdgrad.ts:116-127)."""
+    return (Mulberry32(seed).take(n) - 0.5).astype(np.float32)
+
+
+def wire(graph, param_grads=None, writebacks=None, optimizer=None) -> dict:
+    return {'graph': IR.graph_to_wire(graph), 'paramGrads': {k: v.id for k, v in (param_grads or {}).items()},
+            'writebacks': writebacks or [], 'optimizer': optimizer}
+
+
+def oracle_eval(graph, params=None, inputs=None, param_grads=None):
+    """Evaluate every op of `graph` on the oracle; returns {tensor id: value}."""
+    o = pyoracle.OracleRuntime(wire(graph, param_grads))
+    for k, v in (params or {}).items():
+        o.set_home(k, v)
+    o.retain_all(True)
+    o.run(inputs or {})
+    out = {}
+    for t in graph.tensors:
+        try:
+            out[t.id] = o.tensor(t.id)
+        except RuntimeError:
+            pass
+    return out
+
+
+def fd_check(name, shape, build, eps=1e-3, atol=5e-3, rtol=5e-3, extra=None, init=None):
+    """assertGradMatchesFD (test/_fdgrad.ts:43-106) on the oracle."""
+    extra = extra or {}
+    size = int(np.prod(shape))
+    p0 = random_buf(size) if init is None else np.array(init, np.float32).reshape(-1)
+    g = trace_fn(lambda: build(param_input('w', list(shape))))
+    gr = append_grad(g)
+    vals = oracle_eval(g, {'w': p0}, extra, gr.param_grads)
+    auto = vals[gr.param_grads['w'].id].reshape(-1).astype(np.float64)
+    fg = trace_fn(lambda: build(param_input('w', list(shape))))
+    o = pyoracle.OracleRuntime(wire(fg))
+    fd = np.zeros(size)
+    for i in range(size):
+        p = p0.copy()
+        p[i] = np.float32(p0[i] + eps)
+        o.set_home('w', p)
+        o.run(extra)
+        lp = float(o.output().reshape(-1)[0])
+        p[i] = np.float32(p0[i] - eps)
+        o.set_home('w', p)
+        o.run(extra)
+        lm = float(o.output().reshape(-1)[0])
+        fd[i] = (lp - lm) / (2 * eps)
+    err = np.abs(auto - fd)
+    rel = err / np.maximum(np.abs(fd), 1e-6)
+    worst = int(np.argmax(err))
+    assert not (err[worst] > atol and rel.max() > rtol), \
+        f'{name}: autograd={auto[worst]} fd={fd[worst]} |d|={err[worst]:.2e} rel={rel.max():.2e}'
+    return float(err.max())

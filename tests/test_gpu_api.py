@@ -1,0 +1,139 @@
+"""The compile / step API on the GPU (reference surface of src/compile.ts:198-319 and the
+worker handlers of src/worker.ts): step results, strict parameter upload, reset, setLR,
+attach (forward siblings sharing parameters, polymorphic batch), captures,
+replaceModel, destroy -> aborted."""
+import numpy as np
+import pytest
+
+import pyoracle
+from tensorgrad_amd import configs, nn
+from tensorgrad_amd import ops as O
+from tensorgrad_amd.backend import BackendError
+from tensorgrad_amd.build_ir import build_training_ir
+from tensorgrad_amd.compile import compile as tg_compile
+from tensorgrad_amd.module import Module
+from tensorgrad_amd.trace import capture
+
+pytestmark = pytest.mark.gpu
+
+
+def _c1():
+    cfg = configs.CONFIGS['mlp_sin']
+    return cfg, tg_compile(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer, seed=42)
+
+
+def test_step_matches_oracle_and_returns_completed():
+    cfg, t = _c1()
+    ir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer)
+    o = pyoracle.OracleRuntime(ir.wire())
+    o.upload_params(ir.initial_params(42))
+    for b in configs.batches(cfg, 5):
+        r = t.step(b)
+        assert r.kind == 'completed'
+        assert np.float32(r.loss) == np.float32(o.step(b))
+    assert t.param_names == ['l1.W', 'l1.b', 'l2.W', 'l2.b', 'l3.W', 'l3.b']
+    t.destroy()
+
+
+def test_upload_download_roundtrip_and_strictness():
+    cfg, t = _c1()
+    p = t.download_params()
+    p2 = {k: (v + 1).astype(np.float32) for k, v in p.items()}
+    t.upload_params(p2)
+    back = t.download_params()
+    assert all(np.array_equal(back[k], p2[k]) for k in p)
+    missing = dict(p2)
+    missing.pop('l1.W')
+    with pytest.raises(BackendError, match='missing'):
+        t.upload_params(missing)
+    with pytest.raises(BackendError, match='unknown'):
+        t.upload_params(dict(p2, bogus=np.zeros(3, np.float32)))
+    with pytest.raises(BackendError):
+        t.upload_params(dict(p2, **{'l1.b': np.zeros(3, np.float32)}))
+    t.destroy()
+
+
+def test_step_input_validation_fails_not_raises():
+    cfg, t = _c1()
+    r = t.step({'x': np.zeros((255, 1), np.float32), 'y': np.zeros((256, 1), np.float32)})
+    assert r.kind == 'failed' and 'bytes' in str(r.error)
+    r = t.step({'x': np.zeros((256, 1), np.float32)})
+    assert r.kind == 'failed' and 'missing' in str(r.error)
+    t.destroy()
+
+
+def test_reset_restores_initial_state():
+    cfg, t = _c1()
+    bs = configs.batches(cfg, 3)
+    first = [t.step(b).loss for b in bs]
+    t.reset()
+    again = [t.step(b).loss for b in bs]
+    assert first == again
+    t.reset(params=False, optimizer=True)
+    t.destroy()
+
+
+def test_set_lr_rebases_like_the_oracle():
+    cfg = configs.CONFIGS['mlp_sin']
+    ir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer)
+    t = tg_compile(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer, seed=42)
+    o = pyoracle.OracleRuntime(ir.wire())
+    o.upload_params(ir.initial_params(42))
+    bs = configs.batches(cfg, 12)
+    sched = {'kind': 'linear', 'peak': 0.01, 'final': 0.001, 'steps': 5}
+    for i, b in enumerate(bs):
+        if i == 4:
+            t.set_lr(sched)
+            o.set_lr(sched)
+        assert np.float32(t.step(b).loss) == np.float32(o.step(b))
+    t.destroy()
+
+
+def test_attach_shares_params_and_caches_shapes():
+    cfg, t = _c1()
+
+    def predict(m, inp):
+        return m.l3.fwd(O.relu(m.l2.fwd(O.relu(m.l1.fwd(inp['x'])))))
+    f = t.attach(predict, {'x': [None, 1]}, max_cached_shapes=2)
+    x = np.linspace(-3, 3, 10, dtype=np.float32).reshape(10, 1)
+    r1 = f.run({'x': x})
+    assert r1.kind == 'completed' and r1.output.shape == (10, 1)
+    t.step(configs.batches(cfg, 1)[0])      # training updates are visible to the sibling
+    r2 = f.run({'x': x})
+    assert not np.array_equal(r1.output, r2.output)
+    # same params on the host side give the same prediction through the oracle
+    g = f.graph_for({'x': x})
+    o = pyoracle.OracleRuntime({'graph': __import__('tensorgrad_amd').ir.graph_to_wire(g.graph), 'paramGrads': {},
+                                'writebacks': [], 'optimizer': None})
+    o.upload_params(t.download_params())
+    o.run({'x': x})
+    np.testing.assert_allclose(r2.output, o.output(), rtol=2e-6, atol=1e-7)
+    for n in (1, 3, 7):
+        assert f.run({'x': np.zeros((n, 1), np.float32)}).output.shape == (n, 1)
+    assert len(f._cache) == 2
+    t.destroy()
+    assert f.run({'x': x}).kind == 'aborted'
+
+
+def test_captures_and_replace_model():
+    class Cap(Module):
+        def __init__(self):
+            self.l1 = nn.Linear(1, 8)
+            self.l2 = nn.Linear(8, 1)
+
+    def loss(m, inp):
+        h = capture('hidden', O.relu(m.l1.fwd(inp['x'])))
+        return O.mean(O.square(O.sub(m.l2.fwd(h), inp['y'])))
+    inputs = {'x': [16, 1], 'y': [16, 1]}
+    t = tg_compile(Cap(), loss, inputs, {'kind': 'adam', 'lr': 1e-2}, seed=3)
+    x = np.linspace(-1, 1, 16, dtype=np.float32).reshape(16, 1)
+    r = t.step({'x': x, 'y': np.sin(x)})
+    h = r.captures.get('hidden')
+    assert h.shape == (16, 8) and np.all(h >= 0)
+    assert r.captures.shape('hidden') == (16, 8)
+    t.replace_model(configs.SinMLP(hidden=4), seed=1)
+    assert 'l3.W' in t.param_names and t.download_params()['l1.W'].size == 4
+    with pytest.raises(ValueError):
+        t.replace_model(Cap(), optimizer={'kind': 'sgd', 'lr': 0.1})
+    t.destroy()
+    assert t.step({'x': x, 'y': x}).kind == 'aborted'

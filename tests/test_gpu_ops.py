@@ -1,0 +1,278 @@
+"""Kernel-level parity on the GPU: every IR op kind, run as a one-op forward graph through
+the C ABI (tg_run), against the CPU oracle on the same inputs.
+
+Bar: element-wise, data-movement, stochastic, softmax, pooling, embedding and i32 ops are
+bit-exact; row sums / un-broadcast sums / conv weight gradients accumulate in f64 in a
+different order and must match to 1 ulp of f32; GEMMs accumulate in f32 on the matrix
+cores and must match to 2e-6 relative (norm-wise)."""
+import numpy as np
+import pytest
+
+import pyoracle
+from _helpers import make_range, wire
+from tensorgrad_amd import backend
+from tensorgrad_amd import ir as IR
+from tensorgrad_amd import ops as O
+from tensorgrad_amd.trace import tensor_input, trace_fn
+
+pytestmark = pytest.mark.gpu
+
+
+def _rand(shape, seed, lo=-1.0, hi=1.0):
+    r = np.random.default_rng(seed)
+    return r.uniform(lo, hi, size=shape).astype(np.float32)
+
+
+def run_both(build, inputs):
+    g = trace_fn(build)
+    w = wire(g)
+    rt = backend.NativeRuntime(IR.dumps(w))
+    out_t = g.tensors[g.outputs[0]]
+    dt = np.int32 if out_t.dtype in ('i32', 'bool') else np.float32
+    got = rt.run(inputs, out_t.shape, dt)
+    rt.destroy()
+    o = pyoracle.OracleRuntime(w)
+    o.run(inputs)
+    want = o.output()
+    return got, want
+
+
+def ulp_diff(a, b):
+    a = np.ascontiguousarray(a, np.float32).view(np.int32).astype(np.int64)
+    b = np.ascontiguousarray(b, np.float32).view(np.int32).astype(np.int64)
+    a = np.where(a < 0, -(a & 0x7FFFFFFF), a)
+    b = np.where(b < 0, -(b & 0x7FFFFFFF), b)
+    return int(np.max(np.abs(a - b))) if a.size else 0
+
+
+def exact(got, want):
+    assert got.shape == want.shape
+    assert np.array_equal(got.view(np.int32), want.view(np.int32)) or np.array_equal(got, want), \
+        f'max |diff| {np.max(np.abs(got.astype(np.float64) - want))}'
+
+
+def near(got, want, ulps=1):
+    assert got.shape == want.shape
+    assert ulp_diff(got, want) <= ulps
+
+
+def gemm_close(got, want, tol=2e-6):
+    err = np.linalg.norm(got.astype(np.float64) - want) / max(np.linalg.norm(want.astype(np.float64)), 1e-30)
+    assert err <= tol, f'rel err {err:.2e}'
+
+
+BIN_CASES = [([3, 5], [5]), ([2, 1, 4], [3, 1]), ([6, 7], [6, 7]), ([1000], []), ([4, 1], [1, 9])]
+
+
+@pytest.mark.parametrize('kind', ['add', 'sub', 'mul', 'div', 'min', 'max'])
+@pytest.mark.parametrize('shapes', BIN_CASES)
+def test_binary_broadcast(kind, shapes):
+    sa, sb = shapes
+    fn = {'add': O.add, 'sub': O.sub, 'mul': O.mul, 'div': O.div, 'min': O.minimum, 'max': O.maximum}[kind]
+    a, b = _rand(sa, 1), _rand(sb, 2, 0.5, 2.0)
+    got, want = run_both(lambda: fn(tensor_input('a', sa), tensor_input('b', sb)), {'a': a, 'b': b})
+    exact(got, want)
+
+
+def test_compare_and_where():
+    a, b = _rand([4, 6], 3), _rand([6], 4)
+    got, want = run_both(lambda: O.less(tensor_input('a', [4, 6]), tensor_input('b', [6])), {'a': a, 'b': b})
+    exact(got, want)
+
+    def body():
+        x = tensor_input('a', [4, 6])
+        return O.where(O.greater(x, tensor_input('b', [6])), x, O.mul(x, 0.25))
+    got, want = run_both(body, {'a': a, 'b': b})
+    exact(got, want)
+    got, want = run_both(lambda: O.leaky_relu(tensor_input('a', [4, 6]), 2), {'a': a})
+    exact(got, want)
+
+
+@pytest.mark.parametrize('kind', ['sqrt', 'rsqrt', 'log', 'exp', 'relu', 'neg', 'abs', 'tanh', 'sigmoid', 'erf', 'sin',
+                                  'cos'])
+def test_unary(kind):
+    x = _rand([3001], 5, -3, 3)
+    if kind in ('sqrt', 'rsqrt', 'log'):
+        x = np.abs(x) + np.float32(0.05)
+    fn = getattr(O, kind if kind != 'abs' else 'abs_')
+    got, want = run_both(lambda: fn(tensor_input('x', [3001])), {'x': x})
+    exact(got, want)
+
+
+def test_scalar_ops_and_gelu():
+    x = _rand([257, 3], 6, -4, 4)
+    got, want = run_both(lambda: O.gelu(tensor_input('x', [257, 3])), {'x': x})
+    exact(got, want)
+    got, want = run_both(lambda: O.add(O.mul(tensor_input('x', [257, 3]), 1 / 3), 0.1), {'x': x})
+    exact(got, want)
+
+
+@pytest.mark.parametrize('shape', [[7, 33], [3, 300], [2, 1], [1, 5000], [4096, 256]])
+def test_row_reductions(shape):
+    x = _rand(shape, 7)
+    got, want = run_both(lambda: O.mean(tensor_input('x', shape), -1, keep_dims=True), {'x': x})
+    near(got, want)
+    got, want = run_both(lambda: O.sum_(tensor_input('x', shape), -1), {'x': x})
+    near(got, want)
+    got, want = run_both(lambda: O.argmax(tensor_input('x', shape), -1), {'x': x})
+    exact(got, want)
+
+
+def test_argmax_ties_and_nan_semantics():
+    x = np.array([[1, 3, 3, 2], [np.nan, 5, 6, 1], [1, np.nan, 5, 5], [-0.0, 0.0, -1, -2], [2, 2, 2, 2]], np.float32)
+    x = np.concatenate([x, np.tile(np.array([[0.5, 7, 7, np.nan]], np.float32), (3, 1))])
+    got, want = run_both(lambda: O.argmax(tensor_input('x', [8, 4]), -1), {'x': x})
+    exact(got, want)
+    wide = np.full((3, 200), 1.0, np.float32)
+    wide[0, 150] = 2.0
+    wide[1, 77] = 2.0
+    wide[1, 140] = 2.0
+    wide[2, 0] = np.nan
+    wide[2, 99] = 5.0
+    got, want = run_both(lambda: O.argmax(tensor_input('x', [3, 200]), -1), {'x': wide})
+    exact(got, want)
+
+
+@pytest.mark.parametrize('cells', [([4, 3, 5], [3, 1]), ([6, 5], [5]), ([2, 3, 4, 5], [1, 3, 1, 1]),
+                                   ([65536, 4], [4]), ([1000], []), ([128, 64, 24, 24], [1, 64, 1, 1])])
+def test_sum_to_shape(cells):
+    src, dst = cells
+    x = _rand(src, 8)
+    got, want = run_both(lambda: O.sum_to_shape(tensor_input('x', src), dst), {'x': x})
+    # The GPU sums in f64, so it must equal the f64 sum rounded once (to 1 ulp); the
+    # evaluator's f32 running sum differs from that by its own rounding error, bounded by
+    # n * eps * max|running sum|.
+    xs = x.astype(np.float64).reshape(src)
+    keep = tuple(i for i in range(len(src)) if i >= len(src) - len(dst) and dst[i - len(src) + len(dst)] != 1)
+    axes = tuple(i for i in range(len(src)) if i not in keep)
+    exact64 = xs.sum(axis=axes).reshape(got.shape).astype(np.float32)
+    near(got, exact64)
+    n = np.prod(src) // max(1, np.prod(dst))
+    bound = n * 6e-8 * np.max(np.abs(np.cumsum(np.moveaxis(xs, axes, range(len(axes))).reshape(n, -1), 0)))
+    assert np.max(np.abs(got.astype(np.float64) - want)) <= bound + 1e-7
+
+
+def test_broadcast_permute_slice_concat_scatter():
+    x = _rand([2, 3, 4], 9)
+    got, want = run_both(lambda: O.permute(tensor_input('x', [2, 3, 4]), [2, 0, 1]), {'x': x})
+    exact(got, want)
+    got, want = run_both(lambda: O.reshape(O.permute(tensor_input('x', [2, 3, 4]), [1, 2, 0]), [12, 2]), {'x': x})
+    exact(got, want)
+    got, want = run_both(lambda: O.broadcast_to(tensor_input('x', [2, 3, 4]), [5, 2, 3, 4]), {'x': x})
+    exact(got, want)
+    got, want = run_both(lambda: O.narrow(tensor_input('x', [2, 3, 4]), 1, 1, 2), {'x': x})
+    exact(got, want)
+    y, z = _rand([2, 5, 4], 10), _rand([2, 1, 4], 11)
+    got, want = run_both(lambda: O.concat([tensor_input('x', [2, 3, 4]), tensor_input('y', [2, 5, 4]),
+                                           tensor_input('z', [2, 1, 4])], 1), {'x': x, 'y': y, 'z': z})
+    exact(got, want)
+    got, want = run_both(lambda: O.scatter_axis(tensor_input('x', [2, 3, 4]), [2, 7, 4], 1, 2, 5), {'x': x})
+    exact(got, want)
+    got, want = run_both(lambda: O.add(O.zeros([3, 4]), O.arange(4, 'f32')), {})
+    exact(got, want)
+
+
+def test_softmaxes_and_causal_mask():
+    x = _rand([3, 2, 17, 17], 12, -5, 5)
+    got, want = run_both(lambda: O.softmax_causal(tensor_input('x', [3, 2, 17, 17])), {'x': x})
+    exact(got, want)
+    got, want = run_both(lambda: O.where_causal(tensor_input('x', [3, 2, 17, 17]), -1e30), {'x': x})
+    exact(got, want)
+    y = _rand([50, 65], 13, -8, 8)
+    got, want = run_both(lambda: O.log_softmax(tensor_input('x', [50, 65])), {'x': y})
+    exact(got, want)
+    got, want = run_both(lambda: O.softmax(tensor_input('x', [50, 65]), 0), {'x': y})
+    exact(got, want)
+
+
+GEMMS = [([5, 7], [7, 3], False, False), ([2, 33, 65], [65, 17], False, False), ([129, 64], [64, 300], False, False),
+         ([70, 40], [50, 40], False, True), ([40, 70], [40, 50], True, False), ([4096, 256], [4096, 256], True, False),
+         ([300, 4096], [4096, 64], False, False)]
+
+
+@pytest.mark.parametrize('case', GEMMS)
+def test_matmul(case):
+    sa, sb, ta, tb = case
+    a, b = _rand(sa, 14), _rand(sb, 15)
+
+    def body():
+        A = tensor_input('a', sa)
+        B = tensor_input('b', sb)
+        if ta:
+            A = O.swap_axes(A, -1, -2)
+        if tb:
+            B = O.swap_axes(B, -1, -2)
+        return O.matmul(A, B)
+    got, want = run_both(body, {'a': a, 'b': b})
+    gemm_close(got, want)
+
+
+def test_matmul_batched_head_views():
+    # q @ k^T on split-head views: [B,T,D] -> [B,H,T,d] permutes read in place.
+    B, T, H, d = 3, 20, 4, 8
+    x, y = _rand([B, T, H * d], 16), _rand([B, T, H * d], 17)
+
+    def body():
+        q = O.split_heads(tensor_input('x', [B, T, H * d]), H)
+        k = O.split_heads(tensor_input('y', [B, T, H * d]), H)
+        return O.merge_heads(O.matmul(O.softmax_causal(O.mul(O.matmul(q, O.swap_axes(k, -1, -2)), 0.3)), k))
+    got, want = run_both(body, {'x': x, 'y': y})
+    gemm_close(got, want, 5e-6)
+
+
+def test_embedding_gather_and_scatter():
+    V, N, rows = 65, 48, 300
+    idx = np.random.default_rng(18).integers(-2, V + 2, size=rows).astype(np.int32)   # includes out-of-range ids
+    table, dy = _rand([V, N], 19), _rand([rows, N], 20)
+    got, want = run_both(lambda: O.embedding(tensor_input('t', [V, N]), tensor_input('i', [rows], 'i32')),
+                         {'t': table, 'i': idx})
+    exact(got, want)
+
+    def grad_body():
+        oh = O.reshape(O.one_hot(tensor_input('i', [rows], 'i32'), V), [rows, V])
+        return O.matmul(O.swap_axes(oh, -1, -2), tensor_input('d', [rows, N]))
+    got, want = run_both(grad_body, {'i': idx, 'd': dy})
+    exact(got, want)
+    got, want = run_both(lambda: O.one_hot(tensor_input('i', [rows], 'i32'), V), {'i': idx})
+    exact(got, want)
+
+
+def test_conv_and_pool_kernels():
+    B, Ci, H, W, Co, G = 2, 4, 9, 8, 6, 2
+    x, w = _rand([B, Ci, H, W], 21), _rand([Co, Ci // G, 3, 3], 22)
+    got, want = run_both(lambda: O.conv2d(tensor_input('x', [B, Ci, H, W]), tensor_input('w', [Co, Ci // G, 3, 3]),
+                                          stride=2, padding=1, groups=G), {'x': x, 'w': w})
+    exact(got, want)
+    yshape = list(want.shape)
+    dy = _rand(yshape, 23)
+    got, want = run_both(lambda: O.conv2d_input_grad(tensor_input('w', [Co, Ci // G, 3, 3]), tensor_input('d', yshape),
+                                                     H, W, 2, 2, 1, 1, G), {'w': w, 'd': dy})
+    exact(got, want)
+    got, want = run_both(lambda: O.conv2d_weight_grad(tensor_input('x', [B, Ci, H, W]), tensor_input('d', yshape),
+                                                      3, 3, 2, 2, 1, 1, G), {'x': x, 'd': dy})
+    near(got, want)
+    p = np.round(_rand([2, 3, 8, 8], 24) * 4) / 4   # ties inside windows
+    got, want = run_both(lambda: O.max_pool2d(tensor_input('x', [2, 3, 8, 8]), 3, stride=2, padding=1), {'x': p})
+    exact(got, want)
+    pd = _rand([2, 3, 4, 4], 25)
+    got, want = run_both(lambda: O.max_pool2d_grad(tensor_input('x', [2, 3, 8, 8]), tensor_input('d', [2, 3, 4, 4]),
+                                                    3, 3, 2, 2, 1, 1), {'x': p, 'd': pd})
+    exact(got, want)
+
+
+def test_relu_grad():
+    x, dy = _rand([1000], 26), _rand([1000], 27)
+    got, want = run_both(lambda: O.relu_grad(tensor_input('x', [1000]), tensor_input('d', [1000])), {'x': x, 'd': dy})
+    exact(got, want)
+
+
+def test_stochastic_ops_bit_exact():
+    x = _rand([64, 257], 28)
+    got, want = run_both(lambda: O.dropout(tensor_input('x', [64, 257]), 0.1), {'x': x})
+    exact(got, want)
+    zeros = np.mean(got == 0)
+    assert 0.07 < zeros < 0.13
+    got, want = run_both(lambda: O.randn([300, 7]), {})
+    exact(got, want)
+    got, want = run_both(lambda: O.categorical(tensor_input('x', [40, 65])), {'x': _rand([40, 65], 29)})
+    exact(got, want)
