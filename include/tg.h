@@ -48,7 +48,10 @@ int tg_device_count(void);
 
 /* Build a runtime for a traced graph: plan device memory, lower ops to gfx950 kernels.
  * Replaces the `createRuntime` request (src/worker-protocol.ts:66-74,
- * src/worker.ts:86-122). Initial params are then loaded with tg_upload_params. */
+ * src/worker.ts:86-122). Initial params are then loaded with tg_upload_params.
+ * Each step is captured once into a hipGraph and replayed; with TG_GRAPH=0 in the
+ * environment the same launches are issued directly instead (for profilers that do not
+ * follow graph launches). */
 tg_status tg_runtime_create(const char* ir_json, tg_runtime** out);
 
 /* A forward-only graph sharing `parent`'s parameter buffers. Replaces `compileForward`

@@ -182,6 +182,38 @@ __global__ void k_strided_copy(uint32_t* __restrict__ dst, const uint32_t* __res
   }
 }
 
+// 32-bit index form of strided_copy: merged dims, divisions by invariant multiplication,
+// VEC consecutive elements per thread (VEC = 4: 128-bit loads and stores).
+struct Copy32 {
+  int rank;
+  FastDiv fd[kMaxRank];
+  int32_t sd[kMaxRank], ss[kMaxRank];   // innermost strides already scaled by VEC
+};
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <int VEC>
+__global__ __launch_bounds__(256) void k_copy32(uint32_t* __restrict__ dst, const uint32_t* __restrict__ src, Copy32 c,
+                                                uint32_t nv) {
+  for (uint32_t t = blockIdx.x * 256u + threadIdx.x; t < nv; t += gridDim.x * 256u) {
+    uint32_t rem = t, od = 0, os = 0;
+#pragma unroll
+    for (int d = kMaxRank - 1; d >= 0; --d) {
+      if (d < c.rank) {
+        uint32_t cd = rem;
+        if (d > 0) {
+          const uint32_t q = fastdiv(rem, c.fd[d]);
+          cd = rem - q * c.fd[d].d;
+          rem = q;
+        }
+        od += cd * (uint32_t)c.sd[d];
+        os += cd * (uint32_t)c.ss[d];
+      }
+    }
+    if (VEC == 4) *reinterpret_cast<u32x4*>(dst + od) = *reinterpret_cast<const u32x4*>(src + os);
+    else dst[od] = src[os];
+  }
+}
+
 __global__ void k_fill(uint32_t* __restrict__ dst, uint32_t bits, int64_t n) {
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
     dst[i] = bits;
@@ -307,7 +339,43 @@ void where_causal(const float* a, float* out, int64_t outer, int64_t D, double f
 
 void strided_copy(void* dst, const void* src, const Strided& sp, int64_t n, hipStream_t st) {
   if (n <= 0) return;
-  k_strided_copy<<<grid_for(n), kThreads, 0, st>>>((uint32_t*)dst, (const uint32_t*)src, sp, n);
+  // Drop size-1 dims and merge dims contiguous in both operands.
+  int64_t dd[kMaxRank], s0[kMaxRank], s1[kMaxRank];
+  int r = 0;
+  int64_t span0 = 0, span1 = 0;
+  for (int d = 0; d < sp.rank; ++d) {
+    if (sp.dims[d] == 1) continue;
+    span0 += (sp.dims[d] - 1) * (sp.s0[d] < 0 ? -sp.s0[d] : sp.s0[d]);
+    span1 += (sp.dims[d] - 1) * (sp.s1[d] < 0 ? -sp.s1[d] : sp.s1[d]);
+    if (r > 0 && s0[r - 1] == sp.s0[d] * sp.dims[d] && s1[r - 1] == sp.s1[d] * sp.dims[d]) {
+      dd[r - 1] *= sp.dims[d]; s0[r - 1] = sp.s0[d]; s1[r - 1] = sp.s1[d];
+    } else {
+      dd[r] = sp.dims[d]; s0[r] = sp.s0[d]; s1[r] = sp.s1[d]; ++r;
+    }
+  }
+  bool small = n < (int64_t(1) << 31) && span0 < (int64_t(1) << 31) && span1 < (int64_t(1) << 31);
+  for (int d = 0; d < r; ++d) if (s0[d] < 0 || s1[d] < 0) small = false;
+  if (!small) {
+    k_strided_copy<<<grid_for(n), kThreads, 0, st>>>((uint32_t*)dst, (const uint32_t*)src, sp, n);
+    return;
+  }
+  if (r == 0) { dd[0] = 1; s0[0] = s1[0] = 0; r = 1; }
+  bool v4 = dd[r - 1] % 4 == 0 && s0[r - 1] == 1 && s1[r - 1] == 1 && ((uintptr_t)dst & 15) == 0 &&
+            ((uintptr_t)src & 15) == 0;
+  for (int d = 0; d < r - 1 && v4; ++d) v4 = s0[d] % 4 == 0 && s1[d] % 4 == 0;
+  const int vec = v4 ? 4 : 1;
+  Copy32 c{};
+  c.rank = r;
+  for (int d = 0; d < r; ++d) {
+    c.fd[d] = make_fastdiv((uint32_t)(d == r - 1 ? dd[d] / vec : dd[d]));
+    c.sd[d] = (int32_t)(d == r - 1 ? s0[d] * vec : s0[d]);
+    c.ss[d] = (int32_t)(d == r - 1 ? s1[d] * vec : s1[d]);
+  }
+  const int64_t nv = n / vec;
+  int64_t b = (nv + 255) / 256;
+  if (b > 16384) b = 16384;
+  if (vec == 4) k_copy32<4><<<(int)b, 256, 0, st>>>((uint32_t*)dst, (const uint32_t*)src, c, (uint32_t)nv);
+  else k_copy32<1><<<(int)b, 256, 0, st>>>((uint32_t*)dst, (const uint32_t*)src, c, (uint32_t)nv);
 }
 
 void fill(void* dst, int dt, double value, int64_t n, hipStream_t st) {

@@ -1,0 +1,236 @@
+// Fused element-wise groups for gfx950: one launch evaluates a chain of same-shape
+// pointwise IR ops per output element, keeping intermediates in registers instead of
+// one HBM round trip per op.
+//
+// Each group is a short straight-line program over f64 registers. Every register holds
+// exactly the value the unfused op would have stored (f32-rounded, or an i32 / bool),
+// so a fused group is bit-identical to running its ops one by one. Operands are loaded
+// once per element through per-operand strides (0 on broadcast axes); results that are
+// consumed outside the group are stored. The instruction stream is uniform across a
+// wavefront, so the dispatch costs scalar work only; the kernel stays HBM-bound.
+// Built with -ffp-contract=off.
+#include "kernels.h"
+
+#include <cmath>
+
+namespace tgk {
+namespace {
+
+__device__ __forceinline__ double js_max(double a, double b) {
+  if (isnan(a) || isnan(b)) return __longlong_as_double(0x7ff8000000000000LL);
+  if (a == 0.0 && b == 0.0) return (signbit(a) && signbit(b)) ? -0.0 : 0.0;
+  return a > b ? a : b;
+}
+__device__ __forceinline__ double js_min(double a, double b) {
+  if (isnan(a) || isnan(b)) return __longlong_as_double(0x7ff8000000000000LL);
+  if (a == 0.0 && b == 0.0) return (signbit(a) || signbit(b)) ? -0.0 : 0.0;
+  return a < b ? a : b;
+}
+__device__ __forceinline__ double js_sign(double x) {
+  if (isnan(x)) return x;
+  return x > 0 ? 1.0 : (x < 0 ? -1.0 : x);
+}
+__device__ __forceinline__ int32_t to_int32(double x) {
+  if (!isfinite(x)) return 0;
+  double m = fmod(trunc(x), 4294967296.0);
+  if (m < 0) m += 4294967296.0;
+  return (int32_t)(uint32_t)m;
+}
+__device__ __forceinline__ double round_to(double x, int dt) {
+  return dt == DT_F32 ? (double)(float)x : (double)to_int32(x);
+}
+__device__ __forceinline__ uint32_t pcg_f64(uint32_t seed, uint32_t sc, uint32_t idx) {
+  uint32_t h = seed ^ sc ^ idx;
+  double t = __dadd_rn(__dmul_rn((double)h, 747796405.0), 2891336453.0);
+  h = (uint32_t)(unsigned long long)t;
+  uint32_t x = h ^ (h >> ((h >> 28) + 4));
+  double t2 = __dmul_rn((double)x, 277803737.0);
+  h = (uint32_t)(unsigned long long)t2;
+  return h ^ (h >> 22);
+}
+
+__device__ __forceinline__ uint32_t fbits(float x) { return __float_as_uint(x); }
+__device__ __forceinline__ float bitsf(uint32_t x) { return __uint_as_float(x); }
+__device__ __forceinline__ double num(uint32_t x, int dt) { return dt == DT_F32 ? (double)bitsf(x) : (double)(int32_t)x; }
+__device__ __forceinline__ uint32_t from_num(double v, int dt) {
+  return dt == DT_F32 ? fbits((float)v) : (uint32_t)to_int32(v);
+}
+
+// General forms: one element. Kept out of line so the kernel body stays small.
+__device__ __noinline__ uint32_t general_op(const FusedInstr in, uint32_t x, uint32_t y, uint32_t seed,
+                                               uint32_t elem) {
+  const int ta = in.ta, tb = in.tb;
+  switch (in.op) {
+    case FO_ADD: return from_num(num(x, ta) + num(y, tb), in.dt);
+    case FO_SUB: return from_num(num(x, ta) - num(y, tb), in.dt);
+    case FO_MUL: return from_num(num(x, ta) * num(y, tb), in.dt);
+    case FO_DIV: return from_num(num(x, ta) / num(y, tb), in.dt);
+    case FO_MIN: return from_num(js_min(num(x, ta), num(y, tb)), in.dt);
+    case FO_MAX: return from_num(js_max(num(x, ta), num(y, tb)), in.dt);
+    case FO_LESS: return num(x, ta) < num(y, tb) ? 1u : 0u;
+    case FO_GREATER: return num(x, ta) > num(y, tb) ? 1u : 0u;
+    case FO_RSQRT: return fbits((float)(1.0 / sqrt((double)bitsf(x))));
+    case FO_LOG: return fbits((float)log((double)bitsf(x)));
+    case FO_EXP: return fbits((float)exp((double)bitsf(x)));
+    case FO_TANH: return fbits((float)tanh((double)bitsf(x)));
+    case FO_SIGMOID: return fbits((float)(0.5 + 0.5 * tanh(0.5 * (double)bitsf(x))));
+    case FO_ERF: {
+      // Abramowitz & Stegun 7.1.26, the reference's erf (test/_eval.ts:193-198).
+      const double v = bitsf(x);
+      const double sg = js_sign(v), av = fabs(v);
+      const double t = 1.0 / (1.0 + 0.3275911 * av);
+      const double pl = t * (0.254829592 + t * (-0.284496736 + t * (1.421413741 + t * (-1.453152027 + t * 1.061405429))));
+      return fbits((float)(sg * (1.0 - pl * exp(-av * av))));
+    }
+    case FO_SIN: return fbits((float)sin((double)bitsf(x)));
+    case FO_COS: return fbits((float)cos((double)bitsf(x)));
+    default: {   // FO_DROPOUT
+      const uint32_t hh = pcg_f64(seed, in.salt, elem);
+      const double u = (double)hh / 4294967296.0;
+      return fbits((float)((double)bitsf(x) * (u >= in.imm ? in.imm2 : 0.0)));
+    }
+  }
+}
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Thread t evaluates elements VEC*t .. VEC*t + VEC - 1 of the (row-major) iteration
+// space. The register file lives in LDS: register k of element e of thread j is word
+// (k * VEC + e) * 256 + j, so every register access of a wavefront is one conflict-free
+// LDS instruction, whatever the (wave-uniform) register index.
+template <int VEC>
+__global__ __launch_bounds__(256) void k_fused(const FusedProgram p, uint32_t nv) {
+  extern __shared__ uint32_t regs[];   // (n_in + n_instr) * VEC * 256 words
+  uint32_t* const my = regs + threadIdx.x;
+#define REG(k, e) my[((k) * VEC + (e)) * 256]
+  const uint32_t seed = p.seed ? (uint32_t)*p.seed : 0u;
+  // The program is read-only for the kernel's lifetime: reading it through the constant
+  // address space lets the compiler use scalar loads.
+  typedef const __attribute__((address_space(4))) FusedInstr* ConstCode;
+  const ConstCode code = (ConstCode)(uintptr_t)p.code;
+  for (uint32_t t = blockIdx.x * 256u + threadIdx.x; t < nv; t += gridDim.x * 256u) {
+    uint32_t coord[kMaxRank] = {};
+    if (p.any_strided) {
+      uint32_t rem = t;
+#pragma unroll
+      for (int d = kMaxRank - 1; d >= 1; --d) {
+        if (d < p.rank) {
+          const uint32_t q = fastdiv(rem, p.div[d]);
+          coord[d] = rem - q * p.div[d].d;
+          rem = q;
+        }
+      }
+      coord[0] = rem;
+    }
+#pragma unroll
+    for (int k = 0; k < kFusedMaxIn; ++k) {
+      if (k < p.n_in) {
+        const uint32_t* src = static_cast<const uint32_t*>(p.in[k]);
+        const int mode = p.in_mode[k];
+        uint32_t off = 0;
+        if (mode == FM_CONTIG) {
+          off = t * VEC;
+        } else if (mode != FM_SCALAR) {
+#pragma unroll
+          for (int d = 0; d < kMaxRank; ++d)
+            if (d < p.rank) off += coord[d] * (uint32_t)p.in_strides[k][d];
+        }
+        if (VEC == 4 && (mode == FM_CONTIG || mode == FM_STRIDED_V)) {
+          const u32x4 v = *reinterpret_cast<const u32x4*>(src + off);
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) REG(k, e) = v[e];
+        } else if (VEC == 1 || mode == FM_SCALAR || mode == FM_STRIDED_B) {
+          const uint32_t v = src[off];
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) REG(k, e) = v;
+        } else {
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) REG(k, e) = src[off + e * p.in_inner[k]];
+        }
+      }
+    }
+    for (int q = 0; q < p.n_instr; ++q) {
+      const int op = code[q].op, a = code[q].a, b = code[q].b, dst = code[q].dst;
+      switch (op) {
+#define TG_EACH(EXPR)                                              \
+  _Pragma("unroll") for (int e = 0; e < VEC; ++e) {                \
+    const uint32_t X = REG(a, e);                                  \
+    const uint32_t Y = REG(b, e);                                  \
+    (void)Y;                                                       \
+    REG(dst, e) = (EXPR);                                          \
+  }                                                                \
+  break;
+        // f32 +, -, *, /: the correctly rounded f32 operation equals computing in f64
+        // and rounding once.
+        case FO_FADD: TG_EACH(fbits(bitsf(X) + bitsf(Y)))
+        case FO_FSUB: TG_EACH(fbits(bitsf(X) - bitsf(Y)))
+        case FO_FMUL: TG_EACH(fbits(bitsf(X) * bitsf(Y)))
+        case FO_FDIV: TG_EACH(fbits(bitsf(X) / bitsf(Y)))
+        case FO_MULS: {
+          const double s = code[q].imm;
+          const int ta = code[q].ta;
+          TG_EACH(fbits((float)(num(X, ta) * s)))
+        }
+        case FO_ADDS: {
+          const double s = code[q].imm;
+          const int ta = code[q].ta;
+          TG_EACH(fbits((float)(num(X, ta) + s)))
+        }
+        // f64 sqrt rounded once to f32 is the correctly rounded f32 square root.
+        case FO_SQRT: TG_EACH(fbits((float)sqrt((double)bitsf(X))))
+        case FO_NEG: TG_EACH(X ^ 0x80000000u)
+        case FO_ABS: TG_EACH(X & 0x7fffffffu)
+        // max(x, 0) with JS semantics: NaN stays NaN, -0 becomes +0.
+        case FO_RELU: TG_EACH(bitsf(X) != bitsf(X) ? 0x7fc00000u : (bitsf(X) > 0.0f ? X : 0u))
+        case FO_RELU_GRAD: TG_EACH(bitsf(X) > 0.0f ? Y : 0u)
+        case FO_WHERE: {
+          const int c = code[q].c;
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) REG(dst, e) = REG(a, e) != 0u ? REG(b, e) : REG(c, e);
+          break;
+        }
+        case FO_COPY: TG_EACH(X)
+#undef TG_EACH
+        default: {
+          FusedInstr in;
+          in.op = op; in.dst = dst; in.a = a; in.b = b; in.c = code[q].c;
+          in.dt = code[q].dt; in.ta = code[q].ta; in.tb = code[q].tb; in.salt = code[q].salt;
+          in.imm = code[q].imm; in.imm2 = code[q].imm2;
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) REG(dst, e) = general_op(in, REG(a, e), REG(b, e), seed, t * VEC + e);
+          break;
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kFusedMaxOut; ++k) {
+      if (k < p.n_out) {
+        uint32_t* dstp = static_cast<uint32_t*>(p.out[k]);
+        const int reg = p.out_reg[k];
+        if (VEC == 4) {
+          u32x4 v;
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) v[e] = REG(reg, e);
+          *reinterpret_cast<u32x4*>(dstp + t * VEC) = v;
+        } else {
+          dstp[t] = REG(reg, 0);
+        }
+      }
+    }
+  }
+#undef REG
+}
+
+}  // namespace
+
+void fused(const FusedProgram& prog, int64_t n, hipStream_t st) {
+  if (n <= 0) return;
+  int64_t b = (n + 255) / 256;
+  if (b > 16384) b = 16384;
+  // LDS holds only the registers the program uses.
+  const size_t lds = (size_t)(prog.n_in + prog.n_instr) * prog.vec * 256 * 4;
+  if (prog.vec == 4) k_fused<4><<<(int)b, 256, lds, st>>>(prog, (uint32_t)n);
+  else k_fused<1><<<(int)b, 256, lds, st>>>(prog, (uint32_t)n);
+}
+
+}  // namespace tgk

@@ -5,40 +5,126 @@
 // rather than materialised. The batch index z splits as (z / bdiv, z % bdiv) with one
 // stride each, which covers [B, H, T, d] head views.
 //
-// Block tile BM x BN x 16 staged through LDS (k-major, padded rows: conflict-free MFMA
-// operand reads), 256 threads = 4 waves in a 2 x 2 grid, each wave owning
-// (BM/2) x (BN/2) built from 32 x 32 MFMA tiles. The next k-tile is prefetched into
-// registers while the current one is multiplied. Tails in M, N and K are zero-filled
-// on load and masked on store. Small-output / long-K problems (weight gradients) use a
-// deterministic split-K: each split writes its own partial tile and a second kernel
-// sums the partials in split order (no atomics).
+// Block tile BM x BN x BK (BK = 32 for 128-row tiles, 64 for 64 x 64), 256 threads = 4
+// waves in a 2 x 2 grid, each wave owning (BM/2) x (BN/2) built from 32 x 32 MFMA tiles.
+//
+// k-permuted operand mapping: an MFMA consumes k-pairs, lane half h supplying k index h.
+// Within every group of 8 consecutive k, MFMA number j takes k = 4h + j for lane half h,
+// so over j = 0..3 the two halves cover all 8 k and a lane needs 4 *consecutive* k values
+// per operand. Sums over k are unchanged (every A[m][k] still meets B[k][n]).
+//
+// Each operand is staged in LDS in the layout it has in memory, so global loads and LDS
+// writes are both 128-bit and nothing is transposed on the way in:
+//  * k-contiguous operand: LDS rows [r][BK k] padded by 4 floats; a lane's 4 k values
+//    are one 128-bit LDS read;
+//  * row-contiguous operand: LDS rows [k][rows + 8] (the +8 puts the two lane halves on
+//    disjoint banks); a lane's 4 k values are four 32-bit reads.
+// Interior tiles of 16-byte aligned operands load float4; tails and other strides fall
+// back to bounds-checked scalar loads (zero fill). The next k-tile is prefetched into
+// registers while the current one is multiplied and then stored into the other half of
+// a double-buffered LDS stage, so each stage needs a single barrier.
+//
+// Tiles are numbered so that each of the chip's 8 XCDs (which take workgroups round
+// robin and each own an L2) receives a contiguous run of tiles, n fastest: the A rows of
+// a tile row are then fetched into one L2 instead of several.
+//
+// Accumulation is blocked: each BK-k stage accumulates into a fresh MFMA accumulator
+// that is then added to the running sum, which keeps the f32 rounding error of long
+// reductions well below that of one running sum over all of K. Small-output / long-K problems (weight
+// gradients) use a deterministic split-K: each split writes its own partial tile and a
+// second kernel sums the partials in split order (no atomics).
 #include "kernels.h"
+
+#include <stdexcept>
 
 namespace tgk {
 namespace {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kBK = 16;
 constexpr int kThreads = 256;
+constexpr int kXcds = 8;
 
 struct GemmArgs {
   GemmDesc d;
   int64_t k_per_split;
   int splits;
-  float* out;        // C, or the split-K workspace
-  int64_t sOs, sOz;  // workspace strides (split, batch) when splitting
+  int tiles_n, tiles_m;   // tile grid (per batch and split)
+  float* out;             // split-K workspace (splits > 1)
+  int64_t sOs, sOz;       // workspace strides (split, batch)
 };
 
-template <int BM, int BN>
+// One operand's ROWS x BK tile: element (r, k) at X[r*sr + k*sk].
+template <int ROWS, int BK, bool KFAST>
+struct Tile {
+  static constexpr int LD = KFAST ? BK + 4 : ROWS + 8;
+  static constexpr int SIZE = KFAST ? ROWS * LD : BK * LD;
+  static constexpr int Q = ROWS * BK / (4 * kThreads);
+  static_assert(Q >= 1, "tile too small for the block");
+  f32x4 q[Q];
+
+  __device__ __forceinline__ static void coords(int idx, int& rr, int& kk) {
+    if (KFAST) { rr = idx / (BK / 4); kk = (idx % (BK / 4)) * 4; }
+    else { rr = (idx % (ROWS / 4)) * 4; kk = idx / (ROWS / 4); }
+  }
+
+  __device__ __forceinline__ void load(const float* X, int64_t sr, int64_t sk, int64_t r0, int64_t rlim, int64_t k0,
+                                       int64_t klim, bool vec_ok, int tid) {
+#pragma unroll
+    for (int e = 0; e < Q; ++e) {
+      int rr, kk;
+      coords(tid + e * kThreads, rr, kk);
+      const int64_t gr = r0 + rr, gk = k0 + kk;
+      if (KFAST) {
+        if (vec_ok && gr < rlim && gk + 3 < klim) {
+          q[e] = *reinterpret_cast<const f32x4*>(X + gr * sr + gk);
+        } else {
+#pragma unroll
+          for (int u = 0; u < 4; ++u) q[e][u] = (gr < rlim && gk + u < klim) ? X[gr * sr + (gk + u) * sk] : 0.0f;
+        }
+      } else {
+        if (vec_ok && gr + 3 < rlim && gk < klim) {
+          q[e] = *reinterpret_cast<const f32x4*>(X + gr + gk * sk);
+        } else {
+#pragma unroll
+          for (int u = 0; u < 4; ++u) q[e][u] = (gr + u < rlim && gk < klim) ? X[(gr + u) * sr + gk * sk] : 0.0f;
+        }
+      }
+    }
+  }
+
+  __device__ __forceinline__ void store(float* L, int tid) const {
+#pragma unroll
+    for (int e = 0; e < Q; ++e) {
+      int rr, kk;
+      coords(tid + e * kThreads, rr, kk);
+      if (KFAST) *reinterpret_cast<f32x4*>(L + rr * LD + kk) = q[e];
+      else *reinterpret_cast<f32x4*>(L + kk * LD + rr) = q[e];
+    }
+  }
+
+  // The 4 consecutive-k values (kb .. kb+3) of row `row`.
+  __device__ __forceinline__ static f32x4 frag(const float* L, int row, int kb) {
+    if (KFAST) return *reinterpret_cast<const f32x4*>(L + row * LD + kb);
+    f32x4 v;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) v[u] = L[(kb + u) * LD + row];
+    return v;
+  }
+};
+
+template <int BM, int BN, int BK, bool AK, bool BKF>
 __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g) {
   constexpr int WM = BM / 2, WN = BN / 2;       // wave tile
   constexpr int TM = WM / 32, TN = WN / 32;     // MFMA tiles per wave
-  constexpr int LDA = BM + 4, LDB = BN + 4;
-  constexpr int A_PER_T = BM * kBK / kThreads;  // elements each thread stages
-  constexpr int B_PER_T = BN * kBK / kThreads;
-  __shared__ float As[kBK * LDA];
-  __shared__ float Bs[kBK * LDB];
+  constexpr int NG = BK / 8;                    // k-groups of 8 per stage
+  using TA = Tile<BM, BK, AK>;
+  using TB = Tile<BN, BK, BKF>;
+  // Two stages of LDS: stage s+1 is stored while stage s is multiplied, so each stage
+  // needs one barrier.
+  __shared__ __attribute__((aligned(16))) float As[2][TA::SIZE];
+  __shared__ __attribute__((aligned(16))) float Bs[2][TB::SIZE];
 
   const GemmDesc& d = g.d;
   const int tid = threadIdx.x;
@@ -46,57 +132,28 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g) {
   const int wave = tid / 64;
   const int wm0 = (wave / 2) * WM, wn0 = (wave % 2) * WN;
 
-  const int64_t m0 = (int64_t)blockIdx.y * BM, n0 = (int64_t)blockIdx.x * BN;
-  const int64_t zz = blockIdx.z / g.splits;
-  const int split = blockIdx.z % g.splits;
+  // XCD-contiguous tile numbering (see the header comment).
+  const uint32_t nblk = gridDim.x;
+  uint32_t b = blockIdx.x;
+  if (nblk % kXcds == 0) b = (b % kXcds) * (nblk / kXcds) + b / kXcds;
+  const uint32_t tn = b % g.tiles_n;
+  const uint32_t rest = b / g.tiles_n;
+  const uint32_t tm = rest % g.tiles_m;
+  const uint32_t zs = rest / g.tiles_m;
+  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+  const int64_t zz = zs / g.splits;
+  const int split = zs % g.splits;
   const int64_t z0 = zz / d.bdiv, z1 = zz % d.bdiv;
   const float* A = d.A + z0 * d.sAz0 + z1 * d.sAz1;
   const float* B = d.B + z0 * d.sBz0 + z1 * d.sBz1;
   const int64_t kbeg = split * g.k_per_split;
   const int64_t kend = min(d.K, kbeg + g.k_per_split);
 
-  // Thread -> staged element mapping: the unit-stride dimension varies fastest across
-  // threads so global loads coalesce.
-  const bool a_kfast = d.sAk == 1;
-  const bool b_nfast = d.sBn == 1 || d.sBk != 1;
+  const bool a_vec = ((uintptr_t)A & 15) == 0 && (AK ? (d.sAm & 3) == 0 : (d.sAm == 1 && (d.sAk & 3) == 0));
+  const bool b_vec = ((uintptr_t)B & 15) == 0 && (BKF ? (d.sBn & 3) == 0 : (d.sBn == 1 && (d.sBk & 3) == 0));
 
-  float ra[A_PER_T], rb[B_PER_T];
-
-  auto load_tiles = [&](int64_t k0) {
-#pragma unroll
-    for (int e = 0; e < A_PER_T; ++e) {
-      int idx = tid + e * kThreads;
-      int mm, kk;
-      if (a_kfast) { kk = idx % kBK; mm = idx / kBK; } else { mm = idx % BM; kk = idx / BM; }
-      int64_t gm = m0 + mm, gk = k0 + kk;
-      ra[e] = (gm < d.M && gk < kend) ? A[gm * d.sAm + gk * d.sAk] : 0.0f;
-    }
-#pragma unroll
-    for (int e = 0; e < B_PER_T; ++e) {
-      int idx = tid + e * kThreads;
-      int nn, kk;
-      if (b_nfast) { nn = idx % BN; kk = idx / BN; } else { kk = idx % kBK; nn = idx / kBK; }
-      int64_t gn = n0 + nn, gk = k0 + kk;
-      rb[e] = (gn < d.N && gk < kend) ? B[gk * d.sBk + gn * d.sBn] : 0.0f;
-    }
-  };
-  auto store_tiles = [&]() {
-#pragma unroll
-    for (int e = 0; e < A_PER_T; ++e) {
-      int idx = tid + e * kThreads;
-      int mm, kk;
-      if (a_kfast) { kk = idx % kBK; mm = idx / kBK; } else { mm = idx % BM; kk = idx / BM; }
-      As[kk * LDA + mm] = ra[e];
-    }
-#pragma unroll
-    for (int e = 0; e < B_PER_T; ++e) {
-      int idx = tid + e * kThreads;
-      int nn, kk;
-      if (b_nfast) { nn = idx % BN; kk = idx / BN; } else { kk = idx % kBK; nn = idx / kBK; }
-      Bs[kk * LDB + nn] = rb[e];
-    }
-  };
-
+  TA sa;
+  TB sb;
   f32x16 acc[TM][TN];
 #pragma unroll
   for (int i = 0; i < TM; ++i)
@@ -105,26 +162,65 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  const int lrow = lane % 32, lk = lane / 32;
-  if (kbeg < kend) load_tiles(kbeg);
-  for (int64_t k0 = kbeg; k0 < kend; k0 += kBK) {
-    __syncthreads();
-    store_tiles();
-    __syncthreads();
-    if (k0 + kBK < kend) load_tiles(k0 + kBK);
-#pragma unroll
-    for (int ks = 0; ks < kBK; ks += 2) {
-      float av[TM], bv[TN];
-#pragma unroll
-      for (int i = 0; i < TM; ++i) av[i] = As[(ks + lk) * LDA + wm0 + i * 32 + lrow];
-#pragma unroll
-      for (int j = 0; j < TN; ++j) bv[j] = Bs[(ks + lk) * LDB + wn0 + j * 32 + lrow];
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i], bv[j], acc[i][j], 0, 0, 0);
+  const int lrow = lane % 32, h = lane / 32;
+  const int nst = kbeg < kend ? (int)((kend - kbeg + BK - 1) / BK) : 0;
+  if (nst > 0) {
+    sa.load(A, d.sAm, d.sAk, m0, d.M, kbeg, kend, a_vec, tid);
+    sb.load(B, d.sBn, d.sBk, n0, d.N, kbeg, kend, b_vec, tid);
+    sa.store(As[0], tid);
+    sb.store(Bs[0], tid);
+  }
+  __syncthreads();
+  for (int st = 0; st < nst; ++st) {
+    const int cur = st & 1;
+    const bool more = st + 1 < nst;
+    if (more) {
+      const int64_t k1 = kbeg + (int64_t)(st + 1) * BK;
+      sa.load(A, d.sAm, d.sAk, m0, d.M, k1, kend, a_vec, tid);
+      sb.load(B, d.sBn, d.sBk, n0, d.N, k1, kend, b_vec, tid);
     }
+    const float* Ac = As[cur];
+    const float* Bc = Bs[cur];
+    // One fresh accumulator per stage (blocked summation over k, see header).
+    f32x16 part[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) part[i][j][r] = 0.0f;
+    f32x4 av[2][TM], bv[2][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) av[0][i] = TA::frag(Ac, wm0 + i * 32 + lrow, h * 4);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) bv[0][j] = TB::frag(Bc, wn0 + j * 32 + lrow, h * 4);
+#pragma unroll
+    for (int grp = 0; grp < NG; ++grp) {
+      const int c = grp & 1;
+      if (grp + 1 < NG) {   // fragments of the next k-group while this one multiplies
+        const int kb = (grp + 1) * 8 + h * 4;
+#pragma unroll
+        for (int i = 0; i < TM; ++i) av[c ^ 1][i] = TA::frag(Ac, wm0 + i * 32 + lrow, kb);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) bv[c ^ 1][j] = TB::frag(Bc, wn0 + j * 32 + lrow, kb);
+      }
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            part[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[c][i][jj], bv[c][j][jj], part[i][j], 0, 0, 0);
+    }
+    if (more) {
+      sa.store(As[cur ^ 1], tid);
+      sb.store(Bs[cur ^ 1], tid);
+    }
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) acc[i][j] += part[i][j];
+    __syncthreads();
   }
 
   // Store: register r of lane l holds row (r/4)*8 + (l/32)*4 + r%4, column l%32.
@@ -145,32 +241,39 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g) {
       if (gn >= d.N) continue;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int64_t gm = m0 + wm0 + i * 32 + (r / 4) * 8 + lk * 4 + (r % 4);
+        const int64_t gm = m0 + wm0 + i * 32 + (r / 4) * 8 + h * 4 + (r % 4);
         if (gm < d.M) O[gm * sOm + gn * sOn] = acc[i][j][r];
       }
     }
 }
 
-// Sum split-K partials in split order into C.
+// Sum split-K partials in split order into C (eight partial loads in flight per thread).
 __global__ void k_splitk_reduce(const float* __restrict__ work, int splits, int64_t sOs, GemmDesc d) {
   const int64_t MN = d.M * d.N, total = MN * d.batch;
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
     float s = 0.0f;
-    for (int sp = 0; sp < splits; ++sp) s += work[sp * sOs + i];
+    for (int sp0 = 0; sp0 < splits; sp0 += 8) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = sp0 + u < splits ? work[(sp0 + u) * sOs + i] : 0.0f;
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (sp0 + u < splits) s += v[u];
+    }
     const int64_t zz = i / MN, r = i % MN, m = r / d.N, n = r % d.N;
     const int64_t z0 = zz / d.bdiv, z1 = zz % d.bdiv;
     d.C[z0 * d.sCz0 + z1 * d.sCz1 + m * d.sCm + n * d.sCn] = s;
   }
 }
 
-struct Plan { int bm, bn, splits; int64_t kps; };
+struct Plan { int bm, bn, bk, splits; int64_t kps; };
 
 Plan plan_for(const GemmDesc& d) {
   auto tiles = [&](int bm, int bn) { return ((d.M + bm - 1) / bm) * ((d.N + bn - 1) / bn) * d.batch; };
-  Plan p{64, 64, 1, d.K};
-  if (tiles(128, 128) >= 256) p = Plan{128, 128, 1, d.K};
-  else if (tiles(128, 64) >= 256) p = Plan{128, 64, 1, d.K};
-  else if (tiles(64, 128) >= 256) p = Plan{64, 128, 1, d.K};
+  Plan p{64, 64, 64, 1, d.K};
+  if (tiles(128, 128) >= 256) p = Plan{128, 128, 32, 1, d.K};
+  else if (tiles(128, 64) >= 256) p = Plan{128, 64, 32, 1, d.K};
+  else if (tiles(64, 128) >= 256) p = Plan{64, 128, 32, 1, d.K};
   const int64_t t = tiles(p.bm, p.bn);
   if (t < 128 && d.K >= 1024) {
     int64_t want = (256 + t - 1) / t;
@@ -179,7 +282,7 @@ Plan plan_for(const GemmDesc& d) {
     if (s > 64) s = 64;
     if (s > 1) {
       int64_t kps = (d.K + s - 1) / s;
-      kps = (kps + kBK - 1) / kBK * kBK;
+      kps = (kps + p.bk - 1) / p.bk * p.bk;
       p.splits = (int)((d.K + kps - 1) / kps);
       p.kps = kps;
     }
@@ -197,23 +300,36 @@ int64_t gemm_workspace_floats(const GemmDesc& d) {
 void gemm(const GemmDesc& d, float* work, hipStream_t st) {
   if (d.M <= 0 || d.N <= 0 || d.batch <= 0) return;
   Plan p = plan_for(d);
-  GemmArgs g{d, p.kps, p.splits, nullptr, 0, 0};
+  GemmArgs g{d, p.kps, p.splits, 0, 0, nullptr, 0, 0};
   if (p.splits > 1) {
     g.out = work;
     g.sOz = d.M * d.N;
     g.sOs = d.batch * d.M * d.N;
   }
-  dim3 grid((unsigned)((d.N + p.bn - 1) / p.bn), (unsigned)((d.M + p.bm - 1) / p.bm),
-            (unsigned)(d.batch * p.splits));
-  if (p.bm == 128 && p.bn == 128) k_gemm<128, 128><<<grid, kThreads, 0, st>>>(g);
-  else if (p.bm == 128) k_gemm<128, 64><<<grid, kThreads, 0, st>>>(g);
-  else if (p.bn == 128) k_gemm<64, 128><<<grid, kThreads, 0, st>>>(g);
-  else k_gemm<64, 64><<<grid, kThreads, 0, st>>>(g);
+  g.tiles_n = (int)((d.N + p.bn - 1) / p.bn);
+  g.tiles_m = (int)((d.M + p.bm - 1) / p.bm);
+  const int64_t blocks = (int64_t)g.tiles_n * g.tiles_m * d.batch * p.splits;
+  if (blocks >= (int64_t(1) << 31)) throw std::runtime_error("gemm: too many tiles");
+  const dim3 grid((unsigned)blocks);
+  const bool ak = d.sAk == 1;
+  const bool bk = d.sBk == 1 && d.sBn != 1;
+#define TG_GEMM_LAUNCH(BM_, BN_, BK_)                                                      \
+  do {                                                                                     \
+    if (ak && bk) k_gemm<BM_, BN_, BK_, true, true><<<grid, kThreads, 0, st>>>(g);        \
+    else if (ak) k_gemm<BM_, BN_, BK_, true, false><<<grid, kThreads, 0, st>>>(g);        \
+    else if (bk) k_gemm<BM_, BN_, BK_, false, true><<<grid, kThreads, 0, st>>>(g);        \
+    else k_gemm<BM_, BN_, BK_, false, false><<<grid, kThreads, 0, st>>>(g);               \
+  } while (0)
+  if (p.bm == 128 && p.bn == 128) TG_GEMM_LAUNCH(128, 128, 32);
+  else if (p.bm == 128) TG_GEMM_LAUNCH(128, 64, 32);
+  else if (p.bn == 128) TG_GEMM_LAUNCH(64, 128, 32);
+  else TG_GEMM_LAUNCH(64, 64, 64);
+#undef TG_GEMM_LAUNCH
   if (p.splits > 1) {
     int64_t total = d.batch * d.M * d.N;
-    int64_t b = (total + 255) / 256;
-    if (b > 4096) b = 4096;
-    k_splitk_reduce<<<(int)b, 256, 0, st>>>(work, p.splits, g.sOs, d);
+    int64_t nb = (total + 255) / 256;
+    if (nb > 4096) nb = 4096;
+    k_splitk_reduce<<<(int)nb, 256, 0, st>>>(work, p.splits, g.sOs, d);
   }
 }
 
@@ -231,53 +347,173 @@ __global__ void k_gather_rows(const int32_t* __restrict__ idx, int64_t rows, con
   }
 }
 
-// Stable counting sort of row ids by token: rows with idx == v land in
-// perm[offs[v] .. offs[v+1]) in increasing row order; tokens outside [0, V) are dropped.
-// One 256-thread block: integer-atomic histogram, exclusive scan, then one wavefront
-// places rows 64 at a time — a lane's rank among equal tokens is counted with shuffles,
-// so the order within a bucket is the row order. `cur` is V ints of scratch.
+// Stable counting sort of row ids by token, in one 256-thread block: rows with
+// idx == v land in perm[offs[v] .. offs[v+1]) in increasing row order; tokens outside
+// [0, V) are dropped. Wave w of the block owns a contiguous quarter of the rows (all rows
+// when V > kWaveHistV): a per-wave LDS histogram, one block-wide scan that yields each
+// wave's starting cursor per token, then each wave places its rows 64 at a time. A lane's
+// rank among equal tokens of its group comes from matching the token's bits with ballots.
+// The scan also lays out the segment-sum work: bucket v is cut into ceil(count / kSeg)
+// items starting at item cstart[v]; item_v[i] names the bucket of item i.
+constexpr int kMaxBucketV = 8192;
+constexpr int kWaveHistV = 1024;
+constexpr int kSeg = 16;
+
+__device__ __forceinline__ int block_exclusive_scan(int x, int* lds_tot, int& total) {
+  // 256 threads: shuffle-up scan inside each wavefront, then wavefront totals.
+  const int lane = threadIdx.x % 64, w = threadIdx.x / 64;
+  int inc = x;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(inc, o, 64);
+    if (lane >= o) inc += y;
+  }
+  if (lane == 63) lds_tot[w] = inc;
+  __syncthreads();
+  int before = 0;
+  total = 0;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int t = lds_tot[k];
+    if (k < w) before += t;
+    total += t;
+  }
+  __syncthreads();
+  return before + inc - x;
+}
+
 __global__ __launch_bounds__(256) void k_bucket_rows(const int32_t* __restrict__ idx, int64_t rows, int64_t V,
-                                                     int32_t* __restrict__ perm, int32_t* __restrict__ offs,
-                                                     int32_t* __restrict__ cur) {
-  for (int64_t v = threadIdx.x; v <= V; v += blockDim.x) offs[v] = 0;
+                                                     int stash, int32_t* __restrict__ perm, int32_t* __restrict__ offs,
+                                                     int32_t* __restrict__ cstart, int32_t* __restrict__ item_v) {
+  extern __shared__ int32_t lds[];
+  __shared__ int tot[4];
+  const int nw = V <= kWaveHistV ? 4 : 1;
+  const int VP = (int)V + 1;            // slot V counts dropped tokens
+  int32_t* cnt = lds;                   // [nw][VP]
+  int32_t* tok = lds + nw * VP;         // [rows] when stash != 0
+  const int lane = threadIdx.x % 64, w = threadIdx.x / 64;
+  for (int i = threadIdx.x; i < nw * VP; i += blockDim.x) cnt[i] = 0;
   __syncthreads();
-  for (int64_t r = threadIdx.x; r < rows; r += blockDim.x) {
-    int32_t t = idx[r];
-    if (t >= 0 && t < V) atomicAdd(&offs[t + 1], 1);
-  }
-  __threadfence_block();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    for (int64_t v = 0; v < V; ++v) { offs[v + 1] += offs[v]; cur[v] = offs[v]; }
-  }
-  __threadfence_block();
-  __syncthreads();
-  if (threadIdx.x >= 64) return;
-  const int lane = threadIdx.x;
-  for (int64_t r0 = 0; r0 < rows; r0 += 64) {
-    const int64_t r = r0 + lane;
-    int32_t t = r < rows ? idx[r] : -1;
-    if (t < 0 || t >= V) t = -1;
-    int rank = 0, later = 0;
-    for (int j = 0; j < 64; ++j) {
-      int32_t tj = __shfl(t, j, 64);
-      if (tj == t) { if (j < lane) ++rank; else if (j > lane) ++later; }
+  const int64_t per = ((rows + nw - 1) / nw + 63) / 64 * 64;
+  if (w < nw) {
+    const int64_t r0 = w * per, r1 = min(rows, r0 + per);
+    // Eight token loads in flight per lane before the histogram updates.
+    for (int64_t rb = r0; rb < r1; rb += 64 * 8) {
+      int32_t t[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int64_t r = rb + u * 64 + lane;
+        t[u] = r < r1 ? idx[r] : -1;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int64_t r = rb + u * 64 + lane;
+        if (r < r1) {
+          const int32_t tt = (t[u] < 0 || t[u] >= V) ? (int32_t)V : t[u];
+          atomicAdd(&cnt[w * VP + tt], 1);
+          if (stash) tok[r] = tt;
+        }
+      }
     }
-    int32_t base = t >= 0 ? cur[t] : 0;
-    if (t >= 0) perm[base + rank] = (int32_t)r;
-    if (t >= 0 && later == 0) cur[t] = base + rank + 1;   // last lane of its token group
-    __threadfence_block();
+  }
+  __syncthreads();
+  // Scan over tokens: thread j owns tokens [j*seg, (j+1)*seg).
+  const int seg = (VP + 255) / 256;
+  const int v0 = threadIdx.x * seg, v1 = min(VP - 1, v0 + seg);   // token V (dropped) excluded
+  int my = 0, myc = 0;
+  for (int v = v0; v < v1; ++v) {
+    int c = 0;
+    for (int k = 0; k < nw; ++k) c += cnt[k * VP + v];
+    my += c;
+    myc += (c + kSeg - 1) / kSeg;
+  }
+  int total, totc;
+  int run = block_exclusive_scan(my, tot, total);
+  int runc = block_exclusive_scan(myc, tot, totc);
+  for (int v = v0; v < v1; ++v) {
+    int c = 0;
+    offs[v] = run;
+    cstart[v] = runc;
+    for (int k = 0; k < nw; ++k) {
+      const int ck = cnt[k * VP + v];
+      cnt[k * VP + v] = run + c;        // wave k's first slot for token v
+      c += ck;
+    }
+    const int nc = (c + kSeg - 1) / kSeg;
+    for (int i = 0; i < nc; ++i) item_v[runc + i] = v;
+    run += c;
+    runc += nc;
+  }
+  if (threadIdx.x == 0) { offs[V] = total; cstart[V] = totc; }
+  __syncthreads();
+  if (w >= nw) return;
+  int nbits = 1;
+  while ((1 << nbits) < VP) ++nbits;
+  const int64_t r0 = w * per, r1 = min(rows, r0 + per);
+  const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  for (int64_t rb = r0; rb < r1; rb += 64) {
+    const int64_t r = rb + lane;
+    const bool live = r < r1;
+    int32_t t = (int32_t)V;
+    if (live) {
+      t = stash ? tok[r] : idx[r];
+      if (t < 0 || t >= V) t = (int32_t)V;
+    }
+    uint64_t same = __ballot(live);
+    for (int b = 0; b < nbits; ++b) {
+      const uint64_t ones = __ballot(live && ((t >> b) & 1));
+      same &= ((t >> b) & 1) ? ones : ~ones;
+    }
+    const int rank = __popcll(same & below);
+    const int count = __popcll(same);
+    const bool place = live && t < V;
+    const int base = place ? cnt[w * VP + t] : 0;
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_wave_barrier();
+    if (place) perm[base + rank] = (int32_t)r;
+    if (place && rank == count - 1) cnt[w * VP + t] = base + count;
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_wave_barrier();
   }
 }
 
-__global__ void k_scatter_rows(const float* __restrict__ dy, int64_t V, int64_t N, const int32_t* __restrict__ perm,
-                               const int32_t* __restrict__ offs, float* __restrict__ out) {
-  const int64_t total = V * N;
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t v = i / N, c = i % N;
+// Block i sums item i — up to kSeg consecutive rows of one bucket — per column, in row
+// order, in f64.
+__global__ __launch_bounds__(256) void k_segment_partials(const float* __restrict__ dy, int64_t N, int64_t V,
+                                                          const int32_t* __restrict__ perm,
+                                                          const int32_t* __restrict__ offs,
+                                                          const int32_t* __restrict__ cstart,
+                                                          const int32_t* __restrict__ item_v,
+                                                          double* __restrict__ part) {
+  const int i = blockIdx.x;
+  if (i >= cstart[V]) return;
+  const int v = item_v[i];
+  const int j0 = offs[v] + (i - cstart[v]) * kSeg;
+  const int j1 = min(offs[v + 1], j0 + kSeg);
+  int64_t rr[kSeg];
+#pragma unroll
+  for (int u = 0; u < kSeg; ++u) rr[u] = j0 + u < j1 ? (int64_t)perm[j0 + u] * N : 0;
+  for (int64_t c = blockIdx.y * (int64_t)blockDim.x + threadIdx.x; c < N; c += (int64_t)gridDim.y * blockDim.x) {
+    float x[kSeg];
+#pragma unroll
+    for (int u = 0; u < kSeg; ++u) x[u] = j0 + u < j1 ? dy[rr[u] + c] : 0.0f;
     double s = 0.0;
-    for (int32_t q = offs[v]; q < offs[v + 1]; ++q) s += (double)dy[(int64_t)perm[q] * N + c];
-    out[i] = (float)s;
+#pragma unroll
+    for (int u = 0; u < kSeg; ++u)
+      if (j0 + u < j1) s += (double)x[u];
+    part[(int64_t)i * N + c] = s;
+  }
+}
+
+// out[v, c] = sum of bucket v's item partials, in item (= row) order.
+__global__ void k_segment_finish(const double* __restrict__ part, int64_t N, int64_t V,
+                                 const int32_t* __restrict__ cstart, float* __restrict__ out) {
+  const int64_t total = V * N;
+  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t v = e / N, c = e % N;
+    double s = 0.0;
+    for (int i = cstart[v]; i < cstart[v + 1]; ++i) s += part[(int64_t)i * N + c];
+    out[e] = (float)s;
   }
 }
 
@@ -294,11 +530,32 @@ void gather_rows(const int32_t* idx, int64_t rows, const float* table, int64_t V
   k_gather_rows<<<grid_for(rows * N), 256, 0, st>>>(idx, rows, table, V, N, out);
 }
 
-void scatter_rows(const int32_t* idx, int64_t rows, const float* dy, int64_t V, int64_t N, float* out, int32_t* perm,
-                  int32_t* offs, hipStream_t st) {
+int64_t scatter_workspace_bytes(int64_t rows, int64_t V, int64_t N) {
+  const int64_t items = (rows + kSeg - 1) / kSeg + V;
+  const int64_t ints = rows + 2 * (V + 1) + items;
+  return (ints * 4 + 255) / 256 * 256 + items * N * 8;
+}
+
+void scatter_rows(const int32_t* idx, int64_t rows, const float* dy, int64_t V, int64_t N, float* out, void* work,
+                  hipStream_t st) {
   if (V * N <= 0) return;
-  k_bucket_rows<<<1, 256, 0, st>>>(idx, rows, V, perm, offs, offs + V + 1);
-  k_scatter_rows<<<grid_for(V * N), 256, 0, st>>>(dy, V, N, perm, offs, out);
+  if (V > kMaxBucketV || rows >= (int64_t(1) << 31)) throw std::runtime_error("scatter_rows: V or rows too large");
+  const int64_t items = (rows + kSeg - 1) / kSeg + V;
+  int32_t* perm = static_cast<int32_t*>(work);
+  int32_t* offs = perm + rows;
+  int32_t* cstart = offs + V + 1;
+  int32_t* item_v = cstart + V + 1;
+  const int64_t ints = rows + 2 * (V + 1) + items;
+  double* part = reinterpret_cast<double*>(static_cast<char*>(work) + (ints * 4 + 255) / 256 * 256);
+  const int nw = V <= kWaveHistV ? 4 : 1;
+  const int64_t hist_bytes = (int64_t)nw * (V + 1) * 4;
+  const int stash = hist_bytes + rows * 4 <= 65536 ? 1 : 0;
+  const size_t lds = (size_t)(hist_bytes + (stash ? rows * 4 : 0));
+  k_bucket_rows<<<1, 256, lds, st>>>(idx, rows, V, stash, perm, offs, cstart, item_v);
+  const int64_t ny = (N + 255) / 256;
+  dim3 g2((unsigned)items, (unsigned)(ny > 64 ? 64 : ny));
+  k_segment_partials<<<g2, 256, 0, st>>>(dy, N, V, perm, offs, cstart, item_v, part);
+  k_segment_finish<<<grid_for(V * N), 256, 0, st>>>(part, N, V, cstart, out);
 }
 
 }  // namespace tgk

@@ -58,39 +58,94 @@ __global__ void k_row_argmax(const float* __restrict__ a, int32_t* __restrict__ 
   }
 }
 
+// Row kernels keep a row in registers: lane l holds elements l, l + 64, ... (EPL of them,
+// D <= 64 * EPL), so the row is read from memory once. EPL = 0 selects the looping form
+// for long rows.
+template <int EPL>
 __global__ void k_log_softmax(const float* __restrict__ a, float* __restrict__ out, int64_t outer, int64_t D) {
   const int lane = threadIdx.x % kWave;
   for (int64_t r = blockIdx.x * (int64_t)kRowsPerBlock + threadIdx.x / kWave; r < outer;
        r += (int64_t)gridDim.x * kRowsPerBlock) {
     const float* row = a + r * D;
-    float mx = -INFINITY;
-    for (int64_t j = lane; j < D; j += kWave) mx = fmaxf(mx, row[j]);
-    mx = wave_max(mx);
-    double s = 0.0;
-    for (int64_t j = lane; j < D; j += kWave) s += exp((double)row[j] - (double)mx);
-    s = wave_sum(s);
-    double ls = log(s) + (double)mx;
     float* orow = out + r * D;
-    for (int64_t j = lane; j < D; j += kWave) orow[j] = (float)((double)row[j] - ls);
+    if (EPL > 0) {
+      float x[EPL > 0 ? EPL : 1];
+#pragma unroll
+      for (int u = 0; u < EPL; ++u) {
+        const int64_t j = lane + u * kWave;
+        x[u] = j < D ? row[j] : -INFINITY;
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int u = 0; u < EPL; ++u) mx = fmaxf(mx, x[u]);
+      mx = wave_max(mx);
+      double s = 0.0;
+#pragma unroll
+      for (int u = 0; u < EPL; ++u)
+        if (lane + u * kWave < D) s += exp((double)x[u] - (double)mx);
+      s = wave_sum(s);
+      const double ls = log(s) + (double)mx;
+#pragma unroll
+      for (int u = 0; u < EPL; ++u) {
+        const int64_t j = lane + u * kWave;
+        if (j < D) orow[j] = (float)((double)x[u] - ls);
+      }
+    } else {
+      float mx = -INFINITY;
+      for (int64_t j = lane; j < D; j += kWave) mx = fmaxf(mx, row[j]);
+      mx = wave_max(mx);
+      double s = 0.0;
+      for (int64_t j = lane; j < D; j += kWave) s += exp((double)row[j] - (double)mx);
+      s = wave_sum(s);
+      const double ls = log(s) + (double)mx;
+      for (int64_t j = lane; j < D; j += kWave) orow[j] = (float)((double)row[j] - ls);
+    }
   }
 }
 
 // Row q of each D x D matrix: softmax over columns 0..q, zeros above the diagonal.
+template <int EPL>
 __global__ void k_softmax_causal(const float* __restrict__ a, float* __restrict__ out, int64_t rows, int64_t D) {
   const int lane = threadIdx.x % kWave;
   for (int64_t r = blockIdx.x * (int64_t)kRowsPerBlock + threadIdx.x / kWave; r < rows;
        r += (int64_t)gridDim.x * kRowsPerBlock) {
     const int64_t q = r % D;
     const float* row = a + r * D;
-    float mx = -INFINITY;
-    for (int64_t j = lane; j <= q; j += kWave) mx = fmaxf(mx, row[j]);
-    mx = wave_max(mx);
-    double s = 0.0;
-    for (int64_t j = lane; j <= q; j += kWave) s += exp((double)row[j] - (double)mx);
-    s = wave_sum(s);
     float* orow = out + r * D;
-    for (int64_t j = lane; j < D; j += kWave)
-      orow[j] = j <= q ? (float)(exp((double)row[j] - (double)mx) / s) : 0.0f;
+    if (EPL > 0) {
+      float x[EPL > 0 ? EPL : 1];
+#pragma unroll
+      for (int u = 0; u < EPL; ++u) {
+        const int64_t j = lane + u * kWave;
+        x[u] = j <= q ? row[j] : -INFINITY;
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int u = 0; u < EPL; ++u) mx = fmaxf(mx, x[u]);
+      mx = wave_max(mx);
+      double e[EPL > 0 ? EPL : 1];
+      double s = 0.0;
+#pragma unroll
+      for (int u = 0; u < EPL; ++u) {
+        e[u] = lane + u * kWave <= q ? exp((double)x[u] - (double)mx) : 0.0;
+        if (lane + u * kWave <= q) s += e[u];
+      }
+      s = wave_sum(s);
+#pragma unroll
+      for (int u = 0; u < EPL; ++u) {
+        const int64_t j = lane + u * kWave;
+        if (j < D) orow[j] = j <= q ? (float)(e[u] / s) : 0.0f;
+      }
+    } else {
+      float mx = -INFINITY;
+      for (int64_t j = lane; j <= q; j += kWave) mx = fmaxf(mx, row[j]);
+      mx = wave_max(mx);
+      double s = 0.0;
+      for (int64_t j = lane; j <= q; j += kWave) s += exp((double)row[j] - (double)mx);
+      s = wave_sum(s);
+      for (int64_t j = lane; j < D; j += kWave)
+        orow[j] = j <= q ? (float)(exp((double)row[j] - (double)mx) / s) : 0.0f;
+    }
   }
 }
 
@@ -118,6 +173,9 @@ __device__ __forceinline__ int64_t red_offset(const Strided& sp, int64_t i) {
   return strided_offset(sp, i);
 }
 
+constexpr int kSumUnroll = 8;
+
+// Column form: thread (cell c, chunk q) sums reduced indices [r0, r1) of cell c in order.
 __global__ void k_sum_cols(const float* __restrict__ a, double* __restrict__ part, float* __restrict__ out,
                            Strided cells, Strided red, int64_t ncells, int64_t nred, int64_t chunk, int nchunks,
                            double div) {
@@ -131,9 +189,13 @@ __global__ void k_sum_cols(const float* __restrict__ a, double* __restrict__ par
     const int64_t st = red.s0[0];
     const float* p = a + base + r0 * st;
     int64_t r = r0;
-    for (; r + 4 <= r1; r += 4, p += 4 * st) {
-      float v0 = p[0], v1 = p[st], v2 = p[2 * st], v3 = p[3 * st];
-      s += (double)v0; s += (double)v1; s += (double)v2; s += (double)v3;
+    // Issue kSumUnroll loads before adding them in order: keeps that many in flight.
+    for (; r + kSumUnroll <= r1; r += kSumUnroll, p += kSumUnroll * st) {
+      float v[kSumUnroll];
+#pragma unroll
+      for (int u = 0; u < kSumUnroll; ++u) v[u] = p[u * st];
+#pragma unroll
+      for (int u = 0; u < kSumUnroll; ++u) s += (double)v[u];
     }
     for (; r < r1; ++r, p += st) s += (double)*p;
   } else {
@@ -143,6 +205,8 @@ __global__ void k_sum_cols(const float* __restrict__ a, double* __restrict__ par
   else part[c * nchunks + q] = s;
 }
 
+// Row form: one wavefront per (cell, chunk); lane l sums indices r0 + l, r0 + l + 64, ...
+// in order, then a fixed shuffle tree combines the lanes.
 __global__ void k_sum_rows(const float* __restrict__ a, double* __restrict__ part, float* __restrict__ out,
                            Strided cells, Strided red, int64_t ncells, int64_t nred, int64_t chunk, int nchunks,
                            double div) {
@@ -155,9 +219,20 @@ __global__ void k_sum_rows(const float* __restrict__ a, double* __restrict__ par
     const int64_t base = red_offset(cells, c);
     const int64_t r0 = q * chunk, r1 = min(nred, r0 + chunk);
     double s = 0.0;
-    if (red.rank == 1 && red.s0[0] == 1) {
+    if (red.rank == 1) {
+      const int64_t st = red.s0[0];
       const float* p = a + base;
-      for (int64_t r = r0 + lane; r < r1; r += kWave) s += (double)p[r];
+      for (int64_t r = r0 + lane; r < r1; r += kWave * kSumUnroll) {
+        float v[kSumUnroll];
+#pragma unroll
+        for (int u = 0; u < kSumUnroll; ++u) {
+          const int64_t j = r + u * kWave;
+          v[u] = j < r1 ? p[j * st] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < kSumUnroll; ++u)
+          if (r + u * kWave < r1) s += (double)v[u];
+      }
     } else {
       for (int64_t r = r0 + lane; r < r1; r += kWave) s += (double)a[base + red_offset(red, r)];
     }
@@ -169,12 +244,17 @@ __global__ void k_sum_rows(const float* __restrict__ a, double* __restrict__ par
   }
 }
 
+// Combine the chunk partials of each cell: one wavefront per cell, lanes over chunks,
+// fixed shuffle tree.
 __global__ void k_sum_finish(const double* __restrict__ part, float* __restrict__ out, int64_t ncells, int nchunks,
                              double div) {
-  for (int64_t c = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; c < ncells; c += (int64_t)gridDim.x * blockDim.x) {
+  const int lane = threadIdx.x % kWave;
+  for (int64_t c = blockIdx.x * (int64_t)kRowsPerBlock + threadIdx.x / kWave; c < ncells;
+       c += (int64_t)gridDim.x * kRowsPerBlock) {
     double s = 0.0;
-    for (int q = 0; q < nchunks; ++q) s += part[c * nchunks + q];
-    out[c] = (float)(s / div);
+    for (int q = lane; q < nchunks; q += kWave) s += part[c * nchunks + q];
+    s = wave_sum(s);
+    if (lane == 0) out[c] = (float)(s / div);
   }
 }
 
@@ -183,13 +263,15 @@ struct SumPlan { bool cols; int64_t chunk; int nchunks; };
 SumPlan sum_plan(const Strided& cells, int64_t ncells, int64_t nred) {
   SumPlan p;
   p.cols = cells.rank >= 1 && cells.s0[cells.rank - 1] == 1 && ncells >= 64;
-  // Aim for ~16k work items (columns) or ~4k wavefronts (rows), chunks of >= 256 terms.
-  int64_t target = p.cols ? 16384 : 4096;
+  // Enough independent work to cover the chip's latency with kSumUnroll loads in flight
+  // per lane: ~64k threads in column form (each summing >= 64 terms), ~16k wavefronts in
+  // row form (each >= 512 terms); at most 256 chunks per cell.
+  int64_t target = p.cols ? 65536 : 16384;
   int64_t want = (target + ncells - 1) / ncells;
-  int64_t maxc = nred / 256;
+  int64_t maxc = nred / (p.cols ? 64 : 512);
   if (maxc < 1) maxc = 1;
   int64_t n = want < maxc ? want : maxc;
-  if (n > 4096) n = 4096;
+  if (n > 256) n = 256;
   if (n < 1) n = 1;
   p.chunk = (nred + n - 1) / n;
   p.nchunks = (int)((nred + p.chunk - 1) / p.chunk);
@@ -204,15 +286,27 @@ void row_argmax(const float* a, int32_t* out, int64_t outer, int64_t D, hipStrea
   k_row_argmax<<<blocks_for_rows(outer), kWave * kRowsPerBlock, 0, st>>>(a, out, outer, D);
 }
 
+#define TG_ROW_LAUNCH(KERNEL, ROWS, ...)                                                            \
+  do {                                                                                              \
+    const int g_ = blocks_for_rows(ROWS);                                                           \
+    const int b_ = kWave * kRowsPerBlock;                                                           \
+    if (D <= 64) KERNEL<1><<<g_, b_, 0, st>>>(__VA_ARGS__);                                         \
+    else if (D <= 128) KERNEL<2><<<g_, b_, 0, st>>>(__VA_ARGS__);                                   \
+    else if (D <= 256) KERNEL<4><<<g_, b_, 0, st>>>(__VA_ARGS__);                                   \
+    else if (D <= 512) KERNEL<8><<<g_, b_, 0, st>>>(__VA_ARGS__);                                   \
+    else if (D <= 1024) KERNEL<16><<<g_, b_, 0, st>>>(__VA_ARGS__);                                 \
+    else KERNEL<0><<<g_, b_, 0, st>>>(__VA_ARGS__);                                                 \
+  } while (0)
+
 void log_softmax(const float* a, float* out, int64_t outer, int64_t D, hipStream_t st) {
   if (outer <= 0) return;
-  k_log_softmax<<<blocks_for_rows(outer), kWave * kRowsPerBlock, 0, st>>>(a, out, outer, D);
+  TG_ROW_LAUNCH(k_log_softmax, outer, a, out, outer, D);
 }
 
 void softmax_causal(const float* a, float* out, int64_t mats, int64_t D, hipStream_t st) {
   int64_t rows = mats * D;
   if (rows <= 0) return;
-  k_softmax_causal<<<blocks_for_rows(rows), kWave * kRowsPerBlock, 0, st>>>(a, out, rows, D);
+  TG_ROW_LAUNCH(k_softmax_causal, rows, a, out, rows, D);
 }
 
 int64_t sum_workspace_doubles(const Strided& cells, int64_t ncells, int64_t nred) {
@@ -233,11 +327,7 @@ void reduce_sum(const float* a, float* out, const Strided& cells, const Strided&
     if (b > 16384) b = 16384;
     k_sum_rows<<<(int)b, kWave * kRowsPerBlock, 0, st>>>(a, work, out, cells, red, ncells, nred, p.chunk, p.nchunks, div);
   }
-  if (p.nchunks > 1) {
-    int64_t b = (ncells + 255) / 256;
-    if (b > 4096) b = 4096;
-    k_sum_finish<<<(int)b, 256, 0, st>>>(work, out, ncells, p.nchunks, div);
-  }
+  if (p.nchunks > 1) k_sum_finish<<<blocks_for_rows(ncells), kWave * kRowsPerBlock, 0, st>>>(work, out, ncells, p.nchunks, div);
 }
 
 }  // namespace tgk

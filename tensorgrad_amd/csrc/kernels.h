@@ -12,6 +12,23 @@ constexpr int kMaxRank = 8;
 // dtype codes for element-wise operands
 enum { DT_F32 = 0, DT_I32 = 1 };
 
+// Division by a runtime constant d >= 1 for 0 <= x < 2^31 without a divide instruction:
+// q = (umulhi(x, m) + x) >> s with s = ceil(log2 d), m = floor(2^32 (2^s - d) / d) + 1
+// (Granlund & Montgomery, "Division by invariant integers using multiplication", 1994).
+// umulhi(x, m) <= x, so the sum stays below 2^32.
+struct FastDiv {
+  uint32_t d, m, s;
+};
+inline FastDiv make_fastdiv(uint32_t d) {
+  FastDiv f{d, 0, 0};
+  while ((1ull << f.s) < d) ++f.s;
+  f.m = (uint32_t)((((1ull << 32) * ((1ull << f.s) - d)) / d) + 1);
+  return f;
+}
+__device__ __forceinline__ uint32_t fastdiv(uint32_t x, const FastDiv& f) {
+  return (__umulhi(x, f.m) + x) >> f.s;
+}
+
 // An N-d iteration space with per-operand element strides (0 = broadcast axis).
 struct Strided {
   int rank;
@@ -49,6 +66,51 @@ void randn(float* out, int64_t n, const int32_t* seed, uint32_t salt_const, hipS
 void categorical(const float* a, int32_t* out, int64_t outer, int64_t D, const int32_t* seed, uint32_t salt_const,
                  hipStream_t st);
 
+// ---- fused element-wise groups (k_fused.hip) ------------------------------------------
+constexpr int kFusedRegs = 16;
+constexpr int kFusedMaxIn = 8;
+constexpr int kFusedMaxOut = 8;
+constexpr int kFusedMaxInstr = 16;
+// Opcodes FO_FADD .. FO_COPY are the inexpensive forms (f32 operands and result where
+// typed) evaluated unrolled over a thread's elements; the rest are general forms (mixed
+// i32 / f32 typing, comparisons, f64 transcendentals, dropout).
+enum FusedOp {
+  FO_FADD, FO_FSUB, FO_FMUL, FO_FDIV, FO_MULS, FO_ADDS, FO_SQRT, FO_NEG, FO_ABS, FO_RELU, FO_RELU_GRAD,
+  FO_WHERE, FO_COPY,
+  FO_ADD, FO_SUB, FO_MUL, FO_DIV, FO_MIN, FO_MAX, FO_LESS, FO_GREATER,
+  FO_RSQRT, FO_LOG, FO_EXP, FO_TANH, FO_SIGMOID, FO_ERF, FO_SIN, FO_COS, FO_DROPOUT
+};
+// Operand access modes. With several elements per thread (vec 4), a strided operand's
+// innermost stride decides how the thread's run of elements is read: FM_STRIDED_V one
+// 128-bit load (innermost stride 1, 16-byte aligned), FM_STRIDED_B one load shared by
+// the run (innermost stride 0), FM_STRIDED one load per element.
+enum FusedMode { FM_CONTIG = 0, FM_SCALAR = 1, FM_STRIDED = 2, FM_STRIDED_V = 3, FM_STRIDED_B = 4 };
+struct FusedInstr {
+  int32_t op, dst, a, b, c;
+  int32_t dt, ta, tb;             // result dtype (DT_F32 / DT_I32) and operand dtypes
+  uint32_t salt;                  // dropout salt constant
+  double imm, imm2;               // scalar operand; dropout p and 1/(1-p)
+};
+// A group program: registers 0..n_in-1 are the loaded operands, instructions write
+// further registers, out_reg[] are stored. The header travels as a kernel argument; the
+// instructions live in device memory (`code`) and are read with scalar loads.
+// Each thread handles `vec` consecutive elements; the iteration space is `rank` merged
+// dims (the innermost divided by vec) with 32-bit indices, so every tensor the group
+// touches has fewer than 2^31 elements.
+struct FusedProgram {
+  int32_t n_in, n_out, n_instr, rank, any_strided, vec;
+  FastDiv div[kMaxRank];
+  const void* in[kFusedMaxIn];
+  int32_t in_dt[kFusedMaxIn], in_mode[kFusedMaxIn], in_inner[kFusedMaxIn];
+  int32_t in_strides[kFusedMaxIn][kMaxRank];   // per dim of the iteration space (innermost x vec)
+  void* out[kFusedMaxOut];
+  int32_t out_dt[kFusedMaxOut], out_reg[kFusedMaxOut];
+  const int32_t* seed;
+  const FusedInstr* code;
+};
+// `n` = number of threads' runs (elements / vec).
+void fused(const FusedProgram& prog, int64_t n, hipStream_t st);
+
 // ---- reductions / softmax (k_reduce.hip) --------------------------------------------
 // Deterministic parallel sums with f64 accumulation: out[c] = f32(sum_r a[cell(c) +
 // red(r)] / div) for c < ncells, r < nred. `cells` / `red` carry dims and element
@@ -80,9 +142,11 @@ void gemm(const GemmDesc& d, float* work, hipStream_t st);
 void gather_rows(const int32_t* idx, int64_t rows, const float* table, int64_t V, int64_t N, float* out,
                  hipStream_t st);
 // Embedding gradient: out[v, :] = sum over rows r with idx[r] == v of dy[r, :], in row
-// order, f64 accumulation; needs `perm` (rows ints) and `offs` (2V + 1 ints) scratch.
-void scatter_rows(const int32_t* idx, int64_t rows, const float* dy, int64_t V, int64_t N, float* out,
-                  int32_t* perm, int32_t* offs, hipStream_t st);
+// order, f64 accumulation (V <= 8192); `work` must hold scatter_workspace_bytes(...)
+// bytes, 256-byte aligned.
+int64_t scatter_workspace_bytes(int64_t rows, int64_t V, int64_t N);
+void scatter_rows(const int32_t* idx, int64_t rows, const float* dy, int64_t V, int64_t N, float* out, void* work,
+                  hipStream_t st);
 
 // ---- conv / pool (k_conv.hip) ---------------------------------------------------------
 struct ConvDesc {

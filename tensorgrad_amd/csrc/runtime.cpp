@@ -23,6 +23,8 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <cstdlib>
+#include <deque>
 #include <functional>
 #include <map>
 #include <memory>
@@ -232,6 +234,16 @@ class Runtime {
   hipGraphExec_t graph_exec_ = nullptr;
   bool plan_only_ = false;
 
+  // Element-wise fusion groups: members in op order; the group runs at its first op.
+  struct Group { int first; std::vector<int> ops; Dims shape; };
+  std::vector<Group> groups_;
+  std::vector<int> group_of_;   // op -> group index or -1
+  std::deque<tgk::FusedProgram> programs_;     // kernel-argument images (stable addresses)
+  std::vector<tgk::FusedInstr> fused_code_;    // all groups' instructions, uploaded once
+  tgk::FusedInstr* fused_code_dev_ = nullptr;
+  void form_groups();
+  void lower_group(int gi);
+
   bool is_leaf(int op) const {
     const std::string& k = kinds_[op];
     return k == "param_input" || k == "tensor_input" || k == "state_input";
@@ -254,6 +266,10 @@ class Runtime {
   float step_staged(int slot);
  private:
   void ensure_graph();
+  void replay();
+  // TG_GRAPH=0 in the environment issues each step's launches directly instead of
+  // replaying a captured hipGraph (for tools that do not follow graph launches).
+  bool use_graph_ = true;
   void apply_copy_writebacks(hipStream_t st);
 
   // GEMM lowering helpers
@@ -266,6 +282,7 @@ class Runtime {
 // ---------------------------------------------------------------------------------------
 
 Runtime::Runtime(const char* json, Runtime* par, bool plan_only) : parent(par) {
+  if (const char* g = std::getenv("TG_GRAPH")) use_graph_ = std::string(g) != "0";
   try {
     doc_ = tgj::parse(json);
   } catch (std::exception& e) {
@@ -316,6 +333,7 @@ Runtime::~Runtime() {
   if (arena_) hipFree(arena_);
   if (input_region_) hipFree(input_region_);
   if (workspace_ && !plan_only_) hipFree(workspace_);
+  if (fused_code_dev_ && !plan_only_) hipFree(fused_code_dev_);
   if (adam_tensors_) hipFree(adam_tensors_);
   if (adam_chunk_tensor_) hipFree(adam_chunk_tensor_);
   if (adam_chunk_start_) hipFree(adam_chunk_start_);
@@ -514,9 +532,15 @@ void Runtime::lower() {
     }
   }
 
+  form_groups();
   for (size_t i = 0; i < ops_.size(); ++i) {
     if (is_leaf((int)i) || virtual_[i]) continue;
     if (adam_ops.count((int)i)) continue;
+    int gi = group_of_[i];
+    if (gi >= 0) {
+      if (groups_[gi].first == (int)i) lower_group(gi);
+      continue;
+    }
     lower_op((int)i);
   }
 
@@ -616,6 +640,253 @@ static std::string shape_str(const Dims& d) {
   for (size_t i = 0; i < d.size(); ++i) s += (i ? "," : "") + std::to_string(d[i]);
   return s + "]";
 }
+
+static const std::map<std::string, int>& pointwise_ops() {
+  static const std::map<std::string, int> m = {
+      {"add", tgk::FO_ADD}, {"sub", tgk::FO_SUB}, {"mul", tgk::FO_MUL}, {"div", tgk::FO_DIV},
+      {"min", tgk::FO_MIN}, {"max", tgk::FO_MAX}, {"less", tgk::FO_LESS}, {"greater", tgk::FO_GREATER},
+      {"mul_scalar", tgk::FO_MULS}, {"add_scalar", tgk::FO_ADDS}, {"sqrt", tgk::FO_SQRT}, {"rsqrt", tgk::FO_RSQRT},
+      {"log", tgk::FO_LOG}, {"exp", tgk::FO_EXP}, {"relu", tgk::FO_RELU}, {"neg", tgk::FO_NEG},
+      {"abs", tgk::FO_ABS}, {"tanh", tgk::FO_TANH}, {"sigmoid", tgk::FO_SIGMOID}, {"erf", tgk::FO_ERF},
+      {"sin", tgk::FO_SIN}, {"cos", tgk::FO_COS}, {"relu_grad", tgk::FO_RELU_GRAD}, {"where", tgk::FO_WHERE},
+      {"dropout", tgk::FO_DROPOUT}, {"broadcast_to", tgk::FO_COPY}};
+  return m;
+}
+
+// Greedy convex grouping of same-shape pointwise ops. An op joins a group only if every
+// operand is either produced inside the group or available before the group's first op
+// (an earlier op, a leaf, or an earlier group), so the whole group can run at its first
+// op's position without reordering anything else.
+void Runtime::form_groups() {
+  group_of_.assign(ops_.size(), -1);
+  groups_.clear();
+  const auto& pw = pointwise_ops();
+  // Position at which a tensor's data exists (views resolve to their root).
+  auto eff_pos = [&](int t) {
+    int r = root(t);
+    int src = T_[r].src;
+    if (src < 0 || is_leaf(src)) return -1;
+    return group_of_[src] >= 0 ? groups_[group_of_[src]].first : src;
+  };
+  auto ext_inputs = [&](const Group& g, int extra) {
+    std::set<int> members(g.ops.begin(), g.ops.end());
+    if (extra >= 0) members.insert(extra);
+    std::set<int> ext;
+    for (int m : members)
+      for (int t : op_inputs(*ops_[m])) {
+        if (members.count(T_[t].src)) continue;
+        if (kinds_[m] == "dropout" && t == fld(m, "seed")) continue;
+        ext.insert(t);
+      }
+    return ext.size();
+  };
+  for (size_t i = 0; i < ops_.size(); ++i) {
+    const std::string& k = kinds_[i];
+    if (virtual_[i] || !pw.count(k) || is_leaf((int)i)) continue;
+    const int out = ops_[i]->at("out").i32();
+    const Dims& S = T_[out].shape;
+    if (T_[out].numel <= 0) continue;
+    std::vector<int> cands;
+    for (int t : op_inputs(*ops_[i])) {
+      int src = T_[t].src;
+      if (src >= 0 && group_of_[src] >= 0 && groups_[group_of_[src]].shape == S && T_[t].shape == S)
+        cands.push_back(group_of_[src]);
+    }
+    std::sort(cands.begin(), cands.end(), [&](int a, int b) { return groups_[a].first > groups_[b].first; });
+    int joined = -1;
+    for (int gi : cands) {
+      Group& g = groups_[gi];
+      bool ok = g.ops.size() < (size_t)tgk::kFusedMaxInstr;
+      for (int t : op_inputs(*ops_[i])) {
+        int src = T_[t].src;
+        bool inside = src >= 0 && group_of_[src] == gi;
+        if (!inside && eff_pos(t) >= g.first) ok = false;
+      }
+      if (ok && ext_inputs(g, (int)i) > (size_t)tgk::kFusedMaxIn) ok = false;
+      if (ok && ext_inputs(g, (int)i) + g.ops.size() + 1 > (size_t)tgk::kFusedRegs) ok = false;
+      if (ok) { g.ops.push_back((int)i); group_of_[i] = gi; joined = gi; break; }
+    }
+    if (joined < 0) {
+      groups_.push_back(Group{(int)i, {(int)i}, S});
+      group_of_[i] = (int)groups_.size() - 1;
+    }
+  }
+}
+
+void Runtime::lower_group(int gi) {
+  const Group& g = groups_[gi];
+  const auto& pw = pointwise_ops();
+  std::set<int> members(g.ops.begin(), g.ops.end());
+  Node n;
+  n.op = g.first;
+  n.kind = g.ops.size() == 1 ? "elementwise" : "fused";
+  n.shape = shape_str(g.shape) + " x" + std::to_string(g.ops.size());
+  // External operands (dropout seeds are read through a pointer, not as operands).
+  std::vector<int> ext;
+  int seed = -1;
+  for (int m : g.ops) {
+    for (int t : op_inputs(*ops_[m])) {
+      if (members.count(T_[t].src)) continue;
+      if (kinds_[m] == "dropout" && t == fld(m, "seed")) { seed = t; continue; }
+      if (std::find(ext.begin(), ext.end(), t) == ext.end()) ext.push_back(t);
+    }
+  }
+  if (ext.size() > (size_t)tgk::kFusedMaxIn) throw Error(TG_INTERNAL, "fused group: too many operands");
+  for (int t : ext) n.reads.push_back(root(t));
+  if (seed >= 0) n.reads.push_back(root(seed));
+  // Outputs: members read outside the group (or graph outputs / captures / writeback sources).
+  std::set<int> must_store;
+  for (int o : outputs_) must_store.insert(o);
+  for (auto& c : captures_) must_store.insert(c.second);
+  for (auto& w : copy_writebacks_) must_store.insert(w.first);
+  std::vector<int> outs;
+  for (int m : g.ops) {
+    int t = ops_[m]->at("out").i32();
+    bool ext_use = must_store.count(t) > 0;
+    for (int c : consumers_[t]) if (!members.count(c)) ext_use = true;
+    if (ext_use) outs.push_back(t);
+  }
+  if (outs.size() > (size_t)tgk::kFusedMaxOut) throw Error(TG_INTERNAL, "fused group: too many outputs");
+  for (int t : outs) n.writes.push_back(root(t));
+  double bytes = 0;
+  for (int t : ext) bytes += 4.0 * T_[t].numel;
+  bytes += 4.0 * prod(g.shape) * outs.size();
+  n.bytes = bytes;
+  // Register map: operands first, then one register per member.
+  std::map<int, int> reg;
+  for (size_t q = 0; q < ext.size(); ++q) reg[ext[q]] = (int)q;
+  std::vector<tgk::FusedInstr> code;
+  int next = (int)ext.size();
+  for (int m : g.ops) {
+    const tgj::Value& op = O(m);
+    const std::string& k = kinds_[m];
+    tgk::FusedInstr in{};
+    in.op = pw.at(k);
+    int out = op.at("out").i32();
+    in.dt = kdt(T_[out].dt);
+    auto R = [&](const char* f) { return reg.at(op.at(f).i32()); };
+    auto DT = [&](const char* f) { return kdt(T_[op.at(f).i32()].dt); };
+    if (k == "relu_grad") { in.a = R("x"); in.b = R("dy"); in.ta = DT("x"); in.tb = DT("dy"); }
+    else if (k == "where") { in.a = R("cond"); in.b = R("a"); in.c = R("b"); in.ta = DT("cond"); in.tb = DT("a"); }
+    else {
+      in.a = R("a");
+      in.ta = DT("a");
+      if (op.get("b") && (k != "dropout")) { in.b = R("b"); in.tb = DT("b"); }
+    }
+    if (k == "mul_scalar" || k == "add_scalar") in.imm = op.at("scalar").num();
+    if (k == "dropout") {
+      double p = op.at("p").num();
+      in.imm = p;
+      in.imm2 = 1.0 / (1.0 - p);
+      in.salt = (uint32_t)(uint64_t)std::fmod((double)op.at("salt").i64() * 2654435761.0, 4294967296.0);
+    }
+    // Inexpensive f32 forms of the arithmetic ops.
+    if (in.ta == tgk::DT_F32 && in.tb == tgk::DT_F32 && in.dt == tgk::DT_F32) {
+      if (in.op == tgk::FO_ADD) in.op = tgk::FO_FADD;
+      else if (in.op == tgk::FO_SUB) in.op = tgk::FO_FSUB;
+      else if (in.op == tgk::FO_MUL) in.op = tgk::FO_FMUL;
+      else if (in.op == tgk::FO_DIV) in.op = tgk::FO_FDIV;
+    }
+    in.dst = next;
+    reg[out] = next++;
+    code.push_back(in);
+  }
+  const size_t code_off = fused_code_.size();
+  fused_code_.insert(fused_code_.end(), code.begin(), code.end());
+  const Dims S = g.shape;
+  std::vector<int> out_regs;
+  for (int t : outs) out_regs.push_back(reg.at(t));
+  const size_t slot = programs_.size();
+  programs_.emplace_back();
+  n.bind = [=]() -> std::function<void(hipStream_t)> {
+    tgk::FusedProgram& p = programs_[slot];
+    memset(&p, 0, sizeof(p));
+    const int64_t cnt = prod(S);
+    if (cnt >= (int64_t(1) << 31)) throw Error(TG_INVALID_ARGUMENT, "fused group: 2^31 or more elements");
+    // Broadcast strides of every operand over S, then drop size-1 dims and merge
+    // neighbours that are contiguous in every operand (outputs are contiguous).
+    std::vector<Dims> bs(ext.size(), Dims(S.size(), 0));
+    for (size_t q = 0; q < ext.size(); ++q) {
+      const View& v = view_[ext[q]];
+      if (T_[v.root].numel >= (int64_t(1) << 31)) throw Error(TG_INVALID_ARGUMENT, "fused group: operand too large");
+      int off = (int)S.size() - (int)v.dims.size();
+      for (size_t d = 0; d < v.dims.size(); ++d) bs[q][off + d] = v.dims[d] == 1 ? 0 : v.strides[d];
+      check_span("fused operand", T_[v.root].numel, 0, S.data(), bs[q].data(), (int)S.size());
+    }
+    Dims md;
+    std::vector<Dims> ms(ext.size());
+    for (size_t d = 0; d < S.size(); ++d) {
+      if (S[d] == 1) continue;
+      bool merge = !md.empty();
+      for (size_t q = 0; q < ext.size() && merge; ++q) merge = ms[q].back() == bs[q][d] * S[d];
+      if (merge) {
+        md.back() *= S[d];
+        for (size_t q = 0; q < ext.size(); ++q) ms[q].back() = bs[q][d];
+      } else {
+        md.push_back(S[d]);
+        for (size_t q = 0; q < ext.size(); ++q) ms[q].push_back(bs[q][d]);
+      }
+    }
+    if (md.empty()) {
+      md.push_back(1);
+      for (auto& m : ms) m.push_back(0);
+    }
+    if (md.size() > (size_t)tgk::kMaxRank) throw Error(TG_INTERNAL, "fused group: rank too large");
+    const int R = (int)md.size();
+    const Dims cs = contiguous_strides(md);
+    auto aligned = [](const void* ptr) { return ((uintptr_t)ptr & 15) == 0; };
+    // Four elements per thread when the innermost dim allows it and every 128-bit access
+    // is aligned.
+    bool v4 = md[R - 1] % 4 == 0;
+    std::vector<int> mode(ext.size());
+    for (size_t q = 0; q < ext.size(); ++q) {
+      bool contig = true, scalar = true;
+      for (int d = 0; d < R; ++d) {
+        if (ms[q][d] != cs[d]) contig = false;
+        if (ms[q][d] != 0) scalar = false;
+      }
+      mode[q] = contig ? tgk::FM_CONTIG : (scalar ? tgk::FM_SCALAR : tgk::FM_STRIDED);
+      if (contig && !aligned(ptr_[view_[ext[q]].root])) v4 = false;
+    }
+    for (int t : outs) if (!aligned(dptr(t))) v4 = false;
+    const int vec = v4 ? 4 : 1;
+    p.vec = vec;
+    p.rank = R;
+    for (int d = 0; d < R; ++d) p.div[d] = tgk::make_fastdiv((uint32_t)(d == R - 1 ? md[d] / vec : md[d]));
+    p.n_in = (int)ext.size();
+    for (size_t q = 0; q < ext.size(); ++q) {
+      const View& v = view_[ext[q]];
+      p.in[q] = ptr_[v.root];
+      p.in_dt[q] = kdt(T_[ext[q]].dt);
+      int m = mode[q];
+      const int64_t inner = ms[q][R - 1];
+      if (m == tgk::FM_STRIDED && vec == 4) {
+        bool outer4 = aligned(ptr_[v.root]);
+        for (int d = 0; d < R - 1; ++d) if (ms[q][d] % 4) outer4 = false;
+        if (inner == 1 && outer4) m = tgk::FM_STRIDED_V;
+        else if (inner == 0) m = tgk::FM_STRIDED_B;
+      }
+      p.in_mode[q] = m;
+      p.in_inner[q] = (int32_t)inner;
+      if (m != tgk::FM_CONTIG && m != tgk::FM_SCALAR) p.any_strided = 1;
+      for (int d = 0; d < R; ++d) p.in_strides[q][d] = (int32_t)(d == R - 1 ? inner * vec : ms[q][d]);
+    }
+    p.n_out = (int)outs.size();
+    for (size_t q = 0; q < outs.size(); ++q) {
+      p.out[q] = dptr(outs[q]);
+      p.out_dt[q] = kdt(T_[outs[q]].dt);
+      p.out_reg[q] = out_regs[q];
+      if (T_[root(outs[q])].numel < cnt) throw Error(TG_INTERNAL, "fused group: output too small");
+    }
+    p.seed = seed >= 0 ? (const int32_t*)dptr(seed) : nullptr;
+    p.n_instr = (int)code.size();
+    p.code = fused_code_dev_ + code_off;
+    const int64_t nthreads = cnt / vec;
+    return [this, slot, nthreads](hipStream_t st) { tgk::fused(programs_[slot], nthreads, st); };
+  };
+  add_node(std::move(n));
+}
+
 
 void Runtime::lower_op(int i) {
   const std::string& k = kinds_[i];
@@ -947,8 +1218,11 @@ void Runtime::lower_op(int i) {
     n.shape = shape_str(ash) + "x" + shape_str(bsh);
     // Pattern: embedding forward, one_hot(idx) @ table.
     int asrc = T_[view_[a].root].src;
+    // The one-hot must be read as laid out ([rows, depth] row-major, rows = batch * M,
+    // depth = K), not transposed; with depth 1 a transpose is also contiguous.
     if (!batched && asrc >= 0 && kinds_[asrc] == "one_hot" && view_[a].contiguous() && view_[b].contiguous() &&
-        T_[view_[a].root].dt == F32) {
+        T_[view_[a].root].dt == F32 && T_[fld(asrc, "indices")].numel == batch * M &&
+        O(asrc).at("depth").i64() == K) {
       int idx = fld(asrc, "indices");
       rd(idx); rd(b);
       n.kind = "gather";
@@ -967,19 +1241,18 @@ void Runtime::lower_op(int i) {
       const View& va = view_[a];
       int64_t rows = T_[fld(asrc, "indices")].numel, V = O(asrc).at("depth").i64();
       if (va.dims.size() == 2 && va.dims[0] == V && va.dims[1] == rows && va.strides[0] == 1 && va.strides[1] == V &&
-          view_[b].contiguous()) {
+          view_[b].contiguous() && V <= 8192) {
         int idx = fld(asrc, "indices");
         rd(idx); rd(b);
         n.kind = "scatter";
         n.flops = 0;
         n.bytes = 4.0 * (rows + rows * N + V * N);
-        workspace_bytes_ = std::max(workspace_bytes_, (size_t)(rows + 2 * V + 1) * 4 + 256);
+        workspace_bytes_ = std::max(workspace_bytes_, (size_t)tgk::scatter_workspace_bytes(rows, V, N));
         n.bind = [=]() -> std::function<void(hipStream_t)> {
           const int32_t* pi = (const int32_t*)dptr(idx); const float* pd = (const float*)dptr(b);
           float* po = (float*)dptr(out);
-          int32_t* perm = (int32_t*)workspace_;
-          int32_t* offs = perm + rows;
-          return [=](hipStream_t st) { tgk::scatter_rows(pi, rows, pd, V, N, po, perm, offs, st); };
+          void* work = workspace_;
+          return [=](hipStream_t st) { tgk::scatter_rows(pi, rows, pd, V, N, po, work, st); };
         };
         add_node(std::move(n));
         return;
@@ -1220,6 +1493,7 @@ void Runtime::allocate() {
   for (int t : input_roots) if (internal(t)) { input_offset_[t] = ioff; ioff = align(ioff + std::max<int64_t>(4, T_[t].numel * 4)); }
   input_region_bytes_ = std::max<size_t>(ioff, 256);
   if (plan_only_) {
+    fused_code_dev_ = reinterpret_cast<tgk::FusedInstr*>(fake);
     input_region_ = fake + arena_bytes_ + 4096;
     for (int t : input_roots) ptr_[t] = input_region_ + input_offset_[t];
     workspace_ = reinterpret_cast<float*>(input_region_ + input_region_bytes_ + 4096);
@@ -1233,6 +1507,11 @@ void Runtime::allocate() {
   for (int t : input_roots) ptr_[t] = input_region_ + input_offset_[t];
   hip_check(hipHostMalloc(&loss_host_, 256, hipHostMallocDefault), "hipHostMalloc");
   if (workspace_bytes_) hip_check(hipMalloc(&workspace_, workspace_bytes_), "hipMalloc(workspace)");
+  if (!fused_code_.empty()) {
+    const size_t cb = fused_code_.size() * sizeof(tgk::FusedInstr);
+    hip_check(hipMalloc(&fused_code_dev_, cb), "hipMalloc(fused code)");
+    hip_check(hipMemcpy(fused_code_dev_, fused_code_.data(), cb, hipMemcpyHostToDevice), "hipMemcpy(fused code)");
+  }
   // Zero everything once: params are uploaded by the caller, state starts at initValue.
   hip_check(hipMemset(arena_, 0, arena_bytes_), "hipMemset");
   for (auto& kv : state_tid_) {
@@ -1276,6 +1555,18 @@ void Runtime::apply_copy_writebacks(hipStream_t st) {
     if (sp.rank == 0) { sp.rank = 1; sp.dims[0] = 1; sp.s0[0] = 1; sp.s1[0] = 1; }
     tgk::strided_copy(ptr_[dst], ptr_[v.root], sp, T_[src].numel, st);
   }
+}
+
+// One execution of the step: a replay of the captured graph, or (graphs disabled) the
+// same launches issued directly on the stream.
+void Runtime::replay() {
+  if (!use_graph_) {
+    launch_all(stream_);
+    apply_copy_writebacks(stream_);
+    return;
+  }
+  ensure_graph();
+  hip_check(hipGraphLaunch(graph_exec_, stream_), "hipGraphLaunch");
 }
 
 void Runtime::ensure_graph() {
@@ -1382,8 +1673,7 @@ float Runtime::step_staged(int slot) {
   if (user_bytes_)
     hip_check(hipMemcpyAsync(input_region_, slots_[slot], user_bytes_, hipMemcpyDeviceToDevice, stream_), "hipMemcpyAsync(D2D)");
   stage_scalars();
-  ensure_graph();
-  hip_check(hipGraphLaunch(graph_exec_, stream_), "hipGraphLaunch");
+  replay();
   hip_check(hipMemcpyAsync(loss_host_, dptr(outputs_.at(0)), 4, hipMemcpyDeviceToHost, stream_), "hipMemcpyAsync(D2H)");
   hip_check(hipStreamSynchronize(stream_), "hipStreamSynchronize");
   return loss_host_[0];
@@ -1392,8 +1682,7 @@ float Runtime::step_staged(int slot) {
 float Runtime::step(int n, const char* const* names, const void* const* data, const int64_t* nbytes, bool device) {
   if (!opt_cfg_) throw Error(TG_INVALID_ARGUMENT, "step: graph has no optimizer (use run)");
   upload_inputs(n, names, data, nbytes, device);
-  ensure_graph();
-  hip_check(hipGraphLaunch(graph_exec_, stream_), "hipGraphLaunch");
+  replay();
   int lt = outputs_.at(0);
   hip_check(hipMemcpyAsync(loss_host_, dptr(lt), 4, hipMemcpyDeviceToHost, stream_), "hipMemcpyAsync(D2H)");
   hip_check(hipStreamSynchronize(stream_), "hipStreamSynchronize");
@@ -1403,8 +1692,7 @@ float Runtime::step(int n, const char* const* names, const void* const* data, co
 void Runtime::run(int n, const char* const* names, const void* const* data, const int64_t* nbytes, void* out,
                   int64_t out_bytes) {
   upload_inputs(n, names, data, nbytes, false);
-  ensure_graph();
-  hip_check(hipGraphLaunch(graph_exec_, stream_), "hipGraphLaunch");
+  replay();
   int o = outputs_.at(0);
   if (out_bytes != T_[o].numel * 4) throw Error(TG_INVALID_ARGUMENT, "run: output buffer has the wrong size");
   if (!view_[o].contiguous()) throw Error(TG_INTERNAL, "run: output is not contiguous");
@@ -1500,12 +1788,12 @@ void Runtime::profile_nodes(int iters, double* ms, int64_t nout) {
 }
 
 double Runtime::time_replays(int steps) {
-  ensure_graph();
+  if (use_graph_) ensure_graph();
   hipEvent_t a, b;
   hip_check(hipEventCreate(&a), "hipEventCreate");
   hip_check(hipEventCreate(&b), "hipEventCreate");
   hip_check(hipEventRecord(a, stream_), "hipEventRecord");
-  for (int i = 0; i < steps; ++i) hip_check(hipGraphLaunch(graph_exec_, stream_), "hipGraphLaunch");
+  for (int i = 0; i < steps; ++i) replay();
   hip_check(hipEventRecord(b, stream_), "hipEventRecord");
   hip_check(hipEventSynchronize(b), "hipEventSynchronize");
   float ms = 0;

@@ -17,6 +17,12 @@ from tensorgrad_amd.trace import capture
 pytestmark = pytest.mark.gpu
 
 
+def _close(got, want):
+    # GEMMs accumulate in f32 on the matrix cores where the evaluator accumulates in f64,
+    # so losses agree to f32 rounding noise, not bit for bit.
+    assert abs(got - want) <= 1e-5 * abs(want), (got, want)
+
+
 def _c1():
     cfg = configs.CONFIGS['mlp_sin']
     return cfg, tg_compile(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer, seed=42)
@@ -30,7 +36,7 @@ def test_step_matches_oracle_and_returns_completed():
     for b in configs.batches(cfg, 5):
         r = t.step(b)
         assert r.kind == 'completed'
-        assert np.float32(r.loss) == np.float32(o.step(b))
+        _close(r.loss, o.step(b))
     assert t.param_names == ['l1.W', 'l1.b', 'l2.W', 'l2.b', 'l3.W', 'l3.b']
     t.destroy()
 
@@ -85,7 +91,7 @@ def test_set_lr_rebases_like_the_oracle():
         if i == 4:
             t.set_lr(sched)
             o.set_lr(sched)
-        assert np.float32(t.step(b).loss) == np.float32(o.step(b))
+        _close(t.step(b).loss, o.step(b))
     t.destroy()
 
 

@@ -19,9 +19,16 @@ pytestmark = pytest.mark.gpu
 
 LOSS_TOL = 1e-4
 PARAM_TOL = 1e-4
+GRAD_TOL = 1e-4
 
 
-def _train_both(cfg, steps, seed=42, opt=None):
+def _train_both(cfg, steps, seed=42, opt=None, flip_step=None):
+    """Train the GPU runtime and the oracle side by side; return (worst loss rel error,
+    worst per-tensor param rel error, number of sign-ambiguous elements).
+
+    With `flip_step` set, parameter elements that differ by at least flip_step / 4 are
+    counted as sign-ambiguous and left out of the parameter error (see
+    test_full_config_parity)."""
     ir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, opt or cfg.optimizer)
     rt = backend.NativeRuntime(ir.wire_json())
     o = pyoracle.OracleRuntime(ir.wire())
@@ -37,41 +44,97 @@ def _train_both(cfg, steps, seed=42, opt=None):
         exact_losses += int(np.float32(lg) == np.float32(lo))
         print(f'  [{cfg.key}] step {i + 1}: gpu {lg:.9g} oracle {lo:.9g}', flush=True) if i in (0, steps - 1) else None
     pg = rt.download_params()
-    worst_param = 0.0
+    worst_param, worst_name, worst_max = 0.0, '', 0.0
+    flips = 0
     for n in ir.param_names:
         po = o.get_home(n, pg[n].size).astype(np.float64)
-        d = np.linalg.norm(pg[n].astype(np.float64) - po) / max(np.linalg.norm(po), 1e-30)
-        worst_param = max(worst_param, d)
+        diff = pg[n].astype(np.float64) - po
+        if flip_step is not None:
+            amb = np.abs(diff) >= flip_step / 4
+            flips += int(amb.sum())
+            diff = np.where(amb, 0.0, diff)
+        d = np.linalg.norm(diff) / max(np.linalg.norm(po), 1e-30)
+        if d > worst_param:
+            worst_param, worst_name, worst_max = d, n, float(np.max(np.abs(diff)))
     rt.destroy()
     print(f'  [{cfg.key}] {steps} steps: worst loss rel {worst_loss:.2e} ({exact_losses} bit-exact), '
-          f'worst param rel {worst_param:.2e}', flush=True)
-    return worst_loss, worst_param
+          f'worst param rel {worst_param:.2e} ({worst_name}, max |diff| {worst_max:.2e})'
+          + (f', {flips} sign-ambiguous elements' if flip_step else ''), flush=True)
+    return worst_loss, worst_param, flips
+
+
+def _update_error(cfg, seed=42):
+    """One plain SGD step (no momentum) from identical params and batch on both sides: the
+    update p1 - p0 = -lr * g, so its per-tensor relative error is the gradient's. lr is a
+    large power of two so that |lr * g| dwarfs |p0| and the f32 rounding of p1 does not
+    hide the gradient's low digits."""
+    opt = {'kind': 'sgd', 'lr': float(2 ** 24)}
+    ir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, opt)
+    rt = backend.NativeRuntime(ir.wire_json())
+    o = pyoracle.OracleRuntime(ir.wire())
+    p0 = ir.initial_params(seed)
+    rt.upload_params(p0)
+    o.upload_params(p0)
+    b = configs.batches(cfg, 1)[0]
+    rt.step(b)
+    o.step(b)
+    pg = rt.download_params()
+    worst = 0.0
+    for n in ir.param_names:
+        start = np.asarray(p0[n], np.float64).reshape(-1)
+        ug = pg[n].astype(np.float64) - start
+        uo = o.get_home(n, pg[n].size).astype(np.float64) - start
+        worst = max(worst, np.linalg.norm(ug - uo) / max(np.linalg.norm(uo), 1e-30))
+    rt.destroy()
+    print(f'  [{cfg.key}] gradient (SGD update) worst rel {worst:.2e}', flush=True)
+    return worst
 
 
 @pytest.mark.parametrize('key', ['mlp_sin', 'char_mlp', 'cnn', 'nerf', 'transformer'])
 def test_small_variant_100_steps(key):
-    wl, wp = _train_both(configs.small_variant(key), 100)
+    wl, wp, _ = _train_both(configs.small_variant(key), 100)
     assert wl <= LOSS_TOL and wp <= PARAM_TOL
 
 
 @pytest.mark.parametrize('key,steps', [('mlp_sin', 100), ('char_mlp', 10), ('cnn', 3), ('transformer', 2), ('nerf', 1)])
 def test_full_config_parity(key, steps):
+    """Full-size configs with their own optimizer, for as many steps as the oracle affords.
+
+    Adam's first updates are lr * g / (|g| + eps), about lr * sign(g): a gradient entry
+    whose exact value lies inside the f32 rounding noise of its GEMM (the GPU accumulates
+    in f32, the evaluator in f64) can move either way by lr. One such entry among the cnn's
+    1.2M fc weights moves that tensor's relative error by ~2e-4 after 3 steps, so after a
+    few steps at full size those elements (|diff| >= lr / 4; ordinary differences are
+    ~1e-7) are counted, bounded, and left out of the 1e-4 parameter bar. The reduced
+    variants above apply the bar to every element after 100 steps, and
+    test_full_config_gradients checks the full-size gradients directly."""
     pyoracle.set_threads(16)
     t0 = time.time()
-    wl, wp = _train_both(configs.CONFIGS[key], steps)
+    cfg = configs.CONFIGS[key]
+    lr = cfg.optimizer['lr']
+    wl, wp, flips = _train_both(cfg, steps, flip_step=None if steps >= 100 else lr)
     print(f'  [{key}] {time.time() - t0:.1f}s', flush=True)
     assert wl <= LOSS_TOL and wp <= PARAM_TOL
+    n_params = sum(int(np.prod(s)) for s in build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs,
+                                                                cfg.optimizer).param_shapes().values())
+    assert flips <= max(4, 1e-5 * n_params * steps)
+
+
+@pytest.mark.parametrize('key', ['char_mlp', 'cnn', 'transformer', 'nerf'])
+def test_full_config_gradients(key):
+    pyoracle.set_threads(16)
+    assert _update_error(configs.CONFIGS[key]) <= GRAD_TOL
 
 
 def test_sgd_momentum_nesterov_and_scheduled_adamw():
     cfg = configs.small_variant('mlp_sin')
-    wl, wp = _train_both(cfg, 40, opt={'kind': 'sgd', 'lr': 0.01, 'momentum': 0.9, 'nesterov': True,
+    wl, wp, _ = _train_both(cfg, 40, opt={'kind': 'sgd', 'lr': 0.01, 'momentum': 0.9, 'nesterov': True,
                                        'weightDecay': 1e-3})
     assert wl <= LOSS_TOL and wp <= PARAM_TOL
     sched = {'kind': 'warmup', 'peak': 3e-3, 'steps': 5, 'after': {'kind': 'cosineAnnealing', 'peak': 3e-3,
                                                                    'final': 1e-4, 'steps': 30}}
-    wl, wp = _train_both(configs.small_variant('char_mlp'), 40,
+    wl, wp, _ = _train_both(configs.small_variant('char_mlp'), 40,
                          opt={'kind': 'adamw', 'lr': sched, 'weightDecay': 0.05, 'clipGradNorm': 0.5})
     assert wl <= LOSS_TOL and wp <= PARAM_TOL
-    wl, wp = _train_both(configs.small_variant('nerf'), 30, opt={'kind': 'adam', 'lr': 1e-3, 'normalizeGrads': True})
+    wl, wp, _ = _train_both(configs.small_variant('nerf'), 30, opt={'kind': 'adam', 'lr': 1e-3, 'normalizeGrads': True})
     assert wl <= LOSS_TOL and wp <= PARAM_TOL
