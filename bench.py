@@ -29,7 +29,7 @@ RING = 8
 CPU_STEPS = {'mlp_sin': 50, 'char_mlp': 3, 'cnn': 2, 'nerf': 1, 'transformer': 2}
 
 
-def measure(key, steps, warmup, profile_iters=3):
+def measure(key, steps, warmup, profile_iters=3, kind_iters=20):
     from tensorgrad_amd import backend, configs
     from tensorgrad_amd.build_ir import build_training_ir
     cfg = configs.CONFIGS[key]
@@ -48,12 +48,15 @@ def measure(key, steps, warmup, profile_iters=3):
     replay_ms = rt.time_replays(steps) / steps
     nodes = rt.describe()['nodes']
     ms = rt.profile_nodes(profile_iters)
+    # Kernel-family times: back-to-back passes over just that family's launches, HIP
+    # events on the runtime's stream around the passes.
+    gemm_t, gemm_n = rt.time_kinds('gemm', kind_iters)
+    other_t, other_n = rt.time_kinds('-gemm,conv', kind_iters)
+    conv_t, conv_n = rt.time_kinds('conv', kind_iters)
     rt.destroy()
-    gemm_t = sum(t for n, t in zip(nodes, ms) if n['kind'] == 'gemm')
     gemm_f = sum(n['flops'] for n in nodes if n['kind'] == 'gemm')
-    other_t = sum(t for n, t in zip(nodes, ms) if n['kind'] not in ('gemm', 'conv'))
+    gemm_b = sum(n['bytes'] for n in nodes if n['kind'] == 'gemm')
     other_b = sum(n['bytes'] for n in nodes if n['kind'] not in ('gemm', 'conv'))
-    conv_t = sum(t for n, t in zip(nodes, ms) if n['kind'] == 'conv')
     conv_f = sum(n['flops'] for n in nodes if n['kind'] == 'conv')
     by_kind = {}
     for n, t in zip(nodes, ms):
@@ -71,15 +74,49 @@ def measure(key, steps, warmup, profile_iters=3):
         'device_replay_ms': replay_ms,
         'launch_nodes': len(nodes),
         'final_loss': loss,
-        'gemm': {'flop_per_step': gemm_f, 'ms': gemm_t, 'tflops': gemm_f / max(gemm_t, 1e-12) / 1e9,
+        'gemm': {'flop_per_step': gemm_f, 'bytes_per_step': gemm_b, 'launches': gemm_n, 'ms': gemm_t,
+                 'tflops': gemm_f / max(gemm_t, 1e-12) / 1e9,
                  'frac_f32_peak': gemm_f / max(gemm_t, 1e-12) / 1e9 / PEAK_F32_MFMA_TFLOPS,
                  'top': [{'shape': n['shape'], 'ms': round(t, 4), 'tflops': round(n['flops'] / max(t, 1e-12) / 1e9, 2)}
                          for t, n in top_gemm]},
         'conv': {'flop_per_step': conv_f, 'ms': conv_t, 'tflops': conv_f / max(conv_t, 1e-12) / 1e9},
-        'non_gemm': {'bytes_per_step': other_b, 'ms': other_t, 'gbs': other_b / max(other_t, 1e-12) / 1e6,
+        'non_gemm': {'bytes_per_step': other_b, 'launches': other_n, 'ms': other_t,
+                     'gbs': other_b / max(other_t, 1e-12) / 1e6,
                      'frac_hbm_peak': other_b / max(other_t, 1e-12) / 1e6 / PEAK_HBM_GBS},
         'kinds': by_kind,
     }
+
+
+def copy_probe(n=16 << 20, reps=3):
+    """Run a plain streaming copy of known size (y = x * 1.0 over n f32, one fused
+    launch reading 4n bytes and writing 4n bytes) so that profiler byte counters can be
+    scaled against known traffic. Returns the best kernel-pass time in ms."""
+    import numpy as np
+    from tensorgrad_amd import backend, ir as IR
+    from tensorgrad_amd import ops as O
+    from tensorgrad_amd.trace import tensor_input, trace_fn
+    g = trace_fn(lambda: O.mul_scalar(tensor_input('x', [n]), 1.0))
+    w = {'graph': IR.graph_to_wire(g), 'paramGrads': {}, 'writebacks': [], 'optimizer': None}
+    rt = backend.NativeRuntime(IR.dumps(w))
+    x = np.ones(n, np.float32)
+    for _ in range(reps):
+        rt.run({'x': x}, [n], np.float32)
+    t, _ = rt.time_kinds('elementwise,fused', 10)
+    rt.destroy()
+    return t
+
+
+def profiled_traffic(path):
+    """HBM bytes per GEMM launch recorded by the committed rocprofv3 --pmc summary (the
+    line 'hbm_bytes_per_launch: N'), or None."""
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith('hbm_bytes_per_launch:'):
+                    return float(line.split(':', 1)[1])
+    except OSError:
+        pass
+    return None
 
 
 def cpu_baseline(key):
@@ -111,6 +148,10 @@ def main():
     ap.add_argument('--config', default='transformer')
     ap.add_argument('--only', action='store_true', help='measure the headline config only')
     ap.add_argument('--no-cpu', action='store_true')
+    ap.add_argument('--profile-iters', type=int, default=3, help='eager passes for the per-node breakdown')
+    ap.add_argument('--kind-iters', type=int, default=20, help='passes per kernel-family timing')
+    ap.add_argument('--probe-copy', action='store_true',
+                    help='first run a 64 MiB streaming copy (profiler counter calibration)')
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({'error': 'this build runs on one GPU per process; multi-GPU data parallelism is '
@@ -121,9 +162,14 @@ def main():
         print(json.dumps({'error': 'no HIP device visible'}))
         sys.exit(1)
     keys = [args.config] + ([] if args.only else [k for k in configs.CONFIGS if k != args.config])
+    probe = None
+    if args.probe_copy:
+        t = copy_probe()
+        probe = {'bytes': 2 * 4 * (16 << 20), 'ms': round(t, 4), 'gbs': round(2 * 4 * (16 << 20) / t / 1e6, 1)}
+        print(f'# copy probe: {probe}', file=sys.stderr, flush=True)
     results = {}
     for k in keys:
-        results[k] = measure(k, args.steps, args.warmup)
+        results[k] = measure(k, args.steps, args.warmup, args.profile_iters, args.kind_iters)
         print(f'# {k}: {results[k]["steps_per_s"]:.1f} steps/s, replay {results[k]["device_replay_ms"]:.3f} ms',
               file=sys.stderr, flush=True)
     head = results[args.config]
@@ -146,11 +192,18 @@ def main():
         'config': {'workload': cfg.title, 'samples_per_step': cfg.samples_per_step, 'sample_unit': cfg.sample_unit,
                    'samples_per_s': round(head['samples_per_s'], 1),
                    'device_replay_ms_per_step': round(head['device_replay_ms'], 4)},
-        'roofline': {'bound': 'mfma', 'kernel': 'f32 MFMA GEMMs (all matmul / matmul_batched launches of one step)',
+        'roofline': {'bound': 'mfma', 'kernel': 'k_gemm (f32 MFMA GEMM family: every matmul / matmul_batched '
+                                                'launch of one step, split-K reductions included)',
                      'achieved': round(g['tflops'], 3), 'peak': PEAK_F32_MFMA_TFLOPS, 'unit': 'TFLOP/s',
-                     'frac': round(g['frac_f32_peak'], 4), 'traffic': None},
+                     'frac': round(g['frac_f32_peak'], 4),
+                     'traffic': profiled_traffic(os.path.join(ROOT, 'profiles', 'gemm_transformer_traffic.txt')),
+                     'launches_per_step': g['launches'],
+                     'avg_launch_us': round(1e3 * g['ms'] / max(g['launches'], 1), 3),
+                     'algorithmic_flop_per_launch': round(g['flop_per_step'] / max(g['launches'], 1)),
+                     'algorithmic_bytes_per_launch': round(g['bytes_per_step'] / max(g['launches'], 1))},
         'roofline_non_gemm': {'bound': 'hbm', 'achieved': round(head['non_gemm']['gbs'], 1), 'peak': PEAK_HBM_GBS,
                               'unit': 'GB/s', 'frac': round(head['non_gemm']['frac_hbm_peak'], 4)},
+        'copy_probe': probe,
         'cpu_baseline': None if cpu is None else {k: (round(v, 5) if isinstance(v, float) else v) for k, v in cpu.items()},
         'per_config': [{'config': r['config'], 'steps_per_s': round(r['steps_per_s'], 2),
                         'samples_per_s': round(r['samples_per_s'], 1), 'device_replay_ms': round(r['device_replay_ms'], 4),

@@ -126,6 +126,11 @@ tg_status tg_profile_nodes(tg_runtime* rt, int iters, double* ms_out, int64_t n_
 /* Time `steps` graph replays (device-resident inputs from the previous step) between two
  * HIP events; returns total milliseconds. */
 tg_status tg_time_replays(tg_runtime* rt, int steps, double* total_ms);
+/* Time `iters` back-to-back passes over only the launch nodes whose kind (as reported by
+ * tg_describe) is listed in `kinds` (comma separated; a leading '-' selects all other
+ * nodes); returns milliseconds per pass and the number of launches in a pass. Used for
+ * per-kernel-family roofline figures. No counterpart in the reference. */
+tg_status tg_time_kinds(tg_runtime* rt, const char* kinds, int iters, double* ms_per_pass, int* launches);
 
 #ifdef __cplusplus
 }

@@ -24,7 +24,7 @@ EXPORTED = (
     'tg_last_error', 'tg_device_count', 'tg_runtime_create', 'tg_runtime_create_sibling', 'tg_destroy',
     'tg_param_count', 'tg_param_name', 'tg_param_numel', 'tg_upload_params', 'tg_download_params', 'tg_step',
     'tg_step_device', 'tg_stage_batch', 'tg_step_staged', 'tg_run', 'tg_capture_count', 'tg_capture_name', 'tg_get_capture', 'tg_reset_optimizer',
-    'tg_set_lr', 'tg_describe', 'tg_plan', 'tg_profile_nodes', 'tg_time_replays',
+    'tg_set_lr', 'tg_describe', 'tg_plan', 'tg_profile_nodes', 'tg_time_replays', 'tg_time_kinds',
 )
 
 
@@ -85,6 +85,8 @@ def lib():
     L.tg_plan.argtypes = [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_int64]
     L.tg_profile_nodes.argtypes = [vp, ctypes.c_int, ctypes.POINTER(ctypes.c_double), ctypes.c_int64]
     L.tg_time_replays.argtypes = [vp, ctypes.c_int, ctypes.POINTER(ctypes.c_double)]
+    L.tg_time_kinds.argtypes = [vp, ctypes.c_char_p, ctypes.c_int, ctypes.POINTER(ctypes.c_double),
+                                ctypes.POINTER(ctypes.c_int)]
     _lib = L
     return L
 
@@ -222,3 +224,9 @@ class NativeRuntime:
         ms = ctypes.c_double()
         _check(lib().tg_time_replays(self._h, steps, ctypes.byref(ms)))
         return ms.value
+
+    def time_kinds(self, kinds: str, iters: int):
+        """(milliseconds per pass, launches per pass) over the nodes of the listed kinds."""
+        ms, n = ctypes.c_double(), ctypes.c_int()
+        _check(lib().tg_time_kinds(self._h, kinds.encode(), iters, ctypes.byref(ms), ctypes.byref(n)))
+        return ms.value, n.value

@@ -12,6 +12,8 @@
 //    transpose(one_hot) -> matmul a segmented scatter-add (embedding gradient), so the
 //    one-hot matrix is never built for them; all adam_update_{m,v,p} ops become one fused
 //    multi-tensor kernel updating p, m and v in place (no writeback copies);
+//  * fusion: maximal convex runs of same-shape pointwise ops become one launch of the
+//    fused register-machine kernel (k_fused.hip), storing only values used outside;
 //  * memory: one arena per runtime, persistent regions for params / optimizer state /
 //    inputs, and liveness-pooled intermediates (best fit, as buffers.ts:151-209);
 //  * execution: one HIP stream; the launch sequence is captured once into a hipGraph
@@ -181,6 +183,7 @@ class Runtime {
   std::string describe();
   void profile_nodes(int iters, double* ms, int64_t n);
   double time_replays(int steps);
+  double time_kinds(const std::string& kinds, int iters, int* launches);
 
   std::vector<std::string> capture_names;
   std::vector<Runtime*> children;
@@ -1787,6 +1790,36 @@ void Runtime::profile_nodes(int iters, double* ms, int64_t nout) {
   for (size_t i = 0; i < nodes_.size(); ++i) ms[i] = acc[i] / std::max(1, iters);
 }
 
+// Launch only the nodes whose kind is listed in `kinds` (comma separated; a leading '-'
+// selects every node whose kind is NOT listed), in step order, `iters` times back to
+// back between two HIP events on the runtime's stream. Returns milliseconds per pass and
+// the number of nodes in a pass. The selected kernels read whatever the buffers hold.
+double Runtime::time_kinds(const std::string& kinds, int iters, int* launches) {
+  bool negate = !kinds.empty() && kinds[0] == '-';
+  std::set<std::string> want;
+  std::stringstream ss(negate ? kinds.substr(1) : kinds);
+  for (std::string k; std::getline(ss, k, ',');) if (!k.empty()) want.insert(k);
+  std::vector<size_t> sel;
+  for (size_t i = 0; i < nodes_.size(); ++i)
+    if ((want.count(nodes_[i].kind) > 0) != negate) sel.push_back(i);
+  *launches = (int)sel.size();
+  if (sel.empty() || iters <= 0) return 0.0;
+  hip_check(hipStreamSynchronize(stream_), "hipStreamSynchronize");
+  hipEvent_t a, b;
+  hip_check(hipEventCreate(&a), "hipEventCreate");
+  hip_check(hipEventCreate(&b), "hipEventCreate");
+  hip_check(hipEventRecord(a, stream_), "hipEventRecord");
+  for (int it = 0; it < iters; ++it)
+    for (size_t i : sel) nodes_[i].launch(stream_);
+  hip_check(hipEventRecord(b, stream_), "hipEventRecord");
+  hip_check(hipEventSynchronize(b), "hipEventSynchronize");
+  float ms = 0;
+  hip_check(hipEventElapsedTime(&ms, a, b), "hipEventElapsedTime");
+  hipEventDestroy(a);
+  hipEventDestroy(b);
+  return ms / iters;
+}
+
 double Runtime::time_replays(int steps) {
   if (use_graph_) ensure_graph();
   hipEvent_t a, b;
@@ -2005,6 +2038,11 @@ tg_status tg_profile_nodes(tg_runtime* h, int iters, double* ms_out, int64_t n_o
 tg_status tg_time_replays(tg_runtime* h, int steps, double* total_ms) {
   TG_ENTER(h);
   return guarded([&] { *total_ms = h->rt->time_replays(steps); });
+}
+
+tg_status tg_time_kinds(tg_runtime* h, const char* kinds, int iters, double* ms_per_pass, int* launches) {
+  TG_ENTER(h);
+  return guarded([&] { *ms_per_pass = h->rt->time_kinds(kinds ? kinds : "", iters, launches); });
 }
 
 }  // extern "C"
