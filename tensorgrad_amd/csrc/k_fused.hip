@@ -56,6 +56,22 @@ __device__ __forceinline__ uint32_t from_num(double v, int dt) {
   return dt == DT_F32 ? fbits((float)v) : (uint32_t)to_int32(v);
 }
 
+// Abramowitz & Stegun 7.1.26, the reference's erf (test/_eval.ts:193-198).
+__device__ __forceinline__ float erf_as(float xf) {
+  const double v = xf;
+  const double sg = js_sign(v), av = fabs(v);
+  const double t = 1.0 / (1.0 + 0.3275911 * av);
+  const double pl = t * (0.254829592 + t * (-0.284496736 + t * (1.421413741 + t * (-1.453152027 + t * 1.061405429))));
+  return (float)(sg * (1.0 - pl * exp(-av * av)));
+}
+
+__device__ __forceinline__ uint32_t dropout_bits(uint32_t x, uint32_t seed, uint32_t salt, double p, double scale,
+                                                 uint32_t elem) {
+  const uint32_t hh = pcg_f64(seed, salt, elem);
+  const double u = (double)hh / 4294967296.0;
+  return fbits((float)((double)bitsf(x) * (u >= p ? scale : 0.0)));
+}
+
 // General forms: one element. Kept out of line so the kernel body stays small.
 __device__ __noinline__ uint32_t general_op(const FusedInstr in, uint32_t x, uint32_t y, uint32_t seed,
                                                uint32_t elem) {
@@ -190,6 +206,18 @@ __global__ __launch_bounds__(256) void k_fused(const FusedProgram p, uint32_t nv
           break;
         }
         case FO_COPY: TG_EACH(X)
+        // Frequent f64 transcendentals and dropout inline (one dispatch per instruction).
+        case FO_EXP: TG_EACH(fbits((float)exp((double)bitsf(X))))
+        case FO_LOG: TG_EACH(fbits((float)log((double)bitsf(X))))
+        case FO_TANH: TG_EACH(fbits((float)tanh((double)bitsf(X))))
+        case FO_ERF: TG_EACH(fbits(erf_as(bitsf(X))))
+        case FO_DROPOUT: {
+          const uint32_t salt = code[q].salt;
+          const double pr = code[q].imm, sc = code[q].imm2;
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) REG(dst, e) = dropout_bits(REG(a, e), seed, salt, pr, sc, t * VEC + e);
+          break;
+        }
 #undef TG_EACH
         default: {
           FusedInstr in;

@@ -157,6 +157,10 @@ struct Node {
   std::vector<int> reads, writes;   // storage roots
   double flops = 0, bytes = 0;      // algorithmic work per launch
   std::string shape;
+  std::string detail;  // fused groups: member op kinds in program order
+  int stream = 0;               // capture stream (see Runtime::schedule)
+  std::vector<int> waits;       // nodes on other streams this one waits for
+  bool signal = false;          // some node on another stream waits for this one
   std::function<void(hipStream_t)> launch;   // bound after allocation
   std::function<std::function<void(hipStream_t)>()> bind;
 };
@@ -270,6 +274,22 @@ class Runtime {
  private:
   void ensure_graph();
   void replay();
+  void schedule();
+  void prepare_streams();
+  void launch_streams();
+  // Independent launches of a step can run concurrently on up to kStreams streams inside
+  // the captured graph, each stream with its own workspace slice. Off by default (one
+  // stream): capturing the transformer step across several streams crashed inside the
+  // HIP runtime on the test machine (a one-stream capture of the same step and a
+  // several-stream capture of the small MLP ran correctly). TG_STREAMS=n selects n.
+  static constexpr int kStreams = 4;
+  int nstreams_ = 1;
+  std::vector<hipStream_t> side_;
+  std::vector<hipEvent_t> node_ev_;
+  std::vector<hipEvent_t> join_ev_;
+  hipEvent_t fork_ev_ = nullptr;
+  size_t ws_stride_ = 0;
+  float* cur_ws_ = nullptr;   // workspace slice of the node being bound
   // TG_GRAPH=0 in the environment issues each step's launches directly instead of
   // replaying a captured hipGraph (for tools that do not follow graph launches).
   bool use_graph_ = true;
@@ -286,6 +306,7 @@ class Runtime {
 
 Runtime::Runtime(const char* json, Runtime* par, bool plan_only) : parent(par) {
   if (const char* g = std::getenv("TG_GRAPH")) use_graph_ = std::string(g) != "0";
+  if (const char* g = std::getenv("TG_STREAMS")) nstreams_ = std::max(1, std::min(kStreams, std::atoi(g)));
   try {
     doc_ = tgj::parse(json);
   } catch (std::exception& e) {
@@ -326,13 +347,19 @@ Runtime::Runtime(const char* json, Runtime* par, bool plan_only) : parent(par) {
   lower();
   if (!plan_only) hip_check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate");
   allocate();
+  schedule();
   bind_all();   // in plan-only mode this still runs every launch's host-side bounds proof
+  prepare_streams();
 }
 
 Runtime::~Runtime() {
   if (graph_exec_) hipGraphExecDestroy(graph_exec_);
   if (graph_) hipGraphDestroy(graph_);
   if (stream_) { hipStreamSynchronize(stream_); hipStreamDestroy(stream_); }
+  for (hipStream_t x : side_) { hipStreamSynchronize(x); hipStreamDestroy(x); }
+  for (hipEvent_t e : node_ev_) if (e) hipEventDestroy(e);
+  for (hipEvent_t e : join_ev_) hipEventDestroy(e);
+  if (fork_ev_) hipEventDestroy(fork_ev_);
   if (arena_) hipFree(arena_);
   if (input_region_) hipFree(input_region_);
   if (workspace_ && !plan_only_) hipFree(workspace_);
@@ -582,6 +609,10 @@ void Runtime::lower() {
       n.reads.push_back(root(fld(pi, "p")));
       n.reads.push_back(root(fld(mo, "m")));
       n.reads.push_back(root(fld(vo, "v")));
+      // updated in place
+      n.writes.push_back(root(fld(pi, "p")));
+      n.writes.push_back(root(fld(mo, "m")));
+      n.writes.push_back(root(fld(vo, "v")));
       n.reads.push_back(root(fld(pi, "lrt")));
       const tgj::Value& ds = O(pi).at("decayShrinkTensor");
       if (!ds.null()) n.reads.push_back(root(ds.i32()));
@@ -724,6 +755,7 @@ void Runtime::lower_group(int gi) {
   n.op = g.first;
   n.kind = g.ops.size() == 1 ? "elementwise" : "fused";
   n.shape = shape_str(g.shape) + " x" + std::to_string(g.ops.size());
+  for (size_t q = 0; q < g.ops.size(); ++q) n.detail += (q ? "," : "") + kinds_[g.ops[q]];
   // External operands (dropout seeds are read through a pointer, not as operands).
   std::vector<int> ext;
   int seed = -1;
@@ -1091,7 +1123,7 @@ void Runtime::lower_op(int i) {
       const float* pa = (const float*)dptr(a); void* po = dptr(out);
       if (k == "mean_last" || k == "sum_last") {
         double div = k == "mean_last" ? (double)D : 1.0;
-        double* w = (double*)workspace_;
+        double* w = (double*)cur_ws_;
         return [=](hipStream_t st) { tgk::reduce_sum(pa, (float*)po, cells, red, outer, D, div, w, st); };
       }
       if (k == "argmax_last") return [=](hipStream_t st) { tgk::row_argmax(pa, (int32_t*)po, outer, D, st); };
@@ -1206,7 +1238,7 @@ void Runtime::lower_op(int i) {
         check_span("sum_to_shape src", T_[root(a)].numel, 0, dd, ss, r);
       }
       const float* pa = (const float*)dptr(a); float* po = (float*)dptr(out);
-      double* w = (double*)workspace_;
+      double* w = (double*)cur_ws_;
       return [=](hipStream_t st) { tgk::reduce_sum(pa, po, cells, red, ncells, nred, 1.0, w, st); };
     };
   } else if (k == "matmul" || k == "matmul_batched") {
@@ -1254,7 +1286,7 @@ void Runtime::lower_op(int i) {
         n.bind = [=]() -> std::function<void(hipStream_t)> {
           const int32_t* pi = (const int32_t*)dptr(idx); const float* pd = (const float*)dptr(b);
           float* po = (float*)dptr(out);
-          void* work = workspace_;
+          void* work = cur_ws_;
           return [=](hipStream_t st) { tgk::scatter_rows(pi, rows, pd, V, N, po, work, st); };
         };
         add_node(std::move(n));
@@ -1323,7 +1355,7 @@ void Runtime::lower_op(int i) {
       g.A = (const float*)dptr(a);
       g.B = (const float*)dptr(b);
       g.C = (float*)dptr(out);
-      float* w = workspace_;
+      float* w = cur_ws_;
       return [=](hipStream_t st) { tgk::gemm(g, w, st); };
     };
   } else if (k == "conv2d" || k == "conv2d_input_grad" || k == "conv2d_weight_grad") {
@@ -1509,7 +1541,8 @@ void Runtime::allocate() {
   memset(staging_, 0, input_region_bytes_);
   for (int t : input_roots) ptr_[t] = input_region_ + input_offset_[t];
   hip_check(hipHostMalloc(&loss_host_, 256, hipHostMallocDefault), "hipHostMalloc");
-  if (workspace_bytes_) hip_check(hipMalloc(&workspace_, workspace_bytes_), "hipMalloc(workspace)");
+  ws_stride_ = (workspace_bytes_ + 255) & ~(size_t)255;
+  if (workspace_bytes_) hip_check(hipMalloc(&workspace_, ws_stride_ * nstreams_), "hipMalloc(workspace)");
   if (!fused_code_.empty()) {
     const size_t cb = fused_code_.size() * sizeof(tgk::FusedInstr);
     hip_check(hipMalloc(&fused_code_dev_, cb), "hipMalloc(fused code)");
@@ -1531,8 +1564,114 @@ void Runtime::bind_all() {
   for (auto& n : nodes_) {
     for (int r : n.reads) if (!ptr_[r]) throw Error(TG_INTERNAL, "unallocated operand in node " + n.kind);
     for (int r : n.writes) if (!ptr_[r]) throw Error(TG_INTERNAL, "unallocated output in node " + n.kind);
+    cur_ws_ = workspace_ ? reinterpret_cast<float*>(reinterpret_cast<char*>(workspace_) + ws_stride_ * n.stream)
+                         : nullptr;
     n.launch = n.bind();
   }
+  cur_ws_ = nullptr;
+}
+
+// Assign launch nodes to capture streams. Two nodes conflict when one writes bytes the
+// other reads or writes (byte ranges of their storage roots, so reuse of pooled arena
+// blocks is respected); a node starts after every earlier conflicting node. Greedy list
+// scheduling in step order: each node goes to the stream on which its estimated start is
+// earliest (ties: the stream of its latest dependency), and waits through events for the
+// latest conflicting node on each other stream.
+void Runtime::schedule() {
+  const int n = (int)nodes_.size();
+  for (auto& nd : nodes_) { nd.stream = 0; nd.waits.clear(); nd.signal = false; }
+  if (nstreams_ <= 1 || !use_graph_ || plan_only_ || n == 0) return;
+  struct Range { uintptr_t lo, hi; };
+  auto range = [&](int r) {
+    uintptr_t lo = (uintptr_t)ptr_[r];
+    return Range{lo, lo + (uintptr_t)std::max<int64_t>(4, T_[r].numel * 4)};
+  };
+  std::vector<std::vector<Range>> rd(n), wr(n);
+  for (int i = 0; i < n; ++i) {
+    for (int r : nodes_[i].reads) rd[i].push_back(range(r));
+    for (int r : nodes_[i].writes) wr[i].push_back(range(r));
+  }
+  auto overlap = [](const std::vector<Range>& a, const std::vector<Range>& b) {
+    for (const Range& x : a)
+      for (const Range& y : b)
+        if (x.lo < y.hi && y.lo < x.hi) return true;
+    return false;
+  };
+  std::vector<double> fin(n, 0.0);
+  std::vector<double> ready(nstreams_, 0.0);
+  std::vector<int> last_on(nstreams_, -1);
+  for (int i = 0; i < n; ++i) {
+    // latest conflicting node per stream
+    std::vector<int> dep(nstreams_, -1);
+    double dep_fin = 0.0;
+    int latest = -1;
+    for (int j = i - 1; j >= 0; --j) {
+      const int sj = nodes_[j].stream;
+      if (dep[sj] >= j) continue;
+      if (overlap(wr[i], rd[j]) || overlap(wr[i], wr[j]) || overlap(rd[i], wr[j])) {
+        dep[sj] = std::max(dep[sj], j);
+        dep_fin = std::max(dep_fin, fin[j]);
+        latest = std::max(latest, j);
+      }
+    }
+    int best = latest >= 0 ? nodes_[latest].stream : 0;
+    double best_start = std::max(ready[best], dep_fin);
+    for (int s2 = 0; s2 < nstreams_; ++s2) {
+      const double st = std::max(ready[s2], dep_fin);
+      if (st < best_start - 1e-9) { best = s2; best_start = st; }
+    }
+    Node& nd = nodes_[i];
+    nd.stream = best;
+    for (int s2 = 0; s2 < nstreams_; ++s2)
+      if (s2 != best && dep[s2] >= 0) { nd.waits.push_back(dep[s2]); nodes_[dep[s2]].signal = true; }
+    const double cost = 3e-6 + nd.bytes / 4e12 + nd.flops / 60e12;
+    fin[i] = best_start + cost;
+    ready[best] = fin[i];
+    last_on[best] = i;
+  }
+}
+
+// Issue the step's launches on their streams with the event waits chosen by schedule():
+// fork from stream_, join back into stream_, then the copy writebacks.
+// Streams and events used by launch_streams(). Created up front, never while a capture
+// is open: stream and event creation are not capturable operations.
+void Runtime::prepare_streams() {
+  if (nstreams_ <= 1 || !use_graph_ || plan_only_ || !side_.empty()) return;
+  for (int s2 = 1; s2 < nstreams_; ++s2) {
+    hipStream_t x;
+    hip_check(hipStreamCreateWithFlags(&x, hipStreamNonBlocking), "hipStreamCreate");
+    side_.push_back(x);
+    hipEvent_t e;
+    hip_check(hipEventCreateWithFlags(&e, hipEventDisableTiming), "hipEventCreate");
+    join_ev_.push_back(e);
+  }
+  hip_check(hipEventCreateWithFlags(&fork_ev_, hipEventDisableTiming), "hipEventCreate");
+  node_ev_.assign(nodes_.size(), nullptr);
+  for (size_t i = 0; i < nodes_.size(); ++i)
+    if (nodes_[i].signal) hip_check(hipEventCreateWithFlags(&node_ev_[i], hipEventDisableTiming), "hipEventCreate");
+}
+
+void Runtime::launch_streams() {
+  if ((int)side_.size() != nstreams_ - 1 || node_ev_.size() != nodes_.size() || !fork_ev_)
+    throw Error(TG_INTERNAL, "launch_streams: streams were not prepared");
+  for (size_t i = 0; i < nodes_.size(); ++i)
+    for (int j : nodes_[i].waits)
+      if (j < 0 || j >= (int)i || !node_ev_[j]) throw Error(TG_INTERNAL, "launch_streams: bad wait");
+  auto strm = [&](int s2) { return s2 == 0 ? stream_ : side_[s2 - 1]; };
+  hip_check(hipEventRecord(fork_ev_, stream_), "hipEventRecord");
+  for (hipStream_t x : side_) hip_check(hipStreamWaitEvent(x, fork_ev_, 0), "hipStreamWaitEvent");
+  for (size_t i = 0; i < nodes_.size(); ++i) {
+    Node& nd = nodes_[i];
+    hipStream_t st = strm(nd.stream);
+    for (int j : nd.waits) hip_check(hipStreamWaitEvent(st, node_ev_[j], 0), "hipStreamWaitEvent");
+    nd.launch(st);
+    if (nd.signal) hip_check(hipEventRecord(node_ev_[i], st), "hipEventRecord");
+  }
+  for (size_t q = 0; q < side_.size(); ++q) {
+    hip_check(hipEventRecord(join_ev_[q], side_[q]), "hipEventRecord");
+    hip_check(hipStreamWaitEvent(stream_, join_ev_[q], 0), "hipStreamWaitEvent");
+  }
+  apply_copy_writebacks(stream_);
 }
 
 void Runtime::launch_all(hipStream_t st) {
@@ -1576,8 +1715,12 @@ void Runtime::ensure_graph() {
   if (graph_exec_) return;
   hip_check(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
   try {
-    launch_all(stream_);
-    apply_copy_writebacks(stream_);
+    if (nstreams_ > 1) {
+      launch_streams();
+    } else {
+      launch_all(stream_);
+      apply_copy_writebacks(stream_);
+    }
   } catch (...) {
     hipGraph_t g;
     hipStreamEndCapture(stream_, &g);
@@ -1761,7 +1904,9 @@ std::string Runtime::describe() {
     const Node& n = nodes_[i];
     o << (i ? "," : "") << "{\"kind\":\"" << n.kind << "\",\"op\":" << n.op << ",\"ir_kind\":\""
       << (n.op >= 0 ? kinds_[n.op] : "") << "\",\"shape\":\"" << n.shape << "\",\"flops\":" << n.flops
-      << ",\"bytes\":" << n.bytes << "}";
+      << ",\"bytes\":" << n.bytes;
+    if (!n.detail.empty()) o << ",\"ops\":\"" << n.detail << "\"";
+    o << "}";
   }
   o << "],\"arena_bytes\":" << arena_bytes_ << ",\"workspace_bytes\":" << workspace_bytes_
     << ",\"ir_ops\":" << ops_.size() << "}";
