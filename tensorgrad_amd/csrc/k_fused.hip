@@ -109,20 +109,120 @@ __device__ __noinline__ uint32_t general_op(const FusedInstr in, uint32_t x, uin
 }
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef const __attribute__((address_space(4))) FusedInstr* ConstCode;
 
-// Thread t evaluates elements VEC*t .. VEC*t + VEC - 1 of the (row-major) iteration
-// space. The register file lives in LDS: register k of element e of thread j is word
-// (k * VEC + e) * 256 + j, so every register access of a wavefront is one conflict-free
-// LDS instruction, whatever the (wave-uniform) register index.
+// The program interpreter shared by both kernel forms. A thread owns N elements; register
+// k of element e is my[(k * N + e) * 256] in LDS (my = regs + threadIdx.x), so every
+// register access of a wavefront is one conflict-free LDS instruction whatever the
+// (wave-uniform) register index. Element e has flat index elem0 + e * estride (the
+// dropout hash index). Row form (TPR > 0): the TPR threads of a row hold its elements
+// j = lane + e * TPR, bit e of `live` marks j < D of a real row, and FO_ROWSUM reduces
+// a register over the row (f64, fixed order: each thread's elements in order, a
+// wavefront butterfly, then the row's wavefronts in order through `part`).
+template <int N, int TPR>
+__device__ __forceinline__ void run_program(ConstCode code, int n_instr, uint32_t* my, uint32_t seed, uint32_t elem0,
+                                            uint32_t estride, uint32_t live, double* part) {
+#define REG(k, e) my[((k) * N + (e)) * 256]
+  for (int q = 0; q < n_instr; ++q) {
+    const int op = code[q].op, a = code[q].a, b = code[q].b, dst = code[q].dst;
+    switch (op) {
+#define TG_EACH(EXPR)                                              \
+  _Pragma("unroll") for (int e = 0; e < N; ++e) {                  \
+    const uint32_t X = REG(a, e);                                  \
+    const uint32_t Y = REG(b, e);                                  \
+    (void)Y;                                                       \
+    REG(dst, e) = (EXPR);                                          \
+  }                                                                \
+  break;
+      // f32 +, -, *, /: the correctly rounded f32 operation equals computing in f64 and
+      // rounding once.
+      case FO_FADD: TG_EACH(fbits(bitsf(X) + bitsf(Y)))
+      case FO_FSUB: TG_EACH(fbits(bitsf(X) - bitsf(Y)))
+      case FO_FMUL: TG_EACH(fbits(bitsf(X) * bitsf(Y)))
+      case FO_FDIV: TG_EACH(fbits(bitsf(X) / bitsf(Y)))
+      case FO_MULS: {
+        const double s = code[q].imm;
+        const int ta = code[q].ta;
+        TG_EACH(fbits((float)(num(X, ta) * s)))
+      }
+      case FO_ADDS: {
+        const double s = code[q].imm;
+        const int ta = code[q].ta;
+        TG_EACH(fbits((float)(num(X, ta) + s)))
+      }
+      // f64 sqrt rounded once to f32 is the correctly rounded f32 square root.
+      case FO_SQRT: TG_EACH(fbits((float)sqrt((double)bitsf(X))))
+      case FO_NEG: TG_EACH(X ^ 0x80000000u)
+      case FO_ABS: TG_EACH(X & 0x7fffffffu)
+      // max(x, 0) with JS semantics: NaN stays NaN, -0 becomes +0.
+      case FO_RELU: TG_EACH(bitsf(X) != bitsf(X) ? 0x7fc00000u : (bitsf(X) > 0.0f ? X : 0u))
+      case FO_RELU_GRAD: TG_EACH(bitsf(X) > 0.0f ? Y : 0u)
+      case FO_WHERE: {
+        const int c = code[q].c;
+#pragma unroll
+        for (int e = 0; e < N; ++e) REG(dst, e) = REG(a, e) != 0u ? REG(b, e) : REG(c, e);
+        break;
+      }
+      case FO_COPY: TG_EACH(X)
+      // Frequent f64 transcendentals and dropout inline.
+      case FO_EXP: TG_EACH(fbits((float)exp((double)bitsf(X))))
+      case FO_LOG: TG_EACH(fbits((float)log((double)bitsf(X))))
+      case FO_TANH: TG_EACH(fbits((float)tanh((double)bitsf(X))))
+      case FO_ERF: TG_EACH(fbits(erf_as(bitsf(X))))
+#undef TG_EACH
+      case FO_DROPOUT: {
+        const uint32_t salt = code[q].salt;
+        const double pr = code[q].imm, sc = code[q].imm2;
+#pragma unroll
+        for (int e = 0; e < N; ++e) REG(dst, e) = dropout_bits(REG(a, e), seed, salt, pr, sc, elem0 + e * estride);
+        break;
+      }
+      case FO_ROWSUM: {
+        if (TPR > 0) {
+          double s = 0.0;
+#pragma unroll
+          for (int e = 0; e < N; ++e)
+            if ((live >> e) & 1u) s += (double)bitsf(REG(a, e));
+#pragma unroll
+          for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+          if (TPR > 64) {
+            if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+            __syncthreads();
+            const int w0 = (threadIdx.x / (TPR > 0 ? TPR : 1)) * (TPR / 64);
+            double tsum = 0.0;
+#pragma unroll
+            for (int w = 0; w < TPR / 64; ++w) tsum += part[w0 + w];
+            s = tsum;
+            __syncthreads();
+          }
+          const uint32_t v = fbits((float)(s / code[q].imm));
+#pragma unroll
+          for (int e = 0; e < N; ++e) REG(dst, e) = v;
+        }
+        break;
+      }
+      default: {
+        FusedInstr in;
+        in.op = op; in.dst = dst; in.a = a; in.b = b; in.c = code[q].c;
+        in.dt = code[q].dt; in.ta = code[q].ta; in.tb = code[q].tb; in.salt = code[q].salt;
+        in.imm = code[q].imm; in.imm2 = code[q].imm2;
+#pragma unroll
+        for (int e = 0; e < N; ++e) REG(dst, e) = general_op(in, REG(a, e), REG(b, e), seed, elem0 + e * estride);
+        break;
+      }
+    }
+  }
+#undef REG
+}
+
+// Element form: thread t evaluates elements VEC*t .. VEC*t + VEC - 1 of the (row-major)
+// iteration space.
 template <int VEC>
 __global__ __launch_bounds__(256) void k_fused(const FusedProgram p, uint32_t nv) {
-  extern __shared__ uint32_t regs[];   // (n_in + n_instr) * VEC * 256 words
+  extern __shared__ uint32_t regs[];   // nregs * VEC * 256 words
   uint32_t* const my = regs + threadIdx.x;
 #define REG(k, e) my[((k) * VEC + (e)) * 256]
   const uint32_t seed = p.seed ? (uint32_t)*p.seed : 0u;
-  // The program is read-only for the kernel's lifetime: reading it through the constant
-  // address space lets the compiler use scalar loads.
-  typedef const __attribute__((address_space(4))) FusedInstr* ConstCode;
   const ConstCode code = (ConstCode)(uintptr_t)p.code;
   for (uint32_t t = blockIdx.x * 256u + threadIdx.x; t < nv; t += gridDim.x * 256u) {
     uint32_t coord[kMaxRank] = {};
@@ -165,71 +265,7 @@ __global__ __launch_bounds__(256) void k_fused(const FusedProgram p, uint32_t nv
         }
       }
     }
-    for (int q = 0; q < p.n_instr; ++q) {
-      const int op = code[q].op, a = code[q].a, b = code[q].b, dst = code[q].dst;
-      switch (op) {
-#define TG_EACH(EXPR)                                              \
-  _Pragma("unroll") for (int e = 0; e < VEC; ++e) {                \
-    const uint32_t X = REG(a, e);                                  \
-    const uint32_t Y = REG(b, e);                                  \
-    (void)Y;                                                       \
-    REG(dst, e) = (EXPR);                                          \
-  }                                                                \
-  break;
-        // f32 +, -, *, /: the correctly rounded f32 operation equals computing in f64
-        // and rounding once.
-        case FO_FADD: TG_EACH(fbits(bitsf(X) + bitsf(Y)))
-        case FO_FSUB: TG_EACH(fbits(bitsf(X) - bitsf(Y)))
-        case FO_FMUL: TG_EACH(fbits(bitsf(X) * bitsf(Y)))
-        case FO_FDIV: TG_EACH(fbits(bitsf(X) / bitsf(Y)))
-        case FO_MULS: {
-          const double s = code[q].imm;
-          const int ta = code[q].ta;
-          TG_EACH(fbits((float)(num(X, ta) * s)))
-        }
-        case FO_ADDS: {
-          const double s = code[q].imm;
-          const int ta = code[q].ta;
-          TG_EACH(fbits((float)(num(X, ta) + s)))
-        }
-        // f64 sqrt rounded once to f32 is the correctly rounded f32 square root.
-        case FO_SQRT: TG_EACH(fbits((float)sqrt((double)bitsf(X))))
-        case FO_NEG: TG_EACH(X ^ 0x80000000u)
-        case FO_ABS: TG_EACH(X & 0x7fffffffu)
-        // max(x, 0) with JS semantics: NaN stays NaN, -0 becomes +0.
-        case FO_RELU: TG_EACH(bitsf(X) != bitsf(X) ? 0x7fc00000u : (bitsf(X) > 0.0f ? X : 0u))
-        case FO_RELU_GRAD: TG_EACH(bitsf(X) > 0.0f ? Y : 0u)
-        case FO_WHERE: {
-          const int c = code[q].c;
-#pragma unroll
-          for (int e = 0; e < VEC; ++e) REG(dst, e) = REG(a, e) != 0u ? REG(b, e) : REG(c, e);
-          break;
-        }
-        case FO_COPY: TG_EACH(X)
-        // Frequent f64 transcendentals and dropout inline (one dispatch per instruction).
-        case FO_EXP: TG_EACH(fbits((float)exp((double)bitsf(X))))
-        case FO_LOG: TG_EACH(fbits((float)log((double)bitsf(X))))
-        case FO_TANH: TG_EACH(fbits((float)tanh((double)bitsf(X))))
-        case FO_ERF: TG_EACH(fbits(erf_as(bitsf(X))))
-        case FO_DROPOUT: {
-          const uint32_t salt = code[q].salt;
-          const double pr = code[q].imm, sc = code[q].imm2;
-#pragma unroll
-          for (int e = 0; e < VEC; ++e) REG(dst, e) = dropout_bits(REG(a, e), seed, salt, pr, sc, t * VEC + e);
-          break;
-        }
-#undef TG_EACH
-        default: {
-          FusedInstr in;
-          in.op = op; in.dst = dst; in.a = a; in.b = b; in.c = code[q].c;
-          in.dt = code[q].dt; in.ta = code[q].ta; in.tb = code[q].tb; in.salt = code[q].salt;
-          in.imm = code[q].imm; in.imm2 = code[q].imm2;
-#pragma unroll
-          for (int e = 0; e < VEC; ++e) REG(dst, e) = general_op(in, REG(a, e), REG(b, e), seed, t * VEC + e);
-          break;
-        }
-      }
-    }
+    run_program<VEC, 0>(code, p.n_instr, my, seed, t * VEC, 1, 0xffffffffu, nullptr);
 #pragma unroll
     for (int k = 0; k < kFusedMaxOut; ++k) {
       if (k < p.n_out) {
@@ -249,14 +285,100 @@ __global__ __launch_bounds__(256) void k_fused(const FusedProgram p, uint32_t nv
 #undef REG
 }
 
+// Row form: the iteration space is rows x D; TPR threads own a row (one wavefront as
+// launched), 256 / TPR rows per block, each thread EPT elements (j = lane + e * TPR). Operand
+// k of row r, column j is at rowoff_k(r) + j * in_inner[k], rowoff from the row's
+// coordinates over the merged row dims (p.div / p.in_strides). Outputs flagged in
+// out_row are per-row values, stored once per row at index r.
+template <int TPR, int EPT>
+__global__ __launch_bounds__(256) void k_fused_rows(const FusedProgram p, uint32_t nrows, uint32_t D) {
+  extern __shared__ uint32_t regs[];   // 4 doubles of partials, then nregs * EPT * 256 words
+  double* part = reinterpret_cast<double*>(regs);
+  uint32_t* const my = regs + 8 + threadIdx.x;
+#define REG(k, e) my[((k) * EPT + (e)) * 256]
+  constexpr int RPB = 256 / TPR;
+  const uint32_t seed = p.seed ? (uint32_t)*p.seed : 0u;
+  const ConstCode code = (ConstCode)(uintptr_t)p.code;
+  const uint32_t lane = threadIdx.x % TPR;
+  // Every thread runs every iteration (uniform trip count), so the barriers inside
+  // FO_ROWSUM are reached by the whole block; threads of rows past the end compute on
+  // zeros and store nothing.
+  for (uint32_t rb = blockIdx.x * RPB; rb < nrows; rb += gridDim.x * RPB) {
+    const uint32_t r = rb + threadIdx.x / TPR;
+    const bool live_row = r < nrows;
+    uint32_t live = 0;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e)
+      if (live_row && lane + e * TPR < D) live |= 1u << e;
+    uint32_t coord[kMaxRank] = {};
+    {
+      uint32_t rem = live_row ? r : 0u;
+#pragma unroll
+      for (int d = kMaxRank - 1; d >= 1; --d) {
+        if (d < p.rank) {
+          const uint32_t q = fastdiv(rem, p.div[d]);
+          coord[d] = rem - q * p.div[d].d;
+          rem = q;
+        }
+      }
+      coord[0] = rem;
+    }
+#pragma unroll
+    for (int k = 0; k < kFusedMaxIn; ++k) {
+      if (k < p.n_in) {
+        const uint32_t* src = static_cast<const uint32_t*>(p.in[k]);
+        uint32_t off = 0;
+#pragma unroll
+        for (int d = 0; d < kMaxRank; ++d)
+          if (d < p.rank) off += coord[d] * (uint32_t)p.in_strides[k][d];
+        const uint32_t cs = (uint32_t)p.in_inner[k];
+#pragma unroll
+        for (int e = 0; e < EPT; ++e) REG(k, e) = ((live >> e) & 1u) ? src[off + (lane + e * TPR) * cs] : 0u;
+      }
+    }
+    run_program<EPT, TPR>(code, p.n_instr, my, seed, r * D + lane, TPR, live, part);
+#pragma unroll
+    for (int k = 0; k < kFusedMaxOut; ++k) {
+      if (k < p.n_out) {
+        uint32_t* dstp = static_cast<uint32_t*>(p.out[k]);
+        const int reg = p.out_reg[k];
+        if (p.out_row[k]) {
+          if (live_row && lane == 0) dstp[r] = REG(reg, 0);
+        } else {
+#pragma unroll
+          for (int e = 0; e < EPT; ++e)
+            if ((live >> e) & 1u) dstp[r * D + lane + e * TPR] = REG(reg, e);
+        }
+      }
+    }
+  }
+#undef REG
+}
+
 }  // namespace
 
 void fused(const FusedProgram& prog, int64_t n, hipStream_t st) {
   if (n <= 0) return;
+  if (prog.row_d > 0) {
+    // n = number of rows
+    const int D = prog.row_d;
+    // One wavefront per row (reductions are wavefront butterflies, no block barriers),
+    // four rows per block, ceil(D / 64) elements per lane.
+    const int ept = D <= 64 ? 1 : (D <= 128 ? 2 : (D <= 256 ? 4 : (D <= 512 ? 8 : 16)));
+    int64_t b = (n + 3) / 4;
+    if (b > 16384) b = 16384;
+    const size_t lds = 64 + (size_t)prog.nregs * ept * 256 * 4;
+    if (ept == 1) k_fused_rows<64, 1><<<(int)b, 256, lds, st>>>(prog, (uint32_t)n, (uint32_t)D);
+    else if (ept == 2) k_fused_rows<64, 2><<<(int)b, 256, lds, st>>>(prog, (uint32_t)n, (uint32_t)D);
+    else if (ept == 4) k_fused_rows<64, 4><<<(int)b, 256, lds, st>>>(prog, (uint32_t)n, (uint32_t)D);
+    else if (ept == 8) k_fused_rows<64, 8><<<(int)b, 256, lds, st>>>(prog, (uint32_t)n, (uint32_t)D);
+    else k_fused_rows<64, 16><<<(int)b, 256, lds, st>>>(prog, (uint32_t)n, (uint32_t)D);
+    return;
+  }
   int64_t b = (n + 255) / 256;
   if (b > 16384) b = 16384;
   // LDS holds only the registers the program uses.
-  const size_t lds = (size_t)(prog.n_in + prog.n_instr) * prog.vec * 256 * 4;
+  const size_t lds = (size_t)prog.nregs * prog.vec * 256 * 4;
   if (prog.vec == 4) k_fused<4><<<(int)b, 256, lds, st>>>(prog, (uint32_t)n);
   else k_fused<1><<<(int)b, 256, lds, st>>>(prog, (uint32_t)n);
 }

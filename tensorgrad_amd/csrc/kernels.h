@@ -70,7 +70,7 @@ void categorical(const float* a, int32_t* out, int64_t outer, int64_t D, const i
 constexpr int kFusedRegs = 16;
 constexpr int kFusedMaxIn = 8;
 constexpr int kFusedMaxOut = 8;
-constexpr int kFusedMaxInstr = 16;
+constexpr int kFusedMaxInstr = 64;
 // Opcodes FO_FADD .. FO_COPY are the inexpensive forms (f32 operands and result where
 // typed) evaluated unrolled over a thread's elements; the rest are general forms (mixed
 // i32 / f32 typing, comparisons, f64 transcendentals, dropout).
@@ -78,7 +78,8 @@ enum FusedOp {
   FO_FADD, FO_FSUB, FO_FMUL, FO_FDIV, FO_MULS, FO_ADDS, FO_SQRT, FO_NEG, FO_ABS, FO_RELU, FO_RELU_GRAD,
   FO_WHERE, FO_COPY,
   FO_ADD, FO_SUB, FO_MUL, FO_DIV, FO_MIN, FO_MAX, FO_LESS, FO_GREATER,
-  FO_RSQRT, FO_LOG, FO_EXP, FO_TANH, FO_SIGMOID, FO_ERF, FO_SIN, FO_COS, FO_DROPOUT
+  FO_RSQRT, FO_LOG, FO_EXP, FO_TANH, FO_SIGMOID, FO_ERF, FO_SIN, FO_COS, FO_DROPOUT,
+  FO_ROWSUM   // row form only: dst = f32(sum over the row of a, in f64, / imm)
 };
 // Operand access modes. With several elements per thread (vec 4), a strided operand's
 // innermost stride decides how the thread's run of elements is read: FM_STRIDED_V one
@@ -99,6 +100,12 @@ struct FusedInstr {
 // touches has fewer than 2^31 elements.
 struct FusedProgram {
   int32_t n_in, n_out, n_instr, rank, any_strided, vec;
+  // Row form when row_d > 0: the iteration space is rows x row_d, `rank` / div /
+  // in_strides describe the merged row dims, in_inner the column stride, and out_row
+  // marks per-row outputs.
+  int32_t row_d;
+  int32_t out_row[8];
+  int32_t nregs;          // registers the program uses (LDS is sized from it)
   FastDiv div[kMaxRank];
   const void* in[kFusedMaxIn];
   int32_t in_dt[kFusedMaxIn], in_mode[kFusedMaxIn], in_inner[kFusedMaxIn];
@@ -108,7 +115,7 @@ struct FusedProgram {
   const int32_t* seed;
   const FusedInstr* code;
 };
-// `n` = number of threads' runs (elements / vec).
+// `n` = number of threads' runs (elements / vec), or of rows in the row form.
 void fused(const FusedProgram& prog, int64_t n, hipStream_t st);
 
 // ---- reductions / softmax (k_reduce.hip) --------------------------------------------

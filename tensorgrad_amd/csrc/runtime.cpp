@@ -242,7 +242,26 @@ class Runtime {
   bool plan_only_ = false;
 
   // Element-wise fusion groups: members in op order; the group runs at its first op.
-  struct Group { int first; std::vector<int> ops; Dims shape; };
+  // A fused group: ops evaluated by one launch of the fused kernel. `shape` is the
+  // iteration shape: every member's output for an element group; for a row group (one
+  // that contains last-axis reductions) the full [.., D] shape, members producing either
+  // that shape or its row shape ([..] or [.., 1]).
+  struct Group { int first; std::vector<int> ops; Dims shape; bool row = false; };
+  // Register plan of a group: external operands (tensor + the broadcast class of the
+  // consumer: 0 full, 1 row [..], 2 row [.., 1]), stored outputs, and a linear-scan
+  // register assignment (a register is reused after its value's last read).
+  struct GroupPlan {
+    std::vector<std::pair<int, int>> ext;   // (tensor, class) loaded into registers 0..n-1
+    int seed = -1;
+    std::vector<int> outs;                  // member outputs stored by the launch
+    std::vector<int> out_reg;
+    std::vector<tgk::FusedInstr> code;
+    int nregs = 0;
+  };
+  GroupPlan plan_group(const std::vector<int>& ops, bool row, const Dims& F) const;
+  int producer_group(int t) const;
+  int op_class(int m, bool row, const Dims& F) const;
+  bool is_row_reduce(int m) const;
   std::vector<Group> groups_;
   std::vector<int> group_of_;   // op -> group index or -1
   std::deque<tgk::FusedProgram> programs_;     // kernel-argument images (stable addresses)
@@ -687,10 +706,175 @@ static const std::map<std::string, int>& pointwise_ops() {
   return m;
 }
 
-// Greedy convex grouping of same-shape pointwise ops. An op joins a group only if every
-// operand is either produced inside the group or available before the group's first op
-// (an earlier op, a leaf, or an earlier group), so the whole group can run at its first
-// op's position without reordering anything else.
+static bool is_row_reduce_kind(const std::string& k) { return k == "sum_last" || k == "mean_last"; }
+
+// Row shapes of a full shape F = [.., D]: F without its last dim, or with it set to 1.
+static int row_class(const Dims& s, const Dims& F) {
+  if (F.empty()) return 0;
+  Dims a(F.begin(), F.end() - 1);
+  if (s == a) return 1;
+  a.push_back(1);
+  if (s == a) return 2;
+  return 0;
+}
+
+// Last-axis sums: sum_last, mean_last, and a sum_to_shape that only collapses the last
+// axis (its target is the input shape with the last dim set to 1).
+bool Runtime::is_row_reduce(int m) const {
+  const std::string& k = kinds_[m];
+  if (is_row_reduce_kind(k)) return true;
+  if (k != "sum_to_shape") return false;
+  const Dims& in = T_[fld(m, "a")].shape;
+  const Dims& out = T_[O(m).at("out").i32()].shape;
+  return !in.empty() && in.back() > 1 && row_class(out, in) == 2;
+}
+
+// The group whose member produced tensor t's values, when t is that member's output or
+// a contiguous full-size view of it (a reshape keeps the flat order); -1 otherwise.
+int Runtime::producer_group(int t) const {
+  const int r = root(t);
+  const int src = T_[r].src;
+  if (src < 0 || group_of_[src] < 0) return -1;
+  if (t != r && !(view_[t].contiguous() && T_[t].numel == T_[r].numel)) return -1;
+  if (O(src).at("out").i32() != r) return -1;
+  return group_of_[src];
+}
+
+// Broadcast class of member m's operands: 0 = full (element groups, reductions and
+// full-shaped members of row groups), 1 / 2 = row-shaped member ([..] / [.., 1]).
+int Runtime::op_class(int m, bool row, const Dims& F) const {
+  if (!row || is_row_reduce(m)) return 0;
+  return row_class(T_[O(m).at("out").i32()].shape, F);
+}
+
+Runtime::GroupPlan Runtime::plan_group(const std::vector<int>& ops, bool row, const Dims& F) const {
+  const auto& pw = pointwise_ops();
+  GroupPlan gp;
+  std::set<int> members(ops.begin(), ops.end());
+  auto inside = [&](int t) {
+    const int gi = producer_group(t);
+    return gi >= 0 && members.count(T_[root(t)].src) > 0;
+  };
+  // operands per member, in instruction order
+  std::vector<std::vector<int>> opnds(ops.size());
+  for (size_t q = 0; q < ops.size(); ++q) {
+    const int m = ops[q];
+    const std::string& k = kinds_[m];
+    const tgj::Value& op = O(m);
+    if (k == "relu_grad") opnds[q] = {op.at("x").i32(), op.at("dy").i32()};
+    else if (k == "where") opnds[q] = {op.at("cond").i32(), op.at("a").i32(), op.at("b").i32()};
+    else if (op.get("b") && k != "dropout") opnds[q] = {op.at("a").i32(), op.at("b").i32()};
+    else opnds[q] = {op.at("a").i32()};
+    if (k == "dropout") gp.seed = op.at("seed").i32();
+  }
+  // external operands
+  for (size_t q = 0; q < ops.size(); ++q) {
+    const int cls = op_class(ops[q], row, F);
+    for (int t : opnds[q]) {
+      if (inside(t)) continue;
+      std::pair<int, int> key{t, cls};
+      if (std::find(gp.ext.begin(), gp.ext.end(), key) == gp.ext.end()) gp.ext.push_back(key);
+    }
+  }
+  // stored outputs: members read outside the group, graph outputs, captures, writeback sources
+  std::set<int> must_store;
+  for (int o : outputs_) must_store.insert(o);
+  for (auto& c : captures_) must_store.insert(c.second);
+  for (auto& w : copy_writebacks_) must_store.insert(w.first);
+  std::vector<bool> stored(ops.size(), false);
+  for (size_t q = 0; q < ops.size(); ++q) {
+    const int t = O(ops[q]).at("out").i32();
+    bool ext_use = must_store.count(t) > 0;
+    for (int c : consumers_[t]) if (!members.count(c)) ext_use = true;
+    if (ext_use) { stored[q] = true; gp.outs.push_back(t); }
+  }
+  // last read of every value (ext operand index or member position)
+  std::map<int, int> member_pos;   // producing op -> position
+  for (size_t q = 0; q < ops.size(); ++q) member_pos[ops[q]] = (int)q;
+  std::vector<int> ext_last(gp.ext.size(), -1), val_last(ops.size(), -1);
+  auto ref = [&](size_t q, int t, int cls) -> std::pair<bool, int> {   // (is_member, index)
+    if (inside(t)) return {true, member_pos.at(T_[root(t)].src)};
+    const auto it = std::find(gp.ext.begin(), gp.ext.end(), std::make_pair(t, cls));
+    return {false, (int)(it - gp.ext.begin())};
+  };
+  for (size_t q = 0; q < ops.size(); ++q) {
+    const int cls = op_class(ops[q], row, F);
+    for (int t : opnds[q]) {
+      auto r = ref(q, t, cls);
+      if (r.first) val_last[r.second] = (int)q;
+      else ext_last[r.second] = (int)q;
+    }
+  }
+  // linear scan: ext operands take registers 0..n_ext-1 before the first instruction
+  std::vector<int> ext_reg(gp.ext.size()), val_reg(ops.size(), -1);
+  std::vector<bool> busy;
+  auto take = [&]() {
+    for (size_t r = 0; r < busy.size(); ++r) if (!busy[r]) { busy[r] = true; return (int)r; }
+    busy.push_back(true);
+    return (int)busy.size() - 1;
+  };
+  for (size_t e = 0; e < gp.ext.size(); ++e) ext_reg[e] = take();
+  for (size_t q = 0; q < ops.size(); ++q) {
+    const int m = ops[q];
+    const std::string& k = kinds_[m];
+    const tgj::Value& op = O(m);
+    const int cls = op_class(m, row, F);
+    tgk::FusedInstr in{};
+    std::vector<int> regs;
+    for (int t : opnds[q]) {
+      auto r = ref(q, t, cls);
+      regs.push_back(r.first ? val_reg[r.second] : ext_reg[r.second]);
+    }
+    auto DT = [&](int t) { return kdt(T_[t].dt); };
+    in.a = regs[0];
+    in.ta = DT(opnds[q][0]);
+    if (regs.size() > 1) { in.b = regs[1]; in.tb = DT(opnds[q][1]); }
+    if (regs.size() > 2) in.c = regs[2];
+    const int out = op.at("out").i32();
+    in.dt = kdt(T_[out].dt);
+    if (is_row_reduce(m)) {
+      in.op = tgk::FO_ROWSUM;
+      in.imm = k == "mean_last" ? (double)F.back() : 1.0;
+    } else {
+      in.op = pw.at(k);
+      if (k == "mul_scalar" || k == "add_scalar") in.imm = op.at("scalar").num();
+      if (k == "dropout") {
+        const double p = op.at("p").num();
+        in.imm = p;
+        in.imm2 = 1.0 / (1.0 - p);
+        in.salt = (uint32_t)(uint64_t)std::fmod((double)op.at("salt").i64() * 2654435761.0, 4294967296.0);
+      }
+      // Inexpensive f32 forms of the arithmetic ops.
+      if (in.ta == tgk::DT_F32 && in.tb == tgk::DT_F32 && in.dt == tgk::DT_F32) {
+        if (in.op == tgk::FO_ADD) in.op = tgk::FO_FADD;
+        else if (in.op == tgk::FO_SUB) in.op = tgk::FO_FSUB;
+        else if (in.op == tgk::FO_MUL) in.op = tgk::FO_FMUL;
+        else if (in.op == tgk::FO_DIV) in.op = tgk::FO_FDIV;
+      }
+    }
+    // free operands read for the last time here (an instruction reads all operands of an
+    // element before writing its result, so dst may reuse one of them)
+    for (int t : opnds[q]) {
+      auto r = ref(q, t, cls);
+      if (r.first) { if (val_last[r.second] == (int)q && !stored[r.second]) busy[val_reg[r.second]] = false; }
+      else if (ext_last[r.second] == (int)q) busy[ext_reg[r.second]] = false;
+    }
+    in.dst = val_reg[q] = take();
+    if (val_last[q] < 0 && !stored[q]) busy[in.dst] = false;   // dead value
+    gp.code.push_back(in);
+  }
+  for (size_t q = 0; q < ops.size(); ++q)
+    if (stored[q]) gp.out_reg.push_back(val_reg[q]);
+  gp.nregs = (int)busy.size();
+  return gp;
+}
+
+// Greedy convex grouping. An op joins a group that produces one of its inputs if every
+// operand is produced inside the group or available before the group's first op (an
+// earlier op, a leaf, or an earlier group), so the whole group can run at its first op's
+// position without reordering anything else. Same-shape pointwise ops form element
+// groups; a last-axis sum / mean turns its group into a row group, which may also hold
+// pointwise ops on the row shape (LayerNorm, softmax and cross-entropy chains).
 void Runtime::form_groups() {
   group_of_.assign(ops_.size(), -1);
   groups_.clear();
@@ -702,46 +886,75 @@ void Runtime::form_groups() {
     if (src < 0 || is_leaf(src)) return -1;
     return group_of_[src] >= 0 ? groups_[group_of_[src]].first : src;
   };
-  auto ext_inputs = [&](const Group& g, int extra) {
-    std::set<int> members(g.ops.begin(), g.ops.end());
-    if (extra >= 0) members.insert(extra);
-    std::set<int> ext;
-    for (int m : members)
-      for (int t : op_inputs(*ops_[m])) {
-        if (members.count(T_[t].src)) continue;
-        if (kinds_[m] == "dropout" && t == fld(m, "seed")) continue;
-        ext.insert(t);
-      }
-    return ext.size();
+  auto fits = [&](const std::vector<int>& ops, bool row, const Dims& F) {
+    if (ops.size() > (size_t)tgk::kFusedMaxInstr) return false;
+    GroupPlan gp = plan_group(ops, row, F);
+    return gp.ext.size() <= (size_t)tgk::kFusedMaxIn && gp.outs.size() <= (size_t)tgk::kFusedMaxOut &&
+           gp.nregs <= tgk::kFusedRegs;
   };
   for (size_t i = 0; i < ops_.size(); ++i) {
     const std::string& k = kinds_[i];
-    if (virtual_[i] || !pw.count(k) || is_leaf((int)i)) continue;
+    if (virtual_[i] || is_leaf((int)i)) continue;
+    const bool red = is_row_reduce((int)i);
+    if (!red && !pw.count(k)) continue;
     const int out = ops_[i]->at("out").i32();
-    const Dims& S = T_[out].shape;
+    const Dims& So = T_[out].shape;
     if (T_[out].numel <= 0) continue;
+    Dims In;
+    if (red) {
+      const int a = fld((int)i, "a");
+      In = T_[a].shape;
+      if (In.empty() || In.back() < 1 || In.back() > 1024 || T_[a].numel <= 0) continue;   // standalone kernel
+    }
     std::vector<int> cands;
     for (int t : op_inputs(*ops_[i])) {
-      int src = T_[t].src;
-      if (src >= 0 && group_of_[src] >= 0 && groups_[group_of_[src]].shape == S && T_[t].shape == S)
-        cands.push_back(group_of_[src]);
+      const int gi = producer_group(t);
+      if (gi >= 0 && std::find(cands.begin(), cands.end(), gi) == cands.end()) cands.push_back(gi);
     }
     std::sort(cands.begin(), cands.end(), [&](int a, int b) { return groups_[a].first > groups_[b].first; });
     int joined = -1;
     for (int gi : cands) {
       Group& g = groups_[gi];
-      bool ok = g.ops.size() < (size_t)tgk::kFusedMaxInstr;
-      for (int t : op_inputs(*ops_[i])) {
-        int src = T_[t].src;
-        bool inside = src >= 0 && group_of_[src] == gi;
-        if (!inside && eff_pos(t) >= g.first) ok = false;
+      const Dims& F = g.shape;
+      bool ok = true;
+      bool becomes_row = g.row;
+      if (red) {
+        ok = T_[fld((int)i, "a")].shape == F;
+        becomes_row = true;
+      } else if (!g.row) {
+        ok = So == F;
+      } else {
+        const int cls = row_class(So, F);
+        ok = So == F || (cls > 0 && k != "dropout");
       }
-      if (ok && ext_inputs(g, (int)i) > (size_t)tgk::kFusedMaxIn) ok = false;
-      if (ok && ext_inputs(g, (int)i) + g.ops.size() + 1 > (size_t)tgk::kFusedRegs) ok = false;
-      if (ok) { g.ops.push_back((int)i); group_of_[i] = gi; joined = gi; break; }
+      for (int t : op_inputs(*ops_[i])) {
+        if (!ok) break;
+        const bool in_g = producer_group(t) == gi;
+        if (!in_g) {
+          if (eff_pos(t) >= g.first) ok = false;
+          continue;
+        }
+        if (k == "dropout" && t == fld((int)i, "seed")) continue;
+        const Dims& ts = T_[t].shape;
+        if (red) continue;   // the reduced input has shape F (checked above)
+        if (!g.row) { if (ts != F) ok = false; continue; }
+        if (So == F) { if (!(ts == F || row_class(ts, F) == 2)) ok = false; }
+        else if (ts != So) ok = false;
+      }
+      if (!ok) continue;
+      std::vector<int> ops = g.ops;
+      ops.push_back((int)i);
+      if (!fits(ops, becomes_row, F)) continue;
+      g.ops.push_back((int)i);
+      g.row = becomes_row;
+      group_of_[i] = gi;
+      joined = gi;
+      break;
     }
     if (joined < 0) {
-      groups_.push_back(Group{(int)i, {(int)i}, S});
+      Group g{(int)i, {(int)i}, red ? In : So, red};
+      if (!fits(g.ops, g.row, g.shape)) continue;
+      groups_.push_back(g);
       group_of_[i] = (int)groups_.size() - 1;
     }
   }
@@ -749,174 +962,141 @@ void Runtime::form_groups() {
 
 void Runtime::lower_group(int gi) {
   const Group& g = groups_[gi];
-  const auto& pw = pointwise_ops();
-  std::set<int> members(g.ops.begin(), g.ops.end());
+  const Dims F = g.shape;
+  const bool row = g.row;
+  GroupPlan gp = plan_group(g.ops, row, F);
+  if (gp.ext.size() > (size_t)tgk::kFusedMaxIn || gp.outs.size() > (size_t)tgk::kFusedMaxOut ||
+      gp.nregs > tgk::kFusedRegs)
+    throw Error(TG_INTERNAL, "fused group exceeds the kernel's limits");
   Node n;
   n.op = g.first;
-  n.kind = g.ops.size() == 1 ? "elementwise" : "fused";
-  n.shape = shape_str(g.shape) + " x" + std::to_string(g.ops.size());
+  n.kind = row ? "rowfused" : (g.ops.size() == 1 ? "elementwise" : "fused");
+  n.shape = shape_str(F) + " x" + std::to_string(g.ops.size());
   for (size_t q = 0; q < g.ops.size(); ++q) n.detail += (q ? "," : "") + kinds_[g.ops[q]];
-  // External operands (dropout seeds are read through a pointer, not as operands).
-  std::vector<int> ext;
-  int seed = -1;
-  for (int m : g.ops) {
-    for (int t : op_inputs(*ops_[m])) {
-      if (members.count(T_[t].src)) continue;
-      if (kinds_[m] == "dropout" && t == fld(m, "seed")) { seed = t; continue; }
-      if (std::find(ext.begin(), ext.end(), t) == ext.end()) ext.push_back(t);
-    }
-  }
-  if (ext.size() > (size_t)tgk::kFusedMaxIn) throw Error(TG_INTERNAL, "fused group: too many operands");
-  for (int t : ext) n.reads.push_back(root(t));
-  if (seed >= 0) n.reads.push_back(root(seed));
-  // Outputs: members read outside the group (or graph outputs / captures / writeback sources).
-  std::set<int> must_store;
-  for (int o : outputs_) must_store.insert(o);
-  for (auto& c : captures_) must_store.insert(c.second);
-  for (auto& w : copy_writebacks_) must_store.insert(w.first);
-  std::vector<int> outs;
-  for (int m : g.ops) {
-    int t = ops_[m]->at("out").i32();
-    bool ext_use = must_store.count(t) > 0;
-    for (int c : consumers_[t]) if (!members.count(c)) ext_use = true;
-    if (ext_use) outs.push_back(t);
-  }
-  if (outs.size() > (size_t)tgk::kFusedMaxOut) throw Error(TG_INTERNAL, "fused group: too many outputs");
-  for (int t : outs) n.writes.push_back(root(t));
+  for (auto& e : gp.ext) n.reads.push_back(root(e.first));
+  if (gp.seed >= 0) n.reads.push_back(root(gp.seed));
+  for (int t : gp.outs) n.writes.push_back(root(t));
   double bytes = 0;
-  for (int t : ext) bytes += 4.0 * T_[t].numel;
-  bytes += 4.0 * prod(g.shape) * outs.size();
+  std::set<int> counted;
+  for (auto& e : gp.ext) if (counted.insert(e.first).second) bytes += 4.0 * T_[e.first].numel;
+  for (int t : gp.outs) bytes += 4.0 * T_[t].numel;
   n.bytes = bytes;
-  // Register map: operands first, then one register per member.
-  std::map<int, int> reg;
-  for (size_t q = 0; q < ext.size(); ++q) reg[ext[q]] = (int)q;
-  std::vector<tgk::FusedInstr> code;
-  int next = (int)ext.size();
-  for (int m : g.ops) {
-    const tgj::Value& op = O(m);
-    const std::string& k = kinds_[m];
-    tgk::FusedInstr in{};
-    in.op = pw.at(k);
-    int out = op.at("out").i32();
-    in.dt = kdt(T_[out].dt);
-    auto R = [&](const char* f) { return reg.at(op.at(f).i32()); };
-    auto DT = [&](const char* f) { return kdt(T_[op.at(f).i32()].dt); };
-    if (k == "relu_grad") { in.a = R("x"); in.b = R("dy"); in.ta = DT("x"); in.tb = DT("dy"); }
-    else if (k == "where") { in.a = R("cond"); in.b = R("a"); in.c = R("b"); in.ta = DT("cond"); in.tb = DT("a"); }
-    else {
-      in.a = R("a");
-      in.ta = DT("a");
-      if (op.get("b") && (k != "dropout")) { in.b = R("b"); in.tb = DT("b"); }
-    }
-    if (k == "mul_scalar" || k == "add_scalar") in.imm = op.at("scalar").num();
-    if (k == "dropout") {
-      double p = op.at("p").num();
-      in.imm = p;
-      in.imm2 = 1.0 / (1.0 - p);
-      in.salt = (uint32_t)(uint64_t)std::fmod((double)op.at("salt").i64() * 2654435761.0, 4294967296.0);
-    }
-    // Inexpensive f32 forms of the arithmetic ops.
-    if (in.ta == tgk::DT_F32 && in.tb == tgk::DT_F32 && in.dt == tgk::DT_F32) {
-      if (in.op == tgk::FO_ADD) in.op = tgk::FO_FADD;
-      else if (in.op == tgk::FO_SUB) in.op = tgk::FO_FSUB;
-      else if (in.op == tgk::FO_MUL) in.op = tgk::FO_FMUL;
-      else if (in.op == tgk::FO_DIV) in.op = tgk::FO_FDIV;
-    }
-    in.dst = next;
-    reg[out] = next++;
-    code.push_back(in);
-  }
   const size_t code_off = fused_code_.size();
-  fused_code_.insert(fused_code_.end(), code.begin(), code.end());
-  const Dims S = g.shape;
-  std::vector<int> out_regs;
-  for (int t : outs) out_regs.push_back(reg.at(t));
+  fused_code_.insert(fused_code_.end(), gp.code.begin(), gp.code.end());
+  const int seed = gp.seed;
   const size_t slot = programs_.size();
   programs_.emplace_back();
   n.bind = [=]() -> std::function<void(hipStream_t)> {
     tgk::FusedProgram& p = programs_[slot];
     memset(&p, 0, sizeof(p));
-    const int64_t cnt = prod(S);
+    const int64_t cnt = prod(F);
     if (cnt >= (int64_t(1) << 31)) throw Error(TG_INVALID_ARGUMENT, "fused group: 2^31 or more elements");
-    // Broadcast strides of every operand over S, then drop size-1 dims and merge
-    // neighbours that are contiguous in every operand (outputs are contiguous).
-    std::vector<Dims> bs(ext.size(), Dims(S.size(), 0));
-    for (size_t q = 0; q < ext.size(); ++q) {
-      const View& v = view_[ext[q]];
+    // Broadcast strides of every operand over F (row-class operands broadcast against the
+    // row shape, then stride 0 along D).
+    const size_t nx = gp.ext.size();
+    std::vector<Dims> bs(nx, Dims(F.size(), 0));
+    for (size_t q = 0; q < nx; ++q) {
+      const int t = gp.ext[q].first, cls = gp.ext[q].second;
+      const View& v = view_[t];
       if (T_[v.root].numel >= (int64_t(1) << 31)) throw Error(TG_INVALID_ARGUMENT, "fused group: operand too large");
-      int off = (int)S.size() - (int)v.dims.size();
+      const size_t rankS = cls == 1 ? F.size() - 1 : F.size();
+      const int off = (int)rankS - (int)v.dims.size();
+      if (off < 0) throw Error(TG_INTERNAL, "fused group: operand rank exceeds its consumer's");
       for (size_t d = 0; d < v.dims.size(); ++d) bs[q][off + d] = v.dims[d] == 1 ? 0 : v.strides[d];
-      check_span("fused operand", T_[v.root].numel, 0, S.data(), bs[q].data(), (int)S.size());
+      if (cls > 0) bs[q][F.size() - 1] = 0;
+      check_span("fused operand", T_[v.root].numel, 0, F.data(), bs[q].data(), (int)F.size());
     }
+    // Iteration dims: element groups merge all dims; row groups merge the row dims and keep
+    // D apart. Size-1 dims are dropped.
+    const size_t nmerge = row ? F.size() - 1 : F.size();
     Dims md;
-    std::vector<Dims> ms(ext.size());
-    for (size_t d = 0; d < S.size(); ++d) {
-      if (S[d] == 1) continue;
+    std::vector<Dims> ms(nx);
+    for (size_t d = 0; d < nmerge; ++d) {
+      if (F[d] == 1) continue;
       bool merge = !md.empty();
-      for (size_t q = 0; q < ext.size() && merge; ++q) merge = ms[q].back() == bs[q][d] * S[d];
+      for (size_t q = 0; q < nx && merge; ++q) merge = ms[q].back() == bs[q][d] * F[d];
       if (merge) {
-        md.back() *= S[d];
-        for (size_t q = 0; q < ext.size(); ++q) ms[q].back() = bs[q][d];
+        md.back() *= F[d];
+        for (size_t q = 0; q < nx; ++q) ms[q].back() = bs[q][d];
       } else {
-        md.push_back(S[d]);
-        for (size_t q = 0; q < ext.size(); ++q) ms[q].push_back(bs[q][d]);
+        md.push_back(F[d]);
+        for (size_t q = 0; q < nx; ++q) ms[q].push_back(bs[q][d]);
       }
     }
-    if (md.empty()) {
-      md.push_back(1);
-      for (auto& m : ms) m.push_back(0);
-    }
-    if (md.size() > (size_t)tgk::kMaxRank) throw Error(TG_INTERNAL, "fused group: rank too large");
-    const int R = (int)md.size();
-    const Dims cs = contiguous_strides(md);
     auto aligned = [](const void* ptr) { return ((uintptr_t)ptr & 15) == 0; };
-    // Four elements per thread when the innermost dim allows it and every 128-bit access
-    // is aligned.
-    bool v4 = md[R - 1] % 4 == 0;
-    std::vector<int> mode(ext.size());
-    for (size_t q = 0; q < ext.size(); ++q) {
-      bool contig = true, scalar = true;
-      for (int d = 0; d < R; ++d) {
-        if (ms[q][d] != cs[d]) contig = false;
-        if (ms[q][d] != 0) scalar = false;
+    p.n_in = (int)nx;
+    p.nregs = gp.nregs;
+    if (row) {
+      const int64_t D = F.back();
+      if (md.empty()) { md.push_back(1); for (auto& m : ms) m.push_back(0); }
+      if (md.size() > (size_t)tgk::kMaxRank) throw Error(TG_INTERNAL, "fused group: rank too large");
+      p.row_d = (int32_t)D;
+      p.vec = 1;
+      p.rank = (int)md.size();
+      for (int d = 0; d < p.rank; ++d) p.div[d] = tgk::make_fastdiv((uint32_t)md[d]);
+      for (size_t q = 0; q < nx; ++q) {
+        p.in[q] = ptr_[view_[gp.ext[q].first].root];
+        p.in_dt[q] = kdt(T_[gp.ext[q].first].dt);
+        p.in_mode[q] = tgk::FM_STRIDED;
+        p.in_inner[q] = (int32_t)bs[q][F.size() - 1];
+        for (int d = 0; d < p.rank; ++d) p.in_strides[q][d] = (int32_t)ms[q][d];
       }
-      mode[q] = contig ? tgk::FM_CONTIG : (scalar ? tgk::FM_SCALAR : tgk::FM_STRIDED);
-      if (contig && !aligned(ptr_[view_[ext[q]].root])) v4 = false;
-    }
-    for (int t : outs) if (!aligned(dptr(t))) v4 = false;
-    const int vec = v4 ? 4 : 1;
-    p.vec = vec;
-    p.rank = R;
-    for (int d = 0; d < R; ++d) p.div[d] = tgk::make_fastdiv((uint32_t)(d == R - 1 ? md[d] / vec : md[d]));
-    p.n_in = (int)ext.size();
-    for (size_t q = 0; q < ext.size(); ++q) {
-      const View& v = view_[ext[q]];
-      p.in[q] = ptr_[v.root];
-      p.in_dt[q] = kdt(T_[ext[q]].dt);
-      int m = mode[q];
-      const int64_t inner = ms[q][R - 1];
-      if (m == tgk::FM_STRIDED && vec == 4) {
-        bool outer4 = aligned(ptr_[v.root]);
-        for (int d = 0; d < R - 1; ++d) if (ms[q][d] % 4) outer4 = false;
-        if (inner == 1 && outer4) m = tgk::FM_STRIDED_V;
-        else if (inner == 0) m = tgk::FM_STRIDED_B;
+    } else {
+      if (md.empty()) { md.push_back(1); for (auto& m : ms) m.push_back(0); }
+      if (md.size() > (size_t)tgk::kMaxRank) throw Error(TG_INTERNAL, "fused group: rank too large");
+      const int R = (int)md.size();
+      const Dims cs = contiguous_strides(md);
+      // Four elements per thread when the innermost dim allows it and every 128-bit access
+      // is aligned.
+      bool v4 = md[R - 1] % 4 == 0;
+      std::vector<int> mode(nx);
+      for (size_t q = 0; q < nx; ++q) {
+        bool contig = true, scalar = true;
+        for (int d = 0; d < R; ++d) {
+          if (ms[q][d] != cs[d]) contig = false;
+          if (ms[q][d] != 0) scalar = false;
+        }
+        mode[q] = contig ? tgk::FM_CONTIG : (scalar ? tgk::FM_SCALAR : tgk::FM_STRIDED);
+        if (contig && !aligned(ptr_[view_[gp.ext[q].first].root])) v4 = false;
       }
-      p.in_mode[q] = m;
-      p.in_inner[q] = (int32_t)inner;
-      if (m != tgk::FM_CONTIG && m != tgk::FM_SCALAR) p.any_strided = 1;
-      for (int d = 0; d < R; ++d) p.in_strides[q][d] = (int32_t)(d == R - 1 ? inner * vec : ms[q][d]);
+      for (int t : gp.outs) if (!aligned(dptr(t))) v4 = false;
+      const int vec = v4 ? 4 : 1;
+      p.vec = vec;
+      p.rank = R;
+      for (int d = 0; d < R; ++d) p.div[d] = tgk::make_fastdiv((uint32_t)(d == R - 1 ? md[d] / vec : md[d]));
+      for (size_t q = 0; q < nx; ++q) {
+        const View& v = view_[gp.ext[q].first];
+        p.in[q] = ptr_[v.root];
+        p.in_dt[q] = kdt(T_[gp.ext[q].first].dt);
+        int m = mode[q];
+        const int64_t inner = ms[q][R - 1];
+        if (m == tgk::FM_STRIDED && vec == 4) {
+          bool outer4 = aligned(ptr_[v.root]);
+          for (int d = 0; d < R - 1; ++d) if (ms[q][d] % 4) outer4 = false;
+          if (inner == 1 && outer4) m = tgk::FM_STRIDED_V;
+          else if (inner == 0) m = tgk::FM_STRIDED_B;
+        }
+        p.in_mode[q] = m;
+        p.in_inner[q] = (int32_t)inner;
+        if (m != tgk::FM_CONTIG && m != tgk::FM_SCALAR) p.any_strided = 1;
+        for (int d = 0; d < R; ++d) p.in_strides[q][d] = (int32_t)(d == R - 1 ? inner * vec : ms[q][d]);
+      }
     }
-    p.n_out = (int)outs.size();
-    for (size_t q = 0; q < outs.size(); ++q) {
-      p.out[q] = dptr(outs[q]);
-      p.out_dt[q] = kdt(T_[outs[q]].dt);
-      p.out_reg[q] = out_regs[q];
-      if (T_[root(outs[q])].numel < cnt) throw Error(TG_INTERNAL, "fused group: output too small");
+    p.n_out = (int)gp.outs.size();
+    for (size_t q = 0; q < gp.outs.size(); ++q) {
+      const int t = gp.outs[q];
+      p.out[q] = dptr(t);
+      p.out_dt[q] = kdt(T_[t].dt);
+      p.out_reg[q] = gp.out_reg[q];
+      const bool rowout = row && row_class(T_[t].shape, F) > 0;
+      p.out_row[q] = rowout ? 1 : 0;
+      const int64_t need = rowout ? cnt / F.back() : cnt;
+      if (T_[root(t)].numel < need || T_[t].numel != need) throw Error(TG_INTERNAL, "fused group: output size mismatch");
     }
     p.seed = seed >= 0 ? (const int32_t*)dptr(seed) : nullptr;
-    p.n_instr = (int)code.size();
+    p.n_instr = (int)gp.code.size();
     p.code = fused_code_dev_ + code_off;
-    const int64_t nthreads = cnt / vec;
+    const int64_t nthreads = row ? cnt / F.back() : cnt / p.vec;
     return [this, slot, nthreads](hipStream_t st) { tgk::fused(programs_[slot], nthreads, st); };
   };
   add_node(std::move(n));
