@@ -247,6 +247,209 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g) {
     }
 }
 
+// ---- direct-to-LDS pipeline ------------------------------------------------------------
+//
+// Same tiles, fragments and blocked accumulation as k_gemm, but operand tiles travel from
+// global memory straight into LDS (global_load_lds_dwordx4: each lane's 16 bytes land at
+// wave-base + lane * 16) through a ring of NS stages, so the loads of stages s+1 .. s+NS-1
+// are in flight while stage s is multiplied, without staging registers. LDS rows are not
+// padded; 16-byte chunks are XOR-swizzled instead so fragment reads stay conflict-free:
+//  * k-contiguous operand, rows [r][BK]: chunk c of row r is stored at c ^ swz(r);
+//  * row-contiguous operand, rows [k][ROWS]: chunk c of k-row k is stored at
+//    c ^ (((k >> 2) & 1) << 3), which puts the two lane halves (k and k + 4) on opposite
+//    halves of the banks.
+// Used when K (per split) is a multiple of BK, rows of the row-contiguous operand are a
+// multiple of 4 and both operands are 16-byte aligned; rows past M / N are read clamped
+// to the last row (their results are never stored).
+constexpr int kLdsBlock = 256;   // floats one wavefront-wide DMA writes (1 KiB)
+
+template <int ROWS, int BK, bool KFAST>
+struct DTile {
+  static constexpr int CPR = KFAST ? BK / 4 : ROWS / 4;   // 16-byte chunks per LDS row
+  static constexpr int NCH = ROWS * BK / 4;               // chunks per tile
+  static constexpr int PER = NCH / kThreads;              // DMA instructions per thread
+  static constexpr int SIZE = ROWS * BK;                  // floats
+  static_assert(NCH % kThreads == 0, "tile must be a whole number of DMA rounds");
+  static_assert(KFAST ? (BK == 32 || BK == 64) : ROWS >= 64, "swizzle needs 8 / 16 chunks per row");
+
+  __device__ __forceinline__ static int swz(int lrow) {
+    if (KFAST) return BK == 32 ? ((lrow >> 1) & 7) : (lrow & 15);
+    return ((lrow >> 2) & 1) << 3;
+  }
+
+  __device__ __forceinline__ static void dma(const float* X, int64_t sr, int64_t sk, int64_t r0, int64_t rlim,
+                                             int64_t k0, float* L, int tid) {
+    const int lane = tid & 63, wave = tid >> 6;
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+      const int inst = e * (kThreads / 64) + wave;
+      const int P = inst * 64 + lane;
+      const int row = P / CPR, pc = P % CPR;
+      const int c = pc ^ swz(row);
+      const float* gp;
+      if (KFAST) {
+        const int64_t gr = min(r0 + row, rlim - 1);
+        gp = X + gr * sr + k0 + c * 4;
+      } else {
+        const int64_t gr = min(r0 + c * 4, rlim - 4);
+        gp = X + (k0 + row) * sk + gr;
+      }
+      __builtin_amdgcn_global_load_lds(gp, (__attribute__((address_space(3))) void*)(L + inst * kLdsBlock), 16, 0, 0);
+    }
+  }
+
+  // The 4 consecutive-k values (kb .. kb+3, kb % 4 == 0) of tile row `row`.
+  __device__ __forceinline__ static f32x4 frag(const float* L, int row, int kb) {
+    if (KFAST) return *reinterpret_cast<const f32x4*>(L + row * BK + (((kb >> 2) ^ swz(row)) << 2));
+    f32x4 v;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int k = kb + u;
+      v[u] = L[k * ROWS + ((((row >> 2) ^ swz(k)) << 2) | (row & 3))];
+    }
+    return v;
+  }
+};
+
+// s_waitcnt with vmcnt = N and the other counters left alone (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+template <int BM, int BN, int BK, int NS, bool AK, bool BKF>
+__global__ __launch_bounds__(kThreads) void k_gemm_dma(GemmArgs g) {
+  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int NG = BK / 8;
+  using TA = DTile<BM, BK, AK>;
+  using TB = DTile<BN, BK, BKF>;
+  constexpr int PER = TA::PER + TB::PER;
+  static_assert(PER * (NS - 1) < 64, "too many loads in flight for vmcnt");
+  __shared__ __attribute__((aligned(16))) float As[NS * TA::SIZE];   // NS stages of A
+  __shared__ __attribute__((aligned(16))) float Bs[NS * TB::SIZE];   // NS stages of B
+
+  const GemmDesc& d = g.d;
+  const int tid = threadIdx.x;
+  const int lane = tid % 64;
+  const int wave = tid / 64;
+  const int wm0 = (wave / 2) * WM, wn0 = (wave % 2) * WN;
+
+  const uint32_t nblk = gridDim.x;
+  uint32_t b = blockIdx.x;
+  if (nblk % kXcds == 0) b = (b % kXcds) * (nblk / kXcds) + b / kXcds;
+  const uint32_t tn = b % g.tiles_n;
+  const uint32_t rest = b / g.tiles_n;
+  const uint32_t tm = rest % g.tiles_m;
+  const uint32_t zs = rest / g.tiles_m;
+  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+  const int64_t zz = zs / g.splits;
+  const int split = zs % g.splits;
+  const int64_t z0 = zz / d.bdiv, z1 = zz % d.bdiv;
+  const float* A = d.A + z0 * d.sAz0 + z1 * d.sAz1;
+  const float* B = d.B + z0 * d.sBz0 + z1 * d.sBz1;
+  const int64_t kbeg = split * g.k_per_split;
+  const int64_t kend = min(d.K, kbeg + g.k_per_split);
+  const int nst = kbeg < kend ? (int)((kend - kbeg) / BK) : 0;
+
+  auto issue = [&](int st) {
+    const int slot = st % NS;
+    const int64_t k0 = kbeg + (int64_t)st * BK;
+    TA::dma(A, d.sAm, d.sAk, m0, d.M, k0, As + slot * TA::SIZE, tid);
+    TB::dma(B, d.sBn, d.sBk, n0, d.N, k0, Bs + slot * TB::SIZE, tid);
+  };
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  const int lrow = lane % 32, h = lane / 32;
+#pragma unroll
+  for (int p = 0; p < NS - 1; ++p)
+    if (p < nst) issue(p);
+  for (int st = 0; st < nst; ++st) {
+    // Stage st has landed once at most (stages issued after it) * PER loads are pending.
+    const int after = min(NS - 2, nst - 1 - st);
+    if (NS >= 4 && after >= 2) wait_vmcnt<(NS >= 4 ? 2 : 0) * PER>();
+    else if (NS >= 3 && after >= 1) wait_vmcnt<PER>();
+    else wait_vmcnt<0>();
+    // A bare workgroup barrier: __syncthreads() would also drain every outstanding load
+    // (the stages still in flight). The empty asm statements keep the compiler from
+    // moving LDS accesses across it; each wave has already waited for its own copies of
+    // stage st, and its reads of the slot about to be refilled were consumed by the MFMAs
+    // of the previous stage.
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (st + NS - 1 < nst) issue(st + NS - 1);
+    const float* Ac = As + (st % NS) * TA::SIZE;
+    const float* Bc = Bs + (st % NS) * TB::SIZE;
+    f32x16 part[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) part[i][j][r] = 0.0f;
+    f32x4 av[2][TM], bv[2][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) av[0][i] = TA::frag(Ac, wm0 + i * 32 + lrow, h * 4);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) bv[0][j] = TB::frag(Bc, wn0 + j * 32 + lrow, h * 4);
+#pragma unroll
+    for (int grp = 0; grp < NG; ++grp) {
+      const int c = grp & 1;
+      if (grp + 1 < NG) {
+        const int kb = (grp + 1) * 8 + h * 4;
+#pragma unroll
+        for (int i = 0; i < TM; ++i) av[c ^ 1][i] = TA::frag(Ac, wm0 + i * 32 + lrow, kb);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) bv[c ^ 1][j] = TB::frag(Bc, wn0 + j * 32 + lrow, kb);
+      }
+      // keep the next group's LDS reads ahead of this group's MFMAs
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            part[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[c][i][jj], bv[c][j][jj], part[i][j], 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) acc[i][j] += part[i][j];
+  }
+
+  float* O;
+  int64_t sOm, sOn;
+  if (g.splits > 1) {
+    O = g.out + split * g.sOs + zz * g.sOz;
+    sOm = d.N; sOn = 1;
+  } else {
+    O = d.C + z0 * d.sCz0 + z1 * d.sCz1;
+    sOm = d.sCm; sOn = d.sCn;
+  }
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int64_t gn = n0 + wn0 + j * 32 + lrow;
+      if (gn >= d.N) continue;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t gm = m0 + wm0 + i * 32 + (r / 4) * 8 + h * 4 + (r % 4);
+        if (gm < d.M) O[gm * sOm + gn * sOn] = acc[i][j][r];
+      }
+    }
+}
+
 // Sum split-K partials in split order into C (eight partial loads in flight per thread).
 __global__ void k_splitk_reduce(const float* __restrict__ work, int splits, int64_t sOs, GemmDesc d) {
   const int64_t MN = d.M * d.N, total = MN * d.batch;
@@ -290,6 +493,22 @@ Plan plan_for(const GemmDesc& d) {
   return p;
 }
 
+// Conditions of the direct-to-LDS kernel: whole BK stages in every split, 16-byte aligned
+// operand bases for every batch entry, and per operand either k-contiguous rows with a
+// stride multiple of 4, or contiguous rows (a row count multiple of 4) with a k stride
+// multiple of 4.
+bool dma_ok(const GemmDesc& d, const Plan& p, bool ak, bool bk) {
+  if (d.K % p.bk != 0 || p.kps % p.bk != 0) return false;
+  auto al = [](const float* x) { return ((uintptr_t)x & 15) == 0; };
+  if (!al(d.A) || !al(d.B)) return false;
+  if ((d.batch > 1) && ((d.sAz0 | d.sAz1 | d.sBz0 | d.sBz1) & 3)) return false;
+  if (ak) { if (d.sAm & 3) return false; }
+  else if (!(d.sAm == 1 && (d.sAk & 3) == 0 && d.M % 4 == 0)) return false;
+  if (bk) { if (d.sBn & 3) return false; }
+  else if (!(d.sBn == 1 && (d.sBk & 3) == 0 && d.N % 4 == 0)) return false;
+  return true;
+}
+
 }  // namespace
 
 int64_t gemm_workspace_floats(const GemmDesc& d) {
@@ -313,6 +532,20 @@ void gemm(const GemmDesc& d, float* work, hipStream_t st) {
   const dim3 grid((unsigned)blocks);
   const bool ak = d.sAk == 1;
   const bool bk = d.sBk == 1 && d.sBn != 1;
+  if (dma_ok(d, p, ak, bk)) {
+#define TG_DMA_LAUNCH(BM_, BN_, BK_)                                                           \
+  do {                                                                                       \
+    if (ak && bk) k_gemm_dma<BM_, BN_, BK_, 3, true, true><<<grid, kThreads, 0, st>>>(g);     \
+    else if (ak) k_gemm_dma<BM_, BN_, BK_, 3, true, false><<<grid, kThreads, 0, st>>>(g);     \
+    else if (bk) k_gemm_dma<BM_, BN_, BK_, 3, false, true><<<grid, kThreads, 0, st>>>(g);     \
+    else k_gemm_dma<BM_, BN_, BK_, 3, false, false><<<grid, kThreads, 0, st>>>(g);            \
+  } while (0)
+    if (p.bm == 128 && p.bn == 128) TG_DMA_LAUNCH(128, 128, 32);
+    else if (p.bm == 128) TG_DMA_LAUNCH(128, 64, 32);
+    else if (p.bn == 128) TG_DMA_LAUNCH(64, 128, 32);
+    else TG_DMA_LAUNCH(64, 64, 64);
+#undef TG_DMA_LAUNCH
+  } else {
 #define TG_GEMM_LAUNCH(BM_, BN_, BK_)                                                      \
   do {                                                                                     \
     if (ak && bk) k_gemm<BM_, BN_, BK_, true, true><<<grid, kThreads, 0, st>>>(g);        \
@@ -325,6 +558,7 @@ void gemm(const GemmDesc& d, float* work, hipStream_t st) {
   else if (p.bn == 128) TG_GEMM_LAUNCH(64, 128, 32);
   else TG_GEMM_LAUNCH(64, 64, 64);
 #undef TG_GEMM_LAUNCH
+  }
   if (p.splits > 1) {
     int64_t total = d.batch * d.M * d.N;
     int64_t nb = (total + 255) / 256;
