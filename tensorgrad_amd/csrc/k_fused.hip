@@ -109,80 +109,138 @@ __device__ __noinline__ uint32_t general_op(const FusedInstr in, uint32_t x, uin
 }
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef const __attribute__((address_space(4))) FusedInstr* ConstCode;
 
-// The program interpreter shared by both kernel forms. A thread owns N elements; register
-// k of element e is my[(k * N + e) * 256] in LDS (my = regs + threadIdx.x), so every
-// register access of a wavefront is one conflict-free LDS instruction whatever the
-// (wave-uniform) register index. Element e has flat index elem0 + e * estride (the
-// dropout hash index). Row form (TPR > 0): the TPR threads of a row hold its elements
-// j = lane + e * TPR, bit e of `live` marks j < D of a real row, and FO_ROWSUM reduces
-// a register over the row (f64, fixed order: each thread's elements in order, a
-// wavefront butterfly, then the row's wavefronts in order through `part`).
+// Register k of a thread is N consecutive LDS words at my + k * 256 * N, where
+// my = regs + threadIdx.x * N: one 32/64/128-bit LDS access per register and thread,
+// conflict-free across a wavefront, whatever the (wave-uniform) register index.
+template <int N>
+__device__ __forceinline__ void rload(const uint32_t* p, uint32_t (&v)[N]) {
+  if constexpr (N % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < N / 4; ++i) {
+      const u32x4 t = *reinterpret_cast<const u32x4*>(p + 4 * i);
+      v[4 * i] = t[0]; v[4 * i + 1] = t[1]; v[4 * i + 2] = t[2]; v[4 * i + 3] = t[3];
+    }
+  } else if constexpr (N == 2) {
+    const u32x2 t = *reinterpret_cast<const u32x2*>(p);
+    v[0] = t[0]; v[1] = t[1];
+  } else {
+    v[0] = p[0];
+  }
+}
+template <int N>
+__device__ __forceinline__ void rstore(uint32_t* p, const uint32_t (&v)[N]) {
+  if constexpr (N % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < N / 4; ++i) {
+      u32x4 t;
+      t[0] = v[4 * i]; t[1] = v[4 * i + 1]; t[2] = v[4 * i + 2]; t[3] = v[4 * i + 3];
+      *reinterpret_cast<u32x4*>(p + 4 * i) = t;
+    }
+  } else if constexpr (N == 2) {
+    u32x2 t;
+    t[0] = v[0]; t[1] = v[1];
+    *reinterpret_cast<u32x2*>(p) = t;
+  } else {
+    p[0] = v[0];
+  }
+}
+
+// The program interpreter shared by both kernel forms. A thread owns N elements. Element
+// e has flat index elem0 + e * estride (the dropout hash index). Row form (TPR > 0): the
+// TPR threads of a row hold its elements j = lane + e * TPR, bit e of `live` marks
+// j < D of a real row, and FO_ROWSUM reduces a register over the row (f64, fixed order:
+// each thread's elements in order, a wavefront butterfly, then the row's wavefronts in
+// order through `part`).
 template <int N, int TPR>
 __device__ __forceinline__ void run_program(ConstCode code, int n_instr, uint32_t* my, uint32_t seed, uint32_t elem0,
                                             uint32_t estride, uint32_t live, double* part) {
-#define REG(k, e) my[((k) * N + (e)) * 256]
+#define R(k) (my + (k) * (256 * N))
+#define TG_UN(EXPR)                                                \
+  {                                                                \
+    uint32_t X_[N], Z_[N];                                         \
+    rload<N>(R(a), X_);                                            \
+    _Pragma("unroll") for (int e = 0; e < N; ++e) {                \
+      const uint32_t X = X_[e];                                    \
+      Z_[e] = (EXPR);                                              \
+    }                                                              \
+    rstore<N>(R(dst), Z_);                                         \
+    break;                                                         \
+  }
+#define TG_BIN(EXPR)                                               \
+  {                                                                \
+    uint32_t X_[N], Y_[N], Z_[N];                                  \
+    rload<N>(R(a), X_);                                            \
+    rload<N>(R(b), Y_);                                            \
+    _Pragma("unroll") for (int e = 0; e < N; ++e) {                \
+      const uint32_t X = X_[e], Y = Y_[e];                         \
+      Z_[e] = (EXPR);                                              \
+    }                                                              \
+    rstore<N>(R(dst), Z_);                                         \
+    break;                                                         \
+  }
   for (int q = 0; q < n_instr; ++q) {
     const int op = code[q].op, a = code[q].a, b = code[q].b, dst = code[q].dst;
     switch (op) {
-#define TG_EACH(EXPR)                                              \
-  _Pragma("unroll") for (int e = 0; e < N; ++e) {                  \
-    const uint32_t X = REG(a, e);                                  \
-    const uint32_t Y = REG(b, e);                                  \
-    (void)Y;                                                       \
-    REG(dst, e) = (EXPR);                                          \
-  }                                                                \
-  break;
       // f32 +, -, *, /: the correctly rounded f32 operation equals computing in f64 and
       // rounding once.
-      case FO_FADD: TG_EACH(fbits(bitsf(X) + bitsf(Y)))
-      case FO_FSUB: TG_EACH(fbits(bitsf(X) - bitsf(Y)))
-      case FO_FMUL: TG_EACH(fbits(bitsf(X) * bitsf(Y)))
-      case FO_FDIV: TG_EACH(fbits(bitsf(X) / bitsf(Y)))
+      case FO_FADD: TG_BIN(fbits(bitsf(X) + bitsf(Y)))
+      case FO_FSUB: TG_BIN(fbits(bitsf(X) - bitsf(Y)))
+      case FO_FMUL: TG_BIN(fbits(bitsf(X) * bitsf(Y)))
+      case FO_FDIV: TG_BIN(fbits(bitsf(X) / bitsf(Y)))
       case FO_MULS: {
         const double s = code[q].imm;
         const int ta = code[q].ta;
-        TG_EACH(fbits((float)(num(X, ta) * s)))
+        TG_UN(fbits((float)(num(X, ta) * s)))
       }
       case FO_ADDS: {
         const double s = code[q].imm;
         const int ta = code[q].ta;
-        TG_EACH(fbits((float)(num(X, ta) + s)))
+        TG_UN(fbits((float)(num(X, ta) + s)))
       }
       // f64 sqrt rounded once to f32 is the correctly rounded f32 square root.
-      case FO_SQRT: TG_EACH(fbits((float)sqrt((double)bitsf(X))))
-      case FO_NEG: TG_EACH(X ^ 0x80000000u)
-      case FO_ABS: TG_EACH(X & 0x7fffffffu)
+      case FO_SQRT: TG_UN(fbits((float)sqrt((double)bitsf(X))))
+      case FO_NEG: TG_UN(X ^ 0x80000000u)
+      case FO_ABS: TG_UN(X & 0x7fffffffu)
       // max(x, 0) with JS semantics: NaN stays NaN, -0 becomes +0.
-      case FO_RELU: TG_EACH(bitsf(X) != bitsf(X) ? 0x7fc00000u : (bitsf(X) > 0.0f ? X : 0u))
-      case FO_RELU_GRAD: TG_EACH(bitsf(X) > 0.0f ? Y : 0u)
+      case FO_RELU: TG_UN(bitsf(X) != bitsf(X) ? 0x7fc00000u : (bitsf(X) > 0.0f ? X : 0u))
+      case FO_RELU_GRAD: TG_BIN(bitsf(X) > 0.0f ? Y : 0u)
       case FO_WHERE: {
-        const int c = code[q].c;
+        uint32_t C_[N], A_[N], B_[N];
+        rload<N>(R(a), C_);
+        rload<N>(R(b), A_);
+        rload<N>(R(code[q].c), B_);
 #pragma unroll
-        for (int e = 0; e < N; ++e) REG(dst, e) = REG(a, e) != 0u ? REG(b, e) : REG(c, e);
+        for (int e = 0; e < N; ++e) A_[e] = C_[e] != 0u ? A_[e] : B_[e];
+        rstore<N>(R(dst), A_);
         break;
       }
-      case FO_COPY: TG_EACH(X)
+      case FO_COPY: TG_UN(X)
       // Frequent f64 transcendentals and dropout inline.
-      case FO_EXP: TG_EACH(fbits((float)exp((double)bitsf(X))))
-      case FO_LOG: TG_EACH(fbits((float)log((double)bitsf(X))))
-      case FO_TANH: TG_EACH(fbits((float)tanh((double)bitsf(X))))
-      case FO_ERF: TG_EACH(fbits(erf_as(bitsf(X))))
-#undef TG_EACH
+      case FO_EXP: TG_UN(fbits((float)exp((double)bitsf(X))))
+      case FO_LOG: TG_UN(fbits((float)log((double)bitsf(X))))
+      case FO_TANH: TG_UN(fbits((float)tanh((double)bitsf(X))))
+      case FO_ERF: TG_UN(fbits(erf_as(bitsf(X))))
       case FO_DROPOUT: {
         const uint32_t salt = code[q].salt;
         const double pr = code[q].imm, sc = code[q].imm2;
+        uint32_t X_[N];
+        rload<N>(R(a), X_);
 #pragma unroll
-        for (int e = 0; e < N; ++e) REG(dst, e) = dropout_bits(REG(a, e), seed, salt, pr, sc, elem0 + e * estride);
+        for (int e = 0; e < N; ++e) X_[e] = dropout_bits(X_[e], seed, salt, pr, sc, elem0 + e * estride);
+        rstore<N>(R(dst), X_);
         break;
       }
       case FO_ROWSUM: {
         if (TPR > 0) {
+          uint32_t X_[N];
+          rload<N>(R(a), X_);
           double s = 0.0;
 #pragma unroll
           for (int e = 0; e < N; ++e)
-            if ((live >> e) & 1u) s += (double)bitsf(REG(a, e));
+            if ((live >> e) & 1u) s += (double)bitsf(X_[e]);
 #pragma unroll
           for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
           if (TPR > 64) {
@@ -197,7 +255,8 @@ __device__ __forceinline__ void run_program(ConstCode code, int n_instr, uint32_
           }
           const uint32_t v = fbits((float)(s / code[q].imm));
 #pragma unroll
-          for (int e = 0; e < N; ++e) REG(dst, e) = v;
+          for (int e = 0; e < N; ++e) X_[e] = v;
+          rstore<N>(R(dst), X_);
         }
         break;
       }
@@ -206,22 +265,27 @@ __device__ __forceinline__ void run_program(ConstCode code, int n_instr, uint32_
         in.op = op; in.dst = dst; in.a = a; in.b = b; in.c = code[q].c;
         in.dt = code[q].dt; in.ta = code[q].ta; in.tb = code[q].tb; in.salt = code[q].salt;
         in.imm = code[q].imm; in.imm2 = code[q].imm2;
+        uint32_t X_[N], Y_[N];
+        rload<N>(R(a), X_);
+        rload<N>(R(b), Y_);
 #pragma unroll
-        for (int e = 0; e < N; ++e) REG(dst, e) = general_op(in, REG(a, e), REG(b, e), seed, elem0 + e * estride);
+        for (int e = 0; e < N; ++e) X_[e] = general_op(in, X_[e], Y_[e], seed, elem0 + e * estride);
+        rstore<N>(R(dst), X_);
         break;
       }
     }
   }
-#undef REG
+#undef TG_UN
+#undef TG_BIN
+#undef R
 }
 
 // Element form: thread t evaluates elements VEC*t .. VEC*t + VEC - 1 of the (row-major)
 // iteration space.
 template <int VEC>
 __global__ __launch_bounds__(256) void k_fused(const FusedProgram p, uint32_t nv) {
-  extern __shared__ uint32_t regs[];   // nregs * VEC * 256 words
-  uint32_t* const my = regs + threadIdx.x;
-#define REG(k, e) my[((k) * VEC + (e)) * 256]
+  extern __shared__ __attribute__((aligned(16))) uint32_t regs[];   // nregs * VEC * 256 words
+  uint32_t* const my = regs + threadIdx.x * VEC;
   const uint32_t seed = p.seed ? (uint32_t)*p.seed : 0u;
   const ConstCode code = (ConstCode)(uintptr_t)p.code;
   for (uint32_t t = blockIdx.x * 256u + threadIdx.x; t < nv; t += gridDim.x * 256u) {
@@ -251,18 +315,20 @@ __global__ __launch_bounds__(256) void k_fused(const FusedProgram p, uint32_t nv
           for (int d = 0; d < kMaxRank; ++d)
             if (d < p.rank) off += coord[d] * (uint32_t)p.in_strides[k][d];
         }
+        uint32_t v[VEC];
         if (VEC == 4 && (mode == FM_CONTIG || mode == FM_STRIDED_V)) {
-          const u32x4 v = *reinterpret_cast<const u32x4*>(src + off);
+          const u32x4 w = *reinterpret_cast<const u32x4*>(src + off);
 #pragma unroll
-          for (int e = 0; e < VEC; ++e) REG(k, e) = v[e];
+          for (int e = 0; e < VEC; ++e) v[e] = w[e];
         } else if (VEC == 1 || mode == FM_SCALAR || mode == FM_STRIDED_B) {
-          const uint32_t v = src[off];
+          const uint32_t w = src[off];
 #pragma unroll
-          for (int e = 0; e < VEC; ++e) REG(k, e) = v;
+          for (int e = 0; e < VEC; ++e) v[e] = w;
         } else {
 #pragma unroll
-          for (int e = 0; e < VEC; ++e) REG(k, e) = src[off + e * p.in_inner[k]];
+          for (int e = 0; e < VEC; ++e) v[e] = src[off + e * p.in_inner[k]];
         }
+        rstore<VEC>(my + k * (256 * VEC), v);
       }
     }
     run_program<VEC, 0>(code, p.n_instr, my, seed, t * VEC, 1, 0xffffffffu, nullptr);
@@ -270,39 +336,38 @@ __global__ __launch_bounds__(256) void k_fused(const FusedProgram p, uint32_t nv
     for (int k = 0; k < kFusedMaxOut; ++k) {
       if (k < p.n_out) {
         uint32_t* dstp = static_cast<uint32_t*>(p.out[k]);
-        const int reg = p.out_reg[k];
+        uint32_t v[VEC];
+        rload<VEC>(my + p.out_reg[k] * (256 * VEC), v);
         if (VEC == 4) {
-          u32x4 v;
+          u32x4 w;
 #pragma unroll
-          for (int e = 0; e < VEC; ++e) v[e] = REG(reg, e);
-          *reinterpret_cast<u32x4*>(dstp + t * VEC) = v;
+          for (int e = 0; e < VEC; ++e) w[e] = v[e];
+          *reinterpret_cast<u32x4*>(dstp + t * VEC) = w;
         } else {
-          dstp[t] = REG(reg, 0);
+          dstp[t] = v[0];
         }
       }
     }
   }
-#undef REG
 }
 
 // Row form: the iteration space is rows x D; TPR threads own a row (one wavefront as
-// launched), 256 / TPR rows per block, each thread EPT elements (j = lane + e * TPR). Operand
-// k of row r, column j is at rowoff_k(r) + j * in_inner[k], rowoff from the row's
+// launched), 256 / TPR rows per block, each thread EPT elements (j = lane + e * TPR).
+// Operand k of row r, column j is at rowoff_k(r) + j * in_inner[k], rowoff from the row's
 // coordinates over the merged row dims (p.div / p.in_strides). Outputs flagged in
 // out_row are per-row values, stored once per row at index r.
 template <int TPR, int EPT>
 __global__ __launch_bounds__(256) void k_fused_rows(const FusedProgram p, uint32_t nrows, uint32_t D) {
-  extern __shared__ uint32_t regs[];   // 4 doubles of partials, then nregs * EPT * 256 words
+  extern __shared__ __attribute__((aligned(16))) uint32_t regs[];   // 4 doubles of partials, then registers
   double* part = reinterpret_cast<double*>(regs);
-  uint32_t* const my = regs + 8 + threadIdx.x;
-#define REG(k, e) my[((k) * EPT + (e)) * 256]
+  uint32_t* const my = regs + 16 + threadIdx.x * EPT;
   constexpr int RPB = 256 / TPR;
   const uint32_t seed = p.seed ? (uint32_t)*p.seed : 0u;
   const ConstCode code = (ConstCode)(uintptr_t)p.code;
   const uint32_t lane = threadIdx.x % TPR;
-  // Every thread runs every iteration (uniform trip count), so the barriers inside
-  // FO_ROWSUM are reached by the whole block; threads of rows past the end compute on
-  // zeros and store nothing.
+  // Every thread runs every iteration (uniform trip count), so barriers inside
+  // FO_ROWSUM (TPR > 64) are reached by the whole block; threads of rows past the end
+  // compute on zeros and store nothing.
   for (uint32_t rb = blockIdx.x * RPB; rb < nrows; rb += gridDim.x * RPB) {
     const uint32_t r = rb + threadIdx.x / TPR;
     const bool live_row = r < nrows;
@@ -332,8 +397,10 @@ __global__ __launch_bounds__(256) void k_fused_rows(const FusedProgram p, uint32
         for (int d = 0; d < kMaxRank; ++d)
           if (d < p.rank) off += coord[d] * (uint32_t)p.in_strides[k][d];
         const uint32_t cs = (uint32_t)p.in_inner[k];
+        uint32_t v[EPT];
 #pragma unroll
-        for (int e = 0; e < EPT; ++e) REG(k, e) = ((live >> e) & 1u) ? src[off + (lane + e * TPR) * cs] : 0u;
+        for (int e = 0; e < EPT; ++e) v[e] = ((live >> e) & 1u) ? src[off + (lane + e * TPR) * cs] : 0u;
+        rstore<EPT>(my + k * (256 * EPT), v);
       }
     }
     run_program<EPT, TPR>(code, p.n_instr, my, seed, r * D + lane, TPR, live, part);
@@ -341,18 +408,18 @@ __global__ __launch_bounds__(256) void k_fused_rows(const FusedProgram p, uint32
     for (int k = 0; k < kFusedMaxOut; ++k) {
       if (k < p.n_out) {
         uint32_t* dstp = static_cast<uint32_t*>(p.out[k]);
-        const int reg = p.out_reg[k];
+        uint32_t v[EPT];
+        rload<EPT>(my + p.out_reg[k] * (256 * EPT), v);
         if (p.out_row[k]) {
-          if (live_row && lane == 0) dstp[r] = REG(reg, 0);
+          if (live_row && lane == 0) dstp[r] = v[0];
         } else {
 #pragma unroll
           for (int e = 0; e < EPT; ++e)
-            if ((live >> e) & 1u) dstp[r * D + lane + e * TPR] = REG(reg, e);
+            if ((live >> e) & 1u) dstp[r * D + lane + e * TPR] = v[e];
         }
       }
     }
   }
-#undef REG
 }
 
 }  // namespace
@@ -367,7 +434,7 @@ void fused(const FusedProgram& prog, int64_t n, hipStream_t st) {
     const int ept = D <= 64 ? 1 : (D <= 128 ? 2 : (D <= 256 ? 4 : (D <= 512 ? 8 : 16)));
     int64_t b = (n + 3) / 4;
     if (b > 16384) b = 16384;
-    const size_t lds = 64 + (size_t)prog.nregs * ept * 256 * 4;
+    const size_t lds = 64 + (size_t)prog.nregs * ept * 256 * 4;   // 16 words of partials first
     if (ept == 1) k_fused_rows<64, 1><<<(int)b, 256, lds, st>>>(prog, (uint32_t)n, (uint32_t)D);
     else if (ept == 2) k_fused_rows<64, 2><<<(int)b, 256, lds, st>>>(prog, (uint32_t)n, (uint32_t)D);
     else if (ept == 4) k_fused_rows<64, 4><<<(int)b, 256, lds, st>>>(prog, (uint32_t)n, (uint32_t)D);
