@@ -156,7 +156,7 @@ __device__ __forceinline__ void rstore(uint32_t* p, const uint32_t (&v)[N]) {
 // order through `part`).
 template <int N, int TPR>
 __device__ __forceinline__ void run_program(ConstCode code, int n_instr, uint32_t* my, uint32_t seed, uint32_t elem0,
-                                            uint32_t estride, uint32_t live, double* part) {
+                                            uint32_t estride, uint32_t live, double* part, uint32_t row_q = 0) {
 #define R(k) (my + (k) * (256 * N))
 #define TG_UN(EXPR)                                                \
   {                                                                \
@@ -256,6 +256,45 @@ __device__ __forceinline__ void run_program(ConstCode code, int n_instr, uint32_
           const uint32_t v = fbits((float)(s / code[q].imm));
 #pragma unroll
           for (int e = 0; e < N; ++e) X_[e] = v;
+          rstore<N>(R(dst), X_);
+        }
+        break;
+      }
+      // Row softmaxes, one wavefront per row (TPR == 64): the same arithmetic and
+      // combination order as the standalone k_softmax_causal / k_log_softmax kernels.
+      case FO_SOFTMAX_CAUSAL:
+      case FO_LOG_SOFTMAX: {
+        if (TPR == 64) {
+          const bool causal = op == FO_SOFTMAX_CAUSAL;
+          uint32_t X_[N];
+          rload<N>(R(a), X_);
+          const uint32_t lane = threadIdx.x & 63;
+          bool in_row[N];
+          float mx = -INFINITY;
+#pragma unroll
+          for (int e = 0; e < N; ++e) {
+            in_row[e] = ((live >> e) & 1u) && (!causal || lane + e * 64 <= row_q);
+            if (in_row[e]) mx = fmaxf(mx, bitsf(X_[e]));
+          }
+#pragma unroll
+          for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+          double ex[N];
+          double s = 0.0;
+#pragma unroll
+          for (int e = 0; e < N; ++e) {
+            ex[e] = in_row[e] ? exp((double)bitsf(X_[e]) - (double)mx) : 0.0;
+            if (in_row[e]) s += ex[e];
+          }
+#pragma unroll
+          for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+          if (causal) {
+#pragma unroll
+            for (int e = 0; e < N; ++e) X_[e] = in_row[e] ? fbits((float)(ex[e] / s)) : 0u;
+          } else {
+            const double ls = log(s) + (double)mx;
+#pragma unroll
+            for (int e = 0; e < N; ++e) X_[e] = fbits((float)((double)bitsf(X_[e]) - ls));
+          }
           rstore<N>(R(dst), X_);
         }
         break;
@@ -403,7 +442,7 @@ __global__ __launch_bounds__(256) void k_fused_rows(const FusedProgram p, uint32
         rstore<EPT>(my + k * (256 * EPT), v);
       }
     }
-    run_program<EPT, TPR>(code, p.n_instr, my, seed, r * D + lane, TPR, live, part);
+    run_program<EPT, TPR>(code, p.n_instr, my, seed, r * D + lane, TPR, live, part, live_row ? r % D : 0u);
 #pragma unroll
     for (int k = 0; k < kFusedMaxOut; ++k) {
       if (k < p.n_out) {

@@ -79,7 +79,9 @@ enum FusedOp {
   FO_WHERE, FO_COPY,
   FO_ADD, FO_SUB, FO_MUL, FO_DIV, FO_MIN, FO_MAX, FO_LESS, FO_GREATER,
   FO_RSQRT, FO_LOG, FO_EXP, FO_TANH, FO_SIGMOID, FO_ERF, FO_SIN, FO_COS, FO_DROPOUT,
-  FO_ROWSUM   // row form only: dst = f32(sum over the row of a, in f64, / imm)
+  FO_ROWSUM,        // row form only: dst = f32(sum over the row of a, in f64, / imm)
+  FO_SOFTMAX_CAUSAL,  // row form only: causal softmax of row q = row % D (q + 1 leading entries)
+  FO_LOG_SOFTMAX      // row form only
 };
 // Operand access modes. With several elements per thread (vec 4), a strided operand's
 // innermost stride decides how the thread's run of elements is read: FM_STRIDED_V one

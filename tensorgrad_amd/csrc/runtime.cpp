@@ -315,8 +315,10 @@ class Runtime {
   void apply_copy_writebacks(hipStream_t st);
 
   // GEMM lowering helpers
+  bool gemm_desc(int i, tgk::GemmDesc& d) const;
+  bool fold_into_producer(int perm_op, int a, int out, const std::vector<int64_t>& perm);
   bool gemm_operand(int t, int which, const Dims& op_shape, bool batched, int64_t& M, int64_t& K, int64_t& batch,
-                    int64_t& bdiv, int64_t& s0, int64_t& s1, int64_t& sr, int64_t& sc, bool transposeOk);
+                    int64_t& bdiv, int64_t& s0, int64_t& s1, int64_t& sr, int64_t& sc, bool transposeOk) const;
   void add_node(Node n) { nodes_.push_back(std::move(n)); }
   void lower_op(int i);
 };
@@ -447,6 +449,32 @@ void Runtime::analyse() {
 
 // Views: every tensor is (root storage, dims, strides). Aliasing ops inherit their
 // input's root; permutes are strided views until a consumer needs contiguous data.
+// A permute that must be materialised, applied to the fresh output of a GEMM read by
+// nothing else: let the GEMM write the permuted layout directly. The permute's output
+// becomes the storage root and the GEMM output a strided view of it, so no copy runs.
+bool Runtime::fold_into_producer(int perm_op, int a, int out, const std::vector<int64_t>& perm) {
+  const int src = T_[a].src;
+  if (src < 0 || (kinds_[src] != "matmul" && kinds_[src] != "matmul_batched")) return false;
+  if (view_[a].root != a || !view_[a].contiguous()) return false;
+  if (consumers_[a].size() != 1 || consumers_[a][0] != perm_op) return false;
+  for (int o : outputs_) if (o == a) return false;
+  for (auto& c : captures_) if (c.second == a) return false;
+  if (const tgj::Value* wbs = doc_.get("writebacks"))
+    for (const auto& w : wbs->items) if (w.at("source").i32() == a) return false;
+  const Dims cs = contiguous_strides(T_[out].shape);
+  View va{out, T_[a].shape, Dims(T_[a].shape.size(), 0)};
+  for (size_t d = 0; d < perm.size(); ++d) va.strides[perm[d]] = cs[d];
+  const View saved = view_[a];
+  view_[a] = va;
+  tgk::GemmDesc d{};
+  if (!gemm_desc(src, d)) {
+    view_[a] = saved;
+    return false;
+  }
+  view_[out] = View{out, T_[out].shape, cs};
+  return true;
+}
+
 void Runtime::compute_views() {
   const size_t n = T_.size();
   view_.resize(n);
@@ -517,6 +545,8 @@ void Runtime::compute_views() {
       } else if (v.contiguous()) {
         view_[out] = View{va.root, T_[out].shape, contiguous_strides(T_[out].shape)};
         virtual_[i] = true;
+      } else if (fold_into_producer(i, a, out, perm)) {
+        virtual_[i] = true;
       } else {
         materialize_[out] = true;
       }
@@ -528,7 +558,7 @@ void Runtime::compute_views() {
 // two-level batch decomposition. `op_shape` is the IR shape of the operand.
 bool Runtime::gemm_operand(int t, int which, const Dims& op_shape, bool batched, int64_t& R, int64_t& C,
                            int64_t& batch, int64_t& bdiv, int64_t& s0, int64_t& s1, int64_t& sr, int64_t& sc,
-                           bool) {
+                           bool) const {
   (void)which;
   const View& v = view_[t];
   const int r = (int)v.dims.size();
@@ -554,6 +584,84 @@ bool Runtime::gemm_operand(int t, int which, const Dims& op_shape, bool batched,
   if (d3.size() == 1) { bdiv = 1; s0 = s3[0]; s1 = 0; return true; }
   if (d3.size() == 2) { bdiv = d3[1]; s0 = s3[0]; s1 = s3[1]; return true; }
   return false;
+}
+
+// Shapes and element strides of matmul op i as a GemmDesc (no pointers): operands read
+// through their views (transposes and head permutes in place), the output written
+// through its view (contiguous, or a permuted layout folded in by compute_views).
+// Returns false if some view does not fit the kernel's two-level batch index.
+bool Runtime::gemm_desc(int i, tgk::GemmDesc& d) const {
+  const tgj::Value& op = O(i);
+  const bool batched = kinds_[i] == "matmul_batched";
+  const int a = op.at("a").i32(), b = op.at("b").i32(), out = op.at("out").i32();
+  const Dims& ash = T_[a].shape;
+  const Dims& bsh = T_[b].shape;
+  const int64_t M = ash[ash.size() - 2], K = ash.back(), N = bsh.back();
+  int64_t Ra, Ca, ba, bda, sa0, sa1, sar, sac;
+  int64_t Rb, Cb, bb, bdb, sb0, sb1, sbr, sbc;
+  int64_t Rc, Cc, bc, bdc, sc0, sc1, scr, scc;
+  if (!gemm_operand(a, 0, ash, batched, Ra, Ca, ba, bda, sa0, sa1, sar, sac, true)) return false;
+  if (!gemm_operand(b, 1, bsh, batched, Rb, Cb, bb, bdb, sb0, sb1, sbr, sbc, true)) return false;
+  if (!gemm_operand(out, 2, T_[out].shape, batched, Rc, Cc, bc, bdc, sc0, sc1, scr, scc, true)) return false;
+  const bool c_contig = view_[out].contiguous();
+  d = tgk::GemmDesc{};
+  d.N = N; d.K = K;
+  if (!batched) {
+    // A [..., M, K] @ B [K, N]: fold A's leading dims into M when they are uniformly
+    // strided with the rows (and C's are too); otherwise batch over them with B broadcast.
+    if (ba == 1 || (bda == 1 && sa0 == M * sar && (c_contig || (bdc == 1 && sc0 == M * scr)))) {
+      d.M = M * ba; d.batch = 1; d.bdiv = 1;
+      d.sAz0 = d.sAz1 = 0;
+      d.sCz0 = d.sCz1 = 0;
+    } else {
+      d.M = M; d.batch = ba; d.bdiv = bda;
+      d.sAz0 = sa0; d.sAz1 = sa1;
+      d.sCz0 = M * N * bda; d.sCz1 = M * N;
+    }
+    d.sAm = sar; d.sAk = sac;
+    d.sBz0 = d.sBz1 = 0; d.sBk = sbr; d.sBn = sbc;
+  } else {
+    // Batch dims of A and B must decompose identically.
+    if (ba != bb) return false;
+    d.M = M; d.batch = ba;
+    if (bda == bdb || ba == 1) {
+      d.bdiv = bda;
+      d.sAz0 = sa0; d.sAz1 = sa1; d.sBz0 = sb0; d.sBz1 = sb1;
+    } else if (bda == 1 && bdb != 1) {
+      // A collapsed to one batch dim; split it like B.
+      d.bdiv = bdb;
+      d.sAz0 = sa0 * bdb; d.sAz1 = sa0; d.sBz0 = sb0; d.sBz1 = sb1;
+    } else if (bdb == 1 && bda != 1) {
+      d.bdiv = bda;
+      d.sAz0 = sa0; d.sAz1 = sa1; d.sBz0 = sb0 * bda; d.sBz1 = sb0;
+    } else {
+      return false;
+    }
+    d.sAm = sar; d.sAk = sac; d.sBk = sbr; d.sBn = sbc;
+    d.sCz0 = M * N * d.bdiv; d.sCz1 = M * N;
+  }
+  d.sCm = N; d.sCn = 1;
+  if (!c_contig) {
+    // Output written in a permuted layout: rows / cols from its view, batch split like
+    // the operands'.
+    if (Rc != d.M || Cc != N) return false;
+    d.sCm = scr; d.sCn = scc;
+    if (d.batch > 1) {
+      if (bc != d.batch) return false;
+      if (bdc == d.bdiv) { d.sCz0 = sc0; d.sCz1 = sc1; }
+      else if (bdc == 1) { d.sCz0 = sc0 * d.bdiv; d.sCz1 = sc0; }
+      else if (d.bdiv == 1) {
+        // operands collapsed to one batch dim: split them like C
+        d.bdiv = bdc;
+        d.sAz1 = d.sAz0; d.sAz0 *= bdc;
+        d.sBz1 = d.sBz0; d.sBz0 *= bdc;
+        d.sCz0 = sc0; d.sCz1 = sc1;
+      } else {
+        return false;
+      }
+    }
+  }
+  return true;
 }
 
 void Runtime::lower() {
@@ -718,11 +826,16 @@ static int row_class(const Dims& s, const Dims& F) {
   return 0;
 }
 
-// Last-axis sums: sum_last, mean_last, and a sum_to_shape that only collapses the last
-// axis (its target is the input shape with the last dim set to 1).
+// Ops that need whole rows (row groups only): last-axis sums (sum_last, mean_last, a
+// sum_to_shape that only collapses the last axis) and the row softmaxes.
 bool Runtime::is_row_reduce(int m) const {
   const std::string& k = kinds_[m];
   if (is_row_reduce_kind(k)) return true;
+  if (k == "log_softmax_last") return true;
+  if (k == "softmax_causal_last") {
+    const Dims& in = T_[fld(m, "a")].shape;
+    return in.size() >= 2 && in[in.size() - 2] == in.back();
+  }
   if (k != "sum_to_shape") return false;
   const Dims& in = T_[fld(m, "a")].shape;
   const Dims& out = T_[O(m).at("out").i32()].shape;
@@ -781,12 +894,25 @@ Runtime::GroupPlan Runtime::plan_group(const std::vector<int>& ops, bool row, co
   for (int o : outputs_) must_store.insert(o);
   for (auto& c : captures_) must_store.insert(c.second);
   for (auto& w : copy_writebacks_) must_store.insert(w.first);
+  // A contiguous full-size view (reshape) of a member's output that only members read is
+  // read from the register, not from memory.
+  std::function<bool(int)> read_outside = [&](int t) -> bool {
+    if (must_store.count(t)) return true;
+    for (int c : consumers_[t]) {
+      if (members.count(c)) continue;
+      if (virtual_[c]) {
+        const int v = O(c).at("out").i32();
+        if (root(v) == root(t) && view_[v].contiguous() && T_[v].numel == T_[root(v)].numel && !read_outside(v))
+          continue;
+      }
+      return true;
+    }
+    return false;
+  };
   std::vector<bool> stored(ops.size(), false);
   for (size_t q = 0; q < ops.size(); ++q) {
     const int t = O(ops[q]).at("out").i32();
-    bool ext_use = must_store.count(t) > 0;
-    for (int c : consumers_[t]) if (!members.count(c)) ext_use = true;
-    if (ext_use) { stored[q] = true; gp.outs.push_back(t); }
+    if (read_outside(t)) { stored[q] = true; gp.outs.push_back(t); }
   }
   // last read of every value (ext operand index or member position)
   std::map<int, int> member_pos;   // producing op -> position
@@ -832,7 +958,11 @@ Runtime::GroupPlan Runtime::plan_group(const std::vector<int>& ops, bool row, co
     if (regs.size() > 2) in.c = regs[2];
     const int out = op.at("out").i32();
     in.dt = kdt(T_[out].dt);
-    if (is_row_reduce(m)) {
+    if (k == "softmax_causal_last") {
+      in.op = tgk::FO_SOFTMAX_CAUSAL;
+    } else if (k == "log_softmax_last") {
+      in.op = tgk::FO_LOG_SOFTMAX;
+    } else if (is_row_reduce(m)) {
       in.op = tgk::FO_ROWSUM;
       in.imm = k == "mean_last" ? (double)F.back() : 1.0;
     } else {
@@ -1474,48 +1604,8 @@ void Runtime::lower_op(int i) {
       }
     }
     rd(a); rd(b);
-    int64_t Ra, Ca, ba, bda, sa0, sa1, sar, sac;
-    int64_t Rb, Cb, bb, bdb, sb0, sb1, sbr, sbc;
-    bool okA = gemm_operand(a, 0, ash, batched, Ra, Ca, ba, bda, sa0, sa1, sar, sac, true);
-    bool okB = gemm_operand(b, 1, bsh, batched, Rb, Cb, bb, bdb, sb0, sb1, sbr, sbc, true);
     tgk::GemmDesc d{};
-    d.N = N; d.K = K;
-    if (!okA || !okB) throw Error(TG_INTERNAL, "gemm: operand view not expressible (" + n.shape + ")");
-    if (!batched) {
-      // A [..., M, K] @ B [K, N]: fold A's leading dims into M when they are uniformly
-      // strided with the rows; otherwise batch over them with B broadcast.
-      if (ba == 1 || (bda == 1 && sa0 == M * sar)) {
-        d.M = M * ba; d.batch = 1; d.bdiv = 1;
-        d.sAz0 = d.sAz1 = 0;
-        d.sCz0 = d.sCz1 = 0;
-      } else {
-        d.M = M; d.batch = ba; d.bdiv = bda;
-        d.sAz0 = sa0; d.sAz1 = sa1;
-        d.sCz0 = M * N * bda; d.sCz1 = M * N;
-      }
-      d.sAm = sar; d.sAk = sac;
-      d.sBz0 = d.sBz1 = 0; d.sBk = sbr; d.sBn = sbc;
-    } else {
-      // Batch dims of A and B must decompose identically.
-      if (ba != bb) throw Error(TG_INTERNAL, "gemm: batch mismatch");
-      d.M = M; d.batch = ba;
-      if (bda == bdb || ba == 1) {
-        d.bdiv = bda;
-        d.sAz0 = sa0; d.sAz1 = sa1; d.sBz0 = sb0; d.sBz1 = sb1;
-      } else if (bda == 1 && bdb != 1) {
-        // A collapsed to one batch dim; split it like B.
-        d.bdiv = bdb;
-        d.sAz0 = sa0 * bdb; d.sAz1 = sa0; d.sBz0 = sb0; d.sBz1 = sb1;
-      } else if (bdb == 1 && bda != 1) {
-        d.bdiv = bda;
-        d.sAz0 = sa0; d.sAz1 = sa1; d.sBz0 = sb0 * bda; d.sBz1 = sb0;
-      } else {
-        throw Error(TG_INTERNAL, "gemm: incompatible batch decompositions");
-      }
-      d.sAm = sar; d.sAk = sac; d.sBk = sbr; d.sBn = sbc;
-      d.sCz0 = M * N * d.bdiv; d.sCz1 = M * N;
-    }
-    d.sCm = N; d.sCn = 1;
+    if (!gemm_desc(i, d)) throw Error(TG_INTERNAL, "gemm: operand view not expressible (" + n.shape + ")");
     int64_t ws = tgk::gemm_workspace_floats(d);
     workspace_bytes_ = std::max(workspace_bytes_, (size_t)ws * 4);
     n.bytes = 4.0 * (T_[a].numel + T_[b].numel + to.numel);
@@ -1654,6 +1744,9 @@ void Runtime::allocate() {
       frees_at[last[t]].push_back((int)t);
   std::vector<size_t> block_size(nT, 0);   // size of the pooled block a root occupies
   for (size_t ni = 0; ni < nodes_.size(); ++ni) {
+    // Blocks of outputs nothing reads return to the pool only after every output of the
+    // node is placed: outputs of one launch must never share memory.
+    std::vector<Block> dead;
     for (int r : nodes_[ni].writes) {
       if (persistent[r] || input_roots.count(r) || placed[r]) continue;
       size_t need = align(std::max<int64_t>(4, T_[r].numel * 4));
@@ -1670,11 +1763,33 @@ void Runtime::allocate() {
         pool_end += need;
       }
       placed[r] = true;
-      if (last[r] < 0) free_list.push_back({offset[r], block_size[r]});   // dead on write
+      if (last[r] < 0) dead.push_back({offset[r], block_size[r]});
     }
+    free_list.insert(free_list.end(), dead.begin(), dead.end());
     for (int r : frees_at[ni]) free_list.push_back({offset[r], block_size[r]});
   }
   (void)pool_base;
+  // Plan-only mode (tg_plan, no device) also proves the layout: no two pooled buffers
+  // whose lifetimes (first write .. last read, in node order) meet may overlap, and no
+  // buffer is read before it is written.
+  if (plan_only_) {
+    std::vector<int> pooled;
+    for (size_t t = 0; t < nT; ++t)
+      if (placed[t] && !persistent[t] && root((int)t) == (int)t && def[t] >= 0) pooled.push_back((int)t);
+    for (size_t x = 0; x < pooled.size(); ++x)
+      for (size_t y = x + 1; y < pooled.size(); ++y) {
+        const int a = pooled[x], b = pooled[y];
+        const int la = std::max(last[a], def[a]), lb = std::max(last[b], def[b]);
+        if (la < def[b] || lb < def[a]) continue;
+        const size_t ea = offset[a] + (size_t)T_[a].numel * 4, eb = offset[b] + (size_t)T_[b].numel * 4;
+        if (ea <= offset[b] || eb <= offset[a]) continue;
+        throw Error(TG_INTERNAL, "memory plan: tensors " + std::to_string(a) + " and " + std::to_string(b) +
+                                     " are live together but overlap");
+      }
+    for (int t : pooled)
+      if (last[t] >= 0 && def[t] > last[t])
+        throw Error(TG_INTERNAL, "memory plan: tensor " + std::to_string(t) + " is read before it is written");
+  }
   arena_bytes_ = std::max<size_t>(pool_end, 256);
   // Plan-only mode lays out a fake address space so every bind can run its checks.
   char* fake = reinterpret_cast<char*>((uintptr_t)1 << 40);

@@ -201,6 +201,40 @@ def test_softmaxes_and_causal_mask():
     exact(got, want)
 
 
+CE_SHAPES = [(64, 27), (128, 10), (50, 65), (7, 130)]
+
+
+@pytest.mark.parametrize('R,D', CE_SHAPES)
+def test_cross_entropy_row_chains(R, D):
+    """The row groups of a cross-entropy forward (bias add, log-softmax, exp) and backward
+    (one-hot scaling, row sum, softmax correction), one elements per lane (D <= 64) and
+    several, against the oracle bit for bit."""
+    x = _rand([R, D], 31, -6, 6)
+    b = _rand([D], 32)
+    t = np.random.default_rng(33).integers(0, D, size=[R]).astype(np.int32)
+    g = _rand([R, 1], 34)
+    ins = {'x': x, 'b': b, 't': t, 'g': g}
+
+    def lsm():
+        return O.log_softmax(O.add(tensor_input('x', [R, D]), tensor_input('b', [D])))
+
+    got, want = run_both(lsm, ins)
+    exact(got, want)
+    got, want = run_both(lambda: O.exp(lsm()), ins)
+    exact(got, want)
+
+    def backward(e):
+        oh = O.one_hot(tensor_input('t', [R], 'i32'), D, 'f32')
+        d = O.mul(O.broadcast_to(tensor_input('g', [R, 1]), [R, D]), oh)
+        s = O.reshape(O.sum_(d, -1), [R, 1])
+        return O.sub(d, O.mul(O.broadcast_to(s, [R, D]), e))
+
+    got, want = run_both(lambda: backward(tensor_input('x', [R, D])), ins)
+    exact(got, want)
+    got, want = run_both(lambda: backward(O.exp(lsm())), ins)
+    exact(got, want)
+
+
 GEMMS = [([5, 7], [7, 3], False, False), ([2, 33, 65], [65, 17], False, False), ([129, 64], [64, 300], False, False),
          ([70, 40], [50, 40], False, True), ([40, 70], [40, 50], True, False), ([4096, 256], [4096, 256], True, False),
          ([300, 4096], [4096, 64], False, False)]
