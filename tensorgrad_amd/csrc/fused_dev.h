@@ -1,0 +1,151 @@
+// Element arithmetic of the fused groups: one definition of every opcode's bits, shared
+// by the ahead-of-time group interpreter (k_fused.hip) and the kernels generated per
+// group at run time (jit.cpp compiles them with hipRTC, which reads this file as text,
+// so it includes nothing under hipRTC and needs no host code).
+//
+// Every value is a 32-bit pattern: an f32, or an i32 (the `i32` and `bool` IR dtypes).
+// Arithmetic follows the reference evaluator (test/_eval.ts): f64 operations rounded once
+// to the result dtype, JS semantics for min / max / sign / ToInt32, and the reference's
+// erf and dropout hash. Compile with -ffp-contract=off.
+#ifndef TG_FUSED_DEV_H
+#define TG_FUSED_DEV_H
+#ifndef __HIPCC_RTC__
+#include <hip/hip_runtime.h>
+#include <cstdint>
+#include <cmath>
+#endif
+
+namespace tgk {
+
+// dtype codes for element-wise operands
+enum { DT_F32 = 0, DT_I32 = 1 };
+
+// Opcodes FO_FADD .. FO_COPY are the inexpensive forms (f32 operands and result where
+// typed); the rest are general forms (mixed i32 / f32 typing, comparisons, f64
+// transcendentals, dropout) and the row-only reductions.
+enum FusedOp {
+  FO_FADD, FO_FSUB, FO_FMUL, FO_FDIV, FO_MULS, FO_ADDS, FO_SQRT, FO_NEG, FO_ABS, FO_RELU, FO_RELU_GRAD,
+  FO_WHERE, FO_COPY,
+  FO_ADD, FO_SUB, FO_MUL, FO_DIV, FO_MIN, FO_MAX, FO_LESS, FO_GREATER,
+  FO_RSQRT, FO_LOG, FO_EXP, FO_TANH, FO_SIGMOID, FO_ERF, FO_SIN, FO_COS, FO_DROPOUT,
+  FO_ROWSUM,          // row form only: dst = f32(sum over the row of a, in f64, / imm)
+  FO_SOFTMAX_CAUSAL,  // row form only: causal softmax of row q = row % D (q + 1 leading entries)
+  FO_LOG_SOFTMAX      // row form only
+};
+
+constexpr int kFusedMaxIn = 8;
+constexpr int kFusedMaxOut = 8;
+
+// Kernel argument of a generated group kernel: operand and output base pointers, and the
+// per-step PRNG seed tensor (null without dropout). Shapes and strides are compiled in.
+struct JitArgs {
+  const void* in[kFusedMaxIn];
+  void* out[kFusedMaxOut];
+  const int* seed;
+};
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ unsigned fbits(float x) { return __float_as_uint(x); }
+__device__ __forceinline__ float bitsf(unsigned x) { return __uint_as_float(x); }
+
+__device__ __forceinline__ double js_max(double a, double b) {
+  if (isnan(a) || isnan(b)) return __longlong_as_double(0x7ff8000000000000LL);
+  if (a == 0.0 && b == 0.0) return (signbit(a) && signbit(b)) ? -0.0 : 0.0;
+  return a > b ? a : b;
+}
+__device__ __forceinline__ double js_min(double a, double b) {
+  if (isnan(a) || isnan(b)) return __longlong_as_double(0x7ff8000000000000LL);
+  if (a == 0.0 && b == 0.0) return (signbit(a) || signbit(b)) ? -0.0 : 0.0;
+  return a < b ? a : b;
+}
+__device__ __forceinline__ double js_sign(double x) {
+  if (isnan(x)) return x;
+  return x > 0 ? 1.0 : (x < 0 ? -1.0 : x);
+}
+// ECMAScript ToInt32.
+__device__ __forceinline__ int to_int32(double x) {
+  if (!isfinite(x)) return 0;
+  double m = fmod(trunc(x), 4294967296.0);
+  if (m < 0) m += 4294967296.0;
+  return (int)(unsigned)m;
+}
+// The reference's PCG-style hash with its f64 multiply-adds (products below 2^53 are exact
+// in f64; the casts take the value modulo 2^32).
+__device__ __forceinline__ unsigned pcg_f64(unsigned seed, unsigned sc, unsigned idx) {
+  unsigned h = seed ^ sc ^ idx;
+  double t = __dadd_rn(__dmul_rn((double)h, 747796405.0), 2891336453.0);
+  h = (unsigned)(unsigned long long)t;
+  unsigned x = h ^ (h >> ((h >> 28) + 4));
+  double t2 = __dmul_rn((double)x, 277803737.0);
+  h = (unsigned)(unsigned long long)t2;
+  return h ^ (h >> 22);
+}
+
+__device__ __forceinline__ double num(unsigned x, int dt) { return dt == DT_F32 ? (double)bitsf(x) : (double)(int)x; }
+__device__ __forceinline__ unsigned from_num(double v, int dt) {
+  return dt == DT_F32 ? fbits((float)v) : (unsigned)to_int32(v);
+}
+
+// Abramowitz & Stegun 7.1.26, the reference's erf (test/_eval.ts:193-198).
+__device__ __forceinline__ float erf_as(float xf) {
+  const double v = xf;
+  const double sg = js_sign(v), av = fabs(v);
+  const double t = 1.0 / (1.0 + 0.3275911 * av);
+  const double pl = t * (0.254829592 + t * (-0.284496736 + t * (1.421413741 + t * (-1.453152027 + t * 1.061405429))));
+  return (float)(sg * (1.0 - pl * exp(-av * av)));
+}
+
+// Inverted dropout of one element: keep with probability 1 - p, scaled by 1 / (1 - p)
+// (test/_eval.ts dropout; u = hash / 2^32).
+__device__ __forceinline__ unsigned dropout_bits(unsigned x, unsigned seed, unsigned salt, double p, double scale,
+                                                 unsigned elem) {
+  const unsigned hh = pcg_f64(seed, salt, elem);
+  const double u = (double)hh / 4294967296.0;
+  return fbits((float)((double)bitsf(x) * (u >= p ? scale : 0.0)));
+}
+
+// One element of opcode `op` (every opcode but FO_WHERE and the row-only ones). With a
+// constant opcode and dtypes, inlining leaves only that opcode's arithmetic.
+__device__ __forceinline__ unsigned op_eval(int op, unsigned x, unsigned y, int ta, int tb, int dt, double imm,
+                                            double imm2, unsigned salt, unsigned seed, unsigned elem) {
+  switch (op) {
+    // f32 +, -, *, /: the correctly rounded f32 operation equals computing in f64 and
+    // rounding once.
+    case FO_FADD: return fbits(bitsf(x) + bitsf(y));
+    case FO_FSUB: return fbits(bitsf(x) - bitsf(y));
+    case FO_FMUL: return fbits(bitsf(x) * bitsf(y));
+    case FO_FDIV: return fbits(bitsf(x) / bitsf(y));
+    case FO_MULS: return fbits((float)(num(x, ta) * imm));
+    case FO_ADDS: return fbits((float)(num(x, ta) + imm));
+    // f64 sqrt rounded once to f32 is the correctly rounded f32 square root.
+    case FO_SQRT: return fbits((float)sqrt((double)bitsf(x)));
+    case FO_NEG: return x ^ 0x80000000u;
+    case FO_ABS: return x & 0x7fffffffu;
+    // max(x, 0) with JS semantics: NaN stays NaN, -0 becomes +0.
+    case FO_RELU: return bitsf(x) != bitsf(x) ? 0x7fc00000u : (bitsf(x) > 0.0f ? x : 0u);
+    case FO_RELU_GRAD: return bitsf(x) > 0.0f ? y : 0u;
+    case FO_COPY: return x;
+    case FO_ADD: return from_num(num(x, ta) + num(y, tb), dt);
+    case FO_SUB: return from_num(num(x, ta) - num(y, tb), dt);
+    case FO_MUL: return from_num(num(x, ta) * num(y, tb), dt);
+    case FO_DIV: return from_num(num(x, ta) / num(y, tb), dt);
+    case FO_MIN: return from_num(js_min(num(x, ta), num(y, tb)), dt);
+    case FO_MAX: return from_num(js_max(num(x, ta), num(y, tb)), dt);
+    case FO_LESS: return num(x, ta) < num(y, tb) ? 1u : 0u;
+    case FO_GREATER: return num(x, ta) > num(y, tb) ? 1u : 0u;
+    case FO_RSQRT: return fbits((float)(1.0 / sqrt((double)bitsf(x))));
+    case FO_LOG: return fbits((float)log((double)bitsf(x)));
+    case FO_EXP: return fbits((float)exp((double)bitsf(x)));
+    case FO_TANH: return fbits((float)tanh((double)bitsf(x)));
+    case FO_SIGMOID: return fbits((float)(0.5 + 0.5 * tanh(0.5 * (double)bitsf(x))));
+    case FO_ERF: return fbits(erf_as(bitsf(x)));
+    case FO_SIN: return fbits((float)sin((double)bitsf(x)));
+    case FO_COS: return fbits((float)cos((double)bitsf(x)));
+    case FO_DROPOUT: return dropout_bits(x, seed, salt, imm, imm2, elem);
+    default: return 0u;
+  }
+}
+
+}  // namespace tgk
+
+#endif  // TG_FUSED_DEV_H

@@ -1,0 +1,338 @@
+// Generated fused-group kernels: source generation from a group program, and a
+// process-wide hipRTC compile / module cache. See jit.h.
+#include "jit.h"
+
+#include <hip/hiprtc.h>
+
+#include <cstdio>
+#include <cstdlib>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <set>
+#include <sstream>
+#include <stdexcept>
+
+namespace tgk {
+
+namespace {
+
+// fused_dev.h as text: the prelude of every hipRTC program.
+const char* const kFusedDevSource =
+#include "fused_dev_src.inc"
+    ;
+
+std::string dlit(double v) {   // exact (hexadecimal) double literal
+  char b[64];
+  snprintf(b, sizeof b, "%a", v);
+  return b;
+}
+std::string ulit(int64_t v) { return std::to_string(v) + "u"; }
+
+bool binary_op(int op) {
+  switch (op) {
+    case FO_FADD: case FO_FSUB: case FO_FMUL: case FO_FDIV: case FO_RELU_GRAD:
+    case FO_ADD: case FO_SUB: case FO_MUL: case FO_DIV: case FO_MIN: case FO_MAX: case FO_LESS: case FO_GREATER:
+      return true;
+    default:
+      return false;
+  }
+}
+
+uint64_t fnv1a(const std::string& s) {
+  uint64_t h = 1469598103934665603ull;
+  for (unsigned char c : s) { h ^= c; h *= 1099511628211ull; }
+  return h;
+}
+
+// Linear offset of operand k over coordinates c0..c{rank-1}.
+std::string offset_expr(const FusedProgram& p, int k) {
+  std::string s;
+  for (int d = 0; d < p.rank; ++d) {
+    const int64_t st = p.in_strides[k][d];
+    if (st == 0) continue;
+    if (!s.empty()) s += " + ";
+    s += "c" + std::to_string(d) + (st == 1 ? "" : " * " + ulit(st));
+  }
+  return s.empty() ? "0u" : s;
+}
+
+// Coordinates of `idx` over the iteration dims p.div[0..rank) (row-major).
+void emit_coords(std::ostringstream& o, const FusedProgram& p, const char* idx, const char* ind) {
+  o << ind << "unsigned c0";
+  for (int d = 1; d < p.rank; ++d) o << ", c" << d;
+  o << ";\n" << ind << "{\n" << ind << "  unsigned rem = " << idx << ";\n";
+  for (int d = p.rank - 1; d >= 1; --d) {
+    const std::string D = ulit(p.div[d].d);
+    o << ind << "  c" << d << " = rem % " << D << "; rem /= " << D << ";\n";
+  }
+  o << ind << "  c0 = rem;\n" << ind << "}\n";
+}
+
+}  // namespace
+
+JitKernel fused_kernel(const FusedProgram& p, const FusedInstr* code, int64_t n) {
+  const bool row = p.row_d > 0;
+  const int64_t D = p.row_d;
+  const int N = row ? (int)((D + 63) / 64) : p.vec;   // elements per thread
+  const int FULL = row ? (int)(D / 64) : N;           // row form: chunks live in every lane
+  const int REM = row ? (int)(D % 64) : 0;            // lanes live in the last chunk
+  const std::string NS = std::to_string(N);
+  const char* I = "      ";
+  bool dropout = false;
+  for (int q = 0; q < p.n_instr; ++q) dropout |= code[q].op == FO_DROPOUT;
+
+  std::ostringstream o;
+  o << "extern \"C\" __global__ void __launch_bounds__(256) @NAME@(const tgk::JitArgs A) {\n";
+  o << "  const unsigned seed = " << (dropout ? "A.seed ? (unsigned)*A.seed : 0u" : "0u") << ";\n";
+  if (row) {
+    o << "  const unsigned lane = threadIdx.x & 63u;\n";
+    o << "  for (unsigned rb = blockIdx.x * 4u; rb < " << ulit(n) << "; rb += gridDim.x * 4u) {\n";
+    o << "    const unsigned r = rb + (threadIdx.x >> 6);\n";
+    o << "    if (r < " << ulit(n) << ") {\n";   // wavefront-uniform: no lane of a wave diverges
+    emit_coords(o, p, "r", I);
+  } else {
+    o << "  for (unsigned t = blockIdx.x * 256u + threadIdx.x; t < " << ulit(n) << "; t += gridDim.x * 256u) {\n";
+    o << "    {\n";
+    if (p.any_strided) emit_coords(o, p, "t", I);
+  }
+
+  // operand loads (all issued before any arithmetic)
+  for (int k = 0; k < p.n_in; ++k) {
+    const std::string x = "x" + std::to_string(k);
+    const int64_t inner = p.in_inner[k];
+    o << I << "unsigned " << x << "[" << N << "];\n";
+    o << I << "{\n" << I << "  const unsigned* s = (const unsigned*)A.in[" << k << "];\n";
+    if (row) {
+      o << I << "  const unsigned b = " << offset_expr(p, k) << ";\n";
+      if (inner == 0) {
+        o << I << "  const unsigned w = s[b];\n";
+        for (int e = 0; e < N; ++e) o << I << "  " << x << "[" << e << "] = w;\n";
+      } else {
+        const std::string is = inner == 1 ? "" : " * " + ulit(inner);
+        for (int e = 0; e < FULL; ++e)
+          o << I << "  " << x << "[" << e << "] = s[b + (lane + " << ulit(e * 64) << ")" << is << "];\n";
+        if (REM)
+          o << I << "  " << x << "[" << FULL << "] = lane < " << ulit(REM) << " ? s[b + (lane + " << ulit(FULL * 64)
+            << ")" << is << "] : 0u;\n";
+      }
+    } else {
+      const int m = p.in_mode[k];
+      if (m == FM_CONTIG && N == 4) {
+        o << I << "  const tgk::u32x4 w = *(const tgk::u32x4*)(s + t * 4u);\n";
+        for (int e = 0; e < 4; ++e) o << I << "  " << x << "[" << e << "] = w[" << e << "];\n";
+      } else if (m == FM_CONTIG) {
+        o << I << "  " << x << "[0] = s[t];\n";
+      } else if (m == FM_SCALAR || m == FM_STRIDED_B || (m == FM_STRIDED && inner == 0)) {
+        o << I << "  const unsigned w = s[" << (m == FM_SCALAR ? std::string("0u") : offset_expr(p, k)) << "];\n";
+        for (int e = 0; e < N; ++e) o << I << "  " << x << "[" << e << "] = w;\n";
+      } else if (m == FM_STRIDED_V) {
+        o << I << "  const tgk::u32x4 w = *(const tgk::u32x4*)(s + " << offset_expr(p, k) << ");\n";
+        for (int e = 0; e < 4; ++e) o << I << "  " << x << "[" << e << "] = w[" << e << "];\n";
+      } else {
+        o << I << "  const unsigned b = " << offset_expr(p, k) << ";\n";
+        for (int e = 0; e < N; ++e)
+          o << I << "  " << x << "[" << e << "] = s[b" << (e ? " + " + ulit(e * inner) : "") << "];\n";
+      }
+    }
+    o << I << "}\n";
+  }
+
+  // program: one SSA array per instruction; reg[] maps registers to current arrays
+  std::vector<std::string> reg(64);
+  for (int k = 0; k < p.n_in; ++k) reg[k] = "x" + std::to_string(k);
+  auto R = [&](int r) -> const std::string& {
+    if (r < 0 || r >= (int)reg.size() || reg[r].empty()) throw std::runtime_error("jit: read of an unset register");
+    return reg[r];
+  };
+  const std::string elem = row ? "r * " + ulit(D) + " + lane + (unsigned)e * 64u" : "t * " + ulit(N) + " + (unsigned)e";
+  auto live = [&](int e) -> std::string {   // row form: condition for chunk e (empty = always)
+    return (row && e == FULL && REM) ? "lane < " + ulit(REM) : "";
+  };
+  for (int q = 0; q < p.n_instr; ++q) {
+    const FusedInstr& in = code[q];
+    const std::string v = "v" + std::to_string(q);
+    o << I << "unsigned " << v << "[" << N << "];\n";
+    if (in.op == FO_ROWSUM || in.op == FO_SOFTMAX_CAUSAL || in.op == FO_LOG_SOFTMAX) {
+      if (!row) throw std::runtime_error("jit: row opcode in an element group");
+      const std::string& a = R(in.a);
+      o << I << "{\n";
+      if (in.op == FO_ROWSUM) {
+        // f64, each lane's chunks in order, then a wavefront butterfly (the interpreter's order)
+        o << I << "  double s = 0.0;\n";
+        for (int e = 0; e < N; ++e) {
+          const std::string c = live(e);
+          o << I << "  " << (c.empty() ? "" : "if (" + c + ") ") << "s += (double)tgk::bitsf(" << a << "[" << e << "]);\n";
+        }
+        o << I << "  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);\n";
+        o << I << "  const unsigned w = tgk::fbits((float)(s / " << dlit(in.imm) << "));\n";
+        for (int e = 0; e < N; ++e) o << I << "  " << v << "[" << e << "] = w;\n";
+      } else {
+        const bool causal = in.op == FO_SOFTMAX_CAUSAL;
+        if (causal) o << I << "  const unsigned rq = r % " << ulit(D) << ";\n";
+        o << I << "  bool in_row[" << N << "];\n";
+        for (int e = 0; e < N; ++e) {
+          std::string c = live(e);
+          if (causal) c = (c.empty() ? "" : c + " && ") + "lane + " + ulit(e * 64) + " <= rq";
+          o << I << "  in_row[" << e << "] = " << (c.empty() ? "true" : c) << ";\n";
+        }
+        o << I << "  float mx = tgk::bitsf(0xff800000u);\n";
+        o << I << "#pragma unroll\n" << I << "  for (int e = 0; e < " << N << "; ++e)\n"
+          << I << "    if (in_row[e]) mx = fmaxf(mx, tgk::bitsf(" << a << "[e]));\n";
+        o << I << "  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));\n";
+        o << I << "  double ex[" << N << "];\n" << I << "  double s = 0.0;\n";
+        o << I << "#pragma unroll\n" << I << "  for (int e = 0; e < " << N << "; ++e) {\n"
+          << I << "    ex[e] = in_row[e] ? exp((double)tgk::bitsf(" << a << "[e]) - (double)mx) : 0.0;\n"
+          << I << "    if (in_row[e]) s += ex[e];\n" << I << "  }\n";
+        o << I << "  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);\n";
+        if (causal) {
+          o << I << "#pragma unroll\n" << I << "  for (int e = 0; e < " << N << "; ++e) " << v
+            << "[e] = in_row[e] ? tgk::fbits((float)(ex[e] / s)) : 0u;\n";
+        } else {
+          o << I << "  const double ls = log(s) + (double)mx;\n";
+          o << I << "#pragma unroll\n" << I << "  for (int e = 0; e < " << N << "; ++e) " << v
+            << "[e] = tgk::fbits((float)((double)tgk::bitsf(" << a << "[e]) - ls));\n";
+        }
+      }
+      o << I << "}\n";
+    } else if (in.op == FO_WHERE) {
+      o << I << "#pragma unroll\n" << I << "for (int e = 0; e < " << N << "; ++e) " << v << "[e] = " << R(in.a)
+        << "[e] != 0u ? " << R(in.b) << "[e] : " << R(in.c) << "[e];\n";
+    } else {
+      const std::string b = binary_op(in.op) ? R(in.b) + "[e]" : std::string("0u");
+      o << I << "#pragma unroll\n" << I << "for (int e = 0; e < " << N << "; ++e) " << v << "[e] = tgk::op_eval("
+        << in.op << ", " << R(in.a) << "[e], " << b << ", " << in.ta << ", " << in.tb << ", " << in.dt << ", "
+        << dlit(in.imm) << ", " << dlit(in.imm2) << ", " << in.salt << "u, seed, "
+        << (in.op == FO_DROPOUT ? elem : std::string("0u")) << ");\n";
+    }
+    if (in.dst < 0 || in.dst >= (int)reg.size()) throw std::runtime_error("jit: register out of range");
+    reg[in.dst] = v;
+  }
+
+  // stores
+  for (int k = 0; k < p.n_out; ++k) {
+    const std::string& v = R(p.out_reg[k]);
+    o << I << "{\n" << I << "  unsigned* d = (unsigned*)A.out[" << k << "];\n";
+    if (row && p.out_row[k]) {
+      o << I << "  if (lane == 0u) d[r] = " << v << "[0];\n";
+    } else if (row) {
+      o << I << "  const unsigned b = r * " << ulit(D) << " + lane;\n";
+      for (int e = 0; e < N; ++e) {
+        const std::string c = live(e);
+        o << I << "  " << (c.empty() ? "" : "if (" + c + ") ") << "d[b + " << ulit(e * 64) << "] = " << v << "["
+          << e << "];\n";
+      }
+    } else if (N == 4) {
+      o << I << "  *(tgk::u32x4*)(d + t * 4u) = (tgk::u32x4){" << v << "[0], " << v << "[1], " << v << "[2], " << v
+        << "[3]};\n";
+    } else {
+      o << I << "  d[t] = " << v << "[0];\n";
+    }
+    o << I << "}\n";
+  }
+  o << "    }\n  }\n}\n";
+
+  JitKernel k;
+  std::string body = o.str();
+  char nm[32];
+  snprintf(nm, sizeof nm, "tg_%016llx", (unsigned long long)fnv1a(body));
+  k.name = nm;
+  k.body = body.replace(body.find("@NAME@"), 6, k.name);
+  const int64_t blocks = row ? (n + 3) / 4 : (n + 255) / 256;
+  k.grid = blocks < 16384 ? blocks : 16384;
+  return k;
+}
+
+namespace {
+
+struct Cache {
+  std::mutex mu;
+  std::map<std::string, std::shared_ptr<std::vector<char>>> code_of;   // name -> code object holding it
+  std::map<std::pair<int, const std::vector<char>*>, hipModule_t> modules;
+  std::map<std::pair<int, std::string>, hipFunction_t> fns;
+};
+Cache& cache() {
+  static Cache* c = new Cache();   // never destroyed: modules live until the process ends
+  return *c;
+}
+
+std::shared_ptr<std::vector<char>> compile_program(const std::string& src) {
+  hiprtcProgram prog;
+  if (hiprtcCreateProgram(&prog, src.c_str(), "tg_fused.hip", 0, nullptr, nullptr) != HIPRTC_SUCCESS)
+    throw std::runtime_error("hipRTC: cannot create program");
+  const char* opts[] = {"--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off",
+                        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"};
+  const hiprtcResult rc = hiprtcCompileProgram(prog, (int)(sizeof opts / sizeof opts[0]), opts);
+  if (rc != HIPRTC_SUCCESS) {
+    size_t n = 0;
+    hiprtcGetProgramLogSize(prog, &n);
+    std::string log(n, '\0');
+    if (n) hiprtcGetProgramLog(prog, &log[0]);
+    hiprtcDestroyProgram(&prog);
+    throw std::runtime_error(std::string("hipRTC compile failed: ") + hiprtcGetErrorString(rc) + "\n" + log.substr(0, 4000));
+  }
+  size_t n = 0;
+  hiprtcGetCodeSize(prog, &n);
+  auto code = std::make_shared<std::vector<char>>(n);
+  hiprtcGetCode(prog, code->data());
+  hiprtcDestroyProgram(&prog);
+  return code;
+}
+
+}  // namespace
+
+void jit_compile(const std::vector<JitKernel>& ks, bool load) {
+  Cache& c = cache();
+  std::lock_guard<std::mutex> lock(c.mu);
+  std::string src = kFusedDevSource;
+  std::vector<std::string> fresh;
+  std::set<std::string> seen;
+  for (const auto& k : ks) {
+    if (c.code_of.count(k.name) || !seen.insert(k.name).second) continue;
+    fresh.push_back(k.name);
+    src += "\n" + k.body;
+  }
+  if (!fresh.empty()) {
+    // TG_JIT_DUMP=<file>: append each compiled program's source (for inspection).
+    if (const char* path = std::getenv("TG_JIT_DUMP")) {
+      if (FILE* f = fopen(path, "a")) {
+        fputs(src.c_str(), f);
+        fclose(f);
+      }
+    }
+    auto code = compile_program(src);
+    for (const auto& nm : fresh) c.code_of[nm] = code;
+  }
+  if (!load) return;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) throw std::runtime_error("jit: no current HIP device");
+  for (const auto& k : ks) {
+    const auto key = std::make_pair(dev, k.name);
+    if (c.fns.count(key)) continue;
+    const std::vector<char>* code = c.code_of.at(k.name).get();
+    auto mk = std::make_pair(dev, code);
+    auto it = c.modules.find(mk);
+    if (it == c.modules.end()) {
+      hipModule_t m;
+      const hipError_t e = hipModuleLoadData(&m, code->data());
+      if (e != hipSuccess) throw std::runtime_error(std::string("hipModuleLoadData: ") + hipGetErrorString(e));
+      it = c.modules.emplace(mk, m).first;
+    }
+    hipFunction_t f;
+    const hipError_t e = hipModuleGetFunction(&f, it->second, k.name.c_str());
+    if (e != hipSuccess) throw std::runtime_error("hipModuleGetFunction(" + k.name + "): " + hipGetErrorString(e));
+    c.fns[key] = f;
+  }
+}
+
+hipFunction_t jit_function(const std::string& name) {
+  Cache& c = cache();
+  std::lock_guard<std::mutex> lock(c.mu);
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) throw std::runtime_error("jit: no current HIP device");
+  auto it = c.fns.find(std::make_pair(dev, name));
+  if (it == c.fns.end()) throw std::runtime_error("jit: kernel " + name + " is not loaded");
+  return it->second;
+}
+
+}  // namespace tgk

@@ -16,99 +16,13 @@
 namespace tgk {
 namespace {
 
-__device__ __forceinline__ double js_max(double a, double b) {
-  if (isnan(a) || isnan(b)) return __longlong_as_double(0x7ff8000000000000LL);
-  if (a == 0.0 && b == 0.0) return (signbit(a) && signbit(b)) ? -0.0 : 0.0;
-  return a > b ? a : b;
-}
-__device__ __forceinline__ double js_min(double a, double b) {
-  if (isnan(a) || isnan(b)) return __longlong_as_double(0x7ff8000000000000LL);
-  if (a == 0.0 && b == 0.0) return (signbit(a) || signbit(b)) ? -0.0 : 0.0;
-  return a < b ? a : b;
-}
-__device__ __forceinline__ double js_sign(double x) {
-  if (isnan(x)) return x;
-  return x > 0 ? 1.0 : (x < 0 ? -1.0 : x);
-}
-__device__ __forceinline__ int32_t to_int32(double x) {
-  if (!isfinite(x)) return 0;
-  double m = fmod(trunc(x), 4294967296.0);
-  if (m < 0) m += 4294967296.0;
-  return (int32_t)(uint32_t)m;
-}
-__device__ __forceinline__ double round_to(double x, int dt) {
-  return dt == DT_F32 ? (double)(float)x : (double)to_int32(x);
-}
-__device__ __forceinline__ uint32_t pcg_f64(uint32_t seed, uint32_t sc, uint32_t idx) {
-  uint32_t h = seed ^ sc ^ idx;
-  double t = __dadd_rn(__dmul_rn((double)h, 747796405.0), 2891336453.0);
-  h = (uint32_t)(unsigned long long)t;
-  uint32_t x = h ^ (h >> ((h >> 28) + 4));
-  double t2 = __dmul_rn((double)x, 277803737.0);
-  h = (uint32_t)(unsigned long long)t2;
-  return h ^ (h >> 22);
-}
-
-__device__ __forceinline__ uint32_t fbits(float x) { return __float_as_uint(x); }
-__device__ __forceinline__ float bitsf(uint32_t x) { return __uint_as_float(x); }
-__device__ __forceinline__ double num(uint32_t x, int dt) { return dt == DT_F32 ? (double)bitsf(x) : (double)(int32_t)x; }
-__device__ __forceinline__ uint32_t from_num(double v, int dt) {
-  return dt == DT_F32 ? fbits((float)v) : (uint32_t)to_int32(v);
-}
-
-// Abramowitz & Stegun 7.1.26, the reference's erf (test/_eval.ts:193-198).
-__device__ __forceinline__ float erf_as(float xf) {
-  const double v = xf;
-  const double sg = js_sign(v), av = fabs(v);
-  const double t = 1.0 / (1.0 + 0.3275911 * av);
-  const double pl = t * (0.254829592 + t * (-0.284496736 + t * (1.421413741 + t * (-1.453152027 + t * 1.061405429))));
-  return (float)(sg * (1.0 - pl * exp(-av * av)));
-}
-
-__device__ __forceinline__ uint32_t dropout_bits(uint32_t x, uint32_t seed, uint32_t salt, double p, double scale,
-                                                 uint32_t elem) {
-  const uint32_t hh = pcg_f64(seed, salt, elem);
-  const double u = (double)hh / 4294967296.0;
-  return fbits((float)((double)bitsf(x) * (u >= p ? scale : 0.0)));
-}
-
-// General forms: one element. Kept out of line so the kernel body stays small.
+// General forms: one element through op_eval, kept out of line so the interpreter's body
+// stays small.
 __device__ __noinline__ uint32_t general_op(const FusedInstr in, uint32_t x, uint32_t y, uint32_t seed,
-                                               uint32_t elem) {
-  const int ta = in.ta, tb = in.tb;
-  switch (in.op) {
-    case FO_ADD: return from_num(num(x, ta) + num(y, tb), in.dt);
-    case FO_SUB: return from_num(num(x, ta) - num(y, tb), in.dt);
-    case FO_MUL: return from_num(num(x, ta) * num(y, tb), in.dt);
-    case FO_DIV: return from_num(num(x, ta) / num(y, tb), in.dt);
-    case FO_MIN: return from_num(js_min(num(x, ta), num(y, tb)), in.dt);
-    case FO_MAX: return from_num(js_max(num(x, ta), num(y, tb)), in.dt);
-    case FO_LESS: return num(x, ta) < num(y, tb) ? 1u : 0u;
-    case FO_GREATER: return num(x, ta) > num(y, tb) ? 1u : 0u;
-    case FO_RSQRT: return fbits((float)(1.0 / sqrt((double)bitsf(x))));
-    case FO_LOG: return fbits((float)log((double)bitsf(x)));
-    case FO_EXP: return fbits((float)exp((double)bitsf(x)));
-    case FO_TANH: return fbits((float)tanh((double)bitsf(x)));
-    case FO_SIGMOID: return fbits((float)(0.5 + 0.5 * tanh(0.5 * (double)bitsf(x))));
-    case FO_ERF: {
-      // Abramowitz & Stegun 7.1.26, the reference's erf (test/_eval.ts:193-198).
-      const double v = bitsf(x);
-      const double sg = js_sign(v), av = fabs(v);
-      const double t = 1.0 / (1.0 + 0.3275911 * av);
-      const double pl = t * (0.254829592 + t * (-0.284496736 + t * (1.421413741 + t * (-1.453152027 + t * 1.061405429))));
-      return fbits((float)(sg * (1.0 - pl * exp(-av * av))));
-    }
-    case FO_SIN: return fbits((float)sin((double)bitsf(x)));
-    case FO_COS: return fbits((float)cos((double)bitsf(x)));
-    default: {   // FO_DROPOUT
-      const uint32_t hh = pcg_f64(seed, in.salt, elem);
-      const double u = (double)hh / 4294967296.0;
-      return fbits((float)((double)bitsf(x) * (u >= in.imm ? in.imm2 : 0.0)));
-    }
-  }
+                                            uint32_t elem) {
+  return op_eval(in.op, x, y, in.ta, in.tb, in.dt, in.imm, in.imm2, in.salt, seed, elem);
 }
 
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef const __attribute__((address_space(4))) FusedInstr* ConstCode;
 
@@ -184,29 +98,26 @@ __device__ __forceinline__ void run_program(ConstCode code, int n_instr, uint32_
   for (int q = 0; q < n_instr; ++q) {
     const int op = code[q].op, a = code[q].a, b = code[q].b, dst = code[q].dst;
     switch (op) {
-      // f32 +, -, *, /: the correctly rounded f32 operation equals computing in f64 and
-      // rounding once.
-      case FO_FADD: TG_BIN(fbits(bitsf(X) + bitsf(Y)))
-      case FO_FSUB: TG_BIN(fbits(bitsf(X) - bitsf(Y)))
-      case FO_FMUL: TG_BIN(fbits(bitsf(X) * bitsf(Y)))
-      case FO_FDIV: TG_BIN(fbits(bitsf(X) / bitsf(Y)))
+      // Inexpensive and frequent opcodes inline (constant opcode), the rest out of line.
+      case FO_FADD: TG_BIN(op_eval(FO_FADD, X, Y, DT_F32, DT_F32, DT_F32, 0.0, 0.0, 0u, 0u, 0u))
+      case FO_FSUB: TG_BIN(op_eval(FO_FSUB, X, Y, DT_F32, DT_F32, DT_F32, 0.0, 0.0, 0u, 0u, 0u))
+      case FO_FMUL: TG_BIN(op_eval(FO_FMUL, X, Y, DT_F32, DT_F32, DT_F32, 0.0, 0.0, 0u, 0u, 0u))
+      case FO_FDIV: TG_BIN(op_eval(FO_FDIV, X, Y, DT_F32, DT_F32, DT_F32, 0.0, 0.0, 0u, 0u, 0u))
       case FO_MULS: {
         const double s = code[q].imm;
         const int ta = code[q].ta;
-        TG_UN(fbits((float)(num(X, ta) * s)))
+        TG_UN(op_eval(FO_MULS, X, 0u, ta, DT_F32, DT_F32, s, 0.0, 0u, 0u, 0u))
       }
       case FO_ADDS: {
         const double s = code[q].imm;
         const int ta = code[q].ta;
-        TG_UN(fbits((float)(num(X, ta) + s)))
+        TG_UN(op_eval(FO_ADDS, X, 0u, ta, DT_F32, DT_F32, s, 0.0, 0u, 0u, 0u))
       }
-      // f64 sqrt rounded once to f32 is the correctly rounded f32 square root.
-      case FO_SQRT: TG_UN(fbits((float)sqrt((double)bitsf(X))))
-      case FO_NEG: TG_UN(X ^ 0x80000000u)
-      case FO_ABS: TG_UN(X & 0x7fffffffu)
-      // max(x, 0) with JS semantics: NaN stays NaN, -0 becomes +0.
-      case FO_RELU: TG_UN(bitsf(X) != bitsf(X) ? 0x7fc00000u : (bitsf(X) > 0.0f ? X : 0u))
-      case FO_RELU_GRAD: TG_BIN(bitsf(X) > 0.0f ? Y : 0u)
+      case FO_SQRT: TG_UN(op_eval(FO_SQRT, X, 0u, DT_F32, DT_F32, DT_F32, 0.0, 0.0, 0u, 0u, 0u))
+      case FO_NEG: TG_UN(op_eval(FO_NEG, X, 0u, DT_F32, DT_F32, DT_F32, 0.0, 0.0, 0u, 0u, 0u))
+      case FO_ABS: TG_UN(op_eval(FO_ABS, X, 0u, DT_F32, DT_F32, DT_F32, 0.0, 0.0, 0u, 0u, 0u))
+      case FO_RELU: TG_UN(op_eval(FO_RELU, X, 0u, DT_F32, DT_F32, DT_F32, 0.0, 0.0, 0u, 0u, 0u))
+      case FO_RELU_GRAD: TG_BIN(op_eval(FO_RELU_GRAD, X, Y, DT_F32, DT_F32, DT_F32, 0.0, 0.0, 0u, 0u, 0u))
       case FO_WHERE: {
         uint32_t C_[N], A_[N], B_[N];
         rload<N>(R(a), C_);
@@ -217,12 +128,12 @@ __device__ __forceinline__ void run_program(ConstCode code, int n_instr, uint32_
         rstore<N>(R(dst), A_);
         break;
       }
-      case FO_COPY: TG_UN(X)
+      case FO_COPY: TG_UN(op_eval(FO_COPY, X, 0u, DT_F32, DT_F32, DT_F32, 0.0, 0.0, 0u, 0u, 0u))
       // Frequent f64 transcendentals and dropout inline.
-      case FO_EXP: TG_UN(fbits((float)exp((double)bitsf(X))))
-      case FO_LOG: TG_UN(fbits((float)log((double)bitsf(X))))
-      case FO_TANH: TG_UN(fbits((float)tanh((double)bitsf(X))))
-      case FO_ERF: TG_UN(fbits(erf_as(bitsf(X))))
+      case FO_EXP: TG_UN(op_eval(FO_EXP, X, 0u, DT_F32, DT_F32, DT_F32, 0.0, 0.0, 0u, 0u, 0u))
+      case FO_LOG: TG_UN(op_eval(FO_LOG, X, 0u, DT_F32, DT_F32, DT_F32, 0.0, 0.0, 0u, 0u, 0u))
+      case FO_TANH: TG_UN(op_eval(FO_TANH, X, 0u, DT_F32, DT_F32, DT_F32, 0.0, 0.0, 0u, 0u, 0u))
+      case FO_ERF: TG_UN(op_eval(FO_ERF, X, 0u, DT_F32, DT_F32, DT_F32, 0.0, 0.0, 0u, 0u, 0u))
       case FO_DROPOUT: {
         const uint32_t salt = code[q].salt;
         const double pr = code[q].imm, sc = code[q].imm2;

@@ -5,12 +5,11 @@
 #include <hip/hip_runtime.h>
 #include <cstdint>
 
+#include "fused_dev.h"
+
 namespace tgk {
 
 constexpr int kMaxRank = 8;
-
-// dtype codes for element-wise operands
-enum { DT_F32 = 0, DT_I32 = 1 };
 
 // Division by a runtime constant d >= 1 for 0 <= x < 2^31 without a divide instruction:
 // q = (umulhi(x, m) + x) >> s with s = ceil(log2 d), m = floor(2^32 (2^s - d) / d) + 1
@@ -68,21 +67,7 @@ void categorical(const float* a, int32_t* out, int64_t outer, int64_t D, const i
 
 // ---- fused element-wise groups (k_fused.hip) ------------------------------------------
 constexpr int kFusedRegs = 16;
-constexpr int kFusedMaxIn = 8;
-constexpr int kFusedMaxOut = 8;
 constexpr int kFusedMaxInstr = 64;
-// Opcodes FO_FADD .. FO_COPY are the inexpensive forms (f32 operands and result where
-// typed) evaluated unrolled over a thread's elements; the rest are general forms (mixed
-// i32 / f32 typing, comparisons, f64 transcendentals, dropout).
-enum FusedOp {
-  FO_FADD, FO_FSUB, FO_FMUL, FO_FDIV, FO_MULS, FO_ADDS, FO_SQRT, FO_NEG, FO_ABS, FO_RELU, FO_RELU_GRAD,
-  FO_WHERE, FO_COPY,
-  FO_ADD, FO_SUB, FO_MUL, FO_DIV, FO_MIN, FO_MAX, FO_LESS, FO_GREATER,
-  FO_RSQRT, FO_LOG, FO_EXP, FO_TANH, FO_SIGMOID, FO_ERF, FO_SIN, FO_COS, FO_DROPOUT,
-  FO_ROWSUM,        // row form only: dst = f32(sum over the row of a, in f64, / imm)
-  FO_SOFTMAX_CAUSAL,  // row form only: causal softmax of row q = row % D (q + 1 leading entries)
-  FO_LOG_SOFTMAX      // row form only
-};
 // Operand access modes. With several elements per thread (vec 4), a strided operand's
 // innermost stride decides how the thread's run of elements is read: FM_STRIDED_V one
 // 128-bit load (innermost stride 1, 16-byte aligned), FM_STRIDED_B one load shared by

@@ -40,6 +40,7 @@
 
 #include "../../include/tg.h"
 #include "json.hpp"
+#include "jit.h"
 #include "kernels.h"
 
 namespace tg {
@@ -267,6 +268,18 @@ class Runtime {
   std::deque<tgk::FusedProgram> programs_;     // kernel-argument images (stable addresses)
   std::vector<tgk::FusedInstr> fused_code_;    // all groups' instructions, uploaded once
   tgk::FusedInstr* fused_code_dev_ = nullptr;
+  // Fused groups run as kernels generated per group (default) or, with TG_FUSED=vm in
+  // the environment, through the interpreter kernels of k_fused.hip.
+  bool use_jit_ = true;
+  struct JitSlot {
+    std::string name;
+    hipFunction_t fn = nullptr;
+    tgk::JitArgs args{};
+    int64_t grid = 0;
+  };
+  std::deque<JitSlot> jit_slots_;
+  std::vector<tgk::JitKernel> jit_pending_;
+  void jit_finish();
   void form_groups();
   void lower_group(int gi);
 
@@ -327,6 +340,7 @@ class Runtime {
 
 Runtime::Runtime(const char* json, Runtime* par, bool plan_only) : parent(par) {
   if (const char* g = std::getenv("TG_GRAPH")) use_graph_ = std::string(g) != "0";
+  if (const char* g = std::getenv("TG_FUSED")) use_jit_ = std::string(g) != "vm";
   if (const char* g = std::getenv("TG_STREAMS")) nstreams_ = std::max(1, std::min(kStreams, std::atoi(g)));
   try {
     doc_ = tgj::parse(json);
@@ -370,6 +384,7 @@ Runtime::Runtime(const char* json, Runtime* par, bool plan_only) : parent(par) {
   allocate();
   schedule();
   bind_all();   // in plan-only mode this still runs every launch's host-side bounds proof
+  jit_finish();
   prepare_streams();
 }
 
@@ -1227,7 +1242,23 @@ void Runtime::lower_group(int gi) {
     p.n_instr = (int)gp.code.size();
     p.code = fused_code_dev_ + code_off;
     const int64_t nthreads = row ? cnt / F.back() : cnt / p.vec;
-    return [this, slot, nthreads](hipStream_t st) { tgk::fused(programs_[slot], nthreads, st); };
+    if (!use_jit_) return [this, slot, nthreads](hipStream_t st) { tgk::fused(programs_[slot], nthreads, st); };
+    tgk::JitKernel jk = tgk::fused_kernel(p, fused_code_.data() + code_off, nthreads);
+    const size_t js = jit_slots_.size();
+    jit_slots_.emplace_back();
+    JitSlot& sl = jit_slots_.back();
+    sl.name = jk.name;
+    sl.grid = jk.grid;
+    for (int k = 0; k < p.n_in; ++k) sl.args.in[k] = p.in[k];
+    for (int k = 0; k < p.n_out; ++k) sl.args.out[k] = p.out[k];
+    sl.args.seed = p.seed;
+    jit_pending_.push_back(std::move(jk));
+    return [this, js](hipStream_t st) {
+      JitSlot& j = jit_slots_[js];
+      void* params[] = {&j.args};
+      const hipError_t e = hipModuleLaunchKernel(j.fn, (unsigned)j.grid, 1, 1, 256, 1, 1, 0, st, params, nullptr);
+      if (e != hipSuccess) throw Error(TG_DEVICE_ERROR, std::string("fused group launch: ") + hipGetErrorString(e));
+    };
   };
   add_node(std::move(n));
 }
@@ -1853,6 +1884,20 @@ void Runtime::allocate() {
     state_roots_.push_back(t);
   }
   hip_check(hipStreamSynchronize(stream_), "hipStreamSynchronize");
+}
+
+// Compile the generated group kernels (once per process; plan-only mode compiles them
+// too, which proves they build, but loads nothing) and resolve each launch's function.
+void Runtime::jit_finish() {
+  if (jit_pending_.empty()) return;
+  try {
+    tgk::jit_compile(jit_pending_, !plan_only_);
+    if (!plan_only_)
+      for (auto& s : jit_slots_) s.fn = tgk::jit_function(s.name);
+  } catch (const std::runtime_error& e) {
+    throw Error(TG_INTERNAL, e.what());
+  }
+  jit_pending_.clear();
 }
 
 void Runtime::bind_all() {
