@@ -263,6 +263,18 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g) {
 // to the last row (their results are never stored).
 constexpr int kLdsBlock = 256;   // floats one wavefront-wide DMA writes (1 KiB)
 
+// One wavefront-wide global_load_lds_dwordx4: lane l's 16 bytes from gp land at
+// lds + 16 l. Issued from inline assembly so the compiler does not treat it as an LDS
+// write of unknown extent: for such writes it drains every outstanding load before the
+// next LDS read, which would expose the full load latency at every pipeline stage. The
+// kernel orders LDS reads itself (explicit vmcnt waits and barriers). M0 takes the
+// wave-uniform LDS base; one wait state separates the M0 write from the load.
+__device__ __forceinline__ void dma16(const float* gp, float* lds) {
+  const uint32_t base =
+      __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)lds);
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gp), "{m0}"(base));
+}
+
 template <int ROWS, int BK, bool KFAST>
 struct DTile {
   static constexpr int CPR = KFAST ? BK / 4 : ROWS / 4;   // 16-byte chunks per LDS row
@@ -294,7 +306,7 @@ struct DTile {
         const int64_t gr = min(r0 + c * 4, rlim - 4);
         gp = X + (k0 + row) * sk + gr;
       }
-      __builtin_amdgcn_global_load_lds(gp, (__attribute__((address_space(3))) void*)(L + inst * kLdsBlock), 16, 0, 0);
+      dma16(gp, L + inst * kLdsBlock);
     }
   }
 
