@@ -36,6 +36,7 @@
 #include "kernels.h"
 
 #include <stdexcept>
+#include <cstdlib>
 
 namespace tgk {
 namespace {
@@ -387,7 +388,8 @@ __global__ __launch_bounds__(kThreads) void k_gemm_dma(GemmArgs g) {
   for (int st = 0; st < nst; ++st) {
     // Stage st has landed once at most (stages issued after it) * PER loads are pending.
     const int after = min(NS - 2, nst - 1 - st);
-    if (NS >= 4 && after >= 2) wait_vmcnt<(NS >= 4 ? 2 : 0) * PER>();
+    if (NS >= 5 && after >= 3) wait_vmcnt<(NS >= 5 ? 3 : 0) * PER>();
+    else if (NS >= 4 && after >= 2) wait_vmcnt<(NS >= 4 ? 2 : 0) * PER>();
     else if (NS >= 3 && after >= 1) wait_vmcnt<PER>();
     else wait_vmcnt<0>();
     // A bare workgroup barrier: __syncthreads() would also drain every outstanding load
@@ -482,10 +484,12 @@ __global__ void k_splitk_reduce(const float* __restrict__ work, int splits, int6
 }
 
 struct Plan { int bm, bn, bk, splits; int64_t kps; };
+static int dbg_ns() { static int v = getenv("TG_GEMM_NS") ? atoi(getenv("TG_GEMM_NS")) : 3; return v; }   // DBGTEMP
+static int dbg_bk() { static int v = getenv("TG_GEMM_BK") ? atoi(getenv("TG_GEMM_BK")) : 64; return v; }   // DBGTEMP
 
 Plan plan_for(const GemmDesc& d) {
   auto tiles = [&](int bm, int bn) { return ((d.M + bm - 1) / bm) * ((d.N + bn - 1) / bn) * d.batch; };
-  Plan p{64, 64, 64, 1, d.K};
+  Plan p{64, 64, dbg_bk(), 1, d.K};
   if (tiles(128, 128) >= 256) p = Plan{128, 128, 32, 1, d.K};
   else if (tiles(128, 64) >= 256) p = Plan{128, 64, 32, 1, d.K};
   else if (tiles(64, 128) >= 256) p = Plan{64, 128, 32, 1, d.K};
@@ -545,16 +549,18 @@ void gemm(const GemmDesc& d, float* work, hipStream_t st) {
   const bool ak = d.sAk == 1;
   const bool bk = d.sBk == 1 && d.sBn != 1;
   if (dma_ok(d, p, ak, bk)) {
-#define TG_DMA_LAUNCH(BM_, BN_, BK_)                                                           \
+#define TG_DMA_LAUNCH3(BM_, BN_, BK_, NS_)                                                           \
   do {                                                                                       \
-    if (ak && bk) k_gemm_dma<BM_, BN_, BK_, 3, true, true><<<grid, kThreads, 0, st>>>(g);     \
-    else if (ak) k_gemm_dma<BM_, BN_, BK_, 3, true, false><<<grid, kThreads, 0, st>>>(g);     \
-    else if (bk) k_gemm_dma<BM_, BN_, BK_, 3, false, true><<<grid, kThreads, 0, st>>>(g);     \
-    else k_gemm_dma<BM_, BN_, BK_, 3, false, false><<<grid, kThreads, 0, st>>>(g);            \
+    if (ak && bk) k_gemm_dma<BM_, BN_, BK_, NS_, true, true><<<grid, kThreads, 0, st>>>(g);     \
+    else if (ak) k_gemm_dma<BM_, BN_, BK_, NS_, true, false><<<grid, kThreads, 0, st>>>(g);     \
+    else if (bk) k_gemm_dma<BM_, BN_, BK_, NS_, false, true><<<grid, kThreads, 0, st>>>(g);     \
+    else k_gemm_dma<BM_, BN_, BK_, NS_, false, false><<<grid, kThreads, 0, st>>>(g);            \
   } while (0)
+#define TG_DMA_LAUNCH(BM_, BN_, BK_) do { if (dbg_ns() == 4) TG_DMA_LAUNCH3(BM_, BN_, BK_, 4); else if (dbg_ns() == 5) TG_DMA_LAUNCH3(BM_, BN_, BK_, 5); else TG_DMA_LAUNCH3(BM_, BN_, BK_, 3); } while (0)
     if (p.bm == 128 && p.bn == 128) TG_DMA_LAUNCH(128, 128, 32);
     else if (p.bm == 128) TG_DMA_LAUNCH(128, 64, 32);
     else if (p.bn == 128) TG_DMA_LAUNCH(64, 128, 32);
+    else if (p.bk == 32) TG_DMA_LAUNCH(64, 64, 32);
     else TG_DMA_LAUNCH(64, 64, 64);
 #undef TG_DMA_LAUNCH
   } else {

@@ -258,6 +258,100 @@ __global__ void k_sum_finish(const double* __restrict__ part, float* __restrict_
   }
 }
 
+// Column sums in one launch: out[c] = f32(sum_r a[r * rs + c] / div), c < C, r < R.
+// Block (x, y) takes columns [64x, 64x + 64) and rows [y chunk, (y + 1) chunk): lane l of
+// wave w sums column 64x + l over rows y chunk + w, + 4, ... in order (f64), and the
+// four waves combine in order through LDS into the block's partial. The last block of a
+// column block to finish (counted on counters[x]) adds the chunk partials in a fixed
+// tree (wave w takes chunks w, w + 4, ... in order, then waves in order) and resets its
+// counter, so results do not depend on scheduling and the launch leaves every counter
+// at zero for the next one.
+__global__ __launch_bounds__(256) void k_colsum(const float* __restrict__ a, int64_t C, int64_t R, int64_t rs,
+                                                int64_t chunk, int nchunks, double* __restrict__ part,
+                                                unsigned* __restrict__ counters, float* __restrict__ out,
+                                                double div) {
+  __shared__ double red[4][64];
+  __shared__ int last;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t c = (int64_t)blockIdx.x * 64 + lane;
+  const int y = blockIdx.y;
+  const int64_t r0 = (int64_t)y * chunk, r1 = min(R, r0 + chunk);
+  double s = 0.0;
+  if (c < C) {
+    const float* p = a + c;
+    int64_t r = r0 + w;
+    for (; r + 60 < r1; r += 64) {   // sixteen rows in flight, added in row order
+      float v[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) v[u] = p[(r + 4 * u) * rs];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) s += (double)v[u];
+    }
+    for (; r < r1; r += 4) s += (double)p[r * rs];
+  }
+  red[w][lane] = s;
+  __syncthreads();
+  const double bs = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
+  if (nchunks == 1) {
+    if (w == 0 && c < C) out[c] = (float)(bs / div);
+    return;
+  }
+  // Partials, the counter and the final reads are device-scope atomic accesses: coherent
+  // across the XCDs' separate L2 caches without a full L2 write-back (which a device-scope
+  // fence costs). Each wave's partial stores complete (vmcnt) before the block counts in.
+  if (w == 0 && c < C) __hip_atomic_store(&part[(int64_t)y * C + c], bs, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0)
+    last = __hip_atomic_fetch_add(&counters[blockIdx.x], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+           (unsigned)(nchunks - 1);
+  __syncthreads();
+  if (!last) return;
+  auto ld = [&](int q) { return __hip_atomic_load(&part[(int64_t)q * C + c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+  double t = 0.0;
+  if (c < C) {
+    int q = w;
+    for (; q + 60 < nchunks; q += 64) {
+      double v[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) v[u] = ld(q + 4 * u);
+#pragma unroll
+      for (int u = 0; u < 16; ++u) t += v[u];
+    }
+    double v[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) v[u] = q + 4 * u < nchunks ? ld(q + 4 * u) : 0.0;
+#pragma unroll
+    for (int u = 0; u < 16; ++u)
+      if (q + 4 * u < nchunks) t += v[u];
+  }
+  red[w][lane] = t;
+  __syncthreads();
+  if (w == 0 && c < C) out[c] = (float)((((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane]) / div);
+  if (threadIdx.x == 0) __hip_atomic_store(&counters[blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Column-kernel shape: 64-column blocks and chunks of 64 rows (one round of sixteen loads
+// in flight per lane), more rows per chunk only past 256 chunks; fewer chunks when the
+// column blocks alone fill the chip.
+struct ColPlan { int64_t nx; int64_t chunk; int nchunks; };
+bool col_form(const Strided& cells, const Strided& red) {
+  return cells.rank == 1 && cells.s0[0] == 1 && red.rank == 1;
+}
+ColPlan col_plan(int64_t C, int64_t R) {
+  ColPlan p;
+  p.nx = (C + 63) / 64;
+  int64_t want = (512 + p.nx - 1) / p.nx;
+  int64_t n = (R + 63) / 64;
+  if (n > want) n = want;
+  if (n > 256) n = 256;
+  if (n < 1) n = 1;
+  p.chunk = (R + n - 1) / n;
+  p.nchunks = (int)((R + p.chunk - 1) / p.chunk);
+  if (p.nchunks < 1) p.nchunks = 1;
+  return p;
+}
+
 struct SumPlan { bool cols; int64_t chunk; int nchunks; };
 
 SumPlan sum_plan(const Strided& cells, int64_t ncells, int64_t nred) {
@@ -309,14 +403,30 @@ void softmax_causal(const float* a, float* out, int64_t mats, int64_t D, hipStre
   TG_ROW_LAUNCH(k_softmax_causal, rows, a, out, rows, D);
 }
 
-int64_t sum_workspace_doubles(const Strided& cells, int64_t ncells, int64_t nred) {
+int64_t sum_workspace_doubles(const Strided& cells, const Strided& red, int64_t ncells, int64_t nred) {
+  if (col_form(cells, red)) {
+    ColPlan c = col_plan(ncells, nred);
+    return c.nchunks > 1 ? ncells * c.nchunks : 0;
+  }
   SumPlan p = sum_plan(cells, ncells, nred);
   return p.nchunks > 1 ? ncells * p.nchunks : 0;
 }
 
+int64_t sum_counters(const Strided& cells, const Strided& red, int64_t ncells, int64_t nred) {
+  if (!col_form(cells, red)) return 0;
+  ColPlan c = col_plan(ncells, nred);
+  return c.nchunks > 1 ? c.nx : 0;
+}
+
 void reduce_sum(const float* a, float* out, const Strided& cells, const Strided& red, int64_t ncells, int64_t nred,
-                double div, double* work, hipStream_t st) {
+                double div, double* work, unsigned* counters, hipStream_t st) {
   if (ncells <= 0) return;
+  if (col_form(cells, red)) {
+    ColPlan c = col_plan(ncells, nred);
+    dim3 grid((unsigned)c.nx, (unsigned)c.nchunks);
+    k_colsum<<<grid, 256, 0, st>>>(a, ncells, nred, red.s0[0], c.chunk, c.nchunks, work, counters, out, div);
+    return;
+  }
   SumPlan p = sum_plan(cells, ncells, nred);
   if (p.cols) {
     dim3 grid((unsigned)((ncells + 255) / 256), (unsigned)p.nchunks);

@@ -110,10 +110,12 @@ void fused(const FusedProgram& prog, int64_t n, hipStream_t st);
 // red(r)] / div) for c < ncells, r < nred. `cells` / `red` carry dims and element
 // strides in s0. Used for sum_last / mean_last (red = last axis) and for the
 // un-broadcast sums of autograd (sum_to_shape). `work` must hold
-// sum_workspace_doubles(...) doubles of partials.
-int64_t sum_workspace_doubles(const Strided& cells, int64_t ncells, int64_t nred);
+// sum_workspace_doubles(...) doubles of partials and `counters` sum_counters(...) zeroed
+// counters of its own (a launch leaves them zero again).
+int64_t sum_workspace_doubles(const Strided& cells, const Strided& red, int64_t ncells, int64_t nred);
+int64_t sum_counters(const Strided& cells, const Strided& red, int64_t ncells, int64_t nred);
 void reduce_sum(const float* a, float* out, const Strided& cells, const Strided& red, int64_t ncells, int64_t nred,
-                double div, double* work, hipStream_t st);
+                double div, double* work, unsigned* counters, hipStream_t st);
 void row_argmax(const float* a, int32_t* out, int64_t outer, int64_t D, hipStream_t st);
 void log_softmax(const float* a, float* out, int64_t outer, int64_t D, hipStream_t st);
 void softmax_causal(const float* a, float* out, int64_t mats, int64_t D, hipStream_t st);

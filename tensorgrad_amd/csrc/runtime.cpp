@@ -232,6 +232,15 @@ class Runtime {
   float* loss_host_ = nullptr;      // pinned
   float* workspace_ = nullptr;
   size_t workspace_bytes_ = 0;
+  // Launch-completion counters (zeroed once; every kernel that counts on them leaves them
+  // zero). Nodes reserve slots while lowering.
+  int64_t counter_slots_ = 0;
+  unsigned* counters_ = nullptr;
+  int64_t take_counters(int64_t n) {
+    const int64_t b = counter_slots_;
+    counter_slots_ += n;
+    return b;
+  }
   // fused Adam tables (device)
   tgk::AdamTensor* adam_tensors_ = nullptr;
   int64_t* adam_chunk_tensor_ = nullptr;
@@ -399,6 +408,7 @@ Runtime::~Runtime() {
   if (arena_) hipFree(arena_);
   if (input_region_) hipFree(input_region_);
   if (workspace_ && !plan_only_) hipFree(workspace_);
+  if (counters_ && !plan_only_) hipFree(counters_);
   if (fused_code_dev_ && !plan_only_) hipFree(fused_code_dev_);
   if (adam_tensors_) hipFree(adam_tensors_);
   if (adam_chunk_tensor_) hipFree(adam_chunk_tensor_);
@@ -1458,14 +1468,18 @@ void Runtime::lower_op(int i) {
     tgk::Strided cells{}, red{};
     cells.rank = 1; cells.dims[0] = outer; cells.s0[0] = D;
     red.rank = 1; red.dims[0] = D; red.s0[0] = 1;
-    if (k == "mean_last" || k == "sum_last")
-      workspace_bytes_ = std::max(workspace_bytes_, (size_t)tgk::sum_workspace_doubles(cells, outer, D) * 8);
+    int64_t cbase = 0;
+    if (k == "mean_last" || k == "sum_last") {
+      workspace_bytes_ = std::max(workspace_bytes_, (size_t)tgk::sum_workspace_doubles(cells, red, outer, D) * 8);
+      cbase = take_counters(tgk::sum_counters(cells, red, outer, D));
+    }
     n.bind = [=]() -> std::function<void(hipStream_t)> {
       const float* pa = (const float*)dptr(a); void* po = dptr(out);
       if (k == "mean_last" || k == "sum_last") {
         double div = k == "mean_last" ? (double)D : 1.0;
         double* w = (double*)cur_ws_;
-        return [=](hipStream_t st) { tgk::reduce_sum(pa, (float*)po, cells, red, outer, D, div, w, st); };
+        unsigned* cn = counters_ + cbase;
+        return [=](hipStream_t st) { tgk::reduce_sum(pa, (float*)po, cells, red, outer, D, div, w, cn, st); };
       }
       if (k == "argmax_last") return [=](hipStream_t st) { tgk::row_argmax(pa, (int32_t*)po, outer, D, st); };
       if (k == "log_softmax_last") return [=](hipStream_t st) { tgk::log_softmax(pa, (float*)po, outer, D, st); };
@@ -1569,7 +1583,8 @@ void Runtime::lower_op(int i) {
     tgk::Strided red = make_strided(rdd, rs, {}, {});
     int64_t ncells = prod(cd), nred = prod(rdd);
     if (ncells != to.numel) throw Error(TG_INTERNAL, "sum_to_shape: cell count mismatch");
-    workspace_bytes_ = std::max(workspace_bytes_, (size_t)tgk::sum_workspace_doubles(cells, ncells, nred) * 8);
+    workspace_bytes_ = std::max(workspace_bytes_, (size_t)tgk::sum_workspace_doubles(cells, red, ncells, nred) * 8);
+    const int64_t cbase = take_counters(tgk::sum_counters(cells, red, ncells, nred));
     n.bind = [=]() -> std::function<void(hipStream_t)> {
       {
         int64_t dd[2 * tgk::kMaxRank], ss[2 * tgk::kMaxRank];
@@ -1580,7 +1595,8 @@ void Runtime::lower_op(int i) {
       }
       const float* pa = (const float*)dptr(a); float* po = (float*)dptr(out);
       double* w = (double*)cur_ws_;
-      return [=](hipStream_t st) { tgk::reduce_sum(pa, po, cells, red, ncells, nred, 1.0, w, st); };
+      unsigned* cn = counters_ + cbase;
+      return [=](hipStream_t st) { tgk::reduce_sum(pa, po, cells, red, ncells, nred, 1.0, w, cn, st); };
     };
   } else if (k == "matmul" || k == "matmul_batched") {
     int a = op.at("a").i32(), b = op.at("b").i32();
@@ -1858,6 +1874,7 @@ void Runtime::allocate() {
     input_region_ = fake + arena_bytes_ + 4096;
     for (int t : input_roots) ptr_[t] = input_region_ + input_offset_[t];
     workspace_ = reinterpret_cast<float*>(input_region_ + input_region_bytes_ + 4096);
+    counters_ = reinterpret_cast<unsigned*>(fake + ((uintptr_t)1 << 39));
     arena_ = nullptr;
     input_region_ = nullptr;
     return;
@@ -1869,6 +1886,10 @@ void Runtime::allocate() {
   hip_check(hipHostMalloc(&loss_host_, 256, hipHostMallocDefault), "hipHostMalloc");
   ws_stride_ = (workspace_bytes_ + 255) & ~(size_t)255;
   if (workspace_bytes_) hip_check(hipMalloc(&workspace_, ws_stride_ * nstreams_), "hipMalloc(workspace)");
+  if (counter_slots_) {
+    hip_check(hipMalloc(&counters_, counter_slots_ * sizeof(unsigned)), "hipMalloc(counters)");
+    hip_check(hipMemset(counters_, 0, counter_slots_ * sizeof(unsigned)), "hipMemset(counters)");
+  }
   if (!fused_code_.empty()) {
     const size_t cb = fused_code_.size() * sizeof(tgk::FusedInstr);
     hip_check(hipMalloc(&fused_code_dev_, cb), "hipMalloc(fused code)");

@@ -150,7 +150,8 @@ def test_argmax_ties_and_nan_semantics():
 
 
 @pytest.mark.parametrize('cells', [([4, 3, 5], [3, 1]), ([6, 5], [5]), ([2, 3, 4, 5], [1, 3, 1, 1]),
-                                   ([65536, 4], [4]), ([1000], []), ([128, 64, 24, 24], [1, 64, 1, 1])])
+                                   ([65536, 4], [4]), ([1000], []), ([128, 64, 24, 24], [1, 64, 1, 1]),
+                                   ([4096, 256], [256]), ([3000, 70], [70]), ([32, 128, 256], [128, 256])])
 def test_sum_to_shape(cells):
     src, dst = cells
     x = _rand(src, 8)
@@ -166,6 +167,29 @@ def test_sum_to_shape(cells):
     n = np.prod(src) // max(1, np.prod(dst))
     bound = n * 6e-8 * np.max(np.abs(np.cumsum(np.moveaxis(xs, axes, range(len(axes))).reshape(n, -1), 0)))
     assert np.max(np.abs(got.astype(np.float64) - want)) <= bound + 1e-7
+
+
+def test_column_sums_repeat_bit_identical():
+    """Multi-block column sums count their blocks on device counters that each launch
+    leaves at zero: repeated runs of one runtime (two reductions per run) give the same
+    bits, equal to the f64 sums rounded once."""
+    x = _rand([4096, 256], 21)
+    y = _rand([1000, 1030], 22)
+
+    def build():
+        a = O.sum_to_shape(tensor_input('x', [4096, 256]), [256])
+        b = O.sum_to_shape(tensor_input('y', [1000, 1030]), [1030])
+        return O.add(O.sum_(a), O.sum_(b))
+
+    g = trace_fn(build)
+    rt = backend.NativeRuntime(IR.dumps(wire(g)))
+    outs = [rt.run({'x': x, 'y': y}, [], np.float32) for _ in range(3)]
+    rt.destroy()
+    for r in outs[1:]:
+        exact(r, outs[0])
+    want = np.float32(x.astype(np.float64).sum(0).astype(np.float32).astype(np.float64).sum()
+                      + y.astype(np.float64).sum(0).astype(np.float32).astype(np.float64).sum())
+    assert abs(float(outs[0]) - float(want)) <= 1e-6 * abs(float(want)) + 1e-6
 
 
 def test_broadcast_permute_slice_concat_scatter():
