@@ -44,6 +44,7 @@ struct JitArgs {
   const int* seed;
 };
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ unsigned fbits(float x) { return __float_as_uint(x); }
 __device__ __forceinline__ float bitsf(unsigned x) { return __uint_as_float(x); }

@@ -74,11 +74,29 @@ void emit_coords(std::ostringstream& o, const FusedProgram& p, const char* idx, 
 JitKernel fused_kernel(const FusedProgram& p, const FusedInstr* code, int64_t n) {
   const bool row = p.row_d > 0;
   const int64_t D = p.row_d;
-  const int N = row ? (int)((D + 63) / 64) : p.vec;   // elements per thread
-  const int FULL = row ? (int)(D / 64) : N;           // row form: chunks live in every lane
-  const int REM = row ? (int)(D % 64) : 0;            // lanes live in the last chunk
-  const std::string NS = std::to_string(N);
+  // Row form: one wavefront per row; lane l owns chunks j = 0 .. J-1 of V consecutive
+  // columns, (l + 64 j) V .. (l + 64 j) V + V - 1, so every chunk is one V-wide access and
+  // a wavefront's accesses of a chunk cover 256 V contiguous bytes.
+  int V = 1;
+  if (row && D % 4 == 0 && D >= 256) V = 4;
+  else if (row && D % 2 == 0 && D >= 128) V = 2;
+  const int J = row ? (int)((D + 64 * V - 1) / (64 * V)) : 0;
+  const int N = row ? J * V : p.vec;   // elements per thread
   const char* I = "      ";
+  // chunk j is live in lanes below this bound (-1: in every lane)
+  auto chunk_lanes = [&](int j) -> int64_t {
+    return (int64_t)64 * (j + 1) * V <= D ? -1 : (D + V - 1) / V - (int64_t)64 * j;
+  };
+  auto live = [&](int e) -> std::string {   // row form: condition for element e (empty = always)
+    if (!row) return "";
+    const int64_t l = chunk_lanes(e / V);
+    return l < 0 ? "" : "lane < " + ulit(l);
+  };
+  auto col = [&](int e) -> std::string {   // row form: column of element e
+    const int64_t c0 = (int64_t)64 * (e / V) * V + e % V;
+    return (V == 1 ? std::string("lane") : "lane * " + ulit(V)) + (c0 ? " + " + ulit(c0) : std::string());
+  };
+  const char* vt = V == 4 ? "tgk::u32x4" : "tgk::u32x2";
   bool dropout = false;
   for (int q = 0; q < p.n_instr; ++q) dropout |= code[q].op == FO_DROPOUT;
 
@@ -105,16 +123,27 @@ JitKernel fused_kernel(const FusedProgram& p, const FusedInstr* code, int64_t n)
     o << I << "{\n" << I << "  const unsigned* s = (const unsigned*)A.in[" << k << "];\n";
     if (row) {
       o << I << "  const unsigned b = " << offset_expr(p, k) << ";\n";
+      bool vec = V > 1 && inner == 1;
+      for (int d = 0; d < p.rank; ++d) vec = vec && p.in_strides[k][d] % V == 0;
       if (inner == 0) {
         o << I << "  const unsigned w = s[b];\n";
         for (int e = 0; e < N; ++e) o << I << "  " << x << "[" << e << "] = w;\n";
+      } else if (vec) {
+        for (int j = 0; j < J; ++j) {
+          const std::string c = live(j * V);
+          o << I << "  {\n" << I << "    " << vt << " w = {};\n";
+          o << I << "    " << (c.empty() ? "" : "if (" + c + ") ") << "w = *(const " << vt << "*)(s + b + " << col(j * V)
+            << ");\n";
+          for (int u = 0; u < V; ++u) o << I << "    " << x << "[" << j * V + u << "] = w[" << u << "];\n";
+          o << I << "  }\n";
+        }
       } else {
         const std::string is = inner == 1 ? "" : " * " + ulit(inner);
-        for (int e = 0; e < FULL; ++e)
-          o << I << "  " << x << "[" << e << "] = s[b + (lane + " << ulit(e * 64) << ")" << is << "];\n";
-        if (REM)
-          o << I << "  " << x << "[" << FULL << "] = lane < " << ulit(REM) << " ? s[b + (lane + " << ulit(FULL * 64)
-            << ")" << is << "] : 0u;\n";
+        for (int e = 0; e < N; ++e) {
+          const std::string c = live(e);
+          const std::string ld = "s[b + (" + col(e) + ")" + is + "]";
+          o << I << "  " << x << "[" << e << "] = " << (c.empty() ? ld : c + " ? " + ld + " : 0u") << ";\n";
+        }
       }
     } else {
       const int m = p.in_mode[k];
@@ -145,10 +174,9 @@ JitKernel fused_kernel(const FusedProgram& p, const FusedInstr* code, int64_t n)
     if (r < 0 || r >= (int)reg.size() || reg[r].empty()) throw std::runtime_error("jit: read of an unset register");
     return reg[r];
   };
-  const std::string elem = row ? "r * " + ulit(D) + " + lane + (unsigned)e * 64u" : "t * " + ulit(N) + " + (unsigned)e";
-  auto live = [&](int e) -> std::string {   // row form: condition for chunk e (empty = always)
-    return (row && e == FULL && REM) ? "lane < " + ulit(REM) : "";
-  };
+  const std::string elem = row ? "r * " + ulit(D) + " + (lane + 64u * (unsigned)(e / " + std::to_string(V) + ")) * " +
+                                     ulit(V) + " + (unsigned)(e % " + std::to_string(V) + ")"
+                               : "t * " + ulit(N) + " + (unsigned)e";
   for (int q = 0; q < p.n_instr; ++q) {
     const FusedInstr& in = code[q];
     const std::string v = "v" + std::to_string(q);
@@ -173,7 +201,7 @@ JitKernel fused_kernel(const FusedProgram& p, const FusedInstr* code, int64_t n)
         o << I << "  bool in_row[" << N << "];\n";
         for (int e = 0; e < N; ++e) {
           std::string c = live(e);
-          if (causal) c = (c.empty() ? "" : c + " && ") + "lane + " + ulit(e * 64) + " <= rq";
+          if (causal) c = (c.empty() ? "" : c + " && ") + "(" + col(e) + ") <= rq";
           o << I << "  in_row[" << e << "] = " << (c.empty() ? "true" : c) << ";\n";
         }
         o << I << "  float mx = tgk::bitsf(0xff800000u);\n";
@@ -216,11 +244,21 @@ JitKernel fused_kernel(const FusedProgram& p, const FusedInstr* code, int64_t n)
     if (row && p.out_row[k]) {
       o << I << "  if (lane == 0u) d[r] = " << v << "[0];\n";
     } else if (row) {
-      o << I << "  const unsigned b = r * " << ulit(D) << " + lane;\n";
-      for (int e = 0; e < N; ++e) {
-        const std::string c = live(e);
-        o << I << "  " << (c.empty() ? "" : "if (" + c + ") ") << "d[b + " << ulit(e * 64) << "] = " << v << "["
-          << e << "];\n";
+      o << I << "  const unsigned b = r * " << ulit(D) << ";\n";
+      if (V > 1) {
+        for (int j = 0; j < J; ++j) {
+          const std::string c = live(j * V);
+          o << I << "  " << (c.empty() ? "" : "if (" + c + ") ") << "*(" << vt << "*)(d + b + " << col(j * V) << ") = ("
+            << vt << "){";
+          for (int u = 0; u < V; ++u) o << (u ? ", " : "") << v << "[" << j * V + u << "]";
+          o << "};\n";
+        }
+      } else {
+        for (int e = 0; e < N; ++e) {
+          const std::string c = live(e);
+          o << I << "  " << (c.empty() ? "" : "if (" + c + ") ") << "d[b + " << col(e) << "] = " << v << "[" << e
+            << "];\n";
+        }
       }
     } else if (N == 4) {
       o << I << "  *(tgk::u32x4*)(d + t * 4u) = (tgk::u32x4){" << v << "[0], " << v << "[1], " << v << "[2], " << v

@@ -23,7 +23,6 @@ __device__ __noinline__ uint32_t general_op(const FusedInstr in, uint32_t x, uin
   return op_eval(in.op, x, y, in.ta, in.tb, in.dt, in.imm, in.imm2, in.salt, seed, elem);
 }
 
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef const __attribute__((address_space(4))) FusedInstr* ConstCode;
 
 // Register k of a thread is N consecutive LDS words at my + k * 256 * N, where

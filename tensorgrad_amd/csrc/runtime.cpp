@@ -475,25 +475,57 @@ void Runtime::analyse() {
 // Views: every tensor is (root storage, dims, strides). Aliasing ops inherit their
 // input's root; permutes are strided views until a consumer needs contiguous data.
 // A permute that must be materialised, applied to the fresh output of a GEMM read by
-// nothing else: let the GEMM write the permuted layout directly. The permute's output
-// becomes the storage root and the GEMM output a strided view of it, so no copy runs.
+// nothing else (directly, or through one permuting view that is itself read only by this
+// permute): let the GEMM write the permuted layout directly. The permute's output becomes
+// the storage root and the GEMM output a strided view of it, so no copy runs.
 bool Runtime::fold_into_producer(int perm_op, int a, int out, const std::vector<int64_t>& perm) {
-  const int src = T_[a].src;
+  const int g = view_[a].root;
+  const int src = T_[g].src;
   if (src < 0 || (kinds_[src] != "matmul" && kinds_[src] != "matmul_batched")) return false;
-  if (view_[a].root != a || !view_[a].contiguous()) return false;
+  if (O(src).at("out").i32() != g || !view_[g].contiguous() || view_[g].root != g) return false;
   if (consumers_[a].size() != 1 || consumers_[a][0] != perm_op) return false;
-  for (int o : outputs_) if (o == a) return false;
-  for (auto& c : captures_) if (c.second == a) return false;
-  if (const tgj::Value* wbs = doc_.get("writebacks"))
-    for (const auto& w : wbs->items) if (w.at("source").i32() == a) return false;
+  auto pinned = [&](int t) {
+    for (int o : outputs_) if (o == t) return true;
+    for (auto& c : captures_) if (c.second == t) return true;
+    if (const tgj::Value* wbs = doc_.get("writebacks"))
+      for (const auto& w : wbs->items) if (w.at("source").i32() == t) return true;
+    return false;
+  };
+  if (pinned(a) || pinned(g)) return false;
+  // a == g, or a is a permutation view of g: each dim of a is one dim of g.
+  const Dims cg = contiguous_strides(T_[g].shape);
+  std::vector<int> dim_of_g(T_[a].shape.size(), -1);   // a's dim e -> g's dim
+  if (a != g) {
+    if (consumers_[g].size() != 1 || kinds_[consumers_[g][0]] != "permute" ||
+        O(consumers_[g][0]).at("out").i32() != a)
+      return false;
+    const View& v = view_[a];
+    if (v.dims.size() != T_[g].shape.size()) return false;
+    std::vector<bool> used(cg.size(), false);
+    for (size_t e = 0; e < v.dims.size(); ++e) {
+      for (size_t q = 0; q < cg.size(); ++q)
+        if (!used[q] && T_[g].shape[q] == v.dims[e] && (cg[q] == v.strides[e] || v.dims[e] == 1)) {
+          used[q] = true;
+          dim_of_g[e] = (int)q;
+          break;
+        }
+      if (dim_of_g[e] < 0) return false;
+    }
+  } else {
+    for (size_t e = 0; e < dim_of_g.size(); ++e) dim_of_g[e] = (int)e;
+  }
   const Dims cs = contiguous_strides(T_[out].shape);
   View va{out, T_[a].shape, Dims(T_[a].shape.size(), 0)};
   for (size_t d = 0; d < perm.size(); ++d) va.strides[perm[d]] = cs[d];
-  const View saved = view_[a];
+  View vg{out, T_[g].shape, Dims(T_[g].shape.size(), 0)};
+  for (size_t e = 0; e < dim_of_g.size(); ++e) vg.strides[dim_of_g[e]] = va.strides[e];
+  const View saved_g = view_[g], saved_a = view_[a];
+  view_[g] = vg;
   view_[a] = va;
   tgk::GemmDesc d{};
   if (!gemm_desc(src, d)) {
-    view_[a] = saved;
+    view_[g] = saved_g;
+    view_[a] = saved_a;
     return false;
   }
   view_[out] = View{out, T_[out].shape, cs};

@@ -212,6 +212,24 @@ def test_broadcast_permute_slice_concat_scatter():
     exact(got, want)
 
 
+@pytest.mark.parametrize('T', [128, 300])
+def test_row_groups_wide_rows(T):
+    """Row-fused groups with two or four columns per lane access (D = 128, and 300 with a
+    partly live last chunk): causal softmax with dropout, and a row chain reading one
+    operand through a transposed view (scalar accesses at vector-layout columns)."""
+    x = _rand([2, T, T], 51, -4, 4)
+    got, want = run_both(lambda: O.dropout(O.softmax_causal(O.mul(tensor_input('x', [2, T, T]), 0.125)), 0.1),
+                         {'x': x})
+    exact(got, want)
+    a, bt = _rand([7, T], 52), _rand([T, 7], 53)
+
+    def chain():
+        t = O.mul(tensor_input('a', [7, T]), O.permute(tensor_input('b', [T, 7]), [1, 0]))
+        return O.sub(t, O.mean(t, -1, keep_dims=True))
+    got, want = run_both(chain, {'a': a, 'b': bt})
+    near(got, want)
+
+
 def test_softmaxes_and_causal_mask():
     x = _rand([3, 2, 17, 17], 12, -5, 5)
     got, want = run_both(lambda: O.softmax_causal(tensor_input('x', [3, 2, 17, 17])), {'x': x})
