@@ -331,6 +331,35 @@ __global__ __launch_bounds__(256) void k_colsum(const float* __restrict__ a, int
   if (threadIdx.x == 0) __hip_atomic_store(&counters[blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Few cells with up to 64K terms each: one 256-thread block per cell. Thread t sums terms
+// t, t + 256, ... in order (sixteen loads in flight), then the wavefronts' butterflies
+// and the four wavefront sums in order combine them; one launch, deterministic.
+__global__ __launch_bounds__(256) void k_sum_block(const float* __restrict__ a, Strided cells, Strided red,
+                                                   int64_t nred, float* __restrict__ out, double div) {
+  __shared__ double ws[4];
+  const int64_t c = blockIdx.x;
+  const int64_t base = red_offset(cells, c);
+  const int64_t st = red.s0[0];
+  const float* p = a + base;
+  double s = 0.0;
+  int64_t r = threadIdx.x;
+  for (; r + 15 * 256 < nred; r += 16 * 256) {
+    float v[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) v[u] = p[(r + u * 256) * st];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) s += (double)v[u];
+  }
+  for (; r < nred; r += 256) s += (double)p[r * st];
+  s = wave_sum(s);
+  if ((threadIdx.x & 63) == 0) ws[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) out[c] = (float)((((ws[0] + ws[1]) + ws[2]) + ws[3]) / div);
+}
+bool block_form(const Strided& red, int64_t ncells, int64_t nred) {
+  return red.rank == 1 && ncells <= 64 && nred <= 65536;
+}
+
 // Column-kernel shape: 64-column blocks and chunks of 64 rows (one round of sixteen loads
 // in flight per lane), more rows per chunk only past 256 chunks; fewer chunks when the
 // column blocks alone fill the chip.
@@ -404,6 +433,7 @@ void softmax_causal(const float* a, float* out, int64_t mats, int64_t D, hipStre
 }
 
 int64_t sum_workspace_doubles(const Strided& cells, const Strided& red, int64_t ncells, int64_t nred) {
+  if (!col_form(cells, red) && block_form(red, ncells, nred)) return 0;
   if (col_form(cells, red)) {
     ColPlan c = col_plan(ncells, nred);
     return c.nchunks > 1 ? ncells * c.nchunks : 0;
@@ -425,6 +455,10 @@ void reduce_sum(const float* a, float* out, const Strided& cells, const Strided&
     ColPlan c = col_plan(ncells, nred);
     dim3 grid((unsigned)c.nx, (unsigned)c.nchunks);
     k_colsum<<<grid, 256, 0, st>>>(a, ncells, nred, red.s0[0], c.chunk, c.nchunks, work, counters, out, div);
+    return;
+  }
+  if (block_form(red, ncells, nred)) {
+    k_sum_block<<<(unsigned)ncells, 256, 0, st>>>(a, cells, red, nred, out, div);
     return;
   }
   SumPlan p = sum_plan(cells, ncells, nred);

@@ -569,10 +569,35 @@ void Runtime::compute_views() {
     return false;
   };
 
+  // n if tensor t reads the n x n identity one_hot(arange(n), n) as laid out or transposed,
+  // else -1 (position embeddings: one_hot(arange(T)) @ table and its gradient).
+  auto identity_onehot = [&](int t) -> int64_t {
+    const int r = view_[t].root;
+    const int src = T_[r].src;
+    if (src < 0 || kinds_[src] != "one_hot" || T_[r].dt != F32) return -1;
+    const int idx = fld(src, "indices");
+    const int isrc = T_[view_[idx].root].src;
+    const int64_t n = O(src).at("depth").i64();
+    if (isrc < 0 || kinds_[isrc] != "arange" || T_[idx].numel != n || !view_[idx].contiguous()) return -1;
+    const View& v = view_[t];
+    if (v.dims.size() != 2 || v.dims[0] != n || v.dims[1] != n) return -1;
+    if (!((v.strides[0] == n && v.strides[1] == 1) || (v.strides[0] == 1 && v.strides[1] == n))) return -1;
+    return n;
+  };
+
   for (size_t i = 0; i < ops_.size(); ++i) {
     const std::string& k = kinds_[i];
     int out = ops_[i]->at("out").i32();
-    if (k == "reshape" || k == "stop_gradient") {
+    if (k == "matmul") {
+      // identity(n) @ B = B: the product is B itself (a view, no kernel).
+      const int a = ops_[i]->at("a").i32(), b = ops_[i]->at("b").i32();
+      const int64_t n = identity_onehot(a);
+      if (n > 0 && view_[b].contiguous() && T_[b].shape.size() == 2 && T_[b].shape[0] == n &&
+          T_[out].numel == T_[b].numel) {
+        view_[out] = View{view_[b].root, T_[out].shape, contiguous_strides(T_[out].shape)};
+        virtual_[i] = true;
+      }
+    } else if (k == "reshape" || k == "stop_gradient") {
       int a = ops_[i]->at("a").i32();
       const View& va = view_[a];
       if (va.contiguous()) {
