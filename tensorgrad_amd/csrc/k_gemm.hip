@@ -484,15 +484,19 @@ __global__ void k_splitk_reduce(const float* __restrict__ work, int splits, int6
 }
 
 struct Plan { int bm, bn, bk, splits; int64_t kps; };
-static int dbg_ns() { static int v = getenv("TG_GEMM_NS") ? atoi(getenv("TG_GEMM_NS")) : 3; return v; }   // DBGTEMP
-static int dbg_bk() { static int v = getenv("TG_GEMM_BK") ? atoi(getenv("TG_GEMM_BK")) : 64; return v; }   // DBGTEMP
 
 Plan plan_for(const GemmDesc& d) {
   auto tiles = [&](int bm, int bn) { return ((d.M + bm - 1) / bm) * ((d.N + bn - 1) / bn) * d.batch; };
-  Plan p{64, 64, dbg_bk(), 1, d.K};
-  if (tiles(128, 128) >= 256) p = Plan{128, 128, 32, 1, d.K};
-  else if (tiles(128, 64) >= 256) p = Plan{128, 64, 32, 1, d.K};
-  else if (tiles(64, 128) >= 256) p = Plan{64, 128, 32, 1, d.K};
+  // Tile shape: least padded work per CU, counted as (rounds of 256 tiles) x tile area, so
+  // an M or N below the tile edge does not pay for MFMAs on padding; ties go to the larger
+  // tile (more reuse per LDS byte).
+  const Plan cand[4] = {{128, 128, 32, 1, d.K}, {128, 64, 32, 1, d.K}, {64, 128, 32, 1, d.K}, {64, 64, 64, 1, d.K}};
+  Plan p = cand[3];
+  int64_t best = -1;
+  for (const Plan& c : cand) {
+    const int64_t cost = (tiles(c.bm, c.bn) + 255) / 256 * c.bm * c.bn;
+    if (best < 0 || cost < best) { best = cost; p = c; }
+  }
   const int64_t t = tiles(p.bm, p.bn);
   if (t < 128 && d.K >= 1024) {
     int64_t want = (256 + t - 1) / t;
@@ -549,18 +553,16 @@ void gemm(const GemmDesc& d, float* work, hipStream_t st) {
   const bool ak = d.sAk == 1;
   const bool bk = d.sBk == 1 && d.sBn != 1;
   if (dma_ok(d, p, ak, bk)) {
-#define TG_DMA_LAUNCH3(BM_, BN_, BK_, NS_)                                                           \
+#define TG_DMA_LAUNCH(BM_, BN_, BK_)                                                           \
   do {                                                                                       \
-    if (ak && bk) k_gemm_dma<BM_, BN_, BK_, NS_, true, true><<<grid, kThreads, 0, st>>>(g);     \
-    else if (ak) k_gemm_dma<BM_, BN_, BK_, NS_, true, false><<<grid, kThreads, 0, st>>>(g);     \
-    else if (bk) k_gemm_dma<BM_, BN_, BK_, NS_, false, true><<<grid, kThreads, 0, st>>>(g);     \
-    else k_gemm_dma<BM_, BN_, BK_, NS_, false, false><<<grid, kThreads, 0, st>>>(g);            \
+    if (ak && bk) k_gemm_dma<BM_, BN_, BK_, 3, true, true><<<grid, kThreads, 0, st>>>(g);     \
+    else if (ak) k_gemm_dma<BM_, BN_, BK_, 3, true, false><<<grid, kThreads, 0, st>>>(g);     \
+    else if (bk) k_gemm_dma<BM_, BN_, BK_, 3, false, true><<<grid, kThreads, 0, st>>>(g);     \
+    else k_gemm_dma<BM_, BN_, BK_, 3, false, false><<<grid, kThreads, 0, st>>>(g);            \
   } while (0)
-#define TG_DMA_LAUNCH(BM_, BN_, BK_) do { if (dbg_ns() == 4) TG_DMA_LAUNCH3(BM_, BN_, BK_, 4); else if (dbg_ns() == 5) TG_DMA_LAUNCH3(BM_, BN_, BK_, 5); else TG_DMA_LAUNCH3(BM_, BN_, BK_, 3); } while (0)
     if (p.bm == 128 && p.bn == 128) TG_DMA_LAUNCH(128, 128, 32);
     else if (p.bm == 128) TG_DMA_LAUNCH(128, 64, 32);
     else if (p.bn == 128) TG_DMA_LAUNCH(64, 128, 32);
-    else if (p.bk == 32) TG_DMA_LAUNCH(64, 64, 32);
     else TG_DMA_LAUNCH(64, 64, 64);
 #undef TG_DMA_LAUNCH
   } else {
