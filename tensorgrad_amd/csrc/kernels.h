@@ -120,6 +120,33 @@ void row_argmax(const float* a, int32_t* out, int64_t outer, int64_t D, hipStrea
 void log_softmax(const float* a, float* out, int64_t outer, int64_t D, hipStream_t st);
 void softmax_causal(const float* a, float* out, int64_t mats, int64_t D, hipStream_t st);
 
+// ---- fused causal attention (k_attention.hip) --------------------------------------
+// Per (b, h): O = dropout(causal_softmax(f32(Q K^T * scale))) V, writing P (the softmax)
+// and Pd (after dropout; null without dropout) as [B, H, T, T] contiguous. Q, V, O are
+// [B, H, T, dh] and K [B, H, T, dh] (read as K^T) with unit stride along dh and the
+// given element strides; all 16-byte aligned.
+struct AttnDesc {
+  int B, H, T, dh;
+  const float* q;
+  int64_t sqb, sqh, sqi;
+  const float* k;
+  int64_t skb, skh, skj;
+  const float* v;
+  int64_t svb, svh, svj;
+  float* o;
+  int64_t sob, soh, soi;
+  float* p;
+  float* pd;
+  int has_scale;
+  double scale;
+  int has_dropout;
+  double drop_p, drop_scale;
+  uint32_t salt;
+  const int32_t* seed;
+};
+bool attention_supported(int64_t T, int64_t dh);
+void attention_fwd(const AttnDesc& a, hipStream_t st);
+
 // ---- GEMM (k_gemm.hip) --------------------------------------------------------------
 // C[z][m][n] = sum_k A[z][m][k] * B[z][k][n], f32 MFMA, f32 accumulate.
 // Batch index z decomposes as (z / bdiv, z % bdiv) with two strides per operand, so a

@@ -274,6 +274,13 @@ class Runtime {
   bool is_row_reduce(int m) const;
   std::vector<Group> groups_;
   std::vector<int> group_of_;   // op -> group index or -1
+  // Fused attention: matmul_batched(q, k^T) [-> mul_scalar] -> softmax_causal_last
+  // [-> dropout] -> matmul_batched(., v), run as one node at the first product.
+  struct AttnMatch { int qk, scale, softmax, dropout, pv; };
+  std::vector<AttnMatch> attn_;
+  std::vector<int> attn_of_;    // op -> attention match or -1
+  void match_attention();
+  void lower_attention(int m);
   std::deque<tgk::FusedProgram> programs_;     // kernel-argument images (stable addresses)
   std::vector<tgk::FusedInstr> fused_code_;    // all groups' instructions, uploaded once
   tgk::FusedInstr* fused_code_dev_ = nullptr;
@@ -771,10 +778,15 @@ void Runtime::lower() {
     }
   }
 
+  match_attention();
   form_groups();
   for (size_t i = 0; i < ops_.size(); ++i) {
     if (is_leaf((int)i) || virtual_[i]) continue;
     if (adam_ops.count((int)i)) continue;
+    if (attn_of_[i] >= 0) {
+      if (attn_[attn_of_[i]].qk == (int)i) lower_attention(attn_of_[i]);
+      continue;
+    }
     int gi = group_of_[i];
     if (gi >= 0) {
       if (groups_[gi].first == (int)i) lower_group(gi);
@@ -1106,7 +1118,7 @@ void Runtime::form_groups() {
   };
   for (size_t i = 0; i < ops_.size(); ++i) {
     const std::string& k = kinds_[i];
-    if (virtual_[i] || is_leaf((int)i)) continue;
+    if (virtual_[i] || is_leaf((int)i) || attn_of_[i] >= 0) continue;
     const bool red = is_row_reduce((int)i);
     if (!red && !pw.count(k)) continue;
     const int out = ops_[i]->at("out").i32();
@@ -1330,6 +1342,128 @@ void Runtime::lower_group(int gi) {
   add_node(std::move(n));
 }
 
+
+// Attention chains the fused kernel covers: shapes it supports, unit-stride head dims
+// and 16-byte aligned rows, intermediate products read by nothing else, and v available
+// at the first product (where the fused node runs). TG_ATTN=0 in the environment keeps
+// the ops unfused.
+void Runtime::match_attention() {
+  attn_of_.assign(ops_.size(), -1);
+  attn_.clear();
+  if (const char* e = std::getenv("TG_ATTN"))
+    if (std::string(e) == "0") return;
+  auto only = [&](int t) { return consumers_[t].size() == 1 ? consumers_[t][0] : -1; };
+  auto pinned = [&](int t) {
+    for (int o : outputs_) if (o == t) return true;
+    for (auto& c : captures_) if (c.second == t) return true;
+    for (auto& w : copy_writebacks_) if (w.first == t) return true;
+    return false;
+  };
+  for (size_t i = 0; i < ops_.size(); ++i) {
+    if (kinds_[i] != "matmul_batched" || virtual_[i]) continue;
+    AttnMatch m{(int)i, -1, -1, -1, -1};
+    const int S = O((int)i).at("out").i32();
+    if (pinned(S)) continue;
+    int c = only(S), S2 = S;
+    if (c >= 0 && kinds_[c] == "mul_scalar" && T_[S].dt == F32) {
+      m.scale = c;
+      S2 = O(c).at("out").i32();
+      if (pinned(S2)) continue;
+      c = only(S2);
+    }
+    if (c < 0 || kinds_[c] != "softmax_causal_last" || fld(c, "a") != S2) continue;
+    m.softmax = c;
+    const int P = O(c).at("out").i32();
+    int Pd = P;
+    for (int u : consumers_[P])
+      if (kinds_[u] == "dropout" && fld(u, "a") == P) { m.dropout = u; Pd = O(u).at("out").i32(); break; }
+    for (int u : consumers_[Pd])
+      if (kinds_[u] == "matmul_batched" && fld(u, "a") == Pd) { m.pv = u; break; }
+    if (m.pv < 0) continue;
+    const int q = fld((int)i, "a"), kt = fld((int)i, "b"), v = fld(m.pv, "b"), o = O(m.pv).at("out").i32();
+    const View &vq = view_[q], &vk = view_[kt], &vv = view_[v], &vo = view_[o];
+    if (vq.dims.size() != 4 || vk.dims.size() != 4 || vv.dims.size() != 4 || vo.dims.size() != 4) continue;
+    const int64_t B = vq.dims[0], H = vq.dims[1], T = vq.dims[2], dh = vq.dims[3];
+    if (!tgk::attention_supported(T, dh)) continue;
+    if (vk.dims != Dims({B, H, dh, T}) || vv.dims != Dims({B, H, T, dh}) || vo.dims != Dims({B, H, T, dh})) continue;
+    if (vq.strides[3] != 1 || vk.strides[2] != 1 || vv.strides[3] != 1 || vo.strides[3] != 1) continue;
+    bool al = true;
+    for (int d = 0; d < 3; ++d) al = al && vq.strides[d] % 4 == 0 && vv.strides[d] % 4 == 0;
+    al = al && vk.strides[0] % 4 == 0 && vk.strides[1] % 4 == 0 && vk.strides[3] % 4 == 0;
+    if (!al) continue;
+    if (view_[P].root != P || !view_[P].contiguous() || view_[Pd].root != Pd || !view_[Pd].contiguous()) continue;
+    auto ready = [&](int t) {   // data of t exists before op i runs
+      const int src = T_[view_[t].root].src;
+      return src < 0 || src < (int)i || is_leaf(src);
+    };
+    if (!ready(v) || (m.dropout >= 0 && !ready(fld(m.dropout, "seed")))) continue;
+    bool taken = false;
+    for (int op : {m.qk, m.scale, m.softmax, m.dropout, m.pv}) if (op >= 0 && attn_of_[op] >= 0) taken = true;
+    if (taken) continue;
+    const int id = (int)attn_.size();
+    attn_.push_back(m);
+    for (int op : {m.qk, m.scale, m.softmax, m.dropout, m.pv}) if (op >= 0) attn_of_[op] = id;
+  }
+}
+
+void Runtime::lower_attention(int mi) {
+  const AttnMatch m = attn_[mi];
+  const int q = fld(m.qk, "a"), kt = fld(m.qk, "b"), v = fld(m.pv, "b"), o = O(m.pv).at("out").i32();
+  const int P = O(m.softmax).at("out").i32();
+  const int Pd = m.dropout >= 0 ? O(m.dropout).at("out").i32() : -1;
+  const int seed = m.dropout >= 0 ? fld(m.dropout, "seed") : -1;
+  const View vq = view_[q], vk = view_[kt], vv = view_[v], vo = view_[o];
+  const int64_t B = vq.dims[0], H = vq.dims[1], T = vq.dims[2], dh = vq.dims[3];
+  Node n;
+  n.kind = "attention";
+  n.op = m.qk;
+  n.shape = shape_str(vq.dims) + " T=" + std::to_string(T);
+  n.detail = std::string("matmul_batched") + (m.scale >= 0 ? ",mul_scalar" : "") + ",softmax_causal_last" +
+             (m.dropout >= 0 ? ",dropout" : "") + ",matmul_batched";
+  for (int t : {q, kt, v}) n.reads.push_back(root(t));
+  if (seed >= 0) n.reads.push_back(root(seed));
+  n.writes.push_back(root(P));
+  if (Pd >= 0) n.writes.push_back(root(Pd));
+  n.writes.push_back(root(o));
+  n.flops = 4.0 * (double)B * H * T * T * dh;
+  n.bytes = 4.0 * (double)B * H * T * (4 * dh + (Pd >= 0 ? 2 : 1) * T);
+  const double scale = m.scale >= 0 ? O(m.scale).at("scalar").num() : 1.0;
+  double dp = 0, dsc = 1;
+  uint32_t salt = 0;
+  if (m.dropout >= 0) {
+    dp = O(m.dropout).at("p").num();
+    dsc = 1.0 / (1.0 - dp);
+    salt = (uint32_t)(uint64_t)std::fmod((double)O(m.dropout).at("salt").i64() * 2654435761.0, 4294967296.0);
+  }
+  n.bind = [=]() -> std::function<void(hipStream_t)> {
+    {
+      int64_t dq[4] = {B, H, T, dh}, dk[4] = {B, H, dh, T}, dd[4] = {B, H, T, dh};
+      check_span("attention q", T_[root(q)].numel, 0, dq, vq.strides.data(), 4);
+      check_span("attention k", T_[root(kt)].numel, 0, dk, vk.strides.data(), 4);
+      check_span("attention v", T_[root(v)].numel, 0, dd, vv.strides.data(), 4);
+      check_span("attention o", T_[root(o)].numel, 0, dd, vo.strides.data(), 4);
+      if (T_[root(P)].numel < B * H * T * T || (Pd >= 0 && T_[root(Pd)].numel < B * H * T * T))
+        throw Error(TG_INTERNAL, "attention: probability tensor too small");
+    }
+    tgk::AttnDesc a{};
+    a.B = (int)B; a.H = (int)H; a.T = (int)T; a.dh = (int)dh;
+    a.q = (const float*)dptr(q); a.sqb = vq.strides[0]; a.sqh = vq.strides[1]; a.sqi = vq.strides[2];
+    a.k = (const float*)dptr(kt); a.skb = vk.strides[0]; a.skh = vk.strides[1]; a.skj = vk.strides[3];
+    a.v = (const float*)dptr(v); a.svb = vv.strides[0]; a.svh = vv.strides[1]; a.svj = vv.strides[2];
+    a.o = (float*)dptr(o); a.sob = vo.strides[0]; a.soh = vo.strides[1]; a.soi = vo.strides[2];
+    a.p = (float*)dptr(P);
+    a.pd = Pd >= 0 ? (float*)dptr(Pd) : nullptr;
+    a.has_scale = m.scale >= 0;
+    a.scale = scale;
+    a.has_dropout = m.dropout >= 0;
+    a.drop_p = dp;
+    a.drop_scale = dsc;
+    a.salt = salt;
+    a.seed = seed >= 0 ? (const int32_t*)dptr(seed) : nullptr;
+    return [a](hipStream_t st) { tgk::attention_fwd(a, st); };
+  };
+  add_node(std::move(n));
+}
 
 void Runtime::lower_op(int i) {
   const std::string& k = kinds_[i];

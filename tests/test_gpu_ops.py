@@ -277,6 +277,62 @@ def test_cross_entropy_row_chains(R, D):
     exact(got, want)
 
 
+def _attention_graph(B, H, T, dh, what):
+    def body():
+        q, k, v = (tensor_input(n, [B, H, T, dh]) for n in ('q', 'k', 'v'))
+        s = O.matmul(q, O.permute(k, [0, 1, 3, 2]))
+        p = O.softmax_causal(O.mul(s, 0.125))
+        pd = O.dropout(p, 0.1)
+        o = O.matmul(pd, v)
+        return {'o': o, 'p': p, 'pd': pd}[what]
+    return body
+
+
+def _run_native(g, inputs, env=None):
+    import os
+    old = {k: os.environ.get(k) for k in (env or {})}
+    os.environ.update(env or {})
+    try:
+        rt = backend.NativeRuntime(IR.dumps(wire(g)))
+    finally:
+        for k, v in old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+    out_t = g.tensors[g.outputs[0]]
+    kinds = [n['kind'] for n in rt.describe()['nodes']]
+    got = rt.run(inputs, out_t.shape, np.float32)
+    rt.destroy()
+    return got, kinds
+
+
+@pytest.mark.parametrize('B,H,T', [(2, 3, 64), (2, 3, 128), (32, 4, 128)])
+@pytest.mark.parametrize('what', ['o', 'p', 'pd'])
+def test_fused_attention(B, H, T, what):
+    """The fused attention kernel (Q K^T, scale, causal softmax, dropout, P V in one
+    launch) against the oracle (GEMM tolerance: the products run on f32 matrix cores).
+    At the transformer's shape, where the unfused GEMMs take the tiles whose k-blocking the
+    fused kernel follows (QK^T in stages of 32, PV in stages of 64), it must also equal the
+    unfused kernels bit for bit (same MFMA order, same row-softmax arithmetic and lanes)."""
+    dh = 64
+    ins = {n: _rand([B, H, T, dh], s, -2, 2) for n, s in (('q', 61), ('k', 62), ('v', 63))}
+    g = trace_fn(_attention_graph(B, H, T, dh, what))
+    got, kinds = _run_native(g, ins)
+    assert 'attention' in kinds
+    ref, kinds0 = _run_native(g, ins, {'TG_ATTN': '0'})
+    assert 'attention' not in kinds0
+    if B * H == 128 and T == 128:
+        exact(got, ref)
+    o = pyoracle.OracleRuntime(wire(g))
+    o.run(ins)
+    want = o.output()
+    if what == 'o':
+        gemm_close(got, want)
+    else:
+        assert np.allclose(got, want, rtol=1e-5, atol=1e-7), np.max(np.abs(got.astype(np.float64) - want))
+
+
 GEMMS = [([5, 7], [7, 3], False, False), ([2, 33, 65], [65, 17], False, False), ([129, 64], [64, 300], False, False),
          ([70, 40], [50, 40], False, True), ([40, 70], [40, 50], True, False), ([4096, 256], [4096, 256], True, False),
          ([300, 4096], [4096, 64], False, False)]
