@@ -5,6 +5,8 @@
 // win at index 0" semantics under any combination order.
 #include "kernels.h"
 
+#include <algorithm>
+
 #include <cmath>
 
 namespace tgk {
@@ -258,52 +260,63 @@ __global__ void k_sum_finish(const double* __restrict__ part, float* __restrict_
   }
 }
 
-// Column sums in one launch: out[c] = f32(sum_r a[r * rs + c] / div), c < C, r < R.
-// Block (x, y) takes columns [64x, 64x + 64) and rows [y chunk, (y + 1) chunk): lane l of
-// wave w sums column 64x + l over rows y chunk + w, + 4, ... in order (f64), and the
-// four waves combine in order through LDS into the block's partial. The last block of a
-// column block to finish (counted on counters[x]) adds the chunk partials in a fixed
-// tree (wave w takes chunks w, w + 4, ... in order, then waves in order) and resets its
-// counter, so results do not depend on scheduling and the launch leaves every counter
-// at zero for the next one.
-__global__ __launch_bounds__(256) void k_colsum(const float* __restrict__ a, int64_t C, int64_t R, int64_t rs,
-                                                int64_t chunk, int nchunks, double* __restrict__ part,
-                                                unsigned* __restrict__ counters, float* __restrict__ out,
-                                                double div) {
+// Column sums in one launch: out[c] = f32(sum_r x(r, c) / div), c < C, r < R, where
+// x = a[r rs + c] or the f32 product a[r rs + c] * b[r rs + c]; blockIdx.z picks one of
+// several independent sums launched together. Block (x, y) takes columns [64x, 64x + 64)
+// and rows [y chunk, (y + 1) chunk): lane l of wave w sums column 64x + l over rows
+// y chunk + w, + 4, ... in order (f64), and the four waves combine in order through LDS
+// into the block's partial. The last block of a column block to finish (counted on
+// counters[x]) adds the chunk partials in a fixed tree (wave w takes chunks w, w + 4, ...
+// in order, then waves in order) and resets its counter, so results do not depend on
+// scheduling and the launch leaves every counter at zero for the next one.
+__global__ __launch_bounds__(256) void k_colsum(const ColSumBatch batch) {
+  const ColSum& cs = batch.s[blockIdx.z];
+  if ((int64_t)blockIdx.x >= cs.nx || (int)blockIdx.y >= cs.nchunks) return;
   __shared__ double red[4][64];
   __shared__ int last;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t C = cs.C, rs = cs.rs;
+  const int nchunks = cs.nchunks;
   const int64_t c = (int64_t)blockIdx.x * 64 + lane;
   const int y = blockIdx.y;
-  const int64_t r0 = (int64_t)y * chunk, r1 = min(R, r0 + chunk);
+  const int64_t r0 = (int64_t)y * cs.chunk, r1 = min(cs.R, r0 + cs.chunk);
   double s = 0.0;
   if (c < C) {
-    const float* p = a + c;
+    const float* p = cs.a + c;
+    const float* q = cs.b ? cs.b + c : nullptr;
     int64_t r = r0 + w;
     for (; r + 60 < r1; r += 64) {   // sixteen rows in flight, added in row order
       float v[16];
 #pragma unroll
       for (int u = 0; u < 16; ++u) v[u] = p[(r + 4 * u) * rs];
+      if (q) {
+        float m[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) m[u] = q[(r + 4 * u) * rs];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) v[u] = v[u] * m[u];
+      }
 #pragma unroll
       for (int u = 0; u < 16; ++u) s += (double)v[u];
     }
-    for (; r < r1; r += 4) s += (double)p[r * rs];
+    for (; r < r1; r += 4) s += (double)(q ? p[r * rs] * q[r * rs] : p[r * rs]);
   }
   red[w][lane] = s;
   __syncthreads();
   const double bs = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
   if (nchunks == 1) {
-    if (w == 0 && c < C) out[c] = (float)(bs / div);
+    if (w == 0 && c < C) cs.out[c] = (float)(bs / cs.div);
     return;
   }
   // Partials, the counter and the final reads are device-scope atomic accesses: coherent
   // across the XCDs' separate L2 caches without a full L2 write-back (which a device-scope
   // fence costs). Each wave's partial stores complete (vmcnt) before the block counts in.
+  double* part = cs.part;
   if (w == 0 && c < C) __hip_atomic_store(&part[(int64_t)y * C + c], bs, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0)
-    last = __hip_atomic_fetch_add(&counters[blockIdx.x], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+    last = __hip_atomic_fetch_add(&cs.counters[blockIdx.x], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
            (unsigned)(nchunks - 1);
   __syncthreads();
   if (!last) return;
@@ -327,8 +340,8 @@ __global__ __launch_bounds__(256) void k_colsum(const float* __restrict__ a, int
   }
   red[w][lane] = t;
   __syncthreads();
-  if (w == 0 && c < C) out[c] = (float)((((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane]) / div);
-  if (threadIdx.x == 0) __hip_atomic_store(&counters[blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (w == 0 && c < C) cs.out[c] = (float)((((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane]) / cs.div);
+  if (threadIdx.x == 0) __hip_atomic_store(&cs.counters[blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Few cells with up to 64K terms each: one 256-thread block per cell. Thread t sums terms
@@ -442,6 +455,38 @@ int64_t sum_workspace_doubles(const Strided& cells, const Strided& red, int64_t 
   return p.nchunks > 1 ? ncells * p.nchunks : 0;
 }
 
+ColSum colsum_desc(const float* a, const float* b, float* out, int64_t C, int64_t R, int64_t rs, double div,
+                   double* part, unsigned* counters) {
+  const ColPlan p = col_plan(C, R);
+  ColSum c{};
+  c.a = a; c.b = b; c.out = out;
+  c.C = C; c.R = R; c.rs = rs; c.chunk = p.chunk;
+  c.nchunks = p.nchunks; c.nx = (int)p.nx;
+  c.div = div; c.part = part; c.counters = counters;
+  return c;
+}
+
+int64_t colsum_workspace_doubles(int64_t C, int64_t R) {
+  const ColPlan p = col_plan(C, R);
+  return p.nchunks > 1 ? C * p.nchunks : 0;
+}
+
+int64_t colsum_counters(int64_t C, int64_t R) {
+  const ColPlan p = col_plan(C, R);
+  return p.nchunks > 1 ? p.nx : 0;
+}
+
+void colsum_batch(const ColSumBatch& b, hipStream_t st) {
+  if (b.n <= 0) return;
+  int64_t nx = 0, ny = 0;
+  for (int i = 0; i < b.n; ++i) {
+    nx = std::max<int64_t>(nx, b.s[i].nx);
+    ny = std::max<int64_t>(ny, b.s[i].nchunks);
+  }
+  if (nx <= 0) return;
+  k_colsum<<<dim3((unsigned)nx, (unsigned)ny, (unsigned)b.n), 256, 0, st>>>(b);
+}
+
 int64_t sum_counters(const Strided& cells, const Strided& red, int64_t ncells, int64_t nred) {
   if (!col_form(cells, red)) return 0;
   ColPlan c = col_plan(ncells, nred);
@@ -452,9 +497,10 @@ void reduce_sum(const float* a, float* out, const Strided& cells, const Strided&
                 double div, double* work, unsigned* counters, hipStream_t st) {
   if (ncells <= 0) return;
   if (col_form(cells, red)) {
-    ColPlan c = col_plan(ncells, nred);
-    dim3 grid((unsigned)c.nx, (unsigned)c.nchunks);
-    k_colsum<<<grid, 256, 0, st>>>(a, ncells, nred, red.s0[0], c.chunk, c.nchunks, work, counters, out, div);
+    ColSumBatch bt{};
+    bt.n = 1;
+    bt.s[0] = colsum_desc(a, nullptr, out, ncells, nred, red.s0[0], div, work, counters);
+    colsum_batch(bt, st);
     return;
   }
   if (block_form(red, ncells, nred)) {

@@ -116,6 +116,30 @@ int64_t sum_workspace_doubles(const Strided& cells, const Strided& red, int64_t 
 int64_t sum_counters(const Strided& cells, const Strided& red, int64_t ncells, int64_t nred);
 void reduce_sum(const float* a, float* out, const Strided& cells, const Strided& red, int64_t ncells, int64_t nred,
                 double div, double* work, unsigned* counters, hipStream_t st);
+// Column sums of [R, C] row-major operands (row stride rs), out[c] = f32(sum_r x / div)
+// with x = a or the f32 product a * b, up to kColSumMax independent sums in one launch.
+// `part` holds colsum_workspace_doubles(C, R) doubles and `counters` colsum_counters(C, R)
+// zeroed counters per sum (left zero again).
+struct ColSum {
+  const float* a;
+  const float* b;
+  float* out;
+  int64_t C, R, rs, chunk;
+  int nchunks, nx;
+  double div;
+  double* part;
+  unsigned* counters;
+};
+constexpr int kColSumMax = 4;
+struct ColSumBatch {
+  int n;
+  ColSum s[kColSumMax];
+};
+ColSum colsum_desc(const float* a, const float* b, float* out, int64_t C, int64_t R, int64_t rs, double div,
+                   double* part, unsigned* counters);
+int64_t colsum_workspace_doubles(int64_t C, int64_t R);
+int64_t colsum_counters(int64_t C, int64_t R);
+void colsum_batch(const ColSumBatch& b, hipStream_t st);
 void row_argmax(const float* a, int32_t* out, int64_t outer, int64_t D, hipStream_t st);
 void log_softmax(const float* a, float* out, int64_t outer, int64_t D, hipStream_t st);
 void softmax_causal(const float* a, float* out, int64_t mats, int64_t D, hipStream_t st);

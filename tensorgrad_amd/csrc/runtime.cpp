@@ -281,6 +281,15 @@ class Runtime {
   std::vector<int> attn_of_;    // op -> attention match or -1
   void match_attention();
   void lower_attention(int m);
+  // Column sums (sum_to_shape over a leading block of dims of a contiguous tensor): a
+  // single-use f32 product feeding one is absorbed (the kernel multiplies), and sums of
+  // the same shape whose inputs are ready are launched together.
+  struct ColSumOp { int a, b; int64_t R, C; };   // b >= 0: sum of the product a * b
+  std::map<int, ColSumOp> colsum_;
+  std::vector<bool> colsum_done_, mul_absorbed_;
+  void match_colsums();
+  void lower_colsums(int s);
+  int emit_pos(int op) const;
   std::deque<tgk::FusedProgram> programs_;     // kernel-argument images (stable addresses)
   std::vector<tgk::FusedInstr> fused_code_;    // all groups' instructions, uploaded once
   tgk::FusedInstr* fused_code_dev_ = nullptr;
@@ -779,12 +788,18 @@ void Runtime::lower() {
   }
 
   match_attention();
+  match_colsums();
   form_groups();
   for (size_t i = 0; i < ops_.size(); ++i) {
     if (is_leaf((int)i) || virtual_[i]) continue;
     if (adam_ops.count((int)i)) continue;
     if (attn_of_[i] >= 0) {
       if (attn_[attn_of_[i]].qk == (int)i) lower_attention(attn_of_[i]);
+      continue;
+    }
+    if (mul_absorbed_[i]) continue;
+    if (colsum_.count((int)i)) {
+      if (!colsum_done_[i]) lower_colsums((int)i);
       continue;
     }
     int gi = group_of_[i];
@@ -1118,7 +1133,7 @@ void Runtime::form_groups() {
   };
   for (size_t i = 0; i < ops_.size(); ++i) {
     const std::string& k = kinds_[i];
-    if (virtual_[i] || is_leaf((int)i) || attn_of_[i] >= 0) continue;
+    if (virtual_[i] || is_leaf((int)i) || attn_of_[i] >= 0 || mul_absorbed_[i] || colsum_.count((int)i)) continue;
     const bool red = is_row_reduce((int)i);
     if (!red && !pw.count(k)) continue;
     const int out = ops_[i]->at("out").i32();
@@ -1404,6 +1419,116 @@ void Runtime::match_attention() {
     attn_.push_back(m);
     for (int op : {m.qk, m.scale, m.softmax, m.dropout, m.pv}) if (op >= 0) attn_of_[op] = id;
   }
+}
+
+void Runtime::match_colsums() {
+  colsum_.clear();
+  colsum_done_.assign(ops_.size(), false);
+  mul_absorbed_.assign(ops_.size(), false);
+  auto pinned = [&](int t) {
+    for (int o : outputs_) if (o == t) return true;
+    for (auto& c : captures_) if (c.second == t) return true;
+    for (auto& w : copy_writebacks_) if (w.first == t) return true;
+    return false;
+  };
+  for (size_t i = 0; i < ops_.size(); ++i) {
+    if (kinds_[i] != "sum_to_shape" || virtual_[i] || attn_of_[i] >= 0) continue;
+    const int a = fld((int)i, "a"), out = O((int)i).at("out").i32();
+    if (!view_[a].contiguous() || T_[a].dt != F32) continue;
+    const Dims& as = T_[a].shape;
+    const Dims& os = T_[out].shape;
+    // target = [1.., kept suffix of as]: reduced dims form a leading block
+    const int rdiff = (int)as.size() - (int)os.size();
+    if (rdiff < 0) continue;
+    size_t lead = 0;   // dims of `as` summed over
+    bool ok = true, in_kept = false;
+    for (size_t d = 0; d < as.size(); ++d) {
+      const bool reduced = (int)d < rdiff || (os[d - rdiff] == 1 && as[d] != 1);
+      if (reduced && in_kept) { ok = false; break; }
+      if (!reduced && as[d] != 1) in_kept = true;
+      if (reduced) lead = d + 1;
+    }
+    if (!ok) continue;
+    int64_t R = 1, C = 1;
+    for (size_t d = 0; d < as.size(); ++d) (d < lead ? R : C) *= as[d];
+    if (R <= 1 || C <= 0 || C != T_[out].numel) continue;
+    ColSumOp c{a, -1, R, C};
+    const int m = T_[a].src;
+    if (m >= 0 && kinds_[m] == "mul" && view_[a].root == a && consumers_[a].size() == 1 && !pinned(a) &&
+        attn_of_[m] < 0) {
+      const int x = fld(m, "a"), y = fld(m, "b");
+      if (T_[x].dt == F32 && T_[y].dt == F32 && T_[x].shape == as && T_[y].shape == as && view_[x].contiguous() &&
+          view_[y].contiguous()) {
+        c.a = x;
+        c.b = y;
+        mul_absorbed_[m] = true;
+      }
+    }
+    colsum_[(int)i] = c;
+  }
+}
+
+// Op index at whose position op's node runs (its group's first op, its attention chain's
+// first product, or itself).
+int Runtime::emit_pos(int op) const {
+  if (group_of_[op] >= 0) return groups_[group_of_[op]].first;
+  if (attn_of_[op] >= 0) return attn_[attn_of_[op]].qk;
+  return op;
+}
+
+void Runtime::lower_colsums(int s0) {
+  std::vector<int> batch{s0};
+  const ColSumOp& c0 = colsum_.at(s0);
+  auto ready = [&](int t) {   // t's data exists before op s0's node runs
+    const int p = T_[view_[t].root].src;
+    if (p < 0 || is_leaf(p)) return true;
+    if (colsum_.count(p)) return (bool)colsum_done_[p];
+    if (mul_absorbed_[p]) return false;
+    return emit_pos(p) < s0;
+  };
+  for (auto it = colsum_.upper_bound(s0); it != colsum_.end() && (int)batch.size() < tgk::kColSumMax; ++it) {
+    const ColSumOp& c = it->second;
+    if (colsum_done_[it->first] || c.R != c0.R || c.C != c0.C) continue;
+    if (!ready(c.a) || (c.b >= 0 && !ready(c.b))) continue;
+    batch.push_back(it->first);
+  }
+  for (int sop : batch) colsum_done_[sop] = true;
+  Node n;
+  n.kind = "reduce";
+  n.op = s0;
+  n.shape = "[" + std::to_string(c0.R) + "," + std::to_string(c0.C) + "] x" + std::to_string(batch.size());
+  size_t ws = 0;
+  std::vector<size_t> ws_off;
+  std::vector<int64_t> cbase;
+  for (int sop : batch) {
+    const ColSumOp& c = colsum_.at(sop);
+    n.reads.push_back(root(c.a));
+    if (c.b >= 0) n.reads.push_back(root(c.b));
+    const int out = O(sop).at("out").i32();
+    n.writes.push_back(root(out));
+    n.bytes += 4.0 * (c.R * c.C * (c.b >= 0 ? 2 : 1) + c.C);
+    n.detail += std::string(n.detail.empty() ? "" : ",") + (c.b >= 0 ? "mul,sum_to_shape" : "sum_to_shape");
+    ws_off.push_back(ws);
+    ws += ((size_t)tgk::colsum_workspace_doubles(c.C, c.R) * 8 + 255) & ~(size_t)255;
+    cbase.push_back(take_counters(tgk::colsum_counters(c.C, c.R)));
+  }
+  workspace_bytes_ = std::max(workspace_bytes_, ws);
+  n.bind = [=]() -> std::function<void(hipStream_t)> {
+    tgk::ColSumBatch bt{};
+    bt.n = (int)batch.size();
+    for (size_t q = 0; q < batch.size(); ++q) {
+      const ColSumOp& c = colsum_.at(batch[q]);
+      const int out = O(batch[q]).at("out").i32();
+      if (T_[root(c.a)].numel < c.R * c.C || (c.b >= 0 && T_[root(c.b)].numel < c.R * c.C) ||
+          T_[root(out)].numel < c.C)
+        throw Error(TG_INTERNAL, "column sum: operand smaller than its shape");
+      double* part = reinterpret_cast<double*>(reinterpret_cast<char*>(cur_ws_) + ws_off[q]);
+      bt.s[q] = tgk::colsum_desc((const float*)dptr(c.a), c.b >= 0 ? (const float*)dptr(c.b) : nullptr,
+                                 (float*)dptr(out), c.C, c.R, c.C, 1.0, part, counters_ + cbase[q]);
+    }
+    return [bt](hipStream_t st) { tgk::colsum_batch(bt, st); };
+  };
+  add_node(std::move(n));
 }
 
 void Runtime::lower_attention(int mi) {

@@ -192,6 +192,30 @@ def test_column_sums_repeat_bit_identical():
     assert abs(float(outs[0]) - float(want)) <= 1e-6 * abs(float(want)) + 1e-6
 
 
+def test_column_sums_of_products_batched():
+    """A single-use f32 product feeding a column sum is multiplied inside the sum kernel,
+    and two same-shape column sums share one launch: each result equals the f64 sum of the
+    f32-rounded products (or values), rounded once."""
+    x, y = _rand([3000, 70], 23), _rand([3000, 70], 24)
+
+    def build():
+        ty = tensor_input('y', [3000, 70])
+        a = O.sum_to_shape(O.mul(tensor_input('x', [3000, 70]), ty), [70])
+        b = O.sum_to_shape(ty, [70])
+        return O.sub(a, O.mul(b, 0.5))
+
+    g = trace_fn(build)
+    rt = backend.NativeRuntime(IR.dumps(wire(g)))
+    kinds = [(n['kind'], n.get('ops', '')) for n in rt.describe()['nodes']]
+    got = rt.run({'x': x, 'y': y}, [70], np.float32)
+    rt.destroy()
+    assert ('reduce', 'mul,sum_to_shape,sum_to_shape') in kinds, kinds
+    a = (x * y).astype(np.float64).sum(0).astype(np.float32)
+    b = y.astype(np.float64).sum(0).astype(np.float32)
+    want = (a.astype(np.float64) - (b.astype(np.float64) * 0.5).astype(np.float32)).astype(np.float32)
+    near(got, want, 2)
+
+
 def test_broadcast_permute_slice_concat_scatter():
     x = _rand([2, 3, 4], 9)
     got, want = run_both(lambda: O.permute(tensor_input('x', [2, 3, 4]), [2, 0, 1]), {'x': x})
