@@ -51,13 +51,15 @@ def measure(key, steps, warmup, profile_iters=3, kind_iters=20):
     # Kernel-family times: back-to-back passes over just that family's launches, HIP
     # events on the runtime's stream around the passes.
     gemm_t, gemm_n = rt.time_kinds('gemm', kind_iters)
-    other_t, other_n = rt.time_kinds('-gemm,conv', kind_iters)
+    other_t, other_n = rt.time_kinds('-gemm,conv,attention', kind_iters)
     conv_t, conv_n = rt.time_kinds('conv', kind_iters)
+    attn_t, attn_n = rt.time_kinds('attention', kind_iters)
     rt.destroy()
     gemm_f = sum(n['flops'] for n in nodes if n['kind'] == 'gemm')
     gemm_b = sum(n['bytes'] for n in nodes if n['kind'] == 'gemm')
-    other_b = sum(n['bytes'] for n in nodes if n['kind'] not in ('gemm', 'conv'))
+    other_b = sum(n['bytes'] for n in nodes if n['kind'] not in ('gemm', 'conv', 'attention'))
     conv_f = sum(n['flops'] for n in nodes if n['kind'] == 'conv')
+    attn_f = sum(n['flops'] for n in nodes if n['kind'] == 'attention')
     by_kind = {}
     for n, t in zip(nodes, ms):
         k = by_kind.setdefault(n['kind'], {'launch_nodes': 0, 'ms': 0.0})
@@ -80,6 +82,8 @@ def measure(key, steps, warmup, profile_iters=3, kind_iters=20):
                  'top': [{'shape': n['shape'], 'ms': round(t, 4), 'tflops': round(n['flops'] / max(t, 1e-12) / 1e9, 2)}
                          for t, n in top_gemm]},
         'conv': {'flop_per_step': conv_f, 'ms': conv_t, 'tflops': conv_f / max(conv_t, 1e-12) / 1e9},
+        'attention': {'flop_per_step': attn_f, 'launches': attn_n, 'ms': attn_t,
+                      'tflops': attn_f / max(attn_t, 1e-12) / 1e9},
         'non_gemm': {'bytes_per_step': other_b, 'launches': other_n, 'ms': other_t,
                      'gbs': other_b / max(other_t, 1e-12) / 1e6,
                      'frac_hbm_peak': other_b / max(other_t, 1e-12) / 1e6 / PEAK_HBM_GBS},
@@ -209,6 +213,7 @@ def main():
                         'samples_per_s': round(r['samples_per_s'], 1), 'device_replay_ms': round(r['device_replay_ms'], 4),
                         'gemm_tflops': round(r['gemm']['tflops'], 2), 'gemm_frac_f32_peak': round(r['gemm']['frac_f32_peak'], 4),
                         'conv_tflops': round(r['conv']['tflops'], 2),
+                        'attention_tflops': round(r['attention']['tflops'], 2),
                         'non_gemm_gbs': round(r['non_gemm']['gbs'], 1),
                         'non_gemm_frac_hbm': round(r['non_gemm']['frac_hbm_peak'], 4),
                         'launch_nodes': r['launch_nodes'], 'kinds': r['kinds'], 'top_gemms': r['gemm']['top']}

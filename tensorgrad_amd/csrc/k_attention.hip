@@ -217,6 +217,249 @@ __global__ __launch_bounds__(kNT) void k_attn_fwd(const AttnDesc a) {
   }
 }
 
+// Row-tile loader: rows [r0, r0 + R) of a [.., 64]-wide operand with row stride `rs`
+// (16-byte aligned rows) into LDS rows of `ld` floats, every load in flight first.
+template <int R, int LD>
+__device__ __forceinline__ void load_rows(const float* src, int64_t rs, float* dst, int tid) {
+  constexpr int C = R * kDH / 4 / kNT;
+  f32x4 v[C];
+#pragma unroll
+  for (int u = 0; u < C; ++u) {
+    const int c = u * kNT + tid, row = c / (kDH / 4), c4 = c % (kDH / 4);
+    v[u] = *reinterpret_cast<const f32x4*>(src + (int64_t)row * rs + c4 * 4);
+  }
+#pragma unroll
+  for (int u = 0; u < C; ++u) {
+    const int c = u * kNT + tid, row = c / (kDH / 4), c4 = c % (kDH / 4);
+    *reinterpret_cast<f32x4*>(dst + row * LD + c4 * 4) = v[u];
+  }
+}
+
+// One 32 x 32 tile, one 64-k stage of a product whose operands are read one column per
+// lane from LDS row-major tiles: out(m, n) = sum_k A[k][m] B[k][n] (A rows at a0 + k * lda,
+// B rows at b0 + k * ldb), k = 64 s + 8 g + 4 h + jj in the k_gemm order.
+__device__ __forceinline__ f32x16 stage_cols(const float* a0, int lda, const float* b0, int ldb, int s, int lrow,
+                                             int h) {
+  f32x16 part;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) part[r] = 0.0f;
+#pragma unroll
+  for (int g = 0; g < 8; ++g) {
+    const int kb = s * 64 + g * 8 + h * 4;
+    f32x4 av, bv;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      av[u] = a0[(kb + u) * lda + lrow];
+      bv[u] = b0[(kb + u) * ldb + lrow];
+    }
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) part = __builtin_amdgcn_mfma_f32_32x32x2f32(av[jj], bv[jj], part, 0, 0, 0);
+  }
+  return part;
+}
+
+// Backward, kernel A (per 64 query rows): dPd = dO V^T, the dropout and softmax backward
+// row math giving dS (written out), and dQ = dS K.
+template <int T>
+__global__ __launch_bounds__(kNT) void k_attn_bwd_a(const AttnBwdDesc a) {
+  constexpr int LDS_ = T + 4;
+  __shared__ __attribute__((aligned(16))) float Os[kQB * kLD];   // dO rows; later dQ stage-1 partials
+  __shared__ __attribute__((aligned(16))) float Vs[T * kLD];
+  __shared__ __attribute__((aligned(16))) float Ks[T * kLDV];
+  __shared__ __attribute__((aligned(16))) float Ss[kQB * LDS_];  // dPd, then dS
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lrow = lane & 31, h = lane >> 5;
+  constexpr int RB = T / kQB;
+  const int bh = blockIdx.x / RB, rb = blockIdx.x % RB;
+  const int b = bh / a.H, hd = bh % a.H;
+  const int i0 = rb * kQB;
+
+  load_rows<kQB, kLD>(a.dout + b * a.sob + hd * a.soh + (int64_t)i0 * a.soi, a.soi, Os, tid);
+  load_rows<T, kLD>(a.v + b * a.svb + hd * a.svh, a.svj, Vs, tid);
+  load_rows<T, kLDV>(a.k + b * a.skb + hd * a.skh, a.skj, Ks, tid);
+  __syncthreads();
+
+  // dPd = dO V^T into Ss (the QK^T kernel's tiles and k-blocking)
+  {
+    constexpr int NTILE = 2 * (T / 32);
+    for (int t = wave; t < NTILE; t += kNT / 64) {
+      const int wm = (t / (T / 32)) * 32, wn = (t % (T / 32)) * 32;
+      f32x16 acc;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+#pragma unroll
+      for (int s = 0; s < kDH / 32; ++s) {
+        f32x16 part;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) part[r] = 0.0f;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int kb = s * 32 + g * 8 + h * 4;
+          const f32x4 av = *reinterpret_cast<const f32x4*>(Os + (wm + lrow) * kLD + kb);
+          const f32x4 bv = *reinterpret_cast<const f32x4*>(Vs + (wn + lrow) * kLD + kb);
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) part = __builtin_amdgcn_mfma_f32_32x32x2f32(av[jj], bv[jj], part, 0, 0, 0);
+        }
+        acc += part;
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) Ss[(wm + (r / 4) * 8 + h * 4 + (r % 4)) * LDS_ + wn + lrow] = acc[r];
+    }
+  }
+  __syncthreads();
+
+  // dS rows: v0 = dropout(dPd), v1 = v0 * P, s = f32(rowsum v1) (f64, lanes then
+  // butterfly), dS = f32((v0 - s) * P * scale): the row-fused group's arithmetic and lanes.
+  {
+    constexpr int V = T >= 128 ? 2 : 1;
+    constexpr int RW = 4;
+    constexpr int RPW = kQB / (kNT / 64);
+    const unsigned seed = a.seed ? (unsigned)*a.seed : 0u;
+    for (int rr = 0; rr < RPW; rr += RW) {
+      unsigned v0[RW][V], pv[RW][V];
+      double sum[RW];
+#pragma unroll
+      for (int w = 0; w < RW; ++w) {
+        const int il = wave * RPW + rr + w;
+        const int64_t rflat = (int64_t)bh * T + i0 + il;
+        sum[w] = 0.0;
+#pragma unroll
+        for (int u = 0; u < V; ++u) {
+          const unsigned x = fbits(Ss[il * LDS_ + lane * V + u]);
+          pv[w][u] = reinterpret_cast<const unsigned*>(a.p)[rflat * T + lane * V + u];
+          v0[w][u] = a.has_dropout ? dropout_bits(x, seed, a.salt, a.drop_p, a.drop_scale,
+                                                  (unsigned)(rflat * T + lane * V + u))
+                                   : x;
+          sum[w] += (double)(bitsf(v0[w][u]) * bitsf(pv[w][u]));
+        }
+      }
+      for (int o = 32; o > 0; o >>= 1)
+#pragma unroll
+        for (int w = 0; w < RW; ++w) sum[w] += __shfl_xor(sum[w], o, 64);
+#pragma unroll
+      for (int w = 0; w < RW; ++w) {
+        const int il = wave * RPW + rr + w;
+        const int64_t rflat = (int64_t)bh * T + i0 + il;
+        const float sf = (float)(sum[w] / 1.0);
+        unsigned dv[V];
+#pragma unroll
+        for (int u = 0; u < V; ++u) {
+          const unsigned t = fbits((bitsf(v0[w][u]) - sf) * bitsf(pv[w][u]));
+          dv[u] = a.has_scale ? op_eval(FO_MULS, t, 0u, DT_F32, DT_F32, DT_F32, a.scale, 0.0, 0u, 0u, 0u) : t;
+          Ss[il * LDS_ + lane * V + u] = bitsf(dv[u]);
+        }
+        unsigned* D = reinterpret_cast<unsigned*>(a.ds) + rflat * T + lane * V;
+        if (V == 2) {
+          typedef unsigned u2 __attribute__((ext_vector_type(2)));
+          *reinterpret_cast<u2*>(D) = (u2){dv[0], dv[V - 1]};
+        } else {
+          D[0] = dv[0];
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // dQ = dS K (the PV kernel's tiles and k-blocking; Os now holds stage-1 partials)
+  {
+    constexpr int NS = T / 64;
+    const int tile = wave & 3, s = wave >> 2;
+    const int wm = (tile >> 1) * 32, wn = (tile & 1) * 32;
+    f32x16 part;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) part[r] = 0.0f;
+    if (s < NS) {
+#pragma unroll
+      for (int g = 0; g < 8; ++g) {
+        const int kb = s * 64 + g * 8 + h * 4;
+        const f32x4 av = *reinterpret_cast<const f32x4*>(Ss + (wm + lrow) * LDS_ + kb);
+        f32x4 bv;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) bv[u] = Ks[(kb + u) * kLDV + wn + lrow];
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) part = __builtin_amdgcn_mfma_f32_32x32x2f32(av[jj], bv[jj], part, 0, 0, 0);
+      }
+    }
+    float* Xs = Os;
+    if (NS == 2 && s == 1)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) Xs[(tile * 16 + r) * 64 + lane] = part[r];
+    __syncthreads();
+    if (s == 0) {
+      f32x16 acc;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[r] = 0.0f + part[r];
+      if (NS == 2)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[r] += Xs[(tile * 16 + r) * 64 + lane];
+      float* o = a.dq + b * a.sdqb + hd * a.sdqh;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[(int64_t)(i0 + wm + (r / 4) * 8 + h * 4 + (r % 4)) * a.sdqi + wn + lrow] = acc[r];
+    }
+  }
+}
+
+// Backward, kernel B (per 64 keys): dV = Pd^T dO and dK = dS^T Q over all T query rows,
+// each as two 64-row stages added in order (the unfused GEMMs' blocking).
+template <int T>
+__global__ __launch_bounds__(kNT) void k_attn_bwd_b(const AttnBwdDesc a) {
+  __shared__ __attribute__((aligned(16))) float Pc[T * kLD];   // Pd[i][j0 ..]
+  __shared__ __attribute__((aligned(16))) float Oc[T * kLD];   // dO[i][:]
+  __shared__ __attribute__((aligned(16))) float Sc[T * kLD];   // dS[i][j0 ..]
+  __shared__ __attribute__((aligned(16))) float Qc[T * kLD];   // Q[i][:]
+  __shared__ __attribute__((aligned(16))) float Xs[4 * 16 * 64];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lrow = lane & 31, h = lane >> 5;
+  constexpr int JBn = T / 64;
+  const int bh = blockIdx.x / JBn, jb = blockIdx.x % JBn;
+  const int b = bh / a.H, hd = bh % a.H;
+  const int j0 = jb * 64;
+  const int64_t prow = (int64_t)bh * T * T;
+  load_rows<T, kLD>(a.pd + prow + j0, T, Pc, tid);
+  load_rows<T, kLD>(a.dout + b * a.sob + hd * a.soh, a.soi, Oc, tid);
+  load_rows<T, kLD>(a.ds + prow + j0, T, Sc, tid);
+  load_rows<T, kLD>(a.q + b * a.sqb + hd * a.sqh, a.sqi, Qc, tid);
+  __syncthreads();
+
+  constexpr int NS = T / 64;
+  const int tile = wave & 3, s = wave >> 2;
+  const int wm = (tile >> 1) * 32, wn = (tile & 1) * 32;   // rows: keys j0 + wm, cols: d
+#pragma unroll
+  for (int which = 0; which < 2; ++which) {
+    const float* A = which == 0 ? Pc : Sc;
+    const float* Bm = which == 0 ? Oc : Qc;
+    f32x16 part;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) part[r] = 0.0f;
+    if (s < NS) part = stage_cols(A + wm, kLD, Bm + wn, kLD, s, lrow, h);
+    if (NS == 2 && s == 1)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) Xs[(tile * 16 + r) * 64 + lane] = part[r];
+    __syncthreads();
+    if (s == 0) {
+      f32x16 acc;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[r] = 0.0f + part[r];
+      if (NS == 2)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[r] += Xs[(tile * 16 + r) * 64 + lane];
+      if (which == 0) {
+        float* o = a.dv + b * a.sdvb + hd * a.sdvh;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[(int64_t)(j0 + wm + (r / 4) * 8 + h * 4 + (r % 4)) * a.sdvj + wn + lrow] = acc[r];
+      } else {
+        float* o = a.dk + b * a.sdkb + hd * a.sdkh;
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          o[(int64_t)(j0 + wm + (r / 4) * 8 + h * 4 + (r % 4)) * a.sdkj + (int64_t)(wn + lrow) * a.sdkd] = acc[r];
+      }
+    }
+    __syncthreads();
+  }
+}
+
 }  // namespace
 
 bool attention_supported(int64_t T, int64_t dh) { return dh == kDH && (T == 64 || T == 128); }
@@ -226,6 +469,18 @@ void attention_fwd(const AttnDesc& a, hipStream_t st) {
   if (blocks <= 0) return;
   if (a.T == 128) k_attn_fwd<128><<<blocks, kNT, 0, st>>>(a);
   else k_attn_fwd<64><<<blocks, kNT, 0, st>>>(a);
+}
+
+void attention_bwd(const AttnBwdDesc& a, hipStream_t st) {
+  const int blocks = a.B * a.H * (a.T / kQB);
+  if (blocks <= 0) return;
+  if (a.T == 128) {
+    k_attn_bwd_a<128><<<blocks, kNT, 0, st>>>(a);
+    k_attn_bwd_b<128><<<blocks, kNT, 0, st>>>(a);
+  } else {
+    k_attn_bwd_a<64><<<blocks, kNT, 0, st>>>(a);
+    k_attn_bwd_b<64><<<blocks, kNT, 0, st>>>(a);
+  }
 }
 
 }  // namespace tgk

@@ -170,6 +170,37 @@ struct AttnDesc {
 };
 bool attention_supported(int64_t T, int64_t dh);
 void attention_fwd(const AttnDesc& a, hipStream_t st);
+// Backward of the same chain, given dO: dPd = dO V^T, dP = dropout(dPd) (forward mask),
+// dS = f32(((dP - rowsum(dP * P)) * P) * scale), dQ = dS K, dK = dS^T Q, dV = Pd^T dO.
+// dS is written to `ds` ([B, H, T, T]); dQ, dK, dV through their element strides
+// (b, h, row, d), dQ and dV with unit d stride.
+struct AttnBwdDesc {
+  int B, H, T, dh;
+  const float* dout;
+  int64_t sob, soh, soi;
+  const float* q;
+  int64_t sqb, sqh, sqi;
+  const float* k;
+  int64_t skb, skh, skj;
+  const float* v;
+  int64_t svb, svh, svj;
+  const float* p;
+  const float* pd;
+  float* ds;
+  float* dq;
+  int64_t sdqb, sdqh, sdqi;
+  float* dk;
+  int64_t sdkb, sdkh, sdkj, sdkd;
+  float* dv;
+  int64_t sdvb, sdvh, sdvj;
+  int has_scale;
+  double scale;
+  int has_dropout;
+  double drop_p, drop_scale;
+  uint32_t salt;
+  const int32_t* seed;
+};
+void attention_bwd(const AttnBwdDesc& a, hipStream_t st);
 
 // ---- GEMM (k_gemm.hip) --------------------------------------------------------------
 // C[z][m][n] = sum_k A[z][m][k] * B[z][k][n], f32 MFMA, f32 accumulate.

@@ -278,9 +278,15 @@ class Runtime {
   // [-> dropout] -> matmul_batched(., v), run as one node at the first product.
   struct AttnMatch { int qk, scale, softmax, dropout, pv; };
   std::vector<AttnMatch> attn_;
-  std::vector<int> attn_of_;    // op -> attention match or -1
+  std::vector<int> attn_of_;    // op -> attention match or -1 (forward and backward chains)
   void match_attention();
   void lower_attention(int m);
+  // The backward of a matched chain: dPd = dO V^T, dropout, softmax backward row ops,
+  // dQ = dS K, dK^T = Q^T dS, dV = Pd^T dO, run as one node at its first op.
+  struct AttnBwd { int fwd, first, dpd, dq, dkt, dv, ds_op; std::vector<int> ops; };
+  std::vector<AttnBwd> attn_bwd_;
+  void match_attention_bwd();
+  void lower_attention_bwd(int m);
   // Column sums (sum_to_shape over a leading block of dims of a contiguous tensor): a
   // single-use f32 product feeding one is absorbed (the kernel multiplies), and sums of
   // the same shape whose inputs are ready are launched together.
@@ -788,13 +794,19 @@ void Runtime::lower() {
   }
 
   match_attention();
+  match_attention_bwd();
   match_colsums();
   form_groups();
   for (size_t i = 0; i < ops_.size(); ++i) {
     if (is_leaf((int)i) || virtual_[i]) continue;
     if (adam_ops.count((int)i)) continue;
     if (attn_of_[i] >= 0) {
-      if (attn_[attn_of_[i]].qk == (int)i) lower_attention(attn_of_[i]);
+      const int m = attn_of_[i];
+      if (m < (int)attn_.size()) {
+        if (attn_[m].qk == (int)i) lower_attention(m);
+      } else if (attn_bwd_[m - attn_.size()].first == (int)i) {
+        lower_attention_bwd(m - (int)attn_.size());
+      }
       continue;
     }
     if (mul_absorbed_[i]) continue;
@@ -1472,7 +1484,8 @@ void Runtime::match_colsums() {
 // first product, or itself).
 int Runtime::emit_pos(int op) const {
   if (group_of_[op] >= 0) return groups_[group_of_[op]].first;
-  if (attn_of_[op] >= 0) return attn_[attn_of_[op]].qk;
+  if (attn_of_[op] >= 0)
+    return attn_of_[op] < (int)attn_.size() ? attn_[attn_of_[op]].qk : attn_bwd_[attn_of_[op] - attn_.size()].first;
   return op;
 }
 
@@ -1527,6 +1540,189 @@ void Runtime::lower_colsums(int s0) {
                                  (float*)dptr(out), c.C, c.R, c.C, 1.0, part, counters_ + cbase[q]);
     }
     return [bt](hipStream_t st) { tgk::colsum_batch(bt, st); };
+  };
+  add_node(std::move(n));
+}
+
+void Runtime::match_attention_bwd() {
+  attn_bwd_.clear();
+  if (attn_.empty()) return;
+  auto pinned = [&](int t) {
+    for (int o : outputs_) if (o == t) return true;
+    for (auto& c : captures_) if (c.second == t) return true;
+    for (auto& w : copy_writebacks_) if (w.first == t) return true;
+    return false;
+  };
+  auto out_of = [&](int op) { return O(op).at("out").i32(); };
+  auto only = [&](int t) { return consumers_[t].size() == 1 ? consumers_[t][0] : -1; };
+  // v is a transpose (last two dims) of u, over the same storage
+  auto transposed = [&](int v, int u) {
+    const View &a = view_[v], &b = view_[u];
+    if (a.root != b.root || a.dims.size() != 4 || b.dims.size() != 4) return false;
+    return a.dims[0] == b.dims[0] && a.dims[1] == b.dims[1] && a.dims[2] == b.dims[3] && a.dims[3] == b.dims[2] &&
+           a.strides[0] == b.strides[0] && a.strides[1] == b.strides[1] && a.strides[2] == b.strides[3] &&
+           a.strides[3] == b.strides[2];
+  };
+  auto is_mul_of = [&](int op, int x, int y) {   // op = x * y (either order), f32
+    if (op < 0 || kinds_[op] != "mul") return false;
+    const int a = fld(op, "a"), b = fld(op, "b");
+    return (a == x && b == y) || (a == y && b == x);
+  };
+  for (size_t f = 0; f < attn_.size(); ++f) {
+    const AttnMatch& m = attn_[f];
+    const int q = fld(m.qk, "a"), kt = fld(m.qk, "b"), v = fld(m.pv, "b");
+    const int P = out_of(m.softmax);
+    const int Pd = m.dropout >= 0 ? out_of(m.dropout) : P;
+    AttnBwd bw{(int)f, -1, -1, -1, -1, -1, -1, {}};
+    // dPd = dO @ V^T
+    int dO = -1;
+    for (size_t i = 0; i < ops_.size() && bw.dpd < 0; ++i) {
+      if (kinds_[i] != "matmul_batched" || attn_of_[i] >= 0 || virtual_[i]) continue;
+      if (transposed(fld((int)i, "b"), v)) { bw.dpd = (int)i; dO = fld((int)i, "a"); }
+    }
+    if (bw.dpd < 0) continue;
+    const View& vo = view_[dO];
+    if (vo.dims != view_[v].dims || vo.strides[3] != 1 || vo.strides[0] % 4 || vo.strides[1] % 4 || vo.strides[2] % 4)
+      continue;
+    std::vector<int> chain{bw.dpd};
+    int dP = out_of(bw.dpd);
+    if (pinned(dP)) continue;
+    if (m.dropout >= 0) {
+      const int d = only(dP);
+      if (d < 0 || kinds_[d] != "dropout" || fld(d, "seed") != fld(m.dropout, "seed") ||
+          O(d).at("salt").i64() != O(m.dropout).at("salt").i64() || O(d).at("p").num() != O(m.dropout).at("p").num())
+        continue;
+      chain.push_back(d);
+      dP = out_of(d);
+      if (pinned(dP)) continue;
+    }
+    // softmax backward: s1 = dP - broadcast(reshape(sum_last(dP * P))), dS = s1 * P [* scale]
+    if (consumers_[dP].size() != 2) continue;
+    int m1 = -1, s1 = -1;
+    for (int c : consumers_[dP]) {
+      if (is_mul_of(c, dP, P)) m1 = c;
+      else if (kinds_[c] == "sub" && fld(c, "a") == dP) s1 = c;
+    }
+    if (m1 < 0 || s1 < 0 || pinned(out_of(m1))) continue;
+    const int r1 = only(out_of(m1));
+    if (r1 < 0 || kinds_[r1] != "sum_last" || pinned(out_of(r1))) continue;
+    const int rs = only(out_of(r1));
+    if (rs < 0 || kinds_[rs] != "reshape" || pinned(out_of(rs))) continue;
+    const int bc = only(out_of(rs));
+    if (bc < 0 || kinds_[bc] != "broadcast_to" || pinned(out_of(bc)) || only(out_of(bc)) != s1 ||
+        fld(s1, "b") != out_of(bc))
+      continue;
+    const int m2 = only(out_of(s1));
+    if (!is_mul_of(m2, out_of(s1), P) || pinned(out_of(s1))) continue;
+    chain.insert(chain.end(), {m1, r1, rs, bc, s1, m2});
+    int dS = out_of(m2);
+    if (m.scale >= 0) {
+      const int ms = only(dS);
+      if (ms < 0 || kinds_[ms] != "mul_scalar" || O(ms).at("scalar").num() != O(m.scale).at("scalar").num() ||
+          pinned(dS))
+        continue;
+      chain.push_back(ms);
+      dS = out_of(ms);
+      bw.ds_op = ms;
+    } else {
+      bw.ds_op = m2;
+    }
+    if (pinned(dS) || consumers_[dS].size() != 2) continue;
+    for (int c : consumers_[dS]) {
+      if (kinds_[c] != "matmul_batched" || attn_of_[c] >= 0) continue;
+      if (fld(c, "a") == dS && transposed(fld(c, "b"), kt)) bw.dq = c;
+      else if (fld(c, "b") == dS && transposed(fld(c, "a"), q)) bw.dkt = c;
+    }
+    if (bw.dq < 0 || bw.dkt < 0) continue;
+    // dV = Pd^T dO
+    for (int c : consumers_[dO])
+      if (kinds_[c] == "matmul_batched" && attn_of_[c] < 0 && fld(c, "b") == dO && transposed(fld(c, "a"), Pd))
+        bw.dv = c;
+    if (bw.dv < 0) continue;
+    const View &vq = view_[out_of(bw.dq)], &vk = view_[out_of(bw.dkt)], &vv = view_[out_of(bw.dv)];
+    if (vq.strides[3] != 1 || vv.strides[3] != 1 || vq.dims != vo.dims || vv.dims != vo.dims ||
+        vk.dims != view_[kt].dims)
+      continue;
+    chain.insert(chain.end(), {bw.dq, bw.dkt, bw.dv});
+    bool free_ops = true;
+    for (int op : chain) if (attn_of_[op] >= 0) free_ops = false;
+    if (!free_ops) continue;
+    bw.first = *std::min_element(chain.begin(), chain.end());
+    // everything the node reads exists at its position
+    auto ready = [&](int t) {
+      const int src = T_[view_[t].root].src;
+      return src < 0 || is_leaf(src) || src < bw.first;
+    };
+    if (!ready(dO)) continue;
+    bw.ops = chain;
+    const int id = (int)(attn_.size() + attn_bwd_.size());
+    attn_bwd_.push_back(bw);
+    for (int op : chain) attn_of_[op] = id;
+  }
+}
+
+void Runtime::lower_attention_bwd(int bi) {
+  const AttnBwd bw = attn_bwd_[bi];
+  const AttnMatch m = attn_[bw.fwd];
+  auto out_of = [&](int op) { return O(op).at("out").i32(); };
+  const int q = fld(m.qk, "a"), kt = fld(m.qk, "b"), v = fld(m.pv, "b");
+  const int P = out_of(m.softmax);
+  const int Pd = m.dropout >= 0 ? out_of(m.dropout) : P;
+  const int dO = fld(bw.dpd, "a");
+  const int dS = out_of(bw.ds_op), dQ = out_of(bw.dq), dKt = out_of(bw.dkt), dV = out_of(bw.dv);
+  const int seed = m.dropout >= 0 ? fld(m.dropout, "seed") : -1;
+  const View vq = view_[q], vk = view_[kt], vv = view_[v], vo = view_[dO];
+  const View wq = view_[dQ], wk = view_[dKt], wv = view_[dV];
+  const int64_t B = vq.dims[0], H = vq.dims[1], T = vq.dims[2], dh = vq.dims[3];
+  Node n;
+  n.kind = "attention";
+  n.op = bw.first;
+  n.shape = shape_str(vq.dims) + " T=" + std::to_string(T) + " backward";
+  n.detail = "attention_backward";
+  for (int t : {q, kt, v, P, Pd, dO}) n.reads.push_back(root(t));
+  if (seed >= 0) n.reads.push_back(root(seed));
+  for (int t : {dS, dQ, dKt, dV}) n.writes.push_back(root(t));
+  n.flops = 8.0 * (double)B * H * T * T * dh;
+  n.bytes = 4.0 * (double)B * H * T * (8 * dh + 4 * T);
+  const double scale = m.scale >= 0 ? O(m.scale).at("scalar").num() : 1.0;
+  double dp = 0, dsc = 1;
+  uint32_t salt = 0;
+  if (m.dropout >= 0) {
+    dp = O(m.dropout).at("p").num();
+    dsc = 1.0 / (1.0 - dp);
+    salt = (uint32_t)(uint64_t)std::fmod((double)O(m.dropout).at("salt").i64() * 2654435761.0, 4294967296.0);
+  }
+  n.bind = [=]() -> std::function<void(hipStream_t)> {
+    {
+      int64_t d4[4] = {B, H, T, dh}, dt[4] = {B, H, dh, T};
+      check_span("attention bwd dO", T_[root(dO)].numel, 0, d4, vo.strides.data(), 4);
+      check_span("attention bwd dQ", T_[root(dQ)].numel, 0, d4, wq.strides.data(), 4);
+      check_span("attention bwd dK", T_[root(dKt)].numel, 0, dt, wk.strides.data(), 4);
+      check_span("attention bwd dV", T_[root(dV)].numel, 0, d4, wv.strides.data(), 4);
+      if (T_[root(dS)].numel < B * H * T * T || !view_[dS].contiguous() || view_[dS].root != dS)
+        throw Error(TG_INTERNAL, "attention backward: dS must be a contiguous [B, H, T, T] tensor");
+    }
+    tgk::AttnBwdDesc a{};
+    a.B = (int)B; a.H = (int)H; a.T = (int)T; a.dh = (int)dh;
+    a.dout = (const float*)dptr(dO); a.sob = vo.strides[0]; a.soh = vo.strides[1]; a.soi = vo.strides[2];
+    a.q = (const float*)dptr(q); a.sqb = vq.strides[0]; a.sqh = vq.strides[1]; a.sqi = vq.strides[2];
+    a.k = (const float*)dptr(kt); a.skb = vk.strides[0]; a.skh = vk.strides[1]; a.skj = vk.strides[3];
+    a.v = (const float*)dptr(v); a.svb = vv.strides[0]; a.svh = vv.strides[1]; a.svj = vv.strides[2];
+    a.p = (const float*)dptr(P);
+    a.pd = (const float*)dptr(Pd);
+    a.ds = (float*)dptr(dS);
+    a.dq = (float*)dptr(dQ); a.sdqb = wq.strides[0]; a.sdqh = wq.strides[1]; a.sdqi = wq.strides[2];
+    a.dk = (float*)dptr(dKt); a.sdkb = wk.strides[0]; a.sdkh = wk.strides[1]; a.sdkj = wk.strides[3];
+    a.sdkd = wk.strides[2];
+    a.dv = (float*)dptr(dV); a.sdvb = wv.strides[0]; a.sdvh = wv.strides[1]; a.sdvj = wv.strides[2];
+    a.has_scale = m.scale >= 0;
+    a.scale = scale;
+    a.has_dropout = m.dropout >= 0;
+    a.drop_p = dp;
+    a.drop_scale = dsc;
+    a.salt = salt;
+    a.seed = seed >= 0 ? (const int32_t*)dptr(seed) : nullptr;
+    return [a](hipStream_t st) { tgk::attention_bwd(a, st); };
   };
   add_node(std::move(n));
 }

@@ -13,7 +13,8 @@ from _helpers import make_range, wire
 from tensorgrad_amd import backend
 from tensorgrad_amd import ir as IR
 from tensorgrad_amd import ops as O
-from tensorgrad_amd.trace import tensor_input, trace_fn
+from tensorgrad_amd.grad import append_grad
+from tensorgrad_amd.trace import param_input, tensor_input, trace_fn
 
 pytestmark = pytest.mark.gpu
 
@@ -355,6 +356,59 @@ def test_fused_attention(B, H, T, what):
         gemm_close(got, want)
     else:
         assert np.allclose(got, want, rtol=1e-5, atol=1e-7), np.max(np.abs(got.astype(np.float64) - want))
+
+
+def _attention_grad(B, H, T, dh, which, params, g_in, env=None):
+    """d(sum(attention(q, k, v) * g)) / d`which` on the native runtime, with the graph."""
+    def body():
+        q, k, v = (param_input(n, [B, H, T, dh]) for n in ('q', 'k', 'v'))
+        s = O.matmul(q, O.permute(k, [0, 1, 3, 2]))
+        p = O.softmax_causal(O.mul(s, 0.125))
+        o = O.matmul(O.dropout(p, 0.1), v)
+        return O.sum_(O.mul(o, tensor_input('g', [B, H, T, dh])))
+    g = trace_fn(body)
+    gr = append_grad(g)
+    g.outputs = [gr.param_grads[which].id]
+    w = wire(g, gr.param_grads)
+    import os
+    old = {k: os.environ.get(k) for k in (env or {})}
+    os.environ.update(env or {})
+    try:
+        rt = backend.NativeRuntime(IR.dumps(w))
+    finally:
+        for k, v in old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+    ops = [n.get('ops', '') for n in rt.describe()['nodes']]
+    rt.upload_params(params)
+    got = rt.run({'g': g_in}, [B, H, T, dh], np.float32)
+    rt.destroy()
+    return got, ops, w
+
+
+@pytest.mark.parametrize('B,H,T', [(2, 3, 64), (2, 3, 128), (32, 4, 128)])
+def test_fused_attention_backward(B, H, T):
+    """The fused attention backward (dPd = dO V^T, dropout and softmax backward row math,
+    dQ = dS K, dK = dS^T Q, dV = Pd^T dO in two launches) for the gradients of q, k and v,
+    against the oracle (GEMM tolerance) and, at the transformer's shape, bit for bit against
+    the unfused kernels, whose tiles use the k-blocking the fused kernels follow."""
+    dh = 64
+    params = {n: _rand([B, H, T, dh], s, -2, 2) for n, s in (('q', 71), ('k', 72), ('v', 73))}
+    g_in = _rand([B, H, T, dh], 74)
+    for which in ('q', 'k', 'v'):
+        got, ops, w = _attention_grad(B, H, T, dh, which, params, g_in)
+        assert 'attention_backward' in ops
+        ref, ops0, _ = _attention_grad(B, H, T, dh, which, params, g_in, {'TG_ATTN': '0'})
+        assert 'attention_backward' not in ops0
+        if B * H == 128 and T == 128:
+            exact(got, ref)
+        o = pyoracle.OracleRuntime(w)
+        for k, v in params.items():
+            o.set_home(k, v)
+        o.run({'g': g_in})
+        gemm_close(got, o.output(), 1e-5)
 
 
 GEMMS = [([5, 7], [7, 3], False, False), ([2, 33, 65], [65, 17], False, False), ([129, 64], [64, 300], False, False),
