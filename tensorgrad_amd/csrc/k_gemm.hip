@@ -261,28 +261,20 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g) {
 //    halves of the banks.
 // Used when K (per split) is a multiple of BK, rows of the row-contiguous operand are a
 // multiple of 4 and both operands are 16-byte aligned; rows past M / N are read clamped
-// to the last row (their results are never stored).
+// to the last row (their results are never stored). Tiles with a 128-wide side run eight
+// wavefronts (two per SIMD, 64 x 32 or 32 x 32 each), so one wavefront's barrier wait,
+// partial-sum adds and LDS latency overlap the other's MFMAs; 64 x 64 tiles run four.
+// Loads address the tile through a wave-uniform base (SGPRs, advanced per stage) plus a
+// fixed 32-bit per-lane offset.
 constexpr int kLdsBlock = 256;   // floats one wavefront-wide DMA writes (1 KiB)
 
-// One wavefront-wide global_load_lds_dwordx4: lane l's 16 bytes from gp land at
-// lds + 16 l. Issued from inline assembly so the compiler does not treat it as an LDS
-// write of unknown extent: for such writes it drains every outstanding load before the
-// next LDS read, which would expose the full load latency at every pipeline stage. The
-// kernel orders LDS reads itself (explicit vmcnt waits and barriers). M0 takes the
-// wave-uniform LDS base; one wait state separates the M0 write from the load.
-__device__ __forceinline__ void dma16(const float* gp, float* lds) {
-  const uint32_t base =
-      __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)lds);
-  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gp), "{m0}"(base));
-}
-
-template <int ROWS, int BK, bool KFAST>
+template <int ROWS, int BK, bool KFAST, int NT>
 struct DTile {
   static constexpr int CPR = KFAST ? BK / 4 : ROWS / 4;   // 16-byte chunks per LDS row
   static constexpr int NCH = ROWS * BK / 4;               // chunks per tile
-  static constexpr int PER = NCH / kThreads;              // DMA instructions per thread
+  static constexpr int PER = NCH / NT;                    // DMA instructions per thread
   static constexpr int SIZE = ROWS * BK;                  // floats
-  static_assert(NCH % kThreads == 0, "tile must be a whole number of DMA rounds");
+  static_assert(NCH % NT == 0, "tile must be a whole number of DMA rounds");
   static_assert(KFAST ? (BK == 32 || BK == 64) : ROWS >= 64, "swizzle needs 8 / 16 chunks per row");
 
   __device__ __forceinline__ static int swz(int lrow) {
@@ -290,24 +282,41 @@ struct DTile {
     return ((lrow >> 2) & 1) << 3;
   }
 
-  __device__ __forceinline__ static void dma(const float* X, int64_t sr, int64_t sk, int64_t r0, int64_t rlim,
-                                             int64_t k0, float* L, int tid) {
+  // Per-thread byte offsets of this thread's PER chunks from the tile origin (row r0,
+  // k = k0); fixed for the whole k loop. Rows past `rlim` read the last row.
+  __device__ __forceinline__ static void offsets(int64_t sr, int64_t sk, int64_t r0, int64_t rlim, int tid,
+                                                 uint32_t* off) {
     const int lane = tid & 63, wave = tid >> 6;
 #pragma unroll
     for (int e = 0; e < PER; ++e) {
-      const int inst = e * (kThreads / 64) + wave;
+      const int inst = e * (NT / 64) + wave;
       const int P = inst * 64 + lane;
       const int row = P / CPR, pc = P % CPR;
       const int c = pc ^ swz(row);
-      const float* gp;
       if (KFAST) {
-        const int64_t gr = min(r0 + row, rlim - 1);
-        gp = X + gr * sr + k0 + c * 4;
+        const int64_t gr = min(r0 + row, rlim - 1) - r0;
+        off[e] = (uint32_t)((gr * sr + c * 4) * 4);
       } else {
-        const int64_t gr = min(r0 + c * 4, rlim - 4);
-        gp = X + (k0 + row) * sk + gr;
+        const int64_t gr = min(r0 + c * 4, rlim - 4) - r0;
+        off[e] = (uint32_t)((row * sk + gr) * 4);
       }
-      dma16(gp, L + inst * kLdsBlock);
+    }
+  }
+
+  // Issue this thread's chunks of one stage: global base `gb` (tile origin of the stage,
+  // wave-uniform, in SGPRs) plus the 32-bit per-lane offsets; LDS byte address `lds` of the
+  // stage's slot and the wave index `wave`, both wave-uniform, so M0 is scalar arithmetic.
+  // Each global_load_lds_dwordx4 moves lane l's 16 bytes to M0 + 16 l. It is issued from
+  // inline assembly so the compiler does not treat it as an LDS write of unknown extent:
+  // for such writes it drains every outstanding load before the next LDS read, which would
+  // expose the full load latency at every pipeline stage. The kernel orders LDS reads
+  // itself (explicit vmcnt waits and barriers). One wait state separates the M0 write from
+  // the load.
+  __device__ __forceinline__ static void dma(const float* gb, const uint32_t* off, uint32_t lds, int wave) {
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+      const uint32_t m0v = lds + (uint32_t)((e * (NT / 64) + wave) * kLdsBlock * 4);
+      asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off[e]), "s"(gb), "{m0}"(m0v));
     }
   }
 
@@ -331,13 +340,17 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-template <int BM, int BN, int BK, int NS, bool AK, bool BKF>
-__global__ __launch_bounds__(kThreads) void k_gemm_dma(GemmArgs g) {
-  constexpr int WM = BM / 2, WN = BN / 2;
+template <int BM, int BN, int BK, int NS, bool AK, bool BKF, int NT>
+__global__ __launch_bounds__(NT) void k_gemm_dma(GemmArgs g) {
+  // wavefront grid over the tile: 4 waves 2 x 2; 8 waves 2 x 4 (BN = 128) or 4 x 2
+  constexpr int NW = NT / 64;
+  constexpr int WGM = NW == 8 && BN == 64 ? 4 : 2, WGN = NW / WGM;
+  constexpr int WM = BM / WGM, WN = BN / WGN;
   constexpr int TM = WM / 32, TN = WN / 32;
+  static_assert(TM >= 1 && TN >= 1, "wave tile below 32 x 32");
   constexpr int NG = BK / 8;
-  using TA = DTile<BM, BK, AK>;
-  using TB = DTile<BN, BK, BKF>;
+  using TA = DTile<BM, BK, AK, NT>;
+  using TB = DTile<BN, BK, BKF, NT>;
   constexpr int PER = TA::PER + TB::PER;
   static_assert(PER * (NS - 1) < 64, "too many loads in flight for vmcnt");
   __shared__ __attribute__((aligned(16))) float As[NS * TA::SIZE];   // NS stages of A
@@ -347,7 +360,7 @@ __global__ __launch_bounds__(kThreads) void k_gemm_dma(GemmArgs g) {
   const int tid = threadIdx.x;
   const int lane = tid % 64;
   const int wave = tid / 64;
-  const int wm0 = (wave / 2) * WM, wn0 = (wave % 2) * WN;
+  const int wm0 = (wave / WGN) * WM, wn0 = (wave % WGN) * WN;
 
   const uint32_t nblk = gridDim.x;
   uint32_t b = blockIdx.x;
@@ -365,12 +378,20 @@ __global__ __launch_bounds__(kThreads) void k_gemm_dma(GemmArgs g) {
   const int64_t kbeg = split * g.k_per_split;
   const int64_t kend = min(d.K, kbeg + g.k_per_split);
   const int nst = kbeg < kend ? (int)((kend - kbeg) / BK) : 0;
-
+  // Operand bases of stage 0 and the per-stage advance, all wave-uniform.
+  const float* a0 = A + m0 * (AK ? d.sAm : 1) + kbeg * (AK ? 1 : d.sAk);
+  const float* b0 = B + n0 * (BKF ? d.sBn : 1) + kbeg * (BKF ? 1 : d.sBk);
+  const int64_t a_step = AK ? BK : BK * d.sAk, b_step = BKF ? BK : BK * d.sBk;
+  uint32_t offa[TA::PER], offb[TB::PER];
+  TA::offsets(d.sAm, d.sAk, m0, d.M, tid, offa);
+  TB::offsets(d.sBn, d.sBk, n0, d.N, tid, offb);
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  const uint32_t lds_a = (uint32_t)(uintptr_t)((__attribute__((address_space(3))) float*)As);
+  const uint32_t lds_b = (uint32_t)(uintptr_t)((__attribute__((address_space(3))) float*)Bs);
   auto issue = [&](int st) {
     const int slot = st % NS;
-    const int64_t k0 = kbeg + (int64_t)st * BK;
-    TA::dma(A, d.sAm, d.sAk, m0, d.M, k0, As + slot * TA::SIZE, tid);
-    TB::dma(B, d.sBn, d.sBk, n0, d.N, k0, Bs + slot * TB::SIZE, tid);
+    TA::dma(a0 + st * a_step, offa, lds_a + slot * TA::SIZE * 4, wv);
+    TB::dma(b0 + st * b_step, offb, lds_b + slot * TB::SIZE * 4, wv);
   };
 
   f32x16 acc[TM][TN];
@@ -385,6 +406,7 @@ __global__ __launch_bounds__(kThreads) void k_gemm_dma(GemmArgs g) {
 #pragma unroll
   for (int p = 0; p < NS - 1; ++p)
     if (p < nst) issue(p);
+
   for (int st = 0; st < nst; ++st) {
     // Stage st has landed once at most (stages issued after it) * PER loads are pending.
     const int after = min(NS - 2, nst - 1 - st);
@@ -526,6 +548,10 @@ bool dma_ok(const GemmDesc& d, const Plan& p, bool ak, bool bk) {
   else if (!(d.sAm == 1 && (d.sAk & 3) == 0 && d.M % 4 == 0)) return false;
   if (bk) { if (d.sBn & 3) return false; }
   else if (!(d.sBn == 1 && (d.sBk & 3) == 0 && d.N % 4 == 0)) return false;
+  // per-lane byte offsets from the tile origin stay below 2^31
+  const int64_t span = 128;   // rows (k-contiguous) or k rows (row-contiguous) of a tile, at most
+  if ((ak ? d.sAm : d.sAk) * span * 4 >= (int64_t(1) << 31)) return false;
+  if ((bk ? d.sBn : d.sBk) * span * 4 >= (int64_t(1) << 31)) return false;
   return true;
 }
 
@@ -553,17 +579,17 @@ void gemm(const GemmDesc& d, float* work, hipStream_t st) {
   const bool ak = d.sAk == 1;
   const bool bk = d.sBk == 1 && d.sBn != 1;
   if (dma_ok(d, p, ak, bk)) {
-#define TG_DMA_LAUNCH(BM_, BN_, BK_)                                                           \
+#define TG_DMA_LAUNCH(BM_, BN_, BK_, NT_)                                                      \
   do {                                                                                       \
-    if (ak && bk) k_gemm_dma<BM_, BN_, BK_, 3, true, true><<<grid, kThreads, 0, st>>>(g);     \
-    else if (ak) k_gemm_dma<BM_, BN_, BK_, 3, true, false><<<grid, kThreads, 0, st>>>(g);     \
-    else if (bk) k_gemm_dma<BM_, BN_, BK_, 3, false, true><<<grid, kThreads, 0, st>>>(g);     \
-    else k_gemm_dma<BM_, BN_, BK_, 3, false, false><<<grid, kThreads, 0, st>>>(g);            \
+    if (ak && bk) k_gemm_dma<BM_, BN_, BK_, 3, true, true, NT_><<<grid, NT_, 0, st>>>(g);     \
+    else if (ak) k_gemm_dma<BM_, BN_, BK_, 3, true, false, NT_><<<grid, NT_, 0, st>>>(g);     \
+    else if (bk) k_gemm_dma<BM_, BN_, BK_, 3, false, true, NT_><<<grid, NT_, 0, st>>>(g);     \
+    else k_gemm_dma<BM_, BN_, BK_, 3, false, false, NT_><<<grid, NT_, 0, st>>>(g);            \
   } while (0)
-    if (p.bm == 128 && p.bn == 128) TG_DMA_LAUNCH(128, 128, 32);
-    else if (p.bm == 128) TG_DMA_LAUNCH(128, 64, 32);
-    else if (p.bn == 128) TG_DMA_LAUNCH(64, 128, 32);
-    else TG_DMA_LAUNCH(64, 64, 64);
+    if (p.bm == 128 && p.bn == 128) TG_DMA_LAUNCH(128, 128, 32, 512);
+    else if (p.bm == 128) TG_DMA_LAUNCH(128, 64, 32, 512);
+    else if (p.bn == 128) TG_DMA_LAUNCH(64, 128, 32, 512);
+    else TG_DMA_LAUNCH(64, 64, 64, 256);
 #undef TG_DMA_LAUNCH
   } else {
 #define TG_GEMM_LAUNCH(BM_, BN_, BK_)                                                      \
