@@ -340,26 +340,36 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-template <int BM, int BN, int BK, int NS, bool AK, bool BKF, int NT>
+// KG = 2 splits the k stages of a tile between two groups of four wavefronts by parity
+// (group g multiplies stages g, g + 2, ...; NS slots, NS / 2 per group), for 64 x 64 tiles
+// that have no second 32-column or 32-row wave tile to give a second wavefront per SIMD.
+// The groups' sums meet at the end as (stages 0, 2, ..) + (stages 1, 3, ..); with two
+// stages that is the single group's (0 + stage 0) + stage 1.
+template <int BM, int BN, int BK, int NS, bool AK, bool BKF, int NT, int KG>
 __global__ __launch_bounds__(NT) void k_gemm_dma(GemmArgs g) {
-  // wavefront grid over the tile: 4 waves 2 x 2; 8 waves 2 x 4 (BN = 128) or 4 x 2
-  constexpr int NW = NT / 64;
+  // per k group: 4 waves 2 x 2; 8 waves 2 x 4 (BN = 128) or 4 x 2
+  constexpr int GT = NT / KG;             // threads per k group
+  constexpr int NW = GT / 64;
   constexpr int WGM = NW == 8 && BN == 64 ? 4 : 2, WGN = NW / WGM;
   constexpr int WM = BM / WGM, WN = BN / WGN;
   constexpr int TM = WM / 32, TN = WN / 32;
   static_assert(TM >= 1 && TN >= 1, "wave tile below 32 x 32");
+  static_assert(KG == 1 || (KG == 2 && NS % 2 == 0), "k groups take alternate slots");
+  constexpr int NSG = NS / KG;            // slots per k group
   constexpr int NG = BK / 8;
-  using TA = DTile<BM, BK, AK, NT>;
-  using TB = DTile<BN, BK, BKF, NT>;
+  using TA = DTile<BM, BK, AK, GT>;
+  using TB = DTile<BN, BK, BKF, GT>;
   constexpr int PER = TA::PER + TB::PER;
-  static_assert(PER * (NS - 1) < 64, "too many loads in flight for vmcnt");
+  static_assert(PER * (NSG - 1) < 64, "too many loads in flight for vmcnt");
   __shared__ __attribute__((aligned(16))) float As[NS * TA::SIZE];   // NS stages of A
   __shared__ __attribute__((aligned(16))) float Bs[NS * TB::SIZE];   // NS stages of B
 
   const GemmDesc& d = g.d;
   const int tid = threadIdx.x;
   const int lane = tid % 64;
-  const int wave = tid / 64;
+  const int kg = __builtin_amdgcn_readfirstlane(tid / GT);   // k group (wave-uniform)
+  const int gtid = tid % GT;
+  const int wave = gtid / 64;             // wave within the k group
   const int wm0 = (wave / WGN) * WM, wn0 = (wave % WGN) * WN;
 
   const uint32_t nblk = gridDim.x;
@@ -383,8 +393,8 @@ __global__ __launch_bounds__(NT) void k_gemm_dma(GemmArgs g) {
   const float* b0 = B + n0 * (BKF ? d.sBn : 1) + kbeg * (BKF ? 1 : d.sBk);
   const int64_t a_step = AK ? BK : BK * d.sAk, b_step = BKF ? BK : BK * d.sBk;
   uint32_t offa[TA::PER], offb[TB::PER];
-  TA::offsets(d.sAm, d.sAk, m0, d.M, tid, offa);
-  TB::offsets(d.sBn, d.sBk, n0, d.N, tid, offb);
+  TA::offsets(d.sAm, d.sAk, m0, d.M, gtid, offa);
+  TB::offsets(d.sBn, d.sBk, n0, d.N, gtid, offb);
   const int wv = __builtin_amdgcn_readfirstlane(wave);
   const uint32_t lds_a = (uint32_t)(uintptr_t)((__attribute__((address_space(3))) float*)As);
   const uint32_t lds_b = (uint32_t)(uintptr_t)((__attribute__((address_space(3))) float*)Bs);
@@ -403,26 +413,31 @@ __global__ __launch_bounds__(NT) void k_gemm_dma(GemmArgs g) {
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
   const int lrow = lane % 32, h = lane / 32;
+  // this group's stages are kg, kg + KG, ...; it keeps NSG - 1 of them in flight
 #pragma unroll
-  for (int p = 0; p < NS - 1; ++p)
-    if (p < nst) issue(p);
+  for (int p = 0; p < NSG - 1; ++p)
+    if (kg + p * KG < nst) issue(kg + p * KG);
 
-  for (int st = 0; st < nst; ++st) {
-    // Stage st has landed once at most (stages issued after it) * PER loads are pending.
-    const int after = min(NS - 2, nst - 1 - st);
-    if (NS >= 5 && after >= 3) wait_vmcnt<(NS >= 5 ? 3 : 0) * PER>();
-    else if (NS >= 4 && after >= 2) wait_vmcnt<(NS >= 4 ? 2 : 0) * PER>();
-    else if (NS >= 3 && after >= 1) wait_vmcnt<PER>();
+  const int nit = (nst + KG - 1) / KG;
+  const int mine = nst > kg ? (nst - 1 - kg) / KG : -1;   // this group's last iteration
+  for (int it = 0; it < nit; ++it) {
+    const int st = it * KG + kg;
+    // Stage st has landed once at most (own stages issued after it) * PER loads are pending.
+    const int after = min(NSG - 2, mine - it);
+    if (NSG >= 4 && after >= 3) wait_vmcnt<(NSG >= 4 ? 3 : 0) * PER>();
+    else if (NSG >= 3 && after >= 2) wait_vmcnt<(NSG >= 3 ? 2 : 0) * PER>();
+    else if (after >= 1) wait_vmcnt<PER>();
     else wait_vmcnt<0>();
     // A bare workgroup barrier: __syncthreads() would also drain every outstanding load
     // (the stages still in flight). The empty asm statements keep the compiler from
     // moving LDS accesses across it; each wave has already waited for its own copies of
     // stage st, and its reads of the slot about to be refilled were consumed by the MFMAs
-    // of the previous stage.
+    // of its group's previous stage.
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    if (st + NS - 1 < nst) issue(st + NS - 1);
+    if (st >= nst) continue;              // the other group's last stage (odd count)
+    if (st + (NSG - 1) * KG < nst) issue(st + (NSG - 1) * KG);
     const float* Ac = As + (st % NS) * TA::SIZE;
     const float* Bc = Bs + (st % NS) * TB::SIZE;
     f32x16 part[TM][TN];
@@ -461,6 +476,29 @@ __global__ __launch_bounds__(NT) void k_gemm_dma(GemmArgs g) {
     for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int j = 0; j < TN; ++j) acc[i][j] += part[i][j];
+  }
+
+  if (KG == 2) {
+    // group 1 hands its sums to group 0 through LDS (the A ring, free after the barrier)
+    static_assert(KG == 1 || NW * TM * TN * 16 * 64 <= NS * TA::SIZE, "exchange fits the A ring");
+    __syncthreads();
+    float* X = As;
+    if (kg == 1) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) X[(((wave * TM + i) * TN + j) * 16 + r) * 64 + lane] = acc[i][j][r];
+    }
+    __syncthreads();
+    if (kg == 1) return;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] += X[(((wave * TM + i) * TN + j) * 16 + r) * 64 + lane];
   }
 
   float* O;
@@ -579,17 +617,17 @@ void gemm(const GemmDesc& d, float* work, hipStream_t st) {
   const bool ak = d.sAk == 1;
   const bool bk = d.sBk == 1 && d.sBn != 1;
   if (dma_ok(d, p, ak, bk)) {
-#define TG_DMA_LAUNCH(BM_, BN_, BK_, NT_)                                                      \
-  do {                                                                                       \
-    if (ak && bk) k_gemm_dma<BM_, BN_, BK_, 3, true, true, NT_><<<grid, NT_, 0, st>>>(g);     \
-    else if (ak) k_gemm_dma<BM_, BN_, BK_, 3, true, false, NT_><<<grid, NT_, 0, st>>>(g);     \
-    else if (bk) k_gemm_dma<BM_, BN_, BK_, 3, false, true, NT_><<<grid, NT_, 0, st>>>(g);     \
-    else k_gemm_dma<BM_, BN_, BK_, 3, false, false, NT_><<<grid, NT_, 0, st>>>(g);            \
+#define TG_DMA_LAUNCH(BM_, BN_, BK_, NS_, NT_, KG_)                                                  \
+  do {                                                                                             \
+    if (ak && bk) k_gemm_dma<BM_, BN_, BK_, NS_, true, true, NT_, KG_><<<grid, NT_, 0, st>>>(g);     \
+    else if (ak) k_gemm_dma<BM_, BN_, BK_, NS_, true, false, NT_, KG_><<<grid, NT_, 0, st>>>(g);     \
+    else if (bk) k_gemm_dma<BM_, BN_, BK_, NS_, false, true, NT_, KG_><<<grid, NT_, 0, st>>>(g);     \
+    else k_gemm_dma<BM_, BN_, BK_, NS_, false, false, NT_, KG_><<<grid, NT_, 0, st>>>(g);            \
   } while (0)
-    if (p.bm == 128 && p.bn == 128) TG_DMA_LAUNCH(128, 128, 32, 512);
-    else if (p.bm == 128) TG_DMA_LAUNCH(128, 64, 32, 512);
-    else if (p.bn == 128) TG_DMA_LAUNCH(64, 128, 32, 512);
-    else TG_DMA_LAUNCH(64, 64, 64, 256);
+    if (p.bm == 128 && p.bn == 128) TG_DMA_LAUNCH(128, 128, 32, 3, 512, 1);
+    else if (p.bm == 128) TG_DMA_LAUNCH(128, 64, 32, 3, 512, 1);
+    else if (p.bn == 128) TG_DMA_LAUNCH(64, 128, 32, 3, 512, 1);
+    else TG_DMA_LAUNCH(64, 64, 64, 4, 512, 2);
 #undef TG_DMA_LAUNCH
   } else {
 #define TG_GEMM_LAUNCH(BM_, BN_, BK_)                                                      \
