@@ -345,8 +345,16 @@ __device__ __forceinline__ void wait_vmcnt() {
 // that have no second 32-column or 32-row wave tile to give a second wavefront per SIMD.
 // The groups' sums meet at the end as (stages 0, 2, ..) + (stages 1, 3, ..); with two
 // stages that is the single group's (0 + stage 0) + stage 1.
+// Block b of the launch -> tile number: consecutive tile numbers go to one XCD (the
+// hardware deals blocks to the XCDs round-robin), so tiles sharing operand rows or
+// columns share an L2.
+__device__ __forceinline__ uint32_t xcd_order(uint32_t b, uint32_t nblk) {
+  return nblk % kXcds == 0 ? (b % kXcds) * (nblk / kXcds) + b / kXcds : b;
+}
+
+// One output tile (tile number b of the problem g).
 template <int BM, int BN, int BK, int NS, bool AK, bool BKF, int NT, int KG>
-__global__ __launch_bounds__(NT) void k_gemm_dma(GemmArgs g) {
+__device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint32_t b) {
   // per k group: 4 waves 2 x 2; 8 waves 2 x 4 (BN = 128) or 4 x 2
   constexpr int GT = NT / KG;             // threads per k group
   constexpr int NW = GT / 64;
@@ -372,9 +380,6 @@ __global__ __launch_bounds__(NT) void k_gemm_dma(GemmArgs g) {
   const int wave = gtid / 64;             // wave within the k group
   const int wm0 = (wave / WGN) * WM, wn0 = (wave % WGN) * WN;
 
-  const uint32_t nblk = gridDim.x;
-  uint32_t b = blockIdx.x;
-  if (nblk % kXcds == 0) b = (b % kXcds) * (nblk / kXcds) + b / kXcds;
   const uint32_t tn = b % g.tiles_n;
   const uint32_t rest = b / g.tiles_n;
   const uint32_t tm = rest % g.tiles_m;
@@ -524,6 +529,24 @@ __global__ __launch_bounds__(NT) void k_gemm_dma(GemmArgs g) {
     }
 }
 
+template <int BM, int BN, int BK, int NS, bool AK, bool BKF, int NT, int KG>
+__global__ __launch_bounds__(NT) void k_gemm_dma(GemmArgs g) {
+  gemm_tile<BM, BN, BK, NS, AK, BKF, NT, KG>(g, xcd_order(blockIdx.x, gridDim.x));
+}
+
+// Several independent problems in one launch: problem p owns tile numbers
+// [starts[p], starts[p + 1]); the table lives in device memory (uniform scalar loads).
+template <int BM, int BN, int BK, int NS, bool AK, bool BKF, int NT, int KG>
+__global__ __launch_bounds__(NT) void k_gemm_dma_group(const GemmArgs* __restrict__ table,
+                                                       const uint32_t* __restrict__ starts, int n) {
+  const uint32_t b = xcd_order(blockIdx.x, gridDim.x);
+  int p = 0;
+  for (int q = 1; q < n; ++q)
+    if (starts[q] <= b) p = q;
+  const GemmArgs g = table[p];
+  gemm_tile<BM, BN, BK, NS, AK, BKF, NT, KG>(g, b - starts[p]);
+}
+
 // Sum split-K partials in split order into C (eight partial loads in flight per thread).
 __global__ void k_splitk_reduce(const float* __restrict__ work, int splits, int64_t sOs, GemmDesc d) {
   const int64_t MN = d.M * d.N, total = MN * d.batch;
@@ -648,6 +671,56 @@ void gemm(const GemmDesc& d, float* work, hipStream_t st) {
     int64_t nb = (total + 255) / 256;
     if (nb > 4096) nb = 4096;
     k_splitk_reduce<<<(int)nb, 256, 0, st>>>(work, p.splits, g.sOs, d);
+  }
+}
+
+// ---- grouped GEMMs ---------------------------------------------------------------------
+// Problems of one group launch run whole-K 64 x 64 tiles (two k groups of four wavefronts),
+// so weight gradients with few output tiles fill the chip together instead of each
+// splitting K.
+
+int gemm_group_kind(const GemmDesc& d) {
+  if (d.M <= 0 || d.N <= 0 || d.batch <= 0 || d.K <= 0) return -1;
+  const Plan p{64, 64, 64, 1, d.K};
+  const bool ak = d.sAk == 1;
+  const bool bk = d.sBk == 1 && d.sBn != 1;
+  if (!dma_ok(d, p, ak, bk)) return -1;
+  return (ak ? 2 : 0) + (bk ? 1 : 0);
+}
+
+size_t gemm_group_table(const GemmDesc* ds, int n, std::vector<unsigned char>& image, int64_t& blocks) {
+  const size_t args_bytes = (size_t)n * sizeof(GemmArgs);
+  const size_t starts_off = (args_bytes + 15) / 16 * 16;
+  image.assign(starts_off + (size_t)(n + 1) * sizeof(uint32_t), 0);
+  GemmArgs* args = reinterpret_cast<GemmArgs*>(image.data());
+  uint32_t* starts = reinterpret_cast<uint32_t*>(image.data() + starts_off);
+  int64_t t = 0;
+  for (int q = 0; q < n; ++q) {
+    const GemmDesc& d = ds[q];
+    GemmArgs g{d, d.K, 1, 0, 0, nullptr, 0, 0};
+    g.tiles_n = (int)((d.N + 63) / 64);
+    g.tiles_m = (int)((d.M + 63) / 64);
+    args[q] = g;
+    starts[q] = (uint32_t)t;
+    t += (int64_t)g.tiles_n * g.tiles_m * d.batch;
+  }
+  starts[n] = (uint32_t)t;
+  if (t >= (int64_t(1) << 31)) throw std::runtime_error("gemm group: too many tiles");
+  blocks = t;
+  return starts_off;
+}
+
+void gemm_group(const void* dev_image, size_t starts_off, int n, int64_t blocks, int kind, hipStream_t st) {
+  if (n <= 0 || blocks <= 0) return;
+  const GemmArgs* table = reinterpret_cast<const GemmArgs*>(dev_image);
+  const uint32_t* starts = reinterpret_cast<const uint32_t*>(reinterpret_cast<const unsigned char*>(dev_image) + starts_off);
+  const dim3 grid((unsigned)blocks);
+  switch (kind) {
+    case 3: k_gemm_dma_group<64, 64, 64, 4, true, true, 512, 2><<<grid, 512, 0, st>>>(table, starts, n); break;
+    case 2: k_gemm_dma_group<64, 64, 64, 4, true, false, 512, 2><<<grid, 512, 0, st>>>(table, starts, n); break;
+    case 1: k_gemm_dma_group<64, 64, 64, 4, false, true, 512, 2><<<grid, 512, 0, st>>>(table, starts, n); break;
+    case 0: k_gemm_dma_group<64, 64, 64, 4, false, false, 512, 2><<<grid, 512, 0, st>>>(table, starts, n); break;
+    default: throw std::runtime_error("gemm group: bad kind");
   }
 }
 

@@ -4,6 +4,7 @@
 #pragma once
 #include <hip/hip_runtime.h>
 #include <cstdint>
+#include <vector>
 
 #include "fused_dev.h"
 
@@ -215,6 +216,14 @@ struct GemmDesc {
 // `work` must hold gemm_workspace_floats(d) floats (split-K partials).
 int64_t gemm_workspace_floats(const GemmDesc& d);
 void gemm(const GemmDesc& d, float* work, hipStream_t st);
+// Grouped launch of independent GEMMs (whole-K 64 x 64 tiles, no split-K). Problems of one
+// launch share a kind: gemm_group_kind(d) is 0..3, or -1 when d cannot run grouped.
+// gemm_group_table fills the device image of the problem table (returns the offset of
+// its tile-start array, sets the launch's block count); the image must be copied to
+// device memory and stay there while the launch can run.
+int gemm_group_kind(const GemmDesc& d);
+size_t gemm_group_table(const GemmDesc* ds, int n, std::vector<unsigned char>& image, int64_t& blocks);
+void gemm_group(const void* dev_image, size_t starts_off, int n, int64_t blocks, int kind, hipStream_t st);
 
 // Embedding pattern: out[r, :] = table[idx[r], :] (zero row when idx out of range).
 void gather_rows(const int32_t* idx, int64_t rows, const float* table, int64_t V, int64_t N, float* out,

@@ -365,12 +365,27 @@ class Runtime {
                     int64_t& bdiv, int64_t& s0, int64_t& s1, int64_t& sr, int64_t& sc, bool transposeOk) const;
   void add_node(Node n) { nodes_.push_back(std::move(n)); }
   void lower_op(int i);
+
+  // GEMMs whose results only the fused optimizer reads (weight gradients) and that would
+  // split K run together just before it: one grouped launch per operand-layout kind, with
+  // whole-K tiles, instead of one launch plus a split-K reduction each.
+  struct DeferredGemm { int op; tgk::GemmDesc d; int a, b, out, kind; };
+  std::vector<DeferredGemm> deferred_gemms_;
+  std::vector<char> defer_gemm_;     // op -> runs in a grouped launch
+  std::set<int> adam_ops_;
+  void plan_gemm_groups();
+  bool use_gemm_group_ = true;       // TG_GEMM_GROUP=0 keeps every GEMM in place
+  bool only_optimizer_reads(int t) const;
+  void flush_deferred_gemms();
+  void check_gemm_spans(const tgk::GemmDesc& d, int a, int b, int out) const;
+  std::vector<void*> dev_tables_;    // device copies of grouped-launch tables
 };
 
 // ---------------------------------------------------------------------------------------
 
 Runtime::Runtime(const char* json, Runtime* par, bool plan_only) : parent(par) {
   if (const char* g = std::getenv("TG_GRAPH")) use_graph_ = std::string(g) != "0";
+  if (const char* g = std::getenv("TG_GEMM_GROUP")) use_gemm_group_ = std::string(g) != "0";
   if (const char* g = std::getenv("TG_FUSED")) use_jit_ = std::string(g) != "vm";
   if (const char* g = std::getenv("TG_STREAMS")) nstreams_ = std::max(1, std::min(kStreams, std::atoi(g)));
   try {
@@ -433,6 +448,7 @@ Runtime::~Runtime() {
   if (counters_ && !plan_only_) hipFree(counters_);
   if (fused_code_dev_ && !plan_only_) hipFree(fused_code_dev_);
   if (adam_tensors_) hipFree(adam_tensors_);
+  for (void* t : dev_tables_) hipFree(t);
   if (adam_chunk_tensor_) hipFree(adam_chunk_tensor_);
   if (adam_chunk_start_) hipFree(adam_chunk_start_);
   for (char* p : slots_) if (p) hipFree(p);
@@ -793,6 +809,8 @@ void Runtime::lower() {
     }
   }
 
+  adam_ops_ = adam_ops;
+  plan_gemm_groups();
   match_attention();
   match_attention_bwd();
   match_colsums();
@@ -821,6 +839,7 @@ void Runtime::lower() {
     }
     lower_op((int)i);
   }
+  flush_deferred_gemms();
 
   // Drop nodes whose results nobody reads (e.g. a one_hot consumed only by the
   // gather / scatter patterns, which read its indices instead).
@@ -1786,6 +1805,108 @@ void Runtime::lower_attention(int mi) {
   add_node(std::move(n));
 }
 
+void Runtime::check_gemm_spans(const tgk::GemmDesc& d, int a, int b, int out) const {
+  int64_t nb0 = d.batch / d.bdiv;
+  int64_t da[4] = {nb0, d.bdiv, d.M, d.K}, sa[4] = {d.sAz0, d.sAz1, d.sAm, d.sAk};
+  int64_t db[4] = {nb0, d.bdiv, d.K, d.N}, sb[4] = {d.sBz0, d.sBz1, d.sBk, d.sBn};
+  int64_t dc[4] = {nb0, d.bdiv, d.M, d.N}, sc[4] = {d.sCz0, d.sCz1, d.sCm, d.sCn};
+  if (d.batch % d.bdiv != 0) throw Error(TG_INTERNAL, "gemm: batch not divisible by bdiv");
+  check_span("gemm A", T_[root(a)].numel, 0, da, sa, 4);
+  check_span("gemm B", T_[root(b)].numel, 0, db, sb, 4);
+  check_span("gemm C", T_[root(out)].numel, 0, dc, sc, 4);
+  if (d.batch * d.M * d.N != T_[out].numel) throw Error(TG_INTERNAL, "gemm: output size mismatch");
+}
+
+// True when every reader of tensor t (through views) is an op of the fused optimizer and t
+// is no output, capture or writeback source.
+bool Runtime::only_optimizer_reads(int t) const {
+  for (int o : outputs_) if (root(o) == root(t)) return false;
+  for (auto& c : captures_) if (root(c.second) == root(t)) return false;
+  for (auto& w : copy_writebacks_) if (root(w.first) == root(t)) return false;
+  if (consumers_[t].empty()) return false;
+  for (int c : consumers_[t]) {
+    if (adam_ops_.count(c)) continue;
+    if (virtual_[c] && !is_leaf(c) && kinds_[c] != "matmul" && kinds_[c] != "matmul_batched") {
+      if (!only_optimizer_reads(O(c).at("out").i32())) return false;
+      continue;
+    }
+    return false;
+  }
+  return true;
+}
+
+// Candidates: split-K GEMMs read only by the fused optimizer. A kind's candidates are
+// grouped when their whole-K 64 x 64 tiles fill the chip at least once (256 CUs);
+// fewer, longer tiles would leave CUs idle, so such GEMMs keep their split-K launches.
+void Runtime::plan_gemm_groups() {
+  defer_gemm_.assign(ops_.size(), 0);
+  if (!use_gemm_group_) return;
+  std::vector<int> cand[4];
+  int64_t tiles[4] = {0, 0, 0, 0};
+  for (size_t i = 0; i < ops_.size(); ++i) {
+    if ((kinds_[i] != "matmul" && kinds_[i] != "matmul_batched") || virtual_[i]) continue;
+    const int a = fld((int)i, "a"), b = fld((int)i, "b");
+    if (kinds_[T_[view_[a].root].src] == "one_hot" || kinds_[T_[view_[b].root].src] == "one_hot") continue;
+    tgk::GemmDesc d{};
+    if (!gemm_desc((int)i, d) || tgk::gemm_workspace_floats(d) <= 0) continue;
+    if (!only_optimizer_reads(O((int)i).at("out").i32())) continue;
+    const int kind = tgk::gemm_group_kind(d);
+    if (kind < 0) continue;
+    cand[kind].push_back((int)i);
+    tiles[kind] += ((d.M + 63) / 64) * ((d.N + 63) / 64) * d.batch;
+  }
+  for (int k = 0; k < 4; ++k)
+    if (tiles[k] >= 256)
+      for (int i : cand[k]) defer_gemm_[i] = 1;
+}
+
+void Runtime::flush_deferred_gemms() {
+  for (int kind = 0; kind < 4; ++kind) {
+    std::vector<DeferredGemm> grp;
+    for (const DeferredGemm& g : deferred_gemms_)
+      if (g.kind == kind) grp.push_back(g);
+    if (grp.empty()) continue;
+    Node n;
+    n.kind = "gemm";
+    n.op = grp.front().op;
+    n.detail = "gemm_group";
+    double fl = 0, by = 0;
+    for (const DeferredGemm& g : grp) {
+      n.reads.push_back(root(g.a));
+      n.reads.push_back(root(g.b));
+      n.writes.push_back(root(g.out));
+      fl += 2.0 * (double)g.d.M * g.d.N * g.d.K * g.d.batch;
+      by += 4.0 * ((double)T_[g.a].numel + T_[g.b].numel + T_[g.out].numel);
+    }
+    n.flops = fl;
+    n.bytes = by;
+    n.shape = "group of " + std::to_string(grp.size()) + " GEMMs";
+    n.bind = [this, grp, kind]() -> std::function<void(hipStream_t)> {
+      std::vector<tgk::GemmDesc> ds;
+      for (const DeferredGemm& g : grp) {
+        check_gemm_spans(g.d, g.a, g.b, g.out);
+        tgk::GemmDesc d = g.d;
+        d.A = (const float*)dptr(g.a);
+        d.B = (const float*)dptr(g.b);
+        d.C = (float*)dptr(g.out);
+        ds.push_back(d);
+      }
+      std::vector<unsigned char> img;
+      int64_t blocks = 0;
+      const size_t off = tgk::gemm_group_table(ds.data(), (int)ds.size(), img, blocks);
+      if (plan_only_) return [](hipStream_t) {};
+      void* dev = nullptr;
+      hip_check(hipMalloc(&dev, img.size()), "hipMalloc(gemm group table)");
+      dev_tables_.push_back(dev);
+      hip_check(hipMemcpy(dev, img.data(), img.size(), hipMemcpyHostToDevice), "hipMemcpy(gemm group table)");
+      const int np = (int)ds.size();
+      return [=](hipStream_t st) { tgk::gemm_group(dev, off, np, blocks, kind, st); };
+    };
+    add_node(std::move(n));
+  }
+  deferred_gemms_.clear();
+}
+
 void Runtime::lower_op(int i) {
   const std::string& k = kinds_[i];
   const tgj::Value& op = O(i);
@@ -2166,20 +2287,14 @@ void Runtime::lower_op(int i) {
     tgk::GemmDesc d{};
     if (!gemm_desc(i, d)) throw Error(TG_INTERNAL, "gemm: operand view not expressible (" + n.shape + ")");
     int64_t ws = tgk::gemm_workspace_floats(d);
+    if (defer_gemm_[i]) {
+      deferred_gemms_.push_back({i, d, a, b, out, tgk::gemm_group_kind(d)});
+      return;
+    }
     workspace_bytes_ = std::max(workspace_bytes_, (size_t)ws * 4);
     n.bytes = 4.0 * (T_[a].numel + T_[b].numel + to.numel);
     n.bind = [=]() -> std::function<void(hipStream_t)> {
-      {
-        int64_t nb0 = d.batch / d.bdiv;
-        int64_t da[4] = {nb0, d.bdiv, d.M, d.K}, sa[4] = {d.sAz0, d.sAz1, d.sAm, d.sAk};
-        int64_t db[4] = {nb0, d.bdiv, d.K, d.N}, sb[4] = {d.sBz0, d.sBz1, d.sBk, d.sBn};
-        int64_t dc[4] = {nb0, d.bdiv, d.M, d.N}, sc[4] = {d.sCz0, d.sCz1, d.sCm, d.sCn};
-        if (d.batch % d.bdiv != 0) throw Error(TG_INTERNAL, "gemm: batch not divisible by bdiv");
-        check_span("gemm A", T_[root(a)].numel, 0, da, sa, 4);
-        check_span("gemm B", T_[root(b)].numel, 0, db, sb, 4);
-        check_span("gemm C", T_[root(out)].numel, 0, dc, sc, 4);
-        if (d.batch * d.M * d.N != to.numel) throw Error(TG_INTERNAL, "gemm: output size mismatch");
-      }
+      check_gemm_spans(d, a, b, out);
       tgk::GemmDesc g = d;
       g.A = (const float*)dptr(a);
       g.B = (const float*)dptr(b);

@@ -63,14 +63,17 @@ def _train_both(cfg, steps, seed=42, opt=None, flip_step=None):
     return worst_loss, worst_param, flips
 
 
-def _update_error(cfg, seed=42):
+def _update_error(cfg, seed=42, opt=None, want_ops=None):
     """One plain SGD step (no momentum) from identical params and batch on both sides: the
     update p1 - p0 = -lr * g, so its per-tensor relative error is the gradient's. lr is a
     large power of two so that |lr * g| dwarfs |p0| and the f32 rounding of p1 does not
-    hide the gradient's low digits."""
-    opt = {'kind': 'sgd', 'lr': float(2 ** 24)}
+    hide the gradient's low digits. `opt` replaces the optimizer; `want_ops` names a launch
+    the plan must contain."""
+    opt = opt or {'kind': 'sgd', 'lr': float(2 ** 24)}
     ir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, opt)
     rt = backend.NativeRuntime(ir.wire_json())
+    if want_ops:
+        assert want_ops in [n.get('ops', '') for n in rt.describe()['nodes']]
     o = pyoracle.OracleRuntime(ir.wire())
     p0 = ir.initial_params(seed)
     rt.upload_params(p0)
@@ -88,6 +91,17 @@ def _update_error(cfg, seed=42):
     rt.destroy()
     print(f'  [{cfg.key}] gradient (SGD update) worst rel {worst:.2e}', flush=True)
     return worst
+
+
+@pytest.mark.parametrize('key', ['transformer'])
+def test_grouped_weight_gradients(key):
+    """Weight gradients that only Adam reads run as one grouped GEMM launch (whole-K tiles)
+    just before it. Adam's first update is lr * g / (|g| + eps); with eps = 2^20 far above
+    every |g| it is (lr / eps) * g to a relative 1e-6 or better, the same on both sides, so
+    lr = 2^44 turns it into the SGD gradient check above."""
+    w = _update_error(configs.CONFIGS[key], opt={'kind': 'adam', 'lr': float(2 ** 44), 'eps': float(2 ** 20)},
+                      want_ops='gemm_group')
+    assert w <= GRAD_TOL
 
 
 @pytest.mark.parametrize('key', ['mlp_sin', 'char_mlp', 'cnn', 'nerf', 'transformer'])
