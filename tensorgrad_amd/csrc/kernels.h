@@ -131,7 +131,7 @@ struct ColSum {
   double* part;
   unsigned* counters;
 };
-constexpr int kColSumMax = 4;
+constexpr int kColSumMax = 16;
 struct ColSumBatch {
   int n;
   ColSum s[kColSumMax];

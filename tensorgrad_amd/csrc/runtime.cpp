@@ -374,6 +374,10 @@ class Runtime {
   std::vector<char> defer_gemm_;     // op -> runs in a grouped launch
   std::set<int> adam_ops_;
   void plan_gemm_groups();
+  // Column sums read only by the optimizer (bias, LayerNorm gain / shift gradients) run
+  // together with the grouped GEMMs, kColSumMax per launch.
+  std::vector<char> defer_colsum_;
+  void emit_colsums(const std::vector<int>& batch);
   bool use_gemm_group_ = true;       // TG_GEMM_GROUP=0 keeps every GEMM in place
   bool only_optimizer_reads(int t) const;
   void flush_deferred_gemms();
@@ -814,6 +818,10 @@ void Runtime::lower() {
   match_attention();
   match_attention_bwd();
   match_colsums();
+  defer_colsum_.assign(ops_.size(), 0);
+  if (use_gemm_group_)
+    for (auto& c : colsum_)
+      if (only_optimizer_reads(O(c.first).at("out").i32())) defer_colsum_[c.first] = 1;
   form_groups();
   for (size_t i = 0; i < ops_.size(); ++i) {
     if (is_leaf((int)i) || virtual_[i]) continue;
@@ -829,7 +837,7 @@ void Runtime::lower() {
     }
     if (mul_absorbed_[i]) continue;
     if (colsum_.count((int)i)) {
-      if (!colsum_done_[i]) lower_colsums((int)i);
+      if (!colsum_done_[i] && !defer_colsum_[i]) lower_colsums((int)i);
       continue;
     }
     int gi = group_of_[i];
@@ -840,6 +848,15 @@ void Runtime::lower() {
     lower_op((int)i);
   }
   flush_deferred_gemms();
+  {
+    std::vector<int> batch;
+    for (auto& c : colsum_) {
+      if (!defer_colsum_[c.first] || colsum_done_[c.first]) continue;
+      batch.push_back(c.first);
+      if ((int)batch.size() == tgk::kColSumMax) { emit_colsums(batch); batch.clear(); }
+    }
+    if (!batch.empty()) emit_colsums(batch);
+  }
 
   // Drop nodes whose results nobody reads (e.g. a one_hot consumed only by the
   // gather / scatter patterns, which read its indices instead).
@@ -1520,15 +1537,23 @@ void Runtime::lower_colsums(int s0) {
   };
   for (auto it = colsum_.upper_bound(s0); it != colsum_.end() && (int)batch.size() < tgk::kColSumMax; ++it) {
     const ColSumOp& c = it->second;
-    if (colsum_done_[it->first] || c.R != c0.R || c.C != c0.C) continue;
+    if (colsum_done_[it->first] || defer_colsum_[it->first] || c.R != c0.R || c.C != c0.C) continue;
     if (!ready(c.a) || (c.b >= 0 && !ready(c.b))) continue;
     batch.push_back(it->first);
   }
+  emit_colsums(batch);
+}
+
+void Runtime::emit_colsums(const std::vector<int>& batch) {
+  const int s0 = batch.front();
+  const ColSumOp& c0 = colsum_.at(s0);
   for (int sop : batch) colsum_done_[sop] = true;
   Node n;
   n.kind = "reduce";
   n.op = s0;
   n.shape = "[" + std::to_string(c0.R) + "," + std::to_string(c0.C) + "] x" + std::to_string(batch.size());
+  for (int sop : batch)
+    if (colsum_.at(sop).R != c0.R || colsum_.at(sop).C != c0.C) { n.shape = std::to_string(batch.size()) + " column sums"; break; }
   size_t ws = 0;
   std::vector<size_t> ws_off;
   std::vector<int64_t> cbase;
