@@ -688,6 +688,12 @@ int gemm_group_kind(const GemmDesc& d) {
   return (ak ? 2 : 0) + (bk ? 1 : 0);
 }
 
+bool gemm_prefers_group(const GemmDesc& d) {
+  if (gemm_group_kind(d) < 0) return false;
+  const Plan p = plan_for(d);
+  return p.bm == 64 && p.bn == 64 && p.splits == 1;
+}
+
 size_t gemm_group_table(const GemmDesc* ds, int n, std::vector<unsigned char>& image, int64_t& blocks) {
   const size_t args_bytes = (size_t)n * sizeof(GemmArgs);
   const size_t starts_off = (args_bytes + 15) / 16 * 16;

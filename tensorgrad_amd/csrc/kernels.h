@@ -222,6 +222,9 @@ void gemm(const GemmDesc& d, float* work, hipStream_t st);
 // its tile-start array, sets the launch's block count); the image must be copied to
 // device memory and stay there while the launch can run.
 int gemm_group_kind(const GemmDesc& d);
+// True when d on its own would run one pass of 64 x 64 tiles (the grouped tiling), so a
+// grouped launch computes it with the same arithmetic.
+bool gemm_prefers_group(const GemmDesc& d);
 size_t gemm_group_table(const GemmDesc* ds, int n, std::vector<unsigned char>& image, int64_t& blocks);
 void gemm_group(const void* dev_image, size_t starts_off, int n, int64_t blocks, int kind, hipStream_t st);
 

@@ -381,6 +381,12 @@ class Runtime {
   bool use_gemm_group_ = true;       // TG_GEMM_GROUP=0 keeps every GEMM in place
   bool only_optimizer_reads(int t) const;
   void flush_deferred_gemms();
+  void emit_gemm_group(const std::vector<DeferredGemm>& grp);
+  // Independent GEMMs whose own plan is a single-pass 64 x 64 tiling (few tiles each) and
+  // whose operands are ready share one grouped launch at the first one's position.
+  std::vector<char> gemm_done_;      // op already emitted inside an earlier group
+  bool plain_gemm(int j) const;
+  bool ready_now(int t) const;
   void check_gemm_spans(const tgk::GemmDesc& d, int a, int b, int out) const;
   std::vector<void*> dev_tables_;    // device copies of grouped-launch tables
 };
@@ -814,6 +820,7 @@ void Runtime::lower() {
   }
 
   adam_ops_ = adam_ops;
+  gemm_done_.assign(ops_.size(), 0);
   plan_gemm_groups();
   match_attention();
   match_attention_bwd();
@@ -845,6 +852,7 @@ void Runtime::lower() {
       if (groups_[gi].first == (int)i) lower_group(gi);
       continue;
     }
+    if (gemm_done_[i]) continue;
     lower_op((int)i);
   }
   flush_deferred_gemms();
@@ -1885,51 +1893,77 @@ void Runtime::plan_gemm_groups() {
       for (int i : cand[k]) defer_gemm_[i] = 1;
 }
 
+void Runtime::emit_gemm_group(const std::vector<DeferredGemm>& grp) {
+  const int kind = grp.front().kind;
+  Node n;
+  n.kind = "gemm";
+  n.op = grp.front().op;
+  n.detail = "gemm_group";
+  double fl = 0, by = 0;
+  for (const DeferredGemm& g : grp) {
+    n.reads.push_back(root(g.a));
+    n.reads.push_back(root(g.b));
+    n.writes.push_back(root(g.out));
+    fl += 2.0 * (double)g.d.M * g.d.N * g.d.K * g.d.batch;
+    by += 4.0 * ((double)T_[g.a].numel + T_[g.b].numel + T_[g.out].numel);
+  }
+  n.flops = fl;
+  n.bytes = by;
+  n.shape = "group of " + std::to_string(grp.size()) + " GEMMs";
+  n.bind = [this, grp, kind]() -> std::function<void(hipStream_t)> {
+    std::vector<tgk::GemmDesc> ds;
+    for (const DeferredGemm& g : grp) {
+      check_gemm_spans(g.d, g.a, g.b, g.out);
+      tgk::GemmDesc d = g.d;
+      d.A = (const float*)dptr(g.a);
+      d.B = (const float*)dptr(g.b);
+      d.C = (float*)dptr(g.out);
+      ds.push_back(d);
+    }
+    std::vector<unsigned char> img;
+    int64_t blocks = 0;
+    const size_t off = tgk::gemm_group_table(ds.data(), (int)ds.size(), img, blocks);
+    if (plan_only_) return [](hipStream_t) {};
+    void* dev = nullptr;
+    hip_check(hipMalloc(&dev, img.size()), "hipMalloc(gemm group table)");
+    dev_tables_.push_back(dev);
+    hip_check(hipMemcpy(dev, img.data(), img.size(), hipMemcpyHostToDevice), "hipMemcpy(gemm group table)");
+    const int np = (int)ds.size();
+    return [=](hipStream_t st) { tgk::gemm_group(dev, off, np, blocks, kind, st); };
+  };
+  add_node(std::move(n));
+}
+
 void Runtime::flush_deferred_gemms() {
   for (int kind = 0; kind < 4; ++kind) {
     std::vector<DeferredGemm> grp;
     for (const DeferredGemm& g : deferred_gemms_)
       if (g.kind == kind) grp.push_back(g);
-    if (grp.empty()) continue;
-    Node n;
-    n.kind = "gemm";
-    n.op = grp.front().op;
-    n.detail = "gemm_group";
-    double fl = 0, by = 0;
-    for (const DeferredGemm& g : grp) {
-      n.reads.push_back(root(g.a));
-      n.reads.push_back(root(g.b));
-      n.writes.push_back(root(g.out));
-      fl += 2.0 * (double)g.d.M * g.d.N * g.d.K * g.d.batch;
-      by += 4.0 * ((double)T_[g.a].numel + T_[g.b].numel + T_[g.out].numel);
-    }
-    n.flops = fl;
-    n.bytes = by;
-    n.shape = "group of " + std::to_string(grp.size()) + " GEMMs";
-    n.bind = [this, grp, kind]() -> std::function<void(hipStream_t)> {
-      std::vector<tgk::GemmDesc> ds;
-      for (const DeferredGemm& g : grp) {
-        check_gemm_spans(g.d, g.a, g.b, g.out);
-        tgk::GemmDesc d = g.d;
-        d.A = (const float*)dptr(g.a);
-        d.B = (const float*)dptr(g.b);
-        d.C = (float*)dptr(g.out);
-        ds.push_back(d);
-      }
-      std::vector<unsigned char> img;
-      int64_t blocks = 0;
-      const size_t off = tgk::gemm_group_table(ds.data(), (int)ds.size(), img, blocks);
-      if (plan_only_) return [](hipStream_t) {};
-      void* dev = nullptr;
-      hip_check(hipMalloc(&dev, img.size()), "hipMalloc(gemm group table)");
-      dev_tables_.push_back(dev);
-      hip_check(hipMemcpy(dev, img.data(), img.size(), hipMemcpyHostToDevice), "hipMemcpy(gemm group table)");
-      const int np = (int)ds.size();
-      return [=](hipStream_t st) { tgk::gemm_group(dev, off, np, blocks, kind, st); };
-    };
-    add_node(std::move(n));
+    if (!grp.empty()) emit_gemm_group(grp);
   }
   deferred_gemms_.clear();
+}
+
+// A GEMM that is its own launch (no pattern, not deferred); used to collect independent
+// GEMMs into one grouped launch.
+bool Runtime::plain_gemm(int j) const {
+  if ((kinds_[j] != "matmul" && kinds_[j] != "matmul_batched") || virtual_[j] || is_leaf(j)) return false;
+  if (attn_of_[j] >= 0 || group_of_[j] >= 0 || defer_gemm_[j] || gemm_done_[j] || mul_absorbed_[j]) return false;
+  const int a = fld(j, "a"), b = fld(j, "b");
+  if (kinds_[T_[view_[a].root].src] == "one_hot" || kinds_[T_[view_[b].root].src] == "one_hot") return false;
+  return true;
+}
+
+// Tensor t's data exists already: its root is an input / parameter / state, or a node
+// emitted so far writes it.
+bool Runtime::ready_now(int t) const {
+  const int r = root(t);
+  const int p = T_[r].src;
+  if (p < 0 || is_leaf(p)) return true;
+  for (const Node& n : nodes_)
+    for (int w : n.writes)
+      if (w == r) return true;
+  return false;
 }
 
 void Runtime::lower_op(int i) {
@@ -2315,6 +2349,23 @@ void Runtime::lower_op(int i) {
     if (defer_gemm_[i]) {
       deferred_gemms_.push_back({i, d, a, b, out, tgk::gemm_group_kind(d)});
       return;
+    }
+    if (use_gemm_group_ && tgk::gemm_prefers_group(d)) {
+      const int kind = tgk::gemm_group_kind(d);
+      std::vector<DeferredGemm> grp{{i, d, a, b, out, kind}};
+      for (int j = i + 1; j < (int)ops_.size() && j <= i + 64 && grp.size() < 8; ++j) {
+        if (!plain_gemm(j)) continue;
+        tgk::GemmDesc dj{};
+        if (!gemm_desc(j, dj) || !tgk::gemm_prefers_group(dj) || tgk::gemm_group_kind(dj) != kind) continue;
+        const int aj = fld(j, "a"), bj = fld(j, "b");
+        if (!ready_now(aj) || !ready_now(bj)) continue;
+        grp.push_back({j, dj, aj, bj, O(j).at("out").i32(), kind});
+      }
+      if (grp.size() > 1) {
+        for (const DeferredGemm& g : grp) gemm_done_[g.op] = 1;
+        emit_gemm_group(grp);
+        return;
+      }
     }
     workspace_bytes_ = std::max(workspace_bytes_, (size_t)ws * 4);
     n.bytes = 4.0 * (T_[a].numel + T_[b].numel + to.numel);
