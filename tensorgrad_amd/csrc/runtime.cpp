@@ -1205,6 +1205,14 @@ void Runtime::form_groups() {
     for (int t : op_inputs(*ops_[i])) {
       const int gi = producer_group(t);
       if (gi >= 0 && std::find(cands.begin(), cands.end(), gi) == cands.end()) cands.push_back(gi);
+      // a recent group that already reads t (a sibling): joining it needs every input of
+      // op i to exist before that group runs, which the checks below require
+      for (int c : consumers_[t]) {
+        if (c >= (int)i || group_of_[c] < 0) continue;
+        const int sg = group_of_[c];
+        if ((int)i - groups_[sg].first > 64) continue;
+        if (std::find(cands.begin(), cands.end(), sg) == cands.end()) cands.push_back(sg);
+      }
     }
     std::sort(cands.begin(), cands.end(), [&](int a, int b) { return groups_[a].first > groups_[b].first; });
     int joined = -1;
