@@ -380,10 +380,13 @@ struct ColPlan { int64_t nx; int64_t chunk; int nchunks; };
 bool col_form(const Strided& cells, const Strided& red) {
   return cells.rank == 1 && cells.s0[0] == 1 && red.rank == 1;
 }
-ColPlan col_plan(int64_t C, int64_t R) {
+// `share` sums run in one launch: together they aim at ~1024 blocks (a lone sum at 512),
+// so a batch of many sums gets fewer, longer row chunks per sum.
+ColPlan col_plan(int64_t C, int64_t R, int share) {
   ColPlan p;
   p.nx = (C + 63) / 64;
-  int64_t want = (512 + p.nx - 1) / p.nx;
+  const int64_t target = share <= 1 ? 512 : std::max<int64_t>(64, 1024 / share);
+  int64_t want = (target + p.nx - 1) / p.nx;
   int64_t n = (R + 63) / 64;
   if (n > want) n = want;
   if (n > 256) n = 256;
@@ -448,7 +451,7 @@ void softmax_causal(const float* a, float* out, int64_t mats, int64_t D, hipStre
 int64_t sum_workspace_doubles(const Strided& cells, const Strided& red, int64_t ncells, int64_t nred) {
   if (!col_form(cells, red) && block_form(red, ncells, nred)) return 0;
   if (col_form(cells, red)) {
-    ColPlan c = col_plan(ncells, nred);
+    ColPlan c = col_plan(ncells, nred, 1);
     return c.nchunks > 1 ? ncells * c.nchunks : 0;
   }
   SumPlan p = sum_plan(cells, ncells, nred);
@@ -456,8 +459,8 @@ int64_t sum_workspace_doubles(const Strided& cells, const Strided& red, int64_t 
 }
 
 ColSum colsum_desc(const float* a, const float* b, float* out, int64_t C, int64_t R, int64_t rs, double div,
-                   double* part, unsigned* counters) {
-  const ColPlan p = col_plan(C, R);
+                   double* part, unsigned* counters, int share) {
+  const ColPlan p = col_plan(C, R, share);
   ColSum c{};
   c.a = a; c.b = b; c.out = out;
   c.C = C; c.R = R; c.rs = rs; c.chunk = p.chunk;
@@ -466,13 +469,13 @@ ColSum colsum_desc(const float* a, const float* b, float* out, int64_t C, int64_
   return c;
 }
 
-int64_t colsum_workspace_doubles(int64_t C, int64_t R) {
-  const ColPlan p = col_plan(C, R);
+int64_t colsum_workspace_doubles(int64_t C, int64_t R, int share) {
+  const ColPlan p = col_plan(C, R, share);
   return p.nchunks > 1 ? C * p.nchunks : 0;
 }
 
-int64_t colsum_counters(int64_t C, int64_t R) {
-  const ColPlan p = col_plan(C, R);
+int64_t colsum_counters(int64_t C, int64_t R, int share) {
+  const ColPlan p = col_plan(C, R, share);
   return p.nchunks > 1 ? p.nx : 0;
 }
 
@@ -489,7 +492,7 @@ void colsum_batch(const ColSumBatch& b, hipStream_t st) {
 
 int64_t sum_counters(const Strided& cells, const Strided& red, int64_t ncells, int64_t nred) {
   if (!col_form(cells, red)) return 0;
-  ColPlan c = col_plan(ncells, nred);
+  ColPlan c = col_plan(ncells, nred, 1);
   return c.nchunks > 1 ? c.nx : 0;
 }
 
@@ -499,7 +502,7 @@ void reduce_sum(const float* a, float* out, const Strided& cells, const Strided&
   if (col_form(cells, red)) {
     ColSumBatch bt{};
     bt.n = 1;
-    bt.s[0] = colsum_desc(a, nullptr, out, ncells, nred, red.s0[0], div, work, counters);
+    bt.s[0] = colsum_desc(a, nullptr, out, ncells, nred, red.s0[0], div, work, counters, 1);
     colsum_batch(bt, st);
     return;
   }
