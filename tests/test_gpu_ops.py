@@ -411,6 +411,38 @@ def test_fused_attention_backward(B, H, T):
         gemm_close(got, o.output(), 1e-5)
 
 
+@pytest.mark.skip(reason='sums of products as one GEMM are switched off: the transformer step using them '
+                         'faulted the GPU once, cause not found; the code path is removed until it is')
+@pytest.mark.parametrize('terms,K', [(2, 256), (3, 256), (3, 128)])
+def test_sum_of_products(terms, K):
+    """add(matmul, matmul[, matmul]) with single-use products runs as one GEMM over the
+    concatenated k segments: against the oracle with GEMM tolerance, and against the
+    unfused products and adds (TG_GEMM_GROUP=0) within f32 rounding."""
+    M, N = 512, 256
+    ins = {}
+    for q in range(terms):
+        ins[f'a{q}'] = _rand([M, K], 80 + q)
+        ins[f'b{q}'] = _rand([N, K], 90 + q)
+
+    def body():
+        acc = None
+        for q in range(terms):
+            p = O.matmul(tensor_input(f'a{q}', [M, K]), O.swap_axes(tensor_input(f'b{q}', [N, K]), -1, -2))
+            acc = p if acc is None else O.add(acc, p)
+        return O.relu(acc)
+    g = trace_fn(body)
+    got, kinds = _run_native(g, ins)
+    ref, _ = _run_native(g, ins, {'TG_GEMM_GROUP': '0'})
+    rt = backend.NativeRuntime(IR.dumps(wire(g)))
+    ops = [n.get('ops', '') for n in rt.describe()['nodes']]
+    rt.destroy()
+    assert 'gemm_sum' in ops
+    o = pyoracle.OracleRuntime(wire(g))
+    o.run(ins)
+    gemm_close(got, o.output())
+    gemm_close(got, ref)
+
+
 GEMMS = [([5, 7], [7, 3], False, False), ([2, 33, 65], [65, 17], False, False), ([129, 64], [64, 300], False, False),
          ([70, 40], [50, 40], False, True), ([40, 70], [40, 50], True, False), ([4096, 256], [4096, 256], True, False),
          ([300, 4096], [4096, 64], False, False)]
