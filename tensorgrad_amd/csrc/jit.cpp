@@ -21,6 +21,10 @@ namespace {
 const char* const kFusedDevSource =
 #include "fused_dev_src.inc"
     ;
+// gemm_dev.h as text: added to programs that hold GEMM kernels with fused epilogues.
+const char* const kGemmDevSource =
+#include "gemm_dev_src.inc"
+    ;
 
 std::string dlit(double v) {   // exact (hexadecimal) double literal
   char b[64];
@@ -281,6 +285,74 @@ JitKernel fused_kernel(const FusedProgram& p, const FusedInstr* code, int64_t n)
   return k;
 }
 
+JitKernel gemm_epi_kernel(const FusedProgram& p, const FusedInstr* code, const GemmEpiCfg& c) {
+  if (p.row_d > 0 || p.vec != 1) throw std::runtime_error("jit: GEMM epilogue needs an element program of one element");
+  bool dropout = false;
+  for (int q = 0; q < p.n_instr; ++q) dropout |= code[q].op == FO_DROPOUT;
+  const char* I = "    ";
+  std::ostringstream o;
+  // The epilogue functor: element (gm, gn) of the product is element t = gm * N + gn of
+  // the group's iteration space (the product is contiguous and read in that order).
+  o << "namespace {\nstruct @NAME@_epi {\n  tgk::JitArgs A;\n  unsigned seed;\n";
+  o << "  __device__ __forceinline__ void operator()(const tgk::GemmDesc&, int64_t, int64_t, int64_t gm, int64_t gn, "
+       "float value) const {\n";
+  o << I << "const unsigned t = (unsigned)gm * " << ulit(c.N) << " + (unsigned)gn;\n";
+  if (p.any_strided) emit_coords(o, p, "t", I);
+  for (int k = 0; k < p.n_in; ++k) {
+    const std::string x = "x" + std::to_string(k);
+    if (k == c.h_in) {
+      o << I << "const unsigned " << x << " = tgk::fbits(value);\n";
+      continue;
+    }
+    const int m = p.in_mode[k];
+    o << I << "const unsigned " << x << " = ((const unsigned*)A.in[" << k << "])[";
+    if (m == FM_CONTIG) o << "t";
+    else if (m == FM_SCALAR) o << "0u";
+    else o << offset_expr(p, k);
+    o << "];\n";
+  }
+  std::vector<std::string> reg(64);
+  for (int k = 0; k < p.n_in; ++k) reg[k] = "x" + std::to_string(k);
+  auto R = [&](int r) -> const std::string& {
+    if (r < 0 || r >= (int)reg.size() || reg[r].empty()) throw std::runtime_error("jit: read of an unset register");
+    return reg[r];
+  };
+  for (int q = 0; q < p.n_instr; ++q) {
+    const FusedInstr& in = code[q];
+    const std::string v = "v" + std::to_string(q);
+    if (in.op == FO_ROWSUM || in.op == FO_SOFTMAX_CAUSAL || in.op == FO_LOG_SOFTMAX)
+      throw std::runtime_error("jit: row opcode in a GEMM epilogue");
+    if (in.op == FO_WHERE) {
+      o << I << "const unsigned " << v << " = " << R(in.a) << " != 0u ? " << R(in.b) << " : " << R(in.c) << ";\n";
+    } else {
+      const std::string b = binary_op(in.op) ? R(in.b) : std::string("0u");
+      o << I << "const unsigned " << v << " = tgk::op_eval(" << in.op << ", " << R(in.a) << ", " << b << ", " << in.ta
+        << ", " << in.tb << ", " << in.dt << ", " << dlit(in.imm) << ", " << dlit(in.imm2) << ", " << in.salt
+        << "u, seed, " << (in.op == FO_DROPOUT ? "t" : "0u") << ");\n";
+    }
+    if (in.dst < 0 || in.dst >= (int)reg.size()) throw std::runtime_error("jit: register out of range");
+    reg[in.dst] = v;
+  }
+  for (int k = 0; k < p.n_out; ++k) o << I << "((unsigned*)A.out[" << k << "])[t] = " << R(p.out_reg[k]) << ";\n";
+  o << "  }\n};\n}  // namespace\n";
+  o << "extern \"C\" __global__ void __launch_bounds__(" << c.nt
+    << ") @NAME@(const tgk::gd::GemmArgs g, const tgk::JitArgs A) {\n";
+  o << "  const @NAME@_epi e{A, " << (dropout ? "A.seed ? (unsigned)*A.seed : 0u" : "0u") << "};\n";
+  o << "  tgk::gd::gemm_tile<" << c.bm << ", " << c.bn << ", " << c.bk << ", " << c.ns << ", " << (c.ak ? "true" : "false")
+    << ", " << (c.bkf ? "true" : "false") << ", " << c.nt << ", " << c.kg
+    << ">(g, tgk::gd::xcd_order(blockIdx.x, gridDim.x), e);\n}\n";
+  JitKernel k;
+  std::string body = o.str();
+  char nm[32];
+  snprintf(nm, sizeof nm, "tg_g%016llx", (unsigned long long)fnv1a(body));
+  k.name = nm;
+  for (size_t pos; (pos = body.find("@NAME@")) != std::string::npos;) body.replace(pos, 6, k.name);
+  k.body = body;
+  k.grid = 0;   // set by the caller (the GEMM's tile count)
+  k.gemm = true;
+  return k;
+}
+
 namespace {
 
 struct Cache {
@@ -325,9 +397,16 @@ void jit_compile(const std::vector<JitKernel>& ks, bool load) {
   std::string src = kFusedDevSource;
   std::vector<std::string> fresh;
   std::set<std::string> seen;
+  bool gemm = false;
   for (const auto& k : ks) {
     if (c.code_of.count(k.name) || !seen.insert(k.name).second) continue;
     fresh.push_back(k.name);
+    gemm |= k.gemm;
+  }
+  if (gemm) src += std::string("\n") + kGemmDevSource;
+  seen.clear();
+  for (const auto& k : ks) {
+    if (c.code_of.count(k.name) || !seen.insert(k.name).second) continue;
     src += "\n" + k.body;
   }
   if (!fresh.empty()) {

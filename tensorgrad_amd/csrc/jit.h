@@ -19,7 +19,12 @@ struct JitKernel {
   std::string name;   // tg_<hash of body>
   std::string body;   // extern "C" __global__ definition
   int64_t grid = 0;   // blocks of 256 threads
+  bool gemm = false;  // a GEMM with a fused epilogue (its program needs gemm_dev.h)
 };
+
+// Source of a GEMM kernel (gemm_dev.h's tile) whose epilogue runs the element program p
+// (one element per call, vec = 1) on each product element instead of storing it.
+JitKernel gemm_epi_kernel(const FusedProgram& p, const FusedInstr* code, const GemmEpiCfg& c);
 
 // Source of the kernel for `p` (its code[] instructions) over n threads' runs (element
 // form: elements / vec) or n rows (row form).

@@ -41,20 +41,9 @@
 namespace tgk {
 namespace {
 
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
+using namespace gd;
 
 constexpr int kThreads = 256;
-constexpr int kXcds = 8;
-
-struct GemmArgs {
-  GemmDesc d;
-  int64_t k_per_split;
-  int splits;
-  int tiles_n, tiles_m;   // tile grid (per batch and split)
-  float* out;             // split-K workspace (splits > 1)
-  int64_t sOs, sOz;       // workspace strides (split, batch)
-};
 
 // One operand's ROWS x BK tile: element (r, k) at X[r*sr + k*sk].
 template <int ROWS, int BK, bool KFAST>
@@ -248,290 +237,11 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g) {
     }
 }
 
-// ---- direct-to-LDS pipeline ------------------------------------------------------------
-//
-// Same tiles, fragments and blocked accumulation as k_gemm, but operand tiles travel from
-// global memory straight into LDS (global_load_lds_dwordx4: each lane's 16 bytes land at
-// wave-base + lane * 16) through a ring of NS stages, so the loads of stages s+1 .. s+NS-1
-// are in flight while stage s is multiplied, without staging registers. LDS rows are not
-// padded; 16-byte chunks are XOR-swizzled instead so fragment reads stay conflict-free:
-//  * k-contiguous operand, rows [r][BK]: chunk c of row r is stored at c ^ swz(r);
-//  * row-contiguous operand, rows [k][ROWS]: chunk c of k-row k is stored at
-//    c ^ (((k >> 2) & 1) << 3), which puts the two lane halves (k and k + 4) on opposite
-//    halves of the banks.
-// Used when K (per split) is a multiple of BK, rows of the row-contiguous operand are a
-// multiple of 4 and both operands are 16-byte aligned; rows past M / N are read clamped
-// to the last row (their results are never stored). Tiles with a 128-wide side run eight
-// wavefronts (two per SIMD, 64 x 32 or 32 x 32 each), so one wavefront's barrier wait,
-// partial-sum adds and LDS latency overlap the other's MFMAs; 64 x 64 tiles run four.
-// Loads address the tile through a wave-uniform base (SGPRs, advanced per stage) plus a
-// fixed 32-bit per-lane offset.
-constexpr int kLdsBlock = 256;   // floats one wavefront-wide DMA writes (1 KiB)
-
-template <int ROWS, int BK, bool KFAST, int NT>
-struct DTile {
-  static constexpr int CPR = KFAST ? BK / 4 : ROWS / 4;   // 16-byte chunks per LDS row
-  static constexpr int NCH = ROWS * BK / 4;               // chunks per tile
-  static constexpr int PER = NCH / NT;                    // DMA instructions per thread
-  static constexpr int SIZE = ROWS * BK;                  // floats
-  static_assert(NCH % NT == 0, "tile must be a whole number of DMA rounds");
-  static_assert(KFAST ? (BK == 32 || BK == 64) : ROWS >= 64, "swizzle needs 8 / 16 chunks per row");
-
-  __device__ __forceinline__ static int swz(int lrow) {
-    if (KFAST) return BK == 32 ? ((lrow >> 1) & 7) : (lrow & 15);
-    return ((lrow >> 2) & 1) << 3;
-  }
-
-  // Per-thread byte offsets of this thread's PER chunks from the tile origin (row r0,
-  // k = k0); fixed for the whole k loop. Rows past `rlim` read the last row.
-  __device__ __forceinline__ static void offsets(int64_t sr, int64_t sk, int64_t r0, int64_t rlim, int tid,
-                                                 uint32_t* off) {
-    const int lane = tid & 63, wave = tid >> 6;
-#pragma unroll
-    for (int e = 0; e < PER; ++e) {
-      const int inst = e * (NT / 64) + wave;
-      const int P = inst * 64 + lane;
-      const int row = P / CPR, pc = P % CPR;
-      const int c = pc ^ swz(row);
-      if (KFAST) {
-        const int64_t gr = min(r0 + row, rlim - 1) - r0;
-        off[e] = (uint32_t)((gr * sr + c * 4) * 4);
-      } else {
-        const int64_t gr = min(r0 + c * 4, rlim - 4) - r0;
-        off[e] = (uint32_t)((row * sk + gr) * 4);
-      }
-    }
-  }
-
-  // Issue this thread's chunks of one stage: global base `gb` (tile origin of the stage,
-  // wave-uniform, in SGPRs) plus the 32-bit per-lane offsets; LDS byte address `lds` of the
-  // stage's slot and the wave index `wave`, both wave-uniform, so M0 is scalar arithmetic.
-  // Each global_load_lds_dwordx4 moves lane l's 16 bytes to M0 + 16 l. It is issued from
-  // inline assembly so the compiler does not treat it as an LDS write of unknown extent:
-  // for such writes it drains every outstanding load before the next LDS read, which would
-  // expose the full load latency at every pipeline stage. The kernel orders LDS reads
-  // itself (explicit vmcnt waits and barriers). One wait state separates the M0 write from
-  // the load.
-  __device__ __forceinline__ static void dma(const float* gb, const uint32_t* off, uint32_t lds, int wave) {
-#pragma unroll
-    for (int e = 0; e < PER; ++e) {
-      const uint32_t m0v = lds + (uint32_t)((e * (NT / 64) + wave) * kLdsBlock * 4);
-      asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off[e]), "s"(gb), "{m0}"(m0v));
-    }
-  }
-
-  // The 4 consecutive-k values (kb .. kb+3, kb % 4 == 0) of tile row `row`.
-  __device__ __forceinline__ static f32x4 frag(const float* L, int row, int kb) {
-    if (KFAST) return *reinterpret_cast<const f32x4*>(L + row * BK + (((kb >> 2) ^ swz(row)) << 2));
-    f32x4 v;
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int k = kb + u;
-      v[u] = L[k * ROWS + ((((row >> 2) ^ swz(k)) << 2) | (row & 3))];
-    }
-    return v;
-  }
-};
-
-// s_waitcnt with vmcnt = N and the other counters left alone (gfx9 encoding).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
-// KG = 2 splits the k stages of a tile between two groups of four wavefronts by parity
-// (group g multiplies stages g, g + 2, ...; NS slots, NS / 2 per group), for 64 x 64 tiles
-// that have no second 32-column or 32-row wave tile to give a second wavefront per SIMD.
-// The groups' sums meet at the end as (stages 0, 2, ..) + (stages 1, 3, ..); with two
-// stages that is the single group's (0 + stage 0) + stage 1.
-// Block b of the launch -> tile number: consecutive tile numbers go to one XCD (the
-// hardware deals blocks to the XCDs round-robin), so tiles sharing operand rows or
-// columns share an L2.
-__device__ __forceinline__ uint32_t xcd_order(uint32_t b, uint32_t nblk) {
-  return nblk % kXcds == 0 ? (b % kXcds) * (nblk / kXcds) + b / kXcds : b;
-}
-
-// One output tile (tile number b of the problem g).
-template <int BM, int BN, int BK, int NS, bool AK, bool BKF, int NT, int KG>
-__device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint32_t b) {
-  // per k group: 4 waves 2 x 2; 8 waves 2 x 4 (BN = 128) or 4 x 2
-  constexpr int GT = NT / KG;             // threads per k group
-  constexpr int NW = GT / 64;
-  constexpr int WGM = NW == 8 && BN == 64 ? 4 : 2, WGN = NW / WGM;
-  constexpr int WM = BM / WGM, WN = BN / WGN;
-  constexpr int TM = WM / 32, TN = WN / 32;
-  static_assert(TM >= 1 && TN >= 1, "wave tile below 32 x 32");
-  static_assert(KG == 1 || (KG == 2 && NS % 2 == 0), "k groups take alternate slots");
-  constexpr int NSG = NS / KG;            // slots per k group
-  constexpr int NG = BK / 8;
-  using TA = DTile<BM, BK, AK, GT>;
-  using TB = DTile<BN, BK, BKF, GT>;
-  constexpr int PER = TA::PER + TB::PER;
-  static_assert(PER * (NSG - 1) < 64, "too many loads in flight for vmcnt");
-  __shared__ __attribute__((aligned(16))) float As[NS * TA::SIZE];   // NS stages of A
-  __shared__ __attribute__((aligned(16))) float Bs[NS * TB::SIZE];   // NS stages of B
-
-  const GemmDesc& d = g.d;
-  const int tid = threadIdx.x;
-  const int lane = tid % 64;
-  const int kg = __builtin_amdgcn_readfirstlane(tid / GT);   // k group (wave-uniform)
-  const int gtid = tid % GT;
-  const int wave = gtid / 64;             // wave within the k group
-  const int wm0 = (wave / WGN) * WM, wn0 = (wave % WGN) * WN;
-
-  const uint32_t tn = b % g.tiles_n;
-  const uint32_t rest = b / g.tiles_n;
-  const uint32_t tm = rest % g.tiles_m;
-  const uint32_t zs = rest / g.tiles_m;
-  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
-  const int64_t zz = zs / g.splits;
-  const int split = zs % g.splits;
-  const int64_t z0 = zz / d.bdiv, z1 = zz % d.bdiv;
-  const float* A = d.A + z0 * d.sAz0 + z1 * d.sAz1;
-  const float* B = d.B + z0 * d.sBz0 + z1 * d.sBz1;
-  const int64_t kbeg = split * g.k_per_split;
-  const int64_t kend = min(d.K, kbeg + g.k_per_split);
-  const int nst = kbeg < kend ? (int)((kend - kbeg) / BK) : 0;
-  // Operand bases of stage 0 and the per-stage advance, all wave-uniform.
-  const float* a0 = A + m0 * (AK ? d.sAm : 1) + kbeg * (AK ? 1 : d.sAk);
-  const float* b0 = B + n0 * (BKF ? d.sBn : 1) + kbeg * (BKF ? 1 : d.sBk);
-  const int64_t a_step = AK ? BK : BK * d.sAk, b_step = BKF ? BK : BK * d.sBk;
-  uint32_t offa[TA::PER], offb[TB::PER];
-  TA::offsets(d.sAm, d.sAk, m0, d.M, gtid, offa);
-  TB::offsets(d.sBn, d.sBk, n0, d.N, gtid, offb);
-  const int wv = __builtin_amdgcn_readfirstlane(wave);
-  const uint32_t lds_a = (uint32_t)(uintptr_t)((__attribute__((address_space(3))) float*)As);
-  const uint32_t lds_b = (uint32_t)(uintptr_t)((__attribute__((address_space(3))) float*)Bs);
-  auto issue = [&](int st) {
-    const int slot = st % NS;
-    TA::dma(a0 + st * a_step, offa, lds_a + slot * TA::SIZE * 4, wv);
-    TB::dma(b0 + st * b_step, offb, lds_b + slot * TB::SIZE * 4, wv);
-  };
-
-  f32x16 acc[TM][TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-
-  const int lrow = lane % 32, h = lane / 32;
-  // this group's stages are kg, kg + KG, ...; it keeps NSG - 1 of them in flight
-#pragma unroll
-  for (int p = 0; p < NSG - 1; ++p)
-    if (kg + p * KG < nst) issue(kg + p * KG);
-
-  const int nit = (nst + KG - 1) / KG;
-  const int mine = nst > kg ? (nst - 1 - kg) / KG : -1;   // this group's last iteration
-  for (int it = 0; it < nit; ++it) {
-    const int st = it * KG + kg;
-    // Stage st has landed once at most (own stages issued after it) * PER loads are pending.
-    const int after = min(NSG - 2, mine - it);
-    if (NSG >= 4 && after >= 3) wait_vmcnt<(NSG >= 4 ? 3 : 0) * PER>();
-    else if (NSG >= 3 && after >= 2) wait_vmcnt<(NSG >= 3 ? 2 : 0) * PER>();
-    else if (after >= 1) wait_vmcnt<PER>();
-    else wait_vmcnt<0>();
-    // A bare workgroup barrier: __syncthreads() would also drain every outstanding load
-    // (the stages still in flight). The empty asm statements keep the compiler from
-    // moving LDS accesses across it; each wave has already waited for its own copies of
-    // stage st, and its reads of the slot about to be refilled were consumed by the MFMAs
-    // of its group's previous stage.
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    if (st >= nst) continue;              // the other group's last stage (odd count)
-    if (st + (NSG - 1) * KG < nst) issue(st + (NSG - 1) * KG);
-    const float* Ac = As + (st % NS) * TA::SIZE;
-    const float* Bc = Bs + (st % NS) * TB::SIZE;
-    f32x16 part[TM][TN];
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) part[i][j][r] = 0.0f;
-    f32x4 av[2][TM], bv[2][TN];
-#pragma unroll
-    for (int i = 0; i < TM; ++i) av[0][i] = TA::frag(Ac, wm0 + i * 32 + lrow, h * 4);
-#pragma unroll
-    for (int j = 0; j < TN; ++j) bv[0][j] = TB::frag(Bc, wn0 + j * 32 + lrow, h * 4);
-#pragma unroll
-    for (int grp = 0; grp < NG; ++grp) {
-      const int c = grp & 1;
-      if (grp + 1 < NG) {
-        const int kb = (grp + 1) * 8 + h * 4;
-#pragma unroll
-        for (int i = 0; i < TM; ++i) av[c ^ 1][i] = TA::frag(Ac, wm0 + i * 32 + lrow, kb);
-#pragma unroll
-        for (int j = 0; j < TN; ++j) bv[c ^ 1][j] = TB::frag(Bc, wn0 + j * 32 + lrow, kb);
-      }
-      // keep the next group's LDS reads ahead of this group's MFMAs
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj)
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-          for (int j = 0; j < TN; ++j)
-            part[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[c][i][jj], bv[c][j][jj], part[i][j], 0, 0, 0);
-    }
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j) acc[i][j] += part[i][j];
-  }
-
-  if (KG == 2) {
-    // group 1 hands its sums to group 0 through LDS (the A ring, free after the barrier)
-    static_assert(KG == 1 || NW * TM * TN * 16 * 64 <= NS * TA::SIZE, "exchange fits the A ring");
-    __syncthreads();
-    float* X = As;
-    if (kg == 1) {
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) X[(((wave * TM + i) * TN + j) * 16 + r) * 64 + lane] = acc[i][j][r];
-    }
-    __syncthreads();
-    if (kg == 1) return;
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[i][j][r] += X[(((wave * TM + i) * TN + j) * 16 + r) * 64 + lane];
-  }
-
-  float* O;
-  int64_t sOm, sOn;
-  if (g.splits > 1) {
-    O = g.out + split * g.sOs + zz * g.sOz;
-    sOm = d.N; sOn = 1;
-  } else {
-    O = d.C + z0 * d.sCz0 + z1 * d.sCz1;
-    sOm = d.sCm; sOn = d.sCn;
-  }
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int64_t gn = n0 + wn0 + j * 32 + lrow;
-      if (gn >= d.N) continue;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t gm = m0 + wm0 + i * 32 + (r / 4) * 8 + h * 4 + (r % 4);
-        if (gm < d.M) O[gm * sOm + gn * sOn] = acc[i][j][r];
-      }
-    }
-}
+// ---- direct-to-LDS pipeline (gemm_dev.h) ----------------------------------------------
 
 template <int BM, int BN, int BK, int NS, bool AK, bool BKF, int NT, int KG>
 __global__ __launch_bounds__(NT) void k_gemm_dma(GemmArgs g) {
-  gemm_tile<BM, BN, BK, NS, AK, BKF, NT, KG>(g, xcd_order(blockIdx.x, gridDim.x));
+  gemm_tile<BM, BN, BK, NS, AK, BKF, NT, KG>(g, xcd_order(blockIdx.x, gridDim.x), StoreC{});
 }
 
 // Several independent problems in one launch: problem p owns tile numbers
@@ -544,7 +254,7 @@ __global__ __launch_bounds__(NT) void k_gemm_dma_group(const GemmArgs* __restric
   for (int q = 1; q < n; ++q)
     if (starts[q] <= b) p = q;
   const GemmArgs g = table[p];
-  gemm_tile<BM, BN, BK, NS, AK, BKF, NT, KG>(g, b - starts[p]);
+  gemm_tile<BM, BN, BK, NS, AK, BKF, NT, KG>(g, b - starts[p], StoreC{});
 }
 
 // Sum split-K partials in split order into C (eight partial loads in flight per thread).
@@ -692,6 +402,25 @@ bool gemm_prefers_group(const GemmDesc& d) {
   if (gemm_group_kind(d) < 0) return false;
   const Plan p = plan_for(d);
   return p.bm == 64 && p.bn == 64 && p.splits == 1;
+}
+
+bool gemm_epi_cfg(const GemmDesc& d, GemmEpiCfg& c, GemmArgs& g, int64_t& blocks) {
+  if (d.M <= 0 || d.N <= 0 || d.batch <= 0) return false;
+  const Plan p = plan_for(d);
+  const bool ak = d.sAk == 1;
+  const bool bk = d.sBk == 1 && d.sBn != 1;
+  if (p.splits != 1 || !dma_ok(d, p, ak, bk)) return false;
+  // the same instantiation gemm() launches for this plan
+  c.bm = p.bm; c.bn = p.bn; c.bk = p.bk;
+  c.ns = p.bm == 64 && p.bn == 64 ? 4 : 3;
+  c.nt = 512;
+  c.kg = p.bm == 64 && p.bn == 64 ? 2 : 1;
+  c.ak = ak; c.bkf = bk;
+  g = GemmArgs{d, p.kps, 1, 0, 0, nullptr, 0, 0};
+  g.tiles_n = (int)((d.N + p.bn - 1) / p.bn);
+  g.tiles_m = (int)((d.M + p.bm - 1) / p.bm);
+  blocks = (int64_t)g.tiles_n * g.tiles_m * d.batch;
+  return blocks < (int64_t(1) << 31);
 }
 
 size_t gemm_group_table(const GemmDesc* ds, int n, std::vector<unsigned char>& image, int64_t& blocks) {

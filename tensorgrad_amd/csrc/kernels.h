@@ -7,6 +7,7 @@
 #include <vector>
 
 #include "fused_dev.h"
+#include "gemm_dev.h"
 
 namespace tgk {
 
@@ -205,16 +206,7 @@ struct AttnBwdDesc {
 };
 void attention_bwd(const AttnBwdDesc& a, hipStream_t st);
 
-// ---- GEMM (k_gemm.hip) --------------------------------------------------------------
-// C[z][m][n] = sum_k A[z][m][k] * B[z][k][n], f32 MFMA, f32 accumulate.
-// Batch index z decomposes as (z / bdiv, z % bdiv) with two strides per operand, so a
-// permuted 4-d view [B, H, T, d] is read in place.
-struct GemmDesc {
-  int64_t M, N, K, batch, bdiv;
-  const float* A; int64_t sAz0, sAz1, sAm, sAk;
-  const float* B; int64_t sBz0, sBz1, sBk, sBn;
-  float* C; int64_t sCz0, sCz1, sCm, sCn;
-};
+// ---- GEMM (k_gemm.hip; GemmDesc and the tile in gemm_dev.h) ----------------------------
 // `work` must hold gemm_workspace_floats(d) floats (split-K partials).
 int64_t gemm_workspace_floats(const GemmDesc& d);
 void gemm(const GemmDesc& d, float* work, hipStream_t st);
@@ -224,6 +216,17 @@ void gemm(const GemmDesc& d, float* work, hipStream_t st);
 // its tile-start array, sets the launch's block count); the image must be copied to
 // device memory and stay there while the launch can run.
 int gemm_group_kind(const GemmDesc& d);
+// A GEMM whose epilogue runs a fused element group (a kernel generated at run time): the
+// tile configuration its plain launch would use, the group input that reads the product
+// (h_in) and the product's row length N. gemm_epi_cfg fills the configuration, the launch
+// arguments and the block count; false when d has no direct-to-LDS single-pass launch.
+struct GemmEpiCfg {
+  int bm, bn, bk, ns, nt, kg;
+  bool ak, bkf;
+  int64_t N;
+  int h_in;
+};
+bool gemm_epi_cfg(const GemmDesc& d, GemmEpiCfg& c, gd::GemmArgs& g, int64_t& blocks);
 // True when d on its own would run one pass of 64 x 64 tiles (the grouped tiling), so a
 // grouped launch computes it with the same arithmetic.
 bool gemm_prefers_group(const GemmDesc& d);

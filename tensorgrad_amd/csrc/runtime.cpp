@@ -307,10 +307,21 @@ class Runtime {
     hipFunction_t fn = nullptr;
     tgk::JitArgs args{};
     int64_t grid = 0;
+    bool gemm = false;          // a GEMM with a fused epilogue: launched with gargs first
+    int threads = 256;
+    tgk::gd::GemmArgs gargs{};
   };
   std::deque<JitSlot> jit_slots_;
   std::vector<tgk::JitKernel> jit_pending_;
   void jit_finish();
+  void launch_jit(size_t js, hipStream_t st) {
+    JitSlot& j = jit_slots_[js];
+    void* p1[] = {&j.args};
+    void* p2[] = {&j.gargs, &j.args};
+    const hipError_t e = hipModuleLaunchKernel(j.fn, (unsigned)j.grid, 1, 1, (unsigned)j.threads, 1, 1, 0, st,
+                                               j.gemm ? p2 : p1, nullptr);
+    if (e != hipSuccess) throw Error(TG_DEVICE_ERROR, std::string("generated kernel launch: ") + hipGetErrorString(e));
+  }
   void form_groups();
   void lower_group(int gi);
 
@@ -374,6 +385,16 @@ class Runtime {
   std::vector<char> defer_gemm_;     // op -> runs in a grouped launch
   std::set<int> adam_ops_;
   void plan_gemm_groups();
+  // A GEMM whose product only one element-form group reads (contiguously, in its own
+  // iteration order) can run that group in its epilogue: one launch instead of two, and
+  // the product never reaches memory. Opt-in (TG_GEMM_EPI=1): measured on the C4 / C5
+  // groups it is not faster, since the epilogue's per-element loads and stores are 32-bit
+  // and its arithmetic (f64 transcendentals) runs on the GEMM's eight wavefronts per CU
+  // after the matrix work instead of beside other work.
+  bool use_gemm_epi_ = false;
+  std::vector<char> group_done_;     // group already run inside a GEMM epilogue
+  int epi_group(int op, int out, const tgk::GemmDesc& d) const;
+  void lower_gemm_epi(int op, const tgk::GemmDesc& d, int a, int b, int out, int gi);
   // Column sums read only by the optimizer (bias, LayerNorm gain / shift gradients) run
   // together with the grouped GEMMs, kColSumMax per launch.
   std::vector<char> defer_colsum_;
@@ -396,6 +417,7 @@ class Runtime {
 Runtime::Runtime(const char* json, Runtime* par, bool plan_only) : parent(par) {
   if (const char* g = std::getenv("TG_GRAPH")) use_graph_ = std::string(g) != "0";
   if (const char* g = std::getenv("TG_GEMM_GROUP")) use_gemm_group_ = std::string(g) != "0";
+  if (const char* g = std::getenv("TG_GEMM_EPI")) use_gemm_epi_ = std::string(g) == "1";
   if (const char* g = std::getenv("TG_FUSED")) use_jit_ = std::string(g) != "vm";
   if (const char* g = std::getenv("TG_STREAMS")) nstreams_ = std::max(1, std::min(kStreams, std::atoi(g)));
   try {
@@ -830,6 +852,7 @@ void Runtime::lower() {
     for (auto& c : colsum_)
       if (only_optimizer_reads(O(c.first).at("out").i32())) defer_colsum_[c.first] = 1;
   form_groups();
+  group_done_.assign(groups_.size(), 0);
   for (size_t i = 0; i < ops_.size(); ++i) {
     if (is_leaf((int)i) || virtual_[i]) continue;
     if (adam_ops.count((int)i)) continue;
@@ -849,7 +872,7 @@ void Runtime::lower() {
     }
     int gi = group_of_[i];
     if (gi >= 0) {
-      if (groups_[gi].first == (int)i) lower_group(gi);
+      if (groups_[gi].first == (int)i && !group_done_[gi]) lower_group(gi);
       continue;
     }
     if (gemm_done_[i]) continue;
@@ -1411,12 +1434,7 @@ void Runtime::lower_group(int gi) {
     for (int k = 0; k < p.n_out; ++k) sl.args.out[k] = p.out[k];
     sl.args.seed = p.seed;
     jit_pending_.push_back(std::move(jk));
-    return [this, js](hipStream_t st) {
-      JitSlot& j = jit_slots_[js];
-      void* params[] = {&j.args};
-      const hipError_t e = hipModuleLaunchKernel(j.fn, (unsigned)j.grid, 1, 1, 256, 1, 1, 0, st, params, nullptr);
-      if (e != hipSuccess) throw Error(TG_DEVICE_ERROR, std::string("fused group launch: ") + hipGetErrorString(e));
-    };
+    return [this, js](hipStream_t st) { launch_jit(js, st); };
   };
   add_node(std::move(n));
 }
@@ -1901,6 +1919,170 @@ void Runtime::plan_gemm_groups() {
       for (int i : cand[k]) defer_gemm_[i] = 1;
 }
 
+int Runtime::epi_group(int op, int out, const tgk::GemmDesc& d) const {
+  if (view_[out].root != out || !view_[out].contiguous() || d.batch != 1 || d.sCn != 1 || d.sCm != d.N) return -1;
+  for (int o : outputs_) if (root(o) == out) return -1;
+  for (auto& c : captures_) if (root(c.second) == out) return -1;
+  for (auto& w : copy_writebacks_) if (root(w.first) == out) return -1;
+  // every reader of the product (through views) is a member of one element group
+  int gi = -1;
+  std::vector<int> stack{out};
+  while (!stack.empty()) {
+    const int t = stack.back();
+    stack.pop_back();
+    for (int c : consumers_[t]) {
+      if (virtual_[c] && (kinds_[c] == "reshape" || kinds_[c] == "stop_gradient")) {
+        stack.push_back(O(c).at("out").i32());
+        continue;
+      }
+      const int g = group_of_[c];
+      if (g < 0 || (gi >= 0 && g != gi)) return -1;
+      gi = g;
+    }
+  }
+  if (gi < 0 || group_done_[gi] || groups_[gi].row || groups_[gi].first <= op) return -1;
+  const Group& G = groups_[gi];
+  if (prod(G.shape) != d.M * d.N) return -1;
+  tgk::GemmEpiCfg c{};
+  tgk::gd::GemmArgs ga{};
+  int64_t blocks = 0;
+  if (tgk::gemm_workspace_floats(d) != 0 || !tgk::gemm_epi_cfg(d, c, ga, blocks)) return -1;
+  const GroupPlan gp = plan_group(G.ops, false, G.shape);
+  int hits = 0;
+  for (auto& e : gp.ext) {
+    if (root(e.first) == out) {
+      // read whole and in order: a view of the full product with the group's shape
+      if (T_[e.first].numel != T_[out].numel || !view_[e.first].contiguous() || T_[e.first].shape != G.shape) return -1;
+      ++hits;
+    } else if (!ready_now(e.first)) {
+      return -1;
+    }
+  }
+  if (hits != 1 || (gp.seed >= 0 && !ready_now(gp.seed))) return -1;
+  return gi;
+}
+
+void Runtime::lower_gemm_epi(int op, const tgk::GemmDesc& d, int a, int b, int out, int gi) {
+  group_done_[gi] = 1;
+  const Group G = groups_[gi];
+  const GroupPlan gp = plan_group(G.ops, false, G.shape);
+  Node n;
+  n.kind = "gemm";
+  n.op = op;
+  n.detail = "gemm+";
+  for (size_t q = 0; q < G.ops.size(); ++q) n.detail += (q ? "," : "") + kinds_[G.ops[q]];
+  n.shape = shape_str(T_[out].shape) + " x" + std::to_string(G.ops.size());
+  n.reads.push_back(root(a));
+  n.reads.push_back(root(b));
+  for (auto& e : gp.ext) if (root(e.first) != out) n.reads.push_back(root(e.first));
+  if (gp.seed >= 0) n.reads.push_back(root(gp.seed));
+  for (int t : gp.outs) n.writes.push_back(root(t));
+  n.flops = 2.0 * (double)d.M * d.N * d.K * d.batch;
+  n.bytes = 4.0 * ((double)T_[a].numel + T_[b].numel);
+  for (auto& e : gp.ext) if (root(e.first) != out) n.bytes += 4.0 * T_[e.first].numel;
+  for (int t : gp.outs) n.bytes += 4.0 * T_[t].numel;
+  const size_t code_off = fused_code_.size();
+  fused_code_.insert(fused_code_.end(), gp.code.begin(), gp.code.end());
+  n.bind = [=]() -> std::function<void(hipStream_t)> {
+    check_gemm_spans(d, a, b, out);
+    const Dims F = G.shape;
+    const int64_t cnt = prod(F);
+    if (cnt >= (int64_t(1) << 31)) throw Error(TG_INVALID_ARGUMENT, "GEMM epilogue: 2^31 or more elements");
+    // The group's element program, one element per call: operands by their broadcast
+    // strides over F (merged dims), the product as input h_in.
+    tgk::FusedProgram p;
+    memset(&p, 0, sizeof(p));
+    const size_t nx = gp.ext.size();
+    std::vector<Dims> bs(nx, Dims(F.size(), 0));
+    for (size_t q = 0; q < nx; ++q) {
+      const View& v = view_[gp.ext[q].first];
+      const int off = (int)F.size() - (int)v.dims.size();
+      if (off < 0 || gp.ext[q].second != 0) throw Error(TG_INTERNAL, "GEMM epilogue: operand class");
+      for (size_t dd = 0; dd < v.dims.size(); ++dd) bs[q][off + dd] = v.dims[dd] == 1 ? 0 : v.strides[dd];
+      check_span("epilogue operand", T_[v.root].numel, 0, F.data(), bs[q].data(), (int)F.size());
+    }
+    Dims md;
+    std::vector<Dims> ms(nx);
+    for (size_t dd = 0; dd < F.size(); ++dd) {
+      if (F[dd] == 1) continue;
+      bool merge = !md.empty();
+      for (size_t q = 0; q < nx && merge; ++q) merge = ms[q].back() == bs[q][dd] * F[dd];
+      if (merge) {
+        md.back() *= F[dd];
+        for (size_t q = 0; q < nx; ++q) ms[q].back() = bs[q][dd];
+      } else {
+        md.push_back(F[dd]);
+        for (size_t q = 0; q < nx; ++q) ms[q].push_back(bs[q][dd]);
+      }
+    }
+    if (md.empty()) { md.push_back(1); for (auto& m : ms) m.push_back(0); }
+    if (md.size() > (size_t)tgk::kMaxRank) throw Error(TG_INTERNAL, "GEMM epilogue: rank too large");
+    const int R = (int)md.size();
+    const Dims cs = contiguous_strides(md);
+    p.n_in = (int)nx;
+    p.nregs = gp.nregs;
+    p.vec = 1;
+    p.rank = R;
+    for (int dd = 0; dd < R; ++dd) p.div[dd] = tgk::make_fastdiv((uint32_t)md[dd]);
+    int h_in = -1;
+    for (size_t q = 0; q < nx; ++q) {
+      const View& v = view_[gp.ext[q].first];
+      bool contig = true, scalar = true;
+      for (int dd = 0; dd < R; ++dd) {
+        if (ms[q][dd] != cs[dd]) contig = false;
+        if (ms[q][dd] != 0) scalar = false;
+      }
+      const int m = contig ? tgk::FM_CONTIG : (scalar ? tgk::FM_SCALAR : tgk::FM_STRIDED);
+      if (v.root == out) {
+        if (m != tgk::FM_CONTIG) throw Error(TG_INTERNAL, "GEMM epilogue: the product is not read in order");
+        h_in = (int)q;
+      }
+      p.in[q] = ptr_[v.root];
+      p.in_dt[q] = kdt(T_[gp.ext[q].first].dt);
+      p.in_mode[q] = m;
+      p.in_inner[q] = (int32_t)ms[q][R - 1];
+      if (m == tgk::FM_STRIDED) p.any_strided = 1;
+      for (int dd = 0; dd < R; ++dd) p.in_strides[q][dd] = (int32_t)ms[q][dd];
+    }
+    p.n_out = (int)gp.outs.size();
+    for (size_t q = 0; q < gp.outs.size(); ++q) {
+      const int t = gp.outs[q];
+      p.out[q] = dptr(t);
+      p.out_dt[q] = kdt(T_[t].dt);
+      p.out_reg[q] = gp.out_reg[q];
+      if (T_[root(t)].numel < cnt || T_[t].numel != cnt || !view_[t].contiguous())
+        throw Error(TG_INTERNAL, "GEMM epilogue: output size mismatch");
+    }
+    p.seed = gp.seed >= 0 ? (const int32_t*)dptr(gp.seed) : nullptr;
+    p.n_instr = (int)gp.code.size();
+    tgk::GemmDesc e = d;
+    e.A = (const float*)dptr(a);
+    e.B = (const float*)dptr(b);
+    e.C = nullptr;   // the product is not stored
+    tgk::GemmEpiCfg c{};
+    tgk::gd::GemmArgs ga{};
+    int64_t blocks = 0;
+    if (!tgk::gemm_epi_cfg(e, c, ga, blocks)) throw Error(TG_INTERNAL, "GEMM epilogue: no direct-to-LDS launch");
+    c.N = d.N;
+    c.h_in = h_in;
+    tgk::JitKernel jk = tgk::gemm_epi_kernel(p, fused_code_.data() + code_off, c);
+    const size_t js = jit_slots_.size();
+    jit_slots_.emplace_back();
+    JitSlot& sl = jit_slots_.back();
+    sl.name = jk.name;
+    sl.grid = blocks;
+    sl.gemm = true;
+    sl.threads = c.nt;
+    sl.gargs = ga;
+    for (int k = 0; k < p.n_in; ++k) sl.args.in[k] = p.in[k];
+    for (int k = 0; k < p.n_out; ++k) sl.args.out[k] = p.out[k];
+    sl.args.seed = p.seed;
+    jit_pending_.push_back(std::move(jk));
+    return [this, js](hipStream_t st) { launch_jit(js, st); };
+  };
+  add_node(std::move(n));
+}
+
 void Runtime::emit_gemm_group(const std::vector<DeferredGemm>& grp) {
   const int kind = grp.front().kind;
   Node n;
@@ -2372,6 +2554,13 @@ void Runtime::lower_op(int i) {
       if (grp.size() > 1) {
         for (const DeferredGemm& g : grp) gemm_done_[g.op] = 1;
         emit_gemm_group(grp);
+        return;
+      }
+    }
+    if (use_gemm_epi_ && use_jit_) {
+      const int gi = epi_group(i, out, d);
+      if (gi >= 0) {
+        lower_gemm_epi(i, d, a, b, out, gi);
         return;
       }
     }

@@ -313,6 +313,24 @@ def _attention_graph(B, H, T, dh, what):
     return body
 
 
+def _node_ops(g, env):
+    """The launch list ('ops' of each node) of a runtime created under `env`."""
+    import os
+    old = {k: os.environ.get(k) for k in env}
+    os.environ.update(env)
+    try:
+        rt = backend.NativeRuntime(IR.dumps(wire(g)))
+    finally:
+        for k, v in old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+    ops = [n.get('ops', '') for n in rt.describe()['nodes']]
+    rt.destroy()
+    return ops
+
+
 def _run_native(g, inputs, env=None):
     import os
     old = {k: os.environ.get(k) for k in (env or {})}
@@ -409,6 +427,34 @@ def test_fused_attention_backward(B, H, T):
             o.set_home(k, v)
         o.run({'g': g_in})
         gemm_close(got, o.output(), 1e-5)
+
+
+@pytest.mark.parametrize('M,N,K,act', [(512, 256, 256, 'relu'), (4096, 1024, 256, 'gelu'), (300, 64, 128, 'gelu'),
+                                       (1000, 256, 512, 'dropout')])
+def test_gemm_epilogue(M, N, K, act):
+    """With TG_GEMM_EPI=1, a product read only by one pointwise group runs that group in
+    the GEMM's epilogue (a kernel generated per group): bit-identical to the GEMM and the
+    group run apart (the default), and within GEMM tolerance of the oracle."""
+    ins = {'a': _rand([M, K], 101), 'b': _rand([K, N], 102), 'c': _rand([N], 103), 'r': _rand([M, N], 104)}
+
+    def body():
+        h = O.add(O.matmul(tensor_input('a', [M, K]), tensor_input('b', [K, N])), tensor_input('c', [N]))
+        if act == 'relu':
+            y = O.relu(h)
+        elif act == 'gelu':
+            y = O.mul(O.mul(h, 0.5), O.add(O.erf(O.mul(h, 0.7071067811865476)), 1.0))
+        else:
+            y = O.dropout(O.mul(h, tensor_input('r', [M, N])), 0.25)
+        return O.mul(y, 2.0)
+    g = trace_fn(body)
+    got, _ = _run_native(g, ins, {'TG_GEMM_EPI': '1'})
+    ref, _ = _run_native(g, ins)
+    ops = _node_ops(g, {'TG_GEMM_EPI': '1'})
+    assert any(o.startswith('gemm+') for o in ops), ops
+    exact(got, ref)
+    o = pyoracle.OracleRuntime(wire(g))
+    o.run(ins)
+    gemm_close(got, o.output(), 1e-5)
 
 
 @pytest.mark.skip(reason='sums of products as one GEMM are switched off: the transformer step using them '
