@@ -33,7 +33,7 @@ enum FusedOp {
   FO_LOG_SOFTMAX      // row form only
 };
 
-constexpr int kFusedMaxIn = 8;
+constexpr int kFusedMaxIn = 12;
 constexpr int kFusedMaxOut = 8;
 
 // Kernel argument of a generated group kernel: operand and output base pointers, and the

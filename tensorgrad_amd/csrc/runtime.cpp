@@ -1238,11 +1238,34 @@ void Runtime::form_groups() {
       }
     }
     std::sort(cands.begin(), cands.end(), [&](int a, int b) { return groups_[a].first > groups_[b].first; });
+    // Group gi can run at position i instead of at its first op when nothing outside it
+    // reads its members' results before i (through views; patterns other than plain ops
+    // and groups are not moved around).
+    auto movable_to_i = [&](int gi) {
+      std::vector<int> stack;
+      for (int m : groups_[gi].ops) stack.push_back(ops_[m]->at("out").i32());
+      while (!stack.empty()) {
+        const int t = stack.back();
+        stack.pop_back();
+        for (int c : consumers_[t]) {
+          if (group_of_[c] == gi || c == (int)i) continue;
+          if (virtual_[c] && !is_leaf(c) && kinds_[c] != "matmul" && kinds_[c] != "matmul_batched") {
+            stack.push_back(ops_[c]->at("out").i32());
+            continue;
+          }
+          if (attn_of_[c] >= 0 || mul_absorbed_[c] || colsum_.count(c)) return false;
+          const int pos = group_of_[c] >= 0 ? groups_[group_of_[c]].first : c;
+          if (pos <= (int)i) return false;
+        }
+      }
+      return true;
+    };
     int joined = -1;
     for (int gi : cands) {
       Group& g = groups_[gi];
       const Dims& F = g.shape;
       bool ok = true;
+      bool late = false;   // an input of op i exists only after the group's first op
       bool becomes_row = g.row;
       if (red) {
         ok = T_[fld((int)i, "a")].shape == F;
@@ -1257,7 +1280,7 @@ void Runtime::form_groups() {
         if (!ok) break;
         const bool in_g = producer_group(t) == gi;
         if (!in_g) {
-          if (eff_pos(t) >= g.first) ok = false;
+          if (eff_pos(t) >= g.first) late = true;
           continue;
         }
         if (k == "dropout" && t == fld((int)i, "seed")) continue;
@@ -1267,12 +1290,14 @@ void Runtime::form_groups() {
         if (So == F) { if (!(ts == F || row_class(ts, F) == 2)) ok = false; }
         else if (ts != So) ok = false;
       }
+      if (ok && late) ok = movable_to_i(gi);
       if (!ok) continue;
       std::vector<int> ops = g.ops;
       ops.push_back((int)i);
       if (!fits(ops, becomes_row, F)) continue;
       g.ops.push_back((int)i);
       g.row = becomes_row;
+      if (late) g.first = (int)i;   // the group now runs where its last input exists
       group_of_[i] = gi;
       joined = gi;
       break;
