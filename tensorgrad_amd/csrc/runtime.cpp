@@ -339,6 +339,12 @@ class Runtime {
   void lower();
   void allocate();
   void bind_all();
+  // Launches whose results do not change between steps (constants and what is computed
+  // only from them, e.g. the loss gradient seed) run once after the buffers are bound;
+  // their outputs live in the persistent region.
+  std::vector<Node> init_nodes_;
+  std::set<int> init_roots_;
+  void split_init_nodes();
   void launch_all(hipStream_t st);
   void upload_inputs(int n, const char* const* names, const void* const* data, const int64_t* nbytes, bool device);
   void stage_scalars();
@@ -459,11 +465,16 @@ Runtime::Runtime(const char* json, Runtime* par, bool plan_only) : parent(par) {
   compute_views();
   lower();
   if (!plan_only) hip_check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate");
+  split_init_nodes();
   allocate();
   schedule();
   bind_all();   // in plan-only mode this still runs every launch's host-side bounds proof
   jit_finish();
   prepare_streams();
+  if (!plan_only && !init_nodes_.empty()) {
+    for (auto& n : init_nodes_) n.launch(stream_);
+    hip_check(hipStreamSynchronize(stream_), "hipStreamSynchronize(constants)");
+  }
 }
 
 Runtime::~Runtime() {
@@ -2671,6 +2682,28 @@ void Runtime::lower_op(int i) {
 // Device memory: persistent roots get dedicated regions; intermediates are pooled by
 // liveness over the node order (best fit). Tensor inputs live in one contiguous region
 // so a step uploads them with a single copy.
+void Runtime::split_init_nodes() {
+  init_nodes_.clear();
+  init_roots_.clear();
+  std::set<int> pinned;
+  for (int o : outputs_) pinned.insert(root(o));
+  for (auto& c : captures_) pinned.insert(root(c.second));
+  for (auto& w : copy_writebacks_) pinned.insert(root(w.first));
+  std::vector<Node> step;
+  for (auto& n : nodes_) {
+    bool inv = n.kind != "adam_multi" && !n.writes.empty();
+    for (int r : n.reads) if (!init_roots_.count(r)) inv = false;
+    for (int w : n.writes) if (pinned.count(w)) inv = false;
+    if (inv) {
+      for (int w : n.writes) init_roots_.insert(w);
+      init_nodes_.push_back(std::move(n));
+    } else {
+      step.push_back(std::move(n));
+    }
+  }
+  nodes_ = std::move(step);
+}
+
 void Runtime::allocate() {
   const size_t nT = T_.size();
   ptr_.assign(nT, nullptr);
@@ -2685,6 +2718,7 @@ void Runtime::allocate() {
   for (int o : outputs_) persistent[root(o)] = true;
   for (auto& c : captures_) persistent[root(c.second)] = true;
   for (auto& w : copy_writebacks_) persistent[root(w.first)] = true;
+  for (int r : init_roots_) persistent[r] = used[r] = true;
 
   std::vector<int> def(nT, -1), last(nT, -1);
   for (size_t ni = 0; ni < nodes_.size(); ++ni) {
@@ -2847,6 +2881,11 @@ void Runtime::jit_finish() {
 }
 
 void Runtime::bind_all() {
+  for (auto& n : init_nodes_) {
+    for (int r : n.writes) if (!ptr_[r]) throw Error(TG_INTERNAL, "unallocated output in node " + n.kind);
+    cur_ws_ = workspace_;
+    n.launch = n.bind();
+  }
   for (auto& n : nodes_) {
     for (int r : n.reads) if (!ptr_[r]) throw Error(TG_INTERNAL, "unallocated operand in node " + n.kind);
     for (int r : n.writes) if (!ptr_[r]) throw Error(TG_INTERNAL, "unallocated output in node " + n.kind);
