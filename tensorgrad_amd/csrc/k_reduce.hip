@@ -6,8 +6,8 @@
 #include "kernels.h"
 
 #include <algorithm>
-
 #include <cmath>
+#include <stdexcept>
 
 namespace tgk {
 namespace {
@@ -262,86 +262,146 @@ __global__ void k_sum_finish(const double* __restrict__ part, float* __restrict_
 
 // Column sums in one launch: out[c] = f32(sum_r x(r, c) / div), c < C, r < R, where
 // x = a[r rs + c] or the f32 product a[r rs + c] * b[r rs + c]; blockIdx.z picks one of
-// several independent sums launched together. Block (x, y) takes columns [64x, 64x + 64)
-// and rows [y chunk, (y + 1) chunk): lane l of wave w sums column 64x + l over rows
-// y chunk + w, + 4, ... in order (f64), and the four waves combine in order through LDS
-// into the block's partial. The last block of a column block to finish (counted on
-// counters[x]) adds the chunk partials in a fixed tree (wave w takes chunks w, w + 4, ...
-// in order, then waves in order) and resets its counter, so results do not depend on
-// scheduling and the launch leaves every counter at zero for the next one.
-__global__ __launch_bounds__(256) void k_colsum(const ColSumBatch batch) {
-  const ColSum& cs = batch.s[blockIdx.z];
-  if ((int64_t)blockIdx.x >= cs.nx || (int)blockIdx.y >= cs.nchunks) return;
-  __shared__ double red[4][64];
+// several independent sums launched together, their blocks numbered one after another
+// (sum i's from blk0; a 1-D grid with no idle blocks). A block has kColWaves wavefronts;
+// lane l owns L consecutive columns (L = 4 when C allows, else 1), so block (x, y) of a
+// sum takes columns [64 L x, 64 L (x + 1)) and rows [y chunk, (y + 1) chunk). Wave w sums its lane's
+// columns over rows y chunk + w, + kColWaves, ... in order (f64), and the waves combine in
+// order through LDS into the block's partial. The last block of a column block to finish
+// (counted on counters[x]) adds the chunk partials in a fixed tree (thread j of a
+// column's group takes chunks j, j + TPC, ... in order, then the group in order) and
+// resets its counter, so results do not depend on scheduling and the launch leaves every
+// counter at zero for the next one.
+constexpr int kColWaves = 8;
+constexpr int kColThreads = kColWaves * 64;
+
+__global__ __launch_bounds__(kColThreads) void k_colsum(const ColSumBatch batch) {
+  int z = 0;
+  for (int i = 1; i < batch.n; ++i)
+    if ((int)blockIdx.x >= batch.s[i].blk0) z = i;
+  const ColSum& cs = batch.s[z];
+  const int loc = (int)blockIdx.x - cs.blk0;
+  const int bx = loc % cs.nx, y = loc / cs.nx;
+  constexpr int NW = kColWaves;
+  __shared__ double red[NW][256];
   __shared__ int last;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int64_t C = cs.C, rs = cs.rs;
   const int nchunks = cs.nchunks;
-  const int64_t c = (int64_t)blockIdx.x * 64 + lane;
-  const int y = blockIdx.y;
+  const int L = cs.cpl;                               // columns per lane (1 or 4)
+  const int64_t c0 = ((int64_t)bx * 64 + lane) * L;   // first column of this lane
   const int64_t r0 = (int64_t)y * cs.chunk, r1 = min(cs.R, r0 + cs.chunk);
-  double s = 0.0;
-  if (c < C) {
-    const float* p = cs.a + c;
-    const float* q = cs.b ? cs.b + c : nullptr;
+  double s[4] = {0.0, 0.0, 0.0, 0.0};
+  if (c0 < C) {
+    const float* p = cs.a + c0;
+    const float* q = cs.b ? cs.b + c0 : nullptr;
     int64_t r = r0 + w;
-    for (; r + 60 < r1; r += 64) {   // sixteen rows in flight, added in row order
-      float v[16];
+    if (cs.aligned) {
+      typedef float f4 __attribute__((ext_vector_type(4)));
+      for (; r < r1; r += 8 * NW) {   // eight rows in flight, added in row order
+        f4 v[8];
 #pragma unroll
-      for (int u = 0; u < 16; ++u) v[u] = p[(r + 4 * u) * rs];
-      if (q) {
-        float m[16];
+        for (int u = 0; u < 8; ++u)
+          v[u] = r + NW * u < r1 ? *reinterpret_cast<const f4*>(p + (r + NW * u) * rs) : f4{0.f, 0.f, 0.f, 0.f};
+        if (q) {
+          f4 m[8];
 #pragma unroll
-        for (int u = 0; u < 16; ++u) m[u] = q[(r + 4 * u) * rs];
+          for (int u = 0; u < 8; ++u)
+            m[u] = r + NW * u < r1 ? *reinterpret_cast<const f4*>(q + (r + NW * u) * rs) : f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int u = 0; u < 16; ++u) v[u] = v[u] * m[u];
+          for (int u = 0; u < 8; ++u) v[u] = v[u] * m[u];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          if (r + NW * u < r1)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) s[e] += (double)v[u][e];
       }
+    } else {
+      const int n = (int)min<int64_t>(L, C - c0);
+      for (; r < r1; r += 4 * NW) {   // four rows in flight
+        float v[4][4];
 #pragma unroll
-      for (int u = 0; u < 16; ++u) s += (double)v[u];
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[u][e] = e < n && r + NW * u < r1 ? p[(r + NW * u) * rs + e] : 0.0f;
+        if (q) {
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              v[u][e] = v[u][e] * (e < n && r + NW * u < r1 ? q[(r + NW * u) * rs + e] : 0.0f);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          if (r + NW * u < r1)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) s[e] += (double)v[u][e];
+      }
     }
-    for (; r < r1; r += 4) s += (double)(q ? p[r * rs] * q[r * rs] : p[r * rs]);
   }
-  red[w][lane] = s;
+  // the waves' sums in order, per column of the block (column lane L + e at index lane L + e)
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    if (e < L) red[w][lane * L + e] = s[e];
   __syncthreads();
-  const double bs = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
+  const int64_t cb = (int64_t)bx * 64 * L;    // first column of the block
+  const int ncol = (int)min<int64_t>(64 * L, C - cb);
+  // thread t < 64 L finishes column cb + t
+  double bs = 0.0;
+  if ((int)threadIdx.x < ncol) {
+    bs = red[0][threadIdx.x];
+#pragma unroll
+    for (int v = 1; v < NW; ++v) bs += red[v][threadIdx.x];
+  }
   if (nchunks == 1) {
-    if (w == 0 && c < C) cs.out[c] = (float)(bs / cs.div);
+    if ((int)threadIdx.x < ncol) cs.out[cb + threadIdx.x] = (float)(bs / cs.div);
     return;
   }
   // Partials, the counter and the final reads are device-scope atomic accesses: coherent
   // across the XCDs' separate L2 caches without a full L2 write-back (which a device-scope
   // fence costs). Each wave's partial stores complete (vmcnt) before the block counts in.
   double* part = cs.part;
-  if (w == 0 && c < C) __hip_atomic_store(&part[(int64_t)y * C + c], bs, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if ((int)threadIdx.x < ncol)
+    __hip_atomic_store(&part[(int64_t)y * C + cb + threadIdx.x], bs, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0)
-    last = __hip_atomic_fetch_add(&cs.counters[blockIdx.x], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+    last = __hip_atomic_fetch_add(&cs.counters[bx], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
            (unsigned)(nchunks - 1);
   __syncthreads();
   if (!last) return;
-  auto ld = [&](int q) { return __hip_atomic_load(&part[(int64_t)q * C + c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+  // The last block adds the chunks' partials: column cb + c (c < 64 L) is summed by the
+  // TPC = kColThreads / (64 L) threads c + 64 L j, thread j over chunks j, j + TPC, ... in
+  // order (eight loads in flight); thread c then adds the TPC sums in order j = 0, 1, ...
+  const int cw = 64 * L;
+  const int tpc = kColThreads / cw;
+  const int col = threadIdx.x % cw, sub = threadIdx.x / cw;
   double t = 0.0;
-  if (c < C) {
-    int q = w;
-    for (; q + 60 < nchunks; q += 64) {
-      double v[16];
+  if (col < ncol) {
+    const double* pc = part + cb + col;
+    for (int ch = sub; ch < nchunks; ch += 8 * tpc) {
+      double v[8];
 #pragma unroll
-      for (int u = 0; u < 16; ++u) v[u] = ld(q + 4 * u);
+      for (int u = 0; u < 8; ++u)
+        v[u] = ch + u * tpc < nchunks
+                   ? __hip_atomic_load(pc + (int64_t)(ch + u * tpc) * C, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                   : 0.0;
 #pragma unroll
-      for (int u = 0; u < 16; ++u) t += v[u];
+      for (int u = 0; u < 8; ++u)
+        if (ch + u * tpc < nchunks) t += v[u];
     }
-    double v[16];
-#pragma unroll
-    for (int u = 0; u < 16; ++u) v[u] = q + 4 * u < nchunks ? ld(q + 4 * u) : 0.0;
-#pragma unroll
-    for (int u = 0; u < 16; ++u)
-      if (q + 4 * u < nchunks) t += v[u];
   }
-  red[w][lane] = t;
+  __syncthreads();                                    // the block's reads of red are done
+  reinterpret_cast<double*>(red)[threadIdx.x] = t;    // red as [tpc][64 L]
   __syncthreads();
-  if (w == 0 && c < C) cs.out[c] = (float)((((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane]) / cs.div);
-  if (threadIdx.x == 0) __hip_atomic_store(&cs.counters[blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if ((int)threadIdx.x < ncol) {
+    const double* rr = reinterpret_cast<const double*>(red);
+    double u = rr[threadIdx.x];
+    for (int j = 1; j < tpc; ++j) u += rr[j * cw + threadIdx.x];
+    cs.out[cb + threadIdx.x] = (float)(u / cs.div);
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(&cs.counters[bx], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Few cells with up to 64K terms each: one 256-thread block per cell. Thread t sums terms
@@ -377,18 +437,24 @@ bool block_form(const Strided& red, int64_t ncells, int64_t nred) {
 // in flight per lane), more rows per chunk only past 256 chunks; fewer chunks when the
 // column blocks alone fill the chip.
 struct ColPlan { int64_t nx; int64_t chunk; int nchunks; };
+// Columns per lane of a column sum: four consecutive columns when C is a multiple of 4
+// (and at least 256), so a wavefront reads 1 KiB of a row per access.
+int col_lanes(int64_t C) { return C % 4 == 0 && C >= 256 ? 4 : 1; }
 bool col_form(const Strided& cells, const Strided& red) {
   return cells.rank == 1 && cells.s0[0] == 1 && red.rank == 1;
 }
-// `share` sums run in one launch: together they aim at ~1024 blocks (a lone sum at 512),
-// so a batch of many sums gets fewer, longer row chunks per sum.
-ColPlan col_plan(int64_t C, int64_t R, int share) {
+// Row chunks sized by bytes: a block reads about 256 KiB of its sum's operands (terms = 2
+// when a sum reads the product of two arrays), each of its waves between 1 and 64 rows,
+// at most 256 chunks per sum. Sums of a batch then take block counts in proportion to
+// their size, and the blocks of one launch finish together.
+ColPlan col_plan(int64_t C, int64_t R, int terms) {
   ColPlan p;
-  p.nx = (C + 63) / 64;
-  const int64_t target = share <= 1 ? 512 : std::max<int64_t>(64, 1024 / share);
-  int64_t want = (target + p.nx - 1) / p.nx;
-  int64_t n = (R + 63) / 64;
-  if (n > want) n = want;
+  const int L = col_lanes(C);
+  p.nx = (C + 64 * L - 1) / (64 * L);
+  const int64_t row_bytes = std::min<int64_t>(C, 64 * L) * 4 * std::max(terms, 1);
+  int64_t rows = (262144 / row_bytes) / kColWaves * kColWaves;
+  rows = std::min<int64_t>(std::max<int64_t>(rows, kColWaves), 64 * kColWaves);
+  int64_t n = (R + rows - 1) / rows;
   if (n > 256) n = 256;
   if (n < 1) n = 1;
   p.chunk = (R + n - 1) / n;
@@ -459,35 +525,40 @@ int64_t sum_workspace_doubles(const Strided& cells, const Strided& red, int64_t 
 }
 
 ColSum colsum_desc(const float* a, const float* b, float* out, int64_t C, int64_t R, int64_t rs, double div,
-                   double* part, unsigned* counters, int share) {
-  const ColPlan p = col_plan(C, R, share);
+                   double* part, unsigned* counters) {
+  const ColPlan p = col_plan(C, R, b ? 2 : 1);
   ColSum c{};
   c.a = a; c.b = b; c.out = out;
   c.C = C; c.R = R; c.rs = rs; c.chunk = p.chunk;
   c.nchunks = p.nchunks; c.nx = (int)p.nx;
+  c.cpl = col_lanes(C);
+  auto al = [](const float* x) { return ((uintptr_t)x & 15) == 0; };
+  c.aligned = c.cpl == 4 && rs % 4 == 0 && al(a) && (!b || al(b));
   c.div = div; c.part = part; c.counters = counters;
   return c;
 }
 
-int64_t colsum_workspace_doubles(int64_t C, int64_t R, int share) {
-  const ColPlan p = col_plan(C, R, share);
+int64_t colsum_workspace_doubles(int64_t C, int64_t R, int terms) {
+  const ColPlan p = col_plan(C, R, terms);
   return p.nchunks > 1 ? C * p.nchunks : 0;
 }
 
-int64_t colsum_counters(int64_t C, int64_t R, int share) {
-  const ColPlan p = col_plan(C, R, share);
+int64_t colsum_counters(int64_t C, int64_t R, int terms) {
+  const ColPlan p = col_plan(C, R, terms);
   return p.nchunks > 1 ? p.nx : 0;
 }
 
 void colsum_batch(const ColSumBatch& b, hipStream_t st) {
   if (b.n <= 0) return;
-  int64_t nx = 0, ny = 0;
-  for (int i = 0; i < b.n; ++i) {
-    nx = std::max<int64_t>(nx, b.s[i].nx);
-    ny = std::max<int64_t>(ny, b.s[i].nchunks);
+  ColSumBatch bt = b;
+  int64_t blocks = 0;
+  for (int i = 0; i < bt.n; ++i) {
+    bt.s[i].blk0 = (int)blocks;
+    blocks += (int64_t)bt.s[i].nx * bt.s[i].nchunks;
   }
-  if (nx <= 0) return;
-  k_colsum<<<dim3((unsigned)nx, (unsigned)ny, (unsigned)b.n), 256, 0, st>>>(b);
+  if (blocks <= 0) return;
+  if (blocks > INT32_MAX) throw std::runtime_error("column sums: too many blocks");
+  k_colsum<<<(unsigned)blocks, kColThreads, 0, st>>>(bt);
 }
 
 int64_t sum_counters(const Strided& cells, const Strided& red, int64_t ncells, int64_t nred) {
@@ -502,7 +573,7 @@ void reduce_sum(const float* a, float* out, const Strided& cells, const Strided&
   if (col_form(cells, red)) {
     ColSumBatch bt{};
     bt.n = 1;
-    bt.s[0] = colsum_desc(a, nullptr, out, ncells, nred, red.s0[0], div, work, counters, 1);
+    bt.s[0] = colsum_desc(a, nullptr, out, ncells, nred, red.s0[0], div, work, counters);
     colsum_batch(bt, st);
     return;
   }

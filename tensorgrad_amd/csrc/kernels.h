@@ -120,14 +120,17 @@ void reduce_sum(const float* a, float* out, const Strided& cells, const Strided&
                 double div, double* work, unsigned* counters, hipStream_t st);
 // Column sums of [R, C] row-major operands (row stride rs), out[c] = f32(sum_r x / div)
 // with x = a or the f32 product a * b, up to kColSumMax independent sums in one launch.
-// `part` holds colsum_workspace_doubles(C, R, share) doubles and `counters` colsum_counters(C, R, share)
-// zeroed counters per sum (left zero again).
+// `part` holds colsum_workspace_doubles(C, R, terms) doubles and `counters` colsum_counters(C, R, terms)
+// zeroed counters per sum (left zero again), terms = 2 for a sum of products, else 1.
 struct ColSum {
   const float* a;
   const float* b;
   float* out;
   int64_t C, R, rs, chunk;
   int nchunks, nx;
+  int cpl;                // consecutive columns per lane (4 when C and rs allow, else 1)
+  int aligned;            // cpl == 4 and every row start 16-byte aligned: 128-bit loads
+  int blk0;               // first block of this sum in the launch (set by colsum_batch)
   double div;
   double* part;
   unsigned* counters;
@@ -137,12 +140,10 @@ struct ColSumBatch {
   int n;
   ColSum s[kColSumMax];
 };
-// `share`: how many sums run in the same launch (the row chunking depends on it; pass the
-// same value to all three).
 ColSum colsum_desc(const float* a, const float* b, float* out, int64_t C, int64_t R, int64_t rs, double div,
-                   double* part, unsigned* counters, int share);
-int64_t colsum_workspace_doubles(int64_t C, int64_t R, int share);
-int64_t colsum_counters(int64_t C, int64_t R, int share);
+                   double* part, unsigned* counters);
+int64_t colsum_workspace_doubles(int64_t C, int64_t R, int terms);
+int64_t colsum_counters(int64_t C, int64_t R, int terms);
 void colsum_batch(const ColSumBatch& b, hipStream_t st);
 void row_argmax(const float* a, int32_t* out, int64_t outer, int64_t D, hipStream_t st);
 void log_softmax(const float* a, float* out, int64_t outer, int64_t D, hipStream_t st);

@@ -1636,8 +1636,9 @@ void Runtime::emit_colsums(const std::vector<int>& batch) {
     n.bytes += 4.0 * (c.R * c.C * (c.b >= 0 ? 2 : 1) + c.C);
     n.detail += std::string(n.detail.empty() ? "" : ",") + (c.b >= 0 ? "mul,sum_to_shape" : "sum_to_shape");
     ws_off.push_back(ws);
-    ws += ((size_t)tgk::colsum_workspace_doubles(c.C, c.R, (int)batch.size()) * 8 + 255) & ~(size_t)255;
-    cbase.push_back(take_counters(tgk::colsum_counters(c.C, c.R, (int)batch.size())));
+    const int terms = c.b >= 0 ? 2 : 1;
+    ws += ((size_t)tgk::colsum_workspace_doubles(c.C, c.R, terms) * 8 + 255) & ~(size_t)255;
+    cbase.push_back(take_counters(tgk::colsum_counters(c.C, c.R, terms)));
   }
   workspace_bytes_ = std::max(workspace_bytes_, ws);
   n.bind = [=]() -> std::function<void(hipStream_t)> {
@@ -1651,7 +1652,7 @@ void Runtime::emit_colsums(const std::vector<int>& batch) {
         throw Error(TG_INTERNAL, "column sum: operand smaller than its shape");
       double* part = reinterpret_cast<double*>(reinterpret_cast<char*>(cur_ws_) + ws_off[q]);
       bt.s[q] = tgk::colsum_desc((const float*)dptr(c.a), c.b >= 0 ? (const float*)dptr(c.b) : nullptr,
-                                 (float*)dptr(out), c.C, c.R, c.C, 1.0, part, counters_ + cbase[q], (int)batch.size());
+                                 (float*)dptr(out), c.C, c.R, c.C, 1.0, part, counters_ + cbase[q]);
     }
     return [bt](hipStream_t st) { tgk::colsum_batch(bt, st); };
   };
