@@ -278,6 +278,8 @@ __global__ void k_splitk_reduce(const float* __restrict__ work, int splits, int6
 
 struct Plan { int bm, bn, bk, splits; int64_t kps; };
 
+constexpr int64_t kShortK = 1024;
+
 Plan plan_for(const GemmDesc& d) {
   auto tiles = [&](int bm, int bn) { return ((d.M + bm - 1) / bm) * ((d.N + bn - 1) / bn) * d.batch; };
   // Tile shape: least padded work per CU, counted as (rounds of 256 tiles) x tile area, so
@@ -291,6 +293,10 @@ Plan plan_for(const GemmDesc& d) {
     if (best < 0 || cost < best) { best = cost; p = c; }
   }
   const int64_t t = tiles(p.bm, p.bn);
+  // 64 x 64 tiles two or more per CU with short K: 32-k stages (64 KiB of LDS instead of
+  // 128), so two blocks share a CU and one's operand loads overlap the other's MFMAs (long
+  // K keeps the deeper 64-k ring).
+  if (p.bm == 64 && p.bn == 64 && t >= 512 && d.K <= kShortK) p.bk = 32;
   if (t < 128 && d.K >= 1024) {
     int64_t want = (256 + t - 1) / t;
     int64_t maxs = d.K / 256;
@@ -360,6 +366,7 @@ void gemm(const GemmDesc& d, float* work, hipStream_t st) {
     if (p.bm == 128 && p.bn == 128) TG_DMA_LAUNCH(128, 128, 32, 3, 512, 1);
     else if (p.bm == 128) TG_DMA_LAUNCH(128, 64, 32, 3, 512, 1);
     else if (p.bn == 128) TG_DMA_LAUNCH(64, 128, 32, 3, 512, 1);
+    else if (p.bk == 32) TG_DMA_LAUNCH(64, 64, 32, 4, 512, 2);
     else TG_DMA_LAUNCH(64, 64, 64, 4, 512, 2);
 #undef TG_DMA_LAUNCH
   } else {
@@ -412,7 +419,7 @@ bool gemm_epi_cfg(const GemmDesc& d, GemmEpiCfg& c, GemmArgs& g, int64_t& blocks
   if (p.splits != 1 || !dma_ok(d, p, ak, bk)) return false;
   // the same instantiation gemm() launches for this plan
   c.bm = p.bm; c.bn = p.bn; c.bk = p.bk;
-  c.ns = p.bm == 64 && p.bn == 64 ? 4 : 3;
+  c.ns = p.bm == 64 && p.bn == 64 ? 4 : 3;   // (64 x 64 with p.bk = 32: the 64 KiB variant)
   c.nt = 512;
   c.kg = p.bm == 64 && p.bn == 64 ? 2 : 1;
   c.ak = ak; c.bkf = bk;
@@ -423,7 +430,7 @@ bool gemm_epi_cfg(const GemmDesc& d, GemmEpiCfg& c, GemmArgs& g, int64_t& blocks
   return blocks < (int64_t(1) << 31);
 }
 
-size_t gemm_group_table(const GemmDesc* ds, int n, std::vector<unsigned char>& image, int64_t& blocks) {
+size_t gemm_group_table(const GemmDesc* ds, int n, std::vector<unsigned char>& image, int64_t& blocks, int& tiling) {
   const size_t args_bytes = (size_t)n * sizeof(GemmArgs);
   const size_t starts_off = (args_bytes + 15) / 16 * 16;
   image.assign(starts_off + (size_t)(n + 1) * sizeof(uint32_t), 0);
@@ -442,14 +449,28 @@ size_t gemm_group_table(const GemmDesc* ds, int n, std::vector<unsigned char>& i
   starts[n] = (uint32_t)t;
   if (t >= (int64_t(1) << 31)) throw std::runtime_error("gemm group: too many tiles");
   blocks = t;
+  // the plain launch's rule: 32-k stages for two or more tiles per CU when every K is short
+  int64_t kmax = 0;
+  for (int q = 0; q < n; ++q) kmax = std::max(kmax, ds[q].K);
+  tiling = t >= 512 && kmax <= kShortK ? 1 : 0;
   return starts_off;
 }
 
-void gemm_group(const void* dev_image, size_t starts_off, int n, int64_t blocks, int kind, hipStream_t st) {
+void gemm_group(const void* dev_image, size_t starts_off, int n, int64_t blocks, int kind, int tiling,
+                hipStream_t st) {
   if (n <= 0 || blocks <= 0) return;
   const GemmArgs* table = reinterpret_cast<const GemmArgs*>(dev_image);
   const uint32_t* starts = reinterpret_cast<const uint32_t*>(reinterpret_cast<const unsigned char*>(dev_image) + starts_off);
   const dim3 grid((unsigned)blocks);
+  if (tiling == 1) {   // 32-k stages: the 64 KiB-LDS variant, two blocks per CU
+    switch (kind) {
+      case 3: k_gemm_dma_group<64, 64, 32, 4, true, true, 512, 2><<<grid, 512, 0, st>>>(table, starts, n); return;
+      case 2: k_gemm_dma_group<64, 64, 32, 4, true, false, 512, 2><<<grid, 512, 0, st>>>(table, starts, n); return;
+      case 1: k_gemm_dma_group<64, 64, 32, 4, false, true, 512, 2><<<grid, 512, 0, st>>>(table, starts, n); return;
+      case 0: k_gemm_dma_group<64, 64, 32, 4, false, false, 512, 2><<<grid, 512, 0, st>>>(table, starts, n); return;
+      default: throw std::runtime_error("gemm group: bad kind");
+    }
+  }
   switch (kind) {
     case 3: k_gemm_dma_group<64, 64, 64, 4, true, true, 512, 2><<<grid, 512, 0, st>>>(table, starts, n); break;
     case 2: k_gemm_dma_group<64, 64, 64, 4, true, false, 512, 2><<<grid, 512, 0, st>>>(table, starts, n); break;
@@ -484,6 +505,9 @@ __global__ void k_gather_rows(const int32_t* __restrict__ idx, int64_t rows, con
 constexpr int kMaxBucketV = 8192;
 constexpr int kWaveHistV = 1024;
 constexpr int kSeg = 16;
+// s_waitcnt operand for lgkmcnt(0) alone: vmcnt 63 (bits 3:0 and 15:14), expcnt 7 (6:4),
+// lgkmcnt 0 (11:8).
+constexpr int kWaitLds = 0xF | (0x3 << 14) | (0x7 << 4);
 
 __device__ __forceinline__ int block_exclusive_scan(int x, int* lds_tot, int& total) {
   // 256 threads: shuffle-up scan inside each wavefront, then wavefront totals.
@@ -593,12 +617,16 @@ __global__ __launch_bounds__(256) void k_bucket_rows(const int32_t* __restrict__
     const int rank = __popcll(same & below);
     const int count = __popcll(same);
     const bool place = live && t < V;
+    // Every lane's read of its token's cursor completes before the group's last lane
+    // advances it, and the advance before the next group's reads. The waits cover LDS
+    // only (lgkmcnt 0, vmcnt and expcnt left at their maximum): the perm stores stay in
+    // flight across iterations.
     const int base = place ? cnt[w * VP + t] : 0;
-    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_s_waitcnt(kWaitLds);
     __builtin_amdgcn_wave_barrier();
     if (place) perm[base + rank] = (int32_t)r;
     if (place && rank == count - 1) cnt[w * VP + t] = base + count;
-    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_s_waitcnt(kWaitLds);
     __builtin_amdgcn_wave_barrier();
   }
 }

@@ -261,15 +261,15 @@ __global__ void k_sum_finish(const double* __restrict__ part, float* __restrict_
 }
 
 // Column sums in one launch: out[c] = f32(sum_r x(r, c) / div), c < C, r < R, where
-// x = a[r rs + c] or the f32 product a[r rs + c] * b[r rs + c]; blockIdx.z picks one of
-// several independent sums launched together, their blocks numbered one after another
-// (sum i's from blk0; a 1-D grid with no idle blocks). A block has kColWaves wavefronts;
-// lane l owns L consecutive columns (L = 4 when C allows, else 1), so block (x, y) of a
-// sum takes columns [64 L x, 64 L (x + 1)) and rows [y chunk, (y + 1) chunk). Wave w sums its lane's
-// columns over rows y chunk + w, + kColWaves, ... in order (f64), and the waves combine in
-// order through LDS into the block's partial. The last block of a column block to finish
-// (counted on counters[x]) adds the chunk partials in a fixed tree (thread j of a
-// column's group takes chunks j, j + TPC, ... in order, then the group in order) and
+// x = a[r rs + c] or the f32 product a[r rs + c] * b[r rs + c], for one of several
+// independent sums launched together, their blocks numbered one after another (sum i's
+// from blk0; a 1-D grid with no idle blocks). A block has kColWaves wavefronts; lane l
+// owns L consecutive columns (L = 4 when C allows, else 1), so block (x, y) of a sum takes
+// columns [64 L x, 64 L (x + 1)) and rows [y chunk, (y + 1) chunk). Wave w sums its
+// lane's columns over rows y chunk + w, + kColWaves, ... in order (f64), and the waves
+// combine in order through LDS into the block's partial. The last block of a column block
+// to finish (counted on counters[x]) adds the chunk partials in a fixed tree (thread j of
+// a column's group takes chunks j, j + TPC, ... in order, then the group in order) and
 // resets its counter, so results do not depend on scheduling and the launch leaves every
 // counter at zero for the next one.
 constexpr int kColWaves = 8;

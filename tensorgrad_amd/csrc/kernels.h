@@ -214,8 +214,10 @@ void gemm(const GemmDesc& d, float* work, hipStream_t st);
 // Grouped launch of independent GEMMs (whole-K 64 x 64 tiles, no split-K). Problems of one
 // launch share a kind: gemm_group_kind(d) is 0..3, or -1 when d cannot run grouped.
 // gemm_group_table fills the device image of the problem table (returns the offset of
-// its tile-start array, sets the launch's block count); the image must be copied to
-// device memory and stay there while the launch can run.
+// its tile-start array, sets the launch's block count and the tiling gemm_group takes:
+// 1 for 32-k stages, two blocks per CU, when the launch has two or more tiles per CU and
+// short K, else 0); the image must be copied to device memory and stay there while the
+// launch can run.
 int gemm_group_kind(const GemmDesc& d);
 // A GEMM whose epilogue runs a fused element group (a kernel generated at run time): the
 // tile configuration its plain launch would use, the group input that reads the product
@@ -228,11 +230,12 @@ struct GemmEpiCfg {
   int h_in;
 };
 bool gemm_epi_cfg(const GemmDesc& d, GemmEpiCfg& c, gd::GemmArgs& g, int64_t& blocks);
-// True when d on its own would run one pass of 64 x 64 tiles (the grouped tiling), so a
-// grouped launch computes it with the same arithmetic.
+// True when d on its own would run one pass of 64 x 64 tiles (the grouped tiling); the
+// grouped launch's k-stage depth follows its own tile count, as a plain launch's does.
 bool gemm_prefers_group(const GemmDesc& d);
-size_t gemm_group_table(const GemmDesc* ds, int n, std::vector<unsigned char>& image, int64_t& blocks);
-void gemm_group(const void* dev_image, size_t starts_off, int n, int64_t blocks, int kind, hipStream_t st);
+size_t gemm_group_table(const GemmDesc* ds, int n, std::vector<unsigned char>& image, int64_t& blocks, int& tiling);
+void gemm_group(const void* dev_image, size_t starts_off, int n, int64_t blocks, int kind, int tiling,
+                hipStream_t st);
 
 // Embedding pattern: out[r, :] = table[idx[r], :] (zero row when idx out of range).
 void gather_rows(const int32_t* idx, int64_t rows, const float* table, int64_t V, int64_t N, float* out,

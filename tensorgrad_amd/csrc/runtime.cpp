@@ -2149,14 +2149,15 @@ void Runtime::emit_gemm_group(const std::vector<DeferredGemm>& grp) {
     }
     std::vector<unsigned char> img;
     int64_t blocks = 0;
-    const size_t off = tgk::gemm_group_table(ds.data(), (int)ds.size(), img, blocks);
+    int tiling = 0;
+    const size_t off = tgk::gemm_group_table(ds.data(), (int)ds.size(), img, blocks, tiling);
     if (plan_only_) return [](hipStream_t) {};
     void* dev = nullptr;
     hip_check(hipMalloc(&dev, img.size()), "hipMalloc(gemm group table)");
     dev_tables_.push_back(dev);
     hip_check(hipMemcpy(dev, img.data(), img.size(), hipMemcpyHostToDevice), "hipMemcpy(gemm group table)");
     const int np = (int)ds.size();
-    return [=](hipStream_t st) { tgk::gemm_group(dev, off, np, blocks, kind, st); };
+    return [=](hipStream_t st) { tgk::gemm_group(dev, off, np, blocks, kind, tiling, st); };
   };
   add_node(std::move(n));
 }
