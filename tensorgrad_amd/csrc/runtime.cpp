@@ -256,7 +256,9 @@ class Runtime {
   // iteration shape: every member's output for an element group; for a row group (one
   // that contains last-axis reductions) the full [.., D] shape, members producing either
   // that shape or its row shape ([..] or [.., 1]).
-  struct Group { int first; std::vector<int> ops; Dims shape; bool row = false; };
+  // `dups` are pointwise ops of other groups that this element group evaluates again from
+  // their inputs instead of reading their results (never stored here).
+  struct Group { int first; std::vector<int> ops; Dims shape; bool row = false; std::vector<int> dups; };
   // Register plan of a group: external operands (tensor + the broadcast class of the
   // consumer: 0 full, 1 row [..], 2 row [.., 1]), stored outputs, and a linear-scan
   // register assignment (a register is reused after its value's last read).
@@ -268,7 +270,10 @@ class Runtime {
     std::vector<tgk::FusedInstr> code;
     int nregs = 0;
   };
-  GroupPlan plan_group(const std::vector<int>& ops, bool row, const Dims& F) const;
+  GroupPlan plan_group(const std::vector<int>& ops, bool row, const Dims& F,
+                       const std::vector<int>* dups = nullptr) const;
+  bool dup_in(int gi, int m) const;
+  std::vector<char> dropped_;   // op left out of its own group: only groups recomputing it run it
   int producer_group(int t) const;
   int op_class(int m, bool row, const Dims& F) const;
   bool is_row_reduce(int m) const;
@@ -323,6 +328,7 @@ class Runtime {
     if (e != hipSuccess) throw Error(TG_DEVICE_ERROR, std::string("generated kernel launch: ") + hipGetErrorString(e));
   }
   void form_groups();
+  void remat_groups();
   void lower_group(int gi);
 
   bool is_leaf(int op) const {
@@ -406,6 +412,7 @@ class Runtime {
   std::vector<char> defer_colsum_;
   void emit_colsums(const std::vector<int>& batch);
   bool use_gemm_group_ = true;       // TG_GEMM_GROUP=0 keeps every GEMM in place
+  bool use_remat_ = true;            // TG_REMAT=0 stores every value another group reads
   bool only_optimizer_reads(int t) const;
   void flush_deferred_gemms();
   void emit_gemm_group(const std::vector<DeferredGemm>& grp);
@@ -423,6 +430,7 @@ class Runtime {
 Runtime::Runtime(const char* json, Runtime* par, bool plan_only) : parent(par) {
   if (const char* g = std::getenv("TG_GRAPH")) use_graph_ = std::string(g) != "0";
   if (const char* g = std::getenv("TG_GEMM_GROUP")) use_gemm_group_ = std::string(g) != "0";
+  if (const char* g = std::getenv("TG_REMAT")) use_remat_ = std::string(g) != "0";
   if (const char* g = std::getenv("TG_GEMM_EPI")) use_gemm_epi_ = std::string(g) == "1";
   if (const char* g = std::getenv("TG_FUSED")) use_jit_ = std::string(g) != "vm";
   if (const char* g = std::getenv("TG_STREAMS")) nstreams_ = std::max(1, std::min(kStreams, std::atoi(g)));
@@ -863,6 +871,7 @@ void Runtime::lower() {
     for (auto& c : colsum_)
       if (only_optimizer_reads(O(c.first).at("out").i32())) defer_colsum_[c.first] = 1;
   form_groups();
+  if (use_remat_) remat_groups();
   group_done_.assign(groups_.size(), 0);
   for (size_t i = 0; i < ops_.size(); ++i) {
     if (is_leaf((int)i) || virtual_[i]) continue;
@@ -1059,9 +1068,20 @@ int Runtime::op_class(int m, bool row, const Dims& F) const {
   return row_class(T_[O(m).at("out").i32()].shape, F);
 }
 
-Runtime::GroupPlan Runtime::plan_group(const std::vector<int>& ops, bool row, const Dims& F) const {
+bool Runtime::dup_in(int gi, int m) const {
+  const std::vector<int>& d = groups_[gi].dups;
+  return std::find(d.begin(), d.end(), m) != d.end();
+}
+
+Runtime::GroupPlan Runtime::plan_group(const std::vector<int>& own, bool row, const Dims& F,
+                                       const std::vector<int>* dups) const {
   const auto& pw = pointwise_ops();
   GroupPlan gp;
+  // members in graph order (a topological order): the group's own ops and its recomputed ones
+  std::vector<int> ops(own);
+  const std::set<int> dup(dups ? dups->begin() : own.end(), dups ? dups->end() : own.end());
+  ops.insert(ops.end(), dup.begin(), dup.end());
+  std::sort(ops.begin(), ops.end());
   std::set<int> members(ops.begin(), ops.end());
   auto inside = [&](int t) {
     const int gi = producer_group(t);
@@ -1099,6 +1119,9 @@ Runtime::GroupPlan Runtime::plan_group(const std::vector<int>& ops, bool row, co
     if (must_store.count(t)) return true;
     for (int c : consumers_[t]) {
       if (members.count(c)) continue;
+      // a group that evaluates t's producer again reads nothing of t (nor do the
+      // recomputed copies of a dropped consumer: their groups recompute t's producer too)
+      if (group_of_[c] >= 0 && (dup_in(group_of_[c], T_[root(t)].src) || dropped_[c])) continue;
       if (virtual_[c]) {
         const int v = O(c).at("out").i32();
         if (root(v) == root(t) && view_[v].contiguous() && T_[v].numel == T_[root(v)].numel && !read_outside(v))
@@ -1110,6 +1133,7 @@ Runtime::GroupPlan Runtime::plan_group(const std::vector<int>& ops, bool row, co
   };
   std::vector<bool> stored(ops.size(), false);
   for (size_t q = 0; q < ops.size(); ++q) {
+    if (dup.count(ops[q])) continue;   // the owning group stores what others read
     const int t = O(ops[q]).at("out").i32();
     if (read_outside(t)) { stored[q] = true; gp.outs.push_back(t); }
   }
@@ -1206,6 +1230,7 @@ Runtime::GroupPlan Runtime::plan_group(const std::vector<int>& ops, bool row, co
 // pointwise ops on the row shape (LayerNorm, softmax and cross-entropy chains).
 void Runtime::form_groups() {
   group_of_.assign(ops_.size(), -1);
+  dropped_.assign(ops_.size(), 0);
   groups_.clear();
   const auto& pw = pointwise_ops();
   // Position at which a tensor's data exists (views resolve to their root).
@@ -1322,11 +1347,109 @@ void Runtime::form_groups() {
   }
 }
 
+// Recomputation instead of storage. An element group G that reads values a pointwise
+// chain of another group P produced (same shape as G, no dropout, no row reductions)
+// evaluates that chain again from the chain's own inputs, tensors in memory (GEMM
+// outputs, parameters, other nodes' results), when that reads fewer full-size tensors
+// than it saves. Every reader of a recomputed value must be P or G, so a value all of
+// whose outside readers recompute it is no longer stored by P, and P drops members no
+// stored value needs. Recomputed ops run the same per-element code, so the values are
+// the same bits. (For a GELU layer: the forward group stops storing the erf and exp
+// terms of the derivative, the backward group evaluates them from the pre-activation
+// GEMM output.)
+void Runtime::remat_groups() {
+  const auto& pw = pointwise_ops();
+  // ops whose f64 evaluation costs more than reading their f32 result back
+  static const std::set<std::string> costly = {"erf", "tanh", "sigmoid", "sin", "cos"};
+  bool any = false;
+  for (size_t gi = 0; gi < groups_.size(); ++gi) {
+    Group& G = groups_[gi];
+    if (G.row) continue;
+    const GroupPlan gp = plan_group(G.ops, false, G.shape, &G.dups);
+    const int64_t full = prod(G.shape);
+    std::set<int> ext_roots;
+    for (auto& e : gp.ext) ext_roots.insert(root(e.first));
+    std::set<int> cone, leaves;
+    int pulled = 0;
+    for (auto& e : gp.ext) {
+      const int t = e.first;
+      if (e.second != 0 || t != root(t) || T_[t].numel < full) continue;
+      const int P = producer_group(t);
+      if (P < 0 || P == (int)gi) continue;
+      std::set<int> c2 = cone, l2 = leaves;
+      bool ok = true;
+      std::function<void(int)> visit = [&](int u) {
+        if (!ok) return;
+        const int pg = producer_group(u);
+        if (pg < 0) { l2.insert(u); return; }
+        const int m = T_[root(u)].src;
+        if (c2.count(m)) return;
+        if (u != root(u) || !pw.count(kinds_[m]) || kinds_[m] == "dropout" || T_[u].shape != G.shape ||
+            costly.count(kinds_[m])) {
+          ok = false;
+          return;
+        }
+        for (int c : consumers_[u])
+          if (group_of_[c] != pg && group_of_[c] != (int)gi) { ok = false; return; }
+        c2.insert(m);
+        for (int v : op_inputs(*ops_[m])) visit(v);
+      };
+      visit(t);
+      if (!ok) continue;
+      cone = std::move(c2);
+      leaves = std::move(l2);
+      ++pulled;
+    }
+    if (pulled == 0) continue;
+    int new_reads = 0;
+    for (int l : leaves)
+      if (!ext_roots.count(root(l)) && T_[l].numel >= full) ++new_reads;
+    if (new_reads >= pulled) continue;
+    std::vector<int> dups = G.dups;
+    for (int m : cone) dups.push_back(m);
+    const GroupPlan np = plan_group(G.ops, false, G.shape, &dups);
+    if (np.ext.size() > (size_t)tgk::kFusedMaxIn || np.outs.size() > (size_t)tgk::kFusedMaxOut ||
+        np.nregs > tgk::kFusedRegs || np.code.size() > (size_t)tgk::kFusedMaxInstr)
+      continue;
+    G.dups = dups;
+    any = true;
+  }
+  if (!any) return;
+  // drop the members whose results no stored value of their group needs any more
+  for (Group& P : groups_) {
+    if (P.ops.empty()) continue;
+    const GroupPlan gp = plan_group(P.ops, P.row, P.shape, &P.dups);
+    std::set<int> mem(P.ops.begin(), P.ops.end());
+    mem.insert(P.dups.begin(), P.dups.end());
+    std::set<int> live;
+    std::vector<int> work;
+    for (int m : mem)
+      if (std::find(gp.outs.begin(), gp.outs.end(), O(m).at("out").i32()) != gp.outs.end()) {
+        live.insert(m);
+        work.push_back(m);
+      }
+    while (!work.empty()) {
+      const int m = work.back();
+      work.pop_back();
+      for (int u : op_inputs(*ops_[m])) {
+        const int src = T_[root(u)].src;
+        if (src >= 0 && mem.count(src) && live.insert(src).second) work.push_back(src);
+      }
+    }
+    auto dead = [&](int m) { return !live.count(m); };
+    for (int m : P.ops)
+      if (dead(m)) dropped_[m] = 1;
+    P.ops.erase(std::remove_if(P.ops.begin(), P.ops.end(), dead), P.ops.end());
+    P.dups.erase(std::remove_if(P.dups.begin(), P.dups.end(), dead), P.dups.end());
+  }
+}
+
 void Runtime::lower_group(int gi) {
   const Group& g = groups_[gi];
   const Dims F = g.shape;
   const bool row = g.row;
-  GroupPlan gp = plan_group(g.ops, row, F);
+  if (g.ops.empty()) return;   // every result recomputed where it is read
+  GroupPlan gp = plan_group(g.ops, row, F, &g.dups);
   if (gp.ext.size() > (size_t)tgk::kFusedMaxIn || gp.outs.size() > (size_t)tgk::kFusedMaxOut ||
       gp.nregs > tgk::kFusedRegs)
     throw Error(TG_INTERNAL, "fused group exceeds the kernel's limits");
@@ -1334,6 +1457,7 @@ void Runtime::lower_group(int gi) {
   n.op = g.first;
   n.kind = row ? "rowfused" : (g.ops.size() == 1 ? "elementwise" : "fused");
   n.shape = shape_str(F) + " x" + std::to_string(g.ops.size());
+  if (!g.dups.empty()) n.shape += " +" + std::to_string(g.dups.size()) + " recomputed";
   for (size_t q = 0; q < g.ops.size(); ++q) n.detail += (q ? "," : "") + kinds_[g.ops[q]];
   for (auto& e : gp.ext) n.reads.push_back(root(e.first));
   if (gp.seed >= 0) n.reads.push_back(root(gp.seed));
@@ -1977,7 +2101,7 @@ int Runtime::epi_group(int op, int out, const tgk::GemmDesc& d) const {
       gi = g;
     }
   }
-  if (gi < 0 || group_done_[gi] || groups_[gi].row || groups_[gi].first <= op) return -1;
+  if (gi < 0 || group_done_[gi] || groups_[gi].row || groups_[gi].first <= op || !groups_[gi].dups.empty()) return -1;
   const Group& G = groups_[gi];
   if (prod(G.shape) != d.M * d.N) return -1;
   tgk::GemmEpiCfg c{};

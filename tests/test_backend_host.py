@@ -43,6 +43,25 @@ def test_plan_lowers_every_config(key):
         assert sum(1 for n in p['nodes'] if n['kind'] == 'gemm' and n['shape'].endswith('x[27,24]')) == 0
 
 
+def test_gelu_backward_recomputes_instead_of_reading():
+    """The transformer's GELU backward group evaluates the pre-activation and exp terms
+    again from the FC1 GEMM output (the erf term stays stored: its f64 evaluation costs
+    more than reading it), so per layer the forward group reads 1 and writes 2 full
+    [B, T, 4d] tensors and the backward group reads 3 and writes 1, instead of 1 + 4 and
+    4 + 1."""
+    cfg = configs.CONFIGS['transformer']
+    ir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer)
+    nodes = backend.plan(ir.wire_json())['nodes']
+    full = 4 * 32 * 128 * 1024
+    fwd = [n for n in nodes if n['kind'] == 'fused' and 'erf' in n.get('ops', '')]
+    bwd = [n for n in nodes if n['kind'] == 'fused' and 'recomputed' in n['shape']]
+    assert len(fwd) == 4 and len(bwd) == 4
+    for n in fwd:
+        assert full * 3 <= n['bytes'] < full * 3 + 65536, n
+    for n in bwd:
+        assert full * 4 <= n['bytes'] < full * 4 + 65536, n
+
+
 def test_plan_forward_graph_and_small_variants():
     for key in configs.CONFIGS:
         cfg = configs.small_variant(key)

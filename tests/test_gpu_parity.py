@@ -6,6 +6,7 @@ parameter tensor within 1e-4 relative (L2 norm of the difference over the norm o
 oracle's tensor) after 100 optimizer steps. Reduced-size variants with the same topology
 run the full 100 steps; the full-size configs run the steps the oracle can afford.
 """
+import os
 import time
 
 import numpy as np
@@ -102,6 +103,37 @@ def test_grouped_weight_gradients(key):
     w = _update_error(configs.CONFIGS[key], opt={'kind': 'adam', 'lr': float(2 ** 44), 'eps': float(2 ** 20)},
                       want_ops='gemm_group')
     assert w <= GRAD_TOL
+
+
+def test_recomputed_values_are_bit_identical():
+    """Element groups that evaluate another group's pointwise chain again (the GELU
+    backward recomputing the pre-activation and exp terms from the GEMM output) run the
+    same per-element code as the group that used to store them: two training steps give
+    the same parameters bit for bit with recomputation off (TG_REMAT=0) and on."""
+    cfg = configs.small_variant('transformer')
+    ir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer)
+    p0 = ir.initial_params(3)
+    batches = configs.batches(cfg, 2)
+    out = {}
+    for remat in ('0', '1'):
+        old = os.environ.get('TG_REMAT')
+        os.environ['TG_REMAT'] = remat
+        try:
+            rt = backend.NativeRuntime(ir.wire_json())
+        finally:
+            if old is None:
+                os.environ.pop('TG_REMAT', None)
+            else:
+                os.environ['TG_REMAT'] = old
+        shapes = [n['shape'] for n in rt.describe()['nodes']]
+        assert any('recomputed' in s for s in shapes) == (remat == '1'), shapes
+        rt.upload_params(p0)
+        for b in batches:
+            rt.step(b)
+        out[remat] = rt.download_params()
+        rt.destroy()
+    for n in ir.param_names:
+        assert np.array_equal(out['0'][n].view(np.uint32), out['1'][n].view(np.uint32)), n
 
 
 @pytest.mark.parametrize('key', ['mlp_sin', 'char_mlp', 'cnn', 'nerf', 'transformer'])
