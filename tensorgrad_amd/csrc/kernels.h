@@ -135,11 +135,12 @@ struct ColSum {
   double* part;
   unsigned* counters;
 };
-constexpr int kColSumMax = 16;
+constexpr int kColSumMax = 32;
 struct ColSumBatch {
   int n;
   ColSum s[kColSumMax];
 };
+static_assert(sizeof(ColSumBatch) <= 4096, "column-sum batch fits the kernel argument space");
 ColSum colsum_desc(const float* a, const float* b, float* out, int64_t C, int64_t R, int64_t rs, double div,
                    double* part, unsigned* counters);
 int64_t colsum_workspace_doubles(int64_t C, int64_t R, int terms);
