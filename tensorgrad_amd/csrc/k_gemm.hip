@@ -494,23 +494,25 @@ __global__ void k_gather_rows(const int32_t* __restrict__ idx, int64_t rows, con
   }
 }
 
-// Stable counting sort of row ids by token, in one 256-thread block: rows with
-// idx == v land in perm[offs[v] .. offs[v+1]) in increasing row order; tokens outside
-// [0, V) are dropped. Wave w of the block owns a contiguous quarter of the rows (all rows
-// when V > kWaveHistV): a per-wave LDS histogram, one block-wide scan that yields each
-// wave's starting cursor per token, then each wave places its rows 64 at a time. A lane's
-// rank among equal tokens of its group comes from matching the token's bits with ballots.
-// The scan also lays out the segment-sum work: bucket v is cut into ceil(count / kSeg)
-// items starting at item cstart[v]; item_v[i] names the bucket of item i.
+// Stable counting sort of row ids by token, in one block of kBucketWaves wavefronts: rows
+// with idx == v land in perm[offs[v] .. offs[v+1]) in increasing row order; tokens outside
+// [0, V) are dropped. Wave w of the block owns a contiguous 1 / kBucketWaves of the rows
+// (all rows when V > kWaveHistV): a per-wave LDS histogram, one block-wide scan that
+// yields each wave's starting cursor per token, then each wave places its rows 64 at a
+// time. A lane's rank among equal tokens of its group comes from matching the token's bits
+// with ballots. The scan also lays out the segment-sum work: bucket v is cut into
+// ceil(count / kSeg) items starting at item cstart[v]; item i covers perm positions
+// [item_rng[2i], item_rng[2i + 1]).
 constexpr int kMaxBucketV = 8192;
 constexpr int kWaveHistV = 1024;
+constexpr int kBucketWaves = 16;   // wavefronts of the sorting block (1024 threads)
 constexpr int kSeg = 16;
 // s_waitcnt operand for lgkmcnt(0) alone: vmcnt 63 (bits 3:0 and 15:14), expcnt 7 (6:4),
 // lgkmcnt 0 (11:8).
 constexpr int kWaitLds = 0xF | (0x3 << 14) | (0x7 << 4);
 
 __device__ __forceinline__ int block_exclusive_scan(int x, int* lds_tot, int& total) {
-  // 256 threads: shuffle-up scan inside each wavefront, then wavefront totals.
+  // kBucketWaves wavefronts: shuffle-up scan inside each wavefront, then wavefront totals.
   const int lane = threadIdx.x % 64, w = threadIdx.x / 64;
   int inc = x;
 #pragma unroll
@@ -523,7 +525,7 @@ __device__ __forceinline__ int block_exclusive_scan(int x, int* lds_tot, int& to
   int before = 0;
   total = 0;
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
+  for (int k = 0; k < kBucketWaves; ++k) {
     const int t = lds_tot[k];
     if (k < w) before += t;
     total += t;
@@ -532,12 +534,12 @@ __device__ __forceinline__ int block_exclusive_scan(int x, int* lds_tot, int& to
   return before + inc - x;
 }
 
-__global__ __launch_bounds__(256) void k_bucket_rows(const int32_t* __restrict__ idx, int64_t rows, int64_t V,
+__global__ __launch_bounds__(kBucketWaves * 64) void k_bucket_rows(const int32_t* __restrict__ idx, int64_t rows, int64_t V,
                                                      int stash, int32_t* __restrict__ perm, int32_t* __restrict__ offs,
-                                                     int32_t* __restrict__ cstart, int32_t* __restrict__ item_v) {
+                                                     int32_t* __restrict__ cstart, int32_t* __restrict__ item_rng) {
   extern __shared__ int32_t lds[];
-  __shared__ int tot[4];
-  const int nw = V <= kWaveHistV ? 4 : 1;
+  __shared__ int tot[kBucketWaves];
+  const int nw = V <= kWaveHistV ? kBucketWaves : 1;
   const int VP = (int)V + 1;            // slot V counts dropped tokens
   int32_t* cnt = lds;                   // [nw][VP]
   int32_t* tok = lds + nw * VP;         // [rows] when stash != 0
@@ -568,7 +570,7 @@ __global__ __launch_bounds__(256) void k_bucket_rows(const int32_t* __restrict__
   }
   __syncthreads();
   // Scan over tokens: thread j owns tokens [j*seg, (j+1)*seg).
-  const int seg = (VP + 255) / 256;
+  const int seg = (VP + kBucketWaves * 64 - 1) / (kBucketWaves * 64);
   const int v0 = threadIdx.x * seg, v1 = min(VP - 1, v0 + seg);   // token V (dropped) excluded
   int my = 0, myc = 0;
   for (int v = v0; v < v1; ++v) {
@@ -590,7 +592,10 @@ __global__ __launch_bounds__(256) void k_bucket_rows(const int32_t* __restrict__
       c += ck;
     }
     const int nc = (c + kSeg - 1) / kSeg;
-    for (int i = 0; i < nc; ++i) item_v[runc + i] = v;
+    for (int i = 0; i < nc; ++i) {
+      item_rng[2 * (runc + i)] = run + i * kSeg;
+      item_rng[2 * (runc + i) + 1] = min(run + c, run + (i + 1) * kSeg);
+    }
     run += c;
     runc += nc;
   }
@@ -632,18 +637,17 @@ __global__ __launch_bounds__(256) void k_bucket_rows(const int32_t* __restrict__
 }
 
 // Block i sums item i — up to kSeg consecutive rows of one bucket — per column, in row
-// order, in f64.
+// order, in f64. The item's range and the item count load together, then the row ids,
+// then the rows.
 __global__ __launch_bounds__(256) void k_segment_partials(const float* __restrict__ dy, int64_t N, int64_t V,
                                                           const int32_t* __restrict__ perm,
-                                                          const int32_t* __restrict__ offs,
                                                           const int32_t* __restrict__ cstart,
-                                                          const int32_t* __restrict__ item_v,
+                                                          const int32_t* __restrict__ item_rng,
                                                           double* __restrict__ part) {
   const int i = blockIdx.x;
-  if (i >= cstart[V]) return;
-  const int v = item_v[i];
-  const int j0 = offs[v] + (i - cstart[v]) * kSeg;
-  const int j1 = min(offs[v + 1], j0 + kSeg);
+  const int nitems = cstart[V];
+  const int j0 = item_rng[2 * i], j1 = item_rng[2 * i + 1];
+  if (i >= nitems) return;
   int64_t rr[kSeg];
 #pragma unroll
   for (int u = 0; u < kSeg; ++u) rr[u] = j0 + u < j1 ? (int64_t)perm[j0 + u] * N : 0;
@@ -686,7 +690,7 @@ void gather_rows(const int32_t* idx, int64_t rows, const float* table, int64_t V
 
 int64_t scatter_workspace_bytes(int64_t rows, int64_t V, int64_t N) {
   const int64_t items = (rows + kSeg - 1) / kSeg + V;
-  const int64_t ints = rows + 2 * (V + 1) + items;
+  const int64_t ints = rows + 2 * (V + 1) + 2 * items;
   return (ints * 4 + 255) / 256 * 256 + items * N * 8;
 }
 
@@ -698,17 +702,17 @@ void scatter_rows(const int32_t* idx, int64_t rows, const float* dy, int64_t V, 
   int32_t* perm = static_cast<int32_t*>(work);
   int32_t* offs = perm + rows;
   int32_t* cstart = offs + V + 1;
-  int32_t* item_v = cstart + V + 1;
-  const int64_t ints = rows + 2 * (V + 1) + items;
+  int32_t* item_rng = cstart + V + 1;
+  const int64_t ints = rows + 2 * (V + 1) + 2 * items;
   double* part = reinterpret_cast<double*>(static_cast<char*>(work) + (ints * 4 + 255) / 256 * 256);
-  const int nw = V <= kWaveHistV ? 4 : 1;
+  const int nw = V <= kWaveHistV ? kBucketWaves : 1;
   const int64_t hist_bytes = (int64_t)nw * (V + 1) * 4;
   const int stash = hist_bytes + rows * 4 <= 65536 ? 1 : 0;
   const size_t lds = (size_t)(hist_bytes + (stash ? rows * 4 : 0));
-  k_bucket_rows<<<1, 256, lds, st>>>(idx, rows, V, stash, perm, offs, cstart, item_v);
+  k_bucket_rows<<<1, kBucketWaves * 64, lds, st>>>(idx, rows, V, stash, perm, offs, cstart, item_rng);
   const int64_t ny = (N + 255) / 256;
   dim3 g2((unsigned)items, (unsigned)(ny > 64 ? 64 : ny));
-  k_segment_partials<<<g2, 256, 0, st>>>(dy, N, V, perm, offs, cstart, item_v, part);
+  k_segment_partials<<<g2, 256, 0, st>>>(dy, N, V, perm, cstart, item_rng, part);
   k_segment_finish<<<grid_for(V * N), 256, 0, st>>>(part, N, V, cstart, out);
 }
 
