@@ -62,13 +62,16 @@ struct GemmArgs {
 // fixed 32-bit per-lane offset.
 constexpr int kLdsBlock = 256;   // floats one wavefront-wide DMA writes (1 KiB)
 
-template <int ROWS, int BK, bool KFAST, int NT>
+// DW: the operand's rows need not be 16-byte aligned (a 65-wide matrix): every lane moves
+// one 4-byte element (global_load_lds_dword), four times the instructions, into the same
+// swizzled LDS layout, so fragment reads do not change.
+template <int ROWS, int BK, bool KFAST, int NT, bool DW = false>
 struct DTile {
   static constexpr int CPR = KFAST ? BK / 4 : ROWS / 4;   // 16-byte chunks per LDS row
   static constexpr int NCH = ROWS * BK / 4;               // chunks per tile
-  static constexpr int PER = NCH / NT;                    // DMA instructions per thread
+  static constexpr int PER = (DW ? ROWS * BK : NCH) / NT; // DMA instructions per thread
   static constexpr int SIZE = ROWS * BK;                  // floats
-  static_assert(NCH % NT == 0, "tile must be a whole number of DMA rounds");
+  static_assert((DW ? ROWS * BK : NCH) % NT == 0, "tile must be a whole number of DMA rounds");
   static_assert(KFAST ? (BK == 32 || BK == 64) : ROWS >= 64, "swizzle needs 8 / 16 chunks per row");
 
   __device__ __forceinline__ static int swz(int lrow) {
@@ -76,8 +79,8 @@ struct DTile {
     return ((lrow >> 2) & 1) << 3;
   }
 
-  // Per-thread byte offsets of this thread's PER chunks from the tile origin (row r0,
-  // k = k0); fixed for the whole k loop. Rows past `rlim` read the last row.
+  // Per-thread byte offsets of this thread's PER chunks (elements, DW) from the tile origin
+  // (row r0, k = k0); fixed for the whole k loop. Rows past `rlim` read the last row.
   __device__ __forceinline__ static void offsets(int64_t sr, int64_t sk, int64_t r0, int64_t rlim, int tid,
                                                  uint32_t* off) {
     const int lane = tid & 63, wave = tid >> 6;
@@ -85,6 +88,21 @@ struct DTile {
     for (int e = 0; e < PER; ++e) {
       const int inst = e * (NT / 64) + wave;
       const int P = inst * 64 + lane;
+      if (DW) {
+        // LDS float P of the tile: undo the chunk swizzle to find its (row, k)
+        if (KFAST) {
+          const int row = P / BK, rem = P % BK;
+          const int k = (((rem >> 2) ^ swz(row)) << 2) | (rem & 3);
+          const int64_t gr = min(r0 + row, rlim - 1) - r0;
+          off[e] = (uint32_t)((gr * sr + k) * 4);
+        } else {
+          const int k = P / ROWS, rem = P % ROWS;
+          const int n = (((rem >> 2) ^ swz(k)) << 2) | (rem & 3);
+          const int64_t gr = min(r0 + n, rlim - 1) - r0;
+          off[e] = (uint32_t)((k * sk + gr) * 4);
+        }
+        continue;
+      }
       const int row = P / CPR, pc = P % CPR;
       const int c = pc ^ swz(row);
       if (KFAST) {
@@ -100,17 +118,22 @@ struct DTile {
   // Issue this thread's chunks of one stage: global base `gb` (tile origin of the stage,
   // wave-uniform, in SGPRs) plus the 32-bit per-lane offsets; LDS byte address `lds` of the
   // stage's slot and the wave index `wave`, both wave-uniform, so M0 is scalar arithmetic.
-  // Each global_load_lds_dwordx4 moves lane l's 16 bytes to M0 + 16 l. It is issued from
-  // inline assembly so the compiler does not treat it as an LDS write of unknown extent:
-  // for such writes it drains every outstanding load before the next LDS read, which would
-  // expose the full load latency at every pipeline stage. The kernel orders LDS reads
-  // itself (explicit vmcnt waits and barriers). One wait state separates the M0 write from
-  // the load.
+  // Each global_load_lds_dwordx4 moves lane l's 16 bytes to M0 + 16 l (a dword load: 4
+  // bytes to M0 + 4 l). It is issued from inline assembly so the compiler does not treat it
+  // as an LDS write of unknown extent: for such writes it drains every outstanding load
+  // before the next LDS read, which would expose the full load latency at every pipeline
+  // stage. The kernel orders LDS reads itself (explicit vmcnt waits and barriers). One wait
+  // state separates the M0 write from the load.
   __device__ __forceinline__ static void dma(const float* gb, const uint32_t* off, uint32_t lds, int wave) {
 #pragma unroll
     for (int e = 0; e < PER; ++e) {
-      const uint32_t m0v = lds + (uint32_t)((e * (NT / 64) + wave) * kLdsBlock * 4);
-      asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off[e]), "s"(gb), "{m0}"(m0v));
+      if (DW) {
+        const uint32_t m0v = lds + (uint32_t)((e * (NT / 64) + wave) * 64 * 4);
+        asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(off[e]), "s"(gb), "{m0}"(m0v));
+      } else {
+        const uint32_t m0v = lds + (uint32_t)((e * (NT / 64) + wave) * kLdsBlock * 4);
+        asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off[e]), "s"(gb), "{m0}"(m0v));
+      }
     }
   }
 
@@ -147,7 +170,7 @@ __device__ __forceinline__ uint32_t xcd_order(uint32_t b, uint32_t nblk) {
 }
 
 // One output tile (tile number b of the problem g).
-template <int BM, int BN, int BK, int NS, bool AK, bool BKF, int NT, int KG, class Epi>
+template <int BM, int BN, int BK, int NS, bool AK, bool BKF, int NT, int KG, class Epi, bool BDW = false>
 __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint32_t b, const Epi& epi) {
   // per k group: 4 waves 2 x 2; 8 waves 2 x 4 (BN = 128) or 4 x 2
   constexpr int GT = NT / KG;             // threads per k group
@@ -160,7 +183,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint32_t b, const E
   constexpr int NSG = NS / KG;            // slots per k group
   constexpr int NG = BK / 8;
   using TA = DTile<BM, BK, AK, GT>;
-  using TB = DTile<BN, BK, BKF, GT>;
+  using TB = DTile<BN, BK, BKF, GT, BDW>;
   constexpr int PER = TA::PER + TB::PER;
   static_assert(PER * (NSG - 1) < 64, "too many loads in flight for vmcnt");
   __shared__ __attribute__((aligned(16))) float As[NS * TA::SIZE];   // NS stages of A

@@ -239,9 +239,9 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g) {
 
 // ---- direct-to-LDS pipeline (gemm_dev.h) ----------------------------------------------
 
-template <int BM, int BN, int BK, int NS, bool AK, bool BKF, int NT, int KG>
+template <int BM, int BN, int BK, int NS, bool AK, bool BKF, int NT, int KG, bool BDW = false>
 __global__ __launch_bounds__(NT) void k_gemm_dma(GemmArgs g) {
-  gemm_tile<BM, BN, BK, NS, AK, BKF, NT, KG>(g, xcd_order(blockIdx.x, gridDim.x), StoreC{});
+  gemm_tile<BM, BN, BK, NS, AK, BKF, NT, KG, StoreC, BDW>(g, xcd_order(blockIdx.x, gridDim.x), StoreC{});
 }
 
 // Several independent problems in one launch: problem p owns tile numbers
@@ -332,6 +332,23 @@ bool dma_ok(const GemmDesc& d, const Plan& p, bool ak, bool bk) {
   return true;
 }
 
+// The 64 x 64 direct-to-LDS kernel with a B operand whose rows are not 16-byte aligned
+// (a 65-wide product side): B moves one 4-byte element per lane (the DTile DW mode), A as
+// in dma_ok.
+bool dma_bdw_ok(const GemmDesc& d, const Plan& p, bool ak, bool bk) {
+  if (p.bm != 64 || p.bn != 64 || p.bk != 64) return false;
+  if (d.K % p.bk != 0 || p.kps % p.bk != 0) return false;
+  if (((uintptr_t)d.A & 15) != 0 || ((uintptr_t)d.B & 3) != 0) return false;
+  if ((d.batch > 1) && ((d.sAz0 | d.sAz1) & 3)) return false;
+  if (ak) { if (d.sAm & 3) return false; }
+  else if (!(d.sAm == 1 && (d.sAk & 3) == 0 && d.M % 4 == 0)) return false;
+  if (!bk && d.sBn != 1) return false;
+  const int64_t span = 128;
+  if ((ak ? d.sAm : d.sAk) * span * 4 >= (int64_t(1) << 31)) return false;
+  if ((bk ? d.sBn : d.sBk) * span * 4 >= (int64_t(1) << 31)) return false;
+  return true;
+}
+
 }  // namespace
 
 int64_t gemm_workspace_floats(const GemmDesc& d) {
@@ -369,6 +386,11 @@ void gemm(const GemmDesc& d, float* work, hipStream_t st) {
     else if (p.bk == 32) TG_DMA_LAUNCH(64, 64, 32, 4, 512, 2);
     else TG_DMA_LAUNCH(64, 64, 64, 4, 512, 2);
 #undef TG_DMA_LAUNCH
+  } else if (dma_bdw_ok(d, p, ak, bk)) {
+    if (ak && bk) k_gemm_dma<64, 64, 64, 4, true, true, 512, 2, true><<<grid, 512, 0, st>>>(g);
+    else if (ak) k_gemm_dma<64, 64, 64, 4, true, false, 512, 2, true><<<grid, 512, 0, st>>>(g);
+    else if (bk) k_gemm_dma<64, 64, 64, 4, false, true, 512, 2, true><<<grid, 512, 0, st>>>(g);
+    else k_gemm_dma<64, 64, 64, 4, false, false, 512, 2, true><<<grid, 512, 0, st>>>(g);
   } else {
 #define TG_GEMM_LAUNCH(BM_, BN_, BK_)                                                      \
   do {                                                                                     \

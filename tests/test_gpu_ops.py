@@ -491,7 +491,11 @@ def test_sum_of_products(terms, K):
 
 GEMMS = [([5, 7], [7, 3], False, False), ([2, 33, 65], [65, 17], False, False), ([129, 64], [64, 300], False, False),
          ([70, 40], [50, 40], False, True), ([40, 70], [40, 50], True, False), ([4096, 256], [4096, 256], True, False),
-         ([300, 4096], [4096, 64], False, False)]
+         ([300, 4096], [4096, 64], False, False),
+         # rows of B not 16-byte aligned (65 / 67 wide): the direct-to-LDS tile moving B one
+         # element per lane, a partial last column tile, and split-K for a long K
+         ([4096, 256], [256, 65], False, False), ([4096, 256], [4096, 65], True, False),
+         ([200, 128], [128, 67], False, False)]
 
 
 @pytest.mark.parametrize('case', GEMMS)
