@@ -2046,7 +2046,10 @@ bool Runtime::only_optimizer_reads(int t) const {
   if (consumers_[t].empty()) return false;
   for (int c : consumers_[t]) {
     if (adam_ops_.count(c)) continue;
-    if (virtual_[c] && !is_leaf(c) && kinds_[c] != "matmul" && kinds_[c] != "matmul_batched") {
+    // views of t (a product with an identity one-hot is one; products lowered by other
+    // patterns are not)
+    const bool view = (kinds_[c] != "matmul" && kinds_[c] != "matmul_batched") || root(O(c).at("out").i32()) == root(t);
+    if (virtual_[c] && !is_leaf(c) && view) {
       if (!only_optimizer_reads(O(c).at("out").i32())) return false;
       continue;
     }
