@@ -18,7 +18,7 @@ namespace {
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kQB = 64;     // keys per block (backward kernel B)
+constexpr int kQB = 32;     // keys per block (backward kernel B)
 constexpr int kQBF = 32;    // query rows per block (forward, backward kernel A)
 constexpr int kNT = 512;    // eight wavefronts: two per SIMD hide each other's latencies
 constexpr int kDH = 64;     // head size
@@ -234,24 +234,6 @@ __global__ __launch_bounds__(kNT) void k_attn_fwd(const AttnDesc a) {
   }
 }
 
-
-// Row-tile loader: rows [r0, r0 + R) of a [.., 64]-wide operand with row stride `rs`
-// (16-byte aligned rows) into LDS rows of `ld` floats, every load in flight first.
-template <int R, int LD>
-__device__ __forceinline__ void load_rows(const float* src, int64_t rs, float* dst, int tid) {
-  constexpr int C = R * kDH / 4 / kNT;
-  f32x4 v[C];
-#pragma unroll
-  for (int u = 0; u < C; ++u) {
-    const int c = u * kNT + tid, row = c / (kDH / 4), c4 = c % (kDH / 4);
-    v[u] = *reinterpret_cast<const f32x4*>(src + (int64_t)row * rs + c4 * 4);
-  }
-#pragma unroll
-  for (int u = 0; u < C; ++u) {
-    const int c = u * kNT + tid, row = c / (kDH / 4), c4 = c % (kDH / 4);
-    *reinterpret_cast<f32x4*>(dst + row * LD + c4 * 4) = v[u];
-  }
-}
 
 // One 32 x 32 tile, one 64-k stage of a product whose operands are read one column per
 // lane from LDS row-major tiles: out(m, n) = sum_k A[k][m] B[k][n] (A rows at a0 + k * lda,
@@ -470,63 +452,106 @@ __global__ __launch_bounds__(kNT) void k_attn_bwd_a(const AttnBwdDesc a) {
   }
 }
 
-// Backward, kernel B (per 64 keys): dV = Pd^T dO and dK = dS^T Q over all T query rows,
-// each as two 64-row stages added in order (the unfused GEMMs' blocking).
-template <int T>
+// Rows [0, R) of a COLS-wide slice (row stride rs, 16-byte aligned rows) into registers,
+// every load in flight at once; store_slice writes them to LDS rows of `ld` floats.
+template <int R, int COLS>
+struct Slice {
+  static constexpr int C = R * COLS / 4 / kNT;
+  static_assert(C >= 1 && R * COLS / 4 % kNT == 0, "slice is whole load rounds");
+  f32x4 v[C];
+  __device__ __forceinline__ void load(const float* src, int64_t rs, int tid) {
+#pragma unroll
+    for (int u = 0; u < C; ++u) {
+      const int c = u * kNT + tid, row = c / (COLS / 4), c4 = c % (COLS / 4);
+      v[u] = *reinterpret_cast<const f32x4*>(src + (int64_t)row * rs + c4 * 4);
+    }
+  }
+  __device__ __forceinline__ void store(float* dst, int ld, int tid) const {
+#pragma unroll
+    for (int u = 0; u < C; ++u) {
+      const int c = u * kNT + tid, row = c / (COLS / 4), c4 = c % (COLS / 4);
+      *reinterpret_cast<f32x4*>(dst + row * ld + c4 * 4) = v[u];
+    }
+  }
+};
+
+// Backward, kernel B (per KB keys): dV = Pd^T dO and dK = dS^T Q over all T query rows,
+// each as two 64-row stages added in order (the unfused GEMMs' blocking). LDS: region 1
+// holds the Pd slice, then the dS slice, region 2 dO, then Q (dS and Q wait in registers
+// while dV is formed); the stage-1 partials pass through region 1. 53 KiB: three blocks a
+// CU, the blocks of one head on one XCD.
+template <int T, int KB>
 __global__ __launch_bounds__(kNT) void k_attn_bwd_b(const AttnBwdDesc a) {
-  __shared__ __attribute__((aligned(16))) float Pc[T * kLD];   // Pd[i][j0 ..]
-  __shared__ __attribute__((aligned(16))) float Oc[T * kLD];   // dO[i][:]
-  __shared__ __attribute__((aligned(16))) float Sc[T * kLD];   // dS[i][j0 ..]
-  __shared__ __attribute__((aligned(16))) float Qc[T * kLD];   // Q[i][:]
-  __shared__ __attribute__((aligned(16))) float Xs[4 * 16 * 64];
+  constexpr int LDK = KB + 4;
+  __shared__ __attribute__((aligned(16))) float Reg1[T * LDK];   // Pd[i][j0 ..], then dS[i][j0 ..]
+  __shared__ __attribute__((aligned(16))) float Reg2[T * kLD];   // dO[i][:], then Q[i][:]
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int lrow = lane & 31, h = lane >> 5;
-  constexpr int JBn = T / 64;
-  const int bh = blockIdx.x / JBn, jb = blockIdx.x % JBn;
+  constexpr int NJB = T / KB;
+  const uint32_t L = gd::xcd_order(blockIdx.x, gridDim.x);
+  const int bh = L / NJB, jb = L % NJB;
   const int b = bh / a.H, hd = bh % a.H;
-  const int j0 = jb * 64;
+  const int j0 = jb * KB;
   const int64_t prow = (int64_t)bh * T * T;
-  load_rows<T, kLD>(a.pd + prow + j0, T, Pc, tid);
-  load_rows<T, kLD>(a.dout + b * a.sob + hd * a.soh, a.soi, Oc, tid);
-  load_rows<T, kLD>(a.ds + prow + j0, T, Sc, tid);
-  load_rows<T, kLD>(a.q + b * a.sqb + hd * a.sqh, a.sqi, Qc, tid);
+  {
+    Slice<T, KB> pd;
+    Slice<T, kDH> od;
+    pd.load(a.pd + prow + j0, T, tid);
+    od.load(a.dout + b * a.sob + hd * a.soh, a.soi, tid);
+    pd.store(Reg1, LDK, tid);
+    od.store(Reg2, kLD, tid);
+  }
+  Slice<T, KB> ds;
+  Slice<T, kDH> qq;
+  ds.load(a.ds + prow + j0, T, tid);
+  qq.load(a.q + b * a.sqb + hd * a.sqh, a.sqi, tid);
   __syncthreads();
 
   constexpr int NS = T / 64;
-  const int tile = wave & 3, s = wave >> 2;
-  const int wm = (tile >> 1) * 32, wn = (tile & 1) * 32;   // rows: keys j0 + wm, cols: d
+  constexpr int NTO = (KB / 32) * (kDH / 32);
+  static_assert(NTO * NS <= kNT / 64, "one output tile stage per wavefront");
+  const int tile = wave % NTO, s = wave / NTO;
+  const int wm = (tile / (kDH / 32)) * 32, wn = (tile % (kDH / 32)) * 32;   // rows: keys j0 + wm, cols: d
 #pragma unroll
   for (int which = 0; which < 2; ++which) {
-    const float* A = which == 0 ? Pc : Sc;
-    const float* Bm = which == 0 ? Oc : Qc;
+    if (which == 1) {
+      __syncthreads();   // dV's reads of region 1 (partials included) are done
+      ds.store(Reg1, LDK, tid);
+      qq.store(Reg2, kLD, tid);
+      __syncthreads();
+    }
     f32x16 part;
 #pragma unroll
     for (int r = 0; r < 16; ++r) part[r] = 0.0f;
-    if (s < NS) part = stage_cols(A + wm, kLD, Bm + wn, kLD, s, lrow, h);
-    if (NS == 2 && s == 1)
+    if (s < NS) part = stage_cols(Reg1 + wm, LDK, Reg2 + wn, kLD, s, lrow, h);
+    if (NS == 2) {
+      __syncthreads();   // every read of region 1 is done: it takes the stage-1 partials
+      float* Xs = Reg1;
+      static_assert(NTO * 16 * 64 <= T * LDK, "exchange fits region 1");
+      if (s == 1)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) Xs[(tile * 16 + r) * 64 + lane] = part[r];
-    __syncthreads();
+        for (int r = 0; r < 16; ++r) Xs[(tile * 16 + r) * 64 + lane] = part[r];
+      __syncthreads();
+      if (s == 0)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) part[r] = (0.0f + part[r]) + Xs[(tile * 16 + r) * 64 + lane];
+    } else if (s == 0) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) part[r] = 0.0f + part[r];
+    }
     if (s == 0) {
-      f32x16 acc;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[r] = 0.0f + part[r];
-      if (NS == 2)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[r] += Xs[(tile * 16 + r) * 64 + lane];
       if (which == 0) {
         float* o = a.dv + b * a.sdvb + hd * a.sdvh;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) o[(int64_t)(j0 + wm + (r / 4) * 8 + h * 4 + (r % 4)) * a.sdvj + wn + lrow] = acc[r];
+        for (int r = 0; r < 16; ++r) o[(int64_t)(j0 + wm + (r / 4) * 8 + h * 4 + (r % 4)) * a.sdvj + wn + lrow] = part[r];
       } else {
         float* o = a.dk + b * a.sdkb + hd * a.sdkh;
 #pragma unroll
         for (int r = 0; r < 16; ++r)
-          o[(int64_t)(j0 + wm + (r / 4) * 8 + h * 4 + (r % 4)) * a.sdkj + (int64_t)(wn + lrow) * a.sdkd] = acc[r];
+          o[(int64_t)(j0 + wm + (r / 4) * 8 + h * 4 + (r % 4)) * a.sdkj + (int64_t)(wn + lrow) * a.sdkd] = part[r];
       }
     }
-    __syncthreads();
   }
 }
 
@@ -547,10 +572,10 @@ void attention_bwd(const AttnBwdDesc& a, hipStream_t st) {
   const int blocks_a = a.B * a.H * (a.T / kQBF);
   if (a.T == 128) {
     k_attn_bwd_a<128, kQBF><<<blocks_a, kNT, 0, st>>>(a);
-    k_attn_bwd_b<128><<<blocks, kNT, 0, st>>>(a);
+    k_attn_bwd_b<128, kQB><<<blocks, kNT, 0, st>>>(a);
   } else {
     k_attn_bwd_a<64, kQBF><<<blocks_a, kNT, 0, st>>>(a);
-    k_attn_bwd_b<64><<<blocks, kNT, 0, st>>>(a);
+    k_attn_bwd_b<64, kQB><<<blocks, kNT, 0, st>>>(a);
   }
 }
 
