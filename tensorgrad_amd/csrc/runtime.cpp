@@ -2100,7 +2100,10 @@ int Runtime::epi_group(int op, int out, const tgk::GemmDesc& d) const {
         continue;
       }
       const int g = group_of_[c];
-      if (g < 0 || (gi >= 0 && g != gi)) return -1;
+      if (g < 0 || (gi >= 0 && g != gi) || dropped_[c]) return -1;
+      // a group that recomputes the reader reads the product from memory
+      for (size_t q = 0; q < groups_.size(); ++q)
+        if ((int)q != g && dup_in((int)q, c)) return -1;
       gi = g;
     }
   }

@@ -43,6 +43,19 @@ def test_plan_lowers_every_config(key):
         assert sum(1 for n in p['nodes'] if n['kind'] == 'gemm' and n['shape'].endswith('x[27,24]')) == 0
 
 
+def test_plan_with_gemm_epilogues(monkeypatch):
+    """TG_GEMM_EPI=1 (pointwise groups in GEMM epilogues) lowers every config, also where a
+    backward group recomputes from a GEMM's product (that product keeps its own store)."""
+    monkeypatch.setenv('TG_GEMM_EPI', '1')
+    fused = 0
+    for key in configs.CONFIGS:
+        cfg = configs.CONFIGS[key]
+        ir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer)
+        nodes = backend.plan(ir.wire_json())['nodes']
+        fused += sum(1 for n in nodes if n.get('ops', '').startswith('gemm+'))
+    assert fused > 0
+
+
 def test_gelu_backward_recomputes_instead_of_reading():
     """The transformer's GELU backward group evaluates the pre-activation and exp terms
     again from the FC1 GEMM output (the erf term stays stored: its f64 evaluation costs
