@@ -45,6 +45,14 @@ def measure(key, steps, warmup, profile_iters=3, kind_iters=20):
     for i in range(steps):
         loss = rt.step_staged(i % RING)
     dt = time.perf_counter() - t0
+    # PCIe-inclusive rate (never `value`): host-resident batches, each step copies its batch
+    # host -> device through pinned staging before the replay
+    host_batches = configs.batches(cfg, RING)
+    host_steps = min(steps, 50)
+    t1 = time.perf_counter()
+    for i in range(host_steps):
+        rt.step(host_batches[i % RING])
+    host_dt = time.perf_counter() - t1
     replay_ms = rt.time_replays(steps) / steps
     nodes = rt.describe()['nodes']
     ms = rt.profile_nodes(profile_iters)
@@ -74,6 +82,7 @@ def measure(key, steps, warmup, profile_iters=3, kind_iters=20):
         'samples_per_s': cfg.samples_per_step * steps / dt,
         'sample_unit': cfg.sample_unit,
         'device_replay_ms': replay_ms,
+        'host_batch_steps_per_s': host_steps / host_dt,
         'launch_nodes': len(nodes),
         'final_loss': loss,
         'gemm': {'flop_per_step': gemm_f, 'bytes_per_step': gemm_b, 'launches': gemm_n, 'ms': gemm_t,
@@ -211,6 +220,7 @@ def main():
         'cpu_baseline': None if cpu is None else {k: (round(v, 5) if isinstance(v, float) else v) for k, v in cpu.items()},
         'per_config': [{'config': r['config'], 'steps_per_s': round(r['steps_per_s'], 2),
                         'samples_per_s': round(r['samples_per_s'], 1), 'device_replay_ms': round(r['device_replay_ms'], 4),
+                        'host_batch_steps_per_s': round(r['host_batch_steps_per_s'], 2),
                         'gemm_tflops': round(r['gemm']['tflops'], 2), 'gemm_frac_f32_peak': round(r['gemm']['frac_f32_peak'], 4),
                         'conv_tflops': round(r['conv']['tflops'], 2),
                         'attention_tflops': round(r['attention']['tflops'], 2),
