@@ -159,9 +159,6 @@ struct Node {
   double flops = 0, bytes = 0;      // algorithmic work per launch
   std::string shape;
   std::string detail;  // fused groups: member op kinds in program order
-  int stream = 0;               // capture stream (see Runtime::schedule)
-  std::vector<int> waits;       // nodes on other streams this one waits for
-  bool signal = false;          // some node on another stream waits for this one
   std::function<void(hipStream_t)> launch;   // bound after allocation
   std::function<std::function<void(hipStream_t)>()> bind;
 };
@@ -353,28 +350,14 @@ class Runtime {
   void split_init_nodes();
   void launch_all(hipStream_t st);
   void upload_inputs(int n, const char* const* names, const void* const* data, const int64_t* nbytes, bool device);
-  void stage_scalars();
+  void advance_scalars(bool optimizer);
+  void upload_scalars();
  public:
   void stage_batch(int slot, int n, const char* const* names, const void* const* data, const int64_t* nbytes);
   float step_staged(int slot);
  private:
   void ensure_graph();
   void replay();
-  void schedule();
-  void prepare_streams();
-  void launch_streams();
-  // Independent launches of a step can run concurrently on up to kStreams streams inside
-  // the captured graph, each stream with its own workspace slice. Off by default (one
-  // stream): capturing the transformer step across several streams crashed inside the
-  // HIP runtime on the test machine (a one-stream capture of the same step and a
-  // several-stream capture of the small MLP ran correctly). TG_STREAMS=n selects n.
-  static constexpr int kStreams = 4;
-  int nstreams_ = 1;
-  std::vector<hipStream_t> side_;
-  std::vector<hipEvent_t> node_ev_;
-  std::vector<hipEvent_t> join_ev_;
-  hipEvent_t fork_ev_ = nullptr;
-  size_t ws_stride_ = 0;
   float* cur_ws_ = nullptr;   // workspace slice of the node being bound
   // TG_GRAPH=0 in the environment issues each step's launches directly instead of
   // replaying a captured hipGraph (for tools that do not follow graph launches).
@@ -433,7 +416,11 @@ Runtime::Runtime(const char* json, Runtime* par, bool plan_only) : parent(par) {
   if (const char* g = std::getenv("TG_REMAT")) use_remat_ = std::string(g) != "0";
   if (const char* g = std::getenv("TG_GEMM_EPI")) use_gemm_epi_ = std::string(g) == "1";
   if (const char* g = std::getenv("TG_FUSED")) use_jit_ = std::string(g) != "vm";
-  if (const char* g = std::getenv("TG_STREAMS")) nstreams_ = std::max(1, std::min(kStreams, std::atoi(g)));
+  // A several-stream schedule of the step was tried and crashed inside the HIP runtime
+  // while capturing the transformer step; it is removed, and asking for it is an error.
+  if (const char* g = std::getenv("TG_STREAMS"))
+    if (std::string(g) != "1")
+      throw Error(TG_INVALID_ARGUMENT, "TG_STREAMS: only one stream per step is supported");
   try {
     doc_ = tgj::parse(json);
   } catch (std::exception& e) {
@@ -475,10 +462,8 @@ Runtime::Runtime(const char* json, Runtime* par, bool plan_only) : parent(par) {
   if (!plan_only) hip_check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate");
   split_init_nodes();
   allocate();
-  schedule();
   bind_all();   // in plan-only mode this still runs every launch's host-side bounds proof
   jit_finish();
-  prepare_streams();
   if (!plan_only && !init_nodes_.empty()) {
     for (auto& n : init_nodes_) n.launch(stream_);
     hip_check(hipStreamSynchronize(stream_), "hipStreamSynchronize(constants)");
@@ -489,10 +474,6 @@ Runtime::~Runtime() {
   if (graph_exec_) hipGraphExecDestroy(graph_exec_);
   if (graph_) hipGraphDestroy(graph_);
   if (stream_) { hipStreamSynchronize(stream_); hipStreamDestroy(stream_); }
-  for (hipStream_t x : side_) { hipStreamSynchronize(x); hipStreamDestroy(x); }
-  for (hipEvent_t e : node_ev_) if (e) hipEventDestroy(e);
-  for (hipEvent_t e : join_ev_) hipEventDestroy(e);
-  if (fork_ev_) hipEventDestroy(fork_ev_);
   if (arena_) hipFree(arena_);
   if (input_region_) hipFree(input_region_);
   if (workspace_ && !plan_only_) hipFree(workspace_);
@@ -2975,8 +2956,7 @@ void Runtime::allocate() {
   memset(staging_, 0, input_region_bytes_);
   for (int t : input_roots) ptr_[t] = input_region_ + input_offset_[t];
   hip_check(hipHostMalloc(&loss_host_, 256, hipHostMallocDefault), "hipHostMalloc");
-  ws_stride_ = (workspace_bytes_ + 255) & ~(size_t)255;
-  if (workspace_bytes_) hip_check(hipMalloc(&workspace_, ws_stride_ * nstreams_), "hipMalloc(workspace)");
+  if (workspace_bytes_) hip_check(hipMalloc(&workspace_, (workspace_bytes_ + 255) & ~(size_t)255), "hipMalloc(workspace)");
   if (counter_slots_) {
     hip_check(hipMalloc(&counters_, counter_slots_ * sizeof(unsigned)), "hipMalloc(counters)");
     hip_check(hipMemset(counters_, 0, counter_slots_ * sizeof(unsigned)), "hipMemset(counters)");
@@ -3021,114 +3001,10 @@ void Runtime::bind_all() {
   for (auto& n : nodes_) {
     for (int r : n.reads) if (!ptr_[r]) throw Error(TG_INTERNAL, "unallocated operand in node " + n.kind);
     for (int r : n.writes) if (!ptr_[r]) throw Error(TG_INTERNAL, "unallocated output in node " + n.kind);
-    cur_ws_ = workspace_ ? reinterpret_cast<float*>(reinterpret_cast<char*>(workspace_) + ws_stride_ * n.stream)
-                         : nullptr;
+    cur_ws_ = workspace_;
     n.launch = n.bind();
   }
   cur_ws_ = nullptr;
-}
-
-// Assign launch nodes to capture streams. Two nodes conflict when one writes bytes the
-// other reads or writes (byte ranges of their storage roots, so reuse of pooled arena
-// blocks is respected); a node starts after every earlier conflicting node. Greedy list
-// scheduling in step order: each node goes to the stream on which its estimated start is
-// earliest (ties: the stream of its latest dependency), and waits through events for the
-// latest conflicting node on each other stream.
-void Runtime::schedule() {
-  const int n = (int)nodes_.size();
-  for (auto& nd : nodes_) { nd.stream = 0; nd.waits.clear(); nd.signal = false; }
-  if (nstreams_ <= 1 || !use_graph_ || plan_only_ || n == 0) return;
-  struct Range { uintptr_t lo, hi; };
-  auto range = [&](int r) {
-    uintptr_t lo = (uintptr_t)ptr_[r];
-    return Range{lo, lo + (uintptr_t)std::max<int64_t>(4, T_[r].numel * 4)};
-  };
-  std::vector<std::vector<Range>> rd(n), wr(n);
-  for (int i = 0; i < n; ++i) {
-    for (int r : nodes_[i].reads) rd[i].push_back(range(r));
-    for (int r : nodes_[i].writes) wr[i].push_back(range(r));
-  }
-  auto overlap = [](const std::vector<Range>& a, const std::vector<Range>& b) {
-    for (const Range& x : a)
-      for (const Range& y : b)
-        if (x.lo < y.hi && y.lo < x.hi) return true;
-    return false;
-  };
-  std::vector<double> fin(n, 0.0);
-  std::vector<double> ready(nstreams_, 0.0);
-  std::vector<int> last_on(nstreams_, -1);
-  for (int i = 0; i < n; ++i) {
-    // latest conflicting node per stream
-    std::vector<int> dep(nstreams_, -1);
-    double dep_fin = 0.0;
-    int latest = -1;
-    for (int j = i - 1; j >= 0; --j) {
-      const int sj = nodes_[j].stream;
-      if (dep[sj] >= j) continue;
-      if (overlap(wr[i], rd[j]) || overlap(wr[i], wr[j]) || overlap(rd[i], wr[j])) {
-        dep[sj] = std::max(dep[sj], j);
-        dep_fin = std::max(dep_fin, fin[j]);
-        latest = std::max(latest, j);
-      }
-    }
-    int best = latest >= 0 ? nodes_[latest].stream : 0;
-    double best_start = std::max(ready[best], dep_fin);
-    for (int s2 = 0; s2 < nstreams_; ++s2) {
-      const double st = std::max(ready[s2], dep_fin);
-      if (st < best_start - 1e-9) { best = s2; best_start = st; }
-    }
-    Node& nd = nodes_[i];
-    nd.stream = best;
-    for (int s2 = 0; s2 < nstreams_; ++s2)
-      if (s2 != best && dep[s2] >= 0) { nd.waits.push_back(dep[s2]); nodes_[dep[s2]].signal = true; }
-    const double cost = 3e-6 + nd.bytes / 4e12 + nd.flops / 60e12;
-    fin[i] = best_start + cost;
-    ready[best] = fin[i];
-    last_on[best] = i;
-  }
-}
-
-// Issue the step's launches on their streams with the event waits chosen by schedule():
-// fork from stream_, join back into stream_, then the copy writebacks.
-// Streams and events used by launch_streams(). Created up front, never while a capture
-// is open: stream and event creation are not capturable operations.
-void Runtime::prepare_streams() {
-  if (nstreams_ <= 1 || !use_graph_ || plan_only_ || !side_.empty()) return;
-  for (int s2 = 1; s2 < nstreams_; ++s2) {
-    hipStream_t x;
-    hip_check(hipStreamCreateWithFlags(&x, hipStreamNonBlocking), "hipStreamCreate");
-    side_.push_back(x);
-    hipEvent_t e;
-    hip_check(hipEventCreateWithFlags(&e, hipEventDisableTiming), "hipEventCreate");
-    join_ev_.push_back(e);
-  }
-  hip_check(hipEventCreateWithFlags(&fork_ev_, hipEventDisableTiming), "hipEventCreate");
-  node_ev_.assign(nodes_.size(), nullptr);
-  for (size_t i = 0; i < nodes_.size(); ++i)
-    if (nodes_[i].signal) hip_check(hipEventCreateWithFlags(&node_ev_[i], hipEventDisableTiming), "hipEventCreate");
-}
-
-void Runtime::launch_streams() {
-  if ((int)side_.size() != nstreams_ - 1 || node_ev_.size() != nodes_.size() || !fork_ev_)
-    throw Error(TG_INTERNAL, "launch_streams: streams were not prepared");
-  for (size_t i = 0; i < nodes_.size(); ++i)
-    for (int j : nodes_[i].waits)
-      if (j < 0 || j >= (int)i || !node_ev_[j]) throw Error(TG_INTERNAL, "launch_streams: bad wait");
-  auto strm = [&](int s2) { return s2 == 0 ? stream_ : side_[s2 - 1]; };
-  hip_check(hipEventRecord(fork_ev_, stream_), "hipEventRecord");
-  for (hipStream_t x : side_) hip_check(hipStreamWaitEvent(x, fork_ev_, 0), "hipStreamWaitEvent");
-  for (size_t i = 0; i < nodes_.size(); ++i) {
-    Node& nd = nodes_[i];
-    hipStream_t st = strm(nd.stream);
-    for (int j : nd.waits) hip_check(hipStreamWaitEvent(st, node_ev_[j], 0), "hipStreamWaitEvent");
-    nd.launch(st);
-    if (nd.signal) hip_check(hipEventRecord(node_ev_[i], st), "hipEventRecord");
-  }
-  for (size_t q = 0; q < side_.size(); ++q) {
-    hip_check(hipEventRecord(join_ev_[q], side_[q]), "hipEventRecord");
-    hip_check(hipStreamWaitEvent(stream_, join_ev_[q], 0), "hipStreamWaitEvent");
-  }
-  apply_copy_writebacks(stream_);
 }
 
 void Runtime::launch_all(hipStream_t st) {
@@ -3172,12 +3048,8 @@ void Runtime::ensure_graph() {
   if (graph_exec_) return;
   hip_check(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
   try {
-    if (nstreams_ > 1) {
-      launch_streams();
-    } else {
-      launch_all(stream_);
-      apply_copy_writebacks(stream_);
-    }
+    launch_all(stream_);
+    apply_copy_writebacks(stream_);
   } catch (...) {
     hipGraph_t g;
     hipStreamEndCapture(stream_, &g);
@@ -3188,9 +3060,11 @@ void Runtime::ensure_graph() {
   hip_check(hipGraphInstantiate(&graph_exec_, graph_, nullptr, nullptr, 0), "hipGraphInstantiate");
 }
 
-void Runtime::stage_scalars() {
-  // Per-step scalars (src/worker.ts:187-214), written into the tail of the input region.
-  if (opt_cfg_) {
+void Runtime::advance_scalars(bool optimizer) {
+  // Per-step scalars (src/worker.ts:187-214), written into the host mirror of the tail of
+  // the input region. The worker bumps t and the seed counter before the runtime checks
+  // the inputs (src/worker.ts:225, :249), so a rejected call still consumes both.
+  if (optimizer && opt_cfg_) {
     ++t_;
     double lr_now = resolve_lr(lr_, (double)t_);
     if (opt_kind_ == "adam") {
@@ -3212,6 +3086,9 @@ void Runtime::stage_scalars() {
     int32_t s = (int32_t)(uint32_t)prng_counter_;
     memcpy(staging_ + input_offset_[input_tid_.at("__prngSeed")], &s, 4);
   }
+}
+
+void Runtime::upload_scalars() {
   if (input_region_bytes_ > user_bytes_)
     hip_check(hipMemcpyAsync(input_region_ + user_bytes_, staging_ + user_bytes_, input_region_bytes_ - user_bytes_,
                              hipMemcpyHostToDevice, stream_), "hipMemcpyAsync(H2D scalars)");
@@ -3244,7 +3121,7 @@ void Runtime::upload_inputs(int n, const char* const* names, const void* const* 
   }
   if (!device && user_bytes_)
     hip_check(hipMemcpyAsync(input_region_, staging_, user_bytes_, hipMemcpyHostToDevice, stream_), "hipMemcpyAsync(H2D)");
-  stage_scalars();
+  upload_scalars();
 }
 
 // Device-resident batches for measurement and for callers that prefetch: slot k holds a
@@ -3272,10 +3149,11 @@ void Runtime::stage_batch(int slot, int n, const char* const* names, const void*
 
 float Runtime::step_staged(int slot) {
   if (!opt_cfg_) throw Error(TG_INVALID_ARGUMENT, "step: graph has no optimizer (use run)");
+  advance_scalars(true);
   if (slot < 0 || slot >= (int)slots_.size() || !slots_[slot]) throw Error(TG_INVALID_ARGUMENT, "step: slot not staged");
   if (user_bytes_)
     hip_check(hipMemcpyAsync(input_region_, slots_[slot], user_bytes_, hipMemcpyDeviceToDevice, stream_), "hipMemcpyAsync(D2D)");
-  stage_scalars();
+  upload_scalars();
   replay();
   hip_check(hipMemcpyAsync(loss_host_, dptr(outputs_.at(0)), 4, hipMemcpyDeviceToHost, stream_), "hipMemcpyAsync(D2H)");
   hip_check(hipStreamSynchronize(stream_), "hipStreamSynchronize");
@@ -3284,6 +3162,7 @@ float Runtime::step_staged(int slot) {
 
 float Runtime::step(int n, const char* const* names, const void* const* data, const int64_t* nbytes, bool device) {
   if (!opt_cfg_) throw Error(TG_INVALID_ARGUMENT, "step: graph has no optimizer (use run)");
+  advance_scalars(true);
   upload_inputs(n, names, data, nbytes, device);
   replay();
   int lt = outputs_.at(0);
@@ -3294,6 +3173,13 @@ float Runtime::step(int n, const char* const* names, const void* const* data, co
 
 void Runtime::run(int n, const char* const* names, const void* const* data, const int64_t* nbytes, void* out,
                   int64_t out_bytes) {
+  // `run` injects only the PRNG seed (src/worker.ts:242-250); on a training graph the
+  // optimizer's per-step scalar is then a missing input (src/runtime.ts:323-325).
+  advance_scalars(false);
+  if (opt_cfg_) {
+    const char* f = opt_kind_ == "adam" ? "lrtInputName" : "lrInputName";
+    throw Error(TG_INVALID_ARGUMENT, "tensorgrad: missing input '" + opt_cfg_->at(f).str() + "'");
+  }
   upload_inputs(n, names, data, nbytes, false);
   replay();
   int o = outputs_.at(0);

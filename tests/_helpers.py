@@ -11,6 +11,31 @@ from tensorgrad_amd.module import Mulberry32
 from tensorgrad_amd.trace import param_input, trace_fn
 
 
+def rel_err(got, want, what: str = 'value') -> float:
+    """Relative error ||got - want|| / ||want|| (L2 over all elements; plain relative error
+    for scalars). Raises on any NaN or infinity on either side, so a non-finite GPU result
+    can never pass a tolerance check by comparing false."""
+    g = np.asarray(got, np.float64).reshape(-1)
+    w = np.asarray(want, np.float64).reshape(-1)
+    if g.shape != w.shape:
+        raise AssertionError(f'{what}: {g.size} elements against {w.size}')
+    if not (np.all(np.isfinite(g)) and np.all(np.isfinite(w))):
+        raise AssertionError(f'{what}: non-finite values (got {g[~np.isfinite(g)][:4]}, want {w[~np.isfinite(w)][:4]})')
+    return float(np.linalg.norm(g - w) / max(np.linalg.norm(w), 1e-30))
+
+
+def sign_ambiguous(diff, lr: float, steps: int) -> np.ndarray:
+    """Parameter elements whose difference is that of Adam updates gone opposite ways.
+
+    Adam's first updates are lr * g / (|g| + eps), about lr * sign(g): a gradient entry
+    inside the f32 rounding noise of its GEMM can move either way by lr. Such an element
+    differs by at least lr/4 (ordinary differences are ~1e-7) and by at most 2.5 * lr *
+    steps (two opposite updates of size lr per step, plus slack); a larger difference is
+    never excused."""
+    a = np.abs(np.asarray(diff, np.float64))
+    return (a >= lr / 4) & (a <= 2.5 * lr * steps)
+
+
 def make_range(shape) -> np.ndarray:
     """The reference tests' fixture: sin(0.1 i) * 0.5 (test/grad.ts:254-259)."""
     n = int(np.prod(shape)) if len(shape) else 1

@@ -100,3 +100,25 @@ def test_malformed_ir_is_rejected_with_a_message():
 
 def test_device_count_is_callable():
     assert backend.device_count() >= 0
+
+
+def test_parity_helpers_reject_non_finite_and_bound_the_exclusion():
+    """The comparison helpers of the GPU parity tests fail on NaN / infinity instead of
+    letting a comparison with NaN read as 'within tolerance', and the sign-ambiguous
+    exclusion never covers a difference larger than two opposite updates per step."""
+    import numpy as np
+    import pytest
+    from _helpers import rel_err, sign_ambiguous
+    assert rel_err(1.0, 1.0) == 0.0
+    assert abs(rel_err([1.0, 2.0], [1.0, 2.0 + 1e-6]) - 1e-6 / np.sqrt(5)) < 1e-12
+    for bad in (float('nan'), float('inf')):
+        with pytest.raises(AssertionError, match='non-finite'):
+            rel_err(bad, 1.0)
+        with pytest.raises(AssertionError, match='non-finite'):
+            rel_err([0.5, bad], [0.5, 0.5])
+        with pytest.raises(AssertionError, match='non-finite'):
+            rel_err(1.0, bad)
+    lr, steps = 1e-3, 3
+    d = np.array([1e-7, lr / 4, 2 * lr, 2.5 * lr * steps, 2.5 * lr * steps * 1.01, 1.0])
+    assert sign_ambiguous(d, lr, steps).tolist() == [False, True, True, True, False, False]
+    assert sign_ambiguous(-d, lr, steps).tolist() == [False, True, True, True, False, False]

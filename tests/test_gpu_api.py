@@ -68,6 +68,46 @@ def test_step_input_validation_fails_not_raises():
     t.destroy()
 
 
+def test_failed_step_still_consumes_t_and_seed():
+    """The worker bumps the optimizer step and the PRNG counter before the runtime checks
+    the inputs (src/worker.ts:225), so after a rejected step the next good step runs at
+    t = 2 with seed 2 on both sides. The transformer variant uses dropout, so a seed that
+    did not advance changes the loss."""
+    cfg = configs.small_variant('transformer')
+    ir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer)
+    t = tg_compile(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer, seed=7)
+    o = pyoracle.OracleRuntime(ir.wire())
+    o.upload_params(ir.initial_params(7))
+    b = configs.batches(cfg, 1)[0]
+    bad = {k: v for k, v in b.items() if k != next(iter(b))}
+    r = t.step(bad)
+    assert r.kind == 'failed' and 'missing' in str(r.error)
+    with pytest.raises(RuntimeError, match='missing'):
+        o.step(bad)
+    _close(t.step(b).loss, o.step(b))
+    p = t.download_params()
+    for n in ir.param_names:
+        po = o.get_home(n, p[n].size)
+        assert np.linalg.norm(p[n].reshape(-1) - po) <= 1e-5 * max(np.linalg.norm(po), 1e-30), n
+    t.destroy()
+
+
+def test_run_on_a_training_graph_is_rejected():
+    """`run` injects only the PRNG seed (src/worker.ts:242-250): on a training graph the
+    optimizer's per-step scalar is a missing input, so nothing trains."""
+    from tensorgrad_amd.backend import NativeRuntime
+    cfg = configs.CONFIGS['mlp_sin']
+    ir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer)
+    rt = NativeRuntime(ir.wire_json())
+    p0 = ir.initial_params(42)
+    rt.upload_params(p0)
+    with pytest.raises(BackendError, match='missing input'):
+        rt.run(configs.batches(cfg, 1)[0], (), np.float32)
+    after = rt.download_params()
+    assert all(np.array_equal(after[k].reshape(-1), np.asarray(p0[k], np.float32).reshape(-1)) for k in p0)
+    rt.destroy()
+
+
 def test_reset_restores_initial_state():
     cfg, t = _c1()
     bs = configs.batches(cfg, 3)

@@ -13,6 +13,7 @@ import numpy as np
 import pytest
 
 import pyoracle
+from _helpers import rel_err, sign_ambiguous
 from tensorgrad_amd import backend, configs
 from tensorgrad_amd.build_ir import build_training_ir
 
@@ -40,8 +41,7 @@ def _train_both(cfg, steps, seed=42, opt=None, flip_step=None):
     exact_losses = 0
     for i, b in enumerate(configs.batches(cfg, steps)):
         lg, lo = rt.step(b), o.step(b)
-        r = abs(lg - lo) / max(abs(lo), 1e-30)
-        worst_loss = max(worst_loss, r)
+        worst_loss = max(worst_loss, rel_err(lg, lo, f'[{cfg.key}] step {i + 1} loss'))
         exact_losses += int(np.float32(lg) == np.float32(lo))
         print(f'  [{cfg.key}] step {i + 1}: gpu {lg:.9g} oracle {lo:.9g}', flush=True) if i in (0, steps - 1) else None
     pg = rt.download_params()
@@ -50,11 +50,15 @@ def _train_both(cfg, steps, seed=42, opt=None, flip_step=None):
     for n in ir.param_names:
         po = o.get_home(n, pg[n].size).astype(np.float64)
         diff = pg[n].astype(np.float64) - po
+        if not np.all(np.isfinite(diff)):
+            raise AssertionError(f'[{cfg.key}] {n}: non-finite parameters')
         if flip_step is not None:
-            amb = np.abs(diff) >= flip_step / 4
+            amb = sign_ambiguous(diff, flip_step, steps)
             flips += int(amb.sum())
+            if amb.any():
+                print(f'  [{cfg.key}] {n}: sign-ambiguous at {np.flatnonzero(amb)[:16].tolist()}', flush=True)
             diff = np.where(amb, 0.0, diff)
-        d = np.linalg.norm(diff) / max(np.linalg.norm(po), 1e-30)
+        d = rel_err(po + diff, po, f'[{cfg.key}] {n}')
         if d > worst_param:
             worst_param, worst_name, worst_max = d, n, float(np.max(np.abs(diff)))
     rt.destroy()
@@ -88,7 +92,7 @@ def _update_error(cfg, seed=42, opt=None, want_ops=None):
         start = np.asarray(p0[n], np.float64).reshape(-1)
         ug = pg[n].astype(np.float64) - start
         uo = o.get_home(n, pg[n].size).astype(np.float64) - start
-        worst = max(worst, np.linalg.norm(ug - uo) / max(np.linalg.norm(uo), 1e-30))
+        worst = max(worst, rel_err(ug, uo, f'[{cfg.key}] {n} update'))
     rt.destroy()
     print(f'  [{cfg.key}] gradient (SGD update) worst rel {worst:.2e}', flush=True)
     return worst
