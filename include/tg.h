@@ -112,6 +112,37 @@ tg_status tg_reset_optimizer(tg_runtime* rt);
  * step 1 is the next step (`setLR`, src/worker.ts:304-319, src/lr.ts:108-112). */
 tg_status tg_set_lr(tg_runtime* rt, const char* lr_json);
 
+/* ---- optimizer state and checkpoints ---------------------------------------------
+ * The reference keeps optimizer state on the GPU only and has no resume
+ * (src/worker.ts:295-302 can only zero it); these entry points add export / import
+ * and a checkpoint file. State tensors are the graph's state_input tensors
+ * (appendAdam's adam_m_<param> / adam_v_<param>, appendSGD's velocity), listed in
+ * name order. */
+int tg_state_count(tg_runtime* rt);
+const char* tg_state_name(tg_runtime* rt, int i);
+int64_t tg_state_numel(tg_runtime* rt, int i);
+/* Read the named state tensors, the optimizer step t and the PRNG seed counter. */
+tg_status tg_download_state(tg_runtime* rt, int n, const char* const* names, float* const* data, const int64_t* numel,
+                            int64_t* step_t, int64_t* prng_counter);
+/* Strict (every state tensor exactly once, like tg_upload_params); also sets t and the
+ * seed counter, so the next step runs at t + 1 with seed counter + 1. */
+tg_status tg_upload_state(tg_runtime* rt, int n, const char* const* names, const float* const* data,
+                          const int64_t* numel, int64_t step_t, int64_t prng_counter);
+/* Write every parameter and state tensor to a safetensors file (F32; __metadata__ holds
+ * the optimizer kind, t, the seed counter and the LR schedule). */
+tg_status tg_save_checkpoint(tg_runtime* rt, const char* path);
+/* Load a safetensors file written by tg_save_checkpoint, or any file holding exactly the
+ * graph's parameters (e.g. converted pretrained weights; state is then left alone).
+ * Every parameter must be present with its shape; state is all or nothing; unknown
+ * tensors are an error. Nothing is written unless the whole file checks out. */
+tg_status tg_load_checkpoint(tg_runtime* rt, const char* path);
+/* Index a safetensors container held in memory without a device: JSON
+ * {"dataStart", "tensors": [{name, dtype, shape, begin, end}], "skipped": [...],
+ *  "metadata": {...}} with the checks and messages of `loadSafetensors`
+ * (src/safetensors.ts:49-103): F32 tensors listed, integer / bool tensors skipped, other
+ * dtypes, truncated buffers and offset / shape mismatches rejected. */
+tg_status tg_safetensors_index(const void* buf, int64_t len, char* out_json, int64_t out_len);
+
 /* ---- measurement (no reference counterpart) ---------------------------------------
  * Kernel-level schedule of the lowered step, as JSON: one entry per launch node with
  * its kind, shape summary, algorithmic FLOP and byte counts. */

@@ -25,6 +25,8 @@ EXPORTED = (
     'tg_param_count', 'tg_param_name', 'tg_param_numel', 'tg_upload_params', 'tg_download_params', 'tg_step',
     'tg_step_device', 'tg_stage_batch', 'tg_step_staged', 'tg_run', 'tg_capture_count', 'tg_capture_name', 'tg_get_capture', 'tg_reset_optimizer',
     'tg_set_lr', 'tg_describe', 'tg_plan', 'tg_profile_nodes', 'tg_time_replays', 'tg_time_kinds',
+    'tg_state_count', 'tg_state_name', 'tg_state_numel', 'tg_download_state', 'tg_upload_state',
+    'tg_save_checkpoint', 'tg_load_checkpoint', 'tg_safetensors_index',
 )
 
 
@@ -87,6 +89,17 @@ def lib():
     L.tg_time_replays.argtypes = [vp, ctypes.c_int, ctypes.POINTER(ctypes.c_double)]
     L.tg_time_kinds.argtypes = [vp, ctypes.c_char_p, ctypes.c_int, ctypes.POINTER(ctypes.c_double),
                                 ctypes.POINTER(ctypes.c_int)]
+    L.tg_state_count.argtypes = [vp]
+    L.tg_state_name.argtypes = [vp, ctypes.c_int]
+    L.tg_state_name.restype = ctypes.c_char_p
+    L.tg_state_numel.argtypes = [vp, ctypes.c_int]
+    L.tg_state_numel.restype = ctypes.c_int64
+    L.tg_download_state.argtypes = [vp, ctypes.c_int, c_char_pp, ctypes.POINTER(vp), i64p, i64p, i64p]
+    L.tg_upload_state.argtypes = [vp, ctypes.c_int, c_char_pp, ctypes.POINTER(vp), i64p, ctypes.c_int64,
+                                  ctypes.c_int64]
+    L.tg_save_checkpoint.argtypes = [vp, ctypes.c_char_p]
+    L.tg_load_checkpoint.argtypes = [vp, ctypes.c_char_p]
+    L.tg_safetensors_index.argtypes = [ctypes.c_char_p, ctypes.c_int64, ctypes.c_char_p, ctypes.c_int64]
     _lib = L
     return L
 
@@ -109,6 +122,14 @@ def plan(ir_json: str) -> dict:
     buf = ctypes.create_string_buffer(1 << 24)
     _check(lib().tg_plan(ir_json.encode(), buf, len(buf)))
     return json.loads(buf.value.decode())
+
+
+def safetensors_index(buf: bytes) -> dict:
+    """Index a safetensors container on the host (tg_safetensors_index)."""
+    hlen = int.from_bytes(buf[:8], 'little') if len(buf) >= 8 else 0
+    out = ctypes.create_string_buffer(4096 + 8 * min(hlen, len(buf)))
+    _check(lib().tg_safetensors_index(buf, len(buf), out, len(out)))
+    return json.loads(out.value.decode())
 
 
 def _names(names: Sequence[str]):
@@ -197,6 +218,34 @@ class NativeRuntime:
         out = np.empty(out_shape, out_dtype)
         _check(lib().tg_run(self._h, n, names, ptrs, sizes, out.ctypes.data, out.nbytes))
         return out
+
+    def state_names(self) -> List[str]:
+        L = lib()
+        return [L.tg_state_name(self._h, i).decode() for i in range(L.tg_state_count(self._h))]
+
+    def download_state(self):
+        """({state name: values}, optimizer step t, PRNG seed counter)."""
+        L = lib()
+        names = self.state_names()
+        arrs = [np.empty(L.tg_state_numel(self._h, i), np.float32) for i in range(len(names))]
+        ptrs = (ctypes.c_void_p * len(names))(*[a.ctypes.data for a in arrs])
+        sizes = (ctypes.c_int64 * len(names))(*[a.size for a in arrs])
+        t, c = ctypes.c_int64(), ctypes.c_int64()
+        _check(L.tg_download_state(self._h, len(names), _names(names), ptrs, sizes, ctypes.byref(t), ctypes.byref(c)))
+        return dict(zip(names, arrs)), t.value, c.value
+
+    def upload_state(self, state: Dict[str, np.ndarray], t: int, prng_counter: int) -> None:
+        names = list(state.keys())
+        arrs = [np.ascontiguousarray(state[n], dtype=np.float32).reshape(-1) for n in names]
+        ptrs = (ctypes.c_void_p * len(names))(*[a.ctypes.data for a in arrs])
+        sizes = (ctypes.c_int64 * len(names))(*[a.size for a in arrs])
+        _check(lib().tg_upload_state(self._h, len(names), _names(names), ptrs, sizes, t, prng_counter))
+
+    def save_checkpoint(self, path: str) -> None:
+        _check(lib().tg_save_checkpoint(self._h, os.fsencode(path)))
+
+    def load_checkpoint(self, path: str) -> None:
+        _check(lib().tg_load_checkpoint(self._h, os.fsencode(path)))
 
     def capture(self, name: str, shape, dtype) -> np.ndarray:
         out = np.empty(shape, dtype)

@@ -105,36 +105,9 @@ class CompiledForward:
     def param_names(self):
         return self.parent.param_names
 
-    def _resolve(self, inputs: Dict[str, np.ndarray]) -> Dict:
-        agreed, out = None, {}
-        for name, (shape, dtype) in self.decls.items():
-            nulls = [i for i, d in enumerate(shape) if d is None]
-            if not nulls:
-                out[name] = {'shape': list(shape), 'dtype': dtype}
-                continue
-            if len(nulls) > 1:
-                raise ValueError(f"run: input '{name}' has {len(nulls)} parametric dims; only one is supported.")
-            if name not in inputs:
-                raise ValueError(f"run: missing input '{name}'")
-            concrete = 1
-            for d in shape:
-                if d is not None:
-                    concrete *= d
-            n = np.asarray(inputs[name]).size
-            if n % concrete != 0:
-                raise ValueError(f"run: input '{name}' length {n} is not divisible by {concrete}")
-            dim = n // concrete
-            if agreed is not None and dim != agreed:
-                raise ValueError('run: parametric dim resolved inconsistently across inputs')
-            agreed = dim
-            s = list(shape)
-            s[nulls[0]] = dim
-            out[name] = {'shape': s, 'dtype': dtype}
-        return out
-
     def _sibling(self, inputs):
-        resolved = self._resolve(inputs)
-        key = '|'.join(f"{n}:{'x'.join(map(str, resolved[n]['shape']))}:{resolved[n]['dtype']}" for n in sorted(resolved))
+        resolved = _resolve_decls(self.decls, inputs)
+        key = _shape_key(resolved)
         if key in self._cache:
             self._cache.move_to_end(key)
             return self._cache[key]
@@ -227,6 +200,24 @@ class CompiledTraining:
     def set_lr(self, lr) -> None:
         self._rt.set_lr(lr)
 
+    # ---- checkpoints (no reference counterpart: the reference cannot resume) ----------
+
+    def download_optimizer_state(self):
+        """({state tensor name: flat values}, optimizer step t, PRNG seed counter)."""
+        return self._rt.download_state()
+
+    def upload_optimizer_state(self, state: Dict[str, np.ndarray], t: int, prng_counter: int) -> None:
+        self._rt.upload_state(state, t, prng_counter)
+
+    def save_checkpoint(self, path: str) -> None:
+        """Params, optimizer state, t, seed counter and LR schedule to a safetensors file."""
+        self._rt.save_checkpoint(path)
+
+    def load_checkpoint(self, path: str) -> None:
+        """Restore a checkpoint written by `save_checkpoint` (or load a params-only file);
+        training then continues exactly as it would have from the saved step."""
+        self._rt.load_checkpoint(path)
+
     def attach(self, forward: Callable, inputs: Dict, output: str = 'f32', max_cached_shapes: int = 8) -> CompiledForward:
         child = CompiledForward(self, forward, inputs, output, max_cached_shapes)
         self._children.add(child)
@@ -250,6 +241,157 @@ class CompiledTraining:
             c._invalidate()
         self._children.clear()
         self._rt.destroy()
+
+
+class CompiledForwardExecutor:
+    """Standalone forward-only executor (`compileForward`, compile.ts:424-452; proxy
+    compile.ts:895-1018). It owns its parameters: the owner graph is a runtime created
+    with no optimizer, compiled eagerly when every input dim is concrete, else at the
+    first `run`; other resolved shapes are siblings sharing the owner's parameters,
+    cached LRU. `upload_params` before the owner exists is buffered (merged, later keys
+    win) and applied, strictly, when it is created."""
+
+    def __init__(self, model: Module, forward: Callable, inputs: Dict, output: str = 'f32',
+                 max_cached_shapes: int = 8, seed: Optional[int] = None):
+        self.model = model
+        self.forward = forward
+        self.decls = {k: normalize_decl(v) for k, v in inputs.items()}
+        self.output = output
+        self.max_cached = max_cached_shapes
+        self.seed = seed if seed is not None else random.getrandbits(32)
+        self._owner = None            # (runtime, ir, shape, dtype, capture meta)
+        self._owner_key = None
+        self._cache: 'OrderedDict[str, tuple]' = OrderedDict()
+        self._pending: Optional[Dict[str, np.ndarray]] = None
+        self._destroyed = False
+        # metadata trace: parametric dims as 1 (param shapes do not depend on them)
+        meta = {k: {'shape': [1 if d is None else d for d in s], 'dtype': dt} for k, (s, dt) in self.decls.items()}
+        ir = build_forward_ir(self.model, self.forward, meta)
+        self._param_names = ir.param_names
+        if all(d is not None for s, _ in self.decls.values() for d in s):
+            self._create_owner(meta, ir)
+
+    @property
+    def param_names(self):
+        return list(self._param_names)
+
+    def _entry(self, rt, ir):
+        out_t = ir.graph.tensors[ir.graph.outputs[0]]
+        if out_t.dtype != self.output:
+            rt.destroy()
+            raise ValueError(f"compileForward: forward declares output: '{self.output}' but the traced graph's "
+                             f"output tensor is '{out_t.dtype}'.")
+        return (rt, ir, out_t.shape, _DT[out_t.dtype], _capture_meta(ir))
+
+    def _create_owner(self, resolved, ir=None):
+        ir = ir or build_forward_ir(self.model, self.forward, resolved)
+        rt = NativeRuntime(ir.wire_json())
+        rt.upload_params(ir.initial_params(self.seed))
+        self._owner = self._entry(rt, ir)
+        self._owner_key = _shape_key(resolved)
+        self._param_names = list(rt.param_names)
+        if self._pending is not None:
+            pending, self._pending = self._pending, None
+            rt.upload_params(pending)
+        return self._owner
+
+    def _sibling(self, inputs):
+        resolved = _resolve_decls(self.decls, inputs)
+        key = _shape_key(resolved)
+        if self._owner is None:
+            return self._create_owner(resolved)
+        if key == self._owner_key:
+            return self._owner
+        if key in self._cache:
+            self._cache.move_to_end(key)
+            return self._cache[key]
+        ir = build_forward_ir(self.model, self.forward, resolved)
+        entry = self._entry(NativeRuntime(ir.wire_json(), parent=self._owner[0]), ir)
+        self._cache[key] = entry
+        while len(self._cache) > self.max_cached:
+            _, old = self._cache.popitem(last=False)
+            old[0].destroy()
+        return entry
+
+    def run(self, inputs: Dict[str, np.ndarray]) -> RunResult:
+        def body():
+            if self._destroyed:
+                raise AbortError('run aborted: executor destroyed')
+            rt, ir, shape, dt, meta = self._sibling(inputs)
+            out = rt.run(inputs, shape, dt)
+            return RunResult('completed', output=out, captures=_read_captures(rt, meta))
+        return _guarded(body, RunResult)
+
+    def graph_for(self, inputs) -> TrainingIR:
+        return self._sibling(inputs)[1]
+
+    def upload_params(self, params: Dict[str, np.ndarray]) -> None:
+        if self._owner is None:
+            self._pending = dict(self._pending or {}, **params)
+            return
+        self._owner[0].upload_params(params)
+
+    def download_params(self) -> Dict[str, np.ndarray]:
+        if self._owner is None:
+            raise RuntimeError('compileForward: downloadParams() before any params exist on the GPU. With a '
+                               'parametric (null-wildcard) input shape the param buffers are allocated on the first '
+                               'run(); call run() once (or declare fully concrete input shapes) before downloadParams().')
+        return self._owner[0].download_params()
+
+    def load_checkpoint(self, path: str) -> None:
+        """Load parameters from a safetensors file holding exactly this model's params."""
+        if self._owner is None:
+            from .safetensors import load_safetensors
+            with open(path, 'rb') as f:
+                self.upload_params(load_safetensors(f.read()).tensors)
+            return
+        self._owner[0].load_checkpoint(path)
+
+    def destroy(self) -> None:
+        self._destroyed = True
+        self._cache.clear()          # siblings go with the owner (destroy cascades)
+        if self._owner is not None:
+            self._owner[0].destroy()
+
+
+def _resolve_decls(decls, inputs: Dict[str, np.ndarray]) -> Dict:
+    """Resolve one `None` wildcard per input from the given arrays' lengths; every input
+    must agree on the resolved value (compile.ts:1106-1163)."""
+    agreed, out = None, {}
+    for name, (shape, dtype) in decls.items():
+        nulls = [i for i, d in enumerate(shape) if d is None]
+        if not nulls:
+            out[name] = {'shape': list(shape), 'dtype': dtype}
+            continue
+        if len(nulls) > 1:
+            raise ValueError(f"run: input '{name}' has {len(nulls)} parametric dims; only one is supported.")
+        if name not in inputs:
+            raise ValueError(f"run: missing input '{name}'")
+        concrete = 1
+        for d in shape:
+            if d is not None:
+                concrete *= d
+        n = np.asarray(inputs[name]).size
+        if n % concrete != 0:
+            raise ValueError(f"run: input '{name}' length {n} is not divisible by {concrete}")
+        dim = n // concrete
+        if agreed is not None and dim != agreed:
+            raise ValueError('run: parametric dim resolved inconsistently across inputs')
+        agreed = dim
+        s = list(shape)
+        s[nulls[0]] = dim
+        out[name] = {'shape': s, 'dtype': dtype}
+    return out
+
+
+def _shape_key(resolved: Dict) -> str:
+    return '|'.join(f"{n}:{'x'.join(map(str, resolved[n]['shape']))}:{resolved[n]['dtype']}" for n in sorted(resolved))
+
+
+def compile_forward(model: Module, forward: Callable, inputs: Dict, output: str = 'f32',
+                    max_cached_shapes: int = 8, seed: Optional[int] = None) -> CompiledForwardExecutor:
+    """`compileForward` (compile.ts:424-452): a forward-only graph with its own params."""
+    return CompiledForwardExecutor(model, forward, inputs, output, max_cached_shapes, seed)
 
 
 def compile(model: Module, loss: Callable, inputs: Dict, optimizer: dict, seed: Optional[int] = None) -> CompiledTraining:

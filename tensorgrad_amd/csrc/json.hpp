@@ -1,6 +1,7 @@
 // Small JSON DOM for the runtime's IR document. Numbers go through strtod (correctly
 // rounded), so the f64 scalars baked into IR ops arrive exactly as serialised.
 #pragma once
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <stdexcept>
@@ -130,5 +131,40 @@ class Reader {
 };
 
 inline Value parse(const char* s) { return Reader(s).document(); }
+
+// Serialise a document (numbers with 17 significant digits, so they read back exactly).
+inline void dump_to(const Value& v, std::string& o) {
+  switch (v.kind) {
+    case Value::Null: o += "null"; return;
+    case Value::Bool: o += v.boolean ? "true" : "false"; return;
+    case Value::Number: { char b[32]; snprintf(b, sizeof b, "%.17g", v.number); o += b; return; }
+    case Value::String:
+      o += '"';
+      for (char c : v.string) {
+        if (c == '"' || c == '\\') { o += '\\'; o += c; }
+        else if ((unsigned char)c < 0x20) { char b[8]; snprintf(b, sizeof b, "\\u%04x", c); o += b; }
+        else o += c;
+      }
+      o += '"';
+      return;
+    case Value::Array:
+      o += '[';
+      for (size_t i = 0; i < v.items.size(); ++i) { if (i) o += ','; dump_to(v.items[i], o); }
+      o += ']';
+      return;
+    case Value::Object:
+      o += '{';
+      for (size_t i = 0; i < v.members.size(); ++i) {
+        if (i) o += ',';
+        Value k; k.kind = Value::String; k.string = v.members[i].first;
+        dump_to(k, o);
+        o += ':';
+        dump_to(v.members[i].second, o);
+      }
+      o += '}';
+      return;
+  }
+}
+inline std::string dump(const Value& v) { std::string o; dump_to(v, o); return o; }
 
 }  // namespace tgj

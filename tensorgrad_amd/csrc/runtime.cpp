@@ -42,6 +42,7 @@
 #include "json.hpp"
 #include "jit.h"
 #include "kernels.h"
+#include "safetensors.hpp"
 
 namespace tg {
 
@@ -182,6 +183,18 @@ class Runtime {
   void get_capture(const std::string& name, void* out, int64_t nbytes);
   void reset_optimizer();
   void set_lr(const char* json);
+
+  // Optimizer state (state_input tensors: Adam m / v, SGD velocity) in name order, plus
+  // the step counter t and the PRNG seed counter, for checkpoints.
+  const std::vector<std::string>& state_names();
+  int64_t state_numel(const std::string& name) const;
+  void download_state(int n, const char* const* names, float* const* data, const int64_t* numel);
+  void upload_state(int n, const char* const* names, const float* const* data, const int64_t* numel);
+  long long step_count() const { return t_; }
+  long long prng_count() const { return prng_counter_; }
+  void set_counters(long long t, long long prng) { t_ = t; prng_counter_ = prng; }
+  void save_checkpoint(const std::string& path);
+  void load_checkpoint(const std::string& path);
   std::string describe();
   void profile_nodes(int iters, double* ms, int64_t n);
   double time_replays(int steps);
@@ -202,6 +215,7 @@ class Runtime {
   std::vector<bool> virtual_;        // op not executed (view / folded pattern)
   std::vector<bool> materialize_;    // permute output that needs its own storage
   std::map<std::string, int> input_tid_, state_tid_;
+  std::vector<std::string> state_list_;   // state_tid_'s names, for the C ABI
   std::vector<int> outputs_;
   std::map<std::string, int> captures_;
   std::vector<std::pair<int, std::string>> copy_writebacks_;  // (source tid, dest name) applied by copy
@@ -3324,6 +3338,144 @@ double Runtime::time_replays(int steps) {
   return ms;
 }
 
+const std::vector<std::string>& Runtime::state_names() {
+  if (state_list_.size() != state_tid_.size()) {
+    state_list_.clear();
+    for (auto& kv : state_tid_) state_list_.push_back(kv.first);
+  }
+  return state_list_;
+}
+
+int64_t Runtime::state_numel(const std::string& name) const {
+  auto it = state_tid_.find(name);
+  if (it == state_tid_.end()) throw Error(TG_INVALID_ARGUMENT, "optimizer state: unknown tensor '" + name + "'");
+  return T_[it->second].numel;
+}
+
+void Runtime::download_state(int n, const char* const* names, float* const* data, const int64_t* numel) {
+  hip_check(hipStreamSynchronize(stream_), "hipStreamSynchronize");
+  for (int i = 0; i < n; ++i) {
+    if (numel[i] != state_numel(names[i])) throw Error(TG_INVALID_ARGUMENT, std::string("optimizer state: '") + names[i] + "' has the wrong size");
+    hip_check(hipMemcpy(data[i], ptr_[state_tid_.at(names[i])], (size_t)numel[i] * 4, hipMemcpyDeviceToHost), "hipMemcpy(D2H)");
+  }
+}
+
+void Runtime::upload_state(int n, const char* const* names, const float* const* data, const int64_t* numel) {
+  // Strict like uploadParams (src/runtime.ts:403-429): every state tensor exactly once.
+  std::set<std::string> seen;
+  for (int i = 0; i < n; ++i) {
+    if (numel[i] != state_numel(names[i]))
+      throw Error(TG_INVALID_ARGUMENT, std::string("optimizer state: '") + names[i] + "' expected " +
+                                           std::to_string(state_numel(names[i])) + " elements, got " + std::to_string(numel[i]));
+    if (!seen.insert(names[i]).second) throw Error(TG_INVALID_ARGUMENT, std::string("optimizer state: '") + names[i] + "' given twice");
+  }
+  for (auto& kv : state_tid_)
+    if (!seen.count(kv.first)) throw Error(TG_INVALID_ARGUMENT, "optimizer state: missing tensor '" + kv.first + "'");
+  hip_check(hipStreamSynchronize(stream_), "hipStreamSynchronize");
+  for (int i = 0; i < n; ++i)
+    hip_check(hipMemcpy(ptr_[state_tid_.at(names[i])], data[i], (size_t)numel[i] * 4, hipMemcpyHostToDevice), "hipMemcpy(H2D)");
+}
+
+// Checkpoint file: a safetensors container holding every parameter (F32, its shape),
+// every optimizer state tensor (F32, or I32 for i32 state) and, in __metadata__, the
+// optimizer kind, its step counter t and the PRNG seed counter, so that training
+// resumed from it replays the same per-step scalars and dropout masks.
+void Runtime::save_checkpoint(const std::string& path) {
+  if (parent) throw Error(TG_INVALID_ARGUMENT, "checkpoint: a forward sibling shares its parent's params; save the parent");
+  hip_check(hipStreamSynchronize(stream_), "hipStreamSynchronize");
+  std::vector<tgst::OutTensor> ts;
+  std::vector<int> tids;
+  auto add = [&](const std::string& name, int t) {
+    tgst::OutTensor o;
+    o.name = name;
+    o.dtype = T_[t].dt == F32 ? "F32" : "I32";
+    o.shape = T_[t].shape;
+    o.bytes = T_[t].numel * 4;
+    ts.push_back(o);
+    tids.push_back(t);
+  };
+  for (auto& nm : param_names) add(nm, param_root.at(nm));
+  for (auto& kv : state_tid_) add(kv.first, kv.second);
+  std::vector<std::pair<std::string, std::string>> meta = {
+      {"format", "tensorgrad"}, {"tensorgrad.optimizer", opt_cfg_ ? opt_kind_ : std::string("none")},
+      {"tensorgrad.step", std::to_string(t_)}, {"tensorgrad.prngCounter", std::to_string(prng_counter_)}};
+  if (opt_cfg_) meta.emplace_back("tensorgrad.lr", tgj::dump(lr_));
+  const std::string head = tgst::header(ts, meta);
+  FILE* f = fopen(path.c_str(), "wb");
+  if (!f) throw Error(TG_INVALID_ARGUMENT, "checkpoint: cannot open '" + path + "' for writing");
+  bool ok = fwrite(head.data(), 1, head.size(), f) == head.size();
+  std::vector<char> host;
+  for (size_t i = 0; ok && i < ts.size(); ++i) {
+    host.resize((size_t)ts[i].bytes);
+    if (ts[i].bytes) {
+      hipError_t e = hipMemcpy(host.data(), ptr_[tids[i]], (size_t)ts[i].bytes, hipMemcpyDeviceToHost);
+      if (e != hipSuccess) { fclose(f); hip_check(e, "hipMemcpy(D2H checkpoint)"); }
+    }
+    ok = fwrite(host.data(), 1, host.size(), f) == host.size();
+  }
+  ok = (fclose(f) == 0) && ok;
+  if (!ok) throw Error(TG_INVALID_ARGUMENT, "checkpoint: writing '" + path + "' failed");
+}
+
+void Runtime::load_checkpoint(const std::string& path) {
+  if (parent) throw Error(TG_INVALID_ARGUMENT, "checkpoint: a forward sibling shares its parent's params; load into the parent");
+  FILE* f = fopen(path.c_str(), "rb");
+  if (!f) throw Error(TG_INVALID_ARGUMENT, "checkpoint: cannot open '" + path + "'");
+  std::vector<uint8_t> buf;
+  uint8_t chunk[1 << 16];
+  size_t got;
+  while ((got = fread(chunk, 1, sizeof chunk, f)) > 0) buf.insert(buf.end(), chunk, chunk + got);
+  fclose(f);
+  tgst::Index ix;
+  try {
+    ix = tgst::parse(buf.data(), buf.size(), true);
+  } catch (std::exception& e) {
+    throw Error(TG_INVALID_ARGUMENT, e.what());
+  }
+  // Validate everything before writing anything.
+  auto check = [&](const tgst::Entry& e, int t) {
+    if (e.shape != T_[t].shape || e.dtype != (T_[t].dt == F32 ? "F32" : "I32"))
+      throw Error(TG_INVALID_ARGUMENT, "checkpoint: tensor '" + e.name + "' does not match the graph's shape or dtype");
+  };
+  std::vector<std::pair<const tgst::Entry*, int>> writes;
+  size_t n_state = 0;
+  for (const tgst::Entry& e : ix.tensors) {
+    auto p = param_root.find(e.name);
+    auto s = state_tid_.find(e.name);
+    if (p != param_root.end()) { check(e, p->second); writes.emplace_back(&e, p->second); }
+    else if (s != state_tid_.end()) { check(e, s->second); writes.emplace_back(&e, s->second); ++n_state; }
+    else throw Error(TG_INVALID_ARGUMENT, "checkpoint: unknown tensor '" + e.name + "'");
+  }
+  for (auto& nm : param_names)
+    if (!ix.find(nm)) throw Error(TG_INVALID_ARGUMENT, "checkpoint: missing param '" + nm + "'");
+  if (n_state && n_state != state_tid_.size())
+    throw Error(TG_INVALID_ARGUMENT, "checkpoint: holds part of the optimizer state (" + std::to_string(n_state) + " of " +
+                                         std::to_string(state_tid_.size()) + " tensors)");
+  long long t = t_, c = prng_counter_;
+  if (n_state) {
+    const std::string* k = ix.meta("tensorgrad.optimizer");
+    const std::string mine = opt_cfg_ ? opt_kind_ : std::string("none");
+    if (k && *k != mine) throw Error(TG_INVALID_ARGUMENT, "checkpoint: optimizer '" + *k + "' does not match the graph's '" + mine + "'");
+    const std::string* ts = ix.meta("tensorgrad.step");
+    if (!ts) throw Error(TG_INVALID_ARGUMENT, "checkpoint: optimizer state without a step counter");
+    t = std::stoll(*ts);
+  }
+  if (const std::string* cs = ix.meta("tensorgrad.prngCounter")) c = std::stoll(*cs);
+  tgj::Value lr = lr_;
+  if (const std::string* ls = ix.meta("tensorgrad.lr"))
+    if (n_state && opt_cfg_) {
+      try { lr = tgj::parse(ls->c_str()); } catch (std::exception& e) { throw Error(TG_INVALID_ARGUMENT, std::string("checkpoint: lr: ") + e.what()); }
+    }
+  hip_check(hipStreamSynchronize(stream_), "hipStreamSynchronize");
+  for (auto& w : writes)
+    if (w.first->end > w.first->begin)
+      hip_check(hipMemcpy(ptr_[w.second], buf.data() + ix.data_start + w.first->begin, (size_t)(w.first->end - w.first->begin),
+                          hipMemcpyHostToDevice), "hipMemcpy(H2D checkpoint)");
+  t_ = t;
+  prng_counter_ = c;
+  lr_ = lr;
+}
+
 }  // namespace tg
 
 // ---- C ABI -------------------------------------------------------------------------------
@@ -3497,6 +3649,75 @@ tg_status tg_reset_optimizer(tg_runtime* h) {
 tg_status tg_set_lr(tg_runtime* h, const char* lr_json) {
   TG_ENTER(h);
   return guarded([&] { h->rt->set_lr(lr_json); });
+}
+
+int tg_state_count(tg_runtime* h) { return h && h->rt ? (int)h->rt->state_names().size() : 0; }
+const char* tg_state_name(tg_runtime* h, int i) {
+  if (!h || !h->rt || i < 0 || i >= (int)h->rt->state_names().size()) return nullptr;
+  return h->rt->state_names()[i].c_str();
+}
+int64_t tg_state_numel(tg_runtime* h, int i) {
+  if (!h || !h->rt || i < 0 || i >= (int)h->rt->state_names().size()) return -1;
+  return h->rt->state_numel(h->rt->state_names()[i]);
+}
+
+tg_status tg_download_state(tg_runtime* h, int n, const char* const* names, float* const* data, const int64_t* numel,
+                            int64_t* step_t, int64_t* prng_counter) {
+  TG_ENTER(h);
+  return guarded([&] {
+    h->rt->download_state(n, names, data, numel);
+    if (step_t) *step_t = h->rt->step_count();
+    if (prng_counter) *prng_counter = h->rt->prng_count();
+  });
+}
+
+tg_status tg_upload_state(tg_runtime* h, int n, const char* const* names, const float* const* data, const int64_t* numel,
+                          int64_t step_t, int64_t prng_counter) {
+  TG_ENTER(h);
+  return guarded([&] {
+    if (step_t < 0 || prng_counter < 0) throw tg::Error(TG_INVALID_ARGUMENT, "optimizer state: counters must be >= 0");
+    h->rt->upload_state(n, names, data, numel);
+    h->rt->set_counters(step_t, prng_counter);
+  });
+}
+
+tg_status tg_save_checkpoint(tg_runtime* h, const char* path) {
+  if (!path) { tg::g_error = "null argument"; return TG_INVALID_ARGUMENT; }
+  TG_ENTER(h);
+  return guarded([&] { h->rt->save_checkpoint(path); });
+}
+
+tg_status tg_load_checkpoint(tg_runtime* h, const char* path) {
+  if (!path) { tg::g_error = "null argument"; return TG_INVALID_ARGUMENT; }
+  TG_ENTER(h);
+  return guarded([&] { h->rt->load_checkpoint(path); });
+}
+
+tg_status tg_safetensors_index(const void* buf, int64_t len, char* out, int64_t out_len) {
+  if (!buf || !out || len < 0) { tg::g_error = "null argument"; return TG_INVALID_ARGUMENT; }
+  return guarded([&] {
+    tgst::Index ix;
+    try {
+      ix = tgst::parse(static_cast<const uint8_t*>(buf), (uint64_t)len);
+    } catch (std::exception& e) {
+      throw tg::Error(TG_INVALID_ARGUMENT, e.what());
+    }
+    std::string o = "{\"dataStart\":" + std::to_string(ix.data_start) + ",\"tensors\":[";
+    auto entry = [&](const tgst::Entry& e) {
+      std::string s = "{\"name\":" + tgst::quote(e.name) + ",\"dtype\":" + tgst::quote(e.dtype) + ",\"shape\":[";
+      for (size_t i = 0; i < e.shape.size(); ++i) s += (i ? "," : "") + std::to_string(e.shape[i]);
+      return s + "],\"begin\":" + std::to_string(e.begin) + ",\"end\":" + std::to_string(e.end) + "}";
+    };
+    for (size_t i = 0; i < ix.tensors.size(); ++i) o += (i ? "," : "") + entry(ix.tensors[i]);
+    o += "],\"skipped\":[";
+    for (size_t i = 0; i < ix.skipped.size(); ++i) o += (i ? "," : "") + entry(ix.skipped[i]);
+    o += "],\"metadata\":{";
+    for (size_t i = 0; i < ix.metadata.size(); ++i)
+      o += (i ? "," : "") + tgst::quote(ix.metadata[i].first) + ":" + tgst::quote(ix.metadata[i].second);
+    o += "}}";
+    if ((int64_t)o.size() + 1 > out_len) throw tg::Error(TG_INVALID_ARGUMENT, "safetensors index: output buffer too small");
+    memcpy(out, o.c_str(), o.size() + 1);
+  });
 }
 
 tg_status tg_plan(const char* ir_json, char* buf, int64_t buflen) {

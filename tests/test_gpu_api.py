@@ -183,3 +183,115 @@ def test_captures_and_replace_model():
         t.replace_model(Cap(), optimizer={'kind': 'sgd', 'lr': 0.1})
     t.destroy()
     assert t.step({'x': x, 'y': x}).kind == 'aborted'
+
+
+def _predict(m, inp):
+    return m.l3.fwd(O.relu(m.l2.fwd(O.relu(m.l1.fwd(inp['x'])))))
+
+
+def _oracle_forward(ir, params, inputs):
+    from tensorgrad_amd import ir as IR
+    o = pyoracle.OracleRuntime({'graph': IR.graph_to_wire(ir.graph), 'paramGrads': {}, 'writebacks': [],
+                                'optimizer': None})
+    o.upload_params(params)
+    o.run(inputs)
+    return o.output()
+
+
+def test_compile_forward_owns_its_params():
+    """compileForward (compile.ts:424-452, :895-1018): concrete shapes create the owner
+    eagerly with params from mulberry32(seed); run matches the oracle."""
+    from tensorgrad_amd.build_ir import build_forward_ir
+    from tensorgrad_amd.compile import compile_forward
+    f = compile_forward(configs.SinMLP(), _predict, {'x': [10, 1]}, seed=5)
+    assert f.param_names == ['l1.W', 'l1.b', 'l2.W', 'l2.b', 'l3.W', 'l3.b']
+    ir = build_forward_ir(configs.SinMLP(), _predict, {'x': [10, 1]})
+    p0 = ir.initial_params(5)
+    got = f.download_params()
+    assert all(np.array_equal(got[k], np.asarray(p0[k], np.float32).reshape(-1)) for k in p0)
+    x = np.linspace(-3, 3, 10, dtype=np.float32).reshape(10, 1)
+    r = f.run({'x': x})
+    assert r.kind == 'completed'
+    np.testing.assert_allclose(r.output, _oracle_forward(ir, p0, {'x': x}), rtol=2e-6, atol=1e-7)
+    f.destroy()
+    assert f.run({'x': x}).kind == 'aborted'
+
+
+def test_compile_forward_parametric_shapes_and_buffered_upload():
+    from tensorgrad_amd.build_ir import build_forward_ir
+    from tensorgrad_amd.compile import compile_forward
+    f = compile_forward(configs.SinMLP(), _predict, {'x': [None, 1]}, max_cached_shapes=2, seed=9)
+    with pytest.raises(RuntimeError, match='before any params exist'):
+        f.download_params()
+    rng = np.random.default_rng(3)
+    ir = build_forward_ir(configs.SinMLP(), _predict, {'x': [4, 1]})
+    mine = {k: rng.standard_normal(np.shape(v)).astype(np.float32) for k, v in ir.initial_params(0).items()}
+    f.upload_params(dict(list(mine.items())[:3]))
+    f.upload_params(dict(list(mine.items())[3:]))          # merged with the first call
+    for n in (4, 7, 1, 7):
+        x = rng.standard_normal((n, 1)).astype(np.float32)
+        r = f.run({'x': x})
+        assert r.kind == 'completed' and r.output.shape == (n, 1)
+        irn = build_forward_ir(configs.SinMLP(), _predict, {'x': [n, 1]})
+        np.testing.assert_allclose(r.output, _oracle_forward(irn, mine, {'x': x}), rtol=2e-6, atol=1e-7)
+    assert len(f._cache) == 2          # 7 and 1; the owner (4) is held apart, never evicted
+    back = f.download_params()
+    assert all(np.array_equal(back[k], mine[k].reshape(-1)) for k in mine)
+    f.destroy()
+
+
+def test_checkpoint_resume_is_bit_identical():
+    """50 steps, save, a fresh compile (other init seed) loads the file, 50 more steps:
+    losses and params equal 100 straight steps bit for bit. The transformer variant
+    uses dropout, so the restored seed counter matters, and AdamW's t feeds lrt."""
+    import os
+    import tempfile
+    from tensorgrad_amd.safetensors import load_safetensors
+    cfg = configs.small_variant('transformer')
+    bs = configs.batches(cfg, 100)
+    a = tg_compile(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer, seed=11)
+    straight = [a.step(b).loss for b in bs]
+    want = a.download_params()
+    want_state, want_t, want_c = a.download_optimizer_state()
+    a.destroy()
+    b1 = tg_compile(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer, seed=11)
+    first = [b1.step(b).loss for b in bs[:50]]
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, 'ckpt.safetensors')
+        b1.save_checkpoint(path)
+        b1.destroy()
+        with open(path, 'rb') as fh:
+            saved = load_safetensors(fh.read())
+        assert saved.metadata['tensorgrad.step'] == '50' and saved.metadata['tensorgrad.prngCounter'] == '50'
+        assert set(saved.tensors) == set(want) | set(want_state)
+        b2 = tg_compile(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer, seed=12345)
+        b2.load_checkpoint(path)
+    second = [b2.step(b).loss for b in bs[50:]]
+    assert first + second == straight
+    got = b2.download_params()
+    for k in want:
+        assert np.array_equal(got[k].view(np.uint32), want[k].view(np.uint32)), k
+    st, t, c = b2.download_optimizer_state()
+    assert (t, c) == (want_t, want_c) == (100, 100)
+    for k in want_state:
+        assert np.array_equal(st[k].view(np.uint32), want_state[k].view(np.uint32)), k
+    b2.destroy()
+
+
+def test_optimizer_state_upload_is_strict_and_resumes():
+    cfg, t = _c1()
+    bs = configs.batches(cfg, 6)
+    for b in bs[:3]:
+        t.step(b)
+    p, (st, step_t, cnt) = t.download_params(), t.download_optimizer_state()
+    rest = [t.step(b).loss for b in bs[3:]]
+    u = tg_compile(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer, seed=1)
+    missing = dict(st)
+    missing.pop(next(iter(missing)))
+    with pytest.raises(BackendError, match='missing'):
+        u.upload_optimizer_state(missing, step_t, cnt)
+    u.upload_params(p)
+    u.upload_optimizer_state(st, step_t, cnt)
+    assert [u.step(b).loss for b in bs[3:]] == rest
+    t.destroy()
+    u.destroy()
