@@ -88,6 +88,21 @@ tg_status tg_step(tg_runtime* rt, int n, const char* const* names, const void* c
 tg_status tg_step_device(tg_runtime* rt, int n, const char* const* names, const void* const* dev_data,
                          const int64_t* nbytes, float* loss);
 
+/* Scratch-only step. No counterpart in the reference: it is for callers that cannot
+ * allocate device memory during a step (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). Same arguments and results as
+ * tg_step_device (device-resident user inputs); the step's launches are issued directly
+ * (no graph instantiation) and every scratch buffer they use (split-K and reduction
+ * partials, the embedding-gradient sort, launch-completion counters) lives in one static
+ * device array of TG_SCRATCH_BYTES per GPU instead of memory the runtime allocates. The
+ * call allocates nothing; graphs that need more scratch than TG_SCRATCH_BYTES are
+ * rejected with TG_INVALID_ARGUMENT. All calls on one GPU share that array: calls from
+ * one process are serialised; calls that overlap on one GPU from different processes
+ * race. Bit-identical to tg_step_device. */
+#define TG_SCRATCH_BYTES (8ll << 20)
+tg_status tg_step_noalloc(tg_runtime* rt, int n, const char* const* names, const void* const* dev_data,
+                          const int64_t* nbytes, float* loss);
+
 /* Device-resident batches (no reference counterpart): copy one batch of user inputs
  * (host pointers) into device slot `slot`, then run steps from a slot without any host
  * to device copy of user data. Used by callers that prefetch, and by the benchmark. */

@@ -26,7 +26,7 @@ EXPORTED = (
     'tg_step_device', 'tg_stage_batch', 'tg_step_staged', 'tg_run', 'tg_capture_count', 'tg_capture_name', 'tg_get_capture', 'tg_reset_optimizer',
     'tg_set_lr', 'tg_describe', 'tg_plan', 'tg_profile_nodes', 'tg_time_replays', 'tg_time_kinds',
     'tg_state_count', 'tg_state_name', 'tg_state_numel', 'tg_download_state', 'tg_upload_state',
-    'tg_save_checkpoint', 'tg_load_checkpoint', 'tg_safetensors_index',
+    'tg_save_checkpoint', 'tg_load_checkpoint', 'tg_safetensors_index', 'tg_step_noalloc',
 )
 
 
@@ -74,6 +74,7 @@ def lib():
     L.tg_download_params.argtypes = [vp, ctypes.c_int, c_char_pp, ctypes.POINTER(vp), i64p]
     L.tg_step.argtypes = [vp, ctypes.c_int, c_char_pp, ctypes.POINTER(vp), i64p, ctypes.POINTER(ctypes.c_float)]
     L.tg_step_device.argtypes = L.tg_step.argtypes
+    L.tg_step_noalloc.argtypes = L.tg_step.argtypes
     L.tg_run.argtypes = [vp, ctypes.c_int, c_char_pp, ctypes.POINTER(vp), i64p, vp, ctypes.c_int64]
     L.tg_stage_batch.argtypes = [vp, ctypes.c_int, ctypes.c_int, c_char_pp, ctypes.POINTER(vp), i64p]
     L.tg_step_staged.argtypes = [vp, ctypes.c_int, ctypes.POINTER(ctypes.c_float)]
@@ -202,6 +203,14 @@ class NativeRuntime:
         ptrs = (ctypes.c_void_p * len(names))(*dev_ptrs)
         sizes = (ctypes.c_int64 * len(names))(*nbytes)
         _check(lib().tg_step_device(self._h, len(names), _names(names), ptrs, sizes, ctypes.byref(loss)))
+        return float(loss.value)
+
+    def step_noalloc(self, names: Sequence[str], dev_ptrs: Sequence[int], nbytes: Sequence[int]) -> float:
+        """tg_step_noalloc: tg_step_device with the step's scratch in the static device array."""
+        loss = ctypes.c_float()
+        ptrs = (ctypes.c_void_p * len(names))(*dev_ptrs)
+        sizes = (ctypes.c_int64 * len(names))(*nbytes)
+        _check(lib().tg_step_noalloc(self._h, len(names), _names(names), ptrs, sizes, ctypes.byref(loss)))
         return float(loss.value)
 
     def stage_batch(self, slot: int, inputs: Dict[str, np.ndarray]) -> None:

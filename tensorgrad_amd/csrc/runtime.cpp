@@ -44,9 +44,38 @@
 #include "kernels.h"
 #include "safetensors.hpp"
 
+// Device scratch of the scratch-only step (tg_step_noalloc): split-K partials, reduction
+// partials, the embedding-gradient sort and the launch-completion counters of one step
+// live here instead of in memory the runtime allocates. One copy per GPU, held until the
+// process ends. Host code never passes the array's name to a kernel (on the host it is a
+// stand-in, not a device address): it uses the address hipGetSymbolAddress returns for
+// the current device (scratch_address).
+static constexpr size_t tg_kScratchBytes = (size_t)TG_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[tg_kScratchBytes];
+
 namespace tg {
 
 static thread_local std::string g_error;
+
+// Per-device address of `scratch`, looked up once per device with that device current.
+static char* scratch_address() {
+  static std::mutex mu;
+  static std::map<int, char*> addr;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) throw std::runtime_error(std::string("hipGetDevice: ") + hipGetErrorString(e));
+  std::lock_guard<std::mutex> g(mu);
+  auto it = addr.find(dev);
+  if (it != addr.end()) return it->second;
+  void* p = nullptr;
+  e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || !p) throw std::runtime_error(std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+  addr[dev] = static_cast<char*>(p);
+  return static_cast<char*>(p);
+}
+
+// Scratch-only calls share the one array per GPU; calls from this process are serialised.
+static std::mutex g_noalloc_mu;
 
 struct Error : std::runtime_error {
   tg_status code;
@@ -160,6 +189,7 @@ struct Node {
   double flops = 0, bytes = 0;      // algorithmic work per launch
   std::string shape;
   std::string detail;  // fused groups: member op kinds in program order
+  bool ws = false;     // bind() reads cur_ws_ / cur_counters_ (rebound for the scratch-only step)
   std::function<void(hipStream_t)> launch;   // bound after allocation
   std::function<std::function<void(hipStream_t)>()> bind;
 };
@@ -179,6 +209,7 @@ class Runtime {
   void upload_params(int n, const char* const* names, const float* const* data, const int64_t* numel);
   void download_params(int n, const char* const* names, float* const* data, const int64_t* numel);
   float step(int n, const char* const* names, const void* const* data, const int64_t* nbytes, bool device);
+  float step_noalloc(int n, const char* const* names, const void* const* data, const int64_t* nbytes);
   void run(int n, const char* const* names, const void* const* data, const int64_t* nbytes, void* out, int64_t out_bytes);
   void get_capture(const std::string& name, void* out, int64_t nbytes);
   void reset_optimizer();
@@ -372,7 +403,14 @@ class Runtime {
  private:
   void ensure_graph();
   void replay();
-  float* cur_ws_ = nullptr;   // workspace slice of the node being bound
+  float* cur_ws_ = nullptr;            // workspace of the node being bound
+  unsigned* cur_counters_ = nullptr;   // launch-completion counters of the node being bound
+  // Scratch-only step (tg_step_noalloc): the launches again, with every node that uses the
+  // workspace or the counters bound to the library's static device scratch instead.
+  std::vector<std::function<void(hipStream_t)>> noalloc_launch_;
+  std::string noalloc_error_;
+  unsigned* noalloc_counters_ = nullptr;
+  void prepare_noalloc();
   // TG_GRAPH=0 in the environment issues each step's launches directly instead of
   // replaying a captured hipGraph (for tools that do not follow graph launches).
   bool use_graph_ = true;
@@ -478,6 +516,7 @@ Runtime::Runtime(const char* json, Runtime* par, bool plan_only) : parent(par) {
   allocate();
   bind_all();   // in plan-only mode this still runs every launch's host-side bounds proof
   jit_finish();
+  if (!plan_only) prepare_noalloc();
   if (!plan_only && !init_nodes_.empty()) {
     for (auto& n : init_nodes_) n.launch(stream_);
     hip_check(hipStreamSynchronize(stream_), "hipStreamSynchronize(constants)");
@@ -1760,6 +1799,7 @@ void Runtime::emit_colsums(const std::vector<int>& batch) {
     cbase.push_back(take_counters(tgk::colsum_counters(c.C, c.R, terms)));
   }
   workspace_bytes_ = std::max(workspace_bytes_, ws);
+  n.ws = true;
   n.bind = [=]() -> std::function<void(hipStream_t)> {
     tgk::ColSumBatch bt{};
     bt.n = (int)batch.size();
@@ -1771,7 +1811,7 @@ void Runtime::emit_colsums(const std::vector<int>& batch) {
         throw Error(TG_INTERNAL, "column sum: operand smaller than its shape");
       double* part = reinterpret_cast<double*>(reinterpret_cast<char*>(cur_ws_) + ws_off[q]);
       bt.s[q] = tgk::colsum_desc((const float*)dptr(c.a), c.b >= 0 ? (const float*)dptr(c.b) : nullptr,
-                                 (float*)dptr(out), c.C, c.R, c.C, 1.0, part, counters_ + cbase[q]);
+                                 (float*)dptr(out), c.C, c.R, c.C, 1.0, part, cur_counters_ + cbase[q]);
     }
     return [bt](hipStream_t st) { tgk::colsum_batch(bt, st); };
   };
@@ -2517,13 +2557,14 @@ void Runtime::lower_op(int i) {
     if (k == "mean_last" || k == "sum_last") {
       workspace_bytes_ = std::max(workspace_bytes_, (size_t)tgk::sum_workspace_doubles(cells, red, outer, D) * 8);
       cbase = take_counters(tgk::sum_counters(cells, red, outer, D));
+      n.ws = true;
     }
     n.bind = [=]() -> std::function<void(hipStream_t)> {
       const float* pa = (const float*)dptr(a); void* po = dptr(out);
       if (k == "mean_last" || k == "sum_last") {
         double div = k == "mean_last" ? (double)D : 1.0;
         double* w = (double*)cur_ws_;
-        unsigned* cn = counters_ + cbase;
+        unsigned* cn = cur_counters_ + cbase;
         return [=](hipStream_t st) { tgk::reduce_sum(pa, (float*)po, cells, red, outer, D, div, w, cn, st); };
       }
       if (k == "argmax_last") return [=](hipStream_t st) { tgk::row_argmax(pa, (int32_t*)po, outer, D, st); };
@@ -2630,6 +2671,7 @@ void Runtime::lower_op(int i) {
     if (ncells != to.numel) throw Error(TG_INTERNAL, "sum_to_shape: cell count mismatch");
     workspace_bytes_ = std::max(workspace_bytes_, (size_t)tgk::sum_workspace_doubles(cells, red, ncells, nred) * 8);
     const int64_t cbase = take_counters(tgk::sum_counters(cells, red, ncells, nred));
+    n.ws = true;
     n.bind = [=]() -> std::function<void(hipStream_t)> {
       {
         int64_t dd[2 * tgk::kMaxRank], ss[2 * tgk::kMaxRank];
@@ -2640,7 +2682,7 @@ void Runtime::lower_op(int i) {
       }
       const float* pa = (const float*)dptr(a); float* po = (float*)dptr(out);
       double* w = (double*)cur_ws_;
-      unsigned* cn = counters_ + cbase;
+      unsigned* cn = cur_counters_ + cbase;
       return [=](hipStream_t st) { tgk::reduce_sum(pa, po, cells, red, ncells, nred, 1.0, w, cn, st); };
     };
   } else if (k == "matmul" || k == "matmul_batched") {
@@ -2685,6 +2727,7 @@ void Runtime::lower_op(int i) {
         n.flops = 0;
         n.bytes = 4.0 * (rows + rows * N + V * N);
         workspace_bytes_ = std::max(workspace_bytes_, (size_t)tgk::scatter_workspace_bytes(rows, V, N));
+        n.ws = true;
         n.bind = [=]() -> std::function<void(hipStream_t)> {
           const int32_t* pi = (const int32_t*)dptr(idx); const float* pd = (const float*)dptr(b);
           float* po = (float*)dptr(out);
@@ -2729,6 +2772,7 @@ void Runtime::lower_op(int i) {
     }
     workspace_bytes_ = std::max(workspace_bytes_, (size_t)ws * 4);
     n.bytes = 4.0 * (T_[a].numel + T_[b].numel + to.numel);
+    n.ws = ws > 0;
     n.bind = [=]() -> std::function<void(hipStream_t)> {
       check_gemm_spans(d, a, b, out);
       tgk::GemmDesc g = d;
@@ -3007,6 +3051,7 @@ void Runtime::jit_finish() {
 }
 
 void Runtime::bind_all() {
+  cur_counters_ = counters_;
   for (auto& n : init_nodes_) {
     for (int r : n.writes) if (!ptr_[r]) throw Error(TG_INTERNAL, "unallocated output in node " + n.kind);
     cur_ws_ = workspace_;
@@ -3019,6 +3064,46 @@ void Runtime::bind_all() {
     n.launch = n.bind();
   }
   cur_ws_ = nullptr;
+  cur_counters_ = nullptr;
+}
+
+// Bind the scratch-only launch list: nodes that use the workspace or the counters get
+// new closures over the static scratch (workspace first, counters after it); the others
+// share their regular closure. Runtimes whose workspace does not fit keep the reason.
+void Runtime::prepare_noalloc() {
+  const size_t ws = (workspace_bytes_ + 255) & ~(size_t)255;
+  const size_t need = ws + (size_t)counter_slots_ * sizeof(unsigned);
+  if (need > tg_kScratchBytes) {
+    noalloc_error_ = "step_noalloc: this graph needs " + std::to_string(need) + " bytes of scratch; the limit is " +
+                     std::to_string((size_t)tg_kScratchBytes);
+    return;
+  }
+  char* base = scratch_address();
+  noalloc_counters_ = reinterpret_cast<unsigned*>(base + ws);
+  noalloc_launch_.clear();
+  for (auto& n : nodes_) {
+    if (!n.ws) { noalloc_launch_.push_back(n.launch); continue; }
+    cur_ws_ = reinterpret_cast<float*>(base);
+    cur_counters_ = noalloc_counters_;
+    noalloc_launch_.push_back(n.bind());
+  }
+  cur_ws_ = nullptr;
+  cur_counters_ = nullptr;
+}
+
+float Runtime::step_noalloc(int n, const char* const* names, const void* const* data, const int64_t* nbytes) {
+  if (!opt_cfg_) throw Error(TG_INVALID_ARGUMENT, "step: graph has no optimizer (use run)");
+  if (noalloc_launch_.size() != nodes_.size()) throw Error(TG_INVALID_ARGUMENT, noalloc_error_);
+  std::lock_guard<std::mutex> g(g_noalloc_mu);
+  advance_scalars(true);
+  upload_inputs(n, names, data, nbytes, true);
+  // The counters must start at zero; the scratch keeps whatever the last call left.
+  if (counter_slots_) tgk::fill(noalloc_counters_, tgk::DT_I32, 0.0, counter_slots_, stream_);
+  for (auto& f : noalloc_launch_) f(stream_);
+  apply_copy_writebacks(stream_);
+  hip_check(hipMemcpyAsync(loss_host_, dptr(outputs_.at(0)), 4, hipMemcpyDeviceToHost, stream_), "hipMemcpyAsync(D2H)");
+  hip_check(hipStreamSynchronize(stream_), "hipStreamSynchronize");
+  return loss_host_[0];
 }
 
 void Runtime::launch_all(hipStream_t st) {
@@ -3611,6 +3696,12 @@ tg_status tg_step_device(tg_runtime* h, int n, const char* const* names, const v
                          float* loss) {
   TG_ENTER(h);
   return guarded([&] { float l = h->rt->step(n, names, data, nbytes, true); if (loss) *loss = l; });
+}
+
+tg_status tg_step_noalloc(tg_runtime* h, int n, const char* const* names, const void* const* data,
+                          const int64_t* nbytes, float* loss) {
+  TG_ENTER(h);
+  return guarded([&] { float l = h->rt->step_noalloc(n, names, data, nbytes); if (loss) *loss = l; });
 }
 
 tg_status tg_stage_batch(tg_runtime* h, int slot, int n, const char* const* names, const void* const* data,

@@ -36,6 +36,36 @@ def sign_ambiguous(diff, lr: float, steps: int) -> np.ndarray:
     return (a >= lr / 4) & (a <= 2.5 * lr * steps)
 
 
+class HipBuffers:
+    """Device copies of host arrays, made through the HIP runtime libtg.so itself links
+    (torch ships its own HIP runtime; device pointers are only exchanged within one)."""
+
+    def __init__(self, arrays):
+        import ctypes
+        from tensorgrad_amd import backend
+        backend.lib()                                   # loads /opt/rocm's libamdhip64 first
+        self._hip = ctypes.CDLL('libamdhip64.so.7')
+        self._hip.hipMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t]
+        self._hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+        self._hip.hipFree.argtypes = [ctypes.c_void_p]
+        self.names, self.ptrs, self.nbytes = [], [], []
+        for name, a in arrays.items():
+            a = np.ascontiguousarray(a)
+            p = ctypes.c_void_p()
+            if self._hip.hipMalloc(ctypes.byref(p), max(a.nbytes, 4)) != 0:
+                raise RuntimeError('hipMalloc failed')
+            if self._hip.hipMemcpy(p, a.ctypes.data, a.nbytes, 1) != 0:      # hipMemcpyHostToDevice
+                raise RuntimeError('hipMemcpy failed')
+            self.names.append(name)
+            self.ptrs.append(p.value)
+            self.nbytes.append(a.nbytes)
+
+    def free(self):
+        for p in self.ptrs:
+            self._hip.hipFree(p)
+        self.ptrs = []
+
+
 def make_range(shape) -> np.ndarray:
     """The reference tests' fixture: sin(0.1 i) * 0.5 (test/grad.ts:254-259)."""
     n = int(np.prod(shape)) if len(shape) else 1
