@@ -1,0 +1,227 @@
+'use strict'
+// In-process replacement for the reference's WorkerProxy (src/worker-proxy.ts:16-73),
+// serving the worker protocol's requests (src/worker-protocol.ts:54-63) with the
+// handler semantics of src/worker.ts:86-334 on the MI355X backend through the N-API
+// addon (tg_napi.node -> libtg.so). compile.ts keeps calling request / send /
+// terminate; only the object it constructs changes (see INTEGRATION.md).
+//
+// What the C ABI takes instead of the WebGPU plan: `toWire` recovers, from the
+// createRuntime / compileForward payload's `ir: {graph, plan, kernels}`, the tensor ids
+// of the parameter gradients and of the writeback sources. planBuffers gives both a
+// dedicated (never pooled) buffer (src/buffers.ts:142-145), so inverting
+// plan.tensorToBuffer on those buffers is exact. `kernels` (the WGSL) is not used.
+//
+// Written for Node >= 12 (no optional chaining / nullish coalescing).
+
+const path = require('path')
+
+let addon = null
+function native() {
+  if (!addon) addon = require(path.join(__dirname, 'tg_napi.node'))
+  return addon
+}
+
+function entries(m) {
+  if (m == null) return []
+  if (typeof m.entries === 'function' && !Array.isArray(m)) return Array.from(m.entries())
+  return Object.keys(m).map(k => [k, m[k]])
+}
+
+function numKey(k) { return typeof k === 'string' ? Number(k) : k }
+
+/** createRuntime / compileForward payload -> the C ABI's IR document (include/tg.h). */
+function toWire(ir, optimizer) {
+  const g = ir.graph
+  const plan = ir.plan
+  const owner = new Map()     // buffer id -> the one tensor id it holds, or -1 if pooled
+  for (const [tid, bid] of entries(plan.tensorToBuffer)) {
+    const b = numKey(bid)
+    owner.set(b, owner.has(b) ? -1 : numKey(tid))
+  }
+  const dedicated = (bid, what) => {
+    const t = owner.get(bid)
+    if (t === undefined || t < 0) throw new Error(`toWire: ${what} buffer ${bid} is not a dedicated buffer`)
+    return t
+  }
+  const paramGrads = {}
+  for (const [name, bid] of entries(plan.paramGradsByName)) paramGrads[name] = dedicated(bid, `param grad '${name}'`)
+  const homes = new Map()
+  for (const [name, bid] of entries(plan.paramsByName)) homes.set(bid, { destName: name, destKind: 'param' })
+  for (const [name, bid] of entries(plan.statesByName)) homes.set(bid, { destName: name, destKind: 'state' })
+  const writebacks = (plan.writebacks || []).map(w => {
+    const h = homes.get(w.dest)
+    if (!h) throw new Error(`toWire: writeback destination buffer ${w.dest} is not a param or state`)
+    return { source: dedicated(w.source, 'writeback source'), destName: h.destName, destKind: h.destKind }
+  })
+  const captures = {}
+  for (const [name, tid] of entries(g.captures)) captures[name] = tid
+  return {
+    graph: {
+      ops: g.ops,
+      tensors: g.tensors.map(t => ({ id: t.id, shape: Array.from(t.shape), dtype: t.dtype })),
+      outputs: Array.from(g.outputs),
+      captures,
+    },
+    paramGrads,
+    writebacks,
+    optimizer: optimizer || null,
+  }
+}
+
+function abortErr(msg) {
+  const e = new Error(msg)
+  e.name = 'AbortError'
+  return e
+}
+
+function countOf(shape) { return shape.reduce((a, b) => a * b, 1) }
+
+class NativeWorkerProxy {
+  constructor() {
+    this.graphs = new Map()     // graphId -> slot
+    this.terminated = false
+  }
+
+  _slotMeta(handle, wire) {
+    const g = wire.graph
+    const out = g.tensors[g.outputs[0]]
+    const captureShapes = {}
+    const captureDtypes = {}
+    for (const name of Object.keys(g.captures)) {
+      const t = g.tensors[g.captures[name]]
+      captureShapes[name] = t.shape
+      captureDtypes[name] = t.dtype
+    }
+    const nodes = JSON.parse(native().describe(handle)).nodes
+    return {
+      handle,
+      outputShape: out.shape,
+      outputInt: out.dtype !== 'f32',
+      captureShapes,
+      captureDtypes,
+      kernelCount: nodes.length,
+      paramNames: native().paramNames(handle),
+    }
+  }
+
+  _compileResult(slot) {
+    return {
+      paramNames: slot.paramNames.slice(),
+      outputShape: slot.outputShape.slice(),
+      kernelCount: slot.kernelCount,
+      captureShapes: Object.assign({}, slot.captureShapes),
+    }
+  }
+
+  _captures(slot) {
+    const names = Object.keys(slot.captureShapes)
+    if (names.length === 0) return null
+    const out = {}
+    for (const n of names)
+      out[n] = native().getCapture(slot.handle, n, countOf(slot.captureShapes[n]), slot.captureDtypes[n] !== 'f32')
+    return out
+  }
+
+  _mustGet(graphId) {
+    const slot = this.graphs.get(graphId)
+    if (!slot) throw new Error(`tensorgrad worker: graph ${graphId} not found`)
+    return slot
+  }
+
+  _handle(req) {
+    const p = req.payload
+    const A = native()
+    switch (req.kind) {
+      case 'createRuntime': {
+        const wire = toWire(p.ir, p.optimizer)
+        const h = A.create(JSON.stringify(wire))
+        try {
+          if (Object.keys(p.initialParams || {}).length > 0) A.uploadParams(h, p.initialParams)
+        } catch (e) {
+          A.destroy(h)
+          throw e
+        }
+        const slot = Object.assign(this._slotMeta(h, wire), { parentGraphId: null })
+        this.graphs.set(p.graphId, slot)
+        return this._compileResult(slot)
+      }
+      case 'compileForward': {
+        const parent = this.graphs.get(p.parentGraphId)
+        if (!parent) throw new Error(`compileForward: parent graph ${p.parentGraphId} not found`)
+        const wire = toWire(p.ir, null)
+        const h = A.createSibling(parent.handle, JSON.stringify(wire))
+        const slot = Object.assign(this._slotMeta(h, wire), { parentGraphId: p.parentGraphId })
+        this.graphs.set(p.graphId, slot)
+        return this._compileResult(slot)
+      }
+      case 'step': {
+        const slot = this.graphs.get(p.graphId)
+        if (!slot) throw abortErr('step aborted: graph replaced mid-flight')
+        const loss = A.step(slot.handle, p.inputs)
+        return { loss, captures: this._captures(slot) }
+      }
+      case 'run': {
+        const slot = this.graphs.get(p.graphId)
+        if (!slot) throw abortErr('run aborted: graph replaced mid-flight')
+        const output = A.run(slot.handle, p.inputs, countOf(slot.outputShape), slot.outputInt)
+        return { output, captures: this._captures(slot) }
+      }
+      case 'uploadParams':
+        A.uploadParams(this._mustGet(p.graphId).handle, p.params)
+        return null
+      case 'downloadParams':
+        return { params: A.downloadParams(this._mustGet(p.graphId).handle) }
+      case 'resetOptimizer':
+        A.resetOptimizer(this._mustGet(p.graphId).handle)
+        return null
+      case 'setLR':
+        A.setLR(this._mustGet(p.graphId).handle, JSON.stringify(p.lr))
+        return null
+      case 'destroy': {
+        for (const [id, slot] of Array.from(this.graphs.entries()))
+          if (slot.parentGraphId === p.graphId) this.graphs.delete(id)
+        const slot = this.graphs.get(p.graphId)
+        if (!slot) return null
+        A.destroy(slot.handle)        // cascades to the siblings in the library
+        this.graphs.delete(p.graphId)
+        return null
+      }
+      default:
+        throw new Error(`unknown request kind: ${req.kind}`)
+    }
+  }
+
+  /** Same contract as WorkerProxy.request: resolves with the handler's result, rejects
+   *  with an Error whose `name` survives (AbortError for destroyed / replaced graphs). */
+  request(req, transfer) {
+    if (this.terminated) return Promise.reject(new Error('tensorgrad: worker has been terminated'))
+    return new Promise((resolve, reject) => {
+      setImmediate(() => {
+        if (this.terminated) return reject(new Error('tensorgrad: worker terminated'))
+        try {
+          resolve(this._handle(req))
+        } catch (e) {
+          reject(e instanceof Error ? e : new Error(String(e)))
+        }
+      })
+    })
+  }
+
+  send(req, transfer) {
+    if (this.terminated) return
+    setImmediate(() => {
+      if (this.terminated) return
+      try { this._handle(req) } catch (e) { /* fire-and-forget, as WorkerProxy.send */ }
+    })
+  }
+
+  terminate() {
+    if (this.terminated) return
+    this.terminated = true
+    for (const [id, slot] of Array.from(this.graphs.entries()))
+      if (slot.parentGraphId === null) native().destroy(slot.handle)
+    this.graphs.clear()
+  }
+}
+
+module.exports = { NativeWorkerProxy, toWire, native }
