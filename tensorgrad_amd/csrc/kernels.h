@@ -256,6 +256,17 @@ void conv2d(const float* x, const float* w, float* y, const ConvDesc& c, hipStre
 void conv2d_input_grad(const float* w, const float* dy, float* dx, const ConvDesc& c, hipStream_t st);
 int64_t conv2d_weight_grad_workspace(const ConvDesc& c);
 void conv2d_weight_grad(const float* x, const float* dy, float* dw, const ConvDesc& c, double* work, hipStream_t st);
+// Implicit-GEMM convolutions on the matrix cores (k_conv_gemm.hip); f32 MFMA accumulation
+// (GEMM tolerance against the f64 evaluator). conv_gemm_ok: every tensor indexable in 32
+// bits. The weight gradient splits its batch reduction; `work` holds
+// conv_gemm_workspace_bytes(c) bytes (0: none needed), at most kConvWorkBytes.
+constexpr int64_t kConvWorkBytes = int64_t(4) << 20;
+bool conv_gemm_ok(const ConvDesc& c);
+int64_t conv_gemm_workspace_bytes(const ConvDesc& c);
+void conv2d_gemm(const float* x, const float* w, float* y, const ConvDesc& c, hipStream_t st);
+void conv2d_input_grad_gemm(const float* w, const float* dy, float* dx, const ConvDesc& c, hipStream_t st);
+void conv2d_weight_grad_gemm(const float* x, const float* dy, float* dw, const ConvDesc& c, float* work,
+                             hipStream_t st);
 struct PoolDesc { int64_t B, C, H, W, Ho, Wo, kH, kW, sH, sW, pH, pW; };
 void max_pool(const float* x, float* y, const PoolDesc& p, hipStream_t st);
 void max_pool_grad(const float* x, const float* dy, float* dx, const PoolDesc& p, hipStream_t st);

@@ -349,6 +349,7 @@ class Runtime {
   // Fused groups run as kernels generated per group (default) or, with TG_FUSED=vm in
   // the environment, through the interpreter kernels of k_fused.hip.
   bool use_jit_ = true;
+  bool use_conv_gemm_ = true;   // implicit-GEMM convolutions (TG_CONV=direct: direct f64 kernels)
   struct JitSlot {
     std::string name;
     hipFunction_t fn = nullptr;
@@ -468,6 +469,7 @@ Runtime::Runtime(const char* json, Runtime* par, bool plan_only) : parent(par) {
   if (const char* g = std::getenv("TG_REMAT")) use_remat_ = std::string(g) != "0";
   if (const char* g = std::getenv("TG_GEMM_EPI")) use_gemm_epi_ = std::string(g) == "1";
   if (const char* g = std::getenv("TG_FUSED")) use_jit_ = std::string(g) != "vm";
+  if (const char* g = std::getenv("TG_CONV")) use_conv_gemm_ = std::string(g) != "direct";
   // A several-stream schedule of the step was tried and crashed inside the HIP runtime
   // while capturing the transformer step; it is removed, and asking for it is an error.
   if (const char* g = std::getenv("TG_STREAMS"))
@@ -2808,17 +2810,32 @@ void Runtime::lower_op(int i) {
     n.bytes = 4.0 * (prod(xs) + prod(ws) + prod(ys));
     n.kind = "conv";
     n.shape = shape_str(xs) + "*" + shape_str(ws);
+    // Implicit GEMM on the matrix cores by default; TG_CONV=direct selects the direct f64
+    // kernels (bit-exact with the evaluator, far slower).
+    const bool mfma = use_conv_gemm_ && tgk::conv_gemm_ok(c);
+    if (mfma && k == "conv2d_weight_grad") {
+      const int64_t wsb = tgk::conv_gemm_workspace_bytes(c);
+      workspace_bytes_ = std::max(workspace_bytes_, (size_t)wsb);
+      n.ws = wsb > 0;
+    }
+    if (!mfma) n.detail = "direct";
     n.bind = [=]() -> std::function<void(hipStream_t)> {
       float* po = (float*)dptr(out);
       if (k == "conv2d") {
         const float* px = (const float*)dptr(x); const float* pw = (const float*)dptr(w);
+        if (mfma) return [=](hipStream_t st) { tgk::conv2d_gemm(px, pw, po, c, st); };
         return [=](hipStream_t st) { tgk::conv2d(px, pw, po, c, st); };
       }
       if (k == "conv2d_input_grad") {
         const float* pw = (const float*)dptr(w); const float* pd = (const float*)dptr(dy);
+        if (mfma) return [=](hipStream_t st) { tgk::conv2d_input_grad_gemm(pw, pd, po, c, st); };
         return [=](hipStream_t st) { tgk::conv2d_input_grad(pw, pd, po, c, st); };
       }
       const float* px = (const float*)dptr(x); const float* pd = (const float*)dptr(dy);
+      if (mfma) {
+        float* wk = cur_ws_;
+        return [=](hipStream_t st) { tgk::conv2d_weight_grad_gemm(px, pd, po, c, wk, st); };
+      }
       return [=](hipStream_t st) { tgk::conv2d_weight_grad(px, pd, po, c, nullptr, st); };
     };
   } else if (k == "max_pool_2d" || k == "max_pool_2d_grad") {

@@ -2,9 +2,11 @@
 the C ABI (tg_run), against the CPU oracle on the same inputs.
 
 Bar: element-wise, data-movement, stochastic, softmax, pooling, embedding and i32 ops are
-bit-exact; row sums / un-broadcast sums / conv weight gradients accumulate in f64 in a
-different order and must match to 1 ulp of f32; GEMMs accumulate in f32 on the matrix
-cores and must match to 2e-6 relative (norm-wise)."""
+bit-exact; row sums / un-broadcast sums accumulate in f64 in a different order and must
+match to 1 ulp of f32; GEMMs and the implicit-GEMM convolutions accumulate in f32 on the
+matrix cores and must match to 2e-6 relative (norm-wise)."""
+import os
+
 import numpy as np
 import pytest
 
@@ -556,20 +558,59 @@ def test_embedding_gather_and_scatter(V, N, rows, skew):
     exact(got, want)
 
 
-def test_conv_and_pool_kernels():
-    B, Ci, H, W, Co, G = 2, 4, 9, 8, 6, 2
-    x, w = _rand([B, Ci, H, W], 21), _rand([Co, Ci // G, 3, 3], 22)
-    got, want = run_both(lambda: O.conv2d(tensor_input('x', [B, Ci, H, W]), tensor_input('w', [Co, Ci // G, 3, 3]),
-                                          stride=2, padding=1, groups=G), {'x': x, 'w': w})
-    exact(got, want)
-    yshape = list(want.shape)
-    dy = _rand(yshape, 23)
-    got, want = run_both(lambda: O.conv2d_input_grad(tensor_input('w', [Co, Ci // G, 3, 3]), tensor_input('d', yshape),
-                                                     H, W, 2, 2, 1, 1, G), {'w': w, 'd': dy})
-    exact(got, want)
-    got, want = run_both(lambda: O.conv2d_weight_grad(tensor_input('x', [B, Ci, H, W]), tensor_input('d', yshape),
-                                                      3, 3, 2, 2, 1, 1, G), {'x': x, 'd': dy})
-    near(got, want)
+def _conv_env(impl):
+    """TG_CONV is read when a runtime is created: 'direct' selects the f64 direct kernels."""
+    import os
+    old = os.environ.get('TG_CONV')
+    if impl == 'direct':
+        os.environ['TG_CONV'] = 'direct'
+    else:
+        os.environ.pop('TG_CONV', None)
+    return old
+
+
+CONV_CASES = [
+    # B, Ci, H, W, Co, G, k, stride, pad
+    (2, 4, 9, 8, 6, 2, 3, 2, 1),
+    (128, 1, 28, 28, 32, 1, 3, 1, 0),      # the CNN config's first layer
+    (128, 32, 26, 26, 64, 1, 3, 1, 0),     # its second layer (split-K weight gradient)
+    (3, 5, 11, 7, 130, 1, 5, 1, 2),        # 5x5, padding, Cout above one tile
+]
+
+
+@pytest.mark.parametrize('impl', ['gemm', 'direct'])
+@pytest.mark.parametrize('case', CONV_CASES)
+def test_conv_kernels(impl, case):
+    """Implicit-GEMM convolutions (default) accumulate in f32 on the matrix cores: within
+    2e-6 relative (norm-wise) of the evaluator, like the GEMMs. The direct kernels
+    (TG_CONV=direct) reproduce the evaluator's f64 loops: forward and input gradient bit
+    for bit, the weight gradient (different f64 summation order) within 1 ulp."""
+    B, Ci, H, W, Co, G, k, s, pd = case
+    if impl == 'direct' and B > 8:
+        pytest.skip('the direct kernels are checked at small sizes')
+    old = _conv_env(impl)
+    try:
+        x, w = _rand([B, Ci, H, W], 21), _rand([Co, Ci // G, k, k], 22)
+        got, want = run_both(lambda: O.conv2d(tensor_input('x', [B, Ci, H, W]), tensor_input('w', [Co, Ci // G, k, k]),
+                                              stride=s, padding=pd, groups=G), {'x': x, 'w': w})
+        exact(got, want) if impl == 'direct' else gemm_close(got, want)
+        yshape = list(want.shape)
+        dy = _rand(yshape, 23)
+        got, want = run_both(lambda: O.conv2d_input_grad(tensor_input('w', [Co, Ci // G, k, k]),
+                                                         tensor_input('d', yshape), H, W, s, s, pd, pd, G),
+                             {'w': w, 'd': dy})
+        exact(got, want) if impl == 'direct' else gemm_close(got, want)
+        got, want = run_both(lambda: O.conv2d_weight_grad(tensor_input('x', [B, Ci, H, W]), tensor_input('d', yshape),
+                                                          k, k, s, s, pd, pd, G), {'x': x, 'd': dy})
+        near(got, want) if impl == 'direct' else gemm_close(got, want)
+    finally:
+        if old is None:
+            os.environ.pop('TG_CONV', None)
+        else:
+            os.environ['TG_CONV'] = old
+
+
+def test_pool_kernels():
     p = np.round(_rand([2, 3, 8, 8], 24) * 4) / 4   # ties inside windows
     got, want = run_both(lambda: O.max_pool2d(tensor_input('x', [2, 3, 8, 8]), 3, stride=2, padding=1), {'x': p})
     exact(got, want)
