@@ -99,7 +99,7 @@ tg_status tg_step_device(tg_runtime* rt, int n, const char* const* names, const 
  * rejected with TG_INVALID_ARGUMENT. All calls on one GPU share that array: calls from
  * one process are serialised; calls that overlap on one GPU from different processes
  * race. Bit-identical to tg_step_device. */
-#define TG_SCRATCH_BYTES (8ll << 20)
+#define TG_SCRATCH_BYTES (16ll << 20)
 tg_status tg_step_noalloc(tg_runtime* rt, int n, const char* const* names, const void* const* dev_data,
                           const int64_t* nbytes, float* loss);
 

@@ -166,6 +166,83 @@ __global__ void k_max_pool_grad(const float* __restrict__ x, const float* __rest
   }
 }
 
+// Pooling with 32-bit indexing (every tensor below 2^31 elements): one thread per window,
+// the same scan as k_max_pool (row-major over the window, -3.4e38 start, strict `>`).
+struct Pool32 {
+  int H, W, Ho, Wo, kH, kW, sH, sW, pH, pW;
+  int64_t nwin;
+  FastDiv dWo, dHoWo;
+};
+
+__device__ __forceinline__ void window_of(const Pool32& p, int i, int& bc, int& ho, int& wo) {
+  bc = (int)fastdiv((uint32_t)i, p.dHoWo);
+  const int q = i - bc * p.Ho * p.Wo;
+  ho = (int)fastdiv((uint32_t)q, p.dWo);
+  wo = q - ho * p.Wo;
+}
+
+__global__ void k_max_pool32(const float* __restrict__ x, float* __restrict__ y, Pool32 p) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < p.nwin; i += gridDim.x * blockDim.x) {
+    int bc, ho, wo;
+    window_of(p, i, bc, ho, wo);
+    const float* plane = x + (int64_t)bc * p.H * p.W;
+    float m = -3.4e38f;
+    for (int kh = 0; kh < p.kH; ++kh) {
+      const int hi = ho * p.sH + kh - p.pH;
+      if (hi < 0 || hi >= p.H) continue;
+      for (int kw = 0; kw < p.kW; ++kw) {
+        const int wi = wo * p.sW + kw - p.pW;
+        if (wi < 0 || wi >= p.W) continue;
+        const float v = plane[hi * p.W + wi];
+        if (v > m) m = v;
+      }
+    }
+    y[i] = m;
+  }
+}
+
+// Adjoint when the windows tile the input exactly (stride = window, no padding, H = Ho*sH,
+// W = Wo*sW): every input element lies in exactly one window, so each window writes its
+// own elements: dy at the recomputed argmax (the first maximum in scan order), zero
+// elsewhere. Equal to the gather form bit for bit (one term per element).
+__global__ void k_max_pool_grad_tiled(const float* __restrict__ x, const float* __restrict__ dy,
+                                      float* __restrict__ dx, Pool32 p) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < p.nwin; i += gridDim.x * blockDim.x) {
+    int bc, ho, wo;
+    window_of(p, i, bc, ho, wo);
+    const int64_t base = (int64_t)bc * p.H * p.W;
+    float m = -3.4e38f;
+    int arg = -1;
+    for (int kh = 0; kh < p.kH; ++kh)
+      for (int kw = 0; kw < p.kW; ++kw) {
+        const int off = (ho * p.sH + kh) * p.W + wo * p.sW + kw;
+        const float v = x[base + off];
+        if (v > m) { m = v; arg = off; }
+      }
+    const float g = dy[i];
+    for (int kh = 0; kh < p.kH; ++kh)
+      for (int kw = 0; kw < p.kW; ++kw) {
+        const int off = (ho * p.sH + kh) * p.W + wo * p.sW + kw;
+        dx[base + off] = off == arg ? g : 0.0f;
+      }
+  }
+}
+
+Pool32 pool32(const PoolDesc& d) {
+  Pool32 p{};
+  p.H = (int)d.H; p.W = (int)d.W; p.Ho = (int)d.Ho; p.Wo = (int)d.Wo; p.kH = (int)d.kH; p.kW = (int)d.kW;
+  p.sH = (int)d.sH; p.sW = (int)d.sW; p.pH = (int)d.pH; p.pW = (int)d.pW;
+  p.nwin = d.B * d.C * d.Ho * d.Wo;
+  p.dWo = make_fastdiv((uint32_t)d.Wo);
+  p.dHoWo = make_fastdiv((uint32_t)(d.Ho * d.Wo));
+  return p;
+}
+
+bool pool_small(const PoolDesc& d) {
+  return d.B * d.C * d.H * d.W < (int64_t(1) << 31) && d.B * d.C * d.Ho * d.Wo < (int64_t(1) << 31) && d.Ho > 0 &&
+         d.Wo > 0;
+}
+
 }  // namespace
 
 void conv2d(const float* x, const float* w, float* y, const ConvDesc& c, hipStream_t st) {
@@ -192,12 +269,22 @@ void conv2d_weight_grad(const float* x, const float* dy, float* dw, const ConvDe
 void max_pool(const float* x, float* y, const PoolDesc& p, hipStream_t st) {
   int64_t n = p.B * p.C * p.Ho * p.Wo;
   if (n <= 0) return;
+  if (pool_small(p)) {
+    k_max_pool32<<<grid_for(n), 256, 0, st>>>(x, y, pool32(p));
+    return;
+  }
   k_max_pool<<<grid_for(n), 256, 0, st>>>(x, y, p);
 }
 
 void max_pool_grad(const float* x, const float* dy, float* dx, const PoolDesc& p, hipStream_t st) {
   int64_t n = p.B * p.C * p.H * p.W;
   if (n <= 0) return;
+  const bool tiled = p.sH == p.kH && p.sW == p.kW && p.pH == 0 && p.pW == 0 && p.H == p.Ho * p.sH &&
+                     p.W == p.Wo * p.sW;
+  if (tiled && pool_small(p)) {
+    k_max_pool_grad_tiled<<<grid_for(p.B * p.C * p.Ho * p.Wo), 256, 0, st>>>(x, dy, dx, pool32(p));
+    return;
+  }
   k_max_pool_grad<<<grid_for(n), 256, 0, st>>>(x, dy, dx, p);
 }
 

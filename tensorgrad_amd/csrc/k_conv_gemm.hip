@@ -33,6 +33,7 @@ namespace {
 using namespace gd;
 using namespace cg;
 
+
 // One operand's ROWS x BK stage in registers, as Tile in k_gemm.hip.
 template <int ROWS, bool KFAST>
 struct Stage {
@@ -64,52 +65,35 @@ struct Stage {
   }
 };
 
-template <int MODE, int BM, int BN>
+// Pipeline: two register sets of staged loads, so the global loads of stage s + 2 are in
+// flight while stage s is multiplied and stage s + 1 waits in registers for its LDS slot.
+template <int MODE, bool FAST, int BM, int BN, int F>
 __global__ __launch_bounds__(kCT) void k_conv_gemm(ConvGemmArgs c) {
   constexpr int WGM = BM >= 64 ? 2 : 1, WGN = 4 / WGM;   // wave grid
   constexpr int WM = BM / WGM, WN = BN / WGN;            // wave tile
   constexpr int TM = WM / 32, TN = WN / 32;
   static_assert(TM >= 1 && TN >= 1 && WM % 32 == 0 && WN % 32 == 0, "bad conv tile");
-  constexpr bool BKF = MODE == CV_WGRAD;
+  using L = ConvLoader<MODE, FAST, BM, BN, F>;
   using SA = Stage<BM, true>;
-  using SB = Stage<BN, BKF>;
+  using SB = Stage<BN, L::BKF>;
+  static_assert(SA::Q == L::QA && SB::Q == L::QB, "stage / loader mismatch");
+  constexpr bool TAB = (F & F_TAB) != 0;
   __shared__ __attribute__((aligned(16))) float As[2][SA::SIZE];
   __shared__ __attribute__((aligned(16))) float Bs[2][SB::SIZE];
+  __shared__ uint32_t ktab[TAB ? 2 * kTab : 2];
 
   const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
   const int wm0 = (wave / WGN) * WM, wn0 = (wave % WGN) * WN;
-  // Tiles of one z (one image and group, or one split) are numbered contiguously per XCD.
-  const uint32_t nblk = gridDim.x;
-  uint32_t bid = blockIdx.x;
-  if (nblk % kXcds == 0) bid = (bid % kXcds) * (nblk / kXcds) + bid / kXcds;
-  const int tn = bid % c.tiles_n;
-  const uint32_t rest = bid / c.tiles_n;
-  const int tm = rest % c.tiles_m;
-  const int zs = rest / c.tiles_m;
-  const int m0 = tm * BM, n0 = tn * BN;
-  const int z = MODE == CV_WGRAD ? zs / c.splits : zs;
-  const int split = MODE == CV_WGRAD ? zs % c.splits : 0;
-  const int kbeg = split * c.k_per_split;
-  const int kend = min(c.K, kbeg + c.k_per_split);
+  L ld;
+  ld.init(c, block_pos<BM, BN>(c, blockIdx.x, gridDim.x, MODE), tid);
+  const int kbeg = ld.bp.kbeg, kend = ld.bp.kend;
+  if (TAB) {
+    for (int k = tid; k < c.K; k += kCT) k_term(c, MODE, k, ktab[2 * k], ktab[2 * k + 1]);
+    __syncthreads();
+  }
 
-  SA sa;
-  SB sb;
-  auto load = [&](int k0) {
-#pragma unroll
-    for (int e = 0; e < SA::Q; ++e) {
-      int rr, kk;
-      SA::coords(tid + e * kCT, rr, kk);
-      sa.q[e] = a_elems<MODE>(c, z, m0 + rr, k0 + kk, kend);
-    }
-#pragma unroll
-    for (int e = 0; e < SB::Q; ++e) {
-      int rr, kk;
-      SB::coords(tid + e * kCT, rr, kk);
-      if (BKF) sb.q[e] = b_elems_k(c, z, n0 + rr, k0 + kk, kend);
-      else sb.q[e] = b_elems_n<MODE>(c, z, n0 + rr, k0 + kk, kend);
-    }
-  };
-
+  SA sa[2];
+  SB sb[2];
   f32x16 acc[TM][TN];
 #pragma unroll
   for (int i = 0; i < TM; ++i)
@@ -121,17 +105,22 @@ __global__ __launch_bounds__(kCT) void k_conv_gemm(ConvGemmArgs c) {
   const int lrow = lane % 32, h = lane / 32;
   const int nst = kbeg < kend ? (kend - kbeg + kCBK - 1) / kCBK : 0;
   if (nst > 0) {
-    load(kbeg);
-    sa.store(As[0], tid);
-    sb.store(Bs[0], tid);
+    ld.load(c, kbeg, sa[0].q, sb[0].q, ktab);
+    if (nst > 1) ld.load(c, kbeg + kCBK, sa[1].q, sb[1].q, ktab);
+    sa[0].store(As[0], tid);
+    sb[0].store(Bs[0], tid);
   }
   __syncthreads();
   for (int st = 0; st < nst; ++st) {
     const int cur = st & 1;
-    const bool more = st + 1 < nst;
-    if (more) load(kbeg + (st + 1) * kCBK);
+    // registers of stage st were stored at the previous iteration: refill them with st + 2
+    if (st + 2 < nst) {
+      if (cur == 0) ld.load(c, kbeg + (st + 2) * kCBK, sa[0].q, sb[0].q, ktab);
+      else ld.load(c, kbeg + (st + 2) * kCBK, sa[1].q, sb[1].q, ktab);
+    }
     const float* Ac = As[cur];
     const float* Bc = Bs[cur];
+    // Blocked accumulation: a fresh partial sum per stage, added to the running total.
     f32x16 part[TM][TN];
 #pragma unroll
     for (int i = 0; i < TM; ++i)
@@ -155,9 +144,9 @@ __global__ __launch_bounds__(kCT) void k_conv_gemm(ConvGemmArgs c) {
           for (int j = 0; j < TN; ++j)
             part[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][jj], bv[j][jj], part[i][j], 0, 0, 0);
     }
-    if (more) {
-      sa.store(As[cur ^ 1], tid);
-      sb.store(Bs[cur ^ 1], tid);
+    if (st + 1 < nst) {
+      if (cur == 0) { sa[1].store(As[1], tid); sb[1].store(Bs[1], tid); }
+      else { sa[0].store(As[0], tid); sb[0].store(Bs[0], tid); }
     }
 #pragma unroll
     for (int i = 0; i < TM; ++i)
@@ -167,50 +156,88 @@ __global__ __launch_bounds__(kCT) void k_conv_gemm(ConvGemmArgs c) {
   }
 
   // Register r of lane l holds row (r/4)*8 + (l/32)*4 + r%4, column l%32.
-  float* O;
-  int64_t row_stride;
-  if (MODE == CV_FWD) {
-    const int b = fdiv(z, c.dG), g = z - b * c.G;
-    O = c.out + ((int64_t)b * c.Cout + g * c.CoutPG) * c.N;
-    row_stride = c.N;
-  } else if (MODE == CV_DGRAD) {
-    const int b = fdiv(z, c.dG), g = z - b * c.G;
-    O = c.out + ((int64_t)b * c.Cin + g * c.CinPG) * c.N;
-    row_stride = c.N;
-  } else {
-    O = c.splits > 1 ? c.work + ((int64_t)split * c.G + z) * c.M * c.N : c.out + (int64_t)z * c.M * c.N;
-    row_stride = c.N;
-  }
+  float* O = (MODE == CV_WGRAD && c.splits > 1) ? c.work : c.out;
+  const int64_t rs = ld.out_rs(c);
 #pragma unroll
-  for (int i = 0; i < TM; ++i)
+  for (int j = 0; j < TN; ++j) {
+    const int gn = ld.bp.n0 + wn0 + j * 32 + lrow;
+    if (gn >= c.N) continue;
+    float* col = O + ld.out_col(c, gn);
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int gn = n0 + wn0 + j * 32 + lrow;
-      if (gn >= c.N) continue;
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int gm = m0 + wm0 + i * 32 + (r / 4) * 8 + h * 4 + (r % 4);
-        if (gm < c.M) O[gm * row_stride + gn] = acc[i][j][r];
+        const int gm = ld.bp.m0 + wm0 + i * 32 + (r / 4) * 8 + h * 4 + (r % 4);
+        if (gm < c.M) col[gm * rs] = acc[i][j][r];
       }
-    }
+  }
 }
 
-// dW = sum of the split partials, in split order.
+// dW = sum of the split partials, deterministic. Many outputs: one thread per output
+// adds the splits in split order, 8 loads in flight. Few outputs and many splits (small
+// weights reducing over a large batch): one wavefront per output, lane l adding splits
+// l, l + 64, ... in order, then a fixed butterfly across the lanes.
 __global__ void k_conv_wgrad_reduce(const float* __restrict__ work, int splits, int64_t per_split,
                                     float* __restrict__ dw) {
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < per_split; i += (int64_t)gridDim.x * blockDim.x) {
     float s = 0.0f;
-    for (int sp = 0; sp < splits; ++sp) s += work[sp * per_split + i];
+    for (int sp0 = 0; sp0 < splits; sp0 += 8) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = sp0 + u < splits ? work[(sp0 + u) * per_split + i] : 0.0f;
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (sp0 + u < splits) s += v[u];
+    }
     dw[i] = s;
   }
 }
 
-template <int MODE>
-void launch_mode(const ConvPlan& p, const ConvGemmArgs& a, hipStream_t st) {
+__global__ __launch_bounds__(256) void k_conv_wgrad_reduce_wave(const float* __restrict__ work, int splits,
+                                                                int64_t per_split, float* __restrict__ dw) {
+  const int lane = threadIdx.x % 64;
+  const int64_t i = (int64_t)blockIdx.x * 4 + threadIdx.x / 64;   // one output per wavefront
+  if (i >= per_split) return;                                      // uniform across the wavefront
+  float s = 0.0f;
+  for (int sp = lane; sp < splits; sp += 64) s += work[sp * per_split + i];
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
+  if (lane == 0) dw[i] = s;
+}
+
+template <int MODE, bool FAST, int F>
+void launch_tile(const ConvPlan& p, const ConvGemmArgs& a, hipStream_t st) {
   const dim3 grid((unsigned)p.blocks);
-  if (p.bm == 32) k_conv_gemm<MODE, 32, 128><<<grid, kCT, 0, st>>>(a);
-  else if (p.bn == 128) k_conv_gemm<MODE, 64, 128><<<grid, kCT, 0, st>>>(a);
-  else k_conv_gemm<MODE, 64, 64><<<grid, kCT, 0, st>>>(a);
+  if (p.bm == 32) k_conv_gemm<MODE, FAST, 32, 128, F><<<grid, kCT, 0, st>>>(a);
+  else if (p.bn == 64) k_conv_gemm<MODE, FAST, 64, 64, F><<<grid, kCT, 0, st>>>(a);
+  else k_conv_gemm<MODE, FAST, 64, 128, F><<<grid, kCT, 0, st>>>(a);
+}
+
+// The loader variant (conv_flags) of a launch picks the instantiation.
+template <int MODE>
+void launch_mode(const ConvPlan& p, const ConvGemmArgs& a, bool fast, hipStream_t st) {
+  const int f = conv_flags(a, MODE);
+  if (MODE == CV_DGRAD) {
+    if (!fast) launch_tile<MODE, false, 0>(p, a, st);
+    else if (f & F_TAB) launch_tile<MODE, true, F_TAB>(p, a, st);
+    else launch_tile<MODE, true, 0>(p, a, st);
+    return;
+  }
+  const int fa = f & (F_AVEC | F_PAD);
+  if (MODE == CV_FWD && (f & F_TAB)) {
+    switch (fa) {
+      case 0: launch_tile<MODE, true, F_TAB>(p, a, st); return;
+      case F_AVEC: launch_tile<MODE, true, F_TAB | F_AVEC>(p, a, st); return;
+      case F_PAD: launch_tile<MODE, true, F_TAB | F_PAD>(p, a, st); return;
+      default: launch_tile<MODE, true, F_TAB | F_AVEC | F_PAD>(p, a, st); return;
+    }
+  }
+  switch (fa) {
+    case 0: launch_tile<MODE, true, 0>(p, a, st); return;
+    case F_AVEC: launch_tile<MODE, true, F_AVEC>(p, a, st); return;
+    case F_PAD: launch_tile<MODE, true, F_PAD>(p, a, st); return;
+    default: launch_tile<MODE, true, F_AVEC | F_PAD>(p, a, st); return;
+  }
 }
 
 }  // namespace
@@ -227,14 +254,15 @@ void conv2d_gemm(const float* x, const float* w, float* y, const ConvDesc& d, hi
   const ConvPlan p = conv_plan(CV_FWD, d);
   ConvGemmArgs a = make_args(d, p);
   a.x = x; a.w = w; a.out = y;
-  if (p.blocks > 0) launch_mode<CV_FWD>(p, a, st);
+  a.avec = a.avec && ((uintptr_t)w & 15) == 0;
+  if (p.blocks > 0) launch_mode<CV_FWD>(p, a, true, st);
 }
 
 void conv2d_input_grad_gemm(const float* w, const float* dy, float* dx, const ConvDesc& d, hipStream_t st) {
   const ConvPlan p = conv_plan(CV_DGRAD, d);
   ConvGemmArgs a = make_args(d, p);
   a.w = w; a.dy = dy; a.out = dx;
-  if (p.blocks > 0) launch_mode<CV_DGRAD>(p, a, st);
+  if (p.blocks > 0) launch_mode<CV_DGRAD>(p, a, d.sH == 1 && d.sW == 1, st);
 }
 
 void conv2d_weight_grad_gemm(const float* x, const float* dy, float* dw, const ConvDesc& d, float* work,
@@ -242,13 +270,18 @@ void conv2d_weight_grad_gemm(const float* x, const float* dy, float* dw, const C
   const ConvPlan p = conv_plan(CV_WGRAD, d);
   ConvGemmArgs a = make_args(d, p);
   a.x = x; a.dy = dy; a.out = dw; a.work = work;
+  a.avec = a.avec && ((uintptr_t)dy & 15) == 0;
   if (p.blocks <= 0) return;
   if (p.splits > 1 && !work) throw std::runtime_error("conv2d_weight_grad: missing workspace");
-  launch_mode<CV_WGRAD>(p, a, st);
+  launch_mode<CV_WGRAD>(p, a, true, st);
   if (p.splits > 1) {
     const int64_t per = (int64_t)a.G * a.M * a.N;
-    const int64_t nb = std::min<int64_t>((per + 255) / 256, 4096);
-    k_conv_wgrad_reduce<<<(int)nb, 256, 0, st>>>(work, p.splits, per, dw);
+    if (per < 16384 && p.splits > 16) {
+      k_conv_wgrad_reduce_wave<<<(unsigned)((per + 3) / 4), 256, 0, st>>>(work, p.splits, per, dw);
+    } else {
+      const int64_t nb = std::min<int64_t>((per + 255) / 256, 4096);
+      k_conv_wgrad_reduce<<<(int)nb, 256, 0, st>>>(work, p.splits, per, dw);
+    }
   }
 }
 

@@ -260,7 +260,7 @@ void conv2d_weight_grad(const float* x, const float* dy, float* dw, const ConvDe
 // (GEMM tolerance against the f64 evaluator). conv_gemm_ok: every tensor indexable in 32
 // bits. The weight gradient splits its batch reduction; `work` holds
 // conv_gemm_workspace_bytes(c) bytes (0: none needed), at most kConvWorkBytes.
-constexpr int64_t kConvWorkBytes = int64_t(4) << 20;
+constexpr int64_t kConvWorkBytes = int64_t(12) << 20;
 bool conv_gemm_ok(const ConvDesc& c);
 int64_t conv_gemm_workspace_bytes(const ConvDesc& c);
 void conv2d_gemm(const float* x, const float* w, float* y, const ConvDesc& c, hipStream_t st);

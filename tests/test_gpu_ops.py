@@ -610,13 +610,20 @@ def test_conv_kernels(impl, case):
             os.environ['TG_CONV'] = old
 
 
-def test_pool_kernels():
-    p = np.round(_rand([2, 3, 8, 8], 24) * 4) / 4   # ties inside windows
-    got, want = run_both(lambda: O.max_pool2d(tensor_input('x', [2, 3, 8, 8]), 3, stride=2, padding=1), {'x': p})
+@pytest.mark.parametrize('k,s,pd', [(3, 2, 1), (2, 2, 0), (3, 3, 0)])
+def test_pool_kernels(k, s, pd):
+    """Overlapping / padded windows use the gather adjoint; windows that tile the input
+    (2x2 and 3x3 with stride = window on 12x12) use the scatter adjoint. Both bit-exact,
+    ties resolving to the first element scanned."""
+    H = 12
+    Ho = (H + 2 * pd - k) // s + 1
+    p = np.round(_rand([2, 3, H, H], 24) * 4) / 4   # ties inside windows
+    got, want = run_both(lambda: O.max_pool2d(tensor_input('x', [2, 3, H, H]), k, stride=s, padding=pd), {'x': p})
     exact(got, want)
-    pd = _rand([2, 3, 4, 4], 25)
-    got, want = run_both(lambda: O.max_pool2d_grad(tensor_input('x', [2, 3, 8, 8]), tensor_input('d', [2, 3, 4, 4]),
-                                                    3, 3, 2, 2, 1, 1), {'x': p, 'd': pd})
+    assert got.shape == (2, 3, Ho, Ho)
+    d = _rand([2, 3, Ho, Ho], 25)
+    got, want = run_both(lambda: O.max_pool2d_grad(tensor_input('x', [2, 3, H, H]), tensor_input('d', [2, 3, Ho, Ho]),
+                                                    k, k, s, s, pd, pd), {'x': p, 'd': d})
     exact(got, want)
 
 

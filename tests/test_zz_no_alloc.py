@@ -15,7 +15,7 @@ from tensorgrad_amd.module import Module
 
 pytestmark = pytest.mark.gpu
 
-SCRATCH_BYTES = 8 << 20   # TG_SCRATCH_BYTES in include/tg.h
+SCRATCH_BYTES = 16 << 20   # TG_SCRATCH_BYTES in include/tg.h
 
 
 def _twin_steps(cfg, steps):
