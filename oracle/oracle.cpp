@@ -50,6 +50,49 @@ using Shape = std::vector<int64_t>;
 
 static int64_t numel(const Shape& s) { int64_t n = 1; for (auto d : s) n *= d; return n; }
 
+// C[z] = A[z] * B[z or 0] with f64 running sums in increasing k for every output: the same
+// sequence of roundings as the evaluator's per-output loop, so bit-identical to it. The
+// loops are blocked (4 rows x 256 columns of running sums, k outermost inside a block) so
+// B is read row by row; B's rows are widened to f64 once per block column. Built for AVX2
+// and baseline x86-64 (chosen at load time); -ffp-contract=off keeps mul and add separate.
+__attribute__((target_clones("avx2", "default")))
+static void matmul_block(const float* __restrict__ A, const double* __restrict__ Bd, float* __restrict__ C, int64_t M,
+                         int64_t K, int64_t N, int64_t m0, int64_t mr, int64_t n0, int64_t nn) {
+  constexpr int64_t MR = 4, NB = 256;
+  double acc[MR][NB];
+  for (int64_t r = 0; r < mr; ++r)
+    for (int64_t j = 0; j < nn; ++j) acc[r][j] = 0.0;
+  for (int64_t kk = 0; kk < K; ++kk) {
+    const double* brow = Bd + kk * nn;
+    for (int64_t r = 0; r < mr; ++r) {
+      const double av = (double)A[(m0 + r) * K + kk];
+      double* __restrict__ ar = acc[r];
+      for (int64_t j = 0; j < nn; ++j) ar[j] += av * brow[j];
+    }
+  }
+  for (int64_t r = 0; r < mr; ++r)
+    for (int64_t j = 0; j < nn; ++j) C[(m0 + r) * N + n0 + j] = (float)acc[r][j];
+}
+
+static void matmul_f64(const float* A, const float* B, float* C, int64_t batch, int64_t M, int64_t K, int64_t N,
+                       bool batched) {
+  constexpr int64_t MR = 4, NB = 256;
+  const int64_t mblocks = (M + MR - 1) / MR, nblocks = (N + NB - 1) / NB;
+  for (int64_t bi = 0; bi < batch; ++bi) {
+    const float* Bb = B + (batched ? bi * K * N : 0);
+    for (int64_t nbk = 0; nbk < nblocks; ++nbk) {
+      const int64_t n0 = nbk * NB, nn = std::min(NB, N - n0);
+      std::vector<double> Bd((size_t)(K * nn));
+      for (int64_t kk = 0; kk < K; ++kk)
+        for (int64_t j = 0; j < nn; ++j) Bd[kk * nn + j] = (double)Bb[kk * N + n0 + j];
+#pragma omp parallel for schedule(static)
+      for (int64_t mb = 0; mb < mblocks; ++mb)
+        matmul_block(A + bi * M * K, Bd.data(), C + bi * M * N, M, K, N, mb * MR, std::min(MR, M - mb * MR), n0, nn);
+    }
+  }
+}
+
+
 enum Dt { F32, I32, BOOL };
 static Dt parse_dt(const std::string& s) {
   if (s == "f32") return F32;
@@ -95,6 +138,18 @@ static std::vector<int64_t> strides_of(const Shape& s) {
 }
 
 // Right-aligned broadcast index (_eval.ts:49-70).
+// Source shape equal to the trailing dims of the output (after dropping leading 1s): its
+// element for output index i is i % numel(src) (what bidx computes, without the loop).
+static bool trailing(const Shape& out, const Shape& src) {
+  size_t s0 = 0;
+  while (s0 < src.size() && src[s0] == 1) ++s0;
+  const size_t n = src.size() - s0;
+  if (n > out.size()) return false;
+  for (size_t q = 0; q < n; ++q)
+    if (src[s0 + q] != out[out.size() - n + q]) return false;
+  return true;
+}
+
 static int64_t bidx(int64_t outIdx, const Shape& out, const Shape& src) {
   int64_t rankDiff = (int64_t)out.size() - (int64_t)src.size();
   int64_t aIdx = 0, aStride = 1, rem = outIdx;
@@ -137,15 +192,19 @@ static uint32_t to_uint32(double x) {
   return (uint32_t)m;
 }
 
+// ToUint32 of a non-negative integral f64 below 2^64: its value modulo 2^32.
+static inline uint32_t to_uint32_nonneg(double x) { return (uint32_t)(uint64_t)x; }
+
 // The dropout / categorical hash: PCG-RXS-M-XS evaluated the way _eval.ts:568-571 does,
 // with the two multiplies as IEEE f64 products (rounded above 2^53) before ToUint32.
 static uint32_t pcg_f64(uint32_t seed, uint32_t saltConst, uint32_t idx) {
   uint32_t h = seed ^ saltConst ^ idx;
+  // both products and the sum are non-negative integers below 2^63
   volatile double prod = (double)h * 747796405.0;
-  h = to_uint32(prod + 2891336453.0);
+  h = to_uint32_nonneg(prod + 2891336453.0);
   uint32_t x = h ^ (h >> ((h >> 28) + 4));
   volatile double prod2 = (double)x * 277803737.0;
-  h = to_uint32(prod2);
+  h = to_uint32_nonneg(prod2);
   h = h ^ (h >> 22);
   return h;
 }
@@ -358,16 +417,35 @@ class Oracle {
     std::set<int> keep(outputs_.begin(), outputs_.end());
     for (auto& c : captures_) keep.insert(c.second);
     for (auto& w : writebacks_) keep.insert(w.first);
+    // ORC_PROFILE=1 in the environment prints the time spent per op kind (to stderr).
+    static const bool prof = std::getenv("ORC_PROFILE") != nullptr;
+    std::map<std::string, double> tk;
     for (size_t i = 0; i < ops_.size(); ++i) {
       const JV& op = *ops_[i];
       int out = op["out"].i32();
-      vals_[out] = eval_op(op, inputs);
+      const double t0 = prof ? omp_get_wtime() : 0.0;
+      const std::string& kind = op["kind"].str();
+      const JV* src = op.find("a");
+      if ((kind == "reshape" || kind == "stop_gradient") && !retain_all_ && src && last_use[src->i32()] == (int)i &&
+          !keep.count(src->i32()) && vals_.count(src->i32())) {
+        // the input dies here: hand its storage over instead of copying it
+        Val v = std::move(vals_[src->i32()]);
+        vals_.erase(src->i32());
+        const Dt dt = tinfo_[out].dt;
+        v.dt = dt == BOOL ? I32 : dt;
+        vals_[out] = std::move(v);
+      } else {
+        vals_[out] = eval_op(op, inputs);
+      }
+      if (prof) tk[op["kind"].str()] += omp_get_wtime() - t0;
       if (!retain_all_) {
         for (int id : op_inputs(op)) {
           if (last_use[id] == (int)i && !keep.count(id)) vals_.erase(id);
         }
       }
     }
+    if (prof)
+      for (auto& kv : tk) fprintf(stderr, "oracle %-22s %8.3f s\n", kv.first.c_str(), kv.second);
   }
 
   static std::vector<int> op_inputs(const JV& op) {
@@ -436,10 +514,11 @@ Val Oracle::eval_op(const JV& op, const std::map<std::string, Val>& inputs) {
     const Shape& as = SH(op["a"].i32()); const Shape& bs = SH(op["b"].i32());
     Val o = make(dt, total);
     int which = k == "add" ? 0 : k == "sub" ? 1 : k == "mul" ? 2 : k == "div" ? 3 : k == "min" ? 4 : 5;
-    bool same_a = as == shape, same_b = bs == shape;
+    const bool ta = trailing(shape, as), tb = trailing(shape, bs);
+    const int64_t na = std::max<int64_t>(1, numel(as)), nb = std::max<int64_t>(1, numel(bs));
 #pragma omp parallel for schedule(static)
     for (int64_t i = 0; i < total; ++i) {
-      double x = a.num(same_a ? i : bidx(i, shape, as)), y = b.num(same_b ? i : bidx(i, shape, bs));
+      double x = a.num(ta ? i % na : bidx(i, shape, as)), y = b.num(tb ? i % nb : bidx(i, shape, bs));
       double r;
       switch (which) {
         case 0: r = x + y; break;
@@ -549,17 +628,9 @@ Val Oracle::eval_op(const JV& op, const std::map<std::string, Val>& inputs) {
     int64_t batch = numel(as) / (M * K);
     Val o = make(F32, batch * M * N);
     const float* A = a.f(); const float* B = b.f();
-#pragma omp parallel for collapse(2) schedule(static)
-    for (int64_t bi = 0; bi < batch; ++bi)
-      for (int64_t m = 0; m < M; ++m) {
-        const float* Ar = A + bi * M * K + m * K;
-        const float* Bb = B + (batched ? bi * K * N : 0);
-        for (int64_t n = 0; n < N; ++n) {
-          double s = 0;
-          for (int64_t kk = 0; kk < K; ++kk) s += (double)Ar[kk] * (double)Bb[kk * N + n];
-          o.f()[bi * M * N + m * N + n] = (float)s;
-        }
-      }
+    // Every output is s = ((0 + a0*b0) + a1*b1) + ... in increasing k, in f64 (the
+    // evaluator's loop, _eval.ts:206-219); see matmul_f64.
+    matmul_f64(A, B, o.f(), batch, M, K, N, batched);
     return o;
   }
   if (k == "one_hot") {
@@ -697,31 +768,47 @@ Val Oracle::eval_op(const JV& op, const std::map<std::string, Val>& inputs) {
     const Shape& as = SH(op["a"].i32());
     int64_t aTotal = numel(as);
     int64_t rankDiff = (int64_t)as.size() - (int64_t)shape.size();
-    std::vector<int64_t> target(aTotal);
-#pragma omp parallel for schedule(static)
-    for (int64_t aIdx = 0; aIdx < aTotal; ++aIdx) {
-      int64_t rem = aIdx;
-      std::vector<int64_t> coords(as.size());
-      for (int64_t d = (int64_t)as.size() - 1; d >= 0; --d) { coords[d] = rem % as[d]; rem /= as[d]; }
-      int64_t oi = 0, os = 1;
+    // Source dim d maps to output stride ostr[d] (0 where the output has size 1 or no
+    // dim): the sources of a cell are a product set over the reduced dims, visited here
+    // in increasing flat index (outer reduced dim slowest), as the evaluator's single
+    // pass over the source does for each cell.
+    const int64_t R = (int64_t)as.size();
+    std::vector<int64_t> ostr(R, 0), astr(R, 1);
+    {
+      int64_t os = 1;
       for (int64_t d = (int64_t)shape.size() - 1; d >= 0; --d) {
-        int64_t td = shape[d];
-        int64_t c = td == 1 ? 0 : coords[d + rankDiff];
-        oi += c * os; os *= td;
+        if (shape[d] != 1) ostr[d + rankDiff] = os;
+        os *= shape[d];
       }
-      target[aIdx] = oi;
+      for (int64_t d = R - 2; d >= 0; --d) astr[d] = astr[d + 1] * as[d + 1];
     }
+    std::vector<int64_t> kept, reduced;   // source dims that index the output / that are summed
+    for (int64_t d = 0; d < R; ++d) (ostr[d] ? kept : reduced).push_back(d);
     Val o = make(F32, total);
-    // Bucket sources per output cell preserving order, then reduce each cell in parallel.
-    std::vector<int64_t> cnt(total + 1, 0);
-    for (int64_t i = 0; i < aTotal; ++i) cnt[target[i] + 1]++;
-    for (int64_t c = 0; c < total; ++c) cnt[c + 1] += cnt[c];
-    std::vector<int64_t> order(aTotal), pos(cnt.begin(), cnt.end() - 1);
-    for (int64_t i = 0; i < aTotal; ++i) order[pos[target[i]]++] = i;
+    if (aTotal == 0) return o;
 #pragma omp parallel for schedule(static)
     for (int64_t c = 0; c < total; ++c) {
+      // decompose the cell over the kept dims (outer to inner)
+      int64_t rem = c, base = 0;
+      for (int64_t q = (int64_t)kept.size() - 1; q >= 0; --q) {
+        const int64_t d = kept[q];
+        const int64_t cd = rem % as[d];
+        rem /= as[d];
+        base += cd * astr[d];
+      }
       float s = 0.0f;
-      for (int64_t q = cnt[c]; q < cnt[c + 1]; ++q) s = (float)((double)s + a.num(order[q]));
+      std::vector<int64_t> ctr(reduced.size(), 0);
+      for (;;) {
+        int64_t off = base;
+        for (size_t q = 0; q < reduced.size(); ++q) off += ctr[q] * astr[reduced[q]];
+        s = (float)((double)s + a.num(off));
+        int64_t q = (int64_t)reduced.size() - 1;
+        for (; q >= 0; --q) {
+          if (++ctr[q] < as[reduced[q]]) break;
+          ctr[q] = 0;
+        }
+        if (q < 0) break;
+      }
       o.f()[c] = s;
     }
     return o;

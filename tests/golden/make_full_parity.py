@@ -1,0 +1,76 @@
+"""Writes the full-size training fixtures for tests/test_gpu_parity.py: each benchmark
+config trained for 100 optimizer steps by the CPU oracle (oracle/, the restatement of the
+reference evaluator test/_eval.ts plus the Adam convention of src/codegen.ts:841-905) from
+the seeded initial params on the seeded batches that the GPU test regenerates.
+
+Stored per config in full_<key>.npz (numpy, no pickles): the loss of every step, and per
+parameter tensor at step 100 either all values (tensors up to FULL_LIMIT elements) or a
+fixed seeded sample of SAMPLE indices, with the f64 norm of the whole tensor.
+
+    python tests/golden/make_full_parity.py [keys...] [--threads N]
+"""
+import argparse
+import os
+import sys
+import time
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, 'oracle'))
+
+import pyoracle  # noqa: E402
+from tensorgrad_amd import configs  # noqa: E402
+from tensorgrad_amd.build_ir import build_training_ir  # noqa: E402
+
+STEPS = 100
+FULL_LIMIT = 200_000
+SAMPLE = 4096
+
+
+def sample_indices(name: str, n: int) -> np.ndarray:
+    if n <= FULL_LIMIT:
+        return np.arange(n, dtype=np.int64)
+    seed = sum(ord(ch) * (i + 1) for i, ch in enumerate(name)) + n
+    return np.sort(np.random.default_rng(seed).choice(n, SAMPLE, replace=False)).astype(np.int64)
+
+
+def make(key: str) -> str:
+    cfg = configs.CONFIGS[key]
+    ir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer)
+    o = pyoracle.OracleRuntime(ir.wire())
+    o.upload_params(ir.initial_params(configs.INIT_SEED))
+    losses = []
+    t0 = time.time()
+    for i, b in enumerate(configs.batches(cfg, STEPS)):
+        losses.append(o.step(b))
+        if i % 10 == 9:
+            print(f'  [{key}] step {i + 1} loss {losses[-1]:.9g} ({time.time() - t0:.0f}s)', flush=True)
+    out = {'losses': np.array(losses, np.float64), 'steps': np.array(STEPS)}
+    shapes = ir.param_shapes()
+    for n in ir.param_names:
+        size = int(np.prod(shapes[n])) if shapes[n] else 1
+        v = o.get_home(n, size)
+        idx = sample_indices(n, size)
+        out[f'idx:{n}'] = idx
+        out[f'val:{n}'] = v[idx]
+        out[f'norm:{n}'] = np.array(np.linalg.norm(v.astype(np.float64)))
+    path = os.path.join(HERE, f'full_{key}.npz')
+    np.savez_compressed(path, **out)
+    return path
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument('keys', nargs='*', default=['char_mlp', 'cnn', 'transformer', 'nerf'])
+    ap.add_argument('--threads', type=int, default=os.cpu_count() or 8)
+    a = ap.parse_args()
+    pyoracle.set_threads(a.threads)
+    for k in a.keys:
+        print(k, '->', make(k), flush=True)
+
+
+if __name__ == '__main__':
+    main()
