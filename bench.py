@@ -26,7 +26,6 @@ sys.path.insert(0, ROOT)
 PEAK_F32_MFMA_TFLOPS = 157.3
 PEAK_HBM_GBS = 8000.0
 RING = 8
-CPU_STEPS = {'mlp_sin': 50, 'char_mlp': 3, 'cnn': 2, 'nerf': 1, 'transformer': 2}
 
 
 def measure(key, steps, warmup, profile_iters=3, kind_iters=20):
@@ -132,25 +131,111 @@ def profiled_traffic(path):
     return None
 
 
-def cpu_baseline(key):
+def trace_steps(key, steps, probe):
+    """Profiling driver: `steps` training steps of config `key` (staged batches) with
+    every launch issued directly, optionally after the streaming-copy probe."""
+    os.environ['TG_GRAPH'] = '0'
+    from tensorgrad_amd import backend, configs
+    from tensorgrad_amd.build_ir import build_training_ir
+    if probe:
+        copy_probe()
+    cfg = configs.CONFIGS[key]
+    ir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer)
+    rt = backend.NativeRuntime(ir.wire_json())
+    rt.upload_params(ir.initial_params(configs.INIT_SEED))
+    for i, b in enumerate(configs.batches(cfg, 2)):
+        rt.stage_batch(i, b)
+    loss = None
+    for i in range(steps):
+        loss = rt.step_staged(i % 2)
+    rt.destroy()
+    print(json.dumps({'trace_steps': steps, 'config': key, 'final_loss': loss, 'copy_probe': bool(probe)}), flush=True)
+
+
+def cpu_info():
+    """nproc (CPUs this process may run on), os.cpu_count() and the CPU model name."""
+    model = None
+    try:
+        with open('/proc/cpuinfo') as f:
+            for line in f:
+                if line.startswith('model name'):
+                    model = line.split(':', 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = os.cpu_count()
+    return {'nproc': avail, 'cpu_count': os.cpu_count(), 'cpu_model': model}
+
+
+def cpu_rate(key, threads, min_steps=3, min_seconds=10.0, exact_steps=None):
+    """Steps/s of the CPU oracle (the C++ restatement of the reference's CPU evaluator) on
+    config `key` with `threads` OpenMP threads: the same model, seed-42 init and batch
+    ring as the GPU run. Runs `exact_steps` steps, or else until at least `min_steps`
+    steps or at least `min_seconds` have passed (at least one step)."""
     sys.path.insert(0, os.path.join(ROOT, 'oracle'))
     import pyoracle
     from tensorgrad_amd import configs
     from tensorgrad_amd.build_ir import build_training_ir
-    threads = max(1, min(16, os.cpu_count() or 1))
     pyoracle.set_threads(threads)
     cfg = configs.CONFIGS[key]
     ir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer)
     o = pyoracle.OracleRuntime(ir.wire())
     o.upload_params(ir.initial_params(configs.INIT_SEED))
-    n = CPU_STEPS[key]
-    bs = configs.batches(cfg, n)
-    t0 = time.perf_counter()
-    for b in bs:
-        o.step(b)
-    dt = time.perf_counter() - t0
-    return {'value': n / dt, 'unit': 'steps/s', 'cores': threads, 'kind': 'port',
-            'sample': f'{n} full {key} training steps (fwd+bwd+Adam) of the CPU oracle, OpenMP over output elements'}
+    bs = configs.batches(cfg, RING)
+    n, t0 = 0, time.perf_counter()
+    while True:
+        o.step(bs[n % RING])
+        n += 1
+        dt = time.perf_counter() - t0
+        if exact_steps is not None:
+            if n >= exact_steps:
+                break
+        elif n >= min_steps or dt >= min_seconds:
+            break
+        if dt > 20:
+            print(f'# cpu {key} threads={threads}: {n} steps, {dt:.1f}s', file=sys.stderr, flush=True)
+    return {'steps_per_s': n / dt, 's_per_step': dt / n, 'steps': n, 'seconds': round(dt, 3), 'threads': threads}
+
+
+def cpu_threads():
+    # The GPU box allots 16 host cores per GPU (OMP_NUM_THREADS=16 there); more threads
+    # than the allotment would only time oversubscription.
+    info = cpu_info()
+    return max(1, min(16, info['nproc'] or 1))
+
+
+def cpu_baseline(key):
+    """The headline config's CPU baseline in both modes: `value` from the parallel mode
+    (OpenMP over output elements, `cores` threads), `single_thread` beside it."""
+    info = cpu_info()
+    threads = cpu_threads()
+    par = cpu_rate(key, threads, exact_steps=1000 if key == 'mlp_sin' else None)
+    one = cpu_rate(key, 1, exact_steps=1000 if key == 'mlp_sin' else None)
+    return {'value': par['steps_per_s'], 'unit': 'steps/s', 'cores': threads, 'kind': 'port',
+            'sample': f"{par['steps']} full {key} training steps (fwd+bwd+Adam) of the CPU oracle in "
+                      f"{par['seconds']}s, OpenMP over output elements",
+            'single_thread': {'value': one['steps_per_s'], 'steps': one['steps'], 'seconds': one['seconds']},
+            **info}
+
+
+def cpu_protocol():
+    """Every config in both modes: C1 for 1000 steps, the others until 3 steps or 10 s."""
+    from tensorgrad_amd import configs
+    threads = cpu_threads()
+    out = []
+    for key in configs.CONFIGS:
+        exact = 1000 if key == 'mlp_sin' else None
+        row = {'config': key}
+        for mode, th in (('parallel', threads), ('single_thread', 1)):
+            r = cpu_rate(key, th, exact_steps=exact)
+            row[mode] = {k: (round(v, 6) if isinstance(v, float) else v) for k, v in r.items()}
+            print(f'# cpu {key} {mode} ({th} threads): {r["s_per_step"]:.4f} s/step over {r["steps"]} steps',
+                  file=sys.stderr, flush=True)
+        out.append(row)
+    return {'cpu_protocol': out, **cpu_info()}
 
 
 def main():
@@ -161,11 +246,22 @@ def main():
     ap.add_argument('--config', default='transformer')
     ap.add_argument('--only', action='store_true', help='measure the headline config only')
     ap.add_argument('--no-cpu', action='store_true')
+    ap.add_argument('--trace-steps', type=int, default=0,
+                    help='only run this many steps of --config with launches issued directly (TG_GRAPH=0: '
+                         'profilers trace direct launches, not graph replays), then exit')
+    ap.add_argument('--cpu-protocol', action='store_true',
+                    help='only time the CPU oracle: every config, single-thread and parallel, then exit')
     ap.add_argument('--profile-iters', type=int, default=3, help='eager passes for the per-node breakdown')
     ap.add_argument('--kind-iters', type=int, default=20, help='passes per kernel-family timing')
     ap.add_argument('--probe-copy', action='store_true',
                     help='first run a 64 MiB streaming copy (profiler counter calibration)')
     args = ap.parse_args()
+    if args.cpu_protocol:
+        print(json.dumps(cpu_protocol()), flush=True)
+        return
+    if args.trace_steps > 0:
+        trace_steps(args.config, args.trace_steps, args.probe_copy)
+        return
     if args.gpus != 1:
         print(json.dumps({'error': 'this build runs on one GPU per process; multi-GPU data parallelism is '
                                    'designed (DESIGN.md) but not built, so --gpus must be 1'}))

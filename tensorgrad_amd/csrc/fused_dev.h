@@ -30,7 +30,8 @@ enum FusedOp {
   FO_RSQRT, FO_LOG, FO_EXP, FO_TANH, FO_SIGMOID, FO_ERF, FO_SIN, FO_COS, FO_DROPOUT,
   FO_ROWSUM,          // row form only: dst = f32(sum over the row of a, in f64, / imm)
   FO_SOFTMAX_CAUSAL,  // row form only: causal softmax of row q = row % D (q + 1 leading entries)
-  FO_LOG_SOFTMAX      // row form only
+  FO_LOG_SOFTMAX,     // row form only
+  FO_ONEHOT           // row form only: dst = (i32 a == column) ? one : 0 (1.0f for f32 results, 1 for i32)
 };
 
 constexpr int kFusedMaxIn = 12;

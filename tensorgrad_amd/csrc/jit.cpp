@@ -227,6 +227,12 @@ JitKernel fused_kernel(const FusedProgram& p, const FusedInstr* code, int64_t n)
         }
       }
       o << I << "}\n";
+    } else if (in.op == FO_ONEHOT) {
+      if (!row) throw std::runtime_error("jit: row opcode in an element group");
+      const char* one = in.dt == DT_I32 ? "1u" : "0x3f800000u";
+      for (int e = 0; e < N; ++e)
+        o << I << v << "[" << e << "] = (int)" << R(in.a) << "[" << e << "] == (int)(" << col(e) << ") ? " << one
+          << " : 0u;\n";
     } else if (in.op == FO_WHERE) {
       o << I << "#pragma unroll\n" << I << "for (int e = 0; e < " << N << "; ++e) " << v << "[e] = " << R(in.a)
         << "[e] != 0u ? " << R(in.b) << "[e] : " << R(in.c) << "[e];\n";
@@ -320,7 +326,7 @@ JitKernel gemm_epi_kernel(const FusedProgram& p, const FusedInstr* code, const G
   for (int q = 0; q < p.n_instr; ++q) {
     const FusedInstr& in = code[q];
     const std::string v = "v" + std::to_string(q);
-    if (in.op == FO_ROWSUM || in.op == FO_SOFTMAX_CAUSAL || in.op == FO_LOG_SOFTMAX)
+    if (in.op == FO_ROWSUM || in.op == FO_SOFTMAX_CAUSAL || in.op == FO_LOG_SOFTMAX || in.op == FO_ONEHOT)
       throw std::runtime_error("jit: row opcode in a GEMM epilogue");
     if (in.op == FO_WHERE) {
       o << I << "const unsigned " << v << " = " << R(in.a) << " != 0u ? " << R(in.b) << " : " << R(in.c) << ";\n";

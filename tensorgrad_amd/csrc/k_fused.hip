@@ -170,6 +170,14 @@ __device__ __forceinline__ void run_program(ConstCode code, int n_instr, uint32_
         }
         break;
       }
+      case FO_ONEHOT: {
+        if (TPR > 0) {
+          const uint32_t one = code[q].dt == DT_I32 ? 1u : 0x3f800000u;
+          const int32_t col0 = (int32_t)(threadIdx.x % TPR);
+          TG_UN((int32_t)X == col0 + e * TPR ? one : 0u)
+        }
+        break;
+      }
       // Row softmaxes, one wavefront per row (TPR == 64): the same arithmetic and
       // combination order as the standalone k_softmax_causal / k_log_softmax kernels.
       case FO_SOFTMAX_CAUSAL:

@@ -516,6 +516,17 @@ __global__ void k_gather_rows(const int32_t* __restrict__ idx, int64_t rows, con
   }
 }
 
+// Rows of 4k floats, 16-byte aligned: one float4 per thread, 32-bit index math.
+__global__ void k_gather_rows4(const int32_t* __restrict__ idx, uint32_t rows, const float4* __restrict__ table,
+                               uint32_t V, uint32_t n4, float4* __restrict__ out) {
+  const uint32_t total = rows * n4;
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += gridDim.x * blockDim.x) {
+    const uint32_t r = i / n4, c = i - r * n4;
+    const int32_t v = idx[r];
+    out[i] = (v >= 0 && (uint32_t)v < V) ? table[(size_t)v * n4 + c] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+}
+
 // Stable counting sort of row ids by token, in one block of kBucketWaves wavefronts: rows
 // with idx == v land in perm[offs[v] .. offs[v+1]) in increasing row order; tokens outside
 // [0, V) are dropped. Wave w of the block owns a contiguous 1 / kBucketWaves of the rows
@@ -697,6 +708,78 @@ __global__ void k_segment_finish(const double* __restrict__ part, int64_t N, int
   }
 }
 
+// Small vocabularies (V * rows <= kScatterScanMax) need no sort: block (v, column chunk)
+// walks idx in windows of kScanRows rows. Each of its four wavefronts ballots the rows of
+// its quarter of the window whose token is v; the quarters' counts give each wavefront
+// its offset, so the hits land in LDS as one list in row order. Then every thread adds
+// its column of the listed rows to an f64 accumulator, in list order, kScanLoads loads in
+// flight. The additions happen in increasing row order, the order of the one-hot
+// product's k loop. One launch, no workspace.
+constexpr int kScanRows = 4096;
+constexpr int kScanLoads = 32;
+constexpr int64_t kScatterScanMax = int64_t(1) << 22;
+
+__global__ __launch_bounds__(256) void k_scatter_scan(const int32_t* __restrict__ idx, int64_t rows,
+                                                      const float* __restrict__ dy, int64_t N,
+                                                      float* __restrict__ out) {
+  constexpr int Q = kScanRows / 4;     // rows per wavefront per window
+  constexpr int U = kScanLoads;
+  __shared__ int32_t hits[kScanRows];
+  __shared__ int nhit[4];
+  const int v = blockIdx.x;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t c = blockIdx.y * 256ll + threadIdx.x;
+  const bool col = c < N;
+  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  double acc = 0.0;
+  for (int64_t r0 = 0; r0 < rows; r0 += kScanRows) {
+    const int64_t qa = r0 + (int64_t)w * Q, qb = min(rows, qa + Q);
+    int32_t t[Q / 64];
+#pragma unroll
+    for (int u = 0; u < Q / 64; ++u) {
+      const int64_t r = qa + u * 64 + lane;
+      t[u] = r < qb ? idx[r] : -1;
+    }
+    uint64_t m[Q / 64];
+    int n = 0;
+#pragma unroll
+    for (int u = 0; u < Q / 64; ++u) {
+      m[u] = __ballot(t[u] == v);
+      n += __popcll(m[u]);
+    }
+    if (lane == 0) nhit[w] = n;
+    __syncthreads();
+    int base = 0, total = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int ck = nhit[k];
+      if (k < w) base += ck;
+      total += ck;
+    }
+#pragma unroll
+    for (int u = 0; u < Q / 64; ++u) {
+      if (t[u] == v) hits[base + __popcll(m[u] & below)] = (int32_t)(qa + u * 64 + lane);
+      base += __popcll(m[u]);
+    }
+    __syncthreads();
+    // Every slot loads (slots past the list repeat its entry j, lanes past N read column
+    // 0), so the U loads issue back to back; slots past the list add +0.0, which leaves
+    // the accumulator (+0.0 or a sum that cannot be -0.0) unchanged.
+    const int64_t cc = col ? c : 0;
+    for (int j = 0; j < total; j += U) {
+      float x[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) x[u] = dy[(int64_t)hits[j + u < total ? j + u : j] * N + cc];
+#pragma unroll
+      for (int u = 0; u < U; ++u) acc += j + u < total ? (double)x[u] : 0.0;
+    }
+    __syncthreads();   // the next window rewrites hits and nhit
+  }
+  if (col) out[(int64_t)v * N + c] = (float)acc;
+}
+
+inline bool scatter_scans(int64_t rows, int64_t V) { return V * rows <= kScatterScanMax; }
+
 inline int grid_for(int64_t n) {
   int64_t b = (n + 255) / 256;
   return (int)(b > 2048 ? 2048 : (b < 1 ? 1 : b));
@@ -707,10 +790,17 @@ inline int grid_for(int64_t n) {
 void gather_rows(const int32_t* idx, int64_t rows, const float* table, int64_t V, int64_t N, float* out,
                  hipStream_t st) {
   if (rows * N <= 0) return;
+  if (N % 4 == 0 && rows * N < (int64_t(1) << 32) && V < (int64_t(1) << 32) && ((uintptr_t)table & 15) == 0 &&
+      ((uintptr_t)out & 15) == 0) {
+    k_gather_rows4<<<grid_for(rows * N / 4), 256, 0, st>>>(idx, (uint32_t)rows, (const float4*)table, (uint32_t)V,
+                                                           (uint32_t)(N / 4), (float4*)out);
+    return;
+  }
   k_gather_rows<<<grid_for(rows * N), 256, 0, st>>>(idx, rows, table, V, N, out);
 }
 
 int64_t scatter_workspace_bytes(int64_t rows, int64_t V, int64_t N) {
+  if (scatter_scans(rows, V)) return 0;
   const int64_t items = (rows + kSeg - 1) / kSeg + V;
   const int64_t ints = rows + 2 * (V + 1) + 2 * items;
   return (ints * 4 + 255) / 256 * 256 + items * N * 8;
@@ -720,6 +810,12 @@ void scatter_rows(const int32_t* idx, int64_t rows, const float* dy, int64_t V, 
                   hipStream_t st) {
   if (V * N <= 0) return;
   if (V > kMaxBucketV || rows >= (int64_t(1) << 31)) throw std::runtime_error("scatter_rows: V or rows too large");
+  if (scatter_scans(rows, V)) {
+    const int64_t ny = (N + 255) / 256;
+    if (ny > 65535) throw std::runtime_error("scatter_rows: N too large");
+    k_scatter_scan<<<dim3((unsigned)V, (unsigned)ny), 256, 0, st>>>(idx, rows, dy, N, out);
+    return;
+  }
   const int64_t items = (rows + kSeg - 1) / kSeg + V;
   int32_t* perm = static_cast<int32_t*>(work);
   int32_t* offs = perm + rows;

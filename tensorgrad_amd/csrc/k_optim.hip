@@ -15,41 +15,74 @@ namespace tgk {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kPerThread = 4;
-constexpr int64_t kChunk = kThreads * kPerThread;
+static_assert(kAdamChunk == kThreads * 8, "a thread updates two float4 of a full chunk");
 
-__global__ __launch_bounds__(kThreads) void k_adam_multi(const AdamTensor* __restrict__ ts,
-                                                         const int64_t* __restrict__ chunk_tensor,
-                                                         const int64_t* __restrict__ chunk_start, int64_t nchunks,
-                                                         const float* __restrict__ lrtp, AdamHyper h) {
+struct Upd { float p, m, v; };
+
+__device__ __forceinline__ Upd adam_elem(float gf, float mf0, float vf0, float pf, double lrt, double shrink,
+                                         const AdamHyper& h) {
+  const double g = (double)gf;
+  const double m = __dadd_rn(__dmul_rn(h.beta1, (double)mf0), __dmul_rn(h.one_minus_beta1, g));
+  const double v = __dadd_rn(__dmul_rn(h.beta2, (double)vf0), __dmul_rn(__dmul_rn(h.one_minus_beta2, g), g));
+  const float mf = (float)m, vf = (float)v;
+  const double upd = __ddiv_rn(__dmul_rn(lrt, (double)mf), __dadd_rn(__dsqrt_rn((double)vf), h.eps));
+  return {(float)__dsub_rn(__dmul_rn(shrink, (double)pf), upd), mf, vf};
+}
+
+// Block b updates chunks b, b + grid, ...: one descriptor load per chunk, then every
+// operand of a full, 16-byte aligned chunk as two float4 per thread, all loads issued
+// before the arithmetic; partial or unaligned chunks go element by element.
+__global__ __launch_bounds__(kThreads) void k_adam_chunks(const AdamChunk* __restrict__ cs, int64_t nchunks,
+                                                          const float* __restrict__ lrtp, AdamHyper h) {
   const double lrt = (double)*lrtp;
   for (int64_t c = blockIdx.x; c < nchunks; c += gridDim.x) {
-    const AdamTensor t = ts[chunk_tensor[c]];
-    const double shrink = t.shrink_ptr ? (double)*t.shrink_ptr : t.shrink;
-    const int64_t beg = chunk_start[c];
-    const int64_t end = min(t.n, beg + kChunk);
-    for (int64_t i = beg + threadIdx.x; i < end; i += kThreads) {
-      const double g = (double)t.g[i];
-      const double m = __dadd_rn(__dmul_rn(h.beta1, (double)t.m[i]), __dmul_rn(h.one_minus_beta1, g));
-      const double v = __dadd_rn(__dmul_rn(h.beta2, (double)t.v[i]), __dmul_rn(__dmul_rn(h.one_minus_beta2, g), g));
-      const float mf = (float)m, vf = (float)v;
-      const double upd = __ddiv_rn(__dmul_rn(lrt, (double)mf), __dadd_rn(__dsqrt_rn((double)vf), h.eps));
-      const double p = __dsub_rn(__dmul_rn(shrink, (double)t.p[i]), upd);
-      t.m[i] = mf;
-      t.v[i] = vf;
-      t.p[i] = (float)p;
+    const AdamChunk k = cs[c];
+    const double shrink = k.shrink_ptr ? (double)*k.shrink_ptr : k.shrink;
+    float* __restrict__ P = k.p;
+    float* __restrict__ M = k.m;
+    float* __restrict__ V = k.v;
+    const float* __restrict__ G = k.g;
+    const bool vec = k.n == kAdamChunk &&
+                     ((reinterpret_cast<uintptr_t>(P) | reinterpret_cast<uintptr_t>(M) |
+                       reinterpret_cast<uintptr_t>(V) | reinterpret_cast<uintptr_t>(G)) & 15) == 0;
+    if (vec) {
+      float4 g[2], m[2], v[2], p[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int q = threadIdx.x + u * kThreads;
+        g[u] = reinterpret_cast<const float4*>(G)[q];
+        m[u] = reinterpret_cast<const float4*>(M)[q];
+        v[u] = reinterpret_cast<const float4*>(V)[q];
+        p[u] = reinterpret_cast<const float4*>(P)[q];
+      }
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const Upd a = adam_elem(g[u].x, m[u].x, v[u].x, p[u].x, lrt, shrink, h);
+        const Upd b = adam_elem(g[u].y, m[u].y, v[u].y, p[u].y, lrt, shrink, h);
+        const Upd d = adam_elem(g[u].z, m[u].z, v[u].z, p[u].z, lrt, shrink, h);
+        const Upd e = adam_elem(g[u].w, m[u].w, v[u].w, p[u].w, lrt, shrink, h);
+        const int q = threadIdx.x + u * kThreads;
+        reinterpret_cast<float4*>(P)[q] = make_float4(a.p, b.p, d.p, e.p);
+        reinterpret_cast<float4*>(M)[q] = make_float4(a.m, b.m, d.m, e.m);
+        reinterpret_cast<float4*>(V)[q] = make_float4(a.v, b.v, d.v, e.v);
+      }
+    } else {
+      for (int64_t i = threadIdx.x; i < k.n; i += kThreads) {
+        const Upd a = adam_elem(G[i], M[i], V[i], P[i], lrt, shrink, h);
+        P[i] = a.p;
+        M[i] = a.m;
+        V[i] = a.v;
+      }
     }
   }
 }
 
 }  // namespace
 
-void adam_multi(const AdamTensor* tensors, int count, const int64_t* chunk_tensor, const int64_t* chunk_start,
-                int64_t nchunks, const float* lrt, AdamHyper h, hipStream_t st) {
-  (void)count;
+void adam_multi(const AdamChunk* chunks, int64_t nchunks, const float* lrt, AdamHyper h, hipStream_t st) {
   if (nchunks <= 0) return;
-  int64_t blocks = nchunks < 8192 ? nchunks : 8192;
-  k_adam_multi<<<(int)blocks, kThreads, 0, st>>>(tensors, chunk_tensor, chunk_start, nchunks, lrt, h);
+  const int64_t blocks = nchunks < 8192 ? nchunks : 8192;
+  k_adam_chunks<<<(int)blocks, kThreads, 0, st>>>(chunks, nchunks, lrt, h);
 }
 
 }  // namespace tgk

@@ -273,15 +273,17 @@ void max_pool_grad(const float* x, const float* dy, float* dx, const PoolDesc& p
 
 // ---- optimizer (k_optim.hip) ----------------------------------------------------------
 // One fused multi-tensor Adam/AdamW update, in place on p, m, v.
-struct AdamTensor {
+// One launch unit of the fused Adam update: up to kAdamChunk consecutive elements of one
+// parameter (pointers already offset to the chunk's first element).
+constexpr int64_t kAdamChunk = 2048;
+struct AdamChunk {
   float* p; float* m; float* v; const float* g;
-  int64_t n;
-  double shrink;          // literal decayShrink (used when shrink_ptr is null)
-  const float* shrink_ptr;
+  const float* shrink_ptr;  // per-step decay shrink tensor, or null: use `shrink`
+  double shrink;
+  int64_t n;                // elements in the chunk, 1 .. kAdamChunk
 };
 struct AdamHyper { double beta1, one_minus_beta1, beta2, one_minus_beta2, eps; };
-// `tensors` is a device array of `count` AdamTensor; `chunks` maps blocks to tensors.
-void adam_multi(const AdamTensor* tensors, int count, const int64_t* chunk_tensor, const int64_t* chunk_start,
-                int64_t nchunks, const float* lrt, AdamHyper h, hipStream_t st);
+// `chunks` is a device array of `nchunks` descriptors covering every parameter.
+void adam_multi(const AdamChunk* chunks, int64_t nchunks, const float* lrt, AdamHyper h, hipStream_t st);
 
 }  // namespace tgk

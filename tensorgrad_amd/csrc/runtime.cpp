@@ -284,9 +284,7 @@ class Runtime {
     return b;
   }
   // fused Adam tables (device)
-  tgk::AdamTensor* adam_tensors_ = nullptr;
-  int64_t* adam_chunk_tensor_ = nullptr;
-  int64_t* adam_chunk_start_ = nullptr;
+  tgk::AdamChunk* adam_chunks_ = nullptr;
   std::vector<int> state_roots_;
 
   hipGraph_t graph_ = nullptr;
@@ -318,6 +316,7 @@ class Runtime {
   std::vector<char> dropped_;   // op left out of its own group: only groups recomputing it run it
   int producer_group(int t) const;
   int op_class(int m, bool row, const Dims& F) const;
+  int inline_one_hot(int t, const Dims& F) const;
   bool is_row_reduce(int m) const;
   std::vector<Group> groups_;
   std::vector<int> group_of_;   // op -> group index or -1
@@ -534,10 +533,8 @@ Runtime::~Runtime() {
   if (workspace_ && !plan_only_) hipFree(workspace_);
   if (counters_ && !plan_only_) hipFree(counters_);
   if (fused_code_dev_ && !plan_only_) hipFree(fused_code_dev_);
-  if (adam_tensors_) hipFree(adam_tensors_);
+  if (adam_chunks_) hipFree(adam_chunks_);
   for (void* t : dev_tables_) hipFree(t);
-  if (adam_chunk_tensor_) hipFree(adam_chunk_tensor_);
-  if (adam_chunk_start_) hipFree(adam_chunk_start_);
   for (char* p : slots_) if (p) hipFree(p);
   if (staging_) hipHostFree(staging_);
   if (loss_host_) hipHostFree(loss_host_);
@@ -993,8 +990,7 @@ void Runtime::lower() {
     n.shape = std::to_string(adam_p_ops.size()) + " tensors, " + std::to_string((long long)elems) + " params";
     std::vector<int> pops = adam_p_ops;
     n.bind = [this, pops]() -> std::function<void(hipStream_t)> {
-      std::vector<tgk::AdamTensor> host;
-      std::vector<int64_t> ct, cs;
+      std::vector<tgk::AdamChunk> chunks;
       double b1 = 0.9, b2 = 0.999, eps = 1e-8;
       const float* lrt = nullptr;
       for (size_t q = 0; q < pops.size(); ++q) {
@@ -1005,36 +1001,28 @@ void Runtime::lower() {
         eps = O(pi).at("eps").num();
         lrt = (const float*)dptr(fld(pi, "lrt"));
         const tgj::Value& ds = O(pi).at("decayShrinkTensor");
-        tgk::AdamTensor at{};
-        at.p = (float*)dptr(fld(pi, "p"));
-        at.m = (float*)dptr(fld(mo, "m"));
-        at.v = (float*)dptr(fld(vo, "v"));
         int g = fld(mo, "g");
         if (!view_[g].contiguous()) throw Error(TG_INTERNAL, "adam: gradient is not contiguous");
-        at.g = (const float*)dptr(g);
-        at.n = T_[fld(pi, "p")].numel;
-        if (T_[fld(mo, "m")].numel != at.n || T_[fld(vo, "v")].numel != at.n || T_[g].numel != at.n ||
-            T_[root(g)].numel < at.n)
+        const int64_t n = T_[fld(pi, "p")].numel;
+        if (T_[fld(mo, "m")].numel != n || T_[fld(vo, "v")].numel != n || T_[g].numel != n || T_[root(g)].numel < n)
           throw Error(TG_INVALID_ARGUMENT, "adam: p / m / v / g size mismatch");
-        at.shrink = ds.null() ? O(pi).at("decayShrink").num() : 1.0;
-        at.shrink_ptr = ds.null() ? nullptr : (const float*)dptr(ds.i32());
-        host.push_back(at);
-        for (int64_t s = 0; s < at.n; s += 1024) { ct.push_back((int64_t)q); cs.push_back(s); }
+        float* p = (float*)dptr(fld(pi, "p"));
+        float* m = (float*)dptr(fld(mo, "m"));
+        float* v = (float*)dptr(fld(vo, "v"));
+        const float* gp = (const float*)dptr(g);
+        const double shrink = ds.null() ? O(pi).at("decayShrink").num() : 1.0;
+        const float* shrink_ptr = ds.null() ? nullptr : (const float*)dptr(ds.i32());
+        for (int64_t s = 0; s < n; s += tgk::kAdamChunk)
+          chunks.push_back({p + s, m + s, v + s, gp + s, shrink_ptr, shrink, std::min(tgk::kAdamChunk, n - s)});
       }
       if (plan_only_) return [](hipStream_t) {};
-      hip_check(hipMalloc(&adam_tensors_, host.size() * sizeof(tgk::AdamTensor)), "hipMalloc");
-      hip_check(hipMalloc(&adam_chunk_tensor_, ct.size() * sizeof(int64_t)), "hipMalloc");
-      hip_check(hipMalloc(&adam_chunk_start_, cs.size() * sizeof(int64_t)), "hipMalloc");
-      hip_check(hipMemcpy(adam_tensors_, host.data(), host.size() * sizeof(tgk::AdamTensor), hipMemcpyHostToDevice), "hipMemcpy");
-      hip_check(hipMemcpy(adam_chunk_tensor_, ct.data(), ct.size() * sizeof(int64_t), hipMemcpyHostToDevice), "hipMemcpy");
-      hip_check(hipMemcpy(adam_chunk_start_, cs.data(), cs.size() * sizeof(int64_t), hipMemcpyHostToDevice), "hipMemcpy");
+      hip_check(hipMalloc(&adam_chunks_, chunks.size() * sizeof(tgk::AdamChunk)), "hipMalloc");
+      hip_check(hipMemcpy(adam_chunks_, chunks.data(), chunks.size() * sizeof(tgk::AdamChunk), hipMemcpyHostToDevice),
+                "hipMemcpy");
       tgk::AdamHyper h{b1, 1 - b1, b2, 1 - b2, eps};
-      int count = (int)host.size();
-      int64_t nch = (int64_t)ct.size();
-      auto* tens = adam_tensors_;
-      auto* cT = adam_chunk_tensor_;
-      auto* cS = adam_chunk_start_;
-      return [=](hipStream_t st) { tgk::adam_multi(tens, count, cT, cS, nch, lrt, h, st); };
+      const int64_t nch = (int64_t)chunks.size();
+      const tgk::AdamChunk* dc = adam_chunks_;
+      return [=](hipStream_t st) { tgk::adam_multi(dc, nch, lrt, h, st); };
     };
     add_node(std::move(n));
   }
@@ -1057,6 +1045,8 @@ static const std::map<std::string, int>& pointwise_ops() {
       {"dropout", tgk::FO_DROPOUT}, {"broadcast_to", tgk::FO_COPY}};
   return m;
 }
+
+constexpr int64_t kWideRow = 4096;
 
 static bool is_row_reduce_kind(const std::string& k) { return k == "sum_last" || k == "mean_last"; }
 
@@ -1101,7 +1091,25 @@ int Runtime::producer_group(int t) const {
 // full-shaped members of row groups), 1 / 2 = row-shaped member ([..] / [.., 1]).
 int Runtime::op_class(int m, bool row, const Dims& F) const {
   if (!row || is_row_reduce(m)) return 0;
+  if (kinds_[m] == "one_hot") return 1;   // its indices are one value per row
   return row_class(T_[O(m).at("out").i32()].shape, F);
+}
+
+// The one_hot op whose result operand t of a row group of shape F = [.., D] is, when the
+// group can evaluate it in registers instead of reading it: t is the whole result, of
+// shape F with depth D, and its i32 indices (shape F without D) are a graph input, so they
+// exist before any group runs. -1 otherwise.
+int Runtime::inline_one_hot(int t, const Dims& F) const {
+  const int r = root(t);
+  const int s = T_[r].src;
+  if (s < 0 || kinds_[s] != "one_hot" || virtual_[s] || F.empty() || T_[t].shape != F) return -1;
+  if (t != r && !(view_[t].contiguous() && T_[t].numel == T_[r].numel)) return -1;
+  if (O(s).at("out").i32() != r || O(s).at("depth").i64() != F.back()) return -1;
+  const int ix = fld(s, "indices");
+  const int ixs = T_[root(ix)].src;
+  if (T_[ix].dt != I32 || T_[ix].shape != Dims(F.begin(), F.end() - 1)) return -1;
+  if (ixs >= 0 && !is_leaf(ixs)) return -1;
+  return s;
 }
 
 bool Runtime::dup_in(int gi, int m) const {
@@ -1117,9 +1125,20 @@ Runtime::GroupPlan Runtime::plan_group(const std::vector<int>& own, bool row, co
   std::vector<int> ops(own);
   const std::set<int> dup(dups ? dups->begin() : own.end(), dups ? dups->end() : own.end());
   ops.insert(ops.end(), dup.begin(), dup.end());
+  // A row group evaluates its one-hot operands from their indices (a compare with the
+  // column) as members of its own that store nothing.
+  std::set<int> inl;
+  if (row)
+    for (int m : ops)
+      for (int t : op_inputs(*ops_[m])) {
+        const int s = inline_one_hot(t, F);
+        if (s >= 0) inl.insert(s);
+      }
+  ops.insert(ops.end(), inl.begin(), inl.end());
   std::sort(ops.begin(), ops.end());
   std::set<int> members(ops.begin(), ops.end());
   auto inside = [&](int t) {
+    if (row && inline_one_hot(t, F) >= 0) return true;
     const int gi = producer_group(t);
     return gi >= 0 && members.count(T_[root(t)].src) > 0;
   };
@@ -1130,6 +1149,7 @@ Runtime::GroupPlan Runtime::plan_group(const std::vector<int>& own, bool row, co
     const std::string& k = kinds_[m];
     const tgj::Value& op = O(m);
     if (k == "relu_grad") opnds[q] = {op.at("x").i32(), op.at("dy").i32()};
+    else if (k == "one_hot") opnds[q] = {op.at("indices").i32()};
     else if (k == "where") opnds[q] = {op.at("cond").i32(), op.at("a").i32(), op.at("b").i32()};
     else if (op.get("b") && k != "dropout") opnds[q] = {op.at("a").i32(), op.at("b").i32()};
     else opnds[q] = {op.at("a").i32()};
@@ -1169,7 +1189,7 @@ Runtime::GroupPlan Runtime::plan_group(const std::vector<int>& own, bool row, co
   };
   std::vector<bool> stored(ops.size(), false);
   for (size_t q = 0; q < ops.size(); ++q) {
-    if (dup.count(ops[q])) continue;   // the owning group stores what others read
+    if (dup.count(ops[q]) || inl.count(ops[q])) continue;   // the owning group stores what others read
     const int t = O(ops[q]).at("out").i32();
     if (read_outside(t)) { stored[q] = true; gp.outs.push_back(t); }
   }
@@ -1217,7 +1237,9 @@ Runtime::GroupPlan Runtime::plan_group(const std::vector<int>& own, bool row, co
     if (regs.size() > 2) in.c = regs[2];
     const int out = op.at("out").i32();
     in.dt = kdt(T_[out].dt);
-    if (k == "softmax_causal_last") {
+    if (k == "one_hot") {
+      in.op = tgk::FO_ONEHOT;
+    } else if (k == "softmax_causal_last") {
       in.op = tgk::FO_SOFTMAX_CAUSAL;
     } else if (k == "log_softmax_last") {
       in.op = tgk::FO_LOG_SOFTMAX;
@@ -1279,8 +1301,10 @@ void Runtime::form_groups() {
   auto fits = [&](const std::vector<int>& ops, bool row, const Dims& F) {
     if (ops.size() > (size_t)tgk::kFusedMaxInstr) return false;
     GroupPlan gp = plan_group(ops, row, F);
+    // a wide row keeps 64 or more values per lane in each register: few registers
+    const int maxregs = row && F.back() > 1024 ? 4 : tgk::kFusedRegs;
     return gp.ext.size() <= (size_t)tgk::kFusedMaxIn && gp.outs.size() <= (size_t)tgk::kFusedMaxOut &&
-           gp.nregs <= tgk::kFusedRegs;
+           gp.nregs <= maxregs;
   };
   for (size_t i = 0; i < ops_.size(); ++i) {
     const std::string& k = kinds_[i];
@@ -1294,7 +1318,10 @@ void Runtime::form_groups() {
     if (red) {
       const int a = fld((int)i, "a");
       In = T_[a].shape;
-      if (In.empty() || In.back() < 1 || In.back() > 1024 || T_[a].numel <= 0) continue;   // standalone kernel
+      // Rows up to 1024 wide; a single row (a whole-tensor sum) up to kWideRow in generated
+      // kernels. Wider rows run as standalone reductions.
+      const int64_t maxd = use_jit_ && T_[a].numel == In.back() ? kWideRow : 1024;
+      if (In.empty() || In.back() < 1 || In.back() > maxd || T_[a].numel <= 0) continue;
     }
     std::vector<int> cands;
     for (int t : op_inputs(*ops_[i])) {
@@ -2728,8 +2755,9 @@ void Runtime::lower_op(int i) {
         n.kind = "scatter";
         n.flops = 0;
         n.bytes = 4.0 * (rows + rows * N + V * N);
-        workspace_bytes_ = std::max(workspace_bytes_, (size_t)tgk::scatter_workspace_bytes(rows, V, N));
-        n.ws = true;
+        const int64_t wsb = tgk::scatter_workspace_bytes(rows, V, N);
+        workspace_bytes_ = std::max(workspace_bytes_, (size_t)wsb);
+        n.ws = wsb > 0;
         n.bind = [=]() -> std::function<void(hipStream_t)> {
           const int32_t* pi = (const int32_t*)dptr(idx); const float* pd = (const float*)dptr(b);
           float* po = (float*)dptr(out);

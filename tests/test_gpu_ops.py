@@ -14,6 +14,7 @@ import pyoracle
 from _helpers import make_range, wire
 from tensorgrad_amd import backend
 from tensorgrad_amd import ir as IR
+from tensorgrad_amd import nn
 from tensorgrad_amd import ops as O
 from tensorgrad_amd.grad import append_grad
 from tensorgrad_amd.trace import param_input, tensor_input, trace_fn
@@ -270,7 +271,7 @@ def test_softmaxes_and_causal_mask():
     exact(got, want)
 
 
-CE_SHAPES = [(64, 27), (128, 10), (50, 65), (7, 130)]
+CE_SHAPES = [(64, 27), (128, 10), (50, 65), (7, 130), (4096, 65)]
 
 
 @pytest.mark.parametrize('R,D', CE_SHAPES)
@@ -302,6 +303,12 @@ def test_cross_entropy_row_chains(R, D):
     exact(got, want)
     got, want = run_both(lambda: backward(O.exp(lsm())), ins)
     exact(got, want)
+    # The loss itself: the target pick (one_hot evaluated inside the row group from the
+    # targets) and the batch mean (one wide single-row group when R > 1024), f64 row sums
+    # in lane order: within one f32 ulp of the evaluator's sequential sum.
+    got, want = run_both(lambda: nn.cross_entropy(O.add(tensor_input('x', [R, D]), tensor_input('b', [D])),
+                                                  tensor_input('t', [R], 'i32')), ins)
+    near(got, want)
 
 
 def _attention_graph(B, H, T, dh, what):
@@ -551,8 +558,9 @@ def test_embedding_gather_and_scatter(V, N, rows, skew):
         oh = O.reshape(O.one_hot(tensor_input('i', [rows], 'i32'), V), [rows, V])
         return O.matmul(O.swap_axes(oh, -1, -2), tensor_input('d', [rows, N]))
     got, want = run_both(grad_body, {'i': idx, 'd': dy})
-    # f64 sums in row order, grouped in runs of 16 rows: equal to the evaluator's
-    # sequential f64 sum up to f64 rounding, so at most one f32 ulp apart.
+    # f64 sums in row order (small vocabularies sequentially, large ones in runs of 16
+    # rows): equal to the evaluator's sequential f64 sum up to f64 rounding, so at most
+    # one f32 ulp apart.
     near(got, want)
     got, want = run_both(lambda: O.one_hot(tensor_input('i', [rows], 'i32'), V), {'i': idx})
     exact(got, want)

@@ -1,8 +1,8 @@
 """tg_step_noalloc through the C ABI: the scratch-only step gives the same losses and
 parameters, bit for bit, as tg_step_device on a twin runtime, on two calls in a row
-(the full char-MLP LM, then its reduced variant: a smaller input and a smaller scratch
-footprint, so stale scratch contents from the first call would show), and rejects a
-graph whose scratch need exceeds the static array."""
+(the full CNN, then its reduced variant: a smaller input and a smaller scratch footprint
+of convolution weight-gradient partials, so stale scratch contents from the first call
+would show), and rejects a graph whose scratch need exceeds the static array."""
 import numpy as np
 import pytest
 
@@ -47,8 +47,8 @@ def _twin_steps(cfg, steps):
 
 
 def test_step_noalloc_matches_step_device_twice():
-    big = _twin_steps(configs.CONFIGS['char_mlp'], 3)
-    small = _twin_steps(configs.small_variant('char_mlp'), 3)
+    big = _twin_steps(configs.CONFIGS['cnn'], 3)
+    small = _twin_steps(configs.small_variant('cnn'), 3)
     assert 0 < small < big <= SCRATCH_BYTES
 
 
