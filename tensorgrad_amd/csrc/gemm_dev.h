@@ -80,9 +80,11 @@ struct DTile {
   }
 
   // Per-thread byte offsets of this thread's PER chunks (elements, DW) from the tile origin
-  // (row r0, k = k0); fixed for the whole k loop. Rows past `rlim` read the last row.
+  // (row r0, k = k0); fixed for the whole k loop. Rows past `rlim` read the last row; k at
+  // or past `kv` (a partial last stage) reads k = kv - 1 (whole k rows of a row-contiguous
+  // operand; single elements of a DW k-contiguous one), which the tile then zeroes in LDS.
   __device__ __forceinline__ static void offsets(int64_t sr, int64_t sk, int64_t r0, int64_t rlim, int tid,
-                                                 uint32_t* off) {
+                                                 uint32_t* off, int kv = BK) {
     const int lane = tid & 63, wave = tid >> 6;
 #pragma unroll
     for (int e = 0; e < PER; ++e) {
@@ -92,14 +94,14 @@ struct DTile {
         // LDS float P of the tile: undo the chunk swizzle to find its (row, k)
         if (KFAST) {
           const int row = P / BK, rem = P % BK;
-          const int k = (((rem >> 2) ^ swz(row)) << 2) | (rem & 3);
+          const int k = min((((rem >> 2) ^ swz(row)) << 2) | (rem & 3), kv - 1);
           const int64_t gr = min(r0 + row, rlim - 1) - r0;
           off[e] = (uint32_t)((gr * sr + k) * 4);
         } else {
           const int k = P / ROWS, rem = P % ROWS;
           const int n = (((rem >> 2) ^ swz(k)) << 2) | (rem & 3);
           const int64_t gr = min(r0 + n, rlim - 1) - r0;
-          off[e] = (uint32_t)((k * sk + gr) * 4);
+          off[e] = (uint32_t)((min(k, kv - 1) * sk + gr) * 4);
         }
         continue;
       }
@@ -110,7 +112,7 @@ struct DTile {
         off[e] = (uint32_t)((gr * sr + c * 4) * 4);
       } else {
         const int64_t gr = min(r0 + c * 4, rlim - 4) - r0;
-        off[e] = (uint32_t)((row * sk + gr) * 4);
+        off[e] = (uint32_t)((min(row, kv - 1) * sk + gr) * 4);
       }
     }
   }
@@ -134,6 +136,18 @@ struct DTile {
         const uint32_t m0v = lds + (uint32_t)((e * (NT / 64) + wave) * kLdsBlock * 4);
         asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off[e]), "s"(gb), "{m0}"(m0v));
       }
+    }
+  }
+
+  // Zero the entries of k >= kv in an LDS slot (threads tid of nt).
+  __device__ __forceinline__ static void zero_tail(float* L, int kv, int tid, int nt) {
+    if (KFAST) {
+      for (int P = tid; P < SIZE; P += nt) {
+        const int row = P / BK, rem = P % BK;
+        if (((((rem >> 2) ^ swz(row)) << 2) | (rem & 3)) >= kv) L[P] = 0.0f;
+      }
+    } else {
+      for (int P = kv * ROWS + tid; P < SIZE; P += nt) L[P] = 0.0f;
     }
   }
 
@@ -170,7 +184,12 @@ __device__ __forceinline__ uint32_t xcd_order(uint32_t b, uint32_t nblk) {
 }
 
 // One output tile (tile number b of the problem g).
-template <int BM, int BN, int BK, int NS, bool AK, bool BKF, int NT, int KG, class Epi, bool BDW = false>
+// ADW / BDW: operand A / B moves one 4-byte element per lane (rows need no alignment).
+// KT: the last stage of a split may be partial (K per split not a multiple of BK): its
+// loads clamp k to the last valid k and the tile zeroes the rest of the stage in LDS
+// before multiplying it (KT needs DW for a k-contiguous operand).
+template <int BM, int BN, int BK, int NS, bool AK, bool BKF, int NT, int KG, class Epi, bool BDW = false,
+          bool ADW = false, bool KT = false>
 __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint32_t b, const Epi& epi) {
   // per k group: 4 waves 2 x 2; 8 waves 2 x 4 (BN = 128) or 4 x 2
   constexpr int GT = NT / KG;             // threads per k group
@@ -182,8 +201,9 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint32_t b, const E
   static_assert(KG == 1 || (KG == 2 && NS % 2 == 0), "k groups take alternate slots");
   constexpr int NSG = NS / KG;            // slots per k group
   constexpr int NG = BK / 8;
-  using TA = DTile<BM, BK, AK, GT>;
+  using TA = DTile<BM, BK, AK, GT, ADW>;
   using TB = DTile<BN, BK, BKF, GT, BDW>;
+  static_assert(!KT || ((!AK || ADW) && (!BKF || BDW)), "a partial k stage needs DW k-contiguous operands");
   constexpr int PER = TA::PER + TB::PER;
   static_assert(PER * (NSG - 1) < 64, "too many loads in flight for vmcnt");
   __shared__ __attribute__((aligned(16))) float As[NS * TA::SIZE];   // NS stages of A
@@ -209,7 +229,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint32_t b, const E
   const float* B = d.B + z0 * d.sBz0 + z1 * d.sBz1;
   const int64_t kbeg = split * g.k_per_split;
   const int64_t kend = min(d.K, kbeg + g.k_per_split);
-  const int nst = kbeg < kend ? (int)((kend - kbeg) / BK) : 0;
+  const int nst = kbeg < kend ? (int)((kend - kbeg + (KT ? BK - 1 : 0)) / BK) : 0;
+  const int ktail = KT && nst > 0 ? (int)(kend - kbeg - (int64_t)(nst - 1) * BK) : BK;   // k of the last stage
   // Operand bases of stage 0 and the per-stage advance, all wave-uniform.
   const float* a0 = A + m0 * (AK ? d.sAm : 1) + kbeg * (AK ? 1 : d.sAk);
   const float* b0 = B + n0 * (BKF ? d.sBn : 1) + kbeg * (BKF ? 1 : d.sBk);
@@ -217,11 +238,21 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint32_t b, const E
   uint32_t offa[TA::PER], offb[TB::PER];
   TA::offsets(d.sAm, d.sAk, m0, d.M, gtid, offa);
   TB::offsets(d.sBn, d.sBk, n0, d.N, gtid, offb);
+  uint32_t offat[KT ? TA::PER : 1], offbt[KT ? TB::PER : 1];   // the partial last stage
+  if (KT) {
+    TA::offsets(d.sAm, d.sAk, m0, d.M, gtid, offat, ktail);
+    TB::offsets(d.sBn, d.sBk, n0, d.N, gtid, offbt, ktail);
+  }
   const int wv = __builtin_amdgcn_readfirstlane(wave);
   const uint32_t lds_a = (uint32_t)(unsigned long)((__attribute__((address_space(3))) float*)As);
   const uint32_t lds_b = (uint32_t)(unsigned long)((__attribute__((address_space(3))) float*)Bs);
   auto issue = [&](int st) {
     const int slot = st % NS;
+    if (KT && st == nst - 1 && ktail < BK) {
+      TA::dma(a0 + st * a_step, offat, lds_a + slot * TA::SIZE * 4, wv);
+      TB::dma(b0 + st * b_step, offbt, lds_b + slot * TB::SIZE * 4, wv);
+      return;
+    }
     TA::dma(a0 + st * a_step, offa, lds_a + slot * TA::SIZE * 4, wv);
     TB::dma(b0 + st * b_step, offb, lds_b + slot * TB::SIZE * 4, wv);
   };
@@ -258,6 +289,15 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint32_t b, const E
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
+    if (KT && ktail < BK && it == (nst - 1) / KG) {
+      // The partial last stage has landed (every wave waited for its own copies before the
+      // barrier): the whole block zeroes its k >= ktail entries, then meets again. The
+      // condition is the same in every thread.
+      const int ts = (nst - 1) % NS;
+      TA::zero_tail(As + ts * TA::SIZE, ktail, tid, NT);
+      TB::zero_tail(Bs + ts * TB::SIZE, ktail, tid, NT);
+      __syncthreads();
+    }
     if (st >= nst) continue;              // the other group's last stage (odd count)
     if (st + (NSG - 1) * KG < nst) issue(st + (NSG - 1) * KG);
     const float* Ac = As + (st % NS) * TA::SIZE;

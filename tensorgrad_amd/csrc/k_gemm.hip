@@ -239,9 +239,10 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g) {
 
 // ---- direct-to-LDS pipeline (gemm_dev.h) ----------------------------------------------
 
-template <int BM, int BN, int BK, int NS, bool AK, bool BKF, int NT, int KG, bool BDW = false>
+template <int BM, int BN, int BK, int NS, bool AK, bool BKF, int NT, int KG, bool BDW = false, bool ADW = false,
+          bool KT = false>
 __global__ __launch_bounds__(NT) void k_gemm_dma(GemmArgs g) {
-  gemm_tile<BM, BN, BK, NS, AK, BKF, NT, KG, StoreC, BDW>(g, xcd_order(blockIdx.x, gridDim.x), StoreC{});
+  gemm_tile<BM, BN, BK, NS, AK, BKF, NT, KG, StoreC, BDW, ADW, KT>(g, xcd_order(blockIdx.x, gridDim.x), StoreC{});
 }
 
 // Several independent problems in one launch: problem p owns tile numbers
@@ -349,6 +350,25 @@ bool dma_bdw_ok(const GemmDesc& d, const Plan& p, bool ak, bool bk) {
   return true;
 }
 
+// TG_GEMM_GEN=0 in the environment sends these GEMMs to the register-staged kernel instead.
+bool use_gen_dma() {
+  static const bool on = !(std::getenv("TG_GEMM_GEN") && std::string(std::getenv("TG_GEMM_GEN")) == "0");
+  return on;
+}
+
+// Any other GEMM whose operands each have a unit stride along k or along their rows: both
+// operands move one 4-byte element per lane (no alignment needed) and the last stage of
+// a split may be partial (K = 63, 319, ...): the direct-to-LDS pipeline with DW operands
+// and the KT tail, on 128 x 128 tiles or 64 x 64 tiles with two k groups.
+bool dma_gen_ok(const GemmDesc& d, bool ak, bool bk) {
+  if (!ak && d.sAm != 1) return false;
+  if (!bk && d.sBn != 1) return false;
+  const int64_t span = 128;
+  if ((ak ? d.sAm : d.sAk) * span * 4 >= (int64_t(1) << 31)) return false;
+  if ((bk ? d.sBn : d.sBk) * span * 4 >= (int64_t(1) << 31)) return false;
+  return true;
+}
+
 }  // namespace
 
 int64_t gemm_workspace_floats(const GemmDesc& d) {
@@ -391,6 +411,25 @@ void gemm(const GemmDesc& d, float* work, hipStream_t st) {
     else if (ak) k_gemm_dma<64, 64, 64, 4, true, false, 512, 2, true><<<grid, 512, 0, st>>>(g);
     else if (bk) k_gemm_dma<64, 64, 64, 4, false, true, 512, 2, true><<<grid, 512, 0, st>>>(g);
     else k_gemm_dma<64, 64, 64, 4, false, false, 512, 2, true><<<grid, 512, 0, st>>>(g);
+  } else if (use_gen_dma() && dma_gen_ok(d, ak, bk)) {
+    // 128 x 128 tiles when the plan chose them, else 64 x 64 with 32-k stages (the plan's
+    // k per split is a multiple of 32 either way)
+    const int bt = p.bm == 128 && p.bn == 128 ? 128 : 64;
+    g.tiles_n = (int)((d.N + bt - 1) / bt);
+    g.tiles_m = (int)((d.M + bt - 1) / bt);
+    const int64_t gb = (int64_t)g.tiles_n * g.tiles_m * d.batch * p.splits;
+    if (gb >= (int64_t(1) << 31)) throw std::runtime_error("gemm: too many tiles");
+    const dim3 grid((unsigned)gb);
+#define TG_GEN_LAUNCH(BM_, NS_, KG_)                                                                          \
+  do {                                                                                                        \
+    if (ak && bk) k_gemm_dma<BM_, BM_, 32, NS_, true, true, 512, KG_, true, true, true><<<grid, 512, 0, st>>>(g);   \
+    else if (ak) k_gemm_dma<BM_, BM_, 32, NS_, true, false, 512, KG_, true, true, true><<<grid, 512, 0, st>>>(g);   \
+    else if (bk) k_gemm_dma<BM_, BM_, 32, NS_, false, true, 512, KG_, true, true, true><<<grid, 512, 0, st>>>(g);   \
+    else k_gemm_dma<BM_, BM_, 32, NS_, false, false, 512, KG_, true, true, true><<<grid, 512, 0, st>>>(g);          \
+  } while (0)
+    if (bt == 128) TG_GEN_LAUNCH(128, 3, 1);
+    else TG_GEN_LAUNCH(64, 4, 2);
+#undef TG_GEN_LAUNCH
   } else {
 #define TG_GEMM_LAUNCH(BM_, BN_, BK_)                                                      \
   do {                                                                                     \

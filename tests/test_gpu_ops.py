@@ -504,7 +504,13 @@ GEMMS = [([5, 7], [7, 3], False, False), ([2, 33, 65], [65, 17], False, False), 
          # rows of B not 16-byte aligned (65 / 67 wide): the direct-to-LDS tile moving B one
          # element per lane, a partial last column tile, and split-K for a long K
          ([4096, 256], [256, 65], False, False), ([4096, 256], [4096, 65], True, False),
-         ([200, 128], [128, 67], False, False)]
+         ([200, 128], [128, 67], False, False),
+         # neither operand 16-byte aligned and K not a multiple of 32 (C4's 63- and 319-wide
+         # inputs): both operands one element per lane, a partial last k stage zeroed in LDS
+         ([1000, 63], [63, 256], False, False), ([700, 319], [319, 256], False, False),
+         ([2000, 319], [2000, 256], True, False), ([4096, 4], [4, 256], False, False),
+         ([9000, 63], [9000, 64], True, False), ([3, 33, 17], [17, 9], False, False),
+         ([130, 45], [70, 45], False, True), ([8192, 319], [319, 512], False, False)]
 
 
 @pytest.mark.parametrize('case', GEMMS)
