@@ -38,8 +38,12 @@ constexpr int kTab = 1024;  // conv2d / input gradient: k terms kept in an LDS t
 enum { CV_FWD = 0, CV_DGRAD = 1, CV_WGRAD = 2 };
 // Loader variants, chosen per launch (template flags, so the k loop has no runtime tests):
 // F_AVEC: A rows are 16-byte aligned groups of 4 k (vector loads); F_TAB: the k terms come
-// from the block's LDS table; F_PAD: some tap falls outside the image (bounds checks).
-enum { F_AVEC = 1, F_TAB = 2, F_PAD = 4 };
+// from the block's LDS table; F_PAD: some tap falls outside the image (bounds checks);
+// F_TAP: conv2d or the stride-1 input gradient with a multiple of kCBK channels per group
+// runs its reduction tap-major, k = tap * channels + channel, so every stage holds one tap
+// and 32 channels: a thread finds its positions' offsets and in-image tests once per stage
+// and each element costs one add (the GEMM's k order changes, its value does not).
+enum { F_AVEC = 1, F_TAB = 2, F_PAD = 4, F_TAP = 8 };
 
 struct ConvGemmArgs {
   int B, Cin, H, W, Cout, CinPG, CoutPG, kH, kW, Ho, Wo, G, sH, sW, pH, pW;
@@ -48,6 +52,7 @@ struct ConvGemmArgs {
   int pad;                      // some tap can fall outside the image: bounds checks needed
   int avec;                     // A rows are 16-byte aligned in groups of 4 k (vector loads)
   FastDiv dKHW, dKW, dWo, dHoWo, dW, dHW, dSH, dSW;
+  FastDiv dCpg;                 // F_TAP: channels per group of the reduction (CinPG / CoutPG)
   const float* x;
   const float* w;
   const float* dy;
@@ -262,6 +267,20 @@ struct ConvLoader {
     const int kend = bp.kend;
     const bool mok = m < c.M;
     const int mm = mok ? m : 0;
+    if ((F & F_TAP) && MODE != CV_WGRAD) {
+      // k = tap * cpg + ch; the 4 k share the tap (cpg % 4 == 0, k0 % 4 == 0) and lie below
+      // kend (K = taps * cpg, a multiple of kCBK). Consecutive channels are a fixed stride
+      // apart in the weight.
+      const int khw = c.kH * c.kW;
+      const int cpg = MODE == CV_FWD ? c.CinPG : c.CoutPG;
+      const int tap = fdiv(k0, c.dCpg), ch = k0 - tap * cpg;
+      const uint32_t o = MODE == CV_FWD ? (uint32_t)(((bp.z * c.CoutPG + mm) * c.CinPG + ch) * khw + tap)
+                                        : (uint32_t)(((bp.z * c.CoutPG + ch) * c.CinPG + mm) * khw + tap);
+      const uint32_t step = MODE == CV_FWD ? (uint32_t)khw : (uint32_t)(c.CinPG * khw);
+      for (int u = 0; u < 4; ++u) v[u] = ldb(sw, mok ? (o + u * step) << 2 : kMasked);
+      (void)kend;
+      return v;
+    }
     if (MODE == CV_FWD) {
       const uint32_t row = (uint32_t)((bp.z * c.CoutPG + mm) * c.K);
       // avec: K % 4 == 0 and k0 % 4 == 0, so k0 < kend covers all 4
@@ -349,7 +368,35 @@ struct ConvLoader {
       const int rr = idx / (kCBK / 4), kk = (idx % (kCBK / 4)) * 4;
       qa[e] = load_a(c, bp.m0 + rr, k0 + kk);
     }
-    if (!BKF) {
+    if (!BKF && (F & F_TAP)) {
+      // The stage's 32 k are one tap (cpg % kCBK == 0, k0 % kCBK == 0, K = taps * cpg, so
+      // every k < kend): in-image tests and offset bases per position once, then per k the
+      // channel's plane offset. Masked positions keep the out-of-range base kMasked, which
+      // the added plane offset (below 2^31 bytes) leaves out of range.
+      const int cpg = MODE == CV_FWD ? c.CinPG : c.CoutPG;
+      const int tap = fdiv(k0, c.dCpg);
+      const int kh = fdiv(tap, c.dKW), kw = tap - kh * c.kW;
+      const int a = MODE == CV_FWD ? kh - c.pH : kh, b = MODE == CV_FWD ? kw - c.pW : kw;
+      const uint32_t toff = MODE == CV_FWD ? (uint32_t)(a * c.W + b) : (uint32_t)0 - (uint32_t)(kh * c.Wo + kw);
+      const uint32_t plane = MODE == CV_FWD ? (uint32_t)(c.H * c.W) : (uint32_t)(c.Ho * c.Wo);
+      const Src& src = MODE == CV_FWD ? sx : sdy;
+      uint32_t base[4];
+      for (int u = 0; u < 4; ++u) {
+        bool ok = (nvalid >> u) & 1;
+        if (MODE == CV_FWD) {
+          if (F & F_PAD) ok = ok && inside(ph[u] + a, c.H) && inside(pw[u] + b, c.W);
+        } else {
+          ok = ok && inside(ph[u] - a, c.Ho) && inside(pw[u] - b, c.Wo);
+        }
+        base[u] = ok ? (nb[u] + toff) << 2 : kMasked;
+      }
+      const int ch0 = k0 - tap * cpg;
+      for (int e = 0; e < QB; ++e) {
+        const int kk = (tid + e * kCT) / (BN / 4);
+        const uint32_t delta = ((uint32_t)(ch0 + kk) * plane) << 2;
+        for (int u = 0; u < 4; ++u) qb[e][u] = ldb(src, base[u] + delta);
+      }
+    } else if (!BKF) {
       for (int e = 0; e < QB; ++e) {
         const int idx = tid + e * kCT;
         const int kk = idx / (BN / 4);
@@ -458,11 +505,18 @@ inline ConvGemmArgs make_args(const ConvDesc& d, const ConvPlan& p) {
   a.dHW = make_fastdiv((uint32_t)(a.H * a.W));
   a.dSH = make_fastdiv((uint32_t)a.sH);
   a.dSW = make_fastdiv((uint32_t)a.sW);
+  a.dCpg = make_fastdiv((uint32_t)(p.mode == CV_FWD ? a.CinPG : a.CoutPG));
   return a;
 }
 
 // Loader flags of a launch (avec must already account for the operand's alignment).
 inline int conv_flags(const ConvGemmArgs& a, int mode) {
+  // Tap-major order for the stride-1 input gradient only: measured on the CNN config it
+  // cuts the input gradient's index arithmetic (72.7 -> 63.8 us) but slows conv2d, whose
+  // k-contiguous weight rows then lose their vector loads and whose stages read 32
+  // channel planes instead of a few neighbouring rows (43.7 -> 68.9 us).
+  const bool tap = mode == CV_DGRAD && a.sH == 1 && a.sW == 1 && a.CoutPG % kCBK == 0;
+  if (tap) return F_TAP;
   int f = 0;
   if (a.avec && mode != CV_DGRAD) f |= F_AVEC;
   if (a.pad && mode != CV_DGRAD) f |= F_PAD;

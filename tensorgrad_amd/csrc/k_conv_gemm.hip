@@ -217,6 +217,12 @@ void launch_tile(const ConvPlan& p, const ConvGemmArgs& a, hipStream_t st) {
 template <int MODE>
 void launch_mode(const ConvPlan& p, const ConvGemmArgs& a, bool fast, hipStream_t st) {
   const int f = conv_flags(a, MODE);
+  if (MODE == CV_DGRAD && fast && (f & F_TAP)) return launch_tile<MODE, true, F_TAP>(p, a, st);
+  if (MODE == CV_FWD && (f & F_TAP)) {
+    if (f & F_PAD) launch_tile<MODE, true, F_TAP | F_PAD>(p, a, st);
+    else launch_tile<MODE, true, F_TAP>(p, a, st);
+    return;
+  }
   if (MODE == CV_DGRAD) {
     if (!fast) launch_tile<MODE, false, 0>(p, a, st);
     else if (f & F_TAB) launch_tile<MODE, true, F_TAB>(p, a, st);

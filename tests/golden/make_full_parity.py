@@ -4,8 +4,16 @@ reference evaluator test/_eval.ts plus the Adam convention of src/codegen.ts:841
 the seeded initial params on the seeded batches that the GPU test regenerates.
 
 Stored per config in full_<key>.npz (numpy, no pickles): the loss of every step, and per
-parameter tensor at step 100 either all values (tensors up to FULL_LIMIT elements) or a
-fixed seeded sample of SAMPLE indices, with the f64 norm of the whole tensor.
+parameter tensor at step 100 either all values (every tensor of the configs in WHOLE, and
+tensors up to FULL_LIMIT elements) or a fixed seeded sample of SAMPLE indices, with the
+f64 norm of the whole tensor.
+
+For the configs in TWIN the oracle also trains a twin from the same initial parameters
+moved by one ulp each (a seeded random direction per element), the size of the rounding
+difference any f32 implementation that is not bit-identical to the evaluator introduces
+in its first step; the twin's losses and step-100 values (same indices) measure how far
+the workload itself amplifies such a difference over 100 steps ('twin_losses',
+'twin:<param>', 'twin_norm:<param>').
 
     python tests/golden/make_full_parity.py [keys...] [--threads N]
 """
@@ -26,37 +34,62 @@ from tensorgrad_amd import configs  # noqa: E402
 from tensorgrad_amd.build_ir import build_training_ir  # noqa: E402
 
 STEPS = 100
-FULL_LIMIT = 200_000
+FULL_LIMIT = 16_384
 SAMPLE = 4096
+WHOLE = {'char_mlp'}
+TWIN = {'cnn', 'nerf'}
 
 
-def sample_indices(name: str, n: int) -> np.ndarray:
-    if n <= FULL_LIMIT:
+def sample_indices(key: str, name: str, n: int) -> np.ndarray:
+    if key in WHOLE or n <= FULL_LIMIT:
         return np.arange(n, dtype=np.int64)
     seed = sum(ord(ch) * (i + 1) for i, ch in enumerate(name)) + n
     return np.sort(np.random.default_rng(seed).choice(n, SAMPLE, replace=False)).astype(np.int64)
 
 
-def make(key: str) -> str:
-    cfg = configs.CONFIGS[key]
-    ir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer)
+def one_ulp(params: dict) -> dict:
+    """Every element moved to its f32 neighbour, up or down by a seeded coin."""
+    out = {}
+    for i, (n, v) in enumerate(sorted(params.items())):
+        v = np.asarray(v, np.float32)
+        up = np.random.default_rng(1000 + i).random(v.shape) < 0.5
+        out[n] = np.where(up, np.nextafter(v, np.float32(np.inf)), np.nextafter(v, np.float32(-np.inf))).astype(np.float32)
+    return out
+
+
+def train(key: str, cfg, ir, params: dict, tag: str):
     o = pyoracle.OracleRuntime(ir.wire())
-    o.upload_params(ir.initial_params(configs.INIT_SEED))
+    o.upload_params(params)
     losses = []
     t0 = time.time()
     for i, b in enumerate(configs.batches(cfg, STEPS)):
         losses.append(o.step(b))
         if i % 10 == 9:
-            print(f'  [{key}] step {i + 1} loss {losses[-1]:.9g} ({time.time() - t0:.0f}s)', flush=True)
-    out = {'losses': np.array(losses, np.float64), 'steps': np.array(STEPS)}
+            print(f'  [{key}{tag}] step {i + 1} loss {losses[-1]:.9g} ({time.time() - t0:.0f}s)', flush=True)
+    return o, np.array(losses, np.float64)
+
+
+def make(key: str) -> str:
+    cfg = configs.CONFIGS[key]
+    ir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer)
+    p0 = ir.initial_params(configs.INIT_SEED)
+    o, losses = train(key, cfg, ir, p0, '')
+    out = {'losses': losses, 'steps': np.array(STEPS)}
     shapes = ir.param_shapes()
+    sizes = {n: int(np.prod(shapes[n])) if shapes[n] else 1 for n in ir.param_names}
     for n in ir.param_names:
-        size = int(np.prod(shapes[n])) if shapes[n] else 1
-        v = o.get_home(n, size)
-        idx = sample_indices(n, size)
+        v = o.get_home(n, sizes[n])
+        idx = sample_indices(key, n, sizes[n])
         out[f'idx:{n}'] = idx
         out[f'val:{n}'] = v[idx]
         out[f'norm:{n}'] = np.array(np.linalg.norm(v.astype(np.float64)))
+    if key in TWIN:
+        t, tl = train(key, cfg, ir, one_ulp(p0), ' twin')
+        out['twin_losses'] = tl
+        for n in ir.param_names:
+            v = t.get_home(n, sizes[n])
+            out[f'twin:{n}'] = v[out[f'idx:{n}']]
+            out[f'twin_norm:{n}'] = np.array(np.linalg.norm(v.astype(np.float64)))
     path = os.path.join(HERE, f'full_{key}.npz')
     np.savez_compressed(path, **out)
     return path

@@ -146,28 +146,98 @@ def test_small_variant_100_steps(key):
     assert wl <= LOSS_TOL and wp <= PARAM_TOL
 
 
-@pytest.mark.parametrize('key,steps', [('mlp_sin', 100), ('char_mlp', 10), ('cnn', 3), ('transformer', 2), ('nerf', 1)])
-def test_full_config_parity(key, steps):
-    """Full-size configs with their own optimizer, for as many steps as the oracle affords.
-
-    Adam's first updates are lr * g / (|g| + eps), about lr * sign(g): a gradient entry
-    whose exact value lies inside the f32 rounding noise of its GEMM (the GPU accumulates
-    in f32, the evaluator in f64) can move either way by lr. One such entry among the cnn's
-    1.2M fc weights moves that tensor's relative error by ~2e-4 after 3 steps, so after a
-    few steps at full size those elements (|diff| >= lr / 4; ordinary differences are
-    ~1e-7) are counted, bounded, and left out of the 1e-4 parameter bar. The reduced
-    variants above apply the bar to every element after 100 steps, and
-    test_full_config_gradients checks the full-size gradients directly."""
-    pyoracle.set_threads(16)
-    t0 = time.time()
-    cfg = configs.CONFIGS[key]
-    lr = cfg.optimizer['lr']
-    wl, wp, flips = _train_both(cfg, steps, flip_step=None if steps >= 100 else lr)
-    print(f'  [{key}] {time.time() - t0:.1f}s', flush=True)
+def test_full_mlp_sin_100_steps_live():
+    """C1 at full size against the oracle run live, 100 steps, every element."""
+    wl, wp, _ = _train_both(configs.CONFIGS['mlp_sin'], 100)
     assert wl <= LOSS_TOL and wp <= PARAM_TOL
-    n_params = sum(int(np.prod(s)) for s in build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs,
-                                                                cfg.optimizer).param_shapes().values())
-    assert flips <= max(4, 1e-5 * n_params * steps)
+
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), 'golden')
+
+
+TWIN_FACTOR = 4.0
+
+
+@pytest.mark.parametrize('key', ['char_mlp', 'cnn', 'transformer', 'nerf'])
+def test_full_config_100_steps(key):
+    """Full-size configs for 100 optimizer steps against the oracle's own 100-step run
+    (tests/golden/make_full_parity.py: every step's loss, and at step 100 each parameter
+    tensor whole or a fixed seeded sample of 4096 elements, plus the whole tensor's norm).
+
+    Bar: every step's loss within 1e-4 relative; every tensor's values (whole or sampled)
+    within 1e-4 relative (L2) and its norm within 1e-4, after setting aside the elements
+    whose difference is that of Adam updates gone opposite ways (sign_ambiguous: at least
+    lr/4 and at most 2.5 * lr * 100). Those are printed, counted and bounded.
+
+    Where the fixture also holds the oracle's one-ulp twin (the evaluator trained again
+    from initial parameters one ulp away), the workload's own amplification of a
+    rounding-sized difference is known. A step or tensor at which the twin itself lies
+    beyond the bar is held to TWIN_FACTOR times the twin's distance instead (a step's loss:
+    the twin's worst distance up to that step; a tensor's values: the twin's distance
+    measured the same way; its norm: the larger of the twin's norm and value distances),
+    and the sign-ambiguous count to TWIN_FACTOR times the twin's."""
+    path = os.path.join(GOLDEN, f'full_{key}.npz')
+    g = np.load(path, allow_pickle=False)
+    twin = 'twin_losses' in g.files
+    cfg = configs.CONFIGS[key]
+    steps = int(g['steps'])
+    lr = cfg.optimizer['lr']
+    ir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer)
+    rt = backend.NativeRuntime(ir.wire_json())
+    rt.upload_params(ir.initial_params(configs.INIT_SEED))
+    t0 = time.time()
+    want_l = g['losses']
+    loss_bar = np.full(steps, LOSS_TOL)
+    if twin:
+        terr = np.abs(g['twin_losses'] - want_l) / np.abs(want_l)
+        loss_bar = np.maximum(loss_bar, TWIN_FACTOR * np.maximum.accumulate(terr))
+    worst_loss, worst_excess = 0.0, 0.0
+    for i, b in enumerate(configs.batches(cfg, steps)):
+        e = rel_err(rt.step(b), want_l[i], f'[{key}] step {i + 1} loss')
+        worst_loss = max(worst_loss, e)
+        worst_excess = max(worst_excess, e / loss_bar[i])
+    pg = rt.download_params()
+    rt.destroy()
+    flips, tflips, checked, fails = 0, 0, 0, []
+    worst, worst_name, worst_norm = 0.0, '', 0.0
+    for n in ir.param_names:
+        idx, want = g[f'idx:{n}'], g[f'val:{n}'].astype(np.float64)
+        got = pg[n].astype(np.float64)
+        diff = got[idx] - want
+        if not np.all(np.isfinite(diff)):
+            raise AssertionError(f'[{key}] {n}: non-finite parameters')
+        amb = sign_ambiguous(diff, lr, steps)
+        flips += int(amb.sum())
+        checked += idx.size
+        e = rel_err(want + np.where(amb, 0.0, diff), want, f'[{key}] {n}')
+        en = rel_err(np.linalg.norm(got), float(g[f'norm:{n}']), f'[{key}] {n} norm')
+        bar, nbar, note = PARAM_TOL, PARAM_TOL, ''
+        if twin:
+            tdiff = g[f'twin:{n}'].astype(np.float64) - want
+            tamb = sign_ambiguous(tdiff, lr, steps)
+            tflips += int(tamb.sum())
+            te = rel_err(want + np.where(tamb, 0.0, tdiff), want, f'[{key}] {n} twin')
+            tn = rel_err(float(g[f'twin_norm:{n}']), float(g[f'norm:{n}']), f'[{key}] {n} twin norm')
+            # |norm(a) - norm(b)| <= norm(a - b): a tensor's norm moves at most as far as its
+            # values, so the twin's value distance bounds the norm too (its own norm distance,
+            # one scalar, can cancel by chance)
+            bar, nbar = max(bar, TWIN_FACTOR * te), max(nbar, TWIN_FACTOR * max(tn, te))
+            note = f', twin {te:.2e} (norm {tn:.2e}, {int(tamb.sum())} sign-ambiguous)'
+        if amb.any() or e > PARAM_TOL:
+            print(f'  [{key}] {n}: rel {e:.2e}, norm {en:.2e}, {int(amb.sum())} sign-ambiguous of {idx.size}'
+                  + (f' (max |diff| {np.abs(diff[amb]).max():.2e})' if amb.any() else '') + note, flush=True)
+        if e > bar or en > nbar:
+            fails.append(n)
+        if e > worst:
+            worst, worst_name = e, n
+        worst_norm = max(worst_norm, en)
+    print(f'  [{key}] {steps} steps in {time.time() - t0:.1f}s: worst loss rel {worst_loss:.2e} '
+          f'({worst_excess:.2f} of its bar), worst param rel {worst:.2e} ({worst_name}), worst norm rel '
+          f'{worst_norm:.2e}, {flips} sign-ambiguous of {checked}' + (f' (twin: {tflips})' if twin else ''),
+          flush=True)
+    assert worst_excess <= 1.0
+    assert not fails, fails
+    assert flips <= max(4, 1e-3 * checked, TWIN_FACTOR * tflips)
 
 
 @pytest.mark.parametrize('key', ['char_mlp', 'cnn', 'transformer', 'nerf'])
