@@ -383,6 +383,7 @@ class Runtime {
   int fld(int op, const char* f) const { return O(op).at(f).i32(); }
 
   void analyse();
+  void relu_grads_from_outputs();
   void compute_views();
   void lower();
   void allocate();
@@ -510,6 +511,7 @@ Runtime::Runtime(const char* json, Runtime* par, bool plan_only) : parent(par) {
 
   plan_only_ = plan_only;
   analyse();
+  relu_grads_from_outputs();
   compute_views();
   lower();
   if (!plan_only) hip_check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate");
@@ -591,6 +593,29 @@ void Runtime::analyse() {
     } else if (k == "state_input") {
       state_tid_[ops_[i]->at("name").str()] = out;
     }
+  }
+}
+
+// relu_grad(x, dy) = x > 0 ? dy : 0 reads the pre-activation x. Where relu(x) is also
+// computed, relu(x) > 0 exactly when x > 0 (NaN and -0 included: relu maps them to values
+// that are not > 0), so the gradient reads the relu output instead: the output is kept
+// for the next layer anyway, and the pre-activation then need not be stored at all (an
+// add + relu group writes one [rows, width] tensor instead of two). The IR document is
+// rewritten in place; every value stays bit-identical.
+void Runtime::relu_grads_from_outputs() {
+  for (size_t i = 0; i < ops_.size(); ++i) {
+    if (kinds_[i] != "relu_grad") continue;
+    const int x = fld((int)i, "x");
+    if (T_[x].dt != F32) continue;
+    int r = -1;
+    for (int c : consumers_[x])
+      if (c < (int)i && kinds_[c] == "relu" && fld(c, "a") == x) { r = O(c).at("out").i32(); break; }
+    if (r < 0 || T_[r].shape != T_[x].shape || T_[r].dt != F32) continue;
+    const_cast<tgj::Value&>(ops_[i]->at("x")).number = (double)r;
+    auto& cx = consumers_[x];
+    cx.erase(std::find(cx.begin(), cx.end(), (int)i));
+    consumers_[r].push_back((int)i);
+    std::sort(consumers_[r].begin(), consumers_[r].end());
   }
 }
 
