@@ -8,12 +8,13 @@ parameter tensor at step 100 either all values (every tensor of the configs in W
 tensors up to FULL_LIMIT elements) or a fixed seeded sample of SAMPLE indices, with the
 f64 norm of the whole tensor.
 
-For the configs in TWIN the oracle also trains a twin from the same initial parameters
-moved by one ulp each (a seeded random direction per element), the size of the rounding
-difference any f32 implementation that is not bit-identical to the evaluator introduces
-in its first step; the twin's losses and step-100 values (same indices) measure how far
-the workload itself amplifies such a difference over 100 steps ('twin_losses',
-'twin:<param>', 'twin_norm:<param>').
+For the configs in TWIN the oracle also trains NTWIN twins from the same initial
+parameters moved by one ulp each (a seeded random direction per element, different per
+twin), the size of the rounding difference any f32 implementation that is not
+bit-identical to the evaluator introduces in its first step; the twins' losses and
+step-100 values (same indices) measure how far the workload itself amplifies such a
+difference over 100 steps ('twin_losses' [NTWIN, steps], 'twin:<param>' [NTWIN, sample],
+'twin_norm:<param>' [NTWIN]).
 
     python tests/golden/make_full_parity.py [keys...] [--threads N]
 """
@@ -38,6 +39,7 @@ FULL_LIMIT = 16_384
 SAMPLE = 4096
 WHOLE = {'char_mlp'}
 TWIN = {'cnn', 'nerf'}
+NTWIN = 2
 
 
 def sample_indices(key: str, name: str, n: int) -> np.ndarray:
@@ -47,12 +49,12 @@ def sample_indices(key: str, name: str, n: int) -> np.ndarray:
     return np.sort(np.random.default_rng(seed).choice(n, SAMPLE, replace=False)).astype(np.int64)
 
 
-def one_ulp(params: dict) -> dict:
+def one_ulp(params: dict, twin: int = 0) -> dict:
     """Every element moved to its f32 neighbour, up or down by a seeded coin."""
     out = {}
     for i, (n, v) in enumerate(sorted(params.items())):
         v = np.asarray(v, np.float32)
-        up = np.random.default_rng(1000 + i).random(v.shape) < 0.5
+        up = np.random.default_rng(1000 * (twin + 1) + i).random(v.shape) < 0.5
         out[n] = np.where(up, np.nextafter(v, np.float32(np.inf)), np.nextafter(v, np.float32(-np.inf))).astype(np.float32)
     return out
 
@@ -84,12 +86,12 @@ def make(key: str) -> str:
         out[f'val:{n}'] = v[idx]
         out[f'norm:{n}'] = np.array(np.linalg.norm(v.astype(np.float64)))
     if key in TWIN:
-        t, tl = train(key, cfg, ir, one_ulp(p0), ' twin')
-        out['twin_losses'] = tl
+        runs = [train(key, cfg, ir, one_ulp(p0, j), f' twin {j}') for j in range(NTWIN)]
+        out['twin_losses'] = np.stack([tl for _, tl in runs])
         for n in ir.param_names:
-            v = t.get_home(n, sizes[n])
-            out[f'twin:{n}'] = v[out[f'idx:{n}']]
-            out[f'twin_norm:{n}'] = np.array(np.linalg.norm(v.astype(np.float64)))
+            vs = [t.get_home(n, sizes[n]) for t, _ in runs]
+            out[f'twin:{n}'] = np.stack([v[out[f'idx:{n}']] for v in vs])
+            out[f'twin_norm:{n}'] = np.array([np.linalg.norm(v.astype(np.float64)) for v in vs])
     path = os.path.join(HERE, f'full_{key}.npz')
     np.savez_compressed(path, **out)
     return path

@@ -169,13 +169,15 @@ def test_full_config_100_steps(key):
     whose difference is that of Adam updates gone opposite ways (sign_ambiguous: at least
     lr/4 and at most 2.5 * lr * 100). Those are printed, counted and bounded.
 
-    Where the fixture also holds the oracle's one-ulp twin (the evaluator trained again
-    from initial parameters one ulp away), the workload's own amplification of a
-    rounding-sized difference is known. A step or tensor at which the twin itself lies
-    beyond the bar is held to TWIN_FACTOR times the twin's distance instead (a step's loss:
-    the twin's worst distance up to that step; a tensor's values: the twin's distance
-    measured the same way; its norm: the larger of the twin's norm and value distances),
-    and the sign-ambiguous count to TWIN_FACTOR times the twin's."""
+    Where the fixture also holds the oracle's one-ulp twins (the evaluator trained again
+    from initial parameters one ulp away, in two seeded directions), the workload's own
+    amplification of a rounding-sized difference is known. A step or tensor at which the
+    twins themselves lie beyond the bar is held to TWIN_FACTOR times the farther twin's
+    distance instead (a step's loss: the twins' worst distance up to that step; a tensor's
+    values: the twins' distance measured the same way; its norm: the larger of the twins'
+    norm and value distances), and the sign-ambiguous count to TWIN_FACTOR times the
+    twins' larger count. A twin differs from the evaluator once, at its start; the GPU's
+    rounding differs in every one of the 100 steps, hence a factor above 1."""
     path = os.path.join(GOLDEN, f'full_{key}.npz')
     g = np.load(path, allow_pickle=False)
     twin = 'twin_losses' in g.files
@@ -189,7 +191,7 @@ def test_full_config_100_steps(key):
     want_l = g['losses']
     loss_bar = np.full(steps, LOSS_TOL)
     if twin:
-        terr = np.abs(g['twin_losses'] - want_l) / np.abs(want_l)
+        terr = (np.abs(np.atleast_2d(g['twin_losses']) - want_l) / np.abs(want_l)).max(0)
         loss_bar = np.maximum(loss_bar, TWIN_FACTOR * np.maximum.accumulate(terr))
     worst_loss, worst_excess = 0.0, 0.0
     for i, b in enumerate(configs.batches(cfg, steps)):
@@ -213,16 +215,20 @@ def test_full_config_100_steps(key):
         en = rel_err(np.linalg.norm(got), float(g[f'norm:{n}']), f'[{key}] {n} norm')
         bar, nbar, note = PARAM_TOL, PARAM_TOL, ''
         if twin:
-            tdiff = g[f'twin:{n}'].astype(np.float64) - want
-            tamb = sign_ambiguous(tdiff, lr, steps)
-            tflips += int(tamb.sum())
-            te = rel_err(want + np.where(tamb, 0.0, tdiff), want, f'[{key}] {n} twin')
-            tn = rel_err(float(g[f'twin_norm:{n}']), float(g[f'norm:{n}']), f'[{key}] {n} twin norm')
+            te, tn, ta = 0.0, 0.0, 0
+            for j, tv in enumerate(np.atleast_2d(g[f'twin:{n}'])):
+                tdiff = tv.astype(np.float64) - want
+                tamb = sign_ambiguous(tdiff, lr, steps)
+                ta = max(ta, int(tamb.sum()))
+                te = max(te, rel_err(want + np.where(tamb, 0.0, tdiff), want, f'[{key}] {n} twin {j}'))
+                tn = max(tn, rel_err(float(np.atleast_1d(g[f'twin_norm:{n}'])[j]), float(g[f'norm:{n}']),
+                                     f'[{key}] {n} twin {j} norm'))
+            tflips += ta
             # |norm(a) - norm(b)| <= norm(a - b): a tensor's norm moves at most as far as its
             # values, so the twin's value distance bounds the norm too (its own norm distance,
             # one scalar, can cancel by chance)
             bar, nbar = max(bar, TWIN_FACTOR * te), max(nbar, TWIN_FACTOR * max(tn, te))
-            note = f', twin {te:.2e} (norm {tn:.2e}, {int(tamb.sum())} sign-ambiguous)'
+            note = f', twins {te:.2e} (norm {tn:.2e}, {ta} sign-ambiguous)'
         if amb.any() or e > PARAM_TOL:
             print(f'  [{key}] {n}: rel {e:.2e}, norm {en:.2e}, {int(amb.sum())} sign-ambiguous of {idx.size}'
                   + (f' (max |diff| {np.abs(diff[amb]).max():.2e})' if amb.any() else '') + note, flush=True)
