@@ -122,3 +122,27 @@ def test_parity_helpers_reject_non_finite_and_bound_the_exclusion():
     d = np.array([1e-7, lr / 4, 2 * lr, 2.5 * lr * steps, 2.5 * lr * steps * 1.01, 1.0])
     assert sign_ambiguous(d, lr, steps).tolist() == [False, True, True, True, False, False]
     assert sign_ambiguous(-d, lr, steps).tolist() == [False, True, True, True, False, False]
+
+
+def test_several_streams_are_rejected(monkeypatch):
+    """TG_STREAMS other than 1 is an error at runtime creation (the several-stream
+    schedule is removed), checked through the host-only lowering."""
+    cfg = configs.CONFIGS['mlp_sin']
+    ir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer)
+    monkeypatch.setenv('TG_STREAMS', '1')
+    backend.plan(ir.wire_json())
+    monkeypatch.setenv('TG_STREAMS', '2')
+    with pytest.raises(backend.BackendError, match='TG_STREAMS'):
+        backend.plan(ir.wire_json())
+
+
+def test_relu_grad_reads_the_relu_output():
+    """An add + relu layer whose backward takes relu_grad of the pre-activation stores only
+    the relu output: the gradient reads that instead (relu(x) > 0 exactly when x > 0)."""
+    cfg = configs.CONFIGS['nerf']
+    ir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer)
+    nodes = backend.plan(ir.wire_json())['nodes']
+    relu_groups = [n for n in nodes if n.get('ops') == 'add,relu']
+    assert relu_groups
+    for n in relu_groups:   # reads the product [65536,256] (bias aside), writes one tensor
+        assert n['bytes'] < 2.1 * 4 * 65536 * 256, n
