@@ -300,8 +300,9 @@ JitKernel gemm_epi_kernel(const FusedProgram& p, const FusedInstr* code, const G
   // The epilogue functor: element (gm, gn) of the product is element t = gm * N + gn of
   // the group's iteration space (the product is contiguous and read in that order).
   o << "namespace {\nstruct @NAME@_epi {\n  tgk::JitArgs A;\n  unsigned seed;\n";
-  o << "  __device__ __forceinline__ void operator()(const tgk::GemmDesc&, int64_t, int64_t, int64_t gm, int64_t gn, "
+  o << "  __device__ __forceinline__ void operator()(const tgk::GemmDesc& d, int64_t, int64_t, int64_t gm, int64_t gn, "
        "float value) const {\n";
+  if (c.store_c) o << I << "d.C[gm * d.sCm + gn * d.sCn] = value;\n";
   o << I << "const unsigned t = (unsigned)gm * " << ulit(c.N) << " + (unsigned)gn;\n";
   if (p.any_strided) emit_coords(o, p, "t", I);
   for (int k = 0; k < p.n_in; ++k) {

@@ -229,6 +229,7 @@ struct GemmEpiCfg {
   bool ak, bkf;
   int64_t N;
   int h_in;
+  bool store_c = false;   // the epilogue also stores the product itself to C
 };
 bool gemm_epi_cfg(const GemmDesc& d, GemmEpiCfg& c, gd::GemmArgs& g, int64_t& blocks);
 // True when d on its own would run one pass of 64 x 64 tiles (the grouped tiling); the

@@ -441,8 +441,8 @@ class Runtime {
   // after the matrix work instead of beside other work.
   bool use_gemm_epi_ = false;
   std::vector<char> group_done_;     // group already run inside a GEMM epilogue
-  int epi_group(int op, int out, const tgk::GemmDesc& d) const;
-  void lower_gemm_epi(int op, const tgk::GemmDesc& d, int a, int b, int out, int gi);
+  int epi_group(int op, int out, const tgk::GemmDesc& d, bool& store_c) const;
+  void lower_gemm_epi(int op, const tgk::GemmDesc& d, int a, int b, int out, int gi, bool store_c);
   // Column sums read only by the optimizer (bias, LayerNorm gain / shift gradients) run
   // together with the grouped GEMMs, kColSumMax per launch.
   std::vector<char> defer_colsum_;
@@ -2172,12 +2172,15 @@ void Runtime::plan_gemm_groups() {
       for (int i : cand[k]) defer_gemm_[i] = 1;
 }
 
-int Runtime::epi_group(int op, int out, const tgk::GemmDesc& d) const {
+int Runtime::epi_group(int op, int out, const tgk::GemmDesc& d, bool& store_c) const {
+  store_c = false;
   if (view_[out].root != out || !view_[out].contiguous() || d.batch != 1 || d.sCn != 1 || d.sCm != d.N) return -1;
-  for (int o : outputs_) if (root(o) == out) return -1;
-  for (auto& c : captures_) if (root(c.second) == out) return -1;
-  for (auto& w : copy_writebacks_) if (root(w.first) == out) return -1;
-  // every reader of the product (through views) is a member of one element group
+  for (int o : outputs_) if (root(o) == out) store_c = true;
+  for (auto& c : captures_) if (root(c.second) == out) store_c = true;
+  for (auto& w : copy_writebacks_) if (root(w.first) == out) store_c = true;
+  // The element group that reads the product first (through views). Any other reader
+  // (another group, one that recomputes a member, a GEMM) reads the product from memory,
+  // which the epilogue then stores too.
   int gi = -1;
   std::vector<int> stack{out};
   while (!stack.empty()) {
@@ -2189,11 +2192,12 @@ int Runtime::epi_group(int op, int out, const tgk::GemmDesc& d) const {
         continue;
       }
       const int g = group_of_[c];
-      if (g < 0 || (gi >= 0 && g != gi) || dropped_[c]) return -1;
-      // a group that recomputes the reader reads the product from memory
       for (size_t q = 0; q < groups_.size(); ++q)
-        if ((int)q != g && dup_in((int)q, c)) return -1;
-      gi = g;
+        if ((int)q != g && dup_in((int)q, c)) store_c = true;   // q evaluates c again
+      if (g < 0 || dropped_[c]) { store_c = true; continue; }
+      if (gi < 0 || g == gi) { gi = g; continue; }
+      store_c = true;
+      if (groups_[g].first < groups_[gi].first) gi = g;
     }
   }
   if (gi < 0 || group_done_[gi] || groups_[gi].row || groups_[gi].first <= op || !groups_[gi].dups.empty()) return -1;
@@ -2218,7 +2222,7 @@ int Runtime::epi_group(int op, int out, const tgk::GemmDesc& d) const {
   return gi;
 }
 
-void Runtime::lower_gemm_epi(int op, const tgk::GemmDesc& d, int a, int b, int out, int gi) {
+void Runtime::lower_gemm_epi(int op, const tgk::GemmDesc& d, int a, int b, int out, int gi, bool store_c) {
   group_done_[gi] = 1;
   const Group G = groups_[gi];
   const GroupPlan gp = plan_group(G.ops, false, G.shape);
@@ -2233,8 +2237,9 @@ void Runtime::lower_gemm_epi(int op, const tgk::GemmDesc& d, int a, int b, int o
   for (auto& e : gp.ext) if (root(e.first) != out) n.reads.push_back(root(e.first));
   if (gp.seed >= 0) n.reads.push_back(root(gp.seed));
   for (int t : gp.outs) n.writes.push_back(root(t));
+  if (store_c) n.writes.push_back(root(out));
   n.flops = 2.0 * (double)d.M * d.N * d.K * d.batch;
-  n.bytes = 4.0 * ((double)T_[a].numel + T_[b].numel);
+  n.bytes = 4.0 * ((double)T_[a].numel + T_[b].numel) + (store_c ? 4.0 * T_[out].numel : 0.0);
   for (auto& e : gp.ext) if (root(e.first) != out) n.bytes += 4.0 * T_[e.first].numel;
   for (int t : gp.outs) n.bytes += 4.0 * T_[t].numel;
   const size_t code_off = fused_code_.size();
@@ -2314,13 +2319,14 @@ void Runtime::lower_gemm_epi(int op, const tgk::GemmDesc& d, int a, int b, int o
     tgk::GemmDesc e = d;
     e.A = (const float*)dptr(a);
     e.B = (const float*)dptr(b);
-    e.C = nullptr;   // the product is not stored
+    e.C = store_c ? (float*)dptr(out) : nullptr;   // stored only when something else reads it
     tgk::GemmEpiCfg c{};
     tgk::gd::GemmArgs ga{};
     int64_t blocks = 0;
     if (!tgk::gemm_epi_cfg(e, c, ga, blocks)) throw Error(TG_INTERNAL, "GEMM epilogue: no direct-to-LDS launch");
     c.N = d.N;
     c.h_in = h_in;
+    c.store_c = store_c;
     tgk::JitKernel jk = tgk::gemm_epi_kernel(p, fused_code_.data() + code_off, c);
     const size_t js = jit_slots_.size();
     jit_slots_.emplace_back();
@@ -2819,9 +2825,10 @@ void Runtime::lower_op(int i) {
       }
     }
     if (use_gemm_epi_ && use_jit_) {
-      const int gi = epi_group(i, out, d);
+      bool store_c = false;
+      const int gi = epi_group(i, out, d, store_c);
       if (gi >= 0) {
-        lower_gemm_epi(i, d, a, b, out, gi);
+        lower_gemm_epi(i, d, a, b, out, gi, store_c);
         return;
       }
     }
