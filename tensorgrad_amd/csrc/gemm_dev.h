@@ -34,6 +34,8 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kXcds = 8;
 
+constexpr int kMaxSeg = 4;
+
 struct GemmArgs {
   GemmDesc d;
   int64_t k_per_split;
@@ -41,6 +43,12 @@ struct GemmArgs {
   int tiles_n, tiles_m;   // tile grid (per batch and split)
   float* out;             // split-K workspace (splits > 1)
   int64_t sOs, sOz;       // workspace strides (split, batch)
+  // Sum of products (SEG kernels): C = sum_s A_s B_s with K = nseg * seg_stages * BK, every
+  // segment with its own operand bases and the strides of d (one batch, one split).
+  int nseg = 1;
+  int seg_stages = 0;
+  const float* segA[kMaxSeg] = {};
+  const float* segB[kMaxSeg] = {};
 };
 
 // Same fragments and blocked accumulation as k_gemm (k_gemm.hip), but operand tiles travel from
@@ -188,8 +196,11 @@ __device__ __forceinline__ uint32_t xcd_order(uint32_t b, uint32_t nblk) {
 // KT: the last stage of a split may be partial (K per split not a multiple of BK): its
 // loads clamp k to the last valid k and the tile zeroes the rest of the stage in LDS
 // before multiplying it (KT needs DW for a k-contiguous operand).
+// SEG: a sum of products over k segments (GemmArgs::nseg): stage st reads segment
+// st / seg_stages through that segment's own bases; the per-lane offsets, relative to the
+// tile origin within a segment, are the same for every segment (shared strides).
 template <int BM, int BN, int BK, int NS, bool AK, bool BKF, int NT, int KG, class Epi, bool BDW = false,
-          bool ADW = false, bool KT = false>
+          bool ADW = false, bool KT = false, bool SEG = false>
 __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint32_t b, const Epi& epi) {
   // per k group: 4 waves 2 x 2; 8 waves 2 x 4 (BN = 128) or 4 x 2
   constexpr int GT = NT / KG;             // threads per k group
@@ -248,6 +259,14 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint32_t b, const E
   const uint32_t lds_b = (uint32_t)(unsigned long)((__attribute__((address_space(3))) float*)Bs);
   auto issue = [&](int st) {
     const int slot = st % NS;
+    if (SEG) {   // one batch, one split: kbeg = 0, z = 0
+      const int sg = st / g.seg_stages, sl = st - sg * g.seg_stages;
+      const float* sa = sg == 0 ? g.segA[0] : sg == 1 ? g.segA[1] : sg == 2 ? g.segA[2] : g.segA[3];
+      const float* sb = sg == 0 ? g.segB[0] : sg == 1 ? g.segB[1] : sg == 2 ? g.segB[2] : g.segB[3];
+      TA::dma(sa + m0 * (AK ? d.sAm : 1) + sl * a_step, offa, lds_a + slot * TA::SIZE * 4, wv);
+      TB::dma(sb + n0 * (BKF ? d.sBn : 1) + sl * b_step, offb, lds_b + slot * TB::SIZE * 4, wv);
+      return;
+    }
     if (KT && st == nst - 1 && ktail < BK) {
       TA::dma(a0 + st * a_step, offat, lds_a + slot * TA::SIZE * 4, wv);
       TB::dma(b0 + st * b_step, offbt, lds_b + slot * TB::SIZE * 4, wv);

@@ -240,9 +240,9 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g) {
 // ---- direct-to-LDS pipeline (gemm_dev.h) ----------------------------------------------
 
 template <int BM, int BN, int BK, int NS, bool AK, bool BKF, int NT, int KG, bool BDW = false, bool ADW = false,
-          bool KT = false>
+          bool KT = false, bool SEG = false>
 __global__ __launch_bounds__(NT) void k_gemm_dma(GemmArgs g) {
-  gemm_tile<BM, BN, BK, NS, AK, BKF, NT, KG, StoreC, BDW, ADW, KT>(g, xcd_order(blockIdx.x, gridDim.x), StoreC{});
+  gemm_tile<BM, BN, BK, NS, AK, BKF, NT, KG, StoreC, BDW, ADW, KT, SEG>(g, xcd_order(blockIdx.x, gridDim.x), StoreC{});
 }
 
 // Several independent problems in one launch: problem p owns tile numbers
@@ -450,6 +450,62 @@ void gemm(const GemmDesc& d, float* work, hipStream_t st) {
     if (nb > 4096) nb = 4096;
     k_splitk_reduce<<<(int)nb, 256, 0, st>>>(work, p.splits, g.sOs, d);
   }
+}
+
+// ---- sums of products ------------------------------------------------------------------
+// C = sum_s A_s B_s in one launch: the products' k ranges are stages of one GEMM whose
+// stage st reads segment st / (K_s / BK) through its own bases. Every segment shares the
+// strides, M and N of ds[0] and its K (a multiple of the plan's k stage); one batch and
+// no split-K. The k order is segment after segment, each in the plain GEMM's order.
+
+bool gemm_sum_ok(const GemmDesc* ds, int n) {
+  if (n < 2 || n > kMaxSeg) return false;
+  const GemmDesc& d0 = ds[0];
+  if (d0.batch != 1 || d0.M <= 0 || d0.N <= 0 || d0.K <= 0) return false;
+  for (int s = 1; s < n; ++s) {
+    const GemmDesc& d = ds[s];
+    if (d.batch != 1 || d.M != d0.M || d.N != d0.N || d.K != d0.K || d.sAm != d0.sAm || d.sAk != d0.sAk ||
+        d.sBk != d0.sBk || d.sBn != d0.sBn)
+      return false;
+  }
+  GemmDesc all = d0;
+  all.K = d0.K * n;
+  const Plan p = plan_for(all);
+  if (p.splits != 1 || p.bk != 32 && p.bk != 64 || d0.K % p.bk != 0) return false;
+  if (!(p.bm == 64 && p.bn == 64) && !(p.bm == 128 && p.bn == 128)) return false;
+  const bool ak = d0.sAk == 1;
+  const bool bk = d0.sBk == 1 && d0.sBn != 1;
+  for (int s = 0; s < n; ++s)
+    if (!dma_ok(ds[s], Plan{p.bm, p.bn, p.bk, 1, ds[s].K}, ak, bk)) return false;
+  return true;
+}
+
+void gemm_sum(const GemmDesc* ds, int n, hipStream_t st) {
+  if (!gemm_sum_ok(ds, n)) throw std::runtime_error("gemm_sum: unsupported operands");
+  GemmDesc all = ds[0];
+  all.K = ds[0].K * n;
+  const Plan p = plan_for(all);
+  GemmArgs g{all, all.K, 1, 0, 0, nullptr, 0, 0};
+  g.tiles_n = (int)((all.N + p.bn - 1) / p.bn);
+  g.tiles_m = (int)((all.M + p.bm - 1) / p.bm);
+  g.nseg = n;
+  g.seg_stages = (int)(ds[0].K / p.bk);
+  for (int s = 0; s < n; ++s) { g.segA[s] = ds[s].A; g.segB[s] = ds[s].B; }
+  const int64_t blocks = (int64_t)g.tiles_n * g.tiles_m;
+  const dim3 grid((unsigned)blocks);
+  const bool ak = all.sAk == 1;
+  const bool bk = all.sBk == 1 && all.sBn != 1;
+#define TG_SEG_LAUNCH(BM_, BK_, NS_, KG_)                                                                          \
+  do {                                                                                                           \
+    if (ak && bk) k_gemm_dma<BM_, BM_, BK_, NS_, true, true, 512, KG_, false, false, false, true><<<grid, 512, 0, st>>>(g); \
+    else if (ak) k_gemm_dma<BM_, BM_, BK_, NS_, true, false, 512, KG_, false, false, false, true><<<grid, 512, 0, st>>>(g); \
+    else if (bk) k_gemm_dma<BM_, BM_, BK_, NS_, false, true, 512, KG_, false, false, false, true><<<grid, 512, 0, st>>>(g); \
+    else k_gemm_dma<BM_, BM_, BK_, NS_, false, false, 512, KG_, false, false, false, true><<<grid, 512, 0, st>>>(g);        \
+  } while (0)
+  if (p.bm == 128) TG_SEG_LAUNCH(128, 32, 3, 1);
+  else if (p.bk == 32) TG_SEG_LAUNCH(64, 32, 4, 2);
+  else TG_SEG_LAUNCH(64, 64, 4, 2);
+#undef TG_SEG_LAUNCH
 }
 
 // ---- grouped GEMMs ---------------------------------------------------------------------

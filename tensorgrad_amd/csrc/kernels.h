@@ -224,6 +224,10 @@ int gemm_group_kind(const GemmDesc& d);
 // tile configuration its plain launch would use, the group input that reads the product
 // (h_in) and the product's row length N. gemm_epi_cfg fills the configuration, the launch
 // arguments and the block count; false when d has no direct-to-LDS single-pass launch.
+// Sum of products C = sum_s A_s B_s (n <= 4 terms with one shape and shared strides) as one
+// launch; gemm_sum_ok tells whether the direct-to-LDS kernel takes the terms as given.
+bool gemm_sum_ok(const GemmDesc* ds, int n);
+void gemm_sum(const GemmDesc* ds, int n, hipStream_t st);
 struct GemmEpiCfg {
   int bm, bn, bk, ns, nt, kg;
   bool ak, bkf;

@@ -340,6 +340,14 @@ class Runtime {
   std::map<int, ColSumOp> colsum_;
   std::vector<bool> colsum_done_, mul_absorbed_;
   void match_colsums();
+  // Sums of products: an add tree ((p1 + p2) + p3 ..) over single-use GEMM products of one
+  // shape runs as one GEMM over the products' concatenated k ranges (gemm_sum), emitted at
+  // the final add; the products and the inner adds are absorbed.
+  bool use_gemm_sum_ = true;         // TG_GEMM_SUM=0 keeps the products and adds apart
+  std::map<int, std::vector<int>> gemm_sums_;   // final add -> matmul ops, in k order
+  std::vector<char> sum_absorbed_;
+  void match_gemm_sums();
+  void lower_gemm_sum(int add_op);
   void lower_colsums(int s);
   int emit_pos(int op) const;
   std::deque<tgk::FusedProgram> programs_;     // kernel-argument images (stable addresses)
@@ -466,6 +474,7 @@ class Runtime {
 Runtime::Runtime(const char* json, Runtime* par, bool plan_only) : parent(par) {
   if (const char* g = std::getenv("TG_GRAPH")) use_graph_ = std::string(g) != "0";
   if (const char* g = std::getenv("TG_GEMM_GROUP")) use_gemm_group_ = std::string(g) != "0";
+  if (const char* g = std::getenv("TG_GEMM_SUM")) use_gemm_sum_ = std::string(g) != "0";
   if (const char* g = std::getenv("TG_REMAT")) use_remat_ = std::string(g) != "0";
   if (const char* g = std::getenv("TG_GEMM_EPI")) use_gemm_epi_ = std::string(g) == "1";
   if (const char* g = std::getenv("TG_FUSED")) use_jit_ = std::string(g) != "vm";
@@ -924,6 +933,7 @@ void Runtime::lower() {
   match_attention();
   match_attention_bwd();
   match_colsums();
+  match_gemm_sums();
   defer_colsum_.assign(ops_.size(), 0);
   if (use_gemm_group_)
     for (auto& c : colsum_)
@@ -944,6 +954,10 @@ void Runtime::lower() {
       continue;
     }
     if (mul_absorbed_[i]) continue;
+    if (sum_absorbed_[i]) {
+      if (gemm_sums_.count((int)i)) lower_gemm_sum((int)i);
+      continue;
+    }
     if (colsum_.count((int)i)) {
       if (!colsum_done_[i] && !defer_colsum_[i]) lower_colsums((int)i);
       continue;
@@ -1333,7 +1347,9 @@ void Runtime::form_groups() {
   };
   for (size_t i = 0; i < ops_.size(); ++i) {
     const std::string& k = kinds_[i];
-    if (virtual_[i] || is_leaf((int)i) || attn_of_[i] >= 0 || mul_absorbed_[i] || colsum_.count((int)i)) continue;
+    if (virtual_[i] || is_leaf((int)i) || attn_of_[i] >= 0 || mul_absorbed_[i] || sum_absorbed_[i] ||
+        colsum_.count((int)i))
+      continue;
     const bool red = is_row_reduce((int)i);
     if (!red && !pw.count(k)) continue;
     const int out = ops_[i]->at("out").i32();
@@ -1377,7 +1393,7 @@ void Runtime::form_groups() {
             stack.push_back(ops_[c]->at("out").i32());
             continue;
           }
-          if (attn_of_[c] >= 0 || mul_absorbed_[c] || colsum_.count(c)) return false;
+          if (attn_of_[c] >= 0 || mul_absorbed_[c] || sum_absorbed_[c] || colsum_.count(c)) return false;
           const int pos = group_of_[c] >= 0 ? groups_[group_of_[c]].first : c;
           if (pos <= (int)i) return false;
         }
@@ -2345,6 +2361,115 @@ void Runtime::lower_gemm_epi(int op, const tgk::GemmDesc& d, int a, int b, int o
   add_node(std::move(n));
 }
 
+void Runtime::match_gemm_sums() {
+  sum_absorbed_.assign(ops_.size(), 0);
+  gemm_sums_.clear();
+  if (!use_gemm_sum_ || !use_gemm_group_) return;
+  auto pinned = [&](int t) {
+    for (int o : outputs_) if (root(o) == root(t)) return true;
+    for (auto& c : captures_) if (root(c.second) == root(t)) return true;
+    for (auto& w : copy_writebacks_) if (root(w.first) == root(t)) return true;
+    return false;
+  };
+  // The matmul whose product operand t of add op `reader` is: a plain f32 GEMM (no pattern,
+  // not deferred) reading whole root tensors, whose product only this add reads.
+  auto product = [&](int t, int reader) -> int {
+    if (view_[t].root != t || T_[t].dt != F32 || pinned(t)) return -1;
+    const int m = T_[t].src;
+    if (m < 0 || kinds_[m] != "matmul" || virtual_[m] || attn_of_[m] >= 0 || defer_gemm_[m] || mul_absorbed_[m] ||
+        sum_absorbed_[m])
+      return -1;
+    if (consumers_[t].size() != 1 || consumers_[t][0] != reader) return -1;
+    const int a = fld(m, "a"), b = fld(m, "b");
+    if (kinds_[T_[view_[a].root].src] == "one_hot" || kinds_[T_[view_[b].root].src] == "one_hot") return -1;
+    return m;
+  };
+  // From the last op back, so a chain's final add claims its inner adds first.
+  for (int i = (int)ops_.size() - 1; i >= 0; --i) {
+    if (kinds_[i] != "add" || virtual_[i] || sum_absorbed_[i]) continue;
+    const int out = O(i).at("out").i32();
+    if (view_[out].root != out || !view_[out].contiguous() || T_[out].dt != F32) continue;
+    std::vector<int> terms, inner;
+    bool ok = true;
+    for (int cur = i;;) {
+      const int a = fld(cur, "a"), b = fld(cur, "b");
+      const int pb = product(b, cur);
+      if (pb < 0) { ok = false; break; }
+      terms.insert(terms.begin(), pb);
+      const int pa = product(a, cur);
+      if (pa >= 0) { terms.insert(terms.begin(), pa); break; }
+      const int ia = T_[a].src;
+      if (view_[a].root != a || ia < 0 || kinds_[ia] != "add" || virtual_[ia] || sum_absorbed_[ia] ||
+          consumers_[a].size() != 1 || pinned(a) || (int)terms.size() >= tgk::gd::kMaxSeg) {
+        ok = false;
+        break;
+      }
+      inner.push_back(ia);
+      cur = ia;
+    }
+    if (!ok || terms.size() < 2 || terms.size() > (size_t)tgk::gd::kMaxSeg) continue;
+    std::vector<tgk::GemmDesc> ds;
+    for (int m : terms) {
+      tgk::GemmDesc d{};
+      const int po = O(m).at("out").i32();
+      if (!gemm_desc(m, d) || T_[po].shape != T_[out].shape || d.sCn != 1 || d.sCm != d.N) { ok = false; break; }
+      // operands are whole tensors (arena blocks are 256-byte aligned)
+      const int a = fld(m, "a"), b = fld(m, "b");
+      if (T_[view_[a].root].numel != T_[a].numel || T_[view_[b].root].numel != T_[b].numel) { ok = false; break; }
+      d.A = reinterpret_cast<const float*>(uintptr_t(256));
+      d.B = reinterpret_cast<const float*>(uintptr_t(256));
+      ds.push_back(d);
+    }
+    if (!ok || !tgk::gemm_sum_ok(ds.data(), (int)ds.size())) continue;
+    gemm_sums_[i] = terms;
+    sum_absorbed_[i] = 1;
+    for (int m : terms) sum_absorbed_[m] = 1;
+    for (int a : inner) sum_absorbed_[a] = 1;
+  }
+}
+
+void Runtime::lower_gemm_sum(int add_op) {
+  const std::vector<int> terms = gemm_sums_.at(add_op);
+  const int out = O(add_op).at("out").i32();
+  Node n;
+  n.kind = "gemm";
+  n.op = add_op;
+  n.detail = "gemm_sum";
+  std::vector<tgk::GemmDesc> ds;
+  std::vector<int> as, bs;
+  double fl = 0, by = 4.0 * T_[out].numel;
+  for (int m : terms) {
+    tgk::GemmDesc d{};
+    if (!gemm_desc(m, d)) throw Error(TG_INTERNAL, "gemm_sum: operand view not expressible");
+    const int a = fld(m, "a"), b = fld(m, "b");
+    n.reads.push_back(root(a));
+    n.reads.push_back(root(b));
+    as.push_back(a);
+    bs.push_back(b);
+    ds.push_back(d);
+    fl += 2.0 * (double)d.M * d.N * d.K;
+    by += 4.0 * ((double)T_[a].numel + T_[b].numel);
+  }
+  n.writes.push_back(root(out));
+  n.flops = fl;
+  n.bytes = by;
+  n.shape = shape_str(T_[out].shape) + " sum of " + std::to_string(terms.size()) + " products";
+  n.bind = [this, ds, as, bs, out]() -> std::function<void(hipStream_t)> {
+    std::vector<tgk::GemmDesc> dd = ds;
+    for (size_t s = 0; s < dd.size(); ++s) {
+      // every segment's reads and the sum's writes lie inside their tensors
+      check_gemm_spans(dd[s], as[s], bs[s], out);
+      dd[s].A = (const float*)dptr(as[s]);
+      dd[s].B = (const float*)dptr(bs[s]);
+      dd[s].C = (float*)dptr(out);
+    }
+    if (!plan_only_ && !tgk::gemm_sum_ok(dd.data(), (int)dd.size()))
+      throw Error(TG_INTERNAL, "gemm_sum: operands not aligned for the direct-to-LDS kernel");
+    return [dd](hipStream_t st) { tgk::gemm_sum(dd.data(), (int)dd.size(), st); };
+  };
+  add_node(std::move(n));
+}
+
 void Runtime::emit_gemm_group(const std::vector<DeferredGemm>& grp) {
   const int kind = grp.front().kind;
   Node n;
@@ -2401,7 +2526,8 @@ void Runtime::flush_deferred_gemms() {
 // GEMMs into one grouped launch.
 bool Runtime::plain_gemm(int j) const {
   if ((kinds_[j] != "matmul" && kinds_[j] != "matmul_batched") || virtual_[j] || is_leaf(j)) return false;
-  if (attn_of_[j] >= 0 || group_of_[j] >= 0 || defer_gemm_[j] || gemm_done_[j] || mul_absorbed_[j]) return false;
+  if (attn_of_[j] >= 0 || group_of_[j] >= 0 || defer_gemm_[j] || gemm_done_[j] || mul_absorbed_[j] || sum_absorbed_[j])
+    return false;
   const int a = fld(j, "a"), b = fld(j, "b");
   if (kinds_[T_[view_[a].root].src] == "one_hot" || kinds_[T_[view_[b].root].src] == "one_hot") return false;
   return true;

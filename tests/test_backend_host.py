@@ -146,3 +146,22 @@ def test_relu_grad_reads_the_relu_output():
     assert relu_groups
     for n in relu_groups:   # reads the product [65536,256] (bias aside), writes one tensor
         assert n['bytes'] < 2.1 * 4 * 65536 * 256, n
+
+
+def test_sums_of_products_lower_to_one_gemm(monkeypatch):
+    """The transformer's Q/K/V input gradient dX = dQ Wq^T + dK Wk^T + dV Wv^T is one GEMM
+    over three k segments, each with its own base pointer; the host-only lowering runs the
+    bounds proof of every segment against the real memory plan. TG_GEMM_SUM=0 keeps the
+    products and the adds apart."""
+    cfg = configs.CONFIGS['transformer']
+    ir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer)
+    nodes = backend.plan(ir.wire_json())['nodes']
+    sums = [n for n in nodes if n.get('ops') == 'gemm_sum']
+    assert len(sums) == 4   # one per layer
+    for n in sums:
+        assert n['shape'] == '[32,128,256] sum of 3 products'
+        assert n['flops'] == 3 * 2 * 4096 * 256 * 256
+    monkeypatch.setenv('TG_GEMM_SUM', '0')
+    plain = backend.plan(ir.wire_json())['nodes']
+    assert not [n for n in plain if n.get('ops') == 'gemm_sum']
+    assert sum(n['flops'] for n in plain if n['kind'] == 'gemm') == sum(n['flops'] for n in nodes if n['kind'] == 'gemm')

@@ -466,13 +466,12 @@ def test_gemm_epilogue(M, N, K, act):
     gemm_close(got, o.output(), 1e-5)
 
 
-@pytest.mark.skip(reason='sums of products as one GEMM are switched off: the transformer step using them '
-                         'faulted the GPU once, cause not found; the code path is removed until it is')
 @pytest.mark.parametrize('terms,K', [(2, 256), (3, 256), (3, 128)])
 def test_sum_of_products(terms, K):
     """add(matmul, matmul[, matmul]) with single-use products runs as one GEMM over the
-    concatenated k segments: against the oracle with GEMM tolerance, and against the
-    unfused products and adds (TG_GEMM_GROUP=0) within f32 rounding."""
+    concatenated k segments (each segment read through its own operand bases): against the
+    oracle with GEMM tolerance, and against the unfused products and adds (TG_GEMM_GROUP=0)
+    within f32 rounding."""
     M, N = 512, 256
     ins = {}
     for q in range(terms):
