@@ -152,6 +152,63 @@ def trace_steps(key, steps, probe):
     print(json.dumps({'trace_steps': steps, 'config': key, 'final_loss': loss, 'copy_probe': bool(probe)}), flush=True)
 
 
+def vendor_gemm(key, iters=100):
+    """For every single-GEMM launch node of config `key` whose operands are 2-D after
+    merging the leading dims ("[..,m,k]x[k,n]"): this backend's per-node time (HIP events
+    around the node, eager passes) beside the vendor BLAS (torch.matmul in f32 with TF32
+    off: hipBLASLt / rocBLAS) on the same M, N, K, the faster of its two B layouts."""
+    import torch
+    from tensorgrad_amd import backend, configs
+    from tensorgrad_amd.build_ir import build_training_ir
+    torch.backends.cuda.matmul.allow_tf32 = False
+    cfg = configs.CONFIGS[key]
+    ir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer)
+    rt = backend.NativeRuntime(ir.wire_json())
+    rt.upload_params(ir.initial_params(configs.INIT_SEED))
+    rt.stage_batch(0, configs.batches(cfg, 1)[0])
+    rt.step_staged(0)
+    nodes = rt.describe()['nodes']
+    ms = rt.profile_nodes(20)
+    rt.destroy()
+
+    def lib_us(M, N, K):
+        best = None
+        a = torch.randn(M, K, device='cuda')
+        for bt in (False, True):
+            b = torch.randn(N, K, device='cuda').t() if bt else torch.randn(K, N, device='cuda')
+            for _ in range(10):
+                a @ b
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(iters):
+                a @ b
+            e1.record()
+            torch.cuda.synchronize()
+            t = e0.elapsed_time(e1) * 1e3 / iters
+            best = t if best is None else min(best, t)
+        return best
+
+    rows, seen = [], {}
+    for n, t in zip(nodes, ms):
+        if n['kind'] != 'gemm' or n.get('ops') or 'x[' not in n['shape']:
+            continue
+        left, right = n['shape'].split('x[', 1)
+        ld = [int(v) for v in left.strip('[] ').split(',')]
+        rd = [int(v) for v in right.strip('[] ').split(',')]
+        if len(rd) != 2:
+            continue
+        M, K, N = 1, ld[-1], rd[-1]
+        for v in ld[:-1]:
+            M *= v
+        if (M, N, K) not in seen:
+            seen[(M, N, K)] = lib_us(M, N, K)
+        lu = seen[(M, N, K)]
+        rows.append({'shape': n['shape'], 'M': M, 'N': N, 'K': K, 'us': round(t * 1e3, 2), 'vendor_us': round(lu, 2),
+                     'tflops': round(2.0 * M * N * K / (t * 1e-3) / 1e12, 1),
+                     'vendor_tflops': round(2.0 * M * N * K / (lu * 1e-6) / 1e12, 1)})
+    print(json.dumps({'vendor_gemm': key, 'nodes': rows}), flush=True)
+
+
 def cpu_info():
     """nproc (CPUs this process may run on), os.cpu_count() and the CPU model name."""
     model = None
@@ -253,6 +310,8 @@ def main():
                     help='only time the CPU oracle: every config, single-thread and parallel, then exit')
     ap.add_argument('--profile-iters', type=int, default=3, help='eager passes for the per-node breakdown')
     ap.add_argument('--kind-iters', type=int, default=20, help='passes per kernel-family timing')
+    ap.add_argument('--vendor-gemm', action='store_true',
+                    help='only compare every single-GEMM node of --config with the vendor BLAS, then exit')
     ap.add_argument('--probe-copy', action='store_true',
                     help='first run a 64 MiB streaming copy (profiler counter calibration)')
     args = ap.parse_args()
@@ -261,6 +320,9 @@ def main():
         return
     if args.trace_steps > 0:
         trace_steps(args.config, args.trace_steps, args.probe_copy)
+        return
+    if args.vendor_gemm:
+        vendor_gemm(args.config)
         return
     if args.gpus != 1:
         print(json.dumps({'error': 'this build runs on one GPU per process; multi-GPU data parallelism is '

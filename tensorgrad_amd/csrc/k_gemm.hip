@@ -400,7 +400,11 @@ void gemm(const GemmDesc& d, float* work, hipStream_t st) {
     else if (bk) k_gemm_dma<BM_, BN_, BK_, NS_, false, true, NT_, KG_><<<grid, NT_, 0, st>>>(g);     \
     else k_gemm_dma<BM_, BN_, BK_, NS_, false, false, NT_, KG_><<<grid, NT_, 0, st>>>(g);            \
   } while (0)
-    if (p.bm == 128 && p.bn == 128) TG_DMA_LAUNCH(128, 128, 32, 3, 512, 1);
+    // 128 x 128 tiles two or more per CU: a two-stage ring (64 KiB of LDS) so two blocks
+    // share a CU and one's prologue and stores overlap the other's MFMAs; the ring depth
+    // does not change the summation order
+    if (p.bm == 128 && p.bn == 128 && blocks >= 512) TG_DMA_LAUNCH(128, 128, 32, 2, 512, 1);
+    else if (p.bm == 128 && p.bn == 128) TG_DMA_LAUNCH(128, 128, 32, 3, 512, 1);
     else if (p.bm == 128) TG_DMA_LAUNCH(128, 64, 32, 3, 512, 1);
     else if (p.bn == 128) TG_DMA_LAUNCH(64, 128, 32, 3, 512, 1);
     else if (p.bk == 32) TG_DMA_LAUNCH(64, 64, 32, 4, 512, 2);
@@ -427,7 +431,8 @@ void gemm(const GemmDesc& d, float* work, hipStream_t st) {
     else if (bk) k_gemm_dma<BM_, BM_, 32, NS_, false, true, 512, KG_, true, true, true><<<grid, 512, 0, st>>>(g);   \
     else k_gemm_dma<BM_, BM_, 32, NS_, false, false, 512, KG_, true, true, true><<<grid, 512, 0, st>>>(g);          \
   } while (0)
-    if (bt == 128) TG_GEN_LAUNCH(128, 3, 1);
+    if (bt == 128 && gb >= 512) TG_GEN_LAUNCH(128, 2, 1);   // two blocks per CU, as above
+    else if (bt == 128) TG_GEN_LAUNCH(128, 3, 1);
     else TG_GEN_LAUNCH(64, 4, 2);
 #undef TG_GEN_LAUNCH
   } else {
@@ -536,7 +541,6 @@ bool gemm_epi_cfg(const GemmDesc& d, GemmEpiCfg& c, GemmArgs& g, int64_t& blocks
   if (p.splits != 1 || !dma_ok(d, p, ak, bk)) return false;
   // the same instantiation gemm() launches for this plan
   c.bm = p.bm; c.bn = p.bn; c.bk = p.bk;
-  c.ns = p.bm == 64 && p.bn == 64 ? 4 : 3;   // (64 x 64 with p.bk = 32: the 64 KiB variant)
   c.nt = 512;
   c.kg = p.bm == 64 && p.bn == 64 ? 2 : 1;
   c.ak = ak; c.bkf = bk;
@@ -544,6 +548,8 @@ bool gemm_epi_cfg(const GemmDesc& d, GemmEpiCfg& c, GemmArgs& g, int64_t& blocks
   g.tiles_n = (int)((d.N + p.bn - 1) / p.bn);
   g.tiles_m = (int)((d.M + p.bm - 1) / p.bm);
   blocks = (int64_t)g.tiles_n * g.tiles_m * d.batch;
+  // (64 x 64 with p.bk = 32: the 64 KiB variant; 128 x 128 two or more per CU: two stages)
+  c.ns = p.bm == 64 && p.bn == 64 ? 4 : (p.bm == 128 && p.bn == 128 && blocks >= 512 ? 2 : 3);
   return blocks < (int64_t(1) << 31);
 }
 
