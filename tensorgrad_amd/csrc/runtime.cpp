@@ -378,6 +378,7 @@ class Runtime {
     if (e != hipSuccess) throw Error(TG_DEVICE_ERROR, std::string("generated kernel launch: ") + hipGetErrorString(e));
   }
   void form_groups();
+  void merge_groups();
   void remat_groups();
   void lower_group(int gi);
 
@@ -939,6 +940,7 @@ void Runtime::lower() {
     for (auto& c : colsum_)
       if (only_optimizer_reads(O(c.first).at("out").i32())) defer_colsum_[c.first] = 1;
   form_groups();
+  merge_groups();
   if (use_remat_) remat_groups();
   group_done_.assign(groups_.size(), 0);
   for (size_t i = 0; i < ops_.size(); ++i) {
@@ -1451,6 +1453,99 @@ void Runtime::form_groups() {
   }
 }
 
+// A group B runs inside an earlier group A of the same shape when B reads a result of A
+// and every other tensor B reads exists where A runs (a leaf, or a result produced before
+// A's first op): one launch instead of two, and values of A that only B read stay in
+// registers. Members keep their per-element code, so the results are the same bits. (The
+// cross-entropy gradient rows start from a constant broadcast, so form_groups finds no
+// input tying them to the log-softmax rows they read.)
+void Runtime::merge_groups() {
+  auto eff_pos = [&](int t) {
+    const int r = root(t);
+    const int src = T_[r].src;
+    if (src < 0 || is_leaf(src)) return -1;
+    return group_of_[src] >= 0 ? groups_[group_of_[src]].first : src;
+  };
+  // Ops whose node runs once at runtime creation (split_init_nodes: it reads only such
+  // results and writes nothing pinned): constants, and groups of constant arithmetic.
+  std::set<int> pinned;
+  for (int o : outputs_) pinned.insert(root(o));
+  for (auto& c : captures_) pinned.insert(root(c.second));
+  for (auto& w : copy_writebacks_) pinned.insert(root(w.first));
+  std::vector<signed char> memo(ops_.size(), -1);
+  std::function<bool(int)> init_op = [&](int m) -> bool {
+    if (memo[m] >= 0) return memo[m] != 0;
+    memo[m] = 0;
+    bool r = false;
+    const std::string& k = kinds_[m];
+    if (k == "const_scalar" || k == "const_fill" || k == "arange") {
+      r = !pinned.count(root(O(m).at("out").i32()));
+    } else if (group_of_[m] >= 0) {
+      const int g = group_of_[m];
+      r = true;
+      for (int q : groups_[g].ops) {
+        if (pinned.count(root(O(q).at("out").i32()))) r = false;
+        for (int t : op_inputs(*ops_[q])) {
+          const int src = T_[root(t)].src;
+          if (src >= 0 && group_of_[src] == g) continue;
+          if (src < 0 || is_leaf(src) || !init_op(src)) r = false;
+        }
+      }
+    }
+    memo[m] = r ? 1 : 0;
+    return r;
+  };
+  std::vector<char> init_group(groups_.size(), 0);
+  for (size_t g = 0; g < groups_.size(); ++g)
+    if (!groups_[g].ops.empty()) init_group[g] = init_op(groups_[g].ops.front());
+  for (size_t b = 0; b < groups_.size(); ++b) {
+    if (init_group[b]) continue;
+    for (size_t a = 0; a < groups_.size() && !groups_[b].ops.empty(); ++a) {
+      const Group& A = groups_[a];
+      const Group& B = groups_[b];
+      if (a == b || init_group[a] || A.ops.empty() || A.first >= B.first || A.shape != B.shape) continue;
+      const Dims& F = A.shape;
+      const bool row = A.row || B.row;
+      bool ok = true, reads_a = false;
+      for (int m : B.ops) {
+        const int so = O(m).at("out").i32();
+        const Dims& So = T_[so].shape;
+        for (int t : op_inputs(*ops_[m])) {
+          const int pg = producer_group(t);
+          if (pg != (int)a && pg != (int)b) {
+            const int src = T_[root(t)].src;
+            if (src >= 0 && !is_leaf(src) && init_op(src)) continue;   // exists before any step launch
+            if (eff_pos(t) >= A.first) ok = false;
+            continue;
+          }
+          if (pg == (int)a) reads_a = true;
+          // the operand shapes a member may read from its own group (form_groups' rule)
+          if (kinds_[m] == "dropout" && t == fld(m, "seed")) continue;
+          if (is_row_reduce(m)) continue;
+          const Dims& ts = T_[t].shape;
+          if (!row) ok = ok && ts == F;
+          else if (So == F) ok = ok && (ts == F || row_class(ts, F) == 2);
+          else ok = ok && ts == So;
+        }
+        if (!ok) break;
+      }
+      if (!ok || !reads_a) continue;
+      std::vector<int> ops = A.ops;
+      ops.insert(ops.end(), B.ops.begin(), B.ops.end());
+      std::sort(ops.begin(), ops.end());
+      if (ops.size() > (size_t)tgk::kFusedMaxInstr) continue;
+      const GroupPlan gp = plan_group(ops, row, F);
+      const int maxregs = row && F.back() > 1024 ? 4 : tgk::kFusedRegs;
+      if (gp.ext.size() > (size_t)tgk::kFusedMaxIn || gp.outs.size() > (size_t)tgk::kFusedMaxOut || gp.nregs > maxregs)
+        continue;
+      for (int m : groups_[b].ops) group_of_[m] = (int)a;
+      groups_[a].ops = ops;
+      groups_[a].row = row;
+      groups_[b].ops.clear();
+    }
+  }
+}
+
 // Recomputation instead of storage. An element group G that reads values a pointwise
 // chain of another group P produced (same shape as G, no dropout, no row reductions)
 // evaluates that chain again from the chain's own inputs, tensors in memory (GEMM
@@ -1468,7 +1563,7 @@ void Runtime::remat_groups() {
   bool any = false;
   for (size_t gi = 0; gi < groups_.size(); ++gi) {
     Group& G = groups_[gi];
-    if (G.row) continue;
+    if (G.row || G.ops.empty()) continue;
     const GroupPlan gp = plan_group(G.ops, false, G.shape, &G.dups);
     const int64_t full = prod(G.shape);
     std::set<int> ext_roots;

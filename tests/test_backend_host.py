@@ -165,3 +165,21 @@ def test_sums_of_products_lower_to_one_gemm(monkeypatch):
     plain = backend.plan(ir.wire_json())['nodes']
     assert not [n for n in plain if n.get('ops') == 'gemm_sum']
     assert sum(n['flops'] for n in plain if n['kind'] == 'gemm') == sum(n['flops'] for n in nodes if n['kind'] == 'gemm')
+
+
+def test_loss_gradient_rows_join_the_loss_rows():
+    """The cross-entropy gradient rows (softmax minus one-hot, scaled by a constant) read the
+    log-softmax rows' exp; they start from a constant broadcast, so only the merge pass puts
+    them in the forward row group: one launch for the loss rows and their gradient, the exp
+    kept in registers. The MSE forward and backward element groups merge the same way."""
+    for key, n_rows in (('char_mlp', 1), ('transformer', 1)):
+        cfg = configs.CONFIGS[key]
+        ir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer)
+        nodes = backend.plan(ir.wire_json())['nodes']
+        ce = [n for n in nodes if 'log_softmax_last' in n.get('ops', '')]
+        assert len(ce) == n_rows and ce[0]['ops'].endswith('exp,sum_last,broadcast_to,mul,sub'), ce
+    cfg = configs.CONFIGS['mlp_sin']
+    ir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer)
+    nodes = backend.plan(ir.wire_json())['nodes']
+    assert [n['ops'] for n in nodes if n['kind'] == 'fused' and n['shape'].startswith('[256,1]')] == \
+        ['add,sub,mul,mul,mul,add']
