@@ -205,6 +205,101 @@ __global__ __launch_bounds__(256) void k_conv_wgrad_reduce_wave(const float* __r
   if (lane == 0) dw[i] = s;
 }
 
+// ---- convolutions with few taps ------------------------------------------------------------
+// A first layer over 1-3 channel images has CinPG * kH * kW <= 16 taps per output: as a
+// GEMM its forward has K <= 16 and its weight gradient N <= 16, so most of every 32-wide
+// MFMA stage or tile would multiply padding. Both run on the vector ALU instead (f32 FMAs,
+// GEMM tolerance like the MFMA path).
+constexpr int kSmallTaps = 16;
+constexpr int kSmallCo = 4;   // output channels per weight-gradient block
+
+// The taps of output position (b, g, ho, wo), in (cl, kh, kw) order; zero outside the image.
+__device__ __forceinline__ void small_taps(const ConvGemmArgs& c, int b, int g, int ho, int wo, float* xv) {
+#pragma unroll
+  for (int q = 0; q < kSmallTaps; ++q) {
+    xv[q] = 0.0f;
+    if (q >= c.K) continue;
+    const int cl = fdiv(q, c.dKHW), r = q - cl * c.kH * c.kW;
+    const int kh = fdiv(r, c.dKW), kw = r - kh * c.kW;
+    const int hi = ho * c.sH + kh - c.pH, wi = wo * c.sW + kw - c.pW;
+    if (inside(hi, c.H) && inside(wi, c.W)) xv[q] = c.x[((b * c.Cin + g * c.CinPG + cl) * c.H + hi) * c.W + wi];
+  }
+}
+
+// Forward: one thread per output position (b, g, ho, wo), every output channel of its group
+// (the weights are the same for the whole wavefront: scalar loads).
+__global__ __launch_bounds__(256) void k_conv_small_fwd(const ConvGemmArgs c) {
+  const int hw = c.Ho * c.Wo;
+  const int t = blockIdx.x * 256 + threadIdx.x;
+  if (t >= c.B * c.G * hw) return;
+  const int z = fdiv(t, c.dHoWo), p = t - z * hw;
+  const int b = z / c.G, g = z - b * c.G;
+  const int ho = fdiv(p, c.dWo), wo = p - ho * c.Wo;
+  float xv[kSmallTaps];
+  small_taps(c, b, g, ho, wo, xv);
+  for (int co = 0; co < c.CoutPG; ++co) {
+    const float* w = c.w + (int64_t)(g * c.CoutPG + co) * c.K;
+    float s = 0.0f;
+#pragma unroll
+    for (int q = 0; q < kSmallTaps; ++q)
+      if (q < c.K) s = fmaf(w[q], xv[q], s);
+    c.out[(int64_t)(b * c.Cout + g * c.CoutPG + co) * hw + p] = s;
+  }
+}
+
+// Weight gradient: block (image b, group g, kSmallCo output channels) sums dy * tap over
+// the image's positions (threads take positions t, t + 256, ...), then across the block
+// (a fixed butterfly per wavefront, the four wavefronts in order) into the image's
+// partial dW rows: work[b][g * CoutPG + co][q]. The partials are added in image order.
+__global__ __launch_bounds__(256) void k_conv_small_wgrad(const ConvGemmArgs c) {
+  __shared__ float red[4][kSmallCo * kSmallTaps];
+  const int hw = c.Ho * c.Wo;
+  const int nch = (c.CoutPG + kSmallCo - 1) / kSmallCo;
+  const int blk = blockIdx.x, cc = blk % nch, z = blk / nch;
+  const int b = z / c.G, g = z - b * c.G;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  float acc[kSmallCo][kSmallTaps];
+#pragma unroll
+  for (int j = 0; j < kSmallCo; ++j)
+#pragma unroll
+    for (int q = 0; q < kSmallTaps; ++q) acc[j][q] = 0.0f;
+  for (int p = tid; p < hw; p += 256) {
+    const int ho = fdiv(p, c.dWo), wo = p - ho * c.Wo;
+    float xv[kSmallTaps];
+    small_taps(c, b, g, ho, wo, xv);
+#pragma unroll
+    for (int j = 0; j < kSmallCo; ++j) {
+      const int co = cc * kSmallCo + j;
+      const float d = co < c.CoutPG ? c.dy[(int64_t)(b * c.Cout + g * c.CoutPG + co) * hw + p] : 0.0f;
+#pragma unroll
+      for (int q = 0; q < kSmallTaps; ++q) acc[j][q] = fmaf(d, xv[q], acc[j][q]);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < kSmallCo; ++j)
+#pragma unroll
+    for (int q = 0; q < kSmallTaps; ++q) {
+      float v = acc[j][q];
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+      if (lane == 0) red[wave][j * kSmallTaps + q] = v;
+    }
+  __syncthreads();
+  if (tid < kSmallCo * kSmallTaps) {
+    const int j = tid / kSmallTaps, q = tid % kSmallTaps, co = cc * kSmallCo + j;
+    if (co < c.CoutPG && q < c.K) {
+      const float v = ((red[0][tid] + red[1][tid]) + red[2][tid]) + red[3][tid];
+      c.work[(int64_t)b * c.G * c.CoutPG * c.K + (int64_t)(g * c.CoutPG + co) * c.K + q] = v;
+    }
+  }
+}
+
+// The few-taps weight gradient applies when its per-image partials fit the workspace.
+bool small_wgrad_ok(const ConvDesc& d) {
+  const int64_t taps = d.CinPG * d.kH * d.kW;
+  return taps <= kSmallTaps && d.B * d.Cout * taps * 4 <= kConvWorkBytes;
+}
+
 template <int MODE, bool FAST, int F>
 void launch_tile(const ConvPlan& p, const ConvGemmArgs& a, hipStream_t st) {
   const dim3 grid((unsigned)p.blocks);
@@ -251,6 +346,7 @@ void launch_mode(const ConvPlan& p, const ConvGemmArgs& a, bool fast, hipStream_
 bool conv_gemm_ok(const ConvDesc& d) { return conv_ok(d); }
 
 int64_t conv_gemm_workspace_bytes(const ConvDesc& d) {
+  if (small_wgrad_ok(d)) return d.B * d.Cout * d.CinPG * d.kH * d.kW * 4;
   const ConvPlan p = conv_plan(CV_WGRAD, d);
   if (p.splits <= 1) return 0;
   return (int64_t)p.splits * d.G * (d.Cout / d.G) * d.CinPG * d.kH * d.kW * 4;
@@ -261,6 +357,12 @@ void conv2d_gemm(const float* x, const float* w, float* y, const ConvDesc& d, hi
   ConvGemmArgs a = make_args(d, p);
   a.x = x; a.w = w; a.out = y;
   a.avec = a.avec && ((uintptr_t)w & 15) == 0;
+  if (d.CinPG * d.kH * d.kW <= kSmallTaps) {
+    // the K taps of a row of W are contiguous: W[co][cl][kh][kw] = w[co * K + q]
+    const int64_t n = d.B * d.G * d.Ho * d.Wo;
+    if (n > 0) k_conv_small_fwd<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(a);
+    return;
+  }
   if (p.blocks > 0) launch_mode<CV_FWD>(p, a, true, st);
 }
 
@@ -277,6 +379,22 @@ void conv2d_weight_grad_gemm(const float* x, const float* dy, float* dw, const C
   ConvGemmArgs a = make_args(d, p);
   a.x = x; a.dy = dy; a.out = dw; a.work = work;
   a.avec = a.avec && ((uintptr_t)dy & 15) == 0;
+  if (small_wgrad_ok(d)) {
+    if (!work) throw std::runtime_error("conv2d_weight_grad: missing workspace");
+    if (d.B <= 0 || d.Cout <= 0) return;
+    ConvGemmArgs sa = a;   // K: the taps per output (the GEMM view's N)
+    sa.K = (int)(d.CinPG * d.kH * d.kW);
+    const int64_t per = d.Cout * sa.K;
+    const int64_t nch = (a.CoutPG + kSmallCo - 1) / kSmallCo;
+    k_conv_small_wgrad<<<(unsigned)(d.B * d.G * nch), 256, 0, st>>>(sa);
+    if (per < 16384 && d.B > 16) {
+      k_conv_wgrad_reduce_wave<<<(unsigned)((per + 3) / 4), 256, 0, st>>>(work, (int)d.B, per, dw);
+    } else {
+      const int64_t nb = std::min<int64_t>((per + 255) / 256, 4096);
+      k_conv_wgrad_reduce<<<(int)nb, 256, 0, st>>>(work, (int)d.B, per, dw);
+    }
+    return;
+  }
   if (p.blocks <= 0) return;
   if (p.splits > 1 && !work) throw std::runtime_error("conv2d_weight_grad: missing workspace");
   launch_mode<CV_WGRAD>(p, a, true, st);

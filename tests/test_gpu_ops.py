@@ -588,13 +588,16 @@ CONV_CASES = [
     (128, 1, 28, 28, 32, 1, 3, 1, 0),      # the CNN config's first layer
     (128, 32, 26, 26, 64, 1, 3, 1, 0),     # its second layer (split-K weight gradient)
     (3, 5, 11, 7, 130, 1, 5, 1, 2),        # 5x5, padding, Cout above one tile
+    (4, 2, 10, 9, 6, 2, 3, 2, 1),          # 9 taps per output (vector-ALU forward / weight
+    (5, 2, 7, 7, 5, 1, 2, 1, 0),           # gradient): groups, stride, padding, partial chunks
 ]
 
 
 @pytest.mark.parametrize('impl', ['gemm', 'direct'])
 @pytest.mark.parametrize('case', CONV_CASES)
 def test_conv_kernels(impl, case):
-    """Implicit-GEMM convolutions (default) accumulate in f32 on the matrix cores: within
+    """Implicit-GEMM convolutions (default) accumulate in f32 on the matrix cores (layers
+    with at most 16 taps per output: forward and weight gradient on the vector ALU): within
     2e-6 relative (norm-wise) of the evaluator, like the GEMMs. The direct kernels
     (TG_CONV=direct) reproduce the evaluator's f64 loops: forward and input gradient bit
     for bit, the weight gradient (different f64 summation order) within 1 ulp."""
