@@ -211,53 +211,97 @@ __global__ __launch_bounds__(256) void k_conv_wgrad_reduce_wave(const float* __r
 // MFMA stage or tile would multiply padding. Both run on the vector ALU instead (f32 FMAs,
 // GEMM tolerance like the MFMA path).
 constexpr int kSmallTaps = 16;
-constexpr int kSmallCo = 4;   // output channels per weight-gradient block
+constexpr int kSmallCo = 4;      // output channels per weight-gradient block
+constexpr int kSmallW = 2048;    // forward: a group's weights staged in LDS, CoutPG * kSmallTaps floats
 
-// The taps of output position (b, g, ho, wo), in (cl, kh, kw) order; zero outside the image.
-__device__ __forceinline__ void small_taps(const ConvGemmArgs& c, int b, int g, int ho, int wo, float* xv) {
+// Tap q = (cl, kh, kw) of an output position: its row and column shift and its channel
+// plane offset, decoded once per thread.
+struct SmallTaps {
+  int dh[kSmallTaps], dw[kSmallTaps];
+  uint32_t off[kSmallTaps];
+  __device__ __forceinline__ void init(const ConvGemmArgs& c) {
 #pragma unroll
-  for (int q = 0; q < kSmallTaps; ++q) {
-    xv[q] = 0.0f;
-    if (q >= c.K) continue;
-    const int cl = fdiv(q, c.dKHW), r = q - cl * c.kH * c.kW;
-    const int kh = fdiv(r, c.dKW), kw = r - kh * c.kW;
-    const int hi = ho * c.sH + kh - c.pH, wi = wo * c.sW + kw - c.pW;
-    if (inside(hi, c.H) && inside(wi, c.W)) xv[q] = c.x[((b * c.Cin + g * c.CinPG + cl) * c.H + hi) * c.W + wi];
+    for (int q = 0; q < kSmallTaps; ++q) {
+      const int qq = q < c.K ? q : 0;
+      const int cl = fdiv(qq, c.dKHW), r = qq - cl * c.kH * c.kW;
+      const int kh = fdiv(r, c.dKW), kw = r - kh * c.kW;
+      dh[q] = kh - c.pH;
+      dw[q] = kw - c.pW;
+      off[q] = (uint32_t)(cl * c.H * c.W);
+    }
   }
-}
+  // The taps of output position (ho, wo) of image plane base `base` (x's (b, g * CinPG)
+  // offset), zero outside the image: raw buffer loads, masked ones at an out-of-range
+  // offset, so all of them are in flight together.
+  __device__ __forceinline__ void gather(const ConvGemmArgs& c, const Src& sx, uint32_t base, int ho, int wo,
+                                         float* xv) const {
+#pragma unroll
+    for (int q = 0; q < kSmallTaps; ++q) {
+      const int hi = ho * c.sH + dh[q], wi = wo * c.sW + dw[q];
+      const bool ok = q < c.K && inside(hi, c.H) && inside(wi, c.W);
+      xv[q] = ldb(sx, boff(ok, base + off[q] + (uint32_t)(hi * c.W + wi)));
+    }
+  }
+};
 
-// Forward: one thread per output position (b, g, ho, wo), every output channel of its group
-// (the weights are the same for the whole wavefront: scalar loads).
+// Forward: block (image b, group g, 256 positions), one thread per position, every output
+// channel of the group from the group's weights in LDS, each row padded with zeros to
+// kSmallTaps (the masked taps are zero too), so the product loop has no branches and reads
+// each row as four 128-bit broadcasts.
 __global__ __launch_bounds__(256) void k_conv_small_fwd(const ConvGemmArgs c) {
+  __shared__ __attribute__((aligned(16))) float ws[kSmallW];
   const int hw = c.Ho * c.Wo;
-  const int t = blockIdx.x * 256 + threadIdx.x;
-  if (t >= c.B * c.G * hw) return;
-  const int z = fdiv(t, c.dHoWo), p = t - z * hw;
+  const int nchunk = (hw + 255) / 256;
+  const int z = blockIdx.x / nchunk, chunk = blockIdx.x - z * nchunk;
   const int b = z / c.G, g = z - b * c.G;
+  for (int i = threadIdx.x; i < c.CoutPG * kSmallTaps; i += 256) {
+    const int co = i / kSmallTaps, q = i - co * kSmallTaps;
+    ws[i] = q < c.K ? c.w[(int64_t)(g * c.CoutPG + co) * c.K + q] : 0.0f;
+  }
+  SmallTaps tp;
+  tp.init(c);
+  __syncthreads();
+  const int p = chunk * 256 + threadIdx.x;
+  if (p >= hw) return;
   const int ho = fdiv(p, c.dWo), wo = p - ho * c.Wo;
+  const Src sx = make_src(c.x, (int64_t)c.B * c.Cin * c.H * c.W);
   float xv[kSmallTaps];
-  small_taps(c, b, g, ho, wo, xv);
+  tp.gather(c, sx, (uint32_t)((b * c.Cin + g * c.CinPG) * c.H * c.W), ho, wo, xv);
+  float* y = c.out + (int64_t)(b * c.Cout + g * c.CoutPG) * hw + p;
   for (int co = 0; co < c.CoutPG; ++co) {
-    const float* w = c.w + (int64_t)(g * c.CoutPG + co) * c.K;
+    const f32x4* wr = reinterpret_cast<const f32x4*>(ws + co * kSmallTaps);
     float s = 0.0f;
 #pragma unroll
-    for (int q = 0; q < kSmallTaps; ++q)
-      if (q < c.K) s = fmaf(w[q], xv[q], s);
-    c.out[(int64_t)(b * c.Cout + g * c.CoutPG + co) * hw + p] = s;
+    for (int u = 0; u < kSmallTaps / 4; ++u) {
+      const f32x4 w4 = wr[u];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) s = fmaf(w4[e], xv[u * 4 + e], s);
+    }
+    y[(int64_t)co * hw] = s;
   }
 }
 
 // Weight gradient: block (image b, group g, kSmallCo output channels) sums dy * tap over
-// the image's positions (threads take positions t, t + 256, ...), then across the block
-// (a fixed butterfly per wavefront, the four wavefronts in order) into the image's
-// partial dW rows: work[b][g * CoutPG + co][q]. The partials are added in image order.
+// the image's positions (threads take positions t, t + 256, ...), then across the block in
+// a fixed order: every thread stores its sums in LDS, four threads per sum add 64 threads'
+// values each in thread order, and the four quarters are added in order, giving the
+// image's partial dW rows work[b][g * CoutPG + co][q]. The partials are added in image
+// order.
 __global__ __launch_bounds__(256) void k_conv_small_wgrad(const ConvGemmArgs c) {
-  __shared__ float red[4][kSmallCo * kSmallTaps];
+  constexpr int NV = kSmallCo * kSmallTaps;
+  static_assert(NV * 4 == 256, "four threads per sum");
+  __shared__ float red[256][NV + 1];
   const int hw = c.Ho * c.Wo;
   const int nch = (c.CoutPG + kSmallCo - 1) / kSmallCo;
   const int blk = blockIdx.x, cc = blk % nch, z = blk / nch;
   const int b = z / c.G, g = z - b * c.G;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x;
+  SmallTaps tp;
+  tp.init(c);
+  const Src sx = make_src(c.x, (int64_t)c.B * c.Cin * c.H * c.W);
+  const Src sdy = make_src(c.dy, (int64_t)c.B * c.Cout * hw);
+  const uint32_t xbase = (uint32_t)((b * c.Cin + g * c.CinPG) * c.H * c.W);
+  const uint32_t dbase = (uint32_t)((b * c.Cout + g * c.CoutPG + cc * kSmallCo) * hw);
   float acc[kSmallCo][kSmallTaps];
 #pragma unroll
   for (int j = 0; j < kSmallCo; ++j)
@@ -265,31 +309,32 @@ __global__ __launch_bounds__(256) void k_conv_small_wgrad(const ConvGemmArgs c) 
     for (int q = 0; q < kSmallTaps; ++q) acc[j][q] = 0.0f;
   for (int p = tid; p < hw; p += 256) {
     const int ho = fdiv(p, c.dWo), wo = p - ho * c.Wo;
-    float xv[kSmallTaps];
-    small_taps(c, b, g, ho, wo, xv);
+    float xv[kSmallTaps], d[kSmallCo];
+    tp.gather(c, sx, xbase, ho, wo, xv);
 #pragma unroll
-    for (int j = 0; j < kSmallCo; ++j) {
-      const int co = cc * kSmallCo + j;
-      const float d = co < c.CoutPG ? c.dy[(int64_t)(b * c.Cout + g * c.CoutPG + co) * hw + p] : 0.0f;
+    for (int j = 0; j < kSmallCo; ++j)
+      d[j] = ldb(sdy, boff(cc * kSmallCo + j < c.CoutPG, dbase + (uint32_t)(j * hw + p)));
 #pragma unroll
-      for (int q = 0; q < kSmallTaps; ++q) acc[j][q] = fmaf(d, xv[q], acc[j][q]);
-    }
+    for (int j = 0; j < kSmallCo; ++j)
+#pragma unroll
+      for (int q = 0; q < kSmallTaps; ++q) acc[j][q] = fmaf(d[j], xv[q], acc[j][q]);
   }
 #pragma unroll
   for (int j = 0; j < kSmallCo; ++j)
 #pragma unroll
-    for (int q = 0; q < kSmallTaps; ++q) {
-      float v = acc[j][q];
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-      if (lane == 0) red[wave][j * kSmallTaps + q] = v;
-    }
+    for (int q = 0; q < kSmallTaps; ++q) red[tid][j * kSmallTaps + q] = acc[j][q];
   __syncthreads();
-  if (tid < kSmallCo * kSmallTaps) {
+  const int v = tid % NV, quarter = tid / NV;   // 256 threads = 4 quarters of the NV sums
+  float s = 0.0f;
+  for (int i = 0; i < 64; ++i) s += red[quarter * 64 + i][v];
+  __syncthreads();
+  red[quarter][v] = s;
+  __syncthreads();
+  if (tid < NV) {
     const int j = tid / kSmallTaps, q = tid % kSmallTaps, co = cc * kSmallCo + j;
     if (co < c.CoutPG && q < c.K) {
-      const float v = ((red[0][tid] + red[1][tid]) + red[2][tid]) + red[3][tid];
-      c.work[(int64_t)b * c.G * c.CoutPG * c.K + (int64_t)(g * c.CoutPG + co) * c.K + q] = v;
+      const float t = ((red[0][tid] + red[1][tid]) + red[2][tid]) + red[3][tid];
+      c.work[(int64_t)b * c.G * c.CoutPG * c.K + (int64_t)(g * c.CoutPG + co) * c.K + q] = t;
     }
   }
 }
@@ -357,10 +402,10 @@ void conv2d_gemm(const float* x, const float* w, float* y, const ConvDesc& d, hi
   ConvGemmArgs a = make_args(d, p);
   a.x = x; a.w = w; a.out = y;
   a.avec = a.avec && ((uintptr_t)w & 15) == 0;
-  if (d.CinPG * d.kH * d.kW <= kSmallTaps) {
+  if (d.CinPG * d.kH * d.kW <= kSmallTaps && (d.Cout / d.G) * kSmallTaps <= kSmallW) {
     // the K taps of a row of W are contiguous: W[co][cl][kh][kw] = w[co * K + q]
-    const int64_t n = d.B * d.G * d.Ho * d.Wo;
-    if (n > 0) k_conv_small_fwd<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(a);
+    const int64_t n = d.B * d.G * ((d.Ho * d.Wo + 255) / 256);
+    if (n > 0) k_conv_small_fwd<<<(unsigned)n, 256, 0, st>>>(a);
     return;
   }
   if (p.blocks > 0) launch_mode<CV_FWD>(p, a, true, st);
