@@ -8,15 +8,18 @@ parameter tensor at step 100 either all values (every tensor of the configs in W
 tensors up to FULL_LIMIT elements) or a fixed seeded sample of SAMPLE indices, with the
 f64 norm of the whole tensor.
 
-For the configs in TWIN the oracle also trains NTWIN twins from the same initial
+For the configs in NTWIN the oracle also trains NTWIN[key] twins from the same initial
 parameters moved by one ulp each (a seeded random direction per element, different per
 twin), the size of the rounding difference any f32 implementation that is not
 bit-identical to the evaluator introduces in its first step; the twins' losses and
 step-100 values (same indices) measure how far the workload itself amplifies such a
-difference over 100 steps ('twin_losses' [NTWIN, steps], 'twin:<param>' [NTWIN, sample],
-'twin_norm:<param>' [NTWIN]).
+difference over 100 steps ('twin_losses' [n, steps], 'twin:<param>' [n, sample],
+'twin_norm:<param>' [n]). The test bounds each tensor by its farthest twin, so that
+spread is estimated from several samples: four for the eight-layer NeRF MLP, two for the
+CNN.
 
     python tests/golden/make_full_parity.py [keys...] [--threads N]
+    python tests/golden/make_full_parity.py nerf --add-twins   # train only the missing twins
 """
 import argparse
 import os
@@ -38,8 +41,7 @@ STEPS = 100
 FULL_LIMIT = 16_384
 SAMPLE = 4096
 WHOLE = {'char_mlp'}
-TWIN = {'cnn', 'nerf'}
-NTWIN = 2
+NTWIN = {'cnn': 2, 'nerf': 4}
 
 
 def sample_indices(key: str, name: str, n: int) -> np.ndarray:
@@ -85,14 +87,39 @@ def make(key: str) -> str:
         out[f'idx:{n}'] = idx
         out[f'val:{n}'] = v[idx]
         out[f'norm:{n}'] = np.array(np.linalg.norm(v.astype(np.float64)))
-    if key in TWIN:
-        runs = [train(key, cfg, ir, one_ulp(p0, j), f' twin {j}') for j in range(NTWIN)]
-        out['twin_losses'] = np.stack([tl for _, tl in runs])
-        for n in ir.param_names:
-            vs = [t.get_home(n, sizes[n]) for t, _ in runs]
-            out[f'twin:{n}'] = np.stack([v[out[f'idx:{n}']] for v in vs])
-            out[f'twin_norm:{n}'] = np.array([np.linalg.norm(v.astype(np.float64)) for v in vs])
+    if key in NTWIN:
+        add_twins(key, cfg, ir, p0, out, 0)
     path = os.path.join(HERE, f'full_{key}.npz')
+    np.savez_compressed(path, **out)
+    return path
+
+
+def add_twins(key: str, cfg, ir, p0: dict, out: dict, have: int):
+    """Train twins have .. NTWIN[key] - 1 and append them to the fixture dict `out`."""
+    shapes = ir.param_shapes()
+    sizes = {n: int(np.prod(shapes[n])) if shapes[n] else 1 for n in ir.param_names}
+    runs = [train(key, cfg, ir, one_ulp(p0, j), f' twin {j}') for j in range(have, NTWIN[key])]
+    if not runs:
+        return
+    new_l = np.stack([tl for _, tl in runs])
+    out['twin_losses'] = np.concatenate([out['twin_losses'], new_l]) if have else new_l
+    for n in ir.param_names:
+        vs = [t.get_home(n, sizes[n]) for t, _ in runs]
+        val = np.stack([v[out[f'idx:{n}']] for v in vs])
+        nrm = np.array([np.linalg.norm(v.astype(np.float64)) for v in vs])
+        out[f'twin:{n}'] = np.concatenate([out[f'twin:{n}'], val]) if have else val
+        out[f'twin_norm:{n}'] = np.concatenate([out[f'twin_norm:{n}'], nrm]) if have else nrm
+
+
+def extend(key: str) -> str:
+    """Add the missing twins to an existing fixture (its base run and twins are kept)."""
+    path = os.path.join(HERE, f'full_{key}.npz')
+    with np.load(path) as z:
+        out = {k: z[k] for k in z.files}
+    have = out['twin_losses'].shape[0] if 'twin_losses' in out else 0
+    cfg = configs.CONFIGS[key]
+    ir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer)
+    add_twins(key, cfg, ir, ir.initial_params(configs.INIT_SEED), out, have)
     np.savez_compressed(path, **out)
     return path
 
@@ -101,10 +128,11 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument('keys', nargs='*', default=['char_mlp', 'cnn', 'transformer', 'nerf'])
     ap.add_argument('--threads', type=int, default=os.cpu_count() or 8)
+    ap.add_argument('--add-twins', action='store_true', help='only train the twins the fixture lacks')
     a = ap.parse_args()
     pyoracle.set_threads(a.threads)
     for k in a.keys:
-        print(k, '->', make(k), flush=True)
+        print(k, '->', extend(k) if a.add_twins else make(k), flush=True)
 
 
 if __name__ == '__main__':

@@ -590,6 +590,9 @@ CONV_CASES = [
     (3, 5, 11, 7, 130, 1, 5, 1, 2),        # 5x5, padding, Cout above one tile
     (4, 2, 10, 9, 6, 2, 3, 2, 1),          # 9 taps per output (vector-ALU forward / weight
     (5, 2, 7, 7, 5, 1, 2, 1, 0),           # gradient): groups, stride, padding, partial chunks
+    (2, 64, 9, 10, 40, 2, 3, 2, 1),        # direct-to-LDS conv2d: 32 channels per group, stride,
+    (3, 40, 7, 9, 64, 2, 3, 1, 1),         # padding, partial tiles; direct-to-LDS input gradient
+    (2, 8, 12, 11, 32, 1, 5, 1, 2),        # (32 output channels per group), 3x3 and 5x5, padded
 ]
 
 
