@@ -18,6 +18,9 @@
 //    in f64 from f32 operands with the f64 constants beta1, 1-beta1, beta2, 1-beta2, eps
 //    and the literal decayShrink, each output rounded to f32 once; formula of
 //    src/codegen.ts:854, 873, 899.
+// Two switches for the parity fixtures only (off by default) measure how far other valid
+// roundings drift: orc_set_matmul_f32 makes matmuls accumulate in f32, orc_set_sum_f64
+// makes sum_to_shape accumulate in f64.
 // Per-element loops are parallelised over output elements with OpenMP; each element's
 // own accumulation order is unchanged, so results are bit-identical for any thread count.
 //
@@ -74,9 +77,49 @@ static void matmul_block(const float* __restrict__ A, const double* __restrict__
     for (int64_t j = 0; j < nn; ++j) C[(m0 + r) * N + n0 + j] = (float)acc[r][j];
 }
 
+// The f32 twin of the parity fixtures (orc_set_matmul_f32): the same loop with f32
+// running sums (each product rounded to f32, then added in f32, increasing k), the
+// accumulation an f32 GPU kernel uses; off unless a fixture script turns it on.
+static bool g_matmul_f32 = false;
+// The f64-sum twin (orc_set_sum_f64): sum_to_shape accumulates in f64 and rounds once, as
+// the GPU's column sums do; off unless a fixture script turns it on.
+static bool g_sum_f64 = false;
+
+__attribute__((target_clones("avx2", "default")))
+static void matmul_block_f32(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int64_t M,
+                             int64_t K, int64_t N, int64_t m0, int64_t mr, int64_t n0, int64_t nn) {
+  constexpr int64_t MR = 4, NB = 256;
+  float acc[MR][NB];
+  for (int64_t r = 0; r < mr; ++r)
+    for (int64_t j = 0; j < nn; ++j) acc[r][j] = 0.0f;
+  for (int64_t kk = 0; kk < K; ++kk) {
+    const float* brow = B + kk * N + n0;
+    for (int64_t r = 0; r < mr; ++r) {
+      const float av = A[(m0 + r) * K + kk];
+      float* __restrict__ ar = acc[r];
+      for (int64_t j = 0; j < nn; ++j) ar[j] += av * brow[j];
+    }
+  }
+  for (int64_t r = 0; r < mr; ++r)
+    for (int64_t j = 0; j < nn; ++j) C[(m0 + r) * N + n0 + j] = acc[r][j];
+}
+
 static void matmul_f64(const float* A, const float* B, float* C, int64_t batch, int64_t M, int64_t K, int64_t N,
                        bool batched) {
   constexpr int64_t MR = 4, NB = 256;
+  if (g_matmul_f32) {
+    const int64_t mblocks = (M + MR - 1) / MR, nblocks = (N + NB - 1) / NB;
+    for (int64_t bi = 0; bi < batch; ++bi) {
+      const float* Bb = B + (batched ? bi * K * N : 0);
+      for (int64_t nbk = 0; nbk < nblocks; ++nbk) {
+        const int64_t n0 = nbk * NB, nn = std::min(NB, N - n0);
+#pragma omp parallel for schedule(static)
+        for (int64_t mb = 0; mb < mblocks; ++mb)
+          matmul_block_f32(A + bi * M * K, Bb, C + bi * M * N, M, K, N, mb * MR, std::min(MR, M - mb * MR), n0, nn);
+      }
+    }
+    return;
+  }
   const int64_t mblocks = (M + MR - 1) / MR, nblocks = (N + NB - 1) / NB;
   for (int64_t bi = 0; bi < batch; ++bi) {
     const float* Bb = B + (batched ? bi * K * N : 0);
@@ -797,11 +840,13 @@ Val Oracle::eval_op(const JV& op, const std::map<std::string, Val>& inputs) {
         base += cd * astr[d];
       }
       float s = 0.0f;
+      double sd = 0.0;   // the fixtures' f64-sum twin (orc_set_sum_f64): one rounding at the end
       std::vector<int64_t> ctr(reduced.size(), 0);
       for (;;) {
         int64_t off = base;
         for (size_t q = 0; q < reduced.size(); ++q) off += ctr[q] * astr[reduced[q]];
-        s = (float)((double)s + a.num(off));
+        if (g_sum_f64) sd += a.num(off);
+        else s = (float)((double)s + a.num(off));
         int64_t q = (int64_t)reduced.size() - 1;
         for (; q >= 0; --q) {
           if (++ctr[q] < as[reduced[q]]) break;
@@ -809,7 +854,7 @@ Val Oracle::eval_op(const JV& op, const std::map<std::string, Val>& inputs) {
         }
         if (q < 0) break;
       }
-      o.f()[c] = s;
+      o.f()[c] = g_sum_f64 ? (float)sd : s;
     }
     return o;
   }
@@ -1077,6 +1122,9 @@ using orc::Val;
 extern "C" {
 
 const char* orc_last_error() { return orc::g_err.c_str(); }
+
+void orc_set_matmul_f32(int on) { orc::g_matmul_f32 = on != 0; }
+void orc_set_sum_f64(int on) { orc::g_sum_f64 = on != 0; }
 
 void orc_set_threads(int n) {
 #ifdef _OPENMP

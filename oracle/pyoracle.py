@@ -41,6 +41,8 @@ def lib():
         L.orc_set_lr.argtypes = [ctypes.c_void_p, ctypes.c_char_p]
         L.orc_reset_optimizer.argtypes = [ctypes.c_void_p]
         L.orc_set_threads.argtypes = [ctypes.c_int]
+        L.orc_set_matmul_f32.argtypes = [ctypes.c_int]
+        L.orc_set_sum_f64.argtypes = [ctypes.c_int]
         L.orc_pcg_f64.restype = ctypes.c_uint32
         L.orc_pcg_f64.argtypes = [ctypes.c_uint32] * 3
         L.orc_pcg_imul2.argtypes = [ctypes.c_uint32] * 3 + [ctypes.POINTER(ctypes.c_uint32)] * 2
@@ -54,6 +56,16 @@ def lib():
 
 def set_threads(n: int) -> None:
     lib().orc_set_threads(n)
+
+
+def set_matmul_f32(on: bool) -> None:
+    """Matmuls accumulate in f32 (the parity fixtures' f32 twin); off by default."""
+    lib().orc_set_matmul_f32(1 if on else 0)
+
+
+def set_sum_f64(on: bool) -> None:
+    """sum_to_shape accumulates in f64 (the parity fixtures' f64-sum twin); off by default."""
+    lib().orc_set_sum_f64(1 if on else 0)
 
 
 def _pack_inputs(inputs: Dict[str, np.ndarray]):

@@ -24,16 +24,33 @@ def rel_err(got, want, what: str = 'value') -> float:
     return float(np.linalg.norm(g - w) / max(np.linalg.norm(w), 1e-30))
 
 
-def sign_ambiguous(diff, lr: float, steps: int) -> np.ndarray:
+def sign_ambiguous(diff, lr: float, steps: int, upd=None) -> np.ndarray:
     """Parameter elements whose difference is that of Adam updates gone opposite ways.
 
     Adam's first updates are lr * g / (|g| + eps), about lr * sign(g): a gradient entry
     inside the f32 rounding noise of its GEMM can move either way by lr. Such an element
     differs by at least lr/4 (ordinary differences are ~1e-7) and by at most 2.5 * lr *
     steps (two opposite updates of size lr per step, plus slack); a larger difference is
-    never excused."""
+    never excused. Later updates are lrt * m / (sqrt(v) + eps), smaller than lr where the
+    element's gradient is mostly noise (m near zero) and the bias correction lrt / lr is
+    below 1: given the elements' own update sizes `upd` (from the optimizer state), a
+    difference of at least half the element's update also counts as updates gone opposite
+    ways."""
     a = np.abs(np.asarray(diff, np.float64))
-    return (a >= lr / 4) & (a <= 2.5 * lr * steps)
+    floor = lr / 4 if upd is None else np.minimum(lr / 4, np.asarray(upd, np.float64) / 2)
+    return (a >= floor) & (a <= 2.5 * lr * steps)
+
+
+def adam_update_sizes(state: dict, name: str, idx, opt: dict, steps: int):
+    """|lrt * m / (sqrt(v) + eps)| of parameter `name`'s elements `idx` at step `steps`,
+    from a downloaded optimizer state (None when the state has no Adam moments for it)."""
+    m, v = state.get(f'adam_m_{name}'), state.get(f'adam_v_{name}')
+    if m is None or v is None:
+        return None
+    b1, b2, eps = opt.get('beta1', 0.9), opt.get('beta2', 0.999), opt.get('eps', 1e-8)
+    lrt = opt['lr'] * np.sqrt(1 - b2 ** steps) / (1 - b1 ** steps)
+    m, v = m.astype(np.float64)[idx], v.astype(np.float64)[idx]
+    return np.abs(lrt * m / (np.sqrt(v) + eps))
 
 
 class HipBuffers:

@@ -16,7 +16,12 @@ step-100 values (same indices) measure how far the workload itself amplifies suc
 difference over 100 steps ('twin_losses' [n, steps], 'twin:<param>' [n, sample],
 'twin_norm:<param>' [n]). The test bounds each tensor by its farthest twin, so that
 spread is estimated from several samples: four for the eight-layer NeRF MLP, two for the
-CNN.
+CNN. For the configs in ARITH_TWINS more twins train from the unperturbed parameters with
+another valid rounding at every step rather than once: 'f32', every matmul accumulated in
+f32 (pyoracle.set_matmul_f32), as f32 GPU kernels accumulate (the reference's own WGSL
+kernels among them); 'sum64', sum_to_shape (the bias and LayerNorm-parameter gradients)
+accumulated in f64 and rounded once (pyoracle.set_sum_f64) instead of the evaluator's f32
+running sum, as this backend's column sums do. 'twin_kinds' names each twin.
 
     python tests/golden/make_full_parity.py [keys...] [--threads N]
     python tests/golden/make_full_parity.py nerf --add-twins   # train only the missing twins
@@ -42,6 +47,8 @@ FULL_LIMIT = 16_384
 SAMPLE = 4096
 WHOLE = {'char_mlp'}
 NTWIN = {'cnn': 2, 'nerf': 4}
+ARITH_TWINS = {'nerf': ('f32', 'sum64')}
+SWITCHES = {'f32': pyoracle.set_matmul_f32, 'sum64': pyoracle.set_sum_f64}
 
 
 def sample_indices(key: str, name: str, n: int) -> np.ndarray:
@@ -95,14 +102,29 @@ def make(key: str) -> str:
 
 
 def add_twins(key: str, cfg, ir, p0: dict, out: dict, have: int):
-    """Train twins have .. NTWIN[key] - 1 and append them to the fixture dict `out`."""
+    """Train the one-ulp twins have .. NTWIN[key] - 1 and the ARITH_TWINS kinds the
+    fixture lacks, and append them to the fixture dict `out`."""
     shapes = ir.param_shapes()
     sizes = {n: int(np.prod(shapes[n])) if shapes[n] else 1 for n in ir.param_names}
-    runs = [train(key, cfg, ir, one_ulp(p0, j), f' twin {j}') for j in range(have, NTWIN[key])]
+    kinds = [str(k) for k in out['twin_kinds']] if 'twin_kinds' in out else ['ulp'] * have
+    runs, new_kinds = [], []
+    for j in range(have, NTWIN[key]):
+        runs.append(train(key, cfg, ir, one_ulp(p0, j), f' twin {j}'))
+        new_kinds.append('ulp')
+    for kind in ARITH_TWINS.get(key, ()):
+        if kind in kinds:
+            continue
+        SWITCHES[kind](True)
+        try:
+            runs.append(train(key, cfg, ir, p0, f' {kind} twin'))
+        finally:
+            SWITCHES[kind](False)
+        new_kinds.append(kind)
     if not runs:
         return
     new_l = np.stack([tl for _, tl in runs])
     out['twin_losses'] = np.concatenate([out['twin_losses'], new_l]) if have else new_l
+    out['twin_kinds'] = np.array(kinds + new_kinds)
     for n in ir.param_names:
         vs = [t.get_home(n, sizes[n]) for t, _ in runs]
         val = np.stack([v[out[f'idx:{n}']] for v in vs])
@@ -116,7 +138,8 @@ def extend(key: str) -> str:
     path = os.path.join(HERE, f'full_{key}.npz')
     with np.load(path) as z:
         out = {k: z[k] for k in z.files}
-    have = out['twin_losses'].shape[0] if 'twin_losses' in out else 0
+    have = int(np.sum(out['twin_kinds'] == 'ulp')) if 'twin_kinds' in out else (
+        out['twin_losses'].shape[0] if 'twin_losses' in out else 0)
     cfg = configs.CONFIGS[key]
     ir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer)
     add_twins(key, cfg, ir, ir.initial_params(configs.INIT_SEED), out, have)

@@ -122,6 +122,19 @@ def test_parity_helpers_reject_non_finite_and_bound_the_exclusion():
     d = np.array([1e-7, lr / 4, 2 * lr, 2.5 * lr * steps, 2.5 * lr * steps * 1.01, 1.0])
     assert sign_ambiguous(d, lr, steps).tolist() == [False, True, True, True, False, False]
     assert sign_ambiguous(-d, lr, steps).tolist() == [False, True, True, True, False, False]
+    # with the elements' own update sizes the floor is half an update (never above lr/4);
+    # the ceiling does not move
+    upd = np.full(d.shape, lr / 10)
+    assert sign_ambiguous(np.full(6, lr / 16), lr, steps, upd).all()
+    assert not sign_ambiguous(np.full(6, lr / 32), lr, steps, upd).any()
+    assert sign_ambiguous(d, lr, steps, np.full(6, 4 * lr)).tolist() == [False, True, True, True, False, False]
+    from _helpers import adam_update_sizes
+    opt = {'lr': lr}
+    st = {'adam_m_w': np.array([0.5, -2.0, 0.0], np.float32), 'adam_v_w': np.array([4.0, 1.0, 1.0], np.float32)}
+    lrt = lr * np.sqrt(1 - 0.999 ** steps) / (1 - 0.9 ** steps)
+    u = adam_update_sizes(st, 'w', np.arange(3), opt, steps)
+    assert np.allclose(u, [lrt * 0.5 / (2 + 1e-8), lrt * 2 / (1 + 1e-8), 0.0])
+    assert adam_update_sizes(st, 'other', np.arange(3), opt, steps) is None
 
 
 def test_several_streams_are_rejected(monkeypatch):
@@ -183,3 +196,34 @@ def test_loss_gradient_rows_join_the_loss_rows():
     nodes = backend.plan(ir.wire_json())['nodes']
     assert [n['ops'] for n in nodes if n['kind'] == 'fused' and n['shape'].startswith('[256,1]')] == \
         ['add,sub,mul,mul,mul,add']
+
+
+def test_groups_merge_only_where_their_inputs_exist():
+    """A later group joins an earlier one of the same shape only when everything it reads
+    exists where the earlier group runs: reading the earlier group's result and constants
+    merges; reading a product computed after the earlier group does not."""
+    import sys
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from _helpers import wire
+    from tensorgrad_amd import ir as IR
+    from tensorgrad_amd import ops as O
+    from tensorgrad_amd.trace import tensor_input, trace_fn
+
+    def plan_groups(body):
+        nodes = backend.plan(IR.dumps(wire(trace_fn(body))))['nodes']
+        return [(n['kind'], n.get('ops', '')) for n in nodes]
+
+    def merges():   # b = 2 h + 3 reads only h and constants
+        h = O.relu(O.add_scalar(tensor_input('x', [64, 32]), 1.0))
+        g = O.matmul(h, tensor_input('w', [32, 32]))
+        return [g, O.add_scalar(O.mul_scalar(h, 2.0), 3.0)]
+
+    def stays_apart():  # b = 2 g + h reads the product g, computed after h's group
+        h = O.relu(O.add_scalar(tensor_input('x', [64, 32]), 1.0))
+        g = O.matmul(h, tensor_input('w', [32, 32]))
+        return O.add(O.mul_scalar(g, 2.0), h)
+
+    fused = [k for k in plan_groups(merges) if k[0] in ('fused', 'elementwise')]
+    assert len(fused) == 1 and fused[0][1] == 'add_scalar,relu,mul_scalar,add_scalar', fused
+    kinds = plan_groups(stays_apart)
+    assert [k for k, _ in kinds] == ['fused', 'gemm', 'fused'], kinds
