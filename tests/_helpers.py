@@ -33,11 +33,11 @@ def sign_ambiguous(diff, lr: float, steps: int, upd=None) -> np.ndarray:
     steps (two opposite updates of size lr per step, plus slack); a larger difference is
     never excused. Later updates are lrt * m / (sqrt(v) + eps), smaller than lr where the
     element's gradient is mostly noise (m near zero) and the bias correction lrt / lr is
-    below 1: given the elements' own update sizes `upd` (from the optimizer state), a
-    difference of at least half the element's update also counts as updates gone opposite
-    ways."""
+    below 1: given the elements' own update sizes `upd` (from the optimizer state), the
+    floor is half the element's update, kept within [lr/16, lr/4] (lr/16 is still two
+    orders of magnitude above rounding-sized differences at every benchmark lr)."""
     a = np.abs(np.asarray(diff, np.float64))
-    floor = lr / 4 if upd is None else np.minimum(lr / 4, np.asarray(upd, np.float64) / 2)
+    floor = lr / 4 if upd is None else np.clip(np.asarray(upd, np.float64) / 2, lr / 16, lr / 4)
     return (a >= floor) & (a <= 2.5 * lr * steps)
 
 

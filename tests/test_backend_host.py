@@ -122,11 +122,13 @@ def test_parity_helpers_reject_non_finite_and_bound_the_exclusion():
     d = np.array([1e-7, lr / 4, 2 * lr, 2.5 * lr * steps, 2.5 * lr * steps * 1.01, 1.0])
     assert sign_ambiguous(d, lr, steps).tolist() == [False, True, True, True, False, False]
     assert sign_ambiguous(-d, lr, steps).tolist() == [False, True, True, True, False, False]
-    # with the elements' own update sizes the floor is half an update (never above lr/4);
+    # with the elements' own update sizes the floor is half an update, within [lr/16, lr/4];
     # the ceiling does not move
-    upd = np.full(d.shape, lr / 10)
-    assert sign_ambiguous(np.full(6, lr / 16), lr, steps, upd).all()
-    assert not sign_ambiguous(np.full(6, lr / 32), lr, steps, upd).any()
+    upd = np.full(d.shape, lr / 5)
+    assert sign_ambiguous(np.full(6, lr / 10), lr, steps, upd).all()
+    assert not sign_ambiguous(np.full(6, lr / 11), lr, steps, upd).any()
+    assert not sign_ambiguous(np.full(6, lr / 17), lr, steps, np.zeros(6)).any()
+    assert sign_ambiguous(np.full(6, lr / 16), lr, steps, np.zeros(6)).all()
     assert sign_ambiguous(d, lr, steps, np.full(6, 4 * lr)).tolist() == [False, True, True, True, False, False]
     from _helpers import adam_update_sizes
     opt = {'lr': lr}

@@ -167,8 +167,9 @@ def test_full_config_100_steps(key):
     Bar: every step's loss within 1e-4 relative; every tensor's values (whole or sampled)
     within 1e-4 relative (L2) and its norm within 1e-4, after setting aside the elements
     whose difference is that of Adam updates gone opposite ways (sign_ambiguous: at least
-    lr/4, or half the element's own update at step 100 from the downloaded Adam moments,
-    and at most 2.5 * lr * 100). Those are printed, counted and bounded.
+    half the element's own update at step 100, from the downloaded Adam moments, kept
+    within [lr/16, lr/4], and at most 2.5 * lr * 100). Those are printed, counted and
+    bounded.
 
     Where the fixture also holds the oracle's twins, the workload's own amplification of a
     rounding-sized difference is known: one-ulp twins (the evaluator trained again from
