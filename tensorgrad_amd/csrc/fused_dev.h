@@ -50,6 +50,66 @@ typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ unsigned fbits(float x) { return __float_as_uint(x); }
 __device__ __forceinline__ float bitsf(unsigned x) { return __uint_as_float(x); }
 
+// ---- wavefront butterflies -------------------------------------------------------------------
+// Sum or max over the 64 lanes of a wavefront, every lane receiving the result, as the
+// butterfly over lane distances 32, 16, 8, 4, 2, 1: at distance d each lane combines its
+// value with lane ^ d's. Both lanes of a pair combine the same two values with a commutative
+// operation, so afterwards every lane holds the same bits as lane ^ d, and cheaper moves than
+// an xor shuffle through LDS give the same result bit for bit: permlane32_swap and
+// permlane16_swap hand each lane its own value and its partner's (in either order) for 32
+// and 16; DPP row rotations by 8 and 4 within a 16-lane row for 8 and 4 (after distance 8
+// a row's values repeat with period 8, so the rotation by 4 brings lane ^ 4's value); DPP
+// quad permutations for 2 and 1.
+constexpr int kDppRor8 = 0x128, kDppRor4 = 0x124, kDppQuadXor2 = 0x4E, kDppQuadXor1 = 0xB1;
+
+template <int Ctrl> __device__ __forceinline__ unsigned dpp_u32(unsigned v) {
+  return (unsigned)__builtin_amdgcn_mov_dpp((int)v, Ctrl, 0xF, 0xF, false);
+}
+template <int Ctrl> __device__ __forceinline__ float dpp_move(float v) { return bitsf(dpp_u32<Ctrl>(fbits(v))); }
+template <int Ctrl> __device__ __forceinline__ double dpp_move(double v) {
+  const unsigned long long u = (unsigned long long)__double_as_longlong(v);
+  const unsigned long long lo = dpp_u32<Ctrl>((unsigned)u), hi = dpp_u32<Ctrl>((unsigned)(u >> 32));
+  return __longlong_as_double((long long)((hi << 32) | lo));
+}
+// {a, b} = {own value, value of lane ^ 32} (Half false) or lane ^ 16 (Half true)
+template <bool Half> __device__ __forceinline__ void lane_pair(float v, float& a, float& b) {
+  const auto p = Half ? __builtin_amdgcn_permlane16_swap(fbits(v), fbits(v), false, false)
+                      : __builtin_amdgcn_permlane32_swap(fbits(v), fbits(v), false, false);
+  a = bitsf(p[0]);
+  b = bitsf(p[1]);
+}
+template <bool Half> __device__ __forceinline__ void lane_pair(double v, double& a, double& b) {
+  const unsigned long long u = (unsigned long long)__double_as_longlong(v);
+  const unsigned lo = (unsigned)u, hi = (unsigned)(u >> 32);
+  const auto pl = Half ? __builtin_amdgcn_permlane16_swap(lo, lo, false, false)
+                       : __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
+  const auto ph = Half ? __builtin_amdgcn_permlane16_swap(hi, hi, false, false)
+                       : __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
+  a = __longlong_as_double((long long)(((unsigned long long)ph[0] << 32) | pl[0]));
+  b = __longlong_as_double((long long)(((unsigned long long)ph[1] << 32) | pl[1]));
+}
+struct WaveAdd {
+  template <class T> __device__ __forceinline__ T operator()(T x, T y) const { return x + y; }
+};
+struct WaveMax {
+  __device__ __forceinline__ float operator()(float x, float y) const { return fmaxf(x, y); }
+};
+template <class T, class Op> __device__ __forceinline__ T wave_allreduce(T v, Op op) {
+  T a, b;
+  lane_pair<false>(v, a, b);
+  v = op(a, b);
+  lane_pair<true>(v, a, b);
+  v = op(a, b);
+  v = op(v, dpp_move<kDppRor8>(v));
+  v = op(v, dpp_move<kDppRor4>(v));
+  v = op(v, dpp_move<kDppQuadXor2>(v));
+  v = op(v, dpp_move<kDppQuadXor1>(v));
+  return v;
+}
+__device__ __forceinline__ double wave_allsum(double v) { return wave_allreduce(v, WaveAdd()); }
+__device__ __forceinline__ float wave_allsum(float v) { return wave_allreduce(v, WaveAdd()); }
+__device__ __forceinline__ float wave_allmax(float v) { return wave_allreduce(v, WaveMax()); }
+
 __device__ __forceinline__ double js_max(double a, double b) {
   if (isnan(a) || isnan(b)) return __longlong_as_double(0x7ff8000000000000LL);
   if (a == 0.0 && b == 0.0) return (signbit(a) && signbit(b)) ? -0.0 : 0.0;

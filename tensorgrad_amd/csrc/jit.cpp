@@ -196,7 +196,7 @@ JitKernel fused_kernel(const FusedProgram& p, const FusedInstr* code, int64_t n)
           const std::string c = live(e);
           o << I << "  " << (c.empty() ? "" : "if (" + c + ") ") << "s += (double)tgk::bitsf(" << a << "[" << e << "]);\n";
         }
-        o << I << "  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);\n";
+        o << I << "  s = tgk::wave_allsum(s);\n";
         o << I << "  const unsigned w = tgk::fbits((float)(s / " << dlit(in.imm) << "));\n";
         for (int e = 0; e < N; ++e) o << I << "  " << v << "[" << e << "] = w;\n";
       } else {
@@ -211,12 +211,12 @@ JitKernel fused_kernel(const FusedProgram& p, const FusedInstr* code, int64_t n)
         o << I << "  float mx = tgk::bitsf(0xff800000u);\n";
         o << I << "#pragma unroll\n" << I << "  for (int e = 0; e < " << N << "; ++e)\n"
           << I << "    if (in_row[e]) mx = fmaxf(mx, tgk::bitsf(" << a << "[e]));\n";
-        o << I << "  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));\n";
+        o << I << "  mx = tgk::wave_allmax(mx);\n";
         o << I << "  double ex[" << N << "];\n" << I << "  double s = 0.0;\n";
         o << I << "#pragma unroll\n" << I << "  for (int e = 0; e < " << N << "; ++e) {\n"
           << I << "    ex[e] = in_row[e] ? exp((double)tgk::bitsf(" << a << "[e]) - (double)mx) : 0.0;\n"
           << I << "    if (in_row[e]) s += ex[e];\n" << I << "  }\n";
-        o << I << "  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);\n";
+        o << I << "  s = tgk::wave_allsum(s);\n";
         if (causal) {
           o << I << "#pragma unroll\n" << I << "  for (int e = 0; e < " << N << "; ++e) " << v
             << "[e] = in_row[e] ? tgk::fbits((float)(ex[e] / s)) : 0u;\n";

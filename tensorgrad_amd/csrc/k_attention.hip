@@ -142,9 +142,8 @@ __global__ __launch_bounds__(kNT) void k_attn_fwd(const AttnDesc a) {
           if (in_row[w][u]) mx[w] = fmaxf(mx[w], x[w][u]);
         }
       }
-      for (int o = 32; o > 0; o >>= 1)
 #pragma unroll
-        for (int w = 0; w < RW; ++w) mx[w] = fmaxf(mx[w], __shfl_xor(mx[w], o, 64));
+      for (int w = 0; w < RW; ++w) mx[w] = wave_allmax(mx[w]);
       double ex[RW][V], sum[RW];
 #pragma unroll
       for (int w = 0; w < RW; ++w) {
@@ -155,9 +154,8 @@ __global__ __launch_bounds__(kNT) void k_attn_fwd(const AttnDesc a) {
           if (in_row[w][u]) sum[w] += ex[w][u];
         }
       }
-      for (int o = 32; o > 0; o >>= 1)
 #pragma unroll
-        for (int w = 0; w < RW; ++w) sum[w] += __shfl_xor(sum[w], o, 64);
+      for (int w = 0; w < RW; ++w) sum[w] = wave_allsum(sum[w]);
 #pragma unroll
       for (int w = 0; w < RW; ++w) {
         const int il = wave * RPW + rr + w, i = i0 + il;
@@ -380,9 +378,8 @@ __global__ __launch_bounds__(kNT) void k_attn_bwd_a(const AttnBwdDesc a) {
         sum[w] += (double)(bitsf(v0[w][u]) * bitsf(pv[w][u]));
       }
     }
-    for (int o = 32; o > 0; o >>= 1)
 #pragma unroll
-      for (int w = 0; w < RPW; ++w) sum[w] += __shfl_xor(sum[w], o, 64);
+    for (int w = 0; w < RPW; ++w) sum[w] = wave_allsum(sum[w]);
 #pragma unroll
     for (int w = 0; w < RPW; ++w) {
       const int il = wave * RPW + w;

@@ -200,8 +200,7 @@ __global__ __launch_bounds__(256) void k_conv_wgrad_reduce_wave(const float* __r
   if (i >= per_split) return;                                      // uniform across the wavefront
   float s = 0.0f;
   for (int sp = lane; sp < splits; sp += 64) s += work[sp * per_split + i];
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
+  s = wave_allsum(s);
   if (lane == 0) dw[i] = s;
 }
 

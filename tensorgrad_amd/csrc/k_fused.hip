@@ -151,8 +151,7 @@ __device__ __forceinline__ void run_program(ConstCode code, int n_instr, uint32_
 #pragma unroll
           for (int e = 0; e < N; ++e)
             if ((live >> e) & 1u) s += (double)bitsf(X_[e]);
-#pragma unroll
-          for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+          s = wave_allsum(s);
           if (TPR > 64) {
             if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
             __syncthreads();
@@ -194,8 +193,7 @@ __device__ __forceinline__ void run_program(ConstCode code, int n_instr, uint32_
             in_row[e] = ((live >> e) & 1u) && (!causal || lane + e * 64 <= row_q);
             if (in_row[e]) mx = fmaxf(mx, bitsf(X_[e]));
           }
-#pragma unroll
-          for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+          mx = wave_allmax(mx);
           double ex[N];
           double s = 0.0;
 #pragma unroll
@@ -203,8 +201,7 @@ __device__ __forceinline__ void run_program(ConstCode code, int n_instr, uint32_
             ex[e] = in_row[e] ? exp((double)bitsf(X_[e]) - (double)mx) : 0.0;
             if (in_row[e]) s += ex[e];
           }
-#pragma unroll
-          for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+          s = wave_allsum(s);
           if (causal) {
 #pragma unroll
             for (int e = 0; e < N; ++e) X_[e] = in_row[e] ? fbits((float)(ex[e] / s)) : 0u;

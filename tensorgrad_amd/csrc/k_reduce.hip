@@ -15,14 +15,8 @@ namespace {
 constexpr int kWave = 64;
 constexpr int kRowsPerBlock = 4;   // 256 threads
 
-__device__ __forceinline__ double wave_sum(double v) {
-  for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-  return v;
-}
-__device__ __forceinline__ float wave_max(float v) {
-  for (int o = kWave / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
-  return v;
-}
+__device__ __forceinline__ double wave_sum(double v) { return wave_allsum(v); }
+__device__ __forceinline__ float wave_max(float v) { return wave_allmax(v); }
 
 inline int blocks_for_rows(int64_t rows) {
   int64_t b = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
