@@ -211,6 +211,9 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint32_t b, const E
   static_assert(TM >= 1 && TN >= 1, "wave tile below 32 x 32");
   static_assert(KG == 1 || (KG == 2 && NS % 2 == 0), "k groups take alternate slots");
   constexpr int NSG = NS / KG;            // slots per k group
+  // A group refills a slot right after the barrier that ends its reads of the slot's
+  // previous stage, so it needs a second slot to multiply from meanwhile.
+  static_assert(NS % KG == 0 && NSG >= 2, "every k group needs at least two ring slots");
   constexpr int NG = BK / 8;
   using TA = DTile<BM, BK, AK, GT, ADW>;
   using TB = DTile<BN, BK, BKF, GT, BDW>;
