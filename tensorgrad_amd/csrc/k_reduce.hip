@@ -268,6 +268,7 @@ __global__ void k_sum_finish(const double* __restrict__ part, float* __restrict_
 // counter at zero for the next one.
 constexpr int kColWaves = 8;
 constexpr int kColThreads = kColWaves * 64;
+constexpr int kColRows = 4;
 
 __global__ __launch_bounds__(kColThreads) void k_colsum(const ColSumBatch batch) {
   int z = 0;
@@ -292,21 +293,23 @@ __global__ __launch_bounds__(kColThreads) void k_colsum(const ColSumBatch batch)
     int64_t r = r0 + w;
     if (cs.aligned) {
       typedef float f4 __attribute__((ext_vector_type(4)));
-      for (; r < r1; r += 8 * NW) {   // eight rows in flight, added in row order
-        f4 v[8];
+      // kColRows rows in flight, added in row order; few enough registers that four
+      // blocks share a CU, so a batch's blocks run in one round
+      for (; r < r1; r += kColRows * NW) {
+        f4 v[kColRows];
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
+        for (int u = 0; u < kColRows; ++u)
           v[u] = r + NW * u < r1 ? *reinterpret_cast<const f4*>(p + (r + NW * u) * rs) : f4{0.f, 0.f, 0.f, 0.f};
         if (q) {
-          f4 m[8];
+          f4 m[kColRows];
 #pragma unroll
-          for (int u = 0; u < 8; ++u)
+          for (int u = 0; u < kColRows; ++u)
             m[u] = r + NW * u < r1 ? *reinterpret_cast<const f4*>(q + (r + NW * u) * rs) : f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int u = 0; u < 8; ++u) v[u] = v[u] * m[u];
+          for (int u = 0; u < kColRows; ++u) v[u] = v[u] * m[u];
         }
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
+        for (int u = 0; u < kColRows; ++u)
           if (r + NW * u < r1)
 #pragma unroll
             for (int e = 0; e < 4; ++e) s[e] += (double)v[u][e];
