@@ -34,6 +34,7 @@
 // gradients) use a deterministic split-K: each split writes its own partial tile and a
 // second kernel sums the partials in split order (no atomics).
 #include "kernels.h"
+#include "scatter_dev.h"
 
 #include <stdexcept>
 #include <cstdlib>
@@ -823,73 +824,14 @@ __global__ void k_segment_finish(const double* __restrict__ part, int64_t N, int
 }
 
 // Small vocabularies (V * rows <= kScatterScanMax) need no sort: block (v, column chunk)
-// walks idx in windows of kScanRows rows. Each of its four wavefronts ballots the rows of
-// its quarter of the window whose token is v; the quarters' counts give each wavefront
-// its offset, so the hits land in LDS as one list in row order. Then every thread adds
-// its column of the listed rows to an f64 accumulator, in list order, kScanLoads loads in
-// flight. The additions happen in increasing row order, the order of the one-hot
-// product's k loop. One launch, no workspace.
-constexpr int kScanRows = 4096;
-constexpr int kScanLoads = 32;
+// of four wavefronts runs scatter_scan_block (scatter_dev.h). One launch, no workspace.
 constexpr int64_t kScatterScanMax = int64_t(1) << 22;
 
 __global__ __launch_bounds__(256) void k_scatter_scan(const int32_t* __restrict__ idx, int64_t rows,
                                                       const float* __restrict__ dy, int64_t N,
                                                       float* __restrict__ out) {
-  constexpr int Q = kScanRows / 4;     // rows per wavefront per window
-  constexpr int U = kScanLoads;
-  __shared__ int32_t hits[kScanRows];
-  __shared__ int nhit[4];
-  const int v = blockIdx.x;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int64_t c = blockIdx.y * 256ll + threadIdx.x;
-  const bool col = c < N;
-  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
-  double acc = 0.0;
-  for (int64_t r0 = 0; r0 < rows; r0 += kScanRows) {
-    const int64_t qa = r0 + (int64_t)w * Q, qb = min(rows, qa + Q);
-    int32_t t[Q / 64];
-#pragma unroll
-    for (int u = 0; u < Q / 64; ++u) {
-      const int64_t r = qa + u * 64 + lane;
-      t[u] = r < qb ? idx[r] : -1;
-    }
-    uint64_t m[Q / 64];
-    int n = 0;
-#pragma unroll
-    for (int u = 0; u < Q / 64; ++u) {
-      m[u] = __ballot(t[u] == v);
-      n += __popcll(m[u]);
-    }
-    if (lane == 0) nhit[w] = n;
-    __syncthreads();
-    int base = 0, total = 0;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int ck = nhit[k];
-      if (k < w) base += ck;
-      total += ck;
-    }
-#pragma unroll
-    for (int u = 0; u < Q / 64; ++u) {
-      if (t[u] == v) hits[base + __popcll(m[u] & below)] = (int32_t)(qa + u * 64 + lane);
-      base += __popcll(m[u]);
-    }
-    __syncthreads();
-    // Every slot loads (slots past the list repeat its entry j, lanes past N read column
-    // 0), so the U loads issue back to back; slots past the list add +0.0, which leaves
-    // the accumulator (+0.0 or a sum that cannot be -0.0) unchanged.
-    const int64_t cc = col ? c : 0;
-    for (int j = 0; j < total; j += U) {
-      float x[U];
-#pragma unroll
-      for (int u = 0; u < U; ++u) x[u] = dy[(int64_t)hits[j + u < total ? j + u : j] * N + cc];
-#pragma unroll
-      for (int u = 0; u < U; ++u) acc += j + u < total ? (double)x[u] : 0.0;
-    }
-    __syncthreads();   // the next window rewrites hits and nhit
-  }
-  if (col) out[(int64_t)v * N + c] = (float)acc;
+  __shared__ ScatterScanLds<4> L;
+  scatter_scan_block<4>(idx, rows, dy, N, out, (int)blockIdx.x, blockIdx.y * 256ll, L);
 }
 
 inline bool scatter_scans(int64_t rows, int64_t V) { return V * rows <= kScatterScanMax; }
@@ -912,6 +854,8 @@ void gather_rows(const int32_t* idx, int64_t rows, const float* table, int64_t V
   }
   k_gather_rows<<<grid_for(rows * N), 256, 0, st>>>(idx, rows, table, V, N, out);
 }
+
+bool scatter_scan_form(int64_t rows, int64_t V) { return scatter_scans(rows, V); }
 
 int64_t scatter_workspace_bytes(int64_t rows, int64_t V, int64_t N) {
   if (scatter_scans(rows, V)) return 0;

@@ -4,6 +4,7 @@
 // the exact f32 values; argmax keeps the reference's "first maximum wins, a NaN can only
 // win at index 0" semantics under any combination order.
 #include "kernels.h"
+#include "scatter_dev.h"
 
 #include <algorithm>
 #include <cmath>
@@ -271,11 +272,19 @@ constexpr int kColThreads = kColWaves * 64;
 constexpr int kColRows = 4;
 
 __global__ __launch_bounds__(kColThreads) void k_colsum(const ColSumBatch batch) {
+  if ((int)blockIdx.x < batch.sc.blocks) {   // the embedding gradient run beside the sums
+    __shared__ ScatterScanLds<kColWaves> sl;
+    const int v = (int)blockIdx.x % batch.sc.V, cy = (int)blockIdx.x / batch.sc.V;
+    scatter_scan_block<kColWaves>(batch.sc.idx, batch.sc.rows, batch.sc.dy, batch.sc.N, batch.sc.out, v,
+                                  (int64_t)cy * kColThreads, sl);
+    return;
+  }
+  const int bid = (int)blockIdx.x - batch.sc.blocks;
   int z = 0;
   for (int i = 1; i < batch.n; ++i)
-    if ((int)blockIdx.x >= batch.s[i].blk0) z = i;
+    if (bid >= batch.s[i].blk0) z = i;
   const ColSum& cs = batch.s[z];
-  const int loc = (int)blockIdx.x - cs.blk0;
+  const int loc = bid - cs.blk0;
   const int bx = loc % cs.nx, y = loc / cs.nx;
   constexpr int NW = kColWaves;
   __shared__ double red[NW][256];
@@ -546,11 +555,18 @@ int64_t colsum_counters(int64_t C, int64_t R, int terms) {
 }
 
 void colsum_batch(const ColSumBatch& b, hipStream_t st) {
-  if (b.n <= 0) return;
   ColSumBatch bt = b;
-  int64_t blocks = 0;
+  if (bt.n < 0) bt.n = 0;
+  // the scatter's blocks first, then the sums' (numbered from 0 after them)
+  bt.sc.blocks = 0;
+  if (bt.sc.idx && bt.sc.V > 0 && bt.sc.N > 0) {
+    const int64_t ny = (bt.sc.N + kColThreads - 1) / kColThreads;
+    if ((int64_t)bt.sc.V * ny > INT32_MAX / 2) throw std::runtime_error("column sums: scatter too large");
+    bt.sc.blocks = (int)(bt.sc.V * ny);
+  }
+  int64_t blocks = bt.sc.blocks;
   for (int i = 0; i < bt.n; ++i) {
-    bt.s[i].blk0 = (int)blocks;
+    bt.s[i].blk0 = (int)(blocks - bt.sc.blocks);
     blocks += (int64_t)bt.s[i].nx * bt.s[i].nchunks;
   }
   if (blocks <= 0) return;

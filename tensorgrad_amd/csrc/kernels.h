@@ -136,9 +136,20 @@ struct ColSum {
   unsigned* counters;
 };
 constexpr int kColSumMax = 32;
+// An embedding gradient of the scatter_scan_form run by the first `blocks` blocks of a
+// column-sum launch (blocks = V * ceil(N / 512): one block per token and 512 columns), so
+// its latency hides under the sums; idx null: none.
+struct ColSumScatter {
+  const int32_t* idx;
+  const float* dy;
+  float* out;
+  int64_t rows, N;
+  int V, blocks;
+};
 struct ColSumBatch {
   int n;
   ColSum s[kColSumMax];
+  ColSumScatter sc;
 };
 static_assert(sizeof(ColSumBatch) <= 4096, "column-sum batch fits the kernel argument space");
 ColSum colsum_desc(const float* a, const float* b, float* out, int64_t C, int64_t R, int64_t rs, double div,
@@ -250,6 +261,9 @@ void gather_rows(const int32_t* idx, int64_t rows, const float* table, int64_t V
 // order, f64 accumulation (V <= 8192); `work` must hold scatter_workspace_bytes(...)
 // bytes, 256-byte aligned.
 int64_t scatter_workspace_bytes(int64_t rows, int64_t V, int64_t N);
+// The sort-free form (small V * rows): one launch, no workspace; the form a column-sum
+// launch can run beside its sums (ColSumScatter).
+bool scatter_scan_form(int64_t rows, int64_t V);
 void scatter_rows(const int32_t* idx, int64_t rows, const float* dy, int64_t V, int64_t N, float* out, void* work,
                   hipStream_t st);
 

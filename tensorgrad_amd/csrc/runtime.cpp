@@ -455,7 +455,14 @@ class Runtime {
   // Column sums read only by the optimizer (bias, LayerNorm gain / shift gradients) run
   // together with the grouped GEMMs, kColSumMax per launch.
   std::vector<char> defer_colsum_;
-  void emit_colsums(const std::vector<int>& batch);
+  void emit_colsums(const std::vector<int>& batch, bool with_scatter = false);
+  // An embedding gradient (sort-free scatter form) that only the optimizer reads runs in the
+  // first deferred column-sum launch, its blocks ahead of the sums' (TG_COLSUM_SCATTER=0:
+  // a launch of its own in place).
+  struct DeferredScatter { int op, idx, b, out; int64_t rows, V, N; std::string shape; };
+  std::vector<DeferredScatter> deferred_scatter_;
+  bool use_colsum_scatter_ = true;
+  void emit_scatter(const DeferredScatter& sc);
   bool use_gemm_group_ = true;       // TG_GEMM_GROUP=0 keeps every GEMM in place
   bool use_remat_ = true;            // TG_REMAT=0 stores every value another group reads
   bool only_optimizer_reads(int t) const;
@@ -477,6 +484,7 @@ Runtime::Runtime(const char* json, Runtime* par, bool plan_only) : parent(par) {
   if (const char* g = std::getenv("TG_GEMM_GROUP")) use_gemm_group_ = std::string(g) != "0";
   if (const char* g = std::getenv("TG_GEMM_SUM")) use_gemm_sum_ = std::string(g) != "0";
   if (const char* g = std::getenv("TG_REMAT")) use_remat_ = std::string(g) != "0";
+  if (const char* g = std::getenv("TG_COLSUM_SCATTER")) use_colsum_scatter_ = std::string(g) != "0";
   if (const char* g = std::getenv("TG_GEMM_EPI")) use_gemm_epi_ = std::string(g) == "1";
   if (const char* g = std::getenv("TG_FUSED")) use_jit_ = std::string(g) != "vm";
   if (const char* g = std::getenv("TG_CONV")) use_conv_gemm_ = std::string(g) != "direct";
@@ -975,12 +983,22 @@ void Runtime::lower() {
   flush_deferred_gemms();
   {
     std::vector<int> batch;
+    bool scatter_left = !deferred_scatter_.empty();
     for (auto& c : colsum_) {
       if (!defer_colsum_[c.first] || colsum_done_[c.first]) continue;
       batch.push_back(c.first);
-      if ((int)batch.size() == tgk::kColSumMax) { emit_colsums(batch); batch.clear(); }
+      if ((int)batch.size() == tgk::kColSumMax) {
+        emit_colsums(batch, scatter_left);
+        scatter_left = false;
+        batch.clear();
+      }
     }
-    if (!batch.empty()) emit_colsums(batch);
+    if (!batch.empty()) {
+      emit_colsums(batch, scatter_left);
+      scatter_left = false;
+    }
+    if (scatter_left) emit_scatter(deferred_scatter_.front());   // no column sums to join
+    deferred_scatter_.clear();
   }
 
   // Drop nodes whose results nobody reads (e.g. a one_hot consumed only by the
@@ -1937,7 +1955,31 @@ void Runtime::lower_colsums(int s0) {
   emit_colsums(batch);
 }
 
-void Runtime::emit_colsums(const std::vector<int>& batch) {
+void Runtime::emit_scatter(const DeferredScatter& sc) {
+  Node n;
+  n.kind = "scatter";
+  n.op = sc.op;
+  n.shape = sc.shape;
+  n.reads.push_back(root(sc.idx));
+  n.reads.push_back(root(sc.b));
+  n.writes.push_back(root(sc.out));
+  n.flops = 0;
+  n.bytes = 4.0 * (sc.rows + sc.rows * sc.N + sc.V * sc.N);
+  const int64_t wsb = tgk::scatter_workspace_bytes(sc.rows, sc.V, sc.N);
+  workspace_bytes_ = std::max(workspace_bytes_, (size_t)wsb);
+  n.ws = wsb > 0;
+  n.bind = [=]() -> std::function<void(hipStream_t)> {
+    const int32_t* pi = (const int32_t*)dptr(sc.idx);
+    const float* pd = (const float*)dptr(sc.b);
+    float* po = (float*)dptr(sc.out);
+    void* work = cur_ws_;
+    const int64_t rows = sc.rows, V = sc.V, N = sc.N;
+    return [=](hipStream_t st) { tgk::scatter_rows(pi, rows, pd, V, N, po, work, st); };
+  };
+  add_node(std::move(n));
+}
+
+void Runtime::emit_colsums(const std::vector<int>& batch, bool with_scatter) {
   const int s0 = batch.front();
   const ColSumOp& c0 = colsum_.at(s0);
   for (int sop : batch) colsum_done_[sop] = true;
@@ -1965,9 +2007,30 @@ void Runtime::emit_colsums(const std::vector<int>& batch) {
   }
   workspace_bytes_ = std::max(workspace_bytes_, ws);
   n.ws = true;
+  const bool sct = with_scatter && !deferred_scatter_.empty();
+  const DeferredScatter sc = sct ? deferred_scatter_.front() : DeferredScatter{};
+  if (sct) {
+    n.reads.push_back(root(sc.idx));
+    n.reads.push_back(root(sc.b));
+    n.writes.push_back(root(sc.out));
+    n.bytes += 4.0 * (sc.rows + sc.rows * sc.N + sc.V * sc.N);
+    n.detail += ",scatter";
+    n.shape += " + scatter " + sc.shape;
+  }
   n.bind = [=]() -> std::function<void(hipStream_t)> {
     tgk::ColSumBatch bt{};
     bt.n = (int)batch.size();
+    if (sct) {
+      if (T_[root(sc.b)].numel < sc.rows * sc.N || T_[root(sc.out)].numel < sc.V * sc.N ||
+          T_[root(sc.idx)].numel < sc.rows)
+        throw Error(TG_INTERNAL, "embedding gradient: operand smaller than its shape");
+      bt.sc.idx = (const int32_t*)dptr(sc.idx);
+      bt.sc.dy = (const float*)dptr(sc.b);
+      bt.sc.out = (float*)dptr(sc.out);
+      bt.sc.rows = sc.rows;
+      bt.sc.N = sc.N;
+      bt.sc.V = (int)sc.V;
+    }
     for (size_t q = 0; q < batch.size(); ++q) {
       const ColSumOp& c = colsum_.at(batch[q]);
       const int out = O(batch[q]).at("out").i32();
@@ -3002,21 +3065,13 @@ void Runtime::lower_op(int i) {
       int64_t rows = T_[fld(asrc, "indices")].numel, V = O(asrc).at("depth").i64();
       if (va.dims.size() == 2 && va.dims[0] == V && va.dims[1] == rows && va.strides[0] == 1 && va.strides[1] == V &&
           view_[b].contiguous() && V <= 8192) {
-        int idx = fld(asrc, "indices");
-        rd(idx); rd(b);
-        n.kind = "scatter";
-        n.flops = 0;
-        n.bytes = 4.0 * (rows + rows * N + V * N);
-        const int64_t wsb = tgk::scatter_workspace_bytes(rows, V, N);
-        workspace_bytes_ = std::max(workspace_bytes_, (size_t)wsb);
-        n.ws = wsb > 0;
-        n.bind = [=]() -> std::function<void(hipStream_t)> {
-          const int32_t* pi = (const int32_t*)dptr(idx); const float* pd = (const float*)dptr(b);
-          float* po = (float*)dptr(out);
-          void* work = cur_ws_;
-          return [=](hipStream_t st) { tgk::scatter_rows(pi, rows, pd, V, N, po, work, st); };
-        };
-        add_node(std::move(n));
+        const DeferredScatter sc{i, fld(asrc, "indices"), b, out, rows, V, N, n.shape};
+        if (use_gemm_group_ && use_colsum_scatter_ && deferred_scatter_.empty() && tgk::scatter_scan_form(rows, V) &&
+            only_optimizer_reads(out)) {
+          deferred_scatter_.push_back(sc);
+          return;
+        }
+        emit_scatter(sc);
         return;
       }
     }

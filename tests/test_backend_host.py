@@ -38,9 +38,28 @@ def test_plan_lowers_every_config(key):
     gemm_flops = sum(n['flops'] for n in p['nodes'] if n['kind'] == 'gemm')
     assert gemm_flops > 0
     if key in ('char_mlp', 'transformer'):
-        # embeddings become a gather forward and a segmented scatter-add backward
-        assert 'gather' in kinds and 'scatter' in kinds
+        # embeddings become a gather forward and a segmented scatter-add backward; the
+        # scatter, read only by Adam, runs inside the deferred column-sum launch
+        assert 'gather' in kinds
+        merged = [n for n in p['nodes'] if n['kind'] == 'reduce' and '+ scatter' in n['shape']]
+        assert kinds.count('scatter') + len(merged) == 1, kinds
         assert sum(1 for n in p['nodes'] if n['kind'] == 'gemm' and n['shape'].endswith('x[27,24]')) == 0
+
+
+def test_embedding_gradient_joins_the_column_sums(monkeypatch):
+    """The transformer's embedding gradient (read only by Adam) is planned into the launch of
+    the deferred column sums, with its operands among the node's reads and its output among
+    the writes; TG_COLSUM_SCATTER=0 keeps it a launch of its own."""
+    cfg = configs.CONFIGS['transformer']
+    ir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer)
+    nodes = backend.plan(ir.wire_json())['nodes']
+    merged = [n for n in nodes if n['kind'] == 'reduce' and '+ scatter' in n['shape']]
+    assert len(merged) == 1 and 'scatter' not in [n['kind'] for n in nodes]
+    assert merged[0]['ops'].endswith(',scatter')
+    monkeypatch.setenv('TG_COLSUM_SCATTER', '0')
+    nodes = backend.plan(ir.wire_json())['nodes']
+    assert [n['kind'] for n in nodes].count('scatter') == 1
+    assert not any('+ scatter' in n['shape'] for n in nodes)
 
 
 def test_plan_with_gemm_epilogues(monkeypatch):

@@ -140,6 +140,42 @@ def test_recomputed_values_are_bit_identical():
         assert np.array_equal(out['0'][n].view(np.uint32), out['1'][n].view(np.uint32)), n
 
 
+@pytest.mark.parametrize('key', ['char_mlp', 'transformer'])
+def test_embedding_gradient_beside_column_sums(key):
+    """The embedding gradient, which only Adam reads, runs in the first blocks of the
+    launch of the deferred column sums (bias and LayerNorm gradients), by the same block
+    body as its own launch with eight wavefronts instead of four: two full-size training
+    steps give the same parameters bit for bit with it in its own launch
+    (TG_COLSUM_SCATTER=0) and beside the sums."""
+    cfg = configs.CONFIGS[key]
+    ir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer)
+    p0 = ir.initial_params(5)
+    batches = configs.batches(cfg, 2)
+    out = {}
+    for merged in ('0', '1'):
+        old = os.environ.get('TG_COLSUM_SCATTER')
+        os.environ['TG_COLSUM_SCATTER'] = merged
+        try:
+            rt = backend.NativeRuntime(ir.wire_json())
+        finally:
+            if old is None:
+                os.environ.pop('TG_COLSUM_SCATTER', None)
+            else:
+                os.environ['TG_COLSUM_SCATTER'] = old
+        nodes = rt.describe()['nodes']
+        kinds = [n['kind'] for n in nodes]
+        assert ('scatter' in kinds) == (merged == '0'), kinds
+        assert any('+ scatter' in n['shape'] for n in nodes) == (merged == '1')
+        rt.upload_params(p0)
+        for b in batches:
+            rt.step(b)
+        out[merged] = rt.download_params()
+        rt.destroy()
+    for n in ir.param_names:
+        assert np.all(np.isfinite(out['1'][n])), n
+        assert np.array_equal(out['0'][n].view(np.uint32), out['1'][n].view(np.uint32)), n
+
+
 @pytest.mark.parametrize('key', ['mlp_sin', 'char_mlp', 'cnn', 'nerf', 'transformer'])
 def test_small_variant_100_steps(key):
     wl, wp, _ = _train_both(configs.small_variant(key), 100)
