@@ -11,9 +11,12 @@ namespace tgk {
 constexpr int kScanRows = 4096;
 constexpr int kScanLoads = 32;
 
+constexpr int kScanStage = 4096;   // floats of listed rows staged at once (narrow rows)
+
 template <int NW>
 struct ScatterScanLds {
   int32_t hits[kScanRows];
+  float stage[kScanStage];
   int nhit[NW];
 };
 
@@ -66,18 +69,36 @@ __device__ __forceinline__ void scatter_scan_block(const int32_t* __restrict__ i
       base += __popcll(m[u]);
     }
     __syncthreads();
-    // Every slot loads (slots past the list repeat its entry j, lanes past N read column
-    // 0), so the U loads issue back to back; slots past the list add +0.0, which leaves
-    // the accumulator (+0.0 or a sum that cannot be -0.0) unchanged.
-    const int64_t cc = col ? c : 0;
-    for (int j = 0; j < total; j += U) {
-      float x[U];
+    if (c0 == 0 && N * 4 <= NW * 64) {
+      // Narrow rows (N at most a quarter of the block): the whole block copies chunks of the
+      // listed rows into LDS, about kScanStage / (64 NW) loads in flight per thread, then
+      // each column's thread adds its column of the chunk in list order.
+      const int per = kScanStage / (int)N;   // listed rows per chunk
+      for (int j = 0; j < total; j += per) {
+        const int cnt = min(per, total - j);
+        for (int e = threadIdx.x; e < cnt * (int)N; e += NW * 64) {
+          const int h = e / (int)N;
+          L.stage[e] = dy[(int64_t)L.hits[j + h] * N + (e - h * (int)N)];
+        }
+        __syncthreads();
+        if (col)
+          for (int h = 0; h < cnt; ++h) acc += (double)L.stage[h * (int)N + (int)c];
+        __syncthreads();
+      }
+    } else {
+      // Every slot loads (slots past the list repeat its entry j, lanes past N read column
+      // 0), so the U loads issue back to back; slots past the list add +0.0, which leaves
+      // the accumulator (+0.0 or a sum that cannot be -0.0) unchanged.
+      const int64_t cc = col ? c : 0;
+      for (int j = 0; j < total; j += U) {
+        float x[U];
 #pragma unroll
-      for (int u = 0; u < U; ++u) x[u] = dy[(int64_t)L.hits[j + u < total ? j + u : j] * N + cc];
+        for (int u = 0; u < U; ++u) x[u] = dy[(int64_t)L.hits[j + u < total ? j + u : j] * N + cc];
 #pragma unroll
-      for (int u = 0; u < U; ++u) acc += j + u < total ? (double)x[u] : 0.0;
+        for (int u = 0; u < U; ++u) acc += j + u < total ? (double)x[u] : 0.0;
+      }
     }
-    __syncthreads();   // the next window rewrites hits and nhit
+    __syncthreads();   // the next window rewrites hits, nhit and stage
   }
   if (col) out[(int64_t)v * N + c] = (float)acc;
 }
