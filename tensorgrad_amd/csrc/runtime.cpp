@@ -444,11 +444,14 @@ class Runtime {
   void plan_gemm_groups();
   // A GEMM whose product only one element-form group reads (contiguously, in its own
   // iteration order) can run that group in its epilogue: one launch instead of two, and
-  // the product never reaches memory. Opt-in (TG_GEMM_EPI=1): measured on the C4 / C5
-  // groups it is not faster, since the epilogue's per-element loads and stores are 32-bit
-  // and its arithmetic (f64 transcendentals) runs on the GEMM's eight wavefronts per CU
-  // after the matrix work instead of beside other work.
-  bool use_gemm_epi_ = false;
+  // the product never reaches memory. By default only groups of inexpensive ops (adds,
+  // products, relu and the like; C4's bias + relu layers: 385 -> 393 steps/s): a group with
+  // f64 transcendentals or the dropout hash runs them on the GEMM's eight wavefronts per CU
+  // after the matrix work instead of beside other work, which measured slower (C5's GELU,
+  // C2's tanh). TG_GEMM_EPI=1 takes every group the epilogue can run, 0 none.
+  enum { kEpiOff = 0, kEpiAll = 1, kEpiCheap = 2 };
+  int gemm_epi_mode_ = kEpiCheap;
+  bool epi_cheap(int gi) const;
   std::vector<char> group_done_;     // group already run inside a GEMM epilogue
   int epi_group(int op, int out, const tgk::GemmDesc& d, bool& store_c) const;
   void lower_gemm_epi(int op, const tgk::GemmDesc& d, int a, int b, int out, int gi, bool store_c);
@@ -485,7 +488,7 @@ Runtime::Runtime(const char* json, Runtime* par, bool plan_only) : parent(par) {
   if (const char* g = std::getenv("TG_GEMM_SUM")) use_gemm_sum_ = std::string(g) != "0";
   if (const char* g = std::getenv("TG_REMAT")) use_remat_ = std::string(g) != "0";
   if (const char* g = std::getenv("TG_COLSUM_SCATTER")) use_colsum_scatter_ = std::string(g) != "0";
-  if (const char* g = std::getenv("TG_GEMM_EPI")) use_gemm_epi_ = std::string(g) == "1";
+  if (const char* g = std::getenv("TG_GEMM_EPI")) gemm_epi_mode_ = std::string(g) == "1" ? kEpiAll : (std::string(g) == "0" ? kEpiOff : kEpiCheap);
   if (const char* g = std::getenv("TG_FUSED")) use_jit_ = std::string(g) != "vm";
   if (const char* g = std::getenv("TG_CONV")) use_conv_gemm_ = std::string(g) != "direct";
   // A several-stream schedule of the step was tried and crashed inside the HIP runtime
@@ -2396,6 +2399,15 @@ int Runtime::epi_group(int op, int out, const tgk::GemmDesc& d, bool& store_c) c
   return gi;
 }
 
+bool Runtime::epi_cheap(int gi) const {
+  static const std::set<std::string> costly = {"erf", "tanh", "sigmoid", "sin", "cos", "exp", "log", "rsqrt", "dropout"};
+  for (int m : groups_[gi].ops)
+    if (costly.count(kinds_[m])) return false;
+  for (int m : groups_[gi].dups)
+    if (costly.count(kinds_[m])) return false;
+  return true;
+}
+
 void Runtime::lower_gemm_epi(int op, const tgk::GemmDesc& d, int a, int b, int out, int gi, bool store_c) {
   group_done_[gi] = 1;
   const Group G = groups_[gi];
@@ -3100,10 +3112,10 @@ void Runtime::lower_op(int i) {
         return;
       }
     }
-    if (use_gemm_epi_ && use_jit_) {
+    if (gemm_epi_mode_ != kEpiOff && use_jit_) {
       bool store_c = false;
       const int gi = epi_group(i, out, d, store_c);
-      if (gi >= 0) {
+      if (gi >= 0 && (gemm_epi_mode_ == kEpiAll || epi_cheap(gi))) {
         lower_gemm_epi(i, d, a, b, out, gi, store_c);
         return;
       }

@@ -443,7 +443,8 @@ def test_fused_attention_backward(B, H, T):
 def test_gemm_epilogue(M, N, K, act):
     """With TG_GEMM_EPI=1, a product read only by one pointwise group runs that group in
     the GEMM's epilogue (a kernel generated per group): bit-identical to the GEMM and the
-    group run apart (the default), and within GEMM tolerance of the oracle."""
+    group run apart (TG_GEMM_EPI=0), and within GEMM tolerance of the oracle. By default
+    only groups of inexpensive ops (the relu case) run in the epilogue."""
     ins = {'a': _rand([M, K], 101), 'b': _rand([K, N], 102), 'c': _rand([N], 103), 'r': _rand([M, N], 104)}
 
     def body():
@@ -457,9 +458,13 @@ def test_gemm_epilogue(M, N, K, act):
         return O.mul(y, 2.0)
     g = trace_fn(body)
     got, _ = _run_native(g, ins, {'TG_GEMM_EPI': '1'})
-    ref, _ = _run_native(g, ins)
+    ref, _ = _run_native(g, ins, {'TG_GEMM_EPI': '0'})
     ops = _node_ops(g, {'TG_GEMM_EPI': '1'})
     assert any(o.startswith('gemm+') for o in ops), ops
+    assert not any(o.startswith('gemm+') for o in _node_ops(g, {'TG_GEMM_EPI': '0'}))
+    assert any(o.startswith('gemm+') for o in _node_ops(g, {})) == (act == 'relu')
+    auto, _ = _run_native(g, ins)
+    exact(auto, ref)
     exact(got, ref)
     o = pyoracle.OracleRuntime(wire(g))
     o.run(ins)
