@@ -195,7 +195,27 @@ __global__ void k_sum_cols(const float* __restrict__ a, double* __restrict__ par
       for (int u = 0; u < kSumUnroll; ++u) s += (double)v[u];
     }
     for (; r < r1; ++r, p += st) s += (double)*p;
-  } else {
+  } else if (red.rank == 2 && r0 < r1) {
+    // two reduced axes: the index split once, then stepped with a carry (no 64-bit
+    // division per term); kSumUnroll loads in flight, added in index order
+    const int64_t d1 = red.dims[1], s0 = red.s0[0], s1 = red.s0[1];
+    int64_t hi = r0 / d1, lo = r0 - hi * d1;   // r = hi * d1 + lo
+    int64_t r = r0;
+    for (; r + kSumUnroll <= r1; r += kSumUnroll) {
+      float v[kSumUnroll];
+#pragma unroll
+      for (int u = 0; u < kSumUnroll; ++u) {
+        v[u] = a[base + hi * s0 + lo * s1];
+        if (++lo == d1) { lo = 0; ++hi; }
+      }
+#pragma unroll
+      for (int u = 0; u < kSumUnroll; ++u) s += (double)v[u];
+    }
+    for (; r < r1; ++r) {
+      s += (double)a[base + hi * s0 + lo * s1];
+      if (++lo == d1) { lo = 0; ++hi; }
+    }
+  } else if (red.rank != 2) {
     for (int64_t r = r0; r < r1; ++r) s += (double)a[base + red_offset(red, r)];
   }
   if (nchunks == 1) out[c] = (float)(s / div);
@@ -203,7 +223,9 @@ __global__ void k_sum_cols(const float* __restrict__ a, double* __restrict__ par
 }
 
 // Row form: one wavefront per (cell, chunk); lane l sums indices r0 + l, r0 + l + 64, ...
-// in order, then a fixed shuffle tree combines the lanes.
+// in order, then a fixed shuffle tree combines the lanes. (Finishing in each cell's last
+// wavefront, as k_colsum does, measured 4-5x slower here: a hundred or more wavefronts
+// per cell contend for one device-scope counter.)
 __global__ void k_sum_rows(const float* __restrict__ a, double* __restrict__ part, float* __restrict__ out,
                            Strided cells, Strided red, int64_t ncells, int64_t nred, int64_t chunk, int nchunks,
                            double div) {
@@ -229,6 +251,27 @@ __global__ void k_sum_rows(const float* __restrict__ a, double* __restrict__ par
 #pragma unroll
         for (int u = 0; u < kSumUnroll; ++u)
           if (r + u * kWave < r1) s += (double)v[u];
+      }
+    } else if (red.rank == 2) {
+      // two reduced axes: each lane splits its first index once and steps by the
+      // wavefront width with a carry (no 64-bit division per term); kSumUnroll loads in
+      // flight per lane, added in index order
+      const int64_t d1 = red.dims[1], s0 = red.s0[0], s1 = red.s0[1];
+      if (r0 + lane < r1) {
+        int64_t hi = (r0 + lane) / d1, lo = (r0 + lane) - hi * d1;   // index = hi * d1 + lo
+        for (int64_t r = r0 + lane; r < r1; r += kWave * kSumUnroll) {
+          float v[kSumUnroll];
+#pragma unroll
+          for (int u = 0; u < kSumUnroll; ++u) {
+            const int64_t j = r + u * kWave;
+            v[u] = j < r1 ? a[base + hi * s0 + lo * s1] : 0.0f;
+            lo += kWave;
+            while (lo >= d1) { lo -= d1; ++hi; }
+          }
+#pragma unroll
+          for (int u = 0; u < kSumUnroll; ++u)
+            if (r + u * kWave < r1) s += (double)v[u];
+        }
       }
     } else {
       for (int64_t r = r0 + lane; r < r1; r += kWave) s += (double)a[base + red_offset(red, r)];
@@ -575,9 +618,11 @@ void colsum_batch(const ColSumBatch& b, hipStream_t st) {
 }
 
 int64_t sum_counters(const Strided& cells, const Strided& red, int64_t ncells, int64_t nred) {
-  if (!col_form(cells, red)) return 0;
-  ColPlan c = col_plan(ncells, nred, 1);
-  return c.nchunks > 1 ? c.nx : 0;
+  if (col_form(cells, red)) {
+    ColPlan c = col_plan(ncells, nred, 1);
+    return c.nchunks > 1 ? c.nx : 0;
+  }
+  return 0;
 }
 
 void reduce_sum(const float* a, float* out, const Strided& cells, const Strided& red, int64_t ncells, int64_t nred,
