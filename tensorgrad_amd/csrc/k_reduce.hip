@@ -310,6 +310,13 @@ __global__ void k_sum_finish(const double* __restrict__ part, float* __restrict_
 // a column's group takes chunks j, j + TPC, ... in order, then the group in order) and
 // resets its counter, so results do not depend on scheduling and the launch leaves every
 // counter at zero for the next one.
+// f32(sum / div), then the mul_scalar that followed the sum in the graph (f64 product
+// rounded once, as the fused groups' FO_MULS)
+__device__ __forceinline__ float colsum_result(double s, const ColSum& cs) {
+  const float v = (float)(s / cs.div);
+  return cs.scale == 1.0 ? v : (float)((double)v * cs.scale);
+}
+
 constexpr int kColWaves = 8;
 constexpr int kColThreads = kColWaves * 64;
 constexpr int kColRows = 4;
@@ -404,7 +411,7 @@ __global__ __launch_bounds__(kColThreads) void k_colsum(const ColSumBatch batch)
     for (int v = 1; v < NW; ++v) bs += red[v][threadIdx.x];
   }
   if (nchunks == 1) {
-    if ((int)threadIdx.x < ncol) cs.out[cb + threadIdx.x] = (float)(bs / cs.div);
+    if ((int)threadIdx.x < ncol) cs.out[cb + threadIdx.x] = colsum_result(bs, cs);
     return;
   }
   // Partials, the counter and the final reads are device-scope atomic accesses: coherent
@@ -448,7 +455,7 @@ __global__ __launch_bounds__(kColThreads) void k_colsum(const ColSumBatch batch)
     const double* rr = reinterpret_cast<const double*>(red);
     double u = rr[threadIdx.x];
     for (int j = 1; j < tpc; ++j) u += rr[j * cw + threadIdx.x];
-    cs.out[cb + threadIdx.x] = (float)(u / cs.div);
+    cs.out[cb + threadIdx.x] = colsum_result(u, cs);
   }
   if (threadIdx.x == 0) __hip_atomic_store(&cs.counters[bx], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -503,6 +510,9 @@ ColPlan col_plan(int64_t C, int64_t R, int terms) {
   const int64_t row_bytes = std::min<int64_t>(C, 64 * L) * 4 * std::max(terms, 1);
   int64_t rows = (262144 / row_bytes) / kColWaves * kColWaves;
   rows = std::min<int64_t>(std::max<int64_t>(rows, kColWaves), 64 * kColWaves);
+  // Fewer columns than lanes (a loss mean, a small head's bias): most lanes idle, so a
+  // chunk is one round of loads per wavefront and the work spreads over more blocks.
+  if (C < 64) rows = kColWaves * kColRows;
   int64_t n = (R + rows - 1) / rows;
   if (n > 256) n = 256;
   if (n < 1) n = 1;
@@ -583,7 +593,7 @@ ColSum colsum_desc(const float* a, const float* b, float* out, int64_t C, int64_
   c.cpl = col_lanes(C);
   auto al = [](const float* x) { return ((uintptr_t)x & 15) == 0; };
   c.aligned = c.cpl == 4 && rs % 4 == 0 && al(a) && (!b || al(b));
-  c.div = div; c.part = part; c.counters = counters;
+  c.div = div; c.scale = 1.0; c.part = part; c.counters = counters;
   return c;
 }
 

@@ -132,6 +132,7 @@ struct ColSum {
   int aligned;            // cpl == 4 and every row start 16-byte aligned: 128-bit loads
   int blk0;               // first block of this sum in the launch (set by colsum_batch)
   double div;
+  double scale;           // != 1: out = f32(f32(sum / div) * scale), a mul_scalar after the sum
   double* part;
   unsigned* counters;
 };

@@ -458,7 +458,14 @@ class Runtime {
   // Column sums read only by the optimizer (bias, LayerNorm gain / shift gradients) run
   // together with the grouped GEMMs, kColSumMax per launch.
   std::vector<char> defer_colsum_;
-  void emit_colsums(const std::vector<int>& batch, bool with_scatter = false);
+  void emit_colsums(const std::vector<int>& batch, bool with_scatter = false, bool with_rowsums = false);
+  // A row group that only reduces one row to a scalar the graph outputs (the loss mean:
+  // sum_last or mean_last, then optionally mul_scalar) runs as a one-column sum in the first
+  // deferred column-sum launch (TG_COLSUM_LOSS=0: a launch of its own in place).
+  struct DeferredRowSum { int gi, a, out; int64_t R; double div, scale; std::string detail; };
+  std::vector<DeferredRowSum> deferred_rowsum_;
+  bool use_colsum_loss_ = true;
+  bool tail_rowsum(int gi, DeferredRowSum& d) const;
   // An embedding gradient (sort-free scatter form) that only the optimizer reads runs in the
   // first deferred column-sum launch, its blocks ahead of the sums' (TG_COLSUM_SCATTER=0:
   // a launch of its own in place).
@@ -488,6 +495,7 @@ Runtime::Runtime(const char* json, Runtime* par, bool plan_only) : parent(par) {
   if (const char* g = std::getenv("TG_GEMM_SUM")) use_gemm_sum_ = std::string(g) != "0";
   if (const char* g = std::getenv("TG_REMAT")) use_remat_ = std::string(g) != "0";
   if (const char* g = std::getenv("TG_COLSUM_SCATTER")) use_colsum_scatter_ = std::string(g) != "0";
+  if (const char* g = std::getenv("TG_COLSUM_LOSS")) use_colsum_loss_ = std::string(g) != "0";
   if (const char* g = std::getenv("TG_GEMM_EPI")) gemm_epi_mode_ = std::string(g) == "1" ? kEpiAll : (std::string(g) == "0" ? kEpiOff : kEpiCheap);
   if (const char* g = std::getenv("TG_FUSED")) use_jit_ = std::string(g) != "vm";
   if (const char* g = std::getenv("TG_CONV")) use_conv_gemm_ = std::string(g) != "direct";
@@ -977,7 +985,15 @@ void Runtime::lower() {
     }
     int gi = group_of_[i];
     if (gi >= 0) {
-      if (groups_[gi].first == (int)i && !group_done_[gi]) lower_group(gi);
+      if (groups_[gi].first == (int)i && !group_done_[gi]) {
+        DeferredRowSum d{};
+        if (use_gemm_group_ && use_colsum_loss_ && (int)deferred_rowsum_.size() < 4 && tail_rowsum(gi, d)) {
+          deferred_rowsum_.push_back(d);
+          group_done_[gi] = 1;
+        } else {
+          lower_group(gi);
+        }
+      }
       continue;
     }
     if (gemm_done_[i]) continue;
@@ -986,22 +1002,26 @@ void Runtime::lower() {
   flush_deferred_gemms();
   {
     std::vector<int> batch;
-    bool scatter_left = !deferred_scatter_.empty();
+    bool scatter_left = !deferred_scatter_.empty(), rows_left = !deferred_rowsum_.empty();
+    const int room = tgk::kColSumMax - (int)deferred_rowsum_.size();   // the first batch takes the row sums
     for (auto& c : colsum_) {
       if (!defer_colsum_[c.first] || colsum_done_[c.first]) continue;
       batch.push_back(c.first);
-      if ((int)batch.size() == tgk::kColSumMax) {
-        emit_colsums(batch, scatter_left);
-        scatter_left = false;
+      if ((int)batch.size() == (rows_left ? room : tgk::kColSumMax)) {
+        emit_colsums(batch, scatter_left, rows_left);
+        scatter_left = rows_left = false;
         batch.clear();
       }
     }
     if (!batch.empty()) {
-      emit_colsums(batch, scatter_left);
-      scatter_left = false;
+      emit_colsums(batch, scatter_left, rows_left);
+      scatter_left = rows_left = false;
     }
     if (scatter_left) emit_scatter(deferred_scatter_.front());   // no column sums to join
+    if (rows_left)
+      for (const DeferredRowSum& d : deferred_rowsum_) lower_group(d.gi);
     deferred_scatter_.clear();
+    deferred_rowsum_.clear();
   }
 
   // Drop nodes whose results nobody reads (e.g. a one_hot consumed only by the
@@ -1958,6 +1978,36 @@ void Runtime::lower_colsums(int s0) {
   emit_colsums(batch);
 }
 
+bool Runtime::tail_rowsum(int gi, DeferredRowSum& d) const {
+  const Group& G = groups_[gi];
+  if (!G.row || !G.dups.empty() || G.ops.empty() || G.ops.size() > 2 || G.shape.empty()) return false;
+  const int m0 = G.ops[0];
+  const std::string& k0 = kinds_[m0];
+  if (k0 != "sum_last" && k0 != "mean_last") return false;
+  const int a = fld(m0, "a");
+  const int s0 = O(m0).at("out").i32();
+  const int64_t D = G.shape.back();
+  if (D < 1 || T_[a].dt != F32 || T_[a].numel != D || !view_[a].contiguous()) return false;
+  int out = s0;
+  double scale = 1.0;
+  std::string detail = k0;
+  if (G.ops.size() == 2) {
+    const int m1 = G.ops[1];
+    if (kinds_[m1] != "mul_scalar" || fld(m1, "a") != s0 || consumers_[s0].size() != 1) return false;
+    out = O(m1).at("out").i32();
+    scale = O(m1).at("scalar").num();
+    detail += ",mul_scalar";
+  }
+  if (!consumers_[out].empty() || T_[out].numel != 1 || T_[out].dt != F32 || !view_[out].contiguous()) return false;
+  bool is_out = false;
+  for (int o : outputs_) if (root(o) == root(out)) is_out = true;
+  for (auto& c : captures_) if (root(c.second) == root(out)) is_out = true;
+  for (auto& w : copy_writebacks_) if (root(w.first) == root(out)) return false;
+  if (!is_out) return false;
+  d = DeferredRowSum{gi, a, out, D, k0 == "mean_last" ? (double)D : 1.0, scale, detail};
+  return true;
+}
+
 void Runtime::emit_scatter(const DeferredScatter& sc) {
   Node n;
   n.kind = "scatter";
@@ -1982,7 +2032,7 @@ void Runtime::emit_scatter(const DeferredScatter& sc) {
   add_node(std::move(n));
 }
 
-void Runtime::emit_colsums(const std::vector<int>& batch, bool with_scatter) {
+void Runtime::emit_colsums(const std::vector<int>& batch, bool with_scatter, bool with_rowsums) {
   const int s0 = batch.front();
   const ColSumOp& c0 = colsum_.at(s0);
   for (int sop : batch) colsum_done_[sop] = true;
@@ -2007,6 +2057,19 @@ void Runtime::emit_colsums(const std::vector<int>& batch, bool with_scatter) {
     const int terms = c.b >= 0 ? 2 : 1;
     ws += ((size_t)tgk::colsum_workspace_doubles(c.C, c.R, terms) * 8 + 255) & ~(size_t)255;
     cbase.push_back(take_counters(tgk::colsum_counters(c.C, c.R, terms)));
+  }
+  const std::vector<DeferredRowSum> rsums = with_rowsums ? deferred_rowsum_ : std::vector<DeferredRowSum>{};
+  std::vector<size_t> rws_off;
+  std::vector<int64_t> rcbase;
+  for (const DeferredRowSum& d : rsums) {
+    n.reads.push_back(root(d.a));
+    n.writes.push_back(root(d.out));
+    n.bytes += 4.0 * (d.R + 1);
+    n.detail += "," + d.detail;
+    n.shape += " + loss [" + std::to_string(d.R) + "]";
+    rws_off.push_back(ws);
+    ws += ((size_t)tgk::colsum_workspace_doubles(1, d.R, 1) * 8 + 255) & ~(size_t)255;
+    rcbase.push_back(take_counters(tgk::colsum_counters(1, d.R, 1)));
   }
   workspace_bytes_ = std::max(workspace_bytes_, ws);
   n.ws = true;
@@ -2043,6 +2106,16 @@ void Runtime::emit_colsums(const std::vector<int>& batch, bool with_scatter) {
       double* part = reinterpret_cast<double*>(reinterpret_cast<char*>(cur_ws_) + ws_off[q]);
       bt.s[q] = tgk::colsum_desc((const float*)dptr(c.a), c.b >= 0 ? (const float*)dptr(c.b) : nullptr,
                                  (float*)dptr(out), c.C, c.R, c.C, 1.0, part, cur_counters_ + cbase[q]);
+    }
+    for (size_t q = 0; q < rsums.size(); ++q) {
+      const DeferredRowSum& d = rsums[q];
+      if (T_[root(d.a)].numel < d.R || T_[root(d.out)].numel < 1)
+        throw Error(TG_INTERNAL, "loss sum: operand smaller than its shape");
+      double* part = reinterpret_cast<double*>(reinterpret_cast<char*>(cur_ws_) + rws_off[q]);
+      tgk::ColSum c = tgk::colsum_desc((const float*)dptr(d.a), nullptr, (float*)dptr(d.out), 1, d.R, 1, d.div, part,
+                                       cur_counters_ + rcbase[q]);
+      c.scale = d.scale;
+      bt.s[bt.n++] = c;
     }
     return [bt](hipStream_t st) { tgk::colsum_batch(bt, st); };
   };

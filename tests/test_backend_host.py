@@ -62,6 +62,22 @@ def test_embedding_gradient_joins_the_column_sums(monkeypatch):
     assert not any('+ scatter' in n['shape'] for n in nodes)
 
 
+@pytest.mark.parametrize('key', ['mlp_sin', 'char_mlp', 'cnn', 'transformer'])
+def test_loss_mean_joins_the_column_sums(monkeypatch, key):
+    """The loss mean (a row group reducing the per-sample losses to the output scalar) runs
+    as a one-column sum in the deferred column-sum launch: one launch fewer per step;
+    TG_COLSUM_LOSS=0 keeps its own row-group launch."""
+    cfg = configs.CONFIGS[key]
+    ir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer)
+    nodes = backend.plan(ir.wire_json())['nodes']
+    merged = [n for n in nodes if n['kind'] == 'reduce' and ' + loss [' in n['shape']]
+    assert len(merged) == 1, [n['shape'] for n in nodes if n['kind'] == 'reduce']
+    monkeypatch.setenv('TG_COLSUM_LOSS', '0')
+    apart = backend.plan(ir.wire_json())['nodes']
+    assert not any(' + loss [' in n['shape'] for n in apart)
+    assert len(apart) == len(nodes) + 1
+
+
 def test_plan_with_gemm_epilogues(monkeypatch):
     """TG_GEMM_EPI=1 (pointwise groups in GEMM epilogues) lowers every config, also where a
     backward group recomputes from a GEMM's product (that product keeps its own store)."""

@@ -176,6 +176,39 @@ def test_embedding_gradient_beside_column_sums(key):
         assert np.array_equal(out['0'][n].view(np.uint32), out['1'][n].view(np.uint32)), n
 
 
+@pytest.mark.parametrize('key', ['mlp_sin', 'char_mlp', 'cnn', 'transformer'])
+def test_loss_mean_beside_column_sums(key):
+    """The loss mean runs as a one-column sum in the deferred column-sum launch: f64 sums
+    of the per-sample losses in another order, each rounded once to f32, so the loss is
+    the row group's (TG_COLSUM_LOSS=0) to one f32 ulp; the parameters, which the loss
+    value does not feed, are bit-identical after three full-size steps."""
+    cfg = configs.CONFIGS[key]
+    ir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer)
+    p0 = ir.initial_params(7)
+    batches = configs.batches(cfg, 3)
+    losses, params = {}, {}
+    for merged in ('0', '1'):
+        old = os.environ.get('TG_COLSUM_LOSS')
+        os.environ['TG_COLSUM_LOSS'] = merged
+        try:
+            rt = backend.NativeRuntime(ir.wire_json())
+        finally:
+            if old is None:
+                os.environ.pop('TG_COLSUM_LOSS', None)
+            else:
+                os.environ['TG_COLSUM_LOSS'] = old
+        assert any(' + loss [' in n['shape'] for n in rt.describe()['nodes']) == (merged == '1')
+        rt.upload_params(p0)
+        losses[merged] = np.array([rt.step(b) for b in batches], np.float32)
+        params[merged] = rt.download_params()
+        rt.destroy()
+    assert np.all(np.isfinite(losses['1']))
+    ulps = np.abs(losses['0'].view(np.int32).astype(np.int64) - losses['1'].view(np.int32).astype(np.int64))
+    assert ulps.max() <= 1, (losses['0'], losses['1'])
+    for n in ir.param_names:
+        assert np.array_equal(params['0'][n].view(np.uint32), params['1'][n].view(np.uint32)), n
+
+
 @pytest.mark.parametrize('key', ['mlp_sin', 'char_mlp', 'cnn', 'nerf', 'transformer'])
 def test_small_variant_100_steps(key):
     wl, wp, _ = _train_both(configs.small_variant(key), 100)
