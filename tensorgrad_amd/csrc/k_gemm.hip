@@ -377,8 +377,66 @@ int64_t gemm_workspace_floats(const GemmDesc& d) {
   return p.splits > 1 ? (int64_t)p.splits * d.batch * d.M * d.N : 0;
 }
 
+namespace {
+
+// Small degenerate products (one of M, N, K is 1: outer products and matrix-vector
+// products, up to kTinyMacs multiply-adds; the small MLP's one-wide layers): a 64 x 64
+// MFMA tile would compute one real row or column, and its fixed cost (operand staging,
+// the k-group exchange) dominates. Each output takes L lanes (L divides 64, about K / 8
+// terms per lane): lane g adds terms k = g, g + L, ... in order with f32 FMAs from +0, then
+// an xor butterfly over the L lanes combines them, a fixed order. With K = 1 that is
+// f32(0 + a b), the MFMA tile's bits; otherwise the rounding of another summation order.
+constexpr int64_t kTinyMacs = int64_t(1) << 21;
+
+template <int L>
+__global__ __launch_bounds__(256) void k_gemm_tiny(const GemmDesc d) {
+  constexpr int kPerBlock = 256 / L;
+  const int64_t total = d.M * d.N * d.batch;
+  const int g = (int)threadIdx.x % L;
+  // the loop bound is the same in every thread: all lanes reach the butterfly together
+  for (int64_t e0 = (int64_t)blockIdx.x * kPerBlock; e0 < total; e0 += (int64_t)gridDim.x * kPerBlock) {
+    const int64_t e = e0 + threadIdx.x / L;
+    float acc = 0.0f;
+    int64_t ci = -1;
+    if (e < total) {
+      const int64_t n = e % d.N, t = e / d.N, m = t % d.M, z = t / d.M;
+      const int64_t z0 = z / d.bdiv, z1 = z % d.bdiv;
+      const float* a = d.A + z0 * d.sAz0 + z1 * d.sAz1 + m * d.sAm;
+      const float* b = d.B + z0 * d.sBz0 + z1 * d.sBz1 + n * d.sBn;
+      for (int64_t k = g; k < d.K; k += L) acc = fmaf(a[k * d.sAk], b[k * d.sBk], acc);
+      ci = z0 * d.sCz0 + z1 * d.sCz1 + m * d.sCm + n * d.sCn;
+    }
+#pragma unroll
+    for (int o = L / 2; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+    if (g == 0 && ci >= 0) d.C[ci] = acc;
+  }
+}
+
+}  // namespace
+
+bool gemm_is_tiny(const GemmDesc& d) {
+  return d.M > 0 && d.N > 0 && d.K > 0 && d.batch > 0 && (d.M == 1 || d.N == 1 || d.K == 1) &&
+         d.M * d.N <= kTinyMacs && d.K <= kTinyMacs && d.M * d.N * d.K * d.batch <= kTinyMacs;
+}
+
 void gemm(const GemmDesc& d, float* work, hipStream_t st) {
   if (d.M <= 0 || d.N <= 0 || d.batch <= 0) return;
+  if (gemm_is_tiny(d)) {
+    int L = 1;
+    while (L < 64 && (int64_t)L * 8 < d.K) L *= 2;
+    const int64_t outs = d.M * d.N * d.batch, per = 256 / L;
+    const int64_t b = (outs + per - 1) / per;
+    const dim3 grid((unsigned)(b < 65535 ? b : 65535));
+    switch (L) {
+      case 1: k_gemm_tiny<1><<<grid, 256, 0, st>>>(d); return;
+      case 2: k_gemm_tiny<2><<<grid, 256, 0, st>>>(d); return;
+      case 4: k_gemm_tiny<4><<<grid, 256, 0, st>>>(d); return;
+      case 8: k_gemm_tiny<8><<<grid, 256, 0, st>>>(d); return;
+      case 16: k_gemm_tiny<16><<<grid, 256, 0, st>>>(d); return;
+      case 32: k_gemm_tiny<32><<<grid, 256, 0, st>>>(d); return;
+      default: k_gemm_tiny<64><<<grid, 256, 0, st>>>(d); return;
+    }
+  }
   Plan p = plan_for(d);
   GemmArgs g{d, p.kps, p.splits, 0, 0, nullptr, 0, 0};
   if (p.splits > 1) {
