@@ -534,6 +534,28 @@ def test_matmul(case):
     gemm_close(got, want)
 
 
+@pytest.mark.parametrize('sa,sb,ta', [([256, 1], [1, 64], False), ([256, 64], [64, 1], False),
+                                      ([1, 256], [256, 64], False), ([64, 4096], [4096, 1], False),
+                                      ([3, 1], [1, 5], False), ([256, 1], [64, 1], True),
+                                      ([2, 7, 1], [2, 1, 9], False), ([5, 1, 300], [5, 300, 33], False)])
+def test_degenerate_products(sa, sb, ta):
+    """Products with one of M, N, K equal to 1 (outer products, matrix-vector products,
+    batched too) run on the lane-group kernel: within GEMM tolerance of the oracle, and
+    bit for bit with K = 1, where each output is the single product rounded once."""
+    a, b = _rand(sa, 31), _rand(sb, 32)
+
+    def body():
+        B = tensor_input('b', sb)
+        if ta:
+            B = O.swap_axes(B, -1, -2)
+        return O.matmul(tensor_input('a', sa), B)
+    got, want = run_both(body, {'a': a, 'b': b})
+    if sa[-1] == 1:
+        exact(got, want)
+    else:
+        gemm_close(got, want)
+
+
 def test_matmul_batched_head_views():
     # q @ k^T on split-head views: [B,T,D] -> [B,H,T,d] permutes read in place.
     B, T, H, d = 3, 20, 4, 8
