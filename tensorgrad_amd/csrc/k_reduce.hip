@@ -321,6 +321,52 @@ constexpr int kColWaves = 8;
 constexpr int kColThreads = kColWaves * 64;
 constexpr int kColRows = 4;
 
+// One block of a MidSum: channel c, images q chunk ... Wave w takes images b0 + w, + kColWaves,
+// ...; lane l sums positions l, l + 64, ... of each (four loads in flight), all in f64 in
+// that order; the wave's butterfly, then the waves in order, give the block's partial.
+__device__ __forceinline__ void midsum_block(const MidSum& ms, int loc, double* wsum) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t c = loc / ms.nchunks;
+  const int q = loc % ms.nchunks;
+  const int64_t b0 = (int64_t)q * ms.chunk, b1 = min(ms.B, b0 + ms.chunk);
+  double s = 0.0;
+  for (int64_t b = b0 + w; b < b1; b += kColWaves) {
+    const float* row = ms.a + (b * ms.C + c) * ms.L;
+    for (int64_t l = lane; l < ms.L; l += 64 * 4) {
+      float v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v[u] = l + 64 * u < ms.L ? row[l + 64 * u] : 0.0f;
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (l + 64 * u < ms.L) s += (double)v[u];
+    }
+  }
+  s = wave_allsum(s);
+  if (lane == 0) wsum[w] = s;
+  __syncthreads();
+  if (threadIdx.x != 0) return;   // the rest is one thread's: no barrier follows
+  double bs = wsum[0];
+  for (int v = 1; v < kColWaves; ++v) bs += wsum[v];
+  if (ms.nchunks == 1) {
+    ms.out[c] = (float)bs;
+    return;
+  }
+  // partials and the counter as device-scope atomics, as in the column sums below
+  __hip_atomic_store(&ms.part[c * ms.nchunks + q], bs, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __builtin_amdgcn_s_waitcnt(0);
+  if (__hip_atomic_fetch_add(&ms.counters[c], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) !=
+      (unsigned)(ms.nchunks - 1))
+    return;
+  double t = 0.0;
+  for (int k = 0; k < ms.nchunks; ++k)
+    t += __hip_atomic_load(&ms.part[c * ms.nchunks + k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  ms.out[c] = (float)t;
+  __hip_atomic_store(&ms.counters[c], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// MID: the batch has [B, C, L] sums (a separate instantiation, so launches without them run
+// the column-sum code alone)
+template <bool MID>
 __global__ __launch_bounds__(kColThreads) void k_colsum(const ColSumBatch batch) {
   if ((int)blockIdx.x < batch.sc.blocks) {   // the embedding gradient run beside the sums
     __shared__ ScatterScanLds<kColWaves> sl;
@@ -329,7 +375,21 @@ __global__ __launch_bounds__(kColThreads) void k_colsum(const ColSumBatch batch)
                                   (int64_t)cy * kColThreads, sl);
     return;
   }
-  const int bid = (int)blockIdx.x - batch.sc.blocks;
+  int bid = (int)blockIdx.x - batch.sc.blocks;
+  __shared__ double red[kColWaves][256];
+  __shared__ int last;
+  if (MID) {
+    int mid_blocks = 0;
+    for (int i = 0; i < batch.nmid; ++i) mid_blocks += (int)(batch.m[i].C * batch.m[i].nchunks);
+    if (bid < mid_blocks) {   // the [B, C, L] sums' blocks
+      int zm = 0;
+      for (int i = 1; i < batch.nmid; ++i)
+        if (bid >= batch.m[i].blk0) zm = i;
+      midsum_block(batch.m[zm], bid - batch.m[zm].blk0, &red[0][0]);   // the waves' sums in red
+      return;
+    }
+    bid -= mid_blocks;
+  }
   int z = 0;
   for (int i = 1; i < batch.n; ++i)
     if (bid >= batch.s[i].blk0) z = i;
@@ -337,8 +397,6 @@ __global__ __launch_bounds__(kColThreads) void k_colsum(const ColSumBatch batch)
   const int loc = bid - cs.blk0;
   const int bx = loc % cs.nx, y = loc / cs.nx;
   constexpr int NW = kColWaves;
-  __shared__ double red[NW][256];
-  __shared__ int last;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int64_t C = cs.C, rs = cs.rs;
   const int nchunks = cs.nchunks;
@@ -597,6 +655,28 @@ ColSum colsum_desc(const float* a, const float* b, float* out, int64_t C, int64_
   return c;
 }
 
+// [B, C, L] sums: chunks of at least two images per wavefront, at most 16 per channel (the
+// last block of a channel counts the arrivals on one device-scope counter)
+static int64_t midsum_chunk(int64_t B) { return std::max<int64_t>(2 * kColWaves, (B + 15) / 16); }
+MidSum midsum_desc(const float* a, float* out, int64_t B, int64_t C, int64_t L, double* part, unsigned* counters) {
+  MidSum m{};
+  m.a = a; m.out = out; m.B = B; m.C = C; m.L = L;
+  m.chunk = midsum_chunk(B);
+  m.nchunks = (int)((B + m.chunk - 1) / m.chunk);
+  m.part = part; m.counters = counters;
+  return m;
+}
+int64_t midsum_workspace_doubles(int64_t B, int64_t C, int64_t L) {
+  (void)L;
+  const int64_t ch = midsum_chunk(B), n = (B + ch - 1) / ch;
+  return n > 1 ? C * n : 0;
+}
+int64_t midsum_counters(int64_t B, int64_t C, int64_t L) {
+  (void)L;
+  const int64_t ch = midsum_chunk(B);
+  return (B + ch - 1) / ch > 1 ? C : 0;
+}
+
 int64_t colsum_workspace_doubles(int64_t C, int64_t R, int terms) {
   const ColPlan p = col_plan(C, R, terms);
   return p.nchunks > 1 ? C * p.nchunks : 0;
@@ -617,14 +697,22 @@ void colsum_batch(const ColSumBatch& b, hipStream_t st) {
     if ((int64_t)bt.sc.V * ny > INT32_MAX / 2) throw std::runtime_error("column sums: scatter too large");
     bt.sc.blocks = (int)(bt.sc.V * ny);
   }
-  int64_t blocks = bt.sc.blocks;
+  // then the [B, C, L] sums' blocks, then the column sums' (each numbered from 0 in its range)
+  if (bt.nmid < 0 || bt.nmid > kMidSumMax) throw std::runtime_error("column sums: bad [B, C, L] sum count");
+  int64_t mids = 0;
+  for (int i = 0; i < bt.nmid; ++i) {
+    bt.m[i].blk0 = (int)mids;
+    mids += bt.m[i].C * bt.m[i].nchunks;
+  }
+  int64_t blocks = bt.sc.blocks + mids;
   for (int i = 0; i < bt.n; ++i) {
-    bt.s[i].blk0 = (int)(blocks - bt.sc.blocks);
+    bt.s[i].blk0 = (int)(blocks - bt.sc.blocks - mids);
     blocks += (int64_t)bt.s[i].nx * bt.s[i].nchunks;
   }
   if (blocks <= 0) return;
   if (blocks > INT32_MAX) throw std::runtime_error("column sums: too many blocks");
-  k_colsum<<<(unsigned)blocks, kColThreads, 0, st>>>(bt);
+  if (bt.nmid > 0) k_colsum<true><<<(unsigned)blocks, kColThreads, 0, st>>>(bt);
+  else k_colsum<false><<<(unsigned)blocks, kColThreads, 0, st>>>(bt);
 }
 
 int64_t sum_counters(const Strided& cells, const Strided& red, int64_t ncells, int64_t nred) {

@@ -147,15 +147,33 @@ struct ColSumScatter {
   int64_t rows, N;
   int V, blocks;
 };
+// Sum over the outer and inner axes of a contiguous [B, C, L] array (a convolution's bias
+// gradient: images and spatial positions), out[c] = f32(sum over b and l), run by blocks
+// of a column-sum launch after the scatter's: block (c, q) sums images q chunk .. in f64,
+// and the last of channel c's nchunks blocks adds their partials in chunk order.
+struct MidSum {
+  const float* a;
+  float* out;
+  int64_t B, C, L, chunk;
+  int nchunks, blk0;      // blk0: first block among the launch's MidSum blocks (set by colsum_batch)
+  double* part;           // C * nchunks partials
+  unsigned* counters;     // C counters, zero, left zero
+};
+constexpr int kMidSumMax = 2;
 struct ColSumBatch {
   int n;
   ColSum s[kColSumMax];
   ColSumScatter sc;
+  int nmid;
+  MidSum m[kMidSumMax];
 };
 static_assert(sizeof(ColSumBatch) <= 4096, "column-sum batch fits the kernel argument space");
 ColSum colsum_desc(const float* a, const float* b, float* out, int64_t C, int64_t R, int64_t rs, double div,
                    double* part, unsigned* counters);
 int64_t colsum_workspace_doubles(int64_t C, int64_t R, int terms);
+MidSum midsum_desc(const float* a, float* out, int64_t B, int64_t C, int64_t L, double* part, unsigned* counters);
+int64_t midsum_workspace_doubles(int64_t B, int64_t C, int64_t L);
+int64_t midsum_counters(int64_t B, int64_t C, int64_t L);
 int64_t colsum_counters(int64_t C, int64_t R, int terms);
 void colsum_batch(const ColSumBatch& b, hipStream_t st);
 void row_argmax(const float* a, int32_t* out, int64_t outer, int64_t D, hipStream_t st);

@@ -458,11 +458,19 @@ class Runtime {
   // Column sums read only by the optimizer (bias, LayerNorm gain / shift gradients) run
   // together with the grouped GEMMs, kColSumMax per launch.
   std::vector<char> defer_colsum_;
-  void emit_colsums(const std::vector<int>& batch, bool with_scatter = false, bool with_rowsums = false);
+  void emit_colsums(const std::vector<int>& batch, bool with_scatter = false, bool with_rowsums = false,
+                    bool with_mids = false);
   // A row group that only reduces one row to a scalar the graph outputs (the loss mean:
   // sum_last or mean_last, then optionally mul_scalar) runs as a one-column sum in the first
   // deferred column-sum launch (TG_COLSUM_LOSS=0: a launch of its own in place).
   struct DeferredRowSum { int gi, a, out; int64_t R; double div, scale; std::string detail; };
+  // Sums over the outer and inner axes of a contiguous [B, C, L] array that only the
+  // optimizer reads (convolution bias gradients) run in the same launch (TG_COLSUM_MID=0:
+  // as their own reductions in place).
+  struct DeferredMidSum { int a, out; int64_t B, C, L; };
+  std::vector<DeferredMidSum> deferred_midsum_;
+  bool use_colsum_mid_ = true;
+  bool any_deferred_colsum_ = false;
   std::vector<DeferredRowSum> deferred_rowsum_;
   bool use_colsum_loss_ = true;
   bool tail_rowsum(int gi, DeferredRowSum& d) const;
@@ -496,6 +504,7 @@ Runtime::Runtime(const char* json, Runtime* par, bool plan_only) : parent(par) {
   if (const char* g = std::getenv("TG_REMAT")) use_remat_ = std::string(g) != "0";
   if (const char* g = std::getenv("TG_COLSUM_SCATTER")) use_colsum_scatter_ = std::string(g) != "0";
   if (const char* g = std::getenv("TG_COLSUM_LOSS")) use_colsum_loss_ = std::string(g) != "0";
+  if (const char* g = std::getenv("TG_COLSUM_MID")) use_colsum_mid_ = std::string(g) != "0";
   if (const char* g = std::getenv("TG_GEMM_EPI")) gemm_epi_mode_ = std::string(g) == "1" ? kEpiAll : (std::string(g) == "0" ? kEpiOff : kEpiCheap);
   if (const char* g = std::getenv("TG_FUSED")) use_jit_ = std::string(g) != "vm";
   if (const char* g = std::getenv("TG_CONV")) use_conv_gemm_ = std::string(g) != "direct";
@@ -957,7 +966,7 @@ void Runtime::lower() {
   defer_colsum_.assign(ops_.size(), 0);
   if (use_gemm_group_)
     for (auto& c : colsum_)
-      if (only_optimizer_reads(O(c.first).at("out").i32())) defer_colsum_[c.first] = 1;
+      if (only_optimizer_reads(O(c.first).at("out").i32())) defer_colsum_[c.first] = any_deferred_colsum_ = 1;
   form_groups();
   merge_groups();
   if (use_remat_) remat_groups();
@@ -1003,25 +1012,28 @@ void Runtime::lower() {
   {
     std::vector<int> batch;
     bool scatter_left = !deferred_scatter_.empty(), rows_left = !deferred_rowsum_.empty();
+    bool mids_left = !deferred_midsum_.empty();
     const int room = tgk::kColSumMax - (int)deferred_rowsum_.size();   // the first batch takes the row sums
     for (auto& c : colsum_) {
       if (!defer_colsum_[c.first] || colsum_done_[c.first]) continue;
       batch.push_back(c.first);
       if ((int)batch.size() == (rows_left ? room : tgk::kColSumMax)) {
-        emit_colsums(batch, scatter_left, rows_left);
-        scatter_left = rows_left = false;
+        emit_colsums(batch, scatter_left, rows_left, mids_left);
+        scatter_left = rows_left = mids_left = false;
         batch.clear();
       }
     }
     if (!batch.empty()) {
-      emit_colsums(batch, scatter_left, rows_left);
-      scatter_left = rows_left = false;
+      emit_colsums(batch, scatter_left, rows_left, mids_left);
+      scatter_left = rows_left = mids_left = false;
     }
+    if (mids_left) throw Error(TG_INTERNAL, "[B, C, L] sums deferred without a column-sum launch");
     if (scatter_left) emit_scatter(deferred_scatter_.front());   // no column sums to join
     if (rows_left)
       for (const DeferredRowSum& d : deferred_rowsum_) lower_group(d.gi);
     deferred_scatter_.clear();
     deferred_rowsum_.clear();
+    deferred_midsum_.clear();
   }
 
   // Drop nodes whose results nobody reads (e.g. a one_hot consumed only by the
@@ -2032,7 +2044,7 @@ void Runtime::emit_scatter(const DeferredScatter& sc) {
   add_node(std::move(n));
 }
 
-void Runtime::emit_colsums(const std::vector<int>& batch, bool with_scatter, bool with_rowsums) {
+void Runtime::emit_colsums(const std::vector<int>& batch, bool with_scatter, bool with_rowsums, bool with_mids) {
   const int s0 = batch.front();
   const ColSumOp& c0 = colsum_.at(s0);
   for (int sop : batch) colsum_done_[sop] = true;
@@ -2071,6 +2083,19 @@ void Runtime::emit_colsums(const std::vector<int>& batch, bool with_scatter, boo
     ws += ((size_t)tgk::colsum_workspace_doubles(1, d.R, 1) * 8 + 255) & ~(size_t)255;
     rcbase.push_back(take_counters(tgk::colsum_counters(1, d.R, 1)));
   }
+  const std::vector<DeferredMidSum> mids = with_mids ? deferred_midsum_ : std::vector<DeferredMidSum>{};
+  std::vector<size_t> mws_off;
+  std::vector<int64_t> mcbase;
+  for (const DeferredMidSum& d : mids) {
+    n.reads.push_back(root(d.a));
+    n.writes.push_back(root(d.out));
+    n.bytes += 4.0 * (d.B * d.C * d.L + d.C);
+    n.detail += ",sum_to_shape";
+    n.shape += " + [" + std::to_string(d.B) + "," + std::to_string(d.C) + "," + std::to_string(d.L) + "] sum";
+    mws_off.push_back(ws);
+    ws += ((size_t)tgk::midsum_workspace_doubles(d.B, d.C, d.L) * 8 + 255) & ~(size_t)255;
+    mcbase.push_back(take_counters(tgk::midsum_counters(d.B, d.C, d.L)));
+  }
   workspace_bytes_ = std::max(workspace_bytes_, ws);
   n.ws = true;
   const bool sct = with_scatter && !deferred_scatter_.empty();
@@ -2106,6 +2131,14 @@ void Runtime::emit_colsums(const std::vector<int>& batch, bool with_scatter, boo
       double* part = reinterpret_cast<double*>(reinterpret_cast<char*>(cur_ws_) + ws_off[q]);
       bt.s[q] = tgk::colsum_desc((const float*)dptr(c.a), c.b >= 0 ? (const float*)dptr(c.b) : nullptr,
                                  (float*)dptr(out), c.C, c.R, c.C, 1.0, part, cur_counters_ + cbase[q]);
+    }
+    for (size_t q = 0; q < mids.size(); ++q) {
+      const DeferredMidSum& d = mids[q];
+      if (T_[root(d.a)].numel < d.B * d.C * d.L || T_[root(d.out)].numel < d.C)
+        throw Error(TG_INTERNAL, "[B, C, L] sum: operand smaller than its shape");
+      double* part = reinterpret_cast<double*>(reinterpret_cast<char*>(cur_ws_) + mws_off[q]);
+      bt.m[bt.nmid++] = tgk::midsum_desc((const float*)dptr(d.a), (float*)dptr(d.out), d.B, d.C, d.L, part,
+                                         cur_counters_ + mcbase[q]);
     }
     for (size_t q = 0; q < rsums.size(); ++q) {
       const DeferredRowSum& d = rsums[q];
@@ -3098,6 +3131,15 @@ void Runtime::lower_op(int i) {
     tgk::Strided red = make_strided(rdd, rs, {}, {});
     int64_t ncells = prod(cd), nred = prod(rdd);
     if (ncells != to.numel) throw Error(TG_INTERNAL, "sum_to_shape: cell count mismatch");
+    // [B, C, L] form (kept axis in the middle of a contiguous array), read only by the
+    // optimizer: joins the deferred column-sum launch
+    if (use_gemm_group_ && use_colsum_mid_ && any_deferred_colsum_ && (int)deferred_midsum_.size() < tgk::kMidSumMax &&
+        cells.rank == 1 && red.rank == 2 && red.s0[1] == 1 && cells.s0[0] == red.dims[1] &&
+        red.s0[0] == cells.dims[0] * cells.s0[0] && view_[a].root == a && view_[a].contiguous() &&
+        view_[out].root == out && view_[out].contiguous() && only_optimizer_reads(out)) {
+      deferred_midsum_.push_back({a, out, red.dims[0], cells.dims[0], red.dims[1]});
+      return;
+    }
     workspace_bytes_ = std::max(workspace_bytes_, (size_t)tgk::sum_workspace_doubles(cells, red, ncells, nred) * 8);
     const int64_t cbase = take_counters(tgk::sum_counters(cells, red, ncells, nred));
     n.ws = true;

@@ -78,6 +78,21 @@ def test_loss_mean_joins_the_column_sums(monkeypatch, key):
     assert len(apart) == len(nodes) + 1
 
 
+def test_bias_sums_join_the_column_sums(monkeypatch):
+    """The CNN's convolution bias gradients (sums over images and positions of [B, C, H, W],
+    read only by Adam) run as blocks of the deferred column-sum launch; TG_COLSUM_MID=0
+    keeps them as reductions of their own."""
+    cfg = configs.CONFIGS['cnn']
+    ir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer)
+    nodes = backend.plan(ir.wire_json())['nodes']
+    tail = [n for n in nodes if n['kind'] == 'reduce']
+    assert len(tail) == 1 and tail[0]['shape'].count('] sum') == 2, [n['shape'] for n in tail]
+    monkeypatch.setenv('TG_COLSUM_MID', '0')
+    apart = backend.plan(ir.wire_json())['nodes']
+    assert sum(1 for n in apart if n['kind'] == 'reduce') == 3
+    assert len(apart) == len(nodes) + 2
+
+
 def test_plan_with_gemm_epilogues(monkeypatch):
     """TG_GEMM_EPI=1 (pointwise groups in GEMM epilogues) lowers every config, also where a
     backward group recomputes from a GEMM's product (that product keeps its own store)."""

@@ -209,6 +209,38 @@ def test_loss_mean_beside_column_sums(key):
         assert np.array_equal(params['0'][n].view(np.uint32), params['1'][n].view(np.uint32)), n
 
 
+def test_bias_sums_beside_column_sums():
+    """The CNN's convolution bias gradients run as blocks of the deferred column-sum launch
+    (f64 sums in another order, rounded once): two full-size steps give the parameters of
+    the separate reductions (TG_COLSUM_MID=0) to 2 ulp."""
+    cfg = configs.CONFIGS['cnn']
+    ir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer)
+    p0 = ir.initial_params(9)
+    batches = configs.batches(cfg, 2)
+    params = {}
+    for merged in ('0', '1'):
+        old = os.environ.get('TG_COLSUM_MID')
+        os.environ['TG_COLSUM_MID'] = merged
+        try:
+            rt = backend.NativeRuntime(ir.wire_json())
+        finally:
+            if old is None:
+                os.environ.pop('TG_COLSUM_MID', None)
+            else:
+                os.environ['TG_COLSUM_MID'] = old
+        assert any('] sum' in n['shape'] for n in rt.describe()['nodes']) == (merged == '1')
+        rt.upload_params(p0)
+        for b in batches:
+            rt.step(b)
+        params[merged] = rt.download_params()
+        rt.destroy()
+    for n in ir.param_names:
+        a = params['0'][n].view(np.int32).astype(np.int64)
+        b = params['1'][n].view(np.int32).astype(np.int64)
+        assert np.all(np.isfinite(params['1'][n])), n
+        assert np.max(np.abs(a - b)) <= 2, n
+
+
 @pytest.mark.parametrize('key', ['mlp_sin', 'char_mlp', 'cnn', 'nerf', 'transformer'])
 def test_small_variant_100_steps(key):
     wl, wp, _ = _train_both(configs.small_variant(key), 100)
