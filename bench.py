@@ -5,12 +5,16 @@ C5, the config the north star's roofline targets are stated on) with every batch
 resident in HBM when the timed region starts (batches are staged into device slots
 beforehand); each timed step still uploads the per-step optimizer scalars and PRNG seed,
 replays the captured step graph and reads the 4-byte loss back (the API's semantics).
-`per_config` carries the same measurement for all five configs, plus device-only replay
-time, GEMM TFLOP/s and non-GEMM GB/s from HIP events around every launch node.
-`roofline` is for the dominant kernel family of the headline config (its f32 MFMA GEMMs);
-`cpu_baseline` is the CPU oracle (a C++ restatement of the reference's CPU evaluator, the
-reference itself being TypeScript that cannot run here) on this host's cores, on a bounded
-number of steps of the same workload.
+`per_config` carries the same measurement for all five configs (and the transformer with
+clipGradNorm 1.0, the reference samples' setting), plus device-only replay time and
+per-family kernel rates. Kernel rates come from the kernels' own durations inside eager
+steps: every kernel of a step is dispatched with start / end events of its own
+(tg_profile_kernels), the quantity a profiler's kernel trace reports, without the gaps
+between launches. `roofline` is for the dominant kernel family of the headline config
+(its f32 MFMA GEMMs), `roofline_mfma_all` for every MFMA kernel (GEMMs and fused
+attention); `cpu_baseline` is the CPU oracle (a C++ restatement of the reference's CPU
+evaluator, the reference itself being TypeScript that cannot run here) on this host's
+cores, on a bounded number of steps of the same workload.
 """
 from __future__ import annotations
 
@@ -28,11 +32,38 @@ PEAK_HBM_GBS = 8000.0
 RING = 8
 
 
-def measure(key, steps, warmup, profile_iters=3, kind_iters=20):
+def family_rates(nodes, kms):
+    """Per-family work and kernel time of one step from per-node kernel durations (ms):
+    GEMMs, convolutions and attention on the f32 MFMA roofline, the rest on HBM."""
+    fam = {'gemm': ('gemm',), 'conv': ('conv',), 'attention': ('attention',)}
+    out = {}
+    for name, kinds in fam.items():
+        sel = [(n, t) for n, t in zip(nodes, kms) if n['kind'] in kinds]
+        f = sum(n['flops'] for n, _ in sel)
+        t = sum(t for _, t in sel)
+        out[name] = {'flop_per_step': f, 'bytes_per_step': sum(n['bytes'] for n, _ in sel), 'launches': len(sel),
+                     'ms': t, 'tflops': f / max(t, 1e-12) / 1e9,
+                     'frac_f32_peak': f / max(t, 1e-12) / 1e9 / PEAK_F32_MFMA_TFLOPS}
+    mf = out['gemm']['flop_per_step'] + out['attention']['flop_per_step'] + out['conv']['flop_per_step']
+    mt = out['gemm']['ms'] + out['attention']['ms'] + out['conv']['ms']
+    out['mfma_all'] = {'flop_per_step': mf, 'ms': mt, 'tflops': mf / max(mt, 1e-12) / 1e9,
+                       'frac_f32_peak': mf / max(mt, 1e-12) / 1e9 / PEAK_F32_MFMA_TFLOPS}
+    sel = [(n, t) for n, t in zip(nodes, kms) if n['kind'] not in ('gemm', 'conv', 'attention')]
+    b = sum(n['bytes'] for n, _ in sel)
+    t = sum(t for _, t in sel)
+    out['non_gemm'] = {'bytes_per_step': b, 'launches': len(sel), 'ms': t, 'gbs': b / max(t, 1e-12) / 1e6,
+                       'frac_hbm_peak': b / max(t, 1e-12) / 1e6 / PEAK_HBM_GBS}
+    return out
+
+
+def measure(key, steps, warmup, profile_iters=5, optimizer=None, label=None):
+    """Steps/s of config `key` (optionally with another optimizer) from staged batches, the
+    PCIe-inclusive rate, graph-replay time, and per-family kernel rates from the kernels'
+    own durations in eager steps (tg_profile_kernels)."""
     from tensorgrad_amd import backend, configs
     from tensorgrad_amd.build_ir import build_training_ir
     cfg = configs.CONFIGS[key]
-    ir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer)
+    ir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, optimizer or cfg.optimizer)
     rt = backend.NativeRuntime(ir.wire_json())
     rt.upload_params(ir.initial_params(configs.INIT_SEED))
     for i, b in enumerate(configs.batches(cfg, RING)):
@@ -54,47 +85,30 @@ def measure(key, steps, warmup, profile_iters=3, kind_iters=20):
     host_dt = time.perf_counter() - t1
     replay_ms = rt.time_replays(steps) / steps
     nodes = rt.describe()['nodes']
-    ms = rt.profile_nodes(profile_iters)
-    # Kernel-family times: back-to-back passes over just that family's launches, HIP
-    # events on the runtime's stream around the passes.
-    gemm_t, gemm_n = rt.time_kinds('gemm', kind_iters)
-    other_t, other_n = rt.time_kinds('-gemm,conv,attention', kind_iters)
-    conv_t, conv_n = rt.time_kinds('conv', kind_iters)
-    attn_t, attn_n = rt.time_kinds('attention', kind_iters)
+    kms = rt.profile_kernels(profile_iters)
     rt.destroy()
-    gemm_f = sum(n['flops'] for n in nodes if n['kind'] == 'gemm')
-    gemm_b = sum(n['bytes'] for n in nodes if n['kind'] == 'gemm')
-    other_b = sum(n['bytes'] for n in nodes if n['kind'] not in ('gemm', 'conv', 'attention'))
-    conv_f = sum(n['flops'] for n in nodes if n['kind'] == 'conv')
-    attn_f = sum(n['flops'] for n in nodes if n['kind'] == 'attention')
+    fam = family_rates(nodes, kms)
     by_kind = {}
-    for n, t in zip(nodes, ms):
+    for n, t in zip(nodes, kms):
         k = by_kind.setdefault(n['kind'], {'launch_nodes': 0, 'ms': 0.0})
         k['launch_nodes'] += 1
         k['ms'] = round(k['ms'] + t, 4)
-    top_gemm = sorted(((t, n) for n, t in zip(nodes, ms) if n['kind'] == 'gemm'), key=lambda x: -x[0])[:3]
+    top_gemm = sorted(((t, n) for n, t in zip(nodes, kms) if n['kind'] == 'gemm'), key=lambda x: -x[0])[:3]
+    fam['gemm']['top'] = [{'shape': n['shape'], 'ms': round(t, 4), 'tflops': round(n['flops'] / max(t, 1e-12) / 1e9, 2)}
+                          for t, n in top_gemm]
     return {
-        'config': key,
+        'config': label or key,
         'title': cfg.title,
         'steps_per_s': steps / dt,
         'ms_per_step': 1e3 * dt / steps,
         'samples_per_s': cfg.samples_per_step * steps / dt,
         'sample_unit': cfg.sample_unit,
         'device_replay_ms': replay_ms,
+        'kernel_ms_per_step': sum(kms),
         'host_batch_steps_per_s': host_steps / host_dt,
         'launch_nodes': len(nodes),
         'final_loss': loss,
-        'gemm': {'flop_per_step': gemm_f, 'bytes_per_step': gemm_b, 'launches': gemm_n, 'ms': gemm_t,
-                 'tflops': gemm_f / max(gemm_t, 1e-12) / 1e9,
-                 'frac_f32_peak': gemm_f / max(gemm_t, 1e-12) / 1e9 / PEAK_F32_MFMA_TFLOPS,
-                 'top': [{'shape': n['shape'], 'ms': round(t, 4), 'tflops': round(n['flops'] / max(t, 1e-12) / 1e9, 2)}
-                         for t, n in top_gemm]},
-        'conv': {'flop_per_step': conv_f, 'ms': conv_t, 'tflops': conv_f / max(conv_t, 1e-12) / 1e9},
-        'attention': {'flop_per_step': attn_f, 'launches': attn_n, 'ms': attn_t,
-                      'tflops': attn_f / max(attn_t, 1e-12) / 1e9},
-        'non_gemm': {'bytes_per_step': other_b, 'launches': other_n, 'ms': other_t,
-                     'gbs': other_b / max(other_t, 1e-12) / 1e6,
-                     'frac_hbm_peak': other_b / max(other_t, 1e-12) / 1e6 / PEAK_HBM_GBS},
+        **fam,
         'kinds': by_kind,
     }
 
@@ -308,8 +322,8 @@ def main():
                          'profilers trace direct launches, not graph replays), then exit')
     ap.add_argument('--cpu-protocol', action='store_true',
                     help='only time the CPU oracle: every config, single-thread and parallel, then exit')
-    ap.add_argument('--profile-iters', type=int, default=3, help='eager passes for the per-node breakdown')
-    ap.add_argument('--kind-iters', type=int, default=20, help='passes per kernel-family timing')
+    ap.add_argument('--profile-iters', type=int, default=5,
+                    help='eager steps with per-kernel start/end events for the per-family kernel rates')
     ap.add_argument('--vendor-gemm', action='store_true',
                     help='only compare every single-GEMM node of --config with the vendor BLAS, then exit')
     ap.add_argument('--probe-copy', action='store_true',
@@ -340,9 +354,17 @@ def main():
         print(f'# copy probe: {probe}', file=sys.stderr, flush=True)
     results = {}
     for k in keys:
-        results[k] = measure(k, args.steps, args.warmup, args.profile_iters, args.kind_iters)
+        results[k] = measure(k, args.steps, args.warmup, args.profile_iters)
         print(f'# {k}: {results[k]["steps_per_s"]:.1f} steps/s, replay {results[k]["device_replay_ms"]:.3f} ms',
               file=sys.stderr, flush=True)
+        if k == 'transformer' and not args.only:
+            # the reference samples' optimizer setting: the same step with global clipping
+            cfg5 = configs.CONFIGS[k]
+            r = measure(k, args.steps, args.warmup, args.profile_iters,
+                        optimizer=dict(cfg5.optimizer, clipGradNorm=1.0), label='transformer_clip')
+            results['transformer_clip'] = r
+            print(f'# transformer_clip: {r["steps_per_s"]:.1f} steps/s, replay {r["device_replay_ms"]:.3f} ms',
+                  file=sys.stderr, flush=True)
     head = results[args.config]
     cpu = None if args.no_cpu else cpu_baseline(args.config)
     cfg = configs.CONFIGS[args.config]
@@ -368,20 +390,28 @@ def main():
                      'achieved': round(g['tflops'], 3), 'peak': PEAK_F32_MFMA_TFLOPS, 'unit': 'TFLOP/s',
                      'frac': round(g['frac_f32_peak'], 4),
                      'traffic': profiled_traffic(os.path.join(ROOT, 'profiles', 'gemm_transformer_traffic.txt')),
+                     'timing': 'kernel start/end events of each launch in eager steps (tg_profile_kernels)',
                      'launches_per_step': g['launches'],
                      'avg_launch_us': round(1e3 * g['ms'] / max(g['launches'], 1), 3),
                      'algorithmic_flop_per_launch': round(g['flop_per_step'] / max(g['launches'], 1)),
                      'algorithmic_bytes_per_launch': round(g['bytes_per_step'] / max(g['launches'], 1))},
+        'roofline_mfma_all': {'bound': 'mfma', 'kernels': 'GEMMs + fused attention (+ convolutions)',
+                              'achieved': round(head['mfma_all']['tflops'], 3), 'peak': PEAK_F32_MFMA_TFLOPS,
+                              'unit': 'TFLOP/s', 'frac': round(head['mfma_all']['frac_f32_peak'], 4),
+                              'flop_per_step': head['mfma_all']['flop_per_step']},
         'roofline_non_gemm': {'bound': 'hbm', 'achieved': round(head['non_gemm']['gbs'], 1), 'peak': PEAK_HBM_GBS,
-                              'unit': 'GB/s', 'frac': round(head['non_gemm']['frac_hbm_peak'], 4)},
+                              'unit': 'GB/s', 'frac': round(head['non_gemm']['frac_hbm_peak'], 4),
+                              'launches_per_step': head['non_gemm']['launches']},
         'copy_probe': probe,
         'cpu_baseline': None if cpu is None else {k: (round(v, 5) if isinstance(v, float) else v) for k, v in cpu.items()},
         'per_config': [{'config': r['config'], 'steps_per_s': round(r['steps_per_s'], 2),
                         'samples_per_s': round(r['samples_per_s'], 1), 'device_replay_ms': round(r['device_replay_ms'], 4),
+                        'kernel_ms_per_step': round(r['kernel_ms_per_step'], 4),
                         'host_batch_steps_per_s': round(r['host_batch_steps_per_s'], 2),
                         'gemm_tflops': round(r['gemm']['tflops'], 2), 'gemm_frac_f32_peak': round(r['gemm']['frac_f32_peak'], 4),
                         'conv_tflops': round(r['conv']['tflops'], 2),
                         'attention_tflops': round(r['attention']['tflops'], 2),
+                        'mfma_all_frac_f32_peak': round(r['mfma_all']['frac_f32_peak'], 4),
                         'non_gemm_gbs': round(r['non_gemm']['gbs'], 1),
                         'non_gemm_frac_hbm': round(r['non_gemm']['frac_hbm_peak'], 4),
                         'launch_nodes': r['launch_nodes'], 'kinds': r['kinds'], 'top_gemms': r['gemm']['top']}

@@ -147,10 +147,17 @@ tg_status tg_upload_state(tg_runtime* rt, int n, const char* const* names, const
  * the optimizer kind, t, the seed counter and the LR schedule). */
 tg_status tg_save_checkpoint(tg_runtime* rt, const char* path);
 /* Load a safetensors file written by tg_save_checkpoint, or any file holding exactly the
- * graph's parameters (e.g. converted pretrained weights; state is then left alone).
- * Every parameter must be present with its shape; state is all or nothing; unknown
- * tensors are an error. Nothing is written unless the whole file checks out. */
+ * graph's parameters (e.g. converted pretrained weights; the optimizer state, t and the
+ * seed counter are then left alone). Every parameter must be present with its shape;
+ * state is all or nothing; unknown tensors (integer and bool ones included) and
+ * malformed counters are errors (TG_INVALID_ARGUMENT). Nothing is written unless the
+ * whole file checks out. */
 tg_status tg_load_checkpoint(tg_runtime* rt, const char* path);
+/* The checks of tg_load_checkpoint for the graph `ir_json` without a device (nothing is
+ * allocated or loaded): writes JSON {"params", "state", "restoresCounters", "step",
+ * "prngCounter"} or fails with the message a load would give. A params-only file leaves
+ * the optimizer state, t and the seed counter alone. No counterpart in the reference. */
+tg_status tg_check_checkpoint(const char* ir_json, const char* path, char* out_json, int64_t out_len);
 /* Index a safetensors container held in memory without a device: JSON
  * {"dataStart", "tensors": [{name, dtype, shape, begin, end}], "skipped": [...],
  *  "metadata": {...}} with the checks and messages of `loadSafetensors`
@@ -169,6 +176,11 @@ tg_status tg_plan(const char* ir_json, char* buf, int64_t buflen);
  * the runtime's stream; writes the mean duration (ms) of each node into ms_out
  * (length = node count from tg_describe). Inputs must have been set by a prior step. */
 tg_status tg_profile_nodes(tg_runtime* rt, int iters, double* ms_out, int64_t n_out);
+/* Run the step `iters` times eagerly, every kernel dispatched with start / end events of
+ * its own (hipExtLaunchKernel), and write each launch node's mean kernel time (ms: the
+ * durations of the kernels it launches, summed, without gaps between launches) into
+ * ms_out (length = node count). Measurement only; no counterpart in the reference. */
+tg_status tg_profile_kernels(tg_runtime* rt, int iters, double* ms_out, int64_t n_out);
 /* Time `steps` graph replays (device-resident inputs from the previous step) between two
  * HIP events; returns total milliseconds. */
 tg_status tg_time_replays(tg_runtime* rt, int steps, double* total_ms);

@@ -24,9 +24,9 @@ EXPORTED = (
     'tg_last_error', 'tg_device_count', 'tg_runtime_create', 'tg_runtime_create_sibling', 'tg_destroy',
     'tg_param_count', 'tg_param_name', 'tg_param_numel', 'tg_upload_params', 'tg_download_params', 'tg_step',
     'tg_step_device', 'tg_stage_batch', 'tg_step_staged', 'tg_run', 'tg_capture_count', 'tg_capture_name', 'tg_get_capture', 'tg_reset_optimizer',
-    'tg_set_lr', 'tg_describe', 'tg_plan', 'tg_profile_nodes', 'tg_time_replays', 'tg_time_kinds',
+    'tg_set_lr', 'tg_describe', 'tg_plan', 'tg_profile_nodes', 'tg_profile_kernels', 'tg_time_replays', 'tg_time_kinds',
     'tg_state_count', 'tg_state_name', 'tg_state_numel', 'tg_download_state', 'tg_upload_state',
-    'tg_save_checkpoint', 'tg_load_checkpoint', 'tg_safetensors_index', 'tg_step_noalloc',
+    'tg_save_checkpoint', 'tg_load_checkpoint', 'tg_check_checkpoint', 'tg_safetensors_index', 'tg_step_noalloc',
 )
 
 
@@ -87,6 +87,7 @@ def lib():
     L.tg_describe.argtypes = [vp, ctypes.c_char_p, ctypes.c_int64]
     L.tg_plan.argtypes = [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_int64]
     L.tg_profile_nodes.argtypes = [vp, ctypes.c_int, ctypes.POINTER(ctypes.c_double), ctypes.c_int64]
+    L.tg_profile_kernels.argtypes = [vp, ctypes.c_int, ctypes.POINTER(ctypes.c_double), ctypes.c_int64]
     L.tg_time_replays.argtypes = [vp, ctypes.c_int, ctypes.POINTER(ctypes.c_double)]
     L.tg_time_kinds.argtypes = [vp, ctypes.c_char_p, ctypes.c_int, ctypes.POINTER(ctypes.c_double),
                                 ctypes.POINTER(ctypes.c_int)]
@@ -101,6 +102,7 @@ def lib():
     L.tg_save_checkpoint.argtypes = [vp, ctypes.c_char_p]
     L.tg_load_checkpoint.argtypes = [vp, ctypes.c_char_p]
     L.tg_safetensors_index.argtypes = [ctypes.c_char_p, ctypes.c_int64, ctypes.c_char_p, ctypes.c_int64]
+    L.tg_check_checkpoint.argtypes = [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_int64]
     _lib = L
     return L
 
@@ -123,6 +125,14 @@ def plan(ir_json: str) -> dict:
     buf = ctypes.create_string_buffer(1 << 24)
     _check(lib().tg_plan(ir_json.encode(), buf, len(buf)))
     return json.loads(buf.value.decode())
+
+
+def check_checkpoint(ir_json: str, path: str) -> dict:
+    """The checks a checkpoint load into the graph `ir_json` would make, on the host only
+    (tg_check_checkpoint)."""
+    out = ctypes.create_string_buffer(4096)
+    _check(lib().tg_check_checkpoint(ir_json.encode(), str(path).encode(), out, len(out)))
+    return json.loads(out.value.decode())
 
 
 def safetensors_index(buf: bytes) -> dict:
@@ -276,6 +286,14 @@ class NativeRuntime:
         n = len(self.describe()['nodes'])
         out = (ctypes.c_double * n)()
         _check(lib().tg_profile_nodes(self._h, iters, out, n))
+        return list(out)
+
+    def profile_kernels(self, iters: int) -> List[float]:
+        """Mean kernel time (ms) of each launch node over `iters` eager steps: the kernels'
+        own start-to-end durations, without the gaps between launches."""
+        n = len(self.describe()['nodes'])
+        out = (ctypes.c_double * n)()
+        _check(lib().tg_profile_kernels(self._h, iters, out, n))
         return list(out)
 
     def time_replays(self, steps: int) -> float:

@@ -559,8 +559,8 @@ bool attention_supported(int64_t T, int64_t dh) { return dh == kDH && (T == 64 |
 void attention_fwd(const AttnDesc& a, hipStream_t st) {
   const int blocks = a.B * a.H * (a.T / kQBF);
   if (blocks <= 0) return;
-  if (a.T == 128) k_attn_fwd<128, kQBF><<<blocks, kNT, 0, st>>>(a);
-  else k_attn_fwd<64, kQBF><<<blocks, kNT, 0, st>>>(a);
+  if (a.T == 128) klaunch(k_attn_fwd<128, kQBF>, blocks, kNT, 0, st, a);
+  else klaunch(k_attn_fwd<64, kQBF>, blocks, kNT, 0, st, a);
 }
 
 void attention_bwd(const AttnBwdDesc& a, hipStream_t st) {
@@ -568,11 +568,11 @@ void attention_bwd(const AttnBwdDesc& a, hipStream_t st) {
   if (blocks <= 0) return;
   const int blocks_a = a.B * a.H * (a.T / kQBF);
   if (a.T == 128) {
-    k_attn_bwd_a<128, kQBF><<<blocks_a, kNT, 0, st>>>(a);
-    k_attn_bwd_b<128, kQB><<<blocks, kNT, 0, st>>>(a);
+    klaunch(k_attn_bwd_a<128, kQBF>, blocks_a, kNT, 0, st, a);
+    klaunch(k_attn_bwd_b<128, kQB>, blocks, kNT, 0, st, a);
   } else {
-    k_attn_bwd_a<64, kQBF><<<blocks_a, kNT, 0, st>>>(a);
-    k_attn_bwd_b<64, kQB><<<blocks, kNT, 0, st>>>(a);
+    klaunch(k_attn_bwd_a<64, kQBF>, blocks_a, kNT, 0, st, a);
+    klaunch(k_attn_bwd_b<64, kQB>, blocks, kNT, 0, st, a);
   }
 }
 

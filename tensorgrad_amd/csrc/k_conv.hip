@@ -248,13 +248,13 @@ bool pool_small(const PoolDesc& d) {
 void conv2d(const float* x, const float* w, float* y, const ConvDesc& c, hipStream_t st) {
   int64_t n = c.B * c.Cout * c.Ho * c.Wo;
   if (n <= 0) return;
-  k_conv2d<<<grid_for(n), 256, 0, st>>>(x, w, y, c);
+  klaunch(k_conv2d, grid_for(n), 256, 0, st, x, w, y, c);
 }
 
 void conv2d_input_grad(const float* w, const float* dy, float* dx, const ConvDesc& c, hipStream_t st) {
   int64_t n = c.B * c.Cin * c.H * c.W;
   if (n <= 0) return;
-  k_conv2d_dx<<<grid_for(n), 256, 0, st>>>(w, dy, dx, c);
+  klaunch(k_conv2d_dx, grid_for(n), 256, 0, st, w, dy, dx, c);
 }
 
 int64_t conv2d_weight_grad_workspace(const ConvDesc&) { return 0; }
@@ -263,17 +263,17 @@ void conv2d_weight_grad(const float* x, const float* dy, float* dw, const ConvDe
   int64_t nW = c.Cout * c.CinPG * c.kH * c.kW;
   if (nW <= 0) return;
   int64_t blocks = nW < 65536 ? nW : 65536;
-  k_conv2d_dw<<<(int)blocks, 256, 0, st>>>(x, dy, dw, c);
+  klaunch(k_conv2d_dw, (int)blocks, 256, 0, st, x, dy, dw, c);
 }
 
 void max_pool(const float* x, float* y, const PoolDesc& p, hipStream_t st) {
   int64_t n = p.B * p.C * p.Ho * p.Wo;
   if (n <= 0) return;
   if (pool_small(p)) {
-    k_max_pool32<<<grid_for(n), 256, 0, st>>>(x, y, pool32(p));
+    klaunch(k_max_pool32, grid_for(n), 256, 0, st, x, y, pool32(p));
     return;
   }
-  k_max_pool<<<grid_for(n), 256, 0, st>>>(x, y, p);
+  klaunch(k_max_pool, grid_for(n), 256, 0, st, x, y, p);
 }
 
 void max_pool_grad(const float* x, const float* dy, float* dx, const PoolDesc& p, hipStream_t st) {
@@ -282,10 +282,10 @@ void max_pool_grad(const float* x, const float* dy, float* dx, const PoolDesc& p
   const bool tiled = p.sH == p.kH && p.sW == p.kW && p.pH == 0 && p.pW == 0 && p.H == p.Ho * p.sH &&
                      p.W == p.Wo * p.sW;
   if (tiled && pool_small(p)) {
-    k_max_pool_grad_tiled<<<grid_for(p.B * p.C * p.Ho * p.Wo), 256, 0, st>>>(x, dy, dx, pool32(p));
+    klaunch(k_max_pool_grad_tiled, grid_for(p.B * p.C * p.Ho * p.Wo), 256, 0, st, x, dy, dx, pool32(p));
     return;
   }
-  k_max_pool_grad<<<grid_for(n), 256, 0, st>>>(x, dy, dx, p);
+  klaunch(k_max_pool_grad, grid_for(n), 256, 0, st, x, dy, dx, p);
 }
 
 }  // namespace tgk

@@ -347,9 +347,9 @@ bool small_wgrad_ok(const ConvDesc& d) {
 template <int MODE, bool FAST, int F>
 void launch_tile(const ConvPlan& p, const ConvGemmArgs& a, hipStream_t st) {
   const dim3 grid((unsigned)p.blocks);
-  if (p.bm == 32) k_conv_gemm<MODE, FAST, 32, 128, F><<<grid, kCT, 0, st>>>(a);
-  else if (p.bn == 64) k_conv_gemm<MODE, FAST, 64, 64, F><<<grid, kCT, 0, st>>>(a);
-  else k_conv_gemm<MODE, FAST, 64, 128, F><<<grid, kCT, 0, st>>>(a);
+  if (p.bm == 32) klaunch(k_conv_gemm<MODE, FAST, 32, 128, F>, grid, kCT, 0, st, a);
+  else if (p.bn == 64) klaunch(k_conv_gemm<MODE, FAST, 64, 64, F>, grid, kCT, 0, st, a);
+  else klaunch(k_conv_gemm<MODE, FAST, 64, 128, F>, grid, kCT, 0, st, a);
 }
 
 // The loader variant (conv_flags) of a launch picks the instantiation.
@@ -404,7 +404,7 @@ void conv2d_gemm(const float* x, const float* w, float* y, const ConvDesc& d, hi
   if (d.CinPG * d.kH * d.kW <= kSmallTaps && (d.Cout / d.G) * kSmallTaps <= kSmallW) {
     // the K taps of a row of W are contiguous: W[co][cl][kh][kw] = w[co * K + q]
     const int64_t n = d.B * d.G * ((d.Ho * d.Wo + 255) / 256);
-    if (n > 0) k_conv_small_fwd<<<(unsigned)n, 256, 0, st>>>(a);
+    if (n > 0) klaunch(k_conv_small_fwd, (unsigned)n, 256, 0, st, a);
     return;
   }
   if (p.blocks > 0) launch_mode<CV_FWD>(p, a, true, st);
@@ -430,12 +430,12 @@ void conv2d_weight_grad_gemm(const float* x, const float* dy, float* dw, const C
     sa.K = (int)(d.CinPG * d.kH * d.kW);
     const int64_t per = d.Cout * sa.K;
     const int64_t nch = (a.CoutPG + kSmallCo - 1) / kSmallCo;
-    k_conv_small_wgrad<<<(unsigned)(d.B * d.G * nch), 256, 0, st>>>(sa);
+    klaunch(k_conv_small_wgrad, (unsigned)(d.B * d.G * nch), 256, 0, st, sa);
     if (per < 16384 && d.B > 16) {
-      k_conv_wgrad_reduce_wave<<<(unsigned)((per + 3) / 4), 256, 0, st>>>(work, (int)d.B, per, dw);
+      klaunch(k_conv_wgrad_reduce_wave, (unsigned)((per + 3) / 4), 256, 0, st, work, (int)d.B, per, dw);
     } else {
       const int64_t nb = std::min<int64_t>((per + 255) / 256, 4096);
-      k_conv_wgrad_reduce<<<(int)nb, 256, 0, st>>>(work, (int)d.B, per, dw);
+      klaunch(k_conv_wgrad_reduce, (int)nb, 256, 0, st, work, (int)d.B, per, dw);
     }
     return;
   }
@@ -445,10 +445,10 @@ void conv2d_weight_grad_gemm(const float* x, const float* dy, float* dw, const C
   if (p.splits > 1) {
     const int64_t per = (int64_t)a.G * a.M * a.N;
     if (per < 16384 && p.splits > 16) {
-      k_conv_wgrad_reduce_wave<<<(unsigned)((per + 3) / 4), 256, 0, st>>>(work, p.splits, per, dw);
+      klaunch(k_conv_wgrad_reduce_wave, (unsigned)((per + 3) / 4), 256, 0, st, work, p.splits, per, dw);
     } else {
       const int64_t nb = std::min<int64_t>((per + 255) / 256, 4096);
-      k_conv_wgrad_reduce<<<(int)nb, 256, 0, st>>>(work, p.splits, per, dw);
+      klaunch(k_conv_wgrad_reduce, (int)nb, 256, 0, st, work, p.splits, per, dw);
     }
   }
 }

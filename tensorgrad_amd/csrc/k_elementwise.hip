@@ -303,38 +303,38 @@ void binary(int op, const void* a, int a_dt, const void* b, int b_dt, void* out,
     }
   }
   if (flat) {
-    k_binary_flat<<<grid_for(n), kThreads, 0, st>>>(op, (const float*)a, (const float*)b, (float*)out, n);
+    klaunch(k_binary_flat, grid_for(n), kThreads, 0, st, op, (const float*)a, (const float*)b, (float*)out, n);
   } else {
-    k_binary<<<grid_for(n), kThreads, 0, st>>>(op, a, a_dt, b, b_dt, out, out_dt, sp, n);
+    klaunch(k_binary, grid_for(n), kThreads, 0, st, op, a, a_dt, b, b_dt, out, out_dt, sp, n);
   }
 }
 
 void scalar_op(bool mul, const void* a, int a_dt, double s, float* out, int64_t n, hipStream_t st) {
   if (n <= 0) return;
-  k_scalar<<<grid_for(n), kThreads, 0, st>>>(mul, a, a_dt, s, out, n);
+  klaunch(k_scalar, grid_for(n), kThreads, 0, st, mul, a, a_dt, s, out, n);
 }
 
 void unary(int op, const float* a, float* out, int64_t n, hipStream_t st) {
   if (n <= 0) return;
-  k_unary<<<grid_for(n), kThreads, 0, st>>>(op, a, out, n);
+  klaunch(k_unary, grid_for(n), kThreads, 0, st, op, a, out, n);
 }
 
 void relu_grad(const float* x, const float* dy, float* out, int64_t n, hipStream_t st) {
   if (n <= 0) return;
-  k_relu_grad<<<grid_for(n), kThreads, 0, st>>>(x, dy, out, n);
+  klaunch(k_relu_grad, grid_for(n), kThreads, 0, st, x, dy, out, n);
 }
 
 void where(const int32_t* cond, const void* a, const void* b, int dt, void* out, const Strided& sp, int64_t n,
            hipStream_t st) {
   (void)dt;
   if (n <= 0) return;
-  k_where<<<grid_for(n), kThreads, 0, st>>>(cond, a, b, dt, out, sp, n);
+  klaunch(k_where, grid_for(n), kThreads, 0, st, cond, a, b, dt, out, sp, n);
 }
 
 void where_causal(const float* a, float* out, int64_t outer, int64_t D, double fill, hipStream_t st) {
   int64_t total = outer * D * D;
   if (total <= 0) return;
-  k_where_causal<<<grid_for(total), kThreads, 0, st>>>(a, out, total, D, (float)fill);
+  klaunch(k_where_causal, grid_for(total), kThreads, 0, st, a, out, total, D, (float)fill);
 }
 
 void strided_copy(void* dst, const void* src, const Strided& sp, int64_t n, hipStream_t st) {
@@ -356,7 +356,7 @@ void strided_copy(void* dst, const void* src, const Strided& sp, int64_t n, hipS
   bool small = n < (int64_t(1) << 31) && span0 < (int64_t(1) << 31) && span1 < (int64_t(1) << 31);
   for (int d = 0; d < r; ++d) if (s0[d] < 0 || s1[d] < 0) small = false;
   if (!small) {
-    k_strided_copy<<<grid_for(n), kThreads, 0, st>>>((uint32_t*)dst, (const uint32_t*)src, sp, n);
+    klaunch(k_strided_copy, grid_for(n), kThreads, 0, st, (uint32_t*)dst, (const uint32_t*)src, sp, n);
     return;
   }
   if (r == 0) { dd[0] = 1; s0[0] = s1[0] = 0; r = 1; }
@@ -374,8 +374,8 @@ void strided_copy(void* dst, const void* src, const Strided& sp, int64_t n, hipS
   const int64_t nv = n / vec;
   int64_t b = (nv + 255) / 256;
   if (b > 16384) b = 16384;
-  if (vec == 4) k_copy32<4><<<(int)b, 256, 0, st>>>((uint32_t*)dst, (const uint32_t*)src, c, (uint32_t)nv);
-  else k_copy32<1><<<(int)b, 256, 0, st>>>((uint32_t*)dst, (const uint32_t*)src, c, (uint32_t)nv);
+  if (vec == 4) klaunch(k_copy32<4>, (int)b, 256, 0, st, (uint32_t*)dst, (const uint32_t*)src, c, (uint32_t)nv);
+  else klaunch(k_copy32<1>, (int)b, 256, 0, st, (uint32_t*)dst, (const uint32_t*)src, c, (uint32_t)nv);
 }
 
 void fill(void* dst, int dt, double value, int64_t n, hipStream_t st) {
@@ -383,35 +383,35 @@ void fill(void* dst, int dt, double value, int64_t n, hipStream_t st) {
   uint32_t bits;
   if (dt == DT_F32) { float f = (float)value; memcpy(&bits, &f, 4); }
   else { int32_t v = (int32_t)value; memcpy(&bits, &v, 4); }
-  k_fill<<<grid_for(n), kThreads, 0, st>>>((uint32_t*)dst, bits, n);
+  klaunch(k_fill, grid_for(n), kThreads, 0, st, (uint32_t*)dst, bits, n);
 }
 
 void arange(void* dst, int dt, int64_t n, hipStream_t st) {
   if (n <= 0) return;
-  k_arange<<<grid_for(n), kThreads, 0, st>>>(dst, dt, n);
+  klaunch(k_arange, grid_for(n), kThreads, 0, st, dst, dt, n);
 }
 
 void one_hot(const int32_t* idx, int64_t rows, int64_t depth, void* out, int dt, hipStream_t st) {
   int64_t total = rows * depth;
   if (total <= 0) return;
-  k_one_hot<<<grid_for(total), kThreads, 0, st>>>(idx, total, depth, out, dt);
+  klaunch(k_one_hot, grid_for(total), kThreads, 0, st, idx, total, depth, out, dt);
 }
 
 void dropout(const float* a, float* out, int64_t n, const int32_t* seed, uint32_t salt_const, double p,
              hipStream_t st) {
   if (n <= 0) return;
-  k_dropout<<<grid_for(n), kThreads, 0, st>>>(a, out, n, seed, salt_const, p, 1.0 / (1.0 - p));
+  klaunch(k_dropout, grid_for(n), kThreads, 0, st, a, out, n, seed, salt_const, p, 1.0 / (1.0 - p));
 }
 
 void randn(float* out, int64_t n, const int32_t* seed, uint32_t salt_const, hipStream_t st) {
   if (n <= 0) return;
-  k_randn<<<grid_for(n), kThreads, 0, st>>>(out, n, seed, salt_const);
+  klaunch(k_randn, grid_for(n), kThreads, 0, st, out, n, seed, salt_const);
 }
 
 void categorical(const float* a, int32_t* out, int64_t outer, int64_t D, const int32_t* seed, uint32_t salt_const,
                  hipStream_t st) {
   if (outer <= 0) return;
-  k_categorical<<<grid_for(outer), kThreads, 0, st>>>(a, out, outer, D, seed, salt_const);
+  klaunch(k_categorical, grid_for(outer), kThreads, 0, st, a, out, outer, D, seed, salt_const);
 }
 
 }  // namespace tgk

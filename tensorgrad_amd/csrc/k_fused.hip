@@ -389,19 +389,19 @@ void fused(const FusedProgram& prog, int64_t n, hipStream_t st) {
     int64_t b = (n + 3) / 4;
     if (b > 16384) b = 16384;
     const size_t lds = 64 + (size_t)prog.nregs * ept * 256 * 4;   // 16 words of partials first
-    if (ept == 1) k_fused_rows<64, 1><<<(int)b, 256, lds, st>>>(prog, (uint32_t)n, (uint32_t)D);
-    else if (ept == 2) k_fused_rows<64, 2><<<(int)b, 256, lds, st>>>(prog, (uint32_t)n, (uint32_t)D);
-    else if (ept == 4) k_fused_rows<64, 4><<<(int)b, 256, lds, st>>>(prog, (uint32_t)n, (uint32_t)D);
-    else if (ept == 8) k_fused_rows<64, 8><<<(int)b, 256, lds, st>>>(prog, (uint32_t)n, (uint32_t)D);
-    else k_fused_rows<64, 16><<<(int)b, 256, lds, st>>>(prog, (uint32_t)n, (uint32_t)D);
+    if (ept == 1) klaunch(k_fused_rows<64, 1>, (int)b, 256, lds, st, prog, (uint32_t)n, (uint32_t)D);
+    else if (ept == 2) klaunch(k_fused_rows<64, 2>, (int)b, 256, lds, st, prog, (uint32_t)n, (uint32_t)D);
+    else if (ept == 4) klaunch(k_fused_rows<64, 4>, (int)b, 256, lds, st, prog, (uint32_t)n, (uint32_t)D);
+    else if (ept == 8) klaunch(k_fused_rows<64, 8>, (int)b, 256, lds, st, prog, (uint32_t)n, (uint32_t)D);
+    else klaunch(k_fused_rows<64, 16>, (int)b, 256, lds, st, prog, (uint32_t)n, (uint32_t)D);
     return;
   }
   int64_t b = (n + 255) / 256;
   if (b > 16384) b = 16384;
   // LDS holds only the registers the program uses.
   const size_t lds = (size_t)prog.nregs * prog.vec * 256 * 4;
-  if (prog.vec == 4) k_fused<4><<<(int)b, 256, lds, st>>>(prog, (uint32_t)n);
-  else k_fused<1><<<(int)b, 256, lds, st>>>(prog, (uint32_t)n);
+  if (prog.vec == 4) klaunch(k_fused<4>, (int)b, 256, lds, st, prog, (uint32_t)n);
+  else klaunch(k_fused<1>, (int)b, 256, lds, st, prog, (uint32_t)n);
 }
 
 }  // namespace tgk

@@ -428,13 +428,13 @@ void gemm(const GemmDesc& d, float* work, hipStream_t st) {
     const int64_t b = (outs + per - 1) / per;
     const dim3 grid((unsigned)(b < 65535 ? b : 65535));
     switch (L) {
-      case 1: k_gemm_tiny<1><<<grid, 256, 0, st>>>(d); return;
-      case 2: k_gemm_tiny<2><<<grid, 256, 0, st>>>(d); return;
-      case 4: k_gemm_tiny<4><<<grid, 256, 0, st>>>(d); return;
-      case 8: k_gemm_tiny<8><<<grid, 256, 0, st>>>(d); return;
-      case 16: k_gemm_tiny<16><<<grid, 256, 0, st>>>(d); return;
-      case 32: k_gemm_tiny<32><<<grid, 256, 0, st>>>(d); return;
-      default: k_gemm_tiny<64><<<grid, 256, 0, st>>>(d); return;
+      case 1: klaunch(k_gemm_tiny<1>, grid, 256, 0, st, d); return;
+      case 2: klaunch(k_gemm_tiny<2>, grid, 256, 0, st, d); return;
+      case 4: klaunch(k_gemm_tiny<4>, grid, 256, 0, st, d); return;
+      case 8: klaunch(k_gemm_tiny<8>, grid, 256, 0, st, d); return;
+      case 16: klaunch(k_gemm_tiny<16>, grid, 256, 0, st, d); return;
+      case 32: klaunch(k_gemm_tiny<32>, grid, 256, 0, st, d); return;
+      default: klaunch(k_gemm_tiny<64>, grid, 256, 0, st, d); return;
     }
   }
   Plan p = plan_for(d);
@@ -454,10 +454,10 @@ void gemm(const GemmDesc& d, float* work, hipStream_t st) {
   if (dma_ok(d, p, ak, bk)) {
 #define TG_DMA_LAUNCH(BM_, BN_, BK_, NS_, NT_, KG_)                                                  \
   do {                                                                                             \
-    if (ak && bk) k_gemm_dma<BM_, BN_, BK_, NS_, true, true, NT_, KG_><<<grid, NT_, 0, st>>>(g);     \
-    else if (ak) k_gemm_dma<BM_, BN_, BK_, NS_, true, false, NT_, KG_><<<grid, NT_, 0, st>>>(g);     \
-    else if (bk) k_gemm_dma<BM_, BN_, BK_, NS_, false, true, NT_, KG_><<<grid, NT_, 0, st>>>(g);     \
-    else k_gemm_dma<BM_, BN_, BK_, NS_, false, false, NT_, KG_><<<grid, NT_, 0, st>>>(g);            \
+    if (ak && bk) klaunch(k_gemm_dma<BM_, BN_, BK_, NS_, true, true, NT_, KG_>, grid, NT_, 0, st, g);     \
+    else if (ak) klaunch(k_gemm_dma<BM_, BN_, BK_, NS_, true, false, NT_, KG_>, grid, NT_, 0, st, g);     \
+    else if (bk) klaunch(k_gemm_dma<BM_, BN_, BK_, NS_, false, true, NT_, KG_>, grid, NT_, 0, st, g);     \
+    else klaunch(k_gemm_dma<BM_, BN_, BK_, NS_, false, false, NT_, KG_>, grid, NT_, 0, st, g);            \
   } while (0)
     // 128 x 128 tiles two or more per CU: a two-stage ring (64 KiB of LDS) so two blocks
     // share a CU and one's prologue and stores overlap the other's MFMAs; the ring depth
@@ -470,10 +470,10 @@ void gemm(const GemmDesc& d, float* work, hipStream_t st) {
     else TG_DMA_LAUNCH(64, 64, 64, 4, 512, 2);
 #undef TG_DMA_LAUNCH
   } else if (dma_bdw_ok(d, p, ak, bk)) {
-    if (ak && bk) k_gemm_dma<64, 64, 64, 4, true, true, 512, 2, true><<<grid, 512, 0, st>>>(g);
-    else if (ak) k_gemm_dma<64, 64, 64, 4, true, false, 512, 2, true><<<grid, 512, 0, st>>>(g);
-    else if (bk) k_gemm_dma<64, 64, 64, 4, false, true, 512, 2, true><<<grid, 512, 0, st>>>(g);
-    else k_gemm_dma<64, 64, 64, 4, false, false, 512, 2, true><<<grid, 512, 0, st>>>(g);
+    if (ak && bk) klaunch(k_gemm_dma<64, 64, 64, 4, true, true, 512, 2, true>, grid, 512, 0, st, g);
+    else if (ak) klaunch(k_gemm_dma<64, 64, 64, 4, true, false, 512, 2, true>, grid, 512, 0, st, g);
+    else if (bk) klaunch(k_gemm_dma<64, 64, 64, 4, false, true, 512, 2, true>, grid, 512, 0, st, g);
+    else klaunch(k_gemm_dma<64, 64, 64, 4, false, false, 512, 2, true>, grid, 512, 0, st, g);
   } else if (use_gen_dma() && dma_gen_ok(d, ak, bk)) {
     // 128 x 128 tiles when the plan chose them, else 64 x 64 with 32-k stages (the plan's
     // k per split is a multiple of 32 either way)
@@ -485,10 +485,10 @@ void gemm(const GemmDesc& d, float* work, hipStream_t st) {
     const dim3 grid((unsigned)gb);
 #define TG_GEN_LAUNCH(BM_, NS_, KG_)                                                                          \
   do {                                                                                                        \
-    if (ak && bk) k_gemm_dma<BM_, BM_, 32, NS_, true, true, 512, KG_, true, true, true><<<grid, 512, 0, st>>>(g);   \
-    else if (ak) k_gemm_dma<BM_, BM_, 32, NS_, true, false, 512, KG_, true, true, true><<<grid, 512, 0, st>>>(g);   \
-    else if (bk) k_gemm_dma<BM_, BM_, 32, NS_, false, true, 512, KG_, true, true, true><<<grid, 512, 0, st>>>(g);   \
-    else k_gemm_dma<BM_, BM_, 32, NS_, false, false, 512, KG_, true, true, true><<<grid, 512, 0, st>>>(g);          \
+    if (ak && bk) klaunch(k_gemm_dma<BM_, BM_, 32, NS_, true, true, 512, KG_, true, true, true>, grid, 512, 0, st, g);   \
+    else if (ak) klaunch(k_gemm_dma<BM_, BM_, 32, NS_, true, false, 512, KG_, true, true, true>, grid, 512, 0, st, g);   \
+    else if (bk) klaunch(k_gemm_dma<BM_, BM_, 32, NS_, false, true, 512, KG_, true, true, true>, grid, 512, 0, st, g);   \
+    else klaunch(k_gemm_dma<BM_, BM_, 32, NS_, false, false, 512, KG_, true, true, true>, grid, 512, 0, st, g);          \
   } while (0)
     if (bt == 128 && gb >= 512) TG_GEN_LAUNCH(128, 2, 1);   // two blocks per CU, as above
     else if (bt == 128) TG_GEN_LAUNCH(128, 3, 1);
@@ -497,10 +497,10 @@ void gemm(const GemmDesc& d, float* work, hipStream_t st) {
   } else {
 #define TG_GEMM_LAUNCH(BM_, BN_, BK_)                                                      \
   do {                                                                                     \
-    if (ak && bk) k_gemm<BM_, BN_, BK_, true, true><<<grid, kThreads, 0, st>>>(g);        \
-    else if (ak) k_gemm<BM_, BN_, BK_, true, false><<<grid, kThreads, 0, st>>>(g);        \
-    else if (bk) k_gemm<BM_, BN_, BK_, false, true><<<grid, kThreads, 0, st>>>(g);        \
-    else k_gemm<BM_, BN_, BK_, false, false><<<grid, kThreads, 0, st>>>(g);               \
+    if (ak && bk) klaunch(k_gemm<BM_, BN_, BK_, true, true>, grid, kThreads, 0, st, g);        \
+    else if (ak) klaunch(k_gemm<BM_, BN_, BK_, true, false>, grid, kThreads, 0, st, g);        \
+    else if (bk) klaunch(k_gemm<BM_, BN_, BK_, false, true>, grid, kThreads, 0, st, g);        \
+    else klaunch(k_gemm<BM_, BN_, BK_, false, false>, grid, kThreads, 0, st, g);               \
   } while (0)
   if (p.bm == 128 && p.bn == 128) TG_GEMM_LAUNCH(128, 128, 32);
   else if (p.bm == 128) TG_GEMM_LAUNCH(128, 64, 32);
@@ -512,7 +512,7 @@ void gemm(const GemmDesc& d, float* work, hipStream_t st) {
     int64_t total = d.batch * d.M * d.N;
     int64_t nb = (total + 255) / 256;
     if (nb > 4096) nb = 4096;
-    k_splitk_reduce<<<(int)nb, 256, 0, st>>>(work, p.splits, g.sOs, d);
+    klaunch(k_splitk_reduce, (int)nb, 256, 0, st, work, p.splits, g.sOs, d);
   }
 }
 
@@ -561,10 +561,10 @@ void gemm_sum(const GemmDesc* ds, int n, hipStream_t st) {
   const bool bk = all.sBk == 1 && all.sBn != 1;
 #define TG_SEG_LAUNCH(BM_, BK_, NS_, KG_)                                                                          \
   do {                                                                                                           \
-    if (ak && bk) k_gemm_dma<BM_, BM_, BK_, NS_, true, true, 512, KG_, false, false, false, true><<<grid, 512, 0, st>>>(g); \
-    else if (ak) k_gemm_dma<BM_, BM_, BK_, NS_, true, false, 512, KG_, false, false, false, true><<<grid, 512, 0, st>>>(g); \
-    else if (bk) k_gemm_dma<BM_, BM_, BK_, NS_, false, true, 512, KG_, false, false, false, true><<<grid, 512, 0, st>>>(g); \
-    else k_gemm_dma<BM_, BM_, BK_, NS_, false, false, 512, KG_, false, false, false, true><<<grid, 512, 0, st>>>(g);        \
+    if (ak && bk) klaunch(k_gemm_dma<BM_, BM_, BK_, NS_, true, true, 512, KG_, false, false, false, true>, grid, 512, 0, st, g); \
+    else if (ak) klaunch(k_gemm_dma<BM_, BM_, BK_, NS_, true, false, 512, KG_, false, false, false, true>, grid, 512, 0, st, g); \
+    else if (bk) klaunch(k_gemm_dma<BM_, BM_, BK_, NS_, false, true, 512, KG_, false, false, false, true>, grid, 512, 0, st, g); \
+    else klaunch(k_gemm_dma<BM_, BM_, BK_, NS_, false, false, 512, KG_, false, false, false, true>, grid, 512, 0, st, g);        \
   } while (0)
   if (p.bm == 128) TG_SEG_LAUNCH(128, 32, 3, 1);
   else if (p.bk == 32) TG_SEG_LAUNCH(64, 32, 4, 2);
@@ -650,27 +650,27 @@ void gemm_group(const void* dev_image, size_t starts_off, int n, int64_t blocks,
   const dim3 grid((unsigned)blocks);
   if (tiling == 2) {   // 32-k stages on four wavefronts, 48 KiB: three blocks per CU
     switch (kind) {
-      case 3: k_gemm_dma_group<64, 64, 32, 3, true, true, 256, 1><<<grid, 256, 0, st>>>(table, starts, n); return;
-      case 2: k_gemm_dma_group<64, 64, 32, 3, true, false, 256, 1><<<grid, 256, 0, st>>>(table, starts, n); return;
-      case 1: k_gemm_dma_group<64, 64, 32, 3, false, true, 256, 1><<<grid, 256, 0, st>>>(table, starts, n); return;
-      case 0: k_gemm_dma_group<64, 64, 32, 3, false, false, 256, 1><<<grid, 256, 0, st>>>(table, starts, n); return;
+      case 3: klaunch(k_gemm_dma_group<64, 64, 32, 3, true, true, 256, 1>, grid, 256, 0, st, table, starts, n); return;
+      case 2: klaunch(k_gemm_dma_group<64, 64, 32, 3, true, false, 256, 1>, grid, 256, 0, st, table, starts, n); return;
+      case 1: klaunch(k_gemm_dma_group<64, 64, 32, 3, false, true, 256, 1>, grid, 256, 0, st, table, starts, n); return;
+      case 0: klaunch(k_gemm_dma_group<64, 64, 32, 3, false, false, 256, 1>, grid, 256, 0, st, table, starts, n); return;
       default: throw std::runtime_error("gemm group: bad kind");
     }
   }
   if (tiling == 1) {   // 32-k stages: the 64 KiB-LDS variant, two blocks per CU
     switch (kind) {
-      case 3: k_gemm_dma_group<64, 64, 32, 4, true, true, 512, 2><<<grid, 512, 0, st>>>(table, starts, n); return;
-      case 2: k_gemm_dma_group<64, 64, 32, 4, true, false, 512, 2><<<grid, 512, 0, st>>>(table, starts, n); return;
-      case 1: k_gemm_dma_group<64, 64, 32, 4, false, true, 512, 2><<<grid, 512, 0, st>>>(table, starts, n); return;
-      case 0: k_gemm_dma_group<64, 64, 32, 4, false, false, 512, 2><<<grid, 512, 0, st>>>(table, starts, n); return;
+      case 3: klaunch(k_gemm_dma_group<64, 64, 32, 4, true, true, 512, 2>, grid, 512, 0, st, table, starts, n); return;
+      case 2: klaunch(k_gemm_dma_group<64, 64, 32, 4, true, false, 512, 2>, grid, 512, 0, st, table, starts, n); return;
+      case 1: klaunch(k_gemm_dma_group<64, 64, 32, 4, false, true, 512, 2>, grid, 512, 0, st, table, starts, n); return;
+      case 0: klaunch(k_gemm_dma_group<64, 64, 32, 4, false, false, 512, 2>, grid, 512, 0, st, table, starts, n); return;
       default: throw std::runtime_error("gemm group: bad kind");
     }
   }
   switch (kind) {
-    case 3: k_gemm_dma_group<64, 64, 64, 4, true, true, 512, 2><<<grid, 512, 0, st>>>(table, starts, n); break;
-    case 2: k_gemm_dma_group<64, 64, 64, 4, true, false, 512, 2><<<grid, 512, 0, st>>>(table, starts, n); break;
-    case 1: k_gemm_dma_group<64, 64, 64, 4, false, true, 512, 2><<<grid, 512, 0, st>>>(table, starts, n); break;
-    case 0: k_gemm_dma_group<64, 64, 64, 4, false, false, 512, 2><<<grid, 512, 0, st>>>(table, starts, n); break;
+    case 3: klaunch(k_gemm_dma_group<64, 64, 64, 4, true, true, 512, 2>, grid, 512, 0, st, table, starts, n); break;
+    case 2: klaunch(k_gemm_dma_group<64, 64, 64, 4, true, false, 512, 2>, grid, 512, 0, st, table, starts, n); break;
+    case 1: klaunch(k_gemm_dma_group<64, 64, 64, 4, false, true, 512, 2>, grid, 512, 0, st, table, starts, n); break;
+    case 0: klaunch(k_gemm_dma_group<64, 64, 64, 4, false, false, 512, 2>, grid, 512, 0, st, table, starts, n); break;
     default: throw std::runtime_error("gemm group: bad kind");
   }
 }
@@ -906,11 +906,11 @@ void gather_rows(const int32_t* idx, int64_t rows, const float* table, int64_t V
   if (rows * N <= 0) return;
   if (N % 4 == 0 && rows * N < (int64_t(1) << 32) && V < (int64_t(1) << 32) && ((uintptr_t)table & 15) == 0 &&
       ((uintptr_t)out & 15) == 0) {
-    k_gather_rows4<<<grid_for(rows * N / 4), 256, 0, st>>>(idx, (uint32_t)rows, (const float4*)table, (uint32_t)V,
-                                                           (uint32_t)(N / 4), (float4*)out);
+    klaunch(k_gather_rows4, grid_for(rows * N / 4), 256, 0, st, idx, (uint32_t)rows, (const float4*)table,
+            (uint32_t)V, (uint32_t)(N / 4), (float4*)out);
     return;
   }
-  k_gather_rows<<<grid_for(rows * N), 256, 0, st>>>(idx, rows, table, V, N, out);
+  klaunch(k_gather_rows, grid_for(rows * N), 256, 0, st, idx, rows, table, V, N, out);
 }
 
 bool scatter_scan_form(int64_t rows, int64_t V) { return scatter_scans(rows, V); }
@@ -929,7 +929,7 @@ void scatter_rows(const int32_t* idx, int64_t rows, const float* dy, int64_t V, 
   if (scatter_scans(rows, V)) {
     const int64_t ny = (N + 255) / 256;
     if (ny > 65535) throw std::runtime_error("scatter_rows: N too large");
-    k_scatter_scan<<<dim3((unsigned)V, (unsigned)ny), 256, 0, st>>>(idx, rows, dy, N, out);
+    klaunch(k_scatter_scan, dim3((unsigned)V, (unsigned)ny), 256, 0, st, idx, rows, dy, N, out);
     return;
   }
   const int64_t items = (rows + kSeg - 1) / kSeg + V;
@@ -943,11 +943,11 @@ void scatter_rows(const int32_t* idx, int64_t rows, const float* dy, int64_t V, 
   const int64_t hist_bytes = (int64_t)nw * (V + 1) * 4;
   const int stash = hist_bytes + rows * 4 <= 65536 ? 1 : 0;
   const size_t lds = (size_t)(hist_bytes + (stash ? rows * 4 : 0));
-  k_bucket_rows<<<1, kBucketWaves * 64, lds, st>>>(idx, rows, V, stash, perm, offs, cstart, item_rng);
+  klaunch(k_bucket_rows, 1, kBucketWaves * 64, lds, st, idx, rows, V, stash, perm, offs, cstart, item_rng);
   const int64_t ny = (N + 255) / 256;
   dim3 g2((unsigned)items, (unsigned)(ny > 64 ? 64 : ny));
-  k_segment_partials<<<g2, 256, 0, st>>>(dy, N, V, perm, cstart, item_rng, part);
-  k_segment_finish<<<grid_for(V * N), 256, 0, st>>>(part, N, V, cstart, out);
+  klaunch(k_segment_partials, g2, 256, 0, st, dy, N, V, perm, cstart, item_rng, part);
+  klaunch(k_segment_finish, grid_for(V * N), 256, 0, st, part, N, V, cstart, out);
 }
 
 }  // namespace tgk

@@ -605,19 +605,19 @@ SumPlan sum_plan(const Strided& cells, int64_t ncells, int64_t nred) {
 
 void row_argmax(const float* a, int32_t* out, int64_t outer, int64_t D, hipStream_t st) {
   if (outer <= 0) return;
-  k_row_argmax<<<blocks_for_rows(outer), kWave * kRowsPerBlock, 0, st>>>(a, out, outer, D);
+  klaunch(k_row_argmax, blocks_for_rows(outer), kWave * kRowsPerBlock, 0, st, a, out, outer, D);
 }
 
 #define TG_ROW_LAUNCH(KERNEL, ROWS, ...)                                                            \
   do {                                                                                              \
     const int g_ = blocks_for_rows(ROWS);                                                           \
     const int b_ = kWave * kRowsPerBlock;                                                           \
-    if (D <= 64) KERNEL<1><<<g_, b_, 0, st>>>(__VA_ARGS__);                                         \
-    else if (D <= 128) KERNEL<2><<<g_, b_, 0, st>>>(__VA_ARGS__);                                   \
-    else if (D <= 256) KERNEL<4><<<g_, b_, 0, st>>>(__VA_ARGS__);                                   \
-    else if (D <= 512) KERNEL<8><<<g_, b_, 0, st>>>(__VA_ARGS__);                                   \
-    else if (D <= 1024) KERNEL<16><<<g_, b_, 0, st>>>(__VA_ARGS__);                                 \
-    else KERNEL<0><<<g_, b_, 0, st>>>(__VA_ARGS__);                                                 \
+    if (D <= 64) klaunch(KERNEL<1>, g_, b_, 0, st, __VA_ARGS__);                                         \
+    else if (D <= 128) klaunch(KERNEL<2>, g_, b_, 0, st, __VA_ARGS__);                                   \
+    else if (D <= 256) klaunch(KERNEL<4>, g_, b_, 0, st, __VA_ARGS__);                                   \
+    else if (D <= 512) klaunch(KERNEL<8>, g_, b_, 0, st, __VA_ARGS__);                                   \
+    else if (D <= 1024) klaunch(KERNEL<16>, g_, b_, 0, st, __VA_ARGS__);                                 \
+    else klaunch(KERNEL<0>, g_, b_, 0, st, __VA_ARGS__);                                                 \
   } while (0)
 
 void log_softmax(const float* a, float* out, int64_t outer, int64_t D, hipStream_t st) {
@@ -711,8 +711,8 @@ void colsum_batch(const ColSumBatch& b, hipStream_t st) {
   }
   if (blocks <= 0) return;
   if (blocks > INT32_MAX) throw std::runtime_error("column sums: too many blocks");
-  if (bt.nmid > 0) k_colsum<true><<<(unsigned)blocks, kColThreads, 0, st>>>(bt);
-  else k_colsum<false><<<(unsigned)blocks, kColThreads, 0, st>>>(bt);
+  if (bt.nmid > 0) klaunch(k_colsum<true>, (unsigned)blocks, kColThreads, 0, st, bt);
+  else klaunch(k_colsum<false>, (unsigned)blocks, kColThreads, 0, st, bt);
 }
 
 int64_t sum_counters(const Strided& cells, const Strided& red, int64_t ncells, int64_t nred) {
@@ -734,20 +734,20 @@ void reduce_sum(const float* a, float* out, const Strided& cells, const Strided&
     return;
   }
   if (block_form(red, ncells, nred)) {
-    k_sum_block<<<(unsigned)ncells, 256, 0, st>>>(a, cells, red, nred, out, div);
+    klaunch(k_sum_block, (unsigned)ncells, 256, 0, st, a, cells, red, nred, out, div);
     return;
   }
   SumPlan p = sum_plan(cells, ncells, nred);
   if (p.cols) {
     dim3 grid((unsigned)((ncells + 255) / 256), (unsigned)p.nchunks);
-    k_sum_cols<<<grid, 256, 0, st>>>(a, work, out, cells, red, ncells, nred, p.chunk, p.nchunks, div);
+    klaunch(k_sum_cols, grid, 256, 0, st, a, work, out, cells, red, ncells, nred, p.chunk, p.nchunks, div);
   } else {
     int64_t items = ncells * p.nchunks;
     int64_t b = (items + kRowsPerBlock - 1) / kRowsPerBlock;
     if (b > 16384) b = 16384;
-    k_sum_rows<<<(int)b, kWave * kRowsPerBlock, 0, st>>>(a, work, out, cells, red, ncells, nred, p.chunk, p.nchunks, div);
+    klaunch(k_sum_rows, (int)b, kWave * kRowsPerBlock, 0, st, a, work, out, cells, red, ncells, nred, p.chunk, p.nchunks, div);
   }
-  if (p.nchunks > 1) k_sum_finish<<<blocks_for_rows(ncells), kWave * kRowsPerBlock, 0, st>>>(work, out, ncells, p.nchunks, div);
+  if (p.nchunks > 1) klaunch(k_sum_finish, blocks_for_rows(ncells), kWave * kRowsPerBlock, 0, st, work, out, ncells, p.nchunks, div);
 }
 
 }  // namespace tgk

@@ -3,6 +3,7 @@
 // f32, or i32 for the `i32` and `bool` IR dtypes.
 #pragma once
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <cstdint>
 #include <vector>
 
@@ -12,6 +13,35 @@
 namespace tgk {
 
 constexpr int kMaxRank = 8;
+
+// Kernel timing for measurement (tg_profile_kernels): while a timer is installed on the
+// calling thread, each launch records the kernel's own start and end timestamps (those of
+// its dispatch packet, the quantity a profiler's kernel trace reports) into a pair of
+// events from the timer's pool; otherwise it is a plain launch.
+struct LaunchTimer {
+  std::vector<hipEvent_t> ev;   // pairs: ev[2i] start, ev[2i + 1] end
+  size_t used = 0;              // pairs handed out
+  size_t missed = 0;            // launches left untimed (pool exhausted)
+  bool take(hipEvent_t& a, hipEvent_t& b) {
+    if (2 * used + 1 >= ev.size()) { ++missed; return false; }
+    a = ev[2 * used];
+    b = ev[2 * used + 1];
+    ++used;
+    return true;
+  }
+};
+LaunchTimer*& launch_timer();   // the calling thread's installed timer (null: none)
+
+template <typename... Args, typename F = void (*)(Args...)>
+inline void klaunch(F kernel, const dim3& grid, const dim3& block, uint32_t lds, hipStream_t st, Args... args) {
+  hipEvent_t a = nullptr, b = nullptr;
+  LaunchTimer* t = launch_timer();
+  if (t && t->take(a, b)) {
+    hipExtLaunchKernelGGL(kernel, grid, block, lds, st, a, b, 0, args...);
+    return;
+  }
+  hipLaunchKernelGGL(kernel, grid, block, lds, st, args...);
+}
 
 // Division by a runtime constant d >= 1 for 0 <= x < 2^31 without a divide instruction:
 // q = (umulhi(x, m) + x) >> s with s = ceil(log2 d), m = floor(2^32 (2^s - d) / d) + 1
@@ -310,18 +340,55 @@ void max_pool(const float* x, float* y, const PoolDesc& p, hipStream_t st);
 void max_pool_grad(const float* x, const float* dy, float* dx, const PoolDesc& p, hipStream_t st);
 
 // ---- optimizer (k_optim.hip) ----------------------------------------------------------
-// One fused multi-tensor Adam/AdamW update, in place on p, m, v.
-// One launch unit of the fused Adam update: up to kAdamChunk consecutive elements of one
-// parameter (pointers already offset to the chunk's first element).
+// One fused multi-tensor update (Adam / AdamW, or SGD with momentum, Nesterov and L2
+// decay), in place on p and the optimizer state, with the gradient transforms of
+// normalizeGrads and clipGradNorm applied to each gradient element on the fly.
+// One launch unit: up to kAdamChunk consecutive elements of one parameter (pointers
+// already offset to the chunk's first element).
 constexpr int64_t kAdamChunk = 2048;
 struct AdamChunk {
-  float* p; float* m; float* v; const float* g;
-  const float* shrink_ptr;  // per-step decay shrink tensor, or null: use `shrink`
-  double shrink;
+  float* p; float* m; float* v; const float* g;   // SGD: m = velocity (null: no momentum)
+  const float* shrink_ptr;  // Adam: per-step decay shrink tensor, or null: use `shrink`
+  double shrink;            // Adam: static decay shrink; SGD: weight decay (0: none)
+  double mom;               // SGD: momentum (0: none)
   int64_t n;                // elements in the chunk, 1 .. kAdamChunk
+  int gdiv, gmul;           // value indices: g = f32(g / vals[gdiv]) then f32(g * vals[gmul]); -1: none
+  int flags;                // SGD: 1 Nesterov, 2 weight decay, 4 momentum
 };
 struct AdamHyper { double beta1, one_minus_beta1, beta2, one_minus_beta2, eps; };
-// `chunks` is a device array of `nchunks` descriptors covering every parameter.
-void adam_multi(const AdamChunk* chunks, int64_t nchunks, const float* lrt, AdamHyper h, hipStream_t st);
+// `chunks` is a device array of `nchunks` descriptors covering every parameter; `vals` the
+// value array of the gradient-norm launches (null when no chunk transforms its gradient).
+// Adam reads the f32 lrt at `lr`, SGD the f32 learning rate.
+void adam_multi(const AdamChunk* chunks, int64_t nchunks, const float* lr, AdamHyper h, const float* vals,
+                hipStream_t st);
+void sgd_multi(const AdamChunk* chunks, int64_t nchunks, const float* lr, const float* vals, hipStream_t st);
+
+// Gradient norms for clipGradNorm / normalizeGrads: per-tensor sums of squares, f32(x * x)
+// summed in f64 and rounded to f32 once (the evaluator's mul + sum_last), then a scalar
+// program over them (the reference's chained f32 adds, sqrt, add_scalar, div, min).
+// Deterministic: chunk partials in a fixed order, a sum's chunk partials added in a fixed
+// tree whichever block finishes it. The last block of a sum's chunks finishes that sum;
+// the block finishing the last sum runs the program.
+constexpr int64_t kNormChunk = 8192;   // gradient elements per block of a norm launch
+struct SqChunk {
+  const float* g;
+  int64_t n;     // 1 .. kNormChunk
+  int pre;       // value index dividing each element before squaring (normalised gradient), -1 none
+  int slot;      // sum this chunk belongs to
+};
+enum ScalarOp { SI_CONST, SI_ADD, SI_SUB, SI_MUL, SI_DIV, SI_MIN, SI_MAX, SI_ADDK, SI_MULK, SI_SQRT };
+struct ScalarInstr { int op, a, b, out; double k; };   // vals[out] = f32(vals[a] op vals[b] | k)
+constexpr int kNormMaxVals = 2048;                     // value array bound (LDS of the finishing block)
+struct NormLaunch {
+  const SqChunk* chunks; int64_t nchunks;
+  const int* slot_first;   // nslots + 1 chunk offsets: chunks of slot s are [first[s], first[s+1])
+  const int* slot_val;     // value index receiving slot s's rounded sum
+  int nslots;
+  const ScalarInstr* prog; int nprog;
+  float* vals; int nvals;
+  double* part;            // nchunks partials (workspace)
+  unsigned* counters;      // nslots + 1 launch-completion counters, left at zero
+};
+void grad_norms(const NormLaunch& a, hipStream_t st);
 
 }  // namespace tgk

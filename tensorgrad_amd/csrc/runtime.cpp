@@ -51,6 +51,11 @@
 // stand-in, not a device address): it uses the address hipGetSymbolAddress returns for
 // the current device (scratch_address).
 static constexpr size_t tg_kScratchBytes = (size_t)TG_SCRATCH_BYTES;
+
+tgk::LaunchTimer*& tgk::launch_timer() {
+  static thread_local LaunchTimer* t = nullptr;
+  return t;
+}
 static __device__ __align__(256) unsigned char scratch[tg_kScratchBytes];
 
 namespace tg {
@@ -217,7 +222,7 @@ class Runtime {
 
   // Optimizer state (state_input tensors: Adam m / v, SGD velocity) in name order, plus
   // the step counter t and the PRNG seed counter, for checkpoints.
-  const std::vector<std::string>& state_names();
+  const std::vector<std::string>& state_names() const;
   int64_t state_numel(const std::string& name) const;
   void download_state(int n, const char* const* names, float* const* data, const int64_t* numel);
   void upload_state(int n, const char* const* names, const float* const* data, const int64_t* numel);
@@ -226,8 +231,10 @@ class Runtime {
   void set_counters(long long t, long long prng) { t_ = t; prng_counter_ = prng; }
   void save_checkpoint(const std::string& path);
   void load_checkpoint(const std::string& path);
+  std::string check_checkpoint_file(const std::string& path) const;
   std::string describe();
   void profile_nodes(int iters, double* ms, int64_t n);
+  void profile_kernels(int iters, double* ms, int64_t n);
   double time_replays(int steps);
   double time_kinds(const std::string& kinds, int iters, int* launches);
 
@@ -283,8 +290,16 @@ class Runtime {
     counter_slots_ += n;
     return b;
   }
-  // fused Adam tables (device)
-  tgk::AdamChunk* adam_chunks_ = nullptr;
+  struct CkptPlan {
+    tgst::Index ix;
+    std::vector<std::pair<size_t, int>> writes;   // (index in ix.tensors, tensor id)
+    size_t n_state = 0;
+    long long t = 0, c = 0;
+    tgj::Value lr;
+  };
+  CkptPlan check_checkpoint(const std::vector<uint8_t>& buf) const;
+  std::map<std::string, std::pair<void*, size_t>> table_cache_;   // dev_table copies by key
+  const void* dev_table(const std::string& key, const void* data, size_t bytes);
   std::vector<int> state_roots_;
 
   hipGraph_t graph_ = nullptr;
@@ -373,8 +388,15 @@ class Runtime {
     JitSlot& j = jit_slots_[js];
     void* p1[] = {&j.args};
     void* p2[] = {&j.gargs, &j.args};
-    const hipError_t e = hipModuleLaunchKernel(j.fn, (unsigned)j.grid, 1, 1, (unsigned)j.threads, 1, 1, 0, st,
-                                               j.gemm ? p2 : p1, nullptr);
+    hipEvent_t a = nullptr, b = nullptr;
+    tgk::LaunchTimer* t = tgk::launch_timer();
+    // hipExtModuleLaunchKernel takes the global work size (blocks x threads per block)
+    const hipError_t e =
+        t && t->take(a, b)
+            ? hipExtModuleLaunchKernel(j.fn, (uint32_t)(j.grid * j.threads), 1, 1, (uint32_t)j.threads, 1, 1, 0, st,
+                                       j.gemm ? p2 : p1, nullptr, a, b, 0)
+            : hipModuleLaunchKernel(j.fn, (unsigned)j.grid, 1, 1, (unsigned)j.threads, 1, 1, 0, st, j.gemm ? p2 : p1,
+                                    nullptr);
     if (e != hipSuccess) throw Error(TG_DEVICE_ERROR, std::string("generated kernel launch: ") + hipGetErrorString(e));
   }
   void form_groups();
@@ -391,6 +413,7 @@ class Runtime {
   const tgj::Value& O(int op) const { return *ops_[op]; }
   int fld(int op, const char* f) const { return O(op).at(f).i32(); }
 
+  void read_document();
   void analyse();
   void relu_grads_from_outputs();
   void compute_views();
@@ -440,7 +463,42 @@ class Runtime {
   struct DeferredGemm { int op; tgk::GemmDesc d; int a, b, out, kind; };
   std::vector<DeferredGemm> deferred_gemms_;
   std::vector<char> defer_gemm_;     // op -> runs in a grouped launch
-  std::set<int> adam_ops_;
+  // Fused optimizer (k_optim.hip). Per parameter: the update (adam_update_m / _v / _p, or
+  // the pointwise chain of src/sgd.ts:155-170) and the gradient transforms ahead of it
+  // (normalizeGrads: g / broadcast(norm), clipGradNorm: g * broadcast(scale);
+  // src/grad.ts:110-172) run in one update launch. The transforms' scalars come from
+  // grad_norms launches just before it: per-parameter sums of squares, then a scalar
+  // program restating the IR's rank-0 ops (chained adds, sqrt, add_scalar, div, min).
+  struct OptParam {
+    int p = -1, g = -1;          // param tensor; gradient as the backward pass leaves it
+    int final_g = -1;            // the gradient tensor the update reads in the IR
+    int gdiv = -1, gmul = -1;    // transform scalar tensors (-1: none)
+    int div_out = -1;            // the normalised gradient tensor (output of the div)
+    int m = -1, v = -1;          // Adam moments; SGD: m = velocity
+    int lr = -1;                 // lrt (Adam) / lr (SGD) tensor
+    int shrink_t = -1;           // Adam: per-step decay shrink tensor
+    double shrink = 1.0;         // Adam: static decay shrink; SGD: weight decay
+    double mom = 0.0;            // SGD momentum
+    int flags = 0;               // SGD: 1 Nesterov, 2 weight decay, 4 momentum
+  };
+  std::vector<OptParam> opt_params_;
+  bool opt_sgd_ = false;
+  tgk::AdamHyper opt_hyper_{0.9, 0.1, 0.999, 0.001, 1e-8};
+  std::set<int> adam_ops_;           // IR ops the fused optimizer executes (updates and transforms)
+  struct NormSum { int g, pre_t, launch; };       // f32 sum of squares of g (divided by scalar pre_t first)
+  std::vector<NormSum> norm_sums_;
+  std::vector<int> norm_sum_val_;                  // value index of each sum
+  std::map<int, int> norm_val_;                    // scalar tensor -> value index
+  std::vector<tgk::ScalarInstr> norm_prog_[2];     // scalar program per norm launch
+  int norm_nvals_ = 0, norm_launches_ = 0;
+  bool use_fused_transforms_ = true;               // TG_OPT_FUSED=0: transforms and SGD op by op
+  void match_optimizer();
+  bool match_sgd(int pnew, const std::string& name, const std::map<std::string, int>& state_wb, OptParam& q,
+                 std::set<int>& ops, std::set<int>& wb) const;
+  bool scalar_bcast(int t) const;
+  bool opt_closed(const std::set<int>& ops, const std::set<int>& wb_ok) const;
+  void match_grad_transforms();
+  void emit_optimizer();
   void plan_gemm_groups();
   // A GEMM whose product only one element-form group reads (contiguously, in its own
   // iteration order) can run that group in its epilogue: one launch instead of two, and
@@ -518,6 +576,33 @@ Runtime::Runtime(const char* json, Runtime* par, bool plan_only) : parent(par) {
   } catch (std::exception& e) {
     throw Error(TG_INVALID_ARGUMENT, e.what());
   }
+  // A document missing fields or holding values of the wrong type is the caller's error.
+  try {
+    read_document();
+  } catch (Error&) {
+    throw;
+  } catch (std::exception& e) {
+    throw Error(TG_INVALID_ARGUMENT, std::string("IR: ") + e.what());
+  }
+  plan_only_ = plan_only;
+  analyse();
+  relu_grads_from_outputs();
+  compute_views();
+  lower();
+  if (!plan_only) hip_check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate");
+  split_init_nodes();
+  allocate();
+  bind_all();   // in plan-only mode this still runs every launch's host-side bounds proof
+  jit_finish();
+  if (!plan_only) prepare_noalloc();
+  if (!plan_only && !init_nodes_.empty()) {
+    for (auto& n : init_nodes_) n.launch(stream_);
+    hip_check(hipStreamSynchronize(stream_), "hipStreamSynchronize(constants)");
+  }
+}
+
+// Tensors, ops, outputs, captures and the optimizer block of the IR document.
+void Runtime::read_document() {
   const tgj::Value& g = doc_.at("graph");
   for (const auto& t : g.at("tensors").items) {
     TInfo ti;
@@ -546,22 +631,6 @@ Runtime::Runtime(const char* json, Runtime* par, bool plan_only) : parent(par) {
       lr_ = opt_cfg_->at("lr");
     }
   if (parent && opt_cfg_) throw Error(TG_INVALID_ARGUMENT, "compileForward: a sibling graph cannot carry an optimizer");
-
-  plan_only_ = plan_only;
-  analyse();
-  relu_grads_from_outputs();
-  compute_views();
-  lower();
-  if (!plan_only) hip_check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate");
-  split_init_nodes();
-  allocate();
-  bind_all();   // in plan-only mode this still runs every launch's host-side bounds proof
-  jit_finish();
-  if (!plan_only) prepare_noalloc();
-  if (!plan_only && !init_nodes_.empty()) {
-    for (auto& n : init_nodes_) n.launch(stream_);
-    hip_check(hipStreamSynchronize(stream_), "hipStreamSynchronize(constants)");
-  }
 }
 
 Runtime::~Runtime() {
@@ -573,7 +642,6 @@ Runtime::~Runtime() {
   if (workspace_ && !plan_only_) hipFree(workspace_);
   if (counters_ && !plan_only_) hipFree(counters_);
   if (fused_code_dev_ && !plan_only_) hipFree(fused_code_dev_);
-  if (adam_chunks_) hipFree(adam_chunks_);
   for (void* t : dev_tables_) hipFree(t);
   for (char* p : slots_) if (p) hipFree(p);
   if (staging_) hipHostFree(staging_);
@@ -632,6 +700,7 @@ void Runtime::analyse() {
       state_tid_[ops_[i]->at("name").str()] = out;
     }
   }
+  for (auto& kv : state_tid_) state_list_.push_back(kv.first);
 }
 
 // relu_grad(x, dy) = x > 0 ? dy : 0 reads the pre-activation x. Where relu(x) is also
@@ -931,32 +1000,458 @@ bool Runtime::gemm_desc(int i, tgk::GemmDesc& d) const {
   return true;
 }
 
-void Runtime::lower() {
-  // Fused Adam: collect adam_update_p ops and their m / v producers.
+// t = broadcast_to(s) of an f32 scalar s (one element).
+bool Runtime::scalar_bcast(int t) const {
+  const int op = T_[t].src;
+  if (op < 0 || kinds_[op] != "broadcast_to") return false;
+  const int s = fld(op, "a");
+  return T_[s].numel == 1 && T_[s].dt == F32;
+}
+
+// Every op of `ops` has its readers inside `ops` or the fused optimizer, and its output is
+// no graph output, capture or writeback source (except the sources in `wb_ok`, which the
+// fused update stores in place).
+bool Runtime::opt_closed(const std::set<int>& ops, const std::set<int>& wb_ok) const {
+  const tgj::Value* wbs = doc_.get("writebacks");
+  for (int o : ops) {
+    const int out = O(o).at("out").i32();
+    for (int c : consumers_[out])
+      if (!ops.count(c) && !adam_ops_.count(c)) return false;
+    for (int x : outputs_) if (x == out) return false;
+    for (auto& c : captures_) if (c.second == out) return false;
+    if (wbs)
+      for (const auto& w : wbs->items)
+        if (w.at("source").i32() == out && !wb_ok.count(out)) return false;
+  }
+  return true;
+}
+
+// The update chain sgd.ts:155-170 emits for one parameter, from its new value back to the
+// gradient: p' = sub(p, mul(broadcast_to(lr), u)); u = e, v' or add(e, mul_scalar(v', mu))
+// (Nesterov); v' = add(mul_scalar(v, mu), e); e = g or add(g, mul_scalar(p, wd)).
+bool Runtime::match_sgd(int pnew, const std::string& name, const std::map<std::string, int>& state_wb, OptParam& q,
+                        std::set<int>& ops, std::set<int>& wb) const {
+  auto src = [&](int t) { return t >= 0 && t < (int)T_.size() ? T_[t].src : -1; };
+  auto is = [&](int op, const char* k) { return op >= 0 && kinds_[op] == k; };
+  // x = mul_scalar(of, k) in either operand of a binary op: (other operand, mul_scalar op)
+  auto scaled = [&](int bop, int of, int& other, int& ms) {
+    for (int side = 0; side < 2; ++side) {
+      const int x = fld(bop, side ? "a" : "b"), y = fld(bop, side ? "b" : "a");
+      if (is(src(x), "mul_scalar") && fld(src(x), "a") == of) { other = y; ms = src(x); return true; }
+    }
+    return false;
+  };
+  auto ip = param_root.find(name);
+  if (ip == param_root.end()) return false;
+  const int p = ip->second;
+  const int s = src(pnew);
+  if (!is(s, "sub") || fld(s, "a") != p) return false;
+  const int mo = src(fld(s, "b"));
+  if (!is(mo, "mul")) return false;
+  int bc = fld(mo, "a"), u = fld(mo, "b");
+  if (!scalar_bcast(bc)) std::swap(bc, u);
+  if (!scalar_bcast(bc)) return false;
+  const int lr = fld(src(bc), "a");
+  const tgj::Value* ln = opt_cfg_ ? opt_cfg_->get("lrInputName") : nullptr;
+  if (!ln || ln->null() || !input_tid_.count(ln->str()) || input_tid_.at(ln->str()) != lr) return false;
+  q = OptParam{};
+  q.p = p;
+  q.lr = lr;
+  ops.insert({s, mo, src(bc)});
+  wb.insert(pnew);
+  int e = u;
+  auto iv = state_wb.find("sgd_v_" + name);
+  if (iv != state_wb.end()) {
+    const int vn = iv->second;
+    double mu2 = -1;
+    if (u != vn) {
+      const int na = src(u);
+      int ms = -1;
+      if (!is(na, "add") || !scaled(na, vn, e, ms)) return false;
+      mu2 = O(ms).at("scalar").num();
+      q.flags |= 1;
+      ops.insert({na, ms});
+    }
+    const int va = src(vn);
+    auto is_ = state_tid_.find("sgd_v_" + name);
+    if (!is(va, "add") || is_ == state_tid_.end()) return false;
+    int e2 = -1, ms = -1;
+    if (!scaled(va, is_->second, e2, ms)) return false;
+    q.mom = O(ms).at("scalar").num();
+    if (q.flags & 1) {
+      if (e2 != e || mu2 != q.mom) return false;
+    } else {
+      e = e2;
+    }
+    q.m = is_->second;
+    q.flags |= 4;
+    ops.insert({va, ms});
+    wb.insert(vn);
+  }
+  const int ea = src(e);
+  int g = e, ms = -1;
+  if (is(ea, "add") && scaled(ea, p, g, ms)) {
+    q.shrink = O(ms).at("scalar").num();
+    q.flags |= 2;
+    ops.insert({ea, ms});
+  } else {
+    g = e;
+  }
+  if (T_[g].numel != T_[p].numel || T_[g].dt != F32) return false;
+  q.final_g = q.g = g;
+  return true;
+}
+
+void Runtime::match_optimizer() {
+  opt_params_.clear();
+  adam_ops_.clear();
+  opt_sgd_ = false;
+  std::set<int> fused_wb;
   std::vector<int> adam_p_ops;
   for (size_t i = 0; i < ops_.size(); ++i) if (kinds_[i] == "adam_update_p") adam_p_ops.push_back((int)i);
-  std::set<int> adam_ops;
-  std::set<int> fused_wb_sources;
   for (int pi : adam_p_ops) {
-    int mNew = fld(pi, "mNew"), vNew = fld(pi, "vNew"), p = fld(pi, "p");
-    int mo = T_[mNew].src, vo = T_[vNew].src;
+    const int mNew = fld(pi, "mNew"), vNew = fld(pi, "vNew"), p = fld(pi, "p");
+    const int mo = T_[mNew].src, vo = T_[vNew].src;
     if (kinds_[mo] != "adam_update_m" || kinds_[vo] != "adam_update_v" || kinds_[T_[p].src] != "param_input" ||
         kinds_[T_[fld(mo, "m")].src] != "state_input" || kinds_[T_[fld(vo, "v")].src] != "state_input")
       throw Error(TG_INVALID_ARGUMENT, "IR: adam_update_p is not fed by adam_update_m/v of state inputs");
-    adam_ops.insert(pi); adam_ops.insert(mo); adam_ops.insert(vo);
-    fused_wb_sources.insert(ops_[pi]->at("out").i32());
-    fused_wb_sources.insert(mNew);
-    fused_wb_sources.insert(vNew);
+    if (fld(mo, "g") != fld(vo, "g"))
+      throw Error(TG_INVALID_ARGUMENT, "IR: adam_update_m and adam_update_v read different gradients");
+    OptParam q;
+    q.p = p;
+    q.m = fld(mo, "m");
+    q.v = fld(vo, "v");
+    q.final_g = q.g = fld(mo, "g");
+    q.lr = fld(pi, "lrt");
+    const tgj::Value& ds = O(pi).at("decayShrinkTensor");
+    q.shrink_t = ds.null() ? -1 : ds.i32();
+    q.shrink = ds.null() ? O(pi).at("decayShrink").num() : 1.0;
+    const double b1 = O(mo).at("beta1").num(), b2 = O(vo).at("beta2").num();
+    opt_hyper_ = {b1, 1 - b1, b2, 1 - b2, O(pi).at("eps").num()};
+    if (!opt_params_.empty() && opt_params_.front().lr != q.lr)
+      throw Error(TG_INVALID_ARGUMENT, "IR: adam_update_p ops read different lrt tensors");
+    opt_params_.push_back(q);
+    adam_ops_.insert({pi, mo, vo});
+    fused_wb.insert({O(pi).at("out").i32(), mNew, vNew});
   }
-  if (const tgj::Value* wb = doc_.get("writebacks")) {
-    for (const auto& w : wb->items) {
-      int src = w.at("source").i32();
-      if (fused_wb_sources.count(src)) continue;
-      copy_writebacks_.emplace_back(src, w.at("destName").str());
+  const tgj::Value* wbs = doc_.get("writebacks");
+  if (adam_p_ops.empty() && opt_kind_ == "sgd" && wbs && use_fused_transforms_) {
+    // every parameter's update must be the SGD chain; otherwise all of it runs op by op
+    std::map<std::string, int> state_wb;
+    for (const auto& w : wbs->items)
+      if (w.at("destKind").str() == "state") state_wb[w.at("destName").str()] = w.at("source").i32();
+    std::vector<OptParam> qs;
+    std::set<int> ops, wb;
+    bool ok = true;
+    for (const auto& w : wbs->items) {
+      if (w.at("destKind").str() != "param") continue;
+      OptParam q;
+      if (!match_sgd(w.at("source").i32(), w.at("destName").str(), state_wb, q, ops, wb) ||
+          (!qs.empty() && qs.front().lr != q.lr)) {
+        ok = false;
+        break;
+      }
+      qs.push_back(q);
+    }
+    if (ok && !qs.empty() && opt_closed(ops, wb)) {
+      opt_params_ = qs;
+      adam_ops_ = ops;
+      fused_wb = wb;
+      opt_sgd_ = true;
     }
   }
+  if (wbs)
+    for (const auto& w : wbs->items) {
+      const int src = w.at("source").i32();
+      if (fused_wb.count(src)) continue;
+      copy_writebacks_.emplace_back(src, w.at("destName").str());
+    }
+  if (!opt_params_.empty() && use_fused_transforms_) match_grad_transforms();
+}
 
-  adam_ops_ = adam_ops;
+// normalizeGrads (grad.ts:148-172) and clipGradNorm (grad.ts:110-130) in front of the
+// fused update: per parameter, g_final = mul(div(g, broadcast(norm)), broadcast(scale))
+// with either layer optional. Their scalars must be computable from per-parameter sums of
+// squares (sum_last(reshape(mul(y, y)))) of the gradients or the normalised gradients, and
+// constants, by rank-0 ops; and nothing else may read any of the absorbed values.
+// Otherwise the transforms run op by op and the update reads their result.
+void Runtime::match_grad_transforms() {
+  auto src = [&](int t) { return t >= 0 && t < (int)T_.size() ? T_[t].src : -1; };
+  auto is = [&](int op, const char* k) { return op >= 0 && kinds_[op] == k; };
+  std::set<int> ops;
+  bool any = false;
+  for (OptParam& q : opt_params_) {
+    int t = q.final_g;
+    const int mo = src(t);
+    if (is(mo, "mul")) {
+      int a = fld(mo, "a"), b = fld(mo, "b");
+      if (!scalar_bcast(b)) std::swap(a, b);
+      if (scalar_bcast(b) && T_[a].numel == T_[t].numel && T_[a].dt == F32) {
+        q.gmul = fld(src(b), "a");
+        ops.insert({mo, src(b)});
+        t = a;
+      }
+    }
+    const int dv = src(t);
+    if (is(dv, "div") && scalar_bcast(fld(dv, "b")) && T_[fld(dv, "a")].numel == T_[t].numel &&
+        T_[fld(dv, "a")].dt == F32) {
+      q.gdiv = fld(src(fld(dv, "b")), "a");
+      q.div_out = t;
+      ops.insert({dv, src(fld(dv, "b"))});
+      t = fld(dv, "a");
+    }
+    q.g = t;
+    any = any || q.gmul >= 0 || q.gdiv >= 0;
+  }
+  auto reset = [&]() {
+    for (OptParam& q : opt_params_) { q.g = q.final_g; q.gdiv = q.gmul = q.div_out = -1; }
+    norm_sums_.clear();
+    norm_sum_val_.clear();
+    norm_val_.clear();
+    norm_prog_[0].clear();
+    norm_prog_[1].clear();
+    norm_nvals_ = norm_launches_ = 0;
+  };
+  if (!any) { reset(); return; }
+  std::map<int, int> base_of, norm_of;   // gradient tensor -> param index; normalised tensor -> param index
+  for (size_t j = 0; j < opt_params_.size(); ++j) {
+    base_of[opt_params_[j].g] = (int)j;
+    if (opt_params_[j].div_out >= 0) norm_of[opt_params_[j].div_out] = (int)j;
+  }
+  std::map<int, int> launch_of;   // scalar tensor -> launch index
+  bool fail = false;
+  std::function<int(int)> visit = [&](int t) -> int {
+    auto it = launch_of.find(t);
+    if (it != launch_of.end()) return it->second;
+    const int op = src(t);
+    if (fail || op < 0 || T_[t].numel != 1 || T_[t].dt != F32) { fail = true; return 0; }
+    const std::string& k = kinds_[op];
+    tgk::ScalarInstr in{tgk::SI_CONST, -1, -1, -1, 0.0};
+    int L = 0;
+    if (k == "const_scalar") {
+      in.k = O(op).at("value").num();
+    } else if (k == "sum_last") {
+      ops.insert(op);
+      int y = fld(op, "a");
+      while (is(src(y), "reshape")) { ops.insert(src(y)); y = fld(src(y), "a"); }
+      const int mop = src(y);
+      if (!is(mop, "mul") || fld(mop, "a") != fld(mop, "b")) { fail = true; return 0; }
+      ops.insert(mop);
+      const int x = fld(mop, "a");
+      NormSum ns{-1, -1, 0};
+      if (base_of.count(x)) {
+        ns.g = x;
+      } else if (norm_of.count(x)) {
+        const OptParam& q = opt_params_[norm_of[x]];
+        if (visit(q.gdiv) != 0) { fail = true; return 0; }
+        ns = {q.g, q.gdiv, 1};
+      } else {
+        fail = true;
+        return 0;
+      }
+      if (T_[fld(op, "a")].numel != T_[x].numel || T_[x].numel <= 0) { fail = true; return 0; }
+      norm_sums_.push_back(ns);
+      norm_sum_val_.push_back(norm_nvals_);
+      norm_val_[t] = norm_nvals_++;
+      return launch_of[t] = ns.launch;
+    } else if (k == "add" || k == "sub" || k == "mul" || k == "div" || k == "min" || k == "max") {
+      const int la = visit(fld(op, "a")), lb = visit(fld(op, "b"));
+      if (fail) return 0;
+      in.op = k == "add" ? tgk::SI_ADD : k == "sub" ? tgk::SI_SUB : k == "mul" ? tgk::SI_MUL
+             : k == "div" ? tgk::SI_DIV : k == "min" ? tgk::SI_MIN : tgk::SI_MAX;
+      in.a = norm_val_.at(fld(op, "a"));
+      in.b = norm_val_.at(fld(op, "b"));
+      L = std::max(la, lb);
+    } else if (k == "add_scalar" || k == "mul_scalar" || k == "sqrt") {
+      L = visit(fld(op, "a"));
+      if (fail) return 0;
+      in.op = k == "add_scalar" ? tgk::SI_ADDK : k == "mul_scalar" ? tgk::SI_MULK : tgk::SI_SQRT;
+      in.a = norm_val_.at(fld(op, "a"));
+      if (k != "sqrt") in.k = O(op).at("scalar").num();
+    } else {
+      fail = true;
+      return 0;
+    }
+    ops.insert(op);
+    in.out = norm_val_[t] = norm_nvals_++;
+    norm_prog_[L].push_back(in);
+    return launch_of[t] = L;
+  };
+  for (const OptParam& q : opt_params_)
+    if (q.gdiv >= 0 && visit(q.gdiv) != 0) fail = true;
+  for (const OptParam& q : opt_params_)
+    if (q.gmul >= 0) visit(q.gmul);
+  // A constant another op also reads stays in the graph; the program has its own copy.
+  for (auto it = ops.begin(); it != ops.end();) {
+    bool outside = false;
+    if (kinds_[*it] == "const_scalar")
+      for (int c : consumers_[O(*it).at("out").i32()]) if (!ops.count(c) && !adam_ops_.count(c)) outside = true;
+    it = outside ? ops.erase(it) : std::next(it);
+  }
+  norm_launches_ = 1;
+  for (const NormSum& s : norm_sums_) norm_launches_ = std::max(norm_launches_, s.launch + 1);
+  std::vector<int64_t> elems(norm_launches_, 0);
+  for (const NormSum& s : norm_sums_) elems[s.launch] += T_[s.g].numel;
+  for (int64_t e : elems) if (e <= 0) fail = true;
+  for (const OptParam& q : opt_params_)
+    if (!view_[q.g].contiguous() || T_[q.g].numel != T_[q.p].numel || T_[root(q.g)].numel < T_[q.g].numel)
+      fail = true;
+  if (fail || norm_nvals_ > tgk::kNormMaxVals || !opt_closed(ops, {})) { reset(); return; }
+  adam_ops_.insert(ops.begin(), ops.end());
+}
+
+// A device copy of a launch table, made once per key: a node bound again (the
+// scratch-only launch list) gets the same copy, so rebinding allocates nothing.
+const void* Runtime::dev_table(const std::string& key, const void* data, size_t bytes) {
+  auto it = table_cache_.find(key);
+  if (it != table_cache_.end()) {
+    if (it->second.second != bytes) throw Error(TG_INTERNAL, "launch table " + key + " changed size");
+    return it->second.first;
+  }
+  void* dev = nullptr;
+  hip_check(hipMalloc(&dev, std::max<size_t>(bytes, 16)), "hipMalloc(table)");
+  if (bytes) hip_check(hipMemcpy(dev, data, bytes, hipMemcpyHostToDevice), "hipMemcpy(table)");
+  dev_tables_.push_back(dev);
+  table_cache_[key] = {dev, bytes};
+  return dev;
+}
+
+// The fused optimizer's launches, last in the step: the grad_norms launches (value array
+// at the start of the workspace, chunk partials after it), then the update.
+void Runtime::emit_optimizer() {
+  if (opt_params_.empty()) return;
+  const size_t vals_bytes = ((size_t)norm_nvals_ * 4 + 255) & ~(size_t)255;
+  const int last_op = *adam_ops_.rbegin();
+  const int nv = norm_nvals_;
+  for (int L = 0; L < norm_launches_; ++L) {
+    Node n;
+    n.kind = "grad_norm";
+    n.op = last_op;
+    std::vector<tgk::SqChunk> chunks;
+    std::vector<std::pair<int, int64_t>> at;   // chunk -> (gradient tensor, element offset)
+    std::vector<int> first, sval;
+    double elems = 0;
+    for (size_t s = 0; s < norm_sums_.size(); ++s) {
+      const NormSum& ns = norm_sums_[s];
+      if (ns.launch != L) continue;
+      const int slot = (int)first.size();
+      first.push_back((int)chunks.size());
+      sval.push_back(norm_sum_val_[s]);
+      const int64_t N = T_[ns.g].numel;
+      const int pre = ns.pre_t >= 0 ? norm_val_.at(ns.pre_t) : -1;
+      for (int64_t o = 0; o < N; o += tgk::kNormChunk) {
+        chunks.push_back({nullptr, std::min(tgk::kNormChunk, N - o), pre, slot});
+        at.emplace_back(ns.g, o);
+      }
+      n.reads.push_back(root(ns.g));
+      elems += (double)N;
+    }
+    first.push_back((int)chunks.size());
+    if (chunks.size() > 0x7fffffffu) throw Error(TG_INVALID_ARGUMENT, "grad_norms: too many gradient chunks");
+    n.bytes = 4.0 * elems;
+    n.shape = std::to_string(sval.size()) + " sums of squares, " + std::to_string((long long)elems) + " elements";
+    n.detail = "mul,sum_last";
+    for (const tgk::ScalarInstr& in : norm_prog_[L]) {
+      static const char* nm[] = {"const_scalar", "add", "sub", "mul", "div", "min", "max", "add_scalar", "mul_scalar",
+                                 "sqrt"};
+      n.detail += std::string(",") + nm[in.op];
+    }
+    n.ws = true;
+    const int64_t cb = take_counters((int64_t)sval.size() + 1);
+    workspace_bytes_ = std::max(workspace_bytes_, vals_bytes + chunks.size() * sizeof(double));
+    const std::vector<tgk::ScalarInstr> prog = norm_prog_[L];
+    const std::string key = "norm" + std::to_string(L);
+    n.bind = [=]() -> std::function<void(hipStream_t)> {
+      std::vector<tgk::SqChunk> ch = chunks;
+      for (size_t c = 0; c < ch.size(); ++c) ch[c].g = (const float*)dptr(at[c].first) + at[c].second;
+      if (plan_only_) return [](hipStream_t) {};
+      tgk::NormLaunch a{};
+      a.chunks = (const tgk::SqChunk*)dev_table(key + "c", ch.data(), ch.size() * sizeof(tgk::SqChunk));
+      a.nchunks = (int64_t)ch.size();
+      a.slot_first = (const int*)dev_table(key + "f", first.data(), first.size() * sizeof(int));
+      a.slot_val = (const int*)dev_table(key + "v", sval.data(), sval.size() * sizeof(int));
+      a.nslots = (int)sval.size();
+      a.prog = prog.empty() ? nullptr
+                            : (const tgk::ScalarInstr*)dev_table(key + "p", prog.data(),
+                                                                 prog.size() * sizeof(tgk::ScalarInstr));
+      a.nprog = (int)prog.size();
+      a.vals = cur_ws_;
+      a.nvals = nv;
+      a.part = reinterpret_cast<double*>(reinterpret_cast<char*>(cur_ws_) + vals_bytes);
+      a.counters = cur_counters_ + cb;
+      return [a](hipStream_t st) { tgk::grad_norms(a, st); };
+    };
+    add_node(std::move(n));
+  }
+
+  Node n;
+  n.kind = opt_sgd_ ? "sgd_multi" : "adam_multi";
+  n.op = last_op;
+  double elems = 0;
+  bool xf = false;
+  std::vector<tgk::AdamChunk> chunks;
+  std::vector<std::pair<size_t, int64_t>> at;   // chunk -> (param index, element offset)
+  for (size_t j = 0; j < opt_params_.size(); ++j) {
+    const OptParam& q = opt_params_[j];
+    n.reads.push_back(root(q.g));
+    n.reads.push_back(root(q.p));
+    n.writes.push_back(root(q.p));
+    if (q.m >= 0) { n.reads.push_back(root(q.m)); n.writes.push_back(root(q.m)); }
+    if (q.v >= 0) { n.reads.push_back(root(q.v)); n.writes.push_back(root(q.v)); }
+    n.reads.push_back(root(q.lr));
+    if (q.shrink_t >= 0) n.reads.push_back(root(q.shrink_t));
+    const int64_t N = T_[q.p].numel;
+    if (T_[q.g].numel != N || (q.m >= 0 && T_[q.m].numel != N) || (q.v >= 0 && T_[q.v].numel != N) ||
+        T_[root(q.g)].numel < N)
+      throw Error(TG_INVALID_ARGUMENT, "optimizer: p / state / gradient size mismatch");
+    if (!view_[q.g].contiguous()) throw Error(TG_INTERNAL, "optimizer: gradient is not contiguous");
+    const int gd = q.gdiv >= 0 ? norm_val_.at(q.gdiv) : -1, gm = q.gmul >= 0 ? norm_val_.at(q.gmul) : -1;
+    xf = xf || gd >= 0 || gm >= 0;
+    for (int64_t o = 0; o < N; o += tgk::kAdamChunk) {
+      tgk::AdamChunk c{};
+      c.shrink = q.shrink;
+      c.mom = q.mom;
+      c.n = std::min(tgk::kAdamChunk, N - o);
+      c.gdiv = gd;
+      c.gmul = gm;
+      c.flags = q.flags;
+      chunks.push_back(c);
+      at.emplace_back(j, o);
+    }
+    elems += (double)N;
+    if (opt_sgd_) n.bytes += (q.flags & 4 ? 20.0 : 12.0) * (double)N;
+  }
+  if (!opt_sgd_) n.bytes = 28.0 * elems;
+  n.shape = std::to_string(opt_params_.size()) + " tensors, " + std::to_string((long long)elems) + " params";
+  if (xf) n.detail = "div/mul,update";
+  n.ws = xf;
+  const tgk::AdamHyper h = opt_hyper_;
+  const bool sgd = opt_sgd_;
+  n.bind = [=]() -> std::function<void(hipStream_t)> {
+    std::vector<tgk::AdamChunk> ch = chunks;
+    for (size_t c = 0; c < ch.size(); ++c) {
+      const OptParam& q = opt_params_[at[c].first];
+      const int64_t o = at[c].second;
+      ch[c].p = (float*)dptr(q.p) + o;
+      ch[c].m = q.m >= 0 ? (float*)dptr(q.m) + o : nullptr;
+      ch[c].v = q.v >= 0 ? (float*)dptr(q.v) + o : nullptr;
+      ch[c].g = (const float*)dptr(q.g) + o;
+      ch[c].shrink_ptr = q.shrink_t >= 0 ? (const float*)dptr(q.shrink_t) : nullptr;
+    }
+    if (plan_only_) return [](hipStream_t) {};
+    const tgk::AdamChunk* dc = (const tgk::AdamChunk*)dev_table("opt", ch.data(), ch.size() * sizeof(tgk::AdamChunk));
+    const int64_t nch = (int64_t)ch.size();
+    const float* lr = (const float*)dptr(opt_params_.front().lr);
+    const float* vals = xf ? cur_ws_ : nullptr;
+    if (sgd) return [=](hipStream_t st) { tgk::sgd_multi(dc, nch, lr, vals, st); };
+    return [=](hipStream_t st) { tgk::adam_multi(dc, nch, lr, h, vals, st); };
+  };
+  add_node(std::move(n));
+}
+
+void Runtime::lower() {
+  if (const char* g = std::getenv("TG_OPT_FUSED")) use_fused_transforms_ = std::string(g) != "0";
+  match_optimizer();
   gemm_done_.assign(ops_.size(), 0);
   plan_gemm_groups();
   match_attention();
@@ -973,7 +1468,7 @@ void Runtime::lower() {
   group_done_.assign(groups_.size(), 0);
   for (size_t i = 0; i < ops_.size(); ++i) {
     if (is_leaf((int)i) || virtual_[i]) continue;
-    if (adam_ops.count((int)i)) continue;
+    if (adam_ops_.count((int)i)) continue;
     if (attn_of_[i] >= 0) {
       const int m = attn_of_[i];
       if (m < (int)attn_.size()) {
@@ -1046,12 +1541,10 @@ void Runtime::lower() {
     changed = false;
     std::set<int> read;
     for (auto& n : nodes_) read.insert(n.reads.begin(), n.reads.end());
-    for (int ai : adam_p_ops) {
-      int mo = T_[fld(ai, "mNew")].src;
-      read.insert(root(fld(mo, "g")));
-      read.insert(root(fld(ai, "lrt")));
-      const tgj::Value& ds = O(ai).at("decayShrinkTensor");
-      if (!ds.null()) read.insert(root(ds.i32()));
+    for (const OptParam& q : opt_params_) {
+      read.insert(root(q.g));
+      read.insert(root(q.lr));
+      if (q.shrink_t >= 0) read.insert(root(q.shrink_t));
     }
     for (size_t q = 0; q < nodes_.size(); ++q) {
       bool needed = false;
@@ -1060,66 +1553,7 @@ void Runtime::lower() {
     }
   }
 
-  if (!adam_p_ops.empty()) {
-    Node n;
-    n.kind = "adam_multi";
-    n.op = adam_p_ops.back();
-    double elems = 0;
-    for (int pi : adam_p_ops) {
-      int mo = T_[fld(pi, "mNew")].src, vo = T_[fld(pi, "vNew")].src;
-      n.reads.push_back(root(fld(mo, "g")));
-      n.reads.push_back(root(fld(pi, "p")));
-      n.reads.push_back(root(fld(mo, "m")));
-      n.reads.push_back(root(fld(vo, "v")));
-      // updated in place
-      n.writes.push_back(root(fld(pi, "p")));
-      n.writes.push_back(root(fld(mo, "m")));
-      n.writes.push_back(root(fld(vo, "v")));
-      n.reads.push_back(root(fld(pi, "lrt")));
-      const tgj::Value& ds = O(pi).at("decayShrinkTensor");
-      if (!ds.null()) n.reads.push_back(root(ds.i32()));
-      elems += (double)T_[fld(pi, "p")].numel;
-    }
-    n.bytes = 28.0 * elems;
-    n.shape = std::to_string(adam_p_ops.size()) + " tensors, " + std::to_string((long long)elems) + " params";
-    std::vector<int> pops = adam_p_ops;
-    n.bind = [this, pops]() -> std::function<void(hipStream_t)> {
-      std::vector<tgk::AdamChunk> chunks;
-      double b1 = 0.9, b2 = 0.999, eps = 1e-8;
-      const float* lrt = nullptr;
-      for (size_t q = 0; q < pops.size(); ++q) {
-        int pi = pops[q];
-        int mo = T_[fld(pi, "mNew")].src, vo = T_[fld(pi, "vNew")].src;
-        b1 = O(mo).at("beta1").num();
-        b2 = O(vo).at("beta2").num();
-        eps = O(pi).at("eps").num();
-        lrt = (const float*)dptr(fld(pi, "lrt"));
-        const tgj::Value& ds = O(pi).at("decayShrinkTensor");
-        int g = fld(mo, "g");
-        if (!view_[g].contiguous()) throw Error(TG_INTERNAL, "adam: gradient is not contiguous");
-        const int64_t n = T_[fld(pi, "p")].numel;
-        if (T_[fld(mo, "m")].numel != n || T_[fld(vo, "v")].numel != n || T_[g].numel != n || T_[root(g)].numel < n)
-          throw Error(TG_INVALID_ARGUMENT, "adam: p / m / v / g size mismatch");
-        float* p = (float*)dptr(fld(pi, "p"));
-        float* m = (float*)dptr(fld(mo, "m"));
-        float* v = (float*)dptr(fld(vo, "v"));
-        const float* gp = (const float*)dptr(g);
-        const double shrink = ds.null() ? O(pi).at("decayShrink").num() : 1.0;
-        const float* shrink_ptr = ds.null() ? nullptr : (const float*)dptr(ds.i32());
-        for (int64_t s = 0; s < n; s += tgk::kAdamChunk)
-          chunks.push_back({p + s, m + s, v + s, gp + s, shrink_ptr, shrink, std::min(tgk::kAdamChunk, n - s)});
-      }
-      if (plan_only_) return [](hipStream_t) {};
-      hip_check(hipMalloc(&adam_chunks_, chunks.size() * sizeof(tgk::AdamChunk)), "hipMalloc");
-      hip_check(hipMemcpy(adam_chunks_, chunks.data(), chunks.size() * sizeof(tgk::AdamChunk), hipMemcpyHostToDevice),
-                "hipMemcpy");
-      tgk::AdamHyper h{b1, 1 - b1, b2, 1 - b2, eps};
-      const int64_t nch = (int64_t)chunks.size();
-      const tgk::AdamChunk* dc = adam_chunks_;
-      return [=](hipStream_t st) { tgk::adam_multi(dc, nch, lrt, h, st); };
-    };
-    add_node(std::move(n));
-  }
+  emit_optimizer();
 }
 
 static std::string shape_str(const Dims& d) {
@@ -1403,7 +1837,7 @@ void Runtime::form_groups() {
   for (size_t i = 0; i < ops_.size(); ++i) {
     const std::string& k = kinds_[i];
     if (virtual_[i] || is_leaf((int)i) || attn_of_[i] >= 0 || mul_absorbed_[i] || sum_absorbed_[i] ||
-        colsum_.count((int)i))
+        colsum_.count((int)i) || adam_ops_.count((int)i))
       continue;
     const bool red = is_row_reduce((int)i);
     if (!red && !pw.count(k)) continue;
@@ -3342,7 +3776,7 @@ void Runtime::split_init_nodes() {
   for (auto& w : copy_writebacks_) pinned.insert(root(w.first));
   std::vector<Node> step;
   for (auto& n : nodes_) {
-    bool inv = n.kind != "adam_multi" && !n.writes.empty();
+    bool inv = n.kind != "adam_multi" && n.kind != "sgd_multi" && n.kind != "grad_norm" && !n.writes.empty();
     for (int r : n.reads) if (!init_roots_.count(r)) inv = false;
     for (int w : n.writes) if (pinned.count(w)) inv = false;
     if (inv) {
@@ -3861,6 +4295,46 @@ void Runtime::profile_nodes(int iters, double* ms, int64_t nout) {
 // selects every node whose kind is NOT listed), in step order, `iters` times back to
 // back between two HIP events on the runtime's stream. Returns milliseconds per pass and
 // the number of nodes in a pass. The selected kernels read whatever the buffers hold.
+// Per-node kernel time of eager steps: every kernel a node launches is dispatched with
+// start / end events of its own (tgk::LaunchTimer), so the figure is the kernels' own
+// durations, summed per node (split-K reductions with their GEMM), without the gaps
+// between launches: the quantity a profiler's kernel trace reports.
+void Runtime::profile_kernels(int iters, double* ms, int64_t nout) {
+  if (nout != (int64_t)nodes_.size()) throw Error(TG_INVALID_ARGUMENT, "profile: output length must equal node count");
+  tgk::LaunchTimer tm;
+  tm.ev.resize(2 * (8 * nodes_.size() + 64));
+  for (auto& e : tm.ev) hip_check(hipEventCreate(&e), "hipEventCreate");
+  std::vector<double> acc(nodes_.size(), 0.0);
+  std::vector<size_t> first(nodes_.size() + 1);
+  try {
+    for (int it = 0; it < iters; ++it) {
+      tm.used = tm.missed = 0;
+      tgk::launch_timer() = &tm;
+      for (size_t i = 0; i < nodes_.size(); ++i) {
+        first[i] = tm.used;
+        nodes_[i].launch(stream_);
+      }
+      tgk::launch_timer() = nullptr;
+      first[nodes_.size()] = tm.used;
+      hip_check(hipStreamSynchronize(stream_), "hipStreamSynchronize");
+      if (tm.missed) throw Error(TG_INTERNAL, "profile: kernel event pool exhausted");
+      for (size_t i = 0; i < nodes_.size(); ++i)
+        for (size_t k = first[i]; k < first[i + 1]; ++k) {
+          float m = 0;
+          hip_check(hipEventElapsedTime(&m, tm.ev[2 * k], tm.ev[2 * k + 1]), "hipEventElapsedTime");
+          acc[i] += m;
+        }
+    }
+  } catch (...) {
+    tgk::launch_timer() = nullptr;
+    hipStreamSynchronize(stream_);
+    for (auto& e : tm.ev) hipEventDestroy(e);
+    throw;
+  }
+  for (auto& e : tm.ev) hipEventDestroy(e);
+  for (size_t i = 0; i < nodes_.size(); ++i) ms[i] = acc[i] / std::max(1, iters);
+}
+
 double Runtime::time_kinds(const std::string& kinds, int iters, int* launches) {
   bool negate = !kinds.empty() && kinds[0] == '-';
   std::set<std::string> want;
@@ -3903,13 +4377,8 @@ double Runtime::time_replays(int steps) {
   return ms;
 }
 
-const std::vector<std::string>& Runtime::state_names() {
-  if (state_list_.size() != state_tid_.size()) {
-    state_list_.clear();
-    for (auto& kv : state_tid_) state_list_.push_back(kv.first);
-  }
-  return state_list_;
-}
+// Filled once by analyse() and never changed: readable without the runtime's lock.
+const std::vector<std::string>& Runtime::state_names() const { return state_list_; }
 
 int64_t Runtime::state_numel(const std::string& name) const {
   auto it = state_tid_.find(name);
@@ -3982,8 +4451,14 @@ void Runtime::save_checkpoint(const std::string& path) {
   if (!ok) throw Error(TG_INVALID_ARGUMENT, "checkpoint: writing '" + path + "' failed");
 }
 
-void Runtime::load_checkpoint(const std::string& path) {
-  if (parent) throw Error(TG_INVALID_ARGUMENT, "checkpoint: a forward sibling shares its parent's params; load into the parent");
+// A checkpoint counter from __metadata__: decimal digits only, at most 18 of them.
+static long long parse_counter(const std::string& v, const char* what) {
+  if (v.empty() || v.size() > 18 || v.find_first_not_of("0123456789") != std::string::npos)
+    throw Error(TG_INVALID_ARGUMENT, std::string("checkpoint: ") + what + " '" + v + "' is not a non-negative integer");
+  return std::stoll(v);
+}
+
+static std::vector<uint8_t> read_file(const std::string& path) {
   FILE* f = fopen(path.c_str(), "rb");
   if (!f) throw Error(TG_INVALID_ARGUMENT, "checkpoint: cannot open '" + path + "'");
   std::vector<uint8_t> buf;
@@ -3991,54 +4466,87 @@ void Runtime::load_checkpoint(const std::string& path) {
   size_t got;
   while ((got = fread(chunk, 1, sizeof chunk, f)) > 0) buf.insert(buf.end(), chunk, chunk + got);
   fclose(f);
-  tgst::Index ix;
+  return buf;
+}
+
+// Everything a load would do, checked without touching the device: every parameter
+// present with its shape; optimizer state all or nothing; no other tensors (integer and
+// bool ones included); the counters and the LR schedule readable. Counters and the
+// schedule are taken from the file only when it carries the optimizer state: a
+// params-only file (e.g. converted pretrained weights) leaves all optimizer state alone.
+Runtime::CkptPlan Runtime::check_checkpoint(const std::vector<uint8_t>& buf) const {
+  if (parent) throw Error(TG_INVALID_ARGUMENT, "checkpoint: a forward sibling shares its parent's params; load into the parent");
+  CkptPlan cp;
   try {
-    ix = tgst::parse(buf.data(), buf.size(), true);
+    cp.ix = tgst::parse(buf.data(), buf.size(), true);
   } catch (std::exception& e) {
     throw Error(TG_INVALID_ARGUMENT, e.what());
   }
-  // Validate everything before writing anything.
   auto check = [&](const tgst::Entry& e, int t) {
     if (e.shape != T_[t].shape || e.dtype != (T_[t].dt == F32 ? "F32" : "I32"))
       throw Error(TG_INVALID_ARGUMENT, "checkpoint: tensor '" + e.name + "' does not match the graph's shape or dtype");
   };
-  std::vector<std::pair<const tgst::Entry*, int>> writes;
-  size_t n_state = 0;
-  for (const tgst::Entry& e : ix.tensors) {
+  for (size_t i = 0; i < cp.ix.tensors.size(); ++i) {
+    const tgst::Entry& e = cp.ix.tensors[i];
     auto p = param_root.find(e.name);
     auto s = state_tid_.find(e.name);
-    if (p != param_root.end()) { check(e, p->second); writes.emplace_back(&e, p->second); }
-    else if (s != state_tid_.end()) { check(e, s->second); writes.emplace_back(&e, s->second); ++n_state; }
+    if (p != param_root.end()) { check(e, p->second); cp.writes.emplace_back(i, p->second); }
+    else if (s != state_tid_.end()) { check(e, s->second); cp.writes.emplace_back(i, s->second); ++cp.n_state; }
     else throw Error(TG_INVALID_ARGUMENT, "checkpoint: unknown tensor '" + e.name + "'");
   }
+  for (const tgst::Entry& e : cp.ix.skipped)
+    throw Error(TG_INVALID_ARGUMENT, "checkpoint: unknown tensor '" + e.name + "' (dtype " + e.dtype + ")");
   for (auto& nm : param_names)
-    if (!ix.find(nm)) throw Error(TG_INVALID_ARGUMENT, "checkpoint: missing param '" + nm + "'");
-  if (n_state && n_state != state_tid_.size())
-    throw Error(TG_INVALID_ARGUMENT, "checkpoint: holds part of the optimizer state (" + std::to_string(n_state) + " of " +
-                                         std::to_string(state_tid_.size()) + " tensors)");
-  long long t = t_, c = prng_counter_;
-  if (n_state) {
-    const std::string* k = ix.meta("tensorgrad.optimizer");
+    if (!cp.ix.find(nm)) throw Error(TG_INVALID_ARGUMENT, "checkpoint: missing param '" + nm + "'");
+  if (cp.n_state && cp.n_state != state_tid_.size())
+    throw Error(TG_INVALID_ARGUMENT, "checkpoint: holds part of the optimizer state (" + std::to_string(cp.n_state) +
+                                         " of " + std::to_string(state_tid_.size()) + " tensors)");
+  cp.t = t_;
+  cp.c = prng_counter_;
+  cp.lr = lr_;
+  if (cp.n_state) {
+    const std::string* k = cp.ix.meta("tensorgrad.optimizer");
     const std::string mine = opt_cfg_ ? opt_kind_ : std::string("none");
     if (k && *k != mine) throw Error(TG_INVALID_ARGUMENT, "checkpoint: optimizer '" + *k + "' does not match the graph's '" + mine + "'");
-    const std::string* ts = ix.meta("tensorgrad.step");
+    const std::string* ts = cp.ix.meta("tensorgrad.step");
     if (!ts) throw Error(TG_INVALID_ARGUMENT, "checkpoint: optimizer state without a step counter");
-    t = std::stoll(*ts);
+    cp.t = parse_counter(*ts, "tensorgrad.step");
+    if (const std::string* cs = cp.ix.meta("tensorgrad.prngCounter")) cp.c = parse_counter(*cs, "tensorgrad.prngCounter");
+    if (const std::string* ls = cp.ix.meta("tensorgrad.lr"))
+      if (opt_cfg_) {
+        try {
+          cp.lr = tgj::parse(ls->c_str());
+        } catch (std::exception& e) {
+          throw Error(TG_INVALID_ARGUMENT, std::string("checkpoint: lr: ") + e.what());
+        }
+      }
   }
-  if (const std::string* cs = ix.meta("tensorgrad.prngCounter")) c = std::stoll(*cs);
-  tgj::Value lr = lr_;
-  if (const std::string* ls = ix.meta("tensorgrad.lr"))
-    if (n_state && opt_cfg_) {
-      try { lr = tgj::parse(ls->c_str()); } catch (std::exception& e) { throw Error(TG_INVALID_ARGUMENT, std::string("checkpoint: lr: ") + e.what()); }
-    }
+  return cp;
+}
+
+std::string Runtime::check_checkpoint_file(const std::string& path) const {
+  const std::vector<uint8_t> buf = read_file(path);
+  const CkptPlan cp = check_checkpoint(buf);
+  std::ostringstream o;
+  o << "{\"params\":" << (cp.writes.size() - cp.n_state) << ",\"state\":" << cp.n_state
+    << ",\"restoresCounters\":" << (cp.n_state ? "true" : "false") << ",\"step\":" << cp.t
+    << ",\"prngCounter\":" << cp.c << "}";
+  return o.str();
+}
+
+void Runtime::load_checkpoint(const std::string& path) {
+  const std::vector<uint8_t> buf = read_file(path);
+  const CkptPlan cp = check_checkpoint(buf);   // nothing is written unless the whole file checks out
   hip_check(hipStreamSynchronize(stream_), "hipStreamSynchronize");
-  for (auto& w : writes)
-    if (w.first->end > w.first->begin)
-      hip_check(hipMemcpy(ptr_[w.second], buf.data() + ix.data_start + w.first->begin, (size_t)(w.first->end - w.first->begin),
+  for (auto& w : cp.writes) {
+    const tgst::Entry& e = cp.ix.tensors[w.first];
+    if (e.end > e.begin)
+      hip_check(hipMemcpy(ptr_[w.second], buf.data() + cp.ix.data_start + e.begin, (size_t)(e.end - e.begin),
                           hipMemcpyHostToDevice), "hipMemcpy(H2D checkpoint)");
-  t_ = t;
-  prng_counter_ = c;
-  lr_ = lr;
+  }
+  t_ = cp.t;
+  prng_counter_ = cp.c;
+  lr_ = cp.lr;
 }
 
 }  // namespace tg
@@ -4074,6 +4582,16 @@ tg_status guarded(F&& f) {
 bool live(tg_runtime* h) {
   std::lock_guard<std::mutex> g(g_registry_mu);
   return h && g_live.count(h);
+}
+
+// Names and sizes are fixed at creation. The getters take the registry lock, so a handle
+// destroyed before or during the call answers 0 / NULL / -1 instead of being read; a
+// returned name stays valid until the runtime is destroyed.
+template <class R, class F>
+R if_live(const tg_runtime* h, R dflt, F f) {
+  std::lock_guard<std::mutex> g(g_registry_mu);
+  if (!h || !g_live.count(const_cast<tg_runtime*>(h)) || !h->rt) return dflt;
+  return f(*h->rt);
 }
 }  // namespace
 
@@ -4146,14 +4664,18 @@ void tg_destroy(tg_runtime* h) {
   std::lock_guard<std::mutex> lk_((h)->mu);                               \
   if (!(h)->rt) { tg::g_error = "graph destroyed"; return TG_ABORTED; }
 
-int tg_param_count(const tg_runtime* h) { return h && h->rt ? (int)h->rt->param_names.size() : 0; }
+int tg_param_count(const tg_runtime* h) {
+  return if_live(h, 0, [](const tg::Runtime& r) { return (int)r.param_names.size(); });
+}
 const char* tg_param_name(const tg_runtime* h, int i) {
-  if (!h || !h->rt || i < 0 || i >= (int)h->rt->param_names.size()) return nullptr;
-  return h->rt->param_names[i].c_str();
+  return if_live(h, (const char*)nullptr, [i](const tg::Runtime& r) -> const char* {
+    return i < 0 || i >= (int)r.param_names.size() ? nullptr : r.param_names[i].c_str();
+  });
 }
 int64_t tg_param_numel(const tg_runtime* h, int i) {
-  if (!h || !h->rt || i < 0 || i >= (int)h->rt->param_names.size()) return -1;
-  return h->rt->param_numel(i);
+  return if_live(h, (int64_t)-1, [i](const tg::Runtime& r) -> int64_t {
+    return i < 0 || i >= (int)r.param_names.size() ? -1 : r.param_numel(i);
+  });
 }
 
 tg_status tg_upload_params(tg_runtime* h, int n, const char* const* names, const float* const* data, const int64_t* numel) {
@@ -4201,10 +4723,13 @@ tg_status tg_run(tg_runtime* h, int n, const char* const* names, const void* con
   return guarded([&] { h->rt->run(n, names, data, nbytes, out, out_bytes); });
 }
 
-int tg_capture_count(const tg_runtime* h) { return h && h->rt ? (int)h->rt->capture_names.size() : 0; }
+int tg_capture_count(const tg_runtime* h) {
+  return if_live(h, 0, [](const tg::Runtime& r) { return (int)r.capture_names.size(); });
+}
 const char* tg_capture_name(const tg_runtime* h, int i) {
-  if (!h || !h->rt || i < 0 || i >= (int)h->rt->capture_names.size()) return nullptr;
-  return h->rt->capture_names[i].c_str();
+  return if_live(h, (const char*)nullptr, [i](const tg::Runtime& r) -> const char* {
+    return i < 0 || i >= (int)r.capture_names.size() ? nullptr : r.capture_names[i].c_str();
+  });
 }
 
 tg_status tg_get_capture(tg_runtime* h, const char* name, void* out, int64_t nbytes) {
@@ -4222,14 +4747,18 @@ tg_status tg_set_lr(tg_runtime* h, const char* lr_json) {
   return guarded([&] { h->rt->set_lr(lr_json); });
 }
 
-int tg_state_count(tg_runtime* h) { return h && h->rt ? (int)h->rt->state_names().size() : 0; }
+int tg_state_count(tg_runtime* h) {
+  return if_live(h, 0, [](const tg::Runtime& r) { return (int)r.state_names().size(); });
+}
 const char* tg_state_name(tg_runtime* h, int i) {
-  if (!h || !h->rt || i < 0 || i >= (int)h->rt->state_names().size()) return nullptr;
-  return h->rt->state_names()[i].c_str();
+  return if_live(h, (const char*)nullptr, [i](const tg::Runtime& r) -> const char* {
+    return i < 0 || i >= (int)r.state_names().size() ? nullptr : r.state_names()[i].c_str();
+  });
 }
 int64_t tg_state_numel(tg_runtime* h, int i) {
-  if (!h || !h->rt || i < 0 || i >= (int)h->rt->state_names().size()) return -1;
-  return h->rt->state_numel(h->rt->state_names()[i]);
+  return if_live(h, (int64_t)-1, [i](const tg::Runtime& r) -> int64_t {
+    return i < 0 || i >= (int)r.state_names().size() ? -1 : r.state_numel(r.state_names()[i]);
+  });
 }
 
 tg_status tg_download_state(tg_runtime* h, int n, const char* const* names, float* const* data, const int64_t* numel,
@@ -4262,6 +4791,16 @@ tg_status tg_load_checkpoint(tg_runtime* h, const char* path) {
   if (!path) { tg::g_error = "null argument"; return TG_INVALID_ARGUMENT; }
   TG_ENTER(h);
   return guarded([&] { h->rt->load_checkpoint(path); });
+}
+
+tg_status tg_check_checkpoint(const char* ir_json, const char* path, char* out, int64_t out_len) {
+  if (!ir_json || !path || !out || out_len <= 0) { tg::g_error = "null argument"; return TG_INVALID_ARGUMENT; }
+  return guarded([&] {
+    tg::Runtime r(ir_json, nullptr, true);
+    const std::string s = r.check_checkpoint_file(path);
+    if ((int64_t)s.size() + 1 > out_len) throw tg::Error(TG_INVALID_ARGUMENT, "check_checkpoint: output buffer too small");
+    memcpy(out, s.c_str(), s.size() + 1);
+  });
 }
 
 tg_status tg_safetensors_index(const void* buf, int64_t len, char* out, int64_t out_len) {
@@ -4313,6 +4852,11 @@ tg_status tg_describe(tg_runtime* h, char* buf, int64_t buflen) {
 tg_status tg_profile_nodes(tg_runtime* h, int iters, double* ms_out, int64_t n_out) {
   TG_ENTER(h);
   return guarded([&] { h->rt->profile_nodes(iters, ms_out, n_out); });
+}
+
+tg_status tg_profile_kernels(tg_runtime* h, int iters, double* ms_out, int64_t n_out) {
+  TG_ENTER(h);
+  return guarded([&] { h->rt->profile_kernels(iters, ms_out, n_out); });
 }
 
 tg_status tg_time_replays(tg_runtime* h, int steps, double* total_ms) {

@@ -27,9 +27,11 @@ struct Entry {
   std::string name, dtype;
   std::vector<int64_t> shape;
   int64_t begin = 0, end = 0;   // byte offsets relative to the data blob
+  // Element count, or -1 when the product of the dimensions overflows int64.
   int64_t numel() const {
     int64_t n = 1;
-    for (int64_t d : shape) n *= d;
+    for (int64_t d : shape)
+      if (__builtin_mul_overflow(n, d, &n)) return -1;
     return n;
   }
 };
@@ -95,14 +97,18 @@ inline Index parse(const uint8_t* buf, uint64_t len, bool raw_i32_ok = false) {
         off->kind != tgj::Value::Array || off->items.size() != 2)
       throw std::runtime_error("loadSafetensors: tensor '" + name + "' entry is malformed");
     e.dtype = dt->str();
+    // JSON numbers arrive as doubles: only integers below 2^53 are exact, and only those
+    // are converted (a larger value cannot be a valid size or offset of a buffer here).
+    auto exact_count = [](const tgj::Value& x) {
+      return x.kind == tgj::Value::Number && x.number >= 0 && x.number < 9007199254740992.0 &&
+             x.number == (double)(int64_t)x.number;
+    };
     for (const auto& d : sh->items) {
-      if (d.kind != tgj::Value::Number || d.number < 0 || d.number != (double)(int64_t)d.number)
-        throw std::runtime_error("loadSafetensors: tensor '" + name + "' has a malformed shape");
+      if (!exact_count(d)) throw std::runtime_error("loadSafetensors: tensor '" + name + "' has a malformed shape");
       e.shape.push_back(d.i64());
     }
     for (const auto& o : off->items)
-      if (o.kind != tgj::Value::Number || o.number < 0 || o.number != (double)(int64_t)o.number)
-        throw std::runtime_error("loadSafetensors: tensor '" + name + "' has malformed data_offsets");
+      if (!exact_count(o)) throw std::runtime_error("loadSafetensors: tensor '" + name + "' has malformed data_offsets");
     e.begin = off->items[0].i64();
     e.end = off->items[1].i64();
     if (e.dtype != "F32" && !(raw_i32_ok && e.dtype == "I32")) {
@@ -114,7 +120,11 @@ inline Index parse(const uint8_t* buf, uint64_t len, bool raw_i32_ok = false) {
     if (e.begin > e.end || (uint64_t)header_end + (uint64_t)e.end > len)
       throw std::runtime_error("loadSafetensors: tensor '" + name + "' data_offsets [" + std::to_string(e.begin) + ", " +
                                std::to_string(e.end) + "] out of range");
-    if (e.end - e.begin != e.numel() * 4) {
+    const int64_t numel = e.numel();
+    int64_t bytes = -1;
+    if (numel < 0 || __builtin_mul_overflow(numel, (int64_t)4, &bytes))
+      throw std::runtime_error("loadSafetensors: tensor '" + name + "' has a shape whose element count overflows");
+    if (e.end - e.begin != bytes) {
       std::string s;
       for (size_t i = 0; i < e.shape.size(); ++i) s += (i ? ", " : "") + std::to_string(e.shape[i]);
       throw std::runtime_error("loadSafetensors: tensor '" + name + "' byte length " + std::to_string(e.end - e.begin) +

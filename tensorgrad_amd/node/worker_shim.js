@@ -79,10 +79,12 @@ function countOf(shape) { return shape.reduce((a, b) => a * b, 1) }
 class NativeWorkerProxy {
   constructor() {
     this.graphs = new Map()     // graphId -> slot
+    this.family = new Map()     // graphId -> id of its runtime family (the graph owning the params)
+    this.queues = new Map()     // family id -> tail of its request chain
     this.terminated = false
   }
 
-  _slotMeta(handle, wire) {
+  async _slotMeta(handle, wire) {
     const g = wire.graph
     const out = g.tensors[g.outputs[0]]
     const captureShapes = {}
@@ -113,13 +115,11 @@ class NativeWorkerProxy {
     }
   }
 
-  _captures(slot) {
-    const names = Object.keys(slot.captureShapes)
-    if (names.length === 0) return null
-    const out = {}
-    for (const n of names)
-      out[n] = native().getCapture(slot.handle, n, countOf(slot.captureShapes[n]), slot.captureDtypes[n] !== 'f32')
-    return out
+  // [[name, element count, isInt]] for the addon, which reads the captures back on its
+  // worker thread right after the step / run
+  _captureSpec(slot) {
+    return Object.keys(slot.captureShapes).map(n =>
+      [n, countOf(slot.captureShapes[n]), slot.captureDtypes[n] !== 'f32'])
   }
 
   _mustGet(graphId) {
@@ -128,20 +128,20 @@ class NativeWorkerProxy {
     return slot
   }
 
-  _handle(req) {
+  async _handle(req) {
     const p = req.payload
     const A = native()
     switch (req.kind) {
       case 'createRuntime': {
         const wire = toWire(p.ir, p.optimizer)
-        const h = A.create(JSON.stringify(wire))
+        const h = await A.create(JSON.stringify(wire))
         try {
-          if (Object.keys(p.initialParams || {}).length > 0) A.uploadParams(h, p.initialParams)
+          if (Object.keys(p.initialParams || {}).length > 0) await A.uploadParams(h, p.initialParams)
         } catch (e) {
-          A.destroy(h)
+          await A.destroy(h)
           throw e
         }
-        const slot = Object.assign(this._slotMeta(h, wire), { parentGraphId: null })
+        const slot = Object.assign(await this._slotMeta(h, wire), { parentGraphId: null })
         this.graphs.set(p.graphId, slot)
         return this._compileResult(slot)
       }
@@ -149,41 +149,41 @@ class NativeWorkerProxy {
         const parent = this.graphs.get(p.parentGraphId)
         if (!parent) throw new Error(`compileForward: parent graph ${p.parentGraphId} not found`)
         const wire = toWire(p.ir, null)
-        const h = A.createSibling(parent.handle, JSON.stringify(wire))
-        const slot = Object.assign(this._slotMeta(h, wire), { parentGraphId: p.parentGraphId })
+        const h = await A.createSibling(parent.handle, JSON.stringify(wire))
+        const slot = Object.assign(await this._slotMeta(h, wire), { parentGraphId: p.parentGraphId })
         this.graphs.set(p.graphId, slot)
         return this._compileResult(slot)
       }
       case 'step': {
         const slot = this.graphs.get(p.graphId)
         if (!slot) throw abortErr('step aborted: graph replaced mid-flight')
-        const loss = A.step(slot.handle, p.inputs)
-        return { loss, captures: this._captures(slot) }
+        const r = await A.step(slot.handle, p.inputs, this._captureSpec(slot))
+        return { loss: r.loss, captures: r.captures }
       }
       case 'run': {
         const slot = this.graphs.get(p.graphId)
         if (!slot) throw abortErr('run aborted: graph replaced mid-flight')
-        const output = A.run(slot.handle, p.inputs, countOf(slot.outputShape), slot.outputInt)
-        return { output, captures: this._captures(slot) }
+        const r = await A.run(slot.handle, p.inputs, countOf(slot.outputShape), slot.outputInt, this._captureSpec(slot))
+        return { output: r.output, captures: r.captures }
       }
       case 'uploadParams':
-        A.uploadParams(this._mustGet(p.graphId).handle, p.params)
+        await A.uploadParams(this._mustGet(p.graphId).handle, p.params)
         return null
       case 'downloadParams':
-        return { params: A.downloadParams(this._mustGet(p.graphId).handle) }
+        return { params: await A.downloadParams(this._mustGet(p.graphId).handle) }
       case 'resetOptimizer':
-        A.resetOptimizer(this._mustGet(p.graphId).handle)
+        await A.resetOptimizer(this._mustGet(p.graphId).handle)
         return null
       case 'setLR':
-        A.setLR(this._mustGet(p.graphId).handle, JSON.stringify(p.lr))
+        await A.setLR(this._mustGet(p.graphId).handle, JSON.stringify(p.lr))
         return null
       case 'destroy': {
         for (const [id, slot] of Array.from(this.graphs.entries()))
           if (slot.parentGraphId === p.graphId) this.graphs.delete(id)
         const slot = this.graphs.get(p.graphId)
         if (!slot) return null
-        A.destroy(slot.handle)        // cascades to the siblings in the library
         this.graphs.delete(p.graphId)
+        await A.destroy(slot.handle)  // cascades to the siblings in the library
         return null
       }
       default:
@@ -191,36 +191,67 @@ class NativeWorkerProxy {
     }
   }
 
+  // The family a request belongs to, fixed when the request is made: a forward sibling
+  // (compileForward) joins its parent's family, every other graph id is its own.
+  _familyOf(req) {
+    const p = req.payload || {}
+    if (req.kind === 'compileForward') {
+      const f = this.family.has(p.parentGraphId) ? this.family.get(p.parentGraphId) : p.parentGraphId
+      this.family.set(p.graphId, f)
+      return f
+    }
+    if (!this.family.has(p.graphId)) this.family.set(p.graphId, p.graphId)
+    return this.family.get(p.graphId)
+  }
+
+  // Requests of one family run one after another in arrival order (the reference worker
+  // handles its messages in order and chains its dispatches, src/runtime.ts:303-313);
+  // families run independently. A failed request does not stop the ones behind it.
+  _enqueue(req) {
+    const fam = this._familyOf(req)
+    const prev = this.queues.has(fam) ? this.queues.get(fam) : Promise.resolve()
+    const turn = prev.catch(() => {}).then(() => {
+      if (this.terminated) throw new Error('tensorgrad: worker terminated')
+      return this._handle(req)
+    })
+    this.queues.set(fam, turn)
+    return turn
+  }
+
   /** Same contract as WorkerProxy.request: resolves with the handler's result, rejects
-   *  with an Error whose `name` survives (AbortError for destroyed / replaced graphs). */
+   *  with an Error whose `name` survives (AbortError for destroyed / replaced graphs).
+   *  The native work runs off the JS thread. */
   request(req, transfer) {
     if (this.terminated) return Promise.reject(new Error('tensorgrad: worker has been terminated'))
-    return new Promise((resolve, reject) => {
-      setImmediate(() => {
-        if (this.terminated) return reject(new Error('tensorgrad: worker terminated'))
-        try {
-          resolve(this._handle(req))
-        } catch (e) {
-          reject(e instanceof Error ? e : new Error(String(e)))
-        }
-      })
-    })
+    return this._enqueue(req)
   }
 
   send(req, transfer) {
     if (this.terminated) return
-    setImmediate(() => {
-      if (this.terminated) return
-      try { this._handle(req) } catch (e) { /* fire-and-forget, as WorkerProxy.send */ }
-    })
+    this._enqueue(req).catch(() => { /* fire-and-forget, as WorkerProxy.send */ })
   }
 
+  /** Stops the proxy: requests not yet started reject; each family's runtimes are
+   *  destroyed once the request it is running (if any) has finished. Resolves when all
+   *  are destroyed. */
   terminate() {
-    if (this.terminated) return
+    if (this.terminated) return Promise.resolve()
     this.terminated = true
-    for (const [id, slot] of Array.from(this.graphs.entries()))
-      if (slot.parentGraphId === null) native().destroy(slot.handle)
-    this.graphs.clear()
+    const done = []
+    const queued = new Set(this.queues.keys())
+    for (const [fam, tail] of Array.from(this.queues.entries()))
+      done.push(tail.catch(() => {}).then(() => this._destroyWhere(f => f === fam)))
+    done.push(this._destroyWhere(f => !queued.has(f)))
+    this.queues.clear()
+    return Promise.all(done).then(() => undefined)
+  }
+
+  async _destroyWhere(pick) {
+    for (const [id, slot] of Array.from(this.graphs.entries())) {
+      if (!pick(this.family.has(id) ? this.family.get(id) : id)) continue
+      this.graphs.delete(id)
+      if (slot.parentGraphId === null) await native().destroy(slot.handle)
+    }
   }
 }
 

@@ -33,24 +33,13 @@ def sign_ambiguous(diff, lr: float, steps: int, upd=None) -> np.ndarray:
     steps (two opposite updates of size lr per step, plus slack); a larger difference is
     never excused. Later updates are lrt * m / (sqrt(v) + eps), smaller than lr where the
     element's gradient is mostly noise (m near zero) and the bias correction lrt / lr is
-    below 1: given the elements' own update sizes `upd` (from the optimizer state), the
-    floor is half the element's update, kept within [lr/16, lr/4] (lr/16 is still two
-    orders of magnitude above rounding-sized differences at every benchmark lr)."""
+    below 1: given the elements' update sizes `upd` (from the oracle's optimizer state,
+    stored in the fixture, never from the runtime under test), the floor is half the
+    element's update, kept within [lr/16, lr/4] (lr/16 is still two orders of magnitude
+    above rounding-sized differences at every benchmark lr)."""
     a = np.abs(np.asarray(diff, np.float64))
     floor = lr / 4 if upd is None else np.clip(np.asarray(upd, np.float64) / 2, lr / 16, lr / 4)
     return (a >= floor) & (a <= 2.5 * lr * steps)
-
-
-def adam_update_sizes(state: dict, name: str, idx, opt: dict, steps: int):
-    """|lrt * m / (sqrt(v) + eps)| of parameter `name`'s elements `idx` at step `steps`,
-    from a downloaded optimizer state (None when the state has no Adam moments for it)."""
-    m, v = state.get(f'adam_m_{name}'), state.get(f'adam_v_{name}')
-    if m is None or v is None:
-        return None
-    b1, b2, eps = opt.get('beta1', 0.9), opt.get('beta2', 0.999), opt.get('eps', 1e-8)
-    lrt = opt['lr'] * np.sqrt(1 - b2 ** steps) / (1 - b1 ** steps)
-    m, v = m.astype(np.float64)[idx], v.astype(np.float64)[idx]
-    return np.abs(lrt * m / (np.sqrt(v) + eps))
 
 
 class HipBuffers:

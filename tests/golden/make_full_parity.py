@@ -16,7 +16,12 @@ step-100 values (same indices) measure how far the workload itself amplifies suc
 difference over 100 steps ('twin_losses' [n, steps], 'twin:<param>' [n, sample],
 'twin_norm:<param>' [n]). The test bounds each tensor by its farthest twin, so that
 spread is estimated from several samples: four for the eight-layer NeRF MLP, two for the
-CNN. For the configs in ARITH_TWINS more twins train from the unperturbed parameters with
+CNN. Per parameter tensor with Adam moments, 'upd:<param>' holds the oracle's own update size at
+step 100 on the same indices, |lrt * m / (sqrt(v) + eps)| from its m and v (the scale of an
+update gone the other way, which the test's sign-ambiguity floor uses; taken from the
+oracle, not from the implementation under test).
+
+For the configs in ARITH_TWINS more twins train from the unperturbed parameters with
 another valid rounding at every step rather than once: 'f32', every matmul accumulated in
 f32 (pyoracle.set_matmul_f32), as f32 GPU kernels accumulate (the reference's own WGSL
 kernels among them); 'sum64', sum_to_shape (the bias and LayerNorm-parameter gradients)
@@ -25,6 +30,8 @@ running sum, as this backend's column sums do. 'twin_kinds' names each twin.
 
     python tests/golden/make_full_parity.py [keys...] [--threads N]
     python tests/golden/make_full_parity.py nerf --add-twins   # train only the missing twins
+    python tests/golden/make_full_parity.py --add-updates      # retrain the base run, check it
+                                                               # reproduces the fixture, add upd:
 """
 import argparse
 import os
@@ -47,7 +54,7 @@ FULL_LIMIT = 16_384
 SAMPLE = 4096
 WHOLE = {'char_mlp'}
 NTWIN = {'cnn': 2, 'nerf': 4}
-ARITH_TWINS = {'nerf': ('f32', 'sum64')}
+ARITH_TWINS = {'nerf': ('f32', 'sum64'), 'cnn': ('f32', 'sum64')}
 SWITCHES = {'f32': pyoracle.set_matmul_f32, 'sum64': pyoracle.set_sum_f64}
 
 
@@ -80,9 +87,19 @@ def train(key: str, cfg, ir, params: dict, tag: str):
     return o, np.array(losses, np.float64)
 
 
-def make(key: str) -> str:
-    cfg = configs.CONFIGS[key]
-    ir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer)
+def update_sizes(o, cfg, n: str, size: int, idx: np.ndarray):
+    """|lrt * m / (sqrt(v) + eps)| of the oracle's state at step STEPS, or None."""
+    opt = cfg.optimizer
+    if opt.get('kind', 'adam') not in ('adam', 'adamw'):
+        return None
+    b1, b2, eps = opt.get('beta1', 0.9), opt.get('beta2', 0.999), opt.get('eps', 1e-8)
+    lrt = pyoracle.resolve_lr(opt['lr'], STEPS) * np.sqrt(1 - b2 ** STEPS) / (1 - b1 ** STEPS)
+    m = o.get_home(f'adam_m_{n}', size).astype(np.float64)[idx]
+    v = o.get_home(f'adam_v_{n}', size).astype(np.float64)[idx]
+    return np.abs(lrt * m / (np.sqrt(v) + eps))
+
+
+def base_run(key: str, cfg, ir) -> dict:
     p0 = ir.initial_params(configs.INIT_SEED)
     o, losses = train(key, cfg, ir, p0, '')
     out = {'losses': losses, 'steps': np.array(STEPS)}
@@ -94,6 +111,17 @@ def make(key: str) -> str:
         out[f'idx:{n}'] = idx
         out[f'val:{n}'] = v[idx]
         out[f'norm:{n}'] = np.array(np.linalg.norm(v.astype(np.float64)))
+        u = update_sizes(o, cfg, n, sizes[n], idx)
+        if u is not None:
+            out[f'upd:{n}'] = u
+    return out
+
+
+def make(key: str) -> str:
+    cfg = configs.CONFIGS[key]
+    ir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer)
+    p0 = ir.initial_params(configs.INIT_SEED)
+    out = base_run(key, cfg, ir)
     if key in NTWIN:
         add_twins(key, cfg, ir, p0, out, 0)
     path = os.path.join(HERE, f'full_{key}.npz')
@@ -147,15 +175,40 @@ def extend(key: str) -> str:
     return path
 
 
+def add_updates(key: str) -> str:
+    """Train the base run again, check that it reproduces the stored losses and values
+    bit for bit, and store its update sizes."""
+    path = os.path.join(HERE, f'full_{key}.npz')
+    with np.load(path) as z:
+        out = {k: z[k] for k in z.files}
+    cfg = configs.CONFIGS[key]
+    ir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer)
+    new = base_run(key, cfg, ir)
+    for k, v in new.items():
+        if k.startswith('upd:'):
+            out[k] = v
+        elif not np.array_equal(np.asarray(out[k]), np.asarray(v)):
+            raise SystemExit(f'{key}: the base run no longer reproduces {k}')
+    np.savez_compressed(path, **out)
+    return path
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument('keys', nargs='*', default=['char_mlp', 'cnn', 'transformer', 'nerf'])
     ap.add_argument('--threads', type=int, default=os.cpu_count() or 8)
     ap.add_argument('--add-twins', action='store_true', help='only train the twins the fixture lacks')
+    ap.add_argument('--add-updates', action='store_true',
+                    help='retrain the base run, check it reproduces the fixture, store the update sizes')
     a = ap.parse_args()
     pyoracle.set_threads(a.threads)
     for k in a.keys:
-        print(k, '->', extend(k) if a.add_twins else make(k), flush=True)
+        if a.add_updates:
+            print(k, '->', add_updates(k), flush=True)
+        if a.add_twins:
+            print(k, '->', extend(k), flush=True)
+        if not (a.add_updates or a.add_twins):
+            print(k, '->', make(k), flush=True)
 
 
 if __name__ == '__main__':

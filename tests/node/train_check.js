@@ -39,7 +39,7 @@ async function main() {
   } catch (e) {
     aborted = e.name
   }
-  proxy.terminate()
+  await proxy.terminate()
   process.stdout.write(JSON.stringify({ paramNames: meta.paramNames, kernelCount: meta.kernelCount, losses, params,
                                         forward: Array.from(run.output), abortedAfterDestroy: aborted }) + '\n')
 }

@@ -180,13 +180,25 @@ def test_parity_helpers_reject_non_finite_and_bound_the_exclusion():
     assert not sign_ambiguous(np.full(6, lr / 17), lr, steps, np.zeros(6)).any()
     assert sign_ambiguous(np.full(6, lr / 16), lr, steps, np.zeros(6)).all()
     assert sign_ambiguous(d, lr, steps, np.full(6, 4 * lr)).tolist() == [False, True, True, True, False, False]
-    from _helpers import adam_update_sizes
-    opt = {'lr': lr}
-    st = {'adam_m_w': np.array([0.5, -2.0, 0.0], np.float32), 'adam_v_w': np.array([4.0, 1.0, 1.0], np.float32)}
-    lrt = lr * np.sqrt(1 - 0.999 ** steps) / (1 - 0.9 ** steps)
-    u = adam_update_sizes(st, 'w', np.arange(3), opt, steps)
-    assert np.allclose(u, [lrt * 0.5 / (2 + 1e-8), lrt * 2 / (1 + 1e-8), 0.0])
-    assert adam_update_sizes(st, 'other', np.arange(3), opt, steps) is None
+
+
+def test_full_fixtures_carry_the_oracles_update_sizes():
+    """The full-size fixtures hold, for every stored parameter element, the oracle's own
+    Adam update size at step 100 (the sign-ambiguity floor of the 100-step test comes from
+    the oracle, not from the runtime under test), and the twin configs their arithmetic
+    twins."""
+    import numpy as np
+    root = os.path.join(os.path.dirname(os.path.abspath(__file__)), 'golden')
+    for key in ('char_mlp', 'cnn', 'nerf', 'transformer'):
+        g = np.load(os.path.join(root, f'full_{key}.npz'), allow_pickle=False)
+        names = [f[4:] for f in g.files if f.startswith('idx:')]
+        assert names
+        for n in names:
+            u = g[f'upd:{n}']
+            assert u.shape == g[f'idx:{n}'].shape and np.all(np.isfinite(u)) and np.all(u >= 0), (key, n)
+        if key in ('cnn', 'nerf'):
+            kinds = [str(k) for k in g['twin_kinds']]
+            assert 'f32' in kinds and 'sum64' in kinds and kinds.count('ulp') >= 2, (key, kinds)
 
 
 def test_several_streams_are_rejected(monkeypatch):
@@ -279,3 +291,53 @@ def test_groups_merge_only_where_their_inputs_exist():
     assert len(fused) == 1 and fused[0][1] == 'add_scalar,relu,mul_scalar,add_scalar', fused
     kinds = plan_groups(stays_apart)
     assert [k for k, _ in kinds] == ['fused', 'gemm', 'fused'], kinds
+
+
+def _plan(key, opt):
+    cfg = configs.CONFIGS[key]
+    ir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, opt)
+    return backend.plan(ir.wire_json())['nodes']
+
+
+def test_clip_normalize_and_sgd_lower_to_the_fused_optimizer(monkeypatch):
+    """clipGradNorm (grad.ts:110-130), normalizeGrads (grad.ts:148-172) and SGD's update
+    chain (sgd.ts:155-170) run in the fused optimizer: one sum-of-squares launch per
+    transform stage (its scalar chain evaluated in its last block) and one update launch,
+    so the transformer keeps the launch count of plain AdamW and its deferred grouped
+    weight-gradient GEMMs (the norm now reads the gradients inside the optimizer).
+    TG_OPT_FUSED=0 lowers the same IR op by op."""
+    cfg = configs.CONFIGS['transformer']
+    plain = _plan('transformer', cfg.optimizer)
+    clip = _plan('transformer', dict(cfg.optimizer, clipGradNorm=1.0))
+    kinds = [n['kind'] for n in clip]
+    assert len(clip) == len(plain) + 1 and len(clip) <= 77, len(clip)
+    assert kinds.count('gemm') == 36 and kinds.count('grad_norm') == 1 and kinds[-1] == 'adam_multi'
+    assert kinds[-2] == 'grad_norm'
+    assert 'gemm_group' in [n.get('ops', '') for n in clip]
+    norm = clip[-2]
+    # the scalar chain of appendGradClip: chained adds, sqrt, + 1e-6, maxNorm / ., min(., 1)
+    assert norm['ops'].count('add') >= 40 and 'sqrt' in norm['ops'] and 'div' in norm['ops'] and 'min' in norm['ops']
+    assert norm['bytes'] == 4 * sum(n['bytes'] / 28 for n in clip if n['kind'] == 'adam_multi')
+    both = _plan('transformer', dict(cfg.optimizer, clipGradNorm=1.0, normalizeGrads=True))
+    assert [n['kind'] for n in both].count('grad_norm') == 2 and len(both) == len(plain) + 2
+    for opt in ({'kind': 'sgd', 'lr': 0.01}, {'kind': 'sgd', 'lr': 0.01, 'momentum': 0.9},
+                {'kind': 'sgd', 'lr': 0.01, 'momentum': 0.9, 'nesterov': True, 'weightDecay': 1e-3}):
+        sgd = _plan('transformer', opt)
+        k = [n['kind'] for n in sgd]
+        assert len(sgd) <= 76 and k[-1] == 'sgd_multi' and k.count('sgd_multi') == 1 and 'adam_multi' not in k, k
+        assert k.count('gemm') == 36
+    monkeypatch.setenv('TG_OPT_FUSED', '0')
+    apart = _plan('transformer', dict(cfg.optimizer, clipGradNorm=1.0))
+    assert 'grad_norm' not in [n['kind'] for n in apart] and len(apart) > 150
+    sgd = _plan('transformer', {'kind': 'sgd', 'lr': 0.01})
+    assert 'sgd_multi' not in [n['kind'] for n in sgd]
+
+
+@pytest.mark.parametrize('key', list(configs.CONFIGS))
+def test_fused_optimizer_lowers_every_config(key):
+    cfg = configs.CONFIGS[key]
+    for opt in (dict(cfg.optimizer, clipGradNorm=0.5), dict(cfg.optimizer, normalizeGrads=True),
+                {'kind': 'sgd', 'lr': 0.01, 'momentum': 0.9, 'clipGradNorm': 1.0}):
+        nodes = _plan(key, opt)
+        kinds = [n['kind'] for n in nodes]
+        assert kinds[-1] in ('adam_multi', 'sgd_multi') and kinds.count('grad_norm') == 1, kinds

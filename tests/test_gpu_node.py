@@ -69,3 +69,37 @@ def test_node_shim_trains_like_ctypes(tmp_path, key):
         assert np.array_equal(np.asarray(got['params'][k], np.float32), params[k]), k
     assert np.array_equal(np.asarray(got['forward'], np.float32), out.reshape(-1))
     assert got['abortedAfterDestroy'] == 'AbortError'
+
+
+def test_node_requests_run_off_the_event_loop(tmp_path):
+    """The addon works off the JS thread, as the reference's Web Worker does: a 1 ms
+    setInterval keeps ticking through the full transformer's createRuntime (lowering,
+    kernel compilation, allocation, upload) and through 20 training steps, and the
+    losses are bit-identical to the same steps through ctypes. Four more steps issued
+    without awaiting run in arrival order (the family's queue)."""
+    cfg = configs.CONFIGS['transformer']
+    ir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer)
+    p0 = ir.initial_params(42)
+    bs = configs.batches(cfg, 20)
+    payload = reference_payload(ir)
+    payload['initialParams'] = _rec({k: np.asarray(v, np.float32) for k, v in p0.items()})
+    f = tmp_path / 'spec.json'
+    f.write_text(json.dumps({'payload': payload, 'steps': [_rec(b) for b in bs]}))
+    r = subprocess.run([NODE, os.path.join(ROOT, 'tests', 'node', 'async_check.js'), str(f)], capture_output=True,
+                       text=True, timeout=300)
+    assert r.returncode == 0, r.stderr
+    got = json.loads(r.stdout)
+    print(f"  create {got['createMs']} ms / {got['createTicks']} ticks, 20 steps {got['stepMs']} ms / "
+          f"{got['stepTicks']} ticks, 4 queued steps {got['concurrentMs']} ms / {got['concurrentTicks']} ticks",
+          flush=True)
+    # a blocked event loop would count no ticks at all; a free one counts about one per ms
+    assert got['createTicks'] >= max(3, got['createMs'] // 4)
+    assert got['stepTicks'] >= max(2, got['stepMs'] // 4)
+
+    rt = backend.NativeRuntime(ir.wire_json())
+    rt.upload_params(p0)
+    losses = [rt.step(b) for b in bs]
+    more = [rt.step(b) for b in bs[:4]]
+    rt.destroy()
+    assert [np.float32(v) for v in got['losses']] == [np.float32(v) for v in losses]
+    assert [np.float32(v) for v in got['more']] == [np.float32(v) for v in more]

@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 
 import pyoracle
-from _helpers import adam_update_sizes, rel_err, sign_ambiguous
+from _helpers import rel_err, sign_ambiguous
 from tensorgrad_amd import backend, configs
 from tensorgrad_amd.build_ir import build_training_ir
 
@@ -263,27 +263,30 @@ TWIN_FACTOR = 4.0
 def test_full_config_100_steps(key):
     """Full-size configs for 100 optimizer steps against the oracle's own 100-step run
     (tests/golden/make_full_parity.py: every step's loss, and at step 100 each parameter
-    tensor whole or a fixed seeded sample of 4096 elements, plus the whole tensor's norm).
+    tensor whole or a fixed seeded sample of 4096 elements, plus the whole tensor's norm
+    and the oracle's own update size of each stored element).
 
     Bar: every step's loss within 1e-4 relative; every tensor's values (whole or sampled)
     within 1e-4 relative (L2) and its norm within 1e-4, after setting aside the elements
     whose difference is that of Adam updates gone opposite ways (sign_ambiguous: at least
-    half the element's own update at step 100, from the downloaded Adam moments, kept
-    within [lr/16, lr/4], and at most 2.5 * lr * 100). Those are printed, counted and
-    bounded.
+    half the element's update at step 100 in the oracle's run, kept within [lr/16, lr/4],
+    and at most 2.5 * lr * 100). Those are printed, counted and bounded: without twins at
+    most 4 elements in all; with twins, at most as many as the twins' own count and with a
+    summed |difference| at most TWIN_FACTOR times the twins'.
 
     Where the fixture also holds the oracle's twins, the workload's own amplification of a
     rounding-sized difference is known: one-ulp twins (the evaluator trained again from
-    initial parameters one ulp away, in seeded directions: two for C3, four for C4) and,
-    for C4, an f32 twin (the evaluator with every matmul accumulated in f32, as f32 GPU
-    kernels accumulate: a rounding difference at every step). A step or tensor at which the
-    twins themselves lie beyond the bar is held to TWIN_FACTOR times the farthest twin's
-    distance instead (a step's loss: the twins' worst distance up to that step; a tensor's
-    values: the twins' distance measured the same way; its norm: the larger of the twins'
-    norm and value distances), and the sign-ambiguous count to TWIN_FACTOR times the
-    twins' largest count. The GPU's rounding differs from the evaluator's in every one of
-    the 100 steps and in other places than an f32 twin's (f32 MFMA accumulation order,
-    blocked sums), hence a factor above 1."""
+    initial parameters one ulp away, in seeded directions: two for C3, four for C4) and
+    arithmetic twins (the evaluator with every matmul accumulated in f32, as f32 GPU kernels
+    accumulate; and with the bias / LayerNorm gradient sums in f64: a rounding difference at
+    every step, not once). A step or tensor at which the twins themselves lie beyond the bar
+    is held to TWIN_FACTOR times the farthest twin's distance instead (a step's loss: the
+    twins' worst distance up to that step; a tensor's values: the twins' distance measured
+    the same way; its norm: the larger of the twins' norm and value distances). The GPU's
+    rounding differs from the evaluator's in every one of the 100 steps and in other places
+    than an arithmetic twin's (f32 MFMA accumulation order, blocked sums), hence a factor
+    above 1. test_full_config_trajectory_gradients holds the same runs to the plain 1e-4
+    bar along the trajectory, step by step."""
     path = os.path.join(GOLDEN, f'full_{key}.npz')
     g = np.load(path, allow_pickle=False)
     twin = 'twin_losses' in g.files
@@ -305,9 +308,9 @@ def test_full_config_100_steps(key):
         worst_loss = max(worst_loss, e)
         worst_excess = max(worst_excess, e / loss_bar[i])
     pg = rt.download_params()
-    state, _, _ = rt.download_state()
     rt.destroy()
     flips, tflips, checked, fails = 0, 0, 0, []
+    dev, tdev = 0.0, 0.0
     worst, worst_name, worst_norm = 0.0, '', 0.0
     for n in ir.param_names:
         idx, want = g[f'idx:{n}'], g[f'val:{n}'].astype(np.float64)
@@ -315,23 +318,26 @@ def test_full_config_100_steps(key):
         diff = got[idx] - want
         if not np.all(np.isfinite(diff)):
             raise AssertionError(f'[{key}] {n}: non-finite parameters')
-        upd = adam_update_sizes(state, n, idx, cfg.optimizer, steps)
+        upd = g[f'upd:{n}'] if f'upd:{n}' in g.files else None
         amb = sign_ambiguous(diff, lr, steps, upd)
         flips += int(amb.sum())
+        dev += float(np.abs(diff[amb]).sum())
         checked += idx.size
         e = rel_err(want + np.where(amb, 0.0, diff), want, f'[{key}] {n}')
         en = rel_err(np.linalg.norm(got), float(g[f'norm:{n}']), f'[{key}] {n} norm')
         bar, nbar, note = PARAM_TOL, PARAM_TOL, ''
         if twin:
-            te, tn, ta = 0.0, 0.0, 0
+            te, tn, ta, td = 0.0, 0.0, 0, 0.0
             for j, tv in enumerate(np.atleast_2d(g[f'twin:{n}'])):
                 tdiff = tv.astype(np.float64) - want
                 tamb = sign_ambiguous(tdiff, lr, steps, upd)
                 ta = max(ta, int(tamb.sum()))
+                td = max(td, float(np.abs(tdiff[tamb]).sum()))
                 te = max(te, rel_err(want + np.where(tamb, 0.0, tdiff), want, f'[{key}] {n} twin {j}'))
                 tn = max(tn, rel_err(float(np.atleast_1d(g[f'twin_norm:{n}'])[j]), float(g[f'norm:{n}']),
                                      f'[{key}] {n} twin {j} norm'))
             tflips += ta
+            tdev += td
             # |norm(a) - norm(b)| <= norm(a - b): a tensor's norm moves at most as far as its
             # values, so the twin's value distance bounds the norm too (its own norm distance,
             # one scalar, can cancel by chance)
@@ -347,11 +353,83 @@ def test_full_config_100_steps(key):
         worst_norm = max(worst_norm, en)
     print(f'  [{key}] {steps} steps in {time.time() - t0:.1f}s: worst loss rel {worst_loss:.2e} '
           f'({worst_excess:.2f} of its bar), worst param rel {worst:.2e} ({worst_name}), worst norm rel '
-          f'{worst_norm:.2e}, {flips} sign-ambiguous of {checked}' + (f' (twin: {tflips})' if twin else ''),
-          flush=True)
+          f'{worst_norm:.2e}, {flips} sign-ambiguous of {checked}, summed |diff| {dev:.3e}'
+          + (f' (twins: {tflips}, {tdev:.3e})' if twin else ''), flush=True)
     assert worst_excess <= 1.0
     assert not fails, fails
-    assert flips <= max(4, 1e-3 * checked, TWIN_FACTOR * tflips)
+    if twin:
+        assert flips <= max(4, tflips) and dev <= max(TWIN_FACTOR * tdev, 4 * 2.5 * lr * steps)
+    else:
+        assert flips <= 4
+
+
+TRAJECTORY = (1, 25, 50, 75, 100)
+F32_TWIN_FACTOR = 2.0
+
+
+@pytest.mark.parametrize('key', ['char_mlp', 'cnn', 'nerf', 'transformer'])
+def test_full_config_trajectory_gradients(key):
+    """The gradient kernels on the states the 100-step run visits: the full-size config
+    trains 100 steps on the GPU; after steps 1, 25, 50, 75 and 100 the GPU's parameters go
+    to a plain SGD graph (lr = 2^24, so p1 - p0 = -lr * g) on both the GPU and the oracle,
+    which take one step on the next batch from exactly those parameters. Every tensor's
+    update (its gradient) agrees within 1e-4 relative, independently of the workload's own
+    amplification of rounding differences over the run.
+
+    The bar holds as stated except where f32 arithmetic itself cannot meet it on that
+    state: the oracle also evaluates the same step with every matmul accumulated in f32
+    (the f32 twin: a valid f32 implementation, as the reference's WGSL kernels are). Where
+    that twin lies beyond 1e-4 of the f64 evaluator, the tensor is held to F32_TWIN_FACTOR
+    times the twin's distance instead, and both figures are printed. (C4, late in its run:
+    its ReLU layers below the skip concatenation see gradients that f32 arithmetic
+    reproduces only to a few 1e-4.)"""
+    pyoracle.set_threads(16)
+    cfg = configs.CONFIGS[key]
+    ir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer)
+    sgd = {'kind': 'sgd', 'lr': float(2 ** 24)}
+    sir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, sgd)
+    rt = backend.NativeRuntime(ir.wire_json())
+    srt = backend.NativeRuntime(sir.wire_json())
+    rt.upload_params(ir.initial_params(configs.INIT_SEED))
+    batches = configs.batches(cfg, TRAJECTORY[-1] + 1)
+    fails = []
+    for i in range(TRAJECTORY[-1]):
+        rt.step(batches[i])
+        k = i + 1
+        if k not in TRAJECTORY:
+            continue
+        p = rt.download_params()
+        srt.upload_params(p)
+        srt.step(batches[k])
+        pg = srt.download_params()
+        upd = {}
+        for f32 in (False, True):
+            pyoracle.set_matmul_f32(f32)
+            try:
+                so = pyoracle.OracleRuntime(sir.wire())
+                so.upload_params(p)
+                so.step(batches[k])
+                upd[f32] = {n: so.get_home(n, pg[n].size).astype(np.float64) - np.asarray(p[n], np.float64).reshape(-1)
+                            for n in sir.param_names}
+            finally:
+                pyoracle.set_matmul_f32(False)
+        worst, wn, relaxed = 0.0, '', []
+        for n in sir.param_names:
+            start = np.asarray(p[n], np.float64).reshape(-1)
+            e = rel_err(pg[n].astype(np.float64) - start, upd[False][n], f'[{key}] step {k} {n} update')
+            tw = rel_err(upd[True][n], upd[False][n], f'[{key}] step {k} {n} f32 twin')
+            bar = GRAD_TOL if tw <= GRAD_TOL else F32_TWIN_FACTOR * tw
+            if bar > GRAD_TOL:
+                relaxed.append(f'{n} {e:.2e} (f32 twin {tw:.2e})')
+            if e > bar:
+                fails.append(f'step {k} {n}: {e:.2e} > {bar:.2e}')
+            if e > worst:
+                worst, wn = e, n
+        print(f'  [{key}] after step {k}: worst gradient rel {worst:.2e} ({wn})'
+              + (f'; beyond 1e-4 in f32 itself: {", ".join(relaxed)}' if relaxed else ''), flush=True)
+    rt.destroy()
+    srt.destroy()
+    assert not fails, fails
 
 
 @pytest.mark.parametrize('key', ['char_mlp', 'cnn', 'transformer', 'nerf'])
@@ -371,4 +449,76 @@ def test_sgd_momentum_nesterov_and_scheduled_adamw():
                          opt={'kind': 'adamw', 'lr': sched, 'weightDecay': 0.05, 'clipGradNorm': 0.5})
     assert wl <= LOSS_TOL and wp <= PARAM_TOL
     wl, wp, _ = _train_both(configs.small_variant('nerf'), 30, opt={'kind': 'adam', 'lr': 1e-3, 'normalizeGrads': True})
+    assert wl <= LOSS_TOL and wp <= PARAM_TOL
+
+
+FUSED_OPT_CASES = [
+    ('char_mlp', {'kind': 'adamw', 'lr': 3e-3, 'weightDecay': 0.05, 'clipGradNorm': 0.5}),
+    ('transformer', {'kind': 'adamw', 'lr': 3e-4, 'weightDecay': 0.01, 'clipGradNorm': 0.05}),
+    ('cnn', {'kind': 'adam', 'lr': 1e-3, 'normalizeGrads': True, 'clipGradNorm': 1.0}),
+    ('nerf', {'kind': 'adam', 'lr': 1e-3, 'normalizeGrads': lambda n: n.endswith('.W'), 'clipGradNorm': 0.1}),
+    ('mlp_sin', {'kind': 'sgd', 'lr': 0.01}),
+    ('mlp_sin', {'kind': 'sgd', 'lr': 0.01, 'momentum': 0.9}),
+    ('char_mlp', {'kind': 'sgd', 'lr': 0.05, 'momentum': 0.9, 'weightDecay': 1e-3, 'clipGradNorm': 0.5}),
+    ('nerf', {'kind': 'sgd', 'lr': 0.01, 'momentum': 0.9, 'nesterov': True, 'weightDecay': 1e-3,
+              'normalizeGrads': True}),
+]
+
+
+@pytest.mark.parametrize('case', range(len(FUSED_OPT_CASES)))
+def test_fused_optimizer_against_the_oracle(case):
+    """Clipping, normalisation and SGD in the fused optimizer (one sum-of-squares launch per
+    transform stage, its scalar chain in the launch's last block, then the multi-tensor
+    update) train the small variants 40 steps within the parity bar of the oracle, which
+    evaluates the reference's op-by-op IR (grad.ts:110-172, sgd.ts:155-170)."""
+    key, opt = FUSED_OPT_CASES[case]
+    cfg = configs.small_variant(key)
+    ir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, opt)
+    kinds = [n['kind'] for n in backend.plan(ir.wire_json())['nodes']]
+    assert kinds[-1] == ('sgd_multi' if opt['kind'] == 'sgd' else 'adam_multi'), kinds
+    assert ('grad_norm' in kinds) == ('clipGradNorm' in opt or 'normalizeGrads' in opt)
+    wl, wp, _ = _train_both(cfg, 40, opt=opt)
+    assert wl <= LOSS_TOL and wp <= PARAM_TOL
+
+
+def test_fused_optimizer_against_op_by_op(monkeypatch):
+    """The fused clip + AdamW and the op-by-op lowering of the same IR (TG_OPT_FUSED=0) agree
+    after five full-size transformer steps: the only difference is the summation order of
+    the f64 sums of squares, each rounded once to f32."""
+    cfg = configs.CONFIGS['transformer']
+    opt = dict(cfg.optimizer, clipGradNorm=0.05)
+    ir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, opt)
+    p0 = ir.initial_params(11)
+    batches = configs.batches(cfg, 5)
+    out = {}
+    for fused in ('0', '1'):
+        monkeypatch.setenv('TG_OPT_FUSED', fused)
+        rt = backend.NativeRuntime(ir.wire_json())
+        assert ('grad_norm' in [n['kind'] for n in rt.describe()['nodes']]) == (fused == '1')
+        rt.upload_params(p0)
+        for b in batches:
+            rt.step(b)
+        out[fused] = rt.download_params()
+        rt.destroy()
+    for n in ir.param_names:
+        assert rel_err(out['1'][n], out['0'][n], n) <= 1e-6, n
+
+
+def test_full_transformer_clip_gradients():
+    """Full-size C5 with clipGradNorm below the gradient norm: one SGD step with lr = 2^24
+    from the same params and batch on both sides, so the update is -lr * scale * g and its
+    relative error that of the clipped gradient (the global norm's scale included); the
+    weight gradients stay in the deferred grouped GEMM launch."""
+    pyoracle.set_threads(16)
+    w = _update_error(configs.CONFIGS['transformer'], opt={'kind': 'sgd', 'lr': float(2 ** 24), 'clipGradNorm': 0.05},
+                      want_ops='gemm_group')
+    assert w <= GRAD_TOL
+
+
+def test_full_transformer_clip_20_steps():
+    """Full-size C5 with the reference samples' clipGradNorm 1.0 (AdamW 3e-4, wd 0.01),
+    20 steps against the oracle run live: losses and every parameter tensor within 1e-4."""
+    pyoracle.set_threads(16)
+    cfg = configs.CONFIGS['transformer']
+    wl, wp, _ = _train_both(cfg, 20, opt=dict(cfg.optimizer, clipGradNorm=1.0))
     assert wl <= LOSS_TOL and wp <= PARAM_TOL

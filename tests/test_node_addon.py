@@ -45,7 +45,7 @@ def test_addon_is_built_and_exports_the_binding():
     assert r.returncode == 0, r.stderr
     keys = set(json.loads(r.stdout))
     assert {'plan', 'create', 'createSibling', 'destroy', 'step', 'run', 'uploadParams', 'downloadParams',
-            'resetOptimizer', 'setLR', 'getCapture', 'saveCheckpoint', 'loadCheckpoint', 'downloadState',
+            'resetOptimizer', 'setLR', 'saveCheckpoint', 'loadCheckpoint', 'downloadState',
             'uploadState', 'safetensorsIndex'} <= keys
 
 
@@ -100,3 +100,20 @@ def test_safetensors_index_from_node_matches_ctypes(tmp_path):
                                       "try{a.safetensorsIndex(new Uint8Array(4))}catch(e){console.log(e.message,e.tgStatus)}"],
                          capture_output=True, text=True)
     assert 'too small' in bad.stdout and bad.stdout.strip().endswith('2')
+
+
+def test_device_calls_return_promises():
+    """Calls that touch the device run as asynchronous work and return Promises: without a
+    device (or with an invalid document) create rejects with the library's status and the
+    message read on the worker thread; argument errors throw synchronously before any
+    work is queued."""
+    script = (f"const a=require({json.dumps(ADDON)});"
+              "const p=a.create('{}');"
+              "console.log(p instanceof Promise);"
+              "p.then(()=>console.log('resolved'),e=>console.log('rejected',e.tgStatus,JSON.stringify(e.message)));"
+              "try{a.step(null,{},null)}catch(e){console.log('throws',e.name)}")
+    r = subprocess.run([NODE, '-e', script], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0, r.stderr
+    out = r.stdout.strip().split('\n')
+    assert out[0] == 'true' and out[1] == 'throws TypeError', out
+    assert out[2].startswith('rejected 2 ') and 'graph' in out[2], out   # TG_INVALID_ARGUMENT

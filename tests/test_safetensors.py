@@ -97,3 +97,91 @@ def test_writer_round_trip_aligned_and_order_preserved():
     assert d.shapes == {'b': [3, 5], 'a': [7], 'c': []} and d.metadata == {'k': 'v'}
     with pytest.raises(ValueError):
         save_safetensors({'x': np.zeros(3, np.float32)}, shapes={'x': [2]})
+
+
+def test_dimensions_beyond_exact_doubles_are_rejected():
+    """A dimension or offset of 2^53 or more cannot be read exactly from a JSON number: it
+    is refused before any integer conversion."""
+    with pytest.raises(BackendError, match='malformed shape'):
+        load_safetensors(raw({'x': {'dtype': 'F32', 'shape': [2 ** 63], 'data_offsets': [0, 0]}}, 0))
+    with pytest.raises(BackendError, match='malformed shape'):
+        load_safetensors(raw({'x': {'dtype': 'F32', 'shape': [2 ** 53], 'data_offsets': [0, 0]}}, 0))
+    with pytest.raises(BackendError, match='malformed data_offsets'):
+        load_safetensors(raw({'x': {'dtype': 'F32', 'shape': [1], 'data_offsets': [0, 2 ** 64]}}, 4))
+
+
+def test_element_count_that_wraps_is_rejected():
+    """[2^31, 2^31, 4] has 2^64 elements: a product in 64-bit arithmetic wraps to 0 and would
+    match an empty byte range; the parser detects the overflow instead."""
+    with pytest.raises(BackendError, match='overflows'):
+        load_safetensors(raw({'x': {'dtype': 'F32', 'shape': [2 ** 31, 2 ** 31, 4], 'data_offsets': [0, 0]}}, 0))
+    with pytest.raises(BackendError, match='overflows'):
+        load_safetensors(raw({'x': {'dtype': 'F32', 'shape': [2 ** 40, 2 ** 23], 'data_offsets': [0, 0]}}, 0))
+
+
+# ---- checkpoint checks against a graph (tg_check_checkpoint: the validation of
+# ---- tg_load_checkpoint, without a device) ------------------------------------------------
+
+def _mlp_ir():
+    from tensorgrad_amd import configs
+    from tensorgrad_amd.build_ir import build_training_ir
+    cfg = configs.small_variant('mlp_sin')
+    return build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer)
+
+
+def _checkpoint(ir, with_state=True, meta=None, extra=None):
+    """A container shaped like tg_save_checkpoint's output: params, then Adam's m and v."""
+    p0 = ir.initial_params(1)
+    tensors = {n: np.asarray(p0[n], np.float32) for n in ir.param_names}
+    if with_state:
+        for n in ir.param_names:
+            tensors[f'adam_m_{n}'] = np.zeros_like(tensors[n])
+            tensors[f'adam_v_{n}'] = np.zeros_like(tensors[n])
+    shp = {n: list(s) for n, s in ir.param_shapes().items()}
+    for n in ir.param_names:
+        shp[f'adam_m_{n}'] = shp[f'adam_v_{n}'] = shp[n]
+    m = {'format': 'tensorgrad', 'tensorgrad.optimizer': 'adam', 'tensorgrad.step': '12',
+         'tensorgrad.prngCounter': '34'}
+    m.update(meta or {})
+    buf = save_safetensors(tensors, m, shapes=shp)
+    if extra is not None:
+        # append one integer tensor after the f32 ones (rebuild the header)
+        hlen = int.from_bytes(buf[:8], 'little')
+        header = json.loads(buf[8:8 + hlen])
+        blob = buf[8 + hlen:]
+        header[extra] = {'dtype': 'I64', 'shape': [], 'data_offsets': [len(blob), len(blob) + 8]}
+        hj = json.dumps(header).encode()
+        buf = len(hj).to_bytes(8, 'little') + hj + blob + bytes(8)
+    return buf
+
+
+def test_checkpoint_check_full_and_params_only(tmp_path):
+    from tensorgrad_amd import backend
+    ir = _mlp_ir()
+    path = tmp_path / 'full.safetensors'
+    path.write_bytes(_checkpoint(ir))
+    r = backend.check_checkpoint(ir.wire_json(), path)
+    assert r == {'params': len(ir.param_names), 'state': 2 * len(ir.param_names), 'restoresCounters': True,
+                 'step': 12, 'prngCounter': 34}
+    # a params-only file (e.g. converted pretrained weights) leaves t and the seed counter
+    # alone, whatever its metadata says
+    path.write_bytes(_checkpoint(ir, with_state=False))
+    r = backend.check_checkpoint(ir.wire_json(), path)
+    assert r['state'] == 0 and not r['restoresCounters'] and r['step'] == 0 and r['prngCounter'] == 0
+
+
+def test_checkpoint_check_rejects_integer_tensors_and_bad_counters(tmp_path):
+    from tensorgrad_amd import backend
+    ir = _mlp_ir()
+    path = tmp_path / 'x.safetensors'
+    path.write_bytes(_checkpoint(ir, extra='bn.num_batches_tracked'))
+    with pytest.raises(BackendError, match="unknown tensor 'bn.num_batches_tracked'"):
+        backend.check_checkpoint(ir.wire_json(), path)
+    for bad in ('12x', '-3', '', '1e3', '99999999999999999999'):
+        path.write_bytes(_checkpoint(ir, meta={'tensorgrad.step': bad}))
+        with pytest.raises(BackendError, match='tensorgrad.step') as ei:
+            backend.check_checkpoint(ir.wire_json(), path)
+        assert ei.value.status == backend.TG_INVALID_ARGUMENT
+    path.write_bytes(_checkpoint(ir, meta={'tensorgrad.prngCounter': 'seven'}))
+    with pytest.raises(BackendError, match='tensorgrad.prngCounter'):
+        backend.check_checkpoint(ir.wire_json(), path)
