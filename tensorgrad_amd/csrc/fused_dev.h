@@ -131,15 +131,23 @@ __device__ __forceinline__ int to_int32(double x) {
   if (m < 0) m += 4294967296.0;
   return (int)(unsigned)m;
 }
+// t mod 2^32 of a non-negative integer-valued double below 2^64: t * 2^-32 and its floor
+// are exact, and so is t - q * 2^32 (it fits 32 bits); four f64 operations instead of a
+// general double -> u64 conversion.
+__device__ __forceinline__ unsigned mod32_f64(double t) {
+  const double q = floor(__dmul_rn(t, 2.3283064365386963e-10));
+  return (unsigned)__fma_rn(-q, 4294967296.0, t);
+}
+
 // The reference's PCG-style hash with its f64 multiply-adds (products below 2^53 are exact
-// in f64; the casts take the value modulo 2^32).
+// in f64, larger ones round to integers; the casts take the value modulo 2^32).
 __device__ __forceinline__ unsigned pcg_f64(unsigned seed, unsigned sc, unsigned idx) {
   unsigned h = seed ^ sc ^ idx;
   double t = __dadd_rn(__dmul_rn((double)h, 747796405.0), 2891336453.0);
-  h = (unsigned)(unsigned long long)t;
+  h = mod32_f64(t);
   unsigned x = h ^ (h >> ((h >> 28) + 4));
   double t2 = __dmul_rn((double)x, 277803737.0);
-  h = (unsigned)(unsigned long long)t2;
+  h = mod32_f64(t2);
   return h ^ (h >> 22);
 }
 

@@ -1,15 +1,14 @@
-// Fused causal attention forward for gfx950: one launch computes, per (batch, head) and
-// block of query rows,
-//   S  = Q K^T                      (f32 MFMA, blocked accumulation as in k_gemm)
+// Fused causal attention for gfx950: one launch computes, per (batch, head) and block of
+// 32 query rows,
+//   S  = Q K^T                      (f32 MFMA, 16 x 16 tiles on all eight wavefronts)
 //   S2 = f32(S * scale)             (mul_scalar)
-//   P  = causal softmax of S2 rows  (f64 exp / sum, as the row-fused kernels)
+//   P  = causal softmax of S2 rows  (f32 exp, f64 row sum, one f64 reciprocal per row)
 //   Pd = dropout(P)                 (the reference's hash on the flat [B,H,T,T] index)
-//   O  = Pd V                       (f32 MFMA, blocked accumulation as in k_gemm)
+//   O  = Pd V                       (f32 MFMA, 16 x 16 tiles, one per wavefront)
 // with Q, K, V and S / Pd tiles resident in LDS. P and Pd are written out (the backward
-// pass reads them); S and S2 never reach memory. The MFMA k-order, the accumulation
-// blocking (S: stages of 32 k, O: stages of 64 k), the row softmax's lane layout and
-// reduction order follow the unfused kernels, so the fused and unfused paths produce the
-// same bits. Built with -ffp-contract=off.
+// pass reads them); S and S2 never reach memory. A block of query rows [i0, i0 + 32) reads,
+// multiplies and normalises only keys [0, i0 + 32): the causal mask zeroes the rest, and
+// P / Pd store exact zeros there. Built with -ffp-contract=off.
 #include "kernels.h"
 
 namespace tgk {
@@ -25,17 +24,50 @@ constexpr int kDH = 64;     // head size
 constexpr int kLD = kDH + 4;   // k-contiguous tiles (Q, K, S / Pd rows): conflict-free 128-bit reads
 constexpr int kLDV = kDH + 8;  // V rows, read one column per lane
 
+// v_mfma_f32_16x16x4f32 fragments: A (16 x 4) lane l holds A[l % 16][l / 16], B (4 x 16)
+// lane l holds B[l / 16][l % 16], the accumulator lane l register r holds
+// D[4 (l / 16) + r][l % 16]. A lane's float4 of k-contiguous operand values feeds four
+// consecutive instructions (k = kb + 4 (l / 16) + step), A and B permuted alike.
+__device__ __forceinline__ f32x4 mfma16(const f32x4& a, const f32x4& b, f32x4 c) {
+#pragma unroll
+  for (int s = 0; s < 4; ++s) c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], b[s], c, 0, 0, 0);
+  return c;
+}
+
+// Block -> (batch x head, row block). The dispatcher gives a CU the blocks j and j + 32 of
+// its XCD (32 CUs each), so the second half of each XCD's blocks walks the row blocks in
+// reverse: a CU then holds a long row block (near the end of the sequence, all keys) and
+// a short one, instead of two of the same length. The row blocks of one head stay on one
+// XCD, whose L2 holds their common K and V.
+template <int NRB>
+__device__ __forceinline__ void row_block(uint32_t bid, uint32_t nblk, int& bh, int& rb) {
+  const uint32_t L = gd::xcd_order(bid, nblk);
+  const uint32_t G = nblk % gd::kXcds == 0 ? nblk / gd::kXcds : nblk;   // blocks per XCD (in L order)
+  if (G % (2 * NRB) != 0) {
+    bh = (int)(L / NRB);
+    rb = (int)(L % NRB);
+    return;
+  }
+  const uint32_t x = L / G, j = L % G, half = G / 2;
+  if (j < half) {
+    bh = (int)(x * (G / NRB) + j / NRB);
+    rb = (int)(j % NRB);
+  } else {
+    bh = (int)(x * (G / NRB) + half / NRB + (j - half) / NRB);
+    rb = NRB - 1 - (int)((j - half) % NRB);
+  }
+}
+
 // Forward, per (batch, head) and block of kQBF query rows. LDS holds two regions: A takes
-// the Q tile, then S2 / Pd, then the O stage-1 partials; B takes K, then V (read into
-// registers with Q and K, written once every wave has finished with K). At 54 KiB a CU
-// runs three blocks, so one block's loads and stores overlap another's arithmetic. The
-// blocks of one (batch, head) share an XCD (and its L2) for their common K and V.
-template <int T, int QB>
+// the Q tile, then S2 / Pd; B takes K, then V (read into registers with Q and K, written
+// once every wave has finished with K). At 54 KiB a CU runs two or three blocks.
+template <int T>
 __global__ __launch_bounds__(kNT) void k_attn_fwd(const AttnDesc a) {
+  constexpr int QB = kQBF;
   constexpr int LDS_ = T + 4;
   constexpr int RA = (QB * kLD > QB * LDS_ ? QB * kLD : QB * LDS_);
   constexpr int RB = (T * kLD > T * kLDV ? T * kLD : T * kLDV);
-  __shared__ __attribute__((aligned(16))) float RegA[RA];   // Q, then S2 / Pd, then O stage-1 partials
+  __shared__ __attribute__((aligned(16))) float RegA[RA];   // Q, then S2 / Pd
   __shared__ __attribute__((aligned(16))) float RegB[RB];   // K, then V
   float* Qs = RegA;
   float* Ss = RegA;
@@ -43,12 +75,13 @@ __global__ __launch_bounds__(kNT) void k_attn_fwd(const AttnDesc a) {
   float* Vs = RegB;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int lrow = lane & 31, h = lane >> 5;
+  const int l16 = lane & 15, g4 = lane >> 4;
   constexpr int NRB = T / QB;
-  const uint32_t L = gd::xcd_order(blockIdx.x, gridDim.x);
-  const int bh = L / NRB, rb = L % NRB;
+  int bh, rb;
+  row_block<NRB>(blockIdx.x, gridDim.x, bh, rb);
   const int b = bh / a.H, hd = bh % a.H;
   const int i0 = rb * QB;
+  const int nk = i0 + QB;   // keys this block needs
 
   constexpr int QC = QB * kDH / 4 / kNT, KC = T * kDH / 4 / kNT;
   static_assert(QC >= 1 && QB * kDH / 4 % kNT == 0, "Q tile is whole load rounds");
@@ -66,8 +99,10 @@ __global__ __launch_bounds__(kNT) void k_attn_fwd(const AttnDesc a) {
 #pragma unroll
     for (int u = 0; u < KC; ++u) {
       const int c = u * kNT + tid, row = c / (kDH / 4), c4 = c % (kDH / 4);
-      kv[u] = *reinterpret_cast<const f32x4*>(k + (int64_t)row * a.skj + c4 * 4);
-      vv[u] = *reinterpret_cast<const f32x4*>(v + (int64_t)row * a.svj + c4 * 4);
+      if (row < nk) {
+        kv[u] = *reinterpret_cast<const f32x4*>(k + (int64_t)row * a.skj + c4 * 4);
+        vv[u] = *reinterpret_cast<const f32x4*>(v + (int64_t)row * a.svj + c4 * 4);
+      }
     }
 #pragma unroll
     for (int u = 0; u < QC; ++u) {
@@ -77,219 +112,194 @@ __global__ __launch_bounds__(kNT) void k_attn_fwd(const AttnDesc a) {
 #pragma unroll
     for (int u = 0; u < KC; ++u) {
       const int c = u * kNT + tid, row = c / (kDH / 4), c4 = c % (kDH / 4);
-      *reinterpret_cast<f32x4*>(Ks + row * kLD + c4 * 4) = kv[u];
+      if (row < nk) *reinterpret_cast<f32x4*>(Ks + row * kLD + c4 * 4) = kv[u];
     }
   }
   __syncthreads();
 
-  constexpr int NTILE = (QB / 32) * (T / 32);
-  static_assert(NTILE <= kNT / 64, "one S tile per wavefront");
-  const int wm = (wave / (T / 32)) * 32, wn = (wave % (T / 32)) * 32;
-  f32x16 sacc;
+  // S = Q K^T on 16 x 16 tiles: tile t = (m-tile t % 2, key tile t / 2), wave w takes t = w,
+  // w + 8, ... of the nk / 8 tiles; k in two blocks of 32 added once (blocked accumulation)
+  constexpr int MAXT = (QB / 16) * (T / 16) / (kNT / 64);
+  f32x4 sacc[MAXT];
+  const int ntile = (QB / 16) * (nk / 16);
 #pragma unroll
-  for (int r = 0; r < 16; ++r) sacc[r] = 0.0f;
-  if (wave < NTILE) {
+  for (int u = 0; u < MAXT; ++u) {
+    const int t = wave + u * (kNT / 64);
 #pragma unroll
-    for (int s = 0; s < kDH / 32; ++s) {
-      f32x16 part;
+    for (int r = 0; r < 4; ++r) sacc[u][r] = 0.0f;
+    if (t < ntile) {
+      const int m0 = (t % (QB / 16)) * 16, n0 = (t / (QB / 16)) * 16;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) part[r] = 0.0f;
+      for (int s = 0; s < kDH / 32; ++s) {
+        f32x4 part = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int kb = s * 32 + g * 8 + h * 4;
-        const f32x4 av = *reinterpret_cast<const f32x4*>(Qs + (wm + lrow) * kLD + kb);
-        const f32x4 bv = *reinterpret_cast<const f32x4*>(Ks + (wn + lrow) * kLD + kb);
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) part = __builtin_amdgcn_mfma_f32_32x32x2f32(av[jj], bv[jj], part, 0, 0, 0);
+        for (int kq = 0; kq < 2; ++kq) {
+          const int kb = s * 32 + kq * 16 + g4 * 4;
+          const f32x4 av = *reinterpret_cast<const f32x4*>(Qs + (m0 + l16) * kLD + kb);
+          const f32x4 bv = *reinterpret_cast<const f32x4*>(Ks + (n0 + l16) * kLD + kb);
+          part = mfma16(av, bv, part);
+        }
+        sacc[u] += part;
       }
-      sacc += part;
     }
   }
   __syncthreads();   // every read of Q and K is done: their regions take S2 and V
-  if (wave < NTILE) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int row = wm + (r / 4) * 8 + h * 4 + (r % 4), col = wn + lrow;
-      const unsigned x = fbits(sacc[r]);
-      Ss[row * LDS_ + col] =
-          a.has_scale ? bitsf(op_eval(FO_MULS, x, 0u, DT_F32, DT_F32, DT_F32, a.scale, 0.0, 0u, 0u, 0u)) : bitsf(x);
+  for (int u = 0; u < MAXT; ++u) {
+    const int t = wave + u * (kNT / 64);
+    if (t < ntile) {
+      const int m0 = (t % (QB / 16)) * 16, n0 = (t / (QB / 16)) * 16;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const unsigned x = fbits(sacc[u][r]);
+        Ss[(m0 + g4 * 4 + r) * LDS_ + n0 + l16] =
+            a.has_scale ? bitsf(op_eval(FO_MULS, x, 0u, DT_F32, DT_F32, DT_F32, a.scale, 0.0, 0u, 0u, 0u)) : bitsf(x);
+      }
     }
   }
 #pragma unroll
   for (int u = 0; u < KC; ++u) {
     const int c = u * kNT + tid, row = c / (kDH / 4), c4 = c % (kDH / 4);
-    *reinterpret_cast<f32x4*>(Vs + row * kLDV + c4 * 4) = vv[u];
+    if (row < nk) *reinterpret_cast<f32x4*>(Vs + row * kLDV + c4 * 4) = vv[u];
   }
   __syncthreads();
 
+  // Rows: wave w takes rows w * RPW .. + RPW, all in flight; lane l holds columns l + 64 u.
+  // Columns past the diagonal hold exact zeros in P and Pd (stored for every column < T).
   {
-    constexpr int V = T >= 128 ? 2 : 1;
-    constexpr int RPW = QB / (kNT / 64);   // rows per wavefront
-    constexpr int RW = RPW < 4 ? RPW : 4;  // rows in flight per wavefront
+    constexpr int NU = T / 64;
+    constexpr int RPW = QB / (kNT / 64);
     const unsigned seed = a.seed ? (unsigned)*a.seed : 0u;
-    for (int rr = 0; rr < RPW; rr += RW) {
-      float x[RW][V];
-      bool in_row[RW][V];
-      float mx[RW];
+    // the rows of a wavefront span [i0 + wave * RPW, + RPW): a 64-column chunk past all of
+    // their diagonals is skipped by the whole wavefront (its P / Pd columns are zeros)
+    const int ilw = __builtin_amdgcn_readfirstlane(wave) * RPW;
+    const int nu = min(NU, (i0 + ilw + RPW - 1) / 64 + 1);
+    float x[RPW][NU], mx[RPW];
 #pragma unroll
-      for (int w = 0; w < RW; ++w) {
-        const int il = wave * RPW + rr + w, i = i0 + il;
-        mx[w] = bitsf(0xff800000u);
+    for (int w = 0; w < RPW; ++w) {
+      const int il = ilw + w, i = i0 + il;
+      mx[w] = bitsf(0xff800000u);
 #pragma unroll
-        for (int u = 0; u < V; ++u) {
-          x[w][u] = Ss[il * LDS_ + lane * V + u];
-          in_row[w][u] = lane * V + u <= i;
-          if (in_row[w][u]) mx[w] = fmaxf(mx[w], x[w][u]);
+      for (int u = 0; u < NU; ++u) {
+        const int col = lane + 64 * u;
+        x[w][u] = 0.0f;
+        if (u < nu && col <= i) {
+          x[w][u] = Ss[il * LDS_ + col];
+          mx[w] = fmaxf(mx[w], x[w][u]);
         }
       }
+    }
 #pragma unroll
-      for (int w = 0; w < RW; ++w) mx[w] = wave_allmax(mx[w]);
-      double ex[RW][V], sum[RW];
+    for (int w = 0; w < RPW; ++w) mx[w] = wave_allmax(mx[w]);
+    float ex[RPW][NU];
+    double sum[RPW];
 #pragma unroll
-      for (int w = 0; w < RW; ++w) {
-        sum[w] = 0.0;
+    for (int w = 0; w < RPW; ++w) {
+      const int i = i0 + ilw + w;
+      sum[w] = 0.0;
 #pragma unroll
-        for (int u = 0; u < V; ++u) {
-          ex[w][u] = in_row[w][u] ? exp((double)x[w][u] - (double)mx[w]) : 0.0;
-          if (in_row[w][u]) sum[w] += ex[w][u];
-        }
+      for (int u = 0; u < NU; ++u) {
+        const int col = lane + 64 * u;
+        ex[w][u] = 0.0f;
+        if (u < nu && col <= i) ex[w][u] = expf(x[w][u] - mx[w]);
+        sum[w] += (double)ex[w][u];
       }
+    }
 #pragma unroll
-      for (int w = 0; w < RW; ++w) sum[w] = wave_allsum(sum[w]);
+    for (int w = 0; w < RPW; ++w) sum[w] = wave_allsum(sum[w]);
 #pragma unroll
-      for (int w = 0; w < RW; ++w) {
-        const int il = wave * RPW + rr + w, i = i0 + il;
-        const int64_t rflat = (int64_t)bh * T + i;
-        unsigned pv[V], dv[V];
+    for (int w = 0; w < RPW; ++w) {
+      const int il = ilw + w, i = i0 + il;
+      const int64_t rflat = (int64_t)bh * T + i;
+      const double rs = 1.0 / sum[w];
+      unsigned* P = reinterpret_cast<unsigned*>(a.p) + rflat * T;
+      unsigned* PD = a.pd ? reinterpret_cast<unsigned*>(a.pd) + rflat * T : nullptr;
 #pragma unroll
-        for (int u = 0; u < V; ++u) {
-          pv[u] = in_row[w][u] ? fbits((float)(ex[w][u] / sum[w])) : 0u;
-          dv[u] = a.has_dropout ? dropout_bits(pv[u], seed, a.salt, a.drop_p, a.drop_scale,
-                                               (unsigned)(rflat * T + lane * V + u))
-                                : pv[u];
+      for (int u = 0; u < NU; ++u) {
+        const int col = lane + 64 * u;
+        unsigned pv = 0u, dv = 0u;
+        if (u < nu && col <= i) {
+          pv = fbits((float)((double)ex[w][u] * rs));
+          dv = a.has_dropout ? dropout_bits(pv, seed, a.salt, a.drop_p, a.drop_scale, (unsigned)(rflat * T + col)) : pv;
         }
-        unsigned* P = reinterpret_cast<unsigned*>(a.p) + rflat * T + lane * V;
-        unsigned* PD = a.pd ? reinterpret_cast<unsigned*>(a.pd) + rflat * T + lane * V : nullptr;
-        if (V == 2) {
-          typedef unsigned u2 __attribute__((ext_vector_type(2)));
-          *reinterpret_cast<u2*>(P) = (u2){pv[0], pv[V - 1]};
-          if (PD) *reinterpret_cast<u2*>(PD) = (u2){dv[0], dv[V - 1]};
-        } else {
-          P[0] = pv[0];
-          if (PD) PD[0] = dv[0];
-        }
-#pragma unroll
-        for (int u = 0; u < V; ++u) Ss[il * LDS_ + lane * V + u] = bitsf(dv[u]);
+        P[col] = pv;
+        if (PD) PD[col] = dv;
+        if (col < nk) Ss[il * LDS_ + col] = bitsf(dv);
       }
     }
   }
   __syncthreads();
 
+  // O = Pd V: 16 x 16 tiles, one per wavefront (m-tile w / 4, d-tile w % 4), k over the
+  // nk keys in blocks of 64 added once
   {
-    constexpr int NS = T / 64;
-    constexpr int NTO = (QB / 32) * (kDH / 32);
-    static_assert(NTO * NS <= kNT / 64, "one O tile stage per wavefront");
-    const int tile = wave % NTO, s = wave / NTO;
-    const int om = (tile / (kDH / 32)) * 32, on = (tile % (kDH / 32)) * 32;
-    f32x16 part;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) part[r] = 0.0f;
-    if (s < NS) {
-#pragma unroll
-      for (int g = 0; g < 8; ++g) {
-        const int kb = s * 64 + g * 8 + h * 4;
-        const f32x4 av = *reinterpret_cast<const f32x4*>(Ss + (om + lrow) * LDS_ + kb);
+    static_assert((QB / 16) * (kDH / 16) == kNT / 64, "one O tile per wavefront");
+    const int m0 = (wave / (kDH / 16)) * 16, n0 = (wave % (kDH / 16)) * 16;
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int kb0 = 0; kb0 < nk; kb0 += 64) {
+      f32x4 part = {0.0f, 0.0f, 0.0f, 0.0f};
+      const int kend = min(nk, kb0 + 64);
+      for (int kq = kb0; kq < kend; kq += 16) {
+        const int kb = kq + g4 * 4;
+        const f32x4 av = *reinterpret_cast<const f32x4*>(Ss + (m0 + l16) * LDS_ + kb);
         f32x4 bv;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) bv[u] = Vs[(kb + u) * kLDV + on + lrow];
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) part = __builtin_amdgcn_mfma_f32_32x32x2f32(av[jj], bv[jj], part, 0, 0, 0);
+        for (int s = 0; s < 4; ++s) bv[s] = Vs[(kb + s) * kLDV + n0 + l16];
+        part = mfma16(av, bv, part);
       }
+      acc += part;
     }
-    if (NS == 2) {
-      __syncthreads();   // every read of Pd is done: region A takes the stage-1 partials
-      float* Xs = RegA;
-      static_assert(NTO * 16 * 64 <= RA, "exchange fits region A");
-      if (s == 1)
+    float* o = a.o + b * a.sob + hd * a.soh;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) Xs[(tile * 16 + r) * 64 + lane] = part[r];
-      __syncthreads();
-      if (s == 0)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) part[r] = (0.0f + part[r]) + Xs[(tile * 16 + r) * 64 + lane];
-    } else if (s == 0) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) part[r] = 0.0f + part[r];
-    }
-    if (s == 0) {
-      float* o = a.o + b * a.sob + hd * a.soh;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = om + (r / 4) * 8 + h * 4 + (r % 4);
-        o[(int64_t)(i0 + row) * a.soi + on + lrow] = part[r];
-      }
-    }
+    for (int r = 0; r < 4; ++r) o[(int64_t)(i0 + m0 + g4 * 4 + r) * a.soi + n0 + l16] = acc[r];
   }
 }
 
 
-// One 32 x 32 tile, one 64-k stage of a product whose operands are read one column per
-// lane from LDS row-major tiles: out(m, n) = sum_k A[k][m] B[k][n] (A rows at a0 + k * lda,
-// B rows at b0 + k * ldb), k = 64 s + 8 g + 4 h + jj in the k_gemm order.
-__device__ __forceinline__ f32x16 stage_cols(const float* a0, int lda, const float* b0, int ldb, int s, int lrow,
-                                             int h) {
-  f32x16 part;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) part[r] = 0.0f;
-#pragma unroll
-  for (int g = 0; g < 8; ++g) {
-    const int kb = s * 64 + g * 8 + h * 4;
-    f32x4 av, bv;
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      av[u] = a0[(kb + u) * lda + lrow];
-      bv[u] = b0[(kb + u) * ldb + lrow];
-    }
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj) part = __builtin_amdgcn_mfma_f32_32x32x2f32(av[jj], bv[jj], part, 0, 0, 0);
-  }
-  return part;
-}
-
-// Backward, kernel A (per kQBF query rows): dPd = dO V^T, the dropout and softmax
-// backward row math giving dS (written out), and dQ = dS K. LDS as in the forward:
-// region A takes dO, then dPd / dS, then the dQ stage-1 partials; region B takes V, then
-// K (read into registers at the start with this block's P rows). 54 KiB: three blocks a CU.
-template <int T, int QB>
+// Backward, kernel A (per kQBF query rows [i0, i0 + 32), keys [0, i0 + 32)): dPd = dO V^T,
+// the dropout and softmax backward row math giving dS (written for those keys, the only
+// ones kernel B reads), and dQ = dS K. LDS as in the forward: region A takes dO, then
+// dS; region B takes V, then K (read into registers at the start with this block's P and
+// Pd rows). The dropout mask comes from the stored Pd: where P > 0, the forward kept an
+// element exactly when Pd != 0, and where P = 0 the mask changes no result.
+template <int T>
 __global__ __launch_bounds__(kNT) void k_attn_bwd_a(const AttnBwdDesc a) {
+  constexpr int QB = kQBF;
   constexpr int LDS_ = T + 4;
   constexpr int RA = (QB * kLD > QB * LDS_ ? QB * kLD : QB * LDS_);
   constexpr int RB = (T * kLD > T * kLDV ? T * kLD : T * kLDV);
   __shared__ __attribute__((aligned(16))) float RegA[RA];
   __shared__ __attribute__((aligned(16))) float RegB[RB];
   float* Os = RegA;   // dO rows
-  float* Ss = RegA;   // dPd, then dS
+  float* Ss = RegA;   // dS
   float* Vs = RegB;
   float* Ks = RegB;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int lrow = lane & 31, h = lane >> 5;
+  const int l16 = lane & 15, g4 = lane >> 4;
   constexpr int NRB = T / QB;
-  const uint32_t L = gd::xcd_order(blockIdx.x, gridDim.x);
-  const int bh = L / NRB, rb = L % NRB;
+  int bh, rb;
+  row_block<NRB>(blockIdx.x, gridDim.x, bh, rb);
   const int b = bh / a.H, hd = bh % a.H;
-  const int i0 = rb * QB;
-  constexpr int V = T >= 128 ? 2 : 1;
+  const int i0 = rb * QB, nk = i0 + QB;
+  constexpr int NU = T / 64;
   constexpr int RPW = QB / (kNT / 64);   // rows per wavefront in the row math
-  static_assert(RPW >= 1 && RPW <= 4, "the row math keeps every row of a wavefront in flight");
+  const int ilw = __builtin_amdgcn_readfirstlane(wave) * RPW;
+  const int nu = min(NU, (nk + 63) / 64);   // 64-column chunks holding keys < nk
 
-  // P of this wavefront's rows, dO, V and K: every load in flight before the LDS writes
-  unsigned pv[RPW][V];
+  // P and Pd of this wavefront's rows, dO, V and K: every load in flight before the LDS writes
+  unsigned pv[RPW][NU], dv0[RPW][NU];
 #pragma unroll
   for (int w = 0; w < RPW; ++w) {
-    const int64_t rflat = (int64_t)bh * T + i0 + wave * RPW + w;
+    const int64_t rflat = (int64_t)bh * T + i0 + ilw + w;
 #pragma unroll
-    for (int u = 0; u < V; ++u) pv[w][u] = reinterpret_cast<const unsigned*>(a.p)[rflat * T + lane * V + u];
+    for (int u = 0; u < NU; ++u) {
+      pv[w][u] = dv0[w][u] = 0u;
+      if (u < nu) {
+        pv[w][u] = reinterpret_cast<const unsigned*>(a.p)[rflat * T + lane + 64 * u];
+        dv0[w][u] = reinterpret_cast<const unsigned*>(a.pd)[rflat * T + lane + 64 * u];
+      }
+    }
   }
   constexpr int QC = QB * kDH / 4 / kNT, KC = T * kDH / 4 / kNT;
   static_assert(QC >= 1 && QB * kDH / 4 % kNT == 0, "dO tile is whole load rounds");
@@ -307,8 +317,10 @@ __global__ __launch_bounds__(kNT) void k_attn_bwd_a(const AttnBwdDesc a) {
 #pragma unroll
     for (int u = 0; u < KC; ++u) {
       const int c = u * kNT + tid, row = c / (kDH / 4), c4 = c % (kDH / 4);
-      vv[u] = *reinterpret_cast<const f32x4*>(v + (int64_t)row * a.svj + c4 * 4);
-      kk[u] = *reinterpret_cast<const f32x4*>(k + (int64_t)row * a.skj + c4 * 4);
+      if (row < nk) {
+        vv[u] = *reinterpret_cast<const f32x4*>(v + (int64_t)row * a.svj + c4 * 4);
+        kk[u] = *reinterpret_cast<const f32x4*>(k + (int64_t)row * a.skj + c4 * 4);
+      }
     }
 #pragma unroll
     for (int u = 0; u < QC; ++u) {
@@ -318,236 +330,212 @@ __global__ __launch_bounds__(kNT) void k_attn_bwd_a(const AttnBwdDesc a) {
 #pragma unroll
     for (int u = 0; u < KC; ++u) {
       const int c = u * kNT + tid, row = c / (kDH / 4), c4 = c % (kDH / 4);
-      *reinterpret_cast<f32x4*>(Vs + row * kLD + c4 * 4) = vv[u];
+      if (row < nk) *reinterpret_cast<f32x4*>(Vs + row * kLD + c4 * 4) = vv[u];
     }
   }
   __syncthreads();
 
-  // dPd = dO V^T (the QK^T kernel's tiles and k-blocking), one tile per wavefront
-  constexpr int NTILE = (QB / 32) * (T / 32);
-  static_assert(NTILE <= kNT / 64, "one dPd tile per wavefront");
-  const int wm = (wave / (T / 32)) * 32, wn = (wave % (T / 32)) * 32;
-  f32x16 pacc;
+  // dPd = dO V^T on 16 x 16 tiles (the forward's S tiling)
+  constexpr int MAXT = (QB / 16) * (T / 16) / (kNT / 64);
+  f32x4 pacc[MAXT];
+  const int ntile = (QB / 16) * (nk / 16);
 #pragma unroll
-  for (int r = 0; r < 16; ++r) pacc[r] = 0.0f;
-  if (wave < NTILE) {
+  for (int u = 0; u < MAXT; ++u) {
+    const int t = wave + u * (kNT / 64);
 #pragma unroll
-    for (int s = 0; s < kDH / 32; ++s) {
-      f32x16 part;
+    for (int r = 0; r < 4; ++r) pacc[u][r] = 0.0f;
+    if (t < ntile) {
+      const int m0 = (t % (QB / 16)) * 16, n0 = (t / (QB / 16)) * 16;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) part[r] = 0.0f;
+      for (int s = 0; s < kDH / 32; ++s) {
+        f32x4 part = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int kb = s * 32 + g * 8 + h * 4;
-        const f32x4 av = *reinterpret_cast<const f32x4*>(Os + (wm + lrow) * kLD + kb);
-        const f32x4 bv = *reinterpret_cast<const f32x4*>(Vs + (wn + lrow) * kLD + kb);
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) part = __builtin_amdgcn_mfma_f32_32x32x2f32(av[jj], bv[jj], part, 0, 0, 0);
+        for (int kq = 0; kq < 2; ++kq) {
+          const int kb = s * 32 + kq * 16 + g4 * 4;
+          const f32x4 av = *reinterpret_cast<const f32x4*>(Os + (m0 + l16) * kLD + kb);
+          const f32x4 bv = *reinterpret_cast<const f32x4*>(Vs + (n0 + l16) * kLD + kb);
+          part = mfma16(av, bv, part);
+        }
+        pacc[u] += part;
       }
-      pacc += part;
     }
   }
   __syncthreads();   // every read of dO and V is done: their regions take dPd and K
-  if (wave < NTILE)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) Ss[(wm + (r / 4) * 8 + h * 4 + (r % 4)) * LDS_ + wn + lrow] = pacc[r];
+  for (int u = 0; u < MAXT; ++u) {
+    const int t = wave + u * (kNT / 64);
+    if (t < ntile) {
+      const int m0 = (t % (QB / 16)) * 16, n0 = (t / (QB / 16)) * 16;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) Ss[(m0 + g4 * 4 + r) * LDS_ + n0 + l16] = pacc[u][r];
+    }
+  }
 #pragma unroll
   for (int u = 0; u < KC; ++u) {
     const int c = u * kNT + tid, row = c / (kDH / 4), c4 = c % (kDH / 4);
-    *reinterpret_cast<f32x4*>(Ks + row * kLDV + c4 * 4) = kk[u];
+    if (row < nk) *reinterpret_cast<f32x4*>(Ks + row * kLDV + c4 * 4) = kk[u];
   }
   __syncthreads();
 
-  // dS rows: v0 = dropout(dPd), v1 = v0 * P, s = f32(rowsum v1) (f64, lanes then
-  // butterfly), dS = f32((v0 - s) * P * scale): the row-fused group's arithmetic and lanes.
+  // dS rows: v0 = dropout(dPd), s = f32(rowsum f32(v0 * P)) (f64 sum), dS = f32((v0 - s) * P)
+  // [* scale]: the row-fused group's arithmetic, over the keys < nk (P is zero past the
+  // diagonal: those dS are +-0 and nothing reads them beyond nk)
   {
-    const unsigned seed = a.seed ? (unsigned)*a.seed : 0u;
-    unsigned v0[RPW][V];
+    unsigned v0[RPW][NU];
     double sum[RPW];
 #pragma unroll
     for (int w = 0; w < RPW; ++w) {
-      const int il = wave * RPW + w;
-      const int64_t rflat = (int64_t)bh * T + i0 + il;
+      const int il = ilw + w;
       sum[w] = 0.0;
 #pragma unroll
-      for (int u = 0; u < V; ++u) {
-        const unsigned x = fbits(Ss[il * LDS_ + lane * V + u]);
-        v0[w][u] = a.has_dropout ? dropout_bits(x, seed, a.salt, a.drop_p, a.drop_scale,
-                                                (unsigned)(rflat * T + lane * V + u))
-                                 : x;
-        sum[w] += (double)(bitsf(v0[w][u]) * bitsf(pv[w][u]));
+      for (int u = 0; u < NU; ++u) {
+        const int col = lane + 64 * u;
+        v0[w][u] = 0u;
+        if (u < nu && col < nk) {
+          const unsigned x = fbits(Ss[il * LDS_ + col]);
+          v0[w][u] = a.has_dropout ? fbits((float)((double)bitsf(x) * (dv0[w][u] != 0u ? a.drop_scale : 0.0))) : x;
+          sum[w] += (double)(bitsf(v0[w][u]) * bitsf(pv[w][u]));
+        }
       }
     }
 #pragma unroll
     for (int w = 0; w < RPW; ++w) sum[w] = wave_allsum(sum[w]);
 #pragma unroll
     for (int w = 0; w < RPW; ++w) {
-      const int il = wave * RPW + w;
+      const int il = ilw + w;
       const int64_t rflat = (int64_t)bh * T + i0 + il;
       const float sf = (float)(sum[w] / 1.0);
-      unsigned dv[V];
+      unsigned* D = reinterpret_cast<unsigned*>(a.ds) + rflat * T;
 #pragma unroll
-      for (int u = 0; u < V; ++u) {
-        const unsigned t = fbits((bitsf(v0[w][u]) - sf) * bitsf(pv[w][u]));
-        dv[u] = a.has_scale ? op_eval(FO_MULS, t, 0u, DT_F32, DT_F32, DT_F32, a.scale, 0.0, 0u, 0u, 0u) : t;
-        Ss[il * LDS_ + lane * V + u] = bitsf(dv[u]);
-      }
-      unsigned* D = reinterpret_cast<unsigned*>(a.ds) + rflat * T + lane * V;
-      if (V == 2) {
-        typedef unsigned u2 __attribute__((ext_vector_type(2)));
-        *reinterpret_cast<u2*>(D) = (u2){dv[0], dv[V - 1]};
-      } else {
-        D[0] = dv[0];
+      for (int u = 0; u < NU; ++u) {
+        const int col = lane + 64 * u;
+        if (u < nu && col < nk) {
+          const unsigned t = fbits((bitsf(v0[w][u]) - sf) * bitsf(pv[w][u]));
+          const unsigned d = a.has_scale ? op_eval(FO_MULS, t, 0u, DT_F32, DT_F32, DT_F32, a.scale, 0.0, 0u, 0u, 0u) : t;
+          Ss[il * LDS_ + col] = bitsf(d);
+          D[col] = d;
+        }
       }
     }
   }
   __syncthreads();
 
-  // dQ = dS K (the PV kernel's tiles and k-blocking); the stage-1 partials go through
-  // region A once every wave has finished reading dS
+  // dQ = dS K: 16 x 16 tiles, one per wavefront, k over the nk keys in blocks of 64
   {
-    constexpr int NS = T / 64;
-    constexpr int NTO = (QB / 32) * (kDH / 32);
-    static_assert(NTO * NS <= kNT / 64, "one dQ tile stage per wavefront");
-    const int tile = wave % NTO, s = wave / NTO;
-    const int om = (tile / (kDH / 32)) * 32, on = (tile % (kDH / 32)) * 32;
-    f32x16 part;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) part[r] = 0.0f;
-    if (s < NS) {
-#pragma unroll
-      for (int g = 0; g < 8; ++g) {
-        const int kb = s * 64 + g * 8 + h * 4;
-        const f32x4 av = *reinterpret_cast<const f32x4*>(Ss + (om + lrow) * LDS_ + kb);
+    const int m0 = (wave / (kDH / 16)) * 16, n0 = (wave % (kDH / 16)) * 16;
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int kb0 = 0; kb0 < nk; kb0 += 64) {
+      f32x4 part = {0.0f, 0.0f, 0.0f, 0.0f};
+      const int kend = min(nk, kb0 + 64);
+      for (int kq = kb0; kq < kend; kq += 16) {
+        const int kb = kq + g4 * 4;
+        const f32x4 av = *reinterpret_cast<const f32x4*>(Ss + (m0 + l16) * LDS_ + kb);
         f32x4 bv;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) bv[u] = Ks[(kb + u) * kLDV + on + lrow];
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) part = __builtin_amdgcn_mfma_f32_32x32x2f32(av[jj], bv[jj], part, 0, 0, 0);
+        for (int s = 0; s < 4; ++s) bv[s] = Ks[(kb + s) * kLDV + n0 + l16];
+        part = mfma16(av, bv, part);
       }
+      acc += part;
     }
-    if (NS == 2) {
-      __syncthreads();
-      float* Xs = RegA;
-      static_assert(NTO * 16 * 64 <= RA, "exchange fits region A");
-      if (s == 1)
+    float* o = a.dq + b * a.sdqb + hd * a.sdqh;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) Xs[(tile * 16 + r) * 64 + lane] = part[r];
-      __syncthreads();
-      if (s == 0)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) part[r] = (0.0f + part[r]) + Xs[(tile * 16 + r) * 64 + lane];
-    } else if (s == 0) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) part[r] = 0.0f + part[r];
-    }
-    if (s == 0) {
-      float* o = a.dq + b * a.sdqb + hd * a.sdqh;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[(int64_t)(i0 + om + (r / 4) * 8 + h * 4 + (r % 4)) * a.sdqi + on + lrow] = part[r];
-    }
+    for (int r = 0; r < 4; ++r) o[(int64_t)(i0 + m0 + g4 * 4 + r) * a.sdqi + n0 + l16] = acc[r];
   }
 }
 
-// Rows [0, R) of a COLS-wide slice (row stride rs, 16-byte aligned rows) into registers,
-// every load in flight at once; store_slice writes them to LDS rows of `ld` floats.
+// Rows [i0, R) of a COLS-wide slice (row stride rs, 16-byte aligned rows) into registers,
+// every load in flight at once; store_t writes them transposed to LDS (column c of the
+// slice becomes row c, row i column i - i0 of a row length `ld`).
 template <int R, int COLS>
-struct Slice {
+struct SliceT {
   static constexpr int C = R * COLS / 4 / kNT;
   static_assert(C >= 1 && R * COLS / 4 % kNT == 0, "slice is whole load rounds");
   f32x4 v[C];
-  __device__ __forceinline__ void load(const float* src, int64_t rs, int tid) {
+  __device__ __forceinline__ void load(const float* src, int64_t rs, int i0, int tid) {
 #pragma unroll
     for (int u = 0; u < C; ++u) {
       const int c = u * kNT + tid, row = c / (COLS / 4), c4 = c % (COLS / 4);
-      v[u] = *reinterpret_cast<const f32x4*>(src + (int64_t)row * rs + c4 * 4);
+      if (row >= i0) v[u] = *reinterpret_cast<const f32x4*>(src + (int64_t)row * rs + c4 * 4);
     }
   }
-  __device__ __forceinline__ void store(float* dst, int ld, int tid) const {
+  __device__ __forceinline__ void store_t(float* dst, int ld, int i0, int tid) const {
 #pragma unroll
     for (int u = 0; u < C; ++u) {
       const int c = u * kNT + tid, row = c / (COLS / 4), c4 = c % (COLS / 4);
-      *reinterpret_cast<f32x4*>(dst + row * ld + c4 * 4) = v[u];
+      if (row >= i0)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) dst[(c4 * 4 + e) * ld + row - i0] = v[u][e];
     }
   }
 };
 
-// Backward, kernel B (per KB keys): dV = Pd^T dO and dK = dS^T Q over all T query rows,
-// each as two 64-row stages added in order (the unfused GEMMs' blocking). LDS: region 1
-// holds the Pd slice, then the dS slice, region 2 dO, then Q (dS and Q wait in registers
-// while dV is formed); the stage-1 partials pass through region 1. 53 KiB: three blocks a
-// CU, the blocks of one head on one XCD.
-template <int T, int KB>
+// Backward, kernel B (per KB keys [j0, j0 + 32)): dV = Pd^T dO and dK = dS^T Q over the
+// query rows i >= j0 (the causal mask zeroes Pd and dS above the diagonal), 16 x 16 tiles,
+// one per wavefront, k over the rows in blocks of 64. LDS holds the slices transposed (key
+// rows of Pd / dS, head-dimension rows of dO / Q, rows i contiguous): region 1 the Pd
+// slice, then the dS slice; region 2 dO, then Q (dS and Q wait in registers while dV is
+// formed). The row blocks pair long with short on a CU, as in the forward.
+template <int T>
 __global__ __launch_bounds__(kNT) void k_attn_bwd_b(const AttnBwdDesc a) {
-  constexpr int LDK = KB + 4;
-  __shared__ __attribute__((aligned(16))) float Reg1[T * LDK];   // Pd[i][j0 ..], then dS[i][j0 ..]
-  __shared__ __attribute__((aligned(16))) float Reg2[T * kLD];   // dO[i][:], then Q[i][:]
+  constexpr int KB = kQB;
+  constexpr int LDT = T + 4;
+  __shared__ __attribute__((aligned(16))) float Reg1[KB * LDT];    // Pd^T, then dS^T
+  __shared__ __attribute__((aligned(16))) float Reg2[kDH * LDT];   // dO^T, then Q^T
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int lrow = lane & 31, h = lane >> 5;
+  const int l16 = lane & 15, g4 = lane >> 4;
   constexpr int NJB = T / KB;
-  const uint32_t L = gd::xcd_order(blockIdx.x, gridDim.x);
-  const int bh = L / NJB, jb = L % NJB;
+  int bh, rbk;
+  row_block<NJB>(blockIdx.x, gridDim.x, bh, rbk);
+  const int jb = NJB - 1 - rbk;   // row block rb -> key block from the end: long ones pair with short
   const int b = bh / a.H, hd = bh % a.H;
   const int j0 = jb * KB;
+  const int mt = T - j0;          // query rows i in [j0, T)
   const int64_t prow = (int64_t)bh * T * T;
   {
-    Slice<T, KB> pd;
-    Slice<T, kDH> od;
-    pd.load(a.pd + prow + j0, T, tid);
-    od.load(a.dout + b * a.sob + hd * a.soh, a.soi, tid);
-    pd.store(Reg1, LDK, tid);
-    od.store(Reg2, kLD, tid);
+    SliceT<T, KB> pd;
+    SliceT<T, kDH> od;
+    pd.load(a.pd + prow + j0, T, j0, tid);
+    od.load(a.dout + b * a.sob + hd * a.soh, a.soi, j0, tid);
+    pd.store_t(Reg1, LDT, j0, tid);
+    od.store_t(Reg2, LDT, j0, tid);
   }
-  Slice<T, KB> ds;
-  Slice<T, kDH> qq;
-  ds.load(a.ds + prow + j0, T, tid);
-  qq.load(a.q + b * a.sqb + hd * a.sqh, a.sqi, tid);
+  SliceT<T, KB> ds;
+  SliceT<T, kDH> qq;
+  ds.load(a.ds + prow + j0, T, j0, tid);
+  qq.load(a.q + b * a.sqb + hd * a.sqh, a.sqi, j0, tid);
   __syncthreads();
 
-  constexpr int NS = T / 64;
-  constexpr int NTO = (KB / 32) * (kDH / 32);
-  static_assert(NTO * NS <= kNT / 64, "one output tile stage per wavefront");
-  const int tile = wave % NTO, s = wave / NTO;
-  const int wm = (tile / (kDH / 32)) * 32, wn = (tile % (kDH / 32)) * 32;   // rows: keys j0 + wm, cols: d
+  static_assert((KB / 16) * (kDH / 16) == kNT / 64, "one output tile per wavefront");
+  const int m0 = (wave / (kDH / 16)) * 16, n0 = (wave % (kDH / 16)) * 16;   // rows: keys j0 + m0, cols: d
 #pragma unroll
   for (int which = 0; which < 2; ++which) {
     if (which == 1) {
-      __syncthreads();   // dV's reads of region 1 (partials included) are done
-      ds.store(Reg1, LDK, tid);
-      qq.store(Reg2, kLD, tid);
+      __syncthreads();   // dV's reads of both regions are done
+      ds.store_t(Reg1, LDT, j0, tid);
+      qq.store_t(Reg2, LDT, j0, tid);
       __syncthreads();
     }
-    f32x16 part;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) part[r] = 0.0f;
-    if (s < NS) part = stage_cols(Reg1 + wm, LDK, Reg2 + wn, kLD, s, lrow, h);
-    if (NS == 2) {
-      __syncthreads();   // every read of region 1 is done: it takes the stage-1 partials
-      float* Xs = Reg1;
-      static_assert(NTO * 16 * 64 <= T * LDK, "exchange fits region 1");
-      if (s == 1)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) Xs[(tile * 16 + r) * 64 + lane] = part[r];
-      __syncthreads();
-      if (s == 0)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) part[r] = (0.0f + part[r]) + Xs[(tile * 16 + r) * 64 + lane];
-    } else if (s == 0) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) part[r] = 0.0f + part[r];
-    }
-    if (s == 0) {
-      if (which == 0) {
-        float* o = a.dv + b * a.sdvb + hd * a.sdvh;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o[(int64_t)(j0 + wm + (r / 4) * 8 + h * 4 + (r % 4)) * a.sdvj + wn + lrow] = part[r];
-      } else {
-        float* o = a.dk + b * a.sdkb + hd * a.sdkh;
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-          o[(int64_t)(j0 + wm + (r / 4) * 8 + h * 4 + (r % 4)) * a.sdkj + (int64_t)(wn + lrow) * a.sdkd] = part[r];
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int kb0 = 0; kb0 < mt; kb0 += 64) {
+      f32x4 part = {0.0f, 0.0f, 0.0f, 0.0f};
+      const int kend = min(mt, kb0 + 64);
+      for (int kq = kb0; kq < kend; kq += 16) {
+        const int kb = kq + g4 * 4;
+        const f32x4 av = *reinterpret_cast<const f32x4*>(Reg1 + (m0 + l16) * LDT + kb);
+        const f32x4 bv = *reinterpret_cast<const f32x4*>(Reg2 + (n0 + l16) * LDT + kb);
+        part = mfma16(av, bv, part);
       }
+      acc += part;
+    }
+    if (which == 0) {
+      float* o = a.dv + b * a.sdvb + hd * a.sdvh;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o[(int64_t)(j0 + m0 + g4 * 4 + r) * a.sdvj + n0 + l16] = acc[r];
+    } else {
+      float* o = a.dk + b * a.sdkb + hd * a.sdkh;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o[(int64_t)(j0 + m0 + g4 * 4 + r) * a.sdkj + (int64_t)(n0 + l16) * a.sdkd] = acc[r];
     }
   }
 }
@@ -559,8 +547,8 @@ bool attention_supported(int64_t T, int64_t dh) { return dh == kDH && (T == 64 |
 void attention_fwd(const AttnDesc& a, hipStream_t st) {
   const int blocks = a.B * a.H * (a.T / kQBF);
   if (blocks <= 0) return;
-  if (a.T == 128) klaunch(k_attn_fwd<128, kQBF>, blocks, kNT, 0, st, a);
-  else klaunch(k_attn_fwd<64, kQBF>, blocks, kNT, 0, st, a);
+  if (a.T == 128) klaunch(k_attn_fwd<128>, blocks, kNT, 0, st, a);
+  else klaunch(k_attn_fwd<64>, blocks, kNT, 0, st, a);
 }
 
 void attention_bwd(const AttnBwdDesc& a, hipStream_t st) {
@@ -568,11 +556,11 @@ void attention_bwd(const AttnBwdDesc& a, hipStream_t st) {
   if (blocks <= 0) return;
   const int blocks_a = a.B * a.H * (a.T / kQBF);
   if (a.T == 128) {
-    klaunch(k_attn_bwd_a<128, kQBF>, blocks_a, kNT, 0, st, a);
-    klaunch(k_attn_bwd_b<128, kQB>, blocks, kNT, 0, st, a);
+    klaunch(k_attn_bwd_a<128>, blocks_a, kNT, 0, st, a);
+    klaunch(k_attn_bwd_b<128>, blocks, kNT, 0, st, a);
   } else {
-    klaunch(k_attn_bwd_a<64, kQBF>, blocks_a, kNT, 0, st, a);
-    klaunch(k_attn_bwd_b<64, kQB>, blocks, kNT, 0, st, a);
+    klaunch(k_attn_bwd_a<64>, blocks_a, kNT, 0, st, a);
+    klaunch(k_attn_bwd_b<64>, blocks, kNT, 0, st, a);
   }
 }
 

@@ -363,10 +363,10 @@ def _run_native(g, inputs, env=None):
 @pytest.mark.parametrize('what', ['o', 'p', 'pd'])
 def test_fused_attention(B, H, T, what):
     """The fused attention kernel (Q K^T, scale, causal softmax, dropout, P V in one
-    launch) against the oracle (GEMM tolerance: the products run on f32 matrix cores).
-    At the transformer's shape, where the unfused GEMMs take the tiles whose k-blocking the
-    fused kernel follows (QK^T in stages of 32, PV in stages of 64), it must also equal the
-    unfused kernels bit for bit (same MFMA order, same row-softmax arithmetic and lanes)."""
+    launch) against the oracle (GEMM tolerance: the products run on f32 matrix cores; the
+    softmax takes f32 exp with an f64 row sum), and against the unfused kernels (TG_ATTN=0)
+    within the same tolerance. P and Pd hold exact zeros past the diagonal and the same
+    dropout mask as the oracle (the reference's hash on the flat index)."""
     dh = 64
     ins = {n: _rand([B, H, T, dh], s, -2, 2) for n, s in (('q', 61), ('k', 62), ('v', 63))}
     g = trace_fn(_attention_graph(B, H, T, dh, what))
@@ -374,15 +374,18 @@ def test_fused_attention(B, H, T, what):
     assert 'attention' in kinds
     ref, kinds0 = _run_native(g, ins, {'TG_ATTN': '0'})
     assert 'attention' not in kinds0
-    if B * H == 128 and T == 128:
-        exact(got, ref)
     o = pyoracle.OracleRuntime(wire(g))
     o.run(ins)
     want = o.output()
     if what == 'o':
         gemm_close(got, want)
+        gemm_close(got, ref)
     else:
-        assert np.allclose(got, want, rtol=1e-5, atol=1e-7), np.max(np.abs(got.astype(np.float64) - want))
+        for r in (want, ref):
+            assert np.allclose(got, r, rtol=1e-5, atol=1e-7), np.max(np.abs(got.astype(np.float64) - r))
+        g4 = got.reshape(B, H, T, T)
+        assert np.all(g4[..., np.triu_indices(T, 1)[0], np.triu_indices(T, 1)[1]] == 0)
+        assert np.array_equal(got.reshape(-1) == 0, np.asarray(want).reshape(-1) == 0)
 
 
 def _attention_grad(B, H, T, dh, which, params, g_in, env=None):
@@ -419,8 +422,7 @@ def _attention_grad(B, H, T, dh, which, params, g_in, env=None):
 def test_fused_attention_backward(B, H, T):
     """The fused attention backward (dPd = dO V^T, dropout and softmax backward row math,
     dQ = dS K, dK = dS^T Q, dV = Pd^T dO in two launches) for the gradients of q, k and v,
-    against the oracle (GEMM tolerance) and, at the transformer's shape, bit for bit against
-    the unfused kernels, whose tiles use the k-blocking the fused kernels follow."""
+    against the oracle and the unfused kernels (TG_ATTN=0), GEMM tolerance."""
     dh = 64
     params = {n: _rand([B, H, T, dh], s, -2, 2) for n, s in (('q', 71), ('k', 72), ('v', 73))}
     g_in = _rand([B, H, T, dh], 74)
@@ -429,8 +431,7 @@ def test_fused_attention_backward(B, H, T):
         assert 'attention_backward' in ops
         ref, ops0, _ = _attention_grad(B, H, T, dh, which, params, g_in, {'TG_ATTN': '0'})
         assert 'attention_backward' not in ops0
-        if B * H == 128 and T == 128:
-            exact(got, ref)
+        gemm_close(got, ref, 1e-5)
         o = pyoracle.OracleRuntime(w)
         for k, v in params.items():
             o.set_home(k, v)

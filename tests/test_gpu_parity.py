@@ -390,6 +390,9 @@ def test_full_config_trajectory_gradients(key):
     sir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, sgd)
     rt = backend.NativeRuntime(ir.wire_json())
     srt = backend.NativeRuntime(sir.wire_json())
+    # one runtime per side for all checkpoints: each takes one step per checkpoint, so their
+    # per-step PRNG seeds (dropout) stay equal
+    so = {False: pyoracle.OracleRuntime(sir.wire()), True: pyoracle.OracleRuntime(sir.wire())}
     rt.upload_params(ir.initial_params(configs.INIT_SEED))
     batches = configs.batches(cfg, TRAJECTORY[-1] + 1)
     fails = []
@@ -406,11 +409,10 @@ def test_full_config_trajectory_gradients(key):
         for f32 in (False, True):
             pyoracle.set_matmul_f32(f32)
             try:
-                so = pyoracle.OracleRuntime(sir.wire())
-                so.upload_params(p)
-                so.step(batches[k])
-                upd[f32] = {n: so.get_home(n, pg[n].size).astype(np.float64) - np.asarray(p[n], np.float64).reshape(-1)
-                            for n in sir.param_names}
+                so[f32].upload_params(p)
+                so[f32].step(batches[k])
+                upd[f32] = {n: so[f32].get_home(n, pg[n].size).astype(np.float64)
+                            - np.asarray(p[n], np.float64).reshape(-1) for n in sir.param_names}
             finally:
                 pyoracle.set_matmul_f32(False)
         worst, wn, relaxed = 0.0, '', []
