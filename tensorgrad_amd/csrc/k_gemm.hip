@@ -372,7 +372,186 @@ bool dma_gen_ok(const GemmDesc& d, bool ak, bool bk) {
 
 }  // namespace
 
+namespace {
+
+// ---- skinny products ---------------------------------------------------------------
+// Products with few output columns (N <= 128 and not a multiple of 64: the 65-wide LM
+// head's forward and weight gradient, 27- and 10-wide classifier heads) or a short, odd K
+// (under 128, N <= 256), where the 64-wide tiles above spend most of their MFMAs on
+// padding, and whose operands load coalesced in the layout below (A with unit row stride
+// or 16-byte aligned k-contiguous rows, B with unit column stride). A block owns 16 rows and NT 16-wide column tiles (N padded to a multiple of 16
+// only) over a k range, on v_mfma_f32_16x16x4f32. Operands go from global memory straight
+// into MFMA registers, with no LDS staging and no barrier in the k loop: lane l holds
+// A[m0 + l%16][k + 4(l/16) + s] and B[k + 4(l/16) + s][n0 + l%16] for s = 0..3, and MFMA s
+// of a 16-k step takes k = 4g + s from lane group g. The four wavefronts take interleaved
+// 16-k steps; a batch is 4 steps per wavefront (256 k per block), all of whose loads are
+// issued before its MFMAs, so a block pays one memory latency per batch. Loads read
+// clamped in-bounds addresses and select zero outside M, N and the k range. Each batch
+// sums into a fresh accumulator that is added to the running sum; the four wavefronts'
+// partial tiles are added in wavefront order through LDS. With splits > 1 each block
+// covers kps of K and writes its partial tile to the workspace ([split][M][N]);
+// k_splitk_reduce adds them in split order. Offsets are 32-bit (the host checks that every
+// element offset fits).
+struct SkinnyArgs {
+  GemmDesc d;
+  int nrb, ncb, splits, kps;
+  float* work;
+};
+
+constexpr int kSkinnySteps = 4;   // 16-k steps per wavefront per batch
+
+__device__ __forceinline__ f32x4 mfma16x4(const f32x4& a, const f32x4& b, f32x4 c) {
+#pragma unroll
+  for (int s = 0; s < 4; ++s) c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], b[s], c, 0, 0, 0);
+  return c;
+}
+
+// Zero outside the operand as a bit mask on a value loaded unconditionally (from a clamped
+// address): a select would let the compiler move each load under a branch of its own and
+// wait for it there, one memory latency per element.
+__device__ __forceinline__ unsigned mask_if(bool keep) { return 0u - (unsigned)keep; }
+__device__ __forceinline__ float masked(float v, unsigned keep) { return __uint_as_float(__float_as_uint(v) & keep); }
+
+template <int NT, bool AV>
+__global__ __launch_bounds__(256) void k_gemm_skinny(const SkinnyArgs s) {
+  constexpr int SB = kSkinnySteps;
+  __shared__ float red[4 * NT * 256];
+  const GemmDesc& d = s.d;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, g4 = lane >> 4;
+  // consecutive row blocks (which share A's cache lines when A has unit row stride) on
+  // one XCD
+  const int bid = (int)xcd_order(blockIdx.x, gridDim.x);
+  const int rbk = bid % s.nrb, rest = bid / s.nrb;
+  const int cbk = rest % s.ncb, sp = rest / s.ncb;
+  const int M = (int)d.M, N = (int)d.N, K = (int)d.K;
+  const int sAm = (int)d.sAm, sAk = (int)d.sAk, sBk = (int)d.sBk, sBn = (int)d.sBn;
+  const int kbeg = sp * s.kps, kend = min(K, kbeg + s.kps);
+  const int m = rbk * 16 + l16;
+  const bool mok = m < M;
+  const float* arow = d.A + (mok ? m : M - 1) * sAm;
+  bool nok[NT];
+  const float* bcol[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const int n = cbk * NT * 16 + t * 16 + l16;
+    nok[t] = n < N;
+    bcol[t] = d.B + (nok[t] ? n : N - 1) * sBn;
+  }
+  f32x4 acc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) acc[t] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+  for (int k0 = kbeg; k0 < kend; k0 += 64 * SB) {
+    // every load of the batch is issued before any is used (the scheduling barrier keeps
+    // the compiler from interleaving waits with the loads)
+    f32x4 a[SB];
+    f32x4 b[SB][NT];
+#pragma unroll
+    for (int j = 0; j < SB; ++j) {
+      const int kb = k0 + (j * 4 + wave) * 16 + g4 * 4;
+      if (AV) {
+        a[j] = *reinterpret_cast<const f32x4*>(arow + min(kb, kend - 4));
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) a[j][q] = arow[min(kb + q, kend - 1) * sAk];
+      }
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) b[j][t][q] = bcol[t][min(kb + q, kend - 1) * sBk];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    f32x4 part[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) part[t] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    // steps past the range multiply zeros (a branch around them would let the compiler
+    // sink their loads into it)
+#pragma unroll
+    for (int j = 0; j < SB; ++j) {
+      const int kb = k0 + (j * 4 + wave) * 16 + g4 * 4;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) a[j][q] = masked(a[j][q], mask_if(mok && kb + q < kend));
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) b[j][t][q] = masked(b[j][t][q], mask_if(nok[t] && kb + q < kend));
+        part[t] = mfma16x4(a[j], b[j][t], part[t]);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] += part[t];
+  }
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[(wave * NT + t) * 256 + (g4 * 4 + r) * 16 + l16] = acc[t][r];
+  __syncthreads();
+  const int64_t MN = d.M * d.N;
+  for (int e = tid; e < NT * 256; e += 256) {
+    const float v = ((red[e] + red[NT * 256 + e]) + red[2 * NT * 256 + e]) + red[3 * NT * 256 + e];
+    const int t = e / 256, rc = e % 256;
+    const int gm = rbk * 16 + rc / 16, gn = cbk * NT * 16 + t * 16 + rc % 16;
+    if (gm >= M || gn >= N) continue;
+    if (s.splits > 1) s.work[sp * MN + (int64_t)gm * N + gn] = v;
+    else d.C[gm * d.sCm + gn * d.sCn] = v;
+  }
+}
+
+struct SkinnyPlan { int nt, nrb, ncb, splits, kps; bool av; };
+
+bool skinny_enabled() {
+  static const bool on = [] {
+    const char* e = std::getenv("TG_SKINNY");
+    return !(e && e[0] == '0');
+  }();
+  return on;
+}
+
+// The plan depends on shapes and strides only (never on operand addresses), so the
+// workspace sized at lowering matches the launch.
+bool skinny_plan(const GemmDesc& d, SkinnyPlan& p) {
+  if (!skinny_enabled() || d.batch != 1 || d.M <= 0 || d.N <= 0 || d.K <= 0) return false;
+  const bool narrow_n = d.N <= 128 && d.N % 64 != 0;
+  const bool short_k = d.K < 128 && d.K % 32 != 0 && d.N <= 256 && d.M * d.N <= (int64_t(1) << 21);
+  if (!narrow_n && !short_k) return false;
+  // 32-bit element offsets, non-negative strides
+  const int64_t lim = int64_t(1) << 31;
+  if (d.M >= lim || d.N >= lim || d.K >= lim) return false;
+  if (d.sAm < 0 || d.sAk < 0 || d.sBk < 0 || d.sBn < 0) return false;
+  if ((d.M - 1) * d.sAm + (d.K - 1) * d.sAk >= lim || (d.K - 1) * d.sBk + (d.N - 1) * d.sBn >= lim) return false;
+  // coalesced operand loads only: the 16 lanes of a group read 16 consecutive rows of A
+  // (unit row stride, or one 16-byte k quad per row) and 16 consecutive columns of B
+  const bool aq = d.sAk == 1 && d.sAm % 4 == 0 && d.K % 4 == 0;
+  if (!(d.sAm == 1 || aq) || d.sBn != 1) return false;
+  p.av = aq;   // and a 16-byte aligned A, checked at launch
+  const int64_t ct = (d.N + 15) / 16;
+  p.nt = ct <= 8 ? (int)ct : 4;
+  p.ncb = (int)((ct + p.nt - 1) / p.nt);
+  p.nrb = (int)((d.M + 15) / 16);
+  // with fewer blocks than half the CUs, split K to fill the CUs and to keep each block to
+  // at most four batches (each costs a memory latency), down to one batch (256 k) per block
+  const int64_t tiles = (int64_t)p.nrb * p.ncb, batch = 64 * kSkinnySteps;
+  int64_t splits = 1;
+  if (tiles < 128)
+    splits = std::min<int64_t>((d.K + batch - 1) / batch,
+                               std::max<int64_t>((256 + tiles - 1) / tiles, (d.K + 4 * batch - 1) / (4 * batch)));
+  if (splits > 64) splits = 64;
+  if (splits < 1) splits = 1;
+  int64_t kps = (d.K + splits - 1) / splits;
+  kps = (kps + 15) / 16 * 16;
+  p.splits = (int)((d.K + kps - 1) / kps);
+  p.kps = (int)kps;
+  return true;
+}
+
+}  // namespace
+
+bool gemm_is_tiny(const GemmDesc& d);
+
 int64_t gemm_workspace_floats(const GemmDesc& d) {
+  SkinnyPlan sk;
+  if (!gemm_is_tiny(d) && skinny_plan(d, sk)) return sk.splits > 1 ? (int64_t)sk.splits * d.M * d.N : 0;
   Plan p = plan_for(d);
   return p.splits > 1 ? (int64_t)p.splits * d.batch * d.M * d.N : 0;
 }
@@ -436,6 +615,29 @@ void gemm(const GemmDesc& d, float* work, hipStream_t st) {
       case 32: klaunch(k_gemm_tiny<32>, grid, 256, 0, st, d); return;
       default: klaunch(k_gemm_tiny<64>, grid, 256, 0, st, d); return;
     }
+  }
+  SkinnyPlan sk;
+  if (skinny_plan(d, sk)) {
+    if (((uintptr_t)d.A & 15) != 0) sk.av = false;
+    SkinnyArgs a{d, sk.nrb, sk.ncb, sk.splits, sk.kps, work};
+    const unsigned blocks = (unsigned)((int64_t)sk.nrb * sk.ncb * sk.splits);
+#define TG_SKINNY(NT)                                                                 \
+  case NT:                                                                             \
+    if (sk.av) klaunch(k_gemm_skinny<NT, true>, blocks, 256, 0, st, a);                \
+    else klaunch(k_gemm_skinny<NT, false>, blocks, 256, 0, st, a);                     \
+    break;
+    switch (sk.nt) {
+      TG_SKINNY(1) TG_SKINNY(2) TG_SKINNY(3) TG_SKINNY(4) TG_SKINNY(5) TG_SKINNY(6) TG_SKINNY(7) TG_SKINNY(8)
+      default: throw std::logic_error("skinny gemm: column tiles out of range");
+    }
+#undef TG_SKINNY
+    if (sk.splits > 1) {
+      const int64_t total = d.M * d.N;
+      int64_t nb = (total + 255) / 256;
+      if (nb > 4096) nb = 4096;
+      klaunch(k_splitk_reduce, (int)nb, 256, 0, st, work, sk.splits, total, d);
+    }
+    return;
   }
   Plan p = plan_for(d);
   GemmArgs g{d, p.kps, p.splits, 0, 0, nullptr, 0, 0};

@@ -515,7 +515,15 @@ GEMMS = [([5, 7], [7, 3], False, False), ([2, 33, 65], [65, 17], False, False), 
          ([1000, 63], [63, 256], False, False), ([700, 319], [319, 256], False, False),
          ([2000, 319], [2000, 256], True, False), ([4096, 4], [4, 256], False, False),
          ([9000, 63], [9000, 64], True, False), ([3, 33, 17], [17, 9], False, False),
-         ([130, 45], [70, 45], False, True), ([8192, 319], [319, 512], False, False)]
+         ([130, 45], [70, 45], False, True), ([8192, 319], [319, 512], False, False),
+         # skinny products (16-wide column tiles, N padded to a multiple of 16 only): the LM
+         # head forward, input gradient (K = 65) and weight gradient (split-K), C2's and C3's
+         # heads, 100- and 112-wide products, short k with 256 columns
+         ([4096, 65], [256, 65], False, True), ([1024, 512], [512, 27], False, False),
+         ([1024, 512], [1024, 27], True, False), ([128, 128], [128, 10], False, False),
+         ([128, 10], [128, 10], False, True), ([128, 128], [128, 10], True, False),
+         ([512, 96], [96, 100], False, False), ([333, 200], [200, 112], False, False),
+         ([300, 27], [27, 256], False, False), ([2048, 300], [2048, 65], True, False)]
 
 
 @pytest.mark.parametrize('case', GEMMS)
