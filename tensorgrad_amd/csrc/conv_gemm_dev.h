@@ -51,6 +51,7 @@ struct ConvGemmArgs {
   int tiles_m, tiles_n, splits, k_per_split;
   int pad;                      // some tap can fall outside the image: bounds checks needed
   int avec;                     // A rows are 16-byte aligned in groups of 4 k (vector loads)
+  int ipb;                      // few-taps weight gradient: images per block
   FastDiv dKHW, dKW, dWo, dHoWo, dW, dHW, dSH, dSW;
   FastDiv dCpg;                 // F_TAP: channels per group of the reduction (CinPG / CoutPG)
   const float* x;

@@ -280,12 +280,13 @@ __global__ __launch_bounds__(256) void k_conv_small_fwd(const ConvGemmArgs c) {
   }
 }
 
-// Weight gradient: block (image b, group g, kSmallCo output channels) sums dy * tap over
-// the image's positions (threads take positions t, t + 256, ...), then across the block in
-// a fixed order: every thread stores its sums in LDS, four threads per sum add 64 threads'
-// values each in thread order, and the four quarters are added in order, giving the
-// image's partial dW rows work[b][g * CoutPG + co][q]. The partials are added in image
-// order.
+// Weight gradient: block (ipb consecutive images, group g, kSmallCo output channels) sums
+// dy * tap over the images' positions (threads take positions t, t + 256, ... of each image
+// in turn), then across the block in a fixed order: every thread stores its sums in LDS,
+// four threads per sum add 64 threads' values each in thread order, and the four quarters
+// are added in order, giving the image group's partial dW rows work[ig][g * CoutPG + co][q].
+// The partials are added in image-group order. Several images per block spread the fixed
+// cost of the block sum over more positions.
 __global__ __launch_bounds__(256) void k_conv_small_wgrad(const ConvGemmArgs c) {
   constexpr int NV = kSmallCo * kSmallTaps;
   static_assert(NV * 4 == 256, "four threads per sum");
@@ -293,30 +294,33 @@ __global__ __launch_bounds__(256) void k_conv_small_wgrad(const ConvGemmArgs c) 
   const int hw = c.Ho * c.Wo;
   const int nch = (c.CoutPG + kSmallCo - 1) / kSmallCo;
   const int blk = blockIdx.x, cc = blk % nch, z = blk / nch;
-  const int b = z / c.G, g = z - b * c.G;
+  const int ig = z / c.G, g = z - ig * c.G;
   const int tid = threadIdx.x;
   SmallTaps tp;
   tp.init(c);
   const Src sx = make_src(c.x, (int64_t)c.B * c.Cin * c.H * c.W);
   const Src sdy = make_src(c.dy, (int64_t)c.B * c.Cout * hw);
-  const uint32_t xbase = (uint32_t)((b * c.Cin + g * c.CinPG) * c.H * c.W);
-  const uint32_t dbase = (uint32_t)((b * c.Cout + g * c.CoutPG + cc * kSmallCo) * hw);
   float acc[kSmallCo][kSmallTaps];
 #pragma unroll
   for (int j = 0; j < kSmallCo; ++j)
 #pragma unroll
     for (int q = 0; q < kSmallTaps; ++q) acc[j][q] = 0.0f;
-  for (int p = tid; p < hw; p += 256) {
-    const int ho = fdiv(p, c.dWo), wo = p - ho * c.Wo;
-    float xv[kSmallTaps], d[kSmallCo];
-    tp.gather(c, sx, xbase, ho, wo, xv);
+  const int bend = min(c.B, (ig + 1) * c.ipb);
+  for (int b = ig * c.ipb; b < bend; ++b) {
+    const uint32_t xbase = (uint32_t)((b * c.Cin + g * c.CinPG) * c.H * c.W);
+    const uint32_t dbase = (uint32_t)((b * c.Cout + g * c.CoutPG + cc * kSmallCo) * hw);
+    for (int p = tid; p < hw; p += 256) {
+      const int ho = fdiv(p, c.dWo), wo = p - ho * c.Wo;
+      float xv[kSmallTaps], d[kSmallCo];
+      tp.gather(c, sx, xbase, ho, wo, xv);
 #pragma unroll
-    for (int j = 0; j < kSmallCo; ++j)
-      d[j] = ldb(sdy, boff(cc * kSmallCo + j < c.CoutPG, dbase + (uint32_t)(j * hw + p)));
+      for (int j = 0; j < kSmallCo; ++j)
+        d[j] = ldb(sdy, boff(cc * kSmallCo + j < c.CoutPG, dbase + (uint32_t)(j * hw + p)));
 #pragma unroll
-    for (int j = 0; j < kSmallCo; ++j)
+      for (int j = 0; j < kSmallCo; ++j)
 #pragma unroll
-      for (int q = 0; q < kSmallTaps; ++q) acc[j][q] = fmaf(d[j], xv[q], acc[j][q]);
+        for (int q = 0; q < kSmallTaps; ++q) acc[j][q] = fmaf(d[j], xv[q], acc[j][q]);
+    }
   }
 #pragma unroll
   for (int j = 0; j < kSmallCo; ++j)
@@ -333,7 +337,7 @@ __global__ __launch_bounds__(256) void k_conv_small_wgrad(const ConvGemmArgs c) 
     const int j = tid / kSmallTaps, q = tid % kSmallTaps, co = cc * kSmallCo + j;
     if (co < c.CoutPG && q < c.K) {
       const float t = ((red[0][tid] + red[1][tid]) + red[2][tid]) + red[3][tid];
-      c.work[(int64_t)b * c.G * c.CoutPG * c.K + (int64_t)(g * c.CoutPG + co) * c.K + q] = t;
+      c.work[(int64_t)ig * c.G * c.CoutPG * c.K + (int64_t)(g * c.CoutPG + co) * c.K + q] = t;
     }
   }
 }
@@ -430,12 +434,15 @@ void conv2d_weight_grad_gemm(const float* x, const float* dy, float* dw, const C
     sa.K = (int)(d.CinPG * d.kH * d.kW);
     const int64_t per = d.Cout * sa.K;
     const int64_t nch = (a.CoutPG + kSmallCo - 1) / kSmallCo;
-    klaunch(k_conv_small_wgrad, (unsigned)(d.B * d.G * nch), 256, 0, st, sa);
-    if (per < 16384 && d.B > 16) {
-      klaunch(k_conv_wgrad_reduce_wave, (unsigned)((per + 3) / 4), 256, 0, st, work, (int)d.B, per, dw);
+    // images per block: about two blocks per CU (the block sum's LDS admits two)
+    sa.ipb = (int)std::max<int64_t>(1, d.B * d.G * nch / 512);
+    const int64_t ngroups = (d.B + sa.ipb - 1) / sa.ipb;
+    klaunch(k_conv_small_wgrad, (unsigned)(ngroups * d.G * nch), 256, 0, st, sa);
+    if (per < 16384 && ngroups > 16) {
+      klaunch(k_conv_wgrad_reduce_wave, (unsigned)((per + 3) / 4), 256, 0, st, work, (int)ngroups, per, dw);
     } else {
       const int64_t nb = std::min<int64_t>((per + 255) / 256, 4096);
-      klaunch(k_conv_wgrad_reduce, (int)nb, 256, 0, st, work, (int)d.B, per, dw);
+      klaunch(k_conv_wgrad_reduce, (int)nb, 256, 0, st, work, (int)ngroups, per, dw);
     }
     return;
   }

@@ -15,6 +15,7 @@ import pytest
 import pyoracle
 from _helpers import rel_err, sign_ambiguous
 from tensorgrad_amd import backend, configs
+from tensorgrad_amd import ir as IR
 from tensorgrad_amd.build_ir import build_training_ir
 
 pytestmark = pytest.mark.gpu
@@ -364,7 +365,33 @@ def test_full_config_100_steps(key):
 
 
 TRAJECTORY = (1, 25, 50, 75, 100)
-F32_TWIN_FACTOR = 2.0
+RELU_FLIP_SIG = 1e-5    # a tenth of the gradient bar
+MAX_TIE_DEFER = 5
+
+
+def _relu_flips(o, wire, gpu_x):
+    """ReLU decisions the GPU resolved differently from the oracle in the same step: for
+    each relu_grad, the elements whose forward input has a different sign on the two sides
+    (gpu_x: the GPU's forward inputs, captured). A flipped element moves its whole upstream
+    gradient dy into or out of the layer's gradient: a discrete event of a ReLU input within
+    rounding distance of zero, not an accumulation error. Its weight is the summed |dy| of
+    the flipped elements over the norm of the layer's bias gradient (the sum_to_shape of the
+    relu_grad output; the output's own norm where the layer has none). Returns
+    [(tensor id, flips, weight)]."""
+    ops = wire['graph']['ops']
+    bias_of = {op['a']: op['out'] for op in ops if op['kind'] == 'sum_to_shape'}
+    res = []
+    for op in ops:
+        if op['kind'] != 'relu_grad':
+            continue
+        zo = o.tensor(op['x']).reshape(-1)
+        flip = (zo > 0) != (gpu_x[op['x']].reshape(-1) > 0)
+        if not flip.any():
+            continue
+        dy = np.abs(o.tensor(op['dy']).astype(np.float64).reshape(-1))
+        ref = np.linalg.norm(o.tensor(bias_of.get(op['out'], op['out'])).astype(np.float64))
+        res.append((op['x'], int(flip.sum()), float(dy[flip].sum() / max(ref, 1e-30))))
+    return res
 
 
 @pytest.mark.parametrize('key', ['char_mlp', 'cnn', 'nerf', 'transformer'])
@@ -376,30 +403,46 @@ def test_full_config_trajectory_gradients(key):
     update (its gradient) agrees within 1e-4 relative, independently of the workload's own
     amplification of rounding differences over the run.
 
-    The bar holds as stated except where f32 arithmetic itself cannot meet it on that
-    state: the oracle also evaluates the same step with every matmul accumulated in f32
-    (the f32 twin: a valid f32 implementation, as the reference's WGSL kernels are). Where
-    that twin lies beyond 1e-4 of the f64 evaluator, the tensor is held to F32_TWIN_FACTOR
-    times the twin's distance instead, and both figures are printed. (C4, late in its run:
-    its ReLU layers below the skip concatenation see gradients that f32 arithmetic
-    reproduces only to a few 1e-4.)"""
+    For scale, the oracle also evaluates the same step with every matmul accumulated in
+    f32 (the f32 twin: a plain f32 implementation, as the reference's WGSL kernels are)
+    and prints that twin's distance where it exceeds the bar: on C4's first and last
+    checkpoints it is 1.2-2.0e-4, while the GPU's blocked accumulation stays under 1e-4.
+
+    A ReLU input within rounding distance of zero can land on the other side of zero in
+    any f32 evaluation. The SGD graph captures every ReLU input on the GPU; where the GPU
+    and the oracle resolved one differently and the flipped elements weigh more than
+    RELU_FLIP_SIG of the layer's bias gradient (_relu_flips), the state is a tie and the
+    check moves to the next step (printed), up to MAX_TIE_DEFER steps. (C3 after one step of
+    one build: a conv1 input to the ReLU of -4.7e-10, against values up to ~0.3, came out
+    positive on the GPU and put conv1.W and conv1.b at 1.9e-4 while every other tensor was
+    at a few 1e-7.)"""
     pyoracle.set_threads(16)
     cfg = configs.CONFIGS[key]
     ir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer)
     sgd = {'kind': 'sgd', 'lr': float(2 ** 24)}
     sir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, sgd)
+    swire = sir.wire()
+    relu_x = sorted({op['x'] for op in swire['graph']['ops'] if op['kind'] == 'relu_grad'})
+    shapes = {t['id']: t['shape'] for t in swire['graph']['tensors']}
+    swire['graph']['captures'].update({f'relu_x_{t}': t for t in relu_x})
     rt = backend.NativeRuntime(ir.wire_json())
-    srt = backend.NativeRuntime(sir.wire_json())
+    srt = backend.NativeRuntime(IR.dumps(swire))
     # one runtime per side for all checkpoints: each takes one step per checkpoint, so their
     # per-step PRNG seeds (dropout) stay equal
-    so = {False: pyoracle.OracleRuntime(sir.wire()), True: pyoracle.OracleRuntime(sir.wire())}
+    so = {False: pyoracle.OracleRuntime(swire), True: pyoracle.OracleRuntime(swire)}
+    so[False].retain_all(True)
     rt.upload_params(ir.initial_params(configs.INIT_SEED))
-    batches = configs.batches(cfg, TRAJECTORY[-1] + 1)
+    last = TRAJECTORY[-1] + MAX_TIE_DEFER
+    batches = configs.batches(cfg, last + 1)
     fails = []
-    for i in range(TRAJECTORY[-1]):
+    due = list(TRAJECTORY)
+    deferred = 0
+    for i in range(last):
         rt.step(batches[i])
         k = i + 1
-        if k not in TRAJECTORY:
+        if not due:
+            break
+        if k < due[0]:
             continue
         p = rt.download_params()
         srt.upload_params(p)
@@ -415,22 +458,32 @@ def test_full_config_trajectory_gradients(key):
                             - np.asarray(p[n], np.float64).reshape(-1) for n in sir.param_names}
             finally:
                 pyoracle.set_matmul_f32(False)
+        gpu_x = {t: srt.capture(f'relu_x_{t}', shapes[t], np.float32) for t in relu_x}
+        ties = [f for f in _relu_flips(so[False], swire, gpu_x) if f[2] > RELU_FLIP_SIG]
+        if ties:
+            deferred += 1
+            assert deferred <= MAX_TIE_DEFER, f'[{key}] ReLU ties at {deferred} states in a row: {ties}'
+            print(f'  [{key}] after step {k}: ReLU flips (tensor, count, weight) {ties}; '
+                  f'checkpoint {due[0]} moves to step {k + 1}', flush=True)
+            continue
+        deferred = 0
+        due.pop(0)
         worst, wn, relaxed = 0.0, '', []
         for n in sir.param_names:
             start = np.asarray(p[n], np.float64).reshape(-1)
             e = rel_err(pg[n].astype(np.float64) - start, upd[False][n], f'[{key}] step {k} {n} update')
             tw = rel_err(upd[True][n], upd[False][n], f'[{key}] step {k} {n} f32 twin')
-            bar = GRAD_TOL if tw <= GRAD_TOL else F32_TWIN_FACTOR * tw
-            if bar > GRAD_TOL:
+            if tw > GRAD_TOL:
                 relaxed.append(f'{n} {e:.2e} (f32 twin {tw:.2e})')
-            if e > bar:
-                fails.append(f'step {k} {n}: {e:.2e} > {bar:.2e}')
+            if e > GRAD_TOL:
+                fails.append(f'step {k} {n}: {e:.2e} > {GRAD_TOL:.0e}')
             if e > worst:
                 worst, wn = e, n
         print(f'  [{key}] after step {k}: worst gradient rel {worst:.2e} ({wn})'
-              + (f'; beyond 1e-4 in f32 itself: {", ".join(relaxed)}' if relaxed else ''), flush=True)
+              + (f'; f32 twin beyond 1e-4: {", ".join(relaxed)}' if relaxed else ''), flush=True)
     rt.destroy()
     srt.destroy()
+    assert not due, f'[{key}] checkpoints never reached: {due}'
     assert not fails, fails
 
 
