@@ -401,22 +401,55 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint32_t b, const E
       }
     return;
   }
+  if constexpr (Epi::kPrefetch) {
+    // An epilogue that reads other tensors: every one of its loads for the wave's
+    // accumulator values is issued first (clamped to an element in range), then the values
+    // are computed and stored. Interleaved, each load would wait for the stores before it
+    // (the outputs may alias the inputs as far as the compiler knows): one memory latency
+    // per value.
+    typename Epi::Pre pre[TM][TN][16];
 #pragma unroll
-  for (int i = 0; i < TM; ++i)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int64_t gn = n0 + wn0 + j * 32 + lrow;
-      if (gn >= d.N) continue;
+      for (int j = 0; j < TN; ++j) {
+        const int64_t gn = min((int64_t)(n0 + wn0 + j * 32 + lrow), d.N - 1);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t gm = m0 + wm0 + i * 32 + (r / 4) * 8 + h * 4 + (r % 4);
-        if (gm < d.M) epi(d, z0, z1, gm, gn, acc[i][j][r]);
+        for (int r = 0; r < 16; ++r) {
+          const int64_t gm = min((int64_t)(m0 + wm0 + i * 32 + (r / 4) * 8 + h * 4 + (r % 4)), d.M - 1);
+          pre[i][j][r] = epi.load(d, gm, gn);
+        }
       }
-    }
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int64_t gn = n0 + wn0 + j * 32 + lrow;
+        if (gn >= d.N) continue;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t gm = m0 + wm0 + i * 32 + (r / 4) * 8 + h * 4 + (r % 4);
+          if (gm < d.M) epi(d, z0, z1, gm, gn, acc[i][j][r], pre[i][j][r]);
+        }
+      }
+  } else {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int64_t gn = n0 + wn0 + j * 32 + lrow;
+        if (gn >= d.N) continue;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t gm = m0 + wm0 + i * 32 + (r / 4) * 8 + h * 4 + (r % 4);
+          if (gm < d.M) epi(d, z0, z1, gm, gn, acc[i][j][r]);
+        }
+      }
+  }
 }
 
 // The plain epilogue: element (z, gm, gn) of the product to C.
 struct StoreC {
+  static constexpr bool kPrefetch = false;
   __device__ __forceinline__ void operator()(const GemmDesc& d, int64_t z0, int64_t z1, int64_t gm, int64_t gn,
                                              float v) const {
     d.C[z0 * d.sCz0 + z1 * d.sCz1 + gm * d.sCm + gn * d.sCn] = v;

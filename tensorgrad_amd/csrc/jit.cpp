@@ -299,24 +299,34 @@ JitKernel gemm_epi_kernel(const FusedProgram& p, const FusedInstr* code, const G
   std::ostringstream o;
   // The epilogue functor: element (gm, gn) of the product is element t = gm * N + gn of
   // the group's iteration space (the product is contiguous and read in that order).
+  // Two phases (gemm_tile's kPrefetch): load() reads the group's other inputs for an
+  // element, operator() computes from them and the accumulator value and stores.
   o << "namespace {\nstruct @NAME@_epi {\n  tgk::JitArgs A;\n  unsigned seed;\n";
-  o << "  __device__ __forceinline__ void operator()(const tgk::GemmDesc& d, int64_t, int64_t, int64_t gm, int64_t gn, "
-       "float value) const {\n";
-  if (c.store_c) o << I << "d.C[gm * d.sCm + gn * d.sCn] = value;\n";
+  o << "  static constexpr bool kPrefetch = true;\n";
+  o << "  struct Pre { unsigned x[" << std::max(1, p.n_in) << "]; };\n";
+  o << "  __device__ __forceinline__ Pre load(const tgk::GemmDesc&, int64_t gm, int64_t gn) const {\n";
+  o << I << "Pre q;\n";
   o << I << "const unsigned t = (unsigned)gm * " << ulit(c.N) << " + (unsigned)gn;\n";
   if (p.any_strided) emit_coords(o, p, "t", I);
   for (int k = 0; k < p.n_in; ++k) {
-    const std::string x = "x" + std::to_string(k);
-    if (k == c.h_in) {
-      o << I << "const unsigned " << x << " = tgk::fbits(value);\n";
-      continue;
-    }
+    if (k == c.h_in) continue;
     const int m = p.in_mode[k];
-    o << I << "const unsigned " << x << " = ((const unsigned*)A.in[" << k << "])[";
+    o << I << "q.x[" << k << "] = ((const unsigned*)A.in[" << k << "])[";
     if (m == FM_CONTIG) o << "t";
     else if (m == FM_SCALAR) o << "0u";
     else o << offset_expr(p, k);
     o << "];\n";
+  }
+  o << I << "(void)t;\n" << I << "return q;\n  }\n";
+  o << "  __device__ __forceinline__ void operator()(const tgk::GemmDesc& d, int64_t, int64_t, int64_t gm, int64_t gn, "
+       "float value, const Pre& q) const {\n";
+  if (c.store_c) o << I << "d.C[gm * d.sCm + gn * d.sCn] = value;\n";
+  o << I << "const unsigned t = (unsigned)gm * " << ulit(c.N) << " + (unsigned)gn;\n";
+  o << I << "(void)t;\n";
+  for (int k = 0; k < p.n_in; ++k) {
+    const std::string x = "x" + std::to_string(k);
+    if (k == c.h_in) o << I << "const unsigned " << x << " = tgk::fbits(value);\n";
+    else o << I << "const unsigned " << x << " = q.x[" << k << "];\n";
   }
   std::vector<std::string> reg(64);
   for (int k = 0; k < p.n_in; ++k) reg[k] = "x" + std::to_string(k);
