@@ -244,9 +244,9 @@ __global__ void k_sum_rows(const float* __restrict__ a, double* __restrict__ par
       for (int64_t r = r0 + lane; r < r1; r += kWave * kSumUnroll) {
         float v[kSumUnroll];
 #pragma unroll
-        for (int u = 0; u < kSumUnroll; ++u) {
+        for (int u = 0; u < kSumUnroll; ++u) {   // unconditional loads (clamped): all in flight
           const int64_t j = r + u * kWave;
-          v[u] = j < r1 ? p[j * st] : 0.0f;
+          v[u] = p[(j < r1 ? j : r0) * st];
         }
 #pragma unroll
         for (int u = 0; u < kSumUnroll; ++u)
@@ -260,14 +260,18 @@ __global__ void k_sum_rows(const float* __restrict__ a, double* __restrict__ par
       if (r0 + lane < r1) {
         int64_t hi = (r0 + lane) / d1, lo = (r0 + lane) - hi * d1;   // index = hi * d1 + lo
         for (int64_t r = r0 + lane; r < r1; r += kWave * kSumUnroll) {
-          float v[kSumUnroll];
+          // offsets first (the carry loops), then every load, then the sum: a load between
+          // carry loops waited for its value before the next offset was formed
+          int64_t off[kSumUnroll];
 #pragma unroll
           for (int u = 0; u < kSumUnroll; ++u) {
-            const int64_t j = r + u * kWave;
-            v[u] = j < r1 ? a[base + hi * s0 + lo * s1] : 0.0f;
+            off[u] = r + u * kWave < r1 ? base + hi * s0 + lo * s1 : base;
             lo += kWave;
             while (lo >= d1) { lo -= d1; ++hi; }
           }
+          float v[kSumUnroll];
+#pragma unroll
+          for (int u = 0; u < kSumUnroll; ++u) v[u] = a[off[u]];
 #pragma unroll
           for (int u = 0; u < kSumUnroll; ++u)
             if (r + u * kWave < r1) s += (double)v[u];
