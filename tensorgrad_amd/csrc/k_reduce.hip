@@ -374,9 +374,34 @@ template <bool MID>
 __global__ __launch_bounds__(kColThreads) void k_colsum(const ColSumBatch batch) {
   if ((int)blockIdx.x < batch.sc.blocks) {   // the embedding gradient run beside the sums
     __shared__ ScatterScanLds<kColWaves> sl;
-    const int v = (int)blockIdx.x % batch.sc.V, cy = (int)blockIdx.x / batch.sc.V;
-    scatter_scan_block<kColWaves>(batch.sc.idx, batch.sc.rows, batch.sc.dy, batch.sc.N, batch.sc.out, v,
-                                  (int64_t)cy * kColThreads, sl);
+    const ColSumScatter& sc = batch.sc;
+    const int vc = (int)blockIdx.x % (sc.blocks / sc.nwin), win = (int)blockIdx.x / (sc.blocks / sc.nwin);
+    const int v = vc % sc.V, cy = vc / sc.V;
+    const int64_t c0 = (int64_t)cy * kColThreads, c = c0 + threadIdx.x;
+    const int64_t rb = (int64_t)win * sc.wrows, re = min(sc.rows, rb + sc.wrows);
+    const double acc = scatter_scan_rows<kColWaves>(sc.idx, rb, re, sc.dy, sc.N, v, c0, sl);
+    if (sc.nwin == 1) {
+      if (c < sc.N) sc.out[(int64_t)v * sc.N + c] = (float)acc;
+      return;
+    }
+    // partials and the counter as device-scope atomics, as in the column sums
+    __shared__ int slast;
+    double* part = sc.part + ((int64_t)v * sc.nwin) * sc.N;
+    if (c < sc.N) __hip_atomic_store(&part[(int64_t)win * sc.N + c], acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0)
+      slast = __hip_atomic_fetch_add(&sc.counters[vc], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+              (unsigned)(sc.nwin - 1);
+    __syncthreads();
+    if (!slast) return;
+    if (c < sc.N) {
+      double t = 0.0;
+      for (int k = 0; k < sc.nwin; ++k)
+        t += __hip_atomic_load(&part[(int64_t)k * sc.N + c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      sc.out[(int64_t)v * sc.N + c] = (float)t;
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(&sc.counters[vc], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
   int bid = (int)blockIdx.x - batch.sc.blocks;
@@ -681,6 +706,27 @@ int64_t midsum_counters(int64_t B, int64_t C, int64_t L) {
   return (B + ch - 1) / ch > 1 ? C : 0;
 }
 
+// Row windows for the embedding gradient: about 256 blocks in all, windows of at least 512
+// rows (a window's hits are found and summed with one memory latency or two).
+int scatter_windows(int64_t rows, int64_t V, int64_t N) {
+  if (rows <= 0 || V <= 0 || N <= 0) return 1;
+  const int64_t vc = V * ((N + kColThreads - 1) / kColThreads);
+  int64_t w = std::min<int64_t>((rows + 511) / 512, 256 / vc);
+  if (w < 1) w = 1;
+  if (w > 64) w = 64;
+  const int64_t wrows = (rows + w - 1) / w;
+  return (int)((rows + wrows - 1) / wrows);
+}
+
+int64_t scatter_workspace_doubles(int64_t rows, int64_t V, int64_t N) {
+  const int w = scatter_windows(rows, V, N);
+  return w > 1 ? V * w * N : 0;
+}
+
+int64_t scatter_counters(int64_t rows, int64_t V, int64_t N) {
+  return scatter_windows(rows, V, N) > 1 ? V * ((N + kColThreads - 1) / kColThreads) : 0;
+}
+
 int64_t colsum_workspace_doubles(int64_t C, int64_t R, int terms) {
   const ColPlan p = col_plan(C, R, terms);
   return p.nchunks > 1 ? C * p.nchunks : 0;
@@ -698,8 +744,12 @@ void colsum_batch(const ColSumBatch& b, hipStream_t st) {
   bt.sc.blocks = 0;
   if (bt.sc.idx && bt.sc.V > 0 && bt.sc.N > 0) {
     const int64_t ny = (bt.sc.N + kColThreads - 1) / kColThreads;
-    if ((int64_t)bt.sc.V * ny > INT32_MAX / 2) throw std::runtime_error("column sums: scatter too large");
-    bt.sc.blocks = (int)(bt.sc.V * ny);
+    const int nwin = scatter_windows(bt.sc.rows, bt.sc.V, bt.sc.N);
+    if ((int64_t)bt.sc.V * ny * nwin > INT32_MAX / 2) throw std::runtime_error("column sums: scatter too large");
+    if (nwin > 1 && (!bt.sc.part || !bt.sc.counters)) throw std::runtime_error("column sums: scatter partials missing");
+    bt.sc.nwin = nwin;
+    bt.sc.wrows = (bt.sc.rows + nwin - 1) / nwin;
+    bt.sc.blocks = (int)(bt.sc.V * ny * nwin);
   }
   // then the [B, C, L] sums' blocks, then the column sums' (each numbered from 0 in its range)
   if (bt.nmid < 0 || bt.nmid > kMidSumMax) throw std::runtime_error("column sums: bad [B, C, L] sum count");

@@ -176,7 +176,19 @@ struct ColSumScatter {
   float* out;
   int64_t rows, N;
   int V, blocks;
+  // rows split into nwin windows of wrows: block (v, column block, window) sums its window,
+  // the last of a (v, column block)'s windows adds the f64 partials part[v][window][c] in
+  // window order (counter per (v, column block), left zero)
+  int nwin;
+  int64_t wrows;
+  double* part;
+  unsigned* counters;
 };
+// Row windows of the embedding gradient inside a column-sum launch (1: one block per token
+// and column block walks every row), its partials (doubles) and counters.
+int scatter_windows(int64_t rows, int64_t V, int64_t N);
+int64_t scatter_workspace_doubles(int64_t rows, int64_t V, int64_t N);
+int64_t scatter_counters(int64_t rows, int64_t V, int64_t N);
 // Sum over the outer and inner axes of a contiguous [B, C, L] array (a convolution's bias
 // gradient: images and spatial positions), out[c] = f32(sum over b and l), run by blocks
 // of a column-sum launch after the scatter's: block (c, q) sums images q chunk .. in f64,

@@ -2534,6 +2534,8 @@ void Runtime::emit_colsums(const std::vector<int>& batch, bool with_scatter, boo
   n.ws = true;
   const bool sct = with_scatter && !deferred_scatter_.empty();
   const DeferredScatter sc = sct ? deferred_scatter_.front() : DeferredScatter{};
+  size_t sws_off = 0;
+  int64_t scbase = 0;
   if (sct) {
     n.reads.push_back(root(sc.idx));
     n.reads.push_back(root(sc.b));
@@ -2541,6 +2543,10 @@ void Runtime::emit_colsums(const std::vector<int>& batch, bool with_scatter, boo
     n.bytes += 4.0 * (sc.rows + sc.rows * sc.N + sc.V * sc.N);
     n.detail += ",scatter";
     n.shape += " + scatter " + sc.shape;
+    sws_off = ws;
+    ws += ((size_t)tgk::scatter_workspace_doubles(sc.rows, sc.V, sc.N) * 8 + 255) & ~(size_t)255;
+    scbase = take_counters(tgk::scatter_counters(sc.rows, sc.V, sc.N));
+    workspace_bytes_ = std::max(workspace_bytes_, ws);
   }
   n.bind = [=]() -> std::function<void(hipStream_t)> {
     tgk::ColSumBatch bt{};
@@ -2555,6 +2561,8 @@ void Runtime::emit_colsums(const std::vector<int>& batch, bool with_scatter, boo
       bt.sc.rows = sc.rows;
       bt.sc.N = sc.N;
       bt.sc.V = (int)sc.V;
+      bt.sc.part = reinterpret_cast<double*>(reinterpret_cast<char*>(cur_ws_) + sws_off);
+      bt.sc.counters = cur_counters_ + scbase;
     }
     for (size_t q = 0; q < batch.size(); ++q) {
       const ColSumOp& c = colsum_.at(batch[q]);

@@ -20,17 +20,17 @@ struct ScatterScanLds {
   int nhit[NW];
 };
 
-// Block of NW wavefronts for token v and columns c0 .. c0 + 64 NW - 1: walks idx in windows
-// of kScanRows rows. Each wavefront ballots the rows of its share of the window whose token
+// Block of NW wavefronts for token v and columns c0 .. c0 + 64 NW - 1 over rows [rb, re):
+// walks idx in windows of kScanRows rows. Each wavefront ballots the rows of its share of the window whose token
 // is v; the shares' counts give each wavefront its offset, so the hits land in LDS as one
 // list in row order. Then every thread adds its column of the listed rows to an f64
 // accumulator, in list order, kScanLoads loads in flight. The additions happen in
-// increasing row order, the order of the one-hot product's k loop, whatever NW is.
+// increasing row order, the order of the one-hot product's k loop, whatever NW is. Returns
+// the thread's column sum (f64; 0 for threads past N).
 template <int NW>
-__device__ __forceinline__ void scatter_scan_block(const int32_t* __restrict__ idx, int64_t rows,
-                                                   const float* __restrict__ dy, int64_t N,
-                                                   float* __restrict__ out, int v, int64_t c0,
-                                                   ScatterScanLds<NW>& L) {
+__device__ __forceinline__ double scatter_scan_rows(const int32_t* __restrict__ idx, int64_t rb, int64_t rows,
+                                                    const float* __restrict__ dy, int64_t N, int v, int64_t c0,
+                                                    ScatterScanLds<NW>& L) {
   constexpr int Q = kScanRows / NW;   // rows per wavefront per window
   constexpr int U = kScanLoads;
   static_assert(Q % 64 == 0, "a wavefront's share of a window is whole rounds of 64 rows");
@@ -39,7 +39,7 @@ __device__ __forceinline__ void scatter_scan_block(const int32_t* __restrict__ i
   const bool col = c < N;
   const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
   double acc = 0.0;
-  for (int64_t r0 = 0; r0 < rows; r0 += kScanRows) {
+  for (int64_t r0 = rb; r0 < rows; r0 += kScanRows) {
     const int64_t qa = r0 + (int64_t)w * Q, qb = min(rows, qa + Q);
     int32_t t[Q / 64];
 #pragma unroll
@@ -100,7 +100,18 @@ __device__ __forceinline__ void scatter_scan_block(const int32_t* __restrict__ i
     }
     __syncthreads();   // the next window rewrites hits, nhit and stage
   }
-  if (col) out[(int64_t)v * N + c] = (float)acc;
+  return acc;
+}
+
+// All rows: the column sums rounded to f32 into out[v][c].
+template <int NW>
+__device__ __forceinline__ void scatter_scan_block(const int32_t* __restrict__ idx, int64_t rows,
+                                                   const float* __restrict__ dy, int64_t N,
+                                                   float* __restrict__ out, int v, int64_t c0,
+                                                   ScatterScanLds<NW>& L) {
+  const double acc = scatter_scan_rows<NW>(idx, 0, rows, dy, N, v, c0, L);
+  const int64_t c = c0 + threadIdx.x;
+  if (c < N) out[(int64_t)v * N + c] = (float)acc;
 }
 
 }  // namespace tgk
