@@ -228,6 +228,56 @@ __global__ void k_max_pool_grad_tiled(const float* __restrict__ x, const float* 
   }
 }
 
+// 2 x 2 windows with stride 2 tiling the input (H = 2 Ho, W = 2 Wo, no padding; the
+// CNN's pools): the same scan order and comparisons as above, a window's two input rows as
+// one 8-byte load each (both loads in flight before the comparisons).
+__device__ __forceinline__ const float2* pool22_rows(const float* x, const Pool32& p, int bc, int ho, int wo,
+                                                    int64_t& base) {
+  base = (int64_t)bc * p.H * p.W + (int64_t)(2 * ho) * p.W + 2 * wo;
+  return reinterpret_cast<const float2*>(x + base);
+}
+
+__global__ void k_max_pool22(const float* __restrict__ x, float* __restrict__ y, Pool32 p) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < p.nwin; i += gridDim.x * blockDim.x) {
+    int bc, ho, wo;
+    window_of(p, i, bc, ho, wo);
+    int64_t base;
+    const float2* r = pool22_rows(x, p, bc, ho, wo, base);
+    const float2 a = r[0], b = *reinterpret_cast<const float2*>(x + base + p.W);
+    float m = -3.4e38f;
+    if (a.x > m) m = a.x;
+    if (a.y > m) m = a.y;
+    if (b.x > m) m = b.x;
+    if (b.y > m) m = b.y;
+    y[i] = m;
+  }
+}
+
+__global__ void k_max_pool22_grad(const float* __restrict__ x, const float* __restrict__ dy,
+                                  float* __restrict__ dx, Pool32 p) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < p.nwin; i += gridDim.x * blockDim.x) {
+    int bc, ho, wo;
+    window_of(p, i, bc, ho, wo);
+    int64_t base;
+    const float2* r = pool22_rows(x, p, bc, ho, wo, base);
+    const float2 a = r[0], b = *reinterpret_cast<const float2*>(x + base + p.W);
+    const float g = dy[i];
+    float m = -3.4e38f;
+    int arg = -1;
+    if (a.x > m) { m = a.x; arg = 0; }
+    if (a.y > m) { m = a.y; arg = 1; }
+    if (b.x > m) { m = b.x; arg = 2; }
+    if (b.y > m) { m = b.y; arg = 3; }
+    *reinterpret_cast<float2*>(dx + base) = make_float2(arg == 0 ? g : 0.0f, arg == 1 ? g : 0.0f);
+    *reinterpret_cast<float2*>(dx + base + p.W) = make_float2(arg == 2 ? g : 0.0f, arg == 3 ? g : 0.0f);
+  }
+}
+
+bool pool22(const PoolDesc& d, const void* a, const void* b) {
+  return d.kH == 2 && d.kW == 2 && d.sH == 2 && d.sW == 2 && d.pH == 0 && d.pW == 0 && d.H == 2 * d.Ho &&
+         d.W == 2 * d.Wo && ((uintptr_t)a & 7) == 0 && ((uintptr_t)b & 7) == 0;
+}
+
 Pool32 pool32(const PoolDesc& d) {
   Pool32 p{};
   p.H = (int)d.H; p.W = (int)d.W; p.Ho = (int)d.Ho; p.Wo = (int)d.Wo; p.kH = (int)d.kH; p.kW = (int)d.kW;
@@ -270,7 +320,8 @@ void max_pool(const float* x, float* y, const PoolDesc& p, hipStream_t st) {
   int64_t n = p.B * p.C * p.Ho * p.Wo;
   if (n <= 0) return;
   if (pool_small(p)) {
-    klaunch(k_max_pool32, grid_for(n), 256, 0, st, x, y, pool32(p));
+    if (pool22(p, x, x)) klaunch(k_max_pool22, grid_for(n), 256, 0, st, x, y, pool32(p));
+    else klaunch(k_max_pool32, grid_for(n), 256, 0, st, x, y, pool32(p));
     return;
   }
   klaunch(k_max_pool, grid_for(n), 256, 0, st, x, y, p);
@@ -282,7 +333,8 @@ void max_pool_grad(const float* x, const float* dy, float* dx, const PoolDesc& p
   const bool tiled = p.sH == p.kH && p.sW == p.kW && p.pH == 0 && p.pW == 0 && p.H == p.Ho * p.sH &&
                      p.W == p.Wo * p.sW;
   if (tiled && pool_small(p)) {
-    klaunch(k_max_pool_grad_tiled, grid_for(p.B * p.C * p.Ho * p.Wo), 256, 0, st, x, dy, dx, pool32(p));
+    if (pool22(p, x, dx)) klaunch(k_max_pool22_grad, grid_for(p.B * p.C * p.Ho * p.Wo), 256, 0, st, x, dy, dx, pool32(p));
+    else klaunch(k_max_pool_grad_tiled, grid_for(p.B * p.C * p.Ho * p.Wo), 256, 0, st, x, dy, dx, pool32(p));
     return;
   }
   klaunch(k_max_pool_grad, grid_for(n), 256, 0, st, x, dy, dx, p);

@@ -173,24 +173,33 @@ __global__ __launch_bounds__(kCT) void k_conv_gemm(ConvGemmArgs c) {
   }
 }
 
-// dW = sum of the split partials, deterministic. Many outputs: one thread per output
-// adds the splits in split order, 8 loads in flight. Few outputs and many splits (small
-// weights reducing over a large batch): one wavefront per output, lane l adding splits
-// l, l + 64, ... in order, then a fixed butterfly across the lanes.
-__global__ void k_conv_wgrad_reduce(const float* __restrict__ work, int splits, int64_t per_split,
-                                    float* __restrict__ dw) {
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < per_split; i += (int64_t)gridDim.x * blockDim.x) {
-    float s = 0.0f;
-    for (int sp0 = 0; sp0 < splits; sp0 += 8) {
-      float v[8];
+// dW = sum of the split partials, deterministic. Many outputs: a block of four wavefronts
+// takes 64 consecutive outputs (coalesced), wavefront w adds splits w, w + 4, ... in order
+// (8 loads in flight, clamped to split 0 past the end), and the four sums are added in
+// order through LDS. Few outputs and many splits (small weights reducing over a large
+// batch): one wavefront per output, lane l adding splits l, l + 64, ... in order, then a
+// fixed butterfly across the lanes.
+__global__ __launch_bounds__(256) void k_conv_wgrad_reduce(const float* __restrict__ work, int splits,
+                                                           int64_t per_split, float* __restrict__ dw) {
+  __shared__ float ws[4][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t i = (int64_t)blockIdx.x * 64 + lane;
+  const int64_t ii = i < per_split ? i : per_split - 1;
+  float s = 0.0f;
+  for (int sp0 = w; sp0 < splits; sp0 += 4 * 8) {
+    float v[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) v[u] = sp0 + u < splits ? work[(sp0 + u) * per_split + i] : 0.0f;
-#pragma unroll
-      for (int u = 0; u < 8; ++u)
-        if (sp0 + u < splits) s += v[u];
+    for (int u = 0; u < 8; ++u) {
+      const int sp = sp0 + 4 * u;
+      v[u] = work[(int64_t)(sp < splits ? sp : 0) * per_split + ii];
     }
-    dw[i] = s;
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (sp0 + 4 * u < splits) s += v[u];
   }
+  ws[w][lane] = s;
+  __syncthreads();
+  if (w == 0 && i < per_split) dw[i] = ((ws[0][lane] + ws[1][lane]) + ws[2][lane]) + ws[3][lane];
 }
 
 __global__ __launch_bounds__(256) void k_conv_wgrad_reduce_wave(const float* __restrict__ work, int splits,
@@ -441,8 +450,7 @@ void conv2d_weight_grad_gemm(const float* x, const float* dy, float* dw, const C
     if (per < 16384 && ngroups > 16) {
       klaunch(k_conv_wgrad_reduce_wave, (unsigned)((per + 3) / 4), 256, 0, st, work, (int)ngroups, per, dw);
     } else {
-      const int64_t nb = std::min<int64_t>((per + 255) / 256, 4096);
-      klaunch(k_conv_wgrad_reduce, (int)nb, 256, 0, st, work, (int)ngroups, per, dw);
+      klaunch(k_conv_wgrad_reduce, (unsigned)((per + 63) / 64), 256, 0, st, work, (int)ngroups, per, dw);
     }
     return;
   }
@@ -454,8 +462,7 @@ void conv2d_weight_grad_gemm(const float* x, const float* dy, float* dw, const C
     if (per < 16384 && p.splits > 16) {
       klaunch(k_conv_wgrad_reduce_wave, (unsigned)((per + 3) / 4), 256, 0, st, work, p.splits, per, dw);
     } else {
-      const int64_t nb = std::min<int64_t>((per + 255) / 256, 4096);
-      klaunch(k_conv_wgrad_reduce, (int)nb, 256, 0, st, work, p.splits, per, dw);
+      klaunch(k_conv_wgrad_reduce, (unsigned)((per + 63) / 64), 256, 0, st, work, p.splits, per, dw);
     }
   }
 }
