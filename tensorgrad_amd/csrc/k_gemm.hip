@@ -282,7 +282,7 @@ struct Plan { int bm, bn, bk, splits; int64_t kps; };
 
 constexpr int64_t kShortK = 1024;
 
-Plan plan_for(const GemmDesc& d, bool mid_split = true) {
+Plan plan_for(const GemmDesc& d) {
   auto tiles = [&](int bm, int bn) { return ((d.M + bm - 1) / bm) * ((d.N + bn - 1) / bn) * d.batch; };
   // Tile shape: least padded work per CU, counted as (rounds of 256 tiles) x tile area, so
   // an M or N below the tile edge does not pay for MFMAs on padding; ties go to the larger
@@ -299,13 +299,9 @@ Plan plan_for(const GemmDesc& d, bool mid_split = true) {
   // 128), so two blocks share a CU and one's operand loads overlap the other's MFMAs (long
   // K keeps the deeper 64-k ring).
   if (p.bm == 64 && p.bn == 64 && t >= 512 && d.K <= kShortK) p.bk = 32;
-  // Split K where few tiles meet a long K (at least 256 k per split), or, for products of
-  // 2^24 multiply-adds or more, a K of 256 to 1023 (at least 128 k per split): the split's
-  // reduction launch costs less than the idle CUs.
-  const bool mid_k = mid_split && d.K >= 256 && d.K < 1024 && d.M * d.N * d.K * d.batch >= (int64_t(1) << 24);
-  if (t < 128 && (d.K >= 1024 || mid_k)) {
+  if (t < 128 && d.K >= 1024) {
     int64_t want = (256 + t - 1) / t;
-    int64_t maxs = d.K / (mid_k ? 128 : 256);
+    int64_t maxs = d.K / 256;
     int64_t s = want < maxs ? want : maxs;
     if (s > 64) s = 64;
     if (s > 1) {
@@ -740,7 +736,7 @@ bool gemm_sum_ok(const GemmDesc* ds, int n) {
   }
   GemmDesc all = d0;
   all.K = d0.K * n;
-  const Plan p = plan_for(all, false);   // one launch over the products, no split
+  const Plan p = plan_for(all);
   if (p.splits != 1 || p.bk != 32 && p.bk != 64 || d0.K % p.bk != 0) return false;
   if (!(p.bm == 64 && p.bn == 64) && !(p.bm == 128 && p.bn == 128)) return false;
   const bool ak = d0.sAk == 1;
@@ -754,7 +750,7 @@ void gemm_sum(const GemmDesc* ds, int n, hipStream_t st) {
   if (!gemm_sum_ok(ds, n)) throw std::runtime_error("gemm_sum: unsupported operands");
   GemmDesc all = ds[0];
   all.K = ds[0].K * n;
-  const Plan p = plan_for(all, false);
+  const Plan p = plan_for(all);
   GemmArgs g{all, all.K, 1, 0, 0, nullptr, 0, 0};
   g.tiles_n = (int)((all.N + p.bn - 1) / p.bn);
   g.tiles_m = (int)((all.M + p.bm - 1) / p.bm);
