@@ -113,6 +113,57 @@ def measure(key, steps, warmup, profile_iters=5, optimizer=None, label=None):
     }
 
 
+def kernel_events(key, iters=20, warmup=20):
+    """Markdown report of one config's kernel durations from their own start / end events
+    (tg_profile_kernels, `iters` eager steps after `warmup` graph replays): every launch
+    node with its work and rate, then the per-family figures exactly as the bench line's
+    `roofline`, `roofline_mfma_all` and `roofline_non_gemm` compute them."""
+    from tensorgrad_amd import backend, configs
+    from tensorgrad_amd.build_ir import build_training_ir
+    cfg = configs.CONFIGS[key]
+    ir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer)
+    rt = backend.NativeRuntime(ir.wire_json())
+    rt.upload_params(ir.initial_params(configs.INIT_SEED))
+    for i, b in enumerate(configs.batches(cfg, RING)):
+        rt.stage_batch(i, b)
+    for i in range(warmup):
+        rt.step_staged(i % RING)
+    replay_ms = rt.time_replays(200) / 200
+    nodes = rt.describe()['nodes']
+    kms = rt.profile_kernels(iters)
+    rt.destroy()
+    fam = family_rates(nodes, kms)
+    o = [f'# Kernel durations by launch events: {cfg.title}', '',
+         f'Command: `python3 bench.py --config {key} --kernel-events`', '',
+         f'Every kernel of {iters} eager steps (after {warmup} graph replays) dispatched with start / end events of '
+         'its own on the runtime\'s stream (tg_profile_kernels); a node\'s time is the mean over the steps of the sum '
+         'of its kernels\' durations, without the gaps between launches. These are the durations the bench line\'s '
+         f'rooflines use. Sum per step: {1e3 * sum(kms):.1f} us over {len(nodes)} launch nodes; the graph replay of '
+         f'the whole step takes {1e3 * replay_ms:.1f} us.', '',
+         '| # | kind | shape | us | algorithmic work | rate |', '|---:|---|---|---:|---:|---:|']
+    for i, (n, t) in enumerate(zip(nodes, kms)):
+        if n['kind'] in ('gemm', 'conv', 'attention'):
+            work = f"{n['flops'] / 1e9:.3f} GFLOP"
+            rate = f"{n['flops'] / max(t, 1e-12) / 1e9:.1f} TFLOP/s"
+        else:
+            work = f"{n['bytes'] / 1e6:.2f} MB"
+            rate = f"{n['bytes'] / max(t, 1e-12) / 1e6:.0f} GB/s"
+        o.append(f"| {i} | {n['kind']} | {n['shape'][:60]} | {1e3 * t:.2f} | {work} | {rate} |")
+    o += ['', '| family | launches | us / step | work / step | rate | of peak |', '|---|---:|---:|---:|---:|---:|']
+    for name in ('gemm', 'attention', 'conv'):
+        f = fam[name]
+        if f['launches']:
+            o.append(f"| {name} (f32 MFMA) | {f['launches']} | {1e3 * f['ms']:.1f} | {f['flop_per_step'] / 1e9:.3f} GFLOP | "
+                     f"{f['tflops']:.1f} TFLOP/s | {100 * f['frac_f32_peak']:.1f} % |")
+    m = fam['mfma_all']
+    o.append(f"| all MFMA work | | {1e3 * m['ms']:.1f} | {m['flop_per_step'] / 1e9:.3f} GFLOP | {m['tflops']:.1f} TFLOP/s | "
+             f"{100 * m['frac_f32_peak']:.1f} % |")
+    ng = fam['non_gemm']
+    o.append(f"| other launches (HBM) | {ng['launches']} | {1e3 * ng['ms']:.1f} | {ng['bytes_per_step'] / 1e6:.1f} MB | "
+             f"{ng['gbs']:.0f} GB/s | {100 * ng['frac_hbm_peak']:.1f} % |")
+    return '\n'.join(o) + '\n'
+
+
 def copy_probe(n=16 << 20, reps=3):
     """Run a plain streaming copy of known size (y = x * 1.0 over n f32, one fused
     launch reading 4n bytes and writing 4n bytes) so that profiler byte counters can be
@@ -328,7 +379,12 @@ def main():
                     help='only compare every single-GEMM node of --config with the vendor BLAS, then exit')
     ap.add_argument('--probe-copy', action='store_true',
                     help='first run a 64 MiB streaming copy (profiler counter calibration)')
+    ap.add_argument('--kernel-events', action='store_true',
+                    help='only print a markdown report of --config\'s per-launch kernel durations (events), then exit')
     args = ap.parse_args()
+    if args.kernel_events:
+        print(kernel_events(args.config), end='', flush=True)
+        return
     if args.cpu_protocol:
         print(json.dumps(cpu_protocol()), flush=True)
         return
