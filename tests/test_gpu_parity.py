@@ -145,9 +145,11 @@ def test_recomputed_values_are_bit_identical():
 def test_embedding_gradient_beside_column_sums(key):
     """The embedding gradient, which only Adam reads, runs in the first blocks of the
     launch of the deferred column sums (bias and LayerNorm gradients), by the same block
-    body as its own launch with eight wavefronts instead of four: two full-size training
-    steps give the same parameters bit for bit with it in its own launch
-    (TG_COLSUM_SCATTER=0) and beside the sums."""
+    body as its own launch with eight wavefronts instead of four, its rows split into
+    windows whose f64 partial sums are added in window order (C2: 9 windows, C5: 3). The
+    f64 sums differ from the single pass's only in their last bits, far below one f32 ulp:
+    two full-size training steps give the same parameters bit for bit with the gradient in
+    its own launch (TG_COLSUM_SCATTER=0) and beside the sums."""
     cfg = configs.CONFIGS[key]
     ir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer)
     p0 = ir.initial_params(5)
