@@ -179,6 +179,49 @@ def test_embedding_gradient_beside_column_sums(key):
         assert np.array_equal(out['0'][n].view(np.uint32), out['1'][n].view(np.uint32)), n
 
 
+@pytest.mark.parametrize('V,N,rows', [(7, 24, 5001), (65, 300, 3001), (5, 600, 2501), (3, 8, 700)])
+def test_windowed_embedding_gradient(V, N, rows):
+    """The embedding gradient inside the column-sum launch at sizes where its rows split
+    into windows of unequal length (rows not a multiple of the window count), rows wider
+    than a quarter of the block (one load per listed row and column) and wider than the
+    block (two column blocks per token), and a table smaller than a window: one SGD step
+    with lr = 2^24 from zero parameters (the update is -lr * gradient) against the sum
+    np.add.at forms in f64, rounded once. The row sums are f64 in row order within a window
+    and the windows' partials added in order, so every element is within one f32 ulp."""
+    from tensorgrad_amd import nn as tnn
+    from tensorgrad_amd import ops as O
+    from tensorgrad_amd.module import Module
+
+    class Emb(Module):
+        def __init__(self):
+            self.emb = tnn.Embedding(V, N)
+            self.b = self.param([N])
+
+    def loss(p, inp):
+        e = O.add(p.emb.fwd(inp['i']), p.b)
+        return O.sum_(O.mul(e, inp['g']))
+
+    inputs = {'i': {'shape': [rows], 'dtype': 'i32'}, 'g': [rows, N]}
+    ir = build_training_ir(Emb(), loss, inputs, {'kind': 'sgd', 'lr': float(2 ** 24)})
+    nodes = backend.plan(ir.wire_json())['nodes']
+    assert any('+ scatter' in n['shape'] for n in nodes), [n['shape'] for n in nodes]
+    rng = np.random.default_rng(V * 1000 + N)
+    idx = rng.integers(0, V, size=rows).astype(np.int32)
+    g = rng.uniform(-1, 1, size=(rows, N)).astype(np.float32)
+    rt = backend.NativeRuntime(ir.wire_json())
+    rt.upload_params({n: np.zeros_like(np.asarray(v, np.float32)) for n, v in ir.initial_params(0).items()})
+    rt.step({'i': idx, 'g': g})
+    got = rt.download_params()
+    rt.destroy()
+    want = np.zeros((V, N), np.float64)
+    np.add.at(want, idx, g.astype(np.float64))
+    emb = [n for n in ir.param_names if n.startswith('emb')][0]
+    upd = -got[emb].astype(np.float64).reshape(V, N) / 2 ** 24
+    w32 = want.astype(np.float32).astype(np.float64)
+    ulp = np.spacing(np.abs(want).astype(np.float32)).astype(np.float64)
+    assert np.all(np.abs(upd - w32) <= ulp), float(np.max(np.abs(upd - w32) / np.maximum(ulp, 1e-45)))
+
+
 @pytest.mark.parametrize('key', ['mlp_sin', 'char_mlp', 'cnn', 'transformer'])
 def test_loss_mean_beside_column_sums(key):
     """The loss mean runs as a one-column sum in the deferred column-sum launch: f64 sums
