@@ -8,7 +8,10 @@
 // with Q, K, V and S / Pd tiles resident in LDS. P and Pd are written out (the backward
 // pass reads them); S and S2 never reach memory. A block of query rows [i0, i0 + 32) reads,
 // multiplies and normalises only keys [0, i0 + 32): the causal mask zeroes the rest, and
-// P / Pd store exact zeros there. Built with -ffp-contract=off.
+// P / Pd store exact zeros there. These kernels take dh = 64 with T = 64 or 128; smaller
+// heads (T <= 64, dh <= 64: the reference's sample transformers run T = 8 and 16 with
+// dh = 16) take a one-workgroup-per-head pair, k_attn_small_fwd / _bwd, at the end of the
+// file. Built with -ffp-contract=off.
 #include "kernels.h"
 
 namespace tgk {
@@ -540,11 +543,166 @@ __global__ __launch_bounds__(kNT) void k_attn_bwd_b(const AttnBwdDesc a) {
   }
 }
 
+// ---- small heads: T <= 64 and dh <= 64 ------------------------------------------------
+// One workgroup per (batch, head) holds Q, K, V (and dO) and the T x T rows in LDS. Every
+// product accumulates in f64 in increasing k, the evaluator's order (an f32 x f32
+// product is exact in f64), and rounds once to f32; entries past the diagonal, which
+// the causal mask makes zero, are skipped. The softmax, dropout and softmax-backward row
+// arithmetic is the kernels' above, one wavefront per row (a row fits one wavefront).
+constexpr int kNTS = 256;
+constexpr int kDHM = 64;        // largest head size
+constexpr int kLDH = kDHM + 1;  // Q / K / V / dO rows in LDS
+
+bool big_heads(int64_t T, int64_t dh) { return dh == kDH && (T == 64 || T == 128); }
+
+template <int TM>
+__global__ __launch_bounds__(kNTS) void k_attn_small_fwd(const AttnDesc a) {
+  constexpr int LS = TM + 1;
+  __shared__ float Qs[TM * kLDH], Ks[TM * kLDH], Vs[TM * kLDH];
+  __shared__ float Ss[TM * LS];   // S2, then Pd
+  const int T = a.T, dh = a.dh;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int bh = blockIdx.x, b = bh / a.H, hd = bh % a.H;
+  {
+    const float* q = a.q + b * a.sqb + hd * a.sqh;
+    const float* k = a.k + b * a.skb + hd * a.skh;
+    const float* v = a.v + b * a.svb + hd * a.svh;
+    for (int e = tid; e < T * dh; e += kNTS) {
+      const int i = e / dh, d = e % dh;
+      Qs[i * kLDH + d] = q[(int64_t)i * a.sqi + d];
+      Ks[i * kLDH + d] = k[(int64_t)i * a.skj + d];
+      Vs[i * kLDH + d] = v[(int64_t)i * a.svj + d];
+    }
+  }
+  __syncthreads();
+  for (int e = tid; e < T * T; e += kNTS) {
+    const int i = e / T, j = e % T;
+    if (j > i) continue;
+    double s = 0.0;
+    for (int d = 0; d < dh; ++d) s += (double)Qs[i * kLDH + d] * (double)Ks[j * kLDH + d];
+    const unsigned x = fbits((float)s);
+    Ss[i * LS + j] = a.has_scale ? bitsf(op_eval(FO_MULS, x, 0u, DT_F32, DT_F32, DT_F32, a.scale, 0.0, 0u, 0u, 0u)) : bitsf(x);
+  }
+  __syncthreads();
+  const unsigned seed = a.seed ? (unsigned)*a.seed : 0u;
+  for (int i = wave; i < T; i += kNTS / 64) {
+    const int j = lane;
+    const bool on = j <= i;
+    const float x = on ? Ss[i * LS + j] : 0.0f;
+    const float mx = wave_allmax(on ? x : bitsf(0xff800000u));
+    const float ex = on ? expf(x - mx) : 0.0f;
+    const double rs = 1.0 / wave_allsum((double)ex);
+    const int64_t rflat = (int64_t)bh * T + i;
+    unsigned pv = 0u, dv = 0u;
+    if (on) {
+      pv = fbits((float)((double)ex * rs));
+      dv = a.has_dropout ? dropout_bits(pv, seed, a.salt, a.drop_p, a.drop_scale, (unsigned)(rflat * T + j)) : pv;
+    }
+    if (j < T) {
+      reinterpret_cast<unsigned*>(a.p)[rflat * T + j] = pv;
+      if (a.pd) reinterpret_cast<unsigned*>(a.pd)[rflat * T + j] = dv;
+      Ss[i * LS + j] = bitsf(dv);
+    }
+  }
+  __syncthreads();
+  float* o = a.o + b * a.sob + hd * a.soh;
+  for (int e = tid; e < T * dh; e += kNTS) {
+    const int i = e / dh, d = e % dh;
+    double s = 0.0;
+    for (int j = 0; j <= i; ++j) s += (double)Ss[i * LS + j] * (double)Vs[j * kLDH + d];
+    o[(int64_t)i * a.soi + d] = (float)s;
+  }
+}
+
+template <int TM>
+__global__ __launch_bounds__(kNTS) void k_attn_small_bwd(const AttnBwdDesc a) {
+  constexpr int LS = TM + 1;
+  __shared__ float Qs[TM * kLDH], Ks[TM * kLDH], Vs[TM * kLDH], Os[TM * kLDH];   // Os: dO
+  __shared__ float Ps[TM * LS], Ds[TM * LS], Ss[TM * LS];                         // P, Pd, dPd then dS
+  const int T = a.T, dh = a.dh;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int bh = blockIdx.x, b = bh / a.H, hd = bh % a.H;
+  const int64_t prow = (int64_t)bh * T * T;
+  {
+    const float* q = a.q + b * a.sqb + hd * a.sqh;
+    const float* k = a.k + b * a.skb + hd * a.skh;
+    const float* v = a.v + b * a.svb + hd * a.svh;
+    const float* g = a.dout + b * a.sob + hd * a.soh;
+    for (int e = tid; e < T * dh; e += kNTS) {
+      const int i = e / dh, d = e % dh;
+      Qs[i * kLDH + d] = q[(int64_t)i * a.sqi + d];
+      Ks[i * kLDH + d] = k[(int64_t)i * a.skj + d];
+      Vs[i * kLDH + d] = v[(int64_t)i * a.svj + d];
+      Os[i * kLDH + d] = g[(int64_t)i * a.soi + d];
+    }
+    for (int e = tid; e < T * T; e += kNTS) {
+      const int i = e / T, j = e % T;
+      Ps[i * LS + j] = a.p[prow + e];
+      Ds[i * LS + j] = a.pd[prow + e];
+    }
+  }
+  __syncthreads();
+  for (int e = tid; e < T * T; e += kNTS) {
+    const int i = e / T, j = e % T;
+    if (j > i) continue;
+    double s = 0.0;
+    for (int d = 0; d < dh; ++d) s += (double)Os[i * kLDH + d] * (double)Vs[j * kLDH + d];
+    Ss[i * LS + j] = (float)s;
+  }
+  __syncthreads();
+  // dS rows: v0 = dropout(dPd), s = f32(rowsum f32(v0 * P)) (f64 sum),
+  // dS = f32((v0 - s) * P) [* scale]; zero past the diagonal
+  for (int i = wave; i < T; i += kNTS / 64) {
+    const int j = lane;
+    const bool on = j <= i;
+    unsigned v0 = 0u;
+    double sum = 0.0;
+    if (on) {
+      const unsigned x = fbits(Ss[i * LS + j]);
+      v0 = a.has_dropout ? fbits((float)((double)bitsf(x) * (fbits(Ds[i * LS + j]) != 0u ? a.drop_scale : 0.0))) : x;
+      sum = (double)(bitsf(v0) * Ps[i * LS + j]);
+    }
+    const float sf = (float)(wave_allsum(sum) / 1.0);
+    unsigned dsv = 0u;
+    if (on) {
+      const unsigned t = fbits((bitsf(v0) - sf) * Ps[i * LS + j]);
+      dsv = a.has_scale ? op_eval(FO_MULS, t, 0u, DT_F32, DT_F32, DT_F32, a.scale, 0.0, 0u, 0u, 0u) : t;
+    }
+    if (j < T) {
+      Ss[i * LS + j] = bitsf(dsv);
+      reinterpret_cast<unsigned*>(a.ds)[prow + (int64_t)i * T + j] = dsv;
+    }
+  }
+  __syncthreads();
+  float* dq = a.dq + b * a.sdqb + hd * a.sdqh;
+  float* dk = a.dk + b * a.sdkb + hd * a.sdkh;
+  float* dv = a.dv + b * a.sdvb + hd * a.sdvh;
+  for (int e = tid; e < T * dh; e += kNTS) {
+    const int r = e / dh, d = e % dh;
+    double sq = 0.0, sk = 0.0, sv = 0.0;
+    for (int j = 0; j <= r; ++j) sq += (double)Ss[r * LS + j] * (double)Ks[j * kLDH + d];       // dQ = dS K
+    for (int i = r; i < T; ++i) {
+      sk += (double)Ss[i * LS + r] * (double)Qs[i * kLDH + d];                                   // dK = dS^T Q
+      sv += (double)Ds[i * LS + r] * (double)Os[i * kLDH + d];                                   // dV = Pd^T dO
+    }
+    dq[(int64_t)r * a.sdqi + d] = (float)sq;
+    dk[(int64_t)r * a.sdkj + (int64_t)d * a.sdkd] = (float)sk;
+    dv[(int64_t)r * a.sdvj + d] = (float)sv;
+  }
+}
+
 }  // namespace
 
-bool attention_supported(int64_t T, int64_t dh) { return dh == kDH && (T == 64 || T == 128); }
+bool attention_supported(int64_t T, int64_t dh) { return big_heads(T, dh) || (T >= 1 && T <= 64 && dh >= 1 && dh <= kDHM); }
 
 void attention_fwd(const AttnDesc& a, hipStream_t st) {
+  if (!big_heads(a.T, a.dh)) {
+    const int blocks = a.B * a.H;
+    if (blocks <= 0) return;
+    if (a.T <= 32) klaunch(k_attn_small_fwd<32>, blocks, kNTS, 0, st, a);
+    else klaunch(k_attn_small_fwd<64>, blocks, kNTS, 0, st, a);
+    return;
+  }
   const int blocks = a.B * a.H * (a.T / kQBF);
   if (blocks <= 0) return;
   if (a.T == 128) klaunch(k_attn_fwd<128>, blocks, kNT, 0, st, a);
@@ -552,6 +710,13 @@ void attention_fwd(const AttnDesc& a, hipStream_t st) {
 }
 
 void attention_bwd(const AttnBwdDesc& a, hipStream_t st) {
+  if (!big_heads(a.T, a.dh)) {
+    const int blocks = a.B * a.H;
+    if (blocks <= 0) return;
+    if (a.T <= 32) klaunch(k_attn_small_bwd<32>, blocks, kNTS, 0, st, a);
+    else klaunch(k_attn_small_bwd<64>, blocks, kNTS, 0, st, a);
+    return;
+  }
   const int blocks = a.B * a.H * (a.T / kQB);
   if (blocks <= 0) return;
   const int blocks_a = a.B * a.H * (a.T / kQBF);

@@ -226,7 +226,8 @@ void softmax_causal(const float* a, float* out, int64_t mats, int64_t D, hipStre
 // Per (b, h): O = dropout(causal_softmax(f32(Q K^T * scale))) V, writing P (the softmax)
 // and Pd (after dropout; null without dropout) as [B, H, T, T] contiguous. Q, V, O are
 // [B, H, T, dh] and K [B, H, T, dh] (read as K^T) with unit stride along dh and the
-// given element strides; all 16-byte aligned.
+// given element strides; all 16-byte aligned. Supported: dh = 64 with T = 64 or 128, and
+// any T <= 64 with dh <= 64 (attention_supported).
 struct AttnDesc {
   int B, H, T, dh;
   const float* q;

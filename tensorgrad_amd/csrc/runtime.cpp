@@ -2330,9 +2330,11 @@ void Runtime::match_attention() {
     if (!tgk::attention_supported(T, dh)) continue;
     if (vk.dims != Dims({B, H, dh, T}) || vv.dims != Dims({B, H, T, dh}) || vo.dims != Dims({B, H, T, dh})) continue;
     if (vq.strides[3] != 1 || vk.strides[2] != 1 || vv.strides[3] != 1 || vo.strides[3] != 1) continue;
+    // 16-byte aligned rows (the stride of a size-1 dimension never moves the address)
+    auto al4 = [](const View& w, int d) { return w.dims[d] == 1 || w.strides[d] % 4 == 0; };
     bool al = true;
-    for (int d = 0; d < 3; ++d) al = al && vq.strides[d] % 4 == 0 && vv.strides[d] % 4 == 0;
-    al = al && vk.strides[0] % 4 == 0 && vk.strides[1] % 4 == 0 && vk.strides[3] % 4 == 0;
+    for (int d = 0; d < 3; ++d) al = al && al4(vq, d) && al4(vv, d);
+    al = al && al4(vk, 0) && al4(vk, 1) && al4(vk, 3);
     if (!al) continue;
     if (view_[P].root != P || !view_[P].contiguous() || view_[Pd].root != Pd || !view_[Pd].contiguous()) continue;
     auto ready = [&](int t) {   // data of t exists before op i runs
@@ -2608,13 +2610,15 @@ void Runtime::match_attention_bwd() {
   };
   auto out_of = [&](int op) { return O(op).at("out").i32(); };
   auto only = [&](int t) { return consumers_[t].size() == 1 ? consumers_[t][0] : -1; };
-  // v is a transpose (last two dims) of u, over the same storage
+  // v is a transpose (last two dims) of u, over the same storage (strides of size-1
+  // dimensions do not matter)
   auto transposed = [&](int v, int u) {
     const View &a = view_[v], &b = view_[u];
     if (a.root != b.root || a.dims.size() != 4 || b.dims.size() != 4) return false;
-    return a.dims[0] == b.dims[0] && a.dims[1] == b.dims[1] && a.dims[2] == b.dims[3] && a.dims[3] == b.dims[2] &&
-           a.strides[0] == b.strides[0] && a.strides[1] == b.strides[1] && a.strides[2] == b.strides[3] &&
-           a.strides[3] == b.strides[2];
+    static const int perm[4] = {0, 1, 3, 2};
+    for (int d = 0; d < 4; ++d)
+      if (a.dims[d] != b.dims[perm[d]] || (a.dims[d] != 1 && a.strides[d] != b.strides[perm[d]])) return false;
+    return true;
   };
   auto is_mul_of = [&](int op, int x, int y) {   // op = x * y (either order), f32
     if (op < 0 || kinds_[op] != "mul") return false;
@@ -2635,8 +2639,8 @@ void Runtime::match_attention_bwd() {
     }
     if (bw.dpd < 0) continue;
     const View& vo = view_[dO];
-    if (vo.dims != view_[v].dims || vo.strides[3] != 1 || vo.strides[0] % 4 || vo.strides[1] % 4 || vo.strides[2] % 4)
-      continue;
+    auto al4 = [](const View& w, int d) { return w.dims[d] == 1 || w.strides[d] % 4 == 0; };
+    if (vo.dims != view_[v].dims || vo.strides[3] != 1 || !al4(vo, 0) || !al4(vo, 1) || !al4(vo, 2)) continue;
     std::vector<int> chain{bw.dpd};
     int dP = out_of(bw.dpd);
     if (pinned(dP)) continue;

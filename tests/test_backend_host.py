@@ -138,6 +138,23 @@ def test_plan_forward_graph_and_small_variants():
     assert not any(n['kind'] == 'adam_multi' for n in p['nodes'])
 
 
+@pytest.mark.parametrize('vocab,seq,d,layers', [(12, 8, 64, 3), (27, 16, 64, 2), (65, 128, 256, 4)])
+def test_attention_fuses_at_the_reference_samples_shapes(vocab, seq, d, layers):
+    """Every attention of a training step lowers to one fused forward and one fused
+    backward node: the reference's addition transformer (samples/transformer/spec.ts:12-19:
+    T = 8, 4 heads of 16) and Pokeformer (samples/pokeformer/spec.ts:20-25: T = 16, 4
+    heads of 16) take the small-head kernels, C5 (T = 128, heads of 64) the matrix-core
+    ones."""
+    ir = build_training_ir(configs.Transformer(vocab=vocab, seq=seq, d=d, n_layers=layers, hidden=4 * d),
+                           configs.transformer_loss,
+                           {'tokens': {'shape': [4, seq], 'dtype': 'i32'}, 'targets': {'shape': [4, seq], 'dtype': 'i32'}},
+                           {'kind': 'adamw', 'lr': 1e-3, 'weightDecay': 0.01})
+    nodes = backend.plan(ir.wire_json())['nodes']
+    fwd = [n for n in nodes if n['kind'] == 'attention' and not n['shape'].endswith('backward')]
+    bwd = [n for n in nodes if n['kind'] == 'attention' and n['shape'].endswith('backward')]
+    assert len(fwd) == layers and len(bwd) == layers, [n['shape'] for n in nodes if n['kind'] == 'attention']
+
+
 def test_malformed_ir_is_rejected_with_a_message():
     with pytest.raises(backend.BackendError) as e:
         backend.plan('{"graph": ')

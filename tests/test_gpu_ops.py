@@ -359,15 +359,22 @@ def _run_native(g, inputs, env=None):
     return got, kinds
 
 
-@pytest.mark.parametrize('B,H,T', [(2, 3, 64), (2, 3, 128), (32, 4, 128)])
+# (B, H, T, dh): the matrix-core kernels (dh = 64, T = 64 / 128) and the one-workgroup-per-
+# head kernels for smaller heads, at the reference samples' shapes (T = 8 and 16 with
+# dh = 16), odd sizes, one token, and T = 64 with a head below 64
+ATTN_SHAPES = [(2, 3, 64, 64), (2, 3, 128, 64), (32, 4, 128, 64), (128, 4, 8, 16), (32, 4, 16, 16), (3, 2, 5, 12),
+               (2, 2, 1, 8), (2, 3, 32, 64), (2, 2, 64, 32), (1, 2, 48, 20)]
+
+
+@pytest.mark.parametrize('B,H,T,dh', ATTN_SHAPES)
 @pytest.mark.parametrize('what', ['o', 'p', 'pd'])
-def test_fused_attention(B, H, T, what):
+def test_fused_attention(B, H, T, dh, what):
     """The fused attention kernel (Q K^T, scale, causal softmax, dropout, P V in one
-    launch) against the oracle (GEMM tolerance: the products run on f32 matrix cores; the
-    softmax takes f32 exp with an f64 row sum), and against the unfused kernels (TG_ATTN=0)
-    within the same tolerance. P and Pd hold exact zeros past the diagonal and the same
-    dropout mask as the oracle (the reference's hash on the flat index)."""
-    dh = 64
+    launch) against the oracle (GEMM tolerance: the products run on f32 matrix cores, or
+    for small heads accumulate in f64 as the oracle does; the softmax takes f32 exp with
+    an f64 row sum), and against the unfused kernels (TG_ATTN=0) within the same
+    tolerance. P and Pd hold exact zeros past the diagonal and the same dropout mask as
+    the oracle (the reference's hash on the flat index)."""
     ins = {n: _rand([B, H, T, dh], s, -2, 2) for n, s in (('q', 61), ('k', 62), ('v', 63))}
     g = trace_fn(_attention_graph(B, H, T, dh, what))
     got, kinds = _run_native(g, ins)
@@ -418,12 +425,12 @@ def _attention_grad(B, H, T, dh, which, params, g_in, env=None):
     return got, ops, w
 
 
-@pytest.mark.parametrize('B,H,T', [(2, 3, 64), (2, 3, 128), (32, 4, 128)])
-def test_fused_attention_backward(B, H, T):
+@pytest.mark.parametrize('B,H,T,dh', ATTN_SHAPES)
+def test_fused_attention_backward(B, H, T, dh):
     """The fused attention backward (dPd = dO V^T, dropout and softmax backward row math,
-    dQ = dS K, dK = dS^T Q, dV = Pd^T dO in two launches) for the gradients of q, k and v,
-    against the oracle and the unfused kernels (TG_ATTN=0), GEMM tolerance."""
-    dh = 64
+    dQ = dS K, dK = dS^T Q, dV = Pd^T dO; two launches for dh = 64, one for small heads)
+    for the gradients of q, k and v, against the oracle and the unfused kernels
+    (TG_ATTN=0), GEMM tolerance."""
     params = {n: _rand([B, H, T, dh], s, -2, 2) for n, s in (('q', 71), ('k', 72), ('v', 73))}
     g_in = _rand([B, H, T, dh], 74)
     for which in ('q', 'k', 'v'):
