@@ -590,7 +590,7 @@ bool col_form(const Strided& cells, const Strided& red) {
 // when a sum reads the product of two arrays), each of its waves between 1 and 64 rows,
 // at most 256 chunks per sum. Sums of a batch then take block counts in proportion to
 // their size, and the blocks of one launch finish together.
-ColPlan col_plan(int64_t C, int64_t R, int terms) {
+ColPlan col_plan(int64_t C, int64_t R, int terms, int scale = 1) {
   ColPlan p;
   const int L = col_lanes(C);
   p.nx = (C + 64 * L - 1) / (64 * L);
@@ -600,6 +600,7 @@ ColPlan col_plan(int64_t C, int64_t R, int terms) {
   // Fewer columns than lanes (a loss mean, a small head's bias): most lanes idle, so a
   // chunk is one round of loads per wavefront and the work spreads over more blocks.
   if (C < 64) rows = kColWaves * kColRows;
+  rows *= std::max(scale, 1);
   int64_t n = (R + rows - 1) / rows;
   if (n > 256) n = 256;
   if (n < 1) n = 1;
@@ -671,8 +672,8 @@ int64_t sum_workspace_doubles(const Strided& cells, const Strided& red, int64_t 
 }
 
 ColSum colsum_desc(const float* a, const float* b, float* out, int64_t C, int64_t R, int64_t rs, double div,
-                   double* part, unsigned* counters) {
-  const ColPlan p = col_plan(C, R, b ? 2 : 1);
+                   double* part, unsigned* counters, int scale) {
+  const ColPlan p = col_plan(C, R, b ? 2 : 1, scale);
   ColSum c{};
   c.a = a; c.b = b; c.out = out;
   c.C = C; c.R = R; c.rs = rs; c.chunk = p.chunk;
@@ -727,14 +728,29 @@ int64_t scatter_counters(int64_t rows, int64_t V, int64_t N) {
   return scatter_windows(rows, V, N) > 1 ? V * ((N + kColThreads - 1) / kColThreads) : 0;
 }
 
-int64_t colsum_workspace_doubles(int64_t C, int64_t R, int terms) {
-  const ColPlan p = col_plan(C, R, terms);
+int64_t colsum_workspace_doubles(int64_t C, int64_t R, int terms, int scale) {
+  const ColPlan p = col_plan(C, R, terms, scale);
   return p.nchunks > 1 ? C * p.nchunks : 0;
 }
 
-int64_t colsum_counters(int64_t C, int64_t R, int terms) {
-  const ColPlan p = col_plan(C, R, terms);
+int64_t colsum_counters(int64_t C, int64_t R, int terms, int scale) {
+  const ColPlan p = col_plan(C, R, terms, scale);
   return p.nchunks > 1 ? p.nx : 0;
+}
+
+// A batch whose column sums would take more than four blocks per CU at the default chunk
+// length (C4's nine [65536, 256] bias sums: 2304 blocks) runs its chunks that many times
+// longer to come to about two blocks per CU: measured on C4's batch, 121 us at 2304 blocks,
+// 118 us at 1017, 96 us at 576 and 92 us at 288 (every block's LDS combine, partial store
+// and arrival count is paid once per chunk). Batches within four per CU keep the default:
+// C5's (about 800 blocks of [4096, C] sums) slows down with longer chunks.
+int colsum_batch_scale(const int64_t* C, const int64_t* R, const int* terms, int n) {
+  int64_t blocks = 0;
+  for (int i = 0; i < n; ++i) {
+    const ColPlan p = col_plan(C[i], R[i], terms[i]);
+    blocks += p.nx * p.nchunks;
+  }
+  return blocks <= 1024 ? 1 : (int)((blocks + 511) / 512);
 }
 
 void colsum_batch(const ColSumBatch& b, hipStream_t st) {
@@ -783,7 +799,7 @@ void reduce_sum(const float* a, float* out, const Strided& cells, const Strided&
   if (col_form(cells, red)) {
     ColSumBatch bt{};
     bt.n = 1;
-    bt.s[0] = colsum_desc(a, nullptr, out, ncells, nred, red.s0[0], div, work, counters);
+    bt.s[0] = colsum_desc(a, nullptr, out, ncells, nred, red.s0[0], div, work, counters, 1);
     colsum_batch(bt, st);
     return;
   }

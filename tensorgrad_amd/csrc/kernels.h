@@ -210,13 +210,16 @@ struct ColSumBatch {
   MidSum m[kMidSumMax];
 };
 static_assert(sizeof(ColSumBatch) <= 4096, "column-sum batch fits the kernel argument space");
+// `scale`: chunk-length multiple of the batch (colsum_batch_scale), the same at planning
+// (workspace, counters) and at binding
 ColSum colsum_desc(const float* a, const float* b, float* out, int64_t C, int64_t R, int64_t rs, double div,
-                   double* part, unsigned* counters);
-int64_t colsum_workspace_doubles(int64_t C, int64_t R, int terms);
+                   double* part, unsigned* counters, int scale);
+int64_t colsum_workspace_doubles(int64_t C, int64_t R, int terms, int scale = 1);
+int colsum_batch_scale(const int64_t* C, const int64_t* R, const int* terms, int n);
 MidSum midsum_desc(const float* a, float* out, int64_t B, int64_t C, int64_t L, double* part, unsigned* counters);
 int64_t midsum_workspace_doubles(int64_t B, int64_t C, int64_t L);
 int64_t midsum_counters(int64_t B, int64_t C, int64_t L);
-int64_t colsum_counters(int64_t C, int64_t R, int terms);
+int64_t colsum_counters(int64_t C, int64_t R, int terms, int scale = 1);
 void colsum_batch(const ColSumBatch& b, hipStream_t st);
 void row_argmax(const float* a, int32_t* out, int64_t outer, int64_t D, hipStream_t st);
 void log_softmax(const float* a, float* out, int64_t outer, int64_t D, hipStream_t st);

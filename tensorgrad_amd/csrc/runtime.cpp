@@ -2493,6 +2493,18 @@ void Runtime::emit_colsums(const std::vector<int>& batch, bool with_scatter, boo
   size_t ws = 0;
   std::vector<size_t> ws_off;
   std::vector<int64_t> cbase;
+  int cscale = 1;
+  {
+    std::vector<int64_t> cs, rs;
+    std::vector<int> ts;
+    for (int sop : batch) {
+      const ColSumOp& c = colsum_.at(sop);
+      cs.push_back(c.C);
+      rs.push_back(c.R);
+      ts.push_back(c.b >= 0 ? 2 : 1);
+    }
+    cscale = tgk::colsum_batch_scale(cs.data(), rs.data(), ts.data(), (int)batch.size());
+  }
   for (int sop : batch) {
     const ColSumOp& c = colsum_.at(sop);
     n.reads.push_back(root(c.a));
@@ -2503,8 +2515,8 @@ void Runtime::emit_colsums(const std::vector<int>& batch, bool with_scatter, boo
     n.detail += std::string(n.detail.empty() ? "" : ",") + (c.b >= 0 ? "mul,sum_to_shape" : "sum_to_shape");
     ws_off.push_back(ws);
     const int terms = c.b >= 0 ? 2 : 1;
-    ws += ((size_t)tgk::colsum_workspace_doubles(c.C, c.R, terms) * 8 + 255) & ~(size_t)255;
-    cbase.push_back(take_counters(tgk::colsum_counters(c.C, c.R, terms)));
+    ws += ((size_t)tgk::colsum_workspace_doubles(c.C, c.R, terms, cscale) * 8 + 255) & ~(size_t)255;
+    cbase.push_back(take_counters(tgk::colsum_counters(c.C, c.R, terms, cscale)));
   }
   const std::vector<DeferredRowSum> rsums = with_rowsums ? deferred_rowsum_ : std::vector<DeferredRowSum>{};
   std::vector<size_t> rws_off;
@@ -2574,7 +2586,7 @@ void Runtime::emit_colsums(const std::vector<int>& batch, bool with_scatter, boo
         throw Error(TG_INTERNAL, "column sum: operand smaller than its shape");
       double* part = reinterpret_cast<double*>(reinterpret_cast<char*>(cur_ws_) + ws_off[q]);
       bt.s[q] = tgk::colsum_desc((const float*)dptr(c.a), c.b >= 0 ? (const float*)dptr(c.b) : nullptr,
-                                 (float*)dptr(out), c.C, c.R, c.C, 1.0, part, cur_counters_ + cbase[q]);
+                                 (float*)dptr(out), c.C, c.R, c.C, 1.0, part, cur_counters_ + cbase[q], cscale);
     }
     for (size_t q = 0; q < mids.size(); ++q) {
       const DeferredMidSum& d = mids[q];
@@ -2590,7 +2602,7 @@ void Runtime::emit_colsums(const std::vector<int>& batch, bool with_scatter, boo
         throw Error(TG_INTERNAL, "loss sum: operand smaller than its shape");
       double* part = reinterpret_cast<double*>(reinterpret_cast<char*>(cur_ws_) + rws_off[q]);
       tgk::ColSum c = tgk::colsum_desc((const float*)dptr(d.a), nullptr, (float*)dptr(d.out), 1, d.R, 1, d.div, part,
-                                       cur_counters_ + rcbase[q]);
+                                       cur_counters_ + rcbase[q], 1);
       c.scale = d.scale;
       bt.s[bt.n++] = c;
     }
