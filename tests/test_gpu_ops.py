@@ -530,7 +530,13 @@ GEMMS = [([5, 7], [7, 3], False, False), ([2, 33, 65], [65, 17], False, False), 
          ([1024, 512], [1024, 27], True, False), ([128, 128], [128, 10], False, False),
          ([128, 10], [128, 10], False, True), ([128, 128], [128, 10], True, False),
          ([512, 96], [96, 100], False, False), ([333, 200], [200, 112], False, False),
-         ([300, 27], [27, 256], False, False), ([2048, 300], [2048, 65], True, False)]
+         ([300, 27], [27, 256], False, False), ([2048, 300], [2048, 65], True, False),
+         # short products (K <= 16, at least 64K outputs: the small-K kernel, also taking
+         # [4096, 4] x [4, 256] above): batched with a shared B, B transposed, 33 columns of
+         # a 256-column block, C4's head input gradient, K = 1 beyond the tiny kernel's size
+         ([3, 700, 13], [13, 300], False, False), ([5000, 9], [300, 9], False, True),
+         ([20000, 7], [7, 33], False, False), ([65536, 4], [4, 256], False, False),
+         ([3000, 1], [1, 1000], False, False), ([40, 50, 16], [40, 16, 70], False, False)]
 
 
 @pytest.mark.parametrize('case', GEMMS)
