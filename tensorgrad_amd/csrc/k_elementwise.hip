@@ -11,6 +11,7 @@
 
 #include <cmath>
 #include <cstring>
+#include <stdexcept>
 
 namespace tgk {
 namespace {
@@ -214,6 +215,39 @@ __global__ __launch_bounds__(256) void k_copy32(uint32_t* __restrict__ dst, cons
   }
 }
 
+// Output element t of a last-axis concatenation: row t / W, column c = t % W, taken from
+// the input whose column range holds c. Consecutive threads write consecutive elements, so
+// every output line is written whole by one launch.
+// Four elements per thread and round (t, t + S, t + 2S, t + 3S for the grid's stride S),
+// their loads issued before any store.
+__global__ __launch_bounds__(256) void k_concat_last(uint32_t* __restrict__ dst, const ConcatLast c, FastDiv fw,
+                                                     uint32_t total) {
+  const uint32_t S = gridDim.x * 256u;
+  for (uint32_t t0 = blockIdx.x * 256u + threadIdx.x; t0 < total; t0 += 4 * S) {
+    uint32_t v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const uint32_t t = min(t0 + u * S, total - 1);   // past the end: the last element again
+      const uint32_t r = fastdiv(t, fw), col = t - r * fw.d;
+      // the input holding column col: a uniform loop over the inputs with per-lane selects
+      // (an array index that differs between lanes would place c in scratch memory)
+      const uint32_t* sp = c.src[0];
+      uint32_t lo = 0, hi = c.off[1];
+#pragma unroll
+      for (int j = 1; j < kConcatMax; ++j) {
+        const bool in = j < c.n && col >= c.off[j];
+        sp = in ? c.src[j] : sp;
+        lo = in ? c.off[j] : lo;
+        hi = in ? c.off[j + 1] : hi;
+      }
+      v[u] = sp[r * (hi - lo) + (col - lo)];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (t0 + u * S < total) dst[t0 + u * S] = v[u];
+  }
+}
+
 __global__ void k_fill(uint32_t* __restrict__ dst, uint32_t bits, int64_t n) {
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
     dst[i] = bits;
@@ -335,6 +369,16 @@ void where_causal(const float* a, float* out, int64_t outer, int64_t D, double f
   int64_t total = outer * D * D;
   if (total <= 0) return;
   klaunch(k_where_causal, grid_for(total), kThreads, 0, st, a, out, total, D, (float)fill);
+}
+
+void concat_last(uint32_t* dst, const ConcatLast& c, int64_t rows, hipStream_t st) {
+  if (c.n < 1 || c.n > kConcatMax) throw std::runtime_error("concat: input count out of range");
+  const int64_t W = c.off[c.n], total = rows * W;
+  if (total <= 0) return;
+  if (total >= (int64_t(1) << 31)) throw std::runtime_error("concat: output too large for 32-bit indexing");
+  int64_t b = (total + 1023) / 1024;
+  if (b > 8192) b = 8192;
+  klaunch(k_concat_last, (int)b, 256, 0, st, dst, c, make_fastdiv((uint32_t)W), (uint32_t)total);
 }
 
 void strided_copy(void* dst, const void* src, const Strided& sp, int64_t n, hipStream_t st) {

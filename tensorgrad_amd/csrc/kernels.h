@@ -87,6 +87,15 @@ void where_causal(const float* a, float* out, int64_t outer, int64_t D, double f
 // dst[strided] = src[strided]: permute / broadcast_to / slice / concat / scatter.
 // Operand 0 = dst strides, operand 1 = src strides; both 4-byte elements.
 void strided_copy(void* dst, const void* src, const Strided& sp, int64_t n, hipStream_t st);
+// Concatenation along the last axis of n <= kConcatMax contiguous [rows, w_i] inputs into a
+// contiguous [rows, W] output (W = sum w_i), one launch writing the output in order.
+constexpr int kConcatMax = 8;
+struct ConcatLast {
+  int n;
+  const uint32_t* src[kConcatMax];
+  uint32_t off[kConcatMax + 1];   // first output column of input i; off[n] = W
+};
+void concat_last(uint32_t* dst, const ConcatLast& c, int64_t rows, hipStream_t st);
 void fill(void* dst, int dt, double value, int64_t n, hipStream_t st);
 void arange(void* dst, int dt, int64_t n, hipStream_t st);
 void one_hot(const int32_t* idx, int64_t rows, int64_t depth, void* out, int dt, hipStream_t st);

@@ -3537,6 +3537,30 @@ void Runtime::lower_op(int i) {
     for (int t : ins) total_in += T_[t].numel;
     n.bytes = 4.0 * (total_in + to.numel);
     int64_t start = k == "concat" ? 0 : op.at("start").i64();
+    // along the last axis: one launch writing the output rows in order
+    if (k == "concat" && ax == (int64_t)to.shape.size() - 1 && (int)ins.size() <= tgk::kConcatMax &&
+        to.numel < (int64_t(1) << 31)) {
+      n.bind = [=]() -> std::function<void(hipStream_t)> {
+        tgk::ConcatLast c{};
+        c.n = (int)ins.size();
+        int64_t w = 0;
+        const int64_t rows = to.shape.empty() || to.shape.back() == 0 ? 0 : to.numel / to.shape.back();
+        for (int i = 0; i < c.n; ++i) {
+          const Dims& is = T_[ins[i]].shape;
+          if (T_[root(ins[i])].numel < T_[ins[i]].numel || T_[ins[i]].numel != rows * is.back())
+            throw Error(TG_INTERNAL, "concat: input smaller than its shape");
+          c.src[i] = (const uint32_t*)dptr(ins[i]);
+          c.off[i] = (uint32_t)w;
+          w += is.back();
+        }
+        c.off[c.n] = (uint32_t)w;
+        if (w != to.shape.back() || T_[root(out)].numel < to.numel) throw Error(TG_INTERNAL, "concat: widths do not add up");
+        uint32_t* po = (uint32_t*)dptr(out);
+        return [=](hipStream_t st) { tgk::concat_last(po, c, rows, st); };
+      };
+      add_node(std::move(n));
+      return;
+    }
     n.bind = [=]() -> std::function<void(hipStream_t)> {
       std::vector<std::function<void(hipStream_t)>> parts;
       Dims os = contiguous_strides(to.shape);

@@ -234,6 +234,12 @@ def test_broadcast_permute_slice_concat_scatter():
     got, want = run_both(lambda: O.concat([tensor_input('x', [2, 3, 4]), tensor_input('y', [2, 5, 4]),
                                            tensor_input('z', [2, 1, 4])], 1), {'x': x, 'y': y, 'z': z})
     exact(got, want)
+    # along the last axis (one launch writing whole rows): C4's encoding [x, sin, cos] and
+    # skip [h, pe] at 1000 rows, a 3-d case with a one-wide input
+    for shapes in ([[1000, 3], [1000, 30], [1000, 30]], [[1000, 256], [1000, 63]], [[2, 5, 3], [2, 5, 7], [2, 5, 1]]):
+        ins = {f'i{j}': _rand(s, 20 + j) for j, s in enumerate(shapes)}
+        got, want = run_both(lambda: O.concat([tensor_input(f'i{j}', s) for j, s in enumerate(shapes)], -1), ins)
+        exact(got, want)
     got, want = run_both(lambda: O.scatter_axis(tensor_input('x', [2, 3, 4]), [2, 7, 4], 1, 2, 5), {'x': x})
     exact(got, want)
     got, want = run_both(lambda: O.add(O.zeros([3, 4]), O.arange(4, 'f32')), {})
