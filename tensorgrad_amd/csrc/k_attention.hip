@@ -446,9 +446,18 @@ __global__ __launch_bounds__(kNT) void k_attn_bwd_a(const AttnBwdDesc a) {
   }
 }
 
+// Transposed slices in LDS: element (m, i) (slice column m, slice row i) sits at
+// m ld + (i ^ tswz(m)), ld = R + 16. The XOR moves whole 4-element groups, so a 128-bit
+// read of i .. i + 3 (i % 4 == 0) stays one aligned access; with it the transposed 4-byte
+// stores (lanes over 8 or 16 columns m and 8 or 4 rows i) and the fragment reads (16
+// columns m, 16 rows i) meet no bank twice, where the plain layout (ld = R + 4) put two
+// or four store lanes on a bank.
+template <int R>
+__device__ __forceinline__ int tswz(int m) { return 4 * ((m >> 2) & (R / 4 - 1)); }
+
 // Rows [i0, R) of a COLS-wide slice (row stride rs, 16-byte aligned rows) into registers,
 // every load in flight at once; store_t writes them transposed to LDS (column c of the
-// slice becomes row c, row i column i - i0 of a row length `ld`).
+// slice becomes row c, row i column (i - i0) ^ tswz(c) of a row length `ld`).
 template <int R, int COLS>
 struct SliceT {
   static constexpr int C = R * COLS / 4 / kNT;
@@ -467,7 +476,7 @@ struct SliceT {
       const int c = u * kNT + tid, row = c / (COLS / 4), c4 = c % (COLS / 4);
       if (row >= i0)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) dst[(c4 * 4 + e) * ld + row - i0] = v[u][e];
+        for (int e = 0; e < 4; ++e) dst[(c4 * 4 + e) * ld + ((row - i0) ^ tswz<R>(c4 * 4 + e))] = v[u][e];
     }
   }
 };
@@ -475,13 +484,14 @@ struct SliceT {
 // Backward, kernel B (per KB keys [j0, j0 + 32)): dV = Pd^T dO and dK = dS^T Q over the
 // query rows i >= j0 (the causal mask zeroes Pd and dS above the diagonal), 16 x 16 tiles,
 // one per wavefront, k over the rows in blocks of 64. LDS holds the slices transposed (key
-// rows of Pd / dS, head-dimension rows of dO / Q, rows i contiguous): region 1 the Pd
+// rows of Pd / dS, head-dimension rows of dO / Q, rows i in 4-element groups placed by
+// tswz): region 1 the Pd
 // slice, then the dS slice; region 2 dO, then Q (dS and Q wait in registers while dV is
 // formed). The row blocks pair long with short on a CU, as in the forward.
 template <int T>
 __global__ __launch_bounds__(kNT) void k_attn_bwd_b(const AttnBwdDesc a) {
   constexpr int KB = kQB;
-  constexpr int LDT = T + 4;
+  constexpr int LDT = T + 16;
   __shared__ __attribute__((aligned(16))) float Reg1[KB * LDT];    // Pd^T, then dS^T
   __shared__ __attribute__((aligned(16))) float Reg2[kDH * LDT];   // dO^T, then Q^T
 
@@ -525,8 +535,8 @@ __global__ __launch_bounds__(kNT) void k_attn_bwd_b(const AttnBwdDesc a) {
       const int kend = min(mt, kb0 + 64);
       for (int kq = kb0; kq < kend; kq += 16) {
         const int kb = kq + g4 * 4;
-        const f32x4 av = *reinterpret_cast<const f32x4*>(Reg1 + (m0 + l16) * LDT + kb);
-        const f32x4 bv = *reinterpret_cast<const f32x4*>(Reg2 + (n0 + l16) * LDT + kb);
+        const f32x4 av = *reinterpret_cast<const f32x4*>(Reg1 + (m0 + l16) * LDT + (kb ^ tswz<T>(m0 + l16)));
+        const f32x4 bv = *reinterpret_cast<const f32x4*>(Reg2 + (n0 + l16) * LDT + (kb ^ tswz<T>(n0 + l16)));
         part = mfma16(av, bv, part);
       }
       acc += part;
