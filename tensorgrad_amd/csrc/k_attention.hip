@@ -25,7 +25,7 @@ constexpr int kQBF = 32;    // query rows per block (forward, backward kernel A)
 constexpr int kNT = 512;    // eight wavefronts: two per SIMD hide each other's latencies
 constexpr int kDH = 64;     // head size
 constexpr int kLD = kDH + 4;   // k-contiguous tiles (Q, K, S / Pd rows): conflict-free 128-bit reads
-constexpr int kLDV = kDH + 8;  // V rows, read one column per lane
+constexpr int kLDV = kDH + 4;  // V rows, read one column per lane: 4 rows apart land 16 banks apart
 
 // v_mfma_f32_16x16x4f32 fragments: A (16 x 4) lane l holds A[l % 16][l / 16], B (4 x 16)
 // lane l holds B[l / 16][l % 16], the accumulator lane l register r holds
