@@ -416,6 +416,8 @@ class Runtime {
   void read_document();
   void analyse();
   void relu_grads_from_outputs();
+  void narrow_sliced_products();
+  bool concat_transposed(int t, std::vector<int>& srcs, std::vector<int64_t>& offs) const;
   void compute_views();
   void lower();
   void allocate();
@@ -587,6 +589,7 @@ Runtime::Runtime(const char* json, Runtime* par, bool plan_only) : parent(par) {
   plan_only_ = plan_only;
   analyse();
   relu_grads_from_outputs();
+  narrow_sliced_products();
   compute_views();
   lower();
   if (!plan_only) hip_check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate");
@@ -726,6 +729,37 @@ void Runtime::relu_grads_from_outputs() {
   }
 }
 
+// A product read only by a slice that keeps its first columns (the input gradient of a
+// concatenation's first part): the GEMM computes only those columns, reading the first
+// N' columns of B through the same view, and the slice, which then covers the whole
+// (narrowed) product, becomes a view of it in compute_views. The IR shape of the product
+// is rewritten in place; every kept element is the same dot product as before.
+void Runtime::narrow_sliced_products() {
+  auto pinned = [&](int t) {
+    for (int o : outputs_) if (o == t) return true;
+    for (auto& c : captures_) if (c.second == t) return true;
+    if (const tgj::Value* wbs = doc_.get("writebacks"))
+      for (const auto& w : wbs->items) if (w.at("source").i32() == t) return true;
+    return false;
+  };
+  for (size_t j = 0; j < ops_.size(); ++j) {
+    if (kinds_[j] != "slice_range") continue;
+    const int p = fld((int)j, "a"), s = O((int)j).at("out").i32();
+    const int m = T_[p].src;
+    if (m < 0 || (kinds_[m] != "matmul" && kinds_[m] != "matmul_batched") || T_[p].dt != F32) continue;
+    if (consumers_[p].size() != 1 || pinned(p)) continue;
+    Dims& ps = T_[p].shape;
+    const Dims& ss = T_[s].shape;
+    const int64_t rank = (int64_t)ps.size();
+    int64_t ax = O((int)j).at("axis").i64();
+    if (ax < 0) ax += rank;
+    if (rank < 2 || ax != rank - 1 || O((int)j).at("start").i64() != 0 || ss.size() != ps.size()) continue;
+    if (!std::equal(ps.begin(), ps.end() - 1, ss.begin()) || ss.back() <= 0 || ss.back() >= ps.back()) continue;
+    ps.back() = ss.back();
+    T_[p].numel = prod(ps);
+  }
+}
+
 // Views: every tensor is (root storage, dims, strides). Aliasing ops inherit their
 // input's root; permutes are strided views until a consumer needs contiguous data.
 // A permute that must be materialised, applied to the fresh output of a GEMM read by
@@ -858,6 +892,14 @@ void Runtime::compute_views() {
         view_[out] = View{va.root, T_[out].shape, contiguous_strides(T_[out].shape)};
         virtual_[i] = true;
       }
+    } else if (k == "slice_range" && T_[ops_[i]->at("a").i32()].shape == T_[out].shape &&
+               ops_[i]->at("start").i64() == 0) {
+      // a slice covering its whole input (a narrowed product's)
+      int a = ops_[i]->at("a").i32();
+      if (view_[a].contiguous()) {
+        view_[out] = View{view_[a].root, T_[out].shape, contiguous_strides(T_[out].shape)};
+        virtual_[i] = true;
+      }
     } else if ((k == "sum_to_shape" || k == "broadcast_to") &&
                T_[ops_[i]->at("a").i32()].shape == T_[out].shape) {
       int a = ops_[i]->at("a").i32();
@@ -922,6 +964,34 @@ bool Runtime::gemm_operand(int t, int which, const Dims& op_shape, bool batched,
   return false;
 }
 
+// View t is the transpose [K0 + K1 + ..., R] of a concatenation along the last axis of
+// contiguous f32 sources [R, K_s], each at least one 32-row MFMA block wide (narrower
+// sources would each run a mostly empty tile): the sources and their first rows in the
+// transpose.
+bool Runtime::concat_transposed(int t, std::vector<int>& srcs, std::vector<int64_t>& offs) const {
+  srcs.clear();
+  offs.clear();
+  const View& v = view_[t];
+  const int x = v.root;
+  const int c = T_[x].src;
+  if (c < 0 || kinds_[c] != "concat" || virtual_[c] || T_[x].dt != F32 || T_[x].shape.size() != 2) return false;
+  int64_t ax = O(c).at("axis").i64();
+  if (ax < 0) ax += 2;
+  const int64_t R = T_[x].shape[0], Kt = T_[x].shape[1];
+  if (ax != 1 || v.dims != Dims({Kt, R}) || v.strides != Dims({1, Kt}) || !view_[x].contiguous()) return false;
+  int64_t off = 0;
+  for (const auto& e : O(c).at("inputs").items) {
+    const int s = e.i32();
+    if (T_[s].dt != F32 || T_[s].shape.size() != 2 || T_[s].shape[0] != R || T_[s].shape[1] < 32 ||
+        !view_[s].contiguous())
+      return false;
+    srcs.push_back(s);
+    offs.push_back(off);
+    off += T_[s].shape[1];
+  }
+  return off == Kt && srcs.size() >= 2;
+}
+
 // Shapes and element strides of matmul op i as a GemmDesc (no pointers): operands read
 // through their views (transposes and head permutes in place), the output written
 // through its view (contiguous, or a permuted layout folded in by compute_views).
@@ -932,7 +1002,9 @@ bool Runtime::gemm_desc(int i, tgk::GemmDesc& d) const {
   const int a = op.at("a").i32(), b = op.at("b").i32(), out = op.at("out").i32();
   const Dims& ash = T_[a].shape;
   const Dims& bsh = T_[b].shape;
-  const int64_t M = ash[ash.size() - 2], K = ash.back(), N = bsh.back();
+  // N from the product: a narrowed product reads only the first N columns of B
+  const int64_t M = ash[ash.size() - 2], K = ash.back(), N = T_[out].shape.back();
+  if (N > bsh.back()) return false;
   int64_t Ra, Ca, ba, bda, sa0, sa1, sar, sac;
   int64_t Rb, Cb, bb, bdb, sb0, sb1, sbr, sbc;
   int64_t Rc, Cc, bc, bdc, sc0, sc1, scr, scc;
@@ -2928,7 +3000,7 @@ int Runtime::epi_group(int op, int out, const tgk::GemmDesc& d, bool& store_c) c
     const int t = stack.back();
     stack.pop_back();
     for (int c : consumers_[t]) {
-      if (virtual_[c] && (kinds_[c] == "reshape" || kinds_[c] == "stop_gradient")) {
+      if (virtual_[c] && (kinds_[c] == "reshape" || kinds_[c] == "stop_gradient" || kinds_[c] == "slice_range")) {
         stack.push_back(O(c).at("out").i32());
         continue;
       }
@@ -3643,11 +3715,12 @@ void Runtime::lower_op(int i) {
     bool batched = k == "matmul_batched";
     const Dims& ash = T_[a].shape;
     const Dims& bsh = T_[b].shape;
-    int64_t M = ash[ash.size() - 2], K = ash.back(), N = bsh.back();
+    int64_t M = ash[ash.size() - 2], K = ash.back(), N = to.shape.back();
     int64_t batch = T_[a].numel / (M * K);
     n.flops = 2.0 * (double)batch * M * N * K;
     n.kind = "gemm";
     n.shape = shape_str(ash) + "x" + shape_str(bsh);
+    if (N != bsh.back()) n.shape += " first " + std::to_string(N) + " columns";
     // Pattern: embedding forward, one_hot(idx) @ table.
     int asrc = T_[view_[a].root].src;
     // The one-hot must be read as laid out ([rows, depth] row-major, rows = batch * M,
@@ -3684,8 +3757,52 @@ void Runtime::lower_op(int i) {
         return;
       }
     }
-    rd(a); rd(b);
+    // Pattern: A is the transpose of a last-axis concatenation [R, K0 + K1 + ...] (the
+    // weight gradient of a layer fed by a skip concatenation): one GEMM per source, each
+    // reading its source in place and writing its own rows of the product, so no tile runs
+    // on the concatenation's unaligned rows or straddles two sources.
+    std::vector<int> cat_src;
+    std::vector<int64_t> cat_off;
     tgk::GemmDesc d{};
+    if (!batched && !defer_gemm_[i] && concat_transposed(a, cat_src, cat_off) && gemm_desc(i, d) && d.batch == 1 &&
+        d.sCn == 1 && d.sCm == N && view_[out].root == out && view_[out].contiguous()) {
+      std::vector<tgk::GemmDesc> ds;
+      int64_t ws = 0;
+      for (size_t s = 0; s < cat_src.size(); ++s) {
+        tgk::GemmDesc g = d;
+        g.M = T_[cat_src[s]].shape.back();
+        g.sAm = 1;
+        g.sAk = g.M;
+        ws = std::max(ws, tgk::gemm_workspace_floats(g));
+        ds.push_back(g);
+        rd(cat_src[s]);
+      }
+      rd(b);
+      workspace_bytes_ = std::max(workspace_bytes_, (size_t)ws * 4);
+      n.ws = ws > 0;
+      n.bytes = 4.0 * (T_[a].numel + T_[b].numel + to.numel);
+      n.shape += " by " + std::to_string(cat_src.size()) + " sources";
+      n.bind = [=]() -> std::function<void(hipStream_t)> {
+        std::vector<tgk::GemmDesc> gs = ds;
+        for (size_t s = 0; s < gs.size(); ++s) {
+          tgk::GemmDesc& g = gs[s];
+          const int64_t da[2] = {g.M, g.K}, sa[2] = {g.sAm, g.sAk};
+          const int64_t db[2] = {g.K, g.N}, sb[2] = {g.sBk, g.sBn};
+          const int64_t dc[2] = {g.M, g.N}, sc[2] = {g.sCm, g.sCn};
+          check_span("gemm A (concatenation source)", T_[root(cat_src[s])].numel, 0, da, sa, 2);
+          check_span("gemm B", T_[root(b)].numel, 0, db, sb, 2);
+          check_span("gemm C (source rows)", T_[root(out)].numel, cat_off[s] * g.sCm, dc, sc, 2);
+          g.A = (const float*)dptr(cat_src[s]);
+          g.B = (const float*)dptr(b);
+          g.C = (float*)dptr(out) + cat_off[s] * g.sCm;
+        }
+        float* w = cur_ws_;
+        return [=](hipStream_t st) { for (const tgk::GemmDesc& g : gs) tgk::gemm(g, w, st); };
+      };
+      add_node(std::move(n));
+      return;
+    }
+    rd(a); rd(b);
     if (!gemm_desc(i, d)) throw Error(TG_INTERNAL, "gemm: operand view not expressible (" + n.shape + ")");
     int64_t ws = tgk::gemm_workspace_floats(d);
     if (defer_gemm_[i]) {

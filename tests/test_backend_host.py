@@ -242,6 +242,26 @@ def test_relu_grad_reads_the_relu_output():
         assert n['bytes'] < 2.1 * 4 * 65536 * 256, n
 
 
+def test_skip_concatenation_gradients_lower_without_copies():
+    """C4's skip connection (samples/nerf: the hidden state concatenated with the encoding,
+    [65536, 256 + 63]): the input gradient's product computes only the 256 columns its
+    slice keeps and takes the ReLU gradient in its epilogue (no [65536, 319] product, no
+    slice copy, no separate relu_grad launch), and the weight gradient runs one GEMM per
+    concatenation source instead of one over the concatenation's unaligned rows."""
+    cfg = configs.CONFIGS['nerf']
+    ir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer)
+    nodes = backend.plan(ir.wire_json())['nodes']
+    shapes = [(n['kind'], n['shape']) for n in nodes]
+    assert ('copy', '[65536,256]') not in shapes
+    assert not [s for k, s in shapes if k == 'gemm' and s.startswith('[65536,256]x[256,319]')]
+    assert shapes.count(('gemm', '[319,65536]x[65536,256] by 2 sources')) == 1
+    # the encoding's own concatenation has 3- and 30-wide sources: one GEMM over its 63 rows
+    assert shapes.count(('gemm', '[63,65536]x[65536,256]')) == 1
+    relu_grads = [n for n in nodes if n.get('ops') == 'relu_grad']
+    assert len(relu_grads) == 1, relu_grads   # the head's, after the [256, 4] product
+    assert len([n for n in nodes if n.get('ops') == 'gemm+relu_grad']) == 7
+
+
 def test_sums_of_products_lower_to_one_gemm(monkeypatch):
     """The transformer's Q/K/V input gradient dX = dQ Wq^T + dK Wk^T + dV Wv^T is one GEMM
     over three k segments, each with its own base pointer; the host-only lowering runs the
