@@ -49,6 +49,11 @@ struct GemmArgs {
   int seg_stages = 0;
   const float* segA[kMaxSeg] = {};
   const float* segB[kMaxSeg] = {};
+  // A as a concatenation along k (CAT kernels): stages below cat_stages read d.A, the rest
+  // read catA (row stride catAm, its k from 0); one batch, one split.
+  const float* catA = nullptr;
+  int64_t catAm = 0;
+  int cat_stages = 0;
 };
 
 // Same fragments and blocked accumulation as k_gemm (k_gemm.hip), but operand tiles travel from
@@ -199,8 +204,12 @@ __device__ __forceinline__ uint32_t xcd_order(uint32_t b, uint32_t nblk) {
 // SEG: a sum of products over k segments (GemmArgs::nseg): stage st reads segment
 // st / seg_stages through that segment's own bases; the per-lane offsets, relative to the
 // tile origin within a segment, are the same for every segment (shared strides).
+// CAT: A (k-contiguous) is a concatenation along k of d.A (whole 16-byte aligned stages,
+// stages below g.cat_stages) and g.catA (the rest, rows of any alignment, moved one element
+// per lane into the same LDS layout, the partial last stage included). B runs straight
+// through all K.
 template <int BM, int BN, int BK, int NS, bool AK, bool BKF, int NT, int KG, class Epi, bool BDW = false,
-          bool ADW = false, bool KT = false, bool SEG = false>
+          bool ADW = false, bool KT = false, bool SEG = false, bool CAT = false>
 __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint32_t b, const Epi& epi) {
   // per k group: 4 waves 2 x 2; 8 waves 2 x 4 (BN = 128) or 4 x 2
   constexpr int GT = NT / KG;             // threads per k group
@@ -217,9 +226,14 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint32_t b, const E
   constexpr int NG = BK / 8;
   using TA = DTile<BM, BK, AK, GT, ADW>;
   using TB = DTile<BN, BK, BKF, GT, BDW>;
-  static_assert(!KT || ((!AK || ADW) && (!BKF || BDW)), "a partial k stage needs DW k-contiguous operands");
+  static_assert(!KT || ((!AK || ADW || CAT) && (!BKF || BDW)), "a partial k stage needs DW k-contiguous operands");
+  static_assert(!CAT || (AK && !ADW && !SEG && KG == 1), "CAT: a k-contiguous, 16-byte A source first");
+  // the second source of a CAT tile (its stages issue more loads than PER: the waits below
+  // count PER per stage, the fewer, so they wait at least as long as needed)
+  using TA2 = DTile<BM, BK, true, GT, true>;
   constexpr int PER = TA::PER + TB::PER;
   static_assert(PER * (NSG - 1) < 64, "too many loads in flight for vmcnt");
+  static_assert(!CAT || (TA2::PER + TB::PER) * (NSG - 1) < 64, "too many loads in flight for vmcnt");
   __shared__ __attribute__((aligned(16))) float As[NS * TA::SIZE];   // NS stages of A
   __shared__ __attribute__((aligned(16))) float Bs[NS * TB::SIZE];   // NS stages of B
 
@@ -252,9 +266,9 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint32_t b, const E
   uint32_t offa[TA::PER], offb[TB::PER];
   TA::offsets(d.sAm, d.sAk, m0, d.M, gtid, offa);
   TB::offsets(d.sBn, d.sBk, n0, d.N, gtid, offb);
-  uint32_t offat[KT ? TA::PER : 1], offbt[KT ? TB::PER : 1];   // the partial last stage
+  uint32_t offat[KT && !CAT ? TA::PER : 1], offbt[KT ? TB::PER : 1];   // the partial last stage
   if (KT) {
-    TA::offsets(d.sAm, d.sAk, m0, d.M, gtid, offat, ktail);
+    if (!CAT) TA::offsets(d.sAm, d.sAk, m0, d.M, gtid, offat, ktail);
     TB::offsets(d.sBn, d.sBk, n0, d.N, gtid, offbt, ktail);
   }
   const int wv = __builtin_amdgcn_readfirstlane(wave);
@@ -270,7 +284,23 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint32_t b, const E
       TB::dma(sb + n0 * (BKF ? d.sBn : 1) + sl * b_step, offb, lds_b + slot * TB::SIZE * 4, wv);
       return;
     }
-    if (KT && st == nst - 1 && ktail < BK) {
+    if (CAT && st >= g.cat_stages) {   // one split: kbeg = 0
+      const float* sa = g.catA + m0 * g.catAm + (int64_t)(st - g.cat_stages) * BK;
+      const bool tail = KT && st == nst - 1 && ktail < BK;
+      // The second source's per-lane offsets are computed here, for its few stages, from
+      // values the compiler cannot see through, so no part of them is hoisted out of the k
+      // loop and held in registers across it (that would cost a block per CU).
+      int kv = tail ? ktail : BK;
+      int t2 = gtid;
+      asm volatile("" : "+s"(kv), "+v"(t2));
+      uint32_t o2[TA2::PER];
+      TA2::offsets(g.catAm, 1, m0, d.M, t2, o2, kv);
+      TA2::dma(sa, o2, lds_a + slot * TA::SIZE * 4, wv);
+      if (tail) TB::dma(b0 + st * b_step, offbt, lds_b + slot * TB::SIZE * 4, wv);
+      else TB::dma(b0 + st * b_step, offb, lds_b + slot * TB::SIZE * 4, wv);
+      return;
+    }
+    if (!CAT && KT && st == nst - 1 && ktail < BK) {
       TA::dma(a0 + st * a_step, offat, lds_a + slot * TA::SIZE * 4, wv);
       TB::dma(b0 + st * b_step, offbt, lds_b + slot * TB::SIZE * 4, wv);
       return;

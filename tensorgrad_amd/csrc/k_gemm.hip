@@ -241,9 +241,10 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmArgs g) {
 // ---- direct-to-LDS pipeline (gemm_dev.h) ----------------------------------------------
 
 template <int BM, int BN, int BK, int NS, bool AK, bool BKF, int NT, int KG, bool BDW = false, bool ADW = false,
-          bool KT = false, bool SEG = false>
+          bool KT = false, bool SEG = false, bool CAT = false>
 __global__ __launch_bounds__(NT) void k_gemm_dma(GemmArgs g) {
-  gemm_tile<BM, BN, BK, NS, AK, BKF, NT, KG, StoreC, BDW, ADW, KT, SEG>(g, xcd_order(blockIdx.x, gridDim.x), StoreC{});
+  gemm_tile<BM, BN, BK, NS, AK, BKF, NT, KG, StoreC, BDW, ADW, KT, SEG, CAT>(g, xcd_order(blockIdx.x, gridDim.x),
+                                                                            StoreC{});
 }
 
 // Several independent problems in one launch: problem p owns tile numbers
@@ -800,6 +801,61 @@ void gemm(const GemmDesc& d, float* work, hipStream_t st) {
     if (nb > 4096) nb = 4096;
     klaunch(k_splitk_reduce, (int)nb, 256, 0, st, work, p.splits, g.sOs, d);
   }
+}
+
+// ---- products over a concatenation along k ---------------------------------------------
+// A = [A0 | A1] along k: k < k0 from d.A (row stride d.sAm, 16-byte aligned rows), the rest
+// from c.a1 (row stride c.lda1, any alignment). One launch of 128 x 128 tiles whose stages
+// below k0 / 32 load A0 sixteen bytes per lane and whose later stages load A1 one element
+// per lane, the partial last stage zeroed in LDS; B ([K, N], rows contiguous) runs straight
+// through. Each output element is the same ordered sum over k as a plain GEMM over the
+// materialised concatenation with 32-k stages.
+
+bool gemm_cat_ok(const GemmDesc& d, const GemmCat& c) {
+  if (d.batch != 1 || d.M <= 0 || d.N <= 0 || d.K <= 0) return false;
+  if (d.sAk != 1 || (d.sAm & 3) || c.k0 < 32 || c.k0 % 32 != 0 || d.K <= c.k0 || c.lda1 < d.K - c.k0) return false;
+  if (d.sBn != 1 || (d.sBk & 3) || (d.N & 3)) return false;
+  if (((uintptr_t)d.A & 15) != 0 || ((uintptr_t)d.B & 15) != 0) return false;
+  // per-lane byte offsets from the tile origin stay below 2^31 (128 rows / k rows a tile)
+  const int64_t lim = int64_t(1) << 31;
+  if (d.sAm * 128 * 4 >= lim || d.sBk * 128 * 4 >= lim || c.lda1 * 128 * 4 >= lim) return false;
+  return (d.M + 127) / 128 * ((d.N + 127) / 128) < lim;
+}
+
+static GemmArgs cat_args(const GemmDesc& d, const GemmCat& c, int64_t& blocks) {
+  GemmArgs g{d, d.K, 1, 0, 0, nullptr, 0, 0};
+  g.tiles_n = (int)((d.N + 127) / 128);
+  g.tiles_m = (int)((d.M + 127) / 128);
+  g.catA = c.a1;
+  g.catAm = c.lda1;
+  g.cat_stages = (int)(c.k0 / 32);
+  blocks = (int64_t)g.tiles_n * g.tiles_m;
+  return g;
+}
+
+void gemm_cat(const GemmDesc& d, const GemmCat& c, hipStream_t st) {
+  if (!gemm_cat_ok(d, c)) throw std::runtime_error("gemm_cat: unsupported operands");
+  int64_t blocks = 0;
+  const GemmArgs g = cat_args(d, c, blocks);
+  // two or more tiles per CU: the two-stage ring (two blocks share a CU), as in gemm()
+  if (blocks >= 512) klaunch(k_gemm_dma<128, 128, 32, 2, true, false, 512, 1, false, false, true, false, true>,
+                             (unsigned)blocks, 512, 0, st, g);
+  else klaunch(k_gemm_dma<128, 128, 32, 3, true, false, 512, 1, false, false, true, false, true>, (unsigned)blocks,
+               512, 0, st, g);
+}
+
+bool gemm_cat_epi_cfg(const GemmDesc& d, const GemmCat& c, GemmEpiCfg& cfg, GemmArgs& g, int64_t& blocks) {
+  if (!gemm_cat_ok(d, c)) return false;
+  g = cat_args(d, c, blocks);
+  cfg.bm = cfg.bn = 128;
+  cfg.bk = 32;
+  cfg.nt = 512;
+  cfg.kg = 1;
+  cfg.ak = true;
+  cfg.bkf = false;
+  cfg.ns = blocks >= 512 ? 2 : 3;
+  cfg.cat = true;
+  return true;
 }
 
 // ---- sums of products ------------------------------------------------------------------

@@ -319,8 +319,19 @@ struct GemmEpiCfg {
   int64_t N;
   int h_in;
   bool store_c = false;   // the epilogue also stores the product itself to C
+  bool cat = false;       // A is a concatenation along k (gemm_cat)
 };
 bool gemm_epi_cfg(const GemmDesc& d, GemmEpiCfg& c, gd::GemmArgs& g, int64_t& blocks);
+// A product whose A operand is a concatenation along k of two row-major sources: k < k0
+// from d.A (rows 16-byte aligned, k0 a multiple of 32), the rest from a1 (row stride lda1,
+// any alignment); B rows contiguous, one batch. No workspace.
+struct GemmCat {
+  const float* a1;
+  int64_t k0, lda1;
+};
+bool gemm_cat_ok(const GemmDesc& d, const GemmCat& c);
+void gemm_cat(const GemmDesc& d, const GemmCat& c, hipStream_t st);
+bool gemm_cat_epi_cfg(const GemmDesc& d, const GemmCat& c, GemmEpiCfg& cfg, gd::GemmArgs& g, int64_t& blocks);
 // True when d on its own would run one pass of 64 x 64 tiles (the grouped tiling); the
 // grouped launch's k-stage depth follows its own tile count, as a plain launch's does.
 bool gemm_prefers_group(const GemmDesc& d);

@@ -360,6 +360,14 @@ class Runtime {
   // the final add; the products and the inner adds are absorbed.
   bool use_gemm_sum_ = true;         // TG_GEMM_SUM=0 keeps the products and adds apart
   std::map<int, std::vector<int>> gemm_sums_;   // final add -> matmul ops, in k order
+  // Products reading a last-axis concatenation [R, k0 + k1] of two sources as their A
+  // operand: run as one GEMM over the sources (tgk::gemm_cat). A concatenation all of whose
+  // readers are such products or per-source weight gradients is not materialised.
+  struct CatFwd { int src0, src1; int64_t k0, k1; };
+  std::map<int, CatFwd> cat_fwd_;     // matmul op -> its A's sources
+  std::vector<char> cat_absorbed_;    // concat op -> not lowered
+  void match_concat_products();
+  void check_cat_spans(const tgk::GemmDesc& d, const CatFwd& c, int b, int out, bool with_c) const;
   std::vector<char> sum_absorbed_;
   void match_gemm_sums();
   void lower_gemm_sum(int add_op);
@@ -513,8 +521,9 @@ class Runtime {
   int gemm_epi_mode_ = kEpiCheap;
   bool epi_cheap(int gi) const;
   std::vector<char> group_done_;     // group already run inside a GEMM epilogue
-  int epi_group(int op, int out, const tgk::GemmDesc& d, bool& store_c) const;
-  void lower_gemm_epi(int op, const tgk::GemmDesc& d, int a, int b, int out, int gi, bool store_c);
+  int epi_group(int op, int out, const tgk::GemmDesc& d, bool& store_c, const CatFwd* cat = nullptr) const;
+  void lower_gemm_epi(int op, const tgk::GemmDesc& d, int a, int b, int out, int gi, bool store_c,
+                      const CatFwd* cat = nullptr);
   // Column sums read only by the optimizer (bias, LayerNorm gain / shift gradients) run
   // together with the grouped GEMMs, kColSumMax per launch.
   std::vector<char> defer_colsum_;
@@ -962,6 +971,94 @@ bool Runtime::gemm_operand(int t, int which, const Dims& op_shape, bool batched,
   if (d3.size() == 1) { bdiv = 1; s0 = s3[0]; s1 = 0; return true; }
   if (d3.size() == 2) { bdiv = d3[1]; s0 = s3[0]; s1 = s3[1]; return true; }
   return false;
+}
+
+// Readers of a last-axis concatenation X = [S0 | S1] ([R, k0 + k1], f32, contiguous
+// sources): a product reading X as its A operand (a layer fed by a skip connection) runs
+// as one GEMM over the two sources when S0 fills whole 32-k stages (tgk::gemm_cat); a
+// product reading X's transpose runs one GEMM per source (the weight gradient, in
+// lower_op). When every reader (through reshape / permute views) is one of these, X itself
+// is never written.
+void Runtime::match_concat_products() {
+  cat_fwd_.clear();
+  cat_absorbed_.assign(ops_.size(), 0);
+  if (!use_gemm_group_) return;
+  auto pinned = [&](int t) {
+    for (int o : outputs_) if (root(o) == root(t)) return true;
+    for (auto& c : captures_) if (root(c.second) == root(t)) return true;
+    for (auto& w : copy_writebacks_) if (root(w.first) == root(t)) return true;
+    return false;
+  };
+  for (size_t c = 0; c < ops_.size(); ++c) {
+    if (kinds_[c] != "concat" || virtual_[c]) continue;
+    const int x = O((int)c).at("out").i32();
+    if (view_[x].root != x || !view_[x].contiguous() || T_[x].dt != F32 || T_[x].shape.size() != 2 || pinned(x))
+      continue;
+    int64_t ax = O((int)c).at("axis").i64();
+    if (ax < 0) ax += 2;
+    const auto& ins = O((int)c).at("inputs").items;
+    if (ax != 1 || ins.size() != 2) continue;
+    const int s0 = ins[0].i32(), s1 = ins[1].i32();
+    const int64_t R = T_[x].shape[0], Kt = T_[x].shape[1];
+    bool ok_src = true;
+    for (int s : {s0, s1})
+      ok_src = ok_src && T_[s].dt == F32 && T_[s].shape.size() == 2 && T_[s].shape[0] == R && view_[s].contiguous();
+    if (!ok_src) continue;
+    const CatFwd cf{s0, s1, T_[s0].shape[1], T_[s1].shape[1]};
+    if (cf.k0 + cf.k1 != Kt) continue;
+    // every reader, through views
+    bool all = true;
+    std::vector<int> fwd;
+    std::vector<int> stack{x};
+    while (!stack.empty() && all) {
+      const int t = stack.back();
+      stack.pop_back();
+      for (int u : consumers_[t]) {
+        const std::string& k = kinds_[u];
+        if (virtual_[u] && (k == "reshape" || k == "permute" || k == "stop_gradient")) {
+          stack.push_back(O(u).at("out").i32());
+          continue;
+        }
+        if (k != "matmul" || virtual_[u] || fld(u, "b") == t) { all = false; break; }
+        std::vector<int> srcs;
+        std::vector<int64_t> offs;
+        tgk::GemmDesc d{};
+        if (!gemm_desc(u, d)) { all = false; break; }
+        const View& va = view_[t];
+        if (va.dims == Dims({R, Kt}) && va.strides == Dims({Kt, 1})) {
+          d.sAm = cf.k0;
+          d.A = reinterpret_cast<const float*>(uintptr_t(256));
+          d.B = reinterpret_cast<const float*>(uintptr_t(256));
+          if (!tgk::gemm_cat_ok(d, tgk::GemmCat{reinterpret_cast<const float*>(uintptr_t(256)), cf.k0, cf.k1})) {
+            all = false;
+            break;
+          }
+          fwd.push_back(u);
+        } else if (!(concat_transposed(t, srcs, offs) && !defer_gemm_[u] && d.batch == 1 && d.sCn == 1 &&
+                     d.sCm == d.N && view_[O(u).at("out").i32()].contiguous())) {
+          all = false;
+          break;
+        }
+      }
+    }
+    // the forward products take the sources either way; X is skipped when nothing else reads it
+    for (int u : fwd) cat_fwd_[u] = cf;
+    if (all && !fwd.empty()) cat_absorbed_[c] = 1;
+  }
+}
+
+void Runtime::check_cat_spans(const tgk::GemmDesc& d, const CatFwd& c, int b, int out, bool with_c) const {
+  if (d.batch != 1 || d.K != c.k0 + c.k1 || d.sAm != c.k0 || d.sAk != 1)
+    throw Error(TG_INTERNAL, "gemm_cat: descriptor does not match its sources");
+  const int64_t da0[2] = {d.M, c.k0}, sa0[2] = {c.k0, 1};
+  const int64_t da1[2] = {d.M, c.k1}, sa1[2] = {c.k1, 1};
+  const int64_t db[2] = {d.K, d.N}, sb[2] = {d.sBk, d.sBn};
+  const int64_t dc[2] = {d.M, d.N}, sc[2] = {d.sCm, d.sCn};
+  check_span("gemm_cat A0", T_[root(c.src0)].numel, 0, da0, sa0, 2);
+  check_span("gemm_cat A1", T_[root(c.src1)].numel, 0, da1, sa1, 2);
+  check_span("gemm_cat B", T_[root(b)].numel, 0, db, sb, 2);
+  if (with_c) check_span("gemm_cat C", T_[root(out)].numel, 0, dc, sc, 2);
+  if (d.M * d.N != T_[out].numel) throw Error(TG_INTERNAL, "gemm_cat: output size mismatch");
 }
 
 // View t is the transpose [K0 + K1 + ..., R] of a concatenation along the last axis of
@@ -1526,6 +1623,7 @@ void Runtime::lower() {
   match_optimizer();
   gemm_done_.assign(ops_.size(), 0);
   plan_gemm_groups();
+  match_concat_products();
   match_attention();
   match_attention_bwd();
   match_colsums();
@@ -1539,7 +1637,7 @@ void Runtime::lower() {
   if (use_remat_) remat_groups();
   group_done_.assign(groups_.size(), 0);
   for (size_t i = 0; i < ops_.size(); ++i) {
-    if (is_leaf((int)i) || virtual_[i]) continue;
+    if (is_leaf((int)i) || virtual_[i] || cat_absorbed_[i]) continue;
     if (adam_ops_.count((int)i)) continue;
     if (attn_of_[i] >= 0) {
       const int m = attn_of_[i];
@@ -2985,7 +3083,7 @@ void Runtime::plan_gemm_groups() {
       for (int i : cand[k]) defer_gemm_[i] = 1;
 }
 
-int Runtime::epi_group(int op, int out, const tgk::GemmDesc& d, bool& store_c) const {
+int Runtime::epi_group(int op, int out, const tgk::GemmDesc& d, bool& store_c, const CatFwd* cat) const {
   store_c = false;
   if (view_[out].root != out || !view_[out].contiguous() || d.batch != 1 || d.sCn != 1 || d.sCm != d.N) return -1;
   for (int o : outputs_) if (root(o) == out) store_c = true;
@@ -3019,7 +3117,12 @@ int Runtime::epi_group(int op, int out, const tgk::GemmDesc& d, bool& store_c) c
   tgk::GemmEpiCfg c{};
   tgk::gd::GemmArgs ga{};
   int64_t blocks = 0;
-  if (tgk::gemm_workspace_floats(d) != 0 || !tgk::gemm_epi_cfg(d, c, ga, blocks)) return -1;
+  if (cat) {
+    const tgk::GemmCat gc{nullptr, cat->k0, cat->k1};
+    if (!tgk::gemm_cat_epi_cfg(d, gc, c, ga, blocks)) return -1;
+  } else if (tgk::gemm_workspace_floats(d) != 0 || !tgk::gemm_epi_cfg(d, c, ga, blocks)) {
+    return -1;
+  }
   const GroupPlan gp = plan_group(G.ops, false, G.shape);
   int hits = 0;
   for (auto& e : gp.ext) {
@@ -3044,7 +3147,10 @@ bool Runtime::epi_cheap(int gi) const {
   return true;
 }
 
-void Runtime::lower_gemm_epi(int op, const tgk::GemmDesc& d, int a, int b, int out, int gi, bool store_c) {
+void Runtime::lower_gemm_epi(int op, const tgk::GemmDesc& d, int a, int b, int out, int gi, bool store_c,
+                             const CatFwd* cat) {
+  const bool is_cat = cat != nullptr;
+  const CatFwd cf = is_cat ? *cat : CatFwd{-1, -1, 0, 0};
   group_done_[gi] = 1;
   const Group G = groups_[gi];
   const GroupPlan gp = plan_group(G.ops, false, G.shape);
@@ -3054,7 +3160,13 @@ void Runtime::lower_gemm_epi(int op, const tgk::GemmDesc& d, int a, int b, int o
   n.detail = "gemm+";
   for (size_t q = 0; q < G.ops.size(); ++q) n.detail += (q ? "," : "") + kinds_[G.ops[q]];
   n.shape = shape_str(T_[out].shape) + " x" + std::to_string(G.ops.size());
-  n.reads.push_back(root(a));
+  if (is_cat) {
+    n.detail = "gemm_cat+" + n.detail.substr(5);
+    n.reads.push_back(root(cf.src0));
+    n.reads.push_back(root(cf.src1));
+  } else {
+    n.reads.push_back(root(a));
+  }
   n.reads.push_back(root(b));
   for (auto& e : gp.ext) if (root(e.first) != out) n.reads.push_back(root(e.first));
   if (gp.seed >= 0) n.reads.push_back(root(gp.seed));
@@ -3067,7 +3179,8 @@ void Runtime::lower_gemm_epi(int op, const tgk::GemmDesc& d, int a, int b, int o
   const size_t code_off = fused_code_.size();
   fused_code_.insert(fused_code_.end(), gp.code.begin(), gp.code.end());
   n.bind = [=]() -> std::function<void(hipStream_t)> {
-    check_gemm_spans(d, a, b, out);
+    if (is_cat) check_cat_spans(d, cf, b, out, store_c);
+    else check_gemm_spans(d, a, b, out);
     const Dims F = G.shape;
     const int64_t cnt = prod(F);
     if (cnt >= (int64_t(1) << 31)) throw Error(TG_INVALID_ARGUMENT, "GEMM epilogue: 2^31 or more elements");
@@ -3139,13 +3252,19 @@ void Runtime::lower_gemm_epi(int op, const tgk::GemmDesc& d, int a, int b, int o
     p.seed = gp.seed >= 0 ? (const int32_t*)dptr(gp.seed) : nullptr;
     p.n_instr = (int)gp.code.size();
     tgk::GemmDesc e = d;
-    e.A = (const float*)dptr(a);
+    e.A = (const float*)dptr(is_cat ? cf.src0 : a);
     e.B = (const float*)dptr(b);
     e.C = store_c ? (float*)dptr(out) : nullptr;   // stored only when something else reads it
     tgk::GemmEpiCfg c{};
     tgk::gd::GemmArgs ga{};
     int64_t blocks = 0;
-    if (!tgk::gemm_epi_cfg(e, c, ga, blocks)) throw Error(TG_INTERNAL, "GEMM epilogue: no direct-to-LDS launch");
+    if (is_cat) {
+      const tgk::GemmCat gc{(const float*)dptr(cf.src1), cf.k0, cf.k1};
+      if (!tgk::gemm_cat_epi_cfg(e, gc, c, ga, blocks))
+        throw Error(TG_INTERNAL, "GEMM epilogue: concatenation operands not aligned for the direct-to-LDS kernel");
+    } else if (!tgk::gemm_epi_cfg(e, c, ga, blocks)) {
+      throw Error(TG_INTERNAL, "GEMM epilogue: no direct-to-LDS launch");
+    }
     c.N = d.N;
     c.h_in = h_in;
     c.store_c = store_c;
@@ -3764,6 +3883,36 @@ void Runtime::lower_op(int i) {
     std::vector<int> cat_src;
     std::vector<int64_t> cat_off;
     tgk::GemmDesc d{};
+    // Pattern: A is a last-axis concatenation of two sources: one GEMM reading both in place.
+    if (cat_fwd_.count(i)) {
+      const CatFwd cf = cat_fwd_.at(i);
+      if (!gemm_desc(i, d)) throw Error(TG_INTERNAL, "gemm: operand view not expressible (" + n.shape + ")");
+      d.sAm = cf.k0;   // A0 = the first source, [M, k0] contiguous
+      if (gemm_epi_mode_ != kEpiOff && use_jit_) {
+        bool store_c = false;
+        const int gi = epi_group(i, out, d, store_c, &cf);
+        if (gi >= 0 && (gemm_epi_mode_ == kEpiAll || epi_cheap(gi))) {
+          lower_gemm_epi(i, d, a, b, out, gi, store_c, &cf);
+          return;
+        }
+      }
+      rd(cf.src0); rd(cf.src1); rd(b);
+      n.detail = "gemm_cat";
+      n.bytes = 4.0 * (T_[a].numel + T_[b].numel + to.numel);
+      n.bind = [=]() -> std::function<void(hipStream_t)> {
+        check_cat_spans(d, cf, b, out, true);
+        tgk::GemmDesc g = d;
+        g.A = (const float*)dptr(cf.src0);
+        g.B = (const float*)dptr(b);
+        g.C = (float*)dptr(out);
+        const tgk::GemmCat gc{(const float*)dptr(cf.src1), cf.k0, cf.k1};
+        if (!plan_only_ && !tgk::gemm_cat_ok(g, gc))
+          throw Error(TG_INTERNAL, "gemm_cat: operands not aligned for the direct-to-LDS kernel");
+        return [=](hipStream_t st) { tgk::gemm_cat(g, gc, st); };
+      };
+      add_node(std::move(n));
+      return;
+    }
     if (!batched && !defer_gemm_[i] && concat_transposed(a, cat_src, cat_off) && gemm_desc(i, d) && d.batch == 1 &&
         d.sCn == 1 && d.sCm == N && view_[out].root == out && view_[out].contiguous()) {
       std::vector<tgk::GemmDesc> ds;

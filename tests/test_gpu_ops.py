@@ -516,6 +516,62 @@ def test_sum_of_products(terms, K):
     gemm_close(got, ref)
 
 
+@pytest.mark.parametrize('M,k0,k1,N,epi', [(1000, 32, 63, 256, False), (700, 256, 63, 256, True),
+                                            (513, 64, 1, 100, False), (2048, 128, 32, 64, True),
+                                            (300, 32, 100, 36, False), (4096, 256, 63, 256, True)])
+def test_concat_product(M, k0, k1, N, epi):
+    """matmul(concat([S0, S1], -1), W), C4's skip layer: one GEMM reading both sources in
+    place (S0's 32-k stages sixteen bytes per lane, S1's one element per lane, a partial
+    last stage zeroed in LDS), with the bias + ReLU group in its epilogue when present;
+    the concatenation itself is not materialised. Against the oracle with GEMM tolerance
+    and against the concatenation copied and multiplied (TG_GEMM_GROUP=0)."""
+    ins = {'s0': _rand([M, k0], 111), 's1': _rand([M, k1], 112), 'w': _rand([k0 + k1, N], 113),
+           'c': _rand([N], 114)}
+
+    def body():
+        x = O.concat([tensor_input('s0', [M, k0]), tensor_input('s1', [M, k1])], -1)
+        h = O.matmul(x, tensor_input('w', [k0 + k1, N]))
+        return O.relu(O.add(h, tensor_input('c', [N]))) if epi else h
+    g = trace_fn(body)
+    ops = _node_ops(g, {})
+    assert ('gemm_cat+add,relu' if epi else 'gemm_cat') in ops, ops
+    got, kinds = _run_native(g, ins)
+    assert 'copy' not in kinds, kinds
+    ref, _ = _run_native(g, ins, {'TG_GEMM_GROUP': '0'})
+    o = pyoracle.OracleRuntime(wire(g))
+    o.run(ins)
+    gemm_close(got, o.output())
+    gemm_close(got, ref)
+
+
+def test_concat_forward_and_transposed_readers():
+    """A concatenation read by a product (the forward) and, transposed, by another (the
+    weight gradient): the first runs over the sources in place, the second as one GEMM per
+    source writing its own rows, and the concatenation is never written. Both products
+    (stacked into one output) against the oracle."""
+    M, k0, k1, N = 2000, 64, 40, 96
+    ins = {'s0': _rand([M, k0], 121), 's1': _rand([M, k1], 122), 'w': _rand([k0 + k1, N], 123),
+           'd': _rand([M, N], 124)}
+
+    def body():
+        x = O.concat([tensor_input('s0', [M, k0]), tensor_input('s1', [M, k1])], -1)
+        y = O.matmul(x, tensor_input('w', [k0 + k1, N]))
+        gw = O.matmul(O.swap_axes(x, -1, -2), tensor_input('d', [M, N]))
+        return O.concat([y, gw], 0)
+    g = trace_fn(body)
+    rt = backend.NativeRuntime(IR.dumps(wire(g)))
+    nodes = rt.describe()['nodes']
+    rt.destroy()
+    shapes = [n['shape'] for n in nodes]
+    assert f'[{k0 + k1},{M}]x[{M},{N}] by 2 sources' in shapes, shapes
+    assert 'gemm_cat' in [n.get('ops') for n in nodes], nodes
+    assert not [n for n in nodes if n['kind'] == 'copy' and n['shape'] == f'[{M},{k0 + k1}]'], shapes
+    got, _ = _run_native(g, ins)
+    o = pyoracle.OracleRuntime(wire(g))
+    o.run(ins)
+    gemm_close(got, o.output())
+
+
 GEMMS = [([5, 7], [7, 3], False, False), ([2, 33, 65], [65, 17], False, False), ([129, 64], [64, 300], False, False),
          ([70, 40], [50, 40], False, True), ([40, 70], [40, 50], True, False), ([4096, 256], [4096, 256], True, False),
          ([300, 4096], [4096, 64], False, False),
