@@ -54,6 +54,9 @@ struct GemmArgs {
   const float* catA = nullptr;
   int64_t catAm = 0;
   int cat_stages = 0;
+  // Column partial sums of an epilogue's summed output (Epi::kColSum): row
+  // tm * (waves along M) + the wave's M slot, N columns, f64.
+  double* colsum = nullptr;
 };
 
 // Same fragments and blocked accumulation as k_gemm (k_gemm.hip), but operand tiles travel from
@@ -449,6 +452,35 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint32_t b, const E
           pre[i][j][r] = epi.load(d, gm, gn);
         }
       }
+    if constexpr (Epi::kColSum) {
+      // The epilogue also returns the value of an output whose column sums are wanted: each
+      // lane totals its column over the wave's rows it holds (f64, in (i, r) order), the two
+      // lane halves (h = 0, 1: the other rows of the same column) are added, and lanes of
+      // h = 0 store the wave's partial row (one batch: z = 0).
+      double cs[TN];
+#pragma unroll
+      for (int j = 0; j < TN; ++j) cs[j] = 0.0;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const int64_t gn = n0 + wn0 + j * 32 + lrow;
+          if (gn >= d.N) continue;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int64_t gm = m0 + wm0 + i * 32 + (r / 4) * 8 + h * 4 + (r % 4);
+            if (gm < d.M) cs[j] += (double)epi(d, z0, z1, gm, gn, acc[i][j][r], pre[i][j][r]);
+          }
+        }
+      const int64_t prow = (int64_t)tm * WGM + wave / WGN;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const double t = cs[j] + __shfl_xor(cs[j], 32);
+        const int64_t gn = n0 + wn0 + j * 32 + lrow;
+        if (h == 0 && gn < d.N) g.colsum[prow * d.N + gn] = t;
+      }
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -480,6 +512,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, uint32_t b, const E
 // The plain epilogue: element (z, gm, gn) of the product to C.
 struct StoreC {
   static constexpr bool kPrefetch = false;
+  static constexpr bool kColSum = false;
   __device__ __forceinline__ void operator()(const GemmDesc& d, int64_t z0, int64_t z1, int64_t gm, int64_t gn,
                                              float v) const {
     d.C[z0 * d.sCz0 + z1 * d.sCz1 + gm * d.sCm + gn * d.sCn] = v;

@@ -303,6 +303,9 @@ JitKernel gemm_epi_kernel(const FusedProgram& p, const FusedInstr* code, const G
   // element, operator() computes from them and the accumulator value and stores.
   o << "namespace {\nstruct @NAME@_epi {\n  tgk::JitArgs A;\n  unsigned seed;\n";
   o << "  static constexpr bool kPrefetch = true;\n";
+  // kColSum: operator() returns output colsum_out's value, whose column sums gemm_tile totals
+  if (c.colsum_out >= p.n_out) throw std::runtime_error("jit: column-sum output out of range");
+  o << "  static constexpr bool kColSum = " << (c.colsum_out >= 0 ? "true" : "false") << ";\n";
   o << "  struct Pre { unsigned x[" << std::max(1, p.n_in) << "]; };\n";
   o << "  __device__ __forceinline__ Pre load(const tgk::GemmDesc&, int64_t gm, int64_t gn) const {\n";
   o << I << "Pre q;\n";
@@ -318,7 +321,7 @@ JitKernel gemm_epi_kernel(const FusedProgram& p, const FusedInstr* code, const G
     o << "];\n";
   }
   o << I << "(void)t;\n" << I << "return q;\n  }\n";
-  o << "  __device__ __forceinline__ void operator()(const tgk::GemmDesc& d, int64_t, int64_t, int64_t gm, int64_t gn, "
+  o << "  __device__ __forceinline__ float operator()(const tgk::GemmDesc& d, int64_t, int64_t, int64_t gm, int64_t gn, "
        "float value, const Pre& q) const {\n";
   if (c.store_c) o << I << "d.C[gm * d.sCm + gn * d.sCn] = value;\n";
   o << I << "const unsigned t = (unsigned)gm * " << ulit(c.N) << " + (unsigned)gn;\n";
@@ -351,6 +354,8 @@ JitKernel gemm_epi_kernel(const FusedProgram& p, const FusedInstr* code, const G
     reg[in.dst] = v;
   }
   for (int k = 0; k < p.n_out; ++k) o << I << "((unsigned*)A.out[" << k << "])[t] = " << R(p.out_reg[k]) << ";\n";
+  if (c.colsum_out >= 0) o << I << "return tgk::bitsf(" << R(p.out_reg[c.colsum_out]) << ");\n";
+  else o << I << "return 0.0f;\n";
   o << "  }\n};\n}  // namespace\n";
   o << "extern \"C\" __global__ void __launch_bounds__(" << c.nt
     << ") @NAME@(const tgk::gd::GemmArgs g, const tgk::JitArgs A) {\n";

@@ -954,6 +954,14 @@ bool gemm_epi_cfg(const GemmDesc& d, GemmEpiCfg& c, GemmArgs& g, int64_t& blocks
   return blocks < (int64_t(1) << 31);
 }
 
+int64_t gemm_epi_colsum_rows(const GemmEpiCfg& c, const GemmArgs& g) {
+  // gemm_tile's wavefront grid: NW wavefronts per k group, 4 x 2 for eight with a 64-wide
+  // tile, else 2 along M
+  const int nw = c.nt / c.kg / 64;
+  const int wgm = nw == 8 && c.bn == 64 ? 4 : 2;
+  return (int64_t)g.tiles_m * wgm;
+}
+
 size_t gemm_group_table(const GemmDesc* ds, int n, std::vector<unsigned char>& image, int64_t& blocks, int& tiling) {
   const size_t args_bytes = (size_t)n * sizeof(GemmArgs);
   const size_t starts_off = (args_bytes + 15) / 16 * 16;

@@ -433,7 +433,27 @@ __global__ __launch_bounds__(kColThreads) void k_colsum(const ColSumBatch batch)
   const int64_t c0 = ((int64_t)bx * 64 + lane) * L;   // first column of this lane
   const int64_t r0 = (int64_t)y * cs.chunk, r1 = min(cs.R, r0 + cs.chunk);
   double s[4] = {0.0, 0.0, 0.0, 0.0};
-  if (c0 < C) {
+  if (c0 < C && cs.pin) {
+    // f64 partial rows (a GEMM epilogue's column sums per tile row slot), added in row
+    // order; eight rows' loads issued before their adds (clamped in range, masked after)
+    const double* pd = cs.pin + c0;
+    const int n = (int)min<int64_t>(L, C - c0);
+    for (int64_t r = r0 + w; r < r1; r += 8 * NW) {
+      double v[8][4];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int64_t rr = min(r + NW * u, r1 - 1);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[u][e] = pd[rr * rs + min(e, n - 1)];
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (r + NW * u < r1)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (e < n) s[e] += v[u][e];
+    }
+  } else if (c0 < C) {
     const float* p = cs.a + c0;
     const float* q = cs.b ? cs.b + c0 : nullptr;
     int64_t r = r0 + w;
@@ -682,6 +702,15 @@ ColSum colsum_desc(const float* a, const float* b, float* out, int64_t C, int64_
   auto al = [](const float* x) { return ((uintptr_t)x & 15) == 0; };
   c.aligned = c.cpl == 4 && rs % 4 == 0 && al(a) && (!b || al(b));
   c.div = div; c.scale = 1.0; c.part = part; c.counters = counters;
+  c.pin = nullptr;
+  return c;
+}
+
+ColSum colsum_desc_f64(const double* pin, float* out, int64_t C, int64_t R, double* part, unsigned* counters,
+                       int scale) {
+  ColSum c = colsum_desc(nullptr, nullptr, out, C, R, C, 1.0, part, counters, scale);
+  c.aligned = 0;
+  c.pin = pin;
   return c;
 }
 

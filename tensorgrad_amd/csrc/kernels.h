@@ -174,6 +174,7 @@ struct ColSum {
   double scale;           // != 1: out = f32(f32(sum / div) * scale), a mul_scalar after the sum
   double* part;
   unsigned* counters;
+  const double* pin;      // non-null: sum the f64 rows pin[r * rs + c] (GEMM epilogue partials) instead of a
 };
 constexpr int kColSumMax = 32;
 // An embedding gradient of the scatter_scan_form run by the first `blocks` blocks of a
@@ -223,6 +224,9 @@ static_assert(sizeof(ColSumBatch) <= 4096, "column-sum batch fits the kernel arg
 // (workspace, counters) and at binding
 ColSum colsum_desc(const float* a, const float* b, float* out, int64_t C, int64_t R, int64_t rs, double div,
                    double* part, unsigned* counters, int scale);
+// The same sum over R rows of f64 partials (row stride C), as a term count of one.
+ColSum colsum_desc_f64(const double* pin, float* out, int64_t C, int64_t R, double* part, unsigned* counters,
+                       int scale);
 int64_t colsum_workspace_doubles(int64_t C, int64_t R, int terms, int scale = 1);
 int colsum_batch_scale(const int64_t* C, const int64_t* R, const int* terms, int n);
 MidSum midsum_desc(const float* a, float* out, int64_t B, int64_t C, int64_t L, double* part, unsigned* counters);
@@ -320,7 +324,11 @@ struct GemmEpiCfg {
   int h_in;
   bool store_c = false;   // the epilogue also stores the product itself to C
   bool cat = false;       // A is a concatenation along k (gemm_cat)
+  int colsum_out = -1;    // output whose column partial sums the epilogue writes (GemmArgs::colsum)
 };
+// Rows of the f64 column partials an epilogue with colsum_out writes for this launch
+// (tiles along M times the wavefronts along M of a tile).
+int64_t gemm_epi_colsum_rows(const GemmEpiCfg& c, const gd::GemmArgs& g);
 bool gemm_epi_cfg(const GemmDesc& d, GemmEpiCfg& c, gd::GemmArgs& g, int64_t& blocks);
 // A product whose A operand is a concatenation along k of two row-major sources: k < k0
 // from d.A (rows 16-byte aligned, k0 a multiple of 32), the rest from a1 (row stride lda1,

@@ -290,6 +290,16 @@ class Runtime {
     counter_slots_ += n;
     return b;
   }
+  // Column partial sums written by GEMM epilogues and read by the deferred column-sum
+  // launch of the same step: a region of its own, allocated once (byte offsets, 256-byte
+  // aligned), never pooled.
+  size_t partial_bytes_ = 0;
+  char* partials_ = nullptr;
+  size_t take_partials(size_t bytes) {
+    const size_t b = partial_bytes_;
+    partial_bytes_ += (bytes + 255) & ~(size_t)255;
+    return b;
+  }
   struct CkptPlan {
     tgst::Index ix;
     std::vector<std::pair<size_t, int>> writes;   // (index in ix.tensors, tensor id)
@@ -353,6 +363,12 @@ class Runtime {
   // the same shape whose inputs are ready are launched together.
   struct ColSumOp { int a, b; int64_t R, C; };   // b >= 0: sum of the product a * b
   std::map<int, ColSumOp> colsum_;
+  // Deferred column sums whose operand is an output of a GEMM epilogue: that epilogue writes
+  // f64 column partials (`rows` rows at byte offset `off` of partials_), which the
+  // column-sum launch adds instead of reading the operand back.
+  struct ColPart { size_t off; int64_t rows; };
+  std::map<int, ColPart> colsum_part_;
+  bool use_colsum_epi_ = true;       // TG_COLSUM_EPI=0: the column sums read their operands
   std::vector<bool> colsum_done_, mul_absorbed_;
   void match_colsums();
   // Sums of products: an add tree ((p1 + p2) + p3 ..) over single-use GEMM products of one
@@ -574,6 +590,7 @@ Runtime::Runtime(const char* json, Runtime* par, bool plan_only) : parent(par) {
   if (const char* g = std::getenv("TG_COLSUM_SCATTER")) use_colsum_scatter_ = std::string(g) != "0";
   if (const char* g = std::getenv("TG_COLSUM_LOSS")) use_colsum_loss_ = std::string(g) != "0";
   if (const char* g = std::getenv("TG_COLSUM_MID")) use_colsum_mid_ = std::string(g) != "0";
+  if (const char* g = std::getenv("TG_COLSUM_EPI")) use_colsum_epi_ = std::string(g) != "0";
   if (const char* g = std::getenv("TG_GEMM_EPI")) gemm_epi_mode_ = std::string(g) == "1" ? kEpiAll : (std::string(g) == "0" ? kEpiOff : kEpiCheap);
   if (const char* g = std::getenv("TG_FUSED")) use_jit_ = std::string(g) != "vm";
   if (const char* g = std::getenv("TG_CONV")) use_conv_gemm_ = std::string(g) != "direct";
@@ -653,6 +670,7 @@ Runtime::~Runtime() {
   if (input_region_) hipFree(input_region_);
   if (workspace_ && !plan_only_) hipFree(workspace_);
   if (counters_ && !plan_only_) hipFree(counters_);
+  if (partials_ && !plan_only_) hipFree(partials_);
   if (fused_code_dev_ && !plan_only_) hipFree(fused_code_dev_);
   for (void* t : dev_tables_) hipFree(t);
   for (char* p : slots_) if (p) hipFree(p);
@@ -2669,24 +2687,29 @@ void Runtime::emit_colsums(const std::vector<int>& batch, bool with_scatter, boo
     std::vector<int> ts;
     for (int sop : batch) {
       const ColSumOp& c = colsum_.at(sop);
+      const auto pt = colsum_part_.find(sop);
       cs.push_back(c.C);
-      rs.push_back(c.R);
+      rs.push_back(pt != colsum_part_.end() ? pt->second.rows : c.R);
       ts.push_back(c.b >= 0 ? 2 : 1);
     }
     cscale = tgk::colsum_batch_scale(cs.data(), rs.data(), ts.data(), (int)batch.size());
   }
   for (int sop : batch) {
     const ColSumOp& c = colsum_.at(sop);
-    n.reads.push_back(root(c.a));
+    const auto pt = colsum_part_.find(sop);
+    const bool from_part = pt != colsum_part_.end();   // a GEMM epilogue's f64 partials
+    const int64_t R = from_part ? pt->second.rows : c.R;
+    if (!from_part) n.reads.push_back(root(c.a));
     if (c.b >= 0) n.reads.push_back(root(c.b));
     const int out = O(sop).at("out").i32();
     n.writes.push_back(root(out));
-    n.bytes += 4.0 * (c.R * c.C * (c.b >= 0 ? 2 : 1) + c.C);
-    n.detail += std::string(n.detail.empty() ? "" : ",") + (c.b >= 0 ? "mul,sum_to_shape" : "sum_to_shape");
+    n.bytes += from_part ? 8.0 * R * c.C + 4.0 * c.C : 4.0 * (c.R * c.C * (c.b >= 0 ? 2 : 1) + c.C);
+    n.detail += std::string(n.detail.empty() ? "" : ",") +
+                (c.b >= 0 ? "mul,sum_to_shape" : from_part ? "sum_partials" : "sum_to_shape");
     ws_off.push_back(ws);
     const int terms = c.b >= 0 ? 2 : 1;
-    ws += ((size_t)tgk::colsum_workspace_doubles(c.C, c.R, terms, cscale) * 8 + 255) & ~(size_t)255;
-    cbase.push_back(take_counters(tgk::colsum_counters(c.C, c.R, terms, cscale)));
+    ws += ((size_t)tgk::colsum_workspace_doubles(c.C, R, terms, cscale) * 8 + 255) & ~(size_t)255;
+    cbase.push_back(take_counters(tgk::colsum_counters(c.C, R, terms, cscale)));
   }
   const std::vector<DeferredRowSum> rsums = with_rowsums ? deferred_rowsum_ : std::vector<DeferredRowSum>{};
   std::vector<size_t> rws_off;
@@ -2751,10 +2774,19 @@ void Runtime::emit_colsums(const std::vector<int>& batch, bool with_scatter, boo
     for (size_t q = 0; q < batch.size(); ++q) {
       const ColSumOp& c = colsum_.at(batch[q]);
       const int out = O(batch[q]).at("out").i32();
+      double* part = reinterpret_cast<double*>(reinterpret_cast<char*>(cur_ws_) + ws_off[q]);
+      const auto pt = colsum_part_.find(batch[q]);
+      if (pt != colsum_part_.end()) {
+        if (T_[root(out)].numel < c.C || pt->second.off + (size_t)pt->second.rows * c.C * 8 > partial_bytes_)
+          throw Error(TG_INTERNAL, "column sum: partials outside their region");
+        bt.s[q] = tgk::colsum_desc_f64(reinterpret_cast<const double*>(partials_ + pt->second.off),
+                                       (float*)dptr(out), c.C, pt->second.rows, part, cur_counters_ + cbase[q],
+                                       cscale);
+        continue;
+      }
       if (T_[root(c.a)].numel < c.R * c.C || (c.b >= 0 && T_[root(c.b)].numel < c.R * c.C) ||
           T_[root(out)].numel < c.C)
         throw Error(TG_INTERNAL, "column sum: operand smaller than its shape");
-      double* part = reinterpret_cast<double*>(reinterpret_cast<char*>(cur_ws_) + ws_off[q]);
       bt.s[q] = tgk::colsum_desc((const float*)dptr(c.a), c.b >= 0 ? (const float*)dptr(c.b) : nullptr,
                                  (float*)dptr(out), c.C, c.R, c.C, 1.0, part, cur_counters_ + cbase[q], cscale);
     }
@@ -3176,6 +3208,40 @@ void Runtime::lower_gemm_epi(int op, const tgk::GemmDesc& d, int a, int b, int o
   n.bytes = 4.0 * ((double)T_[a].numel + T_[b].numel) + (store_c ? 4.0 * T_[out].numel : 0.0);
   for (auto& e : gp.ext) if (root(e.first) != out) n.bytes += 4.0 * T_[e.first].numel;
   for (int t : gp.outs) n.bytes += 4.0 * T_[t].numel;
+  // A deferred column sum of one of the group's outputs over all of the product's rows:
+  // the epilogue also writes that output's column partials (one f64 row per tile row slot
+  // of wavefronts), which the column-sum launch adds instead of reading the output back.
+  int cs_out = -1, cs_op = -1;
+  size_t cs_off = 0;
+  if (use_colsum_epi_ && any_deferred_colsum_ && d.batch == 1) {
+    for (size_t q = 0; q < gp.outs.size() && cs_op < 0; ++q) {
+      const int t = gp.outs[q];
+      if (T_[t].dt != F32 || T_[t].numel != d.M * d.N || !view_[t].contiguous()) continue;
+      for (const auto& kv : colsum_) {
+        const ColSumOp& so = kv.second;
+        if (root(so.a) != root(t) || T_[so.a].numel != T_[t].numel || !view_[so.a].contiguous() || so.b >= 0 ||
+            so.C != d.N || so.R != d.M || !defer_colsum_[kv.first] || colsum_done_[kv.first] ||
+            colsum_part_.count(kv.first))
+          continue;
+        cs_op = kv.first;
+        cs_out = (int)q;
+        break;
+      }
+    }
+    if (cs_op >= 0) {
+      tgk::GemmEpiCfg c{};
+      tgk::gd::GemmArgs ga{};
+      int64_t blocks = 0;
+      const bool ok = is_cat ? tgk::gemm_cat_epi_cfg(d, tgk::GemmCat{nullptr, cf.k0, cf.k1}, c, ga, blocks)
+                             : tgk::gemm_epi_cfg(d, c, ga, blocks);
+      if (!ok) throw Error(TG_INTERNAL, "GEMM epilogue: no direct-to-LDS launch");
+      const int64_t rows = tgk::gemm_epi_colsum_rows(c, ga);
+      cs_off = take_partials((size_t)rows * (size_t)d.N * 8);
+      colsum_part_[cs_op] = ColPart{cs_off, rows};
+      n.bytes += 8.0 * (double)rows * (double)d.N;
+      n.detail += ",colsum";
+    }
+  }
   const size_t code_off = fused_code_.size();
   fused_code_.insert(fused_code_.end(), gp.code.begin(), gp.code.end());
   n.bind = [=]() -> std::function<void(hipStream_t)> {
@@ -3268,6 +3334,12 @@ void Runtime::lower_gemm_epi(int op, const tgk::GemmDesc& d, int a, int b, int o
     c.N = d.N;
     c.h_in = h_in;
     c.store_c = store_c;
+    if (cs_op >= 0) {
+      if (tgk::gemm_epi_colsum_rows(c, ga) != colsum_part_.at(cs_op).rows)
+        throw Error(TG_INTERNAL, "GEMM epilogue: column partial rows differ from the plan");
+      c.colsum_out = cs_out;
+      ga.colsum = reinterpret_cast<double*>(partials_ + cs_off);
+    }
     tgk::JitKernel jk = tgk::gemm_epi_kernel(p, fused_code_.data() + code_off, c);
     const size_t js = jit_slots_.size();
     jit_slots_.emplace_back();
@@ -4233,6 +4305,7 @@ void Runtime::allocate() {
     for (int t : input_roots) ptr_[t] = input_region_ + input_offset_[t];
     workspace_ = reinterpret_cast<float*>(input_region_ + input_region_bytes_ + 4096);
     counters_ = reinterpret_cast<unsigned*>(fake + ((uintptr_t)1 << 39));
+    partials_ = fake + ((uintptr_t)1 << 40);
     arena_ = nullptr;
     input_region_ = nullptr;
     return;
@@ -4243,6 +4316,7 @@ void Runtime::allocate() {
   for (int t : input_roots) ptr_[t] = input_region_ + input_offset_[t];
   hip_check(hipHostMalloc(&loss_host_, 256, hipHostMallocDefault), "hipHostMalloc");
   if (workspace_bytes_) hip_check(hipMalloc(&workspace_, (workspace_bytes_ + 255) & ~(size_t)255), "hipMalloc(workspace)");
+  if (partial_bytes_) hip_check(hipMalloc(&partials_, partial_bytes_), "hipMalloc(column partials)");
   if (counter_slots_) {
     hip_check(hipMalloc(&counters_, counter_slots_ * sizeof(unsigned)), "hipMalloc(counters)");
     hip_check(hipMemset(counters_, 0, counter_slots_ * sizeof(unsigned)), "hipMemset(counters)");

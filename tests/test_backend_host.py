@@ -259,7 +259,25 @@ def test_skip_concatenation_gradients_lower_without_copies():
     assert shapes.count(('gemm', '[63,65536]x[65536,256]')) == 1
     relu_grads = [n for n in nodes if n.get('ops') == 'relu_grad']
     assert len(relu_grads) == 1, relu_grads   # the head's, after the [256, 4] product
-    assert len([n for n in nodes if n.get('ops') == 'gemm+relu_grad']) == 7
+    assert len([n for n in nodes if (n.get('ops') or '').startswith('gemm+relu_grad')]) == 7
+
+
+def test_bias_sums_come_from_gemm_epilogues(monkeypatch):
+    """C4's hidden-layer bias gradients are column sums of the ReLU-gradient outputs of
+    GEMM epilogues: those epilogues write f64 column partials (one row per tile row slot of
+    wavefronts) and the deferred column-sum launch adds the partials instead of reading the
+    [65536, 256] gradients back. TG_COLSUM_EPI=0 restores the reads."""
+    cfg = configs.CONFIGS['nerf']
+    ir = build_training_ir(cfg.make_model(), cfg.loss, cfg.inputs, cfg.optimizer)
+    nodes = backend.plan(ir.wire_json())['nodes']
+    epi = [n for n in nodes if (n.get('ops') or '').endswith(',colsum')]
+    assert len(epi) == 7, [n.get('ops') for n in nodes]
+    red = [n for n in nodes if n['kind'] == 'reduce' and 'sum_partials' in (n.get('ops') or '')]
+    assert len(red) == 1 and red[0]['ops'].split(',').count('sum_partials') == 7
+    assert red[0]['bytes'] < 100e6   # 2 operands read whole, 7 x 1024 x 256 partials
+    monkeypatch.setenv('TG_COLSUM_EPI', '0')
+    plain = backend.plan(ir.wire_json())['nodes']
+    assert not [n for n in plain if 'colsum' in (n.get('ops') or '') or 'partials' in (n.get('ops') or '')]
 
 
 def test_sums_of_products_lower_to_one_gemm(monkeypatch):
