@@ -520,6 +520,91 @@ struct StoreC {
 };
 
 
+// Short products (K at most 16, many outputs: C4's head input gradient [65536, 4] x
+// [4, 256]), where a 32-k MFMA stage would be mostly padding and the output is the traffic.
+// Block b of tiles_n x tiles_m x batch takes RM rows and 256 columns: thread t keeps column
+// 256 bn + t of B in registers, the block's rows of A sit in LDS, and each output is an f32
+// FMA chain from +0 in increasing k, four rows' chains side by side, stored as they finish
+// (consecutive threads, consecutive columns). Both operands are padded with zeros from K to
+// KB: a chain starts at +0 and so never holds -0, and adding +0 to it changes no bit.
+// Operand loads are unconditional, from a clamped index, and masked after: a select would
+// let the compiler move each load into a branch with its own wait.
+// An epilogue that reads other tensors (kPrefetch) has the thread's loads for its RM
+// outputs issued first; with kColSum the thread also writes its column's total over the
+// block's rows (f64, in row order) to g.colsum[bm * N + n] (one batch).
+template <int RM, int KB, class Epi>
+__device__ __forceinline__ void smallk_tile(const GemmArgs& g, const Epi& epi) {
+  static_assert(RM % 4 == 0 && KB % 4 == 0, "rows in fours, k in fours");
+  __shared__ __attribute__((aligned(16))) float As[RM * KB];
+  const GemmDesc& d = g.d;
+  const int nblk_n = g.tiles_n, nblk_m = g.tiles_m;
+  const int64_t blk = blockIdx.x;
+  const int bn = (int)(blk % nblk_n);
+  const int64_t rest = blk / nblk_n;
+  const int bm = (int)(rest % nblk_m);
+  const int64_t z = rest / nblk_m;
+  const int64_t z0 = z / d.bdiv, z1 = z % d.bdiv;
+  const int K = (int)d.K;
+  const int64_t m0 = (int64_t)bm * RM, n = (int64_t)bn * 256 + threadIdx.x;
+  const float* A = d.A + z0 * d.sAz0 + z1 * d.sAz1;
+  const float* B = d.B + z0 * d.sBz0 + z1 * d.sBz1;
+  const int rows = (int)min((int64_t)RM, d.M - m0);
+  auto keep = [](float v, bool ok) { return __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, v) & (ok ? ~0u : 0u)); };
+  for (int e = threadIdx.x; e < RM * KB; e += 256) {
+    const int r = e / KB, k = e % KB;
+    const float v = A[(m0 + min(r, rows - 1)) * d.sAm + (int64_t)min(k, K - 1) * d.sAk];
+    As[e] = keep(v, r < rows && k < K);
+  }
+  const bool on = n < d.N;
+  const float* bc = B + (on ? n : 0) * d.sBn;
+  float b[KB];
+#pragma unroll
+  for (int k = 0; k < KB; ++k) b[k] = keep(bc[(int64_t)min(k, K - 1) * d.sBk], on && k < K);
+  __syncthreads();
+  if (!on) return;
+  auto four_rows = [&](int r, float* acc) {
+#pragma unroll
+    for (int k = 0; k < KB; k += 4) {
+      f32x4 a4[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) a4[j] = *reinterpret_cast<const f32x4*>(As + (r + j) * KB + k);
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[j] = fmaf(a4[j][u], b[k + u], acc[j]);
+      asm volatile("" ::: "memory");   // one step's LDS reads at a time
+    }
+  };
+  if constexpr (Epi::kPrefetch) {
+    typename Epi::Pre pre[RM];
+#pragma unroll
+    for (int r = 0; r < RM; ++r) pre[r] = epi.load(d, m0 + min(r, rows - 1), n);
+    double cs = 0.0;
+#pragma unroll
+    for (int r = 0; r < RM; r += 4) {
+      if (r >= rows) break;
+      float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      four_rows(r, acc);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (r + j < rows) {
+          if constexpr (Epi::kColSum) cs += (double)epi(d, z0, z1, m0 + r + j, n, acc[j], pre[r + j]);
+          else epi(d, z0, z1, m0 + r + j, n, acc[j], pre[r + j]);
+        }
+    }
+    if constexpr (Epi::kColSum) g.colsum[(int64_t)bm * d.N + n] = cs;
+  } else {
+    float* C = d.C + z0 * d.sCz0 + z1 * d.sCz1 + n * d.sCn;
+    for (int r = 0; r < rows; r += 4) {
+      float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      four_rows(r, acc);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (r + j < rows) C[(m0 + r + j) * d.sCm] = acc[j];
+    }
+  }
+}
+
 }  // namespace gd
 }  // namespace tgk
 

@@ -360,11 +360,15 @@ JitKernel gemm_epi_kernel(const FusedProgram& p, const FusedInstr* code, const G
   o << "extern \"C\" __global__ void __launch_bounds__(" << c.nt
     << ") @NAME@(const tgk::gd::GemmArgs g, const tgk::JitArgs A) {\n";
   o << "  const @NAME@_epi e{A, " << (dropout ? "A.seed ? (unsigned)*A.seed : 0u" : "0u") << "};\n";
-  o << "  tgk::gd::gemm_tile<" << c.bm << ", " << c.bn << ", " << c.bk << ", " << c.ns << ", " << (c.ak ? "true" : "false")
-    << ", " << (c.bkf ? "true" : "false") << ", " << c.nt << ", " << c.kg;
-  // a concatenation along k: the second A source and the partial last stage (KT, CAT)
-  if (c.cat) o << ", @NAME@_epi, false, false, true, false, true";
-  o << ">(g, tgk::gd::xcd_order(blockIdx.x, gridDim.x), e);\n}\n";
+  if (c.smallk) {
+    o << "  tgk::gd::smallk_tile<" << c.bm << ", " << c.bk << ">(g, e);\n}\n";
+  } else {
+    o << "  tgk::gd::gemm_tile<" << c.bm << ", " << c.bn << ", " << c.bk << ", " << c.ns << ", "
+      << (c.ak ? "true" : "false") << ", " << (c.bkf ? "true" : "false") << ", " << c.nt << ", " << c.kg;
+    // a concatenation along k: the second A source and the partial last stage (KT, CAT)
+    if (c.cat) o << ", @NAME@_epi, false, false, true, false, true";
+    o << ">(g, tgk::gd::xcd_order(blockIdx.x, gridDim.x), e);\n}\n";
+  }
   JitKernel k;
   std::string body = o.str();
   char nm[32];

@@ -595,70 +595,26 @@ __global__ __launch_bounds__(256) void k_gemm_tiny(const GemmDesc d) {
   }
 }
 
-// Short products (K <= kSmallK, many outputs: C4's head input gradient [65536, 4] x
-// [4, 256]): the output is the traffic, and a 32-k MFMA stage would be mostly padding. A
-// block takes RM rows and 256 columns: thread t keeps column n0 + t of B in registers,
-// the block's rows of A sit in LDS, and each output is an f32 FMA chain from +0 in
-// increasing k, four rows' chains side by side, stored as they finish (consecutive
-// threads, consecutive columns). Both operands are padded with zeros from K to KB: a chain
-// starts at +0 and so never holds -0, and adding +0 to it changes no bit. Operand loads
-// are unconditional, from a clamped index, and masked after: a select would let the
-// compiler move each load into a branch with its own wait. (Longer K measured slower
-// here than the tiles: the compiler keeps every unrolled LDS read in registers.)
+// Short products (K <= kSmallK, many outputs): smallk_tile (gemm_dev.h). Longer K measured
+// slower there than the tiles: the compiler keeps every unrolled LDS read in registers.
 constexpr int kSmallK = 16;
 
 template <int RM, int KB>
-__global__ __launch_bounds__(256) void k_gemm_smallk(const GemmDesc d, int nblk_n, int nblk_m) {
-  static_assert(RM % 4 == 0 && KB % 4 == 0, "rows in fours, k in fours");
-  __shared__ __attribute__((aligned(16))) float As[RM * KB];
-  const int64_t blk = blockIdx.x;
-  const int bn = (int)(blk % nblk_n);
-  const int64_t rest = blk / nblk_n;
-  const int bm = (int)(rest % nblk_m);
-  const int64_t z = rest / nblk_m;
-  const int64_t z0 = z / d.bdiv, z1 = z % d.bdiv;
-  const int K = (int)d.K;
-  const int64_t m0 = (int64_t)bm * RM, n = (int64_t)bn * 256 + threadIdx.x;
-  const float* A = d.A + z0 * d.sAz0 + z1 * d.sAz1;
-  const float* B = d.B + z0 * d.sBz0 + z1 * d.sBz1;
-  const int rows = (int)min<int64_t>(RM, d.M - m0);
-  auto keep = [](float v, bool ok) { return __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, v) & (ok ? ~0u : 0u)); };
-  for (int e = threadIdx.x; e < RM * KB; e += 256) {
-    const int r = e / KB, k = e % KB;
-    const float v = A[(m0 + min(r, rows - 1)) * d.sAm + (int64_t)min(k, K - 1) * d.sAk];
-    As[e] = keep(v, r < rows && k < K);
-  }
-  const bool on = n < d.N;
-  const float* bc = B + (on ? n : 0) * d.sBn;
-  float b[KB];
-#pragma unroll
-  for (int k = 0; k < KB; ++k) b[k] = keep(bc[(int64_t)min(k, K - 1) * d.sBk], on && k < K);
-  __syncthreads();
-  if (!on) return;
-  float* C = d.C + z0 * d.sCz0 + z1 * d.sCz1 + n * d.sCn;
-  for (int r = 0; r < rows; r += 4) {
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int k = 0; k < KB; k += 4) {
-      f32x4 a4[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) a4[j] = *reinterpret_cast<const f32x4*>(As + (r + j) * KB + k);
-#pragma unroll
-      for (int u = 0; u < 4; ++u)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[j] = fmaf(a4[j][u], b[k + u], acc[j]);
-      asm volatile("" ::: "memory");   // one step's LDS reads at a time
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (r + j < rows) C[(m0 + r + j) * d.sCm] = acc[j];
-  }
+__global__ __launch_bounds__(256) void k_gemm_smallk(const GemmArgs g) {
+  smallk_tile<RM, KB>(g, StoreC{});
 }
 
 }  // namespace
 
 bool gemm_is_smallk(const GemmDesc& d) {
   return d.M > 0 && d.N > 0 && d.K > 0 && d.batch > 0 && d.K <= kSmallK && d.M * d.N * d.batch >= 65536;
+}
+
+// Rows per small-K block: 16 where that still gives four or more blocks per CU, else 8 or 4
+static int smallk_rows(const GemmDesc& d) {
+  const int64_t nbn = (d.N + 255) / 256;
+  auto nblocks = [&](int rm) { return (d.M + rm - 1) / rm * nbn * d.batch; };
+  return nblocks(16) >= 1024 ? 16 : nblocks(8) >= 1024 ? 8 : 4;
 }
 
 bool gemm_is_tiny(const GemmDesc& d) {
@@ -686,13 +642,12 @@ void gemm(const GemmDesc& d, float* work, hipStream_t st) {
   }
   if (gemm_is_smallk(d)) {
     const int nbn = (int)((d.N + 255) / 256);
-    // 16-row blocks where that still gives four or more blocks per CU, else 8 or 4 rows
-    auto nblocks = [&](int rm) { return (d.M + rm - 1) / rm * nbn * d.batch; };
-    const int rm = nblocks(16) >= 1024 ? 16 : nblocks(8) >= 1024 ? 8 : 4;
+    const int rm = smallk_rows(d);
     const int nbm = (int)((d.M + rm - 1) / rm);
     const int64_t blocks = (int64_t)nbn * nbm * d.batch;
     if (blocks >= (int64_t(1) << 31)) throw std::runtime_error("gemm: too many blocks");
-#define TG_SMALLK(RM_, KB_) klaunch(k_gemm_smallk<RM_, KB_>, (unsigned)blocks, 256, 0, st, d, nbn, nbm)
+    GemmArgs ga{d, d.K, 1, nbn, nbm, nullptr, 0, 0};
+#define TG_SMALLK(RM_, KB_) klaunch(k_gemm_smallk<RM_, KB_>, (unsigned)blocks, 256, 0, st, ga)
 #define TG_SMALLK_RM(RM_)                                                                  \
   if (d.K <= 8) TG_SMALLK(RM_, 8);                                                        \
   else TG_SMALLK(RM_, 16);
@@ -936,6 +891,23 @@ bool gemm_prefers_group(const GemmDesc& d) {
 
 bool gemm_epi_cfg(const GemmDesc& d, GemmEpiCfg& c, GemmArgs& g, int64_t& blocks) {
   if (d.M <= 0 || d.N <= 0 || d.batch <= 0) return false;
+  if (gemm_is_tiny(d)) return false;
+  if (gemm_is_smallk(d)) {   // the small-K kernel gemm() runs, one batch
+    if (d.batch != 1) return false;
+    const int rm = smallk_rows(d);
+    g = GemmArgs{d, d.K, 1, (int)((d.N + 255) / 256), (int)((d.M + rm - 1) / rm), nullptr, 0, 0};
+    blocks = (int64_t)g.tiles_n * g.tiles_m;
+    c.smallk = true;
+    c.bm = rm;
+    c.bk = d.K <= 8 ? 8 : 16;
+    c.bn = 256;
+    c.nt = 256;
+    c.kg = 1;
+    c.ns = 0;
+    c.ak = d.sAk == 1;
+    c.bkf = d.sBk == 1 && d.sBn != 1;
+    return blocks < (int64_t(1) << 31);
+  }
   const Plan p = plan_for(d);
   const bool ak = d.sAk == 1;
   const bool bk = d.sBk == 1 && d.sBn != 1;
@@ -955,6 +927,7 @@ bool gemm_epi_cfg(const GemmDesc& d, GemmEpiCfg& c, GemmArgs& g, int64_t& blocks
 }
 
 int64_t gemm_epi_colsum_rows(const GemmEpiCfg& c, const GemmArgs& g) {
+  if (c.smallk) return g.tiles_m;   // one row per block of rows
   // gemm_tile's wavefront grid: NW wavefronts per k group, 4 x 2 for eight with a 64-wide
   // tile, else 2 along M
   const int nw = c.nt / c.kg / 64;

@@ -325,6 +325,7 @@ struct GemmEpiCfg {
   bool store_c = false;   // the epilogue also stores the product itself to C
   bool cat = false;       // A is a concatenation along k (gemm_cat)
   int colsum_out = -1;    // output whose column partial sums the epilogue writes (GemmArgs::colsum)
+  bool smallk = false;    // the small-K kernel (smallk_tile, bm rows of k padded to bk) instead of the tile
 };
 // Rows of the f64 column partials an epilogue with colsum_out writes for this launch
 // (tiles along M times the wavefronts along M of a tile).
