@@ -130,7 +130,7 @@ __global__ void k_max_pool(const float* __restrict__ x, float* __restrict__ y, P
 // Gather form of the pool adjoint: each input element collects dy from every window
 // whose (recomputed) argmax is this element.
 __global__ void k_max_pool_grad(const float* __restrict__ x, const float* __restrict__ dy, float* __restrict__ dx,
-                                PoolDesc p) {
+                                PoolDesc p, bool relu) {
   const int64_t total = p.B * p.C * p.H * p.W;
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
     int64_t wi = i % p.W, t = i / p.W;
@@ -162,7 +162,7 @@ __global__ void k_max_pool_grad(const float* __restrict__ x, const float* __rest
         if (ah == hi && aw == wi) s += (double)dy[(bc * p.Ho + ho) * p.Wo + wo];
       }
     }
-    dx[i] = (float)s;
+    dx[i] = relu && !(plane[hi * p.W + wi] > 0.0f) ? 0.0f : (float)s;
   }
 }
 
@@ -204,9 +204,11 @@ __global__ void k_max_pool32(const float* __restrict__ x, float* __restrict__ y,
 // Adjoint when the windows tile the input exactly (stride = window, no padding, H = Ho*sH,
 // W = Wo*sW): every input element lies in exactly one window, so each window writes its
 // own elements: dy at the recomputed argmax (the first maximum in scan order), zero
-// elsewhere. Equal to the gather form bit for bit (one term per element).
+// elsewhere. Equal to the gather form bit for bit (one term per element). With `relu` the
+// ReLU gradient of the pooled input follows: only the argmax element can be non-zero, and
+// its mask is the window's maximum > 0 (+0 where it is not, NaN included).
 __global__ void k_max_pool_grad_tiled(const float* __restrict__ x, const float* __restrict__ dy,
-                                      float* __restrict__ dx, Pool32 p) {
+                                      float* __restrict__ dx, Pool32 p, bool relu) {
   for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < p.nwin; i += gridDim.x * blockDim.x) {
     int bc, ho, wo;
     window_of(p, i, bc, ho, wo);
@@ -219,7 +221,7 @@ __global__ void k_max_pool_grad_tiled(const float* __restrict__ x, const float* 
         const float v = x[base + off];
         if (v > m) { m = v; arg = off; }
       }
-    const float g = dy[i];
+    const float g = relu && !(m > 0.0f) ? 0.0f : dy[i];
     for (int kh = 0; kh < p.kH; ++kh)
       for (int kw = 0; kw < p.kW; ++kw) {
         const int off = (ho * p.sH + kh) * p.W + wo * p.sW + kw;
@@ -254,7 +256,7 @@ __global__ void k_max_pool22(const float* __restrict__ x, float* __restrict__ y,
 }
 
 __global__ void k_max_pool22_grad(const float* __restrict__ x, const float* __restrict__ dy,
-                                  float* __restrict__ dx, Pool32 p) {
+                                  float* __restrict__ dx, Pool32 p, bool relu) {
   for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < p.nwin; i += gridDim.x * blockDim.x) {
     int bc, ho, wo;
     window_of(p, i, bc, ho, wo);
@@ -268,6 +270,7 @@ __global__ void k_max_pool22_grad(const float* __restrict__ x, const float* __re
     if (a.y > m) { m = a.y; arg = 1; }
     if (b.x > m) { m = b.x; arg = 2; }
     if (b.y > m) { m = b.y; arg = 3; }
+    if (relu && !(m > 0.0f)) arg = -1;   // the ReLU gradient of the pooled input (see above)
     *reinterpret_cast<float2*>(dx + base) = make_float2(arg == 0 ? g : 0.0f, arg == 1 ? g : 0.0f);
     *reinterpret_cast<float2*>(dx + base + p.W) = make_float2(arg == 2 ? g : 0.0f, arg == 3 ? g : 0.0f);
   }
@@ -327,17 +330,18 @@ void max_pool(const float* x, float* y, const PoolDesc& p, hipStream_t st) {
   klaunch(k_max_pool, grid_for(n), 256, 0, st, x, y, p);
 }
 
-void max_pool_grad(const float* x, const float* dy, float* dx, const PoolDesc& p, hipStream_t st) {
+void max_pool_grad(const float* x, const float* dy, float* dx, const PoolDesc& p, hipStream_t st, bool relu) {
   int64_t n = p.B * p.C * p.H * p.W;
   if (n <= 0) return;
   const bool tiled = p.sH == p.kH && p.sW == p.kW && p.pH == 0 && p.pW == 0 && p.H == p.Ho * p.sH &&
                      p.W == p.Wo * p.sW;
   if (tiled && pool_small(p)) {
-    if (pool22(p, x, dx)) klaunch(k_max_pool22_grad, grid_for(p.B * p.C * p.Ho * p.Wo), 256, 0, st, x, dy, dx, pool32(p));
-    else klaunch(k_max_pool_grad_tiled, grid_for(p.B * p.C * p.Ho * p.Wo), 256, 0, st, x, dy, dx, pool32(p));
+    if (pool22(p, x, dx))
+      klaunch(k_max_pool22_grad, grid_for(p.B * p.C * p.Ho * p.Wo), 256, 0, st, x, dy, dx, pool32(p), relu);
+    else klaunch(k_max_pool_grad_tiled, grid_for(p.B * p.C * p.Ho * p.Wo), 256, 0, st, x, dy, dx, pool32(p), relu);
     return;
   }
-  klaunch(k_max_pool_grad, grid_for(n), 256, 0, st, x, dy, dx, p);
+  klaunch(k_max_pool_grad, grid_for(n), 256, 0, st, x, dy, dx, p, relu);
 }
 
 }  // namespace tgk

@@ -382,7 +382,9 @@ void conv2d_weight_grad_gemm(const float* x, const float* dy, float* dw, const C
                              hipStream_t st);
 struct PoolDesc { int64_t B, C, H, W, Ho, Wo, kH, kW, sH, sW, pH, pW; };
 void max_pool(const float* x, float* y, const PoolDesc& p, hipStream_t st);
-void max_pool_grad(const float* x, const float* dy, float* dx, const PoolDesc& p, hipStream_t st);
+// relu: also apply relu_grad(x, .) with x the pool's input (the ReLU output it pools):
+// dx = x > 0 ? dx : +0, in the same launch.
+void max_pool_grad(const float* x, const float* dy, float* dx, const PoolDesc& p, hipStream_t st, bool relu = false);
 
 // ---- optimizer (k_optim.hip) ----------------------------------------------------------
 // One fused multi-tensor update (Adam / AdamW, or SGD with momentum, Nesterov and L2

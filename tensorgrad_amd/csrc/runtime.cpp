@@ -382,6 +382,7 @@ class Runtime {
   struct CatFwd { int src0, src1; int64_t k0, k1; };
   std::map<int, CatFwd> cat_fwd_;     // matmul op -> its A's sources
   std::vector<char> cat_absorbed_;    // concat op -> not lowered
+  std::vector<char> pool_absorbed_;   // relu_grad op applied by the max-pool gradient launch before it
   void match_concat_products();
   void check_cat_spans(const tgk::GemmDesc& d, const CatFwd& c, int b, int out, bool with_c) const;
   std::vector<char> sum_absorbed_;
@@ -1640,6 +1641,7 @@ void Runtime::lower() {
   if (const char* g = std::getenv("TG_OPT_FUSED")) use_fused_transforms_ = std::string(g) != "0";
   match_optimizer();
   gemm_done_.assign(ops_.size(), 0);
+  pool_absorbed_.assign(ops_.size(), 0);
   plan_gemm_groups();
   match_concat_products();
   match_attention();
@@ -1655,7 +1657,7 @@ void Runtime::lower() {
   if (use_remat_) remat_groups();
   group_done_.assign(groups_.size(), 0);
   for (size_t i = 0; i < ops_.size(); ++i) {
-    if (is_leaf((int)i) || virtual_[i] || cat_absorbed_[i]) continue;
+    if (is_leaf((int)i) || virtual_[i] || cat_absorbed_[i] || pool_absorbed_[i]) continue;
     if (adam_ops_.count((int)i)) continue;
     if (attn_of_[i] >= 0) {
       const int m = attn_of_[i];
@@ -4136,11 +4138,32 @@ void Runtime::lower_op(int i) {
     if (dy >= 0 && (to.numel != prod(xs) || ys[0] != p.B || ys[1] != p.C)) throw Error(TG_INVALID_ARGUMENT, "pool grad: size mismatch");
     n.bytes = 4.0 * (prod(xs) + prod(ys) + (dy >= 0 ? prod(xs) : 0));
     n.kind = "pool";
+    // The gradient read only by relu_grad(x', it) with x' the pool's own input (the ReLU
+    // output it pools, after relu_grads_from_outputs), in a group of its own or none: the
+    // pool launch applies the mask and writes the relu_grad's output; the op is skipped.
+    int rg_out = out;
+    if (dy >= 0 && consumers_[out].size() == 1 && T_[out].dt == F32 && view_[out].root == out) {
+      const int c = consumers_[out][0];
+      const int g = group_of_[c];
+      if (kinds_[c] == "relu_grad" && fld(c, "dy") == out && fld(c, "x") != out && root(fld(c, "x")) == root(x) &&
+          T_[fld(c, "x")].shape == xs && view_[fld(c, "x")].contiguous() && !virtual_[c] &&
+          (g < 0 || (groups_[g].ops.size() == 1 && groups_[g].dups.empty() && !group_done_[g]))) {
+        const int ro = O(c).at("out").i32();
+        if (view_[ro].root == ro && view_[ro].contiguous() && T_[ro].numel == to.numel && T_[ro].dt == F32) {
+          rg_out = ro;
+          if (g >= 0) group_done_[g] = 1;
+          else pool_absorbed_[c] = 1;
+          n.writes = {root(ro)};
+          n.detail = "max_pool_2d_grad,relu_grad";
+        }
+      }
+    }
+    const bool relu = rg_out != out;
     n.bind = [=]() -> std::function<void(hipStream_t)> {
-      const float* px = (const float*)dptr(x); float* po = (float*)dptr(out);
+      const float* px = (const float*)dptr(x); float* po = (float*)dptr(rg_out);
       if (dy < 0) return [=](hipStream_t st) { tgk::max_pool(px, po, p, st); };
       const float* pd = (const float*)dptr(dy);
-      return [=](hipStream_t st) { tgk::max_pool_grad(px, pd, po, p, st); };
+      return [=](hipStream_t st) { tgk::max_pool_grad(px, pd, po, p, st, relu); };
     };
   } else if (k == "adam_update_m" || k == "adam_update_v" || k == "adam_update_p") {
     throw Error(TG_INTERNAL, "adam op outside the fused update");

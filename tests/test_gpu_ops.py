@@ -758,6 +758,28 @@ def test_pool_kernels(k, s, pd):
     exact(got, want)
 
 
+@pytest.mark.parametrize('k,s,pd', [(3, 2, 1), (2, 2, 0), (3, 3, 0)])
+def test_pool_grad_with_relu_grad(k, s, pd):
+    """relu_grad(x, max_pool2d_grad(relu(x), d)) (the CNN's pooled ReLU layer): the pool
+    gradient launch applies the ReLU mask of its own input and writes the relu_grad's
+    output, for the gather and the scatter adjoints. Bit-exact against the oracle, with
+    ties, zeros, negative maxima and whole non-positive windows."""
+    H = 12
+    Ho = (H + 2 * pd - k) // s + 1
+    x = np.round(_rand([2, 3, H, H], 28) * 4) / 4 - 0.25
+    x[0, 0, :4, :4] = -1.0    # windows with no positive element
+    d = _rand([2, 3, Ho, Ho], 29)
+
+    def body():
+        xi = tensor_input('x', [2, 3, H, H])
+        g = O.max_pool2d_grad(O.relu(xi), tensor_input('d', [2, 3, Ho, Ho]), k, k, s, s, pd, pd)
+        return O.relu_grad(xi, g)
+    g = trace_fn(body)
+    assert 'max_pool_2d_grad,relu_grad' in _node_ops(g, {})
+    got, want = run_both(body, {'x': x, 'd': d})
+    exact(got, want)
+
+
 def test_relu_grad():
     x, dy = _rand([1000], 26), _rand([1000], 27)
     got, want = run_both(lambda: O.relu_grad(tensor_input('x', [1000]), tensor_input('d', [1000])), {'x': x, 'd': dy})
