@@ -59,7 +59,17 @@ struct ConvGemmArgs {
   const float* dy;
   float* out;                   // y / dx / dw
   float* work;                  // weight-gradient partials [split][G][M][N] (splits > 1)
+  // A pointwise group applied at the store: kConvEpiBiasRelu on the forward's
+  // output channel ch, kConvEpiReluMask on the input gradient's element.
+  int epi;
+  const float* ebias;           // [Cout]
+  const float* emask;           // laid out as the output
 };
+
+// kConvEpiBiasRelu: relu(v + bias[ch]) as the fused group computes it (f32 add; relu keeps
+// NaN as the canonical NaN and maps -0 to +0). kConvEpiReluMask: relu_grad(mask, v) =
+// mask > 0 ? v : +0, the mask at the output element's offset.
+constexpr int kConvEpiNone = 0, kConvEpiBiasRelu = 1, kConvEpiReluMask = 2;
 
 // x / d for 0 <= x < 2^31 (FastDiv, kernels.h), on the host or the device.
 CG_HD int fdiv(int x, const FastDiv& f) {

@@ -158,6 +158,42 @@ __global__ __launch_bounds__(kCT) void k_conv_gemm(ConvGemmArgs c) {
   // Register r of lane l holds row (r/4)*8 + (l/32)*4 + r%4, column l%32.
   float* O = (MODE == CV_WGRAD && c.splits > 1) ? c.work : c.out;
   const int64_t rs = ld.out_rs(c);
+  if (MODE != CV_WGRAD && c.epi != kConvEpiNone) {
+    // The layer's pointwise step at the store (one group, G = 1: channel gm). Every bias /
+    // mask value of the wavefront's outputs is loaded first (clamped in range): loaded
+    // between the stores, each would wait for the stores before it.
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int gn = min(ld.bp.n0 + wn0 + j * 32 + lrow, c.N - 1);
+      const int64_t cofs = ld.out_col(c, gn);
+      float e[TM][16];
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int gm = min(ld.bp.m0 + wm0 + i * 32 + (r / 4) * 8 + h * 4 + (r % 4), c.M - 1);
+          e[i][r] = c.epi == kConvEpiBiasRelu ? c.ebias[gm] : c.emask[cofs + gm * rs];
+        }
+      if (ld.bp.n0 + wn0 + j * 32 + lrow >= c.N) continue;
+      float* col = O + cofs;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int gm = ld.bp.m0 + wm0 + i * 32 + (r / 4) * 8 + h * 4 + (r % 4);
+          if (gm >= c.M) continue;
+          float v = acc[i][j][r];
+          if (c.epi == kConvEpiBiasRelu) {
+            const float a = v + e[i][r];
+            v = a != a ? __uint_as_float(0x7fc00000u) : (a > 0.0f ? a : 0.0f);
+          } else {
+            v = e[i][r] > 0.0f ? v : 0.0f;
+          }
+          col[gm * rs] = v;
+        }
+    }
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
     const int gn = ld.bp.n0 + wn0 + j * 32 + lrow;
@@ -258,6 +294,7 @@ struct SmallTaps {
 // each row as four 128-bit broadcasts.
 __global__ __launch_bounds__(256) void k_conv_small_fwd(const ConvGemmArgs c) {
   __shared__ __attribute__((aligned(16))) float ws[kSmallW];
+  __shared__ float bs[kSmallW / kSmallTaps];   // the group's biases (kConvEpiBiasRelu)
   const int hw = c.Ho * c.Wo;
   const int nchunk = (hw + 255) / 256;
   const int z = blockIdx.x / nchunk, chunk = blockIdx.x - z * nchunk;
@@ -266,6 +303,8 @@ __global__ __launch_bounds__(256) void k_conv_small_fwd(const ConvGemmArgs c) {
     const int co = i / kSmallTaps, q = i - co * kSmallTaps;
     ws[i] = q < c.K ? c.w[(int64_t)(g * c.CoutPG + co) * c.K + q] : 0.0f;
   }
+  if (c.epi == kConvEpiBiasRelu)
+    for (int i = threadIdx.x; i < c.CoutPG; i += 256) bs[i] = c.ebias[g * c.CoutPG + i];
   SmallTaps tp;
   tp.init(c);
   __syncthreads();
@@ -284,6 +323,10 @@ __global__ __launch_bounds__(256) void k_conv_small_fwd(const ConvGemmArgs c) {
       const f32x4 w4 = wr[u];
 #pragma unroll
       for (int e = 0; e < 4; ++e) s = fmaf(w4[e], xv[u * 4 + e], s);
+    }
+    if (c.epi == kConvEpiBiasRelu) {   // the bias from LDS
+      const float a = s + bs[co];
+      s = a != a ? __uint_as_float(0x7fc00000u) : (a > 0.0f ? a : 0.0f);
     }
     y[(int64_t)co * hw] = s;
   }
@@ -409,10 +452,15 @@ int64_t conv_gemm_workspace_bytes(const ConvDesc& d) {
   return (int64_t)p.splits * d.G * (d.Cout / d.G) * d.CinPG * d.kH * d.kW * 4;
 }
 
-void conv2d_gemm(const float* x, const float* w, float* y, const ConvDesc& d, hipStream_t st) {
+void conv2d_gemm(const float* x, const float* w, float* y, const ConvDesc& d, hipStream_t st, const float* bias) {
   const ConvPlan p = conv_plan(CV_FWD, d);
   ConvGemmArgs a = make_args(d, p);
   a.x = x; a.w = w; a.out = y;
+  if (bias) {
+    if (d.G != 1) throw std::runtime_error("conv2d: a bias epilogue needs one group");
+    a.epi = kConvEpiBiasRelu;
+    a.ebias = bias;
+  }
   a.avec = a.avec && ((uintptr_t)w & 15) == 0;
   if (d.CinPG * d.kH * d.kW <= kSmallTaps && (d.Cout / d.G) * kSmallTaps <= kSmallW) {
     // the K taps of a row of W are contiguous: W[co][cl][kh][kw] = w[co * K + q]
@@ -423,10 +471,15 @@ void conv2d_gemm(const float* x, const float* w, float* y, const ConvDesc& d, hi
   if (p.blocks > 0) launch_mode<CV_FWD>(p, a, true, st);
 }
 
-void conv2d_input_grad_gemm(const float* w, const float* dy, float* dx, const ConvDesc& d, hipStream_t st) {
+void conv2d_input_grad_gemm(const float* w, const float* dy, float* dx, const ConvDesc& d, hipStream_t st,
+                            const float* mask) {
   const ConvPlan p = conv_plan(CV_DGRAD, d);
   ConvGemmArgs a = make_args(d, p);
   a.w = w; a.dy = dy; a.out = dx;
+  if (mask) {
+    a.epi = kConvEpiReluMask;
+    a.emask = mask;
+  }
   if (p.blocks > 0) launch_mode<CV_DGRAD>(p, a, d.sH == 1 && d.sW == 1, st);
 }
 

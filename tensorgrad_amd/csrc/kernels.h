@@ -376,8 +376,12 @@ void conv2d_weight_grad(const float* x, const float* dy, float* dw, const ConvDe
 constexpr int64_t kConvWorkBytes = int64_t(12) << 20;
 bool conv_gemm_ok(const ConvDesc& c);
 int64_t conv_gemm_workspace_bytes(const ConvDesc& c);
-void conv2d_gemm(const float* x, const float* w, float* y, const ConvDesc& c, hipStream_t st);
-void conv2d_input_grad_gemm(const float* w, const float* dy, float* dx, const ConvDesc& c, hipStream_t st);
+// bias: store relu(y + bias[channel]) instead of y (the layer's bias + ReLU group; one
+// group of channels). mask: store relu_grad(mask, dx) = mask > 0 ? dx : +0 instead of dx.
+void conv2d_gemm(const float* x, const float* w, float* y, const ConvDesc& c, hipStream_t st,
+                 const float* bias = nullptr);
+void conv2d_input_grad_gemm(const float* w, const float* dy, float* dx, const ConvDesc& c, hipStream_t st,
+                            const float* mask = nullptr);
 void conv2d_weight_grad_gemm(const float* x, const float* dy, float* dw, const ConvDesc& c, float* work,
                              hipStream_t st);
 struct PoolDesc { int64_t B, C, H, W, Ho, Wo, kH, kW, sH, sW, pH, pW; };

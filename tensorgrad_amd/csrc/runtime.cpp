@@ -4104,16 +4104,70 @@ void Runtime::lower_op(int i) {
       n.ws = wsb > 0;
     }
     if (!mfma) n.detail = "direct";
+    // The output read only by a group of its own applying the layer's pointwise step, done
+    // at the store instead (the group is not lowered, its input never stored):
+    //  forward: relu(add(y, bias)) with bias [Cout] broadcast over channels (one group);
+    //  input gradient: relu_grad(mask, dx) with mask laid out as dx.
+    int epi_out = out, ebias = -1, emask = -1;
+    auto lone_group = [&](int op) {
+      const int g = group_of_[op];
+      return g >= 0 && groups_[g].dups.empty() && !group_done_[g] ? g : -1;
+    };
+    auto plain_out = [&](int t) {
+      return view_[t].root == t && view_[t].contiguous() && T_[t].dt == F32 && T_[t].numel == to.numel;
+    };
+    if (mfma && T_[out].dt == F32 && view_[out].root == out && consumers_[out].size() == 1) {
+      const int u = consumers_[out][0];
+      if (k == "conv2d" && c.G == 1 && kinds_[u] == "add" && lone_group(u) >= 0 &&
+          groups_[lone_group(u)].ops.size() == 2 && groups_[lone_group(u)].ops[0] == u) {
+        const int g = lone_group(u);
+        const int rl = groups_[g].ops[1];
+        const int a_out = O(u).at("out").i32();
+        const int bias = fld(u, "a") == out ? fld(u, "b") : fld(u, "a");
+        Dims bs = T_[bias].shape;
+        while (!bs.empty() && bs.front() == 1) bs.erase(bs.begin());
+        if (kinds_[rl] == "relu" && fld(rl, "a") == a_out && consumers_[a_out].size() == 1 && bias != out &&
+            T_[bias].dt == F32 && view_[bias].contiguous() && T_[bias].numel == c.Cout &&
+            bs == Dims({c.Cout, 1, 1}) && plain_out(O(rl).at("out").i32())) {
+          bool pinned_a = false;
+          for (int o : outputs_) pinned_a = pinned_a || root(o) == root(a_out);
+          for (auto& cp : captures_) pinned_a = pinned_a || root(cp.second) == root(a_out);
+          if (!pinned_a) {
+            epi_out = O(rl).at("out").i32();
+            ebias = bias;
+            group_done_[g] = 1;
+            n.detail = "conv2d,add,relu";
+          }
+        }
+      } else if (k == "conv2d_input_grad" && kinds_[u] == "relu_grad" && fld(u, "dy") == out && lone_group(u) >= 0 &&
+                 groups_[lone_group(u)].ops.size() == 1) {
+        const int m = fld(u, "x");
+        if (m != out && T_[m].dt == F32 && T_[m].shape == to.shape && view_[m].contiguous() &&
+            plain_out(O(u).at("out").i32())) {
+          epi_out = O(u).at("out").i32();
+          emask = m;
+          group_done_[lone_group(u)] = 1;
+          n.detail = "conv2d_input_grad,relu_grad";
+        }
+      }
+    }
+    if (epi_out != out) {
+      n.writes = {root(epi_out)};
+      if (ebias >= 0) rd(ebias);
+      if (emask >= 0) rd(emask);
+    }
     n.bind = [=]() -> std::function<void(hipStream_t)> {
-      float* po = (float*)dptr(out);
+      float* po = (float*)dptr(epi_out);
       if (k == "conv2d") {
         const float* px = (const float*)dptr(x); const float* pw = (const float*)dptr(w);
-        if (mfma) return [=](hipStream_t st) { tgk::conv2d_gemm(px, pw, po, c, st); };
+        const float* pb = ebias >= 0 ? (const float*)dptr(ebias) : nullptr;
+        if (mfma) return [=](hipStream_t st) { tgk::conv2d_gemm(px, pw, po, c, st, pb); };
         return [=](hipStream_t st) { tgk::conv2d(px, pw, po, c, st); };
       }
       if (k == "conv2d_input_grad") {
         const float* pw = (const float*)dptr(w); const float* pd = (const float*)dptr(dy);
-        if (mfma) return [=](hipStream_t st) { tgk::conv2d_input_grad_gemm(pw, pd, po, c, st); };
+        const float* pm = emask >= 0 ? (const float*)dptr(emask) : nullptr;
+        if (mfma) return [=](hipStream_t st) { tgk::conv2d_input_grad_gemm(pw, pd, po, c, st, pm); };
         return [=](hipStream_t st) { tgk::conv2d_input_grad(pw, pd, po, c, st); };
       }
       const float* px = (const float*)dptr(x); const float* pd = (const float*)dptr(dy);

@@ -741,6 +741,36 @@ def test_conv_kernels(impl, case):
             os.environ['TG_CONV'] = old
 
 
+@pytest.mark.parametrize('B,Ci,H,Co,k,pd', [(4, 3, 12, 16, 3, 1), (8, 1, 28, 32, 3, 0), (2, 8, 9, 40, 5, 2)])
+def test_conv_epilogues(B, Ci, H, Co, k, pd):
+    """A convolution whose output only its layer's pointwise step reads applies that step
+    at the store: relu(conv2d(x, w) + b) in the forward (the implicit GEMM, or the few-taps
+    kernel for a 1-channel input) and relu_grad(m, conv2d_input_grad(w, dy)) in the input
+    gradient. Against the oracle with the convolutions' GEMM tolerance; masks with ties at
+    zero and negative values."""
+    Ho = H + 2 * pd - k + 1
+    x, w, b = _rand([B, Ci, H, H], 31), _rand([Co, Ci, k, k], 32), _rand([Co], 33)
+    dy = _rand([B, Co, Ho, Ho], 34)
+    m = np.round(_rand([B, Ci, H, H], 35) * 2) / 2   # zeros, negatives and positives
+
+    def fwd():
+        y = O.conv2d(tensor_input('x', [B, Ci, H, H]), tensor_input('w', [Co, Ci, k, k]), padding=pd)
+        return O.relu(O.add(y, O.reshape(tensor_input('b', [Co]), [1, Co, 1, 1])))
+    assert 'conv2d,add,relu' in _node_ops(trace_fn(fwd), {})
+    got, want = run_both(fwd, {'x': x, 'w': w, 'b': b})
+    gemm_close(got, want)
+    assert np.array_equal(got > 0, want > 0) or np.mean((got > 0) != (want > 0)) < 1e-3
+
+    def dgrad():
+        g = O.conv2d_input_grad(tensor_input('w', [Co, Ci, k, k]), tensor_input('d', [B, Co, Ho, Ho]), H, H, 1, 1,
+                                pd, pd, 1)
+        return O.relu_grad(tensor_input('m', [B, Ci, H, H]), g)
+    assert 'conv2d_input_grad,relu_grad' in _node_ops(trace_fn(dgrad), {})
+    got, want = run_both(dgrad, {'w': w, 'd': dy, 'm': m})
+    gemm_close(got, want)
+    assert np.all(got[m <= 0] == 0) and not np.any(np.signbit(got[m <= 0]))
+
+
 @pytest.mark.parametrize('k,s,pd', [(3, 2, 1), (2, 2, 0), (3, 3, 0)])
 def test_pool_kernels(k, s, pd):
     """Overlapping / padded windows use the gather adjoint; windows that tile the input
