@@ -365,8 +365,10 @@ JitKernel gemm_epi_kernel(const FusedProgram& p, const FusedInstr* code, const G
   } else {
     o << "  tgk::gd::gemm_tile<" << c.bm << ", " << c.bn << ", " << c.bk << ", " << c.ns << ", "
       << (c.ak ? "true" : "false") << ", " << (c.bkf ? "true" : "false") << ", " << c.nt << ", " << c.kg;
-    // a concatenation along k: the second A source and the partial last stage (KT, CAT)
+    // a concatenation along k: the second A source and the partial last stage (KT, CAT);
+    // the element-wise tile: both operands one element per lane (BDW, ADW) and KT
     if (c.cat) o << ", @NAME@_epi, false, false, true, false, true";
+    else if (c.gen) o << ", @NAME@_epi, true, true, true";
     o << ">(g, tgk::gd::xcd_order(blockIdx.x, gridDim.x), e);\n}\n";
   }
   JitKernel k;

@@ -911,7 +911,26 @@ bool gemm_epi_cfg(const GemmDesc& d, GemmEpiCfg& c, GemmArgs& g, int64_t& blocks
   const Plan p = plan_for(d);
   const bool ak = d.sAk == 1;
   const bool bk = d.sBk == 1 && d.sBn != 1;
-  if (p.splits != 1 || !dma_ok(d, p, ak, bk)) return false;
+  if (p.splits != 1) return false;
+  SkinnyPlan sk;
+  if (!dma_ok(d, p, ak, bk) && !dma_bdw_ok(d, p, ak, bk) && use_gen_dma() && dma_gen_ok(d, ak, bk) &&
+      !skinny_plan(d, sk)) {
+    // the element-wise tile gemm() launches for unaligned operands / partial k stages
+    const int bt = p.bm == 128 && p.bn == 128 ? 128 : 64;
+    g = GemmArgs{d, p.kps, 1, 0, 0, nullptr, 0, 0};
+    g.tiles_n = (int)((d.N + bt - 1) / bt);
+    g.tiles_m = (int)((d.M + bt - 1) / bt);
+    blocks = (int64_t)g.tiles_n * g.tiles_m * d.batch;
+    c.bm = c.bn = bt;
+    c.bk = 32;
+    c.nt = 512;
+    c.kg = bt == 128 ? 1 : 2;
+    c.ns = bt == 128 ? (blocks >= 512 ? 2 : 3) : 4;
+    c.ak = ak; c.bkf = bk;
+    c.gen = true;
+    return blocks < (int64_t(1) << 31);
+  }
+  if (!dma_ok(d, p, ak, bk)) return false;
   // the same instantiation gemm() launches for this plan
   c.bm = p.bm; c.bn = p.bn; c.bk = p.bk;
   c.nt = 512;
