@@ -520,6 +520,46 @@ struct StoreC {
 };
 
 
+// Small degenerate products (one of M, N, K is 1: outer products and matrix-vector
+// products; the small MLP's one-wide layers): a 64 x 64 MFMA tile would compute one real
+// row or column, and its fixed cost (operand staging, the k-group exchange) dominates. Each
+// output takes L lanes (L divides 64, about K / 8 terms per lane): lane j adds terms
+// k = j, j + L, ... in order with f32 FMAs from +0, then an xor butterfly over the L lanes
+// combines them, a fixed order. With K = 1 that is f32(0 + a b), the MFMA tile's bits;
+// otherwise the rounding of another summation order. A generated epilogue (kPrefetch)
+// takes the sum in the lane that would store it (one batch).
+template <int L, class Epi>
+__device__ __forceinline__ void tiny_tile(const GemmArgs& g, const Epi& epi) {
+  const GemmDesc& d = g.d;
+  constexpr int kPerBlock = 256 / L;
+  const int64_t total = d.M * d.N * d.batch;
+  const int lj = (int)threadIdx.x % L;
+  // the loop bound is the same in every thread: all lanes reach the butterfly together
+  for (int64_t e0 = (int64_t)blockIdx.x * kPerBlock; e0 < total; e0 += (int64_t)gridDim.x * kPerBlock) {
+    const int64_t e = e0 + threadIdx.x / L;
+    float acc = 0.0f;
+    int64_t ci = -1, m = 0, n = 0, z0 = 0, z1 = 0;
+    if (e < total) {
+      n = e % d.N;
+      const int64_t t = e / d.N;
+      m = t % d.M;
+      const int64_t z = t / d.M;
+      z0 = z / d.bdiv;
+      z1 = z % d.bdiv;
+      const float* a = d.A + z0 * d.sAz0 + z1 * d.sAz1 + m * d.sAm;
+      const float* b = d.B + z0 * d.sBz0 + z1 * d.sBz1 + n * d.sBn;
+      for (int64_t k = lj; k < d.K; k += L) acc = fmaf(a[k * d.sAk], b[k * d.sBk], acc);
+      ci = z0 * d.sCz0 + z1 * d.sCz1 + m * d.sCm + n * d.sCn;
+    }
+#pragma unroll
+    for (int o = L / 2; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+    if (lj == 0 && ci >= 0) {
+      if constexpr (Epi::kPrefetch) epi(d, z0, z1, m, n, acc, epi.load(d, m, n));
+      else d.C[ci] = acc;
+    }
+  }
+}
+
 // Short products (K at most 16, many outputs: C4's head input gradient [65536, 4] x
 // [4, 256]), where a 32-k MFMA stage would be mostly padding and the output is the traffic.
 // Block b of tiles_n x tiles_m x batch takes RM rows and 256 columns: thread t keeps column

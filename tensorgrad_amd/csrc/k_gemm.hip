@@ -562,37 +562,13 @@ int64_t gemm_workspace_floats(const GemmDesc& d) {
 
 namespace {
 
-// Small degenerate products (one of M, N, K is 1: outer products and matrix-vector
-// products, up to kTinyMacs multiply-adds; the small MLP's one-wide layers): a 64 x 64
-// MFMA tile would compute one real row or column, and its fixed cost (operand staging,
-// the k-group exchange) dominates. Each output takes L lanes (L divides 64, about K / 8
-// terms per lane): lane g adds terms k = g, g + L, ... in order with f32 FMAs from +0, then
-// an xor butterfly over the L lanes combines them, a fixed order. With K = 1 that is
-// f32(0 + a b), the MFMA tile's bits; otherwise the rounding of another summation order.
+// Small degenerate products (one of M, N, K is 1, up to kTinyMacs multiply-adds):
+// tiny_tile (gemm_dev.h).
 constexpr int64_t kTinyMacs = int64_t(1) << 21;
 
 template <int L>
-__global__ __launch_bounds__(256) void k_gemm_tiny(const GemmDesc d) {
-  constexpr int kPerBlock = 256 / L;
-  const int64_t total = d.M * d.N * d.batch;
-  const int g = (int)threadIdx.x % L;
-  // the loop bound is the same in every thread: all lanes reach the butterfly together
-  for (int64_t e0 = (int64_t)blockIdx.x * kPerBlock; e0 < total; e0 += (int64_t)gridDim.x * kPerBlock) {
-    const int64_t e = e0 + threadIdx.x / L;
-    float acc = 0.0f;
-    int64_t ci = -1;
-    if (e < total) {
-      const int64_t n = e % d.N, t = e / d.N, m = t % d.M, z = t / d.M;
-      const int64_t z0 = z / d.bdiv, z1 = z % d.bdiv;
-      const float* a = d.A + z0 * d.sAz0 + z1 * d.sAz1 + m * d.sAm;
-      const float* b = d.B + z0 * d.sBz0 + z1 * d.sBz1 + n * d.sBn;
-      for (int64_t k = g; k < d.K; k += L) acc = fmaf(a[k * d.sAk], b[k * d.sBk], acc);
-      ci = z0 * d.sCz0 + z1 * d.sCz1 + m * d.sCm + n * d.sCn;
-    }
-#pragma unroll
-    for (int o = L / 2; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
-    if (g == 0 && ci >= 0) d.C[ci] = acc;
-  }
+__global__ __launch_bounds__(256) void k_gemm_tiny(const GemmArgs g) {
+  tiny_tile<L>(g, StoreC{});
 }
 
 // Short products (K <= kSmallK, many outputs): smallk_tile (gemm_dev.h). Longer K measured
@@ -617,6 +593,18 @@ static int smallk_rows(const GemmDesc& d) {
   return nblocks(16) >= 1024 ? 16 : nblocks(8) >= 1024 ? 8 : 4;
 }
 
+// Lanes per output of a tiny product (about K / 8 terms per lane) and its grid
+static int tiny_lanes(const GemmDesc& d) {
+  int L = 1;
+  while (L < 64 && (int64_t)L * 8 < d.K) L *= 2;
+  return L;
+}
+static int64_t tiny_blocks(const GemmDesc& d, int L) {
+  const int64_t outs = d.M * d.N * d.batch, per = 256 / L;
+  const int64_t b = (outs + per - 1) / per;
+  return b < 65535 ? b : 65535;
+}
+
 bool gemm_is_tiny(const GemmDesc& d) {
   return d.M > 0 && d.N > 0 && d.K > 0 && d.batch > 0 && (d.M == 1 || d.N == 1 || d.K == 1) &&
          d.M * d.N <= kTinyMacs && d.K <= kTinyMacs && d.M * d.N * d.K * d.batch <= kTinyMacs;
@@ -625,19 +613,17 @@ bool gemm_is_tiny(const GemmDesc& d) {
 void gemm(const GemmDesc& d, float* work, hipStream_t st) {
   if (d.M <= 0 || d.N <= 0 || d.batch <= 0) return;
   if (gemm_is_tiny(d)) {
-    int L = 1;
-    while (L < 64 && (int64_t)L * 8 < d.K) L *= 2;
-    const int64_t outs = d.M * d.N * d.batch, per = 256 / L;
-    const int64_t b = (outs + per - 1) / per;
-    const dim3 grid((unsigned)(b < 65535 ? b : 65535));
+    const int L = tiny_lanes(d);
+    const dim3 grid((unsigned)tiny_blocks(d, L));
+    const GemmArgs ga{d, d.K, 1, 0, 0, nullptr, 0, 0};
     switch (L) {
-      case 1: klaunch(k_gemm_tiny<1>, grid, 256, 0, st, d); return;
-      case 2: klaunch(k_gemm_tiny<2>, grid, 256, 0, st, d); return;
-      case 4: klaunch(k_gemm_tiny<4>, grid, 256, 0, st, d); return;
-      case 8: klaunch(k_gemm_tiny<8>, grid, 256, 0, st, d); return;
-      case 16: klaunch(k_gemm_tiny<16>, grid, 256, 0, st, d); return;
-      case 32: klaunch(k_gemm_tiny<32>, grid, 256, 0, st, d); return;
-      default: klaunch(k_gemm_tiny<64>, grid, 256, 0, st, d); return;
+      case 1: klaunch(k_gemm_tiny<1>, grid, 256, 0, st, ga); return;
+      case 2: klaunch(k_gemm_tiny<2>, grid, 256, 0, st, ga); return;
+      case 4: klaunch(k_gemm_tiny<4>, grid, 256, 0, st, ga); return;
+      case 8: klaunch(k_gemm_tiny<8>, grid, 256, 0, st, ga); return;
+      case 16: klaunch(k_gemm_tiny<16>, grid, 256, 0, st, ga); return;
+      case 32: klaunch(k_gemm_tiny<32>, grid, 256, 0, st, ga); return;
+      default: klaunch(k_gemm_tiny<64>, grid, 256, 0, st, ga); return;
     }
   }
   if (gemm_is_smallk(d)) {
@@ -891,7 +877,20 @@ bool gemm_prefers_group(const GemmDesc& d) {
 
 bool gemm_epi_cfg(const GemmDesc& d, GemmEpiCfg& c, GemmArgs& g, int64_t& blocks) {
   if (d.M <= 0 || d.N <= 0 || d.batch <= 0) return false;
-  if (gemm_is_tiny(d)) return false;
+  if (gemm_is_tiny(d)) {   // the tiny kernel gemm() runs, one batch
+    if (d.batch != 1) return false;
+    g = GemmArgs{d, d.K, 1, 0, 0, nullptr, 0, 0};
+    c.tiny = true;
+    c.bm = tiny_lanes(d);
+    c.bn = c.bk = 1;
+    c.nt = 256;
+    c.kg = 1;
+    c.ns = 0;
+    c.ak = d.sAk == 1;
+    c.bkf = d.sBk == 1 && d.sBn != 1;
+    blocks = tiny_blocks(d, c.bm);
+    return true;
+  }
   if (gemm_is_smallk(d)) {   // the small-K kernel gemm() runs, one batch
     if (d.batch != 1) return false;
     const int rm = smallk_rows(d);

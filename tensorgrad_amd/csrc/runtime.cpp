@@ -3237,11 +3237,15 @@ void Runtime::lower_gemm_epi(int op, const tgk::GemmDesc& d, int a, int b, int o
       const bool ok = is_cat ? tgk::gemm_cat_epi_cfg(d, tgk::GemmCat{nullptr, cf.k0, cf.k1}, c, ga, blocks)
                              : tgk::gemm_epi_cfg(d, c, ga, blocks);
       if (!ok) throw Error(TG_INTERNAL, "GEMM epilogue: no direct-to-LDS launch");
-      const int64_t rows = tgk::gemm_epi_colsum_rows(c, ga);
-      cs_off = take_partials((size_t)rows * (size_t)d.N * 8);
-      colsum_part_[cs_op] = ColPart{cs_off, rows};
-      n.bytes += 8.0 * (double)rows * (double)d.N;
-      n.detail += ",colsum";
+      if (c.tiny) {   // the tiny kernel writes no column partials
+        cs_op = cs_out = -1;
+      } else {
+        const int64_t rows = tgk::gemm_epi_colsum_rows(c, ga);
+        cs_off = take_partials((size_t)rows * (size_t)d.N * 8);
+        colsum_part_[cs_op] = ColPart{cs_off, rows};
+        n.bytes += 8.0 * (double)rows * (double)d.N;
+        n.detail += ",colsum";
+      }
     }
   }
   const size_t code_off = fused_code_.size();

@@ -454,14 +454,16 @@ def test_fused_attention_backward(B, H, T, dh):
 
 @pytest.mark.parametrize('M,N,K,act', [(512, 256, 256, 'relu'), (4096, 1024, 256, 'gelu'), (300, 64, 128, 'gelu'),
                                        (1000, 256, 512, 'dropout'), (20000, 256, 4, 'relu'), (3001, 100, 9, 'gelu'),
-                                       (1000, 256, 63, 'relu'), (700, 128, 45, 'gelu'), (130, 64, 10, 'relu')])
+                                       (1000, 256, 63, 'relu'), (700, 128, 45, 'gelu'), (130, 64, 10, 'relu'),
+                                       (256, 64, 1, 'relu'), (300, 1, 64, 'gelu'), (1, 200, 77, 'relu')])
 def test_gemm_epilogue(M, N, K, act):
     """With TG_GEMM_EPI=1, a product read only by one pointwise group runs that group in
     the GEMM's epilogue (a kernel generated per group): bit-identical to the GEMM and the
     group run apart (TG_GEMM_EPI=0), and within GEMM tolerance of the oracle. By default
     only groups of inexpensive ops (the relu case) run in the epilogue. K <= 16 takes the
     small-K kernel (one thread per column, FMA chains) with the epilogue in it; K not a
-    multiple of 32 the element-wise tile (a partial last k stage)."""
+    multiple of 32 the element-wise tile (a partial last k stage); one of M, N, K equal to
+    1 the tiny kernel (lanes per output and a butterfly)."""
     ins = {'a': _rand([M, K], 101), 'b': _rand([K, N], 102), 'c': _rand([N], 103), 'r': _rand([M, N], 104)}
 
     def body():
