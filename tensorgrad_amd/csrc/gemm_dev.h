@@ -520,6 +520,130 @@ struct StoreC {
 };
 
 
+// ---- skinny products (the layout and the choice are described in k_gemm.hip) ----------
+// GemmArgs as: tiles_m = row blocks of 16, tiles_n = column blocks of NT x 16, splits and
+// k_per_split the k ranges, out the split partials [split][M][N].
+constexpr int kSkinnySteps = 4;   // 16-k steps per wavefront per batch
+
+__device__ __forceinline__ f32x4 mfma16x4(const f32x4& a, const f32x4& b, f32x4 c) {
+#pragma unroll
+  for (int s = 0; s < 4; ++s) c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], b[s], c, 0, 0, 0);
+  return c;
+}
+
+// Zero outside the operand as a bit mask on a value loaded unconditionally (from a clamped
+// address): a select would let the compiler move each load under a branch of its own and
+// wait for it there, one memory latency per element.
+__device__ __forceinline__ unsigned mask_if(bool keep) { return 0u - (unsigned)keep; }
+__device__ __forceinline__ float masked(float v, unsigned keep) { return __uint_as_float(__float_as_uint(v) & keep); }
+
+
+template <int NT, bool AV, class Epi>
+__device__ __forceinline__ void skinny_tile(const GemmArgs& s, const Epi& epi) {
+  constexpr int SB = kSkinnySteps;
+  __shared__ float red[4 * NT * 256];
+  const GemmDesc& d = s.d;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, g4 = lane >> 4;
+  // consecutive row blocks (which share A's cache lines when A has unit row stride) on
+  // one XCD
+  const int bid = (int)xcd_order(blockIdx.x, gridDim.x);
+  const int rbk = bid % s.tiles_m, rest = bid / s.tiles_m;
+  const int cbk = rest % s.tiles_n, sp = rest / s.tiles_n;
+  const int M = (int)d.M, N = (int)d.N, K = (int)d.K;
+  const int sAm = (int)d.sAm, sAk = (int)d.sAk, sBk = (int)d.sBk, sBn = (int)d.sBn;
+  const int kbeg = sp * (int)s.k_per_split, kend = min(K, kbeg + (int)s.k_per_split);
+  const int m = rbk * 16 + l16;
+  const bool mok = m < M;
+  const float* arow = d.A + (mok ? m : M - 1) * sAm;
+  bool nok[NT];
+  const float* bcol[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const int n = cbk * NT * 16 + t * 16 + l16;
+    nok[t] = n < N;
+    bcol[t] = d.B + (nok[t] ? n : N - 1) * sBn;
+  }
+  f32x4 acc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) acc[t] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+  for (int k0 = kbeg; k0 < kend; k0 += 64 * SB) {
+    // every load of the batch is issued before any is used (the scheduling barrier keeps
+    // the compiler from interleaving waits with the loads)
+    f32x4 a[SB];
+    f32x4 b[SB][NT];
+#pragma unroll
+    for (int j = 0; j < SB; ++j) {
+      const int kb = k0 + (j * 4 + wave) * 16 + g4 * 4;
+      if (AV) {
+        a[j] = *reinterpret_cast<const f32x4*>(arow + min(kb, kend - 4));
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) a[j][q] = arow[min(kb + q, kend - 1) * sAk];
+      }
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) b[j][t][q] = bcol[t][min(kb + q, kend - 1) * sBk];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    f32x4 part[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) part[t] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    // steps past the range multiply zeros (a branch around them would let the compiler
+    // sink their loads into it)
+#pragma unroll
+    for (int j = 0; j < SB; ++j) {
+      const int kb = k0 + (j * 4 + wave) * 16 + g4 * 4;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) a[j][q] = masked(a[j][q], mask_if(mok && kb + q < kend));
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) b[j][t][q] = masked(b[j][t][q], mask_if(nok[t] && kb + q < kend));
+        part[t] = mfma16x4(a[j], b[j][t], part[t]);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] += part[t];
+  }
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[(wave * NT + t) * 256 + (g4 * 4 + r) * 16 + l16] = acc[t][r];
+  __syncthreads();
+  if constexpr (Epi::kPrefetch) {
+    // a generated epilogue (one split): the group's loads for the thread's NT outputs
+    // first (clamped in range), then the arithmetic and stores
+    typename Epi::Pre pre[NT];
+#pragma unroll
+    for (int q = 0; q < NT; ++q) {
+      const int e = tid + q * 256, rc = e % 256;
+      pre[q] = epi.load(d, min(rbk * 16 + rc / 16, M - 1), min(cbk * NT * 16 + (e / 256) * 16 + rc % 16, N - 1));
+    }
+#pragma unroll
+    for (int q = 0; q < NT; ++q) {
+      const int e = tid + q * 256;
+      const float v = ((red[e] + red[NT * 256 + e]) + red[2 * NT * 256 + e]) + red[3 * NT * 256 + e];
+      const int t = e / 256, rc = e % 256;
+      const int gm = rbk * 16 + rc / 16, gn = cbk * NT * 16 + t * 16 + rc % 16;
+      if (gm < M && gn < N) epi(d, 0, 0, gm, gn, v, pre[q]);
+    }
+    return;
+  }
+  const int64_t MN = d.M * d.N;
+  for (int e = tid; e < NT * 256; e += 256) {
+    const float v = ((red[e] + red[NT * 256 + e]) + red[2 * NT * 256 + e]) + red[3 * NT * 256 + e];
+    const int t = e / 256, rc = e % 256;
+    const int gm = rbk * 16 + rc / 16, gn = cbk * NT * 16 + t * 16 + rc % 16;
+    if (gm >= M || gn >= N) continue;
+    if (s.splits > 1) s.out[sp * MN + (int64_t)gm * N + gn] = v;
+    else d.C[gm * d.sCm + gn * d.sCn] = v;
+  }
+}
+
+
 // Small degenerate products (one of M, N, K is 1: outer products and matrix-vector
 // products; the small MLP's one-wide layers): a 64 x 64 MFMA tile would compute one real
 // row or column, and its fixed cost (operand staging, the k-group exchange) dominates. Each

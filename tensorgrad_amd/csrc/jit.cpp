@@ -360,7 +360,10 @@ JitKernel gemm_epi_kernel(const FusedProgram& p, const FusedInstr* code, const G
   o << "extern \"C\" __global__ void __launch_bounds__(" << c.nt
     << ") @NAME@(const tgk::gd::GemmArgs g, const tgk::JitArgs A) {\n";
   o << "  const @NAME@_epi e{A, " << (dropout ? "A.seed ? (unsigned)*A.seed : 0u" : "0u") << "};\n";
-  if (c.tiny) {
+  if (c.skinny) {
+    if (c.colsum_out >= 0) throw std::runtime_error("jit: no column partials in the skinny kernel");
+    o << "  tgk::gd::skinny_tile<" << c.bm << ", " << (c.bk ? "true" : "false") << ">(g, e);\n}\n";
+  } else if (c.tiny) {
     if (c.colsum_out >= 0) throw std::runtime_error("jit: no column partials in the tiny kernel");
     o << "  tgk::gd::tiny_tile<" << c.bm << ">(g, e);\n}\n";
   } else if (c.smallk) {

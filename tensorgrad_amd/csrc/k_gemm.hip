@@ -393,110 +393,10 @@ namespace {
 // covers kps of K and writes its partial tile to the workspace ([split][M][N]);
 // k_splitk_reduce adds them in split order. Offsets are 32-bit (the host checks that every
 // element offset fits).
-struct SkinnyArgs {
-  GemmDesc d;
-  int nrb, ncb, splits, kps;
-  float* work;
-};
-
-constexpr int kSkinnySteps = 4;   // 16-k steps per wavefront per batch
-
-__device__ __forceinline__ f32x4 mfma16x4(const f32x4& a, const f32x4& b, f32x4 c) {
-#pragma unroll
-  for (int s = 0; s < 4; ++s) c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], b[s], c, 0, 0, 0);
-  return c;
-}
-
-// Zero outside the operand as a bit mask on a value loaded unconditionally (from a clamped
-// address): a select would let the compiler move each load under a branch of its own and
-// wait for it there, one memory latency per element.
-__device__ __forceinline__ unsigned mask_if(bool keep) { return 0u - (unsigned)keep; }
-__device__ __forceinline__ float masked(float v, unsigned keep) { return __uint_as_float(__float_as_uint(v) & keep); }
-
+// (the body: skinny_tile, gemm_dev.h)
 template <int NT, bool AV>
-__global__ __launch_bounds__(256) void k_gemm_skinny(const SkinnyArgs s) {
-  constexpr int SB = kSkinnySteps;
-  __shared__ float red[4 * NT * 256];
-  const GemmDesc& d = s.d;
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int l16 = lane & 15, g4 = lane >> 4;
-  // consecutive row blocks (which share A's cache lines when A has unit row stride) on
-  // one XCD
-  const int bid = (int)xcd_order(blockIdx.x, gridDim.x);
-  const int rbk = bid % s.nrb, rest = bid / s.nrb;
-  const int cbk = rest % s.ncb, sp = rest / s.ncb;
-  const int M = (int)d.M, N = (int)d.N, K = (int)d.K;
-  const int sAm = (int)d.sAm, sAk = (int)d.sAk, sBk = (int)d.sBk, sBn = (int)d.sBn;
-  const int kbeg = sp * s.kps, kend = min(K, kbeg + s.kps);
-  const int m = rbk * 16 + l16;
-  const bool mok = m < M;
-  const float* arow = d.A + (mok ? m : M - 1) * sAm;
-  bool nok[NT];
-  const float* bcol[NT];
-#pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    const int n = cbk * NT * 16 + t * 16 + l16;
-    nok[t] = n < N;
-    bcol[t] = d.B + (nok[t] ? n : N - 1) * sBn;
-  }
-  f32x4 acc[NT];
-#pragma unroll
-  for (int t = 0; t < NT; ++t) acc[t] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-  for (int k0 = kbeg; k0 < kend; k0 += 64 * SB) {
-    // every load of the batch is issued before any is used (the scheduling barrier keeps
-    // the compiler from interleaving waits with the loads)
-    f32x4 a[SB];
-    f32x4 b[SB][NT];
-#pragma unroll
-    for (int j = 0; j < SB; ++j) {
-      const int kb = k0 + (j * 4 + wave) * 16 + g4 * 4;
-      if (AV) {
-        a[j] = *reinterpret_cast<const f32x4*>(arow + min(kb, kend - 4));
-      } else {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) a[j][q] = arow[min(kb + q, kend - 1) * sAk];
-      }
-#pragma unroll
-      for (int t = 0; t < NT; ++t)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) b[j][t][q] = bcol[t][min(kb + q, kend - 1) * sBk];
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    f32x4 part[NT];
-#pragma unroll
-    for (int t = 0; t < NT; ++t) part[t] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-    // steps past the range multiply zeros (a branch around them would let the compiler
-    // sink their loads into it)
-#pragma unroll
-    for (int j = 0; j < SB; ++j) {
-      const int kb = k0 + (j * 4 + wave) * 16 + g4 * 4;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) a[j][q] = masked(a[j][q], mask_if(mok && kb + q < kend));
-#pragma unroll
-      for (int t = 0; t < NT; ++t) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) b[j][t][q] = masked(b[j][t][q], mask_if(nok[t] && kb + q < kend));
-        part[t] = mfma16x4(a[j], b[j][t], part[t]);
-      }
-    }
-#pragma unroll
-    for (int t = 0; t < NT; ++t) acc[t] += part[t];
-  }
-#pragma unroll
-  for (int t = 0; t < NT; ++t)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) red[(wave * NT + t) * 256 + (g4 * 4 + r) * 16 + l16] = acc[t][r];
-  __syncthreads();
-  const int64_t MN = d.M * d.N;
-  for (int e = tid; e < NT * 256; e += 256) {
-    const float v = ((red[e] + red[NT * 256 + e]) + red[2 * NT * 256 + e]) + red[3 * NT * 256 + e];
-    const int t = e / 256, rc = e % 256;
-    const int gm = rbk * 16 + rc / 16, gn = cbk * NT * 16 + t * 16 + rc % 16;
-    if (gm >= M || gn >= N) continue;
-    if (s.splits > 1) s.work[sp * MN + (int64_t)gm * N + gn] = v;
-    else d.C[gm * d.sCm + gn * d.sCn] = v;
-  }
+__global__ __launch_bounds__(256) void k_gemm_skinny(const GemmArgs g) {
+  skinny_tile<NT, AV>(g, StoreC{});
 }
 
 struct SkinnyPlan { int nt, nrb, ncb, splits, kps; bool av; };
@@ -645,7 +545,7 @@ void gemm(const GemmDesc& d, float* work, hipStream_t st) {
   SkinnyPlan sk;
   if (skinny_plan(d, sk)) {
     if (((uintptr_t)d.A & 15) != 0) sk.av = false;
-    SkinnyArgs a{d, sk.nrb, sk.ncb, sk.splits, sk.kps, work};
+    const GemmArgs a{d, sk.kps, sk.splits, sk.ncb, sk.nrb, work, 0, 0};
     const unsigned blocks = (unsigned)((int64_t)sk.nrb * sk.ncb * sk.splits);
 #define TG_SKINNY(NT)                                                                 \
   case NT:                                                                             \
@@ -890,6 +790,25 @@ bool gemm_epi_cfg(const GemmDesc& d, GemmEpiCfg& c, GemmArgs& g, int64_t& blocks
     c.bkf = d.sBk == 1 && d.sBn != 1;
     blocks = tiny_blocks(d, c.bm);
     return true;
+  }
+  {   // the skinny kernel gemm() runs (one split, one batch)
+    SkinnyPlan sk;
+    if (skinny_plan(d, sk)) {
+      if (sk.splits != 1 || d.batch != 1) return false;
+      if (((uintptr_t)d.A & 15) != 0) sk.av = false;
+      g = GemmArgs{d, sk.kps, 1, sk.ncb, sk.nrb, nullptr, 0, 0};
+      blocks = (int64_t)sk.nrb * sk.ncb;
+      c.skinny = true;
+      c.bm = sk.nt;     // column tiles per block
+      c.bk = sk.av ? 1 : 0;
+      c.bn = 16;
+      c.nt = 256;
+      c.kg = 1;
+      c.ns = 0;
+      c.ak = d.sAk == 1;
+      c.bkf = d.sBk == 1 && d.sBn != 1;
+      return true;
+    }
   }
   if (gemm_is_smallk(d)) {   // the small-K kernel gemm() runs, one batch
     if (d.batch != 1) return false;

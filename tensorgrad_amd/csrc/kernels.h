@@ -328,6 +328,7 @@ struct GemmEpiCfg {
   bool smallk = false;    // the small-K kernel (smallk_tile, bm rows of k padded to bk) instead of the tile
   bool gen = false;       // the element-wise tile (both operands one element per lane, partial k stages)
   bool tiny = false;      // the tiny kernel (tiny_tile, bm lanes per output; no column partials)
+  bool skinny = false;    // the skinny kernel (skinny_tile, bm column tiles, bk: 16-byte A loads; no column partials)
 };
 // Rows of the f64 column partials an epilogue with colsum_out writes for this launch
 // (tiles along M times the wavefronts along M of a tile).

@@ -433,6 +433,12 @@ class Runtime {
     const std::string& k = kinds_[op];
     return k == "param_input" || k == "tensor_input" || k == "state_input";
   }
+  // An op with no inputs producing a constant, lowered on its own (not in a group): it can
+  // be lowered ahead of its position (its node then runs once, among the init nodes).
+  bool const_op(int op) const {
+    return op >= 0 && (kinds_[op] == "const_scalar" || kinds_[op] == "const_fill") && !virtual_[op] &&
+           group_of_[op] < 0;
+  }
   int root(int t) const { return view_[t].root; }
   void* dptr(int t) const { return ptr_[root(t)]; }
   const tgj::Value& O(int op) const { return *ops_[op]; }
@@ -3164,7 +3170,7 @@ int Runtime::epi_group(int op, int out, const tgk::GemmDesc& d, bool& store_c, c
       // read whole and in order: a view of the full product with the group's shape
       if (T_[e.first].numel != T_[out].numel || !view_[e.first].contiguous() || T_[e.first].shape != G.shape) return -1;
       ++hits;
-    } else if (!ready_now(e.first)) {
+    } else if (!ready_now(e.first) && !const_op(T_[root(e.first)].src)) {
       return -1;
     }
   }
@@ -3188,6 +3194,14 @@ void Runtime::lower_gemm_epi(int op, const tgk::GemmDesc& d, int a, int b, int o
   group_done_[gi] = 1;
   const Group G = groups_[gi];
   const GroupPlan gp = plan_group(G.ops, false, G.shape);
+  // constants the group reads that are not lowered yet: lowered now, ahead of their position
+  for (auto& e : gp.ext) {
+    const int p = T_[root(e.first)].src;
+    if (root(e.first) != out && !ready_now(e.first) && const_op(p) && !gemm_done_[p]) {
+      lower_op(p);
+      gemm_done_[p] = 1;
+    }
+  }
   Node n;
   n.kind = "gemm";
   n.op = op;
@@ -3237,7 +3251,7 @@ void Runtime::lower_gemm_epi(int op, const tgk::GemmDesc& d, int a, int b, int o
       const bool ok = is_cat ? tgk::gemm_cat_epi_cfg(d, tgk::GemmCat{nullptr, cf.k0, cf.k1}, c, ga, blocks)
                              : tgk::gemm_epi_cfg(d, c, ga, blocks);
       if (!ok) throw Error(TG_INTERNAL, "GEMM epilogue: no direct-to-LDS launch");
-      if (c.tiny) {   // the tiny kernel writes no column partials
+      if (c.tiny || c.skinny) {   // these kernels write no column partials
         cs_op = cs_out = -1;
       } else {
         const int64_t rows = tgk::gemm_epi_colsum_rows(c, ga);
