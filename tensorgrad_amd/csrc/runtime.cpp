@@ -3316,7 +3316,8 @@ void Runtime::lower_gemm_epi(int op, const tgk::GemmDesc& d, int a, int b, int o
       }
       const int m = contig ? tgk::FM_CONTIG : (scalar ? tgk::FM_SCALAR : tgk::FM_STRIDED);
       if (v.root == out) {
-        if (m != tgk::FM_CONTIG) throw Error(TG_INTERNAL, "GEMM epilogue: the product is not read in order");
+        // (a one-element product merges to no dimension and reads as a scalar: the same element)
+        if (m != tgk::FM_CONTIG && cnt != 1) throw Error(TG_INTERNAL, "GEMM epilogue: the product is not read in order");
         h_in = (int)q;
       }
       p.in[q] = ptr_[v.root];
