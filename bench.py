@@ -258,6 +258,7 @@ def vendor_gemm(key, iters=100):
         if n['kind'] != 'gemm' or n.get('ops') or 'x[' not in n['shape']:
             continue
         left, right = n['shape'].split('x[', 1)
+        right = right.split(']', 1)[0]   # drop a note after the shape (" by 2 sources", ...)
         ld = [int(v) for v in left.strip('[] ').split(',')]
         rd = [int(v) for v in right.strip('[] ').split(',')]
         if len(rd) != 2:
