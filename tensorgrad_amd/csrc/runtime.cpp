@@ -433,12 +433,12 @@ class Runtime {
     const std::string& k = kinds_[op];
     return k == "param_input" || k == "tensor_input" || k == "state_input";
   }
-  // An op with no inputs producing a constant, lowered on its own (not in a group): it can
-  // be lowered ahead of its position (its node then runs once, among the init nodes).
-  bool const_op(int op) const {
-    return op >= 0 && (kinds_[op] == "const_scalar" || kinds_[op] == "const_fill") && !virtual_[op] &&
-           group_of_[op] < 0;
-  }
+  // Tensors that depend on constants only (no input, parameter, state or random op): their
+  // producers can be lowered ahead of their positions (the nodes then run once, among the
+  // init nodes). const_early_ok: every producer of t not lowered yet is such an op, on its
+  // own or in a group of such ops only; lower_const_early lowers them, inputs first.
+  bool const_early_ok(int t, int depth = 0) const;
+  void lower_const_early(int t);
   int root(int t) const { return view_[t].root; }
   void* dptr(int t) const { return ptr_[root(t)]; }
   const tgj::Value& O(int op) const { return *ops_[op]; }
@@ -3170,7 +3170,7 @@ int Runtime::epi_group(int op, int out, const tgk::GemmDesc& d, bool& store_c, c
       // read whole and in order: a view of the full product with the group's shape
       if (T_[e.first].numel != T_[out].numel || !view_[e.first].contiguous() || T_[e.first].shape != G.shape) return -1;
       ++hits;
-    } else if (!ready_now(e.first) && !const_op(T_[root(e.first)].src)) {
+    } else if (!ready_now(e.first) && !const_early_ok(e.first)) {
       return -1;
     }
   }
@@ -3195,13 +3195,8 @@ void Runtime::lower_gemm_epi(int op, const tgk::GemmDesc& d, int a, int b, int o
   const Group G = groups_[gi];
   const GroupPlan gp = plan_group(G.ops, false, G.shape);
   // constants the group reads that are not lowered yet: lowered now, ahead of their position
-  for (auto& e : gp.ext) {
-    const int p = T_[root(e.first)].src;
-    if (root(e.first) != out && !ready_now(e.first) && const_op(p) && !gemm_done_[p]) {
-      lower_op(p);
-      gemm_done_[p] = 1;
-    }
-  }
+  for (auto& e : gp.ext)
+    if (root(e.first) != out && !ready_now(e.first)) lower_const_early(e.first);
   Node n;
   n.kind = "gemm";
   n.op = op;
@@ -3553,6 +3548,58 @@ bool Runtime::plain_gemm(int j) const {
 
 // Tensor t's data exists already: its root is an input / parameter / state, or a node
 // emitted so far writes it.
+static bool const_kind(const std::string& k) { return k == "const_scalar" || k == "const_fill" || k == "arange"; }
+static bool pointwise_const_safe(const std::string& k) {
+  return k != "randn" && k != "dropout" && k != "categorical_last" && k != "param_input" && k != "tensor_input" &&
+         k != "state_input" && k.rfind("adam_", 0) != 0 && k != "matmul" && k != "matmul_batched";
+}
+
+bool Runtime::const_early_ok(int t, int depth) const {
+  if (depth > 16) return false;
+  if (ready_now(t)) return true;
+  const int p = T_[root(t)].src;
+  if (p < 0 || is_leaf(p) || virtual_[p] || attn_of_[p] >= 0 || mul_absorbed_[p] || sum_absorbed_[p] ||
+      colsum_.count(p) || !pointwise_const_safe(kinds_[p]))
+    return false;
+  const int g = group_of_[p];
+  auto op_ok = [&](int q) {
+    if (const_kind(kinds_[q])) return true;
+    if (!pointwise_const_safe(kinds_[q]) || is_leaf(q)) return false;
+    for (int in : op_inputs(*ops_[q])) {
+      const int ip = T_[root(in)].src;
+      if (g >= 0 && ip >= 0 && group_of_[ip] == g) continue;   // computed inside the group
+      if (!const_early_ok(in, depth + 1)) return false;
+    }
+    return true;
+  };
+  if (g < 0) return !gemm_done_[p] && op_ok(p);
+  if (group_done_[g] || !groups_[g].dups.empty()) return false;
+  for (int q : groups_[g].ops)
+    if (!op_ok(q)) return false;
+  return true;
+}
+
+void Runtime::lower_const_early(int t) {
+  if (ready_now(t)) return;
+  const int p = T_[root(t)].src;
+  const int g = group_of_[p];
+  const std::vector<int> ops = g < 0 ? std::vector<int>{p} : groups_[g].ops;
+  for (int q : ops)
+    if (!const_kind(kinds_[q]))
+      for (int in : op_inputs(*ops_[q])) {
+        const int ip = T_[root(in)].src;
+        if (g >= 0 && ip >= 0 && group_of_[ip] == g) continue;   // computed inside the group
+        lower_const_early(in);
+      }
+  if (g < 0) {
+    lower_op(p);
+    gemm_done_[p] = 1;
+  } else {
+    lower_group(g);
+    group_done_[g] = 1;
+  }
+}
+
 bool Runtime::ready_now(int t) const {
   const int r = root(t);
   const int p = T_[r].src;
