@@ -782,6 +782,13 @@ void Runtime::narrow_sliced_products() {
     const int m = T_[p].src;
     if (m < 0 || (kinds_[m] != "matmul" && kinds_[m] != "matmul_batched") || T_[p].dt != F32) continue;
     if (consumers_[p].size() != 1 || pinned(p)) continue;
+    // products of a one-hot (the embedding gather and scatter) read B's rows whole
+    const int am = T_[fld(m, "a")].src;
+    if (am >= 0 && (kinds_[am] == "one_hot" || kinds_[am] == "permute" || kinds_[am] == "reshape")) {
+      int r = am;
+      while (r >= 0 && (kinds_[r] == "permute" || kinds_[r] == "reshape")) r = T_[fld(r, "a")].src;
+      if (r >= 0 && kinds_[r] == "one_hot") continue;
+    }
     Dims& ps = T_[p].shape;
     const Dims& ss = T_[s].shape;
     const int64_t rank = (int64_t)ps.size();

@@ -268,6 +268,28 @@ def test_skip_concatenation_gradients_lower_without_copies():
     assert len([n for n in nodes if (n.get('ops') or '').startswith('gemm+relu_grad')]) == 8
 
 
+def test_embedding_products_are_not_narrowed():
+    """A slice of one_hot(idx) @ table keeps the whole-row gather (which reads table rows of
+    the table's width) and slices after it; a plain product is narrowed to the kept columns."""
+    import sys
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from _helpers import wire
+    from tensorgrad_amd import ir as IR
+    from tensorgrad_amd import ops as O
+    from tensorgrad_amd.trace import tensor_input, trace_fn
+
+    def emb():
+        e = O.matmul(O.one_hot(tensor_input('i', [64], 'i32'), 10), tensor_input('t', [10, 32]))
+        return O.narrow(e, -1, 0, 16)
+
+    def prod():
+        return O.narrow(O.matmul(tensor_input('a', [64, 10]), tensor_input('t', [10, 32])), -1, 0, 16)
+    ne = backend.plan(IR.dumps(wire(trace_fn(emb))))['nodes']
+    assert [(n['kind'], n['shape']) for n in ne] == [('gather', '[64,10]x[10,32]'), ('copy', '[64,16]')], ne
+    npr = backend.plan(IR.dumps(wire(trace_fn(prod))))['nodes']
+    assert [n['shape'] for n in npr] == ['[64,10]x[10,32] first 16 columns'], npr
+
+
 def test_bias_sums_come_from_gemm_epilogues(monkeypatch):
     """C4's hidden-layer bias gradients are column sums of the ReLU-gradient outputs of
     GEMM epilogues: those epilogues write f64 column partials (one row per tile row slot of

@@ -549,6 +549,36 @@ def test_concat_product(M, k0, k1, N, epi):
     gemm_close(got, ref)
 
 
+def test_sliced_products():
+    """A product read only by a slice keeping its first columns computes just those columns
+    (B read through the same view, narrowed); an embedding product (one_hot @ table, the
+    row gather) is gathered whole and then sliced, since the gather reads whole table rows.
+    Against the oracle: GEMM tolerance for the product, bit-exact for the gather."""
+    M, K, N, w = 300, 64, 96, 40
+    ins = {'a': _rand([M, K], 131), 'b': _rand([N, K], 132)}
+
+    def prod():
+        p = O.matmul(tensor_input('a', [M, K]), O.swap_axes(tensor_input('b', [N, K]), -1, -2))
+        return O.relu(O.narrow(p, -1, 0, w))
+    g = trace_fn(prod)
+    rt = backend.NativeRuntime(IR.dumps(wire(g)))
+    shapes = [n['shape'] for n in rt.describe()['nodes']]
+    rt.destroy()
+    assert not any('[300,40]' == s for s in shapes if s), shapes   # no slice copy
+    got, want = run_both(prod, ins)
+    gemm_close(got, want)
+
+    idx = np.random.default_rng(133).integers(0, 10, 64).astype(np.int32)
+    tab = _rand([10, 32], 134)
+
+    def emb():
+        e = O.matmul(O.one_hot(tensor_input('i', [64], 'i32'), 10), tensor_input('t', [10, 32]))
+        return O.narrow(e, -1, 0, 16)
+    got, want = run_both(emb, {'i': idx, 't': tab})
+    exact(got, want)
+    assert np.array_equal(got, tab[idx, :16])
+
+
 def test_concat_forward_and_transposed_readers():
     """A concatenation read by a product (the forward) and, transposed, by another (the
     weight gradient): the first runs over the sources in place, the second as one GEMM per
